@@ -1,0 +1,66 @@
+"""C ABI: libsrswa.so loads, exports every function include/srswa.h declares,
+and the ctypes argument structs match the header field for field.  No kernel
+is launched (CPU-only)."""
+
+import ctypes
+import os
+import re
+
+import srswa
+from srswa import _lib
+
+HEADER = os.path.join(os.path.dirname(os.path.dirname(os.path.abspath(__file__))),
+                      "include", "srswa.h")
+
+
+def _header_text():
+    src = open(HEADER).read()
+    src = re.sub(r"/\*.*?\*/", "", src, flags=re.S)
+    return re.sub(r"//[^\n]*", "", src)
+
+
+def _declared_functions():
+    return set(re.findall(r"^\s*(?:const\s+)?[\w\s\*]*?\b(srswa_\w+)\s*\(", _header_text(), flags=re.M))
+
+
+def _declared_structs():
+    out = {}
+    for body, name in re.findall(r"typedef\s+struct\s*\{(.*?)\}\s*(\w+)\s*;", _header_text(), flags=re.S):
+        fields = []
+        for decl in body.split(";"):
+            decl = decl.strip()
+            if not decl:
+                continue
+            m = re.match(r"(const\s+)?([\w]+)\s*(\**)\s*(.*)", decl)
+            names = [n.strip().lstrip("*").strip() for n in m.group(4).split(",")]
+            fields += names
+        out[name] = fields
+    return out
+
+
+def test_library_loads_and_exports_every_declared_symbol():
+    lib = _lib.lib()
+    declared = _declared_functions()
+    assert declared, "no functions parsed from the header"
+    for name in declared:
+        assert hasattr(lib, name), f"{name} declared in srswa.h but not exported"
+    assert set(_lib.SIGNATURES) == declared, set(_lib.SIGNATURES) ^ declared
+    assert lib.srswa_version() >= 100
+
+
+def test_ctypes_structs_match_header():
+    structs = _declared_structs()
+    assert set(structs) == set(_lib.STRUCTS), set(structs) ^ set(_lib.STRUCTS)
+    for cname, fields in structs.items():
+        py = [f[0] for f in _lib.STRUCTS[cname]._fields_]
+        assert py == fields, (cname, py, fields)
+
+
+def test_workspace_query_needs_no_gpu():
+    a = _lib.DecodeArgs()
+    a.B, a.Lq, a.HQ, a.HKV, a.HI, a.D, a.S, a.L = 64, 1, 10, 10, 10, 128, 8, 131072
+    a.block_size, a.local_window, a.in_dtype, a.out_dtype = 64, 512, _lib.SRSWA_BF16, _lib.SRSWA_BF16
+    n = _lib.lib().srswa_gather_decode_workspace(ctypes.byref(a))
+    # 640 (row, head) pairs x 4 workgroups x 160-float records + counters
+    assert n == 2560 + 640 * 4 * 160 * 4
+    assert srswa.__version__

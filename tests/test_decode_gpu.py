@@ -1,0 +1,110 @@
+"""Decode gather-attention: HIP kernel vs the CPU oracle (through the C ABI).
+
+Tolerances (stated by the task): bf16 outputs max-abs <= 2e-2; fp32 outputs
+relative <= 1e-5 (max-abs error / max-abs reference)."""
+
+import math
+
+import pytest
+import torch
+
+from oracle import srswa_oracle as O
+import srswa
+from srswa import workloads as W
+
+pytestmark = pytest.mark.gpu
+
+BF16_TOL = 2e-2
+F32_REL = 1e-5
+
+
+def _rel(a, b):
+    return (a.double() - b.double()).abs().max().item() / max(b.double().abs().max().item(), 1e-30)
+
+
+def test_cfg1_fp32_reference_form(dev):
+    """Config 1 at full size in fp32: the reference's _decode_attend form
+    (one index head per query head here: per-head mean-pool top-8)."""
+    c = W.cpu_decode_config()
+    q, k, v = c["q"], c["k"], c["v"]
+    B, H, _, D = q.shape
+    L = k.shape[2]
+    # per-head selection with the oracle's indexer (mean pool, top-8)
+    sc = O.meanpool_block_scores(q, k, c["q_pos"], c["block_size"], c["local_window"] // c["block_size"])
+    topi = O.topk_blocks(sc, c["k_top"])                     # [B,H,1,8]
+    bias = torch.zeros(topi.shape, dtype=torch.float32)
+    valid = topi >= 0
+    ref = O.decode_attend(q, k, v, topi, bias, valid, c["q_pos"], c["block_size"],
+                          c["local_window"], c["scale"])
+    out = srswa.decode_attend(q.to(dev), k.to(dev), v.to(dev), topi.to(dev), bias.to(dev),
+                              valid.to(dev), c["q_pos"].to(dev), c["block_size"],
+                              c["local_window"], c["scale"]).cpu()
+    assert out.dtype == torch.float32 and out.shape == ref.shape
+    assert _rel(out, ref) <= F32_REL, _rel(out, ref)
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16, torch.float32])
+@pytest.mark.parametrize("Lq", [1, 3])
+def test_reference_signature_shared_index_head(dev, dtype, Lq):
+    """_decode_attend signature: topi [B,Lq,K] shared by all heads, GQA 2:1,
+    random bias, some invalid slots, duplicates, blocks overlapping the window."""
+    g = torch.Generator().manual_seed(7)
+    B, H, Hkv, D, S, BS, LW, K = 3, 8, 4, 128, 1500, 32, 128, 6
+    q = torch.randn(B, H, Lq, D, generator=g).to(dtype)
+    k = torch.randn(B, Hkv, S, D, generator=g).to(dtype)
+    v = torch.randn(B, Hkv, S, D, generator=g).to(dtype)
+    q_pos = torch.tensor([[S - Lq + i for i in range(Lq)], [700 + i for i in range(Lq)],
+                          [90 + i for i in range(Lq)]])
+    nblk = -(-S // BS)
+    topi = torch.randint(0, nblk, (B, Lq, K), generator=g)
+    topi[0, :, 1] = topi[0, :, 0]                             # duplicate id
+    topi[1, :, 2] = q_pos[1, 0] // BS                          # overlaps the window
+    bias = torch.randn(B, Lq, K, generator=g)
+    valid = torch.rand(B, Lq, K, generator=g) > 0.2
+    ref = O.decode_attend(q.double(), k.double(), v.double(), topi, bias.double(), valid, q_pos,
+                          BS, LW, 1 / math.sqrt(D))
+    out = srswa.decode_attend(q.to(dev), k.to(dev), v.to(dev), topi.to(dev), bias.to(dev),
+                              valid.to(dev), q_pos.to(dev), BS, LW, 1 / math.sqrt(D)).cpu()
+    if dtype == torch.float32:
+        assert _rel(out, ref) <= F32_REL
+    else:
+        assert (out.double() - ref).abs().max().item() <= BF16_TOL
+
+
+def test_cfg3_scaled_bf16_vs_gather_oracle(dev):
+    """Config 3 shape family at reduced batch/length (identical CPU bytes)."""
+    c = W.decode_config(B=6, H=10, D=128, Lmax=20000, lo=1500, k=8)
+    ref = O.decode_attend_gather(c["q"], c["k_cache"], c["v_cache"], c["block_idx"], c["q_pos"],
+                                 c["block_size"], c["local_window"], c["scale"])
+    out = srswa.gather_decode(c["q"].to(dev), c["k_cache"].to(dev), c["v_cache"].to(dev),
+                              c["block_idx"].to(dev), c["q_pos"].to(dev),
+                              block_size=c["block_size"], local_window=c["local_window"],
+                              scale=c["scale"]).cpu()
+    assert (out.double() - ref.double()).abs().max().item() <= BF16_TOL
+
+
+def test_edge_rows(dev):
+    """q_pos 0, q_pos inside the first block, kv_len clipping, all slots empty."""
+    g = torch.Generator().manual_seed(3)
+    B, H, D, L, BS, LW = 4, 2, 64, 400, 64, 128
+    q = torch.randn(B, 1, H, D, generator=g).to(torch.bfloat16)
+    kc = torch.randn(B, L, H, D, generator=g).to(torch.bfloat16)
+    vc = torch.randn(B, L, H, D, generator=g).to(torch.bfloat16)
+    q_pos = torch.tensor([[0], [37], [399], [300]])
+    kv_len = torch.tensor([400, 400, 250, 400])
+    idx = torch.tensor([[-1, -1], [0, -1], [0, 1], [-1, -1]]).view(B, 1, 1, 2).expand(B, H, 1, 2).contiguous()
+    out, lse = srswa.gather_decode(q.to(dev), kc.to(dev), vc.to(dev), idx.to(dev), q_pos.to(dev),
+                                   block_size=BS, local_window=LW, scale=0.125,
+                                   kv_len=kv_len.to(dev), return_lse=True)
+    out = out.cpu().double()
+    # oracle on the cache truncated to kv_len (the window stays anchored at q_pos)
+    for b in range(B):
+        Lb = int(kv_len[b])
+        qp = int(q_pos[b])
+        kk = kc[b:b + 1, :Lb].transpose(1, 2).double()
+        vv = vc[b:b + 1, :Lb].transpose(1, 2).double()
+        ti = idx[b:b + 1, :, 0:1, :]
+        ref = O.decode_attend(q[b:b + 1].transpose(1, 2).double(), kk, vv, ti,
+                              torch.zeros(ti.shape), ti >= 0, torch.tensor([[qp]]), BS, LW, 0.125)
+        assert (out[b:b + 1].transpose(1, 2) - ref).abs().max().item() <= BF16_TOL
+    assert torch.isfinite(lse.cpu()).all()

@@ -1,0 +1,476 @@
+// Decode gather-attention for gfx950 (MI355X).
+//
+// Replaces the reference's decode attend: _decode_attend
+// (HF/modeling_deepseekv2.py:454-481) and SGLang's dash_sparse_attn_decode
+// (WHL!layers/attention/unlimited_dash_ops/attend_triton.py:307-518 + the LSE
+// merge in WHL!layers/attention/unlimited_dash_ops/common.py:44-89).
+//
+// Work decomposition.  The keys one query row reads are cut into "units" of
+// UK keys: ceil(BS/UK) units per selected remote block slot, then
+// ceil(LW/UK) units tiling the token window (q_pos-LW, q_pos] from its first
+// key (the window is contiguous, so its units need not be block aligned).
+// One wavefront streams one or more units:
+//   * K and V rows are read straight into VGPRs with 16-byte loads, LPR lanes
+//     per key row (bf16, D=128: 16 lanes x 16 B = the row's two 128-byte
+//     lines), so every load instruction moves whole cache lines;
+//   * q.k partial sums are finished by a butterfly reduce-scatter across the
+//     LPR lanes of a row (each lane ends holding one key's score);
+//   * online softmax in the log2 domain (wave max/sum via shuffles), p is
+//     broadcast back through 256 bytes of LDS per wave, then o += p v;
+// Four waves (one workgroup) merge their (m, l, o) in LDS; the workgroups of
+// one (row, head) merge through a small workspace, the last one to finish
+// (atomic arrival counter) producing the output.  No host sync, no second
+// kernel, the workspace is left zeroed for the next call.
+#include <stdarg.h>
+#include <stdio.h>
+#include <string.h>
+
+#include "common.h"
+
+namespace srswa {
+
+static thread_local char g_err[512];
+void set_error(const char* fmt, ...) {
+  va_list ap;
+  va_start(ap, fmt);
+  vsnprintf(g_err, sizeof(g_err), fmt, ap);
+  va_end(ap);
+}
+const char* last_error() { return g_err; }
+
+namespace {
+
+constexpr int kDecodeWaves = 4;   // waves per workgroup
+
+struct DecodePlan {
+  int UK;              // keys per unit
+  int upb;             // units per remote block slot
+  int n_remote_units;  // S * upb
+  int n_units;         // + window units
+  int upw;             // units per wave
+  int nsplit;          // workgroups per (row, head)
+  int pstride;         // floats per partial record (128-byte multiple)
+  int64_t rowheads;    // B * Lq * HQ
+};
+
+struct DecodeK {
+  srswa_decode_args a;
+  int G, IG;
+  int UK, upb, n_remote_units, n_units, upw, nsplit, pstride;
+  float scale_l2;      // scale * log2(e)
+  float* part;
+  uint32_t* cnt;
+};
+
+template <typename TO>
+__device__ __forceinline__ void store_out(TO* dst, const float* f, int n);
+template <>
+__device__ __forceinline__ void store_out<float>(float* dst, const float* f, int n) {
+  for (int e = 0; e < n; e += 4)
+    *reinterpret_cast<uint4*>(dst + e) = Vec16<float>::pack(f + e);
+}
+template <>
+__device__ __forceinline__ void store_out<bf16_t>(bf16_t* dst, const float* f, int n) {
+  if (n == 8) {
+    *reinterpret_cast<uint4*>(dst) = Vec16<bf16_t>::pack(f);
+  } else {
+    for (int e = 0; e < n; e += 2)
+      *reinterpret_cast<uint32_t*>(dst + e) = pack_bf16x2(f[e], f[e + 1]);
+  }
+}
+template <>
+__device__ __forceinline__ void store_out<__half>(__half* dst, const float* f, int n) {
+  if (n == 8) {
+    *reinterpret_cast<uint4*>(dst) = Vec16<__half>::pack(f);
+  } else {
+    for (int e = 0; e < n; e += 2)
+      *reinterpret_cast<uint32_t*>(dst + e) = pack_h16x2(f[e], f[e + 1]);
+  }
+}
+
+// q.k over one 16-byte chunk.
+template <typename T>
+__device__ __forceinline__ float dot16(const uint4& w, const float* qf) {
+  float f[Vec16<T>::N];
+  Vec16<T>::unpack(w, f);
+  float s = 0.f;
+#pragma unroll
+  for (int e = 0; e < Vec16<T>::N; ++e) s = fmaf(qf[e], f[e], s);
+  return s;
+}
+
+template <typename T, typename TO, int D, int NI>
+__global__ __launch_bounds__(kDecodeWaves * kWave) void decode_kernel(DecodeK p) {
+  using V = Vec16<T>;
+  constexpr int EPV = V::N;           // elements per 16-byte vector
+  constexpr int LPR = D / EPV;        // lanes per key row
+  constexpr int RPI = kWave / LPR;    // key rows per load instruction
+  constexpr int UK = NI * RPI;        // keys per unit
+  constexpr int DUP = LPR / NI;       // lanes sharing one finished score
+  static_assert(LPR <= kWave && kWave % LPR == 0, "row must fit a wavefront");
+  static_assert(NI <= LPR && LPR % NI == 0, "NI must divide LPR");
+
+  __shared__ float s_p[kDecodeWaves][64];
+  __shared__ float s_o[kDecodeWaves][D];
+  __shared__ float s_m[kDecodeWaves], s_l[kDecodeWaves];
+
+  const srswa_decode_args& a = p.a;
+  const int wave = threadIdx.x / kWave;
+  const int lane = threadIdx.x % kWave;
+  const int r = lane / LPR;
+  const int c = lane % LPR;
+
+  const int split = blockIdx.x % p.nsplit;
+  const int64_t rh = blockIdx.x / p.nsplit;     // ((b * Lq) + lq) * HQ + hq
+  const int hq = (int)(rh % a.HQ);
+  const int64_t bl = rh / a.HQ;
+  const int lq = (int)(bl % a.Lq);
+  const int b = (int)(bl / a.Lq);
+  const int kvh = hq / p.G;
+  const int ih = hq / p.IG;
+
+  const int qp = a.q_pos[b * a.pos_sb + lq * a.pos_sq];
+  const int kvl = a.kv_len ? min(a.kv_len[b], a.L) : a.L;
+  const int last = min(qp, kvl - 1);                   // last key this row may read
+  const int ws = max(qp - a.local_window + 1, 0);      // first window key
+  const int remote_end = min(ws, last + 1);            // remote keys are < this
+
+  // this lane's slice of q
+  float qf[EPV];
+  {
+    const T* qrow = reinterpret_cast<const T*>(a.q) + (int64_t)b * a.q_sb +
+                    (int64_t)lq * a.q_sq + (int64_t)hq * a.q_sh + c * EPV;
+    V::unpack(*reinterpret_cast<const uint4*>(qrow), qf);
+  }
+  const int32_t* idx_row = a.idx + (int64_t)b * a.idx_sb + (int64_t)ih * a.idx_sh +
+                           (int64_t)lq * a.idx_sq;
+  const int64_t aux_off = (int64_t)b * a.idx_sb + (int64_t)ih * a.idx_sh +
+                          (int64_t)lq * a.idx_sq;
+
+  const T* kbase = reinterpret_cast<const T*>(a.k) + (int64_t)b * a.k_sb +
+                   (int64_t)kvh * a.k_sh + c * EPV;
+  const T* vbase = reinterpret_cast<const T*>(a.v) + (int64_t)b * a.v_sb +
+                   (int64_t)kvh * a.v_sh + c * EPV;
+  const int max_blk = kvl > 0 ? (kvl - 1) / a.block_size : -1;
+
+  float m = -INFINITY, l = 0.f;
+  float acc[EPV];
+#pragma unroll
+  for (int e = 0; e < EPV; ++e) acc[e] = 0.f;
+
+  const int u_begin = (split * kDecodeWaves + wave) * p.upw;
+  const int u_end = min(u_begin + p.upw, p.n_units);
+  for (int u = u_begin; u < u_end; ++u) {
+    int k0, k1;
+    float bias_l2 = 0.f;
+    if (u < p.n_remote_units) {
+      const int slot = u / p.upb, sub = u % p.upb;
+      const int bid = idx_row[(int64_t)slot * a.idx_ss];
+      bool ok = bid >= 0 && bid <= max_blk && (!a.valid || a.valid[aux_off + (int64_t)slot * a.idx_ss]);
+      // a repeat of an id held by an earlier valid slot is skipped
+      for (int s0 = 0; ok && s0 < slot; s0 += kWave) {
+        const int s = s0 + lane;
+        bool dup = false;
+        if (s < slot) {
+          const int o = idx_row[(int64_t)s * a.idx_ss];
+          dup = (o == bid) && (!a.valid || a.valid[aux_off + (int64_t)s * a.idx_ss]);
+        }
+        if (__any(dup)) ok = false;
+      }
+      k0 = ok ? bid * a.block_size + sub * UK : 0;
+      k1 = ok ? min(min(k0 + UK, bid * a.block_size + a.block_size), remote_end) : 0;
+      if (ok && a.bias) bias_l2 = a.bias[aux_off + (int64_t)slot * a.idx_ss] * kLog2e;
+    } else {
+      k0 = ws + (u - p.n_remote_units) * UK;
+      k1 = min(k0 + UK, last + 1);
+    }
+    if (k1 <= k0) continue;   // uniform across the wave
+
+    uint4 kr[NI], vr[NI];
+#pragma unroll
+    for (int i = 0; i < NI; ++i) {
+      const int key = k0 + i * RPI + r;
+      kr[i] = key < k1 ? *reinterpret_cast<const uint4*>(kbase + (int64_t)key * a.k_st)
+                       : make_uint4(0, 0, 0, 0);
+    }
+#pragma unroll
+    for (int i = 0; i < NI; ++i) {
+      const int key = k0 + i * RPI + r;
+      vr[i] = key < k1 ? *reinterpret_cast<const uint4*>(vbase + (int64_t)key * a.v_st)
+                       : make_uint4(0, 0, 0, 0);
+    }
+
+    float part[NI];
+#pragma unroll
+    for (int i = 0; i < NI; ++i) part[i] = dot16<T>(kr[i], qf);
+    // reduce-scatter across the LPR lanes of a row: NI partials -> 1 score
+#pragma unroll
+    for (int n = NI, o = LPR / 2; n > 1; n >>= 1, o >>= 1) {
+      const bool upper = (c & o) != 0;
+#pragma unroll
+      for (int j = 0; j < n / 2; ++j) {
+        const float send = upper ? part[j] : part[j + n / 2];
+        const float keep = upper ? part[j + n / 2] : part[j];
+        part[j] = keep + __shfl_xor(send, o, kWave);
+      }
+    }
+#pragma unroll
+    for (int o = DUP / 2; o >= 1; o >>= 1) part[0] += __shfl_xor(part[0], o, kWave);
+    const int i_own = c / DUP;                    // which instruction's key this lane holds
+    const int key = k0 + i_own * RPI + r;
+    const bool owner = (c % DUP) == 0;
+    const float t = key < k1 ? part[0] * p.scale_l2 + bias_l2 : -INFINITY;
+    const float mnew = fmaxf(m, wave_max(t));     // finite: key k0 is always kept
+    const float alpha = exp2f(m - mnew);
+    const float pj = exp2f(t - mnew);
+    l = l * alpha + wave_sum(owner ? pj : 0.f);
+    m = mnew;
+#pragma unroll
+    for (int e = 0; e < EPV; ++e) acc[e] *= alpha;
+    if (owner) s_p[wave][r * NI + i_own] = pj;
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+    float pv[NI];
+#pragma unroll
+    for (int i = 0; i < NI; ++i) pv[i] = s_p[wave][r * NI + i];
+#pragma unroll
+    for (int i = 0; i < NI; ++i) {
+      float f[EPV];
+      V::unpack(vr[i], f);
+#pragma unroll
+      for (int e = 0; e < EPV; ++e) acc[e] = fmaf(pv[i], f[e], acc[e]);
+    }
+    __builtin_amdgcn_wave_barrier();
+  }
+
+  // sum the RPI row groups of the wave
+#pragma unroll
+  for (int o = LPR; o < kWave; o <<= 1)
+#pragma unroll
+    for (int e = 0; e < EPV; ++e) acc[e] += __shfl_xor(acc[e], o, kWave);
+
+  if (r == 0) {
+#pragma unroll
+    for (int e = 0; e < EPV; ++e) s_o[wave][c * EPV + e] = acc[e];
+  }
+  if (lane == 0) { s_m[wave] = m; s_l[wave] = l; }
+  __syncthreads();
+  if (wave != 0) return;
+
+  // merge the workgroup's waves (wave 0)
+  float M = -INFINITY;
+#pragma unroll
+  for (int w = 0; w < kDecodeWaves; ++w) M = fmaxf(M, s_m[w]);
+  float L = 0.f, O[EPV];
+#pragma unroll
+  for (int e = 0; e < EPV; ++e) O[e] = 0.f;
+#pragma unroll
+  for (int w = 0; w < kDecodeWaves; ++w) {
+    const float wt = s_m[w] == -INFINITY ? 0.f : exp2f(s_m[w] - M);
+    L += s_l[w] * wt;
+    if (r == 0) {
+#pragma unroll
+      for (int e = 0; e < EPV; ++e) O[e] = fmaf(s_o[w][c * EPV + e], wt, O[e]);
+    }
+  }
+
+  if (p.nsplit > 1) {
+    // record: O[0..D) then M, L; records are 128-byte aligned
+    float* rec = p.part + (rh * p.nsplit + split) * p.pstride;
+    if (r == 0) store_out<float>(rec + c * EPV, O, EPV);
+    if (lane == 0) { rec[D] = M; rec[D + 1] = L; }
+    __threadfence();
+    uint32_t arrived = 0;
+    if (lane == 0) arrived = atomicAdd(&p.cnt[rh], 1u);
+    arrived = __shfl(arrived, 0, kWave);
+    if (arrived != (uint32_t)(p.nsplit - 1)) return;
+    __threadfence();
+    if (lane == 0) p.cnt[rh] = 0u;   // leave the workspace zeroed
+    const float* recs = p.part + rh * p.nsplit * p.pstride;
+    M = -INFINITY;
+    for (int s = 0; s < p.nsplit; ++s) M = fmaxf(M, recs[s * p.pstride + D]);
+    L = 0.f;
+#pragma unroll
+    for (int e = 0; e < EPV; ++e) O[e] = 0.f;
+    for (int s = 0; s < p.nsplit; ++s) {
+      const float ms = recs[s * p.pstride + D];
+      const float wt = ms == -INFINITY ? 0.f : exp2f(ms - M);
+      L += recs[s * p.pstride + D + 1] * wt;
+      if (r == 0) {
+        float f[EPV];
+        for (int e = 0; e < EPV; e += 4)
+          Vec16<float>::unpack(*reinterpret_cast<const uint4*>(recs + s * p.pstride + c * EPV + e), f + e);
+#pragma unroll
+        for (int e = 0; e < EPV; ++e) O[e] = fmaf(f[e], wt, O[e]);
+      }
+    }
+  }
+
+  const float inv = L > 0.f ? 1.f / L : 0.f;
+  if (r == 0) {
+#pragma unroll
+    for (int e = 0; e < EPV; ++e) O[e] *= inv;
+    TO* orow = reinterpret_cast<TO*>(a.out) + (int64_t)b * a.o_sb + (int64_t)lq * a.o_sq +
+               (int64_t)hq * a.o_sh + c * EPV;
+    store_out<TO>(orow, O, EPV);
+  }
+  if (a.lse && lane == 0) {
+    a.lse[(int64_t)b * a.lse_sb + (int64_t)lq * a.lse_sq + (int64_t)hq * a.lse_sh] =
+        L > 0.f ? M * kLn2 + logf(L) : -INFINITY;
+  }
+}
+
+int elem_bytes(int dt) { return dt == SRSWA_F32 ? 4 : 2; }
+
+// keys per unit for (dtype, D): NI * (64 / LPR)
+int decode_ni(int dt, int D) {
+  const int lpr = D * elem_bytes(dt) / 16;
+  return lpr < 16 ? lpr : 16;
+}
+
+DecodePlan make_plan(const srswa_decode_args* a) {
+  DecodePlan pl{};
+  const int lpr = a->D * elem_bytes(a->in_dtype) / 16;
+  const int ni = decode_ni(a->in_dtype, a->D);
+  pl.UK = ni * (kWave / lpr);
+  pl.upb = ceil_div(a->block_size, pl.UK);
+  pl.n_remote_units = a->S * pl.upb;
+  pl.n_units = pl.n_remote_units + ceil_div(a->local_window, pl.UK);
+  pl.upw = 1;
+  pl.nsplit = ceil_div(pl.n_units, kDecodeWaves * pl.upw);
+  pl.pstride = ceil_div(a->D + 2, 32) * 32;
+  pl.rowheads = (int64_t)a->B * a->Lq * a->HQ;
+  return pl;
+}
+
+size_t workspace_bytes(const DecodePlan& pl) {
+  if (pl.nsplit <= 1) return 0;
+  const size_t cnt = ((size_t)pl.rowheads * 4 + 255) / 256 * 256;
+  return cnt + (size_t)pl.rowheads * pl.nsplit * pl.pstride * 4;
+}
+
+template <typename T, typename TO, int D>
+int launch_decode(const DecodeK& k, int64_t grid, hipStream_t st) {
+  constexpr int EPV = Vec16<T>::N;
+  constexpr int LPR = D / EPV;
+  constexpr int NI = LPR < 16 ? LPR : 16;
+  hipLaunchKernelGGL((decode_kernel<T, TO, D, NI>), dim3((unsigned)grid), dim3(kDecodeWaves * kWave),
+                     0, st, k);
+  const hipError_t e = hipGetLastError();
+  if (e != hipSuccess) {
+    set_error("decode launch failed: %s", hipGetErrorString(e));
+    return SRSWA_LAUNCH;
+  }
+  return SRSWA_OK;
+}
+
+template <typename T>
+int dispatch_out(const DecodeK& k, int64_t grid, hipStream_t st) {
+  const int D = k.a.D;
+  const int od = k.a.out_dtype;
+  if (od == SRSWA_F32) {
+    if (D == 64) return launch_decode<T, float, 64>(k, grid, st);
+    if (D == 128) return launch_decode<T, float, 128>(k, grid, st);
+  } else if (od == SRSWA_BF16) {
+    if (D == 64) return launch_decode<T, bf16_t, 64>(k, grid, st);
+    if (D == 128) return launch_decode<T, bf16_t, 128>(k, grid, st);
+  } else if (od == SRSWA_F16) {
+    if (D == 64) return launch_decode<T, __half, 64>(k, grid, st);
+    if (D == 128) return launch_decode<T, __half, 128>(k, grid, st);
+  }
+  set_error("decode: unsupported out dtype %d / D %d", od, D);
+  return SRSWA_UNSUPPORTED;
+}
+
+bool aligned16(const void* p) { return ((uintptr_t)p & 15u) == 0; }
+
+}  // namespace
+}  // namespace srswa
+
+using namespace srswa;
+
+extern "C" int srswa_version(void) { return 100; }
+extern "C" const char* srswa_last_error(void) { return srswa::last_error(); }
+
+extern "C" size_t srswa_gather_decode_workspace(const srswa_decode_args* a) {
+  if (!a) return 0;
+  return workspace_bytes(make_plan(a));
+}
+
+extern "C" int srswa_gather_decode(const srswa_decode_args* a, void* workspace,
+                                   size_t ws_bytes, void* stream) {
+  if (!a || !a->q || !a->k || !a->v || !a->out || !a->q_pos || (!a->idx && a->S > 0)) {
+    set_error("decode: null argument");
+    return SRSWA_INVALID;
+  }
+  if (a->B < 0 || a->Lq < 0 || a->HQ <= 0 || a->HKV <= 0 || a->HI <= 0 || a->S < 0 ||
+      a->L <= 0 || a->block_size <= 0 || a->local_window <= 0) {
+    set_error("decode: bad sizes");
+    return SRSWA_INVALID;
+  }
+  if (a->B == 0 || a->Lq == 0) return SRSWA_OK;
+  if (a->HQ % a->HKV != 0 || a->HQ % a->HI != 0) {
+    set_error("decode: HQ=%d must be a multiple of HKV=%d and HI=%d", a->HQ, a->HKV, a->HI);
+    return SRSWA_UNSUPPORTED;
+  }
+  const int ib = elem_bytes(a->in_dtype);
+  if (!(a->D == 64 || a->D == 128) || a->in_dtype < 0 || a->in_dtype > 2 ||
+      a->out_dtype < 0 || a->out_dtype > 2) {
+    set_error("decode: unsupported D=%d / dtype", a->D);
+    return SRSWA_UNSUPPORTED;
+  }
+  // every row must start on a 16-byte boundary
+  const int64_t strides[] = {a->q_sb, a->q_sq, a->q_sh, a->k_sb, a->k_st, a->k_sh,
+                             a->v_sb, a->v_st, a->v_sh};
+  for (int64_t s : strides)
+    if ((s * ib) % 16 != 0) {
+      set_error("decode: strides must keep rows 16-byte aligned");
+      return SRSWA_UNSUPPORTED;
+    }
+  const int ob = elem_bytes(a->out_dtype);
+  if (((a->o_sb * ob) % 16) || ((a->o_sq * ob) % 16) || ((a->o_sh * ob) % 16) ||
+      !aligned16(a->q) || !aligned16(a->k) || !aligned16(a->v) || !aligned16(a->out)) {
+    set_error("decode: pointers must be 16-byte aligned");
+    return SRSWA_UNSUPPORTED;
+  }
+  if (a->S > 1024) {
+    set_error("decode: at most 1024 slots per row (got %d)", a->S);
+    return SRSWA_UNSUPPORTED;
+  }
+  const DecodePlan pl = make_plan(a);
+  const size_t need = workspace_bytes(pl);
+  if (need > 0 && (!workspace || ws_bytes < need)) {
+    set_error("decode: workspace of %zu bytes required (got %zu)", need, ws_bytes);
+    return SRSWA_WORKSPACE;
+  }
+  DecodeK k{};
+  k.a = *a;
+  k.G = a->HQ / a->HKV;
+  k.IG = a->HQ / a->HI;
+  k.UK = pl.UK;
+  k.upb = pl.upb;
+  k.n_remote_units = pl.n_remote_units;
+  k.n_units = pl.n_units;
+  k.upw = pl.upw;
+  k.nsplit = pl.nsplit;
+  k.pstride = pl.pstride;
+  k.scale_l2 = a->scale * kLog2e;
+  if (need > 0) {
+    const size_t cnt = ((size_t)pl.rowheads * 4 + 255) / 256 * 256;
+    k.cnt = reinterpret_cast<uint32_t*>(workspace);
+    k.part = reinterpret_cast<float*>(reinterpret_cast<char*>(workspace) + cnt);
+  }
+  const int64_t grid = pl.rowheads * pl.nsplit;
+  if (grid > 0x7fffffff) {
+    set_error("decode: grid too large");
+    return SRSWA_UNSUPPORTED;
+  }
+  hipStream_t st = reinterpret_cast<hipStream_t>(stream);
+  switch (a->in_dtype) {
+    case SRSWA_F32: return dispatch_out<float>(k, grid, st);
+    case SRSWA_BF16: return dispatch_out<bf16_t>(k, grid, st);
+    case SRSWA_F16: return dispatch_out<__half>(k, grid, st);
+  }
+  return SRSWA_UNSUPPORTED;
+}

@@ -1,0 +1,136 @@
+"""ctypes binding of libsrswa.so (C ABI declared in include/srswa.h).
+
+The library is loaded after ``import torch`` so that it binds to the HIP
+runtime torch already holds (one runtime per process; torch's stream handles
+are then valid inside the library).  There is no CPU fallback: a missing or
+unloadable library raises ``RuntimeError``.
+"""
+
+from __future__ import annotations
+
+import ctypes
+import os
+import threading
+
+import torch  # noqa: F401  (must precede loading the HIP library)
+
+LIB_PATH = os.path.join(os.path.dirname(os.path.abspath(__file__)), "libsrswa.so")
+
+SRSWA_OK = 0
+SRSWA_UNSUPPORTED = 1
+SRSWA_INVALID = 2
+SRSWA_WORKSPACE = 3
+SRSWA_LAUNCH = 4
+
+SRSWA_F32 = 0
+SRSWA_BF16 = 1
+SRSWA_F16 = 2
+
+_i64 = ctypes.c_int64
+_i32 = ctypes.c_int32
+_vp = ctypes.c_void_p
+
+
+class DecodeArgs(ctypes.Structure):
+    """Mirror of ``srswa_decode_args``."""
+
+    _fields_ = [
+        ("q", _vp), ("q_sb", _i64), ("q_sq", _i64), ("q_sh", _i64),
+        ("k", _vp), ("k_sb", _i64), ("k_st", _i64), ("k_sh", _i64),
+        ("v", _vp), ("v_sb", _i64), ("v_st", _i64), ("v_sh", _i64),
+        ("idx", _vp), ("idx_sb", _i64), ("idx_sh", _i64), ("idx_sq", _i64), ("idx_ss", _i64),
+        ("bias", _vp),
+        ("valid", _vp),
+        ("q_pos", _vp), ("pos_sb", _i64), ("pos_sq", _i64),
+        ("kv_len", _vp),
+        ("out", _vp), ("o_sb", _i64), ("o_sq", _i64), ("o_sh", _i64),
+        ("lse", _vp), ("lse_sb", _i64), ("lse_sq", _i64), ("lse_sh", _i64),
+        ("B", _i32), ("Lq", _i32), ("HQ", _i32), ("HKV", _i32), ("HI", _i32), ("D", _i32),
+        ("S", _i32), ("L", _i32),
+        ("block_size", _i32), ("local_window", _i32),
+        ("scale", ctypes.c_float),
+        ("in_dtype", _i32), ("out_dtype", _i32),
+    ]
+
+
+# name -> (restype, argtypes) of every exported entry point
+SIGNATURES = {
+    "srswa_version": (ctypes.c_int, []),
+    "srswa_last_error": (ctypes.c_char_p, []),
+    "srswa_gather_decode_workspace": (ctypes.c_size_t, [ctypes.POINTER(DecodeArgs)]),
+    "srswa_gather_decode": (ctypes.c_int, [ctypes.POINTER(DecodeArgs), _vp, ctypes.c_size_t, _vp]),
+}
+
+STRUCTS = {"srswa_decode_args": DecodeArgs}
+
+_lib = None
+_lock = threading.Lock()
+
+
+class UnsupportedShape(Exception):
+    """The kernels do not cover this shape/dtype (reference contract: caller falls back)."""
+
+
+def lib() -> ctypes.CDLL:
+    global _lib
+    if _lib is not None:
+        return _lib
+    with _lock:
+        if _lib is None:
+            if not os.path.exists(LIB_PATH):
+                raise RuntimeError(
+                    f"libsrswa.so not built ({LIB_PATH}); run "
+                    "`python unlimited-ocr_amd/build.py` (hipcc, gfx950)")
+            l = ctypes.CDLL(LIB_PATH)
+            for name, (res, args) in SIGNATURES.items():
+                fn = getattr(l, name)
+                fn.restype = res
+                fn.argtypes = args
+            _lib = l
+    return _lib
+
+
+def check(status: int, what: str) -> None:
+    if status == SRSWA_OK:
+        return
+    msg = lib().srswa_last_error().decode(errors="replace")
+    if status == SRSWA_UNSUPPORTED:
+        raise UnsupportedShape(f"{what}: {msg}")
+    raise RuntimeError(f"{what} failed (status {status}): {msg}")
+
+
+def dtype_code(dt: torch.dtype) -> int:
+    if dt == torch.float32:
+        return SRSWA_F32
+    if dt == torch.bfloat16:
+        return SRSWA_BF16
+    if dt == torch.float16:
+        return SRSWA_F16
+    raise UnsupportedShape(f"dtype {dt} not supported")
+
+
+def stream_ptr(device: torch.device) -> int:
+    return torch.cuda.current_stream(device).cuda_stream
+
+
+def ptr(t) -> int | None:
+    return None if t is None else t.data_ptr()
+
+
+_ws_cache: dict = {}
+
+
+def workspace(device: torch.device, nbytes: int) -> torch.Tensor | None:
+    """Zero-filled device workspace cached per (device, stream).
+
+    The kernels that use a workspace leave it zero-filled again, so the cached
+    buffer is reused across calls on the same stream (calls on one stream are
+    ordered; different streams get different buffers)."""
+    if nbytes <= 0:
+        return None
+    key = (device.index, torch.cuda.current_stream(device).cuda_stream)
+    buf = _ws_cache.get(key)
+    if buf is None or buf.numel() < nbytes:
+        buf = torch.zeros(max(nbytes, 1 << 20), dtype=torch.uint8, device=device)
+        _ws_cache[key] = buf
+    return buf

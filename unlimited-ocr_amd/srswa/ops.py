@@ -1,0 +1,158 @@
+"""Torch-facing SR-SWA operators (device tensors in, device tensors out).
+
+Each function validates shapes on the host, builds the C-ABI argument struct
+from tensor pointers/strides (no ``.contiguous()`` copies of q/k/v), and
+launches on torch's current stream.  Unsupported shapes raise
+``UnsupportedShape``; nothing here runs on the CPU.
+"""
+
+from __future__ import annotations
+
+import ctypes
+
+import torch
+
+from . import _lib
+from ._lib import UnsupportedShape
+
+
+def _require_cuda(*ts):
+    for t in ts:
+        if t is not None and not t.is_cuda:
+            raise RuntimeError("srswa ops take device (cuda/hip) tensors; there is no CPU path")
+
+
+def _i32(t: torch.Tensor) -> torch.Tensor:
+    return t if t.dtype == torch.int32 else t.to(torch.int32)
+
+
+class _Launch:
+    """A prepared launch: the C-ABI struct, the tensors it points into (kept
+    alive), the workspace and the entry point.  ``__call__`` enqueues the
+    kernel on the stream captured at preparation time without rebuilding
+    anything (a few microseconds of host time)."""
+
+    def __init__(self, fn, args, keep, ws, nbytes, stream, what):
+        self.fn, self.args, self.keep, self.ws, self.nbytes = fn, args, keep, ws, nbytes
+        self.stream, self.what = stream, what
+        self._ref = ctypes.byref(args)
+        self._ws = _lib.ptr(ws)
+
+    def __call__(self):
+        _lib.check(self.fn(self._ref, self._ws, self.nbytes, self.stream), self.what)
+
+
+def prepare_gather_decode(q, k_cache, v_cache, block_indices, q_pos, *, block_size, local_window,
+                          scale, bias=None, valid=None, kv_len=None, out=None, out_dtype=None,
+                          return_lse=False):
+    """Validate, allocate outputs and build the launch of ``gather_decode``.
+
+    Returns (launch, out, lse); ``launch()`` runs the kernel (again) into
+    ``out``/``lse``.  Shapes as in ``gather_decode``."""
+    _require_cuda(q, k_cache, v_cache, block_indices, q_pos, bias, valid, kv_len, out)
+    squeeze = q.dim() == 3
+    if squeeze:
+        q = q.unsqueeze(1)
+        block_indices = block_indices.unsqueeze(2)
+        if bias is not None:
+            bias = bias.unsqueeze(2)
+        if valid is not None:
+            valid = valid.unsqueeze(2)
+        if q_pos.dim() == 1:
+            q_pos = q_pos.unsqueeze(1)
+    B, Lq, HQ, D = q.shape
+    Bk, L, HKV, Dk = k_cache.shape
+    if Bk != B or Dk != D or tuple(v_cache.shape) != tuple(k_cache.shape):
+        raise ValueError(f"cache shape {tuple(k_cache.shape)} / {tuple(v_cache.shape)} vs q {tuple(q.shape)}")
+    HI, S = block_indices.shape[1], block_indices.shape[-1]
+    if tuple(block_indices.shape) != (B, HI, Lq, S):
+        raise ValueError(f"block_indices shape {tuple(block_indices.shape)} != {(B, HI, Lq, S)}")
+    if q.dtype != k_cache.dtype or q.dtype != v_cache.dtype:
+        raise ValueError("q, k_cache, v_cache must share a dtype")
+    for t in (q, k_cache, v_cache):
+        if t.stride(-1) != 1:
+            raise UnsupportedShape("head dim must be contiguous")
+    idx = _i32(block_indices).contiguous()
+    if bias is not None:
+        bias = bias.to(torch.float32).expand(idx.shape).contiguous()
+    if valid is not None:
+        valid = valid.to(torch.bool).expand(idx.shape).contiguous().view(torch.uint8)
+    pos = _i32(q_pos).contiguous()
+    if tuple(pos.shape) != (B, Lq):
+        raise ValueError(f"q_pos shape {tuple(pos.shape)} != {(B, Lq)}")
+    kvl = None if kv_len is None else _i32(kv_len).contiguous()
+    odt = out_dtype or q.dtype
+    if out is None:
+        out = torch.empty(B, Lq, HQ, D, dtype=odt, device=q.device)
+    elif squeeze:
+        out = out.unsqueeze(1)
+    lse = torch.empty(B, Lq, HQ, dtype=torch.float32, device=q.device) if return_lse else None
+
+    a = _lib.DecodeArgs()
+    a.q = q.data_ptr(); a.q_sb, a.q_sq, a.q_sh = q.stride(0), q.stride(1), q.stride(2)
+    a.k = k_cache.data_ptr(); a.k_sb, a.k_st, a.k_sh = k_cache.stride(0), k_cache.stride(1), k_cache.stride(2)
+    a.v = v_cache.data_ptr(); a.v_sb, a.v_st, a.v_sh = v_cache.stride(0), v_cache.stride(1), v_cache.stride(2)
+    a.idx = idx.data_ptr()
+    a.idx_sb, a.idx_sh, a.idx_sq, a.idx_ss = idx.stride(0), idx.stride(1), idx.stride(2), idx.stride(3)
+    a.bias = _lib.ptr(bias)
+    a.valid = _lib.ptr(valid)
+    a.q_pos = pos.data_ptr(); a.pos_sb, a.pos_sq = pos.stride(0), pos.stride(1)
+    a.kv_len = _lib.ptr(kvl)
+    a.out = out.data_ptr(); a.o_sb, a.o_sq, a.o_sh = out.stride(0), out.stride(1), out.stride(2)
+    if lse is not None:
+        a.lse = lse.data_ptr(); a.lse_sb, a.lse_sq, a.lse_sh = lse.stride(0), lse.stride(1), lse.stride(2)
+    a.B, a.Lq, a.HQ, a.HKV, a.HI, a.D, a.S, a.L = B, Lq, HQ, HKV, HI, D, S, L
+    a.block_size, a.local_window = int(block_size), max(1, int(local_window))
+    a.scale = float(scale)
+    a.in_dtype = _lib.dtype_code(q.dtype)
+    a.out_dtype = _lib.dtype_code(odt)
+    L_ = _lib.lib()
+    nbytes = L_.srswa_gather_decode_workspace(ctypes.byref(a))
+    ws = _lib.workspace(q.device, nbytes)
+    launch = _Launch(L_.srswa_gather_decode, a, (q, k_cache, v_cache, idx, bias, valid, pos, kvl, out, lse),
+                     ws, nbytes, _lib.stream_ptr(q.device), "srswa_gather_decode")
+    if squeeze:
+        out = out.squeeze(1)
+        if lse is not None:
+            lse = lse.squeeze(1)
+    return launch, out, lse
+
+
+def gather_decode(q, k_cache, v_cache, block_indices, q_pos, *, block_size, local_window,
+                  scale, bias=None, valid=None, kv_len=None, out=None, out_dtype=None,
+                  return_lse=False):
+    """Block-sparse decode attention over a KV cache.
+
+    q            [B, Lq, HQ, D] (or [B, HQ, D] for one row per sequence)
+    k_cache      [B, L, HKV, D] any strides with unit head-dim stride
+    v_cache      [B, L, HKV, D]
+    block_indices[B, HI, Lq, S] (or [B, HI, S]) block ids, -1 = empty slot
+    q_pos        [B, Lq] (or [B]) absolute query positions
+    bias, valid  like block_indices (fp32 / bool), optional
+    kv_len       [B] cache fill (keys >= kv_len are never read), optional
+    Returns o [B, Lq, HQ, D] (or [B, HQ, D]) in ``out_dtype`` (default q.dtype)
+    and, if asked, lse [B, Lq, HQ] (natural log).
+    """
+    launch, out, lse = prepare_gather_decode(
+        q, k_cache, v_cache, block_indices, q_pos, block_size=block_size,
+        local_window=local_window, scale=scale, bias=bias, valid=valid, kv_len=kv_len,
+        out=out, out_dtype=out_dtype, return_lse=return_lse)
+    launch()
+    return (out, lse) if return_lse else out
+
+
+def decode_attend(q, k_all, v_all, topi, bias, valid, q_pos, block_size, local_window, scale):
+    """Drop-in for ``_decode_attend`` (HF/modeling_deepseekv2.py:454-481).
+
+    q [B,H,Lq,D]; k_all, v_all [B,Hkv,S,D]; topi/bias/valid [B,Lq,K] (one
+    index head for all heads, as the reference) or [B,HI,Lq,K]; q_pos [B,Lq].
+    Returns fp32 [B,H,Lq,D] like the reference (which computes in fp32)."""
+    if topi.dim() == 3:
+        topi, bias, valid = topi[:, None], bias[:, None], valid[:, None]
+    qv = q.transpose(1, 2)                   # [B,Lq,H,D] view
+    kv = k_all.transpose(1, 2)               # [B,S,Hkv,D] view
+    vv = v_all.transpose(1, 2)
+    o = gather_decode(qv, kv, vv, topi, q_pos, block_size=block_size,
+                      local_window=local_window, scale=scale, bias=bias, valid=valid,
+                      out_dtype=torch.float32)
+    return o.transpose(1, 2)
