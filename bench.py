@@ -122,7 +122,7 @@ def bench_decode(args):
     torch.cuda.synchronize()
     wall = time.perf_counter() - t0
     ms = e0.elapsed_time(e1) / args.steps
-    _log(f"timed {args.steps} steps: {ms * 1e3:.2f} us/step (HIP events), wall {wall * 1e3 / args.steps:.2f} us/step")
+    _log(f"timed {args.steps} steps: {ms * 1e3:.2f} us/step (HIP events), wall {wall * 1e6 / args.steps:.2f} us/step")
     nbytes = W.decode_bytes(B, H, D, K, BS, LW)
     achieved = nbytes / (ms * 1e-3) / 1e9
     res = {
@@ -148,7 +148,7 @@ def bench_decode(args):
         "roofline": {"bound": "hbm", "achieved": achieved, "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": achieved / HBM_PEAK_GBS, "traffic": _pmc_traffic("decode_cfg3_traffic"),
                      "algorithmic_bytes_per_launch": nbytes,
-                     "kernel": "srswa::decode_kernel<bf16,bf16,128,16>"},
+                     "kernel": "srswa::decode_kernel<bf16,bf16,128,8> + decode_merge_kernel (one step)"},
     }
     # parity spot check of the timed output against the oracle on 2 sequences
     if not args.no_check:

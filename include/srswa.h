@@ -76,12 +76,58 @@ typedef struct {
   int32_t in_dtype, out_dtype;                         /* srswa_dtype               */
 } srswa_decode_args;
 
-size_t srswa_gather_decode_workspace(const srswa_decode_args* a);
-/* workspace: device memory of srswa_gather_decode_workspace() bytes whose
- * first call on it finds it zero-filled; the kernels leave it zero-filled
- * again, so it can be reused by later calls on the same stream. */
-int srswa_gather_decode(const srswa_decode_args* a, void* workspace, size_t workspace_bytes,
-                        void* stream);
+/* Workspace query.  scratch: device bytes with no initial-content
+ * requirement; counters: uint32 arrival counters that must be zero before the
+ * first call and that every call leaves zero again (keep one zero-filled
+ * buffer per stream and pass a prefix of it; calls that overlap on one
+ * buffer race). */
+void srswa_gather_decode_workspace(const srswa_decode_args* a, size_t* scratch_bytes,
+                                   size_t* counters);
+int srswa_gather_decode(const srswa_decode_args* a, void* scratch, size_t scratch_bytes,
+                        uint32_t* counters, size_t n_counters, void* stream);
+
+/* ------------------------------------------------------------------------
+ * Block indexer: head_cls / mean-pool block summaries, remote block scores
+ * and top-k selection.  Replaces:
+ *   - _block_scores_infer (stage0 "head_cls")  HF/modeling_deepseekv2.py:380-417
+ *   - DashAttention._block_scores_headcls       HF/dash_attention.py:1053-1143
+ *   - _summary_keys / _score_rows               WHL!layers/attention/unlimited_dash_ops/dash_stage0.py:25-58
+ *   - block_scores.topk(k), -1 for empty slots  HF/_sparse_base_impl.py:3100-3105
+ * k_bar[b,h,blk] = softmax over the block's real keys (pos < kv_len) of
+ * clamp(k.head_cls/sqrt(D)) weighting the keys (head_cls NULL -> plain mean);
+ * score = clamp(q.k_bar/sqrt(D), +-1e4) when blk <= q_pos/BS - local_blocks and
+ * the block holds a real key, else -1e9.  Top-k: descending score, equal
+ * scores -> lower block id, entries <= -5e8 are never selected, missing slots
+ * -1; ascending != 0 re-packs the selected ids in ascending id order.
+ * ---------------------------------------------------------------------- */
+typedef struct {
+  const float* q;      int64_t q_sb, q_sh, q_sq;       /* [B, HI, Lq, D] fp32 index queries   */
+  const void* k;       int64_t k_sb, k_st, k_sh;       /* [B, L, HI, D] index keys; k_sh = 0
+                                                          shares one key head across HI        */
+  float* kbar_out;     int64_t kb_sb, kb_sh, kb_sn;    /* [B, HI, nblk, D] fp32 summaries; NULL = not stored */
+  const float* head_cls;                               /* [D] fp32 summary query; NULL = mean  */
+  const int32_t* q_pos; int64_t pos_sb, pos_sq;        /* [B, Lq] absolute positions          */
+  const int32_t* kv_len;                               /* [B] real keys; NULL = L             */
+  float* scores;       int64_t sc_sb, sc_sh, sc_sq;    /* [B, HI, Lq, nblk] fp32; NULL = scratch */
+  int32_t* topk_idx;   int64_t ti_sb, ti_sh, ti_sq;    /* [B, HI, Lq, K] int32; NULL = no top-k */
+  float* topk_val;                                     /* same strides as topk_idx; NULL = skip */
+  int32_t B, HI, Lq, D, L, nblk, block_size, local_blocks, K, ascending;
+  int32_t k_dtype;                                     /* srswa_dtype of k                    */
+} srswa_index_args;
+
+/* scratch bytes needed when scores == NULL and topk_idx != NULL */
+size_t srswa_index_workspace(const srswa_index_args* a);
+int srswa_index_meanpool_topk(const srswa_index_args* a, void* scratch, size_t scratch_bytes,
+                              void* stream);
+
+/* Top-k of rows of fp32 scores (rows x n, row_stride apart): the K largest
+ * entries > invalid_at per row, descending, equal scores -> lower index,
+ * missing slots -1 (value -inf).  K <= 64.  Replaces block_scores.topk(k) +
+ * masked_fill(score == -inf, -1) (HF/_sparse_base_impl.py:3100-3105,
+ * 3396-3403). */
+int srswa_topk_rows(const float* scores, int64_t rows, int32_t n, int64_t row_stride, int32_t K,
+                    int32_t ascending, float invalid_at, int32_t* out_idx, float* out_val,
+                    int64_t out_stride, void* stream);
 
 #ifdef __cplusplus
 }

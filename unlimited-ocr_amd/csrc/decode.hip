@@ -18,11 +18,12 @@
 //   * online softmax in the log2 domain (wave max/sum via shuffles), p is
 //     broadcast back through 256 bytes of LDS per wave, then o += p v;
 // Four waves (one workgroup) merge their (m, l, o) in LDS; the workgroups of
-// one (row, head) merge through a small workspace, the last one to finish
+// one (row, head) merge through a scratch buffer, the last one to finish
 // (atomic arrival counter) producing the output.  No host sync, no second
-// kernel, the workspace is left zeroed for the next call.
+// kernel; the arrival counters are left zeroed for the next call.
 #include <stdarg.h>
 #include <stdio.h>
+#include <stdlib.h>
 #include <string.h>
 
 #include "common.h"
@@ -58,6 +59,7 @@ struct DecodeK {
   int G, IG;
   int UK, upb, n_remote_units, n_units, upw, nsplit, pstride;
   float scale_l2;      // scale * log2(e)
+  int64_t rowheads;
   float* part;
   uint32_t* cnt;
 };
@@ -66,6 +68,10 @@ template <typename TO>
 __device__ __forceinline__ void store_out(TO* dst, const float* f, int n);
 template <>
 __device__ __forceinline__ void store_out<float>(float* dst, const float* f, int n) {
+  if (n % 4 != 0) {
+    for (int e = 0; e < n; ++e) dst[e] = f[e];
+    return;
+  }
   for (int e = 0; e < n; e += 4)
     *reinterpret_cast<uint4*>(dst + e) = Vec16<float>::pack(f + e);
 }
@@ -73,6 +79,8 @@ template <>
 __device__ __forceinline__ void store_out<bf16_t>(bf16_t* dst, const float* f, int n) {
   if (n == 8) {
     *reinterpret_cast<uint4*>(dst) = Vec16<bf16_t>::pack(f);
+  } else if (n == 1) {
+    dst->bits = f32_to_bf16_rne(f[0]);
   } else {
     for (int e = 0; e < n; e += 2)
       *reinterpret_cast<uint32_t*>(dst + e) = pack_bf16x2(f[e], f[e + 1]);
@@ -82,24 +90,60 @@ template <>
 __device__ __forceinline__ void store_out<__half>(__half* dst, const float* f, int n) {
   if (n == 8) {
     *reinterpret_cast<uint4*>(dst) = Vec16<__half>::pack(f);
+  } else if (n == 1) {
+    *dst = __float2half_rn(f[0]);
   } else {
     for (int e = 0; e < n; e += 2)
       *reinterpret_cast<uint32_t*>(dst + e) = pack_h16x2(f[e], f[e + 1]);
   }
 }
 
-// q.k over one 16-byte chunk.
-template <typename T>
-__device__ __forceinline__ float dot16(const uint4& w, const float* qf) {
-  float f[Vec16<T>::N];
-  Vec16<T>::unpack(w, f);
-  float s = 0.f;
-#pragma unroll
-  for (int e = 0; e < Vec16<T>::N; ++e) s = fmaf(qf[e], f[e], s);
-  return s;
+// q.k over one 16-byte chunk: packed bf16/fp16 dot2 (v_dot2_f32_bf16 /
+// v_dot2_f32_f16: exact products, fp32 accumulation) or fp32 FMAs.
+template <typename T> struct QFrag;
+template <> struct QFrag<float> {
+  float f[4];
+  __device__ __forceinline__ void load(const float* p) {
+    Vec16<float>::unpack(*reinterpret_cast<const uint4*>(p), f);
+  }
+  __device__ __forceinline__ float dot(const uint4& w) const {
+    float s = f[0] * __uint_as_float(w.x);
+    s = fmaf(f[1], __uint_as_float(w.y), s);
+    s = fmaf(f[2], __uint_as_float(w.z), s);
+    return fmaf(f[3], __uint_as_float(w.w), s);
+  }
+};
+typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
+typedef _Float16 f16x2_t __attribute__((ext_vector_type(2)));
+template <> struct QFrag<bf16_t> {
+  uint4 w;
+  __device__ __forceinline__ void load(const bf16_t* p) { w = *reinterpret_cast<const uint4*>(p); }
+  __device__ __forceinline__ float dot(const uint4& k) const {
+    float s = __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2_t, w.x), __builtin_bit_cast(bf16x2_t, k.x), 0.f, false);
+    s = __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2_t, w.y), __builtin_bit_cast(bf16x2_t, k.y), s, false);
+    s = __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2_t, w.z), __builtin_bit_cast(bf16x2_t, k.z), s, false);
+    return __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2_t, w.w), __builtin_bit_cast(bf16x2_t, k.w), s, false);
+  }
+};
+template <> struct QFrag<__half> {
+  uint4 w;
+  __device__ __forceinline__ void load(const __half* p) { w = *reinterpret_cast<const uint4*>(p); }
+  __device__ __forceinline__ float dot(const uint4& k) const {
+    float s = __builtin_amdgcn_fdot2(__builtin_bit_cast(f16x2_t, w.x), __builtin_bit_cast(f16x2_t, k.x), 0.f, false);
+    s = __builtin_amdgcn_fdot2(__builtin_bit_cast(f16x2_t, w.y), __builtin_bit_cast(f16x2_t, k.y), s, false);
+    s = __builtin_amdgcn_fdot2(__builtin_bit_cast(f16x2_t, w.z), __builtin_bit_cast(f16x2_t, k.z), s, false);
+    return __builtin_amdgcn_fdot2(__builtin_bit_cast(f16x2_t, w.w), __builtin_bit_cast(f16x2_t, k.w), s, false);
+  }
+};
+
+// streaming 16-byte load (K/V rows are read once per call)
+typedef unsigned int u32x4_t __attribute__((ext_vector_type(4)));
+__device__ __forceinline__ uint4 load_stream(const void* p) {
+  const u32x4_t v = __builtin_nontemporal_load(reinterpret_cast<const u32x4_t*>(p));
+  return make_uint4(v.x, v.y, v.z, v.w);
 }
 
-template <typename T, typename TO, int D, int NI>
+template <typename T, typename TO, int D, int NI, bool ATOMIC_MERGE>
 __global__ __launch_bounds__(kDecodeWaves * kWave) void decode_kernel(DecodeK p) {
   using V = Vec16<T>;
   constexpr int EPV = V::N;           // elements per 16-byte vector
@@ -136,12 +180,9 @@ __global__ __launch_bounds__(kDecodeWaves * kWave) void decode_kernel(DecodeK p)
   const int remote_end = min(ws, last + 1);            // remote keys are < this
 
   // this lane's slice of q
-  float qf[EPV];
-  {
-    const T* qrow = reinterpret_cast<const T*>(a.q) + (int64_t)b * a.q_sb +
-                    (int64_t)lq * a.q_sq + (int64_t)hq * a.q_sh + c * EPV;
-    V::unpack(*reinterpret_cast<const uint4*>(qrow), qf);
-  }
+  QFrag<T> qf;
+  qf.load(reinterpret_cast<const T*>(a.q) + (int64_t)b * a.q_sb + (int64_t)lq * a.q_sq +
+          (int64_t)hq * a.q_sh + c * EPV);
   const int32_t* idx_row = a.idx + (int64_t)b * a.idx_sb + (int64_t)ih * a.idx_sh +
                            (int64_t)lq * a.idx_sq;
   const int64_t aux_off = (int64_t)b * a.idx_sb + (int64_t)ih * a.idx_sh +
@@ -158,6 +199,29 @@ __global__ __launch_bounds__(kDecodeWaves * kWave) void decode_kernel(DecodeK p)
 #pragma unroll
   for (int e = 0; e < EPV; ++e) acc[e] = 0.f;
 
+  // Slot metadata in one round trip: lane s holds slot s (S <= 64) -- its id,
+  // whether it survives (valid, in range, first slot holding that id) and its
+  // bias.  Wider rows (S > 64) re-read the slots per unit instead.
+  const bool slots_in_regs = a.S <= kWave;
+  int my_bid = -1;
+  bool my_ok = false;
+  float my_bias = 0.f;
+  if (slots_in_regs && lane < a.S) {
+    my_bid = idx_row[(int64_t)lane * a.idx_ss];
+    my_ok = my_bid >= 0 && my_bid <= max_blk &&
+            (!a.valid || a.valid[aux_off + (int64_t)lane * a.idx_ss]);
+    if (a.bias) my_bias = a.bias[aux_off + (int64_t)lane * a.idx_ss];
+  }
+  if (slots_in_regs) {
+    bool dup = false;
+    for (int j = 0; j < a.S - 1; ++j) {
+      const int bj = __shfl(my_bid, j, kWave);
+      const bool okj = __shfl(my_ok ? 1 : 0, j, kWave) != 0;
+      dup |= (j < lane) && okj && (bj == my_bid);
+    }
+    my_ok = my_ok && !dup;
+  }
+
   const int u_begin = (split * kDecodeWaves + wave) * p.upw;
   const int u_end = min(u_begin + p.upw, p.n_units);
   for (int u = u_begin; u < u_end; ++u) {
@@ -165,21 +229,31 @@ __global__ __launch_bounds__(kDecodeWaves * kWave) void decode_kernel(DecodeK p)
     float bias_l2 = 0.f;
     if (u < p.n_remote_units) {
       const int slot = u / p.upb, sub = u % p.upb;
-      const int bid = idx_row[(int64_t)slot * a.idx_ss];
-      bool ok = bid >= 0 && bid <= max_blk && (!a.valid || a.valid[aux_off + (int64_t)slot * a.idx_ss]);
-      // a repeat of an id held by an earlier valid slot is skipped
-      for (int s0 = 0; ok && s0 < slot; s0 += kWave) {
-        const int s = s0 + lane;
-        bool dup = false;
-        if (s < slot) {
-          const int o = idx_row[(int64_t)s * a.idx_ss];
-          dup = (o == bid) && (!a.valid || a.valid[aux_off + (int64_t)s * a.idx_ss]);
+      int bid;
+      bool ok;
+      float bias = 0.f;
+      if (slots_in_regs) {
+        bid = __shfl(my_bid, slot, kWave);
+        ok = __shfl(my_ok ? 1 : 0, slot, kWave) != 0;
+        bias = __shfl(my_bias, slot, kWave);
+      } else {
+        bid = idx_row[(int64_t)slot * a.idx_ss];
+        ok = bid >= 0 && bid <= max_blk && (!a.valid || a.valid[aux_off + (int64_t)slot * a.idx_ss]);
+        // a repeat of an id held by an earlier valid slot is skipped
+        for (int s0 = 0; ok && s0 < slot; s0 += kWave) {
+          const int s = s0 + lane;
+          bool d = false;
+          if (s < slot) {
+            const int o = idx_row[(int64_t)s * a.idx_ss];
+            d = (o == bid) && (!a.valid || a.valid[aux_off + (int64_t)s * a.idx_ss]);
+          }
+          if (__any(d)) ok = false;
         }
-        if (__any(dup)) ok = false;
+        if (ok && a.bias) bias = a.bias[aux_off + (int64_t)slot * a.idx_ss];
       }
       k0 = ok ? bid * a.block_size + sub * UK : 0;
       k1 = ok ? min(min(k0 + UK, bid * a.block_size + a.block_size), remote_end) : 0;
-      if (ok && a.bias) bias_l2 = a.bias[aux_off + (int64_t)slot * a.idx_ss] * kLog2e;
+      bias_l2 = bias * kLog2e;
     } else {
       k0 = ws + (u - p.n_remote_units) * UK;
       k1 = min(k0 + UK, last + 1);
@@ -190,19 +264,19 @@ __global__ __launch_bounds__(kDecodeWaves * kWave) void decode_kernel(DecodeK p)
 #pragma unroll
     for (int i = 0; i < NI; ++i) {
       const int key = k0 + i * RPI + r;
-      kr[i] = key < k1 ? *reinterpret_cast<const uint4*>(kbase + (int64_t)key * a.k_st)
+      kr[i] = key < k1 ? load_stream(kbase + (int64_t)key * a.k_st)
                        : make_uint4(0, 0, 0, 0);
     }
 #pragma unroll
     for (int i = 0; i < NI; ++i) {
       const int key = k0 + i * RPI + r;
-      vr[i] = key < k1 ? *reinterpret_cast<const uint4*>(vbase + (int64_t)key * a.v_st)
+      vr[i] = key < k1 ? load_stream(vbase + (int64_t)key * a.v_st)
                        : make_uint4(0, 0, 0, 0);
     }
 
     float part[NI];
 #pragma unroll
-    for (int i = 0; i < NI; ++i) part[i] = dot16<T>(kr[i], qf);
+    for (int i = 0; i < NI; ++i) part[i] = qf.dot(kr[i]);
     // reduce-scatter across the LPR lanes of a row: NI partials -> 1 score
 #pragma unroll
     for (int n = NI, o = LPR / 2; n > 1; n >>= 1, o >>= 1) {
@@ -223,7 +297,7 @@ __global__ __launch_bounds__(kDecodeWaves * kWave) void decode_kernel(DecodeK p)
     const float mnew = fmaxf(m, wave_max(t));     // finite: key k0 is always kept
     const float alpha = exp2f(m - mnew);
     const float pj = exp2f(t - mnew);
-    l = l * alpha + wave_sum(owner ? pj : 0.f);
+    l = l * alpha + (owner ? pj : 0.f);   // per-lane; summed over the wave once at the end
     m = mnew;
 #pragma unroll
     for (int e = 0; e < EPV; ++e) acc[e] *= alpha;
@@ -254,6 +328,7 @@ __global__ __launch_bounds__(kDecodeWaves * kWave) void decode_kernel(DecodeK p)
 #pragma unroll
     for (int e = 0; e < EPV; ++e) s_o[wave][c * EPV + e] = acc[e];
   }
+  l = wave_sum(l);
   if (lane == 0) { s_m[wave] = m; s_l[wave] = l; }
   __syncthreads();
   if (wave != 0) return;
@@ -280,13 +355,14 @@ __global__ __launch_bounds__(kDecodeWaves * kWave) void decode_kernel(DecodeK p)
     float* rec = p.part + (rh * p.nsplit + split) * p.pstride;
     if (r == 0) store_out<float>(rec + c * EPV, O, EPV);
     if (lane == 0) { rec[D] = M; rec[D + 1] = L; }
+    if (!ATOMIC_MERGE) return;   // decode_merge_kernel combines the records
     __threadfence();
     uint32_t arrived = 0;
     if (lane == 0) arrived = atomicAdd(&p.cnt[rh], 1u);
     arrived = __shfl(arrived, 0, kWave);
     if (arrived != (uint32_t)(p.nsplit - 1)) return;
     __threadfence();
-    if (lane == 0) p.cnt[rh] = 0u;   // leave the workspace zeroed
+    if (lane == 0) p.cnt[rh] = 0u;   // leave the counter zeroed for the next call
     const float* recs = p.part + rh * p.nsplit * p.pstride;
     M = -INFINITY;
     for (int s = 0; s < p.nsplit; ++s) M = fmaxf(M, recs[s * p.pstride + D]);
@@ -321,12 +397,88 @@ __global__ __launch_bounds__(kDecodeWaves * kWave) void decode_kernel(DecodeK p)
   }
 }
 
+// Combines the per-workgroup (O, M, L) records of every (row, head): one
+// wavefront per (row, head), D/64 dims per lane.
+template <typename TO, int D>
+__global__ __launch_bounds__(256) void decode_merge_kernel(DecodeK p) {
+  constexpr int DPL = D / kWave;   // dims per lane
+  const srswa_decode_args& a = p.a;
+  const int wave = threadIdx.x / kWave, lane = threadIdx.x % kWave;
+  const int64_t rh = (int64_t)blockIdx.x * 4 + wave;
+  if (rh >= p.rowheads) return;
+  const float* recs = p.part + rh * p.nsplit * p.pstride;
+  float M = -INFINITY, L = 0.f, O[DPL];
+#pragma unroll
+  for (int e = 0; e < DPL; ++e) O[e] = 0.f;
+  for (int s0 = 0; s0 < p.nsplit; s0 += 8) {
+    // issue all loads of up to 8 records before combining them
+    float ms[8], ls[8], os[8][DPL];
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      const bool in = s0 + j < p.nsplit;
+      const float* rec = recs + (int64_t)(in ? s0 + j : s0) * p.pstride;
+      ms[j] = in ? rec[D] : -INFINITY;
+      ls[j] = in ? rec[D + 1] : 0.f;
+#pragma unroll
+      for (int e = 0; e < DPL; ++e) os[j][e] = in ? rec[lane * DPL + e] : 0.f;
+    }
+    float Mn = M;
+#pragma unroll
+    for (int j = 0; j < 8; ++j) Mn = fmaxf(Mn, ms[j]);
+    const float r0 = M == -INFINITY ? 0.f : exp2f(M - Mn);
+    L *= r0;
+#pragma unroll
+    for (int e = 0; e < DPL; ++e) O[e] *= r0;
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      const float wt = ms[j] == -INFINITY ? 0.f : exp2f(ms[j] - Mn);
+      L = fmaf(ls[j], wt, L);
+#pragma unroll
+      for (int e = 0; e < DPL; ++e) O[e] = fmaf(os[j][e], wt, O[e]);
+    }
+    M = Mn;
+  }
+  const float inv = L > 0.f ? 1.f / L : 0.f;
+#pragma unroll
+  for (int e = 0; e < DPL; ++e) O[e] *= inv;
+  const int hq = (int)(rh % a.HQ);
+  const int64_t bl = rh / a.HQ;
+  const int lq = (int)(bl % a.Lq);
+  const int b = (int)(bl / a.Lq);
+  TO* orow = reinterpret_cast<TO*>(a.out) + (int64_t)b * a.o_sb + (int64_t)lq * a.o_sq +
+             (int64_t)hq * a.o_sh + lane * DPL;
+  store_out<TO>(orow, O, DPL);
+  if (a.lse && lane == 0)
+    a.lse[(int64_t)b * a.lse_sb + (int64_t)lq * a.lse_sq + (int64_t)hq * a.lse_sh] =
+        L > 0.f ? M * kLn2 + logf(L) : -INFINITY;
+}
+
 int elem_bytes(int dt) { return dt == SRSWA_F32 ? 4 : 2; }
 
-// keys per unit for (dtype, D): NI * (64 / LPR)
+// Tuning knobs (environment, read once): SRSWA_DECODE_NI = 8 (default) | 16
+// load instructions per unit (bf16 D=128: 32 | 64 keys); SRSWA_DECODE_UPW =
+// units per wave (default 2); SRSWA_DECODE_MERGE = kernel (a second kernel
+// combines the split records, default) | atomic (the last-arriving workgroup
+// combines them after device-scope fences, which cost ~6x on MI355X: the
+// fences write back / invalidate the per-XCD L2s).
+int env_int(const char* name, int dflt) {
+  const char* v = getenv(name);
+  return (v && *v) ? atoi(v) : dflt;
+}
+bool merge_in_kernel() {
+  static const bool v = [] {
+    const char* m = getenv("SRSWA_DECODE_MERGE");
+    return m && strcmp(m, "atomic") == 0;
+  }();
+  return v;
+}
+
+// row instructions per unit for (dtype, D)
 int decode_ni(int dt, int D) {
+  static const int want = env_int("SRSWA_DECODE_NI", 8);
   const int lpr = D * elem_bytes(dt) / 16;
-  return lpr < 16 ? lpr : 16;
+  const int ni = lpr < 16 ? lpr : 16;
+  return (want == 8 && ni == 16) ? 8 : ni;
 }
 
 DecodePlan make_plan(const srswa_decode_args* a) {
@@ -337,32 +489,45 @@ DecodePlan make_plan(const srswa_decode_args* a) {
   pl.upb = ceil_div(a->block_size, pl.UK);
   pl.n_remote_units = a->S * pl.upb;
   pl.n_units = pl.n_remote_units + ceil_div(a->local_window, pl.UK);
-  pl.upw = 1;
+  static const int upw = env_int("SRSWA_DECODE_UPW", 2);
+  pl.upw = upw > 1 ? upw : 1;
   pl.nsplit = ceil_div(pl.n_units, kDecodeWaves * pl.upw);
   pl.pstride = ceil_div(a->D + 2, 32) * 32;
   pl.rowheads = (int64_t)a->B * a->Lq * a->HQ;
   return pl;
 }
 
-size_t workspace_bytes(const DecodePlan& pl) {
-  if (pl.nsplit <= 1) return 0;
-  const size_t cnt = ((size_t)pl.rowheads * 4 + 255) / 256 * 256;
-  return cnt + (size_t)pl.rowheads * pl.nsplit * pl.pstride * 4;
+size_t scratch_bytes(const DecodePlan& pl) {
+  return pl.nsplit <= 1 ? 0 : (size_t)pl.rowheads * pl.nsplit * pl.pstride * 4;
 }
+size_t counter_count(const DecodePlan& pl) { return pl.nsplit <= 1 ? 0 : (size_t)pl.rowheads; }
 
-template <typename T, typename TO, int D>
-int launch_decode(const DecodeK& k, int64_t grid, hipStream_t st) {
-  constexpr int EPV = Vec16<T>::N;
-  constexpr int LPR = D / EPV;
-  constexpr int NI = LPR < 16 ? LPR : 16;
-  hipLaunchKernelGGL((decode_kernel<T, TO, D, NI>), dim3((unsigned)grid), dim3(kDecodeWaves * kWave),
-                     0, st, k);
+template <typename T, typename TO, int D, int NI>
+int launch_decode_ni(const DecodeK& k, int64_t grid, hipStream_t st) {
+  if (k.nsplit > 1 && merge_in_kernel()) {
+    hipLaunchKernelGGL((decode_kernel<T, TO, D, NI, true>), dim3((unsigned)grid),
+                       dim3(kDecodeWaves * kWave), 0, st, k);
+  } else {
+    hipLaunchKernelGGL((decode_kernel<T, TO, D, NI, false>), dim3((unsigned)grid),
+                       dim3(kDecodeWaves * kWave), 0, st, k);
+    if (k.nsplit > 1)
+      hipLaunchKernelGGL((decode_merge_kernel<TO, D>), dim3((unsigned)((k.rowheads + 3) / 4)),
+                         dim3(256), 0, st, k);
+  }
   const hipError_t e = hipGetLastError();
   if (e != hipSuccess) {
     set_error("decode launch failed: %s", hipGetErrorString(e));
     return SRSWA_LAUNCH;
   }
   return SRSWA_OK;
+}
+
+template <typename T, typename TO, int D>
+int launch_decode(const DecodeK& k, int64_t grid, hipStream_t st) {
+  constexpr int LPR = D / Vec16<T>::N;
+  constexpr int NI_MAX = LPR < 16 ? LPR : 16;
+  if (NI_MAX >= 16 && k.UK == 8 * (kWave / LPR)) return launch_decode_ni<T, TO, D, 8>(k, grid, st);
+  return launch_decode_ni<T, TO, D, NI_MAX>(k, grid, st);
 }
 
 template <typename T>
@@ -393,13 +558,21 @@ using namespace srswa;
 extern "C" int srswa_version(void) { return 100; }
 extern "C" const char* srswa_last_error(void) { return srswa::last_error(); }
 
-extern "C" size_t srswa_gather_decode_workspace(const srswa_decode_args* a) {
-  if (!a) return 0;
-  return workspace_bytes(make_plan(a));
+extern "C" void srswa_gather_decode_workspace(const srswa_decode_args* a, size_t* scratch,
+                                              size_t* counters) {
+  size_t s = 0, c = 0;
+  if (a && a->B > 0 && a->Lq > 0 && a->HQ > 0 && a->D > 0 && a->block_size > 0) {
+    const DecodePlan pl = make_plan(a);
+    s = scratch_bytes(pl);
+    c = counter_count(pl);
+  }
+  if (scratch) *scratch = s;
+  if (counters) *counters = c;
 }
 
-extern "C" int srswa_gather_decode(const srswa_decode_args* a, void* workspace,
-                                   size_t ws_bytes, void* stream) {
+extern "C" int srswa_gather_decode(const srswa_decode_args* a, void* scratch,
+                                   size_t scratch_size, uint32_t* counters, size_t n_counters,
+                                   void* stream) {
   if (!a || !a->q || !a->k || !a->v || !a->out || !a->q_pos || (!a->idx && a->S > 0)) {
     set_error("decode: null argument");
     return SRSWA_INVALID;
@@ -439,9 +612,10 @@ extern "C" int srswa_gather_decode(const srswa_decode_args* a, void* workspace,
     return SRSWA_UNSUPPORTED;
   }
   const DecodePlan pl = make_plan(a);
-  const size_t need = workspace_bytes(pl);
-  if (need > 0 && (!workspace || ws_bytes < need)) {
-    set_error("decode: workspace of %zu bytes required (got %zu)", need, ws_bytes);
+  const size_t need = scratch_bytes(pl), need_cnt = counter_count(pl);
+  if (need > 0 && (!scratch || scratch_size < need || !counters || n_counters < need_cnt)) {
+    set_error("decode: scratch of %zu bytes and %zu counters required (got %zu, %zu)", need,
+              need_cnt, scratch_size, n_counters);
     return SRSWA_WORKSPACE;
   }
   DecodeK k{};
@@ -456,10 +630,10 @@ extern "C" int srswa_gather_decode(const srswa_decode_args* a, void* workspace,
   k.nsplit = pl.nsplit;
   k.pstride = pl.pstride;
   k.scale_l2 = a->scale * kLog2e;
+  k.rowheads = pl.rowheads;
   if (need > 0) {
-    const size_t cnt = ((size_t)pl.rowheads * 4 + 255) / 256 * 256;
-    k.cnt = reinterpret_cast<uint32_t*>(workspace);
-    k.part = reinterpret_cast<float*>(reinterpret_cast<char*>(workspace) + cnt);
+    k.cnt = counters;
+    k.part = reinterpret_cast<float*>(scratch);
   }
   const int64_t grid = pl.rowheads * pl.nsplit;
   if (grid > 0x7fffffff) {

@@ -29,6 +29,7 @@ SRSWA_F16 = 2
 _i64 = ctypes.c_int64
 _i32 = ctypes.c_int32
 _vp = ctypes.c_void_p
+_szp = ctypes.POINTER(ctypes.c_size_t)
 
 
 class DecodeArgs(ctypes.Structure):
@@ -53,15 +54,39 @@ class DecodeArgs(ctypes.Structure):
     ]
 
 
+class IndexArgs(ctypes.Structure):
+    """Mirror of ``srswa_index_args``."""
+
+    _fields_ = [
+        ("q", _vp), ("q_sb", _i64), ("q_sh", _i64), ("q_sq", _i64),
+        ("k", _vp), ("k_sb", _i64), ("k_st", _i64), ("k_sh", _i64),
+        ("kbar_out", _vp), ("kb_sb", _i64), ("kb_sh", _i64), ("kb_sn", _i64),
+        ("head_cls", _vp),
+        ("q_pos", _vp), ("pos_sb", _i64), ("pos_sq", _i64),
+        ("kv_len", _vp),
+        ("scores", _vp), ("sc_sb", _i64), ("sc_sh", _i64), ("sc_sq", _i64),
+        ("topk_idx", _vp), ("ti_sb", _i64), ("ti_sh", _i64), ("ti_sq", _i64),
+        ("topk_val", _vp),
+        ("B", _i32), ("HI", _i32), ("Lq", _i32), ("D", _i32), ("L", _i32), ("nblk", _i32),
+        ("block_size", _i32), ("local_blocks", _i32), ("K", _i32), ("ascending", _i32),
+        ("k_dtype", _i32),
+    ]
+
+
 # name -> (restype, argtypes) of every exported entry point
 SIGNATURES = {
     "srswa_version": (ctypes.c_int, []),
     "srswa_last_error": (ctypes.c_char_p, []),
-    "srswa_gather_decode_workspace": (ctypes.c_size_t, [ctypes.POINTER(DecodeArgs)]),
-    "srswa_gather_decode": (ctypes.c_int, [ctypes.POINTER(DecodeArgs), _vp, ctypes.c_size_t, _vp]),
+    "srswa_gather_decode_workspace": (None, [ctypes.POINTER(DecodeArgs), _szp, _szp]),
+    "srswa_gather_decode": (ctypes.c_int, [ctypes.POINTER(DecodeArgs), _vp, ctypes.c_size_t, _vp,
+                                           ctypes.c_size_t, _vp]),
+    "srswa_index_workspace": (ctypes.c_size_t, [ctypes.POINTER(IndexArgs)]),
+    "srswa_index_meanpool_topk": (ctypes.c_int, [ctypes.POINTER(IndexArgs), _vp, ctypes.c_size_t, _vp]),
+    "srswa_topk_rows": (ctypes.c_int, [_vp, _i64, _i32, _i64, _i32, _i32, ctypes.c_float, _vp, _vp,
+                                       _i64, _vp]),
 }
 
-STRUCTS = {"srswa_decode_args": DecodeArgs}
+STRUCTS = {"srswa_decode_args": DecodeArgs, "srswa_index_args": IndexArgs}
 
 _lib = None
 _lock = threading.Lock()
@@ -117,20 +142,35 @@ def ptr(t) -> int | None:
     return None if t is None else t.data_ptr()
 
 
-_ws_cache: dict = {}
+_scratch_cache: dict = {}
+_counter_cache: dict = {}
 
 
-def workspace(device: torch.device, nbytes: int) -> torch.Tensor | None:
-    """Zero-filled device workspace cached per (device, stream).
+def _stream_key(device: torch.device):
+    return (device.index, torch.cuda.current_stream(device).cuda_stream)
 
-    The kernels that use a workspace leave it zero-filled again, so the cached
-    buffer is reused across calls on the same stream (calls on one stream are
-    ordered; different streams get different buffers)."""
+
+def scratch(device: torch.device, nbytes: int) -> torch.Tensor | None:
+    """Device scratch (no content requirement), cached per (device, stream)."""
     if nbytes <= 0:
         return None
-    key = (device.index, torch.cuda.current_stream(device).cuda_stream)
-    buf = _ws_cache.get(key)
+    key = _stream_key(device)
+    buf = _scratch_cache.get(key)
     if buf is None or buf.numel() < nbytes:
-        buf = torch.zeros(max(nbytes, 1 << 20), dtype=torch.uint8, device=device)
-        _ws_cache[key] = buf
+        buf = torch.empty(max(nbytes, 1 << 20), dtype=torch.uint8, device=device)
+        _scratch_cache[key] = buf
+    return buf
+
+
+def counters(device: torch.device, n: int) -> torch.Tensor | None:
+    """Zero-filled uint32 arrival counters cached per (device, stream).  Every
+    kernel that uses them leaves them zero, so a prefix of one buffer serves all
+    later calls on the same stream (calls on one stream are ordered)."""
+    if n <= 0:
+        return None
+    key = _stream_key(device)
+    buf = _counter_cache.get(key)
+    if buf is None or buf.numel() < n:
+        buf = torch.zeros(max(n, 1 << 16), dtype=torch.int32, device=device)
+        _counter_cache[key] = buf
     return buf

@@ -28,18 +28,18 @@ def _i32(t: torch.Tensor) -> torch.Tensor:
 
 class _Launch:
     """A prepared launch: the C-ABI struct, the tensors it points into (kept
-    alive), the workspace and the entry point.  ``__call__`` enqueues the
-    kernel on the stream captured at preparation time without rebuilding
-    anything (a few microseconds of host time)."""
+    alive), the scratch / counter buffers and the entry point.  ``__call__``
+    enqueues the kernel on the stream captured at preparation time without
+    rebuilding anything (a few microseconds of host time)."""
 
-    def __init__(self, fn, args, keep, ws, nbytes, stream, what):
-        self.fn, self.args, self.keep, self.ws, self.nbytes = fn, args, keep, ws, nbytes
+    def __init__(self, fn, args, keep, extra, stream, what):
+        self.fn, self.args, self.keep, self.extra = fn, args, keep, extra
         self.stream, self.what = stream, what
         self._ref = ctypes.byref(args)
-        self._ws = _lib.ptr(ws)
+        self._extra = tuple(_lib.ptr(x) if isinstance(x, torch.Tensor) else x for x in extra)
 
     def __call__(self):
-        _lib.check(self.fn(self._ref, self._ws, self.nbytes, self.stream), self.what)
+        _lib.check(self.fn(self._ref, *self._extra, self.stream), self.what)
 
 
 def prepare_gather_decode(q, k_cache, v_cache, block_indices, q_pos, *, block_size, local_window,
@@ -107,10 +107,14 @@ def prepare_gather_decode(q, k_cache, v_cache, block_indices, q_pos, *, block_si
     a.in_dtype = _lib.dtype_code(q.dtype)
     a.out_dtype = _lib.dtype_code(odt)
     L_ = _lib.lib()
-    nbytes = L_.srswa_gather_decode_workspace(ctypes.byref(a))
-    ws = _lib.workspace(q.device, nbytes)
-    launch = _Launch(L_.srswa_gather_decode, a, (q, k_cache, v_cache, idx, bias, valid, pos, kvl, out, lse),
-                     ws, nbytes, _lib.stream_ptr(q.device), "srswa_gather_decode")
+    nscr, ncnt = ctypes.c_size_t(0), ctypes.c_size_t(0)
+    L_.srswa_gather_decode_workspace(ctypes.byref(a), ctypes.byref(nscr), ctypes.byref(ncnt))
+    scr = _lib.scratch(q.device, nscr.value)
+    cnt = _lib.counters(q.device, ncnt.value)
+    launch = _Launch(L_.srswa_gather_decode, a,
+                     (q, k_cache, v_cache, idx, bias, valid, pos, kvl, out, lse),
+                     (scr, nscr.value, cnt, 0 if cnt is None else cnt.numel()),
+                     _lib.stream_ptr(q.device), "srswa_gather_decode")
     if squeeze:
         out = out.squeeze(1)
         if lse is not None:
