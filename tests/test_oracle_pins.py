@@ -1,0 +1,400 @@
+"""Pins for the CPU oracle (oracle/srswa_oracle.py), CPU only.
+
+The reference ships no tests, golden vectors or fixtures for this path, so each
+oracle function is checked here against something that does not retype its
+formula: a pure-Python enumeration of the key SETS the reference's kernels
+read (HF/sparse_gather_triton.py:78-111, HF/modeling_deepseekv2.py:454-481),
+textbook routines (torch's scaled_dot_product_attention, sorting), closed
+forms, invariants, and torch.autograd.gradcheck for the backward.  A plausible
+mistake (window off by one, a dropped segment bound, a transposed head map,
+bias on window keys, summed duplicates) fails at least one of them.
+"""
+
+import math
+
+import pytest
+import torch
+import torch.nn.functional as F
+
+from oracle import srswa_oracle as O
+
+
+@pytest.fixture(autouse=True)
+def _fp64_default():
+    """fp64 for every tensor this module creates; restored afterwards."""
+    old = torch.get_default_dtype()
+    torch.set_default_dtype(torch.float64)
+    yield
+    torch.set_default_dtype(old)
+
+
+# ---------------------------------------------------------------- brute force
+def _dot(a, b):
+    return sum(float(x) * float(y) for x, y in zip(a, b))
+
+
+def _softmax_rows(logits, vals):
+    m = max(logits)
+    w = [math.exp(z - m) for z in logits]
+    s = sum(w)
+    d = len(vals[0])
+    o = [sum(w[i] * float(vals[i][e]) for i in range(len(w))) / s for e in range(d)]
+    return o, m + math.log(s)
+
+
+def brute_gather(q, k, v, bi, pos, bs, scale, lw, bias_slots=None):
+    """Set enumeration of window | remote keys per query (pure Python)."""
+    B, HQ, T, D = q.shape
+    Hkv, Sk = k.shape[1], k.shape[2]
+    HI = bi.shape[1]
+    o = torch.zeros(B, HQ, T, v.shape[-1])
+    lse = torch.zeros(B, HQ, T)
+    for b in range(B):
+        for t in range(T):
+            qi = Sk - T + t
+            seg = qi - int(pos[b, t])
+            ls = max(qi - lw + 1, seg)
+            window = list(range(ls, qi + 1))
+            for h in range(HQ):
+                ih, kh = h // (HQ // HI), h // (HQ // Hkv)
+                seen = []
+                remote = {}
+                for si, s in enumerate(bi[b, ih, t].tolist()):
+                    if s < 0 or s * bs >= Sk or s in seen:
+                        continue
+                    seen.append(s)
+                    bval = 0.0 if bias_slots is None else float(bias_slots[b, t, si])
+                    for j in range(s * bs, min((s + 1) * bs, Sk)):
+                        if seg <= j < ls and j <= qi:
+                            remote[j] = bval
+                keys = window + sorted(remote)
+                logits = [scale * _dot(q[b, h, t], k[b, kh, j]) + (remote.get(j, 0.0)) for j in keys]
+                oo, l = _softmax_rows(logits, [v[b, kh, j] for j in keys])
+                o[b, h, t] = torch.tensor(oo)
+                lse[b, h, t] = l
+    return o, lse
+
+
+def brute_decode(q, k, v, topi, bias, valid, q_pos, bs, lw, scale):
+    """_decode_attend semantics by enumeration; topi/bias/valid [B,HI,Lq,K]."""
+    B, H, Lq, D = q.shape
+    Hkv, S = k.shape[1], k.shape[2]
+    HI = topi.shape[1]
+    out = torch.zeros(B, H, Lq, v.shape[-1])
+    for b in range(B):
+        for r in range(Lq):
+            qp = int(q_pos[b, r])
+            win = [j for j in range(S) if qp - lw < j <= qp]
+            for h in range(H):
+                ih, kh = h // (H // HI), h // (H // Hkv)
+                rem = {}
+                for si in range(topi.shape[-1]):
+                    s = int(topi[b, ih, r, si])
+                    if not bool(valid[b, ih, r, si]) or s < 0:
+                        continue
+                    for j in range(s * bs, min((s + 1) * bs, S)):
+                        if j <= qp - lw and j not in rem:     # an earlier slot's bias wins
+                            rem[j] = float(bias[b, ih, r, si])
+                keys = win + sorted(rem)
+                logits = [scale * _dot(q[b, h, r], k[b, kh, j]) + rem.get(j, 0.0) for j in keys]
+                out[b, h, r] = torch.tensor(_softmax_rows(logits, [v[b, kh, j] for j in keys])[0])
+    return out
+
+
+def _rand(*shape, g):
+    return torch.randn(*shape, generator=g)
+
+
+# ------------------------------------------------------- gather attention
+def test_no_selection_full_window_is_causal_sdpa():
+    g = torch.Generator().manual_seed(0)
+    q, k, v = (_rand(2, 4, 150, 16, g=g) for _ in range(3))
+    bi = torch.full((2, 1, 150, 3), -1)
+    pos = torch.arange(150)[None].expand(2, -1)
+    o, _ = O.gather_attention(q, k, v, bi, pos, 16, 0.3, local_window=150)
+    ref = F.scaled_dot_product_attention(q, k, v, is_causal=True, scale=0.3)
+    assert (o - ref).abs().max() < 1e-12
+
+
+def test_all_blocks_selected_is_causal_sdpa():
+    g = torch.Generator().manual_seed(1)
+    T, bs = 133, 16
+    q, k, v = (_rand(1, 2, T, 8, g=g) for _ in range(3))
+    M = -(-T // bs)
+    bi = torch.arange(M).view(1, 1, 1, M).expand(1, 1, T, M).contiguous()
+    pos = torch.arange(T)[None]
+    for lw in (1, 20, 64):
+        o, _ = O.gather_attention(q, k, v, bi, pos, bs, 0.5, local_window=lw)
+        ref = F.scaled_dot_product_attention(q, k, v, is_causal=True, scale=0.5)
+        assert (o - ref).abs().max() < 1e-12, lw
+
+
+def test_no_selection_is_banded_sdpa():
+    g = torch.Generator().manual_seed(2)
+    T, lw = 97, 11
+    q, k, v = (_rand(1, 3, T, 8, g=g) for _ in range(3))
+    band = torch.ones(T, T, dtype=torch.bool).tril().triu(-(lw - 1))
+    ref = F.scaled_dot_product_attention(q, k, v, attn_mask=band, scale=0.7)
+    o, _ = O.gather_attention(q, k, v, torch.full((1, 1, T, 2), -1), torch.arange(T)[None], 8, 0.7,
+                              local_window=lw)
+    assert (o - ref).abs().max() < 1e-12
+
+
+@pytest.mark.parametrize("case", ["plain", "packed", "prefix", "gqa_hi", "bias"])
+def test_gather_matches_bruteforce(case):
+    g = torch.Generator().manual_seed(100 + ["plain", "packed", "prefix", "gqa_hi", "bias"].index(case))
+    B, HQ, Hkv, HI, T, Sk, D, bs, lw, S = 2, 2, 2, 1, 40, 40, 8, 4, 7, 3
+    if case == "gqa_hi":
+        HQ, Hkv, HI = 4, 2, 2
+    if case == "prefix":
+        Sk = 64
+    q = _rand(B, HQ, T, D, g=g)
+    k, v = _rand(B, Hkv, Sk, D, g=g), _rand(B, Hkv, Sk, D, g=g)
+    nblk = -(-Sk // bs)
+    bi = torch.randint(-1, nblk + 2, (B, HI, T, S), generator=g)
+    bi[..., 1] = bi[..., 0]                                   # duplicates
+    if case == "packed":
+        pos = torch.cat([torch.arange(17), torch.arange(T - 17)])[None].expand(B, -1)
+    else:
+        pos = (Sk - T + torch.arange(T))[None].expand(B, -1)
+    bias = None
+    dense = None
+    if case == "bias":
+        bias = _rand(B, T, S, g=g)
+        dense = O.bias_slots_to_dense(bias, bi[:, 0], nblk)
+    o, lse = O.gather_attention(q, k, v, bi, pos, bs, 0.37, lw, blk_bias_dense=dense)
+    ro, rl = brute_gather(q, k, v, bi, pos, bs, 0.37, lw, bias)
+    assert (o - ro).abs().max() < 1e-10
+    assert (lse - rl).abs().max() < 1e-10
+
+
+def test_duplicates_equal_dedup_and_out_of_range_ignored():
+    g = torch.Generator().manual_seed(3)
+    q, k, v = (_rand(1, 1, 50, 8, g=g) for _ in range(3))
+    pos = torch.arange(50)[None]
+    bi = torch.tensor([1, 1, 2, -1, 99]).view(1, 1, 1, 5).expand(1, 1, 50, 5).contiguous()
+    bd = torch.tensor([1, 2, -1, -1, -1]).view(1, 1, 1, 5).expand(1, 1, 50, 5).contiguous()
+    a, _ = O.gather_attention(q, k, v, bi, pos, 8, 0.2, 9)
+    b, _ = O.gather_attention(q, k, v, bd, pos, 8, 0.2, 9)
+    assert (a - b).abs().max() < 1e-14
+
+
+def test_gather_backward_gradcheck():
+    g = torch.Generator().manual_seed(4)
+    B, H, T, D, bs, lw = 1, 2, 24, 4, 4, 5
+    q, k, v = (_rand(B, H, T, D, g=g).requires_grad_() for _ in range(3))
+    bi = torch.randint(-1, T // bs, (B, 1, T, 3), generator=g)
+    pos = torch.arange(T)[None]
+    bias = _rand(B, T, 3, g=g).requires_grad_()
+
+    def f(q, k, v, bias):
+        return O.gather_attention_e2e(q, k, v, bi, bias, pos, bs, 0.5, lw)
+
+    assert torch.autograd.gradcheck(f, (q, k, v, bias), eps=1e-6, atol=1e-6)
+
+
+def test_bias_gradient_is_sum_of_dS_over_remote_keys():
+    """d_bias[t, slot] = sum over heads and the block's remote keys of
+    P*(dP - delta): checked against an explicit P/dP computation."""
+    g = torch.Generator().manual_seed(6)
+    B, H, T, D, bs, lw = 1, 2, 20, 4, 4, 5
+    q, k, v = (_rand(B, H, T, D, g=g) for _ in range(3))
+    bi = torch.randint(0, T // bs, (B, 1, T, 2), generator=g)
+    pos = torch.arange(T)[None]
+    bias = _rand(B, T, 2, g=g).requires_grad_()
+    do = _rand(B, H, T, D, g=g)
+    o = O.gather_attention_e2e(q, k, v, bi, bias, pos, bs, 0.5, lw)
+    (o * do).sum().backward()
+    # explicit: P from the brute-force logits
+    ro, rl = brute_gather(q, k, v, bi, pos, bs, 0.5, lw, bias.detach())
+    keep, remote = O.gather_keep_masks(bi, pos, T, bs, lw)
+    dense = O.bias_slots_to_dense(bias.detach(), bi[:, 0], -(-T // bs))
+    s = (q @ k.transpose(-1, -2)) * 0.5 + torch.where(remote, dense[:, None, :, torch.arange(T) // bs], 0.)
+    P = torch.exp(s - rl[..., None]) * keep
+    dP = do @ v.transpose(-1, -2)
+    delta = (ro * do).sum(-1, keepdim=True)
+    dS = P * (dP - delta)
+    for t in range(T):
+        for si in range(2):
+            blk = int(bi[0, 0, t, si])
+            if si == 1 and blk == int(bi[0, 0, t, 0]):
+                exp = 0.0                      # duplicate slot carries no gradient
+            else:
+                js = [j for j in range(blk * bs, (blk + 1) * bs) if remote[0, 0, t, j]]
+                exp = float(dS[0, :, t, js].sum()) if js else 0.0
+            assert abs(float(bias.grad[0, t, si]) - exp) < 1e-10
+
+
+# ------------------------------------------------------- decode
+def test_decode_matches_bruteforce_with_bias_valid_dups():
+    g = torch.Generator().manual_seed(7)
+    B, H, Hkv, Lq, S, D, bs, lw, K = 2, 4, 2, 2, 90, 8, 8, 13, 4
+    q = _rand(B, H, Lq, D, g=g)
+    k, v = _rand(B, Hkv, S, D, g=g), _rand(B, Hkv, S, D, g=g)
+    topi = torch.randint(0, -(-S // bs), (B, Lq, K), generator=g)
+    topi[:, :, 1] = topi[:, :, 0]
+    bias = _rand(B, Lq, K, g=g)
+    valid = torch.rand(B, Lq, K, generator=g) > 0.3
+    q_pos = torch.tensor([[89, 60], [30, 5]])
+    o = O.decode_attend(q, k, v, topi, bias, valid, q_pos, bs, lw, 0.4)
+    ref = brute_decode(q, k, v, topi[:, None], bias[:, None], valid[:, None], q_pos, bs, lw, 0.4)
+    assert (o - ref).abs().max() < 1e-12
+
+
+def test_decode_agrees_with_prefill_restatement_last_row():
+    """Two independent restatements (decode: _decode_attend; prefill: the Triton
+    kernel's remote/window split) agree on a causal last row without bias."""
+    g = torch.Generator().manual_seed(8)
+    B, H, T, D, bs, lw = 1, 2, 77, 8, 8, 16
+    q, k, v = (_rand(B, H, T, D, g=g) for _ in range(3))
+    bi = torch.randint(0, T // bs, (B, 1, T, 3), generator=g)
+    full, _ = O.gather_attention(q, k, v, bi, torch.arange(T)[None], bs, 0.3, lw)
+    topi = bi[:, 0, -1:, :]
+    dec = O.decode_attend(q[:, :, -1:], k, v, topi, torch.zeros(topi.shape), torch.ones_like(topi, dtype=torch.bool),
+                          torch.tensor([[T - 1]]), bs, lw, 0.3)
+    assert (full[:, :, -1:] - dec).abs().max() < 1e-12
+
+
+def test_decode_gather_form_equals_dense_form():
+    g = torch.Generator().manual_seed(9)
+    B, H, L, D, bs, lw, K = 2, 3, 700, 8, 16, 64, 5
+    q = _rand(B, H, D, g=g)
+    kc, vc = _rand(B, L, H, D, g=g), _rand(B, L, H, D, g=g)
+    idx = torch.randint(-1, L // bs, (B, H, K), generator=g)
+    bias = _rand(B, H, K, g=g)
+    q_pos = torch.tensor([699, 333])
+    a = O.decode_attend_gather(q, kc, vc, idx, q_pos, bs, lw, 0.25, bias=bias)
+    b = O.decode_attend(q[:, :, None], kc.transpose(1, 2), vc.transpose(1, 2), idx[:, :, None],
+                        bias[:, :, None], idx[:, :, None] >= 0, q_pos[:, None], bs, lw, 0.25)[:, :, 0]
+    assert (a - b).abs().max() < 1e-12
+
+
+def test_decode_without_remote_is_window_softmax():
+    g = torch.Generator().manual_seed(10)
+    q, k, v = _rand(1, 1, 1, 8, g=g), _rand(1, 1, 50, 8, g=g), _rand(1, 1, 50, 8, g=g)
+    o = O.decode_attend(q, k, v, torch.zeros(1, 1, 2, dtype=torch.long), torch.zeros(1, 1, 2),
+                        torch.zeros(1, 1, 2, dtype=torch.bool), torch.tensor([[40]]), 8, 10, 0.5)
+    w = torch.softmax((k[0, 0, 31:41] @ q[0, 0, 0]) * 0.5, 0)
+    assert (o[0, 0, 0] - w @ v[0, 0, 31:41]).abs().max() < 1e-12
+
+
+# ------------------------------------------------------- indexer
+def test_meanpool_scores_closed_form_and_invariants():
+    g = torch.Generator().manual_seed(12)
+    B, HI, Lq, S, d, bs, lb = 1, 2, 2, 45, 4, 8, 2
+    q = _rand(B, HI, Lq, d, g=g)
+    k = _rand(B, HI, S, d, g=g)
+    q_pos = torch.tensor([[44, 30]])
+    z = O.meanpool_block_scores(q, k, q_pos, bs, lb)
+    nblk = -(-S // bs)
+    for h in range(HI):
+        for r in range(Lq):
+            for blk in range(nblk):
+                rows = [k[0, h, j].tolist() for j in range(blk * bs, min((blk + 1) * bs, S))]
+                mean = [sum(c) / len(rows) for c in zip(*rows)]
+                remote = blk <= int(q_pos[0, r]) // bs - lb
+                want = _dot(q[0, h, r], mean) / math.sqrt(d) if remote else O.SCORE_NEG
+                assert abs(float(z[0, h, r, blk]) - want) < 1e-12
+    # permuting keys inside a block and scaling q
+    perm = torch.arange(S)
+    perm[:8] = torch.randperm(8, generator=g)
+    assert (O.meanpool_block_scores(q, k[:, :, perm], q_pos, bs, lb) - z).abs().max() < 1e-12
+    z2 = O.meanpool_block_scores(2.5 * q, k, q_pos, bs, lb)
+    valid = z > O.SCORE_NEG * 0.5
+    assert (z2[valid] - 2.5 * z[valid]).abs().max() < 1e-12
+    # zero head_cls is mean pooling
+    assert torch.equal(O.meanpool_block_scores(q, k, q_pos, bs, lb, head_cls=torch.zeros(d)), z)
+
+
+def test_head_cls_weights_are_softmax_over_real_keys():
+    g = torch.Generator().manual_seed(13)
+    d, bs, S = 4, 8, 21
+    q = _rand(1, 1, 1, d, g=g)
+    k = _rand(1, 1, S, d, g=g)
+    hc = _rand(d, g=g)
+    z = O.meanpool_block_scores(q, k, torch.tensor([[100]]), bs, 1, head_cls=hc)
+    for blk in range(-(-S // bs)):
+        js = list(range(blk * bs, min((blk + 1) * bs, S)))
+        a = [_dot(k[0, 0, j], hc) / math.sqrt(d) for j in js]
+        m = max(a)
+        w = [math.exp(x - m) for x in a]
+        kb = [sum(w[i] * float(k[0, 0, j, e]) for i, j in enumerate(js)) / sum(w) for e in range(d)]
+        assert abs(float(z[0, 0, 0, blk]) - _dot(q[0, 0, 0], kb) / math.sqrt(d)) < 1e-12
+
+
+def test_block_max_bruteforce():
+    g = torch.Generator().manual_seed(14)
+    B, C, Sk, D, bs, lw = 2, 6, 50, 4, 8, 10
+    q, k = _rand(B, C, D, g=g), _rand(B, Sk, D, g=g)
+    pos = torch.randint(0, Sk, (B, C), generator=g)
+    seg = torch.randint(0, 10, (B, C), generator=g)
+    nblk = 8
+    s = O.block_max_scores(q, k, pos, seg, bs, nblk, lw)
+    for b in range(B):
+        for c in range(C):
+            ls = max(int(pos[b, c]) - lw + 1, 0)
+            for blk in range(nblk):
+                vals = [_dot(q[b, c], k[b, j]) for j in range(blk * bs, min((blk + 1) * bs, Sk))
+                        if int(seg[b, c]) <= j < ls]
+                want = max(vals) if vals else float("-inf")
+                got = float(s[b, c, blk])
+                assert (got == want) if want == float("-inf") else abs(got - want) < 1e-12
+
+
+def test_topk_bruteforce_ties_invalid():
+    g = torch.Generator().manual_seed(15)
+    s = torch.randint(-3, 4, (20, 30), generator=g).double()
+    s[0] = float("-inf")
+    s[1, 5:] = O.SCORE_NEG
+    s[2, ::3] = float("nan")
+    for k in (1, 4, 10, 35):
+        got = O.topk_blocks(s, k)
+        for r in range(s.shape[0]):
+            items = [(-float(x), j) for j, x in enumerate(s[r].tolist())
+                     if x == x and x > O.SCORE_NEG * 0.5]
+            want = [j for _, j in sorted(items)][:k]
+            want += [-1] * (k - len(want))
+            assert got[r].tolist() == want
+
+
+def test_near_tie_rows():
+    s = torch.tensor([[5.0, 4.0, 3.0, 3.00001, 1.0], [5.0, 4.0, 3.0, 2.0, 1.0]])
+    assert O.near_tie_rows(s, 3).tolist() == [True, False]
+    assert O.near_tie_rows(s, 2).tolist() == [False, False]
+
+
+# ------------------------------------------------------- router (next row)
+def _entmax_bisect(x):
+    """1.5-entmax by bisection on tau: p_i = max(x_i/2 - tau, 0)^2, sum p = 1."""
+    x = [xi / 2 for xi in x]
+    lo, hi = max(x) - 1.0, max(x)
+    for _ in range(200):
+        mid = (lo + hi) / 2
+        if sum(max(xi - mid, 0) ** 2 for xi in x) >= 1:
+            lo = mid
+        else:
+            hi = mid
+    return [max(xi - lo, 0) ** 2 for xi in x]
+
+
+def test_entmax15_matches_bisection():
+    g = torch.Generator().manual_seed(16)
+    for n in (2, 5, 16):
+        x = _rand(4, n, g=g) * 3
+        p = O.entmax15(x)
+        assert (p.sum(-1) - 1).abs().max() < 1e-12
+        for r in range(4):
+            want = _entmax_bisect(x[r].tolist())
+            assert max(abs(a - b) for a, b in zip(p[r].tolist(), want)) < 1e-9
+    assert (O.entmax15(torch.zeros(1, 4)) - 0.25).abs().max() < 1e-12
+
+
+def test_route_select_bias_is_mean_centred():
+    g = torch.Generator().manual_seed(17)
+    sc = _rand(2, 3, 20, g=g) * 4
+    sc[..., 15:] = O.SCORE_NEG
+    xi, bias, valid = O.infer_route_select(sc, None, 1.0, 1e-4, 1.0, K=6, topm=16)
+    assert xi.shape == (2, 3, 6)
+    m = (bias * valid).sum(-1) / valid.sum(-1)
+    assert m.abs().max() < 1e-5
+    assert (xi[valid] < 15).all()

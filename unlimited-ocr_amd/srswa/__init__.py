@@ -11,6 +11,6 @@ from PyTorch-ROCm.  Drop-in modules keep the reference's Python surface:
 
 from . import _lib  # noqa: F401
 from ._lib import UnsupportedShape  # noqa: F401
-from .ops import decode_attend, gather_decode  # noqa: F401
+from .ops import decode_attend, gather_decode, index_meanpool_topk, topk_rows  # noqa: F401
 
 __version__ = "0.1.0"

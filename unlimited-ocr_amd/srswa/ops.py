@@ -160,3 +160,110 @@ def decode_attend(q, k_all, v_all, topi, bias, valid, q_pos, block_size, local_w
                       local_window=local_window, scale=scale, bias=bias, valid=valid,
                       out_dtype=torch.float32)
     return o.transpose(1, 2)
+
+
+# ---------------------------------------------------------------------------
+# indexer
+# ---------------------------------------------------------------------------
+SCORE_NEG = -1.0e9
+
+
+def prepare_index_meanpool_topk(q, k, q_pos, *, block_size, local_blocks, topk, head_cls=None,
+                                kv_len=None, nblk=None, return_scores=False, return_kbar=False,
+                                ascending=False):
+    """Build the launch of the head_cls / mean-pool indexer (see ``index_meanpool_topk``).
+
+    Returns (launch, idx, scores_or_None, kbar_or_None)."""
+    _require_cuda(q, k, q_pos, head_cls, kv_len)
+    squeeze = q.dim() == 3
+    if squeeze:                                   # [B, HI, D] -> one query row
+        q = q.unsqueeze(2)
+        if q_pos.dim() == 1:
+            q_pos = q_pos.unsqueeze(1)
+    B, HI, Lq, D = q.shape
+    if k.dim() == 3:                              # [B, L, D]: one key head shared by all HI
+        k = k.unsqueeze(2)
+    Bk, L, HK, Dk = k.shape
+    if Bk != B or Dk != D or HK not in (1, HI):
+        raise ValueError(f"k shape {tuple(k.shape)} incompatible with q {tuple(q.shape)}")
+    if k.stride(-1) != 1:
+        raise UnsupportedShape("key head dim must be contiguous")
+    nblk = int(nblk) if nblk is not None else -(-L // int(block_size))
+    qf = q.to(torch.float32)
+    pos = _i32(q_pos).contiguous()
+    if tuple(pos.shape) != (B, Lq):
+        raise ValueError(f"q_pos shape {tuple(pos.shape)} != {(B, Lq)}")
+    kvl = None if kv_len is None else _i32(kv_len).contiguous()
+    hc = None if head_cls is None else head_cls.to(torch.float32).contiguous()
+    scores = torch.empty(B, HI, Lq, nblk, dtype=torch.float32, device=q.device) if return_scores else None
+    kbar = torch.empty(B, HI, nblk, D, dtype=torch.float32, device=q.device) if return_kbar else None
+    idx = torch.empty(B, HI, Lq, int(topk), dtype=torch.int32, device=q.device) if topk > 0 else None
+
+    a = _lib.IndexArgs()
+    a.q = qf.data_ptr(); a.q_sb, a.q_sh, a.q_sq = qf.stride(0), qf.stride(1), qf.stride(2)
+    a.k = k.data_ptr(); a.k_sb, a.k_st = k.stride(0), k.stride(1)
+    a.k_sh = 0 if HK == 1 else k.stride(2)
+    if kbar is not None:
+        a.kbar_out = kbar.data_ptr(); a.kb_sb, a.kb_sh, a.kb_sn = kbar.stride(0), kbar.stride(1), kbar.stride(2)
+    a.head_cls = _lib.ptr(hc)
+    a.q_pos = pos.data_ptr(); a.pos_sb, a.pos_sq = pos.stride(0), pos.stride(1)
+    a.kv_len = _lib.ptr(kvl)
+    if scores is not None:
+        a.scores = scores.data_ptr(); a.sc_sb, a.sc_sh, a.sc_sq = scores.stride(0), scores.stride(1), scores.stride(2)
+    if idx is not None:
+        a.topk_idx = idx.data_ptr(); a.ti_sb, a.ti_sh, a.ti_sq = idx.stride(0), idx.stride(1), idx.stride(2)
+    a.B, a.HI, a.Lq, a.D, a.L, a.nblk = B, HI, Lq, D, L, nblk
+    a.block_size, a.local_blocks, a.K, a.ascending = int(block_size), int(local_blocks), int(topk), int(bool(ascending))
+    a.k_dtype = _lib.dtype_code(k.dtype)
+    L_ = _lib.lib()
+    nscr = L_.srswa_index_workspace(ctypes.byref(a))
+    scr = _lib.scratch(q.device, nscr)
+    launch = _Launch(L_.srswa_index_meanpool_topk, a, (qf, k, pos, kvl, hc, scores, kbar, idx),
+                     (scr, nscr), _lib.stream_ptr(q.device), "srswa_index_meanpool_topk")
+    if squeeze:
+        idx = None if idx is None else idx.squeeze(2)
+        scores = None if scores is None else scores.squeeze(2)
+    return launch, idx, scores, kbar
+
+
+def index_meanpool_topk(q, k, q_pos, *, block_size, local_blocks, topk, head_cls=None,
+                        kv_len=None, nblk=None, return_scores=False, return_kbar=False,
+                        ascending=False):
+    """head_cls / mean-pool block indexer with top-k selection.
+
+    q       [B, HI, Lq, D] (or [B, HI, D]) index queries (any float dtype; scored in fp32)
+    k       [B, L, HI, D] or [B, L, D] (one key head shared) index keys, bf16/fp16/fp32
+    q_pos   [B, Lq] (or [B]) absolute positions
+    head_cls[D] learned summary query (None -> mean pooling, the zero-init value)
+    Returns idx [B, HI, Lq, topk] int32 (descending score, ties -> lower id, -1 pad;
+    ``ascending=True`` re-packs ascending), plus scores [B, HI, Lq, nblk] and
+    k_bar [B, HI, nblk, D] when asked.  Restates ``_block_scores_infer`` head_cls +
+    top-k (HF/modeling_deepseekv2.py:380-417, HF/_sparse_base_impl.py:3100-3105).
+    """
+    launch, idx, scores, kbar = prepare_index_meanpool_topk(
+        q, k, q_pos, block_size=block_size, local_blocks=local_blocks, topk=topk,
+        head_cls=head_cls, kv_len=kv_len, nblk=nblk, return_scores=return_scores,
+        return_kbar=return_kbar, ascending=ascending)
+    launch()
+    out = [idx]
+    if return_scores:
+        out.append(scores)
+    if return_kbar:
+        out.append(kbar)
+    return out[0] if len(out) == 1 else tuple(out)
+
+
+def topk_rows(scores, k, *, invalid_at=SCORE_NEG * 0.5, ascending=False, return_values=False):
+    """Top-k along the last dim of an fp32 device tensor: descending, ties ->
+    lower index, entries <= invalid_at (and NaN) never selected, missing -1."""
+    _require_cuda(scores)
+    s = scores.to(torch.float32).contiguous()
+    n = s.shape[-1]
+    rows = s.numel() // max(n, 1)
+    idx = torch.empty(*s.shape[:-1], int(k), dtype=torch.int32, device=s.device)
+    val = torch.empty(idx.shape, dtype=torch.float32, device=s.device) if return_values else None
+    st = _lib.lib().srswa_topk_rows(s.data_ptr(), rows, n, n, int(k), int(bool(ascending)),
+                                    float(invalid_at), idx.data_ptr(), _lib.ptr(val), int(k),
+                                    _lib.stream_ptr(s.device))
+    _lib.check(st, "srswa_topk_rows")
+    return (idx, val) if return_values else idx
