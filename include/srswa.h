@@ -129,6 +129,34 @@ int srswa_topk_rows(const float* scores, int64_t rows, int32_t n, int64_t row_st
                     int32_t ascending, float invalid_at, int32_t* out_idx, float* out_val,
                     int64_t out_stride, void* stream);
 
+/* ------------------------------------------------------------------------
+ * Gather-attention forward on the matrix cores (prefill, training, chunked
+ * prefill over a prefix cache).  Replaces:
+ *   - _gather_attn_fwd_kernel (K1)  HF/sparse_gather_triton.py:35-122
+ *   - _e2e_attn_fwd_kernel (K5)     HF/sparse_gather_e2e_triton.py:36-121
+ * Query t sits at key index qi = Sk - T + t (T == Sk: self-attention), its
+ * sample starts at seg[b, t] (packing; NULL = 0), ls = max(qi - LW + 1, seg):
+ *   window keys ls <= j <= qi                      logit = scale*q.k
+ *   remote keys j of a selected block, seg <= j < ls  logit = scale*q.k + bias
+ * Duplicate ids count once (first slot's bias).  bf16 / fp16 only; q*scale and
+ * P are rounded to the input dtype before their products (as the reference).
+ * ---------------------------------------------------------------------- */
+typedef struct {
+  const void* q;       int64_t q_sb, q_st, q_sh;       /* [B, T, HQ, D]                 */
+  const void* k;       int64_t k_sb, k_st, k_sh;       /* [B, Sk, HKV, D]               */
+  const void* v;       int64_t v_sb, v_st, v_sh;       /* [B, Sk, HKV, D]               */
+  const int32_t* idx;  int64_t idx_sb, idx_sh, idx_st; /* [B, HI, T, S], slot stride 1  */
+  const float* bias;   int64_t bias_sb, bias_sh, bias_st; /* like idx; NULL = no bias   */
+  const int32_t* seg;  int64_t seg_sb;                 /* [B, T] sample start; NULL = 0 */
+  void* out;           int64_t o_sb, o_st, o_sh;       /* [B, T, HQ, D]                 */
+  float* lse;          int64_t lse_sb, lse_st, lse_sh; /* [B, T, HQ]; NULL = skip       */
+  int32_t B, T, Sk, HQ, HKV, HI, D, S, block_size, local_window;
+  float scale;
+  int32_t dtype;                                       /* SRSWA_BF16 or SRSWA_F16        */
+} srswa_fwd_args;
+
+int srswa_gather_fwd(const srswa_fwd_args* a, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -73,6 +73,25 @@ class IndexArgs(ctypes.Structure):
     ]
 
 
+class FwdArgs(ctypes.Structure):
+    """Mirror of ``srswa_fwd_args``."""
+
+    _fields_ = [
+        ("q", _vp), ("q_sb", _i64), ("q_st", _i64), ("q_sh", _i64),
+        ("k", _vp), ("k_sb", _i64), ("k_st", _i64), ("k_sh", _i64),
+        ("v", _vp), ("v_sb", _i64), ("v_st", _i64), ("v_sh", _i64),
+        ("idx", _vp), ("idx_sb", _i64), ("idx_sh", _i64), ("idx_st", _i64),
+        ("bias", _vp), ("bias_sb", _i64), ("bias_sh", _i64), ("bias_st", _i64),
+        ("seg", _vp), ("seg_sb", _i64),
+        ("out", _vp), ("o_sb", _i64), ("o_st", _i64), ("o_sh", _i64),
+        ("lse", _vp), ("lse_sb", _i64), ("lse_st", _i64), ("lse_sh", _i64),
+        ("B", _i32), ("T", _i32), ("Sk", _i32), ("HQ", _i32), ("HKV", _i32), ("HI", _i32),
+        ("D", _i32), ("S", _i32), ("block_size", _i32), ("local_window", _i32),
+        ("scale", ctypes.c_float),
+        ("dtype", _i32),
+    ]
+
+
 # name -> (restype, argtypes) of every exported entry point
 SIGNATURES = {
     "srswa_version": (ctypes.c_int, []),
@@ -84,9 +103,11 @@ SIGNATURES = {
     "srswa_index_meanpool_topk": (ctypes.c_int, [ctypes.POINTER(IndexArgs), _vp, ctypes.c_size_t, _vp]),
     "srswa_topk_rows": (ctypes.c_int, [_vp, _i64, _i32, _i64, _i32, _i32, ctypes.c_float, _vp, _vp,
                                        _i64, _vp]),
+    "srswa_gather_fwd": (ctypes.c_int, [ctypes.POINTER(FwdArgs), _vp]),
 }
 
-STRUCTS = {"srswa_decode_args": DecodeArgs, "srswa_index_args": IndexArgs}
+STRUCTS = {"srswa_decode_args": DecodeArgs, "srswa_index_args": IndexArgs,
+           "srswa_fwd_args": FwdArgs}
 
 _lib = None
 _lock = threading.Lock()

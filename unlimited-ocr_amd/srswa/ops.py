@@ -267,3 +267,68 @@ def topk_rows(scores, k, *, invalid_at=SCORE_NEG * 0.5, ascending=False, return_
                                     _lib.stream_ptr(s.device))
     _lib.check(st, "srswa_topk_rows")
     return (idx, val) if return_values else idx
+
+
+# ---------------------------------------------------------------------------
+# gather-attention forward (matrix cores)
+# ---------------------------------------------------------------------------
+def _seg_from_positions(position_ids, T, Sk, device):
+    """seg[b, t] = (Sk - T + t) - position_ids[b, t]: the key index where query
+    t's sample starts (HF/sparse_gather_triton.py:413-416, generalised to a
+    query chunk at the tail of a prefix cache).  None when all zero."""
+    if position_ids is None:
+        return None
+    qi = torch.arange(Sk - T, Sk, device=device, dtype=torch.int64)
+    seg = (qi[None, :] - position_ids.to(device=device, dtype=torch.int64)).to(torch.int32).contiguous()
+    return seg
+
+
+def gather_fwd(q, k, v, block_indices, *, block_size, local_window, scale, seg=None, bias=None,
+               out=None, need_lse=True):
+    """Fused gather attention forward.
+
+    q [B, T, HQ, D]; k, v [B, Sk, HKV, D] (Sk >= T, queries are the last T
+    keys); block_indices [B, HI, T, S] (-1 pad); seg [B, T] int sample starts
+    (None = 0); bias [B, T, S] or [B, HI, T, S] per-slot bias on remote keys.
+    Returns (o [B, T, HQ, D], lse [B, T, HQ] fp32 or None)."""
+    _require_cuda(q, k, v, block_indices, seg, bias)
+    B, T, HQ, D = q.shape
+    Bk, Sk, HKV, Dk = k.shape
+    if Bk != B or Dk != D or tuple(v.shape) != tuple(k.shape):
+        raise ValueError(f"k/v shape {tuple(k.shape)} incompatible with q {tuple(q.shape)}")
+    if q.dtype != k.dtype or k.dtype != v.dtype:
+        raise ValueError("q, k, v must share a dtype")
+    for t in (q, k, v):
+        if t.stride(-1) != 1:
+            raise UnsupportedShape("head dim must be contiguous")
+    HI, S = block_indices.shape[1], block_indices.shape[-1]
+    if tuple(block_indices.shape) != (B, HI, T, S):
+        raise ValueError(f"block_indices shape {tuple(block_indices.shape)} != {(B, HI, T, S)}")
+    idx = _i32(block_indices).contiguous()
+    if bias is not None:
+        if bias.dim() == 3:
+            bias = bias.unsqueeze(1)
+        bias = bias.to(torch.float32).expand(B, HI, T, S).contiguous()
+    if seg is not None:
+        seg = _i32(seg).contiguous()
+    if out is None:
+        out = torch.empty(B, T, HQ, D, dtype=q.dtype, device=q.device)
+    lse = torch.empty(B, T, HQ, dtype=torch.float32, device=q.device) if need_lse else None
+    a = _lib.FwdArgs()
+    a.q = q.data_ptr(); a.q_sb, a.q_st, a.q_sh = q.stride(0), q.stride(1), q.stride(2)
+    a.k = k.data_ptr(); a.k_sb, a.k_st, a.k_sh = k.stride(0), k.stride(1), k.stride(2)
+    a.v = v.data_ptr(); a.v_sb, a.v_st, a.v_sh = v.stride(0), v.stride(1), v.stride(2)
+    a.idx = idx.data_ptr(); a.idx_sb, a.idx_sh, a.idx_st = idx.stride(0), idx.stride(1), idx.stride(2)
+    if bias is not None:
+        a.bias = bias.data_ptr(); a.bias_sb, a.bias_sh, a.bias_st = bias.stride(0), bias.stride(1), bias.stride(2)
+    if seg is not None:
+        a.seg = seg.data_ptr(); a.seg_sb = seg.stride(0)
+    a.out = out.data_ptr(); a.o_sb, a.o_st, a.o_sh = out.stride(0), out.stride(1), out.stride(2)
+    if lse is not None:
+        a.lse = lse.data_ptr(); a.lse_sb, a.lse_st, a.lse_sh = lse.stride(0), lse.stride(1), lse.stride(2)
+    a.B, a.T, a.Sk, a.HQ, a.HKV, a.HI, a.D, a.S = B, T, Sk, HQ, HKV, HI, D, S
+    a.block_size, a.local_window = int(block_size), max(1, int(local_window))
+    a.scale = float(scale)
+    a.dtype = _lib.dtype_code(q.dtype)
+    _lib.check(_lib.lib().srswa_gather_fwd(ctypes.byref(a), _lib.stream_ptr(q.device)), "srswa_gather_fwd")
+    return out, lse
