@@ -157,6 +157,62 @@ typedef struct {
 
 int srswa_gather_fwd(const srswa_fwd_args* a, void* stream);
 
+/* ------------------------------------------------------------------------
+ * Gather-attention backward (dQ, dK, dV and the per-slot bias gradient).
+ * Replaces:
+ *   - _gather_attn_bwd_dq_kernel / _dkv_kernel (K2, K3)  HF/sparse_gather_triton.py:125-279
+ *   - _e2e_attn_bwd_dq_kernel / _dkv_kernel (K6, K7)     HF/sparse_gather_e2e_triton.py:124-275
+ *   - the torch glue: delta = rowsum(O dO) and the dense block_mask
+ *     (HF/sparse_gather_triton.py:329, 339-343)
+ * Same masks and rounding points as srswa_gather_fwd; o and lse are the
+ * forward's outputs.  dk/dv cover every key (0 where no query reads it).
+ * dbias (optional, needs bias): per QUERY head, [B, HQ, T, S], the sum of dS
+ * over the remote keys of the block in slot s (0 for duplicate / empty slots);
+ * summing over the heads that share an index head gives d(bias).
+ * Deterministic: no floating-point atomics anywhere.
+ * ---------------------------------------------------------------------- */
+typedef struct {
+  const void* q;       int64_t q_sb, q_st, q_sh;       /* [B, T, HQ, D]     */
+  const void* k;       int64_t k_sb, k_st, k_sh;       /* [B, Sk, HKV, D]   */
+  const void* v;       int64_t v_sb, v_st, v_sh;       /* [B, Sk, HKV, D]   */
+  const void* o;       int64_t o_sb, o_st, o_sh;       /* [B, T, HQ, D]     */
+  const float* lse;    int64_t lse_sb, lse_st, lse_sh; /* [B, T, HQ]        */
+  const void* dout;    int64_t do_sb, do_st, do_sh;    /* [B, T, HQ, D]     */
+  const int32_t* idx;  int64_t idx_sb, idx_sh, idx_st; /* [B, HI, T, S]     */
+  const float* bias;   int64_t bias_sb, bias_sh, bias_st; /* like idx; NULL */
+  const int32_t* seg;  int64_t seg_sb;                 /* [B, T]; NULL = 0  */
+  void* dq;            int64_t dq_sb, dq_st, dq_sh;    /* like q            */
+  void* dk;            int64_t dk_sb, dk_st, dk_sh;    /* like k            */
+  void* dv;            int64_t dv_sb, dv_st, dv_sh;    /* like v            */
+  float* dbias;        int64_t db_sb, db_sh, db_st;    /* [B, HQ, T, S], slot stride 1; NULL = skip */
+  int32_t B, T, Sk, HQ, HKV, HI, D, S, block_size, local_window;
+  float scale;
+  int32_t dtype;
+} srswa_bwd_args;
+
+/* scratch bytes: delta [B, T, HQ] fp32 + the query-tile touch bitmap */
+size_t srswa_gather_bwd_workspace(const srswa_bwd_args* a);
+int srswa_gather_bwd(const srswa_bwd_args* a, void* scratch, size_t scratch_bytes, void* stream);
+
+/* ------------------------------------------------------------------------
+ * Indexer block-max score.  Replaces triton_block_max_score / K4
+ * (HF/sparse_gather_triton.py:445-524):
+ *   out[b,c,blk] = max_{j in blk, seg[b,c] <= j < max(pos[b,c]-LW+1, 0)} q[b,c].k[b,j]
+ * unscaled, fp32 accumulation, -inf when the block has no such key.
+ * bf16 / fp16; block size 16, 32 or a multiple of 64.
+ * ---------------------------------------------------------------------- */
+typedef struct {
+  const void* q;       int64_t q_sb, q_sc;             /* [B, C, D]                 */
+  const void* k;       int64_t k_sb, k_sk;             /* [B, Sk, D]                */
+  const int32_t* pos;  int64_t pos_sb, pos_sc;         /* [B, C] global positions   */
+  const int32_t* seg;  int64_t seg_sb, seg_sc;         /* [B, C] segment starts; NULL = 0 */
+  float* out;          int64_t o_sb, o_sc, o_sn;       /* [B, C, nblk] fp32         */
+  int32_t B, C, Sk, D, nblk, block_size, local_window;
+  int32_t dtype;
+} srswa_blockmax_args;
+
+int srswa_block_max_score(const srswa_blockmax_args* a, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

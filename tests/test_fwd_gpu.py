@@ -1,7 +1,8 @@
 """Gather-attention forward on the matrix cores vs the CPU oracle (C ABI).
 
-Bar: bf16/fp16 outputs max-abs <= 2e-2 against the fp64 oracle evaluated on
-the same (rounded) inputs; LSE (natural log) within 2e-2."""
+Bar: bf16/fp16 outputs max-abs <= 2e-2 (beyond the output format's own
+half-ulp, tests/tolerance.py) against the fp64 oracle evaluated on the same
+rounded inputs; fp32 LSE (natural log) within 2e-2."""
 
 import math
 
@@ -10,6 +11,7 @@ import torch
 
 from oracle import srswa_oracle as O
 from srswa import ops
+from tolerance import assert_close_lowp
 
 pytestmark = pytest.mark.gpu
 TOL = 2e-2
@@ -70,5 +72,5 @@ def test_fwd_matches_oracle(dev, name):
     q, k, v, bi, pos, bias = _case(1 + list(CASES).index(name), **c)
     scale = 1 / math.sqrt(c["D"])
     o, lse, ro, rl = _run(dev, q, k, v, bi, pos, bias, bs, lw, scale)
-    assert (o - ro).abs().max().item() <= TOL
+    assert_close_lowp(o, ro, c.get("dtype", torch.bfloat16), TOL, "o")
     assert (lse - rl).abs().max().item() <= TOL

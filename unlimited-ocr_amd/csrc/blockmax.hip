@@ -1,0 +1,174 @@
+// Fused indexer block-max score on the matrix cores (gfx950).
+//
+// Replaces _block_max_score_kernel / triton_block_max_score (K4,
+// HF/sparse_gather_triton.py:445-524), the fused form of the eager
+// "token_future | local_token" masked block amax of DeepseekV2Indexer.forward
+// (HF/_sparse_base_impl.py:3076-3094):
+//   out[b, c, blk] = max over keys j of blk with seg[b,c] <= j < max(pos[b,c]-LW+1, 0)
+//                    of q[b,c] . k[b,j]      (unscaled, fp32 accumulation; -inf if none)
+// One workgroup = (sequence, 64 query rows); two waves of 32 rows, each lane
+// owning one row.  Keys stream in 64-key chunks through LDS, S^T = K Q^T on
+// v_mfma_f32_32x32x16; chunks past the tile's last remote key are skipped and
+// their blocks written as -inf.  No dense [B, C, Sk] score tensor exists.
+#include "mfma_common.h"
+
+namespace srswa {
+namespace {
+
+struct BmaxK {
+  srswa_blockmax_args a;
+  int ntiles;
+};
+
+template <typename T, int D>
+__global__ __launch_bounds__(128) void block_max_kernel(BmaxK p) {
+  using M = Mfma<T>;
+  constexpr int KP = D + 8;
+  constexpr int KS = D / 16;
+  __shared__ __align__(16) T sK[kChunk * KP];
+  __shared__ int s_maxls;
+  const srswa_blockmax_args& a = p.a;
+  const int tid = threadIdx.x, wave = tid / kWave, lane = tid % kWave;
+  const int h = lane / 32, rl = lane % 32;
+  const int tile = blockIdx.x % p.ntiles;
+  const int b = blockIdx.x / p.ntiles;
+  const int row = tile * 64 + wave * 32 + rl;
+  const bool row_ok = row < a.C;
+  const int BS = a.block_size;
+
+  int ls = 0, seg = 0;
+  if (row_ok) {
+    const int pos = a.pos[(int64_t)b * a.pos_sb + (int64_t)row * a.pos_sc];
+    seg = a.seg ? a.seg[(int64_t)b * a.seg_sb + (int64_t)row * a.seg_sc] : 0;
+    ls = max(pos - (a.local_window - 1), 0);
+  }
+  if (tid == 0) s_maxls = 0;
+  __syncthreads();
+  if (row_ok) atomicMax(&s_maxls, min(ls, a.Sk));
+  __syncthreads();
+  const int kend = s_maxls;                       // no row has a remote key >= kend
+  const int nchunks = ceil_div(kend, kChunk);
+
+  uint4 qf[KS];
+  {
+    const T* qrow = reinterpret_cast<const T*>(a.q) + (int64_t)b * a.q_sb + (int64_t)(row_ok ? row : 0) * a.q_sc;
+#pragma unroll
+    for (int ks = 0; ks < KS; ++ks)
+      qf[ks] = row_ok ? *reinterpret_cast<const uint4*>(qrow + 16 * ks + 8 * h) : make_uint4(0, 0, 0, 0);
+  }
+  float* orow = a.out + (int64_t)b * a.o_sb + (int64_t)(row_ok ? row : 0) * a.o_sc;
+  const T* kg = reinterpret_cast<const T*>(a.k) + (int64_t)b * a.k_sb;
+  constexpr int PIECES = kChunk * D / 8;
+  float run = -INFINITY;                          // running max of the open block (BS >= 64)
+
+  for (int c = 0; c < nchunks; ++c) {
+    const int j0 = c * kChunk;
+    __syncthreads();
+    for (int pc = tid; pc < PIECES; pc += blockDim.x) {
+      const int key = pc / (D / 8), col = pc % (D / 8);
+      const int j = j0 + key;
+      const uint4 w = j < a.Sk ? *reinterpret_cast<const uint4*>(kg + (int64_t)j * a.k_sk + col * 8)
+                               : make_uint4(0, 0, 0, 0);
+      *reinterpret_cast<uint4*>(sK + key * KP + col * 8) = w;
+    }
+    __syncthreads();
+    f32x16_t s0 = zero16(), s1 = zero16();
+#pragma unroll
+    for (int ks = 0; ks < KS; ++ks) {
+      s0 = M::mac(*reinterpret_cast<const uint4*>(sK + rl * KP + 16 * ks + 8 * h), qf[ks], s0);
+      s1 = M::mac(*reinterpret_cast<const uint4*>(sK + (32 + rl) * KP + 16 * ks + 8 * h), qf[ks], s1);
+    }
+    if (BS >= kChunk) {
+      float mx = -INFINITY;
+#pragma unroll
+      for (int r = 0; r < 16; ++r)
+#pragma unroll
+        for (int half = 0; half < 2; ++half) {
+          const int j = j0 + 32 * half + d_row(r, h);
+          if (j >= seg && j < ls) mx = fmaxf(mx, half ? s1[r] : s0[r]);
+        }
+      run = fmaxf(run, mx);
+      const bool closes = ((j0 + kChunk) % BS == 0) || (c == nchunks - 1);
+      if (closes) {
+        run = fmaxf(run, __shfl_xor(run, 32, kWave));
+        const int blk = j0 / BS;
+        if (row_ok && h == 0 && blk < a.nblk) orow[(int64_t)blk * a.o_sn] = run;
+        run = -INFINITY;
+      }
+    } else {
+      // BS in {16, 32}: 64 / BS whole blocks per chunk
+      const int nsub = kChunk / BS;
+      for (int sb = 0; sb < nsub; ++sb) {
+        float mx = -INFINITY;
+#pragma unroll
+        for (int r = 0; r < 16; ++r)
+#pragma unroll
+          for (int half = 0; half < 2; ++half) {
+            const int off = 32 * half + d_row(r, h);
+            const int j = j0 + off;
+            if (off / BS == sb && j >= seg && j < ls) mx = fmaxf(mx, half ? s1[r] : s0[r]);
+          }
+        mx = fmaxf(mx, __shfl_xor(mx, 32, kWave));
+        const int blk = j0 / BS + sb;
+        if (row_ok && h == 0 && blk < a.nblk) orow[(int64_t)blk * a.o_sn] = mx;
+      }
+    }
+  }
+  // blocks after the last visited chunk hold no remote key of any row
+  if (row_ok && h == 0) {
+    const int first = nchunks * kChunk / BS + ((nchunks * kChunk) % BS ? 1 : 0);
+    for (int blk = first; blk < a.nblk; ++blk) orow[(int64_t)blk * a.o_sn] = -INFINITY;
+  }
+}
+
+template <typename T, int D>
+int launch_bmax(const BmaxK& k, hipStream_t st) {
+  hipLaunchKernelGGL((block_max_kernel<T, D>), dim3((unsigned)((int64_t)k.a.B * k.ntiles)), dim3(128), 0, st, k);
+  const hipError_t e = hipGetLastError();
+  if (e != hipSuccess) {
+    set_error("block max launch failed: %s", hipGetErrorString(e));
+    return SRSWA_LAUNCH;
+  }
+  return SRSWA_OK;
+}
+
+}  // namespace
+}  // namespace srswa
+
+using namespace srswa;
+
+extern "C" int srswa_block_max_score(const srswa_blockmax_args* a, void* stream) {
+  if (!a || !a->q || !a->k || !a->pos || !a->out) {
+    set_error("block max: null argument");
+    return SRSWA_INVALID;
+  }
+  if (a->B < 0 || a->C < 0 || a->Sk < 0 || a->nblk < 0 || a->block_size <= 0 || a->local_window <= 0) {
+    set_error("block max: bad sizes");
+    return SRSWA_INVALID;
+  }
+  if (a->B == 0 || a->C == 0 || a->nblk == 0) return SRSWA_OK;
+  if (a->dtype != SRSWA_BF16 && a->dtype != SRSWA_F16) {
+    set_error("block max: matrix-core path takes bf16 / fp16");
+    return SRSWA_UNSUPPORTED;
+  }
+  if (!(a->D == 64 || a->D == 128)) {
+    set_error("block max: head dim %d not supported", a->D);
+    return SRSWA_UNSUPPORTED;
+  }
+  const int BS = a->block_size;
+  if (!(BS == 16 || BS == 32 || BS % kChunk == 0)) {
+    set_error("block max: block size must be 16, 32 or a multiple of 64");
+    return SRSWA_UNSUPPORTED;
+  }
+  if (((uintptr_t)a->q & 15) || ((uintptr_t)a->k & 15) || (a->q_sb * 2) % 16 || (a->q_sc * 2) % 16 ||
+      (a->k_sb * 2) % 16 || (a->k_sk * 2) % 16) {
+    set_error("block max: rows must be 16-byte aligned");
+    return SRSWA_UNSUPPORTED;
+  }
+  BmaxK k{};
+  k.a = *a;
+  k.ntiles = ceil_div(a->C, 64);
+  hipStream_t s = reinterpret_cast<hipStream_t>(stream);
+  if (a->dtype == SRSWA_BF16) return a->D == 128 ? launch_bmax<bf16_t, 128>(k, s) : launch_bmax<bf16_t, 64>(k, s);
+  return a->D == 128 ? launch_bmax<__half, 128>(k, s) : launch_bmax<__half, 64>(k, s);
+}

@@ -56,20 +56,67 @@ __device__ __forceinline__ f32x16_t zero16() {
 // key offset (0..31) inside a 32x32 D tile held by register r of lane half h
 __device__ __forceinline__ int d_row(int r, int h) { return 8 * (r >> 2) + 4 * h + (r & 3); }
 
-// Per-tile chunk plan built in LDS by all threads of the workgroup:
-//   rows: key index qi, segment start seg, window start ls = max(qi-LW+1, seg)
-//   ids:  the rows' slot block ids (S per row, -1 = none)
-//   chunks: sorted list of 64-key chunks holding any window key or any key of a
-//           selected block that can be a remote key of some row.
-struct TilePlanSmem {
-  int* qi;        // [64]
-  int* seg;       // [64]
-  int* ls;        // [64]
-  int* ids;       // [64 * S]
-  float* bias;    // [64 * S] or nullptr
-  uint32_t* bits; // [nchunk_words]
-  int* chunks;    // [umax]
-  int* count;     // [1]
-};
+// Per-tile chunk plan, built in LDS by all threads of a workgroup from
+//   s_qi / s_seg / s_ls [64]: each row's key index, sample start and window start
+//   s_ids [64 * S]:           each row's slot block ids (-1 = none)
+// into the sorted list s_chunks of 64-key chunks holding a window key of some
+// row or a key of a selected block that is a remote key of that row.  s_bits
+// (nwords zeroed words) is the scratch bitmap.  Returns the chunk count.
+// Build the tile's chunk list; returns the chunk count (all threads).
+__device__ inline int build_chunk_plan(const int* s_qi, const int* s_seg, const int* s_ls, const int* s_ids,
+                                int S, int BS, int nrows, int nchunk, int nwords, uint32_t* s_bits,
+                                int* s_chunks, int* s_count, int LW, int Sk) {
+  const int tid = threadIdx.x, nthr = blockDim.x;
+  // window ranges: row r covers chunks [ls_r / 64, qi_r / 64]
+  const int wspan = (LW + kChunk - 1) / kChunk + 1;
+  for (int e = tid; e < nrows * wspan; e += nthr) {
+    const int r = e / wspan, k = e % wspan;
+    const int c0 = max(s_ls[r], 0) / kChunk, c1 = s_qi[r] / kChunk;
+    const int c = c0 + k;
+    if (c <= c1) atomicOr(&s_bits[c >> 5], 1u << (c & 31));
+  }
+  // remote keys of every selected block: [max(id*BS, seg), min(id*BS+BS, ls, qi+1))
+  const int bspan = (BS + kChunk - 1) / kChunk + 1;
+  const int maxblk = (Sk - 1) / BS;
+  for (int e = tid; e < nrows * S; e += nthr) {
+    const int r = e / S;
+    const int id = s_ids[e];
+    if (id < 0 || id > maxblk) continue;
+    const int lo = max(id * BS, s_seg[r]);
+    const int hi = min(min(id * BS + BS, s_ls[r]), s_qi[r] + 1);
+    if (lo >= hi) continue;
+    const int c0 = lo / kChunk, c1 = (hi - 1) / kChunk;
+    for (int c = c0; c <= c1 && c < c0 + bspan; ++c) atomicOr(&s_bits[c >> 5], 1u << (c & 31));
+  }
+  __syncthreads();
+  // compaction (wave 0): prefix popcount over the words
+  if (tid < kWave) {
+    int base = 0;
+    for (int w0 = 0; w0 < nwords; w0 += kWave) {
+      const int w = w0 + tid;
+      const uint32_t bits = w < nwords ? s_bits[w] : 0u;
+      const int cnt = __popc(bits);
+      int incl = cnt;
+#pragma unroll
+      for (int o = 1; o < kWave; o <<= 1) {
+        const int v = __shfl_up(incl, o, kWave);
+        if (tid >= o) incl += v;
+      }
+      int pos = base + incl - cnt;
+      uint32_t bb = bits;
+      while (bb) {
+        const int bit = __ffs(bb) - 1;
+        bb &= bb - 1;
+        s_chunks[pos++] = w * 32 + bit;
+      }
+      base += __shfl(incl, kWave - 1, kWave);
+    }
+    if (tid == 0) *s_count = base;
+  }
+  __syncthreads();
+  (void)nchunk;
+  return *s_count;
+}
+
 
 }  // namespace srswa

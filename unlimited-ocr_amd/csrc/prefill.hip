@@ -45,62 +45,6 @@ struct FwdSmem {
   }
 };
 
-// Build the tile's chunk list; returns the chunk count (all threads).
-__device__ int build_chunk_plan(const int* s_qi, const int* s_seg, const int* s_ls, const int* s_ids,
-                                int S, int BS, int nrows, int nchunk, int nwords, uint32_t* s_bits,
-                                int* s_chunks, int* s_count, int LW, int Sk) {
-  const int tid = threadIdx.x, nthr = blockDim.x;
-  // window ranges: row r covers chunks [ls_r / 64, qi_r / 64]
-  const int wspan = (LW + kChunk - 1) / kChunk + 1;
-  for (int e = tid; e < nrows * wspan; e += nthr) {
-    const int r = e / wspan, k = e % wspan;
-    const int c0 = max(s_ls[r], 0) / kChunk, c1 = s_qi[r] / kChunk;
-    const int c = c0 + k;
-    if (c <= c1) atomicOr(&s_bits[c >> 5], 1u << (c & 31));
-  }
-  // remote keys of every selected block: [max(id*BS, seg), min(id*BS+BS, ls, qi+1))
-  const int bspan = (BS + kChunk - 1) / kChunk + 1;
-  const int maxblk = (Sk - 1) / BS;
-  for (int e = tid; e < nrows * S; e += nthr) {
-    const int r = e / S;
-    const int id = s_ids[e];
-    if (id < 0 || id > maxblk) continue;
-    const int lo = max(id * BS, s_seg[r]);
-    const int hi = min(min(id * BS + BS, s_ls[r]), s_qi[r] + 1);
-    if (lo >= hi) continue;
-    const int c0 = lo / kChunk, c1 = (hi - 1) / kChunk;
-    for (int c = c0; c <= c1 && c < c0 + bspan; ++c) atomicOr(&s_bits[c >> 5], 1u << (c & 31));
-  }
-  __syncthreads();
-  // compaction (wave 0): prefix popcount over the words
-  if (tid < kWave) {
-    int base = 0;
-    for (int w0 = 0; w0 < nwords; w0 += kWave) {
-      const int w = w0 + tid;
-      const uint32_t bits = w < nwords ? s_bits[w] : 0u;
-      const int cnt = __popc(bits);
-      int incl = cnt;
-#pragma unroll
-      for (int o = 1; o < kWave; o <<= 1) {
-        const int v = __shfl_up(incl, o, kWave);
-        if (tid >= o) incl += v;
-      }
-      int pos = base + incl - cnt;
-      uint32_t bb = bits;
-      while (bb) {
-        const int bit = __ffs(bb) - 1;
-        bb &= bb - 1;
-        s_chunks[pos++] = w * 32 + bit;
-      }
-      base += __shfl(incl, kWave - 1, kWave);
-    }
-    if (tid == 0) *s_count = base;
-  }
-  __syncthreads();
-  (void)nchunk;
-  return *s_count;
-}
-
 template <typename T, int D>
 __global__ __launch_bounds__(128) void fwd_kernel(FwdK p) {
   using M = Mfma<T>;

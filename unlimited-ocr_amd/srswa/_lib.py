@@ -92,6 +92,45 @@ class FwdArgs(ctypes.Structure):
     ]
 
 
+class BwdArgs(ctypes.Structure):
+    """Mirror of ``srswa_bwd_args``."""
+
+    _fields_ = [
+        ("q", _vp), ("q_sb", _i64), ("q_st", _i64), ("q_sh", _i64),
+        ("k", _vp), ("k_sb", _i64), ("k_st", _i64), ("k_sh", _i64),
+        ("v", _vp), ("v_sb", _i64), ("v_st", _i64), ("v_sh", _i64),
+        ("o", _vp), ("o_sb", _i64), ("o_st", _i64), ("o_sh", _i64),
+        ("lse", _vp), ("lse_sb", _i64), ("lse_st", _i64), ("lse_sh", _i64),
+        ("dout", _vp), ("do_sb", _i64), ("do_st", _i64), ("do_sh", _i64),
+        ("idx", _vp), ("idx_sb", _i64), ("idx_sh", _i64), ("idx_st", _i64),
+        ("bias", _vp), ("bias_sb", _i64), ("bias_sh", _i64), ("bias_st", _i64),
+        ("seg", _vp), ("seg_sb", _i64),
+        ("dq", _vp), ("dq_sb", _i64), ("dq_st", _i64), ("dq_sh", _i64),
+        ("dk", _vp), ("dk_sb", _i64), ("dk_st", _i64), ("dk_sh", _i64),
+        ("dv", _vp), ("dv_sb", _i64), ("dv_st", _i64), ("dv_sh", _i64),
+        ("dbias", _vp), ("db_sb", _i64), ("db_sh", _i64), ("db_st", _i64),
+        ("B", _i32), ("T", _i32), ("Sk", _i32), ("HQ", _i32), ("HKV", _i32), ("HI", _i32),
+        ("D", _i32), ("S", _i32), ("block_size", _i32), ("local_window", _i32),
+        ("scale", ctypes.c_float),
+        ("dtype", _i32),
+    ]
+
+
+class BlockMaxArgs(ctypes.Structure):
+    """Mirror of ``srswa_blockmax_args``."""
+
+    _fields_ = [
+        ("q", _vp), ("q_sb", _i64), ("q_sc", _i64),
+        ("k", _vp), ("k_sb", _i64), ("k_sk", _i64),
+        ("pos", _vp), ("pos_sb", _i64), ("pos_sc", _i64),
+        ("seg", _vp), ("seg_sb", _i64), ("seg_sc", _i64),
+        ("out", _vp), ("o_sb", _i64), ("o_sc", _i64), ("o_sn", _i64),
+        ("B", _i32), ("C", _i32), ("Sk", _i32), ("D", _i32), ("nblk", _i32), ("block_size", _i32),
+        ("local_window", _i32),
+        ("dtype", _i32),
+    ]
+
+
 # name -> (restype, argtypes) of every exported entry point
 SIGNATURES = {
     "srswa_version": (ctypes.c_int, []),
@@ -104,10 +143,14 @@ SIGNATURES = {
     "srswa_topk_rows": (ctypes.c_int, [_vp, _i64, _i32, _i64, _i32, _i32, ctypes.c_float, _vp, _vp,
                                        _i64, _vp]),
     "srswa_gather_fwd": (ctypes.c_int, [ctypes.POINTER(FwdArgs), _vp]),
+    "srswa_gather_bwd_workspace": (ctypes.c_size_t, [ctypes.POINTER(BwdArgs)]),
+    "srswa_gather_bwd": (ctypes.c_int, [ctypes.POINTER(BwdArgs), _vp, ctypes.c_size_t, _vp]),
+    "srswa_block_max_score": (ctypes.c_int, [ctypes.POINTER(BlockMaxArgs), _vp]),
 }
 
 STRUCTS = {"srswa_decode_args": DecodeArgs, "srswa_index_args": IndexArgs,
-           "srswa_fwd_args": FwdArgs}
+           "srswa_fwd_args": FwdArgs, "srswa_bwd_args": BwdArgs,
+           "srswa_blockmax_args": BlockMaxArgs}
 
 _lib = None
 _lock = threading.Lock()

@@ -332,3 +332,116 @@ def gather_fwd(q, k, v, block_indices, *, block_size, local_window, scale, seg=N
     a.dtype = _lib.dtype_code(q.dtype)
     _lib.check(_lib.lib().srswa_gather_fwd(ctypes.byref(a), _lib.stream_ptr(q.device)), "srswa_gather_fwd")
     return out, lse
+
+
+def gather_bwd(q, k, v, o, lse, do, block_indices, *, block_size, local_window, scale, seg=None,
+               bias=None, need_dbias=False):
+    """Backward of ``gather_fwd``.  Returns (dq, dk, dv, dbias_heads) with
+    dbias_heads [B, HQ, T, S] (per query head) when ``need_dbias`` and a bias
+    was used, else None.  Deterministic (no floating-point atomics)."""
+    _require_cuda(q, k, v, o, lse, do, block_indices, seg, bias)
+    B, T, HQ, D = q.shape
+    Sk, HKV = k.shape[1], k.shape[2]
+    HI, S = block_indices.shape[1], block_indices.shape[-1]
+    idx = _i32(block_indices).contiguous()
+    if bias is not None:
+        if bias.dim() == 3:
+            bias = bias.unsqueeze(1)
+        bias = bias.to(torch.float32).expand(B, HI, T, S).contiguous()
+    if seg is not None:
+        seg = _i32(seg).contiguous()
+    if do.stride(-1) != 1:
+        do = do.contiguous()
+    dq = torch.empty(B, T, HQ, D, dtype=q.dtype, device=q.device)
+    dk = torch.empty(B, Sk, HKV, D, dtype=k.dtype, device=k.device)
+    dv = torch.empty(B, Sk, HKV, D, dtype=v.dtype, device=v.device)
+    dbh = None
+    if need_dbias and bias is not None:
+        dbh = torch.empty(B, HQ, T, S, dtype=torch.float32, device=q.device)
+    a = _lib.BwdArgs()
+    for name, t in (("q", q), ("k", k), ("v", v), ("o", o), ("dq", dq), ("dk", dk), ("dv", dv)):
+        setattr(a, name, t.data_ptr())
+        setattr(a, name + "_sb", t.stride(0))
+        setattr(a, name + "_st", t.stride(1))
+        setattr(a, name + "_sh", t.stride(2))
+    a.dout = do.data_ptr(); a.do_sb, a.do_st, a.do_sh = do.stride(0), do.stride(1), do.stride(2)
+    a.lse = lse.data_ptr(); a.lse_sb, a.lse_st, a.lse_sh = lse.stride(0), lse.stride(1), lse.stride(2)
+    a.idx = idx.data_ptr(); a.idx_sb, a.idx_sh, a.idx_st = idx.stride(0), idx.stride(1), idx.stride(2)
+    if bias is not None:
+        a.bias = bias.data_ptr(); a.bias_sb, a.bias_sh, a.bias_st = bias.stride(0), bias.stride(1), bias.stride(2)
+    if seg is not None:
+        a.seg = seg.data_ptr(); a.seg_sb = seg.stride(0)
+    if dbh is not None:
+        a.dbias = dbh.data_ptr(); a.db_sb, a.db_sh, a.db_st = dbh.stride(0), dbh.stride(1), dbh.stride(2)
+    a.B, a.T, a.Sk, a.HQ, a.HKV, a.HI, a.D, a.S = B, T, Sk, HQ, HKV, HI, D, S
+    a.block_size, a.local_window = int(block_size), max(1, int(local_window))
+    a.scale = float(scale)
+    a.dtype = _lib.dtype_code(q.dtype)
+    L_ = _lib.lib()
+    nbytes = L_.srswa_gather_bwd_workspace(ctypes.byref(a))
+    scr = _lib.scratch(q.device, nbytes)
+    st = L_.srswa_gather_bwd(ctypes.byref(a), _lib.ptr(scr), nbytes, _lib.stream_ptr(q.device))
+    _lib.check(st, "srswa_gather_bwd")
+    return dq, dk, dv, dbh
+
+
+class GatherAttnFn(torch.autograd.Function):
+    """Autograd glue of the fused gather attention (forward + backward on the
+    matrix cores).  Inputs are [B, T, H, D] views; ``bias`` (optional) is the
+    per-slot bias [B, T, S] or [B, HI, T, S] and receives a gradient."""
+
+    @staticmethod
+    def forward(ctx, q, k, v, sel, seg, bias, block_size, scale, local_window):
+        o, lse = gather_fwd(q, k, v, sel, block_size=block_size, local_window=local_window,
+                            scale=scale, seg=seg, bias=bias)
+        ctx.save_for_backward(q, k, v, sel, seg, bias, o, lse)
+        ctx.cfg = (block_size, scale, local_window)
+        ctx.bias_shape = None if bias is None else tuple(bias.shape)
+        return o
+
+    @staticmethod
+    def backward(ctx, do):
+        q, k, v, sel, seg, bias, o, lse = ctx.saved_tensors
+        block_size, scale, local_window = ctx.cfg
+        need_db = bias is not None and ctx.needs_input_grad[5]
+        dq, dk, dv, dbh = gather_bwd(q, k, v, o, lse, do, sel, block_size=block_size,
+                                     local_window=local_window, scale=scale, seg=seg, bias=bias,
+                                     need_dbias=need_db)
+        dbias = None
+        if dbh is not None:
+            B, HQ, T, S = dbh.shape
+            HI = sel.shape[1]
+            db = dbh.view(B, HI, HQ // HI, T, S).sum(2)            # heads -> their index head
+            dbias = db[:, 0] if len(ctx.bias_shape) == 3 else db
+            dbias = dbias.to(bias.dtype)
+        return dq, dk, dv, None, None, dbias, None, None, None
+
+
+def block_max_score(q, k, pos, seg, *, block_size, num_key_blocks, local_window):
+    """Indexer block-max score (see srswa_block_max_score): q [B, C, D],
+    k [B, Sk, D], pos / seg [B, C] -> fp32 [B, C, num_key_blocks]."""
+    _require_cuda(q, k, pos, seg)
+    B, C, D = q.shape
+    Sk = k.shape[1]
+    if q.dtype != k.dtype:
+        raise ValueError("q and k must share a dtype")
+    if q.stride(-1) != 1:
+        q = q.contiguous()
+    if k.stride(-1) != 1:
+        k = k.contiguous()
+    posi = _i32(pos).contiguous()
+    segi = None if seg is None else _i32(seg).contiguous()
+    out = torch.empty(B, C, int(num_key_blocks), dtype=torch.float32, device=q.device)
+    a = _lib.BlockMaxArgs()
+    a.q = q.data_ptr(); a.q_sb, a.q_sc = q.stride(0), q.stride(1)
+    a.k = k.data_ptr(); a.k_sb, a.k_sk = k.stride(0), k.stride(1)
+    a.pos = posi.data_ptr(); a.pos_sb, a.pos_sc = posi.stride(0), posi.stride(1)
+    if segi is not None:
+        a.seg = segi.data_ptr(); a.seg_sb, a.seg_sc = segi.stride(0), segi.stride(1)
+    a.out = out.data_ptr(); a.o_sb, a.o_sc, a.o_sn = out.stride(0), out.stride(1), out.stride(2)
+    a.B, a.C, a.Sk, a.D, a.nblk = B, C, Sk, D, int(num_key_blocks)
+    a.block_size, a.local_window = int(block_size), max(1, int(local_window))
+    a.dtype = _lib.dtype_code(q.dtype)
+    _lib.check(_lib.lib().srswa_block_max_score(ctypes.byref(a), _lib.stream_ptr(q.device)),
+               "srswa_block_max_score")
+    return out
