@@ -174,12 +174,143 @@ def bench_decode(args):
     return res
 
 
+def _time_launches(fn, steps, warmup, dev):
+    """Average ms per call of ``fn`` (HIP events on torch's current stream, which
+    is the stream the library launches on)."""
+    import torch
+    for _ in range(warmup):
+        fn()
+    torch.cuda.synchronize()
+    st = torch.cuda.current_stream(dev)
+    e0 = torch.cuda.Event(enable_timing=True)
+    e1 = torch.cuda.Event(enable_timing=True)
+    e0.record(st)
+    for _ in range(steps):
+        fn()
+    e1.record(st)
+    torch.cuda.synchronize()
+    return e0.elapsed_time(e1) / steps
+
+
+def bench_indexer(args):
+    """Config 2: head_cls/mean-pool indexer, B=32 decode queries, 10 heads,
+    L=32768, top-8 per head (HBM-bound streaming of the eligible keys)."""
+    import torch
+    from srswa import ops, workloads as W
+    dev = torch.device("cuda:0")
+    B, H, D, L, BS, LW, K = 32, 10, 128, 32768, 64, 512, 8
+    c = W.indexer_config(B=B, H=H, D=D, L=L, device=dev)
+    launch, idx, _, _ = ops.prepare_index_meanpool_topk(c["q"], c["k"], c["q_pos"].to(dev), block_size=BS,
+                                                         local_blocks=LW // BS, topk=K)
+    ms = _time_launches(launch, args.steps, args.warmup, dev)
+    nbytes = W.indexer_bytes(B, H, D, L, BS, LW)
+    gbs = nbytes / (ms * 1e-3) / 1e9
+    res = {"metric": "indexer queries/s + HBM GB/s (config 2)", "value": B / (ms * 1e-3), "unit": "queries/s",
+           "n_gpus": 1, "steps": args.steps, "warmup": args.warmup, "ms_per_step": ms,
+           "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "bf16 keys, fp32 scores",
+           "data": "synthetic (seeded; 5% hot blocks shifted +3 along the query direction)",
+           "config": {"workload": "config 2: mean-pool indexer, B=32, 10 heads, L=32768, block 64, top-8",
+                      "B": B, "heads": H, "kv_len": L, "block_size": BS, "topk_blocks": K},
+           "roofline": {"bound": "hbm", "achieved": gbs, "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                        "frac": gbs / HBM_PEAK_GBS, "traffic": _pmc_traffic("indexer_cfg2_traffic"),
+                        "algorithmic_bytes_per_launch": nbytes,
+                        "kernel": "srswa::index_summary_kernel<bf16,128,false> + topk_rows_kernel"}}
+    if not args.no_cpu:
+        res["cpu_baseline"] = cpu_baseline_indexer(args.cpu_budget)
+    return res
+
+
+def cpu_baseline_indexer(budget_s):
+    import torch
+    sys.path.insert(0, REPO)
+    from oracle import srswa_oracle as O
+    from srswa import workloads as W
+    n_thr = min(os.cpu_count() or 1, 16)
+    torch.set_num_threads(n_thr)
+    g = torch.Generator().manual_seed(1)
+    H, D, L, BS, LW = 10, 128, 32768, 64, 512
+    t = 0.0
+    n = 0
+    while t < budget_s and n < 32:
+        q = torch.randn(1, H, 1, D, generator=g)
+        k = torch.randn(1, H, L, D, generator=g).to(torch.bfloat16)
+        t0 = time.perf_counter()
+        sc = O.meanpool_block_scores(q, k.float(), torch.tensor([[L - 1]]), BS, LW // BS)
+        O.topk_blocks(sc, 8)
+        t += time.perf_counter() - t0
+        n += 1
+    return {"value": n / t, "unit": "queries/s", "cores": n_thr, "kind": "port",
+            "sample": f"{n} config-2 queries (10 heads x 32768 keys each), oracle restatement of "
+                      f"_block_scores_infer head_cls + top-k (fp32)"}
+
+
+def bench_prefill(args):
+    """Config 4: chunked prefill, B=4 x 2048 query rows at the tail of 65536 keys."""
+    import torch
+    from srswa import ops, workloads as W
+    dev = torch.device("cuda:0")
+    B, T, Sk, H, D, BS, LW, K = 4, 2048, 65536, 10, 128, 64, 512, 8
+    c = W.prefill_config(B=B, T=T, Sk=Sk, H=H, D=D, device=dev)
+    idx = c["block_idx"].to(dev)
+    fn = lambda: ops.gather_fwd(c["q"], c["k"], c["v"], idx, block_size=BS, local_window=LW, scale=c["scale"])
+    ms = _time_launches(fn, args.steps, args.warmup, dev)
+    wp, rp = W.attended_pairs(c["block_idx"], Sk, BS, LW)
+    flops = (wp + rp) * H * 4 * D
+    tfs = flops / (ms * 1e-3) / 1e12
+    return {"metric": "chunked-prefill tokens/s + MFMA TFLOP/s (config 4)", "value": B * T / (ms * 1e-3),
+            "unit": "tokens/s", "n_gpus": 1, "steps": args.steps, "warmup": args.warmup, "ms_per_step": ms,
+            "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "bf16",
+            "data": "synthetic (seeded N(0,1); top-8 per 64-query tile from the prefix)",
+            "config": {"workload": "config 4: chunked prefill B=4, 2048 of 65536, 10 heads, block 64, "
+                                   "top-8 + 512 window", "flops_per_step": flops},
+            "roofline": {"bound": "mfma", "achieved": tfs, "peak": 2500.0, "unit": "TFLOP/s",
+                         "frac": tfs / 2500.0, "traffic": None,
+                         "kernel": "srswa::fwd_kernel<bf16,128>"}}
+
+
+def bench_fwdbwd(args):
+    """Config 5: self-attention forward + backward, B=2, T=16384."""
+    import torch
+    from srswa import ops, workloads as W
+    dev = torch.device("cuda:0")
+    B, T, H, D, BS, LW, K = 2, 16384, 10, 128, 64, 512, 8
+    c = W.fwdbwd_config(B=B, T=T, H=H, D=D, device=dev)
+    idx = c["block_idx"].to(dev)
+    q, k, v, do = c["q"], c["k"], c["v"], c["do"]
+
+    def step():
+        o, lse = ops.gather_fwd(q, k, v, idx, block_size=BS, local_window=LW, scale=c["scale"])
+        ops.gather_bwd(q, k, v, o, lse, do, idx, block_size=BS, local_window=LW, scale=c["scale"])
+
+    ms = _time_launches(step, args.steps, args.warmup, dev)
+    fwd = lambda: ops.gather_fwd(q, k, v, idx, block_size=BS, local_window=LW, scale=c["scale"])
+    ms_f = _time_launches(fwd, args.steps, args.warmup, dev)
+    o, lse = fwd()
+    bwd = lambda: ops.gather_bwd(q, k, v, o, lse, do, idx, block_size=BS, local_window=LW, scale=c["scale"])
+    ms_b = _time_launches(bwd, args.steps, args.warmup, dev)
+    wp, rp = W.attended_pairs(c["block_idx"], T, BS, LW)
+    pairs = (wp + rp) * H
+    flops = pairs * (4 + 10) * D
+    tfs = flops / (ms * 1e-3) / 1e12
+    return {"metric": "fwd+bwd tokens/s + MFMA TFLOP/s (config 5)", "value": B * T / (ms * 1e-3),
+            "unit": "tokens/s", "n_gpus": 1, "steps": args.steps, "warmup": args.warmup, "ms_per_step": ms,
+            "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "bf16",
+            "data": "synthetic (seeded N(0,1); tile m selects min(8, m-8) blocks below m-8)",
+            "config": {"workload": "config 5: fwd+bwd B=2, T=16384, 10 heads, block 64, top-8 + 512 window",
+                       "flops_per_step": flops, "fwd_ms": ms_f, "bwd_ms": ms_b,
+                       "fwd_tflops": pairs * 4 * D / (ms_f * 1e-3) / 1e12,
+                       "bwd_tflops": pairs * 10 * D / (ms_b * 1e-3) / 1e12},
+            "roofline": {"bound": "mfma", "achieved": tfs, "peak": 2500.0, "unit": "TFLOP/s",
+                         "frac": tfs / 2500.0, "traffic": None,
+                         "kernel": "fwd_kernel + delta/touch/dq/dkv kernels"}}
+
+
 def main():
     ap = argparse.ArgumentParser(description=__doc__)
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=200)
     ap.add_argument("--warmup", type=int, default=20)
-    ap.add_argument("--config", default="decode", choices=["decode"])
+    ap.add_argument("--config", default="decode", choices=["decode", "indexer", "prefill", "fwdbwd"])
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--no-check", action="store_true", help="skip the oracle spot check")
     ap.add_argument("--cpu-budget", type=float, default=12.0)
@@ -188,7 +319,9 @@ def main():
         print("bench.py measures one GPU only: this build runs on a single MI355X "
               "(no multi-GPU path); use --gpus 1", file=sys.stderr)
         sys.exit(2)
-    res = bench_decode(args)
+    fn = {"decode": bench_decode, "indexer": bench_indexer, "prefill": bench_prefill,
+          "fwdbwd": bench_fwdbwd}[args.config]
+    res = fn(args)
     print(json.dumps(res), flush=True)
 
 

@@ -104,19 +104,21 @@ __global__ __launch_bounds__(256) void touch_kernel(BwdK p) {
 }
 
 // -------------------------------------------------------------- 3. dQ
+constexpr int kSlotCap = 32;   // planned chunks per tile covered by the slot table
+
 template <typename T, int D>
 __global__ __launch_bounds__(128) void dq_kernel(BwdK p) {
   using M = Mfma<T>;
   constexpr int KP = D + 8;
-  constexpr int VP = kChunk + 8;
   constexpr int KS = D / 16;
   constexpr int MT = D / 32;
+  constexpr int NT = 128;
   extern __shared__ __align__(16) unsigned char smem[];
   const srswa_bwd_args& a = p.a;
   T* sK = reinterpret_cast<T*>(smem);
-  T* sKt = sK + kChunk * KP;
-  T* sV = sKt + D * VP;
-  int* s_qi = reinterpret_cast<int*>(sV + kChunk * KP);
+  T* sV = sK + kChunk * KP;
+  int8_t* s_tab = reinterpret_cast<int8_t*>(sV + kChunk * KP);
+  int* s_qi = reinterpret_cast<int*>(s_tab + kSlotCap * 64 * 8);
   int* s_seg = s_qi + 64;
   int* s_ls = s_seg + 64;
   int* s_ids = s_ls + 64;
@@ -138,7 +140,7 @@ __global__ __launch_bounds__(128) void dq_kernel(BwdK p) {
   const int off = a.Sk - a.T;
   const int BS = a.block_size, LW = a.local_window, S = a.S;
 
-  for (int r = tid; r < 64; r += blockDim.x) {
+  for (int r = tid; r < 64; r += NT) {
     int qi = -1, seg = 0, ls = 0;
     if (r < nrows) {
       qi = off + t0 + r;
@@ -149,7 +151,7 @@ __global__ __launch_bounds__(128) void dq_kernel(BwdK p) {
     s_seg[r] = seg;
     s_ls[r] = ls;
   }
-  for (int e = tid; e < 64 * S; e += blockDim.x) {
+  for (int e = tid; e < 64 * S; e += NT) {
     const int r = e / S, s = e % S;
     int id = -1;
     float bv = 0.f;
@@ -161,14 +163,17 @@ __global__ __launch_bounds__(128) void dq_kernel(BwdK p) {
     s_bias[e] = bv;
     s_dbias[e] = 0.f;
   }
-  for (int w = tid; w < p.nwords; w += blockDim.x) s_bits[w] = 0u;
+  for (int w = tid; w < p.nwords; w += NT) s_bits[w] = 0u;
   __syncthreads();
   const int U = build_chunk_plan(s_qi, s_seg, s_ls, s_ids, S, BS, nrows, p.nchunk, p.nwords,
                                  s_bits, s_chunks, s_count, LW, a.Sk);
+  build_slot_table(s_qi, s_seg, s_ls, s_ids, s_chunks, U, kSlotCap, S, BS, a.Sk, nrows, s_tab);
 
   const int row = wave * 32 + rl;
   const bool row_ok = row < nrows;
   const int my_qi = s_qi[row], my_seg = s_seg[row], my_ls = s_ls[row];
+  const uint32_t wlen = (uint32_t)max(my_qi - my_ls + 1, 0);
+  const uint32_t rlen = (uint32_t)max(min(my_ls, my_qi + 1) - my_seg, 0);
   const int trow = t0 + (row_ok ? row : 0);
   uint4 qf[KS], gf[KS];
   {
@@ -194,85 +199,111 @@ __global__ __launch_bounds__(128) void dq_kernel(BwdK p) {
 
   const T* kg = reinterpret_cast<const T*>(a.k) + (int64_t)b * a.k_sb + (int64_t)kvh * a.k_sh;
   const T* vg = reinterpret_cast<const T*>(a.v) + (int64_t)b * a.v_sb + (int64_t)kvh * a.v_sh;
-  constexpr int PIECES = kChunk * D / 8;
+  constexpr int PPT = kChunk * D / 8 / NT;
+  uint4 kpre[PPT], vpre[PPT];
+  auto fetch = [&](int c) {
+#pragma unroll
+    for (int i = 0; i < PPT; ++i) {
+      const int pc = tid + i * NT;
+      const int j = c * kChunk + pc / (D / 8), col = pc % (D / 8);
+      const bool in = j < a.Sk;
+      kpre[i] = in ? *reinterpret_cast<const uint4*>(kg + (int64_t)j * a.k_st + col * 8) : make_uint4(0, 0, 0, 0);
+      vpre[i] = in ? *reinterpret_cast<const uint4*>(vg + (int64_t)j * a.v_st + col * 8) : make_uint4(0, 0, 0, 0);
+    }
+  };
+  const bool one_blk = (BS % kChunk) == 0;
+  const bool sub_blk = (kChunk % BS) == 0;
+  const int bs_shift = __ffs(BS) - 1;
 
+  if (U > 0) fetch(s_chunks[0]);
   for (int u = 0; u < U; ++u) {
     const int c = s_chunks[u];
     const int j0 = c * kChunk;
     __syncthreads();
-    for (int pc = tid; pc < PIECES; pc += blockDim.x) {
-      const int key = pc / (D / 8), col = pc % (D / 8);
-      const int j = j0 + key;
-      uint4 kw = make_uint4(0, 0, 0, 0), vw = make_uint4(0, 0, 0, 0);
-      if (j < a.Sk) {
-        kw = *reinterpret_cast<const uint4*>(kg + (int64_t)j * a.k_st + col * 8);
-        vw = *reinterpret_cast<const uint4*>(vg + (int64_t)j * a.v_st + col * 8);
-      }
-      *reinterpret_cast<uint4*>(sK + key * KP + col * 8) = kw;
-      *reinterpret_cast<uint4*>(sV + key * KP + col * 8) = vw;
-      const uint16_t* kk = reinterpret_cast<const uint16_t*>(&kw);
 #pragma unroll
-      for (int e = 0; e < 8; ++e) reinterpret_cast<uint16_t*>(sKt)[(col * 8 + e) * VP + key] = kk[e];
+    for (int i = 0; i < PPT; ++i) {
+      const int pc = tid + i * NT;
+      const int key = pc / (D / 8), col = pc % (D / 8);
+      *reinterpret_cast<uint4*>(sK + key * KP + col * 8) = kpre[i];
+      *reinterpret_cast<uint4*>(sV + key * KP + col * 8) = vpre[i];
     }
     __syncthreads();
+    if (u + 1 < U) fetch(s_chunks[u + 1]);
 
-    f32x16_t st0 = zero16(), st1 = zero16(), dp0 = zero16(), dp1 = zero16();
+    f32x16_t st[2] = {zero16(), zero16()}, dp[2] = {zero16(), zero16()};
 #pragma unroll
     for (int ks = 0; ks < KS; ++ks) {
-      st0 = M::mac(*reinterpret_cast<const uint4*>(sK + rl * KP + 16 * ks + 8 * h), qf[ks], st0);
-      st1 = M::mac(*reinterpret_cast<const uint4*>(sK + (32 + rl) * KP + 16 * ks + 8 * h), qf[ks], st1);
-      dp0 = M::mac(*reinterpret_cast<const uint4*>(sV + rl * KP + 16 * ks + 8 * h), gf[ks], dp0);
-      dp1 = M::mac(*reinterpret_cast<const uint4*>(sV + (32 + rl) * KP + 16 * ks + 8 * h), gf[ks], dp1);
+      st[0] = M::mac(*reinterpret_cast<const uint4*>(sK + rl * KP + 16 * ks + 8 * h), qf[ks], st[0]);
+      st[1] = M::mac(*reinterpret_cast<const uint4*>(sK + (32 + rl) * KP + 16 * ks + 8 * h), qf[ks], st[1]);
+      dp[0] = M::mac(*reinterpret_cast<const uint4*>(sV + rl * KP + 16 * ks + 8 * h), gf[ks], dp[0]);
+      dp[1] = M::mac(*reinterpret_cast<const uint4*>(sV + (32 + rl) * KP + 16 * ks + 8 * h), gf[ks], dp[1]);
     }
 
     const int blo = j0 / BS;
-    const int bhi = min(j0 + kChunk - 1, a.Sk - 1) / BS;
     bool memb[5];
     float mbias[5];
     int mslot[5];
+    if (u < kSlotCap) {
+      const uint2 tw = *reinterpret_cast<const uint2*>(s_tab + (u * 64 + row) * 8);
+      const int8_t* t8 = reinterpret_cast<const int8_t*>(&tw);
 #pragma unroll
-    for (int q = 0; q < 5; ++q) {
-      memb[q] = false;
-      mbias[q] = 0.f;
-      mslot[q] = -1;
-      const int blk = blo + q;
-      if (blk <= bhi && row_ok) {
-        for (int s = 0; s < S; ++s) {
-          if (s_ids[row * S + s] == blk) {
-            memb[q] = true;
-            mbias[q] = s_bias[row * S + s];
-            mslot[q] = s;
-            break;
-          }
+      for (int q = 0; q < 5; ++q) {
+        mslot[q] = t8[q];
+        memb[q] = t8[q] >= 0;
+        mbias[q] = memb[q] ? s_bias[row * S + t8[q]] : 0.f;
+      }
+    } else {
+      const int nq = min(j0 + kChunk - 1, a.Sk - 1) / BS - blo + 1;
+#pragma unroll
+      for (int q = 0; q < 5; ++q) {
+        memb[q] = false;
+        mbias[q] = 0.f;
+        mslot[q] = -1;
+        if (q < nq && row_ok) {
+          for (int s = 0; s < S; ++s)
+            if (s_ids[row * S + s] == blo + q) {
+              memb[q] = true;
+              mbias[q] = s_bias[row * S + s];
+              mslot[q] = s;
+              break;
+            }
         }
       }
     }
 
-    float ds[32];
     float dsum[5] = {0.f, 0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-    for (int r = 0; r < 16; ++r) {
+    for (int half = 0; half < 2; ++half)
 #pragma unroll
-      for (int half = 0; half < 2; ++half) {
-        const int j = j0 + 32 * half + d_row(r, h);
-        const float s = half ? st1[r] : st0[r];
-        const float dpv = half ? dp1[r] : dp0[r];
-        const bool win = j >= my_ls && j <= my_qi;
-        const int qb = j / BS - blo;
-        bool rem = !win && j >= my_seg && j < my_ls && j <= my_qi;
-        float bb = 0.f;
+      for (int r = 0; r < 16; ++r) {
+        const int offk = 32 * half + d_row(r, h);
+        const int j = j0 + offk;
+        const bool win = (uint32_t)(j - my_ls) < wlen;
+        bool rem = (uint32_t)(j - my_seg) < rlen;
+        int qb = 0;
+        float bb;
+        if (one_blk) {
+          rem = rem && memb[0];
+          bb = mbias[0];
+        } else {
+          qb = sub_blk ? (offk >> bs_shift) : (j / BS - blo);
+          bb = 0.f;
+          bool mm = false;
 #pragma unroll
-        for (int qq = 0; qq < 5; ++qq)
-          if (qb == qq) { rem = rem && memb[qq]; bb = mbias[qq]; }
-        const bool keep = win || rem;
-        const float pv = keep ? exp2f((rem ? s + bb : s) * kLog2e - lse_l2) : 0.f;
-        const float dsv = pv * (dpv - dlt);
-        ds[half * 16 + r] = dsv;
+          for (int qq = 0; qq < 5; ++qq)
+            if (qb == qq) { mm = memb[qq]; bb = mbias[qq]; }
+          rem = rem && mm;
+        }
+        const float sv = st[half][r];
+        const float pv = (win || rem) ? exp2f((rem ? sv + bb : sv) * kLog2e - lse_l2) : 0.f;
+        const float dsv = pv * (dp[half][r] - dlt);
+        st[half][r] = dsv;
+        if (rem) {
 #pragma unroll
-        for (int qq = 0; qq < 5; ++qq)
-          if (rem && qb == qq) dsum[qq] += dsv;
+          for (int qq = 0; qq < 5; ++qq)
+            if (qb == qq) dsum[qq] += dsv;
+        }
       }
-    }
     if (a.dbias) {
 #pragma unroll
       for (int qq = 0; qq < 5; ++qq) {
@@ -283,20 +314,17 @@ __global__ __launch_bounds__(128) void dq_kernel(BwdK p) {
     uint4 db[4];
 #pragma unroll
     for (int ks = 0; ks < 4; ++ks) {
-      const float* src = ds + (ks >> 1) * 16 + 8 * (ks & 1);
-      db[ks] = make_uint4(M::pack2(src[0], src[1]), M::pack2(src[2], src[3]),
-                          M::pack2(src[4], src[5]), M::pack2(src[6], src[7]));
+      const int hf = ks >> 1, r0 = 8 * (ks & 1);
+      db[ks] = make_uint4(M::pack2(st[hf][r0], st[hf][r0 + 1]), M::pack2(st[hf][r0 + 2], st[hf][r0 + 3]),
+                          M::pack2(st[hf][r0 + 4], st[hf][r0 + 5]), M::pack2(st[hf][r0 + 6], st[hf][r0 + 7]));
     }
+    // dQ^T += K^T dS^T  (K^T operands read column-wise from the natural K tile)
+    const uint16_t* k16 = reinterpret_cast<const uint16_t*>(sK);
 #pragma unroll
-    for (int mt = 0; mt < MT; ++mt) {
-      const T* krow = sKt + (32 * mt + rl) * VP;
+    for (int mt = 0; mt < MT; ++mt)
 #pragma unroll
-      for (int ks = 0; ks < 4; ++ks) {
-        const uint2 lo = *reinterpret_cast<const uint2*>(krow + 16 * ks + 4 * h);
-        const uint2 hi = *reinterpret_cast<const uint2*>(krow + 16 * ks + 8 + 4 * h);
-        dq[mt] = M::mac(make_uint4(lo.x, lo.y, hi.x, hi.y), db[ks], dq[mt]);
-      }
-    }
+      for (int ks = 0; ks < 4; ++ks)
+        dq[mt] = M::mac(a_operand_t<KP>(k16, 32 * mt + rl, ks, h), db[ks], dq[mt]);
   }
 
   if (row_ok) {
@@ -314,7 +342,7 @@ __global__ __launch_bounds__(128) void dq_kernel(BwdK p) {
   }
   if (a.dbias) {
     __syncthreads();
-    for (int e = tid; e < nrows * S; e += blockDim.x) {
+    for (int e = tid; e < nrows * S; e += NT) {
       const int r = e / S, s = e % S;
       a.dbias[(int64_t)b * a.db_sb + (int64_t)hq * a.db_sh + (int64_t)(t0 + r) * a.db_st + s] = s_dbias[e];
     }
@@ -326,17 +354,14 @@ template <typename T, int D>
 __global__ __launch_bounds__(128) void dkv_kernel(BwdK p) {
   using M = Mfma<T>;
   constexpr int KP = D + 8;
-  constexpr int VP = kTileRows + 8;
   constexpr int KS = D / 16;
   constexpr int MT = D / 32;
   constexpr int NQ = 5;                       // blocks a 64-key chunk can overlap (BS >= 16)
   extern __shared__ __align__(16) unsigned char smem[];
   const srswa_bwd_args& a = p.a;
   T* sQ = reinterpret_cast<T*>(smem);         // [64][KP]  q * scale, rounded
-  T* sQt = sQ + kTileRows * KP;               // [D][VP]
-  T* sG = sQt + D * VP;                       // [64][KP]  dO
-  T* sGt = sG + kTileRows * KP;               // [D][VP]
-  int4* s_row = reinterpret_cast<int4*>(sGt + D * VP);   // {qi, ls, seg, lse*log2e bits}
+  T* sG = sQ + kTileRows * KP;                // [64][KP]  dO
+  int4* s_row = reinterpret_cast<int4*>(sG + kTileRows * KP);   // {qi, ls, seg, lse*log2e bits}
   float* s_dlt = reinterpret_cast<float*>(s_row + 64);
   float* s_mb = s_dlt + 64;                   // [64][NQ] bias if member else NaN
   int* s_ids = reinterpret_cast<int*>(s_mb + 64 * NQ);   // [64 * S]
@@ -376,46 +401,69 @@ __global__ __launch_bounds__(128) void dkv_kernel(BwdK p) {
   const int tau_a = max(wlo_t, 0) / kTileRows;
   const int tau_b = whi_t < 0 ? -1 : min(whi_t / kTileRows, p.ntiles - 1);
 
+  constexpr int NT = 128;
+  constexpr int PPT = kTileRows * D / 8 / NT;
+  uint4 qpre[PPT], gpre[PPT];   // one tile's Q / dO pieces (loaded together, then staged)
+  int* s_tiles = reinterpret_cast<int*>(s_bias + 64 * a.S);    // visit list
+  __shared__ int s_ntiles;
+
   for (int gq = 0; gq < p.G; ++gq) {
     const int hq = kvh * p.G + gq;
     const int ih = hq / p.IG;
     const uint32_t* tb = p.touch + (((int64_t)b * a.HI + ih) * p.nchunk + c) * p.twords;
-    for (int w = 0; w < p.twords; ++w) {
-      uint32_t bits = tb[w];
-      // OR in the window range [tau_a, tau_b]
-      const int lo = max(tau_a - 32 * w, 0), hi = min(tau_b - 32 * w, 31);
-      if (lo <= hi) bits |= (hi - lo == 31) ? 0xffffffffu : (((1u << (hi - lo + 1)) - 1u) << lo);
-      while (bits) {
-        const int tau = 32 * w + __ffs(bits) - 1;
-        bits &= bits - 1;
-        if (tau >= p.ntiles) break;
+    // visit list: window tiles [tau_a, tau_b] plus every touched tile, ascending
+    __syncthreads();
+    if (tid == 0) {
+      int n = 0;
+      for (int w = 0; w < p.twords; ++w) {
+        uint32_t bits = tb[w];
+        const int lo = max(tau_a - 32 * w, 0), hi = min(tau_b - 32 * w, 31);
+        if (lo <= hi) bits |= (hi - lo == 31) ? 0xffffffffu : (((1u << (hi - lo + 1)) - 1u) << lo);
+        while (bits) {
+          const int tau = 32 * w + __ffs(bits) - 1;
+          bits &= bits - 1;
+          if (tau < p.ntiles) s_tiles[n++] = tau;
+        }
+      }
+      s_ntiles = n;
+    }
+    __syncthreads();
+    const int nt = s_ntiles;
+    auto fetch = [&](int tau) {
+      const int t0 = tau * kTileRows;
+      const int nrows = min(kTileRows, a.T - t0);
+#pragma unroll
+      for (int i = 0; i < PPT; ++i) {
+        const int pc = tid + i * NT;
+        const int r = pc / (D / 8), col = pc % (D / 8);
+        const bool in = r < nrows;
+        qpre[i] = in ? *reinterpret_cast<const uint4*>(reinterpret_cast<const T*>(a.q) + (int64_t)b * a.q_sb +
+                                                       (int64_t)(t0 + r) * a.q_st + (int64_t)hq * a.q_sh + col * 8)
+                     : make_uint4(0, 0, 0, 0);
+        gpre[i] = in ? *reinterpret_cast<const uint4*>(reinterpret_cast<const T*>(a.dout) + (int64_t)b * a.do_sb +
+                                                       (int64_t)(t0 + r) * a.do_st + (int64_t)hq * a.do_sh + col * 8)
+                     : make_uint4(0, 0, 0, 0);
+      }
+    };
+    for (int it = 0; it < nt; ++it) {
+      const int tau = s_tiles[it];
+      {
         const int t0 = tau * kTileRows;
         const int nrows = min(kTileRows, a.T - t0);
+        fetch(tau);        // all loads of the tile in flight at once
         __syncthreads();   // previous tile consumed
-        // stage the tile: q*scale (natural + transposed), dO (natural + transposed), row data
-        for (int pc = tid; pc < kTileRows * (D / 8); pc += blockDim.x) {
+#pragma unroll
+        for (int i = 0; i < PPT; ++i) {
+          const int pc = tid + i * NT;
           const int r = pc / (D / 8), col = pc % (D / 8);
-          uint4 qw = make_uint4(0, 0, 0, 0), gw = make_uint4(0, 0, 0, 0);
-          if (r < nrows) {
-            qw = *reinterpret_cast<const uint4*>(reinterpret_cast<const T*>(a.q) + (int64_t)b * a.q_sb +
-                                                 (int64_t)(t0 + r) * a.q_st + (int64_t)hq * a.q_sh + col * 8);
-            gw = *reinterpret_cast<const uint4*>(reinterpret_cast<const T*>(a.dout) + (int64_t)b * a.do_sb +
-                                                 (int64_t)(t0 + r) * a.do_st + (int64_t)hq * a.do_sh + col * 8);
-            uint32_t* ww = reinterpret_cast<uint32_t*>(&qw);
+          uint4 qw = qpre[i];
+          uint32_t* ww = reinterpret_cast<uint32_t*>(&qw);
 #pragma unroll
-            for (int e = 0; e < 4; ++e) ww[e] = M::pack2(M::lo(ww[e]) * a.scale, M::hi(ww[e]) * a.scale);
-          }
+          for (int e = 0; e < 4; ++e) ww[e] = M::pack2(M::lo(ww[e]) * a.scale, M::hi(ww[e]) * a.scale);
           *reinterpret_cast<uint4*>(sQ + r * KP + col * 8) = qw;
-          *reinterpret_cast<uint4*>(sG + r * KP + col * 8) = gw;
-          const uint16_t* q16 = reinterpret_cast<const uint16_t*>(&qw);
-          const uint16_t* g16 = reinterpret_cast<const uint16_t*>(&gw);
-#pragma unroll
-          for (int e = 0; e < 8; ++e) {
-            reinterpret_cast<uint16_t*>(sQt)[(col * 8 + e) * VP + r] = q16[e];
-            reinterpret_cast<uint16_t*>(sGt)[(col * 8 + e) * VP + r] = g16[e];
-          }
+          *reinterpret_cast<uint4*>(sG + r * KP + col * 8) = gpre[i];
         }
-        for (int r = tid; r < 64; r += blockDim.x) {
+        for (int r = tid; r < 64; r += NT) {
           int4 ri = make_int4(INT_MIN, 0, 0, 0);   // invalid row: qi < every key
           float dl = 0.f;
           if (r < nrows) {
@@ -429,7 +477,7 @@ __global__ __launch_bounds__(128) void dkv_kernel(BwdK p) {
           s_row[r] = ri;
           s_dlt[r] = dl;
         }
-        for (int e = tid; e < 64 * S; e += blockDim.x) {
+        for (int e = tid; e < 64 * S; e += NT) {
           const int r = e / S, s = e % S;
           int id = -1;
           float bv = 0.f;
@@ -442,7 +490,7 @@ __global__ __launch_bounds__(128) void dkv_kernel(BwdK p) {
         }
         __syncthreads();
         // membership of every row in the chunk's blocks (first slot's bias)
-        for (int e = tid; e < 64 * NQ; e += blockDim.x) {
+        for (int e = tid; e < 64 * NQ; e += NT) {
           const int r = e / NQ, qq = e % NQ;
           float mb = __int_as_float(0x7fc00000);   // NaN: not selected
           const int blk = blo + qq;
@@ -455,54 +503,49 @@ __global__ __launch_bounds__(128) void dkv_kernel(BwdK p) {
         __syncthreads();
 
         // S = Q K^T and dP = dO V^T for the 64 rows x this lane's key
-        f32x16_t s0 = zero16(), s1 = zero16(), g0 = zero16(), g1 = zero16();
+        f32x16_t sp[2] = {zero16(), zero16()}, gd[2] = {zero16(), zero16()};
 #pragma unroll
         for (int ks = 0; ks < KS; ++ks) {
-          s0 = M::mac(*reinterpret_cast<const uint4*>(sQ + rl * KP + 16 * ks + 8 * h), kf[ks], s0);
-          s1 = M::mac(*reinterpret_cast<const uint4*>(sQ + (32 + rl) * KP + 16 * ks + 8 * h), kf[ks], s1);
-          g0 = M::mac(*reinterpret_cast<const uint4*>(sG + rl * KP + 16 * ks + 8 * h), vf[ks], g0);
-          g1 = M::mac(*reinterpret_cast<const uint4*>(sG + (32 + rl) * KP + 16 * ks + 8 * h), vf[ks], g1);
+          sp[0] = M::mac(*reinterpret_cast<const uint4*>(sQ + rl * KP + 16 * ks + 8 * h), kf[ks], sp[0]);
+          sp[1] = M::mac(*reinterpret_cast<const uint4*>(sQ + (32 + rl) * KP + 16 * ks + 8 * h), kf[ks], sp[1]);
+          gd[0] = M::mac(*reinterpret_cast<const uint4*>(sG + rl * KP + 16 * ks + 8 * h), vf[ks], gd[0]);
+          gd[1] = M::mac(*reinterpret_cast<const uint4*>(sG + (32 + rl) * KP + 16 * ks + 8 * h), vf[ks], gd[1]);
         }
-        float pp[32], dd[32];
+        // in place: sp <- P, gd <- dS
 #pragma unroll
-        for (int r = 0; r < 16; ++r) {
+        for (int half = 0; half < 2; ++half)
 #pragma unroll
-          for (int half = 0; half < 2; ++half) {
+          for (int r = 0; r < 16; ++r) {
             const int row = 32 * half + d_row(r, h);
             const int4 ri = s_row[row];
             const float mb = s_mb[row * NQ + qmine];
             const bool win = jmine >= ri.y && jmine <= ri.x;
             const bool rem = !win && jmine >= ri.z && jmine < ri.y && jmine <= ri.x && !(mb != mb);
-            const float s = half ? s1[r] : s0[r];
-            const float pv = (key_ok && (win || rem)) ? exp2f((rem ? s + mb : s) * kLog2e - __int_as_float(ri.w)) : 0.f;
-            const float gv = half ? g1[r] : g0[r];
-            pp[half * 16 + r] = pv;
-            dd[half * 16 + r] = pv * (gv - s_dlt[row]);
+            const float sv = sp[half][r];
+            const float pv = (key_ok && (win || rem)) ? exp2f((rem ? sv + mb : sv) * kLog2e - __int_as_float(ri.w)) : 0.f;
+            sp[half][r] = pv;
+            gd[half][r] = pv * (gd[half][r] - s_dlt[row]);
           }
-        }
         uint4 pb[4], db[4];
 #pragma unroll
         for (int ks = 0; ks < 4; ++ks) {
-          const float* ps = pp + (ks >> 1) * 16 + 8 * (ks & 1);
-          const float* ds = dd + (ks >> 1) * 16 + 8 * (ks & 1);
-          pb[ks] = make_uint4(M::pack2(ps[0], ps[1]), M::pack2(ps[2], ps[3]), M::pack2(ps[4], ps[5]), M::pack2(ps[6], ps[7]));
-          db[ks] = make_uint4(M::pack2(ds[0], ds[1]), M::pack2(ds[2], ds[3]), M::pack2(ds[4], ds[5]), M::pack2(ds[6], ds[7]));
+          const int hf = ks >> 1, r0 = 8 * (ks & 1);
+          pb[ks] = make_uint4(M::pack2(sp[hf][r0], sp[hf][r0 + 1]), M::pack2(sp[hf][r0 + 2], sp[hf][r0 + 3]),
+                              M::pack2(sp[hf][r0 + 4], sp[hf][r0 + 5]), M::pack2(sp[hf][r0 + 6], sp[hf][r0 + 7]));
+          db[ks] = make_uint4(M::pack2(gd[hf][r0], gd[hf][r0 + 1]), M::pack2(gd[hf][r0 + 2], gd[hf][r0 + 3]),
+                              M::pack2(gd[hf][r0 + 4], gd[hf][r0 + 5]), M::pack2(gd[hf][r0 + 6], gd[hf][r0 + 7]));
         }
-        // dV^T += dO^T P ; dK^T += (q*scale)^T dS
+        // dV^T += dO^T P ; dK^T += (q*scale)^T dS  (transposed operands read
+        // column-wise from the natural Q / dO tiles)
+        const uint16_t* g16 = reinterpret_cast<const uint16_t*>(sG);
+        const uint16_t* q16 = reinterpret_cast<const uint16_t*>(sQ);
 #pragma unroll
-        for (int mt = 0; mt < MT; ++mt) {
-          const T* grow = sGt + (32 * mt + rl) * VP;
-          const T* qrow = sQt + (32 * mt + rl) * VP;
+        for (int mt = 0; mt < MT; ++mt)
 #pragma unroll
           for (int ks = 0; ks < 4; ++ks) {
-            const uint2 glo = *reinterpret_cast<const uint2*>(grow + 16 * ks + 4 * h);
-            const uint2 ghi = *reinterpret_cast<const uint2*>(grow + 16 * ks + 8 + 4 * h);
-            dv[mt] = M::mac(make_uint4(glo.x, glo.y, ghi.x, ghi.y), pb[ks], dv[mt]);
-            const uint2 qlo = *reinterpret_cast<const uint2*>(qrow + 16 * ks + 4 * h);
-            const uint2 qhi = *reinterpret_cast<const uint2*>(qrow + 16 * ks + 8 + 4 * h);
-            dk[mt] = M::mac(make_uint4(qlo.x, qlo.y, qhi.x, qhi.y), db[ks], dk[mt]);
+            dv[mt] = M::mac(a_operand_t<KP>(g16, 32 * mt + rl, ks, h), pb[ks], dv[mt]);
+            dk[mt] = M::mac(a_operand_t<KP>(q16, 32 * mt + rl, ks, h), db[ks], dk[mt]);
           }
-        }
       }
     }
   }
@@ -587,27 +630,23 @@ size_t touch_words(const BwdK& k) { return (size_t)k.a.B * k.a.HI * k.nchunk * k
 
 size_t dq_smem(const BwdK& k) {
   const int D = k.a.D;
-  size_t n = (size_t)kChunk * (D + 8) * 2 * 2 + (size_t)D * (kChunk + 8) * 2;
+  size_t n = (size_t)kChunk * (D + 8) * 2 * 2 + (size_t)kSlotCap * 64 * 8;
   n += 3 * 64 * 4 + (size_t)64 * k.a.S * 4 * 3 + (size_t)k.nwords * 4 + (size_t)k.umax * 4 + 16;
   return (n + 15) / 16 * 16;
 }
 size_t dkv_smem(const BwdK& k) {
   const int D = k.a.D;
-  size_t n = (size_t)kTileRows * (D + 8) * 2 * 2 + (size_t)D * (kTileRows + 8) * 2 * 2;
-  n += 64 * 16 + 64 * 4 + 64 * 5 * 4 + (size_t)64 * k.a.S * 4 * 2 + 16;
+  size_t n = (size_t)kTileRows * (D + 8) * 2 * 2;
+  n += 64 * 16 + 64 * 4 + 64 * 5 * 4 + (size_t)64 * k.a.S * 4 * 2 + (size_t)k.ntiles * 4 + 16;
   return (n + 15) / 16 * 16;
 }
 
 template <typename T, int D>
 int launch_bwd(const BwdK& k, hipStream_t st) {
-  static bool attr = false;
-  if (!attr) {
-    hipFuncSetAttribute(reinterpret_cast<const void*>(&dq_kernel<T, D>),
-                        hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024);
-    hipFuncSetAttribute(reinterpret_cast<const void*>(&dkv_kernel<T, D>),
-                        hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024);
-    attr = true;
-  }
+  static size_t granted_dq = 0, granted_dkv = 0;
+  if (!ensure_dynamic_lds(&dq_kernel<T, D>, dq_smem(k), &granted_dq) ||
+      !ensure_dynamic_lds(&dkv_kernel<T, D>, dkv_smem(k), &granted_dkv))
+    return SRSWA_UNSUPPORTED;
   const srswa_bwd_args& a = k.a;
   const int rpw = kWave / (D / 8);
   const int64_t rows = (int64_t)a.B * a.T * a.HQ;
@@ -652,7 +691,7 @@ extern "C" int srswa_gather_bwd(const srswa_bwd_args* a, void* scratch, size_t s
     set_error("bwd: scratch of %zu bytes required (got %zu)", need, scratch_bytes);
     return SRSWA_WORKSPACE;
   }
-  if (dq_smem(k) > 160 * 1024 || dkv_smem(k) > 160 * 1024) {
+  if (dq_smem(k) > 156 * 1024 || dkv_smem(k) > 156 * 1024) {
     set_error("bwd: LDS budget exceeded (key length too large)");
     return SRSWA_UNSUPPORTED;
   }

@@ -62,7 +62,6 @@ __device__ __forceinline__ int d_row(int r, int h) { return 8 * (r >> 2) + 4 * h
 // into the sorted list s_chunks of 64-key chunks holding a window key of some
 // row or a key of a selected block that is a remote key of that row.  s_bits
 // (nwords zeroed words) is the scratch bitmap.  Returns the chunk count.
-// Build the tile's chunk list; returns the chunk count (all threads).
 __device__ inline int build_chunk_plan(const int* s_qi, const int* s_seg, const int* s_ls, const int* s_ids,
                                 int S, int BS, int nrows, int nchunk, int nwords, uint32_t* s_bits,
                                 int* s_chunks, int* s_count, int LW, int Sk) {
@@ -118,5 +117,76 @@ __device__ inline int build_chunk_plan(const int* s_qi, const int* s_seg, const 
   return *s_count;
 }
 
+
+// A operand of a transposed product X^T P^T (M = feature d, K = 16 rows of X)
+// read from X stored naturally in LDS as [row][pitch]: lane (m = d, half h)
+// needs X[row(h, j)][d] for the permuted row order of the B operand (see the
+// header comment).  Eight 16-bit reads; lanes of one read touch 32 consecutive
+// columns of two rows 4 apart, which with a pitch of D+8 elements land in
+// disjoint bank ranges (no conflicts).
+template <int PITCH>
+__device__ __forceinline__ uint4 a_operand_t(const uint16_t* x, int d, int ks, int h) {
+  const uint16_t* p = x + (16 * ks + 4 * h) * PITCH + d;
+  uint32_t w[4];
+#pragma unroll
+  for (int i = 0; i < 2; ++i) {
+    const uint16_t* q = p + 8 * i * PITCH;
+    w[2 * i] = (uint32_t)q[0] | ((uint32_t)q[PITCH] << 16);
+    w[2 * i + 1] = (uint32_t)q[2 * PITCH] | ((uint32_t)q[3 * PITCH] << 16);
+  }
+  return make_uint4(w[0], w[1], w[2], w[3]);
+}
+
+// First slot (or -1) of each row's selected blocks overlapping each planned
+// chunk: tab[(u * 64 + row) * 8 + q] for chunk position u < ucap and the q-th
+// block overlapping the chunk.  Built by one thread per row walking its slots
+// in order, so the first slot holding an id wins (duplicates never count twice).
+__device__ inline void build_slot_table(const int* s_qi, const int* s_seg, const int* s_ls,
+                                        const int* s_ids, const int* s_chunks, int U, int ucap,
+                                        int S, int BS, int Sk, int nrows, int8_t* tab) {
+  const int tid = threadIdx.x;
+  const int ulim = min(U, ucap);
+  for (int w = tid; w < ulim * 64 * 8 / 4; w += blockDim.x) reinterpret_cast<int*>(tab)[w] = -1;
+  __syncthreads();
+  if (tid < nrows) {
+    const int r = tid;
+    const int maxblk = (Sk - 1) / BS;
+    for (int s = 0; s < S; ++s) {
+      const int id = s_ids[r * S + s];
+      if (id < 0 || id > maxblk) continue;
+      const int lo = max(id * BS, s_seg[r]);
+      const int hi = min(min(id * BS + BS, s_ls[r]), s_qi[r] + 1);
+      if (lo >= hi) continue;
+      for (int c = lo / kChunk; c <= (hi - 1) / kChunk; ++c) {
+        int a = 0, b = U;                       // lower_bound of c in s_chunks
+        while (a < b) {
+          const int m = (a + b) >> 1;
+          if (s_chunks[m] < c) a = m + 1; else b = m;
+        }
+        if (a >= ulim || s_chunks[a] != c) continue;
+        const int q = id - (c * kChunk) / BS;
+        int8_t* e = tab + ((a * 64 + r) * 8 + q);
+        if (q >= 0 && q < 8 && *e < 0) *e = (int8_t)s;
+      }
+    }
+  }
+  __syncthreads();
+}
+
+// Raise a kernel's dynamic-LDS limit to `bytes` when it needs more than the
+// default; returns false (error recorded) when the runtime refuses.
+template <typename F>
+inline bool ensure_dynamic_lds(F* kernel, size_t bytes, size_t* granted) {
+  if (bytes <= 64 * 1024 || bytes <= *granted) return true;
+  const hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(kernel),
+                                           hipFuncAttributeMaxDynamicSharedMemorySize, (int)bytes);
+  if (e != hipSuccess) {
+    (void)hipGetLastError();
+    set_error("cannot grant %zu bytes of LDS: %s", bytes, hipGetErrorString(e));
+    return false;
+  }
+  *granted = bytes;
+  return true;
+}
 
 }  // namespace srswa

@@ -19,8 +19,9 @@
 // visit (window ranges and selected blocks of all 64 rows, as a bitmap then a
 // prefix-popcount compaction), so a tile whose rows share their selection (the
 // indexer selects per 64-query tile) visits |selected| + |window| chunks once
-// instead of once per row.  Per chunk: K (row pitch D+8) and V^T (pitch 72)
-// are staged in LDS, S^T = K Q^T and O^T += V^T P^T run on
+// instead of once per row.  Per chunk: K and V (row pitch D+8) are staged in
+// LDS, S^T = K Q^T and O^T += V^T P^T (V^T operands read column-wise from the
+// natural V tile, bank-conflict free) run on
 // v_mfma_f32_32x32x16_{bf16,f16}; q is pre-multiplied by the scale and rounded
 // to the input dtype and P is rounded to it before the PV product, the same
 // rounding points as the reference kernels (HF/sparse_gather_triton.py:68,94).
@@ -37,9 +38,12 @@ struct FwdK {
   int G, IG;
 };
 
+constexpr int kSlotCap = 32;   // planned chunks per tile covered by the slot table
+
 struct FwdSmem {
   static size_t bytes(int D, int S, bool bias, int nwords, int umax, int esz) {
-    size_t n = (size_t)kChunk * (D + 8) * esz + (size_t)D * (kChunk + 8) * esz;
+    size_t n = (size_t)kChunk * (D + 8) * esz * 2;                 // K, V (natural)
+    n += (size_t)kSlotCap * 64 * 8;                                // slot table
     n += 3 * 64 * 4 + (size_t)64 * S * 4 * (bias ? 2 : 1) + (size_t)nwords * 4 + (size_t)umax * 4 + 16;
     return (n + 15) / 16 * 16;
   }
@@ -48,15 +52,15 @@ struct FwdSmem {
 template <typename T, int D>
 __global__ __launch_bounds__(128) void fwd_kernel(FwdK p) {
   using M = Mfma<T>;
-  constexpr int KP = D + 8;          // K row pitch (elements)
-  constexpr int VP = kChunk + 8;     // V^T row pitch
+  constexpr int KP = D + 8;          // K / V row pitch (elements)
   constexpr int KS = D / 16;         // k-steps over the head dim
   constexpr int MT = D / 32;         // 32-row tiles of O^T
   extern __shared__ __align__(16) unsigned char smem[];
   const srswa_fwd_args& a = p.a;
   T* sK = reinterpret_cast<T*>(smem);
-  T* sVt = sK + kChunk * KP;
-  int* s_qi = reinterpret_cast<int*>(sVt + D * VP);
+  T* sV = sK + kChunk * KP;
+  int8_t* s_tab = reinterpret_cast<int8_t*>(sV + kChunk * KP);
+  int* s_qi = reinterpret_cast<int*>(s_tab + kSlotCap * 64 * 8);
   int* s_seg = s_qi + 64;
   int* s_ls = s_seg + 64;
   int* s_ids = s_ls + 64;
@@ -65,6 +69,7 @@ __global__ __launch_bounds__(128) void fwd_kernel(FwdK p) {
   int* s_chunks = reinterpret_cast<int*>(s_bits + p.nwords);
   int* s_count = s_chunks + p.umax;
 
+  constexpr int NT = 128;
   const int tid = threadIdx.x, wave = tid / kWave, lane = tid % kWave;
   const int h = lane / 32, rl = lane % 32;
   const int tile = blockIdx.x % p.ntiles;
@@ -77,7 +82,7 @@ __global__ __launch_bounds__(128) void fwd_kernel(FwdK p) {
   const int off = a.Sk - a.T;
   const int BS = a.block_size, LW = a.local_window, S = a.S;
 
-  for (int r = tid; r < 64; r += blockDim.x) {
+  for (int r = tid; r < 64; r += NT) {
     int qi = -1, seg = 0, ls = 0;
     if (r < nrows) {
       qi = off + t0 + r;
@@ -88,7 +93,7 @@ __global__ __launch_bounds__(128) void fwd_kernel(FwdK p) {
     s_seg[r] = seg;
     s_ls[r] = ls;
   }
-  for (int e = tid; e < 64 * S; e += blockDim.x) {
+  for (int e = tid; e < 64 * S; e += NT) {
     const int r = e / S, s = e % S;
     int id = -1;
     float bv = 0.f;
@@ -99,15 +104,18 @@ __global__ __launch_bounds__(128) void fwd_kernel(FwdK p) {
     s_ids[e] = id;
     if (a.bias) s_bias[e] = bv;
   }
-  for (int w = tid; w < p.nwords; w += blockDim.x) s_bits[w] = 0u;
+  for (int w = tid; w < p.nwords; w += NT) s_bits[w] = 0u;
   __syncthreads();
   const int U = build_chunk_plan(s_qi, s_seg, s_ls, s_ids, S, BS, nrows, p.nchunk, p.nwords,
                                  s_bits, s_chunks, s_count, LW, a.Sk);
+  build_slot_table(s_qi, s_seg, s_ls, s_ids, s_chunks, U, kSlotCap, S, BS, a.Sk, nrows, s_tab);
 
-  // this lane's row and its pre-scaled q fragments (B operand of S^T = K Q^T)
+  // this lane's row: window [ls, qi] and remote range [seg, min(ls, qi+1))
   const int row = wave * 32 + rl;
   const bool row_ok = row < nrows;
   const int my_qi = s_qi[row], my_seg = s_seg[row], my_ls = s_ls[row];
+  const uint32_t wlen = (uint32_t)max(my_qi - my_ls + 1, 0);
+  const uint32_t rlen = (uint32_t)max(min(my_ls, my_qi + 1) - my_seg, 0);
   uint4 qf[KS];
   {
     const T* qrow = reinterpret_cast<const T*>(a.q) + (int64_t)b * a.q_sb +
@@ -129,115 +137,142 @@ __global__ __launch_bounds__(128) void fwd_kernel(FwdK p) {
 
   const T* kg = reinterpret_cast<const T*>(a.k) + (int64_t)b * a.k_sb + (int64_t)kvh * a.k_sh;
   const T* vg = reinterpret_cast<const T*>(a.v) + (int64_t)b * a.v_sb + (int64_t)kvh * a.v_sh;
-  constexpr int PIECES = kChunk * D / 8;     // 16-byte pieces per chunk and tensor
+  // chunk staging: every thread owns PPT 16-byte pieces of K and of V; the next
+  // chunk's pieces are fetched into registers while the current one computes
+  constexpr int PPT = kChunk * D / 8 / NT;
+  uint4 kpre[PPT], vpre[PPT];
+  auto fetch = [&](int c) {
+#pragma unroll
+    for (int i = 0; i < PPT; ++i) {
+      const int pc = tid + i * NT;
+      const int j = c * kChunk + pc / (D / 8), col = pc % (D / 8);
+      const bool in = j < a.Sk;
+      kpre[i] = in ? *reinterpret_cast<const uint4*>(kg + (int64_t)j * a.k_st + col * 8) : make_uint4(0, 0, 0, 0);
+      vpre[i] = in ? *reinterpret_cast<const uint4*>(vg + (int64_t)j * a.v_st + col * 8) : make_uint4(0, 0, 0, 0);
+    }
+  };
+  const bool one_blk = (BS % kChunk) == 0;      // every chunk lies inside one block
+  const bool sub_blk = (kChunk % BS) == 0;      // every chunk holds 64/BS whole blocks
+  const int bs_shift = __ffs(BS) - 1;
 
+  if (U > 0) fetch(s_chunks[0]);
   for (int u = 0; u < U; ++u) {
     const int c = s_chunks[u];
     const int j0 = c * kChunk;
     __syncthreads();   // previous chunk fully consumed
-    for (int pc = tid; pc < PIECES; pc += blockDim.x) {
-      const int key = pc / (D / 8), col = pc % (D / 8);
-      const int j = j0 + key;
-      uint4 kw = make_uint4(0, 0, 0, 0), vw = make_uint4(0, 0, 0, 0);
-      if (j < a.Sk) {
-        kw = *reinterpret_cast<const uint4*>(kg + (int64_t)j * a.k_st + col * 8);
-        vw = *reinterpret_cast<const uint4*>(vg + (int64_t)j * a.v_st + col * 8);
-      }
-      *reinterpret_cast<uint4*>(sK + key * KP + col * 8) = kw;
-      const uint16_t* vv = reinterpret_cast<const uint16_t*>(&vw);
 #pragma unroll
-      for (int e = 0; e < 8; ++e) reinterpret_cast<uint16_t*>(sVt)[(col * 8 + e) * VP + key] = vv[e];
+    for (int i = 0; i < PPT; ++i) {
+      const int pc = tid + i * NT;
+      const int key = pc / (D / 8), col = pc % (D / 8);
+      *reinterpret_cast<uint4*>(sK + key * KP + col * 8) = kpre[i];
+      *reinterpret_cast<uint4*>(sV + key * KP + col * 8) = vpre[i];
     }
     __syncthreads();
+    if (u + 1 < U) fetch(s_chunks[u + 1]);
 
     // S^T (keys x rows) for the two 32-key halves of the chunk
-    f32x16_t st0 = zero16(), st1 = zero16();
+    f32x16_t st[2] = {zero16(), zero16()};
 #pragma unroll
     for (int ks = 0; ks < KS; ++ks) {
       const uint4 a0 = *reinterpret_cast<const uint4*>(sK + rl * KP + 16 * ks + 8 * h);
       const uint4 a1 = *reinterpret_cast<const uint4*>(sK + (32 + rl) * KP + 16 * ks + 8 * h);
-      st0 = M::mac(a0, qf[ks], st0);
-      st1 = M::mac(a1, qf[ks], st1);
+      st[0] = M::mac(a0, qf[ks], st[0]);
+      st[1] = M::mac(a1, qf[ks], st[1]);
     }
 
-    // membership of this row in the (<= 5) blocks the chunk overlaps
+    // this row's selected blocks among the (<= 5) the chunk overlaps
     const int blo = j0 / BS;
-    const int bhi = min(j0 + kChunk - 1, a.Sk - 1) / BS;
     bool memb[5];
     float mbias[5];
+    if (u < kSlotCap) {
+      const uint2 tw = *reinterpret_cast<const uint2*>(s_tab + (u * 64 + row) * 8);
+      const int8_t* t8 = reinterpret_cast<const int8_t*>(&tw);
 #pragma unroll
-    for (int q = 0; q < 5; ++q) {
-      memb[q] = false;
-      mbias[q] = 0.f;
-      const int blk = blo + q;
-      if (blk <= bhi && row_ok) {
-        for (int s = 0; s < S; ++s) {
-          if (s_ids[row * S + s] == blk) {
-            memb[q] = true;
-            if (a.bias) mbias[q] = s_bias[row * S + s];
-            break;
-          }
+      for (int q = 0; q < 5; ++q) {
+        memb[q] = t8[q] >= 0;
+        mbias[q] = (a.bias && memb[q]) ? s_bias[row * S + t8[q]] : 0.f;
+      }
+    } else {
+      const int nq = min(j0 + kChunk - 1, a.Sk - 1) / BS - blo + 1;
+#pragma unroll
+      for (int q = 0; q < 5; ++q) {
+        memb[q] = false;
+        mbias[q] = 0.f;
+        if (q < nq && row_ok) {
+          for (int s = 0; s < S; ++s)
+            if (s_ids[row * S + s] == blo + q) {
+              memb[q] = true;
+              if (a.bias) mbias[q] = s_bias[row * S + s];
+              break;
+            }
         }
       }
     }
 
-    float lg[32];
+    // masked logits (log2 domain) in place, row max over the chunk
     float mloc = -INFINITY;
 #pragma unroll
-    for (int r = 0; r < 16; ++r) {
+    for (int half = 0; half < 2; ++half)
 #pragma unroll
-      for (int half = 0; half < 2; ++half) {
-        const int key = 32 * half + d_row(r, h);
-        const int j = j0 + key;
-        const float s = half ? st1[r] : st0[r];
-        const bool win = j >= my_ls && j <= my_qi;
-        const int q = j / BS - blo;
-        bool rem = !win && j >= my_seg && j < my_ls && j <= my_qi;
-        float bb = 0.f;
+      for (int r = 0; r < 16; ++r) {
+        const int offk = 32 * half + d_row(r, h);
+        const int j = j0 + offk;
+        const bool win = (uint32_t)(j - my_ls) < wlen;
+        bool rem = (uint32_t)(j - my_seg) < rlen;
+        float bb;
+        if (one_blk) {
+          rem = rem && memb[0];
+          bb = mbias[0];
+        } else {
+          const int qb = sub_blk ? (offk >> bs_shift) : (j / BS - blo);
+          bb = 0.f;
+          bool mm = false;
 #pragma unroll
-        for (int qq = 0; qq < 5; ++qq)
-          if (q == qq) { rem = rem && memb[qq]; bb = mbias[qq]; }
-        const float x = win ? s * kLog2e : (rem ? (s + bb) * kLog2e : -INFINITY);
-        lg[half * 16 + r] = x;
+          for (int qq = 0; qq < 5; ++qq)
+            if (qb == qq) { mm = memb[qq]; bb = mbias[qq]; }
+          rem = rem && mm;
+        }
+        const float x = win ? st[half][r] * kLog2e : (rem ? (st[half][r] + bb) * kLog2e : -INFINITY);
+        st[half][r] = x;
         mloc = fmaxf(mloc, x);
       }
-    }
     mloc = fmaxf(mloc, __shfl_xor(mloc, 32, kWave));
     const float m_new = fmaxf(m_run, mloc);
     const float alpha = m_new == -INFINITY ? 1.f : exp2f(m_run - m_new);
+    const float m_use = m_new == -INFINITY ? 0.f : m_new;
     float psum = 0.f;
 #pragma unroll
-    for (int i = 0; i < 32; ++i) {
-      const float pv = m_new == -INFINITY ? 0.f : exp2f(lg[i] - m_new);
-      lg[i] = pv;
-      psum += pv;
-    }
+    for (int half = 0; half < 2; ++half)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        const float pv = exp2f(st[half][r] - m_use);
+        st[half][r] = pv;
+        psum += pv;
+      }
     l_run = l_run * alpha + psum;
     m_run = m_new;
+    if (alpha != 1.f) {
 #pragma unroll
-    for (int mt = 0; mt < MT; ++mt)
+      for (int mt = 0; mt < MT; ++mt)
 #pragma unroll
-      for (int r = 0; r < 16; ++r) o[mt][r] *= alpha;
+        for (int r = 0; r < 16; ++r) o[mt][r] *= alpha;
+    }
 
     // P^T as B operands (4 steps of 16 keys), rounded to the input dtype
     uint4 pb[4];
 #pragma unroll
     for (int ks = 0; ks < 4; ++ks) {
-      const float* src = lg + (ks >> 1) * 16 + 8 * (ks & 1);
-      pb[ks] = make_uint4(M::pack2(src[0], src[1]), M::pack2(src[2], src[3]),
-                          M::pack2(src[4], src[5]), M::pack2(src[6], src[7]));
+      const int hf = ks >> 1, r0 = 8 * (ks & 1);
+      pb[ks] = make_uint4(M::pack2(st[hf][r0], st[hf][r0 + 1]), M::pack2(st[hf][r0 + 2], st[hf][r0 + 3]),
+                          M::pack2(st[hf][r0 + 4], st[hf][r0 + 5]), M::pack2(st[hf][r0 + 6], st[hf][r0 + 7]));
     }
-    // O^T += V^T P^T
+    // O^T += V^T P^T  (V^T operands read column-wise from the natural V tile)
+    const uint16_t* v16 = reinterpret_cast<const uint16_t*>(sV);
 #pragma unroll
-    for (int mt = 0; mt < MT; ++mt) {
-      const T* vrow = sVt + (32 * mt + rl) * VP;
+    for (int mt = 0; mt < MT; ++mt)
 #pragma unroll
-      for (int ks = 0; ks < 4; ++ks) {
-        const uint2 lo = *reinterpret_cast<const uint2*>(vrow + 16 * ks + 4 * h);
-        const uint2 hi = *reinterpret_cast<const uint2*>(vrow + 16 * ks + 8 + 4 * h);
-        o[mt] = M::mac(make_uint4(lo.x, lo.y, hi.x, hi.y), pb[ks], o[mt]);
-      }
-    }
+      for (int ks = 0; ks < 4; ++ks)
+        o[mt] = M::mac(a_operand_t<KP>(v16, 32 * mt + rl, ks, h), pb[ks], o[mt]);
   }
 
   const float l_tot = l_run + __shfl_xor(l_run, 32, kWave);
@@ -304,12 +339,8 @@ int check_fwd(const srswa_fwd_args* a) {
 
 template <typename T, int D>
 int launch_fwd(const FwdK& k, size_t smem, hipStream_t st) {
-  static bool attr = false;
-  if (!attr) {
-    hipFuncSetAttribute(reinterpret_cast<const void*>(&fwd_kernel<T, D>),
-                        hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024);
-    attr = true;
-  }
+  static size_t granted = 0;
+  if (!ensure_dynamic_lds(&fwd_kernel<T, D>, smem, &granted)) return SRSWA_UNSUPPORTED;
   const int64_t grid = (int64_t)k.a.B * k.a.HQ * k.ntiles;
   hipLaunchKernelGGL((fwd_kernel<T, D>), dim3((unsigned)grid), dim3(128), smem, st, k);
   const hipError_t e = hipGetLastError();
@@ -339,7 +370,7 @@ extern "C" int srswa_gather_fwd(const srswa_fwd_args* a, void* stream) {
   k.G = a->HQ / a->HKV;
   k.IG = a->HQ / a->HI;
   const size_t smem = FwdSmem::bytes(a->D, a->S, a->bias != nullptr, k.nwords, k.umax, 2);
-  if (smem > 160 * 1024) {
+  if (smem > 156 * 1024) {
     set_error("fwd: %zu bytes of LDS needed (key length too large)", smem);
     return SRSWA_UNSUPPORTED;
   }

@@ -130,3 +130,80 @@ def indexer_bytes(B, H, D, L, block_size, local_window, elem=2):
     nblk = L // block_size
     elig = nblk - local_window // block_size
     return B * elig * block_size * H * D * elem + B * H * D * 4 + B * H * 8 * 4
+
+
+# ---------------------------------------------------------------- configs 4 / 5
+def tile_block_indices(B, T, Sk, block_size, local_window, k, tile=64, cfg=4, HI=1,
+                       mode="prefix"):
+    """[B, HI, T, k] int32 per-token indices broadcast from one selection per
+    64-query tile.  ``mode="prefix"`` (config 4): k sorted unique blocks drawn
+    from {b : BS*(b+1) <= t0_key - LW + 1} (fully before the tile's first
+    window).  ``mode="selfattn"`` (config 5): tile m takes min(k, m - 8) blocks
+    from {b <= m - 9}."""
+    g = _gen(cfg)
+    ntile = -(-T // tile)
+    out = torch.full((B, HI, T, k), -1, dtype=torch.int32)
+    off = Sk - T
+    for b in range(B):
+        for hi in range(HI):
+            for m in range(ntile):
+                t0 = m * tile
+                if mode == "prefix":
+                    n = max(0, (off + t0 - local_window + 1) // block_size)
+                    kk = min(k, n)
+                else:
+                    n = max(0, m - 8)             # blocks 0 .. m-9
+                    kk = min(k, n)
+                if kk <= 0:
+                    continue
+                sel = torch.randperm(n, generator=g)[:kk].sort().values.to(torch.int32)
+                out[b, hi, t0:t0 + tile, :kk] = sel
+    return out
+
+
+def prefill_config(B=4, T=2048, Sk=65536, H=10, D=128, block_size=64, local_window=512, k=8,
+                   dtype=torch.bfloat16, device=None, cfg=4):
+    """Config 4: chunked prefill, T query rows at the tail of an Sk-key cache."""
+    idx = tile_block_indices(B, T, Sk, block_size, local_window, k, cfg=cfg, mode="prefix")
+    gd = torch.Generator(device=device) if device is not None else torch.Generator()
+    gd.manual_seed(SEED0 + cfg)
+    kw = dict(generator=gd, dtype=dtype, device=device) if device is not None else dict(generator=gd)
+    q = torch.randn(B, T, H, D, **kw)
+    kc = torch.randn(B, Sk, H, D, **kw)
+    vc = torch.randn(B, Sk, H, D, **kw)
+    if device is None:
+        q, kc, vc = q.to(dtype), kc.to(dtype), vc.to(dtype)
+    return dict(q=q, k=kc, v=vc, block_idx=idx, block_size=block_size, local_window=local_window,
+                scale=1.0 / math.sqrt(D))
+
+
+def fwdbwd_config(B=2, T=16384, H=10, D=128, block_size=64, local_window=512, k=8,
+                  dtype=torch.bfloat16, device=None, cfg=5):
+    """Config 5: self-attention forward + backward, selection per 64-query tile."""
+    idx = tile_block_indices(B, T, T, block_size, local_window, k, cfg=cfg, mode="selfattn")
+    gd = torch.Generator(device=device) if device is not None else torch.Generator()
+    gd.manual_seed(SEED0 + cfg)
+    kw = dict(generator=gd, dtype=dtype, device=device) if device is not None else dict(generator=gd)
+    q, kc, vc, do = (torch.randn(B, T, H, D, **kw) for _ in range(4))
+    if device is None:
+        q, kc, vc, do = (x.to(dtype) for x in (q, kc, vc, do))
+    return dict(q=q, k=kc, v=vc, do=do, block_idx=idx, block_size=block_size,
+                local_window=local_window, scale=1.0 / math.sqrt(D))
+
+
+def attended_pairs(block_idx, Sk, block_size, local_window):
+    """(window pairs, remote pairs) summed over rows of one head, for a tile-shared
+    selection [B, HI, T, k]: the FLOP basis of configs 4 / 5."""
+    B, HI, T, K = block_idx.shape
+    off = Sk - T
+    qi = torch.arange(T, dtype=torch.int64) + off
+    win = torch.clamp(qi, max=local_window - 1) + 1                  # window length per row
+    ls = qi - local_window + 1
+    rem = torch.zeros(B, HI, T, dtype=torch.int64)
+    for s in range(K):
+        ids = block_idx[..., s].long()
+        lo = ids * block_size
+        hi = torch.minimum(lo + block_size, ls[None, None, :].clamp(min=0))
+        hi = torch.minimum(hi, qi[None, None, :] + 1)
+        rem += torch.where(ids >= 0, (hi - lo).clamp(min=0), torch.zeros_like(lo))
+    return int(win.sum()) * B, int(rem[:, 0].sum())
