@@ -305,12 +305,29 @@ def bench_fwdbwd(args):
                          "kernel": "fwd_kernel + delta/touch/dq/dkv kernels"}}
 
 
+def bench_copycal(args):
+    """Calibration for the HBM traffic counters: a plain device copy of a known
+    size (4 GiB read + 4 GiB written per launch, far beyond the 256 MB
+    Infinity Cache), so rocprofv3's FETCH_SIZE / WRITE_SIZE readings per
+    dispatch can be scaled to bytes."""
+    import torch
+    dev = torch.device("cuda:0")
+    n = 4 * 1024 * 1024 * 1024
+    src = torch.empty(n, dtype=torch.uint8, device=dev).fill_(1)
+    dst = torch.empty_like(src)
+    ms = _time_launches(lambda: dst.copy_(src), args.steps, args.warmup, dev)
+    return {"metric": "copy calibration", "value": 2 * n / (ms * 1e-3) / 1e9, "unit": "GB/s",
+            "bytes_read_per_launch": n, "bytes_written_per_launch": n, "ms_per_step": ms,
+            "steps": args.steps, "warmup": args.warmup, "n_gpus": 1, "higher_is_better": True}
+
+
 def main():
     ap = argparse.ArgumentParser(description=__doc__)
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=200)
     ap.add_argument("--warmup", type=int, default=20)
-    ap.add_argument("--config", default="decode", choices=["decode", "indexer", "prefill", "fwdbwd"])
+    ap.add_argument("--config", default="decode",
+                    choices=["decode", "indexer", "prefill", "fwdbwd", "copycal"])
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--no-check", action="store_true", help="skip the oracle spot check")
     ap.add_argument("--cpu-budget", type=float, default=12.0)
@@ -320,7 +337,7 @@ def main():
               "(no multi-GPU path); use --gpus 1", file=sys.stderr)
         sys.exit(2)
     fn = {"decode": bench_decode, "indexer": bench_indexer, "prefill": bench_prefill,
-          "fwdbwd": bench_fwdbwd}[args.config]
+          "fwdbwd": bench_fwdbwd, "copycal": bench_copycal}[args.config]
     res = fn(args)
     print(json.dumps(res), flush=True)
 

@@ -222,9 +222,12 @@ __global__ __launch_bounds__(kDecodeWaves * kWave) void decode_kernel(DecodeK p)
     my_ok = my_ok && !dup;
   }
 
-  const int u_begin = (split * kDecodeWaves + wave) * p.upw;
-  const int u_end = min(u_begin + p.upw, p.n_units);
-  for (int u = u_begin; u < u_end; ++u) {
+  // the workgroup's units, dealt round-robin to its waves so that every wave
+  // mixes remote (scattered) and window (contiguous) units
+  const int u_base = split * kDecodeWaves * p.upw;
+  for (int i = 0; i < p.upw; ++i) {
+    const int u = u_base + wave + i * kDecodeWaves;
+    if (u >= p.n_units) break;
     int k0, k1;
     float bias_l2 = 0.f;
     if (u < p.n_remote_units) {
