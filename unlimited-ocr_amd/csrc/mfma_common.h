@@ -46,6 +46,18 @@ template <> struct Mfma<__half> {
   __device__ __forceinline__ static float hi(uint32_t w) { return h16_hi(w); }
 };
 
+// Raw buffer loads (gfx9 buffer resource, byte offsets): one 32-bit lane
+// offset plus a scalar offset per load instead of a 64-bit address per load,
+// and a hardware range check -- bytes at or beyond `bytes` read as zero.
+typedef unsigned int u32x4_t __attribute__((ext_vector_type(4)));
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void* base, uint32_t bytes) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, (int)bytes, 0x00020000);
+}
+__device__ __forceinline__ uint4 buffer_load16(__amdgpu_buffer_rsrc_t r, uint32_t voff, uint32_t soff) {
+  const u32x4_t v = __builtin_amdgcn_raw_buffer_load_b128(r, voff, soff, 0);
+  return make_uint4(v[0], v[1], v[2], v[3]);
+}
+
 __device__ __forceinline__ f32x16_t zero16() {
   f32x16_t z;
 #pragma unroll
@@ -135,6 +147,118 @@ __device__ __forceinline__ uint4 a_operand_t(const uint16_t* x, int d, int ks, i
     w[2 * i + 1] = (uint32_t)q[2 * PITCH] | ((uint32_t)q[3 * PITCH] << 16);
   }
   return make_uint4(w[0], w[1], w[2], w[3]);
+}
+
+typedef short s16x4_t __attribute__((ext_vector_type(4)));
+typedef __attribute__((address_space(3))) s16x4_t lds_s16x4_t;
+
+// The same A operand (X^T, M = feature d, K = 16 rows of X in the permuted
+// order) from two transposing LDS reads, ds_read_b64_tr_b16.  That instruction
+// works on groups of 16 lanes: output lane L, element e is element L % 4 of
+// the 8 bytes addressed by source lane 4e + L / 4 of its group.  Source lane
+// s of group g (h = l / 32) therefore points at row r0 + 4h + s / 4, column
+// c0 + 16(g % 2) + 4(s % 4), and lane (d = l % 32, h) receives
+// X[r0 + 4h + e][c0 + d] (first read) and X[r0 + 8 + 4h + e][c0 + d]
+// (second read, eight rows further), e = 0..3.
+template <int PITCH>
+__device__ __forceinline__ uint4 a_operand_tr(const uint16_t* x, int r0, int c0, int lane) {
+  const int s = lane & 15, g = (lane >> 4) & 1, h = lane >> 5;
+  const uint16_t* p = x + (r0 + 4 * h + (s >> 2)) * PITCH + c0 + 16 * g + 4 * (s & 3);
+  const s16x4_t lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4_t*)p);
+  const s16x4_t hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4_t*)(p + 8 * PITCH));
+  const uint2 a = __builtin_bit_cast(uint2, lo), b = __builtin_bit_cast(uint2, hi);
+  return make_uint4(a.x, a.y, b.x, b.y);
+}
+
+// bits [lo, hi) of a 64-bit word, 0 <= lo, hi <= 64
+__device__ __forceinline__ uint64_t range64(int lo, int hi) {
+  if (hi <= lo) return 0ull;
+  const uint64_t top = hi >= 64 ? ~0ull : ((1ull << hi) - 1ull);
+  return top & ~((1ull << lo) - 1ull);
+}
+
+constexpr int kIdEnd = 0x7fffffff;   // sentinel closing a row's sorted id list
+
+// One row's selected blocks, as the kernels walk them: the valid ids that hold
+// at least one remote key of the row (seg <= j < ls, j <= qi), ascending, a
+// repeated id kept once with its first slot's bias, then kIdEnd padding up to
+// SP = S + 1 entries (so a cursor never runs past the list).
+__device__ inline void sort_row_ids(const int32_t* ids, const float* bias, int S, int SP, int BS,
+                                    int maxblk, int qi, int seg, int ls, int* sid, float* sb) {
+  int n = 0;
+  for (int s = 0; s < S; ++s) {
+    const int id = ids[s];
+    if (id < 0 || id > maxblk) continue;
+    const int lo = max(id * BS, seg), hi = min(min(id * BS + BS, ls), qi + 1);
+    if (lo >= hi) continue;
+    bool dup = false;
+    for (int k = 0; k < n; ++k) dup |= sid[k] == id;
+    if (dup) continue;
+    const float bv = bias ? bias[s] : 0.f;
+    int i = n;
+    while (i > 0 && sid[i - 1] > id) {
+      sid[i] = sid[i - 1];
+      if (sb) sb[i] = sb[i - 1];
+      --i;
+    }
+    sid[i] = id;
+    if (sb) sb[i] = bv;
+    ++n;
+  }
+  for (int i = n; i < SP; ++i) sid[i] = kIdEnd;
+}
+
+// Sorted list of the 64-key chunks a tile visits, from the rows' windows
+// [ls, qi] and the remote keys of their sorted ids (sid, SP entries per row):
+// a bitmap over chunks (s_bits, nwords words, zeroed here) compacted by a
+// prefix popcount into s_chunks.  Every thread of the workgroup calls it;
+// returns the chunk count.
+__device__ inline int plan_chunks(const int* s_qi, const int* s_seg, const int* s_ls, const int* sid,
+                                  int SP, int BS, int LW, int nrows, int nwords, uint32_t* s_bits,
+                                  uint16_t* s_chunks, int* s_count) {
+  const int tid = threadIdx.x, nthr = blockDim.x;
+  for (int w = tid; w < nwords; w += nthr) s_bits[w] = 0u;
+  __syncthreads();
+  const int wspan = (LW + kChunk - 1) / kChunk + 1;
+  for (int e = tid; e < nrows * wspan; e += nthr) {
+    const int r = e / wspan, k = e % wspan;
+    const int c = max(s_ls[r], 0) / kChunk + k;
+    if (c <= s_qi[r] / kChunk) atomicOr(&s_bits[c >> 5], 1u << (c & 31));
+  }
+  for (int e = tid; e < nrows * SP; e += nthr) {
+    const int r = e / SP;
+    const int id = sid[e];
+    if (id == kIdEnd) continue;
+    const int lo = max(id * BS, s_seg[r]);
+    const int hi = min(min(id * BS + BS, s_ls[r]), s_qi[r] + 1);
+    for (int c = lo / kChunk; c <= (hi - 1) / kChunk; ++c) atomicOr(&s_bits[c >> 5], 1u << (c & 31));
+  }
+  __syncthreads();
+  if (tid < kWave) {
+    int base = 0;
+    for (int w0 = 0; w0 < nwords; w0 += kWave) {
+      const int w = w0 + tid;
+      const uint32_t bits = w < nwords ? s_bits[w] : 0u;
+      const int cnt = __popc(bits);
+      int incl = cnt;
+#pragma unroll
+      for (int o = 1; o < kWave; o <<= 1) {
+        const int v = __shfl_up(incl, o, kWave);
+        if (tid >= o) incl += v;
+      }
+      int pos = base + incl - cnt;
+      uint32_t bb = bits;
+      while (bb) {
+        const int bit = __ffs(bb) - 1;
+        bb &= bb - 1;
+        s_chunks[pos++] = (uint16_t)(w * 32 + bit);
+      }
+      base += __shfl(incl, kWave - 1, kWave);
+    }
+    if (tid == 0) *s_count = base;
+  }
+  __syncthreads();
+  return *s_count;
 }
 
 // First slot (or -1) of each row's selected blocks overlapping each planned

@@ -12,19 +12,33 @@
 //   window keys ls <= j <= qi                       logit = scale*q.k
 //   remote keys j in a selected block, seg <= j < ls  logit = scale*q.k + bias
 // one softmax over both (disjoint) sets, O in the input dtype, LSE in fp32.
-// Duplicate block ids count once (the first slot's bias is used).
+// Duplicate block ids count once (the first slot's bias is used).  The block
+// size is a power of two >= 16, as the reference's tl.arange(0, BS) requires
+// (HF/sparse_gather_triton.py:86), so every aligned 16-key quarter of a
+// 64-key chunk lies inside one block.
 //
 // One workgroup = (sequence, query head, 64-row query tile), two waves of 32
-// rows.  Set-up builds in LDS the sorted list of 64-key chunks the tile must
-// visit (window ranges and selected blocks of all 64 rows, as a bitmap then a
-// prefix-popcount compaction), so a tile whose rows share their selection (the
-// indexer selects per 64-query tile) visits |selected| + |window| chunks once
-// instead of once per row.  Per chunk: K and V (row pitch D+8) are staged in
-// LDS, S^T = K Q^T and O^T += V^T P^T (V^T operands read column-wise from the
-// natural V tile, bank-conflict free) run on
-// v_mfma_f32_32x32x16_{bf16,f16}; q is pre-multiplied by the scale and rounded
-// to the input dtype and P is rounded to it before the PV product, the same
-// rounding points as the reference kernels (HF/sparse_gather_triton.py:68,94).
+// rows; at most ~40 KB of LDS and 256 registers per lane, so four workgroups
+// (two waves per SIMD) share a CU and hide each other's latencies.
+// Set-up: every row's block ids are sorted and deduplicated into LDS, and the
+// sorted list of 64-key chunks the tile visits is built (window ranges and
+// selected blocks of all 64 rows: bitmap + prefix popcount), so a tile whose
+// rows share their selection visits |selected| + |window| chunks once.
+// Per chunk:
+//   * K (row pitch D+8) and V (row pitch D+16) are staged in LDS from
+//     registers fetched one chunk ahead;
+//   * S^T = K Q^T on v_mfma_f32_32x32x16_{bf16,f16}: every lane owns one
+//     query row and 32 of the chunk's keys;
+//   * each lane derives its row's 64-bit keep mask for the chunk (window range
+//     | remote range & selected quarters); a chunk that every row of the wave
+//     keeps whole (the common case) skips all per-key masking;
+//   * softmax in the log2 domain with lazy rescaling: the running max moves
+//     only when a chunk exceeds it by more than 2^8, so the O accumulators are
+//     rescaled only on those rare chunks;
+//   * O^T += V^T P^T, the V^T operand read from the natural V tile by
+//     ds_read_b64_tr_b16 (two transposing reads per operand).
+// q*scale and P are rounded to the input dtype before their products, the
+// same rounding points as the reference kernels (HF/sparse_gather_triton.py:68,94).
 #include <algorithm>
 
 #include "mfma_common.h"
@@ -34,55 +48,63 @@ namespace {
 
 struct FwdK {
   srswa_fwd_args a;
-  int ntiles, nchunk, nwords, umax;
-  int G, IG;
+  int ntiles, nwords, SP, G, IG, bs_shift;
+  int nlogical, per_xcd;       // XCD-aware workgroup order
+  int chunks_off, sid_off;     // LDS byte offsets of the chunk list and sorted ids
 };
 
-constexpr int kSlotCap = 32;   // planned chunks per tile covered by the slot table
-
-struct FwdSmem {
-  static size_t bytes(int D, int S, bool bias, int nwords, int umax, int esz) {
-    size_t n = (size_t)kChunk * (D + 8) * esz * 2;                 // K, V (natural)
-    n += (size_t)kSlotCap * 64 * 8;                                // slot table
-    n += 3 * 64 * 4 + (size_t)64 * S * 4 * (bias ? 2 : 1) + (size_t)nwords * 4 + (size_t)umax * 4 + 16;
-    return (n + 15) / 16 * 16;
-  }
+template <int D> struct FwdLds {
+  static constexpr int KP = D + 8;    // K row pitch (elements): conflict-free 16-byte row reads
+  static constexpr int VP = D + 16;   // V row pitch: conflict-free transposing reads
+  static constexpr int kOff = 0;
+  static constexpr int vOff = kChunk * KP * 2;
+  static constexpr int tileBytes = vOff + kChunk * VP * 2;
 };
 
 template <typename T, int D>
-__global__ __launch_bounds__(128) void fwd_kernel(FwdK p) {
+__global__ __launch_bounds__(128, 2) void fwd_kernel(FwdK p) {
   using M = Mfma<T>;
-  constexpr int KP = D + 8;          // K / V row pitch (elements)
+  using L = FwdLds<D>;
+  constexpr int KP = L::KP, VP = L::VP;
   constexpr int KS = D / 16;         // k-steps over the head dim
   constexpr int MT = D / 32;         // 32-row tiles of O^T
+  constexpr int NT = 128;
+  constexpr int PPT = kChunk * D / 8 / NT;   // 16-byte pieces of K (and of V) per thread
   extern __shared__ __align__(16) unsigned char smem[];
   const srswa_fwd_args& a = p.a;
-  T* sK = reinterpret_cast<T*>(smem);
-  T* sV = sK + kChunk * KP;
-  int8_t* s_tab = reinterpret_cast<int8_t*>(sV + kChunk * KP);
-  int* s_qi = reinterpret_cast<int*>(s_tab + kSlotCap * 64 * 8);
+
+  // The hardware deals workgroups to the 8 XCDs round-robin; logical tile
+  // xcd * per_xcd + k keeps neighbouring tiles of one (sequence, head), which
+  // share most of their window keys, on the same L2.
+  const int lid = (int)(blockIdx.x & 7) * p.per_xcd + (int)(blockIdx.x >> 3);
+  if (lid >= p.nlogical) return;
+
+  T* sK = reinterpret_cast<T*>(smem + L::kOff);
+  T* sV = reinterpret_cast<T*>(smem + L::vOff);
+  // set-up arrays alias the K/V tiles (dead once the chunk loop starts)
+  int* s_qi = reinterpret_cast<int*>(smem);
   int* s_seg = s_qi + 64;
   int* s_ls = s_seg + 64;
-  int* s_ids = s_ls + 64;
-  float* s_bias = reinterpret_cast<float*>(s_ids + 64 * a.S);
-  uint32_t* s_bits = reinterpret_cast<uint32_t*>(s_bias + (a.bias ? 64 * a.S : 0));
-  int* s_chunks = reinterpret_cast<int*>(s_bits + p.nwords);
-  int* s_count = s_chunks + p.umax;
+  int* s_count = s_ls + 64;
+  uint32_t* s_bits = reinterpret_cast<uint32_t*>(s_count + 4);
+  uint16_t* s_chunks = reinterpret_cast<uint16_t*>(smem + p.chunks_off);
+  int* s_sid = reinterpret_cast<int*>(smem + p.sid_off);
+  float* s_sb = a.bias ? reinterpret_cast<float*>(s_sid + 64 * p.SP) : nullptr;
 
-  constexpr int NT = 128;
   const int tid = threadIdx.x, wave = tid / kWave, lane = tid % kWave;
-  const int h = lane / 32, rl = lane % 32;
-  const int tile = blockIdx.x % p.ntiles;
-  const int64_t bh = blockIdx.x / p.ntiles;
-  const int hq = (int)(bh % a.HQ);
-  const int b = (int)(bh / a.HQ);
+  const int h = lane >> 5, rl = lane & 31;
+  const int tile = lid % p.ntiles;
+  const int bh = lid / p.ntiles;
+  const int hq = bh % a.HQ, b = bh / a.HQ;
   const int kvh = hq / p.G, ih = hq / p.IG;
   const int t0 = tile * kTileRows;
   const int nrows = min(kTileRows, a.T - t0);
   const int off = a.Sk - a.T;
-  const int BS = a.block_size, LW = a.local_window, S = a.S;
+  const int BS = a.block_size, LW = a.local_window, SP = p.SP;
+  const int maxblk = (a.Sk - 1) >> p.bs_shift;
 
-  for (int r = tid; r < 64; r += NT) {
+  if (tid < 64) {
+    const int r = tid;
     int qi = -1, seg = 0, ls = 0;
     if (r < nrows) {
       qi = off + t0 + r;
@@ -92,30 +114,25 @@ __global__ __launch_bounds__(128) void fwd_kernel(FwdK p) {
     s_qi[r] = qi;
     s_seg[r] = seg;
     s_ls[r] = ls;
+    const int rr = min(r, nrows - 1);
+    const int32_t* ids = a.idx + (int64_t)b * a.idx_sb + (int64_t)ih * a.idx_sh + (int64_t)(t0 + rr) * a.idx_st;
+    const float* bias =
+        a.bias ? a.bias + (int64_t)b * a.bias_sb + (int64_t)ih * a.bias_sh + (int64_t)(t0 + rr) * a.bias_st : nullptr;
+    sort_row_ids(ids, bias, r < nrows ? a.S : 0, SP, BS, maxblk, qi, seg, ls, s_sid + r * SP,
+                 s_sb ? s_sb + r * SP : nullptr);
   }
-  for (int e = tid; e < 64 * S; e += NT) {
-    const int r = e / S, s = e % S;
-    int id = -1;
-    float bv = 0.f;
-    if (r < nrows) {
-      id = a.idx[(int64_t)b * a.idx_sb + (int64_t)ih * a.idx_sh + (int64_t)(t0 + r) * a.idx_st + s];
-      if (a.bias) bv = a.bias[(int64_t)b * a.bias_sb + (int64_t)ih * a.bias_sh + (int64_t)(t0 + r) * a.bias_st + s];
-    }
-    s_ids[e] = id;
-    if (a.bias) s_bias[e] = bv;
-  }
-  for (int w = tid; w < p.nwords; w += NT) s_bits[w] = 0u;
   __syncthreads();
-  const int U = build_chunk_plan(s_qi, s_seg, s_ls, s_ids, S, BS, nrows, p.nchunk, p.nwords,
-                                 s_bits, s_chunks, s_count, LW, a.Sk);
-  build_slot_table(s_qi, s_seg, s_ls, s_ids, s_chunks, U, kSlotCap, S, BS, a.Sk, nrows, s_tab);
+  const int U = plan_chunks(s_qi, s_seg, s_ls, s_sid, SP, BS, LW, nrows, p.nwords, s_bits, s_chunks, s_count);
 
-  // this lane's row: window [ls, qi] and remote range [seg, min(ls, qi+1))
+  // this lane's row: window [ls, qi], remote candidates [seg, min(ls, qi + 1))
   const int row = wave * 32 + rl;
   const bool row_ok = row < nrows;
-  const int my_qi = s_qi[row], my_seg = s_seg[row], my_ls = s_ls[row];
-  const uint32_t wlen = (uint32_t)max(my_qi - my_ls + 1, 0);
-  const uint32_t rlen = (uint32_t)max(min(my_ls, my_qi + 1) - my_seg, 0);
+  const int my_ls = s_ls[row], my_seg = s_seg[row];
+  const int my_hi = s_qi[row] + 1;
+  const int rem_hi = min(my_ls, my_hi);
+  const int* my_sid = s_sid + row * SP;
+  const float* my_sb = s_sb ? s_sb + row * SP : nullptr;
+
   uint4 qf[KS];
   {
     const T* qrow = reinterpret_cast<const T*>(a.q) + (int64_t)b * a.q_sb +
@@ -133,42 +150,77 @@ __global__ __launch_bounds__(128) void fwd_kernel(FwdK p) {
   f32x16_t o[MT];
 #pragma unroll
   for (int mt = 0; mt < MT; ++mt) o[mt] = zero16();
-  float m_run = -INFINITY, l_run = 0.f;
+  float m_b = -INFINITY, l_run = 0.f;     // running max (log2 units) and row sum
+  int cur = 0, nid = my_sid[0];           // cursor into the row's sorted ids
 
-  const T* kg = reinterpret_cast<const T*>(a.k) + (int64_t)b * a.k_sb + (int64_t)kvh * a.k_sh;
-  const T* vg = reinterpret_cast<const T*>(a.v) + (int64_t)b * a.v_sb + (int64_t)kvh * a.v_sh;
-  // chunk staging: every thread owns PPT 16-byte pieces of K and of V; the next
-  // chunk's pieces are fetched into registers while the current one computes
-  constexpr int PPT = kChunk * D / 8 / NT;
+  // K / V of this (sequence, kv head) as buffer resources ending at key Sk - 1
+  // (keys of a chunk beyond Sk read as zero)
+  const __amdgpu_buffer_rsrc_t krs = make_rsrc(
+      reinterpret_cast<const T*>(a.k) + (int64_t)b * a.k_sb + (int64_t)kvh * a.k_sh,
+      (uint32_t)(((int64_t)(a.Sk - 1) * a.k_st + D) * 2));
+  const __amdgpu_buffer_rsrc_t vrs = make_rsrc(
+      reinterpret_cast<const T*>(a.v) + (int64_t)b * a.v_sb + (int64_t)kvh * a.v_sh,
+      (uint32_t)(((int64_t)(a.Sk - 1) * a.v_st + D) * 2));
+  constexpr int RPP = NT / (D / 8);            // rows per pass of the 128 threads
+  const uint32_t kvo = (uint32_t)((tid / (D / 8)) * a.k_st + (tid % (D / 8)) * 8) * 2;
+  const uint32_t vvo = (uint32_t)((tid / (D / 8)) * a.v_st + (tid % (D / 8)) * 8) * 2;
+  // this thread's 16-byte piece of the first staged row; later pieces are RPP rows apart
+  T* sKw = sK + (tid / (D / 8)) * KP + (tid % (D / 8)) * 8;
+  T* sVw = sV + (tid / (D / 8)) * VP + (tid % (D / 8)) * 8;
   uint4 kpre[PPT], vpre[PPT];
   auto fetch = [&](int c) {
+    const uint32_t kso = (uint32_t)c * kChunk * (uint32_t)a.k_st * 2u;
+    const uint32_t vso = (uint32_t)c * kChunk * (uint32_t)a.v_st * 2u;
 #pragma unroll
     for (int i = 0; i < PPT; ++i) {
-      const int pc = tid + i * NT;
-      const int j = c * kChunk + pc / (D / 8), col = pc % (D / 8);
-      const bool in = j < a.Sk;
-      kpre[i] = in ? *reinterpret_cast<const uint4*>(kg + (int64_t)j * a.k_st + col * 8) : make_uint4(0, 0, 0, 0);
-      vpre[i] = in ? *reinterpret_cast<const uint4*>(vg + (int64_t)j * a.v_st + col * 8) : make_uint4(0, 0, 0, 0);
+      kpre[i] = buffer_load16(krs, kvo, kso + (uint32_t)(i * RPP) * (uint32_t)a.k_st * 2u);
+      vpre[i] = buffer_load16(vrs, vvo, vso + (uint32_t)(i * RPP) * (uint32_t)a.v_st * 2u);
     }
   };
-  const bool one_blk = (BS % kChunk) == 0;      // every chunk lies inside one block
-  const bool sub_blk = (kChunk % BS) == 0;      // every chunk holds 64/BS whole blocks
-  const int bs_shift = __ffs(BS) - 1;
+  const uint16_t* v16 = reinterpret_cast<const uint16_t*>(sV);
 
   if (U > 0) fetch(s_chunks[0]);
   for (int u = 0; u < U; ++u) {
-    const int c = s_chunks[u];
-    const int j0 = c * kChunk;
+    const int j0 = (int)s_chunks[u] * kChunk;
     __syncthreads();   // previous chunk fully consumed
 #pragma unroll
     for (int i = 0; i < PPT; ++i) {
-      const int pc = tid + i * NT;
-      const int key = pc / (D / 8), col = pc % (D / 8);
-      *reinterpret_cast<uint4*>(sK + key * KP + col * 8) = kpre[i];
-      *reinterpret_cast<uint4*>(sV + key * KP + col * 8) = vpre[i];
+      *reinterpret_cast<uint4*>(sKw + i * RPP * KP) = kpre[i];
+      *reinterpret_cast<uint4*>(sVw + i * RPP * VP) = vpre[i];
     }
     __syncthreads();
     if (u + 1 < U) fetch(s_chunks[u + 1]);
+
+    // the row's selected 16-key quarters of the chunk and their bias
+    uint32_t qmem = 0;
+    float bq[4] = {0.f, 0.f, 0.f, 0.f};
+    if (BS >= kChunk) {
+      const int blk = j0 >> p.bs_shift;
+      while (nid < blk) nid = my_sid[++cur];
+      if (nid == blk) {
+        qmem = 15u;
+        if (my_sb) bq[0] = bq[1] = bq[2] = bq[3] = my_sb[cur] * kLog2e;
+      }
+    } else {
+#pragma unroll
+      for (int qq = 0; qq < 4; ++qq) {
+        const int blk = (j0 + 16 * qq) >> p.bs_shift;
+        while (nid < blk) nid = my_sid[++cur];
+        if (nid == blk) {
+          qmem |= 1u << qq;
+          if (my_sb) bq[qq] = my_sb[cur] * kLog2e;
+        }
+      }
+    }
+    uint64_t qm = 0;
+#pragma unroll
+    for (int qq = 0; qq < 4; ++qq)
+      if (qmem & (1u << qq)) qm |= 0xffffull << (16 * qq);
+    const uint64_t wm = range64(min(max(my_ls - j0, 0), 64), min(max(my_hi - j0, 0), 64));
+    const uint64_t rm = range64(min(max(my_seg - j0, 0), 64), min(max(rem_hi - j0, 0), 64)) & qm;
+    const uint64_t keep = wm | rm;
+    const bool whole = !row_ok || (keep == ~0ull && (!my_sb || rm == 0ull || (rm == ~0ull && BS >= kChunk)));
+    const bool fast = __all(whole);
 
     // S^T (keys x rows) for the two 32-key halves of the chunk
     f32x16_t st[2] = {zero16(), zero16()};
@@ -180,83 +232,72 @@ __global__ __launch_bounds__(128) void fwd_kernel(FwdK p) {
       st[1] = M::mac(a1, qf[ks], st[1]);
     }
 
-    // this row's selected blocks among the (<= 5) the chunk overlaps
-    const int blo = j0 / BS;
-    bool memb[5];
-    float mbias[5];
-    if (u < kSlotCap) {
-      const uint2 tw = *reinterpret_cast<const uint2*>(s_tab + (u * 64 + row) * 8);
-      const int8_t* t8 = reinterpret_cast<const int8_t*>(&tw);
+    // row max of the chunk's logits (log2 units); lane (l, h) holds keys
+    // 32 half + 8 (r / 4) + 4h + r % 4
+    float mloc = -INFINITY, addb = 0.f;
+    if (fast) {
+      if (my_sb && rm != 0ull) addb = bq[0];
 #pragma unroll
-      for (int q = 0; q < 5; ++q) {
-        memb[q] = t8[q] >= 0;
-        mbias[q] = (a.bias && memb[q]) ? s_bias[row * S + t8[q]] : 0.f;
-      }
+      for (int half = 0; half < 2; ++half)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) mloc = fmaxf(mloc, st[half][r]);
+      mloc = fmaf(mloc, kLog2e, addb);
     } else {
-      const int nq = min(j0 + kChunk - 1, a.Sk - 1) / BS - blo + 1;
+      const uint64_t kh = keep >> (4 * h), rh = rm >> (4 * h);
 #pragma unroll
-      for (int q = 0; q < 5; ++q) {
-        memb[q] = false;
-        mbias[q] = 0.f;
-        if (q < nq && row_ok) {
-          for (int s = 0; s < S; ++s)
-            if (s_ids[row * S + s] == blo + q) {
-              memb[q] = true;
-              if (a.bias) mbias[q] = s_bias[row * S + s];
-              break;
-            }
+      for (int half = 0; half < 2; ++half) {
+        const uint32_t k32 = (uint32_t)(kh >> (32 * half)), r32 = (uint32_t)(rh >> (32 * half));
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+          const int bit = 8 * (r >> 2) + (r & 3);
+          float x = st[half][r] * kLog2e;
+          if (my_sb) x += ((r32 >> bit) & 1u) ? bq[2 * half + (r >> 3)] : 0.f;
+          x = ((k32 >> bit) & 1u) ? x : -INFINITY;
+          st[half][r] = x;
+          mloc = fmaxf(mloc, x);
         }
       }
     }
-
-    // masked logits (log2 domain) in place, row max over the chunk
-    float mloc = -INFINITY;
-#pragma unroll
-    for (int half = 0; half < 2; ++half)
-#pragma unroll
-      for (int r = 0; r < 16; ++r) {
-        const int offk = 32 * half + d_row(r, h);
-        const int j = j0 + offk;
-        const bool win = (uint32_t)(j - my_ls) < wlen;
-        bool rem = (uint32_t)(j - my_seg) < rlen;
-        float bb;
-        if (one_blk) {
-          rem = rem && memb[0];
-          bb = mbias[0];
-        } else {
-          const int qb = sub_blk ? (offk >> bs_shift) : (j / BS - blo);
-          bb = 0.f;
-          bool mm = false;
-#pragma unroll
-          for (int qq = 0; qq < 5; ++qq)
-            if (qb == qq) { mm = memb[qq]; bb = mbias[qq]; }
-          rem = rem && mm;
-        }
-        const float x = win ? st[half][r] * kLog2e : (rem ? (st[half][r] + bb) * kLog2e : -INFINITY);
-        st[half][r] = x;
-        mloc = fmaxf(mloc, x);
-      }
     mloc = fmaxf(mloc, __shfl_xor(mloc, 32, kWave));
-    const float m_new = fmaxf(m_run, mloc);
-    const float alpha = m_new == -INFINITY ? 1.f : exp2f(m_run - m_new);
-    const float m_use = m_new == -INFINITY ? 0.f : m_new;
-    float psum = 0.f;
-#pragma unroll
-    for (int half = 0; half < 2; ++half)
-#pragma unroll
-      for (int r = 0; r < 16; ++r) {
-        const float pv = exp2f(st[half][r] - m_use);
-        st[half][r] = pv;
-        psum += pv;
+    // lazy rescaling: the reference point m_b moves only when the chunk's max
+    // exceeds it by more than 8 (p <= 2^8 stays exact in fp32 and in P's
+    // rounding), so O is rescaled only on the rare chunks where a row's max jumps
+    const bool grow = mloc > m_b + 8.f;
+    if (__any(grow)) {
+      float alpha = 1.f;
+      if (grow) {
+        alpha = exp2f(m_b - mloc);    // 0 on a row's first non-empty chunk
+        m_b = mloc;
       }
-    l_run = l_run * alpha + psum;
-    m_run = m_new;
-    if (alpha != 1.f) {
+      l_run *= alpha;
 #pragma unroll
       for (int mt = 0; mt < MT; ++mt)
 #pragma unroll
         for (int r = 0; r < 16; ++r) o[mt][r] *= alpha;
     }
+    const float mb = m_b == -INFINITY ? 0.f : m_b;
+    float psum = 0.f;
+    if (fast) {
+      const float sub = addb - mb;
+#pragma unroll
+      for (int half = 0; half < 2; ++half)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+          const float pv = __builtin_amdgcn_exp2f(fmaf(st[half][r], kLog2e, sub));
+          st[half][r] = pv;
+          psum += pv;
+        }
+    } else {
+#pragma unroll
+      for (int half = 0; half < 2; ++half)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+          const float pv = __builtin_amdgcn_exp2f(st[half][r] - mb);
+          st[half][r] = pv;
+          psum += pv;
+        }
+    }
+    l_run += psum;
 
     // P^T as B operands (4 steps of 16 keys), rounded to the input dtype
     uint4 pb[4];
@@ -266,13 +307,11 @@ __global__ __launch_bounds__(128) void fwd_kernel(FwdK p) {
       pb[ks] = make_uint4(M::pack2(st[hf][r0], st[hf][r0 + 1]), M::pack2(st[hf][r0 + 2], st[hf][r0 + 3]),
                           M::pack2(st[hf][r0 + 4], st[hf][r0 + 5]), M::pack2(st[hf][r0 + 6], st[hf][r0 + 7]));
     }
-    // O^T += V^T P^T  (V^T operands read column-wise from the natural V tile)
-    const uint16_t* v16 = reinterpret_cast<const uint16_t*>(sV);
+    // O^T += V^T P^T
 #pragma unroll
     for (int mt = 0; mt < MT; ++mt)
 #pragma unroll
-      for (int ks = 0; ks < 4; ++ks)
-        o[mt] = M::mac(a_operand_t<KP>(v16, 32 * mt + rl, ks, h), pb[ks], o[mt]);
+      for (int ks = 0; ks < 4; ++ks) o[mt] = M::mac(a_operand_tr<VP>(v16, 16 * ks, 32 * mt, lane), pb[ks], o[mt]);
   }
 
   const float l_tot = l_run + __shfl_xor(l_run, 32, kWave);
@@ -292,7 +331,7 @@ __global__ __launch_bounds__(128) void fwd_kernel(FwdK p) {
     }
   if (a.lse && h == 0)
     a.lse[(int64_t)b * a.lse_sb + (int64_t)(t0 + row) * a.lse_st + (int64_t)hq * a.lse_sh] =
-        l_tot > 0.f ? (m_run + log2f(l_tot)) * kLn2 : -INFINITY;
+        l_tot > 0.f ? (m_b + log2f(l_tot)) * kLn2 : -INFINITY;
 }
 
 bool al16(const void* p) { return ((uintptr_t)p & 15u) == 0; }
@@ -319,8 +358,18 @@ int check_fwd(const srswa_fwd_args* a) {
     set_error("fwd: head dim %d not supported (64, 128)", a->D);
     return SRSWA_UNSUPPORTED;
   }
-  if (a->block_size < 16 || a->S > 64) {
-    set_error("fwd: block size >= 16 and <= 64 slots required");
+  if (a->block_size < 16 || (a->block_size & (a->block_size - 1)) || a->S > 64) {
+    set_error("fwd: block size must be a power of two >= 16, at most 64 slots");
+    return SRSWA_UNSUPPORTED;
+  }
+  if (ceil_div(a->Sk, kChunk) > 65536) {
+    set_error("fwd: key length above 4M");
+    return SRSWA_UNSUPPORTED;
+  }
+  // K / V of one (sequence, kv head) are addressed with 32-bit byte offsets
+  const int64_t span = ((int64_t)ceil_div(a->Sk, kChunk) * kChunk * std::max(a->k_st, a->v_st) + a->D) * 2;
+  if (span >= ((int64_t)1 << 32)) {
+    set_error("fwd: one sequence's K / V span 4 GiB or more");
     return SRSWA_UNSUPPORTED;
   }
   const int64_t st[] = {a->q_sb, a->q_st, a->q_sh, a->k_sb, a->k_st, a->k_sh, a->v_sb, a->v_st,
@@ -341,8 +390,7 @@ template <typename T, int D>
 int launch_fwd(const FwdK& k, size_t smem, hipStream_t st) {
   static size_t granted = 0;
   if (!ensure_dynamic_lds(&fwd_kernel<T, D>, smem, &granted)) return SRSWA_UNSUPPORTED;
-  const int64_t grid = (int64_t)k.a.B * k.a.HQ * k.ntiles;
-  hipLaunchKernelGGL((fwd_kernel<T, D>), dim3((unsigned)grid), dim3(128), smem, st, k);
+  hipLaunchKernelGGL((fwd_kernel<T, D>), dim3((unsigned)(8 * k.per_xcd)), dim3(128), smem, st, k);
   const hipError_t e = hipGetLastError();
   if (e != hipSuccess) {
     set_error("fwd launch failed: %s", hipGetErrorString(e));
@@ -363,13 +411,32 @@ extern "C" int srswa_gather_fwd(const srswa_fwd_args* a, void* stream) {
   FwdK k{};
   k.a = *a;
   k.ntiles = ceil_div(a->T, kTileRows);
-  k.nchunk = ceil_div(a->Sk, kChunk);
-  k.nwords = ceil_div(k.nchunk, 32);
-  const int per_row = a->S * (ceil_div(a->block_size, kChunk) + 1) + ceil_div(a->local_window, kChunk) + 1;
-  k.umax = (int)std::min<int64_t>((int64_t)k.nchunk, (int64_t)kTileRows * per_row);
+  const int nchunk = ceil_div(a->Sk, kChunk);
+  k.nwords = ceil_div(nchunk, 32);
+  k.SP = a->S + 1;
   k.G = a->HQ / a->HKV;
   k.IG = a->HQ / a->HI;
-  const size_t smem = FwdSmem::bytes(a->D, a->S, a->bias != nullptr, k.nwords, k.umax, 2);
+  k.bs_shift = __builtin_ctz((unsigned)a->block_size);
+  const int64_t nlogical = (int64_t)a->B * a->HQ * k.ntiles;
+  if (nlogical > (int64_t)1 << 30) {
+    set_error("fwd: too many query tiles");
+    return SRSWA_UNSUPPORTED;
+  }
+  k.nlogical = (int)nlogical;
+  k.per_xcd = ceil_div(k.nlogical, 8);
+  // distinct chunks one tile can visit: the selected blocks of 64 rows plus
+  // the window span of 64 consecutive rows
+  const int64_t per_tile = (int64_t)kTileRows * a->S * (ceil_div(a->block_size, kChunk) + 1) +
+                           ceil_div(a->local_window + kTileRows - 1, kChunk) + 1;
+  const int umax = (int)std::min<int64_t>(nchunk, per_tile);
+  const size_t tile = a->D == 128 ? FwdLds<128>::tileBytes : FwdLds<64>::tileBytes;
+  const size_t setup = (3 * 64 + 4) * 4 + (size_t)k.nwords * 4;
+  size_t n = std::max(tile, setup);
+  k.chunks_off = (int)n;
+  n += ((size_t)umax * 2 + 15) / 16 * 16;
+  k.sid_off = (int)n;
+  n += (size_t)64 * k.SP * 4 * (a->bias ? 2 : 1);
+  const size_t smem = (n + 15) / 16 * 16;
   if (smem > 156 * 1024) {
     set_error("fwd: %zu bytes of LDS needed (key length too large)", smem);
     return SRSWA_UNSUPPORTED;
