@@ -34,8 +34,11 @@ namespace {
 
 struct BwdK {
   srswa_bwd_args a;
-  int ntiles, nchunk, nwords, umax, twords;
+  int ntiles, nchunk, nwords, umax, twords, SP, bs_shift;
   int G, IG;
+  int nlogical, per_xcd;          // dQ workgroups (sequence, query head, tile), XCD-aware order
+  int nlogical_kv, per_xcd_kv;    // dK/dV workgroups (sequence, kv head, chunk)
+  int chunks_off, sid_off;        // dQ LDS byte offsets of the chunk list and sorted ids
   float* delta;       // [B, T, HQ]
   uint32_t* touch;    // [B, HI, nchunk, twords]
 };
@@ -104,43 +107,62 @@ __global__ __launch_bounds__(256) void touch_kernel(BwdK p) {
 }
 
 // -------------------------------------------------------------- 3. dQ
-constexpr int kSlotCap = 32;   // planned chunks per tile covered by the slot table
+template <int D> struct DqLds {
+  static constexpr int KP = D + 16;   // K: row reads (S^T) and transposing reads (dQ)
+  static constexpr int VP = D + 8;    // V: row reads only
+  static constexpr int vOff = kChunk * KP * 2;
+  static constexpr int tileBytes = vOff + kChunk * VP * 2;
+};
 
+// One workgroup = (sequence, query head, 64-row tile), two waves of 32 rows,
+// the forward's chunk plan; per chunk S^T = K Q^T and dP^T = V dO^T (lanes own
+// rows, so lse and delta are per-lane registers), dS = P (dP - delta),
+// dQ^T += K^T dS^T with the K^T operand read by transposing LDS reads.  The
+// bias gradient (sum of fp32 dS over the remote keys of a selected block) is
+// summed per (row, sorted block) in LDS in a fixed order and written per slot
+// at the end (0 for repeated ids) -- no atomics.
 template <typename T, int D>
-__global__ __launch_bounds__(128) void dq_kernel(BwdK p) {
+__global__ __launch_bounds__(128, D == 128 ? 1 : 2) void dq_kernel(BwdK p) {
   using M = Mfma<T>;
-  constexpr int KP = D + 8;
-  constexpr int KS = D / 16;
-  constexpr int MT = D / 32;
-  constexpr int NT = 128;
+  using L = DqLds<D>;
+  constexpr int KP = L::KP, VP = L::VP;
+  constexpr int KS = D / 16, MT = D / 32, NT = 128;
+  constexpr int PPT = kChunk * D / 8 / NT;
+  constexpr int RPP = NT / (D / 8);
   extern __shared__ __align__(16) unsigned char smem[];
   const srswa_bwd_args& a = p.a;
+
+  const int lid = (int)(blockIdx.x & 7) * p.per_xcd + (int)(blockIdx.x >> 3);
+  if (lid >= p.nlogical) return;
+
   T* sK = reinterpret_cast<T*>(smem);
-  T* sV = sK + kChunk * KP;
-  int8_t* s_tab = reinterpret_cast<int8_t*>(sV + kChunk * KP);
-  int* s_qi = reinterpret_cast<int*>(s_tab + kSlotCap * 64 * 8);
+  T* sV = reinterpret_cast<T*>(smem + L::vOff);
+  int* s_qi = reinterpret_cast<int*>(smem);          // set-up only (aliases the tiles)
   int* s_seg = s_qi + 64;
   int* s_ls = s_seg + 64;
-  int* s_ids = s_ls + 64;
-  float* s_bias = reinterpret_cast<float*>(s_ids + 64 * a.S);
-  float* s_dbias = s_bias + 64 * a.S;
-  uint32_t* s_bits = reinterpret_cast<uint32_t*>(s_dbias + 64 * a.S);
-  int* s_chunks = reinterpret_cast<int*>(s_bits + p.nwords);
-  int* s_count = s_chunks + p.umax;
+  int* s_count = s_ls + 64;
+  uint32_t* s_bits = reinterpret_cast<uint32_t*>(s_count + 4);
+  uint16_t* s_chunks = reinterpret_cast<uint16_t*>(smem + p.chunks_off);
+  int* s_sid = reinterpret_cast<int*>(smem + p.sid_off);
+  float* s_sb = a.bias ? reinterpret_cast<float*>(s_sid + 64 * p.SP) : nullptr;
+  int* s_sslot = a.dbias ? reinterpret_cast<int*>(s_sid + 64 * p.SP * (a.bias ? 2 : 1)) : nullptr;
+  float* s_sdb = a.dbias ? reinterpret_cast<float*>(s_sslot + 64 * p.SP) : nullptr;
 
   const int tid = threadIdx.x, wave = tid / kWave, lane = tid % kWave;
-  const int h = lane / 32, rl = lane % 32;
-  const int tile = blockIdx.x % p.ntiles;
-  const int64_t bh = blockIdx.x / p.ntiles;
-  const int hq = (int)(bh % a.HQ);
-  const int b = (int)(bh / a.HQ);
+  const int h = lane >> 5, rl = lane & 31;
+  const int tile = lid % p.ntiles;
+  const int bh = lid / p.ntiles;
+  const int hq = bh % a.HQ, b = bh / a.HQ;
   const int kvh = hq / p.G, ih = hq / p.IG;
   const int t0 = tile * kTileRows;
   const int nrows = min(kTileRows, a.T - t0);
   const int off = a.Sk - a.T;
-  const int BS = a.block_size, LW = a.local_window, S = a.S;
+  const int BS = a.block_size, LW = a.local_window, SP = p.SP;
+  const int maxblk = (a.Sk - 1) >> p.bs_shift;
+  const bool blk64 = BS >= kChunk;
 
-  for (int r = tid; r < 64; r += NT) {
+  if (tid < 64) {
+    const int r = tid;
     int qi = -1, seg = 0, ls = 0;
     if (r < nrows) {
       qi = off + t0 + r;
@@ -150,237 +172,226 @@ __global__ __launch_bounds__(128) void dq_kernel(BwdK p) {
     s_qi[r] = qi;
     s_seg[r] = seg;
     s_ls[r] = ls;
+    const int rr = min(r, nrows - 1);
+    const int32_t* ids = a.idx + (int64_t)b * a.idx_sb + (int64_t)ih * a.idx_sh + (int64_t)(t0 + rr) * a.idx_st;
+    const float* bias =
+        a.bias ? a.bias + (int64_t)b * a.bias_sb + (int64_t)ih * a.bias_sh + (int64_t)(t0 + rr) * a.bias_st : nullptr;
+    sort_row_ids(ids, bias, r < nrows ? a.S : 0, SP, BS, maxblk, qi, seg, ls, s_sid + r * SP,
+                 s_sb ? s_sb + r * SP : nullptr, s_sslot ? s_sslot + r * SP : nullptr);
+    if (s_sdb)
+      for (int i = 0; i < SP; ++i) s_sdb[r * SP + i] = 0.f;
   }
-  for (int e = tid; e < 64 * S; e += NT) {
-    const int r = e / S, s = e % S;
-    int id = -1;
-    float bv = 0.f;
-    if (r < nrows) {
-      id = a.idx[(int64_t)b * a.idx_sb + (int64_t)ih * a.idx_sh + (int64_t)(t0 + r) * a.idx_st + s];
-      if (a.bias) bv = a.bias[(int64_t)b * a.bias_sb + (int64_t)ih * a.bias_sh + (int64_t)(t0 + r) * a.bias_st + s];
-    }
-    s_ids[e] = id;
-    s_bias[e] = bv;
-    s_dbias[e] = 0.f;
-  }
-  for (int w = tid; w < p.nwords; w += NT) s_bits[w] = 0u;
   __syncthreads();
-  const int U = build_chunk_plan(s_qi, s_seg, s_ls, s_ids, S, BS, nrows, p.nchunk, p.nwords,
-                                 s_bits, s_chunks, s_count, LW, a.Sk);
-  build_slot_table(s_qi, s_seg, s_ls, s_ids, s_chunks, U, kSlotCap, S, BS, a.Sk, nrows, s_tab);
+  const int U = plan_chunks(s_qi, s_seg, s_ls, s_sid, SP, BS, LW, nrows, p.nwords, s_bits, s_chunks, s_count);
 
   const int row = wave * 32 + rl;
-  const bool row_ok = row < nrows;
-  const int my_qi = s_qi[row], my_seg = s_seg[row], my_ls = s_ls[row];
-  const uint32_t wlen = (uint32_t)max(my_qi - my_ls + 1, 0);
-  const uint32_t rlen = (uint32_t)max(min(my_ls, my_qi + 1) - my_seg, 0);
-  const int trow = t0 + (row_ok ? row : 0);
+  RowWalk w;
+  w.ok = row < nrows;
+  w.ls = s_ls[row];
+  w.seg = s_seg[row];
+  w.hi = s_qi[row] + 1;
+  w.rem_hi = min(w.ls, w.hi);
+  w.sid = s_sid + row * SP;
+  w.sb = s_sb ? s_sb + row * SP : nullptr;
+  w.cur = 0;
+  w.nid = w.sid[0];
+  const int trow = t0 + (w.ok ? row : 0);
   uint4 qf[KS], gf[KS];
   {
     const T* qrow = reinterpret_cast<const T*>(a.q) + (int64_t)b * a.q_sb + (int64_t)trow * a.q_st + (int64_t)hq * a.q_sh;
     const T* grow = reinterpret_cast<const T*>(a.dout) + (int64_t)b * a.do_sb + (int64_t)trow * a.do_st + (int64_t)hq * a.do_sh;
 #pragma unroll
     for (int ks = 0; ks < KS; ++ks) {
-      uint4 w = row_ok ? *reinterpret_cast<const uint4*>(qrow + 16 * ks + 8 * h) : make_uint4(0, 0, 0, 0);
-      uint32_t* ww = reinterpret_cast<uint32_t*>(&w);
+      uint4 x = w.ok ? *reinterpret_cast<const uint4*>(qrow + 16 * ks + 8 * h) : make_uint4(0, 0, 0, 0);
+      uint32_t* xx = reinterpret_cast<uint32_t*>(&x);
 #pragma unroll
-      for (int e = 0; e < 4; ++e) ww[e] = M::pack2(M::lo(ww[e]) * a.scale, M::hi(ww[e]) * a.scale);
-      qf[ks] = w;
-      gf[ks] = row_ok ? *reinterpret_cast<const uint4*>(grow + 16 * ks + 8 * h) : make_uint4(0, 0, 0, 0);
+      for (int e = 0; e < 4; ++e) xx[e] = M::pack2(M::lo(xx[e]) * a.scale, M::hi(xx[e]) * a.scale);
+      qf[ks] = x;
+      gf[ks] = w.ok ? *reinterpret_cast<const uint4*>(grow + 16 * ks + 8 * h) : make_uint4(0, 0, 0, 0);
     }
   }
-  const float lse_l2 = row_ok ? a.lse[(int64_t)b * a.lse_sb + (int64_t)trow * a.lse_st + (int64_t)hq * a.lse_sh] * kLog2e
-                              : INFINITY;
-  const float dlt = row_ok ? p.delta[((int64_t)b * a.T + trow) * a.HQ + hq] : 0.f;
+  // lse in log2 units (+inf for rows past T: every P is then 0) and delta
+  const float lse_l2 = w.ok ? a.lse[(int64_t)b * a.lse_sb + (int64_t)trow * a.lse_st + (int64_t)hq * a.lse_sh] * kLog2e
+                            : INFINITY;
+  const float dlt = w.ok ? p.delta[((int64_t)b * a.T + trow) * a.HQ + hq] : 0.f;
 
   f32x16_t dq[MT];
 #pragma unroll
   for (int mt = 0; mt < MT; ++mt) dq[mt] = zero16();
 
-  const T* kg = reinterpret_cast<const T*>(a.k) + (int64_t)b * a.k_sb + (int64_t)kvh * a.k_sh;
-  const T* vg = reinterpret_cast<const T*>(a.v) + (int64_t)b * a.v_sb + (int64_t)kvh * a.v_sh;
-  constexpr int PPT = kChunk * D / 8 / NT;
+  const __amdgpu_buffer_rsrc_t krs = make_rsrc(
+      reinterpret_cast<const T*>(a.k) + (int64_t)b * a.k_sb + (int64_t)kvh * a.k_sh,
+      (uint32_t)(((int64_t)(a.Sk - 1) * a.k_st + D) * 2));
+  const __amdgpu_buffer_rsrc_t vrs = make_rsrc(
+      reinterpret_cast<const T*>(a.v) + (int64_t)b * a.v_sb + (int64_t)kvh * a.v_sh,
+      (uint32_t)(((int64_t)(a.Sk - 1) * a.v_st + D) * 2));
+  const uint32_t kvo = (uint32_t)((tid / (D / 8)) * a.k_st + (tid % (D / 8)) * 8) * 2;
+  const uint32_t vvo = (uint32_t)((tid / (D / 8)) * a.v_st + (tid % (D / 8)) * 8) * 2;
+  T* sKw = sK + (tid / (D / 8)) * KP + (tid % (D / 8)) * 8;
+  T* sVw = sV + (tid / (D / 8)) * VP + (tid % (D / 8)) * 8;
   uint4 kpre[PPT], vpre[PPT];
   auto fetch = [&](int c) {
+    const uint32_t kso = (uint32_t)c * kChunk * (uint32_t)a.k_st * 2u;
+    const uint32_t vso = (uint32_t)c * kChunk * (uint32_t)a.v_st * 2u;
 #pragma unroll
     for (int i = 0; i < PPT; ++i) {
-      const int pc = tid + i * NT;
-      const int j = c * kChunk + pc / (D / 8), col = pc % (D / 8);
-      const bool in = j < a.Sk;
-      kpre[i] = in ? *reinterpret_cast<const uint4*>(kg + (int64_t)j * a.k_st + col * 8) : make_uint4(0, 0, 0, 0);
-      vpre[i] = in ? *reinterpret_cast<const uint4*>(vg + (int64_t)j * a.v_st + col * 8) : make_uint4(0, 0, 0, 0);
+      kpre[i] = buffer_load16(krs, kvo, kso + (uint32_t)(i * RPP) * (uint32_t)a.k_st * 2u);
+      vpre[i] = buffer_load16(vrs, vvo, vso + (uint32_t)(i * RPP) * (uint32_t)a.v_st * 2u);
     }
   };
-  const bool one_blk = (BS % kChunk) == 0;
-  const bool sub_blk = (kChunk % BS) == 0;
-  const int bs_shift = __ffs(BS) - 1;
+  const uint16_t* k16 = reinterpret_cast<const uint16_t*>(sK);
 
   if (U > 0) fetch(s_chunks[0]);
   for (int u = 0; u < U; ++u) {
-    const int c = s_chunks[u];
-    const int j0 = c * kChunk;
-    __syncthreads();
+    const int j0 = (int)s_chunks[u] * kChunk;
+    __syncthreads();   // previous chunk fully consumed
 #pragma unroll
     for (int i = 0; i < PPT; ++i) {
-      const int pc = tid + i * NT;
-      const int key = pc / (D / 8), col = pc % (D / 8);
-      *reinterpret_cast<uint4*>(sK + key * KP + col * 8) = kpre[i];
-      *reinterpret_cast<uint4*>(sV + key * KP + col * 8) = vpre[i];
+      *reinterpret_cast<uint4*>(sKw + i * RPP * KP) = kpre[i];
+      *reinterpret_cast<uint4*>(sVw + i * RPP * VP) = vpre[i];
     }
     __syncthreads();
     if (u + 1 < U) fetch(s_chunks[u + 1]);
 
-    f32x16_t st[2] = {zero16(), zero16()}, dp[2] = {zero16(), zero16()};
-#pragma unroll
-    for (int ks = 0; ks < KS; ++ks) {
-      st[0] = M::mac(*reinterpret_cast<const uint4*>(sK + rl * KP + 16 * ks + 8 * h), qf[ks], st[0]);
-      st[1] = M::mac(*reinterpret_cast<const uint4*>(sK + (32 + rl) * KP + 16 * ks + 8 * h), qf[ks], st[1]);
-      dp[0] = M::mac(*reinterpret_cast<const uint4*>(sV + rl * KP + 16 * ks + 8 * h), gf[ks], dp[0]);
-      dp[1] = M::mac(*reinterpret_cast<const uint4*>(sV + (32 + rl) * KP + 16 * ks + 8 * h), gf[ks], dp[1]);
-    }
-
-    const int blo = j0 / BS;
-    bool memb[5];
-    float mbias[5];
-    int mslot[5];
-    if (u < kSlotCap) {
-      const uint2 tw = *reinterpret_cast<const uint2*>(s_tab + (u * 64 + row) * 8);
-      const int8_t* t8 = reinterpret_cast<const int8_t*>(&tw);
-#pragma unroll
-      for (int q = 0; q < 5; ++q) {
-        mslot[q] = t8[q];
-        memb[q] = t8[q] >= 0;
-        mbias[q] = memb[q] ? s_bias[row * S + t8[q]] : 0.f;
-      }
-    } else {
-      const int nq = min(j0 + kChunk - 1, a.Sk - 1) / BS - blo + 1;
-#pragma unroll
-      for (int q = 0; q < 5; ++q) {
-        memb[q] = false;
-        mbias[q] = 0.f;
-        mslot[q] = -1;
-        if (q < nq && row_ok) {
-          for (int s = 0; s < S; ++s)
-            if (s_ids[row * S + s] == blo + q) {
-              memb[q] = true;
-              mbias[q] = s_bias[row * S + s];
-              mslot[q] = s;
-              break;
-            }
-        }
-      }
-    }
-
-    float dsum[5] = {0.f, 0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-    for (int half = 0; half < 2; ++half)
-#pragma unroll
-      for (int r = 0; r < 16; ++r) {
-        const int offk = 32 * half + d_row(r, h);
-        const int j = j0 + offk;
-        const bool win = (uint32_t)(j - my_ls) < wlen;
-        bool rem = (uint32_t)(j - my_seg) < rlen;
-        int qb = 0;
-        float bb;
-        if (one_blk) {
-          rem = rem && memb[0];
-          bb = mbias[0];
-        } else {
-          qb = sub_blk ? (offk >> bs_shift) : (j / BS - blo);
-          bb = 0.f;
-          bool mm = false;
-#pragma unroll
-          for (int qq = 0; qq < 5; ++qq)
-            if (qb == qq) { mm = memb[qq]; bb = mbias[qq]; }
-          rem = rem && mm;
-        }
-        const float sv = st[half][r];
-        const float pv = (win || rem) ? exp2f((rem ? sv + bb : sv) * kLog2e - lse_l2) : 0.f;
-        const float dsv = pv * (dp[half][r] - dlt);
-        st[half][r] = dsv;
-        if (rem) {
-#pragma unroll
-          for (int qq = 0; qq < 5; ++qq)
-            if (qb == qq) dsum[qq] += dsv;
-        }
-      }
-    if (a.dbias) {
-#pragma unroll
-      for (int qq = 0; qq < 5; ++qq) {
-        const float tot = dsum[qq] + __shfl_xor(dsum[qq], 32, kWave);
-        if (h == 0 && mslot[qq] >= 0) s_dbias[row * S + mslot[qq]] += tot;
-      }
-    }
+    uint64_t keep, rm;
+    float bq[4];
+    int qix[4];
+    const bool fast = __all(chunk_mask(w, j0, p.bs_shift, blk64, keep, rm, bq, qix));
+    const float addb = (fast && w.sb && rm != 0ull) ? bq[0] : 0.f;
+    float dsum[4] = {0.f, 0.f, 0.f, 0.f};
     uint4 db[4];
 #pragma unroll
-    for (int ks = 0; ks < 4; ++ks) {
-      const int hf = ks >> 1, r0 = 8 * (ks & 1);
-      db[ks] = make_uint4(M::pack2(st[hf][r0], st[hf][r0 + 1]), M::pack2(st[hf][r0 + 2], st[hf][r0 + 3]),
-                          M::pack2(st[hf][r0 + 4], st[hf][r0 + 5]), M::pack2(st[hf][r0 + 6], st[hf][r0 + 7]));
+    for (int half = 0; half < 2; ++half) {
+      f32x16_t st = zero16(), dp = zero16();
+#pragma unroll
+      for (int ks = 0; ks < KS; ++ks) {
+        st = M::mac(*reinterpret_cast<const uint4*>(sK + (32 * half + rl) * KP + 16 * ks + 8 * h), qf[ks], st);
+        dp = M::mac(*reinterpret_cast<const uint4*>(sV + (32 * half + rl) * VP + 16 * ks + 8 * h), gf[ks], dp);
+      }
+      if (fast) {
+        const float sub = addb - lse_l2;
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+          const float pv = __builtin_amdgcn_exp2f(fmaf(st[r], kLog2e, sub));
+          const float dsv = pv * (dp[r] - dlt);
+          st[r] = dsv;
+          dsum[0] += dsv;
+        }
+        if (rm == 0ull) dsum[0] = 0.f;
+      } else {
+        const uint32_t k32 = (uint32_t)((keep >> (4 * h)) >> (32 * half));
+        const uint32_t r32 = (uint32_t)((rm >> (4 * h)) >> (32 * half));
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+          const int bit = 8 * (r >> 2) + (r & 3);
+          const int qq = 2 * half + (r >> 3);
+          const bool remb = (r32 >> bit) & 1u;
+          const float x = fmaf(st[r], kLog2e, (remb ? bq[qq] : 0.f) - lse_l2);
+          const float pv = ((k32 >> bit) & 1u) ? __builtin_amdgcn_exp2f(x) : 0.f;
+          const float dsv = pv * (dp[r] - dlt);
+          st[r] = dsv;
+          if (remb) dsum[qq] += dsv;
+        }
+      }
+      db[2 * half] = make_uint4(M::pack2(st[0], st[1]), M::pack2(st[2], st[3]), M::pack2(st[4], st[5]),
+                                M::pack2(st[6], st[7]));
+      db[2 * half + 1] = make_uint4(M::pack2(st[8], st[9]), M::pack2(st[10], st[11]), M::pack2(st[12], st[13]),
+                                    M::pack2(st[14], st[15]));
     }
-    // dQ^T += K^T dS^T  (K^T operands read column-wise from the natural K tile)
-    const uint16_t* k16 = reinterpret_cast<const uint16_t*>(sK);
+    // dQ^T += K^T dS^T
 #pragma unroll
     for (int mt = 0; mt < MT; ++mt)
 #pragma unroll
-      for (int ks = 0; ks < 4; ++ks)
-        dq[mt] = M::mac(a_operand_t<KP>(k16, 32 * mt + rl, ks, h), db[ks], dq[mt]);
+      for (int ks = 0; ks < 4; ++ks) dq[mt] = M::mac(a_operand_tr<KP>(k16, 16 * ks, 32 * mt, lane), db[ks], dq[mt]);
+
+    if (s_sdb) {
+#pragma unroll
+      for (int qq = 0; qq < 4; ++qq) {
+        const float tot = dsum[qq] + __shfl_xor(dsum[qq], 32, kWave);
+        if (h == 0 && w.ok && qix[qq] >= 0) s_sdb[row * SP + qix[qq]] += tot;
+      }
+    }
   }
 
-  if (row_ok) {
+  if (w.ok) {
     T* qrow = reinterpret_cast<T*>(a.dq) + (int64_t)b * a.dq_sb + (int64_t)(t0 + row) * a.dq_st + (int64_t)hq * a.dq_sh;
 #pragma unroll
     for (int mt = 0; mt < MT; ++mt)
 #pragma unroll
       for (int g = 0; g < 4; ++g) {
         const int d0 = 32 * mt + 8 * g + 4 * h;
-        uint2 w;
-        w.x = M::pack2(dq[mt][4 * g] * a.scale, dq[mt][4 * g + 1] * a.scale);
-        w.y = M::pack2(dq[mt][4 * g + 2] * a.scale, dq[mt][4 * g + 3] * a.scale);
-        *reinterpret_cast<uint2*>(qrow + d0) = w;
+        uint2 x;
+        x.x = M::pack2(dq[mt][4 * g] * a.scale, dq[mt][4 * g + 1] * a.scale);
+        x.y = M::pack2(dq[mt][4 * g + 2] * a.scale, dq[mt][4 * g + 3] * a.scale);
+        *reinterpret_cast<uint2*>(qrow + d0) = x;
       }
   }
-  if (a.dbias) {
+  if (s_sdb) {
     __syncthreads();
-    for (int e = tid; e < nrows * S; e += NT) {
-      const int r = e / S, s = e % S;
-      a.dbias[(int64_t)b * a.db_sb + (int64_t)hq * a.db_sh + (int64_t)(t0 + r) * a.db_st + s] = s_dbias[e];
+    for (int e = tid; e < nrows * a.S; e += NT) {
+      const int r = e / a.S, s = e % a.S;
+      float v = 0.f;
+      for (int i = 0; i < SP; ++i)
+        if (s_sslot[r * SP + i] == s) v = s_sdb[r * SP + i];
+      a.dbias[(int64_t)b * a.db_sb + (int64_t)hq * a.db_sh + (int64_t)(t0 + r) * a.db_st + s] = v;
     }
   }
 }
 
 // -------------------------------------------------------------- 4. dK / dV
+template <int D> struct DkvLds {
+  static constexpr int QP = D + 16;   // Q / dO tiles: row reads and transposing reads
+  static constexpr int gOff = kTileRows * QP * 2;
+  static constexpr int tileBytes = 2 * gOff;
+};
+
+// One workgroup = (sequence, kv head, 64-key chunk), two waves of 32 keys
+// each holding their keys' K / V as MFMA operands and dK / dV accumulators.
+// For every query head of the group, the query tiles whose windows cover the
+// chunk or whose touch bit is set are visited in ascending order: Q (scaled,
+// rounded) and dO are staged in LDS (the next tile prefetched into registers),
+// one wave derives every row's keep mask over the chunk, each wave transposes
+// the masks of its keys with ballots (skipped when every row keeps every key),
+// then S = Q K^T, dP = dO V^T, dV^T += dO^T P and dK^T += Q^T dS, the
+// transposed operands read with ds_read_b64_tr_b16.  Deterministic: fixed
+// visiting order, no atomics.
 template <typename T, int D>
-__global__ __launch_bounds__(128) void dkv_kernel(BwdK p) {
+__global__ __launch_bounds__(128, 1) void dkv_kernel(BwdK p) {
   using M = Mfma<T>;
-  constexpr int KP = D + 8;
-  constexpr int KS = D / 16;
-  constexpr int MT = D / 32;
-  constexpr int NQ = 5;                       // blocks a 64-key chunk can overlap (BS >= 16)
+  using L = DkvLds<D>;
+  constexpr int QP = L::QP;
+  constexpr int KS = D / 16, MT = D / 32, NT = 128;
+  constexpr int PPT = kTileRows * D / 8 / NT;
+  constexpr int RPP = NT / (D / 8);
   extern __shared__ __align__(16) unsigned char smem[];
   const srswa_bwd_args& a = p.a;
-  T* sQ = reinterpret_cast<T*>(smem);         // [64][KP]  q * scale, rounded
-  T* sG = sQ + kTileRows * KP;                // [64][KP]  dO
-  int4* s_row = reinterpret_cast<int4*>(sG + kTileRows * KP);   // {qi, ls, seg, lse*log2e bits}
-  float* s_dlt = reinterpret_cast<float*>(s_row + 64);
-  float* s_mb = s_dlt + 64;                   // [64][NQ] bias if member else NaN
-  int* s_ids = reinterpret_cast<int*>(s_mb + 64 * NQ);   // [64 * S]
-  float* s_bias = reinterpret_cast<float*>(s_ids + 64 * a.S);
+
+  const int lid = (int)(blockIdx.x & 7) * p.per_xcd_kv + (int)(blockIdx.x >> 3);
+  if (lid >= p.nlogical_kv) return;
+
+  T* sQ = reinterpret_cast<T*>(smem);
+  T* sG = reinterpret_cast<T*>(smem + L::gOff);
+  float* s_lse = reinterpret_cast<float*>(smem + L::tileBytes);   // [64] lse * log2e (+inf past T)
+  float* s_dlt = s_lse + 64;                                      // [64] delta
+  uint64_t* s_keep = reinterpret_cast<uint64_t*>(s_dlt + 64);     // [64] row -> keys kept
+  uint64_t* s_rem = s_keep + 64;                                  // [64] row -> remote keys kept
+  float* s_bq = reinterpret_cast<float*>(s_rem + 64);             // [4][64] bias (log2) per quarter, row
+  int* s_flag = reinterpret_cast<int*>(s_bq + 4 * 64);            // [4]: every row keeps the whole chunk
+  int* s_tiles = s_flag + 4;                                      // visit list
 
   const int tid = threadIdx.x, wave = tid / kWave, lane = tid % kWave;
-  const int h = lane / 32, rl = lane % 32;
-  const int c = blockIdx.x % p.nchunk;
-  const int64_t bk = blockIdx.x / p.nchunk;
-  const int kvh = (int)(bk % a.HKV);
-  const int b = (int)(bk / a.HKV);
+  const int h = lane >> 5, rl = lane & 31;
+  const int c = lid % p.nchunk;
+  const int bk = lid / p.nchunk;
+  const int kvh = bk % a.HKV, b = bk / a.HKV;
   const int j0 = c * kChunk;
-  const int jmine = j0 + 32 * wave + rl;       // this lane's key
+  const int kk = 32 * wave + rl;               // this lane's key within the chunk
+  const int jmine = j0 + kk;
   const bool key_ok = jmine < a.Sk;
   const int off = a.Sk - a.T;
   const int BS = a.block_size, LW = a.local_window, S = a.S;
-  const int blo = j0 / BS;
-  const int bhi = min(j0 + kChunk - 1, a.Sk - 1) / BS;
-  const int qmine = jmine / BS - blo;
+  const int maxblk = (a.Sk - 1) >> p.bs_shift;
+  const int myq = kk >> 4;                     // this key's 16-key quarter
 
   uint4 kf[KS], vf[KS];
   {
@@ -401,26 +412,26 @@ __global__ __launch_bounds__(128) void dkv_kernel(BwdK p) {
   const int tau_a = max(wlo_t, 0) / kTileRows;
   const int tau_b = whi_t < 0 ? -1 : min(whi_t / kTileRows, p.ntiles - 1);
 
-  constexpr int NT = 128;
-  constexpr int PPT = kTileRows * D / 8 / NT;
-  uint4 qpre[PPT], gpre[PPT];   // one tile's Q / dO pieces (loaded together, then staged)
-  int* s_tiles = reinterpret_cast<int*>(s_bias + 64 * a.S);    // visit list
+  T* sQw = sQ + (tid / (D / 8)) * QP + (tid % (D / 8)) * 8;
+  T* sGw = sG + (tid / (D / 8)) * QP + (tid % (D / 8)) * 8;
+  const uint16_t* q16 = reinterpret_cast<const uint16_t*>(sQ);
+  const uint16_t* g16 = reinterpret_cast<const uint16_t*>(sG);
   __shared__ int s_ntiles;
+  uint4 qpre[PPT], gpre[PPT];
 
   for (int gq = 0; gq < p.G; ++gq) {
     const int hq = kvh * p.G + gq;
     const int ih = hq / p.IG;
     const uint32_t* tb = p.touch + (((int64_t)b * a.HI + ih) * p.nchunk + c) * p.twords;
-    // visit list: window tiles [tau_a, tau_b] plus every touched tile, ascending
     __syncthreads();
     if (tid == 0) {
       int n = 0;
-      for (int w = 0; w < p.twords; ++w) {
-        uint32_t bits = tb[w];
-        const int lo = max(tau_a - 32 * w, 0), hi = min(tau_b - 32 * w, 31);
+      for (int wd = 0; wd < p.twords; ++wd) {
+        uint32_t bits = tb[wd];
+        const int lo = max(tau_a - 32 * wd, 0), hi = min(tau_b - 32 * wd, 31);
         if (lo <= hi) bits |= (hi - lo == 31) ? 0xffffffffu : (((1u << (hi - lo + 1)) - 1u) << lo);
         while (bits) {
-          const int tau = 32 * w + __ffs(bits) - 1;
+          const int tau = 32 * wd + __ffs(bits) - 1;
           bits &= bits - 1;
           if (tau < p.ntiles) s_tiles[n++] = tau;
         }
@@ -429,124 +440,156 @@ __global__ __launch_bounds__(128) void dkv_kernel(BwdK p) {
     }
     __syncthreads();
     const int nt = s_ntiles;
+    const __amdgpu_buffer_rsrc_t qrs = make_rsrc(
+        reinterpret_cast<const T*>(a.q) + (int64_t)b * a.q_sb + (int64_t)hq * a.q_sh,
+        (uint32_t)(((int64_t)(a.T - 1) * a.q_st + D) * 2));
+    const __amdgpu_buffer_rsrc_t grs = make_rsrc(
+        reinterpret_cast<const T*>(a.dout) + (int64_t)b * a.do_sb + (int64_t)hq * a.do_sh,
+        (uint32_t)(((int64_t)(a.T - 1) * a.do_st + D) * 2));
+    const uint32_t qvo = (uint32_t)((tid / (D / 8)) * a.q_st + (tid % (D / 8)) * 8) * 2;
+    const uint32_t gvo = (uint32_t)((tid / (D / 8)) * a.do_st + (tid % (D / 8)) * 8) * 2;
     auto fetch = [&](int tau) {
-      const int t0 = tau * kTileRows;
-      const int nrows = min(kTileRows, a.T - t0);
+      const uint32_t qso = (uint32_t)tau * kTileRows * (uint32_t)a.q_st * 2u;
+      const uint32_t gso = (uint32_t)tau * kTileRows * (uint32_t)a.do_st * 2u;
 #pragma unroll
       for (int i = 0; i < PPT; ++i) {
-        const int pc = tid + i * NT;
-        const int r = pc / (D / 8), col = pc % (D / 8);
-        const bool in = r < nrows;
-        qpre[i] = in ? *reinterpret_cast<const uint4*>(reinterpret_cast<const T*>(a.q) + (int64_t)b * a.q_sb +
-                                                       (int64_t)(t0 + r) * a.q_st + (int64_t)hq * a.q_sh + col * 8)
-                     : make_uint4(0, 0, 0, 0);
-        gpre[i] = in ? *reinterpret_cast<const uint4*>(reinterpret_cast<const T*>(a.dout) + (int64_t)b * a.do_sb +
-                                                       (int64_t)(t0 + r) * a.do_st + (int64_t)hq * a.do_sh + col * 8)
-                     : make_uint4(0, 0, 0, 0);
+        qpre[i] = buffer_load16(qrs, qvo, qso + (uint32_t)(i * RPP) * (uint32_t)a.q_st * 2u);
+        gpre[i] = buffer_load16(grs, gvo, gso + (uint32_t)(i * RPP) * (uint32_t)a.do_st * 2u);
       }
     };
+    if (nt > 0) fetch(s_tiles[0]);
     for (int it = 0; it < nt; ++it) {
       const int tau = s_tiles[it];
-      {
-        const int t0 = tau * kTileRows;
-        const int nrows = min(kTileRows, a.T - t0);
-        fetch(tau);        // all loads of the tile in flight at once
-        __syncthreads();   // previous tile consumed
+      const int t0 = tau * kTileRows;
+      const int nrows = min(kTileRows, a.T - t0);
+      __syncthreads();   // previous tile consumed
 #pragma unroll
-        for (int i = 0; i < PPT; ++i) {
-          const int pc = tid + i * NT;
-          const int r = pc / (D / 8), col = pc % (D / 8);
-          uint4 qw = qpre[i];
-          uint32_t* ww = reinterpret_cast<uint32_t*>(&qw);
+      for (int i = 0; i < PPT; ++i) {
+        uint4 x = qpre[i];
+        uint32_t* xx = reinterpret_cast<uint32_t*>(&x);
 #pragma unroll
-          for (int e = 0; e < 4; ++e) ww[e] = M::pack2(M::lo(ww[e]) * a.scale, M::hi(ww[e]) * a.scale);
-          *reinterpret_cast<uint4*>(sQ + r * KP + col * 8) = qw;
-          *reinterpret_cast<uint4*>(sG + r * KP + col * 8) = gpre[i];
-        }
-        for (int r = tid; r < 64; r += NT) {
-          int4 ri = make_int4(INT_MIN, 0, 0, 0);   // invalid row: qi < every key
-          float dl = 0.f;
-          if (r < nrows) {
-            const int t = t0 + r;
-            const int qi = off + t;
-            const int seg = a.seg ? a.seg[(int64_t)b * a.seg_sb + t] : 0;
-            const float lse = a.lse[(int64_t)b * a.lse_sb + (int64_t)t * a.lse_st + (int64_t)hq * a.lse_sh];
-            ri = make_int4(qi, max(qi - LW + 1, seg), seg, __float_as_int(lse * kLog2e));
-            dl = p.delta[((int64_t)b * a.T + t) * a.HQ + hq];
+        for (int e = 0; e < 4; ++e) xx[e] = M::pack2(M::lo(xx[e]) * a.scale, M::hi(xx[e]) * a.scale);
+        *reinterpret_cast<uint4*>(sQw + i * RPP * QP) = x;
+        *reinterpret_cast<uint4*>(sGw + i * RPP * QP) = gpre[i];
+      }
+      if (it + 1 < nt) fetch(s_tiles[it + 1]);
+      // wave 0: every row's keep mask over the chunk's keys
+      if (tid < 64) {
+        const int r = tid;
+        uint64_t keep = 0ull, rm = 0ull;
+        float bqv[4] = {0.f, 0.f, 0.f, 0.f};
+        float lse2 = INFINITY, dl = 0.f;
+        if (r < nrows) {
+          const int t = t0 + r;
+          const int qi = off + t;
+          const int seg = a.seg ? a.seg[(int64_t)b * a.seg_sb + t] : 0;
+          const int ls = max(qi - LW + 1, seg);
+          lse2 = a.lse[(int64_t)b * a.lse_sb + (int64_t)t * a.lse_st + (int64_t)hq * a.lse_sh] * kLog2e;
+          dl = p.delta[((int64_t)b * a.T + t) * a.HQ + hq];
+          uint32_t qmem = 0;
+          const int32_t* ids = a.idx + (int64_t)b * a.idx_sb + (int64_t)ih * a.idx_sh + (int64_t)t * a.idx_st;
+          const float* bias = a.bias ? a.bias + (int64_t)b * a.bias_sb + (int64_t)ih * a.bias_sh + (int64_t)t * a.bias_st : nullptr;
+          for (int s = 0; s < S; ++s) {
+            const int id = ids[s];
+            if (id < 0 || id > maxblk) continue;
+#pragma unroll
+            for (int qq = 0; qq < 4; ++qq)
+              if (id == ((j0 + 16 * qq) >> p.bs_shift) && !(qmem & (1u << qq))) {   // first slot wins
+                qmem |= 1u << qq;
+                if (bias) bqv[qq] = bias[s] * kLog2e;
+              }
           }
-          s_row[r] = ri;
-          s_dlt[r] = dl;
+          uint64_t qm = 0;
+#pragma unroll
+          for (int qq = 0; qq < 4; ++qq)
+            if (qmem & (1u << qq)) qm |= 0xffffull << (16 * qq);
+          const uint64_t wm = range64(min(max(ls - j0, 0), 64), min(max(qi + 1 - j0, 0), 64));
+          rm = range64(min(max(seg - j0, 0), 64), min(max(min(ls, qi + 1) - j0, 0), 64)) & qm;
+          keep = wm | rm;
         }
-        for (int e = tid; e < 64 * S; e += NT) {
-          const int r = e / S, s = e % S;
-          int id = -1;
-          float bv = 0.f;
-          if (r < nrows) {
-            id = a.idx[(int64_t)b * a.idx_sb + (int64_t)ih * a.idx_sh + (int64_t)(t0 + r) * a.idx_st + s];
-            if (a.bias) bv = a.bias[(int64_t)b * a.bias_sb + (int64_t)ih * a.bias_sh + (int64_t)(t0 + r) * a.bias_st + s];
-          }
-          s_ids[e] = id;
-          s_bias[e] = bv;
+        s_keep[r] = keep;
+        s_rem[r] = rm;
+        s_lse[r] = lse2;
+        s_dlt[r] = dl;
+#pragma unroll
+        for (int qq = 0; qq < 4; ++qq) s_bq[qq * 64 + r] = bqv[qq];
+        const bool whole = r >= nrows || (keep == ~0ull && (!a.bias || rm == 0ull));
+        const bool all = __all(whole);
+        if (r == 0) s_flag[0] = all ? 1 : 0;
+      }
+      __syncthreads();
+      const bool fast = s_flag[0] != 0;
+      // this key's kept rows (bit = row), by ballots over the rows' masks
+      uint64_t kt = ~0ull, rt = 0ull;
+      if (!fast) {
+        const uint64_t km = s_keep[lane], rmm = s_rem[lane];
+        const int sh = 32 * wave;
+        const uint32_t k32 = (uint32_t)(km >> sh), r32 = (uint32_t)(rmm >> sh);
+#pragma unroll 1
+        for (int k = 0; k < 32; ++k) {
+          const uint64_t bk = __ballot((k32 >> k) & 1u);
+          const uint64_t br = a.bias ? __ballot((r32 >> k) & 1u) : 0ull;
+          if (rl == k) { kt = bk; rt = br; }
         }
-        __syncthreads();
-        // membership of every row in the chunk's blocks (first slot's bias)
-        for (int e = tid; e < 64 * NQ; e += NT) {
-          const int r = e / NQ, qq = e % NQ;
-          float mb = __int_as_float(0x7fc00000);   // NaN: not selected
-          const int blk = blo + qq;
-          if (r < nrows && blk <= bhi) {
-            for (int s = 0; s < S; ++s)
-              if (s_ids[r * S + s] == blk) { mb = s_bias[r * S + s]; break; }
-          }
-          s_mb[e] = mb;
-        }
-        __syncthreads();
+      }
 
-        // S = Q K^T and dP = dO V^T for the 64 rows x this lane's key
-        f32x16_t sp[2] = {zero16(), zero16()}, gd[2] = {zero16(), zero16()};
+      // S = Q K^T and dP = dO V^T: 64 rows x this lane's key
+      f32x16_t sp[2] = {zero16(), zero16()}, gd[2] = {zero16(), zero16()};
 #pragma unroll
-        for (int ks = 0; ks < KS; ++ks) {
-          sp[0] = M::mac(*reinterpret_cast<const uint4*>(sQ + rl * KP + 16 * ks + 8 * h), kf[ks], sp[0]);
-          sp[1] = M::mac(*reinterpret_cast<const uint4*>(sQ + (32 + rl) * KP + 16 * ks + 8 * h), kf[ks], sp[1]);
-          gd[0] = M::mac(*reinterpret_cast<const uint4*>(sG + rl * KP + 16 * ks + 8 * h), vf[ks], gd[0]);
-          gd[1] = M::mac(*reinterpret_cast<const uint4*>(sG + (32 + rl) * KP + 16 * ks + 8 * h), vf[ks], gd[1]);
+      for (int ks = 0; ks < KS; ++ks) {
+#pragma unroll
+        for (int half = 0; half < 2; ++half) {
+          sp[half] = M::mac(*reinterpret_cast<const uint4*>(sQ + (32 * half + rl) * QP + 16 * ks + 8 * h), kf[ks], sp[half]);
+          gd[half] = M::mac(*reinterpret_cast<const uint4*>(sG + (32 * half + rl) * QP + 16 * ks + 8 * h), vf[ks], gd[half]);
         }
-        // in place: sp <- P, gd <- dS
+      }
+      // in place: sp <- P, gd <- dS; register r of half `half` is row 32 half + 8 (r / 4) + 4h + r % 4
+      const uint64_t kth = kt >> (4 * h), rth = rt >> (4 * h);
 #pragma unroll
-        for (int half = 0; half < 2; ++half)
+      for (int half = 0; half < 2; ++half)
 #pragma unroll
-          for (int r = 0; r < 16; ++r) {
-            const int row = 32 * half + d_row(r, h);
-            const int4 ri = s_row[row];
-            const float mb = s_mb[row * NQ + qmine];
-            const bool win = jmine >= ri.y && jmine <= ri.x;
-            const bool rem = !win && jmine >= ri.z && jmine < ri.y && jmine <= ri.x && !(mb != mb);
-            const float sv = sp[half][r];
-            const float pv = (key_ok && (win || rem)) ? exp2f((rem ? sv + mb : sv) * kLog2e - __int_as_float(ri.w)) : 0.f;
+        for (int r4 = 0; r4 < 4; ++r4) {
+          const int row0 = 32 * half + 8 * r4 + 4 * h;
+          const float4 l4 = *reinterpret_cast<const float4*>(s_lse + row0);
+          const float4 d4 = *reinterpret_cast<const float4*>(s_dlt + row0);
+          float4 b4 = make_float4(0.f, 0.f, 0.f, 0.f);
+          if (a.bias && !fast) b4 = *reinterpret_cast<const float4*>(s_bq + myq * 64 + row0);
+          const float lv[4] = {l4.x, l4.y, l4.z, l4.w}, dv4[4] = {d4.x, d4.y, d4.z, d4.w};
+          const float bv[4] = {b4.x, b4.y, b4.z, b4.w};
+#pragma unroll
+          for (int e = 0; e < 4; ++e) {
+            const int r = 4 * r4 + e;
+            const int bit = 32 * half + 8 * r4 + e;
+            float pv;
+            if (fast) {
+              pv = __builtin_amdgcn_exp2f(fmaf(sp[half][r], kLog2e, -lv[e]));
+            } else {
+              const bool remb = (rth >> bit) & 1ull;
+              const float x = fmaf(sp[half][r], kLog2e, (remb ? bv[e] : 0.f) - lv[e]);
+              pv = ((kth >> bit) & 1ull) ? __builtin_amdgcn_exp2f(x) : 0.f;
+            }
+            pv = key_ok ? pv : 0.f;
             sp[half][r] = pv;
-            gd[half][r] = pv * (gd[half][r] - s_dlt[row]);
+            gd[half][r] = pv * (gd[half][r] - dv4[e]);
           }
-        uint4 pb[4], db[4];
+        }
+      uint4 pb[4], db[4];
+#pragma unroll
+      for (int ks = 0; ks < 4; ++ks) {
+        const int hf = ks >> 1, r0 = 8 * (ks & 1);
+        pb[ks] = make_uint4(M::pack2(sp[hf][r0], sp[hf][r0 + 1]), M::pack2(sp[hf][r0 + 2], sp[hf][r0 + 3]),
+                            M::pack2(sp[hf][r0 + 4], sp[hf][r0 + 5]), M::pack2(sp[hf][r0 + 6], sp[hf][r0 + 7]));
+        db[ks] = make_uint4(M::pack2(gd[hf][r0], gd[hf][r0 + 1]), M::pack2(gd[hf][r0 + 2], gd[hf][r0 + 3]),
+                            M::pack2(gd[hf][r0 + 4], gd[hf][r0 + 5]), M::pack2(gd[hf][r0 + 6], gd[hf][r0 + 7]));
+      }
+      // dV^T += dO^T P ; dK^T += (q*scale)^T dS
+#pragma unroll
+      for (int mt = 0; mt < MT; ++mt)
 #pragma unroll
         for (int ks = 0; ks < 4; ++ks) {
-          const int hf = ks >> 1, r0 = 8 * (ks & 1);
-          pb[ks] = make_uint4(M::pack2(sp[hf][r0], sp[hf][r0 + 1]), M::pack2(sp[hf][r0 + 2], sp[hf][r0 + 3]),
-                              M::pack2(sp[hf][r0 + 4], sp[hf][r0 + 5]), M::pack2(sp[hf][r0 + 6], sp[hf][r0 + 7]));
-          db[ks] = make_uint4(M::pack2(gd[hf][r0], gd[hf][r0 + 1]), M::pack2(gd[hf][r0 + 2], gd[hf][r0 + 3]),
-                              M::pack2(gd[hf][r0 + 4], gd[hf][r0 + 5]), M::pack2(gd[hf][r0 + 6], gd[hf][r0 + 7]));
+          dv[mt] = M::mac(a_operand_tr<QP>(g16, 16 * ks, 32 * mt, lane), pb[ks], dv[mt]);
+          dk[mt] = M::mac(a_operand_tr<QP>(q16, 16 * ks, 32 * mt, lane), db[ks], dk[mt]);
         }
-        // dV^T += dO^T P ; dK^T += (q*scale)^T dS  (transposed operands read
-        // column-wise from the natural Q / dO tiles)
-        const uint16_t* g16 = reinterpret_cast<const uint16_t*>(sG);
-        const uint16_t* q16 = reinterpret_cast<const uint16_t*>(sQ);
-#pragma unroll
-        for (int mt = 0; mt < MT; ++mt)
-#pragma unroll
-          for (int ks = 0; ks < 4; ++ks) {
-            dv[mt] = M::mac(a_operand_t<KP>(g16, 32 * mt + rl, ks, h), pb[ks], dv[mt]);
-            dk[mt] = M::mac(a_operand_t<KP>(q16, 32 * mt + rl, ks, h), db[ks], dk[mt]);
-          }
-      }
     }
   }
 
@@ -590,8 +633,22 @@ int check_bwd(const srswa_bwd_args* a) {
     set_error("bwd: matrix-core path takes bf16 / fp16");
     return SRSWA_UNSUPPORTED;
   }
-  if (!(a->D == 64 || a->D == 128) || a->block_size < 16 || a->S > 64) {
-    set_error("bwd: D in {64,128}, block size >= 16, <= 64 slots");
+  if (!(a->D == 64 || a->D == 128) || a->block_size < 16 || (a->block_size & (a->block_size - 1)) || a->S > 64) {
+    set_error("bwd: D in {64,128}, block size a power of two >= 16, <= 64 slots");
+    return SRSWA_UNSUPPORTED;
+  }
+  if (a->dbias && !a->bias) {
+    set_error("bwd: a bias gradient needs the bias");
+    return SRSWA_INVALID;
+  }
+  if (ceil_div(a->Sk, kChunk) > 65536) {
+    set_error("bwd: key length above 4M");
+    return SRSWA_UNSUPPORTED;
+  }
+  const int64_t span = ((int64_t)ceil_div(a->Sk, kChunk) * kChunk * std::max(a->k_st, a->v_st) + a->D) * 2;
+  const int64_t qspan = ((int64_t)ceil_div(a->T, kTileRows) * kTileRows * std::max(a->q_st, a->do_st) + a->D) * 2;
+  if (span >= ((int64_t)1 << 32) || qspan >= ((int64_t)1 << 32)) {
+    set_error("bwd: one sequence's tensors span 4 GiB or more");
     return SRSWA_UNSUPPORTED;
   }
   const int64_t st[] = {a->q_sb, a->q_st, a->q_sh, a->k_sb, a->k_st, a->k_sh, a->v_sb, a->v_st, a->v_sh,
@@ -616,11 +673,26 @@ void plan_bwd(const srswa_bwd_args* a, BwdK& k) {
   k.ntiles = ceil_div(a->T, kTileRows);
   k.nchunk = ceil_div(a->Sk, kChunk);
   k.nwords = ceil_div(k.nchunk, 32);
-  const int per_row = a->S * (ceil_div(a->block_size, kChunk) + 1) + ceil_div(a->local_window, kChunk) + 1;
-  k.umax = (int)std::min<int64_t>((int64_t)k.nchunk, (int64_t)kTileRows * per_row);
+  const int64_t per_tile = (int64_t)kTileRows * a->S * (ceil_div(a->block_size, kChunk) + 1) +
+                           ceil_div(a->local_window + kTileRows - 1, kChunk) + 1;
+  k.umax = (int)std::min<int64_t>((int64_t)k.nchunk, per_tile);
   k.twords = ceil_div(k.ntiles, 32);
+  k.SP = a->S + 1;
+  k.bs_shift = __builtin_ctz((unsigned)std::max(a->block_size, 1));
   k.G = a->HQ / a->HKV;
   k.IG = a->HQ / a->HI;
+  k.nlogical = (int)std::min<int64_t>((int64_t)a->B * a->HQ * k.ntiles, INT32_MAX);
+  k.per_xcd = ceil_div(k.nlogical, 8);
+  k.nlogical_kv = (int)std::min<int64_t>((int64_t)a->B * a->HKV * k.nchunk, INT32_MAX);
+  k.per_xcd_kv = ceil_div(k.nlogical_kv, 8);
+  // dQ LDS: K / V tiles (the set-up arrays alias them), chunk list, sorted ids
+  // (+ bias, + slot map and bias-gradient sums)
+  const size_t tile = a->D == 128 ? DqLds<128>::tileBytes : DqLds<64>::tileBytes;
+  const size_t setup = (3 * 64 + 4) * 4 + (size_t)k.nwords * 4;
+  size_t n = std::max(tile, setup);
+  k.chunks_off = (int)n;
+  n += ((size_t)k.umax * 2 + 15) / 16 * 16;
+  k.sid_off = (int)n;
 }
 
 size_t delta_bytes(const BwdK& k) {
@@ -629,15 +701,12 @@ size_t delta_bytes(const BwdK& k) {
 size_t touch_words(const BwdK& k) { return (size_t)k.a.B * k.a.HI * k.nchunk * k.twords; }
 
 size_t dq_smem(const BwdK& k) {
-  const int D = k.a.D;
-  size_t n = (size_t)kChunk * (D + 8) * 2 * 2 + (size_t)kSlotCap * 64 * 8;
-  n += 3 * 64 * 4 + (size_t)64 * k.a.S * 4 * 3 + (size_t)k.nwords * 4 + (size_t)k.umax * 4 + 16;
+  const size_t n = (size_t)k.sid_off + (size_t)64 * k.SP * 4 * (1 + (k.a.bias ? 1 : 0) + (k.a.dbias ? 2 : 0));
   return (n + 15) / 16 * 16;
 }
 size_t dkv_smem(const BwdK& k) {
-  const int D = k.a.D;
-  size_t n = (size_t)kTileRows * (D + 8) * 2 * 2;
-  n += 64 * 16 + 64 * 4 + 64 * 5 * 4 + (size_t)64 * k.a.S * 4 * 2 + (size_t)k.ntiles * 4 + 16;
+  const size_t tile = k.a.D == 128 ? DkvLds<128>::tileBytes : DkvLds<64>::tileBytes;
+  const size_t n = tile + 64 * 4 * 2 + 64 * 8 * 2 + 4 * 64 * 4 + 16 + (size_t)k.ntiles * 4;
   return (n + 15) / 16 * 16;
 }
 
@@ -655,10 +724,8 @@ int launch_bwd(const BwdK& k, hipStream_t st) {
   if (nw > 0) hipLaunchKernelGGL(zero_words_kernel, dim3((unsigned)((nw + 255) / 256)), dim3(256), 0, st, k.touch, nw);
   const int64_t ne = (int64_t)a.B * a.HI * a.T * a.S;
   if (ne > 0) hipLaunchKernelGGL(touch_kernel, dim3((unsigned)((ne + 255) / 256)), dim3(256), 0, st, k);
-  hipLaunchKernelGGL((dq_kernel<T, D>), dim3((unsigned)((int64_t)a.B * a.HQ * k.ntiles)), dim3(128),
-                     dq_smem(k), st, k);
-  hipLaunchKernelGGL((dkv_kernel<T, D>), dim3((unsigned)((int64_t)a.B * a.HKV * k.nchunk)), dim3(128),
-                     dkv_smem(k), st, k);
+  hipLaunchKernelGGL((dq_kernel<T, D>), dim3((unsigned)(8 * k.per_xcd)), dim3(128), dq_smem(k), st, k);
+  hipLaunchKernelGGL((dkv_kernel<T, D>), dim3((unsigned)(8 * k.per_xcd_kv)), dim3(128), dkv_smem(k), st, k);
   const hipError_t e = hipGetLastError();
   if (e != hipSuccess) {
     set_error("bwd launch failed: %s", hipGetErrorString(e));

@@ -181,10 +181,12 @@ constexpr int kIdEnd = 0x7fffffff;   // sentinel closing a row's sorted id list
 
 // One row's selected blocks, as the kernels walk them: the valid ids that hold
 // at least one remote key of the row (seg <= j < ls, j <= qi), ascending, a
-// repeated id kept once with its first slot's bias, then kIdEnd padding up to
-// SP = S + 1 entries (so a cursor never runs past the list).
+// repeated id kept once with its first slot's bias (and, when sslot is given,
+// that slot's index), then kIdEnd padding up to SP = S + 1 entries (so a
+// cursor never runs past the list).
 __device__ inline void sort_row_ids(const int32_t* ids, const float* bias, int S, int SP, int BS,
-                                    int maxblk, int qi, int seg, int ls, int* sid, float* sb) {
+                                    int maxblk, int qi, int seg, int ls, int* sid, float* sb,
+                                    int* sslot = nullptr) {
   int n = 0;
   for (int s = 0; s < S; ++s) {
     const int id = ids[s];
@@ -199,13 +201,74 @@ __device__ inline void sort_row_ids(const int32_t* ids, const float* bias, int S
     while (i > 0 && sid[i - 1] > id) {
       sid[i] = sid[i - 1];
       if (sb) sb[i] = sb[i - 1];
+      if (sslot) sslot[i] = sslot[i - 1];
       --i;
     }
     sid[i] = id;
     if (sb) sb[i] = bv;
+    if (sslot) sslot[i] = s;
     ++n;
   }
-  for (int i = n; i < SP; ++i) sid[i] = kIdEnd;
+  for (int i = n; i < SP; ++i) {
+    sid[i] = kIdEnd;
+    if (sslot) sslot[i] = -1;
+  }
+}
+
+// One row's walk over its sorted selected blocks, chunk by chunk (ascending).
+struct RowWalk {
+  const int* sid;      // sorted ids (kIdEnd-terminated)
+  const float* sb;     // their bias (nullptr: no bias)
+  int cur, nid;        // cursor and the id under it
+  int ls, seg, hi, rem_hi;   // window [ls, hi), remote candidates [seg, rem_hi)
+  bool ok;
+};
+
+// The row's keep mask over a chunk's 64 keys (bit k = key j0 + k), its remote
+// part, the bias (log2 units) of each 16-key quarter and the sorted index of
+// the block covering each quarter (-1: not selected).  Block sizes are powers
+// of two >= 16, so a quarter never straddles two blocks.  Returns whether the
+// row keeps the whole chunk with one bias for every key.
+__device__ __forceinline__ bool chunk_mask(RowWalk& w, int j0, int bs_shift, bool blk64, uint64_t& keep,
+                                           uint64_t& rm, float bq[4], int qix[4]) {
+  uint32_t qmem = 0;
+#pragma unroll
+  for (int qq = 0; qq < 4; ++qq) {
+    bq[qq] = 0.f;
+    qix[qq] = -1;
+  }
+  if (blk64) {
+    const int blk = j0 >> bs_shift;
+    while (w.nid < blk) w.nid = w.sid[++w.cur];
+    if (w.nid == blk) {
+      qmem = 15u;
+      const float bv = w.sb ? w.sb[w.cur] * kLog2e : 0.f;
+#pragma unroll
+      for (int qq = 0; qq < 4; ++qq) {
+        bq[qq] = bv;
+        qix[qq] = w.cur;
+      }
+    }
+  } else {
+#pragma unroll
+    for (int qq = 0; qq < 4; ++qq) {
+      const int blk = (j0 + 16 * qq) >> bs_shift;
+      while (w.nid < blk) w.nid = w.sid[++w.cur];
+      if (w.nid == blk) {
+        qmem |= 1u << qq;
+        if (w.sb) bq[qq] = w.sb[w.cur] * kLog2e;
+        qix[qq] = w.cur;
+      }
+    }
+  }
+  uint64_t qm = 0;
+#pragma unroll
+  for (int qq = 0; qq < 4; ++qq)
+    if (qmem & (1u << qq)) qm |= 0xffffull << (16 * qq);
+  const uint64_t wm = range64(min(max(w.ls - j0, 0), 64), min(max(w.hi - j0, 0), 64));
+  rm = range64(min(max(w.seg - j0, 0), 64), min(max(w.rem_hi - j0, 0), 64)) & qm;
+  keep = wm | rm;
+  return !w.ok || (keep == ~0ull && (!w.sb || rm == 0ull || (rm == ~0ull && blk64)));
 }
 
 // Sorted list of the 64-key chunks a tile visits, from the rows' windows
