@@ -339,6 +339,8 @@ __global__ __launch_bounds__(128, D == 128 ? 1 : 2) void dq_kernel(BwdK p) {
 }
 
 // -------------------------------------------------------------- 4. dK / dV
+constexpr int kPreSlots = 8;          // selected ids per row fetched one visit ahead
+
 template <int D> struct DkvLds {
   static constexpr int QP = D + 16;   // Q / dO tiles: row reads and transposing reads
   static constexpr int gOff = kTileRows * QP * 2;
@@ -457,7 +459,29 @@ __global__ __launch_bounds__(128, 1) void dkv_kernel(BwdK p) {
         gpre[i] = buffer_load16(grs, gvo, gso + (uint32_t)(i * RPP) * (uint32_t)a.do_st * 2u);
       }
     };
-    if (nt > 0) fetch(s_tiles[0]);
+    // row data of a tile for wave 0 (lane = row): sample start, lse (log2
+    // units, +inf past T), delta and the first kPreSlots selected ids / biases
+    int pf_seg = 0, pf_id[kPreSlots];
+    float pf_lse = INFINITY, pf_dlt = 0.f, pf_b[kPreSlots];
+    auto rfetch = [&](int tau) {
+      const int t = tau * kTileRows + tid;
+      const bool valid = t < a.T;
+      const int tt = valid ? t : 0;
+      pf_seg = (valid && a.seg) ? a.seg[(int64_t)b * a.seg_sb + tt] : 0;
+      pf_lse = valid ? a.lse[(int64_t)b * a.lse_sb + (int64_t)tt * a.lse_st + (int64_t)hq * a.lse_sh] * kLog2e : INFINITY;
+      pf_dlt = valid ? p.delta[((int64_t)b * a.T + tt) * a.HQ + hq] : 0.f;
+      const int32_t* ids = a.idx + (int64_t)b * a.idx_sb + (int64_t)ih * a.idx_sh + (int64_t)tt * a.idx_st;
+      const float* bias = a.bias ? a.bias + (int64_t)b * a.bias_sb + (int64_t)ih * a.bias_sh + (int64_t)tt * a.bias_st : nullptr;
+#pragma unroll
+      for (int s = 0; s < kPreSlots; ++s) {
+        pf_id[s] = (valid && s < S) ? ids[s] : -1;
+        pf_b[s] = (valid && s < S && bias) ? bias[s] : 0.f;
+      }
+    };
+    if (nt > 0) {
+      fetch(s_tiles[0]);
+      if (tid < 64) rfetch(s_tiles[0]);
+    }
     for (int it = 0; it < nt; ++it) {
       const int tau = s_tiles[it];
       const int t0 = tau * kTileRows;
@@ -473,31 +497,33 @@ __global__ __launch_bounds__(128, 1) void dkv_kernel(BwdK p) {
         *reinterpret_cast<uint4*>(sGw + i * RPP * QP) = gpre[i];
       }
       if (it + 1 < nt) fetch(s_tiles[it + 1]);
-      // wave 0: every row's keep mask over the chunk's keys
+      // wave 0: every row's keep mask over the chunk's keys, from the row data
+      // fetched one visit ahead (slots past the first kPreSlots load here)
       if (tid < 64) {
         const int r = tid;
         uint64_t keep = 0ull, rm = 0ull;
         float bqv[4] = {0.f, 0.f, 0.f, 0.f};
-        float lse2 = INFINITY, dl = 0.f;
         if (r < nrows) {
           const int t = t0 + r;
           const int qi = off + t;
-          const int seg = a.seg ? a.seg[(int64_t)b * a.seg_sb + t] : 0;
+          const int seg = pf_seg;
           const int ls = max(qi - LW + 1, seg);
-          lse2 = a.lse[(int64_t)b * a.lse_sb + (int64_t)t * a.lse_st + (int64_t)hq * a.lse_sh] * kLog2e;
-          dl = p.delta[((int64_t)b * a.T + t) * a.HQ + hq];
           uint32_t qmem = 0;
-          const int32_t* ids = a.idx + (int64_t)b * a.idx_sb + (int64_t)ih * a.idx_sh + (int64_t)t * a.idx_st;
-          const float* bias = a.bias ? a.bias + (int64_t)b * a.bias_sb + (int64_t)ih * a.bias_sh + (int64_t)t * a.bias_st : nullptr;
-          for (int s = 0; s < S; ++s) {
-            const int id = ids[s];
-            if (id < 0 || id > maxblk) continue;
+          auto take = [&](int s, int id, float bv) {
+            if (id < 0 || id > maxblk) return;
 #pragma unroll
             for (int qq = 0; qq < 4; ++qq)
               if (id == ((j0 + 16 * qq) >> p.bs_shift) && !(qmem & (1u << qq))) {   // first slot wins
                 qmem |= 1u << qq;
-                if (bias) bqv[qq] = bias[s] * kLog2e;
+                bqv[qq] = bv * kLog2e;
               }
+          };
+#pragma unroll
+          for (int s = 0; s < kPreSlots; ++s) take(s, pf_id[s], pf_b[s]);
+          if (S > kPreSlots) {
+            const int32_t* ids = a.idx + (int64_t)b * a.idx_sb + (int64_t)ih * a.idx_sh + (int64_t)t * a.idx_st;
+            const float* bias = a.bias ? a.bias + (int64_t)b * a.bias_sb + (int64_t)ih * a.bias_sh + (int64_t)t * a.bias_st : nullptr;
+            for (int s = kPreSlots; s < S; ++s) take(s, ids[s], bias ? bias[s] : 0.f);
           }
           uint64_t qm = 0;
 #pragma unroll
@@ -509,13 +535,14 @@ __global__ __launch_bounds__(128, 1) void dkv_kernel(BwdK p) {
         }
         s_keep[r] = keep;
         s_rem[r] = rm;
-        s_lse[r] = lse2;
-        s_dlt[r] = dl;
+        s_lse[r] = pf_lse;
+        s_dlt[r] = pf_dlt;
 #pragma unroll
         for (int qq = 0; qq < 4; ++qq) s_bq[qq * 64 + r] = bqv[qq];
         const bool whole = r >= nrows || (keep == ~0ull && (!a.bias || rm == 0ull));
         const bool all = __all(whole);
         if (r == 0) s_flag[0] = all ? 1 : 0;
+        if (it + 1 < nt) rfetch(s_tiles[it + 1]);
       }
       __syncthreads();
       const bool fast = s_flag[0] != 0;
