@@ -213,6 +213,33 @@ typedef struct {
 
 int srswa_block_max_score(const srswa_blockmax_args* a, void* stream);
 
+/* ------------------------------------------------------------------------
+ * DASH router: block scores -> selected blocks + bias for the gather kernels.
+ * Replaces _infer_route_select (HF/modeling_deepseekv2.py:338-362; vLLM
+ * DashRouterMath.route_and_select with budget_topk=True, the DASH decode and
+ * prefill selection of HF/modeling_deepseekv2.py:535-546):
+ *   cand   = remote & block_cand (remote = score > -5e8), or every remote
+ *            block when that set is empty; x = cand ? score * idx_scale : -1e4
+ *            (NaN / inf -> -1e4)
+ *   top-M window of x (descending, equal x -> lower block id),
+ *   1.5-entmax prior over the M values, the first K of them:
+ *   topi = block ids, valid = cand, bias = valid ? (log(max(prior, floor)) - mu)
+ *   / sigma : 0 with mu the mean log-prior over the valid slots.
+ * M = topm > 0 ? min(topm, nblk) : nblk must be <= 64; K is clamped to [1, M].
+ * ---------------------------------------------------------------------- */
+typedef struct {
+  const float* scores;  int64_t sc_sb, sc_sq;          /* [B, Lq, nblk] fp32, block stride 1 */
+  const uint8_t* cand;  int64_t cd_sb, cd_sq;          /* [B, Lq, nblk] bool; NULL = all remote */
+  int32_t* topi;        int64_t ti_sb, ti_sq;          /* [B, Lq, K] int32                     */
+  float* bias;          int64_t bi_sb, bi_sq;          /* [B, Lq, K] fp32                      */
+  uint8_t* valid;       int64_t va_sb, va_sq;          /* [B, Lq, K] bool                      */
+  int32_t B, Lq, nblk, K, topm;
+  float idx_scale, floor;
+  double sigma;
+} srswa_route_args;
+
+int srswa_dash_route(const srswa_route_args* a, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -96,9 +96,32 @@ def blockmax_case():
                 nblk=nblk, out=out.numpy())
 
 
+def router_case():
+    """DASH router: shipped parameters (K 12, top-M 16, sigma 1, floor 1e-4), a
+    page mask with one row whose masked set is empty (fallback to every remote
+    block), equal scores (tie order), a short row (nblk < M) in its own case."""
+    g = torch.Generator().manual_seed(105)
+    B, Lq, nblk = 2, 5, 90
+    sc = (torch.randn(B, Lq, nblk, generator=g) * 0.3).float()
+    sc[..., 80:] = O.SCORE_NEG                          # local / future blocks
+    sc[0, 1, 10:20] = 0.5                               # ties
+    sc[1, 2, 5] = float("nan")
+    cand = torch.rand(B, Lq, nblk, generator=g) > 0.4
+    cand[1, 3] = False                                  # empty candidate set -> fallback
+    idx_scale, floor, sigma, K, topm = 128.0 / math.sqrt(128), 1e-4, 1.0, 12, 16
+    xi, bias, valid = O.infer_route_select(sc, cand, idx_scale, floor, sigma, K, topm)
+    sc2 = sc[:, :, :10].clone()
+    sc2[..., 7:] = O.SCORE_NEG
+    xi2, bias2, valid2 = O.infer_route_select(sc2, None, idx_scale, floor, sigma, K, topm)
+    return dict(scores=sc.numpy(), cand=cand.numpy(), idx_scale=idx_scale, floor=floor, sigma=sigma, K=K,
+                topm=topm, topi=xi.numpy(), bias=bias.numpy(), valid=valid.numpy(),
+                scores_short=sc2.numpy(), topi_short=xi2.numpy(), bias_short=bias2.numpy(),
+                valid_short=valid2.numpy())
+
+
 def main():
     for name, fn in (("decode", decode_case), ("gather", gather_case), ("indexer", indexer_case),
-                     ("blockmax", blockmax_case)):
+                     ("blockmax", blockmax_case), ("router", router_case)):
         d = fn()
         path = os.path.join(HERE, f"{name}.npz")
         np.savez_compressed(path, **{k: np.asarray(v) for k, v in d.items()})

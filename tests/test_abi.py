@@ -23,7 +23,12 @@ def _declared_functions():
     return set(re.findall(r"^\s*(?:const\s+)?[\w\s\*]*?\b(srswa_\w+)\s*\(", _header_text(), flags=re.M))
 
 
+_CTYPES = {"int64_t": ctypes.c_int64, "int32_t": ctypes.c_int32, "float": ctypes.c_float,
+           "double": ctypes.c_double}
+
+
 def _declared_structs():
+    """{struct name: [(field, ctypes type), ...]} from the header (pointers -> c_void_p)."""
     out = {}
     for body, name in re.findall(r"typedef\s+struct\s*\{(.*?)\}\s*(\w+)\s*;", _header_text(), flags=re.S):
         fields = []
@@ -31,9 +36,12 @@ def _declared_structs():
             decl = decl.strip()
             if not decl:
                 continue
-            m = re.match(r"(const\s+)?([\w]+)\s*(\**)\s*(.*)", decl)
-            names = [n.strip().lstrip("*").strip() for n in m.group(4).split(",")]
-            fields += names
+            m = re.match(r"(const\s+)?([\w]+)\s*(.*)", decl)
+            base = m.group(2)
+            for n in m.group(3).split(","):
+                n = n.strip()
+                ty = ctypes.c_void_p if n.startswith("*") else _CTYPES[base]
+                fields.append((n.lstrip("*").strip(), ty))
         out[name] = fields
     return out
 
@@ -52,7 +60,7 @@ def test_ctypes_structs_match_header():
     structs = _declared_structs()
     assert set(structs) == set(_lib.STRUCTS), set(structs) ^ set(_lib.STRUCTS)
     for cname, fields in structs.items():
-        py = [f[0] for f in _lib.STRUCTS[cname]._fields_]
+        py = [(f[0], f[1]) for f in _lib.STRUCTS[cname]._fields_]
         assert py == fields, (cname, py, fields)
 
 

@@ -34,6 +34,10 @@ def test_oracle_reproduces_fixtures():
     out = O.block_max_scores(b["q"].double(), b["k"].double(), b["pos"], b["seg"], b["block_size"], b["nblk"],
                              b["local_window"])
     assert torch.equal(torch.isfinite(out), torch.isfinite(b["out"]))
+    r = load("router")
+    xi, bias, valid = O.infer_route_select(r["scores"], r["cand"], r["idx_scale"], r["floor"], r["sigma"],
+                                           r["K"], r["topm"])
+    assert torch.equal(xi, r["topi"]) and torch.equal(valid, r["valid"]) and torch.equal(bias, r["bias"])
 
 
 @pytest.mark.gpu
@@ -82,3 +86,11 @@ def test_kernels_match_fixtures(dev):
     fin = torch.isfinite(b["out"])
     assert torch.equal(torch.isfinite(got), fin)
     assert (got[fin] - b["out"][fin]).abs().max().item() <= 1e-3 * max(1.0, b["out"][fin].abs().max().item())
+
+    r = load("router")
+    p = dict(idx_scale=r["idx_scale"], floor=r["floor"], sigma=r["sigma"], K=r["K"], topm=r["topm"])
+    for sfx, cand in (("", r["cand"].to(dev)), ("_short", None)):
+        xi, bias, valid = ops.dash_route(r["scores" + sfx].to(dev), cand, p)
+        assert torch.equal(xi.cpu(), r["topi" + sfx]) and torch.equal(valid.cpu(), r["valid" + sfx])
+        ref = r["bias" + sfx]
+        assert ((bias.cpu() - ref).abs() <= 1e-5 * ref.abs().clamp(min=1.0)).all()

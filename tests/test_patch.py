@@ -25,19 +25,26 @@ def _fake_module():
         calls.append("scores")
         return "eager-scores"
 
-    return types.SimpleNamespace(_decode_attend=_decode_attend, _block_scores_infer=_block_scores_infer), calls
+    def _infer_route_select(*args):
+        calls.append("route")
+        return "eager-route"
+
+    return types.SimpleNamespace(_decode_attend=_decode_attend, _block_scores_infer=_block_scores_infer,
+                                 _infer_route_select=_infer_route_select), calls
 
 
 def test_apply_restore_and_host_fallback():
     mod, calls = _fake_module()
     orig = mod._decode_attend
-    assert patch.apply(mod) == ["_decode_attend", "_block_scores_infer"]
-    assert patch.apply(mod) == ["_decode_attend", "_block_scores_infer"]     # idempotent
+    names = ["_decode_attend", "_block_scores_infer", "_infer_route_select"]
+    assert patch.apply(mod) == names
+    assert patch.apply(mod) == names     # idempotent
     q = torch.zeros(1, 1, 1, 8)
     assert mod._decode_attend(q, q, q, None, None, None, None, 8, 8, 1.0) == "eager-decode"
     router = types.SimpleNamespace(stage0="head_cls")
     assert mod._block_scores_infer(router, q, q, None, 4) == "eager-scores"
-    assert calls == ["decode", "scores"]
+    assert mod._infer_route_select(torch.zeros(1, 1, 4), None, {}) == "eager-route"
+    assert calls == ["decode", "scores", "route"]
     patch.restore(mod)
     assert mod._decode_attend is orig
 
@@ -73,4 +80,10 @@ def test_patched_functions_on_device(dev):
     valid_b = ref > O.SCORE_NEG * 0.5
     assert torch.equal(sc > O.SCORE_NEG * 0.5, valid_b)
     assert (sc[valid_b] - ref[valid_b]).abs().max().item() <= 1e-4
+    # router on those scores (shipped parameters)
+    p = dict(idx_scale=128.0 / math.sqrt(d), floor=1e-4, sigma=1.0, K=12, topm=16)
+    xi, rb, rv = mod._infer_route_select(sc.to(dev), None, p)
+    ox, ob, ov = O.infer_route_select(sc, None, p["idx_scale"], p["floor"], p["sigma"], p["K"], p["topm"])
+    assert torch.equal(xi.cpu(), ox) and torch.equal(rv.cpu(), ov)
+    assert ((rb.cpu() - ob).abs() <= 1e-5 * ob.abs().clamp(min=1.0)).all()
     assert calls == []

@@ -131,6 +131,21 @@ class BlockMaxArgs(ctypes.Structure):
     ]
 
 
+class RouteArgs(ctypes.Structure):
+    """Mirror of ``srswa_route_args``."""
+
+    _fields_ = [
+        ("scores", _vp), ("sc_sb", _i64), ("sc_sq", _i64),
+        ("cand", _vp), ("cd_sb", _i64), ("cd_sq", _i64),
+        ("topi", _vp), ("ti_sb", _i64), ("ti_sq", _i64),
+        ("bias", _vp), ("bi_sb", _i64), ("bi_sq", _i64),
+        ("valid", _vp), ("va_sb", _i64), ("va_sq", _i64),
+        ("B", _i32), ("Lq", _i32), ("nblk", _i32), ("K", _i32), ("topm", _i32),
+        ("idx_scale", ctypes.c_float), ("floor", ctypes.c_float),
+        ("sigma", ctypes.c_double),
+    ]
+
+
 # name -> (restype, argtypes) of every exported entry point
 SIGNATURES = {
     "srswa_version": (ctypes.c_int, []),
@@ -146,11 +161,12 @@ SIGNATURES = {
     "srswa_gather_bwd_workspace": (ctypes.c_size_t, [ctypes.POINTER(BwdArgs)]),
     "srswa_gather_bwd": (ctypes.c_int, [ctypes.POINTER(BwdArgs), _vp, ctypes.c_size_t, _vp]),
     "srswa_block_max_score": (ctypes.c_int, [ctypes.POINTER(BlockMaxArgs), _vp]),
+    "srswa_dash_route": (ctypes.c_int, [ctypes.POINTER(RouteArgs), _vp]),
 }
 
 STRUCTS = {"srswa_decode_args": DecodeArgs, "srswa_index_args": IndexArgs,
            "srswa_fwd_args": FwdArgs, "srswa_bwd_args": BwdArgs,
-           "srswa_blockmax_args": BlockMaxArgs}
+           "srswa_blockmax_args": BlockMaxArgs, "srswa_route_args": RouteArgs}
 
 _lib = None
 _lock = threading.Lock()

@@ -270,6 +270,45 @@ def topk_rows(scores, k, *, invalid_at=SCORE_NEG * 0.5, ascending=False, return_
 
 
 # ---------------------------------------------------------------------------
+# DASH router
+# ---------------------------------------------------------------------------
+def dash_route(block_scores, block_cand, p):
+    """``_infer_route_select`` (HF/modeling_deepseekv2.py:338-362) on the GPU.
+
+    block_scores [B, Lq, nblk] fp32 (``SCORE_NEG`` = not a remote block);
+    block_cand [B, Lq, nblk] bool page mask or None; ``p`` the router's
+    ``_infer_params`` dict (idx_scale, floor, sigma, K, topm).  Returns
+    (topi [B, Lq, K] int64, bias [B, Lq, K] fp32, valid [B, Lq, K] bool).
+    Raises ``UnsupportedShape`` for a top-M window above 64 blocks."""
+    _require_cuda(block_scores, block_cand)
+    B, Lq, nblk = block_scores.shape
+    sc = block_scores.to(torch.float32)
+    if sc.stride(-1) != 1:
+        sc = sc.contiguous()
+    cd = None
+    if block_cand is not None:
+        cd = block_cand.to(torch.bool).expand(B, Lq, nblk)
+        if cd.stride(-1) != 1:
+            cd = cd.contiguous()
+        cd = cd.view(torch.uint8)
+    M = max(1, min(int(p["topm"]), nblk)) if int(p["topm"]) > 0 else nblk
+    K = max(1, min(int(p["K"]), M))
+    topi = torch.empty(B, Lq, K, dtype=torch.int32, device=sc.device)
+    bias = torch.empty(B, Lq, K, dtype=torch.float32, device=sc.device)
+    valid = torch.empty(B, Lq, K, dtype=torch.bool, device=sc.device)
+    a = _lib.RouteArgs(
+        scores=sc.data_ptr(), sc_sb=sc.stride(0), sc_sq=sc.stride(1),
+        cand=_lib.ptr(cd), cd_sb=cd.stride(0) if cd is not None else 0, cd_sq=cd.stride(1) if cd is not None else 0,
+        topi=topi.data_ptr(), ti_sb=topi.stride(0), ti_sq=topi.stride(1),
+        bias=bias.data_ptr(), bi_sb=bias.stride(0), bi_sq=bias.stride(1),
+        valid=valid.data_ptr(), va_sb=valid.stride(0), va_sq=valid.stride(1),
+        B=B, Lq=Lq, nblk=nblk, K=int(p["K"]), topm=int(p["topm"]),
+        idx_scale=float(p["idx_scale"]), floor=float(p["floor"]), sigma=float(p["sigma"]))
+    _lib.check(_lib.lib().srswa_dash_route(ctypes.byref(a), _lib.stream_ptr(sc.device)), "srswa_dash_route")
+    return topi.to(torch.int64), bias, valid
+
+
+# ---------------------------------------------------------------------------
 # gather-attention forward (matrix cores)
 # ---------------------------------------------------------------------------
 def _seg_from_positions(position_ids, T, Sk, device):

@@ -9,6 +9,7 @@ two kernel files (those are replaced file-for-file by
 * ``_decode_attend``       (HF/modeling_deepseekv2.py:454-481) -> ``srswa.ops.decode_attend``
 * ``_block_scores_infer``  (HF/modeling_deepseekv2.py:380-430), stage0 "head_cls"
                            -> the head_cls / mean-pool indexer kernel
+* ``_infer_route_select``  (HF/modeling_deepseekv2.py:338-362) -> ``srswa.ops.dash_route``
 
 Every replacement keeps the reference signature and return convention, runs
 the HIP kernels for device tensors, and hands host tensors (or a case the
@@ -76,6 +77,21 @@ def apply(modeling_deepseekv2) -> list:
 
         mod._block_scores_infer = _block_scores_infer
         done.append("_block_scores_infer")
+
+    orig_route = getattr(mod, "_srswa_orig_infer_route_select", None) or getattr(mod, "_infer_route_select", None)
+    if orig_route is not None:
+        mod._srswa_orig_infer_route_select = orig_route
+
+        def _infer_route_select(block_scores, block_cand, p):
+            if block_scores.is_cuda:
+                try:
+                    return ops.dash_route(block_scores, block_cand, p)
+                except UnsupportedShape:
+                    pass
+            return orig_route(block_scores, block_cand, p)
+
+        mod._infer_route_select = _infer_route_select
+        done.append("_infer_route_select")
     return done
 
 
@@ -88,3 +104,6 @@ def restore(modeling_deepseekv2) -> None:
     if hasattr(mod, "_srswa_orig_block_scores_infer"):
         mod._block_scores_infer = mod._srswa_orig_block_scores_infer
         del mod._srswa_orig_block_scores_infer
+    if hasattr(mod, "_srswa_orig_infer_route_select"):
+        mod._infer_route_select = mod._srswa_orig_infer_route_select
+        del mod._srswa_orig_infer_route_select
