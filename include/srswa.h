@@ -214,6 +214,37 @@ typedef struct {
 int srswa_block_max_score(const srswa_blockmax_args* a, void* stream);
 
 /* ------------------------------------------------------------------------
+ * Paged decode gather-attention (the serving cache layout).  Replaces
+ * dash_sparse_attn_decode (WHL!layers/attention/unlimited_dash_ops/
+ * attend_triton.py:600-715: kernel :307-518, split-K merge common.py:44-89).
+ * One KV page holds one block (page_size == block size, a power of two).
+ * Request r has seq_lens[r] cached tokens and dql decode queries at positions
+ * seq_lens[r] - dql + i; query row n = r * dql + i.  Per (row, kv head):
+ *   window  keys [max(pos - local_blocks*page_size + 1, 0), pos], no bias
+ *   remote  keys of the listed blocks below the window start, + bias
+ * topk holds logical block ids per kv head (-1 = empty; a repeated id counts
+ * once); block_table maps a request's logical block to its page.
+ * ---------------------------------------------------------------------- */
+typedef struct {
+  const void* q;        int64_t q_sn, q_sh;            /* [total_q, HQ, D]                  */
+  const void* k_cache;  int64_t k_sp, k_st, k_sh;      /* [num_pages, page_size, HKV, D]    */
+  const void* v_cache;  int64_t v_sp, v_st, v_sh;      /* [num_pages, page_size, HKV, D]    */
+  const int32_t* topk;  int64_t t_sh, t_sn, t_sk;      /* [HKV, total_q, topk_n] block ids  */
+  const float* bias;                                   /* same strides as topk; NULL = 0    */
+  const int32_t* block_table; int64_t bt_sr;           /* [R, max_blocks] page ids          */
+  const int32_t* seq_lens;                             /* [R]                               */
+  void* out;            int64_t o_sn, o_sh;            /* [total_q, HQ, D]                  */
+  int32_t R, dql, HQ, HKV, D, topk_n, max_blocks, page_size, local_blocks;
+  float scale;
+  int32_t in_dtype, out_dtype;
+} srswa_paged_decode_args;
+
+void srswa_gather_decode_paged_workspace(const srswa_paged_decode_args* a, size_t* scratch_bytes,
+                                         size_t* counters);
+int srswa_gather_decode_paged(const srswa_paged_decode_args* a, void* scratch, size_t scratch_bytes,
+                              uint32_t* counters, size_t n_counters, void* stream);
+
+/* ------------------------------------------------------------------------
  * DASH router: block scores -> selected blocks + bias for the gather kernels.
  * Replaces _infer_route_select (HF/modeling_deepseekv2.py:338-362; vLLM
  * DashRouterMath.route_and_select with budget_topk=True, the DASH decode and

@@ -241,6 +241,43 @@ def decode_attend(q, k_all, v_all, topi, bias, valid, q_pos, block_size, local_w
     return torch.matmul(torch.softmax(s, dim=-1), vv)
 
 
+def paged_decode_attend(q, k_cache, v_cache, topk, bias, block_table, seq_lens, dql, local_blocks, scale):
+    """The serving decode over a paged cache: ``dash_sparse_attn_decode``
+    (WHL!layers/attention/unlimited_dash_ops/attend_triton.py:307-518, 600-715).
+
+    q [R*dql, H, D]; k_cache, v_cache [num_pages, page, Hkv, D] (one page per
+    block); topk / bias [Hkv, R*dql, K] (per kv head; -1 = empty); block_table
+    [R, max_blocks]; seq_lens [R].  Query i of request r sits at
+    ``seq_lens[r] - dql + i``; window = the last ``local_blocks * page`` keys up
+    to it, unbiased; remote = keys of the listed blocks below the window.  The
+    same attention as ``decode_attend`` on the request's cache gathered page by
+    page (a repeated id counts once, as there).  Returns [R*dql, H, D]."""
+    R = block_table.shape[0]
+    page = k_cache.shape[1]
+    Hkv, H, D = k_cache.shape[2], q.shape[1], q.shape[2]
+    nb = block_table.shape[1]
+    out = []
+    for r in range(R):
+        pages = block_table[r].long()
+        kr = k_cache[pages].reshape(nb * page, Hkv, D).transpose(0, 1)[None]       # [1,Hkv,S,D]
+        vr = v_cache[pages].reshape(nb * page, Hkv, v_cache.shape[-1]).transpose(0, 1)[None]
+        L = int(seq_lens[r])
+        kr, vr = kr[:, :, :L], vr[:, :, :L]
+        rows = slice(r * dql, (r + 1) * dql)
+        qr = q[rows].transpose(0, 1)[None]                                           # [1,H,dql,D]
+        ti = topk[:, rows].long()[None]                                              # [1,Hkv,dql,K]
+        ti = ti.masked_fill(ti >= -(-L // page), -1)     # blocks past seq_len hold no key (pos < kv_len)
+        bi = bias[:, rows][None] if bias is not None else torch.zeros(ti.shape, dtype=torch.float64)
+        valid = ti >= 0
+        q_pos = (L - dql + torch.arange(dql))[None]
+        o = decode_attend(qr, kr, vr, ti, bi, valid, q_pos, page, local_blocks * page, scale)
+        # a row with no key at all (no window, nothing selected) is 0, not NaN:
+        # attend_triton.py:495-497 scales by 0 when its lse stays -inf
+        o = torch.nan_to_num(o, nan=0.0)
+        out.append(o[0].transpose(0, 1))                                             # [dql,H,D]
+    return torch.cat(out, 0)
+
+
 def decode_attend_gather(q, k_cache, v_cache, block_idx, q_pos, block_size, local_window,
                          scale, bias=None):
     """Gather-form decode for caches too large for the dense form.

@@ -398,3 +398,70 @@ def test_route_select_bias_is_mean_centred():
     m = (bias * valid).sum(-1) / valid.sum(-1)
     assert m.abs().max() < 1e-5
     assert (xi[valid] < 15).all()
+
+
+# ------------------------------------------------------- paged decode (serving layout)
+def _paged_brute(q, kc, vc, topk, bias, bt, sl, dql, lb, scale):
+    """Key-by-key loop over attend_triton.py:307-518's two passes."""
+    page = kc.shape[1]
+    H, Hkv = q.shape[1], kc.shape[2]
+    out = torch.zeros(q.shape, dtype=torch.float64)
+    for n in range(q.shape[0]):
+        r, i = n // dql, n % dql
+        pos = int(sl[r]) - dql + i
+        lws = max(0, pos - lb * page + 1)
+        for h in range(H):
+            kh = h // (H // Hkv)
+            logits, vals = [], []
+            seen = set()
+            for s_ in range(topk.shape[-1]):
+                blk = int(topk[kh, n, s_])
+                if blk < 0 or blk in seen:
+                    continue
+                seen.add(blk)
+                for j in range(blk * page, blk * page + page):
+                    if j < pos + 1 and j < lws:
+                        pg, off = int(bt[r, j // page]), j % page
+                        logits.append(float(q[n, h] @ kc[pg, off, kh]) * scale + float(bias[kh, n, s_]))
+                        vals.append(vc[pg, off, kh])
+            if lb > 0:
+                for j in range(lws, pos + 1):
+                    pg, off = int(bt[r, j // page]), j % page
+                    logits.append(float(q[n, h] @ kc[pg, off, kh]) * scale)
+                    vals.append(vc[pg, off, kh])
+            if logits:
+                w = torch.softmax(torch.tensor(logits, dtype=torch.float64), 0)
+                out[n, h] = (w[:, None] * torch.stack(vals)).sum(0)
+    return out
+
+
+def test_paged_decode_matches_key_loop_and_page_permutation():
+    g = torch.Generator().manual_seed(31)
+    R, dql, H, Hkv, D, page, nb, K, lb = 2, 2, 4, 2, 8, 4, 6, 3, 2
+    npages = R * nb + 3
+    q = _rand(R * dql, H, D, g=g)
+    kc, vc = _rand(npages, page, Hkv, D, g=g), _rand(npages, page, Hkv, D, g=g)
+    perm = torch.randperm(npages, generator=g)[:R * nb]
+    bt = perm.view(R, nb)
+    sl = torch.tensor([23, 17])
+    topk = torch.randint(-1, nb, (Hkv, R * dql, K), generator=g)     # some ids past seq_len 17
+    topk[0, 0, 1] = topk[0, 0, 0]                                  # repeated id
+    topk[:, 3] = -1                                                # a row that selects nothing
+    bias = _rand(Hkv, R * dql, K, g=g)
+    want = _paged_brute(q, kc, vc, topk, bias, bt, sl, dql, lb, 0.5)
+    got = O.paged_decode_attend(q, kc, vc, topk, bias, bt, sl, dql, lb, 0.5)
+    assert (got - want).abs().max() < 1e-10
+    # the same cache stored under other page ids gives the same result
+    remap = torch.randperm(npages, generator=g)
+    kc2, vc2 = torch.empty_like(kc), torch.empty_like(vc)
+    kc2[remap], vc2[remap] = kc, vc
+    got2 = O.paged_decode_attend(q, kc2, vc2, topk, bias, remap[bt], sl, dql, lb, 0.5)
+    assert (got2 - got).abs().max() < 1e-12
+    # no bias == zero bias
+    z = torch.zeros_like(bias)
+    assert (O.paged_decode_attend(q, kc, vc, topk, None, bt, sl, dql, lb, 0.5) -
+            O.paged_decode_attend(q, kc, vc, topk, z, bt, sl, dql, lb, 0.5)).abs().max() < 1e-12
+    # no window (local_blocks = 0): remote keys only, up to the query
+    want0 = _paged_brute(q, kc, vc, topk, bias, bt, sl, dql, 0, 0.5)
+    assert (want0[3] == 0).all()                                   # empty row -> zeros
+    assert (O.paged_decode_attend(q, kc, vc, topk, bias, bt, sl, dql, 0, 0.5) - want0).abs().max() < 1e-10

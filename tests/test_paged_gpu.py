@@ -1,0 +1,64 @@
+"""Paged decode (srswa_gather_decode_paged, the serving cache layout of
+dash_sparse_attn_decode) vs the CPU oracle ``paged_decode_attend``: pages in
+random order, ragged sequence lengths, 1 and 2 decode queries per request,
+GQA, page sizes 16..128, no window (local_blocks 0), -1 padding, repeated ids,
+bias and no bias; bf16 within 2e-2 (beyond output rounding), fp32 within
+1e-5 relative (max-abs error / max-abs reference)."""
+
+import math
+
+import pytest
+import torch
+
+from oracle import srswa_oracle as O
+from tolerance import assert_close_lowp
+
+pytestmark = pytest.mark.gpu
+
+
+def _case(seed, R, dql, H, Hkv, D, page, nb, K, lb, dtype, with_bias):
+    g = torch.Generator().manual_seed(seed)
+    npages = R * nb + 5
+    q = torch.randn(R * dql, H, D, generator=g).to(dtype)
+    kc = torch.randn(npages, page, Hkv, D, generator=g).to(dtype)
+    vc = torch.randn(npages, page, Hkv, D, generator=g).to(dtype)
+    bt = torch.randperm(npages, generator=g)[:R * nb].view(R, nb).to(torch.int32)
+    sl = torch.randint(max(dql, page), nb * page + 1, (R,), generator=g).to(torch.int32)
+    sl[0] = nb * page                                     # a full table
+    topk = torch.randint(-1, nb, (Hkv, R * dql, K), generator=g).to(torch.int32)
+    topk[:, 0, 1] = topk[:, 0, 0]                        # a repeated id
+    bias = torch.randn(Hkv, R * dql, K, generator=g) if with_bias else None
+    return q, kc, vc, topk, bias, bt, sl
+
+
+CASES = {
+    "bf16_p64": dict(R=5, dql=1, H=10, Hkv=10, D=128, page=64, nb=24, K=8, lb=8, dtype=torch.bfloat16, with_bias=True),
+    "bf16_p32_gqa_dql2": dict(R=3, dql=2, H=8, Hkv=2, D=128, page=32, nb=40, K=12, lb=4, dtype=torch.bfloat16,
+                             with_bias=True),
+    "bf16_p16_nowin": dict(R=4, dql=1, H=4, Hkv=4, D=128, page=16, nb=30, K=6, lb=0, dtype=torch.bfloat16,
+                          with_bias=False),
+    "bf16_d64_p128": dict(R=2, dql=1, H=4, Hkv=1, D=64, page=128, nb=10, K=4, lb=2, dtype=torch.bfloat16,
+                         with_bias=True),
+    "fp32_p32": dict(R=3, dql=1, H=4, Hkv=2, D=128, page=32, nb=20, K=5, lb=3, dtype=torch.float32,
+                    with_bias=True),
+}
+
+
+@pytest.mark.parametrize("name", list(CASES))
+def test_paged_decode_matches_oracle(dev, name):
+    from srswa import unlimited_dash_ops as U
+
+    c = CASES[name]
+    q, kc, vc, topk, bias, bt, sl = _case(40 + list(CASES).index(name), **c)
+    scale = 1 / math.sqrt(c["D"])
+    out = torch.empty(q.shape, dtype=q.dtype, device=dev)
+    U.dash_sparse_attn_decode(q.to(dev), kc.to(dev), vc.to(dev), topk.to(dev),
+                              None if bias is None else bias.to(dev), bt.to(dev), sl.to(dev), c["Hkv"], scale,
+                              out, c["dql"], local_blocks=c["lb"], sparse_block_size=c["page"])
+    ref = O.paged_decode_attend(q.double(), kc.double(), vc.double(), topk, None if bias is None else bias.double(),
+                                bt, sl, c["dql"], c["lb"], scale)
+    if c["dtype"] == torch.float32:
+        rel = ((out.cpu().double() - ref).abs().max() / ref.abs().max()).item()   # max-abs err / max-abs ref
+        assert rel <= 1e-5, rel
+    else:
+        assert_close_lowp(out.cpu(), ref, c["dtype"], 2e-2, name)

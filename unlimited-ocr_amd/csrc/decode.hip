@@ -62,6 +62,12 @@ struct DecodeK {
   int64_t rowheads;
   float* part;
   uint32_t* cnt;
+  // paged cache (PAGED kernels): key j of sequence b lives in page
+  // bt[b * bt_sb + j / block_size] at row j % block_size; q positions come
+  // from kv_len: q_pos = kv_len[b] - Lq + lq
+  const int32_t* bt;
+  int64_t bt_sb, k_pst, v_pst;   // block-table row stride, page strides (elements)
+  int bs_shift, max_blocks;
 };
 
 template <typename TO>
@@ -143,7 +149,7 @@ __device__ __forceinline__ uint4 load_stream(const void* p) {
   return make_uint4(v.x, v.y, v.z, v.w);
 }
 
-template <typename T, typename TO, int D, int NI, bool ATOMIC_MERGE>
+template <typename T, typename TO, int D, int NI, bool ATOMIC_MERGE, bool PAGED>
 __global__ __launch_bounds__(kDecodeWaves * kWave) void decode_kernel(DecodeK p) {
   using V = Vec16<T>;
   constexpr int EPV = V::N;           // elements per 16-byte vector
@@ -173,8 +179,8 @@ __global__ __launch_bounds__(kDecodeWaves * kWave) void decode_kernel(DecodeK p)
   const int kvh = hq / p.G;
   const int ih = hq / p.IG;
 
-  const int qp = a.q_pos[b * a.pos_sb + lq * a.pos_sq];
   const int kvl = a.kv_len ? min(a.kv_len[b], a.L) : a.L;
+  const int qp = PAGED ? a.kv_len[b] - a.Lq + lq : a.q_pos[b * a.pos_sb + lq * a.pos_sq];
   const int last = min(qp, kvl - 1);                   // last key this row may read
   const int ws = max(qp - a.local_window + 1, 0);      // first window key
   const int remote_end = min(ws, last + 1);            // remote keys are < this
@@ -188,11 +194,22 @@ __global__ __launch_bounds__(kDecodeWaves * kWave) void decode_kernel(DecodeK p)
   const int64_t aux_off = (int64_t)b * a.idx_sb + (int64_t)ih * a.idx_sh +
                           (int64_t)lq * a.idx_sq;
 
-  const T* kbase = reinterpret_cast<const T*>(a.k) + (int64_t)b * a.k_sb +
+  const T* kbase = reinterpret_cast<const T*>(a.k) + (PAGED ? 0 : (int64_t)b * a.k_sb) +
                    (int64_t)kvh * a.k_sh + c * EPV;
-  const T* vbase = reinterpret_cast<const T*>(a.v) + (int64_t)b * a.v_sb +
+  const T* vbase = reinterpret_cast<const T*>(a.v) + (PAGED ? 0 : (int64_t)b * a.v_sb) +
                    (int64_t)kvh * a.v_sh + c * EPV;
-  const int max_blk = kvl > 0 ? (kvl - 1) / a.block_size : -1;
+  int max_blk = kvl > 0 ? (kvl - 1) / a.block_size : -1;
+  if (PAGED) max_blk = min(max_blk, p.max_blocks - 1);
+  const int32_t* bt_row = PAGED ? p.bt + (int64_t)b * p.bt_sb : nullptr;
+  // paged window: units on the UK grid from ws_al (each inside one block);
+  // lane i holds the page of the window's i-th block
+  const int ws_al = PAGED ? (ws & ~(p.UK - 1)) : ws;
+  const int wblk0 = ws_al >> (PAGED ? p.bs_shift : 0);
+  int win_page = 0;
+  if (PAGED && a.local_window > 0) {
+    const int wb = wblk0 + lane;
+    if (wb <= max_blk) win_page = bt_row[wb];
+  }
 
   float m = -INFINITY, l = 0.f;
   float acc[EPV];
@@ -203,7 +220,7 @@ __global__ __launch_bounds__(kDecodeWaves * kWave) void decode_kernel(DecodeK p)
   // whether it survives (valid, in range, first slot holding that id) and its
   // bias.  Wider rows (S > 64) re-read the slots per unit instead.
   const bool slots_in_regs = a.S <= kWave;
-  int my_bid = -1;
+  int my_bid = -1, my_page = 0;
   bool my_ok = false;
   float my_bias = 0.f;
   if (slots_in_regs && lane < a.S) {
@@ -211,6 +228,7 @@ __global__ __launch_bounds__(kDecodeWaves * kWave) void decode_kernel(DecodeK p)
     my_ok = my_bid >= 0 && my_bid <= max_blk &&
             (!a.valid || a.valid[aux_off + (int64_t)lane * a.idx_ss]);
     if (a.bias) my_bias = a.bias[aux_off + (int64_t)lane * a.idx_ss];
+    if (PAGED && my_ok) my_page = bt_row[my_bid];
   }
   if (slots_in_regs) {
     bool dup = false;
@@ -228,7 +246,8 @@ __global__ __launch_bounds__(kDecodeWaves * kWave) void decode_kernel(DecodeK p)
   for (int i = 0; i < p.upw; ++i) {
     const int u = u_base + wave + i * kDecodeWaves;
     if (u >= p.n_units) break;
-    int k0, k1;
+    int k0, k1, klo;
+    int page = 0;
     float bias_l2 = 0.f;
     if (u < p.n_remote_units) {
       const int slot = u / p.upb, sub = u % p.upb;
@@ -239,6 +258,7 @@ __global__ __launch_bounds__(kDecodeWaves * kWave) void decode_kernel(DecodeK p)
         bid = __shfl(my_bid, slot, kWave);
         ok = __shfl(my_ok ? 1 : 0, slot, kWave) != 0;
         bias = __shfl(my_bias, slot, kWave);
+        if (PAGED) page = __shfl(my_page, slot, kWave);
       } else {
         bid = idx_row[(int64_t)slot * a.idx_ss];
         ok = bid >= 0 && bid <= max_blk && (!a.valid || a.valid[aux_off + (int64_t)slot * a.idx_ss]);
@@ -253,28 +273,41 @@ __global__ __launch_bounds__(kDecodeWaves * kWave) void decode_kernel(DecodeK p)
           if (__any(d)) ok = false;
         }
         if (ok && a.bias) bias = a.bias[aux_off + (int64_t)slot * a.idx_ss];
+        if (PAGED && ok) page = bt_row[bid];
       }
       k0 = ok ? bid * a.block_size + sub * UK : 0;
       k1 = ok ? min(min(k0 + UK, bid * a.block_size + a.block_size), remote_end) : 0;
+      klo = k0;
       bias_l2 = bias * kLog2e;
     } else {
-      k0 = ws + (u - p.n_remote_units) * UK;
+      k0 = ws_al + (u - p.n_remote_units) * UK;
       k1 = min(k0 + UK, last + 1);
+      klo = PAGED ? max(k0, ws) : k0;
+      if (PAGED) page = __shfl(win_page, (k0 >> p.bs_shift) - wblk0, kWave);
     }
-    if (k1 <= k0) continue;   // uniform across the wave
+    if (k1 <= klo) continue;   // uniform across the wave
 
+    // unit base: the sequence's K / V rows (contiguous) or the unit's page
+    const T* kb = kbase;
+    const T* vb = vbase;
+    int kr0 = k0;              // row of key k0 in kb / vb
+    if (PAGED) {
+      kb += (int64_t)page * p.k_pst;
+      vb += (int64_t)page * p.v_pst;
+      kr0 = k0 & (a.block_size - 1);
+    }
     uint4 kr[NI], vr[NI];
 #pragma unroll
     for (int i = 0; i < NI; ++i) {
       const int key = k0 + i * RPI + r;
-      kr[i] = key < k1 ? load_stream(kbase + (int64_t)key * a.k_st)
-                       : make_uint4(0, 0, 0, 0);
+      kr[i] = ((!PAGED || key >= klo) && key < k1) ? load_stream(kb + (int64_t)(kr0 + i * RPI + r) * a.k_st)
+                                                   : make_uint4(0, 0, 0, 0);
     }
 #pragma unroll
     for (int i = 0; i < NI; ++i) {
       const int key = k0 + i * RPI + r;
-      vr[i] = key < k1 ? load_stream(vbase + (int64_t)key * a.v_st)
-                       : make_uint4(0, 0, 0, 0);
+      vr[i] = ((!PAGED || key >= klo) && key < k1) ? load_stream(vb + (int64_t)(kr0 + i * RPI + r) * a.v_st)
+                                                   : make_uint4(0, 0, 0, 0);
     }
 
     float part[NI];
@@ -296,8 +329,8 @@ __global__ __launch_bounds__(kDecodeWaves * kWave) void decode_kernel(DecodeK p)
     const int i_own = c / DUP;                    // which instruction's key this lane holds
     const int key = k0 + i_own * RPI + r;
     const bool owner = (c % DUP) == 0;
-    const float t = key < k1 ? part[0] * p.scale_l2 + bias_l2 : -INFINITY;
-    const float mnew = fmaxf(m, wave_max(t));     // finite: key k0 is always kept
+    const float t = ((!PAGED || key >= klo) && key < k1) ? part[0] * p.scale_l2 + bias_l2 : -INFINITY;
+    const float mnew = fmaxf(m, wave_max(t));     // finite: key klo is always kept
     const float alpha = exp2f(m - mnew);
     const float pj = exp2f(t - mnew);
     l = l * alpha + (owner ? pj : 0.f);   // per-lane; summed over the wave once at the end
@@ -484,14 +517,19 @@ int decode_ni(int dt, int D) {
   return (want == 8 && ni == 16) ? 8 : ni;
 }
 
-DecodePlan make_plan(const srswa_decode_args* a) {
+DecodePlan make_plan(const srswa_decode_args* a, bool paged = false) {
   DecodePlan pl{};
   const int lpr = a->D * elem_bytes(a->in_dtype) / 16;
-  const int ni = decode_ni(a->in_dtype, a->D);
+  int ni = decode_ni(a->in_dtype, a->D);
+  // a paged unit must stay inside one block (one page): UK <= block size
+  while (paged && ni > 1 && ni * (kWave / lpr) > a->block_size) ni >>= 1;
   pl.UK = ni * (kWave / lpr);
   pl.upb = ceil_div(a->block_size, pl.UK);
   pl.n_remote_units = a->S * pl.upb;
-  pl.n_units = pl.n_remote_units + ceil_div(a->local_window, pl.UK);
+  // paged windows run on the UK grid: one extra unit for the unaligned start
+  pl.n_units = pl.n_remote_units +
+               (paged ? (a->local_window > 0 ? ceil_div(a->local_window, pl.UK) + 1 : 0)
+                      : ceil_div(a->local_window, pl.UK));
   static const int upw = env_int("SRSWA_DECODE_UPW", 2);
   pl.upw = upw > 1 ? upw : 1;
   pl.nsplit = ceil_div(pl.n_units, kDecodeWaves * pl.upw);
@@ -507,11 +545,17 @@ size_t counter_count(const DecodePlan& pl) { return pl.nsplit <= 1 ? 0 : (size_t
 
 template <typename T, typename TO, int D, int NI>
 int launch_decode_ni(const DecodeK& k, int64_t grid, hipStream_t st) {
-  if (k.nsplit > 1 && merge_in_kernel()) {
-    hipLaunchKernelGGL((decode_kernel<T, TO, D, NI, true>), dim3((unsigned)grid),
+  if (k.bt) {
+    hipLaunchKernelGGL((decode_kernel<T, TO, D, NI, false, true>), dim3((unsigned)grid),
+                       dim3(kDecodeWaves * kWave), 0, st, k);
+    if (k.nsplit > 1)
+      hipLaunchKernelGGL((decode_merge_kernel<TO, D>), dim3((unsigned)((k.rowheads + 3) / 4)),
+                         dim3(256), 0, st, k);
+  } else if (k.nsplit > 1 && merge_in_kernel()) {
+    hipLaunchKernelGGL((decode_kernel<T, TO, D, NI, true, false>), dim3((unsigned)grid),
                        dim3(kDecodeWaves * kWave), 0, st, k);
   } else {
-    hipLaunchKernelGGL((decode_kernel<T, TO, D, NI, false>), dim3((unsigned)grid),
+    hipLaunchKernelGGL((decode_kernel<T, TO, D, NI, false, false>), dim3((unsigned)grid),
                        dim3(kDecodeWaves * kWave), 0, st, k);
     if (k.nsplit > 1)
       hipLaunchKernelGGL((decode_merge_kernel<TO, D>), dim3((unsigned)((k.rowheads + 3) / 4)),
@@ -529,8 +573,12 @@ template <typename T, typename TO, int D>
 int launch_decode(const DecodeK& k, int64_t grid, hipStream_t st) {
   constexpr int LPR = D / Vec16<T>::N;
   constexpr int NI_MAX = LPR < 16 ? LPR : 16;
-  if (NI_MAX >= 16 && k.UK == 8 * (kWave / LPR)) return launch_decode_ni<T, TO, D, 8>(k, grid, st);
-  return launch_decode_ni<T, TO, D, NI_MAX>(k, grid, st);
+  const int ni = k.UK / (kWave / LPR);
+  if (NI_MAX >= 16 && ni == 16) return launch_decode_ni<T, TO, D, 16 <= NI_MAX ? 16 : NI_MAX>(k, grid, st);
+  if (ni == 8) return launch_decode_ni<T, TO, D, 8 <= NI_MAX ? 8 : NI_MAX>(k, grid, st);
+  if (ni == 4) return launch_decode_ni<T, TO, D, 4>(k, grid, st);
+  if (ni == 2) return launch_decode_ni<T, TO, D, 2>(k, grid, st);
+  return launch_decode_ni<T, TO, D, 1>(k, grid, st);
 }
 
 template <typename T>
@@ -641,6 +689,132 @@ extern "C" int srswa_gather_decode(const srswa_decode_args* a, void* scratch,
   const int64_t grid = pl.rowheads * pl.nsplit;
   if (grid > 0x7fffffff) {
     set_error("decode: grid too large");
+    return SRSWA_UNSUPPORTED;
+  }
+  hipStream_t st = reinterpret_cast<hipStream_t>(stream);
+  switch (a->in_dtype) {
+    case SRSWA_F32: return dispatch_out<float>(k, grid, st);
+    case SRSWA_BF16: return dispatch_out<bf16_t>(k, grid, st);
+    case SRSWA_F16: return dispatch_out<__half>(k, grid, st);
+  }
+  return SRSWA_UNSUPPORTED;
+}
+
+namespace {
+
+// The paged arguments as a decode over R sequences of dql query rows, the
+// caches addressed per page (k_sb / v_sb unused) and positions from seq_lens.
+srswa_decode_args paged_as_decode(const srswa_paged_decode_args* a) {
+  srswa_decode_args d{};
+  d.q = a->q;  d.q_sb = (int64_t)a->dql * a->q_sn;  d.q_sq = a->q_sn;  d.q_sh = a->q_sh;
+  d.k = a->k_cache;  d.k_sb = 0;  d.k_st = a->k_st;  d.k_sh = a->k_sh;
+  d.v = a->v_cache;  d.v_sb = 0;  d.v_st = a->v_st;  d.v_sh = a->v_sh;
+  d.idx = a->topk;  d.idx_sb = (int64_t)a->dql * a->t_sn;  d.idx_sh = a->t_sh;  d.idx_sq = a->t_sn;
+  d.idx_ss = a->t_sk;
+  d.bias = a->bias;  d.valid = nullptr;
+  d.q_pos = nullptr;  d.kv_len = a->seq_lens;
+  d.out = a->out;  d.o_sb = (int64_t)a->dql * a->o_sn;  d.o_sq = a->o_sn;  d.o_sh = a->o_sh;
+  d.lse = nullptr;
+  d.B = a->R;  d.Lq = a->dql;  d.HQ = a->HQ;  d.HKV = a->HKV;  d.HI = a->HKV;  d.D = a->D;
+  d.S = a->topk_n;  d.L = a->max_blocks * a->page_size;
+  d.block_size = a->page_size;  d.local_window = a->local_blocks * a->page_size;
+  d.scale = a->scale;  d.in_dtype = a->in_dtype;  d.out_dtype = a->out_dtype;
+  return d;
+}
+
+}  // namespace
+
+extern "C" void srswa_gather_decode_paged_workspace(const srswa_paged_decode_args* a, size_t* scratch,
+                                                    size_t* counters) {
+  size_t s = 0, c = 0;
+  if (a && a->R > 0 && a->dql > 0 && a->HQ > 0 && a->D > 0 && a->page_size > 0) {
+    const srswa_decode_args d = paged_as_decode(a);
+    const DecodePlan pl = make_plan(&d, true);
+    s = scratch_bytes(pl);
+    c = counter_count(pl);
+  }
+  if (scratch) *scratch = s;
+  if (counters) *counters = c;
+}
+
+extern "C" int srswa_gather_decode_paged(const srswa_paged_decode_args* a, void* scratch,
+                                         size_t scratch_size, uint32_t* counters, size_t n_counters,
+                                         void* stream) {
+  if (!a || !a->q || !a->k_cache || !a->v_cache || !a->out || !a->block_table || !a->seq_lens ||
+      (!a->topk && a->topk_n > 0)) {
+    set_error("paged decode: null argument");
+    return SRSWA_INVALID;
+  }
+  if (a->R < 0 || a->dql <= 0 || a->HQ <= 0 || a->HKV <= 0 || a->topk_n < 0 || a->max_blocks <= 0 ||
+      a->page_size <= 0 || a->local_blocks < 0) {
+    set_error("paged decode: bad sizes");
+    return SRSWA_INVALID;
+  }
+  if (a->R == 0) return SRSWA_OK;
+  if (a->HQ % a->HKV != 0) {
+    set_error("paged decode: HQ=%d must be a multiple of HKV=%d", a->HQ, a->HKV);
+    return SRSWA_UNSUPPORTED;
+  }
+  if (!(a->D == 64 || a->D == 128) || a->in_dtype < 0 || a->in_dtype > 2 || a->out_dtype < 0 ||
+      a->out_dtype > 2) {
+    set_error("paged decode: unsupported D=%d / dtype", a->D);
+    return SRSWA_UNSUPPORTED;
+  }
+  const int ib = elem_bytes(a->in_dtype), ob = elem_bytes(a->out_dtype);
+  const int rpi = kWave / (a->D * ib / 16);
+  if ((a->page_size & (a->page_size - 1)) || a->page_size < rpi) {
+    set_error("paged decode: page size %d must be a power of two >= %d", a->page_size, rpi);
+    return SRSWA_UNSUPPORTED;
+  }
+  if (a->local_blocks > kWave - 1 || a->topk_n > 1024) {
+    set_error("paged decode: at most 63 local blocks and 1024 slots");
+    return SRSWA_UNSUPPORTED;
+  }
+  const int64_t strides[] = {a->q_sn, a->q_sh, a->k_sp, a->k_st, a->k_sh, a->v_sp, a->v_st, a->v_sh};
+  for (int64_t st : strides)
+    if ((st * ib) % 16 != 0) {
+      set_error("paged decode: strides must keep rows 16-byte aligned");
+      return SRSWA_UNSUPPORTED;
+    }
+  if (((a->o_sn * ob) % 16) || ((a->o_sh * ob) % 16) || !aligned16(a->q) || !aligned16(a->k_cache) ||
+      !aligned16(a->v_cache) || !aligned16(a->out)) {
+    set_error("paged decode: pointers must be 16-byte aligned");
+    return SRSWA_UNSUPPORTED;
+  }
+  const srswa_decode_args d = paged_as_decode(a);
+  const DecodePlan pl = make_plan(&d, true);
+  const size_t need = scratch_bytes(pl), need_cnt = counter_count(pl);
+  if (need > 0 && (!scratch || scratch_size < need || !counters || n_counters < need_cnt)) {
+    set_error("paged decode: scratch of %zu bytes and %zu counters required (got %zu, %zu)", need,
+              need_cnt, scratch_size, n_counters);
+    return SRSWA_WORKSPACE;
+  }
+  DecodeK k{};
+  k.a = d;
+  k.G = d.HQ / d.HKV;
+  k.IG = d.HQ / d.HI;
+  k.UK = pl.UK;
+  k.upb = pl.upb;
+  k.n_remote_units = pl.n_remote_units;
+  k.n_units = pl.n_units;
+  k.upw = pl.upw;
+  k.nsplit = pl.nsplit;
+  k.pstride = pl.pstride;
+  k.scale_l2 = d.scale * kLog2e;
+  k.rowheads = pl.rowheads;
+  if (need > 0) {
+    k.cnt = counters;
+    k.part = reinterpret_cast<float*>(scratch);
+  }
+  k.bt = a->block_table;
+  k.bt_sb = a->bt_sr;
+  k.k_pst = a->k_sp;
+  k.v_pst = a->v_sp;
+  k.bs_shift = __builtin_ctz((unsigned)a->page_size);
+  k.max_blocks = a->max_blocks;
+  const int64_t grid = pl.rowheads * pl.nsplit;
+  if (grid > 0x7fffffff) {
+    set_error("paged decode: grid too large");
     return SRSWA_UNSUPPORTED;
   }
   hipStream_t st = reinterpret_cast<hipStream_t>(stream);

@@ -131,6 +131,25 @@ class BlockMaxArgs(ctypes.Structure):
     ]
 
 
+class PagedDecodeArgs(ctypes.Structure):
+    """Mirror of ``srswa_paged_decode_args``."""
+
+    _fields_ = [
+        ("q", _vp), ("q_sn", _i64), ("q_sh", _i64),
+        ("k_cache", _vp), ("k_sp", _i64), ("k_st", _i64), ("k_sh", _i64),
+        ("v_cache", _vp), ("v_sp", _i64), ("v_st", _i64), ("v_sh", _i64),
+        ("topk", _vp), ("t_sh", _i64), ("t_sn", _i64), ("t_sk", _i64),
+        ("bias", _vp),
+        ("block_table", _vp), ("bt_sr", _i64),
+        ("seq_lens", _vp),
+        ("out", _vp), ("o_sn", _i64), ("o_sh", _i64),
+        ("R", _i32), ("dql", _i32), ("HQ", _i32), ("HKV", _i32), ("D", _i32), ("topk_n", _i32),
+        ("max_blocks", _i32), ("page_size", _i32), ("local_blocks", _i32),
+        ("scale", ctypes.c_float),
+        ("in_dtype", _i32), ("out_dtype", _i32),
+    ]
+
+
 class RouteArgs(ctypes.Structure):
     """Mirror of ``srswa_route_args``."""
 
@@ -162,11 +181,15 @@ SIGNATURES = {
     "srswa_gather_bwd": (ctypes.c_int, [ctypes.POINTER(BwdArgs), _vp, ctypes.c_size_t, _vp]),
     "srswa_block_max_score": (ctypes.c_int, [ctypes.POINTER(BlockMaxArgs), _vp]),
     "srswa_dash_route": (ctypes.c_int, [ctypes.POINTER(RouteArgs), _vp]),
+    "srswa_gather_decode_paged_workspace": (None, [ctypes.POINTER(PagedDecodeArgs), _szp, _szp]),
+    "srswa_gather_decode_paged": (ctypes.c_int, [ctypes.POINTER(PagedDecodeArgs), _vp, ctypes.c_size_t, _vp,
+                                                 ctypes.c_size_t, _vp]),
 }
 
 STRUCTS = {"srswa_decode_args": DecodeArgs, "srswa_index_args": IndexArgs,
            "srswa_fwd_args": FwdArgs, "srswa_bwd_args": BwdArgs,
-           "srswa_blockmax_args": BlockMaxArgs, "srswa_route_args": RouteArgs}
+           "srswa_blockmax_args": BlockMaxArgs, "srswa_route_args": RouteArgs,
+           "srswa_paged_decode_args": PagedDecodeArgs}
 
 _lib = None
 _lock = threading.Lock()

@@ -269,6 +269,78 @@ def topk_rows(scores, k, *, invalid_at=SCORE_NEG * 0.5, ascending=False, return_
     return (idx, val) if return_values else idx
 
 
+def prepare_gather_decode_paged(q, k_cache, v_cache, topk_idx, blk_bias, block_table, seq_lens, *,
+                                decode_query_len, local_blocks, scale, out=None):
+    """Validate, allocate and build the launch of the paged decode
+    (``srswa_gather_decode_paged``).  Returns (launch, out).
+
+    q [total_q, HQ, D] with total_q = R * decode_query_len; k_cache, v_cache
+    [num_pages, page_size, HKV, D] (page_size = block size); topk_idx
+    [HKV, total_q, K] logical block ids (-1 = empty); blk_bias like topk_idx
+    (fp32) or None; block_table [R, max_blocks] page ids; seq_lens [R]."""
+    _require_cuda(q, k_cache, v_cache, topk_idx, blk_bias, block_table, seq_lens, out)
+    total_q, HQ, D = q.shape
+    npages, page, HKV, Dk = k_cache.shape
+    dql = int(decode_query_len)
+    R = seq_lens.shape[0]
+    if total_q != R * dql:
+        raise ValueError(f"total_q {total_q} != {R} requests x {dql} queries")
+    if Dk != D or tuple(v_cache.shape) != tuple(k_cache.shape):
+        raise ValueError(f"cache shape {tuple(k_cache.shape)} / {tuple(v_cache.shape)} vs q {tuple(q.shape)}")
+    if topk_idx.dim() != 3 or topk_idx.shape[0] != HKV or topk_idx.shape[1] != total_q:
+        raise ValueError(f"topk_idx shape {tuple(topk_idx.shape)} != ({HKV}, {total_q}, K)")
+    if q.dtype != k_cache.dtype or q.dtype != v_cache.dtype:
+        raise ValueError("q, k_cache, v_cache must share a dtype")
+    for t in (q, k_cache, v_cache):
+        if t.stride(-1) != 1:
+            raise UnsupportedShape("head dim must be contiguous")
+    ti = _i32(topk_idx).contiguous()
+    bias = None
+    if blk_bias is not None:
+        if tuple(blk_bias.shape) != tuple(topk_idx.shape):
+            raise ValueError(f"blk_bias shape {tuple(blk_bias.shape)} != topk_idx {tuple(topk_idx.shape)}")
+        bias = blk_bias.to(torch.float32).contiguous()
+    bt = _i32(block_table)
+    if bt.stride(-1) != 1:
+        bt = bt.contiguous()
+    sl = _i32(seq_lens).contiguous()
+    if out is None:
+        out = torch.empty(total_q, HQ, D, dtype=q.dtype, device=q.device)
+    a = _lib.PagedDecodeArgs()
+    a.q = q.data_ptr(); a.q_sn, a.q_sh = q.stride(0), q.stride(1)
+    a.k_cache = k_cache.data_ptr(); a.k_sp, a.k_st, a.k_sh = k_cache.stride(0), k_cache.stride(1), k_cache.stride(2)
+    a.v_cache = v_cache.data_ptr(); a.v_sp, a.v_st, a.v_sh = v_cache.stride(0), v_cache.stride(1), v_cache.stride(2)
+    a.topk = ti.data_ptr(); a.t_sh, a.t_sn, a.t_sk = ti.stride(0), ti.stride(1), ti.stride(2)
+    a.bias = _lib.ptr(bias)
+    a.block_table = bt.data_ptr(); a.bt_sr = bt.stride(0)
+    a.seq_lens = sl.data_ptr()
+    a.out = out.data_ptr(); a.o_sn, a.o_sh = out.stride(0), out.stride(1)
+    a.R, a.dql, a.HQ, a.HKV, a.D, a.topk_n = R, dql, HQ, HKV, D, ti.shape[-1]
+    a.max_blocks, a.page_size, a.local_blocks = bt.shape[1], page, int(local_blocks)
+    a.scale = float(scale)
+    a.in_dtype = _lib.dtype_code(q.dtype)
+    a.out_dtype = _lib.dtype_code(out.dtype)
+    L_ = _lib.lib()
+    nscr, ncnt = ctypes.c_size_t(0), ctypes.c_size_t(0)
+    L_.srswa_gather_decode_paged_workspace(ctypes.byref(a), ctypes.byref(nscr), ctypes.byref(ncnt))
+    scr = _lib.scratch(q.device, nscr.value)
+    cnt = _lib.counters(q.device, ncnt.value)
+    launch = _Launch(L_.srswa_gather_decode_paged, a, (q, k_cache, v_cache, ti, bias, bt, sl, out),
+                     (scr, nscr.value, cnt, 0 if cnt is None else cnt.numel()),
+                     _lib.stream_ptr(q.device), "srswa_gather_decode_paged")
+    return launch, out
+
+
+def gather_decode_paged(q, k_cache, v_cache, topk_idx, blk_bias, block_table, seq_lens, *,
+                        decode_query_len, local_blocks, scale, out=None):
+    """Block-sparse decode over a paged KV cache (see ``prepare_gather_decode_paged``)."""
+    launch, out = prepare_gather_decode_paged(q, k_cache, v_cache, topk_idx, blk_bias, block_table, seq_lens,
+                                              decode_query_len=decode_query_len, local_blocks=local_blocks,
+                                              scale=scale, out=out)
+    launch()
+    return out
+
+
 # ---------------------------------------------------------------------------
 # DASH router
 # ---------------------------------------------------------------------------
