@@ -245,6 +245,51 @@ int srswa_gather_decode_paged(const srswa_paged_decode_args* a, void* scratch, s
                               uint32_t* counters, size_t n_counters, void* stream);
 
 /* ------------------------------------------------------------------------
+ * head_cls summary cache over a paged index-key cache (the serving stage 0).
+ * Replaces KBarCache.put / refresh_tail and headcls_scores_decode
+ * (WHL!layers/attention/unlimited_dash_ops/dash_stage0.py:79-199): one fp32
+ * summary row k_bar per KV page, so a decode step scores nblk cached rows
+ * instead of re-reading every key.
+ *
+ * srswa_kbar_pages: for every request r and logical block b < nb_r =
+ * ceil(seq_lens[r] / page_size) (only the last tail_blocks blocks when
+ * tail_blocks > 0), kbar[block_table[r, b]] = summary of the block's
+ * min(page_size, seq_lens[r] - b * page_size) keys (head_cls softmax-weighted
+ * mean, the plain mean when head_cls is NULL).
+ * ---------------------------------------------------------------------- */
+typedef struct {
+  const void* keys;     int64_t k_sp, k_st;            /* [num_pages, page_size, D] index keys */
+  const float* head_cls;                               /* [D] fp32; NULL = mean              */
+  const int32_t* block_table; int64_t bt_sr;           /* [R, max_blocks] page ids           */
+  const int32_t* seq_lens;                             /* [R]                                */
+  float* kbar;          int64_t kb_sp;                 /* [num_pages, D] fp32, written per page */
+  int32_t R, max_blocks, page_size, D, tail_blocks;
+  int32_t k_dtype;                                     /* srswa_dtype of keys                */
+} srswa_kbar_pages_args;
+
+int srswa_kbar_pages(const srswa_kbar_pages_args* a, void* stream);
+
+/* Scores of query rows against the cached summaries: row n (request
+ * row_req[n], position row_pos[n]; NULL arrays = decode rows: request n / dql,
+ * position seq_lens[r] - dql + n % dql) gets, for blocks b < width,
+ *   z = clamp(q_n . kbar[block_table[r, b]] / sqrt(D), +-1e4)
+ * when b <= pos / page_size - local_blocks and b * page_size < seq_lens[r],
+ * else -1e9 (headcls_scores_decode, dash_stage0.py:151-199; the prefill rows
+ * of headcls_scores_prefill, :62-103). */
+typedef struct {
+  const float* q;       int64_t q_sn;                  /* [nrows, D] fp32 index queries      */
+  const float* kbar;    int64_t kb_sp;                 /* [num_pages, D] fp32                */
+  const int32_t* block_table; int64_t bt_sr;           /* [R, max_blocks]                    */
+  const int32_t* seq_lens;                             /* [R]                                */
+  const int32_t* row_req;                              /* [nrows] or NULL                    */
+  const int32_t* row_pos;                              /* [nrows] or NULL                    */
+  float* scores;        int64_t sc_sn;                 /* [nrows, width] fp32                */
+  int32_t nrows, R, dql, max_blocks, width, page_size, local_blocks, D;
+} srswa_kbar_scores_args;
+
+int srswa_kbar_scores(const srswa_kbar_scores_args* a, void* stream);
+
+/* ------------------------------------------------------------------------
  * DASH router: block scores -> selected blocks + bias for the gather kernels.
  * Replaces _infer_route_select (HF/modeling_deepseekv2.py:338-362; vLLM
  * DashRouterMath.route_and_select with budget_topk=True, the DASH decode and

@@ -358,6 +358,64 @@ def meanpool_block_scores(q, k, q_pos, block_size, local_blocks, head_cls=None):
     return z.masked_fill(~keep, SCORE_NEG)
 
 
+def kbar_summaries(keys, valid, head_cls=None):
+    """``_summary_keys`` (WHL!layers/attention/unlimited_dash_ops/dash_stage0.py:25-43):
+    [nb, bs, d] keys, [nb, bs] real-key mask -> [nb, d] head_cls softmax-weighted
+    means (the plain mean when head_cls is None); a block without keys -> 0."""
+    d = keys.shape[-1]
+    inv_sqrt_d = 1.0 / math.sqrt(d)
+    hc = torch.zeros(d, dtype=keys.dtype) if head_cls is None else head_cls.to(keys.dtype)
+    aw = ((keys * hc).sum(-1) * inv_sqrt_d).clamp(-ACT_CLAMP, ACT_CLAMP)
+    neg = torch.finfo(aw.dtype).min
+    row_max = torch.where(valid, aw, torch.full((), neg, dtype=aw.dtype)).amax(-1, keepdim=True)
+    row_max = torch.where(valid.any(-1, keepdim=True), row_max, torch.zeros_like(row_max))
+    e = torch.exp(aw - row_max) * valid.to(aw.dtype)
+    w = e / e.sum(-1, keepdim=True).clamp_min(1e-6)
+    return torch.nan_to_num((w.unsqueeze(-1) * keys).sum(1), nan=0.0, posinf=0.0, neginf=0.0)
+
+
+def kbar_pages(keys_cache, head_cls, block_table, seq_lens, kbar, tail_blocks=0):
+    """``KBarCache.put`` for every used page (headcls_scores_prefill,
+    dash_stage0.py:62-103) or ``refresh_tail`` (:123-148, tail_blocks > 0):
+    kbar[block_table[r, b]] = summary of the block's real keys for the
+    request's blocks b < ceil(seq_len / page) (only the last tail_blocks).
+    keys_cache [num_pages, page, d]; returns the updated copy of kbar."""
+    kbar = kbar.clone()
+    page = keys_cache.shape[1]
+    for r in range(block_table.shape[0]):
+        sl = int(seq_lens[r])
+        nb = min(-(-sl // page), block_table.shape[1])
+        blks = range(max(nb - tail_blocks, 0), nb) if tail_blocks > 0 else range(nb)
+        for b in blks:
+            pg = int(block_table[r, b])
+            valid = (torch.arange(page) < sl - b * page)[None]
+            kbar[pg] = kbar_summaries(keys_cache[pg][None].to(kbar.dtype), valid, head_cls)[0]
+    return kbar
+
+
+def kbar_scores(q, kbar, block_table, seq_lens, width, page, local_blocks, dql=None, row_req=None,
+                row_pos=None):
+    """``headcls_scores_decode`` (dash_stage0.py:151-199; prefill rows as
+    ``_score_rows``, :45-58) off the summary cache: row n of request r at
+    position pos scores block b as clamp(q . kbar[block_table[r, b]] / sqrt d,
+    +-1e4) when b <= pos // page - local_blocks and b * page < seq_lens[r], else
+    SCORE_NEG.  Decode rows (row_req / row_pos None): r = n // dql, pos =
+    seq_lens[r] - dql + n % dql.  Returns [nrows, width]."""
+    n_rows, d = q.shape
+    out = torch.full((n_rows, width), SCORE_NEG, dtype=kbar.dtype)
+    for n in range(n_rows):
+        r = int(row_req[n]) if row_req is not None else n // dql
+        sl = int(seq_lens[r])
+        pos = int(row_pos[n]) if row_pos is not None else sl - dql + n % dql
+        if pos < 0:
+            continue
+        for b in range(min(width, block_table.shape[1])):
+            if b <= pos // page - local_blocks and b * page < sl:
+                z = (q[n].to(kbar.dtype) @ kbar[int(block_table[r, b])]) / math.sqrt(d)
+                out[n, b] = z.clamp(-ACT_CLAMP, ACT_CLAMP)
+    return out
+
+
 def block_max_scores(q, k, pos, seg, block_size, num_key_blocks, local_window=None):
     """Fused indexer block-max score: ``max_{j in blk, seg <= j < local_start} q.k_j``.
 

@@ -465,3 +465,39 @@ def test_paged_decode_matches_key_loop_and_page_permutation():
     want0 = _paged_brute(q, kc, vc, topk, bias, bt, sl, dql, 0, 0.5)
     assert (want0[3] == 0).all()                                   # empty row -> zeros
     assert (O.paged_decode_attend(q, kc, vc, topk, bias, bt, sl, dql, 0, 0.5) - want0).abs().max() < 1e-10
+
+
+# ------------------------------------------------------- head_cls summary cache (paged)
+def test_kbar_cache_scores_equal_contiguous_scores():
+    """Scores off the per-page summary cache == the contiguous head_cls scorer
+    (itself pinned above) on each request's gathered keys; refresh_tail after an
+    append equals a full rebuild; no head_cls == plain mean."""
+    g = torch.Generator().manual_seed(41)
+    R, page, nb, d, dql, lb = 3, 8, 9, 16, 2, 2
+    npages = R * nb + 4
+    keys = _rand(npages, page, d, g=g)
+    bt = torch.randperm(npages, generator=g)[:R * nb].view(R, nb)
+    sl = torch.tensor([70, 33, 65])
+    hc = _rand(d, g=g)
+    kbar = O.kbar_pages(keys, hc, bt, sl, torch.zeros(npages, d))
+    q = _rand(R * dql, d, g=g)
+    got = O.kbar_scores(q, kbar, bt, sl, nb, page, lb, dql=dql)
+    for r in range(R):
+        k = keys[bt[r]].reshape(nb * page, d)[: int(sl[r])][None, None]
+        pos = (sl[r] - dql + torch.arange(dql))[None]
+        want = O.meanpool_block_scores(q[r * dql:(r + 1) * dql][None, None], k, pos, page, lb, head_cls=hc)[0, 0]
+        w = want.shape[-1]
+        assert (got[r * dql:(r + 1) * dql, :w] - want).abs().max() < 1e-12
+        assert (got[r * dql:(r + 1) * dql, w:] == O.SCORE_NEG).all()
+    # append 5 tokens to request 1 (its last page changes) and refresh the tail
+    keys2 = keys.clone()
+    sl2 = sl.clone()
+    sl2[1] += 5
+    keys2[bt[1, 4], 1:6] = _rand(5, d, g=g)
+    full = O.kbar_pages(keys2, hc, bt, sl2, torch.zeros(npages, d))
+    tail = O.kbar_pages(keys2, hc, bt, sl2, kbar, tail_blocks=2)
+    used = bt.flatten()
+    assert (full[used] - tail[used]).abs().max() < 1e-12
+    # no head_cls -> plain mean of the real keys
+    m = O.kbar_pages(keys, None, bt, sl, torch.zeros(npages, d))
+    assert (m[bt[1, 4]] - keys[bt[1, 4], :1].mean(0)).abs().max() < 1e-12

@@ -23,13 +23,11 @@
 // equal scores rank the LOWER id first); K rounds of "largest key below the
 // previous winner" (per-lane scan + 64-lane max) give the K best in
 // descending order, exactly and deterministically; invalid rows pad with -1.
-#include "common.h"
+#include "summary.h"
 
 namespace srswa {
 namespace {
 
-constexpr float kScoreNeg = -1.0e9f;   // HF/dash_attention.py:741
-constexpr float kActClamp = 1.0e4f;    // HF/dash_attention.py:747
 constexpr int kIdxWaves = 4;
 
 struct IndexK {
@@ -78,89 +76,10 @@ __global__ __launch_bounds__(kIdxWaves * kWave) void index_summary_kernel(IndexK
 #pragma unroll
   for (int e = 0; e < EPV; ++e) kb[e] = 0.f;
   const bool has_keys = k1 > k0;
-  if (needed && has_keys) {
-    const T* kbase = reinterpret_cast<const T*>(a.k) + (int64_t)b * a.k_sb + (int64_t)h * a.k_sh + c * EPV;
-    const float* hc = HC ? a.head_cls + c * EPV : nullptr;
-    float hcf[EPV];
-    if (HC) {
-#pragma unroll
-      for (int e = 0; e < EPV; ++e) hcf[e] = hc[e];
-    }
-    // walk the block in chunks of 64 rows (RPI rows per instruction)
-    constexpr int NI = kWave / RPI;      // instructions per 64-row chunk (== LPR)
-    float wsum = 0.f, wmax = -INFINITY;  // head_cls softmax state (HC)
-    for (int j0 = k0; j0 < k1; j0 += NI * RPI) {
-      uint4 kr[NI];
-#pragma unroll
-      for (int i = 0; i < NI; ++i) {
-        const int key = j0 + i * RPI + r;
-        kr[i] = key < k1 ? *reinterpret_cast<const uint4*>(kbase + (int64_t)key * a.k_st)
-                         : make_uint4(0, 0, 0, 0);
-      }
-      if (!HC) {
-#pragma unroll
-        for (int i = 0; i < NI; ++i) {
-          float f[EPV];
-          V::unpack(kr[i], f);
-#pragma unroll
-          for (int e = 0; e < EPV; ++e) kb[e] += f[e];
-        }
-      } else {
-        // per-key logits k.hc / sqrt(d): reduce-scatter over the LPR lanes of a row
-        float part[NI];
-#pragma unroll
-        for (int i = 0; i < NI; ++i) {
-          float f[EPV];
-          V::unpack(kr[i], f);
-          float s = 0.f;
-#pragma unroll
-          for (int e = 0; e < EPV; ++e) s = fmaf(f[e], hcf[e], s);
-          part[i] = s;
-        }
-#pragma unroll
-        for (int n = NI, o = LPR / 2; n > 1; n >>= 1, o >>= 1) {
-          const bool upper = (c & o) != 0;
-#pragma unroll
-          for (int jj = 0; jj < n / 2; ++jj) {
-            const float send = upper ? part[jj] : part[jj + n / 2];
-            const float keep = upper ? part[jj + n / 2] : part[jj];
-            part[jj] = keep + __shfl_xor(send, o, kWave);
-          }
-        }
-        const int key = j0 + c * RPI + r;                 // the key this lane owns
-        float aw = fminf(fmaxf(part[0] * p.inv_sqrt_d, -kActClamp), kActClamp);
-        aw = key < k1 ? aw : -INFINITY;
-        const float mnew = fmaxf(wmax, wave_max(aw));
-        const float alpha = exp2f((wmax - mnew) * kLog2e);
-        const float w = key < k1 ? exp2f((aw - mnew) * kLog2e) : 0.f;
-        wsum = wsum * alpha + wave_sum(w);
-        wmax = mnew;
-#pragma unroll
-        for (int e = 0; e < EPV; ++e) kb[e] *= alpha;
-        s_w[wave][r * NI + c] = w;
-        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-        __builtin_amdgcn_wave_barrier();
-        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-#pragma unroll
-        for (int i = 0; i < NI; ++i) {
-          const float wi = s_w[wave][r * NI + i];
-          float f[EPV];
-          V::unpack(kr[i], f);
-#pragma unroll
-          for (int e = 0; e < EPV; ++e) kb[e] = fmaf(wi, f[e], kb[e]);
-        }
-        __builtin_amdgcn_wave_barrier();
-      }
-    }
-    // sum the RPI row groups, then normalise
-#pragma unroll
-    for (int o = LPR; o < kWave; o <<= 1)
-#pragma unroll
-      for (int e = 0; e < EPV; ++e) kb[e] += __shfl_xor(kb[e], o, kWave);
-    const float norm = HC ? 1.f / fmaxf(wsum, 1e-6f) : 1.f / (float)(k1 - k0);
-#pragma unroll
-    for (int e = 0; e < EPV; ++e) kb[e] *= norm;
-  }
+  if (needed && has_keys)
+    summarize_rows<T, D, HC>(reinterpret_cast<const T*>(a.k) + (int64_t)b * a.k_sb + (int64_t)h * a.k_sh +
+                                 (int64_t)k0 * a.k_st + c * EPV,
+                             a.k_st, k1 - k0, HC ? a.head_cls + c * EPV : nullptr, p.inv_sqrt_d, s_w[wave], kb);
 
   if (a.kbar_out && r == 0) {
     float* dst = a.kbar_out + (int64_t)b * a.kb_sb + (int64_t)h * a.kb_sh + (int64_t)blk * a.kb_sn + c * EPV;

@@ -1,0 +1,179 @@
+// head_cls summary cache over a paged index-key cache: the serving stage 0 of
+// the DASH router on gfx950.
+//
+// Replaces (WHL!layers/attention/unlimited_dash_ops/dash_stage0.py):
+//   KBarCache.put + headcls_scores_prefill's summaries  :62-121
+//   KBarCache.refresh_tail                               :123-148
+//   headcls_scores_decode / _score_rows                  :45-58, :151-199
+// and the Triton pair K11/K12 that serves them (route_triton.py:37-126).
+//
+// kbar_pages_kernel: one wavefront per (request, logical block); the page's
+//   real keys are streamed once and reduced to an fp32 summary row written
+//   at the page id (summary.h).
+// kbar_scores_kernel: one wavefront per (query row, 64 blocks); 32 lanes x
+//   16 bytes read one fp32 summary row (D = 128) so two blocks are scored
+//   per step, the dot finished by a 32-lane butterfly.
+#include "summary.h"
+
+namespace srswa {
+namespace {
+
+constexpr int kKbWaves = 4;
+
+template <typename T, int D, bool HC>
+__global__ __launch_bounds__(kKbWaves * kWave) void kbar_pages_kernel(srswa_kbar_pages_args a, int per_req,
+                                                                      float inv_sqrt_d) {
+  using V = Vec16<T>;
+  constexpr int EPV = V::N;
+  constexpr int LPR = D / EPV;
+  __shared__ float s_w[kKbWaves][64];
+  const int wave = threadIdx.x / kWave, lane = threadIdx.x % kWave;
+  const int64_t w = (int64_t)blockIdx.x * kKbWaves + wave;
+  if (w >= (int64_t)a.R * per_req) return;
+  const int r = (int)(w / per_req), j = (int)(w % per_req);
+  const int sl = a.seq_lens[r];
+  const int nb = min(ceil_div(max(sl, 0), a.page_size), a.max_blocks);
+  const int blk = a.tail_blocks > 0 ? nb - a.tail_blocks + j : j;
+  if (blk < 0 || blk >= nb) return;
+  const int page = a.block_table[(int64_t)r * a.bt_sr + blk];
+  const int nkeys = min(a.page_size, sl - blk * a.page_size);
+  const int c = lane % LPR;
+  float kb[EPV];
+  summarize_rows<T, D, HC>(reinterpret_cast<const T*>(a.keys) + (int64_t)page * a.k_sp + c * EPV, a.k_st, nkeys,
+                           HC ? a.head_cls + c * EPV : nullptr, inv_sqrt_d, s_w[wave], kb);
+  if (lane < LPR) {
+    float* dst = a.kbar + (int64_t)page * a.kb_sp + c * EPV;
+#pragma unroll
+    for (int e = 0; e < EPV; e += 4) *reinterpret_cast<uint4*>(dst + e) = Vec16<float>::pack(kb + e);
+  }
+}
+
+// D fp32 dims = D / 4 lanes of 16 bytes; 64 / (D / 4) blocks per step
+template <int D>
+__global__ __launch_bounds__(kKbWaves * kWave) void kbar_scores_kernel(srswa_kbar_scores_args a, int chunks,
+                                                                       float inv_sqrt_d) {
+  constexpr int LPB = D / 4;               // lanes per summary row
+  constexpr int BPS = kWave / LPB;         // blocks per step
+  const int wave = threadIdx.x / kWave, lane = threadIdx.x % kWave;
+  const int64_t w = (int64_t)blockIdx.x * kKbWaves + wave;
+  if (w >= (int64_t)a.nrows * chunks) return;
+  const int n = (int)(w / chunks), ch = (int)(w % chunks);
+  const int r = a.row_req ? a.row_req[n] : n / a.dql;
+  const int sl = a.seq_lens[r];
+  const int pos = a.row_pos ? a.row_pos[n] : sl - a.dql + n % a.dql;
+  const int qblk = pos >= 0 ? pos / a.page_size : -1;
+  const int lim = min(min(qblk - a.local_blocks, ceil_div(max(sl, 0), a.page_size) - 1), a.max_blocks - 1);
+  const int sub = lane / LPB, c = lane % LPB;
+  const float4 qv = *reinterpret_cast<const float4*>(a.q + (int64_t)n * a.q_sn + c * 4);
+  float* out = a.scores + (int64_t)n * a.sc_sn;
+  const int b0 = ch * kWave;
+  for (int s = 0; s < kWave; s += BPS) {
+    const int blk = b0 + s + sub;
+    const bool remote = blk <= lim && pos >= 0;
+    float z = 0.f;
+    if (remote) {
+      const int page = a.block_table[(int64_t)r * a.bt_sr + blk];
+      const float4 kv = *reinterpret_cast<const float4*>(a.kbar + (int64_t)page * a.kb_sp + c * 4);
+      z = qv.x * kv.x + qv.y * kv.y + qv.z * kv.z + qv.w * kv.w;
+    }
+#pragma unroll
+    for (int o = LPB / 2; o >= 1; o >>= 1) z += __shfl_xor(z, o, kWave);
+    if (c == 0 && blk < a.width)
+      out[blk] = remote ? fminf(fmaxf(z * inv_sqrt_d, -kActClamp), kActClamp) : kScoreNeg;
+  }
+}
+
+bool al16k(const void* p) { return ((uintptr_t)p & 15u) == 0; }
+
+template <typename T, bool HC>
+void launch_pages(const srswa_kbar_pages_args& a, int per_req, float inv, hipStream_t st) {
+  const int64_t waves = (int64_t)a.R * per_req;
+  const dim3 grid((unsigned)((waves + kKbWaves - 1) / kKbWaves));
+  if (a.D == 64)
+    hipLaunchKernelGGL((kbar_pages_kernel<T, 64, HC>), grid, dim3(kKbWaves * kWave), 0, st, a, per_req, inv);
+  else
+    hipLaunchKernelGGL((kbar_pages_kernel<T, 128, HC>), grid, dim3(kKbWaves * kWave), 0, st, a, per_req, inv);
+}
+
+template <typename T>
+void launch_pages_hc(const srswa_kbar_pages_args& a, int per_req, float inv, hipStream_t st) {
+  if (a.head_cls) launch_pages<T, true>(a, per_req, inv, st);
+  else launch_pages<T, false>(a, per_req, inv, st);
+}
+
+}  // namespace
+}  // namespace srswa
+
+using namespace srswa;
+
+extern "C" int srswa_kbar_pages(const srswa_kbar_pages_args* a, void* stream) {
+  if (!a || !a->keys || !a->block_table || !a->seq_lens || !a->kbar) {
+    set_error("kbar pages: null argument");
+    return SRSWA_INVALID;
+  }
+  if (a->R < 0 || a->max_blocks <= 0 || a->page_size <= 0 || a->tail_blocks < 0) {
+    set_error("kbar pages: bad sizes");
+    return SRSWA_INVALID;
+  }
+  if (!(a->D == 64 || a->D == 128) || a->k_dtype < 0 || a->k_dtype > 2) {
+    set_error("kbar pages: D=%d / dtype not supported", a->D);
+    return SRSWA_UNSUPPORTED;
+  }
+  const int eb = a->k_dtype == SRSWA_F32 ? 4 : 2;
+  if (!al16k(a->keys) || !al16k(a->kbar) || (a->k_sp * eb) % 16 || (a->k_st * eb) % 16 || (a->kb_sp * 4) % 16 ||
+      (a->head_cls && !al16k(a->head_cls))) {
+    set_error("kbar pages: rows must be 16-byte aligned");
+    return SRSWA_UNSUPPORTED;
+  }
+  if (a->R == 0) return SRSWA_OK;
+  const int per_req = a->tail_blocks > 0 ? std::min(a->tail_blocks, a->max_blocks) : a->max_blocks;
+  const float inv = 1.0f / sqrtf((float)a->D);
+  hipStream_t st = reinterpret_cast<hipStream_t>(stream);
+  switch (a->k_dtype) {
+    case SRSWA_F32: launch_pages_hc<float>(*a, per_req, inv, st); break;
+    case SRSWA_BF16: launch_pages_hc<bf16_t>(*a, per_req, inv, st); break;
+    default: launch_pages_hc<__half>(*a, per_req, inv, st); break;
+  }
+  const hipError_t e = hipGetLastError();
+  if (e != hipSuccess) {
+    set_error("kbar pages launch failed: %s", hipGetErrorString(e));
+    return SRSWA_LAUNCH;
+  }
+  return SRSWA_OK;
+}
+
+extern "C" int srswa_kbar_scores(const srswa_kbar_scores_args* a, void* stream) {
+  if (!a || !a->q || !a->kbar || !a->block_table || !a->seq_lens || !a->scores) {
+    set_error("kbar scores: null argument");
+    return SRSWA_INVALID;
+  }
+  if (a->nrows < 0 || a->R <= 0 || a->max_blocks <= 0 || a->width <= 0 || a->page_size <= 0 ||
+      a->local_blocks < 0 || ((!a->row_req || !a->row_pos) && (a->dql <= 0 || a->nrows != a->R * a->dql))) {
+    set_error("kbar scores: bad sizes");
+    return SRSWA_INVALID;
+  }
+  if (!(a->D == 64 || a->D == 128)) {
+    set_error("kbar scores: D=%d not supported (64, 128)", a->D);
+    return SRSWA_UNSUPPORTED;
+  }
+  if (!al16k(a->q) || !al16k(a->kbar) || (a->q_sn * 4) % 16 || (a->kb_sp * 4) % 16) {
+    set_error("kbar scores: rows must be 16-byte aligned");
+    return SRSWA_UNSUPPORTED;
+  }
+  if (a->nrows == 0) return SRSWA_OK;
+  const int chunks = ceil_div(a->width, kWave);
+  const int64_t waves = (int64_t)a->nrows * chunks;
+  const dim3 grid((unsigned)((waves + kKbWaves - 1) / kKbWaves));
+  const float inv = 1.0f / sqrtf((float)a->D);
+  hipStream_t st = reinterpret_cast<hipStream_t>(stream);
+  if (a->D == 64)
+    hipLaunchKernelGGL(kbar_scores_kernel<64>, grid, dim3(kKbWaves * kWave), 0, st, *a, chunks, inv);
+  else
+    hipLaunchKernelGGL(kbar_scores_kernel<128>, grid, dim3(kKbWaves * kWave), 0, st, *a, chunks, inv);
+  const hipError_t e = hipGetLastError();
+  if (e != hipSuccess) {
+    set_error("kbar scores launch failed: %s", hipGetErrorString(e));
+    return SRSWA_LAUNCH;
+  }
+  return SRSWA_OK;
+}

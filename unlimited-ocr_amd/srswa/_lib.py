@@ -150,6 +150,36 @@ class PagedDecodeArgs(ctypes.Structure):
     ]
 
 
+class KbarPagesArgs(ctypes.Structure):
+    """Mirror of ``srswa_kbar_pages_args``."""
+
+    _fields_ = [
+        ("keys", _vp), ("k_sp", _i64), ("k_st", _i64),
+        ("head_cls", _vp),
+        ("block_table", _vp), ("bt_sr", _i64),
+        ("seq_lens", _vp),
+        ("kbar", _vp), ("kb_sp", _i64),
+        ("R", _i32), ("max_blocks", _i32), ("page_size", _i32), ("D", _i32), ("tail_blocks", _i32),
+        ("k_dtype", _i32),
+    ]
+
+
+class KbarScoresArgs(ctypes.Structure):
+    """Mirror of ``srswa_kbar_scores_args``."""
+
+    _fields_ = [
+        ("q", _vp), ("q_sn", _i64),
+        ("kbar", _vp), ("kb_sp", _i64),
+        ("block_table", _vp), ("bt_sr", _i64),
+        ("seq_lens", _vp),
+        ("row_req", _vp),
+        ("row_pos", _vp),
+        ("scores", _vp), ("sc_sn", _i64),
+        ("nrows", _i32), ("R", _i32), ("dql", _i32), ("max_blocks", _i32), ("width", _i32),
+        ("page_size", _i32), ("local_blocks", _i32), ("D", _i32),
+    ]
+
+
 class RouteArgs(ctypes.Structure):
     """Mirror of ``srswa_route_args``."""
 
@@ -181,6 +211,8 @@ SIGNATURES = {
     "srswa_gather_bwd": (ctypes.c_int, [ctypes.POINTER(BwdArgs), _vp, ctypes.c_size_t, _vp]),
     "srswa_block_max_score": (ctypes.c_int, [ctypes.POINTER(BlockMaxArgs), _vp]),
     "srswa_dash_route": (ctypes.c_int, [ctypes.POINTER(RouteArgs), _vp]),
+    "srswa_kbar_pages": (ctypes.c_int, [ctypes.POINTER(KbarPagesArgs), _vp]),
+    "srswa_kbar_scores": (ctypes.c_int, [ctypes.POINTER(KbarScoresArgs), _vp]),
     "srswa_gather_decode_paged_workspace": (None, [ctypes.POINTER(PagedDecodeArgs), _szp, _szp]),
     "srswa_gather_decode_paged": (ctypes.c_int, [ctypes.POINTER(PagedDecodeArgs), _vp, ctypes.c_size_t, _vp,
                                                  ctypes.c_size_t, _vp]),
@@ -189,7 +221,8 @@ SIGNATURES = {
 STRUCTS = {"srswa_decode_args": DecodeArgs, "srswa_index_args": IndexArgs,
            "srswa_fwd_args": FwdArgs, "srswa_bwd_args": BwdArgs,
            "srswa_blockmax_args": BlockMaxArgs, "srswa_route_args": RouteArgs,
-           "srswa_paged_decode_args": PagedDecodeArgs}
+           "srswa_paged_decode_args": PagedDecodeArgs, "srswa_kbar_pages_args": KbarPagesArgs,
+           "srswa_kbar_scores_args": KbarScoresArgs}
 
 _lib = None
 _lock = threading.Lock()

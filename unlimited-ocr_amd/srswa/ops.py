@@ -342,6 +342,61 @@ def gather_decode_paged(q, k_cache, v_cache, topk_idx, blk_bias, block_table, se
 
 
 # ---------------------------------------------------------------------------
+# head_cls summary cache over a paged index-key cache
+# ---------------------------------------------------------------------------
+def kbar_pages(keys_cache, head_cls, block_table, seq_lens, kbar, *, tail_blocks=0):
+    """Write the summary row of every used page (or each request's last
+    ``tail_blocks`` pages) into ``kbar`` [num_pages, D] fp32, in place.
+    keys_cache [num_pages, page_size, D] (bf16/fp16/fp32); head_cls [D] or None
+    (plain mean); block_table [R, max_blocks]; seq_lens [R]."""
+    _require_cuda(keys_cache, head_cls, block_table, seq_lens, kbar)
+    npages, page, D = keys_cache.shape
+    if keys_cache.stride(-1) != 1 or kbar.stride(-1) != 1 or kbar.dtype != torch.float32:
+        raise UnsupportedShape("keys / kbar rows must be contiguous, kbar fp32")
+    hc = None if head_cls is None else head_cls.detach().to(torch.float32).contiguous()
+    bt = _i32(block_table)
+    if bt.stride(-1) != 1:
+        bt = bt.contiguous()
+    sl = _i32(seq_lens).contiguous()
+    a = _lib.KbarPagesArgs(keys=keys_cache.data_ptr(), k_sp=keys_cache.stride(0), k_st=keys_cache.stride(1),
+                           head_cls=_lib.ptr(hc), block_table=bt.data_ptr(), bt_sr=bt.stride(0),
+                           seq_lens=sl.data_ptr(), kbar=kbar.data_ptr(), kb_sp=kbar.stride(0),
+                           R=bt.shape[0], max_blocks=bt.shape[1], page_size=page, D=D,
+                           tail_blocks=int(tail_blocks), k_dtype=_lib.dtype_code(keys_cache.dtype))
+    _lib.check(_lib.lib().srswa_kbar_pages(ctypes.byref(a), _lib.stream_ptr(kbar.device)), "srswa_kbar_pages")
+    return kbar
+
+
+def kbar_scores(q, kbar, block_table, seq_lens, *, width, page_size, local_blocks, dql=None, row_req=None,
+                row_pos=None, out=None):
+    """Scores [nrows, width] fp32 of index queries q [nrows, D] (fp32) against
+    the cached page summaries (SCORE_NEG off the remote blocks).  Decode rows
+    by default (request n // dql at seq_len - dql + n % dql), or explicit
+    per-row request / position tensors."""
+    _require_cuda(q, kbar, block_table, seq_lens, row_req, row_pos, out)
+    nrows, D = q.shape
+    qf = q.to(torch.float32)
+    if qf.stride(-1) != 1:
+        qf = qf.contiguous()
+    bt = _i32(block_table)
+    if bt.stride(-1) != 1:
+        bt = bt.contiguous()
+    sl = _i32(seq_lens).contiguous()
+    rr = None if row_req is None else _i32(row_req).contiguous()
+    rp = None if row_pos is None else _i32(row_pos).contiguous()
+    if out is None:
+        out = torch.empty(nrows, int(width), dtype=torch.float32, device=q.device)
+    a = _lib.KbarScoresArgs(q=qf.data_ptr(), q_sn=qf.stride(0), kbar=kbar.data_ptr(), kb_sp=kbar.stride(0),
+                            block_table=bt.data_ptr(), bt_sr=bt.stride(0), seq_lens=sl.data_ptr(),
+                            row_req=_lib.ptr(rr), row_pos=_lib.ptr(rp), scores=out.data_ptr(),
+                            sc_sn=out.stride(0), nrows=nrows, R=bt.shape[0], dql=int(dql or 0),
+                            max_blocks=bt.shape[1], width=int(width), page_size=int(page_size),
+                            local_blocks=int(local_blocks), D=D)
+    _lib.check(_lib.lib().srswa_kbar_scores(ctypes.byref(a), _lib.stream_ptr(q.device)), "srswa_kbar_scores")
+    return out
+
+
+# ---------------------------------------------------------------------------
 # DASH router
 # ---------------------------------------------------------------------------
 def dash_route(block_scores, block_cand, p):
