@@ -305,6 +305,73 @@ def bench_fwdbwd(args):
                          "kernel": "fwd_kernel + delta/touch/dq/dkv kernels"}}
 
 
+def bench_paged(args):
+    """Config 3 over the serving (paged) cache: the same selections and bytes as
+    the default leg, each sequence's blocks in randomly ordered pages."""
+    import torch
+    from srswa import ops, workloads as W
+    dev = torch.device("cuda:0")
+    B, H, D, K, BS, LW = 64, 10, 128, 8, 64, 512
+    c = W.paged_decode_config(B=B, H=H, D=D, k=K, block_size=BS, local_window=LW, device=dev)
+    q = c["q"].view(B, H, D)
+    launch, out = ops.prepare_gather_decode_paged(q, c["k_cache"], c["v_cache"], c["topk"].to(dev), None,
+                                                  c["block_table"].to(dev), c["seq_lens"].to(dev),
+                                                  decode_query_len=1, local_blocks=c["local_blocks"],
+                                                  scale=c["scale"])
+    ms = _time_launches(launch, args.steps, args.warmup, dev)
+    nbytes = W.decode_bytes(B, H, D, K, BS, LW)
+    achieved = nbytes / (ms * 1e-3) / 1e9
+    return {"metric": "paged decode sparse-attn tokens/s (config 3 over randomly ordered KV pages)",
+            "value": B / (ms * 1e-3), "unit": "tokens/s", "n_gpus": 1, "steps": args.steps,
+            "warmup": args.warmup, "ms_per_step": ms, "higher_is_better": True, "scaling": "weak",
+            "vs_baseline": None, "dtype": "bf16", "data": "synthetic (seeded), pages in seeded random order",
+            "config": {"workload": "config 3, paged [num_pages, 64, 10, 128] bf16 cache", "B": B,
+                       "num_pages": c["num_pages"]},
+            "roofline": {"bound": "hbm", "achieved": achieved, "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                         "frac": achieved / HBM_PEAK_GBS, "traffic": None, "algorithmic_bytes_per_launch": nbytes,
+                         "kernel": "srswa::decode_kernel<bf16,bf16,128,8,paged> + decode_merge_kernel"}}
+
+
+def bench_dash(args):
+    """One serving DASH decode step on config 3's paged cache: head_cls scores off
+    the per-page summary cache (one router head) -> router (entmax-1.5 top-16
+    window, 8 blocks, centred log-prior bias) -> paged decode with those blocks
+    and biases for all 10 kv heads."""
+    import torch
+    from srswa import ops, unlimited_dash_ops as U, workloads as W
+    dev = torch.device("cuda:0")
+    B, H, D, K, BS, LW = 64, 10, 128, 8, 64, 512
+    c = W.paged_decode_config(B=B, H=H, D=D, k=K, block_size=BS, local_window=LW, device=dev)
+    bt, sl = c["block_table"].to(dev), c["seq_lens"].to(dev)
+    cache = U.KBarCache(c["num_pages"], 128, dev)
+    hc = torch.randn(128, device=dev)
+    U.headcls_scores_prefill(idx_q=c["idx_q"], kv_cache=c["idx_k_cache"], block_table=bt,
+                             cu_seqlens_q=torch.arange(B + 1, device=dev), seq_lens=sl, context_lens=sl - 1,
+                             head_cls=hc, max_block=bt.shape[1], block_size=BS, local_blocks=LW // BS, cache=cache)
+    p = dict(idx_scale=128.0 / math.sqrt(128), floor=1e-4, sigma=1.0, K=K, topm=16)
+    q = c["q"].view(B, H, D)
+    out = torch.empty_like(q)
+
+    def step():
+        cache.refresh_tail(kv_cache=c["idx_k_cache"], block_table=bt, seq_lens=sl, head_cls=hc, block_size=BS,
+                           tail_pages=2)
+        sc = U.headcls_scores_decode(idx_q=c["idx_q"], cache=cache, block_table=bt, seq_lens=sl,
+                                     max_block=bt.shape[1], block_size=BS, local_blocks=LW // BS, decode_query_len=1)
+        topi, bias, valid = ops.dash_route(sc[0][:, None, :], None, p)           # [B, 1, K]
+        topi = torch.where(valid, topi, -1).to(torch.int32)[:, 0]                 # [B, K]
+        U.dash_sparse_attn_decode(q, c["k_cache"], c["v_cache"], topi[None].expand(H, B, K),
+                                  bias[:, 0][None].expand(H, B, K), bt, sl, H, c["scale"], out, 1,
+                                  local_blocks=LW // BS, sparse_block_size=BS)
+
+    ms = _time_launches(step, args.steps, args.warmup, dev)
+    return {"metric": "DASH serving decode step tokens/s (summary-cache scores -> router -> paged decode)",
+            "value": B / (ms * 1e-3), "unit": "tokens/s", "n_gpus": 1, "steps": args.steps,
+            "warmup": args.warmup, "ms_per_step": ms, "higher_is_better": True, "scaling": "weak",
+            "vs_baseline": None, "dtype": "bf16", "data": "synthetic (seeded)",
+            "config": {"workload": "config 3 paged cache, one router head (d 128), top-16 window, 8 blocks + "
+                                   "512-token window, 10 kv heads", "B": B, "max_blocks": int(bt.shape[1])}}
+
+
 def bench_copycal(args):
     """Calibration for the HBM traffic counters: a plain device copy of a known
     size (4 GiB read + 4 GiB written per launch, far beyond the 256 MB
@@ -327,7 +394,7 @@ def main():
     ap.add_argument("--steps", type=int, default=200)
     ap.add_argument("--warmup", type=int, default=20)
     ap.add_argument("--config", default="decode",
-                    choices=["decode", "indexer", "prefill", "fwdbwd", "copycal"])
+                    choices=["decode", "indexer", "prefill", "fwdbwd", "paged", "dash", "copycal"])
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--no-check", action="store_true", help="skip the oracle spot check")
     ap.add_argument("--cpu-budget", type=float, default=12.0)
@@ -337,7 +404,7 @@ def main():
               "(no multi-GPU path); use --gpus 1", file=sys.stderr)
         sys.exit(2)
     fn = {"decode": bench_decode, "indexer": bench_indexer, "prefill": bench_prefill,
-          "fwdbwd": bench_fwdbwd, "copycal": bench_copycal}[args.config]
+          "fwdbwd": bench_fwdbwd, "paged": bench_paged, "dash": bench_dash, "copycal": bench_copycal}[args.config]
     res = fn(args)
     print(json.dumps(res), flush=True)
 

@@ -73,6 +73,45 @@ def decode_config(B=64, H=10, D=128, Lmax=131072, lo=4096, k=8, block_size=64,
                 block_size=block_size, local_window=local_window, scale=1.0 / math.sqrt(D))
 
 
+def paged_decode_config(B=64, H=10, D=128, Lmax=131072, lo=4096, k=8, block_size=64, local_window=512,
+                        dtype=torch.bfloat16, device=None, cfg=3, d_index=128):
+    """Config 3 over the serving cache layout: each sequence's blocks live in
+    pages [num_pages, block_size, H, D] dealt in a seeded random order (one page
+    per block, as the serving backend asserts), block_table [B, max_blocks],
+    seq_lens [B], per-kv-head selections topk [H, B, k] (config 3's indices),
+    plus an index-key page cache [num_pages, block_size, d_index] and one
+    router query per sequence for the stage-0 scorer."""
+    lengths = decode_lengths(B, lo, Lmax, cfg)
+    idx = decode_block_indices(lengths, H, k, block_size, local_window, cfg)
+    nb = (lengths + block_size - 1) // block_size
+    max_blocks = int(nb.max())
+    npages = int(nb.sum())
+    g = _gen(cfg, 0)
+    perm = torch.randperm(npages, generator=g).to(torch.int32)
+    bt = torch.zeros(B, max_blocks, dtype=torch.int32)
+    o = 0
+    for b in range(B):
+        n = int(nb[b])
+        bt[b, :n] = perm[o:o + n]
+        o += n
+    q = torch.randn(B, H, D, generator=g, dtype=torch.float32).to(dtype)
+    iq = torch.randn(B, d_index, generator=g, dtype=torch.float32)
+    gd = torch.Generator(device=device) if device is not None else g
+    if device is not None:
+        gd.manual_seed(SEED0 + cfg)
+    kw = dict(generator=gd, dtype=dtype, device=device) if device is not None else dict(generator=gd)
+    kc = torch.randn(npages, block_size, H, D, **kw)
+    vc = torch.randn(npages, block_size, H, D, **kw)
+    ikc = torch.randn(npages, block_size, d_index, **kw)
+    if device is None:
+        kc, vc, ikc = kc.to(dtype), vc.to(dtype), ikc.to(dtype)
+    else:
+        q, iq = q.to(device), iq.to(device)
+    return dict(q=q, k_cache=kc, v_cache=vc, idx_k_cache=ikc, idx_q=iq, topk=idx.permute(1, 0, 2).contiguous(),
+                block_table=bt, seq_lens=lengths.to(torch.int32), block_size=block_size,
+                local_blocks=local_window // block_size, scale=1.0 / math.sqrt(D), num_pages=npages)
+
+
 def decode_bytes(B, H, D, k, block_size, local_window, elem=2):
     """Algorithmic HBM bytes of one decode step: K and V of (k*BS + LW) keys per
     (b, h) plus q, o and the index tensor."""
