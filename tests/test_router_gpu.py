@@ -28,7 +28,8 @@ def _check(dev, sc, cand, p):
     assert err.max().item() <= 1e-5, err.max().item()
 
 
-@pytest.mark.parametrize("nblk,K,topm", [(2048, 12, 16), (300, 8, 64), (40, 12, 16), (10, 12, 16), (5, 3, 0)])
+@pytest.mark.parametrize("nblk,K,topm", [(2048, 12, 16), (3000, 12, 16), (5000, 8, 16), (300, 8, 64),
+                                        (40, 12, 16), (10, 12, 16), (5, 3, 0)])
 def test_route_random(dev, nblk, K, topm):
     g = torch.Generator().manual_seed(nblk + K)
     B, Lq = 4, 3

@@ -50,6 +50,10 @@ struct RouteK {
   float inv_sigma;
 };
 
+// NPL > 0: each lane keeps the order keys of its NPL blocks (j = lane + 64 i)
+// in registers, built once, so the M selection rounds never touch memory;
+// NPL == 0 rescans the row from memory every round (rows above 4096 blocks).
+template <int NPL>
 __global__ __launch_bounds__(256) void dash_route_kernel(RouteK p) {
 #pragma clang fp contract(off)
   const srswa_route_args& a = p.a;
@@ -73,14 +77,31 @@ __global__ __launch_bounds__(256) void dash_route_kernel(RouteK p) {
   };
 
   // top-M window: M rounds of "largest key below the previous one"
+  uint64_t keys[NPL > 0 ? NPL : 1];
+  if (NPL > 0) {
+#pragma unroll
+    for (int i = 0; i < NPL; ++i) {
+      const int j = lane + i * kWave;
+      bool isc;
+      keys[i] = j < n ? route_key(xval(j, isc), j) : 0ull;   // real keys are > 0
+    }
+  }
   uint64_t prev = ~0ull;
   int my_id = 0;
   for (int k = 0; k < M; ++k) {
     uint64_t best = 0;
-    for (int j = lane; j < n; j += kWave) {
-      bool isc;
-      const uint64_t key = route_key(xval(j, isc), j);
-      if (key < prev && key > best) best = key;
+    if (NPL > 0) {
+#pragma unroll
+      for (int i = 0; i < NPL; ++i) {
+        const uint64_t key = keys[i];
+        best = (key < prev && key > best) ? key : best;
+      }
+    } else {
+      for (int j = lane; j < n; j += kWave) {
+        bool isc;
+        const uint64_t key = route_key(xval(j, isc), j);
+        if (key < prev && key > best) best = key;
+      }
     }
     best = wave_max_key(best);
     prev = best;
@@ -161,8 +182,12 @@ extern "C" int srswa_dash_route(const srswa_route_args* a, void* stream) {
   k.K = std::max(1, std::min(a->K, M));
   k.inv_sigma = (float)(1.0 / a->sigma);
   const int64_t rows = (int64_t)a->B * a->Lq;
-  hipLaunchKernelGGL(dash_route_kernel, dim3((unsigned)((rows + 3) / 4)), dim3(256), 0,
-                     reinterpret_cast<hipStream_t>(stream), k);
+  const dim3 grid((unsigned)((rows + 3) / 4));
+  hipStream_t st = reinterpret_cast<hipStream_t>(stream);
+  if (a->nblk <= 8 * kWave) hipLaunchKernelGGL(dash_route_kernel<8>, grid, dim3(256), 0, st, k);
+  else if (a->nblk <= 32 * kWave) hipLaunchKernelGGL(dash_route_kernel<32>, grid, dim3(256), 0, st, k);
+  else if (a->nblk <= 64 * kWave) hipLaunchKernelGGL(dash_route_kernel<64>, grid, dim3(256), 0, st, k);
+  else hipLaunchKernelGGL(dash_route_kernel<0>, grid, dim3(256), 0, st, k);
   const hipError_t e = hipGetLastError();
   if (e != hipSuccess) {
     set_error("route launch failed: %s", hipGetErrorString(e));
