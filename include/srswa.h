@@ -316,6 +316,155 @@ typedef struct {
 
 int srswa_dash_route(const srswa_route_args* a, void* stream);
 
+/* ------------------------------------------------------------------------
+ * Page isolation and Page2D RoPE: the metadata step before scoring.
+ * Index arrays marked "i32/i64" take int32 or int64 elements, chosen by the
+ * matching *_i64 flag (0 = int32, 1 = int64).
+ * ---------------------------------------------------------------------- */
+
+/* One-token decode step of the page-isolation state and the Page2D
+ * coordinates, per request r (replaces _decode_meta_kernel and
+ * decode_meta_fused, WHL!layers/attention/unlimited_dash_ops/decode_meta_triton.py:18-104,246-315):
+ *   is_img = id >= 1000000 || id == image_token_id, is_mark = has_marker && id == page_token_id
+ *   carry-in (marker count, image run, prompt pages) from the slot of position
+ *   seq_lens[r] - 2 (zeros when < 0), then
+ *   img_page = is_img ? (marker > 0 ? marker - 1 : (run - 1) / per_page) : -1
+ *   pp = max(is_img ? marker : 0, carried pp), q_page = is_img ? img_page :
+ *   (marker - 1 - pp >= 0 ? marker - 1 - pp : -1);
+ *   the four per-slot states are written at slot_mapping[r] (clamped to
+ *   [0, n_slots)), the image page of every slot past seq_lens[r] in the last
+ *   block is reset to -1; coordinates: c_m = c_mark[row] + is_mark,
+ *   c_p = max(is_img ? c_m : 0, c_pp[row]), page = clamp(min(max(c_m - c_p, 0),
+ *   c_p), 0, max_pages - 1), tok = c_cnt[row, page] (then incremented), with
+ *   row = coord_row[r] clamped to [0, n_rows). */
+typedef struct {
+  const void* input_ids;     int32_t ids_i64;          /* [R] i32/i64                         */
+  const void* block_table;   int32_t bt_i64; int64_t bt_sr;  /* [R, bt_w] i32/i64 page ids    */
+  const void* seq_lens;      int32_t seq_i64;          /* [R] length including this token     */
+  const void* slot_mapping;  int32_t slot_i64;         /* [R] KV slot of this token           */
+  const int64_t* coord_row;                            /* [R] coordinate-state row            */
+  int32_t* s_page; int32_t* s_mark; int32_t* s_run; int32_t* s_pp;   /* [n_slots] state   */
+  int32_t* c_mark; int32_t* c_pp; int32_t* c_cnt; int64_t cnt_sr;    /* [n_rows], [n_rows, max_pages] */
+  int32_t* q_page;                                     /* [R] out                             */
+  int64_t* tok;  int64_t* page;                        /* [R] out coordinates                 */
+  int64_t image_token_id, page_token_id;
+  int32_t R, bt_w, n_slots, n_rows, max_pages, block_size, per_page, has_marker;
+} srswa_page_meta_args;
+
+int srswa_page_decode_meta(const srswa_page_meta_args* a, void* stream);
+
+/* Page-isolation candidate mask of the decode rows (replaces
+ * _decode_allow_kernel / decode_allow_fused, decode_meta_triton.py:107-163,318-351):
+ * per request r and column w < max_block, with W = min(max_block, bt_w),
+ * page = clamp(block_table[r, w], 0, num_blocks - 1) and (lo, hi) the min and
+ * max image page over the page's block_size slots (-1 when none):
+ *   same = w < W && w * block_size < seq_lens[r] && lo >= 0 && lo <= q_page[r] <= hi
+ *   out[r, w] = same || q_page[r] < 0 || no column of r is `same`.
+ * Workspace: partial[R * ceil(max_block / 64)] int32, no initial content. */
+typedef struct {
+  const void* block_table;   int32_t bt_i64; int64_t bt_sr;  /* [R, bt_w]                     */
+  const int32_t* s_page;     int64_t n_slots;          /* [n_slots] per-slot image page, 16-byte aligned; */
+                                                       /* n_slots >= num_blocks * block_size  */
+  const int32_t* q_page;                               /* [R]                                 */
+  const void* seq_lens;      int32_t seq_i64;          /* [R]                                 */
+  int8_t* out;               int64_t out_sr;           /* [R, max_block] 0/1                  */
+  int32_t R, bt_w, max_block, num_blocks, block_size;
+} srswa_page_allow_args;
+
+int srswa_page_decode_allow_workspace(const srswa_page_allow_args* a, size_t* scratch_bytes);
+int srswa_page_decode_allow(const srswa_page_allow_args* a, void* scratch, size_t scratch_bytes, void* stream);
+
+/* Local-window union of a candidate mask (replaces _local_union_kernel /
+ * local_union_fused, decode_meta_triton.py:212-243,392-422): q_blk =
+ * (seq_lens[r] - 1) / block_size, hi = clamp(q_blk, 0, max_block - 1),
+ * lo = clamp(q_blk - local_blocks + 1, 0, max_block - 1);
+ *   out[r, w] = (w < a_w && allow[r, w] != 0) || lo <= w <= hi   for w < min(max_block, o_w). */
+typedef struct {
+  const int8_t* allow;       int64_t a_sr;             /* [R, a_w]                            */
+  int8_t* out;               int64_t o_sr;             /* [R, o_w]                            */
+  const void* seq_lens;      int32_t seq_i64;          /* [R]                                 */
+  int32_t R, a_w, o_w, max_block, block_size, local_blocks;
+} srswa_local_union_args;
+
+int srswa_page_local_union(const srswa_local_union_args* a, void* stream);
+
+/* Page2D cos/sin table (replaces _cos_sin_2d_kernel / cos_sin_2d_fused,
+ * decode_meta_triton.py:166-209,354-389; PageRope2D.cos_sin,
+ * WHL!…/page2d_rope.py:108-127; DeepseekV2IndexerRotary2D.forward,
+ * HF/_sparse_base_impl.py:2049-2061): for token t and column j < dim,
+ * i = j mod dim/2,
+ *   ang = i < n_tok ? float(tok[t]) * inv_tok[i] : float(pm(page[t])) * inv_page[i - n_tok]
+ * (fp32 product; pm(p) = page_mod > 0 ? p mod page_mod (non-negative) : p),
+ * cos[t, j] = cos(ang), sin[t, j] = sin(ang) in fp32, stored as out_dtype. */
+typedef struct {
+  const void* tok;           int32_t tok_i64;          /* [T]                                 */
+  const void* page;          int32_t page_i64;         /* [T]                                 */
+  const float* inv_tok;                                /* [n_tok]                             */
+  const float* inv_page;                               /* [dim/2 - n_tok]                     */
+  void* cos;                 int64_t c_st;             /* [T, dim]                            */
+  void* sin;                 int64_t s_st;             /* [T, dim]                            */
+  int64_t page_mod;
+  int32_t T, dim, n_tok, out_dtype;                    /* srswa_dtype                         */
+} srswa_cos_sin_args;
+
+int srswa_page2d_cos_sin(const srswa_cos_sin_args* a, void* stream);
+
+/* Rotary embedding of one or two tensors with one cos/sin table (replaces
+ * apply_page2d_rope / apply_page2d_rope_pair and their kernels,
+ * WHL!…/page2d_rope.py:130-324; transformers' llama apply_rotary_pos_emb
+ * that the HF indexer imports and applies, HF/_sparse_base_impl.py:39-41,3049):
+ * token n = (b, s), head h,
+ * with x1 / x2 the two halves of the head:
+ *   o = x * cos + rotate_half(x) * sin,  rotate_half(x) = (-x2, x1)
+ * each product and the sum rounded to the tensor dtype (the eager torch
+ * order).  x, y, o*, cos, sin share one dtype; y = NULL -> one tensor. */
+typedef struct {
+  const void* x;  int64_t x_sb, x_ss, x_sh;            /* [B, S, HX, hd]  (any strides, dim 1) */
+  void* ox;       int64_t ox_sb, ox_ss, ox_sh;
+  const void* y;  int64_t y_sb, y_ss, y_sh;            /* [B, S, HY, hd] or NULL              */
+  void* oy;       int64_t oy_sb, oy_ss, oy_sh;
+  const void* cos; int64_t c_sb, c_ss;                 /* [B, S, hd]                          */
+  const void* sin; int64_t s_sb, s_ss;
+  int32_t B, S, HX, HY, head_dim, dtype;               /* srswa_dtype                         */
+} srswa_rope_args;
+
+int srswa_page2d_rope(const srswa_rope_args* a, void* stream);
+
+/* Per-block image-page bounds (PageIsolationState.block_page_bounds,
+ * WHL!…/page_state.py:315-328; the prefill bmin / bmax of
+ * _uocr_dash_decode_allow, HF/modeling_unlimitedocr.py:498-510): for row b and
+ * block k < nblk over ids[b, k*bs .. k*bs+bs) (positions >= L count as -1),
+ *   hi = max id (or -1), lo = min id >= 0 (or -1 when hi < 0). */
+typedef struct {
+  const void* ids;           int32_t ids_i64; int64_t id_sb;   /* [B, L] page id per token, -1 = none */
+  int32_t* bounds;           int64_t bd_sb;            /* [B, nblk, 2] (lo, hi)               */
+  int32_t B, L, nblk, block_size;
+} srswa_block_bounds_args;
+
+int srswa_page_block_bounds(const srswa_block_bounds_args* a, void* stream);
+
+/* Page-aware candidate mask of query rows (the page-aware branch of
+ * _build_kl_candidate_mask, HF/_sparse_base_impl.py:2629-2649,2706-2737, and
+ * the decode rows of _uocr_dash_decode_allow, HF/modeling_unlimitedocr.py:512-528):
+ * row (b, i) with query page qp = qpage[b, clamp(pos[b, i], 0, qlen - 1)]
+ * (pos = NULL: qp = qpage[b, i]); for blocks k < nbd (those with bounds)
+ *   range_test = 0: same[k] = qp >= 0 && block k of ids holds a token with
+ *                   page id qp (token-level; decided from the bounds when
+ *                   hi - lo <= 1, by scanning the block's ids otherwise)
+ *   range_test = 1: same[k] = qp >= 0 && lo <= qp <= hi (ids may be NULL)
+ * and same[k] = 0 for nbd <= k < nblk;
+ *   out[b, i, k] = same[k] || no k of the row is `same`. */
+typedef struct {
+  const int32_t* bounds;     int64_t bd_sb;            /* [B, nbd, 2] from srswa_page_block_bounds */
+  const void* ids;           int32_t ids_i64; int64_t id_sb;   /* [B, L] the ids the bounds came from */
+  const void* qpage;         int32_t qp_i64; int64_t qp_sb;    /* [B, qlen]                   */
+  const void* pos;           int32_t pos_i64; int64_t pos_sb;  /* [B, nq] or NULL             */
+  uint8_t* out;              int64_t o_sb, o_sq;       /* [B, nq, nblk] bool                  */
+  int32_t B, nq, qlen, L, nblk, nbd, block_size, range_test;
+} srswa_candidate_args;
+
+int srswa_page_candidate_mask(const srswa_candidate_args* a, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -37,7 +37,10 @@ def test_oracle_reproduces_fixtures():
     r = load("router")
     xi, bias, valid = O.infer_route_select(r["scores"], r["cand"], r["idx_scale"], r["floor"], r["sigma"],
                                            r["K"], r["topm"])
-    assert torch.equal(xi, r["topi"]) and torch.equal(valid, r["valid"]) and torch.equal(bias, r["bias"])
+    assert torch.equal(xi, r["topi"]) and torch.equal(valid, r["valid"])
+    # fp32 logs of torch's vectorised CPU path differ in the last bits across
+    # host CPUs, so the bias is compared to a few ulps
+    assert (bias - r["bias"]).abs().max().item() <= 1e-6 * max(1.0, r["bias"].abs().max().item())
 
 
 @pytest.mark.gpu

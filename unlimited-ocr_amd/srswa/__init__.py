@@ -5,8 +5,10 @@ from PyTorch-ROCm.  Drop-in modules keep the reference's Python surface:
 
 * ``srswa.sparse_gather_triton``      -- triton_gather_attention, triton_block_max_score
 * ``srswa.sparse_gather_e2e_triton``  -- triton_gather_attention_e2e
-* ``srswa.indexer``                   -- indexer scoring / top-k / build_block_mask
-* ``srswa.ops``                       -- decode attention and the raw operators
+* ``srswa.unlimited_dash_ops``        -- the SGLang serving operators, module for module
+* ``srswa.patch``                     -- rebinding of the HF model's decode attend, router
+                                         scores / selection, page isolation and Page2D RoPE
+* ``srswa.ops`` / ``srswa.page_ops``  -- the raw operators over the C ABI
 """
 
 from . import _lib  # noqa: F401

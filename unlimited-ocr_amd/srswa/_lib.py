@@ -195,6 +195,101 @@ class RouteArgs(ctypes.Structure):
     ]
 
 
+class PageMetaArgs(ctypes.Structure):
+    """Mirror of ``srswa_page_meta_args``."""
+
+    _fields_ = [
+        ("input_ids", _vp), ("ids_i64", _i32),
+        ("block_table", _vp), ("bt_i64", _i32), ("bt_sr", _i64),
+        ("seq_lens", _vp), ("seq_i64", _i32),
+        ("slot_mapping", _vp), ("slot_i64", _i32),
+        ("coord_row", _vp),
+        ("s_page", _vp), ("s_mark", _vp), ("s_run", _vp), ("s_pp", _vp),
+        ("c_mark", _vp), ("c_pp", _vp), ("c_cnt", _vp), ("cnt_sr", _i64),
+        ("q_page", _vp), ("tok", _vp), ("page", _vp),
+        ("image_token_id", _i64), ("page_token_id", _i64),
+        ("R", _i32), ("bt_w", _i32), ("n_slots", _i32), ("n_rows", _i32), ("max_pages", _i32),
+        ("block_size", _i32), ("per_page", _i32), ("has_marker", _i32),
+    ]
+
+
+class PageAllowArgs(ctypes.Structure):
+    """Mirror of ``srswa_page_allow_args``."""
+
+    _fields_ = [
+        ("block_table", _vp), ("bt_i64", _i32), ("bt_sr", _i64),
+        ("s_page", _vp), ("n_slots", _i64),
+        ("q_page", _vp),
+        ("seq_lens", _vp), ("seq_i64", _i32),
+        ("out", _vp), ("out_sr", _i64),
+        ("R", _i32), ("bt_w", _i32), ("max_block", _i32), ("num_blocks", _i32), ("block_size", _i32),
+    ]
+
+
+class LocalUnionArgs(ctypes.Structure):
+    """Mirror of ``srswa_local_union_args``."""
+
+    _fields_ = [
+        ("allow", _vp), ("a_sr", _i64),
+        ("out", _vp), ("o_sr", _i64),
+        ("seq_lens", _vp), ("seq_i64", _i32),
+        ("R", _i32), ("a_w", _i32), ("o_w", _i32), ("max_block", _i32), ("block_size", _i32),
+        ("local_blocks", _i32),
+    ]
+
+
+class CosSinArgs(ctypes.Structure):
+    """Mirror of ``srswa_cos_sin_args``."""
+
+    _fields_ = [
+        ("tok", _vp), ("tok_i64", _i32),
+        ("page", _vp), ("page_i64", _i32),
+        ("inv_tok", _vp), ("inv_page", _vp),
+        ("cos", _vp), ("c_st", _i64),
+        ("sin", _vp), ("s_st", _i64),
+        ("page_mod", _i64),
+        ("T", _i32), ("dim", _i32), ("n_tok", _i32), ("out_dtype", _i32),
+    ]
+
+
+class RopeArgs(ctypes.Structure):
+    """Mirror of ``srswa_rope_args``."""
+
+    _fields_ = [
+        ("x", _vp), ("x_sb", _i64), ("x_ss", _i64), ("x_sh", _i64),
+        ("ox", _vp), ("ox_sb", _i64), ("ox_ss", _i64), ("ox_sh", _i64),
+        ("y", _vp), ("y_sb", _i64), ("y_ss", _i64), ("y_sh", _i64),
+        ("oy", _vp), ("oy_sb", _i64), ("oy_ss", _i64), ("oy_sh", _i64),
+        ("cos", _vp), ("c_sb", _i64), ("c_ss", _i64),
+        ("sin", _vp), ("s_sb", _i64), ("s_ss", _i64),
+        ("B", _i32), ("S", _i32), ("HX", _i32), ("HY", _i32), ("head_dim", _i32), ("dtype", _i32),
+    ]
+
+
+class BlockBoundsArgs(ctypes.Structure):
+    """Mirror of ``srswa_block_bounds_args``."""
+
+    _fields_ = [
+        ("ids", _vp), ("ids_i64", _i32), ("id_sb", _i64),
+        ("bounds", _vp), ("bd_sb", _i64),
+        ("B", _i32), ("L", _i32), ("nblk", _i32), ("block_size", _i32),
+    ]
+
+
+class CandidateArgs(ctypes.Structure):
+    """Mirror of ``srswa_candidate_args``."""
+
+    _fields_ = [
+        ("bounds", _vp), ("bd_sb", _i64),
+        ("ids", _vp), ("ids_i64", _i32), ("id_sb", _i64),
+        ("qpage", _vp), ("qp_i64", _i32), ("qp_sb", _i64),
+        ("pos", _vp), ("pos_i64", _i32), ("pos_sb", _i64),
+        ("out", _vp), ("o_sb", _i64), ("o_sq", _i64),
+        ("B", _i32), ("nq", _i32), ("qlen", _i32), ("L", _i32), ("nblk", _i32), ("nbd", _i32),
+        ("block_size", _i32), ("range_test", _i32),
+    ]
+
+
 # name -> (restype, argtypes) of every exported entry point
 SIGNATURES = {
     "srswa_version": (ctypes.c_int, []),
@@ -216,13 +311,24 @@ SIGNATURES = {
     "srswa_gather_decode_paged_workspace": (None, [ctypes.POINTER(PagedDecodeArgs), _szp, _szp]),
     "srswa_gather_decode_paged": (ctypes.c_int, [ctypes.POINTER(PagedDecodeArgs), _vp, ctypes.c_size_t, _vp,
                                                  ctypes.c_size_t, _vp]),
+    "srswa_page_decode_meta": (ctypes.c_int, [ctypes.POINTER(PageMetaArgs), _vp]),
+    "srswa_page_decode_allow_workspace": (ctypes.c_int, [ctypes.POINTER(PageAllowArgs), _szp]),
+    "srswa_page_decode_allow": (ctypes.c_int, [ctypes.POINTER(PageAllowArgs), _vp, ctypes.c_size_t, _vp]),
+    "srswa_page_local_union": (ctypes.c_int, [ctypes.POINTER(LocalUnionArgs), _vp]),
+    "srswa_page2d_cos_sin": (ctypes.c_int, [ctypes.POINTER(CosSinArgs), _vp]),
+    "srswa_page2d_rope": (ctypes.c_int, [ctypes.POINTER(RopeArgs), _vp]),
+    "srswa_page_block_bounds": (ctypes.c_int, [ctypes.POINTER(BlockBoundsArgs), _vp]),
+    "srswa_page_candidate_mask": (ctypes.c_int, [ctypes.POINTER(CandidateArgs), _vp]),
 }
 
 STRUCTS = {"srswa_decode_args": DecodeArgs, "srswa_index_args": IndexArgs,
            "srswa_fwd_args": FwdArgs, "srswa_bwd_args": BwdArgs,
            "srswa_blockmax_args": BlockMaxArgs, "srswa_route_args": RouteArgs,
            "srswa_paged_decode_args": PagedDecodeArgs, "srswa_kbar_pages_args": KbarPagesArgs,
-           "srswa_kbar_scores_args": KbarScoresArgs}
+           "srswa_kbar_scores_args": KbarScoresArgs, "srswa_page_meta_args": PageMetaArgs,
+           "srswa_page_allow_args": PageAllowArgs, "srswa_local_union_args": LocalUnionArgs,
+           "srswa_cos_sin_args": CosSinArgs, "srswa_rope_args": RopeArgs,
+           "srswa_block_bounds_args": BlockBoundsArgs, "srswa_candidate_args": CandidateArgs}
 
 _lib = None
 _lock = threading.Lock()

@@ -10,6 +10,12 @@ two kernel files (those are replaced file-for-file by
 * ``_block_scores_infer``  (HF/modeling_deepseekv2.py:380-430), stage0 "head_cls"
                            -> the head_cls / mean-pool indexer kernel
 * ``_infer_route_select``  (HF/modeling_deepseekv2.py:338-362) -> ``srswa.ops.dash_route``
+* page isolation and the Page2D indexer RoPE of ``_sparse_base_impl`` (reached as
+  ``modeling_deepseekv2._base``): ``DeepseekV2Indexer._build_kl_candidate_mask``
+  (HF/_sparse_base_impl.py:2706-2737), ``DeepseekV2IndexerRotary2D.forward``
+  (:2046-2061) and the module's ``_llama_apply_rotary_pos_emb`` (:39-41)
+  -> ``srswa.page_isolation``; with ``modeling_unlimitedocr`` given, also its
+  ``_uocr_dash_decode_allow`` (HF/modeling_unlimitedocr.py:481-528)
 
 Every replacement keeps the reference signature and return convention, runs
 the HIP kernels for device tensors, and hands host tensors (or a case the
@@ -21,7 +27,7 @@ from __future__ import annotations
 
 import torch
 
-from . import ops
+from . import ops, page_isolation
 from ._lib import UnsupportedShape
 
 SCORE_NEG = -1.0e9
@@ -38,12 +44,84 @@ def head_cls_block_scores(idx_q, idx_k, q_pos, nblk, block_size, local_blocks, h
     return scores[:, 0]
 
 
-def apply(modeling_deepseekv2) -> list:
+def _rebind(owner, name: str, make, done: list, label: str) -> None:
+    """owner.name = make(original); the original is kept once as
+    owner._srswa_orig_<name> so ``restore`` can put it back."""
+    keep = "_srswa_orig_" + name
+    orig = getattr(owner, keep, None) or getattr(owner, name, None)
+    if orig is None:
+        return
+    setattr(owner, keep, orig)
+    setattr(owner, name, make(orig))
+    done.append(label)
+
+
+def _unbind(owner, name: str) -> None:
+    keep = "_srswa_orig_" + name
+    if owner is not None and keep in vars(owner):
+        setattr(owner, name, vars(owner)[keep])
+        delattr(owner, keep)
+
+
+def _page_isolation(mod, base, done: list) -> None:
+    indexer_cls = getattr(base, "DeepseekV2Indexer", None)
+    if indexer_cls is not None:
+        def make_mask(orig):
+            def _build_kl_candidate_mask(self, pos_chunk, num_key_blocks, image_token_mask, batch, cq,
+                                         image_token_page_ids=None, query_token_page_ids=None):
+                if pos_chunk.is_cuda:
+                    try:
+                        return page_isolation.build_kl_candidate_mask(
+                            self, pos_chunk, num_key_blocks, image_token_mask, batch, cq,
+                            image_token_page_ids, query_token_page_ids)
+                    except UnsupportedShape:
+                        pass
+                return orig(self, pos_chunk, num_key_blocks, image_token_mask, batch, cq,
+                            image_token_page_ids, query_token_page_ids)
+            return _build_kl_candidate_mask
+        _rebind(indexer_cls, "_build_kl_candidate_mask", make_mask, done, "DeepseekV2Indexer._build_kl_candidate_mask")
+    rot_cls = getattr(base, "DeepseekV2IndexerRotary2D", None)
+    if rot_cls is not None:
+        def make_rot(orig):
+            def forward(self, x, tok_pos, page_pos):
+                if x.is_cuda:
+                    try:
+                        return page_isolation.rotary2d_forward(self, x, tok_pos, page_pos)
+                    except UnsupportedShape:
+                        pass
+                return orig(self, x, tok_pos, page_pos)
+            return forward
+        _rebind(rot_cls, "forward", make_rot, done, "DeepseekV2IndexerRotary2D.forward")
+    for owner in (base, mod):
+        if owner is not None and hasattr(owner, "_llama_apply_rotary_pos_emb"):
+            def make_rope(orig):
+                def _llama_apply_rotary_pos_emb(q, k, cos, sin, position_ids=None, unsqueeze_dim=1):
+                    return page_isolation.apply_rotary_pos_emb(q, k, cos, sin, position_ids, unsqueeze_dim,
+                                                               orig=orig)
+                return _llama_apply_rotary_pos_emb
+            _rebind(owner, "_llama_apply_rotary_pos_emb", make_rope, done,
+                    f"{getattr(owner, '__name__', 'module')}._llama_apply_rotary_pos_emb")
+
+
+def apply(modeling_deepseekv2, modeling_unlimitedocr=None) -> list:
     """Rebind the hot-path functions of a loaded ``modeling_deepseekv2`` module
-    (the reference's DASH overlay).  Returns the names rebound; calling it
-    twice is harmless (the originals are kept once)."""
+    (the reference's DASH overlay), of its ``_sparse_base_impl`` (``_base``)
+    and, when given, of ``modeling_unlimitedocr``.  Returns the names rebound;
+    calling it twice is harmless (the originals are kept once)."""
     mod = modeling_deepseekv2
     done = []
+    _page_isolation(mod, getattr(mod, "_base", None), done)
+    if modeling_unlimitedocr is not None:
+        def make_allow(orig):
+            def _uocr_dash_decode_allow(indexer, input_ids, cache):
+                if input_ids.is_cuda:
+                    try:
+                        return page_isolation.uocr_dash_decode_allow(indexer, input_ids, cache)
+                    except UnsupportedShape:
+                        pass
+                return orig(indexer, input_ids, cache)
+            return _uocr_dash_decode_allow
+        _rebind(modeling_unlimitedocr, "_uocr_dash_decode_allow", make_allow, done, "_uocr_dash_decode_allow")
     orig_decode = getattr(mod, "_srswa_orig_decode_attend", None) or getattr(mod, "_decode_attend", None)
     if orig_decode is not None:
         mod._srswa_orig_decode_attend = orig_decode
@@ -95,9 +173,15 @@ def apply(modeling_deepseekv2) -> list:
     return done
 
 
-def restore(modeling_deepseekv2) -> None:
+def restore(modeling_deepseekv2, modeling_unlimitedocr=None) -> None:
     """Undo ``apply``."""
     mod = modeling_deepseekv2
+    base = getattr(mod, "_base", None)
+    for owner, name in ((getattr(base, "DeepseekV2Indexer", None), "_build_kl_candidate_mask"),
+                        (getattr(base, "DeepseekV2IndexerRotary2D", None), "forward"),
+                        (base, "_llama_apply_rotary_pos_emb"), (mod, "_llama_apply_rotary_pos_emb"),
+                        (modeling_unlimitedocr, "_uocr_dash_decode_allow")):
+        _unbind(owner, name)
     if hasattr(mod, "_srswa_orig_decode_attend"):
         mod._decode_attend = mod._srswa_orig_decode_attend
         del mod._srswa_orig_decode_attend

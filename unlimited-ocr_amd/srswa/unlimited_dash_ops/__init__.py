@@ -1,0 +1,20 @@
+"""Drop-in for the reference's serving operators,
+``sglang.srt.layers.attention.unlimited_dash_ops`` (WHL!layers/attention/unlimited_dash_ops/),
+module for module, on the MI355X kernels:
+
+* ``attend_triton``       -- ``dash_sparse_attn_decode``
+* ``dash_stage0``         -- ``KBarCache``, ``headcls_scores_prefill``, ``headcls_scores_decode``
+* ``decode_meta_triton``  -- ``decode_meta_fused``, ``decode_allow_fused``, ``cos_sin_2d_fused``,
+                             ``local_union_fused``
+* ``page2d_rope``         -- ``PageRope2D``, ``apply_page2d_rope``, ``apply_page2d_rope_pair``,
+                             ``page_capacity``
+
+Every tensor the kernels see must live on the GPU (no host path).
+"""
+
+from .attend_triton import SPARSE_BLOCK_SIZE, dash_sparse_attn_decode  # noqa: F401
+from .dash_stage0 import KBarCache, headcls_scores_decode, headcls_scores_prefill  # noqa: F401
+from .decode_meta_triton import (  # noqa: F401
+    cos_sin_2d_fused, decode_allow_fused, decode_meta_fused, local_union_fused)
+from .page2d_rope import (  # noqa: F401
+    MIN_PAGE_TOKENS, PageRope2D, apply_page2d_rope, apply_page2d_rope_pair, page_capacity)

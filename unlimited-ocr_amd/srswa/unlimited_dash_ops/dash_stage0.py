@@ -1,46 +1,14 @@
-"""Drop-in for the serving-side DASH operators of the reference's SGLang
-integration (``sglang.srt.layers.attention.unlimited_dash_ops``), backed by the
-MI355X kernels:
-
-* ``dash_sparse_attn_decode`` -- WHL!layers/attention/unlimited_dash_ops/
-  attend_triton.py:600-715 (paged bias-aware decode, split-K + merge);
-* ``KBarCache``, ``headcls_scores_prefill``, ``headcls_scores_decode`` --
-  WHL!layers/attention/unlimited_dash_ops/dash_stage0.py:62-199 (one fp32
-  head_cls summary per KV page; decode scores off the cache).
-
-Same names, arguments and in-place output convention as the reference; every
-tensor must live on the GPU (no host path).
+"""Drop-in for ``sglang.srt.layers.attention.unlimited_dash_ops.dash_stage0``:
+``KBarCache``, ``headcls_scores_prefill``, ``headcls_scores_decode``
+(WHL!layers/attention/unlimited_dash_ops/dash_stage0.py:62-199: one fp32 head_cls
+summary per KV page, decode scores off the cache), on the MI355X summary kernels.
 """
 
 from __future__ import annotations
 
 import torch
 
-from . import ops
-
-SPARSE_BLOCK_SIZE = 128     # fallback page size, WHL!layers/attention/unlimited_dash_ops/common.py:10
-
-
-def dash_sparse_attn_decode(q, k_cache, v_cache, topk_idx, blk_bias, block_table, seq_lens, num_kv_heads,
-                            sm_scale, output, decode_query_len, local_blocks=0,
-                            sparse_block_size=SPARSE_BLOCK_SIZE, chunk_width=None, cg_rows=None):
-    """Bias-aware block-sparse decode over the paged cache, written into ``output``.
-
-    q [total_q, num_heads, D]; k_cache, v_cache [num_pages, page_size,
-    num_kv_heads, D]; topk_idx / blk_bias [num_kv_heads, total_q, K];
-    block_table [num_reqs, max_blocks]; seq_lens [num_reqs].  One page is one
-    sparse block (``sparse_block_size`` must equal the page size).
-    ``chunk_width`` / ``cg_rows`` (the reference's split-K sizing hints) are
-    accepted and unused: the split and its scratch are sized by the kernel."""
-    del chunk_width, cg_rows
-    if k_cache.shape[2] != int(num_kv_heads):
-        raise ValueError(f"k_cache has {k_cache.shape[2]} kv heads, num_kv_heads={num_kv_heads}")
-    if k_cache.shape[1] != int(sparse_block_size):
-        raise ValueError(f"page size {k_cache.shape[1]} != sparse_block_size {sparse_block_size}")
-    ops.gather_decode_paged(q, k_cache, v_cache, topk_idx, blk_bias, block_table, seq_lens,
-                            decode_query_len=decode_query_len, local_blocks=local_blocks, scale=sm_scale,
-                            out=output)
-    return None
+from .. import ops
 
 
 class KBarCache:
