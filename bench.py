@@ -19,6 +19,7 @@ from __future__ import annotations
 import argparse
 import json
 import math
+import types
 import os
 import re
 import sys
@@ -372,6 +373,99 @@ def bench_dash(args):
                                    "512-token window, 10 kv heads", "B": B, "max_blocks": int(bt.shape[1])}}
 
 
+def bench_page(args):
+    """Page isolation + Page2D RoPE.  Headline: the rotary applied to the main
+    branch's q and k of a 16k-token prefill ([16384, 10*128] bf16 each, one
+    launch), HBM-bound.  Beside it: the decode allow mask over config 3's paged
+    cache (64 requests, per-slot image pages of every live page read once) and
+    the whole one-token decode metadata step (page state + allow mask + local
+    union + cos/sin table + rotary of q, k, idx_q, idx_k)."""
+    import torch
+    from srswa import page_ops, unlimited_dash_ops as U, workloads as W
+    dev = torch.device("cuda:0")
+    g = torch.Generator(device=dev).manual_seed(7)
+    # --- rotary at prefill size
+    T, H, hd = 16384, 10, 128
+    x = torch.randn(T, H * hd, device=dev, generator=g).to(torch.bfloat16)
+    y = torch.randn(T, H * hd, device=dev, generator=g).to(torch.bfloat16)
+    rope = U.PageRope2D(hd, 10000.0, 256.0, 8)
+    tok = torch.randint(0, 4000, (T,), device=dev, generator=g)
+    page = torch.randint(0, 40, (T,), device=dev, generator=g)
+    cos, sin = rope.cos_sin(tok, page, torch.bfloat16)
+    ms_rope = _time_launches(lambda: page_ops.page2d_rope(x, cos, sin, hd, y=y), args.steps, args.warmup, dev)
+    rope_bytes = 2 * (2 * T * H * hd * 2) + 2 * T * hd * 2
+    rope_gbs = rope_bytes / (ms_rope * 1e-3) / 1e9
+    ms_cs = _time_launches(lambda: rope.cos_sin(tok, page, torch.bfloat16), args.steps, args.warmup, dev)
+    # --- decode allow mask over config 3's paged cache
+    B, BS = 64, 64
+    c = W.paged_decode_config(B=B, H=H, D=hd, k=8, block_size=BS, local_window=512, device=dev)
+    bt, sl = c["block_table"].to(dev), c["seq_lens"].to(dev)
+    npg, maxb = c["num_pages"], bt.shape[1]
+    s_page = torch.full((npg * BS,), -1, dtype=torch.int32, device=dev)
+    pos = torch.arange(maxb * BS, device=dev)
+    for r in range(B):                            # image pages of ~1135 tokens, text between them
+        L = int(sl[r])
+        p = pos[:L]
+        img = torch.where(p % 1200 < 1135, p // 1200, torch.full_like(p, -1)).to(torch.int32)
+        s_page[bt[r, p // BS].long() * BS + p % BS] = img
+    q_page = ((sl // 1200) // 2).to(torch.int32)
+    q_page[::5] = -1
+    out = torch.empty(B, maxb, dtype=torch.int8, device=dev)
+    allow = lambda: page_ops.page_decode_allow(bt, s_page, q_page, sl, max_block=maxb, num_blocks=npg,
+                                               block_size=BS, out=out)
+    ms_allow = _time_launches(allow, args.steps, args.warmup, dev)
+    live = int(((sl + BS - 1) // BS).sum())
+    allow_bytes = live * BS * 4 + live * 4 + B * maxb
+    allow_gbs = allow_bytes / (ms_allow * 1e-3) / 1e9
+    # --- one decode metadata step (page state, mask, union, cos/sin, rotary of both branches)
+    ps = types.SimpleNamespace(image_token_id=128815, page_token_id=128816, per_page_image_tokens=273,
+                               _slot_img_page=s_page, _slot_marker_cum=torch.zeros_like(s_page),
+                               _slot_img_run=torch.zeros_like(s_page), _slot_prompt_pages=torch.zeros_like(s_page),
+                               _ensure=lambda n, d: None)
+    rows = torch.arange(B, device=dev)
+    cs = types.SimpleNamespace(st_marker=torch.zeros(B, dtype=torch.int32, device=dev),
+                               st_pp=torch.zeros(B, dtype=torch.int32, device=dev),
+                               cnt=torch.zeros(B, 64, dtype=torch.int32, device=dev), max_pages=64,
+                               _ensure=lambda d: None, _rows=lambda layout: rows)
+    ids = torch.randint(10, 1000, (B,), device=dev, generator=g)
+    slot = bt[torch.arange(B, device=dev), ((sl - 1) // BS).long()].long() * BS + (sl - 1) % BS
+    qd = torch.randn(B, H * hd, device=dev, generator=g).to(torch.bfloat16)
+    kd = torch.randn(B, H * hd, device=dev, generator=g).to(torch.bfloat16)
+    iq = torch.randn(B, hd, device=dev, generator=g).to(torch.bfloat16)
+    ik = torch.randn(B, hd, device=dev, generator=g).to(torch.bfloat16)
+    cbuf = torch.empty(B, hd, dtype=torch.bfloat16, device=dev)
+    sbuf = torch.empty(B, hd, dtype=torch.bfloat16, device=dev)
+    union = torch.empty(B, maxb, dtype=torch.int8, device=dev)
+
+    def meta_step():
+        qp, (tk, pg) = U.decode_meta_fused(input_ids=ids, block_table=bt, seq_lens=sl, slot_mapping=slot,
+                                           page_state=ps, coord_state=cs, num_slots=npg * BS, block_size=BS)
+        al = U.decode_allow_fused(block_table=bt, page_state=ps, q_page=qp, seq_lens=sl, max_block=maxb,
+                                  num_blocks=npg, block_size=BS, out=out)
+        U.local_union_fused(allow=al, seq_lens=sl, out=union, max_block=maxb, block_size=BS, local_blocks=8)
+        cc, ss = U.cos_sin_2d_fused(rope=rope, tok_pos=tk, page_pos=pg, dtype=torch.bfloat16, out_cos=cbuf,
+                                    out_sin=sbuf)
+        U.apply_page2d_rope_pair(qd, kd, cc, ss, hd)
+        U.apply_page2d_rope_pair(iq, ik, cc, ss, hd)
+
+    ms_meta = _time_launches(meta_step, args.steps, args.warmup, dev)
+    return {"metric": "Page2D rotary of a 16k-token prefill's q and k (tokens/s)", "value": T / (ms_rope * 1e-3),
+            "unit": "tokens/s", "n_gpus": 1, "steps": args.steps, "warmup": args.warmup, "ms_per_step": ms_rope,
+            "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "bf16",
+            "data": "synthetic (seeded)",
+            "config": {"workload": "apply_page2d_rope_pair, q and k [16384, 10*128] bf16, cos/sin [16384, 128]",
+                       "T": T, "heads": H, "head_dim": hd},
+            "roofline": {"bound": "hbm", "achieved": rope_gbs, "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                         "frac": rope_gbs / HBM_PEAK_GBS, "traffic": None, "algorithmic_bytes_per_launch": rope_bytes,
+                         "kernel": "srswa::rope_kernel<bf16>"},
+            "cos_sin_table_us": ms_cs * 1e3,
+            "decode_allow": {"workload": "config 3 paged cache, 64 requests, per-slot image pages of every live page",
+                             "us": ms_allow * 1e3, "achieved_GBs": allow_gbs, "frac": allow_gbs / HBM_PEAK_GBS,
+                             "algorithmic_bytes": allow_bytes,
+                             "kernels": "page_allow_scan_kernel<64> + page_allow_open_kernel"},
+            "decode_meta_step_us": ms_meta * 1e3}
+
+
 def bench_copycal(args):
     """Calibration for the HBM traffic counters: a plain device copy of a known
     size (4 GiB read + 4 GiB written per launch, far beyond the 256 MB
@@ -394,7 +488,7 @@ def main():
     ap.add_argument("--steps", type=int, default=200)
     ap.add_argument("--warmup", type=int, default=20)
     ap.add_argument("--config", default="decode",
-                    choices=["decode", "indexer", "prefill", "fwdbwd", "paged", "dash", "copycal"])
+                    choices=["decode", "indexer", "prefill", "fwdbwd", "paged", "dash", "page", "copycal"])
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--no-check", action="store_true", help="skip the oracle spot check")
     ap.add_argument("--cpu-budget", type=float, default=12.0)
@@ -404,7 +498,7 @@ def main():
               "(no multi-GPU path); use --gpus 1", file=sys.stderr)
         sys.exit(2)
     fn = {"decode": bench_decode, "indexer": bench_indexer, "prefill": bench_prefill,
-          "fwdbwd": bench_fwdbwd, "paged": bench_paged, "dash": bench_dash, "copycal": bench_copycal}[args.config]
+          "fwdbwd": bench_fwdbwd, "paged": bench_paged, "dash": bench_dash, "page": bench_page, "copycal": bench_copycal}[args.config]
     res = fn(args)
     print(json.dumps(res), flush=True)
 

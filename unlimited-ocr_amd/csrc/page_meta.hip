@@ -106,55 +106,69 @@ __global__ __launch_bounds__(64) void page_meta_kernel(srswa_page_meta_args a) {
 }
 
 // ------------------------------------------------------------ decode allow
-// Pass 1: one wavefront per (request, 64 columns).  A page's block_size
-// image-page slots are read by LPP = BS/4 lanes with one 16-byte load each
-// (BS=64: four pages per load instruction, every 256-byte page read whole),
-// reduced to (min, max) by a butterfly inside the lane group; lane j of the
-// wave ends up with column c0 + j.  `same` is written as the mask byte and
-// the column count of the wave goes to partial[r, chunk] (a plain store, so
-// the workspace needs no clearing).
+// Pass 1: one wavefront per (request, 64 columns).  Lane j loads the page id
+// of column c0 + j (one coalesced load); a page's block_size image-page slots
+// are then read by LPP = BS/4 lanes with one 16-byte load each (BS=64: four
+// pages per load instruction, every 256-byte page read whole), the page ids
+// reaching the lane groups by shuffles, so all of a batch's loads are in
+// flight together (two dependent round trips per wave).  (min, max) is
+// reduced by a butterfly inside each lane group and lane j ends up with
+// column c0 + j.  `same` is written as the mask byte and the column count of
+// the wave goes to partial[r, chunk] (a plain store: no clearing needed).
 template <int BS>
 __global__ __launch_bounds__(64) void page_allow_scan_kernel(srswa_page_allow_args a, int32_t* partial,
                                                              int nchunk, int W) {
   constexpr int LPP = BS / 4;             // lanes per page
   constexpr int PPW = kWave / LPP;        // pages per load instruction
+  constexpr int ITER = kWave / PPW;       // load instructions per 64 columns
+  constexpr int NB = ITER < 16 ? ITER : 16;   // loads kept in flight per batch
   const int chunk = blockIdx.x;
   const int r = blockIdx.y;
   const int lane = threadIdx.x;
   const int c0 = chunk * kWave;
   const int32_t qp = a.q_page[r];
   const int32_t seq = (int32_t)ld_ix(a.seq_lens, r, a.seq_i64);
-  const int64_t bt_row = (int64_t)r * a.bt_sr;
   const int g = lane / LPP, gl = lane % LPP;
+  const int wl = c0 + lane;
+  int32_t pg = 0;
+  if (wl < W) {     // issued beside the seq_lens load, not after it
+    const int64_t page = ld_ix(a.block_table, (int64_t)r * a.bt_sr + wl, a.bt_i64);
+    pg = (int32_t)(page < 0 ? 0 : (page > a.num_blocks - 1 ? a.num_blocks - 1 : page));
+  }
+  const bool live_l = wl < W && (int64_t)wl * BS < seq;
   bool mine = false;
-#pragma unroll 4
-  for (int it = 0; it < kWave / PPW; ++it) {
-    const int w = c0 + it * PPW + g;
-    const bool live = w < W && (int64_t)w * BS < seq;
-    int32_t lo = kInt16Max, hi = -1;
-    if (live) {
-      int64_t page = ld_ix(a.block_table, bt_row + w, a.bt_i64);
-      page = page < 0 ? 0 : (page > a.num_blocks - 1 ? a.num_blocks - 1 : page);
-      const int4 v = *reinterpret_cast<const int4*>(a.s_page + page * BS + gl * 4);
-      const int32_t e[4] = {v.x, v.y, v.z, v.w};
+  for (int b0 = 0; b0 < ITER; b0 += NB) {
+    int4 v[NB];
+    bool live[NB];
+#pragma unroll
+    for (int i = 0; i < NB; ++i) {
+      const int src = (b0 + i) * PPW + g;
+      const int page = __shfl(pg, src, kWave);
+      live[i] = __shfl(live_l ? 1 : 0, src, kWave) != 0;
+      v[i] = live[i] ? *reinterpret_cast<const int4*>(a.s_page + (int64_t)page * BS + gl * 4)
+                     : make_int4(-1, -1, -1, -1);
+    }
+#pragma unroll
+    for (int i = 0; i < NB; ++i) {
+      const int32_t e[4] = {v[i].x, v[i].y, v[i].z, v[i].w};
+      int32_t lo = kInt16Max, hi = -1;
 #pragma unroll
       for (int k = 0; k < 4; ++k) {
         hi = max(hi, e[k] >= 0 ? e[k] : -1);
         lo = min(lo, e[k] >= 0 ? e[k] : kInt16Max);
       }
-    }
 #pragma unroll
-    for (int o = 1; o < LPP; o <<= 1) {
-      hi = max(hi, __shfl_xor(hi, o, kWave));
-      lo = min(lo, __shfl_xor(lo, o, kWave));
+      for (int o = 1; o < LPP; o <<= 1) {
+        hi = max(hi, __shfl_xor(hi, o, kWave));
+        lo = min(lo, __shfl_xor(lo, o, kWave));
+      }
+      const int32_t bmin = hi >= 0 ? lo : -1;
+      const bool same = live[i] && bmin >= 0 && bmin <= qp && qp <= hi && qp >= 0;
+      const bool sv = __shfl(same ? 1 : 0, (lane % PPW) * LPP, kWave) != 0;
+      if (lane / PPW == b0 + i) mine = sv;
     }
-    const int32_t bmin = hi >= 0 ? lo : -1;
-    const bool same = live && bmin >= 0 && bmin <= qp && qp <= hi && qp >= 0;
-    const bool v = __shfl(same, (lane % PPW) * LPP, kWave);
-    if (lane / PPW == it) mine = v;
   }
-  const int col = c0 + lane;
-  if (col < a.max_block) a.out[(int64_t)r * a.out_sr + col] = mine ? 1 : 0;
+  if (wl < a.max_block) a.out[(int64_t)r * a.out_sr + wl] = mine ? 1 : 0;
   const int n = __popcll(__ballot(mine));
   if (lane == 0) partial[(int64_t)r * nchunk + chunk] = n;
 }
@@ -175,7 +189,13 @@ __global__ __launch_bounds__(64) void page_allow_open_kernel(srswa_page_allow_ar
 }
 
 // ------------------------------------------------------------ local union
-__global__ __launch_bounds__(64) void local_union_kernel(srswa_local_union_args a) {
+// One 256-lane workgroup per request; each lane owns 16 consecutive mask
+// bytes (one 16-byte load and store when the rows are aligned), so a row of
+// up to 4096 blocks takes one pass.
+constexpr int kUnionThreads = 256;
+
+__global__ __launch_bounds__(kUnionThreads) void local_union_kernel(srswa_local_union_args a) {
+  constexpr int CH = 16;
   const int r = blockIdx.x;
   const int lane = threadIdx.x;
   const int32_t seq = (int32_t)ld_ix(a.seq_lens, r, a.seq_i64);
@@ -183,11 +203,41 @@ __global__ __launch_bounds__(64) void local_union_kernel(srswa_local_union_args 
   const int32_t hi = min(max(q_blk, 0), a.max_block - 1);
   const int32_t lo = min(max(q_blk - (a.local_blocks - 1), 0), a.max_block - 1);
   const int n = min(a.max_block, a.o_w);
-  const int8_t* src = a.allow + (int64_t)r * a.a_sr;
-  int8_t* dst = a.out + (int64_t)r * a.o_sr;
-  for (int w = lane; w < n; w += kWave) {
-    const bool al = w < a.a_w && src[w] != 0;
-    dst[w] = (al || (w >= lo && w <= hi)) ? 1 : 0;
+  const int8_t* __restrict__ src = a.allow + (int64_t)r * a.a_sr;
+  int8_t* __restrict__ dst = a.out + (int64_t)r * a.o_sr;
+  const bool vec = (((uintptr_t)src | (uintptr_t)dst) & 15) == 0 && a.a_w >= n;
+  int w0 = lane * CH;
+  if (vec) {        // whole 16-byte pieces as one load and one store per lane
+    for (; w0 + CH <= n; w0 += kUnionThreads * CH) {
+      const uint4 in = *reinterpret_cast<const uint4*>(src + w0);
+      const uint32_t iw[4] = {in.x, in.y, in.z, in.w};
+      uint32_t ow[4];
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        uint32_t o = 0;
+#pragma unroll
+        for (int k = 0; k < 4; ++k) {
+          const int w = w0 + 4 * q + k;
+          const bool on = ((iw[q] >> (8 * k)) & 0xffu) != 0 || (w >= lo && w <= hi);
+          o |= (on ? 1u : 0u) << (8 * k);
+        }
+        ow[q] = o;
+      }
+      *reinterpret_cast<uint4*>(dst + w0) = make_uint4(ow[0], ow[1], ow[2], ow[3]);
+    }
+  }
+  for (; w0 < n; w0 += kUnionThreads * CH) {
+    int8_t v[CH];
+#pragma unroll
+    for (int i = 0; i < CH; ++i) {
+      const int w = w0 + i;
+      v[i] = (w < n && w < a.a_w) ? src[w] : 0;
+    }
+#pragma unroll
+    for (int i = 0; i < CH; ++i) {
+      const int w = w0 + i;
+      if (w < n) dst[w] = (v[i] != 0 || (w >= lo && w <= hi)) ? 1 : 0;
+    }
   }
 }
 
@@ -369,7 +419,8 @@ extern "C" int srswa_page_local_union(const srswa_local_union_args* a, void* str
     return SRSWA_INVALID;
   }
   if (a->R == 0) return SRSWA_OK;
-  hipLaunchKernelGGL(local_union_kernel, dim3(a->R), dim3(kWave), 0, reinterpret_cast<hipStream_t>(stream), *a);
+  hipLaunchKernelGGL(local_union_kernel, dim3(a->R), dim3(kUnionThreads), 0, reinterpret_cast<hipStream_t>(stream),
+                     *a);
   const hipError_t e = hipGetLastError();
   if (e != hipSuccess) {
     set_error("local union launch failed: %s", hipGetErrorString(e));
