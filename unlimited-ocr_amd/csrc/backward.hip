@@ -26,6 +26,7 @@
 // Rounding points follow the reference: q*scale and P / dS are rounded to the
 // input dtype before their products; delta, P, dS and all accumulators are fp32.
 #include <algorithm>
+#include <type_traits>
 
 #include "mfma_common.h"
 
@@ -298,11 +299,15 @@ __global__ __launch_bounds__(128, D == 128 ? 1 : 2) void dq_kernel(BwdK p) {
       db[2 * half + 1] = make_uint4(M::pack2(st[8], st[9]), M::pack2(st[10], st[11]), M::pack2(st[12], st[13]),
                                     M::pack2(st[14], st[15]));
     }
-    // dQ^T += K^T dS^T
+    // dQ^T += K^T dS^T (k-step outer: MT interleaved accumulator chains)
 #pragma unroll
-    for (int mt = 0; mt < MT; ++mt)
+    for (int ks = 0; ks < 4; ++ks) {
+      uint4 ka[MT];
 #pragma unroll
-      for (int ks = 0; ks < 4; ++ks) dq[mt] = M::mac(a_operand_tr<KP>(k16, 16 * ks, 32 * mt, lane), db[ks], dq[mt]);
+      for (int mt = 0; mt < MT; ++mt) ka[mt] = a_operand_tr<KP>(k16, 16 * ks, 32 * mt, lane);
+#pragma unroll
+      for (int mt = 0; mt < MT; ++mt) dq[mt] = M::mac(ka[mt], db[ks], dq[mt]);
+    }
 
     if (s_sdb) {
 #pragma unroll
@@ -394,6 +399,8 @@ __global__ __launch_bounds__(128, 1) void dkv_kernel(BwdK p) {
   const int BS = a.block_size, LW = a.local_window, S = a.S;
   const int maxblk = (a.Sk - 1) >> p.bs_shift;
   const int myq = kk >> 4;                     // this key's 16-key quarter
+  const int qb0 = j0 >> p.bs_shift;            // block of the chunk's first quarter
+  const bool one_blk = ((j0 + kChunk - 1) >> p.bs_shift) == qb0;   // block size >= 64
 
   uint4 kf[KS], vf[KS];
   {
@@ -518,12 +525,38 @@ __global__ __launch_bounds__(128, 1) void dkv_kernel(BwdK p) {
                 bqv[qq] = bv * kLog2e;
               }
           };
+          if (one_blk) {
+            // the chunk lies in one block: one compare per slot, first slot's bias
+            bool found = false;
+            float bv = 0.f;
 #pragma unroll
-          for (int s = 0; s < kPreSlots; ++s) take(s, pf_id[s], pf_b[s]);
-          if (S > kPreSlots) {
-            const int32_t* ids = a.idx + (int64_t)b * a.idx_sb + (int64_t)ih * a.idx_sh + (int64_t)t * a.idx_st;
-            const float* bias = a.bias ? a.bias + (int64_t)b * a.bias_sb + (int64_t)ih * a.bias_sh + (int64_t)t * a.bias_st : nullptr;
-            for (int s = kPreSlots; s < S; ++s) take(s, ids[s], bias ? bias[s] : 0.f);
+            for (int s = 0; s < kPreSlots; ++s) {
+              const bool hit = pf_id[s] == qb0;
+              bv = (hit && !found) ? pf_b[s] : bv;
+              found = found || hit;
+            }
+            if (S > kPreSlots) {
+              const int32_t* ids = a.idx + (int64_t)b * a.idx_sb + (int64_t)ih * a.idx_sh + (int64_t)t * a.idx_st;
+              const float* bias = a.bias ? a.bias + (int64_t)b * a.bias_sb + (int64_t)ih * a.bias_sh + (int64_t)t * a.bias_st : nullptr;
+              for (int s = kPreSlots; s < S && !found; ++s)
+                if (ids[s] == qb0) {
+                  found = true;
+                  bv = bias ? bias[s] : 0.f;
+                }
+            }
+            if (found) {
+              qmem = 0xfu;
+#pragma unroll
+              for (int qq = 0; qq < 4; ++qq) bqv[qq] = bv * kLog2e;
+            }
+          } else {
+#pragma unroll
+            for (int s = 0; s < kPreSlots; ++s) take(s, pf_id[s], pf_b[s]);
+            if (S > kPreSlots) {
+              const int32_t* ids = a.idx + (int64_t)b * a.idx_sb + (int64_t)ih * a.idx_sh + (int64_t)t * a.idx_st;
+              const float* bias = a.bias ? a.bias + (int64_t)b * a.bias_sb + (int64_t)ih * a.bias_sh + (int64_t)t * a.bias_st : nullptr;
+              for (int s = kPreSlots; s < S; ++s) take(s, ids[s], bias ? bias[s] : 0.f);
+            }
           }
           uint64_t qm = 0;
 #pragma unroll
@@ -546,18 +579,34 @@ __global__ __launch_bounds__(128, 1) void dkv_kernel(BwdK p) {
       }
       __syncthreads();
       const bool fast = s_flag[0] != 0;
-      // this key's kept rows (bit = row), by ballots over the rows' masks
-      uint64_t kt = ~0ull, rt = 0ull;
+      // keep / remote bits of this lane's key for the 32 rows it holds in the
+      // MFMA layout (bit 16 half + 4 r4 + e <-> row 32 half + 8 r4 + 4 h + e),
+      // read from the rows' 64-bit masks: four rows per pair of 16-byte LDS
+      // reads, the same address for every lane of a half-wave
+      uint32_t km32 = ~0u, rm32 = 0u;
       if (!fast) {
-        const uint64_t km = s_keep[lane], rmm = s_rem[lane];
-        const int sh = 32 * wave;
-        const uint32_t k32 = (uint32_t)(km >> sh), r32 = (uint32_t)(rmm >> sh);
-#pragma unroll 1
-        for (int k = 0; k < 32; ++k) {
-          const uint64_t bk = __ballot((k32 >> k) & 1u);
-          const uint64_t br = a.bias ? __ballot((r32 >> k) & 1u) : 0ull;
-          if (rl == k) { kt = bk; rt = br; }
-        }
+        km32 = 0u;
+#pragma unroll
+        for (int half = 0; half < 2; ++half)
+#pragma unroll
+          for (int r4 = 0; r4 < 4; ++r4) {
+            const int row0 = 32 * half + 8 * r4 + 4 * h;
+            const int b0 = 16 * half + 4 * r4;
+            const uint4 k01 = *reinterpret_cast<const uint4*>(s_keep + row0);
+            const uint4 k23 = *reinterpret_cast<const uint4*>(s_keep + row0 + 2);
+            const uint32_t kw[8] = {k01.x, k01.y, k01.z, k01.w, k23.x, k23.y, k23.z, k23.w};
+#pragma unroll
+            for (int e = 0; e < 4; ++e)
+              km32 |= ((kk < 32 ? kw[2 * e] >> kk : kw[2 * e + 1] >> (kk - 32)) & 1u) << (b0 + e);
+            if (a.bias) {
+              const uint4 r01 = *reinterpret_cast<const uint4*>(s_rem + row0);
+              const uint4 r23 = *reinterpret_cast<const uint4*>(s_rem + row0 + 2);
+              const uint32_t rw[8] = {r01.x, r01.y, r01.z, r01.w, r23.x, r23.y, r23.z, r23.w};
+#pragma unroll
+              for (int e = 0; e < 4; ++e)
+                rm32 |= ((kk < 32 ? rw[2 * e] >> kk : rw[2 * e + 1] >> (kk - 32)) & 1u) << (b0 + e);
+            }
+          }
       }
 
       // S = Q K^T and dP = dO V^T: 64 rows x this lane's key
@@ -570,36 +619,46 @@ __global__ __launch_bounds__(128, 1) void dkv_kernel(BwdK p) {
           gd[half] = M::mac(*reinterpret_cast<const uint4*>(sG + (32 * half + rl) * QP + 16 * ks + 8 * h), vf[ks], gd[half]);
         }
       }
-      // in place: sp <- P, gd <- dS; register r of half `half` is row 32 half + 8 (r / 4) + 4h + r % 4
-      const uint64_t kth = kt >> (4 * h), rth = rt >> (4 * h);
+      // in place: sp <- P, gd <- dS; register r of half `half` is row 32 half + 8 (r / 4) + 4h + r % 4.
+      // Two straight-line copies (every row keeps the chunk whole / masked):
+      // a uniform test per element would split the unrolled loop into one
+      // basic block per exp.
+      auto softmax = [&](auto fast_tag) {
+        constexpr bool FAST = decltype(fast_tag)::value;
 #pragma unroll
-      for (int half = 0; half < 2; ++half)
+        for (int half = 0; half < 2; ++half)
 #pragma unroll
-        for (int r4 = 0; r4 < 4; ++r4) {
-          const int row0 = 32 * half + 8 * r4 + 4 * h;
-          const float4 l4 = *reinterpret_cast<const float4*>(s_lse + row0);
-          const float4 d4 = *reinterpret_cast<const float4*>(s_dlt + row0);
-          float4 b4 = make_float4(0.f, 0.f, 0.f, 0.f);
-          if (a.bias && !fast) b4 = *reinterpret_cast<const float4*>(s_bq + myq * 64 + row0);
-          const float lv[4] = {l4.x, l4.y, l4.z, l4.w}, dv4[4] = {d4.x, d4.y, d4.z, d4.w};
-          const float bv[4] = {b4.x, b4.y, b4.z, b4.w};
+          for (int r4 = 0; r4 < 4; ++r4) {
+            const int row0 = 32 * half + 8 * r4 + 4 * h;
+            const float4 l4 = *reinterpret_cast<const float4*>(s_lse + row0);
+            const float4 d4 = *reinterpret_cast<const float4*>(s_dlt + row0);
+            float4 b4 = make_float4(0.f, 0.f, 0.f, 0.f);
+            if constexpr (!FAST)
+              if (a.bias) b4 = *reinterpret_cast<const float4*>(s_bq + myq * 64 + row0);
+            const float lv[4] = {l4.x, l4.y, l4.z, l4.w}, dv4[4] = {d4.x, d4.y, d4.z, d4.w};
+            const float bv[4] = {b4.x, b4.y, b4.z, b4.w};
 #pragma unroll
-          for (int e = 0; e < 4; ++e) {
-            const int r = 4 * r4 + e;
-            const int bit = 32 * half + 8 * r4 + e;
-            float pv;
-            if (fast) {
-              pv = __builtin_amdgcn_exp2f(fmaf(sp[half][r], kLog2e, -lv[e]));
-            } else {
-              const bool remb = (rth >> bit) & 1ull;
-              const float x = fmaf(sp[half][r], kLog2e, (remb ? bv[e] : 0.f) - lv[e]);
-              pv = ((kth >> bit) & 1ull) ? __builtin_amdgcn_exp2f(x) : 0.f;
+            for (int e = 0; e < 4; ++e) {
+              const int r = 4 * r4 + e;
+              float x;
+              if constexpr (FAST) {
+                x = fmaf(sp[half][r], kLog2e, -lv[e]);
+              } else {
+                const int bit = 16 * half + 4 * r4 + e;
+                const bool remb = (rm32 >> bit) & 1u;
+                x = fmaf(sp[half][r], kLog2e, (remb ? bv[e] : 0.f) - lv[e]);
+                x = ((km32 >> bit) & 1u) ? x : -INFINITY;      // exp2(-inf) = 0
+              }
+              const float pv = key_ok ? __builtin_amdgcn_exp2f(x) : 0.f;
+              sp[half][r] = pv;
+              gd[half][r] = pv * (gd[half][r] - dv4[e]);
             }
-            pv = key_ok ? pv : 0.f;
-            sp[half][r] = pv;
-            gd[half][r] = pv * (gd[half][r] - dv4[e]);
           }
-        }
+      };
+      if (fast)
+        softmax(std::true_type{});
+      else
+        softmax(std::false_type{});
       uint4 pb[4], db[4];
 #pragma unroll
       for (int ks = 0; ks < 4; ++ks) {
@@ -609,14 +668,22 @@ __global__ __launch_bounds__(128, 1) void dkv_kernel(BwdK p) {
         db[ks] = make_uint4(M::pack2(gd[hf][r0], gd[hf][r0 + 1]), M::pack2(gd[hf][r0 + 2], gd[hf][r0 + 3]),
                             M::pack2(gd[hf][r0 + 4], gd[hf][r0 + 5]), M::pack2(gd[hf][r0 + 6], gd[hf][r0 + 7]));
       }
-      // dV^T += dO^T P ; dK^T += (q*scale)^T dS
+      // dV^T += dO^T P ; dK^T += (q*scale)^T dS (k-step outer: 2 MT interleaved
+      // accumulator chains, a step's operands read before its MFMAs)
 #pragma unroll
-      for (int mt = 0; mt < MT; ++mt)
+      for (int ks = 0; ks < 4; ++ks) {
+        uint4 ga[MT], qa[MT];
 #pragma unroll
-        for (int ks = 0; ks < 4; ++ks) {
-          dv[mt] = M::mac(a_operand_tr<QP>(g16, 16 * ks, 32 * mt, lane), pb[ks], dv[mt]);
-          dk[mt] = M::mac(a_operand_tr<QP>(q16, 16 * ks, 32 * mt, lane), db[ks], dk[mt]);
+        for (int mt = 0; mt < MT; ++mt) {
+          ga[mt] = a_operand_tr<QP>(g16, 16 * ks, 32 * mt, lane);
+          qa[mt] = a_operand_tr<QP>(q16, 16 * ks, 32 * mt, lane);
         }
+#pragma unroll
+        for (int mt = 0; mt < MT; ++mt) {
+          dv[mt] = M::mac(ga[mt], pb[ks], dv[mt]);
+          dk[mt] = M::mac(qa[mt], db[ks], dk[mt]);
+        }
+      }
     }
   }
 

@@ -307,11 +307,16 @@ __global__ __launch_bounds__(128, 2) void fwd_kernel(FwdK p) {
       pb[ks] = make_uint4(M::pack2(st[hf][r0], st[hf][r0 + 1]), M::pack2(st[hf][r0 + 2], st[hf][r0 + 3]),
                           M::pack2(st[hf][r0 + 4], st[hf][r0 + 5]), M::pack2(st[hf][r0 + 6], st[hf][r0 + 7]));
     }
-    // O^T += V^T P^T
+    // O^T += V^T P^T, k-step outer: the MT accumulators form independent
+    // chains that interleave, and a step's operands are read before its MFMAs
 #pragma unroll
-    for (int mt = 0; mt < MT; ++mt)
+    for (int ks = 0; ks < 4; ++ks) {
+      uint4 va[MT];
 #pragma unroll
-      for (int ks = 0; ks < 4; ++ks) o[mt] = M::mac(a_operand_tr<VP>(v16, 16 * ks, 32 * mt, lane), pb[ks], o[mt]);
+      for (int mt = 0; mt < MT; ++mt) va[mt] = a_operand_tr<VP>(v16, 16 * ks, 32 * mt, lane);
+#pragma unroll
+      for (int mt = 0; mt < MT; ++mt) o[mt] = M::mac(va[mt], pb[ks], o[mt]);
+    }
   }
 
   const float l_tot = l_run + __shfl_xor(l_run, 32, kWave);
