@@ -466,6 +466,51 @@ def bench_page(args):
             "decode_meta_step_us": ms_meta * 1e3}
 
 
+def bench_kl(args):
+    """Indexer distillation KL (training, DASH / "sparse" stage) on config 5's
+    shape: B=2, T=16384 rows of one index head against the mean of 10 main
+    heads over each row's selected remote keys (config 5's per-tile top-8
+    blocks), forward (KL + dsel) and backward (d idx_q, d idx_k)."""
+    import torch
+    from srswa import kl as KL, workloads as W
+    dev = torch.device("cuda:0")
+    B, T, H, D, BS, LW, K = 2, 16384, 10, 128, 64, 512, 8
+    g = torch.Generator(device=dev).manual_seed(11)
+    sel = W.tile_block_indices(B, T, T, BS, LW, K, cfg=5, mode="selfattn").to(dev)        # [B, 1, T, K]
+    q_idx = (torch.randn(B, 1, T, D, device=dev, generator=g) * D ** -0.5).to(torch.bfloat16).requires_grad_()
+    idx_k = torch.randn(B, T, D, device=dev, generator=g).to(torch.bfloat16).requires_grad_()
+    q_main = torch.randn(B, H, T, D, device=dev, generator=g).to(torch.bfloat16)
+    k_main = torch.randn(B, H, T, D, device=dev, generator=g).to(torch.bfloat16)
+    pos = torch.arange(T, device=dev, dtype=torch.int32).expand(B, T).contiguous()
+    scaling = D ** -0.5
+
+    def fwd():
+        return KL.kl_forward(q_idx.detach(), idx_k.detach(), q_main, k_main, sel, pos, block_size=BS,
+                             local_window=LW, scaling=scaling)
+
+    def step():
+        kl, valid = KL.gather_kl(q_idx, idx_k, q_main, k_main, sel, pos, block_size=BS, local_window=LW,
+                                 scaling=scaling)
+        (kl * valid).sum().backward()
+
+    ms = _time_launches(step, args.steps, args.warmup, dev)
+    ms_f = _time_launches(fwd, args.steps, args.warmup, dev)
+    _, rp = W.attended_pairs(sel.cpu(), T, BS, LW)              # kept (row, remote key) pairs of all B
+    fwd_flops = rp * (H + 1) * 2 * D                            # one pass of the 10 teacher heads + student
+    bwd_flops = rp * 2 * 2 * D                                  # d idx_q and d idx_k
+    tf_f = fwd_flops / (ms_f * 1e-3) / 1e12
+    return {"metric": "indexer distillation KL fwd+bwd tokens/s (config 5 shape)", "value": B * T / (ms * 1e-3),
+            "unit": "tokens/s", "n_gpus": 1, "steps": args.steps, "warmup": args.warmup, "ms_per_step": ms,
+            "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "bf16",
+            "data": "synthetic (seeded), config 5's per-tile top-8 selections",
+            "config": {"workload": "gather-KL, B=2, T=16384, 1 index head vs 10 main heads, D=128, top-8 64-key "
+                                   "blocks, 512-token window excluded", "fwd_ms": ms_f, "kept_pairs": rp,
+                       "fwd_flops": fwd_flops, "bwd_flops": bwd_flops},
+            "roofline": {"bound": "mfma", "achieved": tf_f, "peak": 2500.0, "unit": "TFLOP/s", "frac": tf_f / 2500.0,
+                         "traffic": None, "kernel": "srswa::kl_fwd_kernel<bf16,128> (one pass of algorithmic flops; "
+                                                     "the kernel runs two)"}}
+
+
 def bench_copycal(args):
     """Calibration for the HBM traffic counters: a plain device copy of a known
     size (4 GiB read + 4 GiB written per launch, far beyond the 256 MB
@@ -488,7 +533,7 @@ def main():
     ap.add_argument("--steps", type=int, default=200)
     ap.add_argument("--warmup", type=int, default=20)
     ap.add_argument("--config", default="decode",
-                    choices=["decode", "indexer", "prefill", "fwdbwd", "paged", "dash", "page", "copycal"])
+                    choices=["decode", "indexer", "prefill", "fwdbwd", "paged", "dash", "page", "kl", "copycal"])
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--no-check", action="store_true", help="skip the oracle spot check")
     ap.add_argument("--cpu-budget", type=float, default=12.0)
@@ -498,7 +543,8 @@ def main():
               "(no multi-GPU path); use --gpus 1", file=sys.stderr)
         sys.exit(2)
     fn = {"decode": bench_decode, "indexer": bench_indexer, "prefill": bench_prefill,
-          "fwdbwd": bench_fwdbwd, "paged": bench_paged, "dash": bench_dash, "page": bench_page, "copycal": bench_copycal}[args.config]
+          "fwdbwd": bench_fwdbwd, "paged": bench_paged, "dash": bench_dash, "page": bench_page, "kl": bench_kl,
+          "copycal": bench_copycal}[args.config]
     res = fn(args)
     print(json.dumps(res), flush=True)
 

@@ -465,6 +465,57 @@ typedef struct {
 
 int srswa_page_candidate_mask(const srswa_candidate_args* a, void* stream);
 
+/* ------------------------------------------------------------------------
+ * Gather-KL of the indexer distillation loss (training, DASH / "sparse"
+ * stage).  Replaces the KL of the n_idx_heads == 1 gather branch of
+ * select_and_kl_loss (HF/_sparse_base_impl.py:3413-3478) and _kl_chunk_core /
+ * _KLChunkFn (:2071-2190).  Row t of index head ih keeps key j of its selected
+ * blocks (64 keys each; a repeated id counts once) when
+ * seg[t] <= j < max(pos[t] - local_window + 1, 0) and j < Sk;
+ *   p_j = mean over the HQ/HI query heads h of ih of
+ *         softmax_j(scaling * rnd(q_main[h, t] . k_main[kv(h), j]))
+ *   log q_j = log_softmax_j(rnd(q_idx[ih, t] . idx_k[j]))       (rnd: to the input dtype)
+ *   kl[t] = sum_j p_j (log max(p_j, 1e-12) - log q_j), valid[t] = any key kept
+ * dsel (optional, [.., K, 64] fp32 per row) = q_j - p_j on kept keys, else 0:
+ * d kl / d logit, the input of srswa_gather_kl_bwd.  kv(h) = h / (HQ / HKV).
+ * ---------------------------------------------------------------------- */
+typedef struct {
+  const void* q_idx;  int64_t qi_sb, qi_sh, qi_st;     /* [B, HI, T, D] index queries     */
+  const void* idx_k;  int64_t ik_sb, ik_st;            /* [B, Sk, D] index keys           */
+  const void* q_main; int64_t qm_sb, qm_sh, qm_st;     /* [B, HQ, T, D] main queries      */
+  const void* k_main; int64_t km_sb, km_sh, km_st;     /* [B, HKV, Sk, D] main keys       */
+  const int32_t* sel; int64_t sel_sb, sel_sh, sel_st;  /* [B, HI, T, K] block ids, -1 = none */
+  const int32_t* pos; int64_t pos_sb;                  /* [B, T] key position of each row */
+  const int32_t* seg; int64_t seg_sb;                  /* [B, T] first key of the row's sample, NULL = 0 */
+  float* kl;          int64_t kl_sb, kl_sh;            /* [B, HI, T]                      */
+  uint8_t* valid;     int64_t va_sb, va_sh;            /* [B, HI, T]                      */
+  float* dsel;        int64_t ds_sb, ds_sh, ds_st;     /* [B, HI, T, K, 64] or NULL       */
+  int32_t B, HI, HQ, HKV, T, Sk, D, K, block_size, local_window;
+  float scaling;
+  int32_t dtype;                                       /* srswa_dtype: bf16 or fp16       */
+} srswa_kl_args;
+
+int srswa_gather_kl_fwd(const srswa_kl_args* a, void* stream);
+
+/* Backward of the student path (the teacher carries no gradient): with
+ * g = grad[b, ih, t] and ds_j = rnd(g * dsel_j),
+ *   dq_idx[b, ih, t] = rnd(sum_j ds_j idx_k[j]),  dk_idx[b, j] = rnd(sum_{rows} ds_j q_idx[row])
+ * (fp32 sums, one rounding; every row of dq_idx and every key of dk_idx is
+ * written).  Deterministic. */
+typedef struct {
+  const void* q_idx;  int64_t qi_sb, qi_sh, qi_st;     /* [B, HI, T, D]                   */
+  const void* idx_k;  int64_t ik_sb, ik_st;            /* [B, Sk, D]                      */
+  const int32_t* sel; int64_t sel_sb, sel_sh, sel_st;  /* [B, HI, T, K]                   */
+  const float* dsel;  int64_t ds_sb, ds_sh, ds_st;     /* [B, HI, T, K, 64] from the forward */
+  const float* grad;  int64_t g_sb, g_sh;              /* [B, HI, T] d loss / d kl        */
+  void* dq_idx;       int64_t dq_sb, dq_sh, dq_st;     /* [B, HI, T, D]                   */
+  void* dk_idx;       int64_t dk_sb, dk_st;            /* [B, Sk, D]                      */
+  int32_t B, HI, T, Sk, D, K, block_size;
+  int32_t dtype;
+} srswa_kl_bwd_args;
+
+int srswa_gather_kl_bwd(const srswa_kl_bwd_args* a, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -271,6 +271,38 @@ __device__ __forceinline__ bool chunk_mask(RowWalk& w, int j0, int bs_shift, boo
   return !w.ok || (keep == ~0ull && (!w.sb || rm == 0ull || (rm == ~0ull && blk64)));
 }
 
+// Ascending list of the set bits of a bitmap (nwords words) by a prefix
+// popcount in the first wavefront; every thread of the workgroup calls it
+// after the bitmap is complete and gets the count.
+__device__ inline int compact_bitmap(const uint32_t* s_bits, int nwords, uint16_t* s_chunks, int* s_count) {
+  const int tid = threadIdx.x;
+  if (tid < kWave) {
+    int base = 0;
+    for (int w0 = 0; w0 < nwords; w0 += kWave) {
+      const int w = w0 + tid;
+      const uint32_t bits = w < nwords ? s_bits[w] : 0u;
+      const int cnt = __popc(bits);
+      int incl = cnt;
+#pragma unroll
+      for (int o = 1; o < kWave; o <<= 1) {
+        const int v = __shfl_up(incl, o, kWave);
+        if (tid >= o) incl += v;
+      }
+      int pos = base + incl - cnt;
+      uint32_t bb = bits;
+      while (bb) {
+        const int bit = __ffs(bb) - 1;
+        bb &= bb - 1;
+        s_chunks[pos++] = (uint16_t)(w * 32 + bit);
+      }
+      base += __shfl(incl, kWave - 1, kWave);
+    }
+    if (tid == 0) *s_count = base;
+  }
+  __syncthreads();
+  return *s_count;
+}
+
 // Sorted list of the 64-key chunks a tile visits, from the rows' windows
 // [ls, qi] and the remote keys of their sorted ids (sid, SP entries per row):
 // a bitmap over chunks (s_bits, nwords words, zeroed here) compacted by a
@@ -297,31 +329,7 @@ __device__ inline int plan_chunks(const int* s_qi, const int* s_seg, const int* 
     for (int c = lo / kChunk; c <= (hi - 1) / kChunk; ++c) atomicOr(&s_bits[c >> 5], 1u << (c & 31));
   }
   __syncthreads();
-  if (tid < kWave) {
-    int base = 0;
-    for (int w0 = 0; w0 < nwords; w0 += kWave) {
-      const int w = w0 + tid;
-      const uint32_t bits = w < nwords ? s_bits[w] : 0u;
-      const int cnt = __popc(bits);
-      int incl = cnt;
-#pragma unroll
-      for (int o = 1; o < kWave; o <<= 1) {
-        const int v = __shfl_up(incl, o, kWave);
-        if (tid >= o) incl += v;
-      }
-      int pos = base + incl - cnt;
-      uint32_t bb = bits;
-      while (bb) {
-        const int bit = __ffs(bb) - 1;
-        bb &= bb - 1;
-        s_chunks[pos++] = (uint16_t)(w * 32 + bit);
-      }
-      base += __shfl(incl, kWave - 1, kWave);
-    }
-    if (tid == 0) *s_count = base;
-  }
-  __syncthreads();
-  return *s_count;
+  return compact_bitmap(s_bits, nwords, s_chunks, s_count);
 }
 
 // First slot (or -1) of each row's selected blocks overlapping each planned

@@ -290,6 +290,43 @@ class CandidateArgs(ctypes.Structure):
     ]
 
 
+class KlArgs(ctypes.Structure):
+    """Mirror of ``srswa_kl_args``."""
+
+    _fields_ = [
+        ("q_idx", _vp), ("qi_sb", _i64), ("qi_sh", _i64), ("qi_st", _i64),
+        ("idx_k", _vp), ("ik_sb", _i64), ("ik_st", _i64),
+        ("q_main", _vp), ("qm_sb", _i64), ("qm_sh", _i64), ("qm_st", _i64),
+        ("k_main", _vp), ("km_sb", _i64), ("km_sh", _i64), ("km_st", _i64),
+        ("sel", _vp), ("sel_sb", _i64), ("sel_sh", _i64), ("sel_st", _i64),
+        ("pos", _vp), ("pos_sb", _i64),
+        ("seg", _vp), ("seg_sb", _i64),
+        ("kl", _vp), ("kl_sb", _i64), ("kl_sh", _i64),
+        ("valid", _vp), ("va_sb", _i64), ("va_sh", _i64),
+        ("dsel", _vp), ("ds_sb", _i64), ("ds_sh", _i64), ("ds_st", _i64),
+        ("B", _i32), ("HI", _i32), ("HQ", _i32), ("HKV", _i32), ("T", _i32), ("Sk", _i32), ("D", _i32),
+        ("K", _i32), ("block_size", _i32), ("local_window", _i32),
+        ("scaling", ctypes.c_float),
+        ("dtype", _i32),
+    ]
+
+
+class KlBwdArgs(ctypes.Structure):
+    """Mirror of ``srswa_kl_bwd_args``."""
+
+    _fields_ = [
+        ("q_idx", _vp), ("qi_sb", _i64), ("qi_sh", _i64), ("qi_st", _i64),
+        ("idx_k", _vp), ("ik_sb", _i64), ("ik_st", _i64),
+        ("sel", _vp), ("sel_sb", _i64), ("sel_sh", _i64), ("sel_st", _i64),
+        ("dsel", _vp), ("ds_sb", _i64), ("ds_sh", _i64), ("ds_st", _i64),
+        ("grad", _vp), ("g_sb", _i64), ("g_sh", _i64),
+        ("dq_idx", _vp), ("dq_sb", _i64), ("dq_sh", _i64), ("dq_st", _i64),
+        ("dk_idx", _vp), ("dk_sb", _i64), ("dk_st", _i64),
+        ("B", _i32), ("HI", _i32), ("T", _i32), ("Sk", _i32), ("D", _i32), ("K", _i32), ("block_size", _i32),
+        ("dtype", _i32),
+    ]
+
+
 # name -> (restype, argtypes) of every exported entry point
 SIGNATURES = {
     "srswa_version": (ctypes.c_int, []),
@@ -319,6 +356,8 @@ SIGNATURES = {
     "srswa_page2d_rope": (ctypes.c_int, [ctypes.POINTER(RopeArgs), _vp]),
     "srswa_page_block_bounds": (ctypes.c_int, [ctypes.POINTER(BlockBoundsArgs), _vp]),
     "srswa_page_candidate_mask": (ctypes.c_int, [ctypes.POINTER(CandidateArgs), _vp]),
+    "srswa_gather_kl_fwd": (ctypes.c_int, [ctypes.POINTER(KlArgs), _vp]),
+    "srswa_gather_kl_bwd": (ctypes.c_int, [ctypes.POINTER(KlBwdArgs), _vp]),
 }
 
 STRUCTS = {"srswa_decode_args": DecodeArgs, "srswa_index_args": IndexArgs,
@@ -328,7 +367,8 @@ STRUCTS = {"srswa_decode_args": DecodeArgs, "srswa_index_args": IndexArgs,
            "srswa_kbar_scores_args": KbarScoresArgs, "srswa_page_meta_args": PageMetaArgs,
            "srswa_page_allow_args": PageAllowArgs, "srswa_local_union_args": LocalUnionArgs,
            "srswa_cos_sin_args": CosSinArgs, "srswa_rope_args": RopeArgs,
-           "srswa_block_bounds_args": BlockBoundsArgs, "srswa_candidate_args": CandidateArgs}
+           "srswa_block_bounds_args": BlockBoundsArgs, "srswa_candidate_args": CandidateArgs,
+           "srswa_kl_args": KlArgs, "srswa_kl_bwd_args": KlBwdArgs}
 
 _lib = None
 _lock = threading.Lock()

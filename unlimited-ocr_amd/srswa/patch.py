@@ -16,6 +16,8 @@ two kernel files (those are replaced file-for-file by
   (:2046-2061) and the module's ``_llama_apply_rotary_pos_emb`` (:39-41)
   -> ``srswa.page_isolation``; with ``modeling_unlimitedocr`` given, also its
   ``_uocr_dash_decode_allow`` (HF/modeling_unlimitedocr.py:481-528)
+* ``_KLChunkFn`` (HF/_sparse_base_impl.py:2158-2190), the KL of the indexer
+  distillation loss -> ``srswa.kl.KLChunkFn``
 
 Every replacement keeps the reference signature and return convention, runs
 the HIP kernels for device tensors, and hands host tensors (or a case the
@@ -27,7 +29,7 @@ from __future__ import annotations
 
 import torch
 
-from . import ops, page_isolation
+from . import kl, ops, page_isolation
 from ._lib import UnsupportedShape
 
 SCORE_NEG = -1.0e9
@@ -103,6 +105,30 @@ def _page_isolation(mod, base, done: list) -> None:
                     f"{getattr(owner, '__name__', 'module')}._llama_apply_rotary_pos_emb")
 
 
+def _kl_chunk(base, done: list) -> None:
+    if base is None or not hasattr(base, "_KLChunkFn"):
+        return
+
+    def make(orig):
+        class _KLChunkFn:
+            """``_KLChunkFn`` on the gather-KL kernels; host tensors and shapes
+            the kernels do not take use the original."""
+
+            @staticmethod
+            def apply(q_chunk, idx_k, q_main_chunk, k_main, keep_block, pos_chunk, block_size, scaling, group,
+                      kv_group, local_window=None, same_seg=None):
+                if q_chunk.is_cuda:
+                    try:
+                        return kl.KLChunkFn.apply(q_chunk, idx_k, q_main_chunk, k_main, keep_block, pos_chunk,
+                                                  block_size, scaling, group, kv_group, local_window, same_seg)
+                    except UnsupportedShape:
+                        pass
+                return orig.apply(q_chunk, idx_k, q_main_chunk, k_main, keep_block, pos_chunk, block_size, scaling,
+                                  group, kv_group, local_window, same_seg)
+        return _KLChunkFn
+    _rebind(base, "_KLChunkFn", make, done, "_KLChunkFn")
+
+
 def apply(modeling_deepseekv2, modeling_unlimitedocr=None) -> list:
     """Rebind the hot-path functions of a loaded ``modeling_deepseekv2`` module
     (the reference's DASH overlay), of its ``_sparse_base_impl`` (``_base``)
@@ -111,6 +137,7 @@ def apply(modeling_deepseekv2, modeling_unlimitedocr=None) -> list:
     mod = modeling_deepseekv2
     done = []
     _page_isolation(mod, getattr(mod, "_base", None), done)
+    _kl_chunk(getattr(mod, "_base", None), done)
     if modeling_unlimitedocr is not None:
         def make_allow(orig):
             def _uocr_dash_decode_allow(indexer, input_ids, cache):
@@ -180,6 +207,7 @@ def restore(modeling_deepseekv2, modeling_unlimitedocr=None) -> None:
     for owner, name in ((getattr(base, "DeepseekV2Indexer", None), "_build_kl_candidate_mask"),
                         (getattr(base, "DeepseekV2IndexerRotary2D", None), "forward"),
                         (base, "_llama_apply_rotary_pos_emb"), (mod, "_llama_apply_rotary_pos_emb"),
+                        (base, "_KLChunkFn"),
                         (modeling_unlimitedocr, "_uocr_dash_decode_allow")):
         _unbind(owner, name)
     if hasattr(mod, "_srswa_orig_decode_attend"):
