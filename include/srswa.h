@@ -501,7 +501,7 @@ int srswa_gather_kl_fwd(const srswa_kl_args* a, void* stream);
  * g = grad[b, ih, t] and ds_j = rnd(g * dsel_j),
  *   dq_idx[b, ih, t] = rnd(sum_j ds_j idx_k[j]),  dk_idx[b, j] = rnd(sum_{rows} ds_j q_idx[row])
  * (fp32 sums, one rounding; every row of dq_idx and every key of dk_idx is
- * written).  Deterministic. */
+ * written).  Deterministic.  At most 2048 key blocks. */
 typedef struct {
   const void* q_idx;  int64_t qi_sb, qi_sh, qi_st;     /* [B, HI, T, D]                   */
   const void* idx_k;  int64_t ik_sb, ik_st;            /* [B, Sk, D]                      */
@@ -514,7 +514,9 @@ typedef struct {
   int32_t dtype;
 } srswa_kl_bwd_args;
 
-int srswa_gather_kl_bwd(const srswa_kl_bwd_args* a, void* stream);
+/* Workspace: a (block, 64-row tile) touch bitmap, no initial content. */
+int srswa_gather_kl_bwd_workspace(const srswa_kl_bwd_args* a, size_t* scratch_bytes);
+int srswa_gather_kl_bwd(const srswa_kl_bwd_args* a, void* scratch, size_t scratch_bytes, void* stream);
 
 #ifdef __cplusplus
 }

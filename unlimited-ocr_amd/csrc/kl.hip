@@ -20,10 +20,8 @@
 //            registers, the student's log-softmax, the KL terms and dsel.
 // Keys are staged per (head, block) in LDS from registers fetched one stage
 // ahead (with the next stage's query fragments).
-// Backward (student path only, the teacher carries no gradient):
-//   dq_kernel -- one wavefront per row: dq = sum_j bf16(g dsel_j) ki_j;
-//   dk_kernel -- one workgroup per (sequence, block): the rows that selected
-//                the block, in row order (deterministic), dk_u += bf16(g dsel_u) qi.
+// Backward (student path only, the teacher carries no gradient): tile
+// products on the matrix cores with ds = bf16(g dsel), see below.
 #include <algorithm>
 
 #include "mfma_common.h"
@@ -259,32 +257,31 @@ __global__ __launch_bounds__(128, 1) void kl_fwd_kernel(KlK p) {
       }
       continue;
     }
-    // student: log-softmax, KL terms, dsel; then the next block starts from zero
-    const float lse = ml.y > 0.f ? ml.x + logf(ml.y) : 0.f;
+    // student: log-softmax, KL terms, dsel (4 keys per store); then the
+    // next block starts from zero.  log via the hardware log2.
+    const float lse = ml.y > 0.f ? ml.x + __builtin_amdgcn_logf(ml.y) * kLn2 : 0.f;
     const float invg = 1.f / (float)G;
-    float dsv[32];
+    const bool wr = a.dsel && row_ok && slot >= 0;
+    float* drow = wr ? a.dsel + ds_tile + (int64_t)(t0 + row) * a.ds_st + (int64_t)slot * kChunk : nullptr;
 #pragma unroll
     for (int half = 0; half < 2; ++half)
 #pragma unroll
-      for (int r = 0; r < 16; ++r) {
-        const bool kp = (kh >> (32 * half + 8 * (r >> 2) + (r & 3))) & 1ull;
-        const float x = round_to<T>(st[half][r]);
-        const float pv = pacc[16 * half + r] * invg;
-        const float logq = x - lse;
-        if (kp) kl_acc += pv * (logf(fmaxf(pv, 1e-12f)) - logq);
-        dsv[16 * half + r] = kp ? __builtin_amdgcn_exp2f(logq * kLog2e) - pv : 0.f;
-        pacc[16 * half + r] = 0.f;
+      for (int r4 = 0; r4 < 4; ++r4) {
+        float dv[4];
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          const int r = 4 * r4 + e;
+          const bool kp = (kh >> (32 * half + 8 * r4 + e)) & 1ull;
+          const float x = round_to<T>(st[half][r]);
+          const float pv = pacc[16 * half + r] * invg;
+          const float logq = x - lse;
+          const float lp = __builtin_amdgcn_logf(fmaxf(pv, 1e-12f)) * kLn2;
+          kl_acc += kp ? pv * (lp - logq) : 0.f;
+          dv[e] = kp ? __builtin_amdgcn_exp2f(logq * kLog2e) - pv : 0.f;
+          pacc[16 * half + r] = 0.f;
+        }
+        if (wr) *reinterpret_cast<float4*>(drow + 32 * half + 8 * r4 + 4 * h) = make_float4(dv[0], dv[1], dv[2], dv[3]);
       }
-    if (a.dsel && row_ok && slot >= 0) {
-      float* drow = a.dsel + ds_tile + (int64_t)(t0 + row) * a.ds_st + (int64_t)slot * kChunk;
-#pragma unroll
-      for (int half = 0; half < 2; ++half)
-#pragma unroll
-        for (int r4 = 0; r4 < 4; ++r4)
-          *reinterpret_cast<float4*>(drow + 32 * half + 8 * r4 + 4 * h) =
-              make_float4(dsv[16 * half + 4 * r4], dsv[16 * half + 4 * r4 + 1], dsv[16 * half + 4 * r4 + 2],
-                          dsv[16 * half + 4 * r4 + 3]);
-    }
   }
 
   const float kl_row = kl_acc + __shfl_xor(kl_acc, 32, kWave);
@@ -297,142 +294,225 @@ __global__ __launch_bounds__(128, 1) void kl_fwd_kernel(KlK p) {
 }
 
 // -------------------------------------------------------------- backward
-// dq: one wavefront per (sequence, index head, row); lane l owns head-dim
-// elements 2l, 2l + 1 (D = 128) or l (D = 64); ds broadcast by shuffles.
-template <typename T, int D>
-__global__ __launch_bounds__(256) void kl_dq_kernel(srswa_kl_bwd_args a) {
-  constexpr int EPL = D / kWave;                   // elements per lane (1 or 2)
-  const int wave = threadIdx.x / kWave, lane = threadIdx.x % kWave;
-  const int64_t rowi = (int64_t)blockIdx.x * 4 + wave;
-  if (rowi >= (int64_t)a.B * a.HI * a.T) return;
-  const int t = (int)(rowi % a.T);
-  const int ih = (int)((rowi / a.T) % a.HI);
-  const int b = (int)(rowi / ((int64_t)a.T * a.HI));
-  const float g = a.grad[(int64_t)b * a.g_sb + (int64_t)ih * a.g_sh + t];
-  float acc[EPL];
+// Both kernels are tile products on the matrix cores with ds = rnd(g * dsel)
+// (the reference's bf16 gradient of the logits) staged in LDS:
+//   dq_kernel: per (sequence, index head, 64-row tile), over the tile's
+//              selected blocks: dQ[rows, d] += DS[rows, keys] K[keys, d];
+//   dk_kernel: per (sequence, block), over the 64-row tiles that selected it
+//              (a touch bitmap that dq_kernel sets; ascending: deterministic):
+//              dK[keys, d] += DS^T[keys, rows] Q[rows, d].
+// Four waves; wave w owns output tiles (w / TPW halves of 32 rows / keys,
+// 32-wide head-dim slices); K and Q rows are read as B operands with
+// ds_read_b64_tr_b16 from their natural layout.
+constexpr int kBwdThreads = 256;
+
+struct KlBwdK {
+  srswa_kl_bwd_args a;
+  int ntiles, nblk, twords;
+  uint32_t* touch;          // [B, HI, nblk, twords]
+};
+
+template <int D> struct KlBwdLds {
+  static constexpr int XP = D + 16;          // K / Q rows: conflict-free transposing reads
+  static constexpr int SP = kChunk + 8;      // DS rows: 16-byte row reads
+  static constexpr int dsOff = kChunk * XP * 2;
+  static constexpr int bytes = dsOff + 64 * SP * 2;
+};
+
+// the slot of block c among row (b, ih, t)'s ids (first occurrence), -1 if none
+__device__ __forceinline__ int find_slot(const srswa_kl_bwd_args& a, int b, int ih, int t, int c) {
+  const int32_t* ids = a.sel + (int64_t)b * a.sel_sb + (int64_t)ih * a.sel_sh + (int64_t)t * a.sel_st;
+  for (int s = 0; s < a.K; ++s)
+    if (ids[s] == c) return s;
+  return -1;
+}
+
+// 16 values ds = rnd(g * dsel[t, slot, k0 .. k0 + 15]) (zeros without a slot)
+template <typename T>
+__device__ __forceinline__ void ds16(const srswa_kl_bwd_args& a, int b, int ih, int t, int slot, int k0,
+                                     float* out) {
+  if (slot < 0) {
 #pragma unroll
-  for (int e = 0; e < EPL; ++e) acc[e] = 0.f;
-  const T* kb = reinterpret_cast<const T*>(a.idx_k) + (int64_t)b * a.ik_sb;
-  if (g != 0.f) {
-    const int32_t* ids = a.sel + (int64_t)b * a.sel_sb + (int64_t)ih * a.sel_sh + (int64_t)t * a.sel_st;
-    const float* drow = a.dsel + (int64_t)b * a.ds_sb + (int64_t)ih * a.ds_sh + (int64_t)t * a.ds_st;
-    for (int s = 0; s < a.K; ++s) {
-      const int id = ids[s];
-      if (id < 0 || (int64_t)id * kChunk >= a.Sk) continue;
-      const float dsl = round_to<T>(g * drow[s * kChunk + lane]);   // d s in the input dtype
-      const int nk = min(kChunk, a.Sk - id * kChunk);
-      for (int u = 0; u < nk; ++u) {
-        const float dsu = __shfl(dsl, u, kWave);
-        if (dsu == 0.f) continue;
-        const T* kr = kb + (int64_t)(id * kChunk + u) * a.ik_st + lane * EPL;
-        if constexpr (EPL == 2) {
-          const uint32_t w = *reinterpret_cast<const uint32_t*>(kr);
-          acc[0] += dsu * Mfma<T>::lo(w);
-          acc[1] += dsu * Mfma<T>::hi(w);
-        } else {
-          const uint16_t w = *reinterpret_cast<const uint16_t*>(kr);
-          acc[0] += dsu * Mfma<T>::lo((uint32_t)w);
-        }
-      }
-    }
+    for (int i = 0; i < 16; ++i) out[i] = 0.f;
+    return;
   }
-  T* out = reinterpret_cast<T*>(a.dq_idx) + (int64_t)b * a.dq_sb + (int64_t)ih * a.dq_sh + (int64_t)t * a.dq_st +
-           lane * EPL;
-  if constexpr (EPL == 2) {
-    *reinterpret_cast<uint32_t*>(out) = Mfma<T>::pack2(acc[0], acc[1]);
-  } else {
-    *reinterpret_cast<uint16_t*>(out) = (uint16_t)(Mfma<T>::pack2(acc[0], 0.f) & 0xffffu);
+  const float g = a.grad[(int64_t)b * a.g_sb + (int64_t)ih * a.g_sh + t];
+  const float4* src = reinterpret_cast<const float4*>(a.dsel + (int64_t)b * a.ds_sb + (int64_t)ih * a.ds_sh +
+                                                      (int64_t)t * a.ds_st + (int64_t)slot * kChunk + k0);
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const float4 v = src[i];
+    out[4 * i] = round_to<T>(g * v.x);
+    out[4 * i + 1] = round_to<T>(g * v.y);
+    out[4 * i + 2] = round_to<T>(g * v.z);
+    out[4 * i + 3] = round_to<T>(g * v.w);
   }
 }
 
-// dk: one workgroup of 256 threads per (sequence, block); thread (u, q) owns
-// key u's head-dim quarter q.  The rows of every index head are scanned in
-// order, 256 at a time; the rows that selected the block are compacted into
-// LDS and applied in order (deterministic).
-constexpr int kDkThreads = 256;
+// 64 rows of D elements (row r at base + r * st, rows >= n zero) into LDS
+template <typename T, int D>
+__device__ __forceinline__ void stage_rows(T* dst, const T* base, int64_t st, int n) {
+  constexpr int XP = KlBwdLds<D>::XP;
+  constexpr int PR = D / 8;                       // 16-byte pieces per row
+  for (int e = threadIdx.x; e < 64 * PR; e += kBwdThreads) {
+    const int r = e / PR, c = (e % PR) * 8;
+    const uint4 v = r < n ? *reinterpret_cast<const uint4*>(base + (int64_t)r * st + c) : make_uint4(0, 0, 0, 0);
+    *reinterpret_cast<uint4*>(dst + r * XP + c) = v;
+  }
+}
+
+__global__ __launch_bounds__(256) void kl_zero_kernel(uint32_t* p, int64_t n) {
+  const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i < n) p[i] = 0u;
+}
 
 template <typename T, int D>
-__global__ __launch_bounds__(kDkThreads) void kl_dk_kernel(srswa_kl_bwd_args a, int nblk) {
-  constexpr int DQ = D / 4;                        // head-dim elements per thread
-  __shared__ int s_row[kDkThreads];                // (ih * T + t) of a matching row
-  __shared__ int s_slot[kDkThreads];
-  __shared__ int s_n;
-  __shared__ int s_wc[kDkThreads / kWave];
-  const int tid = threadIdx.x;
-  const int c = blockIdx.x % nblk, b = blockIdx.x / nblk;
-  const int u = tid / 4, q = tid % 4;
-  float acc[DQ];
+__device__ __forceinline__ void store_tiles(T* base, int64_t st, int nvalid, const f32x16_t* acc, int wave,
+                                            int lane) {
+  // acc[i] = output tile (rows / keys half = i0 >> ..., dims 32 * dt): see the callers' mapping
+  constexpr int MT = D / 32;
+  constexpr int TPW = 2 * MT / 4;                 // output tiles per wave
 #pragma unroll
-  for (int e = 0; e < DQ; ++e) acc[e] = 0.f;
-  const int64_t nrow = (int64_t)a.HI * a.T;
-  for (int64_t r0 = 0; r0 < nrow; r0 += kDkThreads) {
-    if (tid == 0) s_n = 0;
+  for (int i = 0; i < TPW; ++i) {
+    const int tix = wave * TPW + i;
+    const int half = tix / MT, dt = tix % MT;
+#pragma unroll
+    for (int r = 0; r < 16; ++r) {
+      const int m = 32 * half + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3);
+      if (m < nvalid) {
+        const uint32_t w = Mfma<T>::pack2(acc[i][r], 0.f);
+        *reinterpret_cast<uint16_t*>(base + (int64_t)m * st + 32 * dt + (lane & 31)) = (uint16_t)(w & 0xffffu);
+      }
+    }
+  }
+}
+
+template <typename T, int D>
+__global__ __launch_bounds__(kBwdThreads) void kl_dq_kernel(KlBwdK p) {
+  using M = Mfma<T>;
+  using L = KlBwdLds<D>;
+  constexpr int XP = L::XP, SP = L::SP, MT = D / 32, TPW = 2 * MT / 4;
+  extern __shared__ __align__(16) unsigned char smem[];
+  T* sK = reinterpret_cast<T*>(smem);
+  T* sDS = reinterpret_cast<T*>(smem + L::dsOff);
+  __shared__ uint32_t s_bits[64];
+  __shared__ uint16_t s_chunks[64 * 64];
+  __shared__ int s_count;
+  const srswa_kl_bwd_args& a = p.a;
+  const int tid = threadIdx.x, wave = tid / kWave, lane = tid % kWave;
+  const int tile = blockIdx.x % p.ntiles;
+  const int bh = blockIdx.x / p.ntiles;
+  const int ih = bh % a.HI, b = bh / a.HI;
+  const int t0 = tile * kTileRows;
+  const int nrows = min(kTileRows, a.T - t0);
+  // the tile's selected blocks (rows with a nonzero gradient)
+  const int nwords = (p.nblk + 31) / 32;
+  for (int w = tid; w < nwords; w += kBwdThreads) s_bits[w] = 0u;
+  __syncthreads();
+  for (int e = tid; e < nrows * a.K; e += kBwdThreads) {
+    const int r = e / a.K, s = e % a.K;
+    const int id = a.sel[(int64_t)b * a.sel_sb + (int64_t)ih * a.sel_sh + (int64_t)(t0 + r) * a.sel_st + s];
+    if (id >= 0 && id < p.nblk) atomicOr(&s_bits[id >> 5], 1u << (id & 31));
+  }
+  __syncthreads();
+  const int U = compact_bitmap(s_bits, nwords, s_chunks, &s_count);
+  // this tile touches these blocks: one bit per (block, tile) for dk_kernel
+  for (int u = tid; u < U; u += kBwdThreads)
+    atomicOr(&p.touch[(((int64_t)b * a.HI + ih) * p.nblk + s_chunks[u]) * p.twords + (tile >> 5)], 1u << (tile & 31));
+
+  f32x16_t acc[TPW];
+#pragma unroll
+  for (int i = 0; i < TPW; ++i) acc[i] = zero16();
+  const uint16_t* k16 = reinterpret_cast<const uint16_t*>(sK);
+  const int rr = tid / 4, kq = (tid % 4) * 16;    // DS staging: row, 16-key quarter
+  for (int u = 0; u < U; ++u) {
+    const int c = s_chunks[u];
     __syncthreads();
-    const int64_t r = r0 + tid;
-    int found = -1;
-    if (r < nrow) {
-      const int ih = (int)(r / a.T), t = (int)(r % a.T);
-      const int32_t* ids = a.sel + (int64_t)b * a.sel_sb + (int64_t)ih * a.sel_sh + (int64_t)t * a.sel_st;
-      for (int s = 0; s < a.K; ++s)
-        if (ids[s] == c) {
-          found = s;
-          break;
+    stage_rows<T, D>(sK, reinterpret_cast<const T*>(a.idx_k) + (int64_t)b * a.ik_sb + (int64_t)c * kChunk * a.ik_st,
+                     a.ik_st, min(kChunk, a.Sk - c * kChunk));
+    {
+      float v[16];
+      const int slot = rr < nrows ? find_slot(a, b, ih, t0 + rr, c) : -1;
+      ds16<T>(a, b, ih, t0 + rr, slot, kq, v);
+      uint4 w0, w1;
+      w0 = make_uint4(M::pack2(v[0], v[1]), M::pack2(v[2], v[3]), M::pack2(v[4], v[5]), M::pack2(v[6], v[7]));
+      w1 = make_uint4(M::pack2(v[8], v[9]), M::pack2(v[10], v[11]), M::pack2(v[12], v[13]), M::pack2(v[14], v[15]));
+      *reinterpret_cast<uint4*>(sDS + rr * SP + kq) = w0;
+      *reinterpret_cast<uint4*>(sDS + rr * SP + kq + 8) = w1;
+    }
+    __syncthreads();
+    // dQ[row, d] += DS[row, key] K[key, d]: A = DS rows, B = K via transposing reads
+#pragma unroll
+    for (int ks = 0; ks < 4; ++ks) {
+#pragma unroll
+      for (int i = 0; i < TPW; ++i) {
+        const int tix = wave * TPW + i;
+        const int half = tix / MT, dt = tix % MT;
+        const uint4 av = *reinterpret_cast<const uint4*>(sDS + (32 * half + (lane & 31)) * SP + 16 * ks + 8 * (lane >> 5));
+        acc[i] = M::mac(av, a_operand_tr<XP>(k16, 16 * ks, 32 * dt, lane), acc[i]);
+      }
+    }
+  }
+  store_tiles<T, D>(reinterpret_cast<T*>(a.dq_idx) + (int64_t)b * a.dq_sb + (int64_t)ih * a.dq_sh +
+                        (int64_t)t0 * a.dq_st,
+                    a.dq_st, nrows, acc, wave, lane);
+}
+
+template <typename T, int D>
+__global__ __launch_bounds__(kBwdThreads) void kl_dk_kernel(KlBwdK p) {
+  using M = Mfma<T>;
+  using L = KlBwdLds<D>;
+  constexpr int XP = L::XP, SP = L::SP, MT = D / 32, TPW = 2 * MT / 4;
+  extern __shared__ __align__(16) unsigned char smem[];
+  T* sQ = reinterpret_cast<T*>(smem);
+  T* sDT = reinterpret_cast<T*>(smem + L::dsOff);   // DS^T [key][row]
+  const srswa_kl_bwd_args& a = p.a;
+  const int tid = threadIdx.x, wave = tid / kWave, lane = tid % kWave;
+  const int c = blockIdx.x % p.nblk, b = blockIdx.x / p.nblk;
+  f32x16_t acc[TPW];
+#pragma unroll
+  for (int i = 0; i < TPW; ++i) acc[i] = zero16();
+  const uint16_t* q16 = reinterpret_cast<const uint16_t*>(sQ);
+  const int rr = tid / 4, kq = (tid % 4) * 16;
+  for (int ih = 0; ih < a.HI; ++ih) {
+    const uint32_t* tb = p.touch + (((int64_t)b * a.HI + ih) * p.nblk + c) * p.twords;
+    for (int wd = 0; wd < p.twords; ++wd) {
+      uint32_t bits = tb[wd];
+      while (bits) {
+        const int tile = 32 * wd + __ffs(bits) - 1;
+        bits &= bits - 1;
+        const int t0 = tile * kTileRows;
+        const int nrows = min(kTileRows, a.T - t0);
+        __syncthreads();
+        stage_rows<T, D>(sQ, reinterpret_cast<const T*>(a.q_idx) + (int64_t)b * a.qi_sb + (int64_t)ih * a.qi_sh +
+                                 (int64_t)t0 * a.qi_st,
+                         a.qi_st, nrows);
+        {
+          float v[16];
+          const int slot = rr < nrows ? find_slot(a, b, ih, t0 + rr, c) : -1;
+          ds16<T>(a, b, ih, t0 + rr, slot, kq, v);
+#pragma unroll
+          for (int i = 0; i < 16; ++i)
+            reinterpret_cast<uint16_t*>(sDT)[(kq + i) * SP + rr] = (uint16_t)(M::pack2(v[i], 0.f) & 0xffffu);
         }
-      if (found >= 0 && a.grad[(int64_t)b * a.g_sb + (int64_t)ih * a.g_sh + t] == 0.f) found = -1;
-    }
-    // order-preserving compaction: the prefix count of matches before this thread
-    const uint64_t bal = __ballot(found >= 0);
-    const int w = tid / kWave;
-    if ((tid % kWave) == 0) s_wc[w] = __popcll(bal);
-    __syncthreads();
-    int base = 0;
-    for (int i = 0; i < w; ++i) base += s_wc[i];
-    if (found >= 0) {
-      const int idx = base + __popcll(bal & ((1ull << (tid % kWave)) - 1ull));
-      s_row[idx] = (int)r;
-      s_slot[idx] = found;
-    }
-    if (tid == 0) {
-      int n = 0;
-      for (int i = 0; i < kDkThreads / kWave; ++i) n += s_wc[i];
-      s_n = n;
-    }
-    __syncthreads();
-    const int n = s_n;
-    for (int e = 0; e < n; ++e) {
-      const int rr = s_row[e], s = s_slot[e];
-      const int ih = rr / a.T, t = rr % a.T;
-      const float g = a.grad[(int64_t)b * a.g_sb + (int64_t)ih * a.g_sh + t];
-      const float ds = round_to<T>(g * a.dsel[(int64_t)b * a.ds_sb + (int64_t)ih * a.ds_sh + (int64_t)t * a.ds_st +
-                                             (int64_t)s * kChunk + u]);
-      if (ds == 0.f) continue;
-      const T* qr = reinterpret_cast<const T*>(a.q_idx) + (int64_t)b * a.qi_sb + (int64_t)ih * a.qi_sh +
-                    (int64_t)t * a.qi_st + q * DQ;
+        __syncthreads();
+        // dK[key, d] += DS^T[key, row] Q[row, d]
 #pragma unroll
-      for (int e8 = 0; e8 < DQ / 8; ++e8) {
-        const uint4 w4 = *reinterpret_cast<const uint4*>(qr + 8 * e8);
-        const uint32_t ww[4] = {w4.x, w4.y, w4.z, w4.w};
+        for (int ks = 0; ks < 4; ++ks) {
 #pragma unroll
-        for (int k = 0; k < 4; ++k) {
-          acc[8 * e8 + 2 * k] += ds * Mfma<T>::lo(ww[k]);
-          acc[8 * e8 + 2 * k + 1] += ds * Mfma<T>::hi(ww[k]);
+          for (int i = 0; i < TPW; ++i) {
+            const int tix = wave * TPW + i;
+            const int half = tix / MT, dt = tix % MT;
+            const uint4 av =
+                *reinterpret_cast<const uint4*>(sDT + (32 * half + (lane & 31)) * SP + 16 * ks + 8 * (lane >> 5));
+            acc[i] = M::mac(av, a_operand_tr<XP>(q16, 16 * ks, 32 * dt, lane), acc[i]);
+          }
         }
       }
     }
-    __syncthreads();
   }
-  const int key = c * kChunk + u;
-  if (key >= a.Sk) return;
-  T* out = reinterpret_cast<T*>(a.dk_idx) + (int64_t)b * a.dk_sb + (int64_t)key * a.dk_st + q * DQ;
-#pragma unroll
-  for (int e8 = 0; e8 < DQ / 8; ++e8) {
-    uint4 w4;
-    w4.x = Mfma<T>::pack2(acc[8 * e8], acc[8 * e8 + 1]);
-    w4.y = Mfma<T>::pack2(acc[8 * e8 + 2], acc[8 * e8 + 3]);
-    w4.z = Mfma<T>::pack2(acc[8 * e8 + 4], acc[8 * e8 + 5]);
-    w4.w = Mfma<T>::pack2(acc[8 * e8 + 6], acc[8 * e8 + 7]);
-    *reinterpret_cast<uint4*>(out + 8 * e8) = w4;
-  }
+  store_tiles<T, D>(reinterpret_cast<T*>(a.dk_idx) + (int64_t)b * a.dk_sb + (int64_t)c * kChunk * a.dk_st, a.dk_st,
+                    min(kChunk, a.Sk - c * kChunk), acc, wave, lane);
 }
 
 bool al16(const void* p) { return ((uintptr_t)p & 15u) == 0; }
@@ -532,7 +612,17 @@ extern "C" int srswa_gather_kl_fwd(const srswa_kl_args* a, void* stream) {
   return SRSWA_OK;
 }
 
-extern "C" int srswa_gather_kl_bwd(const srswa_kl_bwd_args* a, void* stream) {
+extern "C" int srswa_gather_kl_bwd_workspace(const srswa_kl_bwd_args* a, size_t* scratch_bytes) {
+  if (!a || !scratch_bytes) {
+    set_error("gather kl backward workspace: null argument");
+    return SRSWA_INVALID;
+  }
+  const int64_t words = (int64_t)a->B * a->HI * ceil_div(a->Sk, kChunk) * ceil_div(ceil_div(a->T, kTileRows), 32);
+  *scratch_bytes = (size_t)std::max<int64_t>(words, 0) * 4;
+  return SRSWA_OK;
+}
+
+extern "C" int srswa_gather_kl_bwd(const srswa_kl_bwd_args* a, void* scratch, size_t scratch_bytes, void* stream) {
   if (!a || !a->q_idx || !a->idx_k || !a->sel || !a->dsel || !a->grad || !a->dq_idx || !a->dk_idx) {
     set_error("gather kl backward: null argument");
     return SRSWA_INVALID;
@@ -543,37 +633,44 @@ extern "C" int srswa_gather_kl_bwd(const srswa_kl_bwd_args* a, void* stream) {
   }
   int rc = check_common(a->dtype, a->D, a->block_size, a->K, "gather kl backward");
   if (rc != SRSWA_OK) return rc;
-  bool ok = al16(a->q_idx) && al16(a->dk_idx) && al16(a->idx_k) && al16(a->dq_idx);
-  for (int64_t st : {a->qi_sb, a->qi_sh, a->qi_st, a->dk_sb, a->dk_st, a->ik_sb, a->ik_st, a->dq_sb, a->dq_sh,
-                     a->dq_st})
-    ok = ok && (st * 2) % 16 == 0;
+  bool ok = al16(a->q_idx) && al16(a->idx_k) && al16(a->dsel);
+  for (int64_t st : {a->qi_sb, a->qi_sh, a->qi_st, a->ik_sb, a->ik_st}) ok = ok && (st * 2) % 16 == 0;
+  ok = ok && (a->ds_sb * 4) % 16 == 0 && (a->ds_sh * 4) % 16 == 0 && (a->ds_st * 4) % 16 == 0;
   if (!ok) {
     set_error("gather kl backward: rows must be 16-byte aligned");
     return SRSWA_UNSUPPORTED;
   }
+  if (ceil_div(a->Sk, kChunk) > 64 * 32) {
+    set_error("gather kl backward: more than 2048 key blocks");
+    return SRSWA_UNSUPPORTED;
+  }
+  size_t need = 0;
+  srswa_gather_kl_bwd_workspace(a, &need);
+  if (a->B == 0 || a->T == 0) return SRSWA_OK;
+  if (!scratch || scratch_bytes < need) {
+    set_error("gather kl backward: workspace too small (%zu < %zu)", scratch_bytes, need);
+    return SRSWA_WORKSPACE;
+  }
+  KlBwdK k;
+  k.a = *a;
+  k.ntiles = ceil_div(a->T, kTileRows);
+  k.nblk = ceil_div(a->Sk, kChunk);
+  k.twords = ceil_div(k.ntiles, 32);
+  k.touch = static_cast<uint32_t*>(scratch);
   hipStream_t st = reinterpret_cast<hipStream_t>(stream);
-  const int nblk = ceil_div(a->Sk, kChunk);
-  const int64_t rows = (int64_t)a->B * a->HI * a->T;
-  if (a->B > 0) {
-    const dim3 gdk((unsigned)((int64_t)a->B * nblk));
-    if (a->dtype == SRSWA_BF16) {
-      if (a->D == 128) hipLaunchKernelGGL((kl_dk_kernel<bf16_t, 128>), gdk, dim3(kDkThreads), 0, st, *a, nblk);
-      else hipLaunchKernelGGL((kl_dk_kernel<bf16_t, 64>), gdk, dim3(kDkThreads), 0, st, *a, nblk);
-    } else {
-      if (a->D == 128) hipLaunchKernelGGL((kl_dk_kernel<__half, 128>), gdk, dim3(kDkThreads), 0, st, *a, nblk);
-      else hipLaunchKernelGGL((kl_dk_kernel<__half, 64>), gdk, dim3(kDkThreads), 0, st, *a, nblk);
-    }
+  const int64_t words = (int64_t)need / 4;
+  hipLaunchKernelGGL(kl_zero_kernel, dim3((unsigned)((words + 255) / 256)), dim3(256), 0, st, k.touch, words);
+  const dim3 gdq((unsigned)((int64_t)a->B * a->HI * k.ntiles)), gdk((unsigned)((int64_t)a->B * k.nblk));
+  const size_t lds = a->D == 128 ? KlBwdLds<128>::bytes : KlBwdLds<64>::bytes;
+#define KL_BWD(T_, D_)                                                                      \
+  hipLaunchKernelGGL((kl_dq_kernel<T_, D_>), gdq, dim3(kBwdThreads), lds, st, k);          \
+  hipLaunchKernelGGL((kl_dk_kernel<T_, D_>), gdk, dim3(kBwdThreads), lds, st, k);
+  if (a->dtype == SRSWA_BF16) {
+    if (a->D == 128) { KL_BWD(bf16_t, 128) } else { KL_BWD(bf16_t, 64) }
+  } else {
+    if (a->D == 128) { KL_BWD(__half, 128) } else { KL_BWD(__half, 64) }
   }
-  if (rows > 0) {
-    const dim3 gdq((unsigned)((rows + 3) / 4));
-    if (a->dtype == SRSWA_BF16) {
-      if (a->D == 128) hipLaunchKernelGGL((kl_dq_kernel<bf16_t, 128>), gdq, dim3(256), 0, st, *a);
-      else hipLaunchKernelGGL((kl_dq_kernel<bf16_t, 64>), gdq, dim3(256), 0, st, *a);
-    } else {
-      if (a->D == 128) hipLaunchKernelGGL((kl_dq_kernel<__half, 128>), gdq, dim3(256), 0, st, *a);
-      else hipLaunchKernelGGL((kl_dq_kernel<__half, 64>), gdq, dim3(256), 0, st, *a);
-    }
-  }
+#undef KL_BWD
   const hipError_t e = hipGetLastError();
   if (e != hipSuccess) {
     set_error("gather kl backward launch failed: %s", hipGetErrorString(e));

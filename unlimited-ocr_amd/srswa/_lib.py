@@ -357,7 +357,8 @@ SIGNATURES = {
     "srswa_page_block_bounds": (ctypes.c_int, [ctypes.POINTER(BlockBoundsArgs), _vp]),
     "srswa_page_candidate_mask": (ctypes.c_int, [ctypes.POINTER(CandidateArgs), _vp]),
     "srswa_gather_kl_fwd": (ctypes.c_int, [ctypes.POINTER(KlArgs), _vp]),
-    "srswa_gather_kl_bwd": (ctypes.c_int, [ctypes.POINTER(KlBwdArgs), _vp]),
+    "srswa_gather_kl_bwd_workspace": (ctypes.c_int, [ctypes.POINTER(KlBwdArgs), _szp]),
+    "srswa_gather_kl_bwd": (ctypes.c_int, [ctypes.POINTER(KlBwdArgs), _vp, ctypes.c_size_t, _vp]),
 }
 
 STRUCTS = {"srswa_decode_args": DecodeArgs, "srswa_index_args": IndexArgs,

@@ -94,7 +94,12 @@ def kl_backward(grad, q_idx, idx_k, sel, dsel, *, block_size):
         dq_idx=dq.data_ptr(), dq_sb=dq.stride(0), dq_sh=dq.stride(1), dq_st=dq.stride(2),
         dk_idx=dk.data_ptr(), dk_sb=dk.stride(0), dk_st=dk.stride(1),
         B=B, HI=HI, T=T, Sk=Sk, D=D, K=s.shape[-1], block_size=int(block_size), dtype=_lib.dtype_code(qi.dtype))
-    _lib.check(_lib.lib().srswa_gather_kl_bwd(ctypes.byref(a), _lib.stream_ptr(qi.device)), "srswa_gather_kl_bwd")
+    need = ctypes.c_size_t()
+    _lib.check(_lib.lib().srswa_gather_kl_bwd_workspace(ctypes.byref(a), ctypes.byref(need)),
+               "srswa_gather_kl_bwd_workspace")
+    scr = _lib.scratch(qi.device, need.value)
+    _lib.check(_lib.lib().srswa_gather_kl_bwd(ctypes.byref(a), _lib.ptr(scr), need.value, _lib.stream_ptr(qi.device)),
+               "srswa_gather_kl_bwd")
     return dq, dk.view(idx_k.shape)
 
 
