@@ -358,8 +358,8 @@ def bench_dash(args):
                            tail_pages=2)
         sc = U.headcls_scores_decode(idx_q=c["idx_q"], cache=cache, block_table=bt, seq_lens=sl,
                                      max_block=bt.shape[1], block_size=BS, local_blocks=LW // BS, decode_query_len=1)
-        topi, bias, valid = ops.dash_route(sc[0][:, None, :], None, p)           # [B, 1, K]
-        topi = torch.where(valid, topi, -1).to(torch.int32)[:, 0]                 # [B, K]
+        topi, bias, _ = ops.dash_route(sc[0][:, None, :], None, p, attend_ids=True)   # [B, 1, K], -1 = invalid
+        topi = topi[:, 0]                                                              # [B, K]
         U.dash_sparse_attn_decode(q, c["k_cache"], c["v_cache"], topi[None].expand(H, B, K),
                                   bias[:, 0][None].expand(H, B, K), bt, sl, H, c["scale"], out, 1,
                                   local_blocks=LW // BS, sparse_block_size=BS)

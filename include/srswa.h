@@ -302,6 +302,8 @@ int srswa_kbar_scores(const srswa_kbar_scores_args* a, void* stream);
  *   topi = block ids, valid = cand, bias = valid ? (log(max(prior, floor)) - mu)
  *   / sigma : 0 with mu the mean log-prior over the valid slots.
  * M = topm > 0 ? min(topm, nblk) : nblk must be <= 64; K is clamped to [1, M].
+ * mask_ids != 0 writes -1 instead of the block id in the invalid slots (the
+ * form the gather-attention kernels take), saving the caller a pass.
  * ---------------------------------------------------------------------- */
 typedef struct {
   const float* scores;  int64_t sc_sb, sc_sq;          /* [B, Lq, nblk] fp32, block stride 1 */
@@ -312,6 +314,7 @@ typedef struct {
   int32_t B, Lq, nblk, K, topm;
   float idx_scale, floor;
   double sigma;
+  int32_t mask_ids;                                    /* 1: invalid slots get id -1 */
 } srswa_route_args;
 
 int srswa_dash_route(const srswa_route_args* a, void* stream);

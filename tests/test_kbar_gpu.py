@@ -70,3 +70,7 @@ def test_pages_scores_and_tail_refresh(dev, d, use_hc):
     got = sd[0].cpu()
     assert torch.equal(got > O.SCORE_NEG * 0.5, ref > O.SCORE_NEG * 0.5)
     _close(got, ref, "decode scores")
+    # a score row wider than the block table: the extra columns are SCORE_NEG
+    sw = U.headcls_scores_decode(idx_q=dq.to(dev), cache=cache, block_table=bt.to(dev), seq_lens=sl2.to(dev),
+                                 max_block=nb + 3, block_size=page, local_blocks=lb, decode_query_len=dql)
+    assert torch.equal(sw[0, :, :nb], sd[0]) and bool((sw[0, :, nb:] == O.SCORE_NEG).all())

@@ -62,3 +62,30 @@ def test_paged_decode_matches_oracle(dev, name):
         assert rel <= 1e-5, rel
     else:
         assert_close_lowp(out.cpu(), ref, c["dtype"], 2e-2, name)
+
+
+@pytest.mark.parametrize("with_bias", [True, False])
+def test_paged_decode_head_expanded_ids(dev, with_bias):
+    """One id / bias row shared by every kv head, passed as a stride-0 view
+    (the DASH step's topi[None].expand(H, ...)): the oracle on the expanded
+    tensors, and bit-identical to the contiguous copy."""
+    from srswa import unlimited_dash_ops as U
+
+    c = dict(CASES["bf16_p64"], with_bias=with_bias)
+    q, kc, vc, topk, bias, bt, sl = _case(77, **c)
+    Hkv = c["Hkv"]
+    ids = topk[0][None].expand(Hkv, -1, -1)
+    bi = None if bias is None else bias[0][None].expand(Hkv, -1, -1)
+    scale = 1 / math.sqrt(c["D"])
+    outs = []
+    for t, b in ((ids.to(dev), None if bi is None else bi.to(dev)),
+                 (ids.contiguous().to(dev), None if bi is None else bi.contiguous().to(dev))):
+        out = torch.empty(q.shape, dtype=q.dtype, device=dev)
+        U.dash_sparse_attn_decode(q.to(dev), kc.to(dev), vc.to(dev), t, b, bt.to(dev), sl.to(dev), Hkv, scale, out,
+                                  c["dql"], local_blocks=c["lb"], sparse_block_size=c["page"])
+        outs.append(out)
+    assert outs[0].is_contiguous()
+    assert torch.equal(outs[0], outs[1])
+    ref = O.paged_decode_attend(q.double(), kc.double(), vc.double(), ids.contiguous(),
+                                None if bi is None else bi.contiguous().double(), bt, sl, c["dql"], c["lb"], scale)
+    assert_close_lowp(outs[0].cpu(), ref, c["dtype"], 2e-2, "expanded ids")

@@ -26,6 +26,11 @@ def _check(dev, sc, cand, p):
     assert torch.equal(valid.cpu(), rv)
     err = (bias.cpu() - rb).abs() / rb.abs().clamp(min=1.0)
     assert err.max().item() <= 1e-5, err.max().item()
+    # attend-ready ids: int32, -1 in the invalid slots; bias and valid unchanged
+    ai, ab, av = ops.dash_route(sc.to(dev), None if cand is None else cand.to(dev), p, attend_ids=True)
+    assert ai.dtype == torch.int32
+    assert torch.equal(ai.cpu(), torch.where(rv, rx, -1).to(torch.int32))
+    assert torch.equal(ab, bias) and torch.equal(av, valid)
 
 
 @pytest.mark.parametrize("nblk,K,topm", [(2048, 12, 16), (3000, 12, 16), (5000, 8, 16), (300, 8, 64),
@@ -51,6 +56,22 @@ def test_route_ties_and_nonfinite(dev):
     sc[..., 90:] = O.SCORE_NEG
     _check(dev, sc, None, P)
     _check(dev, sc, torch.rand(2, 4, 96, generator=g) > 0.3, dict(P, sigma=0.7, floor=1e-6))
+
+
+@pytest.mark.parametrize("nblk", [2048, 300, 4000])
+def test_route_many_keys_in_few_lanes(dev, nblk):
+    """Blocks j = 0, 1 (mod 64) hold the largest scores: the threshold from the
+    per-lane maxima then admits more than 64 keys and the kernel takes its
+    round-by-round selection; j = 5 (mod 64) alone stays on the sorted path."""
+    g = torch.Generator().manual_seed(11)
+    j = torch.arange(nblk)
+    sc = torch.randn(2, 2, nblk, generator=g) * 0.1
+    sc[0, :, (j % 64) <= 1] += 5.0
+    sc[1, :, (j % 64) == 5] += 5.0
+    sc[..., -3:] = O.SCORE_NEG
+    for cand in (None, torch.rand(2, 2, nblk, generator=g) > 0.2):
+        _check(dev, sc, cand, dict(P, K=8, topm=16))
+        _check(dev, sc, cand, dict(P, K=16, topm=64))
 
 
 def test_route_expanded_mask_and_decode_shapes(dev):

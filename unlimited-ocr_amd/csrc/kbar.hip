@@ -10,9 +10,9 @@
 // kbar_pages_kernel: one wavefront per (request, logical block); the page's
 //   real keys are streamed once and reduced to an fp32 summary row written
 //   at the page id (summary.h).
-// kbar_scores_kernel: one wavefront per (query row, 64 blocks); 32 lanes x
-//   16 bytes read one fp32 summary row (D = 128) so two blocks are scored
-//   per step, the dot finished by a 32-lane butterfly.
+// kbar_scores_kernel: one wavefront per (query row, 64 blocks), every summary
+//   row of the chunk in flight at once, the dots finished by a transposing
+//   butterfly.
 #include "summary.h"
 
 namespace srswa {
@@ -48,12 +48,38 @@ __global__ __launch_bounds__(kKbWaves * kWave) void kbar_pages_kernel(srswa_kbar
   }
 }
 
-// D fp32 dims = D / 4 lanes of 16 bytes; 64 / (D / 4) blocks per step
+// One level of the transposing butterfly (then the next, HALF a compile-time
+// constant so z stays in registers): lanes differing in bit HALF of c swap the
+// halves of z they do not keep and add them to the halves they do.
+template <int HALF, int N>
+__device__ __forceinline__ void transpose_sum(float (&z)[N], int c) {
+  if constexpr (HALF >= 1) {
+    const bool hi = (c & HALF) != 0;
+#pragma unroll
+    for (int i = 0; i < HALF; ++i) {
+      const float keep = hi ? z[i + HALF] : z[i];
+      const float send = hi ? z[i] : z[i + HALF];
+      z[i] = keep + __shfl_xor(send, HALF, kWave);
+    }
+    transpose_sum<HALF / 2>(z, c);
+  }
+}
+
+// kbar_scores_kernel: one wavefront per (query row, 64 blocks).  Lane l reads
+//   the block-table entry of block b0 + l once; then every summary row of the
+//   chunk is fetched at once (LPB = D/4 lanes x 16 bytes per row, BPS = 64/LPB
+//   rows per step, STEPS = LPB steps, all loads in flight before the first
+//   product), and the LPB-lane dot products are finished by a transposing
+//   butterfly: at each level a lane keeps half of its partial sums and adds its
+//   partner's matching half, so after log2(LPB) levels lane (sub, c) holds the
+//   full dot of step c, block b0 + BPS c + sub (31 exchanges for D = 128
+//   instead of 5 per step).
 template <int D>
 __global__ __launch_bounds__(kKbWaves * kWave) void kbar_scores_kernel(srswa_kbar_scores_args a, int chunks,
                                                                        float inv_sqrt_d) {
   constexpr int LPB = D / 4;               // lanes per summary row
   constexpr int BPS = kWave / LPB;         // blocks per step
+  constexpr int STEPS = kWave / BPS;       // == LPB
   const int wave = threadIdx.x / kWave, lane = threadIdx.x % kWave;
   const int64_t w = (int64_t)blockIdx.x * kKbWaves + wave;
   if (w >= (int64_t)a.nrows * chunks) return;
@@ -64,23 +90,29 @@ __global__ __launch_bounds__(kKbWaves * kWave) void kbar_scores_kernel(srswa_kba
   const int qblk = pos >= 0 ? pos / a.page_size : -1;
   const int lim = min(min(qblk - a.local_blocks, ceil_div(max(sl, 0), a.page_size) - 1), a.max_blocks - 1);
   const int sub = lane / LPB, c = lane % LPB;
-  const float4 qv = *reinterpret_cast<const float4*>(a.q + (int64_t)n * a.q_sn + c * 4);
-  float* out = a.scores + (int64_t)n * a.sc_sn;
+  const float* qrow = a.q + (int64_t)n * a.q_sn + c * 4;
+  const float4 qv = *reinterpret_cast<const float4*>(qrow);
   const int b0 = ch * kWave;
-  for (int s = 0; s < kWave; s += BPS) {
-    const int blk = b0 + s + sub;
-    const bool remote = blk <= lim && pos >= 0;
-    float z = 0.f;
-    if (remote) {
-      const int page = a.block_table[(int64_t)r * a.bt_sr + blk];
-      const float4 kv = *reinterpret_cast<const float4*>(a.kbar + (int64_t)page * a.kb_sp + c * 4);
-      z = qv.x * kv.x + qv.y * kv.y + qv.z * kv.z + qv.w * kv.w;
-    }
+  // lane l: page of block b0 + l (-1 = not a remote block)
+  const int lb = b0 + lane;
+  const int lpage = (pos >= 0 && lb <= lim) ? a.block_table[(int64_t)r * a.bt_sr + lb] : -1;
+  float4 kv[STEPS];
 #pragma unroll
-    for (int o = LPB / 2; o >= 1; o >>= 1) z += __shfl_xor(z, o, kWave);
-    if (c == 0 && blk < a.width)
-      out[blk] = remote ? fminf(fmaxf(z * inv_sqrt_d, -kActClamp), kActClamp) : kScoreNeg;
+  for (int s = 0; s < STEPS; ++s) {
+    const int pg = __shfl(lpage, s * BPS + sub, kWave);
+    // a non-remote block reads the row's own query (in bounds) and is dropped below
+    const float* src = pg >= 0 ? a.kbar + (int64_t)pg * a.kb_sp + c * 4 : qrow;
+    kv[s] = *reinterpret_cast<const float4*>(src);
   }
+  float z[STEPS];
+#pragma unroll
+  for (int s = 0; s < STEPS; ++s) z[s] = qv.x * kv[s].x + qv.y * kv[s].y + qv.z * kv[s].z + qv.w * kv[s].w;
+  transpose_sum<STEPS / 2>(z, c);
+  const int blk = b0 + BPS * c + sub;
+  const bool remote = blk <= lim && pos >= 0;
+  if (blk < a.width)
+    a.scores[(int64_t)n * a.sc_sn + blk] =
+        remote ? fminf(fmaxf(z[0] * inv_sqrt_d, -kActClamp), kActClamp) : kScoreNeg;
 }
 
 bool al16k(const void* p) { return ((uintptr_t)p & 15u) == 0; }

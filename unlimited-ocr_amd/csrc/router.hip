@@ -29,19 +29,49 @@ namespace {
 constexpr float kScoreNeg = -1.0e9f;    // _SCORE_NEG, HF/dash_attention.py:741
 constexpr float kEntmaxNeg = -1.0e4f;   // _ENTMAX_NEG, HF/modeling_deepseekv2.py:65
 
-__device__ __forceinline__ uint64_t route_key(float s, int idx) {
-  uint32_t u = __float_as_uint(s);
+// Order key of a window entry: the fp32 x mapped to an order-preserving
+// unsigned (high word), then 0x7fffffff - idx (equal x: the lower block id is
+// the larger key), then the candidate flag in bit 0 so the selected key alone
+// gives back x, the block id and the flag.  Every key of a real block is > 0.
+__device__ __forceinline__ uint64_t route_key(float x, int idx, bool cand) {
+  uint32_t u = __float_as_uint(x);
   u = (u & 0x80000000u) ? ~u : (u | 0x80000000u);
-  return ((uint64_t)u << 32) | (uint64_t)(0xffffffffu - (uint32_t)idx);
+  return ((uint64_t)u << 32) | ((uint64_t)(0x7fffffffu - (uint32_t)idx) << 1) | (cand ? 1u : 0u);
 }
+__device__ __forceinline__ float key_x(uint64_t k) {
+  const uint32_t u = (uint32_t)(k >> 32);
+  return __uint_as_float((u & 0x80000000u) ? (u & 0x7fffffffu) : ~u);
+}
+__device__ __forceinline__ int key_id(uint64_t k) { return (int)(0x7fffffffu - ((uint32_t)k >> 1)); }
+__device__ __forceinline__ bool key_cand(uint64_t k) { return (k & 1u) != 0; }
+__device__ __forceinline__ uint64_t kmax(uint64_t a, uint64_t b) { return a > b ? a : b; }
 
 __device__ __forceinline__ uint64_t wave_max_key(uint64_t v) {
 #pragma unroll
-  for (int o = 32; o >= 1; o >>= 1) {
-    const uint64_t w = __shfl_xor(v, o, kWave);
-    v = w > v ? w : v;
-  }
+  for (int o = 32; o >= 1; o >>= 1) v = kmax(v, __shfl_xor(v, o, kWave));
   return v;
+}
+
+// Bitonic sort of one value per lane, descending over the wave (lane 0 the
+// largest): stage (K, J) compares lanes J apart; blocks with bit K of the lane
+// clear end descending, the others ascending, and K = 64 makes one run.
+template <int K, int J>
+__device__ __forceinline__ uint64_t bitonic_merge(uint64_t v, int lane) {
+  const uint64_t w = __shfl_xor(v, J, kWave);
+  const bool take_max = ((lane & J) == 0) == ((lane & K) == 0);
+  v = take_max ? kmax(v, w) : (w > v ? v : w);
+  if constexpr (J > 1) return bitonic_merge<K, J / 2>(v, lane);
+  else return v;
+}
+template <int K>
+__device__ __forceinline__ uint64_t wave_sort_desc(uint64_t v, int lane) {
+  v = bitonic_merge<K, K / 2>(v, lane);
+  if constexpr (K < kWave) return wave_sort_desc<K * 2>(v, lane);
+  else return v;
+}
+
+__device__ __forceinline__ float readlane_f(float v, int l) {
+  return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), l));
 }
 
 struct RouteK {
@@ -50,13 +80,19 @@ struct RouteK {
   float inv_sigma;
 };
 
-// NPL > 0: each lane keeps the order keys of its NPL blocks (j = lane + 64 i)
-// in registers, built once, so the M selection rounds never touch memory;
-// NPL == 0 rescans the row from memory every round (rows above 4096 blocks).
+// NPL > 0: each lane keeps the keys of its NPL blocks (j = lane + 64 i) in
+// registers.  The window is found without M rounds over every key: the M-th
+// largest of the 64 lane maxima is a threshold T with at least M keys >= T
+// (those M maxima); the keys >= T (at most 64 in any ordinary row) are
+// compacted through LDS and sorted across the wave, lane k then holding the
+// k-th largest key.  A row with more than 64 keys >= T takes the M rounds of
+// "largest key below the previous one" instead.  NPL == 0 rescans the row
+// from memory every round (rows above 4096 blocks).
 template <int NPL>
 __global__ __launch_bounds__(256) void dash_route_kernel(RouteK p) {
 #pragma clang fp contract(off)
   const srswa_route_args& a = p.a;
+  __shared__ uint64_t s_sel[4][kWave];
   const int wave = threadIdx.x / kWave, lane = threadIdx.x % kWave;
   const int64_t row = (int64_t)blockIdx.x * 4 + wave;
   if (row >= (int64_t)a.B * a.Lq) return;
@@ -65,61 +101,114 @@ __global__ __launch_bounds__(256) void dash_route_kernel(RouteK p) {
   const uint8_t* c = a.cand ? a.cand + (int64_t)b * a.cd_sb + (int64_t)q * a.cd_sq : nullptr;
   const int n = a.nblk, M = p.M, K = p.K;
 
+  // the row's scores (and mask bytes) in one batch, past-end lanes reading the
+  // last block (in bounds) and dropped below
+  constexpr int NR = NPL > 0 ? NPL : 1;
+  float sv[NR];
+  uint8_t cv[NR];
   bool any = false;
-  if (c)
+  if (NPL > 0) {
+#pragma unroll
+    for (int i = 0; i < NPL; ++i) sv[i] = s[min(lane + i * kWave, n - 1)];
+    if (c) {
+#pragma unroll
+      for (int i = 0; i < NPL; ++i) cv[i] = c[min(lane + i * kWave, n - 1)];
+#pragma unroll
+      for (int i = 0; i < NPL; ++i) any |= lane + i * kWave < n && sv[i] > kScoreNeg * 0.5f && cv[i] != 0;
+    } else {
+#pragma unroll
+      for (int i = 0; i < NPL; ++i) cv[i] = 1;
+    }
+  } else if (c) {
     for (int j = lane; j < n; j += kWave) any |= (s[j] > kScoreNeg * 0.5f) && c[j] != 0;
+  }
   const bool use_c = c != nullptr && __any(any);
-  auto xval = [&](int j, bool& isc) {
-    const float v = s[j];
-    isc = (v > kScoreNeg * 0.5f) && (!use_c || c[j] != 0);
+  auto key_of = [&](float v, bool cbit, int j) {
+    const bool isc = (v > kScoreNeg * 0.5f) && (!use_c || cbit);
     const float x = v * a.idx_scale;
-    return (isc && isfinite(x)) ? x : kEntmaxNeg;
+    return route_key((isc && isfinite(x)) ? x : kEntmaxNeg, j, isc);
   };
 
-  // top-M window: M rounds of "largest key below the previous one"
-  uint64_t keys[NPL > 0 ? NPL : 1];
+  uint64_t my_key = 0;
+  bool sorted = false;
+  uint64_t keys[NR];
   if (NPL > 0) {
 #pragma unroll
     for (int i = 0; i < NPL; ++i) {
       const int j = lane + i * kWave;
-      bool isc;
-      keys[i] = j < n ? route_key(xval(j, isc), j) : 0ull;   // real keys are > 0
+      const uint64_t k = key_of(sv[i], cv[i] != 0, j);
+      keys[i] = j < n ? k : 0ull;
     }
-  }
-  uint64_t prev = ~0ull;
-  int my_id = 0;
-  for (int k = 0; k < M; ++k) {
-    uint64_t best = 0;
-    if (NPL > 0) {
+    uint64_t m0 = 0, m1 = 0, m2 = 0, m3 = 0;
 #pragma unroll
-      for (int i = 0; i < NPL; ++i) {
-        const uint64_t key = keys[i];
-        best = (key < prev && key > best) ? key : best;
-      }
-    } else {
-      for (int j = lane; j < n; j += kWave) {
-        bool isc;
-        const uint64_t key = route_key(xval(j, isc), j);
-        if (key < prev && key > best) best = key;
-      }
+    for (int i = 0; i < NPL; i += 4) {
+      m0 = kmax(m0, keys[i]);
+      m1 = kmax(m1, keys[i + 1]);
+      m2 = kmax(m2, keys[i + 2]);
+      m3 = kmax(m3, keys[i + 3]);
     }
-    best = wave_max_key(best);
-    prev = best;
-    if (lane == k) my_id = (int)(0xffffffffu - (uint32_t)(best & 0xffffffffu));
+    // min(n, 64) >= M lanes hold a real key, so T > 0
+    const uint64_t lanes_sorted = wave_sort_desc<2>(kmax(kmax(m0, m1), kmax(m2, m3)), lane);
+    const uint64_t T = __shfl(lanes_sorted, M - 1, kWave);
+    int cnt = 0;
+#pragma unroll
+    for (int i = 0; i < NPL; ++i) cnt += keys[i] >= T ? 1 : 0;
+    int incl = cnt;
+#pragma unroll
+    for (int o = 1; o < kWave; o <<= 1) {
+      const int t = __shfl_up(incl, o, kWave);
+      incl += lane >= o ? t : 0;
+    }
+    const int total = __shfl(incl, kWave - 1, kWave);
+    if (total <= kWave) {
+      int off = incl - cnt;
+#pragma unroll
+      for (int i = 0; i < NPL; ++i)
+        if (keys[i] >= T) s_sel[wave][off++] = keys[i];
+      __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+      __builtin_amdgcn_wave_barrier();
+      __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+      my_key = wave_sort_desc<2>(lane < total ? s_sel[wave][lane] : 0ull, lane);
+      sorted = true;
+    }
   }
-  bool my_c = false;
-  const float my_x = lane < M ? xval(my_id, my_c) : kEntmaxNeg;
-  my_c = my_c && lane < M;
+  if (!sorted) {
+    // M rounds of "largest key below the previous one"
+    uint64_t prev = ~0ull;
+    for (int k = 0; k < M; ++k) {
+      uint64_t best = 0;
+      if (NPL > 0) {
+#pragma unroll
+        for (int i = 0; i < NPL; ++i) {
+          const uint64_t key = keys[i];
+          best = (key < prev && key > best) ? key : best;
+        }
+      } else {
+        for (int j = lane; j < n; j += kWave) {
+          const uint64_t key = key_of(s[j], c == nullptr || c[j] != 0, j);
+          if (key < prev && key > best) best = key;
+        }
+      }
+      best = wave_max_key(best);
+      prev = best;
+      if (lane == k) my_key = best;
+    }
+  }
+  const int my_id = key_id(my_key);
+  const bool my_c = lane < M && key_cand(my_key);
+  const float my_x = lane < M ? key_x(my_key) : kEntmaxNeg;
 
   // 1.5-entmax over the window (descending already)
-  const float xmax = __shfl(my_x, 0, kWave);
+  const float xmax = readlane_f(my_x, 0);
   const float z = (my_x - xmax) / 2.f;
   const float zsq = z * z;
   double cs = 0.0, cs2 = 0.0;
   float my_cs = 0.f, my_cs2 = 0.f;
-  for (int k = 0; k < M; ++k) {
-    cs += (double)__shfl(z, k, kWave);
-    cs2 += (double)__shfl(zsq, k, kWave);
+#pragma unroll
+  for (int k = 0; k < kWave; ++k) {
+    if (k >= M) break;
+    cs += (double)readlane_f(z, k);
+    cs2 += (double)readlane_f(zsq, k);
     if (lane == k) {
       my_cs = (float)cs;
       my_cs2 = (float)cs2;
@@ -145,12 +234,16 @@ __global__ __launch_bounds__(256) void dash_route_kernel(RouteK p) {
   cnt = cnt < 1 ? 1 : cnt;
   const float lv = v ? logp : 0.f;
   float sum = 0.f;
-  for (int k = 0; k < K; ++k) sum += __shfl(lv, k, kWave);
+#pragma unroll
+  for (int k = 0; k < kWave; ++k) {
+    if (k >= K) break;
+    sum += readlane_f(lv, k);
+  }
   const float mu = sum / (float)cnt;
   const float diff = logp - mu;
   const float bias = v ? diff * p.inv_sigma : 0.f;
   if (lane < K) {
-    a.topi[(int64_t)b * a.ti_sb + (int64_t)q * a.ti_sq + lane] = my_id;
+    a.topi[(int64_t)b * a.ti_sb + (int64_t)q * a.ti_sq + lane] = (a.mask_ids && !v) ? -1 : my_id;
     a.bias[(int64_t)b * a.bi_sb + (int64_t)q * a.bi_sq + lane] = bias;
     a.valid[(int64_t)b * a.va_sb + (int64_t)q * a.va_sq + lane] = v ? 1 : 0;
   }

@@ -191,7 +191,7 @@ class RouteArgs(ctypes.Structure):
         ("valid", _vp), ("va_sb", _i64), ("va_sq", _i64),
         ("B", _i32), ("Lq", _i32), ("nblk", _i32), ("K", _i32), ("topm", _i32),
         ("idx_scale", ctypes.c_float), ("floor", ctypes.c_float),
-        ("sigma", ctypes.c_double),
+        ("sigma", ctypes.c_double), ("mask_ids", _i32),
     ]
 
 

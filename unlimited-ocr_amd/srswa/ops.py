@@ -294,12 +294,16 @@ def prepare_gather_decode_paged(q, k_cache, v_cache, topk_idx, blk_bias, block_t
     for t in (q, k_cache, v_cache):
         if t.stride(-1) != 1:
             raise UnsupportedShape("head dim must be contiguous")
-    ti = _i32(topk_idx).contiguous()
+    # ids and bias are read through strides (a head-expanded view is taken as
+    # is); the kernel addresses both with the ids' strides
+    ti = _i32(topk_idx)
     bias = None
     if blk_bias is not None:
         if tuple(blk_bias.shape) != tuple(topk_idx.shape):
             raise ValueError(f"blk_bias shape {tuple(blk_bias.shape)} != topk_idx {tuple(topk_idx.shape)}")
-        bias = blk_bias.to(torch.float32).contiguous()
+        bias = blk_bias.to(torch.float32)
+        if bias.stride() != ti.stride():
+            ti, bias = ti.contiguous(), bias.contiguous()
     bt = _i32(block_table)
     if bt.stride(-1) != 1:
         bt = bt.contiguous()
@@ -399,13 +403,15 @@ def kbar_scores(q, kbar, block_table, seq_lens, *, width, page_size, local_block
 # ---------------------------------------------------------------------------
 # DASH router
 # ---------------------------------------------------------------------------
-def dash_route(block_scores, block_cand, p):
+def dash_route(block_scores, block_cand, p, *, attend_ids=False):
     """``_infer_route_select`` (HF/modeling_deepseekv2.py:338-362) on the GPU.
 
     block_scores [B, Lq, nblk] fp32 (``SCORE_NEG`` = not a remote block);
     block_cand [B, Lq, nblk] bool page mask or None; ``p`` the router's
     ``_infer_params`` dict (idx_scale, floor, sigma, K, topm).  Returns
-    (topi [B, Lq, K] int64, bias [B, Lq, K] fp32, valid [B, Lq, K] bool).
+    (topi [B, Lq, K] int64, bias [B, Lq, K] fp32, valid [B, Lq, K] bool);
+    with ``attend_ids`` topi is int32 with -1 in the invalid slots instead
+    (``torch.where(valid, topi, -1)``, the ids the gather-attention kernels take).
     Raises ``UnsupportedShape`` for a top-M window above 64 blocks."""
     _require_cuda(block_scores, block_cand)
     B, Lq, nblk = block_scores.shape
@@ -430,9 +436,10 @@ def dash_route(block_scores, block_cand, p):
         bias=bias.data_ptr(), bi_sb=bias.stride(0), bi_sq=bias.stride(1),
         valid=valid.data_ptr(), va_sb=valid.stride(0), va_sq=valid.stride(1),
         B=B, Lq=Lq, nblk=nblk, K=int(p["K"]), topm=int(p["topm"]),
-        idx_scale=float(p["idx_scale"]), floor=float(p["floor"]), sigma=float(p["sigma"]))
+        idx_scale=float(p["idx_scale"]), floor=float(p["floor"]), sigma=float(p["sigma"]),
+        mask_ids=1 if attend_ids else 0)
     _lib.check(_lib.lib().srswa_dash_route(ctypes.byref(a), _lib.stream_ptr(sc.device)), "srswa_dash_route")
-    return topi.to(torch.int64), bias, valid
+    return (topi if attend_ids else topi.to(torch.int64)), bias, valid
 
 
 # ---------------------------------------------------------------------------

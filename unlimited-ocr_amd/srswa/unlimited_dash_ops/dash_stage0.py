@@ -69,7 +69,9 @@ def headcls_scores_decode(*, idx_q, cache, block_table, seq_lens, max_block, blo
     dql = max(1, int(decode_query_len))
     R = int(seq_lens.shape[0])
     width = min(int(max_block), block_table.shape[1])
-    out = torch.full((1, R * dql, int(max_block)), -1.0e9, dtype=torch.float32, device=idx_q.device)
+    out = torch.empty((1, R * dql, int(max_block)), dtype=torch.float32, device=idx_q.device)
+    if width < int(max_block):            # the kernel writes every column below width
+        out[..., width:] = -1.0e9
     ops.kbar_scores(idx_q, cache.k_bar, block_table, seq_lens, width=width, page_size=int(block_size),
                     local_blocks=local_blocks, dql=dql, out=out[0, :, :width])
     return out
