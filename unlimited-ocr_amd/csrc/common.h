@@ -91,6 +91,27 @@ __device__ __forceinline__ float wave_sum(float v) {
   return v;
 }
 
+// Reduce-scatter of N partial sums per lane over the 2 O lanes of a row (c =
+// the lane's index in the row): at each level the lanes differing in bit O of c
+// swap the halves of part they do not keep and add them to the halves they do.
+// After log2(N) levels, part[0] of lane c holds the row-wide sum of partial
+// c / (2 O / N).  The levels are template arguments: a run-time-halving loop
+// is left rolled by hipcc and turns part[] into a compare / select chain.
+template <int N, int O, int NA>
+__device__ __forceinline__ void reduce_scatter(float (&part)[NA], int c) {
+  if constexpr (N > 1) {
+    static_assert(O >= 1 && N <= NA, "reduce_scatter: a level without a lane bit");
+    const bool upper = (c & O) != 0;
+#pragma unroll
+    for (int j = 0; j < N / 2; ++j) {
+      const float send = upper ? part[j] : part[j + N / 2];
+      const float keep = upper ? part[j + N / 2] : part[j];
+      part[j] = keep + __shfl_xor(send, O, kWave);
+    }
+    reduce_scatter<N / 2, O / 2>(part, c);
+  }
+}
+
 __host__ __device__ constexpr int ceil_div(int a, int b) { return (a + b - 1) / b; }
 
 }  // namespace srswa

@@ -314,16 +314,7 @@ __global__ __launch_bounds__(kDecodeWaves * kWave) void decode_kernel(DecodeK p)
 #pragma unroll
     for (int i = 0; i < NI; ++i) part[i] = qf.dot(kr[i]);
     // reduce-scatter across the LPR lanes of a row: NI partials -> 1 score
-#pragma unroll
-    for (int n = NI, o = LPR / 2; n > 1; n >>= 1, o >>= 1) {
-      const bool upper = (c & o) != 0;
-#pragma unroll
-      for (int j = 0; j < n / 2; ++j) {
-        const float send = upper ? part[j] : part[j + n / 2];
-        const float keep = upper ? part[j + n / 2] : part[j];
-        part[j] = keep + __shfl_xor(send, o, kWave);
-      }
-    }
+    reduce_scatter<NI, LPR / 2>(part, c);
 #pragma unroll
     for (int o = DUP / 2; o >= 1; o >>= 1) part[0] += __shfl_xor(part[0], o, kWave);
     const int i_own = c / DUP;                    // which instruction's key this lane holds

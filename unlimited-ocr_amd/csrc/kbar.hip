@@ -48,23 +48,6 @@ __global__ __launch_bounds__(kKbWaves * kWave) void kbar_pages_kernel(srswa_kbar
   }
 }
 
-// One level of the transposing butterfly (then the next, HALF a compile-time
-// constant so z stays in registers): lanes differing in bit HALF of c swap the
-// halves of z they do not keep and add them to the halves they do.
-template <int HALF, int N>
-__device__ __forceinline__ void transpose_sum(float (&z)[N], int c) {
-  if constexpr (HALF >= 1) {
-    const bool hi = (c & HALF) != 0;
-#pragma unroll
-    for (int i = 0; i < HALF; ++i) {
-      const float keep = hi ? z[i + HALF] : z[i];
-      const float send = hi ? z[i] : z[i + HALF];
-      z[i] = keep + __shfl_xor(send, HALF, kWave);
-    }
-    transpose_sum<HALF / 2>(z, c);
-  }
-}
-
 // kbar_scores_kernel: one wavefront per (query row, 64 blocks).  Lane l reads
 //   the block-table entry of block b0 + l once; then every summary row of the
 //   chunk is fetched at once (LPB = D/4 lanes x 16 bytes per row, BPS = 64/LPB
@@ -107,7 +90,7 @@ __global__ __launch_bounds__(kKbWaves * kWave) void kbar_scores_kernel(srswa_kba
   float z[STEPS];
 #pragma unroll
   for (int s = 0; s < STEPS; ++s) z[s] = qv.x * kv[s].x + qv.y * kv[s].y + qv.z * kv[s].z + qv.w * kv[s].w;
-  transpose_sum<STEPS / 2>(z, c);
+  reduce_scatter<STEPS, LPB / 2>(z, c);
   const int blk = b0 + BPS * c + sub;
   const bool remote = blk <= lim && pos >= 0;
   if (blk < a.width)

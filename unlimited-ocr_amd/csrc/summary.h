@@ -67,16 +67,7 @@ __device__ __forceinline__ void summarize_rows(const T* kbase, int64_t k_st, int
         for (int e = 0; e < EPV; ++e) s = fmaf(f[e], hcf[e], s);
         part[i] = s;
       }
-#pragma unroll
-      for (int n = NI, o = LPR / 2; n > 1; n >>= 1, o >>= 1) {
-        const bool upper = (c & o) != 0;
-#pragma unroll
-        for (int jj = 0; jj < n / 2; ++jj) {
-          const float send = upper ? part[jj] : part[jj + n / 2];
-          const float keep = upper ? part[jj + n / 2] : part[jj];
-          part[jj] = keep + __shfl_xor(send, o, kWave);
-        }
-      }
+      reduce_scatter<NI, LPR / 2>(part, c);
       const int key = j0 + c * RPI + r;                 // the key this lane owns
       float aw = fminf(fmaxf(part[0] * inv_sqrt_d, -kActClamp), kActClamp);
       aw = key < nkeys ? aw : -INFINITY;
