@@ -190,7 +190,8 @@ typedef struct {
   int32_t dtype;
 } srswa_bwd_args;
 
-/* scratch bytes: delta [B, T, HQ] fp32 + the query-tile touch bitmap */
+/* scratch bytes: delta [B, T, HQ] fp32 + q*scale [B, HQ, T, D] in the input
+ * dtype (the dK / dV operand) + the query-tile touch bitmap */
 size_t srswa_gather_bwd_workspace(const srswa_bwd_args* a);
 int srswa_gather_bwd(const srswa_bwd_args* a, void* scratch, size_t scratch_bytes, void* stream);
 

@@ -9,7 +9,8 @@
 // [B, HI, T, M] block_mask scatter, HF/sparse_gather_triton.py:329,339-343).
 //
 // Kernels, in stream order:
-//   1. delta_kernel  -- delta[b,t,hq] = sum_d O*dO in fp32.
+//   1. delta_kernel  -- delta[b,t,hq] = sum_d O*dO in fp32, and q*scale rounded
+//      to the input dtype as [B, HQ, T, D] (the dK operand, staged as is).
 //   2. zero + touch_kernel -- bit (chunk c, query tile tau) set when some row of
 //      tau reads a REMOTE key of chunk c.  The bitmap is tile-granular (64x
 //      smaller than the reference's per-token dense block mask) and its
@@ -21,7 +22,8 @@
 //      no atomics (the reference uses tl.atomic_add).
 //   4. dkv_kernel -- per 64-key chunk and kv head, every query tile whose
 //      window covers the chunk or whose touch bit is set, in ascending order:
-//      S = Q K^T, dP = dO V^T, dV^T += dO^T P, dK^T += Q^T dS.  Deterministic
+//      S = Q K^T, dP = dO V^T, dV^T += dO^T P, dK^T += Q^T dS, four waves split
+//      by key half and role (S / softmax / dV, dP / dS / dK).  Deterministic
 //      (fixed visiting order, no atomics).
 // Rounding points follow the reference: q*scale and P / dS are rounded to the
 // input dtype before their products; delta, P, dS and all accumulators are fp32.
@@ -42,6 +44,7 @@ struct BwdK {
   int chunks_off, sid_off;        // dQ LDS byte offsets of the chunk list and sorted ids
   float* delta;       // [B, T, HQ]
   uint32_t* touch;    // [B, HI, nchunk, twords]
+  void* qs;           // [B, HQ, T, D] q * scale rounded to the input dtype (dK / dV operand)
 };
 
 // -------------------------------------------------------------- 1. delta
@@ -69,6 +72,16 @@ __global__ __launch_bounds__(256) void delta_kernel(BwdK p) {
     const uint32_t* g4 = reinterpret_cast<const uint32_t*>(&gw);
 #pragma unroll
     for (int e = 0; e < 4; ++e) s += M::lo(o4[e]) * M::lo(g4[e]) + M::hi(o4[e]) * M::hi(g4[e]);
+    if (p.qs) {
+      // q * scale rounded to the input dtype, [B, HQ, T, D]: the dK / dV kernel
+      // stages it as is (the reference's rounding point of the scaled query)
+      uint4 qw = *reinterpret_cast<const uint4*>(reinterpret_cast<const T*>(a.q) + (int64_t)b * a.q_sb +
+                                                 (int64_t)t * a.q_st + (int64_t)hq * a.q_sh + c * 8);
+      uint32_t* q4 = reinterpret_cast<uint32_t*>(&qw);
+#pragma unroll
+      for (int e = 0; e < 4; ++e) q4[e] = M::pack2(M::lo(q4[e]) * a.scale, M::hi(q4[e]) * a.scale);
+      *reinterpret_cast<uint4*>(reinterpret_cast<T*>(p.qs) + (((int64_t)b * a.HQ + hq) * a.T + t) * D + c * 8) = qw;
+    }
   }
 #pragma unroll
   for (int o = LPR / 2; o >= 1; o >>= 1) s += __shfl_xor(s, o, kWave);
@@ -81,30 +94,52 @@ __global__ __launch_bounds__(256) void zero_words_kernel(uint32_t* w, int64_t n)
   if (i < n) w[i] = 0u;
 }
 
+// One wavefront per (sequence, index head, query tile, slot), lane = row of
+// the tile.  When every live lane's block maps to the same chunk range (rows
+// of a tile sharing a selection), one lane sets the bits for the wave;
+// otherwise each lane sets its own.  Either way the bitmap gets the same bits.
 __global__ __launch_bounds__(256) void touch_kernel(BwdK p) {
   const srswa_bwd_args& a = p.a;
-  const int64_t e = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-  const int64_t n = (int64_t)a.B * a.HI * a.T * a.S;
-  if (e >= n) return;
-  const int s = (int)(e % a.S);
-  int64_t r = e / a.S;
-  const int t = (int)(r % a.T);
-  r /= a.T;
+  const int lane = threadIdx.x % kWave;
+  const int64_t w = (int64_t)blockIdx.x * (blockDim.x / kWave) + threadIdx.x / kWave;
+  const int64_t nw = (int64_t)a.B * a.HI * p.ntiles * a.S;
+  if (w >= nw) return;
+  const int s = (int)(w % a.S);
+  int64_t r = w / a.S;
+  const int tau = (int)(r % p.ntiles);
+  r /= p.ntiles;
   const int ih = (int)(r % a.HI);
   const int b = (int)(r / a.HI);
-  const int id = a.idx[(int64_t)b * a.idx_sb + (int64_t)ih * a.idx_sh + (int64_t)t * a.idx_st + s];
-  const int BS = a.block_size;
-  if (id < 0 || id > (a.Sk - 1) / BS) return;
-  const int qi = a.Sk - a.T + t;
-  const int seg = a.seg ? a.seg[(int64_t)b * a.seg_sb + t] : 0;
-  const int ls = max(qi - a.local_window + 1, seg);
-  const int lo = max(id * BS, seg);
-  const int hi = min(min(id * BS + BS, ls), qi + 1);
-  if (lo >= hi) return;
-  const int tau = t / kTileRows;
-  uint32_t* base = p.touch + ((int64_t)b * a.HI + ih) * p.nchunk * p.twords;
-  for (int c = lo / kChunk; c <= (hi - 1) / kChunk; ++c)
-    atomicOr(base + (int64_t)c * p.twords + (tau >> 5), 1u << (tau & 31));
+  const int t = tau * kTileRows + lane;
+  int c0 = 0, c1 = -1;                       // chunk range of this row's slot (empty: c1 < c0)
+  if (t < a.T) {
+    const int id = a.idx[(int64_t)b * a.idx_sb + (int64_t)ih * a.idx_sh + (int64_t)t * a.idx_st + s];
+    const int BS = a.block_size;
+    if (id >= 0 && id <= (a.Sk - 1) / BS) {
+      const int qi = a.Sk - a.T + t;
+      const int seg = a.seg ? a.seg[(int64_t)b * a.seg_sb + t] : 0;
+      const int ls = max(qi - a.local_window + 1, seg);
+      const int lo = max(id * BS, seg);
+      const int hi = min(min(id * BS + BS, ls), qi + 1);
+      if (lo < hi) {
+        c0 = lo / kChunk;
+        c1 = (hi - 1) / kChunk;
+      }
+    }
+  }
+  const bool live = c1 >= c0;
+  const uint64_t lm = __ballot(live);
+  if (lm == 0ull) return;
+  const int first = __ffsll((long long)lm) - 1;
+  const int f0 = __shfl(c0, first, kWave), f1 = __shfl(c1, first, kWave);
+  const bool same = __all(!live || (c0 == f0 && c1 == f1));
+  uint32_t* base = p.touch + ((int64_t)b * a.HI + ih) * p.nchunk * p.twords + (tau >> 5);
+  if (same) {
+    if (lane == first)
+      for (int c = f0; c <= f1; ++c) atomicOr(base + (int64_t)c * p.twords, 1u << (tau & 31));
+  } else if (live) {
+    for (int c = c0; c <= c1; ++c) atomicOr(base + (int64_t)c * p.twords, 1u << (tau & 31));
+  }
 }
 
 // -------------------------------------------------------------- 3. dQ
@@ -346,30 +381,40 @@ __global__ __launch_bounds__(128, D == 128 ? 1 : 2) void dq_kernel(BwdK p) {
 // -------------------------------------------------------------- 4. dK / dV
 constexpr int kPreSlots = 8;          // selected ids per row fetched one visit ahead
 
+// One workgroup = (sequence, kv head, 64-key chunk), four waves.  For every
+// query head of the group, the query tiles whose windows cover the chunk or
+// whose touch bit is set are visited in ascending order (deterministic: fixed
+// order, no atomics).  The work of each 32-key half is split by role, so a
+// wave holds one operand set and one accumulator set (two waves per SIMD):
+//   role A (waves 0, 1): K of its keys; S = Q K^T, the masks, bias and
+//     softmax -> P (fp32, published through LDS), dV^T += dO^T P;
+//   role B (waves 2, 3): V of its keys; dP = dO V^T, then dS = P (dP - delta)
+//     from the published P, dK^T += (q*scale)^T dS.
+// Per visit: stage Q / dO | S (A) and dP (B) | barrier | dV (A), dS and dK
+// (B) while wave 3 derives the NEXT visit's row data (keep masks, lse, delta,
+// bias) into the other of two buffers, off the S / softmax path.  A lane
+// holds the same (row, key) elements in both roles (the same MFMA shape), so
+// role B reads role A's P lane for lane.
 template <int D> struct DkvLds {
-  static constexpr int QP = D + 16;   // Q / dO tiles: row reads and transposing reads
-  static constexpr int gOff = kTileRows * QP * 2;
-  static constexpr int tileBytes = 2 * gOff;
+  static constexpr int QP = D + 16;                 // Q / dO tiles: row reads and transposing reads
+  static constexpr int gOff = kTileRows * QP * 2;   // dO tile
+  static constexpr int pOff = 2 * gOff;             // P: [key half][8 x float4][64 lanes]
+  static constexpr int rowOff = pOff + 2 * 8 * 64 * 16;
+  // one row-data buffer: lse[64], delta[64], keep[2][64], remote[2][64] (32-bit
+  // masks per key half), bias[4][64] per 16-key quarter, flag[4]
+  static constexpr int rowBytes = (64 + 64 + 128 + 128 + 256) * 4 + 16;
+  static constexpr int fixedBytes = rowOff + 2 * rowBytes;
 };
 
-// One workgroup = (sequence, kv head, 64-key chunk), two waves of 32 keys
-// each holding their keys' K / V as MFMA operands and dK / dV accumulators.
-// For every query head of the group, the query tiles whose windows cover the
-// chunk or whose touch bit is set are visited in ascending order: Q (scaled,
-// rounded) and dO are staged in LDS (the next tile prefetched into registers),
-// one wave derives every row's keep mask over the chunk, each wave transposes
-// the masks of its keys with ballots (skipped when every row keeps every key),
-// then S = Q K^T, dP = dO V^T, dV^T += dO^T P and dK^T += Q^T dS, the
-// transposed operands read with ds_read_b64_tr_b16.  Deterministic: fixed
-// visiting order, no atomics.
 template <typename T, int D>
-__global__ __launch_bounds__(128, 1) void dkv_kernel(BwdK p) {
+__global__ __launch_bounds__(256, 2) void dkv_kernel(BwdK p) {
   using M = Mfma<T>;
   using L = DkvLds<D>;
   constexpr int QP = L::QP;
-  constexpr int KS = D / 16, MT = D / 32, NT = 128;
+  constexpr int KS = D / 16, MT = D / 32, NT = 256;
   constexpr int PPT = kTileRows * D / 8 / NT;
   constexpr int RPP = NT / (D / 8);
+  constexpr int kMaskWave = 3;
   extern __shared__ __align__(16) unsigned char smem[];
   const srswa_bwd_args& a = p.a;
 
@@ -378,43 +423,47 @@ __global__ __launch_bounds__(128, 1) void dkv_kernel(BwdK p) {
 
   T* sQ = reinterpret_cast<T*>(smem);
   T* sG = reinterpret_cast<T*>(smem + L::gOff);
-  float* s_lse = reinterpret_cast<float*>(smem + L::tileBytes);   // [64] lse * log2e (+inf past T)
-  float* s_dlt = s_lse + 64;                                      // [64] delta
-  uint64_t* s_keep = reinterpret_cast<uint64_t*>(s_dlt + 64);     // [64] row -> keys kept
-  uint64_t* s_rem = s_keep + 64;                                  // [64] row -> remote keys kept
-  float* s_bq = reinterpret_cast<float*>(s_rem + 64);             // [4][64] bias (log2) per quarter, row
-  int* s_flag = reinterpret_cast<int*>(s_bq + 4 * 64);            // [4]: every row keeps the whole chunk
-  int* s_tiles = s_flag + 4;                                      // visit list
+  float4* sP = reinterpret_cast<float4*>(smem + L::pOff);
+  int* s_tiles = reinterpret_cast<int*>(smem + L::fixedBytes);    // visit list
+  // row-data buffer `buf`
+  auto s_lse = [&](int buf) { return reinterpret_cast<float*>(smem + L::rowOff + buf * L::rowBytes); };
+  auto s_dlt = [&](int buf) { return s_lse(buf) + 64; };
+  auto s_keep = [&](int buf) { return reinterpret_cast<uint32_t*>(s_lse(buf) + 128); };   // [2][64]
+  auto s_rem = [&](int buf) { return s_keep(buf) + 128; };                                 // [2][64]
+  auto s_bq = [&](int buf) { return reinterpret_cast<float*>(s_keep(buf) + 256); };        // [4][64]
+  auto s_flag = [&](int buf) { return reinterpret_cast<int*>(s_bq(buf) + 256); };
 
   const int tid = threadIdx.x, wave = tid / kWave, lane = tid % kWave;
+  const int kh = wave & 1, role = wave >> 1;     // key half, 0 = S / P / dV, 1 = dP / dS / dK
   const int h = lane >> 5, rl = lane & 31;
   const int c = lid % p.nchunk;
   const int bk = lid / p.nchunk;
   const int kvh = bk % a.HKV, b = bk / a.HKV;
   const int j0 = c * kChunk;
-  const int kk = 32 * wave + rl;               // this lane's key within the chunk
+  const int kk = 32 * kh + rl;                 // this lane's key within the chunk
   const int jmine = j0 + kk;
   const bool key_ok = jmine < a.Sk;
   const int off = a.Sk - a.T;
-  const int BS = a.block_size, LW = a.local_window, S = a.S;
+  const int LW = a.local_window, S = a.S;
   const int maxblk = (a.Sk - 1) >> p.bs_shift;
   const int myq = kk >> 4;                     // this key's 16-key quarter
   const int qb0 = j0 >> p.bs_shift;            // block of the chunk's first quarter
   const bool one_blk = ((j0 + kChunk - 1) >> p.bs_shift) == qb0;   // block size >= 64
 
-  uint4 kf[KS], vf[KS];
+  // role A: K of this lane's key; role B: V
+  uint4 kv[KS];
   {
-    const T* krow = reinterpret_cast<const T*>(a.k) + (int64_t)b * a.k_sb + (int64_t)(key_ok ? jmine : 0) * a.k_st + (int64_t)kvh * a.k_sh;
-    const T* vrow = reinterpret_cast<const T*>(a.v) + (int64_t)b * a.v_sb + (int64_t)(key_ok ? jmine : 0) * a.v_st + (int64_t)kvh * a.v_sh;
+    const T* base = role == 0 ? reinterpret_cast<const T*>(a.k) + (int64_t)b * a.k_sb + (int64_t)kvh * a.k_sh
+                              : reinterpret_cast<const T*>(a.v) + (int64_t)b * a.v_sb + (int64_t)kvh * a.v_sh;
+    const int64_t st = role == 0 ? a.k_st : a.v_st;
+    const T* row = base + (int64_t)(key_ok ? jmine : 0) * st;
 #pragma unroll
-    for (int ks = 0; ks < KS; ++ks) {
-      kf[ks] = key_ok ? *reinterpret_cast<const uint4*>(krow + 16 * ks + 8 * h) : make_uint4(0, 0, 0, 0);
-      vf[ks] = key_ok ? *reinterpret_cast<const uint4*>(vrow + 16 * ks + 8 * h) : make_uint4(0, 0, 0, 0);
-    }
+    for (int ks = 0; ks < KS; ++ks)
+      kv[ks] = key_ok ? *reinterpret_cast<const uint4*>(row + 16 * ks + 8 * h) : make_uint4(0, 0, 0, 0);
   }
-  f32x16_t dk[MT], dv[MT];
+  f32x16_t acc[MT];                            // role A: dV^T, role B: dK^T
 #pragma unroll
-  for (int mt = 0; mt < MT; ++mt) { dk[mt] = zero16(); dv[mt] = zero16(); }
+  for (int mt = 0; mt < MT; ++mt) acc[mt] = zero16();
 
   // query tiles whose windows can reach this chunk: qi in [j0, j0 + 63 + LW - 1]
   const int wlo_t = j0 - off, whi_t = j0 + kChunk - 1 + LW - 1 - off;
@@ -425,6 +474,9 @@ __global__ __launch_bounds__(128, 1) void dkv_kernel(BwdK p) {
   T* sGw = sG + (tid / (D / 8)) * QP + (tid % (D / 8)) * 8;
   const uint16_t* q16 = reinterpret_cast<const uint16_t*>(sQ);
   const uint16_t* g16 = reinterpret_cast<const uint16_t*>(sG);
+  const T* sX = role == 0 ? sQ : sG;           // the row operand of S (A) / dP (B)
+  const uint16_t* x16 = role == 0 ? g16 : q16; // the transposed operand of dV (A) / dK (B)
+  float4* sPl = sP + kh * 8 * 64 + lane;       // this lane's P records
   __shared__ int s_ntiles;
   uint4 qpre[PPT], gpre[PPT];
 
@@ -449,29 +501,29 @@ __global__ __launch_bounds__(128, 1) void dkv_kernel(BwdK p) {
     }
     __syncthreads();
     const int nt = s_ntiles;
+    // the scaled query from the delta pass ([T, D] rows of this head), dO as given
     const __amdgpu_buffer_rsrc_t qrs = make_rsrc(
-        reinterpret_cast<const T*>(a.q) + (int64_t)b * a.q_sb + (int64_t)hq * a.q_sh,
-        (uint32_t)(((int64_t)(a.T - 1) * a.q_st + D) * 2));
+        reinterpret_cast<const T*>(p.qs) + ((int64_t)b * a.HQ + hq) * a.T * D, (uint32_t)((int64_t)a.T * D * 2));
     const __amdgpu_buffer_rsrc_t grs = make_rsrc(
         reinterpret_cast<const T*>(a.dout) + (int64_t)b * a.do_sb + (int64_t)hq * a.do_sh,
         (uint32_t)(((int64_t)(a.T - 1) * a.do_st + D) * 2));
-    const uint32_t qvo = (uint32_t)((tid / (D / 8)) * a.q_st + (tid % (D / 8)) * 8) * 2;
+    const uint32_t qvo = (uint32_t)((tid / (D / 8)) * D + (tid % (D / 8)) * 8) * 2;
     const uint32_t gvo = (uint32_t)((tid / (D / 8)) * a.do_st + (tid % (D / 8)) * 8) * 2;
     auto fetch = [&](int tau) {
-      const uint32_t qso = (uint32_t)tau * kTileRows * (uint32_t)a.q_st * 2u;
+      const uint32_t qso = (uint32_t)tau * kTileRows * (uint32_t)D * 2u;
       const uint32_t gso = (uint32_t)tau * kTileRows * (uint32_t)a.do_st * 2u;
 #pragma unroll
       for (int i = 0; i < PPT; ++i) {
-        qpre[i] = buffer_load16(qrs, qvo, qso + (uint32_t)(i * RPP) * (uint32_t)a.q_st * 2u);
+        qpre[i] = buffer_load16(qrs, qvo, qso + (uint32_t)(i * RPP) * (uint32_t)D * 2u);
         gpre[i] = buffer_load16(grs, gvo, gso + (uint32_t)(i * RPP) * (uint32_t)a.do_st * 2u);
       }
     };
-    // row data of a tile for wave 0 (lane = row): sample start, lse (log2
-    // units, +inf past T), delta and the first kPreSlots selected ids / biases
+    // row data of a tile for the mask wave (lane = row): sample start, lse
+    // (log2 units, +inf past T), delta and the first kPreSlots ids / biases
     int pf_seg = 0, pf_id[kPreSlots];
     float pf_lse = INFINITY, pf_dlt = 0.f, pf_b[kPreSlots];
     auto rfetch = [&](int tau) {
-      const int t = tau * kTileRows + tid;
+      const int t = tau * kTileRows + lane;
       const bool valid = t < a.T;
       const int tt = valid ? t : 0;
       pf_seg = (valid && a.seg) ? a.seg[(int64_t)b * a.seg_sb + tt] : 0;
@@ -485,223 +537,229 @@ __global__ __launch_bounds__(128, 1) void dkv_kernel(BwdK p) {
         pf_b[s] = (valid && s < S && bias) ? bias[s] : 0.f;
       }
     };
+    // the mask wave: row data of visit `v` (fetched by rfetch) into buffer v & 1,
+    // then the fetch of visit v + 1
+    auto row_masks = [&](int v) {
+      const int buf = v & 1;
+      const int t0 = s_tiles[v] * kTileRows;
+      const int nrows = min(kTileRows, a.T - t0);
+      const int r = lane;
+      uint64_t keep = 0ull, rm = 0ull;
+      float bqv[4] = {0.f, 0.f, 0.f, 0.f};
+      if (r < nrows) {
+        const int t = t0 + r;
+        const int qi = off + t;
+        const int seg = pf_seg;
+        const int ls = max(qi - LW + 1, seg);
+        uint32_t qmem = 0;
+        auto take = [&](int id, float bv) {
+          if (id < 0 || id > maxblk) return;
+#pragma unroll
+          for (int qq = 0; qq < 4; ++qq)
+            if (id == ((j0 + 16 * qq) >> p.bs_shift) && !(qmem & (1u << qq))) {   // first slot wins
+              qmem |= 1u << qq;
+              bqv[qq] = bv * kLog2e;
+            }
+        };
+        if (one_blk) {
+          // the chunk lies in one block: one compare per slot, first slot's bias
+          bool found = false;
+          float bv = 0.f;
+#pragma unroll
+          for (int s = 0; s < kPreSlots; ++s) {
+            const bool hit = pf_id[s] == qb0;
+            bv = (hit && !found) ? pf_b[s] : bv;
+            found = found || hit;
+          }
+          if (S > kPreSlots) {
+            const int32_t* ids = a.idx + (int64_t)b * a.idx_sb + (int64_t)ih * a.idx_sh + (int64_t)t * a.idx_st;
+            const float* bias = a.bias ? a.bias + (int64_t)b * a.bias_sb + (int64_t)ih * a.bias_sh + (int64_t)t * a.bias_st : nullptr;
+            for (int s = kPreSlots; s < S && !found; ++s)
+              if (ids[s] == qb0) {
+                found = true;
+                bv = bias ? bias[s] : 0.f;
+              }
+          }
+          if (found) {
+            qmem = 0xfu;
+#pragma unroll
+            for (int qq = 0; qq < 4; ++qq) bqv[qq] = bv * kLog2e;
+          }
+        } else {
+#pragma unroll
+          for (int s = 0; s < kPreSlots; ++s) take(pf_id[s], pf_b[s]);
+          if (S > kPreSlots) {
+            const int32_t* ids = a.idx + (int64_t)b * a.idx_sb + (int64_t)ih * a.idx_sh + (int64_t)t * a.idx_st;
+            const float* bias = a.bias ? a.bias + (int64_t)b * a.bias_sb + (int64_t)ih * a.bias_sh + (int64_t)t * a.bias_st : nullptr;
+            for (int s = kPreSlots; s < S; ++s) take(ids[s], bias ? bias[s] : 0.f);
+          }
+        }
+        uint64_t qm = 0;
+#pragma unroll
+        for (int qq = 0; qq < 4; ++qq)
+          if (qmem & (1u << qq)) qm |= 0xffffull << (16 * qq);
+        const uint64_t wm = range64(min(max(ls - j0, 0), 64), min(max(qi + 1 - j0, 0), 64));
+        rm = range64(min(max(seg - j0, 0), 64), min(max(min(ls, qi + 1) - j0, 0), 64)) & qm;
+        keep = wm | rm;
+      }
+      s_keep(buf)[r] = (uint32_t)keep;
+      s_keep(buf)[64 + r] = (uint32_t)(keep >> 32);
+      s_rem(buf)[r] = (uint32_t)rm;
+      s_rem(buf)[64 + r] = (uint32_t)(rm >> 32);
+      s_lse(buf)[r] = pf_lse;
+      s_dlt(buf)[r] = pf_dlt;
+#pragma unroll
+      for (int qq = 0; qq < 4; ++qq) s_bq(buf)[qq * 64 + r] = bqv[qq];
+      const bool whole = r >= nrows || (keep == ~0ull && (!a.bias || rm == 0ull));
+      const bool all = __all(whole);
+      if (r == 0) s_flag(buf)[0] = all ? 1 : 0;
+      if (v + 1 < nt) rfetch(s_tiles[v + 1]);
+    };
     if (nt > 0) {
       fetch(s_tiles[0]);
-      if (tid < 64) rfetch(s_tiles[0]);
+      if (wave == kMaskWave) {
+        rfetch(s_tiles[0]);
+        row_masks(0);
+      }
     }
     for (int it = 0; it < nt; ++it) {
-      const int tau = s_tiles[it];
-      const int t0 = tau * kTileRows;
-      const int nrows = min(kTileRows, a.T - t0);
-      __syncthreads();   // previous tile consumed
+      const int buf = it & 1;
+      __syncthreads();   // previous tile consumed (Q, dO, P); this visit's row data written
 #pragma unroll
       for (int i = 0; i < PPT; ++i) {
-        uint4 x = qpre[i];
-        uint32_t* xx = reinterpret_cast<uint32_t*>(&x);
-#pragma unroll
-        for (int e = 0; e < 4; ++e) xx[e] = M::pack2(M::lo(xx[e]) * a.scale, M::hi(xx[e]) * a.scale);
-        *reinterpret_cast<uint4*>(sQw + i * RPP * QP) = x;
+        *reinterpret_cast<uint4*>(sQw + i * RPP * QP) = qpre[i];
         *reinterpret_cast<uint4*>(sGw + i * RPP * QP) = gpre[i];
       }
       if (it + 1 < nt) fetch(s_tiles[it + 1]);
-      // wave 0: every row's keep mask over the chunk's keys, from the row data
-      // fetched one visit ahead (slots past the first kPreSlots load here)
-      if (tid < 64) {
-        const int r = tid;
-        uint64_t keep = 0ull, rm = 0ull;
-        float bqv[4] = {0.f, 0.f, 0.f, 0.f};
-        if (r < nrows) {
-          const int t = t0 + r;
-          const int qi = off + t;
-          const int seg = pf_seg;
-          const int ls = max(qi - LW + 1, seg);
-          uint32_t qmem = 0;
-          auto take = [&](int s, int id, float bv) {
-            if (id < 0 || id > maxblk) return;
-#pragma unroll
-            for (int qq = 0; qq < 4; ++qq)
-              if (id == ((j0 + 16 * qq) >> p.bs_shift) && !(qmem & (1u << qq))) {   // first slot wins
-                qmem |= 1u << qq;
-                bqv[qq] = bv * kLog2e;
-              }
-          };
-          if (one_blk) {
-            // the chunk lies in one block: one compare per slot, first slot's bias
-            bool found = false;
-            float bv = 0.f;
-#pragma unroll
-            for (int s = 0; s < kPreSlots; ++s) {
-              const bool hit = pf_id[s] == qb0;
-              bv = (hit && !found) ? pf_b[s] : bv;
-              found = found || hit;
-            }
-            if (S > kPreSlots) {
-              const int32_t* ids = a.idx + (int64_t)b * a.idx_sb + (int64_t)ih * a.idx_sh + (int64_t)t * a.idx_st;
-              const float* bias = a.bias ? a.bias + (int64_t)b * a.bias_sb + (int64_t)ih * a.bias_sh + (int64_t)t * a.bias_st : nullptr;
-              for (int s = kPreSlots; s < S && !found; ++s)
-                if (ids[s] == qb0) {
-                  found = true;
-                  bv = bias ? bias[s] : 0.f;
-                }
-            }
-            if (found) {
-              qmem = 0xfu;
-#pragma unroll
-              for (int qq = 0; qq < 4; ++qq) bqv[qq] = bv * kLog2e;
-            }
-          } else {
-#pragma unroll
-            for (int s = 0; s < kPreSlots; ++s) take(s, pf_id[s], pf_b[s]);
-            if (S > kPreSlots) {
-              const int32_t* ids = a.idx + (int64_t)b * a.idx_sb + (int64_t)ih * a.idx_sh + (int64_t)t * a.idx_st;
-              const float* bias = a.bias ? a.bias + (int64_t)b * a.bias_sb + (int64_t)ih * a.bias_sh + (int64_t)t * a.bias_st : nullptr;
-              for (int s = kPreSlots; s < S; ++s) take(s, ids[s], bias ? bias[s] : 0.f);
-            }
-          }
-          uint64_t qm = 0;
-#pragma unroll
-          for (int qq = 0; qq < 4; ++qq)
-            if (qmem & (1u << qq)) qm |= 0xffffull << (16 * qq);
-          const uint64_t wm = range64(min(max(ls - j0, 0), 64), min(max(qi + 1 - j0, 0), 64));
-          rm = range64(min(max(seg - j0, 0), 64), min(max(min(ls, qi + 1) - j0, 0), 64)) & qm;
-          keep = wm | rm;
-        }
-        s_keep[r] = keep;
-        s_rem[r] = rm;
-        s_lse[r] = pf_lse;
-        s_dlt[r] = pf_dlt;
-#pragma unroll
-        for (int qq = 0; qq < 4; ++qq) s_bq[qq * 64 + r] = bqv[qq];
-        const bool whole = r >= nrows || (keep == ~0ull && (!a.bias || rm == 0ull));
-        const bool all = __all(whole);
-        if (r == 0) s_flag[0] = all ? 1 : 0;
-        if (it + 1 < nt) rfetch(s_tiles[it + 1]);
-      }
       __syncthreads();
-      const bool fast = s_flag[0] != 0;
-      // keep / remote bits of this lane's key for the 32 rows it holds in the
-      // MFMA layout (bit 16 half + 4 r4 + e <-> row 32 half + 8 r4 + 4 h + e),
-      // read from the rows' 64-bit masks: four rows per pair of 16-byte LDS
-      // reads, the same address for every lane of a half-wave
-      uint32_t km32 = ~0u, rm32 = 0u;
-      if (!fast) {
-        km32 = 0u;
-#pragma unroll
-        for (int half = 0; half < 2; ++half)
-#pragma unroll
-          for (int r4 = 0; r4 < 4; ++r4) {
-            const int row0 = 32 * half + 8 * r4 + 4 * h;
-            const int b0 = 16 * half + 4 * r4;
-            const uint4 k01 = *reinterpret_cast<const uint4*>(s_keep + row0);
-            const uint4 k23 = *reinterpret_cast<const uint4*>(s_keep + row0 + 2);
-            const uint32_t kw[8] = {k01.x, k01.y, k01.z, k01.w, k23.x, k23.y, k23.z, k23.w};
-#pragma unroll
-            for (int e = 0; e < 4; ++e)
-              km32 |= ((kk < 32 ? kw[2 * e] >> kk : kw[2 * e + 1] >> (kk - 32)) & 1u) << (b0 + e);
-            if (a.bias) {
-              const uint4 r01 = *reinterpret_cast<const uint4*>(s_rem + row0);
-              const uint4 r23 = *reinterpret_cast<const uint4*>(s_rem + row0 + 2);
-              const uint32_t rw[8] = {r01.x, r01.y, r01.z, r01.w, r23.x, r23.y, r23.z, r23.w};
-#pragma unroll
-              for (int e = 0; e < 4; ++e)
-                rm32 |= ((kk < 32 ? rw[2 * e] >> kk : rw[2 * e + 1] >> (kk - 32)) & 1u) << (b0 + e);
-            }
-          }
-      }
 
-      // S = Q K^T and dP = dO V^T: 64 rows x this lane's key
-      f32x16_t sp[2] = {zero16(), zero16()}, gd[2] = {zero16(), zero16()};
+      // S = Q K^T (A) or dP = dO V^T (B): 64 rows x this lane's key; register r
+      // of half `half` is row 32 half + 8 (r / 4) + 4h + r % 4
+      f32x16_t sg[2] = {zero16(), zero16()};
 #pragma unroll
       for (int ks = 0; ks < KS; ++ks) {
 #pragma unroll
-        for (int half = 0; half < 2; ++half) {
-          sp[half] = M::mac(*reinterpret_cast<const uint4*>(sQ + (32 * half + rl) * QP + 16 * ks + 8 * h), kf[ks], sp[half]);
-          gd[half] = M::mac(*reinterpret_cast<const uint4*>(sG + (32 * half + rl) * QP + 16 * ks + 8 * h), vf[ks], gd[half]);
-        }
+        for (int half = 0; half < 2; ++half)
+          sg[half] = M::mac(*reinterpret_cast<const uint4*>(sX + (32 * half + rl) * QP + 16 * ks + 8 * h), kv[ks], sg[half]);
       }
-      // in place: sp <- P, gd <- dS; register r of half `half` is row 32 half + 8 (r / 4) + 4h + r % 4.
-      // Two straight-line copies (every row keeps the chunk whole / masked):
-      // a uniform test per element would split the unrolled loop into one
-      // basic block per exp.
-      auto softmax = [&](auto fast_tag) {
-        constexpr bool FAST = decltype(fast_tag)::value;
+      if (role == 0) {
+        const bool fast = s_flag(buf)[0] != 0;
+        const float* lse = s_lse(buf);
+        // keep / remote bits of this lane's key for the 32 rows it holds in the
+        // MFMA layout (bit 16 half + 4 r4 + e <-> row 32 half + 8 r4 + 4 h + e),
+        // from the rows' 32-bit masks of this key half, four rows per read
+        uint32_t km32 = ~0u, rm32 = 0u;
+        if (!fast) {
+          km32 = 0u;
+          const uint32_t* kw = s_keep(buf) + 64 * kh;
+          const uint32_t* rw = s_rem(buf) + 64 * kh;
+#pragma unroll
+          for (int half = 0; half < 2; ++half)
+#pragma unroll
+            for (int r4 = 0; r4 < 4; ++r4) {
+              const int row0 = 32 * half + 8 * r4 + 4 * h;
+              const int b0 = 16 * half + 4 * r4;
+              const uint4 k4 = *reinterpret_cast<const uint4*>(kw + row0);
+              km32 |= (((k4.x >> rl) & 1u) | (((k4.y >> rl) & 1u) << 1) | (((k4.z >> rl) & 1u) << 2) |
+                       (((k4.w >> rl) & 1u) << 3)) << b0;
+              if (a.bias) {
+                const uint4 r4v = *reinterpret_cast<const uint4*>(rw + row0);
+                rm32 |= (((r4v.x >> rl) & 1u) | (((r4v.y >> rl) & 1u) << 1) | (((r4v.z >> rl) & 1u) << 2) |
+                         (((r4v.w >> rl) & 1u) << 3)) << b0;
+              }
+            }
+        }
+        // sg <- P in place; two straight-line copies (every row keeps the
+        // chunk whole / masked): a uniform test per element would split the
+        // unrolled loop into one basic block per exp
+        auto softmax = [&](auto fast_tag) {
+          constexpr bool FAST = decltype(fast_tag)::value;
+#pragma unroll
+          for (int half = 0; half < 2; ++half)
+#pragma unroll
+            for (int r4 = 0; r4 < 4; ++r4) {
+              const int row0 = 32 * half + 8 * r4 + 4 * h;
+              const float4 l4 = *reinterpret_cast<const float4*>(lse + row0);
+              float4 b4 = make_float4(0.f, 0.f, 0.f, 0.f);
+              if constexpr (!FAST)
+                if (a.bias) b4 = *reinterpret_cast<const float4*>(s_bq(buf) + myq * 64 + row0);
+              const float lv[4] = {l4.x, l4.y, l4.z, l4.w};
+              const float bv[4] = {b4.x, b4.y, b4.z, b4.w};
+              float pv[4];
+#pragma unroll
+              for (int e = 0; e < 4; ++e) {
+                const int r = 4 * r4 + e;
+                float x;
+                if constexpr (FAST) {
+                  x = fmaf(sg[half][r], kLog2e, -lv[e]);
+                } else {
+                  const int bit = 16 * half + 4 * r4 + e;
+                  const bool remb = (rm32 >> bit) & 1u;
+                  x = fmaf(sg[half][r], kLog2e, (remb ? bv[e] : 0.f) - lv[e]);
+                  x = ((km32 >> bit) & 1u) ? x : -INFINITY;      // exp2(-inf) = 0
+                }
+                pv[e] = key_ok ? __builtin_amdgcn_exp2f(x) : 0.f;
+                sg[half][r] = pv[e];
+              }
+              sPl[(4 * half + r4) * 64] = make_float4(pv[0], pv[1], pv[2], pv[3]);
+            }
+        };
+        if (fast)
+          softmax(std::true_type{});
+        else
+          softmax(std::false_type{});
+      }
+      __syncthreads();   // P published
+      if (role == 1) {
+        // sg <- dS = P (dP - delta) in place
+        const float* dlt = s_dlt(buf);
 #pragma unroll
         for (int half = 0; half < 2; ++half)
 #pragma unroll
           for (int r4 = 0; r4 < 4; ++r4) {
             const int row0 = 32 * half + 8 * r4 + 4 * h;
-            const float4 l4 = *reinterpret_cast<const float4*>(s_lse + row0);
-            const float4 d4 = *reinterpret_cast<const float4*>(s_dlt + row0);
-            float4 b4 = make_float4(0.f, 0.f, 0.f, 0.f);
-            if constexpr (!FAST)
-              if (a.bias) b4 = *reinterpret_cast<const float4*>(s_bq + myq * 64 + row0);
-            const float lv[4] = {l4.x, l4.y, l4.z, l4.w}, dv4[4] = {d4.x, d4.y, d4.z, d4.w};
-            const float bv[4] = {b4.x, b4.y, b4.z, b4.w};
+            const float4 d4 = *reinterpret_cast<const float4*>(dlt + row0);
+            const float4 p4 = sPl[(4 * half + r4) * 64];
+            const float dv4[4] = {d4.x, d4.y, d4.z, d4.w}, pv[4] = {p4.x, p4.y, p4.z, p4.w};
 #pragma unroll
-            for (int e = 0; e < 4; ++e) {
-              const int r = 4 * r4 + e;
-              float x;
-              if constexpr (FAST) {
-                x = fmaf(sp[half][r], kLog2e, -lv[e]);
-              } else {
-                const int bit = 16 * half + 4 * r4 + e;
-                const bool remb = (rm32 >> bit) & 1u;
-                x = fmaf(sp[half][r], kLog2e, (remb ? bv[e] : 0.f) - lv[e]);
-                x = ((km32 >> bit) & 1u) ? x : -INFINITY;      // exp2(-inf) = 0
-              }
-              const float pv = key_ok ? __builtin_amdgcn_exp2f(x) : 0.f;
-              sp[half][r] = pv;
-              gd[half][r] = pv * (gd[half][r] - dv4[e]);
-            }
+            for (int e = 0; e < 4; ++e) sg[half][4 * r4 + e] = pv[e] * (sg[half][4 * r4 + e] - dv4[e]);
           }
-      };
-      if (fast)
-        softmax(std::true_type{});
-      else
-        softmax(std::false_type{});
-      uint4 pb[4], db[4];
+      }
+      uint4 pk[4];
 #pragma unroll
       for (int ks = 0; ks < 4; ++ks) {
         const int hf = ks >> 1, r0 = 8 * (ks & 1);
-        pb[ks] = make_uint4(M::pack2(sp[hf][r0], sp[hf][r0 + 1]), M::pack2(sp[hf][r0 + 2], sp[hf][r0 + 3]),
-                            M::pack2(sp[hf][r0 + 4], sp[hf][r0 + 5]), M::pack2(sp[hf][r0 + 6], sp[hf][r0 + 7]));
-        db[ks] = make_uint4(M::pack2(gd[hf][r0], gd[hf][r0 + 1]), M::pack2(gd[hf][r0 + 2], gd[hf][r0 + 3]),
-                            M::pack2(gd[hf][r0 + 4], gd[hf][r0 + 5]), M::pack2(gd[hf][r0 + 6], gd[hf][r0 + 7]));
+        pk[ks] = make_uint4(M::pack2(sg[hf][r0], sg[hf][r0 + 1]), M::pack2(sg[hf][r0 + 2], sg[hf][r0 + 3]),
+                            M::pack2(sg[hf][r0 + 4], sg[hf][r0 + 5]), M::pack2(sg[hf][r0 + 6], sg[hf][r0 + 7]));
       }
-      // dV^T += dO^T P ; dK^T += (q*scale)^T dS (k-step outer: 2 MT interleaved
-      // accumulator chains, a step's operands read before its MFMAs)
+      // A: dV^T += dO^T P; B: dK^T += (q*scale)^T dS (k-step outer, a step's
+      // operands read before its MFMAs)
 #pragma unroll
       for (int ks = 0; ks < 4; ++ks) {
-        uint4 ga[MT], qa[MT];
+        uint4 xa[MT];
 #pragma unroll
-        for (int mt = 0; mt < MT; ++mt) {
-          ga[mt] = a_operand_tr<QP>(g16, 16 * ks, 32 * mt, lane);
-          qa[mt] = a_operand_tr<QP>(q16, 16 * ks, 32 * mt, lane);
-        }
+        for (int mt = 0; mt < MT; ++mt) xa[mt] = a_operand_tr<QP>(x16, 16 * ks, 32 * mt, lane);
 #pragma unroll
-        for (int mt = 0; mt < MT; ++mt) {
-          dv[mt] = M::mac(ga[mt], pb[ks], dv[mt]);
-          dk[mt] = M::mac(qa[mt], db[ks], dk[mt]);
-        }
+        for (int mt = 0; mt < MT; ++mt) acc[mt] = M::mac(xa[mt], pk[ks], acc[mt]);
       }
+      // the next visit's row data, while the matrix cores finish dK
+      if (wave == kMaskWave && it + 1 < nt) row_masks(it + 1);
     }
   }
 
   if (!key_ok) return;
-  T* kout = reinterpret_cast<T*>(a.dk) + (int64_t)b * a.dk_sb + (int64_t)jmine * a.dk_st + (int64_t)kvh * a.dk_sh;
-  T* vout = reinterpret_cast<T*>(a.dv) + (int64_t)b * a.dv_sb + (int64_t)jmine * a.dv_st + (int64_t)kvh * a.dv_sh;
+  T* out = role == 0
+               ? reinterpret_cast<T*>(a.dv) + (int64_t)b * a.dv_sb + (int64_t)jmine * a.dv_st + (int64_t)kvh * a.dv_sh
+               : reinterpret_cast<T*>(a.dk) + (int64_t)b * a.dk_sb + (int64_t)jmine * a.dk_st + (int64_t)kvh * a.dk_sh;
 #pragma unroll
   for (int mt = 0; mt < MT; ++mt)
 #pragma unroll
     for (int g = 0; g < 4; ++g) {
       const int d0 = 32 * mt + 8 * g + 4 * h;
-      uint2 wk, wv;
-      wk.x = M::pack2(dk[mt][4 * g], dk[mt][4 * g + 1]);
-      wk.y = M::pack2(dk[mt][4 * g + 2], dk[mt][4 * g + 3]);
-      wv.x = M::pack2(dv[mt][4 * g], dv[mt][4 * g + 1]);
-      wv.y = M::pack2(dv[mt][4 * g + 2], dv[mt][4 * g + 3]);
-      *reinterpret_cast<uint2*>(kout + d0) = wk;
-      *reinterpret_cast<uint2*>(vout + d0) = wv;
+      uint2 w;
+      w.x = M::pack2(acc[mt][4 * g], acc[mt][4 * g + 1]);
+      w.y = M::pack2(acc[mt][4 * g + 2], acc[mt][4 * g + 3]);
+      *reinterpret_cast<uint2*>(out + d0) = w;
     }
 }
 
@@ -793,15 +851,16 @@ size_t delta_bytes(const BwdK& k) {
   return ((size_t)k.a.B * k.a.T * k.a.HQ * 4 + 255) / 256 * 256;
 }
 size_t touch_words(const BwdK& k) { return (size_t)k.a.B * k.a.HI * k.nchunk * k.twords; }
+size_t qs_bytes(const BwdK& k) { return ((size_t)k.a.B * k.a.HQ * k.a.T * k.a.D * 2 + 255) / 256 * 256; }
 
 size_t dq_smem(const BwdK& k) {
   const size_t n = (size_t)k.sid_off + (size_t)64 * k.SP * 4 * (1 + (k.a.bias ? 1 : 0) + (k.a.dbias ? 2 : 0));
   return (n + 15) / 16 * 16;
 }
+
 size_t dkv_smem(const BwdK& k) {
-  const size_t tile = k.a.D == 128 ? DkvLds<128>::tileBytes : DkvLds<64>::tileBytes;
-  const size_t n = tile + 64 * 4 * 2 + 64 * 8 * 2 + 4 * 64 * 4 + 16 + (size_t)k.ntiles * 4;
-  return (n + 15) / 16 * 16;
+  const size_t fixed = k.a.D == 128 ? DkvLds<128>::fixedBytes : DkvLds<64>::fixedBytes;  // + visit list
+  return (fixed + (size_t)k.ntiles * 4 + 15) / 16 * 16;
 }
 
 template <typename T, int D>
@@ -816,10 +875,10 @@ int launch_bwd(const BwdK& k, hipStream_t st) {
   hipLaunchKernelGGL((delta_kernel<T, D>), dim3((unsigned)((rows + 4 * rpw - 1) / (4 * rpw))), dim3(256), 0, st, k);
   const int64_t nw = (int64_t)touch_words(k);
   if (nw > 0) hipLaunchKernelGGL(zero_words_kernel, dim3((unsigned)((nw + 255) / 256)), dim3(256), 0, st, k.touch, nw);
-  const int64_t ne = (int64_t)a.B * a.HI * a.T * a.S;
-  if (ne > 0) hipLaunchKernelGGL(touch_kernel, dim3((unsigned)((ne + 255) / 256)), dim3(256), 0, st, k);
+  const int64_t ne = (int64_t)a.B * a.HI * k.ntiles * a.S;     // one wavefront each
+  if (ne > 0) hipLaunchKernelGGL(touch_kernel, dim3((unsigned)((ne + 3) / 4)), dim3(256), 0, st, k);
   hipLaunchKernelGGL((dq_kernel<T, D>), dim3((unsigned)(8 * k.per_xcd)), dim3(128), dq_smem(k), st, k);
-  hipLaunchKernelGGL((dkv_kernel<T, D>), dim3((unsigned)(8 * k.per_xcd_kv)), dim3(128), dkv_smem(k), st, k);
+  hipLaunchKernelGGL((dkv_kernel<T, D>), dim3((unsigned)(8 * k.per_xcd_kv)), dim3(256), dkv_smem(k), st, k);
   const hipError_t e = hipGetLastError();
   if (e != hipSuccess) {
     set_error("bwd launch failed: %s", hipGetErrorString(e));
@@ -837,7 +896,7 @@ extern "C" size_t srswa_gather_bwd_workspace(const srswa_bwd_args* a) {
   if (!a || a->B <= 0 || a->T <= 0 || a->HQ <= 0 || a->HI <= 0 || a->Sk <= 0) return 0;
   BwdK k{};
   plan_bwd(a, k);
-  return delta_bytes(k) + touch_words(k) * 4;
+  return delta_bytes(k) + qs_bytes(k) + touch_words(k) * 4;
 }
 
 extern "C" int srswa_gather_bwd(const srswa_bwd_args* a, void* scratch, size_t scratch_bytes,
@@ -847,7 +906,7 @@ extern "C" int srswa_gather_bwd(const srswa_bwd_args* a, void* scratch, size_t s
   if (a->B == 0 || a->T == 0) return SRSWA_OK;
   BwdK k{};
   plan_bwd(a, k);
-  const size_t need = delta_bytes(k) + touch_words(k) * 4;
+  const size_t need = delta_bytes(k) + qs_bytes(k) + touch_words(k) * 4;
   if (!scratch || scratch_bytes < need) {
     set_error("bwd: scratch of %zu bytes required (got %zu)", need, scratch_bytes);
     return SRSWA_WORKSPACE;
@@ -857,7 +916,8 @@ extern "C" int srswa_gather_bwd(const srswa_bwd_args* a, void* scratch, size_t s
     return SRSWA_UNSUPPORTED;
   }
   k.delta = reinterpret_cast<float*>(scratch);
-  k.touch = reinterpret_cast<uint32_t*>(reinterpret_cast<char*>(scratch) + delta_bytes(k));
+  k.qs = reinterpret_cast<char*>(scratch) + delta_bytes(k);
+  k.touch = reinterpret_cast<uint32_t*>(reinterpret_cast<char*>(scratch) + delta_bytes(k) + qs_bytes(k));
   hipStream_t s = reinterpret_cast<hipStream_t>(stream);
   if (a->dtype == SRSWA_BF16)
     return a->D == 128 ? launch_bwd<bf16_t, 128>(k, s) : launch_bwd<bf16_t, 64>(k, s);
