@@ -24,6 +24,8 @@
 // products on the matrix cores with ds = bf16(g dsel), see below.
 #include <algorithm>
 
+#include <type_traits>
+
 #include "mfma_common.h"
 
 namespace srswa {
@@ -114,17 +116,37 @@ __global__ __launch_bounds__(128, 1) void kl_fwd_kernel(KlK p) {
   int lo = 0, hi = 0;
   if (row_ok) row_range(row, lo, hi);
   const int* my_ids = s_ids + row * K;
+  // the row's first kKlIdRegs filtered ids in registers (the slot search of
+  // every stage then has no LDS round trip); slots past them are read from LDS
+  constexpr int kKlIdRegs = 8;
+  int id_reg[kKlIdRegs];
+#pragma unroll
+  for (int s = 0; s < kKlIdRegs; ++s) id_reg[s] = s < K ? my_ids[s] : -1;
+  auto find_slot_of = [&](int c) __attribute__((always_inline)) {
+    int found = -1;
+#pragma unroll
+    for (int s = kKlIdRegs - 1; s >= 0; --s) found = id_reg[s] == c ? s : found;   // first slot wins
+    for (int s = kKlIdRegs; s < K && found < 0; ++s)
+      if (my_ids[s] == c) found = s;
+    return found;
+  };
 
   // stages: pass 1 (hh, u) head-outer, pass 2 (u, hh) block-outer; hh == G is the student
   const int per_pass = (G + 1) * U;
   const int nstage = 2 * per_pass;
-  auto stage_of = [&](int i, int& hh, int& u) {
-    if (i < per_pass) {
-      hh = i / U;
-      u = i % U;
-    } else {
-      u = (i - per_pass) / (G + 1);
-      hh = (i - per_pass) % (G + 1);
+  // (hh, u) of stage i -> of stage i + 1 (counters instead of divisions by U)
+  auto next_of = [&](int i, int& hh, int& u) {
+    if (i + 1 < per_pass) {
+      if (++u == U) {
+        u = 0;
+        ++hh;
+      }
+    } else if (i + 1 == per_pass) {
+      hh = 0;
+      u = 0;
+    } else if (++hh == G + 1) {
+      hh = 0;
+      ++u;
     }
   };
   auto key_base = [&](int hh, int64_t& st) -> const T* {
@@ -146,9 +168,7 @@ __global__ __launch_bounds__(128, 1) void kl_fwd_kernel(KlK p) {
 
   T* sKw = sK + (tid / (D / 8)) * KP + (tid % (D / 8)) * 8;
   uint4 kpre[PPT], qpre[KS], qf[KS];
-  auto fetch = [&](int i) {
-    int hh, u;
-    stage_of(i, hh, u);
+  auto fetch = [&](int hh, int u) {
     int64_t st;
     const T* base = key_base(hh, st);
     const __amdgpu_buffer_rsrc_t rs = make_rsrc(base, (uint32_t)(((int64_t)(a.Sk - 1) * st + D) * 2));
@@ -169,11 +189,14 @@ __global__ __launch_bounds__(128, 1) void kl_fwd_kernel(KlK p) {
   float kl_acc = 0.f;
   int slot = -1;
   uint64_t keep = 0ull;
+  bool full = false;
 
-  if (nstage > 0) fetch(0);
+  int hh_c = 0, u_c = 0;                 // stage i
+  int hh_f = 0, u_f = 0;                 // stage i + 1, the next fetch
+  if (nstage > 0) fetch(0, 0);
+  next_of(0, hh_f, u_f);
   for (int i = 0; i < nstage; ++i) {
-    int hh, u;
-    stage_of(i, hh, u);
+    const int hh = hh_c, u = u_c;
     const bool pass2 = i >= per_pass;
     __syncthreads();                       // previous stage's keys consumed
 #pragma unroll
@@ -181,18 +204,14 @@ __global__ __launch_bounds__(128, 1) void kl_fwd_kernel(KlK p) {
 #pragma unroll
     for (int ks = 0; ks < KS; ++ks) qf[ks] = qpre[ks];
     __syncthreads();
-    if (i + 1 < nstage) fetch(i + 1);
+    if (i + 1 < nstage) fetch(hh_f, u_f);
 
     const int c = s_chunks[u];
     const int j0 = c * kChunk;
     if (!pass2 || hh == 0) {              // the row's slot of this block and its kept keys
-      slot = -1;
-      for (int s = 0; s < K; ++s)
-        if (my_ids[s] == c) {
-          slot = s;
-          break;
-        }
+      slot = find_slot_of(c);
       keep = (row_ok && slot >= 0) ? range64(min(max(lo - j0, 0), 64), min(max(hi - j0, 0), 64)) : 0ull;
+      full = __all(keep == ~0ull);        // every row of the wave keeps the whole block
     }
     f32x16_t st[2] = {zero16(), zero16()};
 #pragma unroll
@@ -205,83 +224,96 @@ __global__ __launch_bounds__(128, 1) void kl_fwd_kernel(KlK p) {
     // 32 half + 8 (r / 4) + 4h + r % 4
     const float mul = hh == G ? 1.f : a.scaling;
     const uint64_t kh = keep >> (4 * h);
-    if (!pass2) {
-      float mloc = -INFINITY;
-#pragma unroll
-      for (int half = 0; half < 2; ++half)
-#pragma unroll
-        for (int r = 0; r < 16; ++r) {
-          const float x = round_to<T>(st[half][r]) * mul;
-          st[half][r] = x;
-          if ((kh >> (32 * half + 8 * (r >> 2) + (r & 3))) & 1ull) mloc = fmaxf(mloc, x);
-        }
-      if (mloc > -INFINITY) {
-        const float mn = fmaxf(m_run, mloc);
-        float l = m_run > -INFINITY ? l_run * __builtin_amdgcn_exp2f((m_run - mn) * kLog2e) : 0.f;
-#pragma unroll
-        for (int half = 0; half < 2; ++half)
-#pragma unroll
-          for (int r = 0; r < 16; ++r)
-            if ((kh >> (32 * half + 8 * (r >> 2) + (r & 3))) & 1ull)
-              l += __builtin_amdgcn_exp2f((st[half][r] - mn) * kLog2e);
-        m_run = mn;
-        l_run = l;
-      }
-      if (u == U - 1) {                    // the head's statistics for the row: merge the lane pair
-        const float mo = __shfl_xor(m_run, 32, kWave), lo2 = __shfl_xor(l_run, 32, kWave);
-        const float mm = fmaxf(m_run, mo);
-        float ll = 0.f;
-        if (mm > -INFINITY) {
-          if (m_run > -INFINITY) ll += l_run * __builtin_amdgcn_exp2f((m_run - mm) * kLog2e);
-          if (mo > -INFINITY) ll += lo2 * __builtin_amdgcn_exp2f((mo - mm) * kLog2e);
-        }
-        if (h == 0) s_st[hh * 64 + row] = make_float2(mm, ll);
-        m_run = -INFINITY;
-        l_run = 0.f;
-      }
-      continue;
-    }
-    // pass 2
-    const float2 ml = s_st[hh * 64 + row];
-    if (hh < G) {
-      if (ml.y > 0.f) {
-        const float inv = 1.f / ml.y;
+    // two straight-line copies: every row of the wave keeps the whole block
+    // (no per-key tests) / masked
+    auto compute = [&](auto full_tag) __attribute__((always_inline)) {
+      constexpr bool FULL = decltype(full_tag)::value;
+      auto kept = [&](int bit) __attribute__((always_inline)) { return FULL || ((kh >> bit) & 1ull) != 0; };
+      if (!pass2) {
+        float mloc = -INFINITY;
 #pragma unroll
         for (int half = 0; half < 2; ++half)
 #pragma unroll
           for (int r = 0; r < 16; ++r) {
-            const bool kp = (kh >> (32 * half + 8 * (r >> 2) + (r & 3))) & 1ull;
             const float x = round_to<T>(st[half][r]) * mul;
-            pacc[16 * half + r] += kp ? __builtin_amdgcn_exp2f((x - ml.x) * kLog2e) * inv : 0.f;
+            st[half][r] = x;
+            if (kept(32 * half + 8 * (r >> 2) + (r & 3))) mloc = fmaxf(mloc, x);
           }
-      }
-      continue;
-    }
-    // student: log-softmax, KL terms, dsel (4 keys per store); then the
-    // next block starts from zero.  log via the hardware log2.
-    const float lse = ml.y > 0.f ? ml.x + __builtin_amdgcn_logf(ml.y) * kLn2 : 0.f;
-    const float invg = 1.f / (float)G;
-    const bool wr = a.dsel && row_ok && slot >= 0;
-    float* drow = wr ? a.dsel + ds_tile + (int64_t)(t0 + row) * a.ds_st + (int64_t)slot * kChunk : nullptr;
+        if (mloc > -INFINITY) {
+          const float mn = fmaxf(m_run, mloc);
+          float l = m_run > -INFINITY ? l_run * __builtin_amdgcn_exp2f((m_run - mn) * kLog2e) : 0.f;
 #pragma unroll
-    for (int half = 0; half < 2; ++half)
+          for (int half = 0; half < 2; ++half)
 #pragma unroll
-      for (int r4 = 0; r4 < 4; ++r4) {
-        float dv[4];
-#pragma unroll
-        for (int e = 0; e < 4; ++e) {
-          const int r = 4 * r4 + e;
-          const bool kp = (kh >> (32 * half + 8 * r4 + e)) & 1ull;
-          const float x = round_to<T>(st[half][r]);
-          const float pv = pacc[16 * half + r] * invg;
-          const float logq = x - lse;
-          const float lp = __builtin_amdgcn_logf(fmaxf(pv, 1e-12f)) * kLn2;
-          kl_acc += kp ? pv * (lp - logq) : 0.f;
-          dv[e] = kp ? __builtin_amdgcn_exp2f(logq * kLog2e) - pv : 0.f;
-          pacc[16 * half + r] = 0.f;
+            for (int r = 0; r < 16; ++r)
+              if (kept(32 * half + 8 * (r >> 2) + (r & 3)))
+                l += __builtin_amdgcn_exp2f((st[half][r] - mn) * kLog2e);
+          m_run = mn;
+          l_run = l;
         }
-        if (wr) *reinterpret_cast<float4*>(drow + 32 * half + 8 * r4 + 4 * h) = make_float4(dv[0], dv[1], dv[2], dv[3]);
+        if (u == U - 1) {                    // the head's statistics for the row: merge the lane pair
+          const float mo = __shfl_xor(m_run, 32, kWave), lo2 = __shfl_xor(l_run, 32, kWave);
+          const float mm = fmaxf(m_run, mo);
+          float ll = 0.f;
+          if (mm > -INFINITY) {
+            if (m_run > -INFINITY) ll += l_run * __builtin_amdgcn_exp2f((m_run - mm) * kLog2e);
+            if (mo > -INFINITY) ll += lo2 * __builtin_amdgcn_exp2f((mo - mm) * kLog2e);
+          }
+          if (h == 0) s_st[hh * 64 + row] = make_float2(mm, ll);
+          m_run = -INFINITY;
+          l_run = 0.f;
+        }
+        return;
       }
+      // pass 2
+      const float2 ml = s_st[hh * 64 + row];
+      if (hh < G) {
+        if (ml.y > 0.f) {
+          const float inv = 1.f / ml.y;
+#pragma unroll
+          for (int half = 0; half < 2; ++half)
+#pragma unroll
+            for (int r = 0; r < 16; ++r) {
+              const bool kp = kept(32 * half + 8 * (r >> 2) + (r & 3));
+              const float x = round_to<T>(st[half][r]) * mul;
+              pacc[16 * half + r] += kp ? __builtin_amdgcn_exp2f((x - ml.x) * kLog2e) * inv : 0.f;
+            }
+        }
+        return;
+      }
+      // student: log-softmax, KL terms, dsel (4 keys per store); then the
+      // next block starts from zero.  log via the hardware log2.
+      const float lse = ml.y > 0.f ? ml.x + __builtin_amdgcn_logf(ml.y) * kLn2 : 0.f;
+      const float invg = 1.f / (float)G;
+      const bool wr = a.dsel && row_ok && slot >= 0;
+      float* drow = wr ? a.dsel + ds_tile + (int64_t)(t0 + row) * a.ds_st + (int64_t)slot * kChunk : nullptr;
+#pragma unroll
+      for (int half = 0; half < 2; ++half)
+#pragma unroll
+        for (int r4 = 0; r4 < 4; ++r4) {
+          float dv[4];
+#pragma unroll
+          for (int e = 0; e < 4; ++e) {
+            const int r = 4 * r4 + e;
+            const bool kp = kept(32 * half + 8 * r4 + e);
+            const float x = round_to<T>(st[half][r]);
+            const float pv = pacc[16 * half + r] * invg;
+            const float logq = x - lse;
+            const float lp = __builtin_amdgcn_logf(fmaxf(pv, 1e-12f)) * kLn2;
+            kl_acc += kp ? pv * (lp - logq) : 0.f;
+            dv[e] = kp ? __builtin_amdgcn_exp2f(logq * kLog2e) - pv : 0.f;
+            pacc[16 * half + r] = 0.f;
+          }
+          if (wr) *reinterpret_cast<float4*>(drow + 32 * half + 8 * r4 + 4 * h) = make_float4(dv[0], dv[1], dv[2], dv[3]);
+        }
+    };
+    if (full)
+      compute(std::true_type{});
+    else
+      compute(std::false_type{});
+    hh_c = hh_f;
+    u_c = u_f;
+    next_of(i + 1, hh_f, u_f);
   }
 
   const float kl_row = kl_acc + __shfl_xor(kl_acc, 32, kWave);
