@@ -11,15 +11,21 @@
 // and, for the backward, dsel[t, slot, u] = q_j - p_j for key j = 64 id + u of
 // each selected slot (0 where not kept): d kl / d s_j.
 //
-// Forward: one workgroup per (sequence, index head, 64-row tile), two waves of
-// 32 rows (lane = row, S^T = K Q^T as in the attention forward).  The tile
-// visits the union of its rows' selected 64-key blocks that hold kept keys:
-//   pass 1, head-outer: each head's (max, sum) softmax statistics per row
-//            (the G teacher heads, then the student);
+// Forward: one workgroup per (sequence, index head, 64-row tile), four waves:
+// two teams, team t owning keys [32 t, 32 t + 32) of every block, each team's
+// two waves 32 rows (lane = row, S^T = K Q^T as in the attention forward).
+// The tile visits the union of its rows' selected 64-key blocks that hold
+// kept keys:
+//   pass 1, head-outer: each head's (max, sum) softmax statistics per row and
+//            key half (the G teacher heads, then the student), merged when read;
 //   pass 2, block-outer: every head's logits again, p mixed over the heads in
 //            registers, the student's log-softmax, the KL terms and dsel.
-// Keys are staged per (head, block) in LDS from registers fetched one stage
-// ahead (with the next stage's query fragments).
+// Logits are carried in log2 units (scale * log2 e folded in once) so every
+// probability is one fused multiply-add and exp2; masked keys enter the sums
+// as exp2(-inf) = 0, and a wave whose rows all keep its key half takes a copy
+// without per-key tests.  Keys are staged per (head, block) in LDS from
+// registers fetched one stage ahead (with the next stage's query fragments;
+// pass 1 reloads the query only when the head changes).
 // Backward (student path only, the teacher carries no gradient): tile
 // products on the matrix cores with ds = bf16(g dsel), see below.
 #include <algorithm>
@@ -50,10 +56,10 @@ template <> __device__ __forceinline__ float round_to<__half>(float v) {
 }
 
 template <typename T, int D>
-__global__ __launch_bounds__(128, 1) void kl_fwd_kernel(KlK p) {
+__global__ __launch_bounds__(256, 2) void kl_fwd_kernel(KlK p) {
   using M = Mfma<T>;
   using L = KlLds<D>;
-  constexpr int KP = L::KP, KS = D / 16, NT = 128;
+  constexpr int KP = L::KP, KS = D / 16, NT = 256;
   constexpr int PPT = kChunk * D / 8 / NT;
   constexpr int RPP = NT / (D / 8);
   extern __shared__ __align__(16) unsigned char smem[];
@@ -66,10 +72,14 @@ __global__ __launch_bounds__(128, 1) void kl_fwd_kernel(KlK p) {
   uint32_t* s_bits = reinterpret_cast<uint32_t*>(smem + p.bits_off);
   uint16_t* s_chunks = reinterpret_cast<uint16_t*>(smem + p.chunks_off);
   int* s_count = reinterpret_cast<int*>(s_bits + p.nwords);
-  float2* s_st = reinterpret_cast<float2*>(smem + p.stats_off);   // [G + 1][64] (max, sum)
+  float2* s_st = reinterpret_cast<float2*>(smem + p.stats_off);   // [2][G + 1][64] (max, sum) per key half
+  float* s_kl = reinterpret_cast<float*>(s_st + 2 * (p.G + 1) * 64);  // [64] key half 1's KL sums
 
   const int tid = threadIdx.x, wave = tid / kWave, lane = tid % kWave;
   const int h = lane >> 5, rl = lane & 31;
+  // two teams of two waves: team `team` owns keys [32 team, 32 team + 32) of
+  // every block for the tile's 64 rows (wave rw of the team: rows 32 rw ..)
+  const int team = wave >> 1, rw = wave & 1;
   const int tile = lid % p.ntiles;
   const int bh = lid / p.ntiles;
   const int ih = bh % a.HI, b = bh / a.HI;
@@ -111,8 +121,20 @@ __global__ __launch_bounds__(128, 1) void kl_fwd_kernel(KlK p) {
   __syncthreads();
   const int U = compact_bitmap(s_bits, p.nwords, s_chunks, s_count);
 
-  const int row = wave * 32 + rl;
+  const int row = rw * 32 + rl;
   const bool row_ok = row < nrows;
+  // a row's softmax statistics of head hh (max in log2 units, sum), merged
+  // over the two key halves
+  auto stats = [&](int hh) __attribute__((always_inline)) {
+    const float2 s0 = s_st[hh * 64 + row], s1 = s_st[((p.G + 1) + hh) * 64 + row];
+    const float mm = fmaxf(s0.x, s1.x);
+    float ll = 0.f;
+    if (mm > -INFINITY) {
+      if (s0.x > -INFINITY) ll += s0.y * __builtin_amdgcn_exp2f(s0.x - mm);
+      if (s1.x > -INFINITY) ll += s1.y * __builtin_amdgcn_exp2f(s1.x - mm);
+    }
+    return make_float2(mm, ll);
+  };
   int lo = 0, hi = 0;
   if (row_ok) row_range(row, lo, hi);
   const int* my_ids = s_ids + row * K;
@@ -168,7 +190,7 @@ __global__ __launch_bounds__(128, 1) void kl_fwd_kernel(KlK p) {
 
   T* sKw = sK + (tid / (D / 8)) * KP + (tid % (D / 8)) * 8;
   uint4 kpre[PPT], qpre[KS], qf[KS];
-  auto fetch = [&](int hh, int u) {
+  auto fetch = [&](int hh, int u, bool with_q) {
     int64_t st;
     const T* base = key_base(hh, st);
     const __amdgpu_buffer_rsrc_t rs = make_rsrc(base, (uint32_t)(((int64_t)(a.Sk - 1) * st + D) * 2));
@@ -176,16 +198,18 @@ __global__ __launch_bounds__(128, 1) void kl_fwd_kernel(KlK p) {
     const uint32_t so = (uint32_t)s_chunks[u] * kChunk * (uint32_t)st * 2u;
 #pragma unroll
     for (int k = 0; k < PPT; ++k) kpre[k] = buffer_load16(rs, vo, so + (uint32_t)(k * RPP) * (uint32_t)st * 2u);
-    const T* qr = q_row(hh);
+    // the query of a row past the tile end is row t0's (its keys are never kept)
+    if (with_q) {
+      const T* qr = q_row(hh);
 #pragma unroll
-    for (int ks = 0; ks < KS; ++ks)
-      qpre[ks] = row_ok ? *reinterpret_cast<const uint4*>(qr + 16 * ks + 8 * h) : make_uint4(0, 0, 0, 0);
+      for (int ks = 0; ks < KS; ++ks) qpre[ks] = *reinterpret_cast<const uint4*>(qr + 16 * ks + 8 * h);
+    }
   };
 
   float m_run = -INFINITY, l_run = 0.f;   // pass 1: this lane's keys of the current head
-  float pacc[32];                         // pass 2: teacher p of this lane's 32 keys of the block
+  float pacc[16];                         // pass 2: teacher p of this lane's 16 keys of the block
 #pragma unroll
-  for (int r = 0; r < 32; ++r) pacc[r] = 0.f;
+  for (int r = 0; r < 16; ++r) pacc[r] = 0.f;
   float kl_acc = 0.f;
   int slot = -1;
   uint64_t keep = 0ull;
@@ -193,7 +217,7 @@ __global__ __launch_bounds__(128, 1) void kl_fwd_kernel(KlK p) {
 
   int hh_c = 0, u_c = 0;                 // stage i
   int hh_f = 0, u_f = 0;                 // stage i + 1, the next fetch
-  if (nstage > 0) fetch(0, 0);
+  if (nstage > 0) fetch(0, 0, true);
   next_of(0, hh_f, u_f);
   for (int i = 0; i < nstage; ++i) {
     const int hh = hh_c, u = u_c;
@@ -204,50 +228,44 @@ __global__ __launch_bounds__(128, 1) void kl_fwd_kernel(KlK p) {
 #pragma unroll
     for (int ks = 0; ks < KS; ++ks) qf[ks] = qpre[ks];
     __syncthreads();
-    if (i + 1 < nstage) fetch(hh_f, u_f);
+    // pass 1 runs head-outer: the query changes only with the head
+    if (i + 1 < nstage) fetch(hh_f, u_f, i + 1 >= per_pass || u_f == 0);
 
     const int c = s_chunks[u];
     const int j0 = c * kChunk;
     if (!pass2 || hh == 0) {              // the row's slot of this block and its kept keys
       slot = find_slot_of(c);
       keep = (row_ok && slot >= 0) ? range64(min(max(lo - j0, 0), 64), min(max(hi - j0, 0), 64)) : 0ull;
-      full = __all(keep == ~0ull);        // every row of the wave keeps the whole block
+      full = __all((uint32_t)(keep >> (32 * team)) == ~0u);   // every row keeps the team's half whole
     }
-    f32x16_t st[2] = {zero16(), zero16()};
+    f32x16_t st = zero16();
 #pragma unroll
-    for (int ks = 0; ks < KS; ++ks) {
-      st[0] = M::mac(*reinterpret_cast<const uint4*>(sK + rl * KP + 16 * ks + 8 * h), qf[ks], st[0]);
-      st[1] = M::mac(*reinterpret_cast<const uint4*>(sK + (32 + rl) * KP + 16 * ks + 8 * h), qf[ks], st[1]);
-    }
+    for (int ks = 0; ks < KS; ++ks)
+      st = M::mac(*reinterpret_cast<const uint4*>(sK + (32 * team + rl) * KP + 16 * ks + 8 * h), qf[ks], st);
     // logits in the reference's rounding: the product rounded to the input
-    // dtype, the teacher's then scaled; key of register r of half `half`:
-    // 32 half + 8 (r / 4) + 4h + r % 4
-    const float mul = hh == G ? 1.f : a.scaling;
-    const uint64_t kh = keep >> (4 * h);
+    // dtype, the teacher's then scaled; key of register r:
+    // 32 team + 8 (r / 4) + 4h + r % 4
+    const float mul2 = (hh == G ? 1.f : a.scaling) * kLog2e;   // logits in log2 units
+    const uint32_t kh = (uint32_t)(keep >> (32 * team + 4 * h));   // bit 8 (r / 4) + r % 4 <-> register r
     // two straight-line copies: every row of the wave keeps the whole block
     // (no per-key tests) / masked
     auto compute = [&](auto full_tag) __attribute__((always_inline)) {
       constexpr bool FULL = decltype(full_tag)::value;
-      auto kept = [&](int bit) __attribute__((always_inline)) { return FULL || ((kh >> bit) & 1ull) != 0; };
+      auto kept = [&](int bit) __attribute__((always_inline)) { return FULL || ((kh >> bit) & 1u) != 0; };
       if (!pass2) {
         float mloc = -INFINITY;
 #pragma unroll
-        for (int half = 0; half < 2; ++half)
-#pragma unroll
-          for (int r = 0; r < 16; ++r) {
-            const float x = round_to<T>(st[half][r]) * mul;
-            st[half][r] = x;
-            if (kept(32 * half + 8 * (r >> 2) + (r & 3))) mloc = fmaxf(mloc, x);
-          }
+        for (int r = 0; r < 16; ++r) {
+          const float x = round_to<T>(st[r]) * mul2;
+          st[r] = x;
+          if (kept(8 * (r >> 2) + (r & 3))) mloc = fmaxf(mloc, x);
+        }
         if (mloc > -INFINITY) {
           const float mn = fmaxf(m_run, mloc);
-          float l = m_run > -INFINITY ? l_run * __builtin_amdgcn_exp2f((m_run - mn) * kLog2e) : 0.f;
+          float l = m_run > -INFINITY ? l_run * __builtin_amdgcn_exp2f(m_run - mn) : 0.f;
 #pragma unroll
-          for (int half = 0; half < 2; ++half)
-#pragma unroll
-            for (int r = 0; r < 16; ++r)
-              if (kept(32 * half + 8 * (r >> 2) + (r & 3)))
-                l += __builtin_amdgcn_exp2f((st[half][r] - mn) * kLog2e);
+          for (int r = 0; r < 16; ++r)   // a masked key adds exp2(-inf) = 0 (no branch)
+            l += __builtin_amdgcn_exp2f(kept(8 * (r >> 2) + (r & 3)) ? st[r] - mn : -INFINITY);
           m_run = mn;
           l_run = l;
         }
@@ -256,56 +274,52 @@ __global__ __launch_bounds__(128, 1) void kl_fwd_kernel(KlK p) {
           const float mm = fmaxf(m_run, mo);
           float ll = 0.f;
           if (mm > -INFINITY) {
-            if (m_run > -INFINITY) ll += l_run * __builtin_amdgcn_exp2f((m_run - mm) * kLog2e);
-            if (mo > -INFINITY) ll += lo2 * __builtin_amdgcn_exp2f((mo - mm) * kLog2e);
+            if (m_run > -INFINITY) ll += l_run * __builtin_amdgcn_exp2f(m_run - mm);
+            if (mo > -INFINITY) ll += lo2 * __builtin_amdgcn_exp2f(mo - mm);
           }
-          if (h == 0) s_st[hh * 64 + row] = make_float2(mm, ll);
+          if (h == 0) s_st[(team * (G + 1) + hh) * 64 + row] = make_float2(mm, ll);
           m_run = -INFINITY;
           l_run = 0.f;
         }
         return;
       }
       // pass 2
-      const float2 ml = s_st[hh * 64 + row];
+      const float2 ml = stats(hh);
       if (hh < G) {
         if (ml.y > 0.f) {
-          const float inv = 1.f / ml.y;
+          // p = exp2(x - m) / l = exp2(x - (m + log2 l))
+          const float c = ml.x + __builtin_amdgcn_logf(ml.y);
 #pragma unroll
-          for (int half = 0; half < 2; ++half)
-#pragma unroll
-            for (int r = 0; r < 16; ++r) {
-              const bool kp = kept(32 * half + 8 * (r >> 2) + (r & 3));
-              const float x = round_to<T>(st[half][r]) * mul;
-              pacc[16 * half + r] += kp ? __builtin_amdgcn_exp2f((x - ml.x) * kLog2e) * inv : 0.f;
-            }
+          for (int r = 0; r < 16; ++r) {
+            const bool kp = kept(8 * (r >> 2) + (r & 3));
+            pacc[r] += __builtin_amdgcn_exp2f(kp ? fmaf(round_to<T>(st[r]), mul2, -c) : -INFINITY);
+          }
         }
         return;
       }
       // student: log-softmax, KL terms, dsel (4 keys per store); then the
       // next block starts from zero.  log via the hardware log2.
-      const float lse = ml.y > 0.f ? ml.x + __builtin_amdgcn_logf(ml.y) * kLn2 : 0.f;
+      const float lse2 = ml.y > 0.f ? ml.x + __builtin_amdgcn_logf(ml.y) : 0.f;   // log2 units
       const float invg = 1.f / (float)G;
       const bool wr = a.dsel && row_ok && slot >= 0;
       float* drow = wr ? a.dsel + ds_tile + (int64_t)(t0 + row) * a.ds_st + (int64_t)slot * kChunk : nullptr;
 #pragma unroll
-      for (int half = 0; half < 2; ++half)
+      for (int r4 = 0; r4 < 4; ++r4) {
+        float dv[4];
 #pragma unroll
-        for (int r4 = 0; r4 < 4; ++r4) {
-          float dv[4];
-#pragma unroll
-          for (int e = 0; e < 4; ++e) {
-            const int r = 4 * r4 + e;
-            const bool kp = kept(32 * half + 8 * r4 + e);
-            const float x = round_to<T>(st[half][r]);
-            const float pv = pacc[16 * half + r] * invg;
-            const float logq = x - lse;
-            const float lp = __builtin_amdgcn_logf(fmaxf(pv, 1e-12f)) * kLn2;
-            kl_acc += kp ? pv * (lp - logq) : 0.f;
-            dv[e] = kp ? __builtin_amdgcn_exp2f(logq * kLog2e) - pv : 0.f;
-            pacc[16 * half + r] = 0.f;
-          }
-          if (wr) *reinterpret_cast<float4*>(drow + 32 * half + 8 * r4 + 4 * h) = make_float4(dv[0], dv[1], dv[2], dv[3]);
+        for (int e = 0; e < 4; ++e) {
+          const int r = 4 * r4 + e;
+          const bool kp = kept(8 * r4 + e);
+          const float pv = pacc[r] * invg;
+          const float logq2 = fmaf(round_to<T>(st[r]), kLog2e, -lse2);
+          const float lp2 = __builtin_amdgcn_logf(fmaxf(pv, 1e-12f));
+          const float term = pv * (lp2 - logq2), d = __builtin_amdgcn_exp2f(logq2) - pv;
+          kl_acc += kp ? term : 0.f;                               // log2 units
+          dv[e] = kp ? d : 0.f;
+          pacc[r] = 0.f;
         }
+        if (wr) *reinterpret_cast<float4*>(drow + 32 * team + 8 * r4 + 4 * h) = make_float4(dv[0], dv[1], dv[2], dv[3]);
+      }
     };
     if (full)
       compute(std::true_type{});
@@ -316,9 +330,13 @@ __global__ __launch_bounds__(128, 1) void kl_fwd_kernel(KlK p) {
     next_of(i + 1, hh_f, u_f);
   }
 
-  const float kl_row = kl_acc + __shfl_xor(kl_acc, 32, kWave);
-  if (row_ok && h == 0) {
-    const float2 sst = U > 0 ? s_st[G * 64 + row] : make_float2(-INFINITY, 0.f);
+  // the row's KL: the lane pair, then the two key halves (team 0 writes)
+  const float kl_half = (kl_acc + __shfl_xor(kl_acc, 32, kWave)) * kLn2;
+  if (team == 1 && h == 0) s_kl[row] = kl_half;
+  __syncthreads();
+  if (team == 0 && row_ok && h == 0) {
+    const float kl_row = kl_half + s_kl[row];
+    const float2 sst = U > 0 ? stats(G) : make_float2(-INFINITY, 0.f);
     const bool valid = sst.y > 0.f;
     a.kl[(int64_t)b * a.kl_sb + (int64_t)ih * a.kl_sh + t0 + row] = valid ? kl_row : 0.f;
     a.valid[(int64_t)b * a.va_sb + (int64_t)ih * a.va_sh + t0 + row] = valid ? 1 : 0;
@@ -617,13 +635,13 @@ extern "C" int srswa_gather_kl_fwd(const srswa_kl_args* a, void* stream) {
   k.chunks_off = k.bits_off + (k.nwords + 4) * 4;
   const int nchunk_max = std::min(kTileRows * a->K, nblk);
   k.stats_off = (k.chunks_off + nchunk_max * 2 + 15) & ~15;
-  const size_t lds = (size_t)k.stats_off + (size_t)(k.G + 1) * kTileRows * 8;
+  const size_t lds = (size_t)k.stats_off + 2 * (size_t)(k.G + 1) * kTileRows * 8 + kTileRows * 4;
   if (lds > 160 * 1024) {
     set_error("gather kl: %zu bytes of LDS needed", lds);
     return SRSWA_UNSUPPORTED;
   }
   hipStream_t st = reinterpret_cast<hipStream_t>(stream);
-  const dim3 grid((unsigned)(8 * k.per_xcd)), block(128);
+  const dim3 grid((unsigned)(8 * k.per_xcd)), block(256);
   static size_t granted[4] = {0, 0, 0, 0};
   bool lds_ok = true;
 #define KL_LAUNCH(T_, D_, I_)                                                                    \
