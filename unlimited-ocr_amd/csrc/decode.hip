@@ -8,7 +8,9 @@
 // Work decomposition.  The keys one query row reads are cut into "units" of
 // UK keys: ceil(BS/UK) units per selected remote block slot, then
 // ceil(LW/UK) units tiling the token window (q_pos-LW, q_pos] from its first
-// key (the window is contiguous, so its units need not be block aligned).
+// key (the window is contiguous, so its units need not be block aligned).  A
+// paged window's units sit on the UK grid inside one page each; its first
+// unit also carries the window's last keys, so it still takes LW/UK units.
 // One wavefront streams one or more units:
 //   * K and V rows are read straight into VGPRs with 16-byte loads, LPR lanes
 //     per key row (bf16, D=128: 16 lanes x 16 B = the row's two 128-byte
@@ -18,9 +20,10 @@
 //   * online softmax in the log2 domain (wave max/sum via shuffles), p is
 //     broadcast back through 256 bytes of LDS per wave, then o += p v;
 // Four waves (one workgroup) merge their (m, l, o) in LDS; the workgroups of
-// one (row, head) merge through a scratch buffer, the last one to finish
-// (atomic arrival counter) producing the output.  No host sync, no second
-// kernel; the arrival counters are left zeroed for the next call.
+// one (row, head) write (O, M, L) records to a scratch buffer, and a second
+// small kernel combines them (decode_merge_kernel).  The in-kernel form, where
+// the last workgroup to arrive (atomic counter, left zeroed for the next
+// call) combines them, is kept behind SRSWA_DECODE_MERGE=atomic.
 #include <stdarg.h>
 #include <stdio.h>
 #include <stdlib.h>
@@ -247,7 +250,8 @@ __global__ __launch_bounds__(kDecodeWaves * kWave) void decode_kernel(DecodeK p)
     const int u = u_base + wave + i * kDecodeWaves;
     if (u >= p.n_units) break;
     int k0, k1, klo;
-    int page = 0;
+    int page = 0, page2 = 0;
+    int wrap = 0;            // keys k0 + kk, kk < wrap, are read LW keys further on
     float bias_l2 = 0.f;
     if (u < p.n_remote_units) {
       const int slot = u / p.upb, sub = u % p.upb;
@@ -280,10 +284,23 @@ __global__ __launch_bounds__(kDecodeWaves * kWave) void decode_kernel(DecodeK p)
       klo = k0;
       bias_l2 = bias * kLog2e;
     } else {
-      k0 = ws_al + (u - p.n_remote_units) * UK;
+      const int j = u - p.n_remote_units;
+      k0 = ws_al + j * UK;
       k1 = min(k0 + UK, last + 1);
       klo = PAGED ? max(k0, ws) : k0;
-      if (PAGED) page = __shfl(win_page, (k0 >> p.bs_shift) - wblk0, kWave);
+      if (PAGED) {
+        page = __shfl(win_page, (k0 >> p.bs_shift) - wblk0, kWave);
+        // The paged window [ws, ws + LW) on the UK grid: units j = 1.. are
+        // whole; unit 0 holds its first UK - (ws - ws_al) keys and, in the
+        // slots before them, the window's last ws - ws_al keys (LW further
+        // on, another page), so LW / UK units cover any window
+        wrap = j == 0 ? ws - ws_al : 0;
+        if (wrap > 0) {
+          page2 = __shfl(win_page, ((k0 + a.local_window) >> p.bs_shift) - wblk0, kWave);
+          klo = ws;
+          k1 = last + 1;
+        }
+      }
     }
     if (k1 <= klo) continue;   // uniform across the wave
 
@@ -297,17 +314,38 @@ __global__ __launch_bounds__(kDecodeWaves * kWave) void decode_kernel(DecodeK p)
       kr0 = k0 & (a.block_size - 1);
     }
     uint4 kr[NI], vr[NI];
+    // key of unit slot kk (wrapped slots: LW further on, in page2)
+    auto key_of = [&](int kk) { return k0 + kk + (PAGED && kk < wrap ? a.local_window : 0); };
+    if (PAGED && wrap > 0) {
+      const int64_t dk = (int64_t)(page2 - page) * p.k_pst, dv = (int64_t)(page2 - page) * p.v_pst;
+      const int w0 = (k0 + a.local_window) & (a.block_size - 1);   // row of the first wrapped key
 #pragma unroll
-    for (int i = 0; i < NI; ++i) {
-      const int key = k0 + i * RPI + r;
-      kr[i] = ((!PAGED || key >= klo) && key < k1) ? load_stream(kb + (int64_t)(kr0 + i * RPI + r) * a.k_st)
-                                                   : make_uint4(0, 0, 0, 0);
-    }
+      for (int i = 0; i < NI; ++i) {
+        const int kk = i * RPI + r;
+        const int key = key_of(kk);
+        const int64_t ro = kk < wrap ? dk + (int64_t)(w0 + kk) * a.k_st : (int64_t)(kr0 + kk) * a.k_st;
+        kr[i] = (key >= klo && key < k1) ? load_stream(kb + ro) : make_uint4(0, 0, 0, 0);
+      }
 #pragma unroll
-    for (int i = 0; i < NI; ++i) {
-      const int key = k0 + i * RPI + r;
-      vr[i] = ((!PAGED || key >= klo) && key < k1) ? load_stream(vb + (int64_t)(kr0 + i * RPI + r) * a.v_st)
-                                                   : make_uint4(0, 0, 0, 0);
+      for (int i = 0; i < NI; ++i) {
+        const int kk = i * RPI + r;
+        const int key = key_of(kk);
+        const int64_t ro = kk < wrap ? dv + (int64_t)(w0 + kk) * a.v_st : (int64_t)(kr0 + kk) * a.v_st;
+        vr[i] = (key >= klo && key < k1) ? load_stream(vb + ro) : make_uint4(0, 0, 0, 0);
+      }
+    } else {
+#pragma unroll
+      for (int i = 0; i < NI; ++i) {
+        const int key = k0 + i * RPI + r;
+        kr[i] = ((!PAGED || key >= klo) && key < k1) ? load_stream(kb + (int64_t)(kr0 + i * RPI + r) * a.k_st)
+                                                     : make_uint4(0, 0, 0, 0);
+      }
+#pragma unroll
+      for (int i = 0; i < NI; ++i) {
+        const int key = k0 + i * RPI + r;
+        vr[i] = ((!PAGED || key >= klo) && key < k1) ? load_stream(vb + (int64_t)(kr0 + i * RPI + r) * a.v_st)
+                                                     : make_uint4(0, 0, 0, 0);
+      }
     }
 
     float part[NI];
@@ -318,7 +356,7 @@ __global__ __launch_bounds__(kDecodeWaves * kWave) void decode_kernel(DecodeK p)
 #pragma unroll
     for (int o = DUP / 2; o >= 1; o >>= 1) part[0] += __shfl_xor(part[0], o, kWave);
     const int i_own = c / DUP;                    // which instruction's key this lane holds
-    const int key = k0 + i_own * RPI + r;
+    const int key = key_of(i_own * RPI + r);
     const bool owner = (c % DUP) == 0;
     const float t = ((!PAGED || key >= klo) && key < k1) ? part[0] * p.scale_l2 + bias_l2 : -INFINITY;
     const float mnew = fmaxf(m, wave_max(t));     // finite: key klo is always kept
@@ -517,10 +555,9 @@ DecodePlan make_plan(const srswa_decode_args* a, bool paged = false) {
   pl.UK = ni * (kWave / lpr);
   pl.upb = ceil_div(a->block_size, pl.UK);
   pl.n_remote_units = a->S * pl.upb;
-  // paged windows run on the UK grid: one extra unit for the unaligned start
-  pl.n_units = pl.n_remote_units +
-               (paged ? (a->local_window > 0 ? ceil_div(a->local_window, pl.UK) + 1 : 0)
-                      : ceil_div(a->local_window, pl.UK));
+  // paged windows run on the UK grid, LW / UK units with the first one
+  // wrapped (UK divides the page size, which divides LW)
+  pl.n_units = pl.n_remote_units + ceil_div(a->local_window, pl.UK);
   static const int upw = env_int("SRSWA_DECODE_UPW", 2);
   pl.upw = upw > 1 ? upw : 1;
   pl.nsplit = ceil_div(pl.n_units, kDecodeWaves * pl.upw);
