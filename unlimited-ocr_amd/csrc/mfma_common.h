@@ -68,87 +68,6 @@ __device__ __forceinline__ f32x16_t zero16() {
 // key offset (0..31) inside a 32x32 D tile held by register r of lane half h
 __device__ __forceinline__ int d_row(int r, int h) { return 8 * (r >> 2) + 4 * h + (r & 3); }
 
-// Per-tile chunk plan, built in LDS by all threads of a workgroup from
-//   s_qi / s_seg / s_ls [64]: each row's key index, sample start and window start
-//   s_ids [64 * S]:           each row's slot block ids (-1 = none)
-// into the sorted list s_chunks of 64-key chunks holding a window key of some
-// row or a key of a selected block that is a remote key of that row.  s_bits
-// (nwords zeroed words) is the scratch bitmap.  Returns the chunk count.
-__device__ inline int build_chunk_plan(const int* s_qi, const int* s_seg, const int* s_ls, const int* s_ids,
-                                int S, int BS, int nrows, int nchunk, int nwords, uint32_t* s_bits,
-                                int* s_chunks, int* s_count, int LW, int Sk) {
-  const int tid = threadIdx.x, nthr = blockDim.x;
-  // window ranges: row r covers chunks [ls_r / 64, qi_r / 64]
-  const int wspan = (LW + kChunk - 1) / kChunk + 1;
-  for (int e = tid; e < nrows * wspan; e += nthr) {
-    const int r = e / wspan, k = e % wspan;
-    const int c0 = max(s_ls[r], 0) / kChunk, c1 = s_qi[r] / kChunk;
-    const int c = c0 + k;
-    if (c <= c1) atomicOr(&s_bits[c >> 5], 1u << (c & 31));
-  }
-  // remote keys of every selected block: [max(id*BS, seg), min(id*BS+BS, ls, qi+1))
-  const int bspan = (BS + kChunk - 1) / kChunk + 1;
-  const int maxblk = (Sk - 1) / BS;
-  for (int e = tid; e < nrows * S; e += nthr) {
-    const int r = e / S;
-    const int id = s_ids[e];
-    if (id < 0 || id > maxblk) continue;
-    const int lo = max(id * BS, s_seg[r]);
-    const int hi = min(min(id * BS + BS, s_ls[r]), s_qi[r] + 1);
-    if (lo >= hi) continue;
-    const int c0 = lo / kChunk, c1 = (hi - 1) / kChunk;
-    for (int c = c0; c <= c1 && c < c0 + bspan; ++c) atomicOr(&s_bits[c >> 5], 1u << (c & 31));
-  }
-  __syncthreads();
-  // compaction (wave 0): prefix popcount over the words
-  if (tid < kWave) {
-    int base = 0;
-    for (int w0 = 0; w0 < nwords; w0 += kWave) {
-      const int w = w0 + tid;
-      const uint32_t bits = w < nwords ? s_bits[w] : 0u;
-      const int cnt = __popc(bits);
-      int incl = cnt;
-#pragma unroll
-      for (int o = 1; o < kWave; o <<= 1) {
-        const int v = __shfl_up(incl, o, kWave);
-        if (tid >= o) incl += v;
-      }
-      int pos = base + incl - cnt;
-      uint32_t bb = bits;
-      while (bb) {
-        const int bit = __ffs(bb) - 1;
-        bb &= bb - 1;
-        s_chunks[pos++] = w * 32 + bit;
-      }
-      base += __shfl(incl, kWave - 1, kWave);
-    }
-    if (tid == 0) *s_count = base;
-  }
-  __syncthreads();
-  (void)nchunk;
-  return *s_count;
-}
-
-
-// A operand of a transposed product X^T P^T (M = feature d, K = 16 rows of X)
-// read from X stored naturally in LDS as [row][pitch]: lane (m = d, half h)
-// needs X[row(h, j)][d] for the permuted row order of the B operand (see the
-// header comment).  Eight 16-bit reads; lanes of one read touch 32 consecutive
-// columns of two rows 4 apart, which with a pitch of D+8 elements land in
-// disjoint bank ranges (no conflicts).
-template <int PITCH>
-__device__ __forceinline__ uint4 a_operand_t(const uint16_t* x, int d, int ks, int h) {
-  const uint16_t* p = x + (16 * ks + 4 * h) * PITCH + d;
-  uint32_t w[4];
-#pragma unroll
-  for (int i = 0; i < 2; ++i) {
-    const uint16_t* q = p + 8 * i * PITCH;
-    w[2 * i] = (uint32_t)q[0] | ((uint32_t)q[PITCH] << 16);
-    w[2 * i + 1] = (uint32_t)q[2 * PITCH] | ((uint32_t)q[3 * PITCH] << 16);
-  }
-  return make_uint4(w[0], w[1], w[2], w[3]);
-}
-
 typedef short s16x4_t __attribute__((ext_vector_type(4)));
 typedef __attribute__((address_space(3))) s16x4_t lds_s16x4_t;
 
@@ -330,42 +249,6 @@ __device__ inline int plan_chunks(const int* s_qi, const int* s_seg, const int* 
   }
   __syncthreads();
   return compact_bitmap(s_bits, nwords, s_chunks, s_count);
-}
-
-// First slot (or -1) of each row's selected blocks overlapping each planned
-// chunk: tab[(u * 64 + row) * 8 + q] for chunk position u < ucap and the q-th
-// block overlapping the chunk.  Built by one thread per row walking its slots
-// in order, so the first slot holding an id wins (duplicates never count twice).
-__device__ inline void build_slot_table(const int* s_qi, const int* s_seg, const int* s_ls,
-                                        const int* s_ids, const int* s_chunks, int U, int ucap,
-                                        int S, int BS, int Sk, int nrows, int8_t* tab) {
-  const int tid = threadIdx.x;
-  const int ulim = min(U, ucap);
-  for (int w = tid; w < ulim * 64 * 8 / 4; w += blockDim.x) reinterpret_cast<int*>(tab)[w] = -1;
-  __syncthreads();
-  if (tid < nrows) {
-    const int r = tid;
-    const int maxblk = (Sk - 1) / BS;
-    for (int s = 0; s < S; ++s) {
-      const int id = s_ids[r * S + s];
-      if (id < 0 || id > maxblk) continue;
-      const int lo = max(id * BS, s_seg[r]);
-      const int hi = min(min(id * BS + BS, s_ls[r]), s_qi[r] + 1);
-      if (lo >= hi) continue;
-      for (int c = lo / kChunk; c <= (hi - 1) / kChunk; ++c) {
-        int a = 0, b = U;                       // lower_bound of c in s_chunks
-        while (a < b) {
-          const int m = (a + b) >> 1;
-          if (s_chunks[m] < c) a = m + 1; else b = m;
-        }
-        if (a >= ulim || s_chunks[a] != c) continue;
-        const int q = id - (c * kChunk) / BS;
-        int8_t* e = tab + ((a * 64 + r) * 8 + q);
-        if (q >= 0 && q < 8 && *e < 0) *e = (int8_t)s;
-      }
-    }
-  }
-  __syncthreads();
 }
 
 // Raise a kernel's dynamic-LDS limit to `bytes` when it needs more than the
