@@ -418,32 +418,66 @@ __global__ __launch_bounds__(kDecodeWaves * kWave) void decode_kernel(DecodeK p)
   if (p.nsplit > 1) {
     // record: O[0..D) then M, L; records are 128-byte aligned
     float* rec = p.part + (rh * p.nsplit + split) * p.pstride;
-    if (r == 0) store_out<float>(rec + c * EPV, O, EPV);
-    if (lane == 0) { rec[D] = M; rec[D + 1] = L; }
-    if (!ATOMIC_MERGE) return;   // decode_merge_kernel combines the records
-    __threadfence();
-    uint32_t arrived = 0;
-    if (lane == 0) arrived = atomicAdd(&p.cnt[rh], 1u);
-    arrived = __shfl(arrived, 0, kWave);
-    if (arrived != (uint32_t)(p.nsplit - 1)) return;
-    __threadfence();
-    if (lane == 0) p.cnt[rh] = 0u;   // leave the counter zeroed for the next call
-    const float* recs = p.part + rh * p.nsplit * p.pstride;
-    M = -INFINITY;
-    for (int s = 0; s < p.nsplit; ++s) M = fmaxf(M, recs[s * p.pstride + D]);
-    L = 0.f;
-#pragma unroll
-    for (int e = 0; e < EPV; ++e) O[e] = 0.f;
-    for (int s = 0; s < p.nsplit; ++s) {
-      const float ms = recs[s * p.pstride + D];
-      const float wt = ms == -INFINITY ? 0.f : exp2f(ms - M);
-      L += recs[s * p.pstride + D + 1] * wt;
+    if constexpr (!ATOMIC_MERGE) {
+      if (r == 0) store_out<float>(rec + c * EPV, O, EPV);
+      if (lane == 0) { rec[D] = M; rec[D + 1] = L; }
+      return;   // decode_merge_kernel combines the records
+    } else {
+      // The last workgroup of the row to arrive combines the records.  Every
+      // access to the records and the counter is an agent-scope atomic: the
+      // stores are written through to the device's coherence point and the
+      // loads read from it (no per-XCD L2 copy), so neither side needs the
+      // L2-wide write-back / invalidate of a device-scope fence.  The explicit
+      // wait completes this wave's record stores before its counter update;
+      // the reader's loads are issued only after its counter update returned.
       if (r == 0) {
-        float f[EPV];
-        for (int e = 0; e < EPV; e += 4)
-          Vec16<float>::unpack(*reinterpret_cast<const uint4*>(recs + s * p.pstride + c * EPV + e), f + e);
 #pragma unroll
-        for (int e = 0; e < EPV; ++e) O[e] = fmaf(f[e], wt, O[e]);
+        for (int e = 0; e < EPV; ++e)
+          __hip_atomic_store(rec + c * EPV + e, O[e], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      }
+      if (lane == 0) {
+        __hip_atomic_store(rec + D, M, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        __hip_atomic_store(rec + D + 1, L, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      }
+      __builtin_amdgcn_s_waitcnt(0);
+      uint32_t arrived = 0;
+      if (lane == 0) arrived = __hip_atomic_fetch_add(p.cnt + rh, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      arrived = __shfl(arrived, 0, kWave);
+      if (arrived != (uint32_t)(p.nsplit - 1)) return;
+      if (lane == 0) __hip_atomic_store(p.cnt + rh, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      const float* recs = p.part + rh * p.nsplit * p.pstride;
+      auto ld = [](const float* q) { return __hip_atomic_load(q, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT); };
+      M = -INFINITY;
+      L = 0.f;
+#pragma unroll
+      for (int e = 0; e < EPV; ++e) O[e] = 0.f;
+      for (int s0 = 0; s0 < p.nsplit; s0 += 8) {
+        // every load of up to 8 records in flight before they are combined
+        float ms[8], ls[8], os[8][EPV];
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+          const bool in = s0 + j < p.nsplit;
+          const float* q = recs + (int64_t)(in ? s0 + j : s0) * p.pstride;
+          ms[j] = in ? ld(q + D) : -INFINITY;
+          ls[j] = in ? ld(q + D + 1) : 0.f;
+#pragma unroll
+          for (int e = 0; e < EPV; ++e) os[j][e] = (in && r == 0) ? ld(q + c * EPV + e) : 0.f;
+        }
+        float Mn = M;
+#pragma unroll
+        for (int j = 0; j < 8; ++j) Mn = fmaxf(Mn, ms[j]);
+        const float r0 = M == -INFINITY ? 0.f : exp2f(M - Mn);
+        L *= r0;
+#pragma unroll
+        for (int e = 0; e < EPV; ++e) O[e] *= r0;
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+          const float wt = ms[j] == -INFINITY ? 0.f : exp2f(ms[j] - Mn);
+          L = fmaf(ls[j], wt, L);
+#pragma unroll
+          for (int e = 0; e < EPV; ++e) O[e] = fmaf(os[j][e], wt, O[e]);
+        }
+        M = Mn;
       }
     }
   }
@@ -524,8 +558,7 @@ int elem_bytes(int dt) { return dt == SRSWA_F32 ? 4 : 2; }
 // load instructions per unit (bf16 D=128: 32 | 64 keys); SRSWA_DECODE_UPW =
 // units per wave (default 2); SRSWA_DECODE_MERGE = kernel (a second kernel
 // combines the split records, default) | atomic (the last-arriving workgroup
-// combines them after device-scope fences, which cost ~6x on MI355X: the
-// fences write back / invalidate the per-XCD L2s).
+// combines them, records and counter as agent-scope atomics).
 int env_int(const char* name, int dflt) {
   const char* v = getenv(name);
   return (v && *v) ? atoi(v) : dflt;
