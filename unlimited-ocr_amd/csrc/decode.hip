@@ -563,12 +563,9 @@ int env_int(const char* name, int dflt) {
   const char* v = getenv(name);
   return (v && *v) ? atoi(v) : dflt;
 }
-bool merge_in_kernel() {
-  static const bool v = [] {
-    const char* m = getenv("SRSWA_DECODE_MERGE");
-    return m && strcmp(m, "atomic") == 0;
-  }();
-  return v;
+bool merge_in_kernel() {   // read per call, so a process can switch it
+  const char* m = getenv("SRSWA_DECODE_MERGE");
+  return m && strcmp(m, "atomic") == 0;
 }
 
 // row instructions per unit for (dtype, D)
