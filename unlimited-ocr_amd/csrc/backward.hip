@@ -865,7 +865,7 @@ size_t dkv_smem(const BwdK& k) {
 
 template <typename T, int D>
 int launch_bwd(const BwdK& k, hipStream_t st) {
-  static size_t granted_dq = 0, granted_dkv = 0;
+  static LdsGrant granted_dq, granted_dkv;
   if (!ensure_dynamic_lds(&dq_kernel<T, D>, dq_smem(k), &granted_dq) ||
       !ensure_dynamic_lds(&dkv_kernel<T, D>, dkv_smem(k), &granted_dkv))
     return SRSWA_UNSUPPORTED;

@@ -642,7 +642,7 @@ extern "C" int srswa_gather_kl_fwd(const srswa_kl_args* a, void* stream) {
   }
   hipStream_t st = reinterpret_cast<hipStream_t>(stream);
   const dim3 grid((unsigned)(8 * k.per_xcd)), block(256);
-  static size_t granted[4] = {0, 0, 0, 0};
+  static LdsGrant granted[4];
   bool lds_ok = true;
 #define KL_LAUNCH(T_, D_, I_)                                                                    \
   lds_ok = ensure_dynamic_lds(kl_fwd_kernel<T_, D_>, lds, &granted[I_]);                       \

@@ -15,6 +15,8 @@
 // that the A operand reproduces with two 8-byte LDS reads.
 #pragma once
 
+#include <atomic>
+
 #include "common.h"
 
 namespace srswa {
@@ -252,10 +254,23 @@ __device__ inline int plan_chunks(const int* s_qi, const int* s_seg, const int* 
 }
 
 // Raise a kernel's dynamic-LDS limit to `bytes` when it needs more than the
-// default; returns false (error recorded) when the runtime refuses.
+// default; returns false (error recorded) when the runtime refuses.  The grant
+// is remembered per device (the attribute is set with that device current) in
+// atomics, so calls from several host threads are safe.
+constexpr int kMaxDevices = 64;
+struct LdsGrant {
+  std::atomic<size_t> bytes[kMaxDevices];   // zero-initialised in static storage
+};
 template <typename F>
-inline bool ensure_dynamic_lds(F* kernel, size_t bytes, size_t* granted) {
-  if (bytes <= 64 * 1024 || bytes <= *granted) return true;
+inline bool ensure_dynamic_lds(F* kernel, size_t bytes, LdsGrant* g) {
+  if (bytes <= 64 * 1024) return true;
+  int dev = -1;
+  if (hipGetDevice(&dev) != hipSuccess) {
+    (void)hipGetLastError();
+    dev = -1;
+  }
+  const bool cached = dev >= 0 && dev < kMaxDevices;
+  if (cached && bytes <= g->bytes[dev].load(std::memory_order_relaxed)) return true;
   const hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(kernel),
                                            hipFuncAttributeMaxDynamicSharedMemorySize, (int)bytes);
   if (e != hipSuccess) {
@@ -263,7 +278,11 @@ inline bool ensure_dynamic_lds(F* kernel, size_t bytes, size_t* granted) {
     set_error("cannot grant %zu bytes of LDS: %s", bytes, hipGetErrorString(e));
     return false;
   }
-  *granted = bytes;
+  if (cached) {
+    size_t cur = g->bytes[dev].load(std::memory_order_relaxed);
+    while (cur < bytes && !g->bytes[dev].compare_exchange_weak(cur, bytes, std::memory_order_relaxed)) {
+    }
+  }
   return true;
 }
 

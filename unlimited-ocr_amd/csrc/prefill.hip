@@ -393,7 +393,7 @@ int check_fwd(const srswa_fwd_args* a) {
 
 template <typename T, int D>
 int launch_fwd(const FwdK& k, size_t smem, hipStream_t st) {
-  static size_t granted = 0;
+  static LdsGrant granted;
   if (!ensure_dynamic_lds(&fwd_kernel<T, D>, smem, &granted)) return SRSWA_UNSUPPORTED;
   hipLaunchKernelGGL((fwd_kernel<T, D>), dim3((unsigned)(8 * k.per_xcd)), dim3(128), smem, st, k);
   const hipError_t e = hipGetLastError();
