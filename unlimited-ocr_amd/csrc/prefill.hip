@@ -224,6 +224,10 @@ __global__ __launch_bounds__(128, 2) void fwd_kernel(FwdK p) {
 
     // S^T (keys x rows) for the two 32-key halves of the chunk
     f32x16_t st[2] = {zero16(), zero16()};
+    // the wave's issue priority is raised over its MFMA blocks: of the two waves
+    // of a SIMD, the one with matrix work issues it first and the other's
+    // softmax VALU fills the MFMA execution time
+    __builtin_amdgcn_s_setprio(1);
 #pragma unroll
     for (int ks = 0; ks < KS; ++ks) {
       const uint4 a0 = *reinterpret_cast<const uint4*>(sK + rl * KP + 16 * ks + 8 * h);
@@ -231,6 +235,7 @@ __global__ __launch_bounds__(128, 2) void fwd_kernel(FwdK p) {
       st[0] = M::mac(a0, qf[ks], st[0]);
       st[1] = M::mac(a1, qf[ks], st[1]);
     }
+    __builtin_amdgcn_s_setprio(0);
 
     // row max of the chunk's logits (log2 units); lane (l, h) holds keys
     // 32 half + 8 (r / 4) + 4h + r % 4
@@ -309,6 +314,7 @@ __global__ __launch_bounds__(128, 2) void fwd_kernel(FwdK p) {
     }
     // O^T += V^T P^T, k-step outer: the MT accumulators form independent
     // chains that interleave, and a step's operands are read before its MFMAs
+    __builtin_amdgcn_s_setprio(1);
 #pragma unroll
     for (int ks = 0; ks < 4; ++ks) {
       uint4 va[MT];
@@ -317,6 +323,7 @@ __global__ __launch_bounds__(128, 2) void fwd_kernel(FwdK p) {
 #pragma unroll
       for (int mt = 0; mt < MT; ++mt) o[mt] = M::mac(va[mt], pb[ks], o[mt]);
     }
+    __builtin_amdgcn_s_setprio(0);
   }
 
   const float l_tot = l_run + __shfl_xor(l_run, 32, kWave);
