@@ -239,9 +239,11 @@ __global__ __launch_bounds__(256, 2) void kl_fwd_kernel(KlK p) {
       full = __all((uint32_t)(keep >> (32 * team)) == ~0u);   // every row keeps the team's half whole
     }
     f32x16_t st = zero16();
+    __builtin_amdgcn_s_setprio(1);   // matrix work first; the other wave of the SIMD fills it with VALU
 #pragma unroll
     for (int ks = 0; ks < KS; ++ks)
       st = M::mac(*reinterpret_cast<const uint4*>(sK + (32 * team + rl) * KP + 16 * ks + 8 * h), qf[ks], st);
+    __builtin_amdgcn_s_setprio(0);
     // logits in the reference's rounding: the product rounded to the input
     // dtype, the teacher's then scaled; key of register r:
     // 32 team + 8 (r / 4) + 4h + r % 4
@@ -629,6 +631,7 @@ extern "C" int srswa_gather_kl_fwd(const srswa_kl_args* a, void* stream) {
   k.KV = a->HQ / a->HKV;
   k.nlogical = a->B * a->HI * k.ntiles;
   k.per_xcd = ceil_div(k.nlogical, 8);
+
   const int tile_bytes = a->D == 64 ? KlLds<64>::tileBytes : KlLds<128>::tileBytes;
   k.ids_off = tile_bytes;
   k.bits_off = k.ids_off + kTileRows * a->K * 4;
