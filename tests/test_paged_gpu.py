@@ -1,9 +1,9 @@
 """Paged decode (srswa_gather_decode_paged, the serving cache layout of
 dash_sparse_attn_decode) vs the CPU oracle ``paged_decode_attend``: pages in
 random order, ragged sequence lengths, 1 and 2 decode queries per request,
-GQA, page sizes 16..128, no window (local_blocks 0), -1 padding, repeated ids,
-bias and no bias; bf16 within 2e-2 (beyond output rounding), fp32 within
-1e-5 relative (max-abs error / max-abs reference)."""
+GQA, page sizes 16..128, no window (local_blocks 0) and the widest one (63),
+-1 padding, repeated ids, bias and no bias; bf16 within 2e-2 (beyond output
+rounding), fp32 within 1e-5 relative (max-abs error / max-abs reference)."""
 
 import math
 
@@ -41,6 +41,10 @@ CASES = {
                          with_bias=True),
     "fp32_p32": dict(R=3, dql=1, H=4, Hkv=2, D=128, page=32, nb=20, K=5, lb=3, dtype=torch.float32,
                     with_bias=True),
+    # the widest window (63 pages): the wrapped first unit reads its last keys
+    # from the window's 64th page
+    "bf16_p16_lb63": dict(R=3, dql=2, H=4, Hkv=4, D=128, page=16, nb=80, K=4, lb=63, dtype=torch.bfloat16,
+                         with_bias=True),
 }
 
 
