@@ -269,6 +269,37 @@ def bench_prefill(args):
                          "kernel": "srswa::fwd_kernel<bf16,128>"}}
 
 
+def bench_blockmax(args):
+    """Block-max indexer scoring (the reference's K4, HF/sparse_gather_triton.py:445-524)
+    on config 4's prefill chunk: one index head, B=4 sequences x 2048 query rows at the
+    tail of 65536 keys; a row scores every key before its 512-token window."""
+    import torch
+    from srswa import ops
+    dev = torch.device("cuda:0")
+    B, C, Sk, D, BS, LW = 4, 2048, 65536, 128, 64, 512
+    g = torch.Generator().manual_seed(20261204)
+    q = (torch.randn(B, C, D, generator=g) / D ** 0.5).to(torch.bfloat16).to(dev)
+    k = torch.randn(B, Sk, D, generator=g).to(torch.bfloat16).to(dev)
+    pos = (torch.arange(C) + (Sk - C)).expand(B, C).contiguous()
+    seg = torch.zeros(B, C, dtype=torch.long)
+    nblk = Sk // BS
+    posd, segd = pos.to(dev), seg.to(dev)
+    fn = lambda: ops.block_max_score(q, k, posd, segd, block_size=BS, num_key_blocks=nblk, local_window=LW)
+    ms = _time_launches(fn, args.steps, args.warmup, dev)
+    pairs = B * int((pos[0] - LW + 1).clamp(min=0).sum())       # keys j <= pos - LW of every row
+    flops = pairs * 2 * D
+    tfs = flops / (ms * 1e-3) / 1e12
+    return {"metric": "block-max indexer scoring rows/s + MFMA TFLOP/s (config 4 chunk)",
+            "value": B * C / (ms * 1e-3), "unit": "query rows/s", "n_gpus": 1, "steps": args.steps,
+            "warmup": args.warmup, "ms_per_step": ms, "higher_is_better": True, "scaling": "weak",
+            "vs_baseline": None, "dtype": "bf16", "data": "synthetic (seeded N(0,1) keys, N(0,1/D) queries)",
+            "config": {"workload": "block-max scores of B=4 x 2048 rows at positions 63488..65535 over "
+                                   "65536 keys, one index head, D=128, block 64, window 512",
+                       "flops_per_step": flops, "scored_pairs": pairs},
+            "roofline": {"bound": "mfma", "achieved": tfs, "peak": 2500.0, "unit": "TFLOP/s",
+                         "frac": tfs / 2500.0, "traffic": None, "kernel": "srswa::block_max_kernel<bf16,128>"}}
+
+
 def bench_fwdbwd(args):
     """Config 5: self-attention forward + backward, B=2, T=16384."""
     import torch
@@ -533,7 +564,8 @@ def main():
     ap.add_argument("--steps", type=int, default=200)
     ap.add_argument("--warmup", type=int, default=20)
     ap.add_argument("--config", default="decode",
-                    choices=["decode", "indexer", "prefill", "fwdbwd", "paged", "dash", "page", "kl", "copycal"])
+                    choices=["decode", "indexer", "prefill", "fwdbwd", "paged", "dash", "page", "kl", "blockmax",
+                             "copycal"])
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--no-check", action="store_true", help="skip the oracle spot check")
     ap.add_argument("--cpu-budget", type=float, default=12.0)
@@ -544,6 +576,7 @@ def main():
         sys.exit(2)
     fn = {"decode": bench_decode, "indexer": bench_indexer, "prefill": bench_prefill,
           "fwdbwd": bench_fwdbwd, "paged": bench_paged, "dash": bench_dash, "page": bench_page, "kl": bench_kl,
+          "blockmax": bench_blockmax,
           "copycal": bench_copycal}[args.config]
     res = fn(args)
     print(json.dumps(res), flush=True)

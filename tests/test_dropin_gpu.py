@@ -78,3 +78,24 @@ def test_block_max_score(dev, bs):
     fin = torch.isfinite(ref)
     assert torch.equal(torch.isfinite(got), fin)
     assert (got.double()[fin] - ref[fin]).abs().max().item() <= 1e-3 * max(1.0, ref[fin].abs().max().item())
+
+
+@pytest.mark.parametrize("bs,d", [(16, 128), (64, 128), (192, 64)])
+def test_block_max_score_key_slabs(dev, bs, d):
+    """Keys long enough for several key slabs per query tile (slabs of >= 16
+    64-key chunks of whole blocks, 3 chunks per block at bs=192); positions from
+    0 to the end, so some tiles stop inside a slab and later slabs hold only -inf
+    blocks; two blocks past the keys."""
+    g = torch.Generator().manual_seed(100 + bs)
+    B, C, Sk, lw = 2, 130, 5000, 256
+    q = torch.randn(B, C, d, generator=g).to(torch.bfloat16)
+    k = torch.randn(B, Sk, d, generator=g).to(torch.bfloat16)
+    pos = torch.randint(0, Sk, (B, C), generator=g)
+    pos[0, :64] = torch.arange(64) + 300          # a tile that ends in the first slab
+    seg = torch.randint(0, 400, (B, C), generator=g)
+    nblk = -(-Sk // bs) + 2
+    got = SG.triton_block_max_score(q.to(dev), k.to(dev), pos.to(dev), seg.to(dev), bs, nblk, lw).cpu()
+    ref = O.block_max_scores(q.double(), k.double(), pos, seg, bs, nblk, lw)
+    fin = torch.isfinite(ref)
+    assert torch.equal(torch.isfinite(got), fin)
+    assert (got.double()[fin] - ref[fin]).abs().max().item() <= 1e-3 * max(1.0, ref[fin].abs().max().item())

@@ -6,10 +6,17 @@
 // (HF/_sparse_base_impl.py:3076-3094):
 //   out[b, c, blk] = max over keys j of blk with seg[b,c] <= j < max(pos[b,c]-LW+1, 0)
 //                    of q[b,c] . k[b,j]      (unscaled, fp32 accumulation; -inf if none)
-// One workgroup = (sequence, 64 query rows); two waves of 32 rows, each lane
-// owning one row.  Keys stream in 64-key chunks through LDS, S^T = K Q^T on
-// v_mfma_f32_32x32x16; chunks past the tile's last remote key are skipped and
-// their blocks written as -inf.  No dense [B, C, Sk] score tensor exists.
+// One workgroup = (sequence, 64 query rows, slab of keys); two waves of 32
+// rows, each lane owning one row.  The blocks are independent, so the keys are
+// cut into slabs of whole blocks (>= 16 chunks of 64 keys) spread over the
+// grid, and every workgroup writes exactly its slab's blocks.  Keys stream in
+// 64-key chunks through LDS (the next chunk prefetched into registers), S^T =
+// K Q^T on v_mfma_f32_32x32x16; a chunk every row of the wave scores whole
+// skips the per-key masking; chunks past the tile's last remote key are
+// skipped and their blocks written as -inf.  No dense [B, C, Sk] score tensor
+// exists.
+#include <algorithm>
+
 #include "mfma_common.h"
 
 namespace srswa {
@@ -18,6 +25,7 @@ namespace {
 struct BmaxK {
   srswa_blockmax_args a;
   int ntiles;
+  int nslab, slab_chunks;   // key slabs per (sequence, tile); chunks per slab (whole blocks)
 };
 
 template <typename T, int D>
@@ -30,8 +38,10 @@ __global__ __launch_bounds__(128) void block_max_kernel(BmaxK p) {
   const srswa_blockmax_args& a = p.a;
   const int tid = threadIdx.x, wave = tid / kWave, lane = tid % kWave;
   const int h = lane / 32, rl = lane % 32;
-  const int tile = blockIdx.x % p.ntiles;
-  const int b = blockIdx.x / p.ntiles;
+  const int slab = blockIdx.x % p.nslab;
+  const int bt = blockIdx.x / p.nslab;
+  const int tile = bt % p.ntiles;
+  const int b = bt / p.ntiles;
   const int row = tile * 64 + wave * 32 + rl;
   const bool row_ok = row < a.C;
   const int BS = a.block_size;
@@ -48,6 +58,11 @@ __global__ __launch_bounds__(128) void block_max_kernel(BmaxK p) {
   __syncthreads();
   const int kend = s_maxls;                       // no row has a remote key >= kend
   const int nchunks = ceil_div(kend, kChunk);
+  // this slab: chunks [c_lo, c_hi) visited, blocks [blk_lo, blk_hi) written
+  const int c_lo = slab * p.slab_chunks;
+  const int c_hi = min(c_lo + p.slab_chunks, nchunks);
+  const int blk_lo = c_lo * kChunk / BS;
+  const int blk_hi = slab == p.nslab - 1 ? a.nblk : min(a.nblk, (c_lo + p.slab_chunks) * kChunk / BS);
 
   uint4 qf[KS];
   {
@@ -58,37 +73,55 @@ __global__ __launch_bounds__(128) void block_max_kernel(BmaxK p) {
   }
   float* orow = a.out + (int64_t)b * a.o_sb + (int64_t)(row_ok ? row : 0) * a.o_sc;
   const T* kg = reinterpret_cast<const T*>(a.k) + (int64_t)b * a.k_sb;
-  constexpr int PIECES = kChunk * D / 8;
+  constexpr int PIECES = kChunk * D / 8;          // 16-byte pieces of a chunk
+  constexpr int PPT = PIECES / 128;               // per thread
   float run = -INFINITY;                          // running max of the open block (BS >= 64)
+  uint4 pre[PPT];
+  auto fetch = [&](int c) {
+#pragma unroll
+    for (int i = 0; i < PPT; ++i) {
+      const int pc = tid + 128 * i;
+      const int j = c * kChunk + pc / (D / 8), col = pc % (D / 8);
+      pre[i] = j < a.Sk ? *reinterpret_cast<const uint4*>(kg + (int64_t)j * a.k_sk + col * 8)
+                        : make_uint4(0, 0, 0, 0);
+    }
+  };
 
-  for (int c = 0; c < nchunks; ++c) {
+  if (c_lo < c_hi) fetch(c_lo);
+  for (int c = c_lo; c < c_hi; ++c) {
     const int j0 = c * kChunk;
-    __syncthreads();
-    for (int pc = tid; pc < PIECES; pc += blockDim.x) {
-      const int key = pc / (D / 8), col = pc % (D / 8);
-      const int j = j0 + key;
-      const uint4 w = j < a.Sk ? *reinterpret_cast<const uint4*>(kg + (int64_t)j * a.k_sk + col * 8)
-                               : make_uint4(0, 0, 0, 0);
-      *reinterpret_cast<uint4*>(sK + key * KP + col * 8) = w;
+    __syncthreads();   // the previous chunk is consumed
+#pragma unroll
+    for (int i = 0; i < PPT; ++i) {
+      const int pc = tid + 128 * i;
+      *reinterpret_cast<uint4*>(sK + (pc / (D / 8)) * KP + (pc % (D / 8)) * 8) = pre[i];
     }
     __syncthreads();
+    if (c + 1 < c_hi) fetch(c + 1);
     f32x16_t s0 = zero16(), s1 = zero16();
 #pragma unroll
     for (int ks = 0; ks < KS; ++ks) {
       s0 = M::mac(*reinterpret_cast<const uint4*>(sK + rl * KP + 16 * ks + 8 * h), qf[ks], s0);
       s1 = M::mac(*reinterpret_cast<const uint4*>(sK + (32 + rl) * KP + 16 * ks + 8 * h), qf[ks], s1);
     }
+    // every row of the wave scores the whole chunk: no per-key masks
+    const bool whole = __all(!row_ok || (j0 >= seg && j0 + kChunk <= ls));
     if (BS >= kChunk) {
       float mx = -INFINITY;
+      if (whole) {
 #pragma unroll
-      for (int r = 0; r < 16; ++r)
+        for (int r = 0; r < 16; ++r) mx = fmaxf(mx, fmaxf(s0[r], s1[r]));
+      } else {
 #pragma unroll
-        for (int half = 0; half < 2; ++half) {
-          const int j = j0 + 32 * half + d_row(r, h);
-          if (j >= seg && j < ls) mx = fmaxf(mx, half ? s1[r] : s0[r]);
-        }
+        for (int r = 0; r < 16; ++r)
+#pragma unroll
+          for (int half = 0; half < 2; ++half) {
+            const int j = j0 + 32 * half + d_row(r, h);
+            if (j >= seg && j < ls) mx = fmaxf(mx, half ? s1[r] : s0[r]);
+          }
+      }
       run = fmaxf(run, mx);
-      const bool closes = ((j0 + kChunk) % BS == 0) || (c == nchunks - 1);
+      const bool closes = ((j0 + kChunk) % BS == 0) || (c == c_hi - 1);
       if (closes) {
         run = fmaxf(run, __shfl_xor(run, 32, kWave));
         const int blk = j0 / BS;
@@ -114,16 +147,17 @@ __global__ __launch_bounds__(128) void block_max_kernel(BmaxK p) {
       }
     }
   }
-  // blocks after the last visited chunk hold no remote key of any row
+  // the slab's blocks after the last visited chunk hold no remote key of any row
   if (row_ok && h == 0) {
-    const int first = nchunks * kChunk / BS + ((nchunks * kChunk) % BS ? 1 : 0);
-    for (int blk = first; blk < a.nblk; ++blk) orow[(int64_t)blk * a.o_sn] = -INFINITY;
+    const int first = c_hi > c_lo ? c_hi * kChunk / BS + ((c_hi * kChunk) % BS ? 1 : 0) : blk_lo;
+    for (int blk = max(first, blk_lo); blk < blk_hi; ++blk) orow[(int64_t)blk * a.o_sn] = -INFINITY;
   }
 }
 
 template <typename T, int D>
 int launch_bmax(const BmaxK& k, hipStream_t st) {
-  hipLaunchKernelGGL((block_max_kernel<T, D>), dim3((unsigned)((int64_t)k.a.B * k.ntiles)), dim3(128), 0, st, k);
+  hipLaunchKernelGGL((block_max_kernel<T, D>), dim3((unsigned)((int64_t)k.a.B * k.ntiles * k.nslab)), dim3(128), 0, st,
+                     k);
   const hipError_t e = hipGetLastError();
   if (e != hipSuccess) {
     set_error("block max launch failed: %s", hipGetErrorString(e));
@@ -168,6 +202,14 @@ extern "C" int srswa_block_max_score(const srswa_blockmax_args* a, void* stream)
   BmaxK k{};
   k.a = *a;
   k.ntiles = ceil_div(a->C, 64);
+  // slabs of whole blocks, at least 16 chunks (1024 keys) each
+  const int cpb = BS >= kChunk ? BS / kChunk : 1;          // chunks per block
+  k.slab_chunks = cpb * ceil_div(16, cpb);
+  k.nslab = std::max(1, ceil_div(ceil_div(a->Sk, kChunk), k.slab_chunks));
+  if ((int64_t)a->B * k.ntiles * k.nslab > 0x7fffffff) {
+    set_error("block max: grid too large");
+    return SRSWA_UNSUPPORTED;
+  }
   hipStream_t s = reinterpret_cast<hipStream_t>(stream);
   if (a->dtype == SRSWA_BF16) return a->D == 128 ? launch_bmax<bf16_t, 128>(k, s) : launch_bmax<bf16_t, 64>(k, s);
   return a->D == 128 ? launch_bmax<__half, 128>(k, s) : launch_bmax<__half, 64>(k, s);
