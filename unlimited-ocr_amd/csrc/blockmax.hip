@@ -6,8 +6,9 @@
 // (HF/_sparse_base_impl.py:3076-3094):
 //   out[b, c, blk] = max over keys j of blk with seg[b,c] <= j < max(pos[b,c]-LW+1, 0)
 //                    of q[b,c] . k[b,j]      (unscaled, fp32 accumulation; -inf if none)
-// One workgroup = (sequence, 64 query rows, slab of keys); two waves of 32
-// rows, each lane owning one row.  The blocks are independent, so the keys are
+// One workgroup = (sequence, kBmaxRows = 256 query rows, slab of keys); eight
+// waves of 32 rows (two per SIMD) share every staged chunk, each lane owning
+// one row.  The blocks are independent, so the keys are
 // cut into slabs of whole blocks (>= 16 chunks of 64 keys) spread over the
 // grid, and every workgroup writes exactly its slab's blocks.  Keys stream in
 // 64-key chunks through LDS (the next chunk prefetched into registers), S^T =
@@ -22,6 +23,9 @@
 namespace srswa {
 namespace {
 
+constexpr int kBmaxRows = 256;              // query rows per workgroup (8 waves)
+constexpr int kBmaxThreads = 2 * kBmaxRows;
+
 struct BmaxK {
   srswa_blockmax_args a;
   int ntiles;
@@ -29,7 +33,7 @@ struct BmaxK {
 };
 
 template <typename T, int D>
-__global__ __launch_bounds__(128) void block_max_kernel(BmaxK p) {
+__global__ __launch_bounds__(kBmaxThreads) void block_max_kernel(BmaxK p) {
   using M = Mfma<T>;
   constexpr int KP = D + 8;
   constexpr int KS = D / 16;
@@ -42,7 +46,7 @@ __global__ __launch_bounds__(128) void block_max_kernel(BmaxK p) {
   const int bt = blockIdx.x / p.nslab;
   const int tile = bt % p.ntiles;
   const int b = bt / p.ntiles;
-  const int row = tile * 64 + wave * 32 + rl;
+  const int row = tile * kBmaxRows + wave * 32 + rl;
   const bool row_ok = row < a.C;
   const int BS = a.block_size;
 
@@ -74,13 +78,13 @@ __global__ __launch_bounds__(128) void block_max_kernel(BmaxK p) {
   float* orow = a.out + (int64_t)b * a.o_sb + (int64_t)(row_ok ? row : 0) * a.o_sc;
   const T* kg = reinterpret_cast<const T*>(a.k) + (int64_t)b * a.k_sb;
   constexpr int PIECES = kChunk * D / 8;          // 16-byte pieces of a chunk
-  constexpr int PPT = PIECES / 128;               // per thread
+  constexpr int PPT = PIECES / kBmaxThreads;      // per thread
   float run = -INFINITY;                          // running max of the open block (BS >= 64)
   uint4 pre[PPT];
   auto fetch = [&](int c) {
 #pragma unroll
     for (int i = 0; i < PPT; ++i) {
-      const int pc = tid + 128 * i;
+      const int pc = tid + kBmaxThreads * i;
       const int j = c * kChunk + pc / (D / 8), col = pc % (D / 8);
       pre[i] = j < a.Sk ? *reinterpret_cast<const uint4*>(kg + (int64_t)j * a.k_sk + col * 8)
                         : make_uint4(0, 0, 0, 0);
@@ -93,7 +97,7 @@ __global__ __launch_bounds__(128) void block_max_kernel(BmaxK p) {
     __syncthreads();   // the previous chunk is consumed
 #pragma unroll
     for (int i = 0; i < PPT; ++i) {
-      const int pc = tid + 128 * i;
+      const int pc = tid + kBmaxThreads * i;
       *reinterpret_cast<uint4*>(sK + (pc / (D / 8)) * KP + (pc % (D / 8)) * 8) = pre[i];
     }
     __syncthreads();
@@ -156,7 +160,7 @@ __global__ __launch_bounds__(128) void block_max_kernel(BmaxK p) {
 
 template <typename T, int D>
 int launch_bmax(const BmaxK& k, hipStream_t st) {
-  hipLaunchKernelGGL((block_max_kernel<T, D>), dim3((unsigned)((int64_t)k.a.B * k.ntiles * k.nslab)), dim3(128), 0, st,
+  hipLaunchKernelGGL((block_max_kernel<T, D>), dim3((unsigned)((int64_t)k.a.B * k.ntiles * k.nslab)), dim3(kBmaxThreads), 0, st,
                      k);
   const hipError_t e = hipGetLastError();
   if (e != hipSuccess) {
@@ -201,7 +205,7 @@ extern "C" int srswa_block_max_score(const srswa_blockmax_args* a, void* stream)
   }
   BmaxK k{};
   k.a = *a;
-  k.ntiles = ceil_div(a->C, 64);
+  k.ntiles = ceil_div(a->C, kBmaxRows);
   // slabs of whole blocks, at least 16 chunks (1024 keys) each
   const int cpb = BS >= kChunk ? BS / kChunk : 1;          // chunks per block
   k.slab_chunks = cpb * ceil_div(16, cpb);
