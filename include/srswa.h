@@ -76,15 +76,11 @@ typedef struct {
   int32_t in_dtype, out_dtype;                         /* srswa_dtype               */
 } srswa_decode_args;
 
-/* Workspace query.  scratch: device bytes with no initial-content
- * requirement; counters: uint32 arrival counters that must be zero before the
- * first call and that every call leaves zero again (keep one zero-filled
- * buffer per stream and pass a prefix of it; calls that overlap on one
- * buffer race). */
-void srswa_gather_decode_workspace(const srswa_decode_args* a, size_t* scratch_bytes,
-                                   size_t* counters);
-int srswa_gather_decode(const srswa_decode_args* a, void* scratch, size_t scratch_bytes,
-                        uint32_t* counters, size_t n_counters, void* stream);
+/* Workspace query: device scratch bytes (no initial-content requirement)
+ * for the split-K (O, M, L) records of each (row, head); 0 when a row needs
+ * no split.  Calls that overlap on one scratch buffer race. */
+size_t srswa_gather_decode_workspace(const srswa_decode_args* a);
+int srswa_gather_decode(const srswa_decode_args* a, void* scratch, size_t scratch_bytes, void* stream);
 
 /* ------------------------------------------------------------------------
  * Block indexer: head_cls / mean-pool block summaries, remote block scores
@@ -240,10 +236,10 @@ typedef struct {
   int32_t in_dtype, out_dtype;
 } srswa_paged_decode_args;
 
-void srswa_gather_decode_paged_workspace(const srswa_paged_decode_args* a, size_t* scratch_bytes,
-                                         size_t* counters);
+/* scratch bytes for the split-K records, as srswa_gather_decode_workspace */
+size_t srswa_gather_decode_paged_workspace(const srswa_paged_decode_args* a);
 int srswa_gather_decode_paged(const srswa_paged_decode_args* a, void* scratch, size_t scratch_bytes,
-                              uint32_t* counters, size_t n_counters, void* stream);
+                              void* stream);
 
 /* ------------------------------------------------------------------------
  * head_cls summary cache over a paged index-key cache (the serving stage 0).

@@ -25,3 +25,16 @@ def dev():
     import torch
     assert torch.cuda.is_available(), "GPU tests need a HIP device"
     return torch.device("cuda:0")
+
+
+def pytest_terminal_summary(terminalreporter):
+    """Repeat the parity figures (near-tie counts, plain max-abs errors) the
+    tests reported, so they are visible in a quiet run's log."""
+    try:
+        from parity_report import LINES
+    except ImportError:
+        return
+    if LINES:
+        terminalreporter.section("parity figures")
+        for line in LINES:
+            terminalreporter.write_line(line)

@@ -86,7 +86,7 @@ def test_bwd_matches_oracle(dev, name):
     ref = _ref(q, k, v, do, bi, pos, bsl, bs, lw, scale)
     dt = c.get("dtype", torch.bfloat16)
     for nm, gt, rf in zip(("dq", "dk", "dv", "dbias"), got, ref):
-        assert_close_lowp(gt, rf, dt if nm != "dbias" else torch.float32, TOL, nm)
+        assert_close_lowp(gt, rf, dt if nm != "dbias" else torch.float32, TOL, f"backward {name}: {nm}")
 
 
 def test_bwd_is_deterministic(dev):
@@ -97,3 +97,40 @@ def test_bwd_is_deterministic(dev):
     b = _gpu(dev, q, k, v, do, bi, pos, bsl, bs, lw, 0.1)
     for x, y in zip(a, b):
         assert torch.equal(x, y)
+
+
+@pytest.mark.parametrize("bias_dims", [3, 4])
+def test_bias_shared_by_two_index_heads(dev, bias_dims):
+    """A per-slot bias that does not name the index head ([B, T, S], or
+    [B, 1, T, S]) feeds slot s of EVERY index head; its gradient is the sum over
+    the index heads.  Reference: one fp64 oracle per index head (its own blocks,
+    the same slot biases), the gradients accumulated by autograd."""
+    g = torch.Generator().manual_seed(41 + bias_dims)
+    B, HQ, HI, T, D, bs, lw, S = 1, 4, 2, 256, 128, 32, 64, 4
+    q = torch.randn(B, T, HQ, D, generator=g).to(torch.bfloat16)
+    k = torch.randn(B, T, HQ, D, generator=g).to(torch.bfloat16)
+    v = torch.randn(B, T, HQ, D, generator=g).to(torch.bfloat16)
+    do = torch.randn(B, T, HQ, D, generator=g).to(torch.bfloat16)
+    nblk = T // bs
+    bi = torch.randint(-1, nblk, (B, HI, T, S), generator=g)
+    bsl = torch.randn(B, T, S, generator=g)
+    if bias_dims == 4:
+        bsl = bsl[:, None]
+    pos = torch.arange(T)[None]
+    scale = 1 / math.sqrt(D)
+    got = _gpu(dev, q, k, v, do, bi, pos, bsl, bs, lw, scale)
+    assert got[3].shape == bsl.shape
+    qd, kd, vd = (x.double().transpose(1, 2).requires_grad_() for x in (q, k, v))
+    bd = bsl.double().requires_grad_()
+    b3 = bd if bias_dims == 3 else bd[:, 0]
+    gh = HQ // HI
+    for h in range(HI):
+        hs = slice(h * gh, (h + 1) * gh)
+        dense = O.bias_slots_to_dense(b3, bi[:, h], nblk)
+        o, _ = O.gather_attention(qd[:, hs], kd[:, hs], vd[:, hs], bi[:, h:h + 1], pos, bs, scale, lw,
+                                  blk_bias_dense=dense)
+        (o * do.double().transpose(1, 2)[:, hs]).sum().backward()
+    ref = [x.grad.transpose(1, 2) for x in (qd, kd, vd)] + [bd.grad]
+    for nm, gt, rf in zip(("dq", "dk", "dv", "dbias"), got, ref):
+        assert_close_lowp(gt, rf, torch.bfloat16 if nm != "dbias" else torch.float32, TOL,
+                          f"{nm}, [{'B, T, S' if bias_dims == 3 else 'B, 1, T, S'}] bias over HI=2")

@@ -8,6 +8,8 @@ import pytest
 import torch
 
 from oracle import srswa_oracle as O
+from parity_report import compare_selection, report
+import srswa
 from srswa import sparse_gather_e2e_triton as E2E
 from srswa import sparse_gather_triton as SG
 
@@ -64,6 +66,22 @@ def test_gather_attention_e2e_bias_grad(dev):
     assert E2E.SPARSE_E2E_SENTINEL == 1
 
 
+def _check_block_max(got, q, k, pos, seg, bs, nblk, lw, what):
+    """got [B, C, nblk] against the fp64 oracle: the same -inf pattern, and
+    |got - ref| <= 1e-5 * max over the block's scored keys of sum_i |q_i k_i|
+    (a correct fp32 sum of the exact bf16 products stays within
+    128 * 2^-24 = 7.6e-6 of that sum; a bf16-rounded accumulator would not)."""
+    ref = O.block_max_scores(q.double(), k.double(), pos, seg, bs, nblk, lw)
+    bound = O.block_max_scores(q.double().abs(), k.double().abs(), pos, seg, bs, nblk, lw)
+    fin = torch.isfinite(ref)
+    assert torch.equal(torch.isfinite(got), fin), what
+    err = (got.double()[fin] - ref[fin]).abs()
+    rel = (err / bound[fin].clamp(min=1e-30)).max().item() if fin.any() else 0.0
+    report(f"[err] {what}: max-abs {err.max().item() if fin.any() else 0.0:.3e}, "
+           f"max |err| / sum|q k| {rel:.3e} (bar 1e-5)")
+    assert rel <= 1e-5, (what, rel)
+
+
 @pytest.mark.parametrize("bs", [16, 32, 64, 128])
 def test_block_max_score(dev, bs):
     g = torch.Generator().manual_seed(bs)
@@ -74,10 +92,55 @@ def test_block_max_score(dev, bs):
     seg = torch.randint(0, 50, (B, C), generator=g)
     nblk = -(-Sk // bs) + 1
     got = SG.triton_block_max_score(q.to(dev), k.to(dev), pos.to(dev), seg.to(dev), bs, nblk, lw).cpu()
-    ref = O.block_max_scores(q.double(), k.double(), pos, seg, bs, nblk, lw)
-    fin = torch.isfinite(ref)
-    assert torch.equal(torch.isfinite(got), fin)
-    assert (got.double()[fin] - ref[fin]).abs().max().item() <= 1e-3 * max(1.0, ref[fin].abs().max().item())
+    _check_block_max(got, q, k, pos, seg, bs, nblk, lw, f"block max bs={bs}")
+
+
+@pytest.mark.parametrize("bs", [32, 64])
+def test_block_max_score_positions_past_the_keys(dev, bs):
+    """Rows whose window starts past the last key (pos - LW + 1 > Sk, Sk not a
+    multiple of 64): keys >= Sk are never scored (the reference's j < Sk mask,
+    HF/sparse_gather_triton.py:471,478), so the partial last block's max comes
+    from its real keys only and the blocks past Sk are -inf."""
+    g = torch.Generator().manual_seed(300 + bs)
+    B, C, Sk, D, lw = 2, 130, 700, 128, 64
+    q = torch.randn(B, C, D, generator=g).to(torch.bfloat16)
+    k = torch.randn(B, Sk, D, generator=g).to(torch.bfloat16)
+    pos = torch.randint(600, 1000, (B, C), generator=g)
+    seg = torch.zeros(B, C, dtype=torch.long)
+    seg[1] = torch.randint(0, 690, (C,), generator=g)
+    nblk = -(-Sk // bs) + 2
+    got = SG.triton_block_max_score(q.to(dev), k.to(dev), pos.to(dev), seg.to(dev), bs, nblk, lw).cpu()
+    _check_block_max(got, q, k, pos, seg, bs, nblk, lw, f"block max past the keys bs={bs}")
+    # the partial last block holds 700 % bs real keys, all remote for rows with pos >= Sk + lw - 1
+    last = (Sk - 1) // bs
+    far = pos >= Sk + lw - 1
+    assert torch.isfinite(got[..., last][far & (seg <= last * bs)]).all()
+    assert torch.isinf(got[..., last + 1:]).all()
+
+
+def test_block_max_topk_ids_cfg4_chunk(dev):
+    """Config 4's chunk through the path select_and_kl_loss takes
+    (HF/_sparse_base_impl.py:3322-3403): block-max scores of B=4 x 2048 rows at
+    the tail of 65536 keys (one index head, bf16) -> top-8 per row, -inf never
+    selected.  Sampled rows (tile edges, first / last, random) against the fp64
+    oracle: scores within 1e-5 of sum |q k|, ids bit-exact outside near-ties."""
+    g = torch.Generator().manual_seed(20261204)
+    B, C, Sk, D, bs, lw, K = 4, 2048, 65536, 128, 64, 512, 8
+    q = torch.randn(B, C, D, generator=g).to(torch.bfloat16)
+    k = torch.randn(B, Sk, D, generator=g).to(torch.bfloat16)
+    pos = (torch.arange(C) + (Sk - C)).expand(B, C).contiguous()
+    seg = torch.zeros(B, C, dtype=torch.long)
+    nblk = Sk // bs
+    sc = SG.triton_block_max_score(q.to(dev), k.to(dev), pos.to(dev), seg.to(dev), bs, nblk, lw)
+    ids = srswa.topk_rows(sc, K, invalid_at=float("-inf")).cpu()
+    rows = sorted({0, 1, 63, 64, 1023, 1024, C - 65, C - 64, C - 1}
+                  | set(torch.randint(0, C, (23,), generator=g).tolist()))
+    r = torch.tensor(rows)
+    got = sc.cpu()[:, r]
+    _check_block_max(got, q[:, r], k, pos[:, r], seg[:, r], bs, nblk, lw, "config 4 chunk block max (sampled rows)")
+    ref = O.block_max_scores(q[:, r].double(), k.double(), pos[:, r], seg[:, r], bs, nblk, lw)
+    compare_selection(ids[:, r], ref, K, "config 4 chunk block max -> top-8 (sampled rows)",
+                      invalid_at=float("-inf"))
 
 
 @pytest.mark.parametrize("bs,d", [(16, 128), (64, 128), (192, 64)])
@@ -95,7 +158,4 @@ def test_block_max_score_key_slabs(dev, bs, d):
     seg = torch.randint(0, 400, (B, C), generator=g)
     nblk = -(-Sk // bs) + 2
     got = SG.triton_block_max_score(q.to(dev), k.to(dev), pos.to(dev), seg.to(dev), bs, nblk, lw).cpu()
-    ref = O.block_max_scores(q.double(), k.double(), pos, seg, bs, nblk, lw)
-    fin = torch.isfinite(ref)
-    assert torch.equal(torch.isfinite(got), fin)
-    assert (got.double()[fin] - ref[fin]).abs().max().item() <= 1e-3 * max(1.0, ref[fin].abs().max().item())
+    _check_block_max(got, q, k, pos, seg, bs, nblk, lw, f"block max key slabs bs={bs} d={d}")

@@ -72,5 +72,5 @@ def test_fwd_matches_oracle(dev, name):
     q, k, v, bi, pos, bias = _case(1 + list(CASES).index(name), **c)
     scale = 1 / math.sqrt(c["D"])
     o, lse, ro, rl = _run(dev, q, k, v, bi, pos, bias, bs, lw, scale)
-    assert_close_lowp(o, ro, c.get("dtype", torch.bfloat16), TOL, "o")
+    assert_close_lowp(o, ro, c.get("dtype", torch.bfloat16), TOL, f"forward {name}: o")
     assert (lse - rl).abs().max().item() <= TOL

@@ -389,6 +389,91 @@ def test_entmax15_matches_bisection():
     assert (O.entmax15(torch.zeros(1, 4)) - 0.25).abs().max() < 1e-12
 
 
+def _route_row(scores, cand_mask, idx_scale, floor, sigma, K, topm, window_all=False):
+    """Pure-Python restatement of one row of ``_infer_route_select``
+    (HF/modeling_deepseekv2.py:338-362): candidates (remote, intersected with
+    the page mask unless that leaves none), x = score * idx_scale (sentinel for
+    the rest and for NaN / inf), the top-M by (-x, id), 1.5-entmax of those M
+    by bisection, the first K, log(max(prior, floor)) centred over the valid
+    slots and divided by sigma.  ``window_all`` is a planted mistake (entmax
+    over every block instead of the top-M window) used to show the cases below
+    tell the two apart."""
+    n = len(scores)
+    remote = [s > O.SCORE_NEG * 0.5 for s in scores]          # NaN compares False
+    cand = remote if cand_mask is None else [r and c for r, c in zip(remote, cand_mask)]
+    if not any(cand):
+        cand = remote
+    x = []
+    for i in range(n):
+        v = scores[i] * idx_scale if cand[i] else O.ENTMAX_NEG
+        x.append(v if math.isfinite(v) else O.ENTMAX_NEG)
+    M = max(1, min(topm, n)) if topm > 0 else n
+    order = sorted(range(n), key=lambda i: (-x[i], i))
+    if window_all:
+        full = _entmax_bisect(x)
+        prior = [full[i] for i in order[:M]]
+    else:
+        prior = _entmax_bisect([x[i] for i in order[:M]])
+    Kc = max(1, min(K, M))
+    ids, prior = order[:Kc], prior[:Kc]
+    valid = [cand[i] for i in ids]
+    logp = [math.log(max(p, floor)) for p in prior]
+    mu = sum(lp for lp, v in zip(logp, valid) if v) / max(1, sum(valid))
+    bias = [(lp - mu) / sigma if v else 0.0 for lp, v in zip(logp, valid)]
+    return ids, bias, valid
+
+
+def _route_cases():
+    g = torch.Generator().manual_seed(18)
+    n = 40
+    base = _rand(6, n, g=g)
+    base[:, 30:] = O.SCORE_NEG                                 # blocks 30.. are not remote
+    cases = []
+    # narrow spread (broad entmax support, wider than the top-M window), sigma != 1
+    cases.append(("narrow spread, M < candidates, sigma 0.7", base.clone(), None,
+                  dict(idx_scale=0.3, floor=1e-4, sigma=0.7, K=6, topm=8)))
+    # wide spread and a large floor: the floor binds on most slots
+    cases.append(("binding floor", base.clone(), None, dict(idx_scale=4.0, floor=0.05, sigma=1.3, K=8, topm=16)))
+    # page mask: row 0 no candidate left (remote fallback), row 1 fewer candidates than K
+    cm = torch.rand(6, n, generator=g) < 0.5
+    cm[0] = False
+    cm[1] = False
+    cm[1, :3] = True
+    cases.append(("page mask, fallback, fewer candidates than K", base.clone(), cm,
+                  dict(idx_scale=1.0, floor=1e-4, sigma=1.0, K=6, topm=16)))
+    # topm = 0 (window = every block) and K > M
+    small = base[:, :20].clone()
+    cases.append(("topm 0, K > M", small, None, dict(idx_scale=0.5, floor=1e-5, sigma=2.0, K=50, topm=0)))
+    # NaN / +inf / -inf scores, exact ties, a row with no remote block
+    odd = torch.randint(-3, 4, (6, n), generator=g).double()
+    odd[0, 5] = float("nan")
+    odd[0, 6] = float("inf")
+    odd[0, 7] = float("-inf")
+    odd[1] = O.SCORE_NEG
+    cases.append(("NaN, inf, ties, no remote row", odd, None, dict(idx_scale=0.7, floor=1e-4, sigma=1.0, K=5,
+                                                                  topm=12)))
+    return cases
+
+
+@pytest.mark.parametrize("case", range(5))
+def test_route_select_matches_pure_python(case):
+    what, sc, cm, p = _route_cases()[case]
+    xi, bias, valid = O.infer_route_select(sc, cm, p["idx_scale"], p["floor"], p["sigma"], p["K"], p["topm"])
+    differs = False
+    for r in range(sc.shape[0]):
+        row = sc[r].tolist()
+        mrow = None if cm is None else cm[r].tolist()
+        ids, b, v = _route_row(row, mrow, **p)
+        assert xi[r].tolist() == ids, (what, r)
+        assert valid[r].tolist() == v, (what, r)
+        assert max(abs(a - c) / max(1.0, abs(c)) for a, c in zip(bias[r].tolist(), b)) < 1e-6, (what, r)
+        _, bm, _ = _route_row(row, mrow, **p, window_all=True)
+        differs |= max(abs(a - c) for a, c in zip(bm, b)) > 1e-3
+    if case == 0:
+        # the planted mistake (entmax over every block) is visible in this case
+        assert differs
+
+
 def test_route_select_bias_is_mean_centred():
     g = torch.Generator().manual_seed(17)
     sc = _rand(2, 3, 20, g=g) * 4

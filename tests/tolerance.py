@@ -18,8 +18,15 @@ def half_ulp(ref: torch.Tensor, dtype: torch.dtype) -> torch.Tensor:
 
 
 def assert_close_lowp(got, ref, dtype, tol=2e-2, what=""):
+    """Assert the bar above and report the plain max-abs error beside the
+    error left after removing the output format's own rounding."""
+    from parity_report import report
+
     got = got.double()
     ref = ref.double()
+    plain = (got - ref).abs().max().item() if got.numel() else 0.0
     excess = (got - ref).abs() - half_ulp(ref, dtype)
-    worst = excess.max().item()
-    assert worst <= tol, f"{what}: max |err| - ulp/2 = {worst:.4g} > {tol} (max |err| {(got - ref).abs().max().item():.4g})"
+    worst = excess.max().item() if got.numel() else 0.0
+    if what:
+        report(f"[err] {what}: max-abs {plain:.3e}, beyond ulp/2 {worst:.3e} (bar {tol})")
+    assert worst <= tol, f"{what}: max |err| - ulp/2 = {worst:.4g} > {tol} (max |err| {plain:.4g})"

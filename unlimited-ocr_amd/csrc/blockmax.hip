@@ -4,7 +4,7 @@
 // HF/sparse_gather_triton.py:445-524), the fused form of the eager
 // "token_future | local_token" masked block amax of DeepseekV2Indexer.forward
 // (HF/_sparse_base_impl.py:3076-3094):
-//   out[b, c, blk] = max over keys j of blk with seg[b,c] <= j < max(pos[b,c]-LW+1, 0)
+//   out[b, c, blk] = max over keys j of blk with seg[b,c] <= j < min(max(pos[b,c]-LW+1, 0), Sk)
 //                    of q[b,c] . k[b,j]      (unscaled, fp32 accumulation; -inf if none)
 // One workgroup = (sequence, kBmaxRows = 256 query rows, slab of keys); eight
 // waves of 32 rows (two per SIMD) share every staged chunk, each lane owning
@@ -54,11 +54,12 @@ __global__ __launch_bounds__(kBmaxThreads) void block_max_kernel(BmaxK p) {
   if (row_ok) {
     const int pos = a.pos[(int64_t)b * a.pos_sb + (int64_t)row * a.pos_sc];
     seg = a.seg ? a.seg[(int64_t)b * a.seg_sb + (int64_t)row * a.seg_sc] : 0;
-    ls = max(pos - (a.local_window - 1), 0);
+    // remote keys end at the local window's start and at the last key (j < Sk)
+    ls = min(max(pos - (a.local_window - 1), 0), a.Sk);
   }
   if (tid == 0) s_maxls = 0;
   __syncthreads();
-  if (row_ok) atomicMax(&s_maxls, min(ls, a.Sk));
+  if (row_ok) atomicMax(&s_maxls, ls);
   __syncthreads();
   const int kend = s_maxls;                       // no row has a remote key >= kend
   const int nchunks = ceil_div(kend, kChunk);

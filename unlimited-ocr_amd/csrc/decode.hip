@@ -21,9 +21,7 @@
 //     broadcast back through 256 bytes of LDS per wave, then o += p v;
 // Four waves (one workgroup) merge their (m, l, o) in LDS; the workgroups of
 // one (row, head) write (O, M, L) records to a scratch buffer, and a second
-// small kernel combines them (decode_merge_kernel).  The in-kernel form, where
-// the last workgroup to arrive (atomic counter, left zeroed for the next
-// call) combines them, is kept behind SRSWA_DECODE_MERGE=atomic.
+// small kernel combines them (decode_merge_kernel).
 #include <stdarg.h>
 #include <stdio.h>
 #include <stdlib.h>
@@ -64,7 +62,6 @@ struct DecodeK {
   float scale_l2;      // scale * log2(e)
   int64_t rowheads;
   float* part;
-  uint32_t* cnt;
   // paged cache (PAGED kernels): key j of sequence b lives in page
   // bt[b * bt_sb + j / block_size] at row j % block_size; q positions come
   // from kv_len: q_pos = kv_len[b] - Lq + lq
@@ -152,7 +149,7 @@ __device__ __forceinline__ uint4 load_stream(const void* p) {
   return make_uint4(v.x, v.y, v.z, v.w);
 }
 
-template <typename T, typename TO, int D, int NI, bool ATOMIC_MERGE, bool PAGED>
+template <typename T, typename TO, int D, int NI, bool PAGED>
 __global__ __launch_bounds__(kDecodeWaves * kWave) void decode_kernel(DecodeK p) {
   using V = Vec16<T>;
   constexpr int EPV = V::N;           // elements per 16-byte vector
@@ -418,68 +415,9 @@ __global__ __launch_bounds__(kDecodeWaves * kWave) void decode_kernel(DecodeK p)
   if (p.nsplit > 1) {
     // record: O[0..D) then M, L; records are 128-byte aligned
     float* rec = p.part + (rh * p.nsplit + split) * p.pstride;
-    if constexpr (!ATOMIC_MERGE) {
-      if (r == 0) store_out<float>(rec + c * EPV, O, EPV);
-      if (lane == 0) { rec[D] = M; rec[D + 1] = L; }
-      return;   // decode_merge_kernel combines the records
-    } else {
-      // The last workgroup of the row to arrive combines the records.  Every
-      // access to the records and the counter is an agent-scope atomic: the
-      // stores are written through to the device's coherence point and the
-      // loads read from it (no per-XCD L2 copy), so neither side needs the
-      // L2-wide write-back / invalidate of a device-scope fence.  The explicit
-      // wait completes this wave's record stores before its counter update;
-      // the reader's loads are issued only after its counter update returned.
-      if (r == 0) {
-#pragma unroll
-        for (int e = 0; e < EPV; ++e)
-          __hip_atomic_store(rec + c * EPV + e, O[e], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-      }
-      if (lane == 0) {
-        __hip_atomic_store(rec + D, M, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        __hip_atomic_store(rec + D + 1, L, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-      }
-      __builtin_amdgcn_s_waitcnt(0);
-      uint32_t arrived = 0;
-      if (lane == 0) arrived = __hip_atomic_fetch_add(p.cnt + rh, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-      arrived = __shfl(arrived, 0, kWave);
-      if (arrived != (uint32_t)(p.nsplit - 1)) return;
-      if (lane == 0) __hip_atomic_store(p.cnt + rh, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-      const float* recs = p.part + rh * p.nsplit * p.pstride;
-      auto ld = [](const float* q) { return __hip_atomic_load(q, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT); };
-      M = -INFINITY;
-      L = 0.f;
-#pragma unroll
-      for (int e = 0; e < EPV; ++e) O[e] = 0.f;
-      for (int s0 = 0; s0 < p.nsplit; s0 += 8) {
-        // every load of up to 8 records in flight before they are combined
-        float ms[8], ls[8], os[8][EPV];
-#pragma unroll
-        for (int j = 0; j < 8; ++j) {
-          const bool in = s0 + j < p.nsplit;
-          const float* q = recs + (int64_t)(in ? s0 + j : s0) * p.pstride;
-          ms[j] = in ? ld(q + D) : -INFINITY;
-          ls[j] = in ? ld(q + D + 1) : 0.f;
-#pragma unroll
-          for (int e = 0; e < EPV; ++e) os[j][e] = (in && r == 0) ? ld(q + c * EPV + e) : 0.f;
-        }
-        float Mn = M;
-#pragma unroll
-        for (int j = 0; j < 8; ++j) Mn = fmaxf(Mn, ms[j]);
-        const float r0 = M == -INFINITY ? 0.f : exp2f(M - Mn);
-        L *= r0;
-#pragma unroll
-        for (int e = 0; e < EPV; ++e) O[e] *= r0;
-#pragma unroll
-        for (int j = 0; j < 8; ++j) {
-          const float wt = ms[j] == -INFINITY ? 0.f : exp2f(ms[j] - Mn);
-          L = fmaf(ls[j], wt, L);
-#pragma unroll
-          for (int e = 0; e < EPV; ++e) O[e] = fmaf(os[j][e], wt, O[e]);
-        }
-        M = Mn;
-      }
-    }
+    if (r == 0) store_out<float>(rec + c * EPV, O, EPV);
+    if (lane == 0) { rec[D] = M; rec[D + 1] = L; }
+    return;   // decode_merge_kernel combines the records
   }
 
   const float inv = L > 0.f ? 1.f / L : 0.f;
@@ -556,16 +494,10 @@ int elem_bytes(int dt) { return dt == SRSWA_F32 ? 4 : 2; }
 
 // Tuning knobs (environment, read once): SRSWA_DECODE_NI = 8 (default) | 16
 // load instructions per unit (bf16 D=128: 32 | 64 keys); SRSWA_DECODE_UPW =
-// units per wave (default 2); SRSWA_DECODE_MERGE = kernel (a second kernel
-// combines the split records, default) | atomic (the last-arriving workgroup
-// combines them, records and counter as agent-scope atomics).
+// units per wave (default 2).
 int env_int(const char* name, int dflt) {
   const char* v = getenv(name);
   return (v && *v) ? atoi(v) : dflt;
-}
-bool merge_in_kernel() {   // read per call, so a process can switch it
-  const char* m = getenv("SRSWA_DECODE_MERGE");
-  return m && strcmp(m, "atomic") == 0;
 }
 
 // row instructions per unit for (dtype, D)
@@ -599,26 +531,18 @@ DecodePlan make_plan(const srswa_decode_args* a, bool paged = false) {
 size_t scratch_bytes(const DecodePlan& pl) {
   return pl.nsplit <= 1 ? 0 : (size_t)pl.rowheads * pl.nsplit * pl.pstride * 4;
 }
-size_t counter_count(const DecodePlan& pl) { return pl.nsplit <= 1 ? 0 : (size_t)pl.rowheads; }
 
 template <typename T, typename TO, int D, int NI>
 int launch_decode_ni(const DecodeK& k, int64_t grid, hipStream_t st) {
-  if (k.bt) {
-    hipLaunchKernelGGL((decode_kernel<T, TO, D, NI, false, true>), dim3((unsigned)grid),
+  if (k.bt)
+    hipLaunchKernelGGL((decode_kernel<T, TO, D, NI, true>), dim3((unsigned)grid),
                        dim3(kDecodeWaves * kWave), 0, st, k);
-    if (k.nsplit > 1)
-      hipLaunchKernelGGL((decode_merge_kernel<TO, D>), dim3((unsigned)((k.rowheads + 3) / 4)),
-                         dim3(256), 0, st, k);
-  } else if (k.nsplit > 1 && merge_in_kernel()) {
-    hipLaunchKernelGGL((decode_kernel<T, TO, D, NI, true, false>), dim3((unsigned)grid),
+  else
+    hipLaunchKernelGGL((decode_kernel<T, TO, D, NI, false>), dim3((unsigned)grid),
                        dim3(kDecodeWaves * kWave), 0, st, k);
-  } else {
-    hipLaunchKernelGGL((decode_kernel<T, TO, D, NI, false, false>), dim3((unsigned)grid),
-                       dim3(kDecodeWaves * kWave), 0, st, k);
-    if (k.nsplit > 1)
-      hipLaunchKernelGGL((decode_merge_kernel<TO, D>), dim3((unsigned)((k.rowheads + 3) / 4)),
-                         dim3(256), 0, st, k);
-  }
+  if (k.nsplit > 1)
+    hipLaunchKernelGGL((decode_merge_kernel<TO, D>), dim3((unsigned)((k.rowheads + 3) / 4)),
+                       dim3(256), 0, st, k);
   const hipError_t e = hipGetLastError();
   if (e != hipSuccess) {
     set_error("decode launch failed: %s", hipGetErrorString(e));
@@ -667,21 +591,15 @@ using namespace srswa;
 extern "C" int srswa_version(void) { return 100; }
 extern "C" const char* srswa_last_error(void) { return srswa::last_error(); }
 
-extern "C" void srswa_gather_decode_workspace(const srswa_decode_args* a, size_t* scratch,
-                                              size_t* counters) {
-  size_t s = 0, c = 0;
-  if (a && a->B > 0 && a->Lq > 0 && a->HQ > 0 && a->D > 0 && a->block_size > 0) {
-    const DecodePlan pl = make_plan(a);
-    s = scratch_bytes(pl);
-    c = counter_count(pl);
-  }
-  if (scratch) *scratch = s;
-  if (counters) *counters = c;
+extern "C" size_t srswa_gather_decode_workspace(const srswa_decode_args* a) {
+  if (a && a->B > 0 && a->Lq > 0 && a->HQ > 0 && a->D > 0 && a->block_size > 0 && a->S >= 0 &&
+      a->local_window > 0)
+    return scratch_bytes(make_plan(a));
+  return 0;
 }
 
 extern "C" int srswa_gather_decode(const srswa_decode_args* a, void* scratch,
-                                   size_t scratch_size, uint32_t* counters, size_t n_counters,
-                                   void* stream) {
+                                   size_t scratch_size, void* stream) {
   if (!a || !a->q || !a->k || !a->v || !a->out || !a->q_pos || (!a->idx && a->S > 0)) {
     set_error("decode: null argument");
     return SRSWA_INVALID;
@@ -721,10 +639,9 @@ extern "C" int srswa_gather_decode(const srswa_decode_args* a, void* scratch,
     return SRSWA_UNSUPPORTED;
   }
   const DecodePlan pl = make_plan(a);
-  const size_t need = scratch_bytes(pl), need_cnt = counter_count(pl);
-  if (need > 0 && (!scratch || scratch_size < need || !counters || n_counters < need_cnt)) {
-    set_error("decode: scratch of %zu bytes and %zu counters required (got %zu, %zu)", need,
-              need_cnt, scratch_size, n_counters);
+  const size_t need = scratch_bytes(pl);
+  if (need > 0 && (!scratch || scratch_size < need)) {
+    set_error("decode: scratch of %zu bytes required (got %zu)", need, scratch_size);
     return SRSWA_WORKSPACE;
   }
   DecodeK k{};
@@ -740,10 +657,7 @@ extern "C" int srswa_gather_decode(const srswa_decode_args* a, void* scratch,
   k.pstride = pl.pstride;
   k.scale_l2 = a->scale * kLog2e;
   k.rowheads = pl.rowheads;
-  if (need > 0) {
-    k.cnt = counters;
-    k.part = reinterpret_cast<float*>(scratch);
-  }
+  if (need > 0) k.part = reinterpret_cast<float*>(scratch);
   const int64_t grid = pl.rowheads * pl.nsplit;
   if (grid > 0x7fffffff) {
     set_error("decode: grid too large");
@@ -782,22 +696,17 @@ srswa_decode_args paged_as_decode(const srswa_paged_decode_args* a) {
 
 }  // namespace
 
-extern "C" void srswa_gather_decode_paged_workspace(const srswa_paged_decode_args* a, size_t* scratch,
-                                                    size_t* counters) {
-  size_t s = 0, c = 0;
-  if (a && a->R > 0 && a->dql > 0 && a->HQ > 0 && a->D > 0 && a->page_size > 0) {
+extern "C" size_t srswa_gather_decode_paged_workspace(const srswa_paged_decode_args* a) {
+  if (a && a->R > 0 && a->dql > 0 && a->HQ > 0 && a->D > 0 && a->page_size > 0 && a->topk_n >= 0 &&
+      a->local_blocks >= 0) {
     const srswa_decode_args d = paged_as_decode(a);
-    const DecodePlan pl = make_plan(&d, true);
-    s = scratch_bytes(pl);
-    c = counter_count(pl);
+    return scratch_bytes(make_plan(&d, true));
   }
-  if (scratch) *scratch = s;
-  if (counters) *counters = c;
+  return 0;
 }
 
 extern "C" int srswa_gather_decode_paged(const srswa_paged_decode_args* a, void* scratch,
-                                         size_t scratch_size, uint32_t* counters, size_t n_counters,
-                                         void* stream) {
+                                         size_t scratch_size, void* stream) {
   if (!a || !a->q || !a->k_cache || !a->v_cache || !a->out || !a->block_table || !a->seq_lens ||
       (!a->topk && a->topk_n > 0)) {
     set_error("paged decode: null argument");
@@ -841,10 +750,9 @@ extern "C" int srswa_gather_decode_paged(const srswa_paged_decode_args* a, void*
   }
   const srswa_decode_args d = paged_as_decode(a);
   const DecodePlan pl = make_plan(&d, true);
-  const size_t need = scratch_bytes(pl), need_cnt = counter_count(pl);
-  if (need > 0 && (!scratch || scratch_size < need || !counters || n_counters < need_cnt)) {
-    set_error("paged decode: scratch of %zu bytes and %zu counters required (got %zu, %zu)", need,
-              need_cnt, scratch_size, n_counters);
+  const size_t need = scratch_bytes(pl);
+  if (need > 0 && (!scratch || scratch_size < need)) {
+    set_error("paged decode: scratch of %zu bytes required (got %zu)", need, scratch_size);
     return SRSWA_WORKSPACE;
   }
   DecodeK k{};
@@ -860,10 +768,7 @@ extern "C" int srswa_gather_decode_paged(const srswa_paged_decode_args* a, void*
   k.pstride = pl.pstride;
   k.scale_l2 = d.scale * kLog2e;
   k.rowheads = pl.rowheads;
-  if (need > 0) {
-    k.cnt = counters;
-    k.part = reinterpret_cast<float*>(scratch);
-  }
+  if (need > 0) k.part = reinterpret_cast<float*>(scratch);
   k.bt = a->block_table;
   k.bt_sb = a->bt_sr;
   k.k_pst = a->k_sp;

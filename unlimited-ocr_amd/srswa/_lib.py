@@ -331,9 +331,8 @@ class KlBwdArgs(ctypes.Structure):
 SIGNATURES = {
     "srswa_version": (ctypes.c_int, []),
     "srswa_last_error": (ctypes.c_char_p, []),
-    "srswa_gather_decode_workspace": (None, [ctypes.POINTER(DecodeArgs), _szp, _szp]),
-    "srswa_gather_decode": (ctypes.c_int, [ctypes.POINTER(DecodeArgs), _vp, ctypes.c_size_t, _vp,
-                                           ctypes.c_size_t, _vp]),
+    "srswa_gather_decode_workspace": (ctypes.c_size_t, [ctypes.POINTER(DecodeArgs)]),
+    "srswa_gather_decode": (ctypes.c_int, [ctypes.POINTER(DecodeArgs), _vp, ctypes.c_size_t, _vp]),
     "srswa_index_workspace": (ctypes.c_size_t, [ctypes.POINTER(IndexArgs)]),
     "srswa_index_meanpool_topk": (ctypes.c_int, [ctypes.POINTER(IndexArgs), _vp, ctypes.c_size_t, _vp]),
     "srswa_topk_rows": (ctypes.c_int, [_vp, _i64, _i32, _i64, _i32, _i32, ctypes.c_float, _vp, _vp,
@@ -345,9 +344,8 @@ SIGNATURES = {
     "srswa_dash_route": (ctypes.c_int, [ctypes.POINTER(RouteArgs), _vp]),
     "srswa_kbar_pages": (ctypes.c_int, [ctypes.POINTER(KbarPagesArgs), _vp]),
     "srswa_kbar_scores": (ctypes.c_int, [ctypes.POINTER(KbarScoresArgs), _vp]),
-    "srswa_gather_decode_paged_workspace": (None, [ctypes.POINTER(PagedDecodeArgs), _szp, _szp]),
-    "srswa_gather_decode_paged": (ctypes.c_int, [ctypes.POINTER(PagedDecodeArgs), _vp, ctypes.c_size_t, _vp,
-                                                 ctypes.c_size_t, _vp]),
+    "srswa_gather_decode_paged_workspace": (ctypes.c_size_t, [ctypes.POINTER(PagedDecodeArgs)]),
+    "srswa_gather_decode_paged": (ctypes.c_int, [ctypes.POINTER(PagedDecodeArgs), _vp, ctypes.c_size_t, _vp]),
     "srswa_page_decode_meta": (ctypes.c_int, [ctypes.POINTER(PageMetaArgs), _vp]),
     "srswa_page_decode_allow_workspace": (ctypes.c_int, [ctypes.POINTER(PageAllowArgs), _szp]),
     "srswa_page_decode_allow": (ctypes.c_int, [ctypes.POINTER(PageAllowArgs), _vp, ctypes.c_size_t, _vp]),
@@ -426,7 +424,6 @@ def ptr(t) -> int | None:
 
 
 _scratch_cache: dict = {}
-_counter_cache: dict = {}
 
 
 def _stream_key(device: torch.device):
@@ -442,18 +439,4 @@ def scratch(device: torch.device, nbytes: int) -> torch.Tensor | None:
     if buf is None or buf.numel() < nbytes:
         buf = torch.empty(max(nbytes, 1 << 20), dtype=torch.uint8, device=device)
         _scratch_cache[key] = buf
-    return buf
-
-
-def counters(device: torch.device, n: int) -> torch.Tensor | None:
-    """Zero-filled uint32 arrival counters cached per (device, stream).  Every
-    kernel that uses them leaves them zero, so a prefix of one buffer serves all
-    later calls on the same stream (calls on one stream are ordered)."""
-    if n <= 0:
-        return None
-    key = _stream_key(device)
-    buf = _counter_cache.get(key)
-    if buf is None or buf.numel() < n:
-        buf = torch.zeros(max(n, 1 << 16), dtype=torch.int32, device=device)
-        _counter_cache[key] = buf
     return buf

@@ -28,7 +28,7 @@ def _i32(t: torch.Tensor) -> torch.Tensor:
 
 class _Launch:
     """A prepared launch: the C-ABI struct, the tensors it points into (kept
-    alive), the scratch / counter buffers and the entry point.  ``__call__``
+    alive), the scratch buffer and the entry point.  ``__call__``
     enqueues the kernel on the stream captured at preparation time without
     rebuilding anything (a few microseconds of host time)."""
 
@@ -107,14 +107,11 @@ def prepare_gather_decode(q, k_cache, v_cache, block_indices, q_pos, *, block_si
     a.in_dtype = _lib.dtype_code(q.dtype)
     a.out_dtype = _lib.dtype_code(odt)
     L_ = _lib.lib()
-    nscr, ncnt = ctypes.c_size_t(0), ctypes.c_size_t(0)
-    L_.srswa_gather_decode_workspace(ctypes.byref(a), ctypes.byref(nscr), ctypes.byref(ncnt))
-    scr = _lib.scratch(q.device, nscr.value)
-    cnt = _lib.counters(q.device, ncnt.value)
+    nscr = L_.srswa_gather_decode_workspace(ctypes.byref(a))
+    scr = _lib.scratch(q.device, nscr)
     launch = _Launch(L_.srswa_gather_decode, a,
                      (q, k_cache, v_cache, idx, bias, valid, pos, kvl, out, lse),
-                     (scr, nscr.value, cnt, 0 if cnt is None else cnt.numel()),
-                     _lib.stream_ptr(q.device), "srswa_gather_decode")
+                     (scr, nscr), _lib.stream_ptr(q.device), "srswa_gather_decode")
     if squeeze:
         out = out.squeeze(1)
         if lse is not None:
@@ -325,13 +322,10 @@ def prepare_gather_decode_paged(q, k_cache, v_cache, topk_idx, blk_bias, block_t
     a.in_dtype = _lib.dtype_code(q.dtype)
     a.out_dtype = _lib.dtype_code(out.dtype)
     L_ = _lib.lib()
-    nscr, ncnt = ctypes.c_size_t(0), ctypes.c_size_t(0)
-    L_.srswa_gather_decode_paged_workspace(ctypes.byref(a), ctypes.byref(nscr), ctypes.byref(ncnt))
-    scr = _lib.scratch(q.device, nscr.value)
-    cnt = _lib.counters(q.device, ncnt.value)
+    nscr = L_.srswa_gather_decode_paged_workspace(ctypes.byref(a))
+    scr = _lib.scratch(q.device, nscr)
     launch = _Launch(L_.srswa_gather_decode_paged, a, (q, k_cache, v_cache, ti, bias, bt, sl, out),
-                     (scr, nscr.value, cnt, 0 if cnt is None else cnt.numel()),
-                     _lib.stream_ptr(q.device), "srswa_gather_decode_paged")
+                     (scr, nscr), _lib.stream_ptr(q.device), "srswa_gather_decode_paged")
     return launch, out
 
 
@@ -585,8 +579,11 @@ class GatherAttnFn(torch.autograd.Function):
             B, HQ, T, S = dbh.shape
             HI = sel.shape[1]
             db = dbh.view(B, HI, HQ // HI, T, S).sum(2)            # heads -> their index head
-            dbias = db[:, 0] if len(ctx.bias_shape) == 3 else db
-            dbias = dbias.to(bias.dtype)
+            # the forward broadcast the bias to [B, HI, T, S]: sum the gradient
+            # over every broadcast dim (a [B, T, S] bias feeds all HI heads)
+            shape4 = (B, 1, T, S) if len(ctx.bias_shape) == 3 else ctx.bias_shape
+            db = db.sum_to_size(shape4)
+            dbias = (db[:, 0] if len(ctx.bias_shape) == 3 else db).to(bias.dtype)
         return dq, dk, dv, None, None, dbias, None, None, None
 
 
