@@ -464,10 +464,12 @@ def topk_blocks(scores, k, invalid_at=SCORE_NEG * 0.5):
     return out
 
 
-def near_tie_rows(scores, k, rel=1e-4, invalid_at=SCORE_NEG * 0.5):
+def near_tie_rows(scores, k, rel=1e-4, invalid_at=SCORE_NEG * 0.5, floor=1.0):
     """bool [...]: rows whose k-th and (k+1)-th best valid scores differ by less
-    than ``rel * max(1, |s_k|)`` -- there the selected SET is not determined by
-    fp32 summation order and bit-exact comparison is reported separately."""
+    than ``rel * max(floor, |s_k|)`` -- there the selected SET is not determined by
+    fp32 summation order and bit-exact comparison is reported separately.
+    ``floor`` = 1 for scores of order one and above; 0 makes the gap purely
+    relative (scores far below one, e.g. config 1's 1/sqrt(D)-scaled inputs)."""
     s = torch.nan_to_num(scores.double(), nan=float("-inf"))
     s = torch.where(s > invalid_at, s, torch.full((), float("-inf"), dtype=s.dtype))
     n = s.shape[-1]
@@ -476,7 +478,7 @@ def near_tie_rows(scores, k, rel=1e-4, invalid_at=SCORE_NEG * 0.5):
     top = torch.sort(s, dim=-1, descending=True).values
     sk, sk1 = top[..., k - 1], top[..., k]
     fin = torch.isfinite(sk) & torch.isfinite(sk1)
-    return fin & ((sk - sk1).abs() < rel * torch.clamp(sk.abs(), min=1.0))
+    return fin & ((sk - sk1).abs() < rel * torch.clamp(sk.abs(), min=float(floor)))
 
 
 # ---------------------------------------------------------------------------

@@ -26,11 +26,13 @@ def report(line: str) -> None:
     print(line, flush=True)
 
 
-def compare_selection(got, ref_scores, k, what, *, invalid_at=O.SCORE_NEG * 0.5, max_near_frac=0.05):
+def compare_selection(got, ref_scores, k, what, *, invalid_at=O.SCORE_NEG * 0.5, max_near_frac=0.05,
+                      tie_floor=1.0):
     """got int [..., k] selected ids (any order, -1 = empty); ref_scores [..., n]
-    the oracle's scores of the same rows.  Returns the counts dict."""
+    the oracle's scores of the same rows.  ``tie_floor``: the near-tie gap is
+    1e-4 * max(tie_floor, |s_k|).  Returns the counts dict."""
     ref = O.topk_blocks(ref_scores, k, invalid_at=invalid_at)
-    ties = O.near_tie_rows(ref_scores, k, invalid_at=invalid_at)
+    ties = O.near_tie_rows(ref_scores, k, invalid_at=invalid_at, floor=tie_floor)
     same = (torch.sort(got.long(), -1).values == torch.sort(ref, -1).values).all(-1)
     counts = {"rows": int(same.numel()), "exact": int(same.sum()), "near_tie": int(ties.sum()),
               "near_tie_differ": int(((~same) & ties).sum()), "mismatched": int(((~same) & (~ties)).sum())}
