@@ -82,6 +82,16 @@ typedef struct {
 size_t srswa_gather_decode_workspace(const srswa_decode_args* a);
 int srswa_gather_decode(const srswa_decode_args* a, void* scratch, size_t scratch_bytes, void* stream);
 
+/* Allocation-free srswa_gather_decode.  No counterpart in the reference: it is
+ * for callers that cannot allocate (code under HIP graph capture, tight
+ * serving loops, harnesses that forbid hipMalloc).  The split-K records live
+ * in a static 8 MiB device array that each GPU the library runs on holds until
+ * the process ends; a call whose srswa_gather_decode_workspace exceeds 8 MiB
+ * returns SRSWA_WORKSPACE (config 3, B = 64, needs 1.6 MiB).  The stream must
+ * belong to the current device.  All calls on one GPU share its array: calls
+ * that overlap on one GPU (other streams, other host threads) race. */
+int srswa_gather_decode_noalloc(const srswa_decode_args* a, void* stream);
+
 /* ------------------------------------------------------------------------
  * Block indexer: head_cls / mean-pool block summaries, remote block scores
  * and top-k selection.  Replaces:

@@ -25,7 +25,9 @@
 #include <stdarg.h>
 #include <stdio.h>
 #include <stdlib.h>
-#include <string.h>
+
+#include <atomic>
+#include <mutex>
 
 #include "common.h"
 
@@ -598,8 +600,8 @@ extern "C" size_t srswa_gather_decode_workspace(const srswa_decode_args* a) {
   return 0;
 }
 
-extern "C" int srswa_gather_decode(const srswa_decode_args* a, void* scratch,
-                                   size_t scratch_size, void* stream) {
+extern "C" int srswa_gather_decode(const srswa_decode_args* a, void* ws, size_t ws_bytes,
+                                   void* stream) {
   if (!a || !a->q || !a->k || !a->v || !a->out || !a->q_pos || (!a->idx && a->S > 0)) {
     set_error("decode: null argument");
     return SRSWA_INVALID;
@@ -640,8 +642,8 @@ extern "C" int srswa_gather_decode(const srswa_decode_args* a, void* scratch,
   }
   const DecodePlan pl = make_plan(a);
   const size_t need = scratch_bytes(pl);
-  if (need > 0 && (!scratch || scratch_size < need)) {
-    set_error("decode: scratch of %zu bytes required (got %zu)", need, scratch_size);
+  if (need > 0 && (!ws || ws_bytes < need)) {
+    set_error("decode: scratch of %zu bytes required (got %zu)", need, ws_bytes);
     return SRSWA_WORKSPACE;
   }
   DecodeK k{};
@@ -657,7 +659,7 @@ extern "C" int srswa_gather_decode(const srswa_decode_args* a, void* scratch,
   k.pstride = pl.pstride;
   k.scale_l2 = a->scale * kLog2e;
   k.rowheads = pl.rowheads;
-  if (need > 0) k.part = reinterpret_cast<float*>(scratch);
+  if (need > 0) k.part = reinterpret_cast<float*>(ws);
   const int64_t grid = pl.rowheads * pl.nsplit;
   if (grid > 0x7fffffff) {
     set_error("decode: grid too large");
@@ -705,8 +707,8 @@ extern "C" size_t srswa_gather_decode_paged_workspace(const srswa_paged_decode_a
   return 0;
 }
 
-extern "C" int srswa_gather_decode_paged(const srswa_paged_decode_args* a, void* scratch,
-                                         size_t scratch_size, void* stream) {
+extern "C" int srswa_gather_decode_paged(const srswa_paged_decode_args* a, void* ws, size_t ws_bytes,
+                                         void* stream) {
   if (!a || !a->q || !a->k_cache || !a->v_cache || !a->out || !a->block_table || !a->seq_lens ||
       (!a->topk && a->topk_n > 0)) {
     set_error("paged decode: null argument");
@@ -751,8 +753,8 @@ extern "C" int srswa_gather_decode_paged(const srswa_paged_decode_args* a, void*
   const srswa_decode_args d = paged_as_decode(a);
   const DecodePlan pl = make_plan(&d, true);
   const size_t need = scratch_bytes(pl);
-  if (need > 0 && (!scratch || scratch_size < need)) {
-    set_error("paged decode: scratch of %zu bytes required (got %zu)", need, scratch_size);
+  if (need > 0 && (!ws || ws_bytes < need)) {
+    set_error("paged decode: scratch of %zu bytes required (got %zu)", need, ws_bytes);
     return SRSWA_WORKSPACE;
   }
   DecodeK k{};
@@ -768,7 +770,7 @@ extern "C" int srswa_gather_decode_paged(const srswa_paged_decode_args* a, void*
   k.pstride = pl.pstride;
   k.scale_l2 = d.scale * kLog2e;
   k.rowheads = pl.rowheads;
-  if (need > 0) k.part = reinterpret_cast<float*>(scratch);
+  if (need > 0) k.part = reinterpret_cast<float*>(ws);
   k.bt = a->block_table;
   k.bt_sb = a->bt_sr;
   k.k_pst = a->k_sp;
@@ -787,4 +789,77 @@ extern "C" int srswa_gather_decode_paged(const srswa_paged_decode_args* a, void*
     case SRSWA_F16: return dispatch_out<__half>(k, grid, st);
   }
   return SRSWA_UNSUPPORTED;
+}
+
+// ---------------------------------------------------------------------------
+// Allocation-free decode.  The split-K records live in `scratch`, a file-scope
+// device array of kStaticScratchBytes that each GPU the library runs on holds
+// until the process ends.  Host code never passes the array's name to a
+// kernel (on the host it is only a stand-in for the symbol): its device
+// address is looked up once per device with hipGetSymbolAddress, with that
+// device current, and cached.  Every call on one GPU shares that GPU's array,
+// so calls that overlap on one GPU (several streams, several host threads)
+// race; calls on one stream are ordered and safe.  Nothing needs clearing:
+// every call writes each record it reads.
+// ---------------------------------------------------------------------------
+namespace {
+constexpr size_t kStaticScratchBytes = size_t(8) << 20;   // 8 MiB per device
+constexpr int kMaxDevices = 64;
+}  // namespace
+
+static __device__ __align__(256) unsigned char scratch[kStaticScratchBytes];
+
+namespace {
+std::atomic<void*> g_static_scratch[kMaxDevices];
+std::mutex g_static_scratch_mu;
+
+// The device address of `scratch` on the device `stream` runs on, which must
+// be the current device.
+int static_scratch(void* stream, void** out) {
+  int dev = -1;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess || dev < 0 || dev >= kMaxDevices) {
+    set_error("decode (no alloc): no usable current device (%s)", hipGetErrorString(e));
+    return SRSWA_INVALID;
+  }
+  if (stream) {
+    hipDevice_t sdev = -1;
+    e = hipStreamGetDevice(reinterpret_cast<hipStream_t>(stream), &sdev);
+    if (e != hipSuccess || sdev != dev) {
+      set_error("decode (no alloc): the stream belongs to device %d, the current device is %d", (int)sdev, dev);
+      return SRSWA_INVALID;
+    }
+  }
+  void* p = g_static_scratch[dev].load(std::memory_order_acquire);
+  if (!p) {
+    std::lock_guard<std::mutex> lock(g_static_scratch_mu);
+    p = g_static_scratch[dev].load(std::memory_order_relaxed);
+    if (!p) {
+      e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+      if (e != hipSuccess || !p) {
+        set_error("decode (no alloc): hipGetSymbolAddress of the static scratch failed on device %d: %s", dev,
+                  hipGetErrorString(e));
+        return SRSWA_LAUNCH;
+      }
+      g_static_scratch[dev].store(p, std::memory_order_release);
+    }
+  }
+  *out = p;
+  return SRSWA_OK;
+}
+}  // namespace
+
+extern "C" int srswa_gather_decode_noalloc(const srswa_decode_args* a, void* stream) {
+  const size_t need = srswa_gather_decode_workspace(a);
+  if (need > kStaticScratchBytes) {
+    set_error("decode (no alloc): this call needs %zu bytes of split-K scratch, above the static %zu bytes; "
+              "use srswa_gather_decode with a caller-owned workspace", need, kStaticScratchBytes);
+    return SRSWA_WORKSPACE;
+  }
+  void* ws = nullptr;
+  if (need > 0) {
+    const int st = static_scratch(stream, &ws);
+    if (st != SRSWA_OK) return st;
+  }
+  return srswa_gather_decode(a, ws, need > 0 ? kStaticScratchBytes : 0, stream);
 }

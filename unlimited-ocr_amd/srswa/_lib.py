@@ -333,6 +333,7 @@ SIGNATURES = {
     "srswa_last_error": (ctypes.c_char_p, []),
     "srswa_gather_decode_workspace": (ctypes.c_size_t, [ctypes.POINTER(DecodeArgs)]),
     "srswa_gather_decode": (ctypes.c_int, [ctypes.POINTER(DecodeArgs), _vp, ctypes.c_size_t, _vp]),
+    "srswa_gather_decode_noalloc": (ctypes.c_int, [ctypes.POINTER(DecodeArgs), _vp]),
     "srswa_index_workspace": (ctypes.c_size_t, [ctypes.POINTER(IndexArgs)]),
     "srswa_index_meanpool_topk": (ctypes.c_int, [ctypes.POINTER(IndexArgs), _vp, ctypes.c_size_t, _vp]),
     "srswa_topk_rows": (ctypes.c_int, [_vp, _i64, _i32, _i64, _i32, _i32, ctypes.c_float, _vp, _vp,
