@@ -276,23 +276,48 @@ typedef struct {
 
 int srswa_kbar_pages(const srswa_kbar_pages_args* a, void* stream);
 
-/* Scores of query rows against the cached summaries: row n (request
- * row_req[n], position row_pos[n]; NULL arrays = decode rows: request n / dql,
- * position seq_lens[r] - dql + n % dql) gets, for blocks b < width,
- *   z = clamp(q_n . kbar[block_table[r, b]] / sqrt(D), +-1e4)
+/* Scores of query rows against the cached summaries: row n gets, for blocks
+ * b < width,
+ *   z = clamp(q_n . kbar[block_table[r, b]] * fp32(1/sqrt(D)), +-1e4)
  * when b <= pos / page_size - local_blocks and b * page_size < seq_lens[r],
  * else -1e9 (headcls_scores_decode, dash_stage0.py:151-199; the prefill rows
- * of headcls_scores_prefill, :62-103). */
+ * of headcls_scores_prefill, :62-103; the score kernels of the serving router,
+ * WHL!layers/attention/unlimited_dash_ops/route_triton.py:75-126, 529-572).
+ * The row's request r and position pos:
+ *   - decode rows (row_req NULL): r = n / dql, pos = seq_lens[r] - dql + n % dql;
+ *   - explicit rows: r = row_req[n], pos = row_pos[n];
+ *   - prefill rows (cu_q and ctx set, row_pos NULL): query m = row_off + n,
+ *     r = row_req[m], pos = ctx[r] + m - cu_q[r] (q rows and scores are
+ *     indexed by n). */
 typedef struct {
   const float* q;       int64_t q_sn;                  /* [nrows, D] fp32 index queries      */
   const float* kbar;    int64_t kb_sp;                 /* [num_pages, D] fp32                */
   const int32_t* block_table; int64_t bt_sr;           /* [R, max_blocks]                    */
   const int32_t* seq_lens;                             /* [R]                                */
-  const int32_t* row_req;                              /* [nrows] or NULL                    */
+  const int32_t* row_req;                              /* [nrows] (or [row_off + nrows]); NULL */
   const int32_t* row_pos;                              /* [nrows] or NULL                    */
+  const int32_t* cu_q;                                 /* [R + 1] query row offsets or NULL  */
+  const int32_t* ctx;                                  /* [R] cached tokens before the chunk or NULL */
   float* scores;        int64_t sc_sn;                 /* [nrows, width] fp32                */
-  int32_t nrows, R, dql, max_blocks, width, page_size, local_blocks, D;
+  int32_t nrows, R, dql, max_blocks, width, page_size, local_blocks, D, row_off;
 } srswa_kbar_scores_args;
+
+/* Summaries of explicitly listed pages (the refresh plan of the serving
+ * backend: kbar_tail_plan / kbar_all_plan, route_triton.py:575-601, 681-703):
+ * kbar[pages[i]] = summary of the page's first tok[i] keys, entries with
+ * tok[i] <= 0 skipped (route_triton.py:37-72, kbar_refresh_tail_triton
+ * :706-726). */
+typedef struct {
+  const void* keys;     int64_t k_sp, k_st;            /* [num_pages, page_size, D] index keys */
+  const float* head_cls;                               /* [D] fp32; NULL = mean              */
+  const int64_t* pages;                                /* [n] page ids                       */
+  const int32_t* tok;                                  /* [n] live keys of each page         */
+  float* kbar;          int64_t kb_sp;                 /* [num_pages, D] fp32                */
+  int32_t n, num_pages, page_size, D;
+  int32_t k_dtype;
+} srswa_kbar_plan_args;
+
+int srswa_kbar_plan(const srswa_kbar_plan_args* a, void* stream);
 
 int srswa_kbar_scores(const srswa_kbar_scores_args* a, void* stream);
 
@@ -325,6 +350,55 @@ typedef struct {
 } srswa_route_args;
 
 int srswa_dash_route(const srswa_route_args* a, void* stream);
+
+/* ------------------------------------------------------------------------
+ * Serving DASH router: per query row, 1.5-entmax over every candidate block,
+ * a hard top-K budget and the centred log-prior bias, packed ascending.
+ * Replaces _entmax_kernel / _entmax_tiled_kernel of the SGLang backend
+ * (WHL!layers/attention/unlimited_dash_ops/route_triton.py:129-221, 280-463),
+ * behind route_decode_triton / route_prefill_triton (:623-678, 729-847):
+ *   remote = score > -5e8; cand = remote & img when any, else remote;
+ *   x = cand ? score * idx_scale : -1e4 (NaN -> -1e4); xm = max_cand x (0 if
+ *   no candidate); z = (x - xm) * 0.5 (fp32);
+ *   tau: 24 bisection steps on [-1, 0], mid = (lo + hi) * 0.5, going up when
+ *     fp32(sum over cand, in fp64, of fp32(max(z - mid, 0))^2) > 1;
+ *     tau = (lo + hi) * 0.5; prior = max(z - tau, 0)^2;
+ *   budget: when more than K candidates, 40 bisection steps on
+ *     [min_cand z - 1, 0] keeping more than K above lo and at most K above
+ *     hi; active = cand & z > hi (else active = cand);
+ *   logp = log(max(prior, floor)); mu = fp32(sum_active logp in fp64) / n_active;
+ *   bias = (logp - mu) * inv_sigma;
+ *   out_idx[0 .. n_active) = the active block ids ascending (bias alike),
+ *   slots n_active .. M - 1 = -1 / 0 (slots >= M untouched).
+ * The budget bisection's steps depend only on the (K+1)-th largest candidate
+ * z, which the kernel selects exactly and then replays the 40 steps on.
+ * ---------------------------------------------------------------------- */
+typedef struct {
+  const float* scores;  int64_t sc_sn;                 /* [rows, W] fp32, column = block id  */
+  const int8_t* img;    int64_t img_sn;                /* [rows, >= W] page mask; NULL = none */
+  int32_t* out_idx;     int64_t oi_sn;                 /* [rows, >= M] int32                 */
+  float* out_bias;      int64_t ob_sn;                 /* [rows, >= M] fp32                  */
+  int32_t rows, W, K, M;
+  float idx_scale, prior_floor, inv_sigma;
+} srswa_route_serve_args;
+
+int srswa_route_serve(const srswa_route_serve_args* a, void* stream);
+
+/* Remote page span of each decode query row for the windowed router scans
+ * (_win_bounds_kernel / win_bounds_decode, route_triton.py:466-526): over the
+ * allowed live remote blocks b < min(W, WQ) (allow != 0, b <= pos / block_size
+ * - local_blocks, b * block_size < seq), lo = the first, hi = the last + 1;
+ * none: lo = 0, hi = 0 when the row has no remote block, else min(W,
+ * max(ceil(seq / block_size), 1)); fit = hi - lo <= tile. */
+typedef struct {
+  const int8_t* allow;  int64_t a_sn;                  /* [>= rows, WQ] page mask bytes      */
+  const int32_t* seq_lens;                             /* [R]                                */
+  int32_t* lo;          int32_t* hi;                   /* [rows]                             */
+  int8_t* fit;                                         /* [rows]                             */
+  int32_t rows, W, WQ, block_size, local_blocks, dql, tile;
+} srswa_win_bounds_args;
+
+int srswa_win_bounds(const srswa_win_bounds_args* a, void* stream);
 
 /* ------------------------------------------------------------------------
  * Page isolation and Page2D RoPE: the metadata step before scoring.

@@ -90,6 +90,46 @@ __device__ __forceinline__ float wave_sum(float v) {
   for (int o = 32; o >= 1; o >>= 1) v += __shfl_xor(v, o, kWave);
   return v;
 }
+__device__ __forceinline__ float wave_min(float v) {
+#pragma unroll
+  for (int o = 32; o >= 1; o >>= 1) v = fminf(v, __shfl_xor(v, o, kWave));
+  return v;
+}
+// fp64 butterfly sum: every lane ends with the same bits (each level adds the
+// same two values, in either order, on both partners)
+__device__ __forceinline__ double wave_sum_f64(double v) {
+#pragma unroll
+  for (int o = 32; o >= 1; o >>= 1) v += __shfl_xor(v, o, kWave);
+  return v;
+}
+
+// Bitonic sort of one unsigned value per lane, descending over the wave (lane 0
+// the largest): stage (K, J) compares lanes J apart; blocks with bit K of the
+// lane clear end descending, the others ascending, and K = 64 makes one run.
+template <typename U, int K, int J>
+__device__ __forceinline__ U bitonic_merge(U v, int lane) {
+  const U w = __shfl_xor(v, J, kWave);
+  const bool take_max = ((lane & J) == 0) == ((lane & K) == 0);
+  v = take_max ? (w > v ? w : v) : (w > v ? v : w);
+  if constexpr (J > 1) return bitonic_merge<U, K, J / 2>(v, lane);
+  else return v;
+}
+template <typename U, int K = 2>
+__device__ __forceinline__ U wave_sort_desc(U v, int lane) {
+  v = bitonic_merge<U, K, K / 2>(v, lane);
+  if constexpr (K < kWave) return wave_sort_desc<U, K * 2>(v, lane);
+  else return v;
+}
+
+// Order-preserving map of an fp32 value to an unsigned key (a > b <=> key(a) >
+// key(b) for non-NaN values) and back.
+__device__ __forceinline__ uint32_t f32_order_key(float x) {
+  const uint32_t u = __float_as_uint(x);
+  return (u & 0x80000000u) ? ~u : (u | 0x80000000u);
+}
+__device__ __forceinline__ float f32_from_order_key(uint32_t k) {
+  return __uint_as_float((k & 0x80000000u) ? (k & 0x7fffffffu) : ~k);
+}
 
 // Reduce-scatter of N partial sums per lane over the 2 O lanes of a row (c =
 // the lane's index in the row): at each level the lanes differing in bit O of c

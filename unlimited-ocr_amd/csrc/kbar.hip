@@ -20,6 +20,22 @@ namespace {
 
 constexpr int kKbWaves = 4;
 
+// One summary row slice (EPV floats) to memory; a NaN component is stored as 0
+// (a page whose head_cls weights are NaN, route_triton.py:68).
+template <int EPV>
+__device__ __forceinline__ void store_summary(float* dst, const float* kb, bool write) {
+  if (!write) return;
+  float o[EPV];
+#pragma unroll
+  for (int e = 0; e < EPV; ++e) o[e] = kb[e] == kb[e] ? kb[e] : 0.f;
+#pragma unroll
+  for (int e = 0; e < EPV; e += 4) *reinterpret_cast<uint4*>(dst + e) = Vec16<float>::pack(o + e);
+}
+
+// 1/sqrt(D) rounded once to fp32 from the double value, as the reference
+// passes it (route_triton.py:665, 723, 803)
+float inv_sqrt(int D) { return (float)(1.0 / sqrt((double)D)); }
+
 template <typename T, int D, bool HC>
 __global__ __launch_bounds__(kKbWaves * kWave) void kbar_pages_kernel(srswa_kbar_pages_args a, int per_req,
                                                                       float inv_sqrt_d) {
@@ -41,11 +57,29 @@ __global__ __launch_bounds__(kKbWaves * kWave) void kbar_pages_kernel(srswa_kbar
   float kb[EPV];
   summarize_rows<T, D, HC>(reinterpret_cast<const T*>(a.keys) + (int64_t)page * a.k_sp + c * EPV, a.k_st, nkeys,
                            HC ? a.head_cls + c * EPV : nullptr, inv_sqrt_d, s_w[wave], kb);
-  if (lane < LPR) {
-    float* dst = a.kbar + (int64_t)page * a.kb_sp + c * EPV;
-#pragma unroll
-    for (int e = 0; e < EPV; e += 4) *reinterpret_cast<uint4*>(dst + e) = Vec16<float>::pack(kb + e);
-  }
+  store_summary<EPV>(a.kbar + (int64_t)page * a.kb_sp + c * EPV, kb, lane < LPR);
+}
+
+// kbar_plan_kernel: one wavefront per plan entry (page id, live keys); entries
+//   with no live key are skipped (they mark slots of a dense plan that hold no
+//   page, and writing them would clobber another request's page).
+template <typename T, int D, bool HC>
+__global__ __launch_bounds__(kKbWaves * kWave) void kbar_plan_kernel(srswa_kbar_plan_args a, float inv_sqrt_d) {
+  using V = Vec16<T>;
+  constexpr int EPV = V::N;
+  constexpr int LPR = D / EPV;
+  __shared__ float s_w[kKbWaves][64];
+  const int wave = threadIdx.x / kWave, lane = threadIdx.x % kWave;
+  const int64_t i = (int64_t)blockIdx.x * kKbWaves + wave;
+  if (i >= a.n) return;
+  const int nkeys = min(a.tok[i], a.page_size);
+  const int64_t page = a.pages[i];
+  if (nkeys <= 0 || page < 0 || page >= a.num_pages) return;
+  const int c = lane % LPR;
+  float kb[EPV];
+  summarize_rows<T, D, HC>(reinterpret_cast<const T*>(a.keys) + page * a.k_sp + c * EPV, a.k_st, nkeys,
+                           HC ? a.head_cls + c * EPV : nullptr, inv_sqrt_d, s_w[wave], kb);
+  store_summary<EPV>(a.kbar + page * a.kb_sp + c * EPV, kb, lane < LPR);
 }
 
 // kbar_scores_kernel: one wavefront per (query row, 64 blocks).  Lane l reads
@@ -67,9 +101,11 @@ __global__ __launch_bounds__(kKbWaves * kWave) void kbar_scores_kernel(srswa_kba
   const int64_t w = (int64_t)blockIdx.x * kKbWaves + wave;
   if (w >= (int64_t)a.nrows * chunks) return;
   const int n = (int)(w / chunks), ch = (int)(w % chunks);
-  const int r = a.row_req ? a.row_req[n] : n / a.dql;
+  const bool prefill = a.cu_q && a.ctx && !a.row_pos;    // chunk-local row n = query row_off + n
+  const int m = prefill ? a.row_off + n : n;
+  const int r = a.row_req ? a.row_req[m] : n / a.dql;
   const int sl = a.seq_lens[r];
-  const int pos = a.row_pos ? a.row_pos[n] : sl - a.dql + n % a.dql;
+  const int pos = prefill ? a.ctx[r] + (m - a.cu_q[r]) : a.row_pos ? a.row_pos[n] : sl - a.dql + n % a.dql;
   const int qblk = pos >= 0 ? pos / a.page_size : -1;
   const int lim = min(min(qblk - a.local_blocks, ceil_div(max(sl, 0), a.page_size) - 1), a.max_blocks - 1);
   const int sub = lane / LPB, c = lane % LPB;
@@ -142,7 +178,7 @@ extern "C" int srswa_kbar_pages(const srswa_kbar_pages_args* a, void* stream) {
   }
   if (a->R == 0) return SRSWA_OK;
   const int per_req = a->tail_blocks > 0 ? std::min(a->tail_blocks, a->max_blocks) : a->max_blocks;
-  const float inv = 1.0f / sqrtf((float)a->D);
+  const float inv = inv_sqrt(a->D);
   hipStream_t st = reinterpret_cast<hipStream_t>(stream);
   switch (a->k_dtype) {
     case SRSWA_F32: launch_pages_hc<float>(*a, per_req, inv, st); break;
@@ -162,8 +198,11 @@ extern "C" int srswa_kbar_scores(const srswa_kbar_scores_args* a, void* stream) 
     set_error("kbar scores: null argument");
     return SRSWA_INVALID;
   }
+  const bool prefill = a->cu_q && a->ctx && !a->row_pos && a->row_req;
+  const bool explicit_rows = a->row_req && a->row_pos;
   if (a->nrows < 0 || a->R <= 0 || a->max_blocks <= 0 || a->width <= 0 || a->page_size <= 0 ||
-      a->local_blocks < 0 || ((!a->row_req || !a->row_pos) && (a->dql <= 0 || a->nrows != a->R * a->dql))) {
+      a->local_blocks < 0 || a->row_off < 0 ||
+      (!prefill && !explicit_rows && (a->dql <= 0 || a->nrows != a->R * a->dql))) {
     set_error("kbar scores: bad sizes");
     return SRSWA_INVALID;
   }
@@ -179,7 +218,7 @@ extern "C" int srswa_kbar_scores(const srswa_kbar_scores_args* a, void* stream) 
   const int chunks = ceil_div(a->width, kWave);
   const int64_t waves = (int64_t)a->nrows * chunks;
   const dim3 grid((unsigned)((waves + kKbWaves - 1) / kKbWaves));
-  const float inv = 1.0f / sqrtf((float)a->D);
+  const float inv = inv_sqrt(a->D);
   hipStream_t st = reinterpret_cast<hipStream_t>(stream);
   if (a->D == 64)
     hipLaunchKernelGGL(kbar_scores_kernel<64>, grid, dim3(kKbWaves * kWave), 0, st, *a, chunks, inv);
@@ -188,6 +227,59 @@ extern "C" int srswa_kbar_scores(const srswa_kbar_scores_args* a, void* stream) 
   const hipError_t e = hipGetLastError();
   if (e != hipSuccess) {
     set_error("kbar scores launch failed: %s", hipGetErrorString(e));
+    return SRSWA_LAUNCH;
+  }
+  return SRSWA_OK;
+}
+
+namespace srswa {
+namespace {
+template <typename T, bool HC>
+void launch_plan(const srswa_kbar_plan_args& a, float inv, hipStream_t st) {
+  const dim3 grid((unsigned)((a.n + kKbWaves - 1) / kKbWaves));
+  if (a.D == 64)
+    hipLaunchKernelGGL((kbar_plan_kernel<T, 64, HC>), grid, dim3(kKbWaves * kWave), 0, st, a, inv);
+  else
+    hipLaunchKernelGGL((kbar_plan_kernel<T, 128, HC>), grid, dim3(kKbWaves * kWave), 0, st, a, inv);
+}
+template <typename T>
+void launch_plan_hc(const srswa_kbar_plan_args& a, float inv, hipStream_t st) {
+  if (a.head_cls) launch_plan<T, true>(a, inv, st);
+  else launch_plan<T, false>(a, inv, st);
+}
+}  // namespace
+}  // namespace srswa
+
+extern "C" int srswa_kbar_plan(const srswa_kbar_plan_args* a, void* stream) {
+  if (!a || !a->keys || !a->kbar || (a->n > 0 && (!a->pages || !a->tok))) {
+    set_error("kbar plan: null argument");
+    return SRSWA_INVALID;
+  }
+  if (a->n < 0 || a->num_pages <= 0 || a->page_size <= 0) {
+    set_error("kbar plan: bad sizes");
+    return SRSWA_INVALID;
+  }
+  if (!(a->D == 64 || a->D == 128) || a->k_dtype < 0 || a->k_dtype > 2) {
+    set_error("kbar plan: D=%d / dtype not supported", a->D);
+    return SRSWA_UNSUPPORTED;
+  }
+  const int eb = a->k_dtype == SRSWA_F32 ? 4 : 2;
+  if (!al16k(a->keys) || !al16k(a->kbar) || (a->k_sp * eb) % 16 || (a->k_st * eb) % 16 || (a->kb_sp * 4) % 16 ||
+      (a->head_cls && !al16k(a->head_cls))) {
+    set_error("kbar plan: rows must be 16-byte aligned");
+    return SRSWA_UNSUPPORTED;
+  }
+  if (a->n == 0) return SRSWA_OK;
+  const float inv = inv_sqrt(a->D);
+  hipStream_t st = reinterpret_cast<hipStream_t>(stream);
+  switch (a->k_dtype) {
+    case SRSWA_F32: launch_plan_hc<float>(*a, inv, st); break;
+    case SRSWA_BF16: launch_plan_hc<bf16_t>(*a, inv, st); break;
+    default: launch_plan_hc<__half>(*a, inv, st); break;
+  }
+  const hipError_t e = hipGetLastError();
+  if (e != hipSuccess) {
+    set_error("kbar plan launch failed: %s", hipGetErrorString(e));
     return SRSWA_LAUNCH;
   }
   return SRSWA_OK;

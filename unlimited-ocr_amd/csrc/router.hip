@@ -52,24 +52,6 @@ __device__ __forceinline__ uint64_t wave_max_key(uint64_t v) {
   return v;
 }
 
-// Bitonic sort of one value per lane, descending over the wave (lane 0 the
-// largest): stage (K, J) compares lanes J apart; blocks with bit K of the lane
-// clear end descending, the others ascending, and K = 64 makes one run.
-template <int K, int J>
-__device__ __forceinline__ uint64_t bitonic_merge(uint64_t v, int lane) {
-  const uint64_t w = __shfl_xor(v, J, kWave);
-  const bool take_max = ((lane & J) == 0) == ((lane & K) == 0);
-  v = take_max ? kmax(v, w) : (w > v ? v : w);
-  if constexpr (J > 1) return bitonic_merge<K, J / 2>(v, lane);
-  else return v;
-}
-template <int K>
-__device__ __forceinline__ uint64_t wave_sort_desc(uint64_t v, int lane) {
-  v = bitonic_merge<K, K / 2>(v, lane);
-  if constexpr (K < kWave) return wave_sort_desc<K * 2>(v, lane);
-  else return v;
-}
-
 __device__ __forceinline__ float readlane_f(float v, int l) {
   return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), l));
 }
@@ -148,7 +130,7 @@ __global__ __launch_bounds__(256) void dash_route_kernel(RouteK p) {
       m3 = kmax(m3, keys[i + 3]);
     }
     // min(n, 64) >= M lanes hold a real key, so T > 0
-    const uint64_t lanes_sorted = wave_sort_desc<2>(kmax(kmax(m0, m1), kmax(m2, m3)), lane);
+    const uint64_t lanes_sorted = wave_sort_desc<uint64_t>(kmax(kmax(m0, m1), kmax(m2, m3)), lane);
     const uint64_t T = __shfl(lanes_sorted, M - 1, kWave);
     int cnt = 0;
 #pragma unroll
@@ -168,7 +150,7 @@ __global__ __launch_bounds__(256) void dash_route_kernel(RouteK p) {
       __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
       __builtin_amdgcn_wave_barrier();
       __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-      my_key = wave_sort_desc<2>(lane < total ? s_sel[wave][lane] : 0ull, lane);
+      my_key = wave_sort_desc<uint64_t>(lane < total ? s_sel[wave][lane] : 0ull, lane);
       sorted = true;
     }
   }

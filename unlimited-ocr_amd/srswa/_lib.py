@@ -174,9 +174,51 @@ class KbarScoresArgs(ctypes.Structure):
         ("seq_lens", _vp),
         ("row_req", _vp),
         ("row_pos", _vp),
+        ("cu_q", _vp),
+        ("ctx", _vp),
         ("scores", _vp), ("sc_sn", _i64),
         ("nrows", _i32), ("R", _i32), ("dql", _i32), ("max_blocks", _i32), ("width", _i32),
-        ("page_size", _i32), ("local_blocks", _i32), ("D", _i32),
+        ("page_size", _i32), ("local_blocks", _i32), ("D", _i32), ("row_off", _i32),
+    ]
+
+
+class KbarPlanArgs(ctypes.Structure):
+    """Mirror of ``srswa_kbar_plan_args``."""
+
+    _fields_ = [
+        ("keys", _vp), ("k_sp", _i64), ("k_st", _i64),
+        ("head_cls", _vp),
+        ("pages", _vp),
+        ("tok", _vp),
+        ("kbar", _vp), ("kb_sp", _i64),
+        ("n", _i32), ("num_pages", _i32), ("page_size", _i32), ("D", _i32),
+        ("k_dtype", _i32),
+    ]
+
+
+class RouteServeArgs(ctypes.Structure):
+    """Mirror of ``srswa_route_serve_args``."""
+
+    _fields_ = [
+        ("scores", _vp), ("sc_sn", _i64),
+        ("img", _vp), ("img_sn", _i64),
+        ("out_idx", _vp), ("oi_sn", _i64),
+        ("out_bias", _vp), ("ob_sn", _i64),
+        ("rows", _i32), ("W", _i32), ("K", _i32), ("M", _i32),
+        ("idx_scale", ctypes.c_float), ("prior_floor", ctypes.c_float), ("inv_sigma", ctypes.c_float),
+    ]
+
+
+class WinBoundsArgs(ctypes.Structure):
+    """Mirror of ``srswa_win_bounds_args``."""
+
+    _fields_ = [
+        ("allow", _vp), ("a_sn", _i64),
+        ("seq_lens", _vp),
+        ("lo", _vp), ("hi", _vp),
+        ("fit", _vp),
+        ("rows", _i32), ("W", _i32), ("WQ", _i32), ("block_size", _i32), ("local_blocks", _i32),
+        ("dql", _i32), ("tile", _i32),
     ]
 
 
@@ -345,6 +387,9 @@ SIGNATURES = {
     "srswa_dash_route": (ctypes.c_int, [ctypes.POINTER(RouteArgs), _vp]),
     "srswa_kbar_pages": (ctypes.c_int, [ctypes.POINTER(KbarPagesArgs), _vp]),
     "srswa_kbar_scores": (ctypes.c_int, [ctypes.POINTER(KbarScoresArgs), _vp]),
+    "srswa_kbar_plan": (ctypes.c_int, [ctypes.POINTER(KbarPlanArgs), _vp]),
+    "srswa_route_serve": (ctypes.c_int, [ctypes.POINTER(RouteServeArgs), _vp]),
+    "srswa_win_bounds": (ctypes.c_int, [ctypes.POINTER(WinBoundsArgs), _vp]),
     "srswa_gather_decode_paged_workspace": (ctypes.c_size_t, [ctypes.POINTER(PagedDecodeArgs)]),
     "srswa_gather_decode_paged": (ctypes.c_int, [ctypes.POINTER(PagedDecodeArgs), _vp, ctypes.c_size_t, _vp]),
     "srswa_page_decode_meta": (ctypes.c_int, [ctypes.POINTER(PageMetaArgs), _vp]),
@@ -364,7 +409,9 @@ STRUCTS = {"srswa_decode_args": DecodeArgs, "srswa_index_args": IndexArgs,
            "srswa_fwd_args": FwdArgs, "srswa_bwd_args": BwdArgs,
            "srswa_blockmax_args": BlockMaxArgs, "srswa_route_args": RouteArgs,
            "srswa_paged_decode_args": PagedDecodeArgs, "srswa_kbar_pages_args": KbarPagesArgs,
-           "srswa_kbar_scores_args": KbarScoresArgs, "srswa_page_meta_args": PageMetaArgs,
+           "srswa_kbar_scores_args": KbarScoresArgs, "srswa_kbar_plan_args": KbarPlanArgs,
+           "srswa_route_serve_args": RouteServeArgs, "srswa_win_bounds_args": WinBoundsArgs,
+           "srswa_page_meta_args": PageMetaArgs,
            "srswa_page_allow_args": PageAllowArgs, "srswa_local_union_args": LocalUnionArgs,
            "srswa_cos_sin_args": CosSinArgs, "srswa_rope_args": RopeArgs,
            "srswa_block_bounds_args": BlockBoundsArgs, "srswa_candidate_args": CandidateArgs,

@@ -366,12 +366,14 @@ def kbar_pages(keys_cache, head_cls, block_table, seq_lens, kbar, *, tail_blocks
 
 
 def kbar_scores(q, kbar, block_table, seq_lens, *, width, page_size, local_blocks, dql=None, row_req=None,
-                row_pos=None, out=None):
-    """Scores [nrows, width] fp32 of index queries q [nrows, D] (fp32) against
-    the cached page summaries (SCORE_NEG off the remote blocks).  Decode rows
-    by default (request n // dql at seq_len - dql + n % dql), or explicit
-    per-row request / position tensors."""
-    _require_cuda(q, kbar, block_table, seq_lens, row_req, row_pos, out)
+                row_pos=None, cu_q=None, ctx=None, row_off=0, out=None):
+    """Scores [nrows, width] fp32 of index queries q [nrows, D] against the
+    cached page summaries (SCORE_NEG off the remote blocks).  Decode rows by
+    default (request n // dql at seq_len - dql + n % dql); explicit per-row
+    request / position tensors; or prefill rows (``row_req`` the row -> request
+    map of every query, ``cu_q`` / ``ctx`` the per-request query offsets and
+    cached lengths, ``row_off`` the first query of this chunk)."""
+    _require_cuda(q, kbar, block_table, seq_lens, row_req, row_pos, cu_q, ctx, out)
     nrows, D = q.shape
     qf = q.to(torch.float32)
     if qf.stride(-1) != 1:
@@ -382,16 +384,100 @@ def kbar_scores(q, kbar, block_table, seq_lens, *, width, page_size, local_block
     sl = _i32(seq_lens).contiguous()
     rr = None if row_req is None else _i32(row_req).contiguous()
     rp = None if row_pos is None else _i32(row_pos).contiguous()
+    cu = None if cu_q is None else _i32(cu_q).contiguous()
+    cx = None if ctx is None else _i32(ctx).contiguous()
     if out is None:
         out = torch.empty(nrows, int(width), dtype=torch.float32, device=q.device)
+    if out.stride(-1) != 1:
+        raise UnsupportedShape("score rows must be contiguous")
+    if out.shape[0] < nrows or out.shape[1] < int(width):
+        raise ValueError(f"scores {tuple(out.shape)} smaller than {nrows} x {width}")
+    if cu is not None and (rr is None or rr.numel() < int(row_off) + nrows or cu.numel() != sl.numel() + 1
+                           or cx.numel() != sl.numel()):
+        raise ValueError("prefill rows need row_req covering row_off + nrows rows, cu_q [R + 1], ctx [R]")
+    if rp is not None and (rr is None or rr.numel() < nrows or rp.numel() < nrows):
+        raise ValueError("explicit rows need row_req and row_pos of nrows entries")
     a = _lib.KbarScoresArgs(q=qf.data_ptr(), q_sn=qf.stride(0), kbar=kbar.data_ptr(), kb_sp=kbar.stride(0),
                             block_table=bt.data_ptr(), bt_sr=bt.stride(0), seq_lens=sl.data_ptr(),
-                            row_req=_lib.ptr(rr), row_pos=_lib.ptr(rp), scores=out.data_ptr(),
-                            sc_sn=out.stride(0), nrows=nrows, R=bt.shape[0], dql=int(dql or 0),
-                            max_blocks=bt.shape[1], width=int(width), page_size=int(page_size),
-                            local_blocks=int(local_blocks), D=D)
+                            row_req=_lib.ptr(rr), row_pos=_lib.ptr(rp), cu_q=_lib.ptr(cu), ctx=_lib.ptr(cx),
+                            scores=out.data_ptr(), sc_sn=out.stride(0), nrows=nrows, R=bt.shape[0],
+                            dql=int(dql or 0), max_blocks=bt.shape[1], width=int(width), page_size=int(page_size),
+                            local_blocks=int(local_blocks), D=D, row_off=int(row_off))
     _lib.check(_lib.lib().srswa_kbar_scores(ctypes.byref(a), _lib.stream_ptr(q.device)), "srswa_kbar_scores")
     return out
+
+
+def kbar_plan(keys_cache, head_cls, pages, tok, kbar):
+    """Summaries of the listed pages (``pages`` int64 [n], ``tok`` their live
+    keys, <= 0 skipped) written into ``kbar`` [num_pages, D] fp32 in place."""
+    _require_cuda(keys_cache, head_cls, pages, tok, kbar)
+    npages, page, D = keys_cache.shape
+    if keys_cache.stride(-1) != 1 or kbar.stride(-1) != 1 or kbar.dtype != torch.float32:
+        raise UnsupportedShape("keys / kbar rows must be contiguous, kbar fp32")
+    hc = None if head_cls is None else head_cls.detach().to(torch.float32).contiguous()
+    pg = pages.to(torch.int64).contiguous()
+    tk = _i32(tok).contiguous()
+    a = _lib.KbarPlanArgs(keys=keys_cache.data_ptr(), k_sp=keys_cache.stride(0), k_st=keys_cache.stride(1),
+                          head_cls=_lib.ptr(hc), pages=pg.data_ptr(), tok=tk.data_ptr(), kbar=kbar.data_ptr(),
+                          kb_sp=kbar.stride(0), n=pg.numel(), num_pages=min(npages, kbar.shape[0]),
+                          page_size=page, D=D, k_dtype=_lib.dtype_code(keys_cache.dtype))
+    _lib.check(_lib.lib().srswa_kbar_plan(ctypes.byref(a), _lib.stream_ptr(kbar.device)), "srswa_kbar_plan")
+    return kbar
+
+
+def route_serve(scores, image_allow, out_idx, out_bias, *, K, M, idx_scale, prior_floor, inv_sigma):
+    """The serving router over fp32 block scores [rows, W] (see
+    ``srswa_route_serve``): writes the first M slots of each row of
+    ``out_idx`` (int32) / ``out_bias`` (fp32) in place."""
+    _require_cuda(scores, image_allow, out_idx, out_bias)
+    rows, W = scores.shape
+    if scores.dtype != torch.float32 or scores.stride(-1) != 1:
+        raise UnsupportedShape("scores must be fp32 with contiguous rows")
+    if out_idx.dtype != torch.int32 or out_bias.dtype != torch.float32 or out_idx.stride(-1) != 1 \
+            or out_bias.stride(-1) != 1:
+        raise UnsupportedShape("out_idx int32 / out_bias fp32 with contiguous rows")
+    if out_idx.shape[0] < rows or out_bias.shape[0] < rows or out_idx.shape[-1] < M or out_bias.shape[-1] < M:
+        raise ValueError(f"outputs {tuple(out_idx.shape)} / {tuple(out_bias.shape)} too small for {rows} x {M}")
+    img = None
+    if image_allow is not None:
+        img = image_allow.view(torch.int8) if image_allow.dtype in (torch.bool, torch.uint8) else image_allow
+        if img.dtype != torch.int8:
+            img = (img != 0).to(torch.int8)
+        if img.stride(-1) != 1:
+            img = img.contiguous()
+        if img.shape[0] < rows or img.shape[-1] < W:
+            raise ValueError(f"image_allow {tuple(image_allow.shape)} smaller than the scores {rows} x {W}")
+    a = _lib.RouteServeArgs(scores=scores.data_ptr(), sc_sn=scores.stride(0),
+                            img=_lib.ptr(img), img_sn=img.stride(0) if img is not None else 0,
+                            out_idx=out_idx.data_ptr(), oi_sn=out_idx.stride(0),
+                            out_bias=out_bias.data_ptr(), ob_sn=out_bias.stride(0),
+                            rows=rows, W=W, K=int(K), M=int(M), idx_scale=float(idx_scale),
+                            prior_floor=float(prior_floor), inv_sigma=float(inv_sigma))
+    _lib.check(_lib.lib().srswa_route_serve(ctypes.byref(a), _lib.stream_ptr(scores.device)), "srswa_route_serve")
+
+
+def win_bounds(allow, seq_lens, lo, hi, fit, *, max_block, block_size, local_blocks, dql, tile):
+    """Remote page span (lo, hi) and the narrow-tile flag of every decode row
+    (see ``srswa_win_bounds``), written into int32 ``lo`` / ``hi`` and int8 ``fit``."""
+    _require_cuda(allow, seq_lens, lo, hi, fit)
+    nd = int(lo.numel())
+    al = allow.view(torch.int8) if allow.dtype in (torch.bool, torch.uint8) else allow
+    if al.dtype != torch.int8:
+        al = (al != 0).to(torch.int8)
+    if al.stride(-1) != 1:
+        al = al.contiguous()
+    if lo.dtype != torch.int32 or hi.dtype != torch.int32 or fit.dtype != torch.int8 or not (
+            lo.is_contiguous() and hi.is_contiguous() and fit.is_contiguous()):
+        raise UnsupportedShape("lo / hi int32, fit int8, contiguous")
+    sl = _i32(seq_lens).contiguous()
+    if al.shape[0] < nd or sl.numel() * max(1, int(dql)) < nd or hi.numel() < nd or fit.numel() < nd:
+        raise ValueError(f"win bounds: {nd} rows need allow rows {al.shape[0]}, seq_lens x dql "
+                         f"{sl.numel()} x {dql}, hi {hi.numel()}, fit {fit.numel()}")
+    a = _lib.WinBoundsArgs(allow=al.data_ptr(), a_sn=al.stride(0), seq_lens=sl.data_ptr(), lo=lo.data_ptr(),
+                           hi=hi.data_ptr(), fit=fit.data_ptr(), rows=nd, W=int(max_block), WQ=al.shape[1],
+                           block_size=int(block_size), local_blocks=int(local_blocks), dql=max(1, int(dql)),
+                           tile=int(tile))
+    _lib.check(_lib.lib().srswa_win_bounds(ctypes.byref(a), _lib.stream_ptr(lo.device)), "srswa_win_bounds")
 
 
 # ---------------------------------------------------------------------------

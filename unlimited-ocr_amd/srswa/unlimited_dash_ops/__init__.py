@@ -8,6 +8,9 @@ module for module, on the MI355X kernels:
                              ``local_union_fused``
 * ``page2d_rope``         -- ``PageRope2D``, ``apply_page2d_rope``, ``apply_page2d_rope_pair``,
                              ``page_capacity``
+* ``route_triton``        -- ``route_decode_triton``, ``route_prefill_triton``,
+                             ``kbar_refresh_tail_triton``, ``win_bounds_decode``,
+                             ``kbar_tail_plan``, ``kbar_all_plan``, ``prefill_row2req``
 
 Every tensor the kernels see must live on the GPU (no host path).
 """
@@ -18,3 +21,6 @@ from .decode_meta_triton import (  # noqa: F401
     cos_sin_2d_fused, decode_allow_fused, decode_meta_fused, local_union_fused)
 from .page2d_rope import (  # noqa: F401
     MIN_PAGE_TOKENS, PageRope2D, apply_page2d_rope, apply_page2d_rope_pair, page_capacity)
+from .route_triton import (  # noqa: F401
+    SCAN_TILE, kbar_all_plan, kbar_refresh_tail_triton, kbar_tail_plan, prefill_row2req, route_decode_triton,
+    route_prefill_triton, win_bounds_decode)
