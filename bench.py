@@ -405,6 +405,51 @@ def cpu_baseline_rows(c, Sk, T, BS, LW, budget_s, backward):
             "host": host_info()}
 
 
+def bench_paged_prefill(args):
+    """Config 4's chunked prefill over the serving (paged) cache: the drop-in
+    for the backend's K10 ``dash_sparse_attn``.  B=4 requests, each 2048 query
+    rows at the tail of 65536 keys in randomly ordered 64-key pages; config 4's
+    per-tile top-8 blocks, one router row per query expanded over the 10 kv
+    heads (stride 0, as the backend passes them); window 8 blocks."""
+    import torch
+    from srswa import unlimited_dash_ops as U, workloads as W
+    dev = torch.device("cuda:0")
+    B, T, Sk, H, D, BS, LW, K = 4, 2048, 65536, 10, 128, 64, 512, 8
+    c = W.prefill_config(B=B, T=T, Sk=Sk, H=H, D=D, device=dev)
+    nb = Sk // BS
+    g = torch.Generator().manual_seed(W.SEED0 + 44)
+    perm = torch.randperm(B * nb, generator=g)
+    bt = perm.view(B, nb).to(torch.int32).to(dev)
+    kc = torch.empty(B * nb, BS, H, D, dtype=torch.bfloat16, device=dev)
+    vc = torch.empty_like(kc)
+    for b in range(B):                       # scatter each sequence's blocks into its pages
+        kc[bt[b].long()] = c["k"][b].view(nb, BS, H, D)
+        vc[bt[b].long()] = c["v"][b].view(nb, BS, H, D)
+    q = c["q"].reshape(B * T, H, D)
+    ids = c["block_idx"][:, 0].reshape(B * T, K).to(torch.int32).to(dev)       # [total_q, K]
+    di = ids.unsqueeze(0).expand(H, -1, -1)
+    cu = (torch.arange(B + 1, dtype=torch.int32) * T).to(dev)
+    seq = torch.full((B,), Sk, dtype=torch.int32, device=dev)
+    pre = torch.full((B,), Sk - T, dtype=torch.int32, device=dev)
+    out = torch.empty_like(q)
+    fn = lambda: U.dash_sparse_attn(q, kc, vc, di, None, bt, cu, seq, pre, T, H, c["scale"], out,
+                                    local_blocks=LW // BS, sparse_block_size=BS)
+    ms = _time_launches(fn, args.steps, args.warmup, dev)
+    wp, rp = W.attended_pairs(c["block_idx"], Sk, BS, LW)
+    flops = (wp + rp) * H * 4 * D
+    tfs = flops / (ms * 1e-3) / 1e12
+    return {"metric": "paged chunked-prefill tokens/s + MFMA TFLOP/s (config 4 over KV pages)",
+            "value": B * T / (ms * 1e-3), "unit": "tokens/s", "n_gpus": 1, "steps": args.steps,
+            "warmup": args.warmup, "ms_per_step": ms, "higher_is_better": True, "scaling": "weak",
+            "vs_baseline": None, "dtype": "bf16", "data": "synthetic (seeded), pages in seeded random order",
+            "config": {"workload": "config 4 (B=4, 2048 of 65536 keys, 10 heads, block 64, top-8 + 512 window) "
+                                   "through dash_sparse_attn over a [16384, 64, 10, 128] paged cache",
+                       "flops_per_step": flops},
+            "roofline": {"bound": "mfma", "achieved": tfs, "peak": 2500.0, "unit": "TFLOP/s",
+                         "frac": tfs / 2500.0, "traffic": None,
+                         "kernel": "srswa::fwd_kernel<bf16,128,paged>"}}
+
+
 def bench_blockmax(args):
     """Block-max indexer scoring (the reference's K4, HF/sparse_gather_triton.py:445-524)
     on config 4's prefill chunk: one index head, B=4 sequences x 2048 query rows at the
@@ -703,8 +748,8 @@ def main():
     ap.add_argument("--steps", type=int, default=200)
     ap.add_argument("--warmup", type=int, default=20)
     ap.add_argument("--config", default="decode",
-                    choices=["decode", "indexer", "prefill", "fwdbwd", "paged", "dash", "page", "kl", "blockmax",
-                             "copycal"])
+                    choices=["decode", "indexer", "prefill", "fwdbwd", "paged", "paged_prefill", "dash", "page", "kl",
+                             "blockmax", "copycal"])
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--no-check", action="store_true", help="skip the oracle spot check")
     ap.add_argument("--cpu-budget", type=float, default=12.0)
@@ -714,7 +759,8 @@ def main():
               "(no multi-GPU path); use --gpus 1", file=sys.stderr)
         sys.exit(2)
     fn = {"decode": bench_decode, "indexer": bench_indexer, "prefill": bench_prefill,
-          "fwdbwd": bench_fwdbwd, "paged": bench_paged, "dash": bench_dash, "page": bench_page, "kl": bench_kl,
+          "fwdbwd": bench_fwdbwd, "paged": bench_paged, "paged_prefill": bench_paged_prefill, "dash": bench_dash,
+          "page": bench_page, "kl": bench_kl,
           "blockmax": bench_blockmax,
           "copycal": bench_copycal}[args.config]
     res = fn(args)

@@ -164,6 +164,41 @@ typedef struct {
 int srswa_gather_fwd(const srswa_fwd_args* a, void* stream);
 
 /* ------------------------------------------------------------------------
+ * Paged block-sparse prefill of the serving backend.  Replaces
+ * _dash_sparse_fwd_kernel / dash_sparse_attn (K10,
+ * WHL!layers/attention/unlimited_dash_ops/attend_triton.py:76-292, 521-597).
+ * Request r's query rows are cu_seqlens_q[r] .. cu_seqlens_q[r + 1) of q, out
+ * and the ids; row t of the request sits at key qp = prefix_lens[r] + t; the
+ * request's key j (< seq_lens[r]) is row j % page_size of page
+ * block_table[r, j / page_size].  With LW = local_blocks * page_size, per query
+ * head hq (kv head hq / (HQ / HKV), which also picks the ids):
+ *   window keys  qp - LW < j <= qp                   logit = scale * q.k
+ *   remote keys  of each id >= 0 of the row, j <= qp - LW
+ *                                                     logit = scale * q.k + bias[slot]
+ * one softmax over both, O in the input dtype.  The scale is applied to the
+ * fp32 product, as K10 does.  The reference runs the first count(id >= 0)
+ * slots, which the router packs at the front; here every slot with id >= 0
+ * counts, and a repeated id counts once (the router emits no repeats).
+ * ---------------------------------------------------------------------- */
+typedef struct {
+  const void* q;        int64_t q_sn, q_sh;            /* [total_q, HQ, D]                  */
+  const void* k_cache;  int64_t k_sp, k_st, k_sh;      /* [num_pages, page_size, HKV, D]    */
+  const void* v_cache;  int64_t v_sp, v_st, v_sh;      /* [num_pages, page_size, HKV, D]    */
+  const int32_t* topk;  int64_t t_sh, t_sn;            /* [HKV, total_q, S], slot stride 1  */
+  const float* bias;    int64_t b_sh, b_sn;            /* [HKV, total_q, S], slot stride 1; NULL */
+  const int32_t* block_table; int64_t bt_sr;           /* [R, max_blocks]                   */
+  const int32_t* cu_seqlens_q;                         /* [R + 1]                           */
+  const int32_t* seq_lens;                             /* [R]                               */
+  const int32_t* prefix_lens;                          /* [R]                               */
+  void* out;            int64_t o_sn, o_sh;            /* [total_q, HQ, D]                  */
+  int32_t R, max_query_len, HQ, HKV, D, S, max_blocks, page_size, local_blocks;
+  float scale;
+  int32_t dtype;                                       /* SRSWA_BF16 or SRSWA_F16           */
+} srswa_paged_fwd_args;
+
+int srswa_gather_fwd_paged(const srswa_paged_fwd_args* a, void* stream);
+
+/* ------------------------------------------------------------------------
  * Gather-attention backward (dQ, dK, dV and the per-slot bias gradient).
  * Replaces:
  *   - _gather_attn_bwd_dq_kernel / _dkv_kernel (K2, K3)  HF/sparse_gather_triton.py:125-279

@@ -278,6 +278,60 @@ def paged_decode_attend(q, k_cache, v_cache, topk, bias, block_table, seq_lens, 
     return torch.cat(out, 0)
 
 
+def paged_prefill_attend(q, k_cache, v_cache, topk, bias, block_table, cu_seqlens_q, seq_lens, prefix_lens,
+                         local_blocks, scale):
+    """The serving prefill over a paged cache: ``dash_sparse_attn`` /
+    ``_dash_sparse_fwd_kernel`` (K10, WHL!layers/attention/unlimited_dash_ops/
+    attend_triton.py:76-292, 521-597), query by query in its two passes.
+
+    q [total_q, H, D]; k_cache, v_cache [num_pages, page, Hkv, D]; topk / bias
+    [Hkv, total_q, K] (bias None = 0); block_table [R, max_blocks]; request r
+    owns query rows cu_seqlens_q[r] .. cu_seqlens_q[r + 1), row t at position
+    qp = prefix_lens[r] + t.  Per query head (kv head h // (H / Hkv)):
+      remote pass: the first count(id >= 0) slots, in slot order (:162-177),
+        keys c + n of each slot's block with c + n <= qp - LB * page and
+        c + n < seq_lens[r] (:183-211), logit scale * q.k + bias[slot];
+      window pass (LB > 0): blocks qp // page - o, o = 0 .. LB, keys in
+        [qp - LB * page + 1, qp] below seq_lens[r] (:231-263), logit scale * q.k.
+    One softmax over everything; returns [total_q, H, Dv] in fp64 (or the
+    promoted input dtype).  A row with no key at all is 0 here (the reference's
+    final acc * exp2(m - lse) is NaN there: -inf - -inf); with a window it
+    always holds its own key."""
+    page = k_cache.shape[1]
+    Hkv, H = k_cache.shape[2], q.shape[1]
+    G = H // Hkv
+    LW = int(local_blocks) * page
+    dt = torch.promote_types(q.dtype, torch.float32)
+    out = torch.zeros(q.shape[0], H, v_cache.shape[-1], dtype=dt)
+    for r in range(block_table.shape[0]):
+        sl, pre = int(seq_lens[r]), int(prefix_lens[r])
+        pages = block_table[r].long()
+        for n in range(int(cu_seqlens_q[r]), int(cu_seqlens_q[r + 1])):
+            qp = pre + n - int(cu_seqlens_q[r])
+            for h in range(H):
+                kh = h // G
+                ids = topk[kh, n].tolist()
+                real = sum(1 for i in ids if i >= 0)
+                keys, bvals = [], []
+                for si in range(real):
+                    c = ids[si] * page
+                    kk = [j for j in range(c, c + page) if j <= qp - LW and j < sl]
+                    keys += kk
+                    bvals += [0.0 if bias is None else float(bias[kh, n, si])] * len(kk)
+                if local_blocks > 0:
+                    kk = [j for j in range(max(qp - LW + 1, 0), qp + 1) if j < sl]
+                    keys += kk
+                    bvals += [0.0] * len(kk)
+                if not keys:
+                    continue
+                kt = torch.tensor(keys)
+                kv = k_cache[pages[kt // page], kt % page, kh].to(dt)
+                vv = v_cache[pages[kt // page], kt % page, kh].to(dt)
+                s = (kv @ q[n, h].to(dt)) * scale + torch.tensor(bvals, dtype=dt)
+                out[n, h] = torch.softmax(s, 0) @ vv
+    return out
+
+
 def decode_attend_gather(q, k_cache, v_cache, block_idx, q_pos, block_size, local_window,
                          scale, bias=None):
     """Gather-form decode for caches too large for the dense form.

@@ -586,3 +586,69 @@ def test_kbar_cache_scores_equal_contiguous_scores():
     # no head_cls -> plain mean of the real keys
     m = O.kbar_pages(keys, None, bt, sl, torch.zeros(npages, d))
     assert (m[bt[1, 4]] - keys[bt[1, 4], :1].mean(0)).abs().max() < 1e-12
+
+
+# ------------------------------------------------------- paged prefill (serving K10)
+def test_paged_prefill_equals_gather_attention_per_kv_head():
+    """paged_prefill_attend (K10's two passes, query by query) against the dense
+    gather_attention restatement on each request's cache gathered page by page,
+    one kv head at a time with that head's ids and slot biases (packed unique
+    ids, as the serving router emits): prefix lengths, GQA 2:1, LB = 2."""
+    g = torch.Generator().manual_seed(31)
+    page, Hkv, G, D, LB = 16, 2, 2, 8, 2
+    H = Hkv * G
+    q_lens, seq_lens = [5, 9, 3], [40, 9, 70]
+    prefix = [s - q for s, q in zip(seq_lens, q_lens)]
+    cu = [0, 5, 14, 17]
+    R, nb = 3, 5
+    npages = R * nb + 2
+    kc = torch.randn(npages, page, Hkv, D, generator=g)
+    vc = torch.randn(npages, page, Hkv, D, generator=g)
+    bt = torch.randperm(npages, generator=g)[:R * nb].view(R, nb)
+    total = cu[-1]
+    q = torch.randn(total, H, D, generator=g)
+    S = 3
+    topk = torch.full((Hkv, total, S), -1, dtype=torch.long)
+    for n in range(total):
+        for kh in range(Hkv):
+            ids = torch.randperm(nb, generator=g)[:int(torch.randint(0, S + 1, (1,), generator=g))].sort().values
+            topk[kh, n, :len(ids)] = ids
+    bias = torch.randn(Hkv, total, S, generator=g)
+    got = O.paged_prefill_attend(q, kc, vc, topk, bias, bt, cu, seq_lens, prefix, LB, 0.3)
+    for r in range(R):
+        rows = slice(cu[r], cu[r + 1])
+        L = seq_lens[r]
+        kr = kc[bt[r]].reshape(nb * page, Hkv, D)[:L]
+        vr = vc[bt[r]].reshape(nb * page, Hkv, D)[:L]
+        pos = (prefix[r] + torch.arange(q_lens[r]))[None]
+        for kh in range(Hkv):
+            hs = slice(kh * G, (kh + 1) * G)
+            bi = topk[kh, rows][None, None]                                  # [1,1,T,S]
+            dense = O.bias_slots_to_dense(bias[kh, rows][None], bi[:, 0], -(-L // page))
+            o, _ = O.gather_attention(q[rows, hs].transpose(0, 1)[None], kr[:, kh:kh + 1].transpose(0, 1)[None],
+                                      vr[:, kh:kh + 1].transpose(0, 1)[None], bi, pos, page, 0.3, LB * page,
+                                      blk_bias_dense=dense)
+            assert (got[rows, hs] - o[0].transpose(0, 1)).abs().max() < 1e-10
+
+
+def test_paged_prefill_no_window_is_causal_selected_keys():
+    """LB = 0: no window pass; a query attends only its selected blocks' keys up
+    to and including its own position (enumerated by hand)."""
+    g = torch.Generator().manual_seed(32)
+    page, D = 16, 4
+    kc = torch.randn(4, page, 1, D, generator=g)
+    vc = torch.randn(4, page, 1, D, generator=g)
+    bt = torch.tensor([[2, 0, 3, 1]])
+    q = torch.randn(2, 1, D, generator=g)
+    topk = torch.tensor([[[1, 3], [0, -1]]])                 # row 0: blocks 1, 3; row 1: block 0
+    got = O.paged_prefill_attend(q, kc, vc, topk, None, bt, [0, 2], [40], [30], 0, 1.0)
+    # row 0 at position 30: block 1 keys 16..30 (block 3 starts at 48 > 30)
+    keys = list(range(16, 31))
+    kv = torch.stack([kc[bt[0, j // page], j % page, 0] for j in keys])
+    vv = torch.stack([vc[bt[0, j // page], j % page, 0] for j in keys])
+    want = torch.softmax(kv @ q[0, 0], 0) @ vv
+    assert (got[0, 0] - want).abs().max() < 1e-12
+    # row 1 at position 31: block 0 keys 0..15
+    kv = torch.stack([kc[bt[0, 0], j, 0] for j in range(16)])
+    vv = torch.stack([vc[bt[0, 0], j, 0] for j in range(16)])
+    assert (got[1, 0] - torch.softmax(kv @ q[1, 0], 0) @ vv).abs().max() < 1e-12

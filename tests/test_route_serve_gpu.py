@@ -119,7 +119,9 @@ def _check_ids_chain(what, got_i, got_b, sc_gpu, sc_ref, img, K, M, p):
         cand = np.where(ci.any(1, keepdims=True), ci, cand)
     x = np.where(cand, sc_ref * p["idx_scale"], -np.inf)
     top = -np.sort(-x, 1)
-    gap = top[:, K - 1] - top[:, K] if x.shape[1] > K else np.full(rows, np.inf)
+    with np.errstate(invalid="ignore"):          # -inf - -inf in rows with few candidates: not a tie
+        gap = top[:, K - 1] - top[:, K] if x.shape[1] > K else np.full(rows, np.inf)
+    gap = np.where(np.isnan(gap), np.inf, gap)
     near = np.abs(gap) < 1e-4 * np.maximum(1.0, np.abs(top[:, K - 1]))
     report(f"[ids] {what}: rows {rows}, equal to the oracle on its own scores {int(same.sum())}, "
            f"near-tie {int(near.sum())}, differ outside near-ties {int(((~same) & (~near)).sum())}")

@@ -51,6 +51,16 @@ struct FwdK {
   int ntiles, nwords, SP, G, IG, bs_shift;
   int nlogical, per_xcd;       // XCD-aware workgroup order
   int chunks_off, sid_off;     // LDS byte offsets of the chunk list and sorted ids
+  int pages_off;               // paged: LDS byte offset of the visited chunks' page ids
+  int ppc, page_cap;           // paged: page ids per chunk (1 when BS >= 64, else 4); chunks held in LDS
+  // paged form (the serving prefill): request b's queries are rows cu[b] ..
+  // cu[b + 1) of q / out / ids / bias, query t sits at key prefix[b] + t, the
+  // request holds seqlen[b] keys, and key j is row j % BS of page bt[b, j / BS]
+  const int32_t* cu;
+  const int32_t* prefix;
+  const int32_t* seqlen;
+  const int32_t* bt;
+  int64_t bt_sr, k_pst, v_pst;
 };
 
 template <int D> struct FwdLds {
@@ -61,7 +71,7 @@ template <int D> struct FwdLds {
   static constexpr int tileBytes = vOff + kChunk * VP * 2;
 };
 
-template <typename T, int D>
+template <typename T, int D, bool PAGED>
 __global__ __launch_bounds__(128, 2) void fwd_kernel(FwdK p) {
   using M = Mfma<T>;
   using L = FwdLds<D>;
@@ -98,10 +108,23 @@ __global__ __launch_bounds__(128, 2) void fwd_kernel(FwdK p) {
   const int hq = bh % a.HQ, b = bh / a.HQ;
   const int kvh = hq / p.G, ih = hq / p.IG;
   const int t0 = tile * kTileRows;
-  const int nrows = min(kTileRows, a.T - t0);
-  const int off = a.Sk - a.T;
+  // this tile's sequence: its query rows (q0 = first row in q / out / ids),
+  // key count and the key index of its first query
+  int q0 = 0, Tb = a.T, Skb = a.Sk;
+  if constexpr (PAGED) {
+    q0 = p.cu[b];
+    Tb = p.cu[b + 1] - q0;
+    Skb = p.seqlen[b];
+    if (t0 >= Tb) return;             // the grid covers the longest request
+  }
+  const int nrows = min(kTileRows, Tb - t0);
+  const int off = PAGED ? p.prefix[b] : a.Sk - a.T;
   const int BS = a.block_size, LW = a.local_window, SP = p.SP;
-  const int maxblk = (a.Sk - 1) >> p.bs_shift;
+  const int maxblk = (Skb - 1) >> p.bs_shift;
+  // logits to log2 units: the matrix-core prefill rounds q * scale to the input
+  // dtype first (K1 / K5, HF/sparse_gather_triton.py:68); the serving prefill
+  // scales the fp32 product (attend_triton.py:204)
+  const float l2s = PAGED ? a.scale * kLog2e : kLog2e;
 
   if (tid < 64) {
     const int r = tid;
@@ -115,14 +138,31 @@ __global__ __launch_bounds__(128, 2) void fwd_kernel(FwdK p) {
     s_seg[r] = seg;
     s_ls[r] = ls;
     const int rr = min(r, nrows - 1);
-    const int32_t* ids = a.idx + (int64_t)b * a.idx_sb + (int64_t)ih * a.idx_sh + (int64_t)(t0 + rr) * a.idx_st;
-    const float* bias =
-        a.bias ? a.bias + (int64_t)b * a.bias_sb + (int64_t)ih * a.bias_sh + (int64_t)(t0 + rr) * a.bias_st : nullptr;
+    const int32_t* ids =
+        a.idx + (int64_t)b * a.idx_sb + (int64_t)ih * a.idx_sh + (int64_t)(q0 + t0 + rr) * a.idx_st;
+    const float* bias = a.bias ? a.bias + (int64_t)b * a.bias_sb + (int64_t)ih * a.bias_sh +
+                                     (int64_t)(q0 + t0 + rr) * a.bias_st
+                               : nullptr;
     sort_row_ids(ids, bias, r < nrows ? a.S : 0, SP, BS, maxblk, qi, seg, ls, s_sid + r * SP,
                  s_sb ? s_sb + r * SP : nullptr);
   }
   __syncthreads();
   const int U = plan_chunks(s_qi, s_seg, s_ls, s_sid, SP, BS, LW, nrows, p.nwords, s_bits, s_chunks, s_count);
+  // paged: the page of each 16-key quarter of every visited chunk, looked up
+  // once here, so a prefetch issues its K / V loads without a dependent read
+  // (the first page_cap chunks; a longer list reads the rest from the table)
+  int* s_pages = PAGED ? reinterpret_cast<int*>(smem + p.pages_off) : nullptr;
+  const int32_t* bt_r = PAGED ? p.bt + (int64_t)b * p.bt_sr : nullptr;
+  const int nblk_live = (Skb + BS - 1) >> p.bs_shift;
+  auto page_of = [&](int c, int qq) {    // page of quarter qq of chunk c
+    const int blk = (c * kChunk + 16 * qq) >> p.bs_shift;
+    return blk < nblk_live ? bt_r[blk] : 0;
+  };
+  if constexpr (PAGED) {
+    const int held = min(U, p.page_cap);
+    for (int e = tid; e < held * p.ppc; e += 128) s_pages[e] = page_of(s_chunks[e / p.ppc], e % p.ppc);
+    __syncthreads();
+  }
 
   // this lane's row: window [ls, qi], remote candidates [seg, min(ls, qi + 1))
   const int row = wave * 32 + rl;
@@ -136,13 +176,15 @@ __global__ __launch_bounds__(128, 2) void fwd_kernel(FwdK p) {
   uint4 qf[KS];
   {
     const T* qrow = reinterpret_cast<const T*>(a.q) + (int64_t)b * a.q_sb +
-                    (int64_t)(t0 + (row_ok ? row : 0)) * a.q_st + (int64_t)hq * a.q_sh;
+                    (int64_t)(q0 + t0 + (row_ok ? row : 0)) * a.q_st + (int64_t)hq * a.q_sh;
 #pragma unroll
     for (int ks = 0; ks < KS; ++ks) {
       uint4 w = row_ok ? *reinterpret_cast<const uint4*>(qrow + 16 * ks + 8 * h) : make_uint4(0, 0, 0, 0);
-      uint32_t* ww = reinterpret_cast<uint32_t*>(&w);
+      if constexpr (!PAGED) {
+        uint32_t* ww = reinterpret_cast<uint32_t*>(&w);
 #pragma unroll
-      for (int e = 0; e < 4; ++e) ww[e] = M::pack2(M::lo(ww[e]) * a.scale, M::hi(ww[e]) * a.scale);
+        for (int e = 0; e < 4; ++e) ww[e] = M::pack2(M::lo(ww[e]) * a.scale, M::hi(ww[e]) * a.scale);
+      }
       qf[ks] = w;
     }
   }
@@ -168,18 +210,61 @@ __global__ __launch_bounds__(128, 2) void fwd_kernel(FwdK p) {
   T* sKw = sK + (tid / (D / 8)) * KP + (tid % (D / 8)) * 8;
   T* sVw = sV + (tid / (D / 8)) * VP + (tid % (D / 8)) * 8;
   uint4 kpre[PPT], vpre[PPT];
-  auto fetch = [&](int c) {
-    const uint32_t kso = (uint32_t)c * kChunk * (uint32_t)a.k_st * 2u;
-    const uint32_t vso = (uint32_t)c * kChunk * (uint32_t)a.v_st * 2u;
+  // paged: the kv head's base (uniform) and this thread's column byte offset.
+  // Piece i of a thread covers chunk row tid / (D/8) + i * RPP, whose 16-key
+  // quarter is (i * RPP) / 16 for every thread (tid / (D/8) < RPP <= 16), so
+  // the page of each piece is uniform: its base goes to scalar registers
+  // (readfirstlane) and only a 32-bit in-page offset stays per lane.
+  const char* kpg = reinterpret_cast<const char*>(reinterpret_cast<const T*>(a.k) + (int64_t)kvh * a.k_sh);
+  const char* vpg = reinterpret_cast<const char*>(reinterpret_cast<const T*>(a.v) + (int64_t)kvh * a.v_sh);
+  const uint32_t col_b = (uint32_t)(tid % (D / 8)) * 16u;
+  auto fetch = [&](int u) {
+    const int c = s_chunks[u];
+    if constexpr (PAGED) {
+      static_assert(RPP <= 16 && 16 % RPP == 0, "a piece's quarter must not depend on the thread");
+      // the chunk's (up to) four quarter pages, uniform: from LDS, or past the
+      // held list from the block table
+      int qpg[4];
+      if (u < p.page_cap) {
+        if (p.ppc == 1) {
+          qpg[0] = qpg[1] = qpg[2] = qpg[3] = __builtin_amdgcn_readfirstlane(s_pages[u]);
+        } else {
 #pragma unroll
-    for (int i = 0; i < PPT; ++i) {
-      kpre[i] = buffer_load16(krs, kvo, kso + (uint32_t)(i * RPP) * (uint32_t)a.k_st * 2u);
-      vpre[i] = buffer_load16(vrs, vvo, vso + (uint32_t)(i * RPP) * (uint32_t)a.v_st * 2u);
+          for (int qq = 0; qq < 4; ++qq) qpg[qq] = __builtin_amdgcn_readfirstlane(s_pages[4 * u + qq]);
+        }
+      } else {
+#pragma unroll
+        for (int qq = 0; qq < 4; ++qq) qpg[qq] = __builtin_amdgcn_readfirstlane(page_of(c, qq));
+      }
+#pragma unroll
+      for (int i = 0; i < PPT; ++i) {
+        const int row = tid / (D / 8) + i * RPP;
+        const int j = c * kChunk + row;
+        const int pg = qpg[(i * RPP) >> 4];
+        const uint32_t jr = (uint32_t)(j & (BS - 1));
+        const char* kb = kpg + (int64_t)pg * p.k_pst * (int64_t)sizeof(T);
+        const char* vb = vpg + (int64_t)pg * p.v_pst * (int64_t)sizeof(T);
+        if (j < Skb) {
+          kpre[i] = *reinterpret_cast<const uint4*>(kb + (jr * (uint32_t)a.k_st * (uint32_t)sizeof(T) + col_b));
+          vpre[i] = *reinterpret_cast<const uint4*>(vb + (jr * (uint32_t)a.v_st * (uint32_t)sizeof(T) + col_b));
+        } else {
+          kpre[i] = make_uint4(0, 0, 0, 0);
+          vpre[i] = make_uint4(0, 0, 0, 0);
+        }
+      }
+    } else {
+      const uint32_t kso = (uint32_t)c * kChunk * (uint32_t)a.k_st * 2u;
+      const uint32_t vso = (uint32_t)c * kChunk * (uint32_t)a.v_st * 2u;
+#pragma unroll
+      for (int i = 0; i < PPT; ++i) {
+        kpre[i] = buffer_load16(krs, kvo, kso + (uint32_t)(i * RPP) * (uint32_t)a.k_st * 2u);
+        vpre[i] = buffer_load16(vrs, vvo, vso + (uint32_t)(i * RPP) * (uint32_t)a.v_st * 2u);
+      }
     }
   };
   const uint16_t* v16 = reinterpret_cast<const uint16_t*>(sV);
 
-  if (U > 0) fetch(s_chunks[0]);
+  if (U > 0) fetch(0);
   for (int u = 0; u < U; ++u) {
     const int j0 = (int)s_chunks[u] * kChunk;
     __syncthreads();   // previous chunk fully consumed
@@ -189,7 +274,7 @@ __global__ __launch_bounds__(128, 2) void fwd_kernel(FwdK p) {
       *reinterpret_cast<uint4*>(sVw + i * RPP * VP) = vpre[i];
     }
     __syncthreads();
-    if (u + 1 < U) fetch(s_chunks[u + 1]);
+    if (u + 1 < U) fetch(u + 1);
 
     // the row's selected 16-key quarters of the chunk and their bias
     uint32_t qmem = 0;
@@ -246,7 +331,7 @@ __global__ __launch_bounds__(128, 2) void fwd_kernel(FwdK p) {
       for (int half = 0; half < 2; ++half)
 #pragma unroll
         for (int r = 0; r < 16; ++r) mloc = fmaxf(mloc, st[half][r]);
-      mloc = fmaf(mloc, kLog2e, addb);
+      mloc = fmaf(mloc, l2s, addb);
     } else {
       const uint64_t kh = keep >> (4 * h), rh = rm >> (4 * h);
 #pragma unroll
@@ -255,7 +340,7 @@ __global__ __launch_bounds__(128, 2) void fwd_kernel(FwdK p) {
 #pragma unroll
         for (int r = 0; r < 16; ++r) {
           const int bit = 8 * (r >> 2) + (r & 3);
-          float x = st[half][r] * kLog2e;
+          float x = st[half][r] * l2s;
           if (my_sb) x += ((r32 >> bit) & 1u) ? bq[2 * half + (r >> 3)] : 0.f;
           x = ((k32 >> bit) & 1u) ? x : -INFINITY;
           st[half][r] = x;
@@ -288,7 +373,7 @@ __global__ __launch_bounds__(128, 2) void fwd_kernel(FwdK p) {
       for (int half = 0; half < 2; ++half)
 #pragma unroll
         for (int r = 0; r < 16; ++r) {
-          const float pv = __builtin_amdgcn_exp2f(fmaf(st[half][r], kLog2e, sub));
+          const float pv = __builtin_amdgcn_exp2f(fmaf(st[half][r], l2s, sub));
           st[half][r] = pv;
           psum += pv;
         }
@@ -329,7 +414,7 @@ __global__ __launch_bounds__(128, 2) void fwd_kernel(FwdK p) {
   const float l_tot = l_run + __shfl_xor(l_run, 32, kWave);
   if (!row_ok) return;
   const float inv = l_tot > 0.f ? 1.f / l_tot : 0.f;
-  T* orow = reinterpret_cast<T*>(a.out) + (int64_t)b * a.o_sb + (int64_t)(t0 + row) * a.o_st +
+  T* orow = reinterpret_cast<T*>(a.out) + (int64_t)b * a.o_sb + (int64_t)(q0 + t0 + row) * a.o_st +
             (int64_t)hq * a.o_sh;
 #pragma unroll
   for (int mt = 0; mt < MT; ++mt)
@@ -341,7 +426,7 @@ __global__ __launch_bounds__(128, 2) void fwd_kernel(FwdK p) {
       w.y = M::pack2(o[mt][4 * g + 2] * inv, o[mt][4 * g + 3] * inv);
       *reinterpret_cast<uint2*>(orow + d0) = w;
     }
-  if (a.lse && h == 0)
+  if (!PAGED && a.lse && h == 0)
     a.lse[(int64_t)b * a.lse_sb + (int64_t)(t0 + row) * a.lse_st + (int64_t)hq * a.lse_sh] =
         l_tot > 0.f ? (m_b + log2f(l_tot)) * kLn2 : -INFINITY;
 }
@@ -398,11 +483,11 @@ int check_fwd(const srswa_fwd_args* a) {
   return SRSWA_OK;
 }
 
-template <typename T, int D>
+template <typename T, int D, bool PAGED>
 int launch_fwd(const FwdK& k, size_t smem, hipStream_t st) {
   static LdsGrant granted;
-  if (!ensure_dynamic_lds(&fwd_kernel<T, D>, smem, &granted)) return SRSWA_UNSUPPORTED;
-  hipLaunchKernelGGL((fwd_kernel<T, D>), dim3((unsigned)(8 * k.per_xcd)), dim3(128), smem, st, k);
+  if (!ensure_dynamic_lds(&fwd_kernel<T, D, PAGED>, smem, &granted)) return SRSWA_UNSUPPORTED;
+  hipLaunchKernelGGL((fwd_kernel<T, D, PAGED>), dim3((unsigned)(8 * k.per_xcd)), dim3(128), smem, st, k);
   const hipError_t e = hipGetLastError();
   if (e != hipSuccess) {
     set_error("fwd launch failed: %s", hipGetErrorString(e));
@@ -455,6 +540,111 @@ extern "C" int srswa_gather_fwd(const srswa_fwd_args* a, void* stream) {
   }
   hipStream_t s = reinterpret_cast<hipStream_t>(stream);
   if (a->dtype == SRSWA_BF16)
-    return a->D == 128 ? launch_fwd<bf16_t, 128>(k, smem, s) : launch_fwd<bf16_t, 64>(k, smem, s);
-  return a->D == 128 ? launch_fwd<__half, 128>(k, smem, s) : launch_fwd<__half, 64>(k, smem, s);
+    return a->D == 128 ? launch_fwd<bf16_t, 128, false>(k, smem, s) : launch_fwd<bf16_t, 64, false>(k, smem, s);
+  return a->D == 128 ? launch_fwd<__half, 128, false>(k, smem, s) : launch_fwd<__half, 64, false>(k, smem, s);
+}
+
+extern "C" int srswa_gather_fwd_paged(const srswa_paged_fwd_args* a, void* stream) {
+  if (!a || !a->q || !a->k_cache || !a->v_cache || !a->out || !a->block_table || !a->cu_seqlens_q ||
+      !a->seq_lens || !a->prefix_lens || (!a->topk && a->S > 0)) {
+    set_error("paged fwd: null argument");
+    return SRSWA_INVALID;
+  }
+  if (a->R < 0 || a->max_query_len < 0 || a->HQ <= 0 || a->HKV <= 0 || a->S < 0 || a->max_blocks <= 0 ||
+      a->page_size <= 0 || a->local_blocks < 0) {
+    set_error("paged fwd: bad sizes");
+    return SRSWA_INVALID;
+  }
+  if (a->R == 0 || a->max_query_len == 0) return SRSWA_OK;
+  if (a->HQ % a->HKV) {
+    set_error("paged fwd: HQ must be a multiple of HKV");
+    return SRSWA_UNSUPPORTED;
+  }
+  if (a->dtype != SRSWA_BF16 && a->dtype != SRSWA_F16) {
+    set_error("paged fwd: matrix-core path takes bf16 / fp16");
+    return SRSWA_UNSUPPORTED;
+  }
+  if (!(a->D == 64 || a->D == 128)) {
+    set_error("paged fwd: head dim %d not supported (64, 128)", a->D);
+    return SRSWA_UNSUPPORTED;
+  }
+  if (a->page_size < 16 || (a->page_size & (a->page_size - 1)) || a->S > 64) {
+    set_error("paged fwd: page size must be a power of two >= 16, at most 64 slots");
+    return SRSWA_UNSUPPORTED;
+  }
+  const int64_t keys = (int64_t)a->max_blocks * a->page_size;
+  if (ceil_div((int)std::min<int64_t>(keys, 1 << 30), kChunk) > 65536 || keys > (1 << 30)) {
+    set_error("paged fwd: block table spans more than 4M keys");
+    return SRSWA_UNSUPPORTED;
+  }
+  const int64_t st[] = {a->q_sn, a->q_sh, a->k_sp, a->k_st, a->k_sh, a->v_sp, a->v_st, a->v_sh, a->o_sn, a->o_sh};
+  for (int64_t v : st)
+    if ((v * 2) % 16) {
+      set_error("paged fwd: rows must be 16-byte aligned");
+      return SRSWA_UNSUPPORTED;
+    }
+  if (!al16(a->q) || !al16(a->k_cache) || !al16(a->v_cache) || !al16(a->out)) {
+    set_error("paged fwd: pointers must be 16-byte aligned");
+    return SRSWA_UNSUPPORTED;
+  }
+  FwdK k{};
+  srswa_fwd_args& f = k.a;
+  f.q = a->q;  f.q_sb = 0;  f.q_st = a->q_sn;  f.q_sh = a->q_sh;
+  f.k = a->k_cache;  f.k_sb = 0;  f.k_st = a->k_st;  f.k_sh = a->k_sh;
+  f.v = a->v_cache;  f.v_sb = 0;  f.v_st = a->v_st;  f.v_sh = a->v_sh;
+  f.idx = a->topk;  f.idx_sb = 0;  f.idx_sh = a->t_sh;  f.idx_st = a->t_sn;
+  f.bias = a->bias;  f.bias_sb = 0;  f.bias_sh = a->b_sh;  f.bias_st = a->b_sn;
+  f.seg = nullptr;
+  f.out = a->out;  f.o_sb = 0;  f.o_st = a->o_sn;  f.o_sh = a->o_sh;
+  f.lse = nullptr;
+  f.B = a->R;  f.T = a->max_query_len;  f.Sk = (int)keys;  f.HQ = a->HQ;  f.HKV = a->HKV;  f.HI = a->HKV;
+  f.D = a->D;  f.S = a->S;  f.block_size = a->page_size;  f.local_window = a->local_blocks * a->page_size;
+  f.scale = a->scale;  f.dtype = a->dtype;
+  k.cu = a->cu_seqlens_q;
+  k.prefix = a->prefix_lens;
+  k.seqlen = a->seq_lens;
+  k.bt = a->block_table;
+  k.bt_sr = a->bt_sr;
+  k.k_pst = a->k_sp;
+  k.v_pst = a->v_sp;
+  k.ntiles = ceil_div(a->max_query_len, kTileRows);
+  const int nchunk = ceil_div((int)keys, kChunk);
+  k.nwords = ceil_div(nchunk, 32);
+  k.SP = a->S + 1;
+  k.G = a->HQ / a->HKV;
+  k.IG = k.G;                      // one selection per kv head
+  k.bs_shift = __builtin_ctz((unsigned)a->page_size);
+  const int64_t nlogical = (int64_t)a->R * a->HQ * k.ntiles;
+  if (nlogical > (int64_t)1 << 30) {
+    set_error("paged fwd: too many query tiles");
+    return SRSWA_UNSUPPORTED;
+  }
+  k.nlogical = (int)nlogical;
+  k.per_xcd = ceil_div(k.nlogical, 8);
+  const int64_t per_tile = (int64_t)kTileRows * a->S * (ceil_div(a->page_size, kChunk) + 1) +
+                           ceil_div(f.local_window + kTileRows - 1, kChunk) + 1;
+  const int umax = (int)std::min<int64_t>(nchunk, per_tile);
+  const size_t tile = a->D == 128 ? FwdLds<128>::tileBytes : FwdLds<64>::tileBytes;
+  const size_t setup = (3 * 64 + 4) * 4 + (size_t)k.nwords * 4;
+  size_t n = std::max(tile, setup);
+  k.chunks_off = (int)n;
+  n += ((size_t)umax * 2 + 15) / 16 * 16;
+  k.sid_off = (int)n;
+  n += (size_t)64 * k.SP * 4 * (a->bias ? 2 : 1);
+  // page ids of the visited chunks in the LDS left below 40 KB (four
+  // workgroups per CU), or below 52 KB when the rest already exceeds it
+  k.ppc = a->page_size >= kChunk ? 1 : 4;
+  k.pages_off = (int)((n + 15) / 16 * 16);
+  const size_t budget = k.pages_off <= 40 * 1024 - 64 ? 40 * 1024 : 52 * 1024;
+  k.page_cap = (int)std::min<int64_t>(umax, k.pages_off < (int)budget ? (budget - k.pages_off) / (4 * k.ppc) : 0);
+  n = k.pages_off + (size_t)k.page_cap * 4 * k.ppc;
+  const size_t smem = (n + 15) / 16 * 16;
+  if (smem > 156 * 1024) {
+    set_error("paged fwd: %zu bytes of LDS needed (block table too wide)", smem);
+    return SRSWA_UNSUPPORTED;
+  }
+  hipStream_t s = reinterpret_cast<hipStream_t>(stream);
+  if (a->dtype == SRSWA_BF16)
+    return a->D == 128 ? launch_fwd<bf16_t, 128, true>(k, smem, s) : launch_fwd<bf16_t, 64, true>(k, smem, s);
+  return a->D == 128 ? launch_fwd<__half, 128, true>(k, smem, s) : launch_fwd<__half, 64, true>(k, smem, s);
 }

@@ -92,6 +92,27 @@ class FwdArgs(ctypes.Structure):
     ]
 
 
+class PagedFwdArgs(ctypes.Structure):
+    """Mirror of ``srswa_paged_fwd_args``."""
+
+    _fields_ = [
+        ("q", _vp), ("q_sn", _i64), ("q_sh", _i64),
+        ("k_cache", _vp), ("k_sp", _i64), ("k_st", _i64), ("k_sh", _i64),
+        ("v_cache", _vp), ("v_sp", _i64), ("v_st", _i64), ("v_sh", _i64),
+        ("topk", _vp), ("t_sh", _i64), ("t_sn", _i64),
+        ("bias", _vp), ("b_sh", _i64), ("b_sn", _i64),
+        ("block_table", _vp), ("bt_sr", _i64),
+        ("cu_seqlens_q", _vp),
+        ("seq_lens", _vp),
+        ("prefix_lens", _vp),
+        ("out", _vp), ("o_sn", _i64), ("o_sh", _i64),
+        ("R", _i32), ("max_query_len", _i32), ("HQ", _i32), ("HKV", _i32), ("D", _i32), ("S", _i32),
+        ("max_blocks", _i32), ("page_size", _i32), ("local_blocks", _i32),
+        ("scale", ctypes.c_float),
+        ("dtype", _i32),
+    ]
+
+
 class BwdArgs(ctypes.Structure):
     """Mirror of ``srswa_bwd_args``."""
 
@@ -381,6 +402,7 @@ SIGNATURES = {
     "srswa_topk_rows": (ctypes.c_int, [_vp, _i64, _i32, _i64, _i32, _i32, ctypes.c_float, _vp, _vp,
                                        _i64, _vp]),
     "srswa_gather_fwd": (ctypes.c_int, [ctypes.POINTER(FwdArgs), _vp]),
+    "srswa_gather_fwd_paged": (ctypes.c_int, [ctypes.POINTER(PagedFwdArgs), _vp]),
     "srswa_gather_bwd_workspace": (ctypes.c_size_t, [ctypes.POINTER(BwdArgs)]),
     "srswa_gather_bwd": (ctypes.c_int, [ctypes.POINTER(BwdArgs), _vp, ctypes.c_size_t, _vp]),
     "srswa_block_max_score": (ctypes.c_int, [ctypes.POINTER(BlockMaxArgs), _vp]),
@@ -406,7 +428,7 @@ SIGNATURES = {
 }
 
 STRUCTS = {"srswa_decode_args": DecodeArgs, "srswa_index_args": IndexArgs,
-           "srswa_fwd_args": FwdArgs, "srswa_bwd_args": BwdArgs,
+           "srswa_fwd_args": FwdArgs, "srswa_paged_fwd_args": PagedFwdArgs, "srswa_bwd_args": BwdArgs,
            "srswa_blockmax_args": BlockMaxArgs, "srswa_route_args": RouteArgs,
            "srswa_paged_decode_args": PagedDecodeArgs, "srswa_kbar_pages_args": KbarPagesArgs,
            "srswa_kbar_scores_args": KbarScoresArgs, "srswa_kbar_plan_args": KbarPlanArgs,

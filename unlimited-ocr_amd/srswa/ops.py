@@ -339,6 +339,68 @@ def gather_decode_paged(q, k_cache, v_cache, topk_idx, blk_bias, block_table, se
     return out
 
 
+def gather_fwd_paged(q, k_cache, v_cache, topk_idx, blk_bias, block_table, cu_seqlens_q, seq_lens, prefix_lens,
+                     max_query_len, *, local_blocks, scale, out=None):
+    """Block-sparse prefill over the paged cache (see ``srswa_gather_fwd_paged``).
+
+    q [total_q, HQ, D]; k_cache, v_cache [num_pages, page_size, HKV, D];
+    topk_idx [HKV, total_q, K] block ids (-1 = empty) and blk_bias like it
+    (fp32) or None, both read through their strides (slot stride 1);
+    block_table [R, max_blocks]; cu_seqlens_q [R + 1]; seq_lens, prefix_lens
+    [R]; ``max_query_len`` the longest request (sizes the grid)."""
+    _require_cuda(q, k_cache, v_cache, topk_idx, blk_bias, block_table, cu_seqlens_q, seq_lens, prefix_lens, out)
+    total_q, HQ, D = q.shape
+    npages, page, HKV, Dk = k_cache.shape
+    if Dk != D or tuple(v_cache.shape) != tuple(k_cache.shape):
+        raise ValueError(f"cache shape {tuple(k_cache.shape)} / {tuple(v_cache.shape)} vs q {tuple(q.shape)}")
+    if topk_idx.dim() != 3 or topk_idx.shape[0] != HKV or topk_idx.shape[1] != total_q:
+        raise ValueError(f"topk_idx shape {tuple(topk_idx.shape)} != ({HKV}, {total_q}, K)")
+    if q.dtype != k_cache.dtype or q.dtype != v_cache.dtype:
+        raise ValueError("q, k_cache, v_cache must share a dtype")
+    for t in (q, k_cache, v_cache):
+        if t.stride(-1) != 1:
+            raise UnsupportedShape("head dim must be contiguous")
+    ti = _i32(topk_idx)
+    if ti.stride(-1) != 1:
+        ti = ti.contiguous()
+    bias = None
+    if blk_bias is not None:
+        if tuple(blk_bias.shape) != tuple(topk_idx.shape):
+            raise ValueError(f"blk_bias shape {tuple(blk_bias.shape)} != topk_idx {tuple(topk_idx.shape)}")
+        bias = blk_bias.to(torch.float32)
+        if bias.stride(-1) != 1:
+            bias = bias.contiguous()
+    bt = _i32(block_table)
+    if bt.stride(-1) != 1:
+        bt = bt.contiguous()
+    cu = _i32(cu_seqlens_q).contiguous()
+    sl = _i32(seq_lens).contiguous()
+    pl = _i32(prefix_lens).contiguous()
+    R = sl.numel()
+    if cu.numel() != R + 1 or pl.numel() != R or bt.shape[0] < R:
+        raise ValueError(f"cu_seqlens_q [{cu.numel()}], prefix_lens [{pl.numel()}], block_table rows "
+                         f"{bt.shape[0]} for {R} requests")
+    if out is None:
+        out = torch.empty(total_q, HQ, D, dtype=q.dtype, device=q.device)
+    a = _lib.PagedFwdArgs()
+    a.q = q.data_ptr(); a.q_sn, a.q_sh = q.stride(0), q.stride(1)
+    a.k_cache = k_cache.data_ptr(); a.k_sp, a.k_st, a.k_sh = k_cache.stride(0), k_cache.stride(1), k_cache.stride(2)
+    a.v_cache = v_cache.data_ptr(); a.v_sp, a.v_st, a.v_sh = v_cache.stride(0), v_cache.stride(1), v_cache.stride(2)
+    a.topk = ti.data_ptr(); a.t_sh, a.t_sn = ti.stride(0), ti.stride(1)
+    if bias is not None:
+        a.bias = bias.data_ptr(); a.b_sh, a.b_sn = bias.stride(0), bias.stride(1)
+    a.block_table = bt.data_ptr(); a.bt_sr = bt.stride(0)
+    a.cu_seqlens_q, a.seq_lens, a.prefix_lens = cu.data_ptr(), sl.data_ptr(), pl.data_ptr()
+    a.out = out.data_ptr(); a.o_sn, a.o_sh = out.stride(0), out.stride(1)
+    a.R, a.max_query_len, a.HQ, a.HKV, a.D, a.S = R, int(max_query_len), HQ, HKV, D, ti.shape[-1]
+    a.max_blocks, a.page_size, a.local_blocks = bt.shape[1], page, int(local_blocks)
+    a.scale = float(scale)
+    a.dtype = _lib.dtype_code(q.dtype)
+    _lib.check(_lib.lib().srswa_gather_fwd_paged(ctypes.byref(a), _lib.stream_ptr(q.device)),
+               "srswa_gather_fwd_paged")
+    return out
+
+
 # ---------------------------------------------------------------------------
 # head_cls summary cache over a paged index-key cache
 # ---------------------------------------------------------------------------

@@ -2,7 +2,7 @@
 ``sglang.srt.layers.attention.unlimited_dash_ops`` (WHL!layers/attention/unlimited_dash_ops/),
 module for module, on the MI355X kernels:
 
-* ``attend_triton``       -- ``dash_sparse_attn_decode``
+* ``attend_triton``       -- ``dash_sparse_attn``, ``dash_sparse_attn_decode``
 * ``dash_stage0``         -- ``KBarCache``, ``headcls_scores_prefill``, ``headcls_scores_decode``
 * ``decode_meta_triton``  -- ``decode_meta_fused``, ``decode_allow_fused``, ``cos_sin_2d_fused``,
                              ``local_union_fused``
@@ -15,7 +15,7 @@ module for module, on the MI355X kernels:
 Every tensor the kernels see must live on the GPU (no host path).
 """
 
-from .attend_triton import SPARSE_BLOCK_SIZE, dash_sparse_attn_decode  # noqa: F401
+from .attend_triton import SPARSE_BLOCK_SIZE, dash_sparse_attn, dash_sparse_attn_decode  # noqa: F401
 from .dash_stage0 import KBarCache, headcls_scores_decode, headcls_scores_prefill  # noqa: F401
 from .decode_meta_triton import (  # noqa: F401
     cos_sin_2d_fused, decode_allow_fused, decode_meta_fused, local_union_fused)
