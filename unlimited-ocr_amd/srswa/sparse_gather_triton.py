@@ -7,10 +7,13 @@ the gfx950 HIP kernels of libsrswa.so instead of Triton.  Return conventions
 are the reference's: ``triton_gather_attention`` returns ``None`` for inputs
 the fused path does not take (attention mask present, index-head count not
 tiling the heads, malformed position ids, a dtype/shape the kernels do not
-cover) so the caller falls back to its eager path.  Differences, both
+cover) so the caller falls back to its eager path.  Differences, all
 supersets: a query chunk at the tail of a longer KV cache (q_len < k_len) is
-accepted instead of returning None, and duplicate block ids are collapsed
-inside the kernels (no host-side sort).
+accepted instead of returning None; index heads need only divide the query
+heads (the reference also requires them to divide the kv heads,
+HF/sparse_gather_triton.py:405-407: each query head here picks its own index
+and kv head); and duplicate block ids are collapsed inside the kernels (no
+host-side sort).
 """
 
 from __future__ import annotations
