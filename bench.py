@@ -155,26 +155,28 @@ def bench_decode(args):
     ms_warm = e0.elapsed_time(e1) / args.steps
     _log(f"warm: {args.steps} steps back to back, {ms_warm * 1e3:.2f} us/step (HIP events), "
          f"wall {wall * 1e6 / args.steps:.2f} us/step")
-    # (2) cold (the reported value): before each step a 1 GiB device copy (2 GiB
-    # of traffic, eight times the Infinity Cache) evicts the step's read set, and
-    # each step is timed alone between its own events, the copy outside them.
-    # A real decode step meets its layer's cache cold too: the other layers'
-    # caches pass through between two reads of one layer's.
-    flush_src = torch.empty(1 << 30, dtype=torch.uint8, device=dev).fill_(1)
-    flush_dst = torch.empty_like(flush_src)
-    evs = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(args.steps)]
+    # (2) cold (the reported value): the same K steps back to back, alternating
+    # between two copies of the config-3 instance in different memory (2 x 43 GB).
+    # Each step's 336 MB read set then follows another step's 336 MB of other
+    # data, so the 256 MB Infinity Cache holds none of it; one event pair brackets
+    # all K steps, as in (1).  A real decode step meets its layer's cache cold the
+    # same way: the other layers' caches pass through between two reads of one.
+    _log("cold: cloning the cache into a second instance")
+    kc2, vc2 = c["k_cache"].clone(), c["v_cache"].clone()
+    launch2, _, _ = ops.prepare_gather_decode(
+        c["q"], kc2, vc2, idx, qpos, block_size=BS, local_window=LW, scale=c["scale"])
+    pair = (launch, launch2)
+    for i in range(4):
+        pair[i % 2]()
     torch.cuda.synchronize()
-    for a0, a1 in evs:
-        flush_dst.copy_(flush_src)
-        a0.record(st)
-        launch()
-        a1.record(st)
+    e0.record(st)
+    for i in range(args.steps):
+        pair[i % 2]()
+    e1.record(st)
     torch.cuda.synchronize()
-    per = sorted(a0.elapsed_time(a1) for a0, a1 in evs)
-    ms = sum(per) / len(per)
-    del flush_src, flush_dst
-    _log(f"cold: {args.steps} steps, each after a 1 GiB copy: {ms * 1e3:.2f} us/step mean "
-         f"(median {per[len(per) // 2] * 1e3:.2f}, min {per[0] * 1e3:.2f}, max {per[-1] * 1e3:.2f})")
+    ms = e0.elapsed_time(e1) / args.steps
+    del launch2, pair, kc2, vc2
+    _log(f"cold: {args.steps} steps back to back, alternating two cache instances: {ms * 1e3:.2f} us/step")
     nbytes = W.decode_bytes(B, H, D, K, BS, LW)
     achieved = nbytes / (ms * 1e-3) / 1e9
     res = {
@@ -185,8 +187,8 @@ def bench_decode(args):
         "steps": args.steps,
         "warmup": args.warmup,
         "ms_per_step": ms,
-        "cache": ("cold: each timed step follows a 1 GiB device copy that evicts the 256 MB Infinity "
-                  "Cache; the copy is outside the step's HIP event pair"),
+        "cache": ("cold: the K steps alternate between two copies of the instance in different memory, "
+                  "so each step's 336 MB follows 336 MB of other data and misses the 256 MB Infinity Cache"),
         "warm": {"ms_per_step": ms_warm, "tokens_per_s": B / (ms_warm * 1e-3),
                  "achieved_GBs": nbytes / (ms_warm * 1e-3) / 1e9,
                  "frac": nbytes / (ms_warm * 1e-3) / 1e9 / HBM_PEAK_GBS,
