@@ -379,6 +379,13 @@ __device__ __forceinline__ int find_slot(const srswa_kl_bwd_args& a, int b, int 
   return -1;
 }
 
+// The B operand comes from a_operand_tr, whose lane half h holds the 16-row
+// group's rows 4h .. 4h + 3 and 8 + 4h .. 8 + 4h + 3 (the MFMA output order);
+// the A operand read as 8 contiguous values from LDS must list its k index in
+// that same order, so DS is staged with element x of each 16-group at
+// position slot_of_key(x): bits 2 and 3 swapped.
+__device__ __forceinline__ int slot_of_key(int x) { return (x & ~12) | ((x & 4) << 1) | ((x & 8) >> 1); }
+
 // 16 values ds = rnd(g * dsel[t, slot, k0 .. k0 + 15]) (zeros without a slot)
 template <typename T>
 __device__ __forceinline__ void ds16(const srswa_kl_bwd_args& a, int b, int ih, int t, int slot, int k0,
@@ -486,9 +493,10 @@ __global__ __launch_bounds__(kBwdThreads) void kl_dq_kernel(KlBwdK p) {
       float v[16];
       const int slot = rr < nrows ? find_slot(a, b, ih, t0 + rr, c) : -1;
       ds16<T>(a, b, ih, t0 + rr, slot, kq, v);
+      // keys in the transposing read's order (slot_of_key): 0-3, 8-11 | 4-7, 12-15
       uint4 w0, w1;
-      w0 = make_uint4(M::pack2(v[0], v[1]), M::pack2(v[2], v[3]), M::pack2(v[4], v[5]), M::pack2(v[6], v[7]));
-      w1 = make_uint4(M::pack2(v[8], v[9]), M::pack2(v[10], v[11]), M::pack2(v[12], v[13]), M::pack2(v[14], v[15]));
+      w0 = make_uint4(M::pack2(v[0], v[1]), M::pack2(v[2], v[3]), M::pack2(v[8], v[9]), M::pack2(v[10], v[11]));
+      w1 = make_uint4(M::pack2(v[4], v[5]), M::pack2(v[6], v[7]), M::pack2(v[12], v[13]), M::pack2(v[14], v[15]));
       *reinterpret_cast<uint4*>(sDS + rr * SP + kq) = w0;
       *reinterpret_cast<uint4*>(sDS + rr * SP + kq + 8) = w1;
     }
@@ -544,8 +552,9 @@ __global__ __launch_bounds__(kBwdThreads) void kl_dk_kernel(KlBwdK p) {
           const int slot = rr < nrows ? find_slot(a, b, ih, t0 + rr, c) : -1;
           ds16<T>(a, b, ih, t0 + rr, slot, kq, v);
 #pragma unroll
-          for (int i = 0; i < 16; ++i)
-            reinterpret_cast<uint16_t*>(sDT)[(kq + i) * SP + rr] = (uint16_t)(M::pack2(v[i], 0.f) & 0xffffu);
+          for (int i = 0; i < 16; ++i)   // rows in the transposing read's order (slot_of_key)
+            reinterpret_cast<uint16_t*>(sDT)[(kq + i) * SP + slot_of_key(rr)] =
+                (uint16_t)(M::pack2(v[i], 0.f) & 0xffffu);
         }
         __syncthreads();
         // dK[key, d] += DS^T[key, row] Q[row, d]
