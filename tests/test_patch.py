@@ -87,3 +87,31 @@ def test_patched_functions_on_device(dev):
     assert torch.equal(xi.cpu(), ox) and torch.equal(rv.cpu(), ov)
     assert ((rb.cpu() - ob).abs() <= 1e-5 * ob.abs().clamp(min=1.0)).all()
     assert calls == []
+
+
+def test_select_and_kl_loss_rebinding_host_fallback():
+    """Host tensors reach the indexer's own select_and_kl_loss; restore puts
+    it back."""
+    calls = []
+
+    class DeepseekV2Indexer:
+        block_size = 64
+
+        def select_and_kl_loss(self, hidden_states, query_states, key_states, position_embeddings, position_ids,
+                               scaling, image_token_mask=None, image_token_page_ids=None, query_token_page_ids=None):
+            calls.append((image_token_mask, image_token_page_ids, query_token_page_ids))
+            return "eager-select"
+
+    orig = DeepseekV2Indexer.select_and_kl_loss
+    base = types.ModuleType("_sparse_base_impl")
+    base.DeepseekV2Indexer = DeepseekV2Indexer
+    mod = types.SimpleNamespace(_base=base)
+    assert "DeepseekV2Indexer.select_and_kl_loss" in patch.apply(mod)
+    assert DeepseekV2Indexer.select_and_kl_loss is not orig
+    x = torch.zeros(1, 4, 8)
+    q = torch.zeros(1, 2, 4, 64)
+    got = DeepseekV2Indexer().select_and_kl_loss(x, q, q, None, torch.arange(4)[None], 0.1, image_token_mask="m",
+                                                  image_token_page_ids="p", query_token_page_ids="qp")
+    assert got == "eager-select" and calls == [("m", "p", "qp")]
+    patch.restore(mod)
+    assert DeepseekV2Indexer.select_and_kl_loss is orig

@@ -18,6 +18,8 @@ two kernel files (those are replaced file-for-file by
   ``_uocr_dash_decode_allow`` (HF/modeling_unlimitedocr.py:481-528)
 * ``_KLChunkFn`` (HF/_sparse_base_impl.py:2158-2190), the KL of the indexer
   distillation loss -> ``srswa.kl.KLChunkFn``
+* ``DeepseekV2Indexer.select_and_kl_loss`` (HF/_sparse_base_impl.py:3240-3516),
+  the indexer's training selection and KL -> ``srswa.indexer.select_and_kl_loss``
 
 Every replacement keeps the reference signature and return convention, runs
 the HIP kernels for device tensors, and hands host tensors (or a case the
@@ -29,7 +31,7 @@ from __future__ import annotations
 
 import torch
 
-from . import kl, ops, page_isolation
+from . import indexer, kl, ops, page_isolation
 from ._lib import UnsupportedShape
 
 SCORE_NEG = -1.0e9
@@ -129,6 +131,27 @@ def _kl_chunk(base, done: list) -> None:
     _rebind(base, "_KLChunkFn", make, done, "_KLChunkFn")
 
 
+def _select_and_kl(base, done: list) -> None:
+    indexer_cls = getattr(base, "DeepseekV2Indexer", None)
+    if indexer_cls is None:
+        return
+
+    def make(orig):
+        def select_and_kl_loss(self, hidden_states, query_states, key_states, position_embeddings, position_ids,
+                               scaling, image_token_mask=None, image_token_page_ids=None, query_token_page_ids=None):
+            try:
+                return indexer.select_and_kl_loss(self, hidden_states, query_states, key_states, position_embeddings,
+                                                  position_ids, scaling, image_token_mask, image_token_page_ids,
+                                                  query_token_page_ids, pk=getattr(base, "_pk", None))
+            except UnsupportedShape:
+                pass
+            return orig(self, hidden_states, query_states, key_states, position_embeddings, position_ids, scaling,
+                        image_token_mask=image_token_mask, image_token_page_ids=image_token_page_ids,
+                        query_token_page_ids=query_token_page_ids)
+        return select_and_kl_loss
+    _rebind(indexer_cls, "select_and_kl_loss", make, done, "DeepseekV2Indexer.select_and_kl_loss")
+
+
 def apply(modeling_deepseekv2, modeling_unlimitedocr=None) -> list:
     """Rebind the hot-path functions of a loaded ``modeling_deepseekv2`` module
     (the reference's DASH overlay), of its ``_sparse_base_impl`` (``_base``)
@@ -138,6 +161,7 @@ def apply(modeling_deepseekv2, modeling_unlimitedocr=None) -> list:
     done = []
     _page_isolation(mod, getattr(mod, "_base", None), done)
     _kl_chunk(getattr(mod, "_base", None), done)
+    _select_and_kl(getattr(mod, "_base", None), done)
     if modeling_unlimitedocr is not None:
         def make_allow(orig):
             def _uocr_dash_decode_allow(indexer, input_ids, cache):
@@ -205,6 +229,7 @@ def restore(modeling_deepseekv2, modeling_unlimitedocr=None) -> None:
     mod = modeling_deepseekv2
     base = getattr(mod, "_base", None)
     for owner, name in ((getattr(base, "DeepseekV2Indexer", None), "_build_kl_candidate_mask"),
+                        (getattr(base, "DeepseekV2Indexer", None), "select_and_kl_loss"),
                         (getattr(base, "DeepseekV2IndexerRotary2D", None), "forward"),
                         (base, "_llama_apply_rotary_pos_emb"), (mod, "_llama_apply_rotary_pos_emb"),
                         (base, "_KLChunkFn"),
