@@ -497,6 +497,61 @@ def block_max_scores(q, k, pos, seg, block_size, num_key_blocks, local_window=No
     return s.view(B, C, nblk, bs).amax(-1)
 
 
+def indexer_forward_ids(idx_q, idx_k, position_ids, block_size, local_window, topk, chunk=0, img_blk=None):
+    """``DeepseekV2Indexer.forward`` (HF/_sparse_base_impl.py:3065-3105) from its
+    projections: idx_q [B, HI, T, d], idx_k [B, 1, Sk, d], position_ids [B, T];
+    per chunk the q . k scores with future and local-window keys at -inf,
+    padded to whole blocks, block amax; blocks outside ``img_blk`` [B, nblk]
+    (bool, or None) at -inf; then the top-k (ties -> lower id), -1 where -inf.
+    int64 [B, HI, T, topk]."""
+    B, HI, T, _ = idx_q.shape
+    Sk = idx_k.shape[2]
+    nblk = -(-Sk // block_size)
+    kpos = torch.arange(Sk)
+    step = chunk if chunk and chunk > 0 else T
+    out = []
+    for c0 in range(0, T, step):
+        c1 = min(c0 + step, T)
+        sc = torch.matmul(idx_q[:, :, c0:c1], idx_k.transpose(-1, -2))
+        pos = position_ids[:, c0:c1].long()
+        future = kpos[None, None, None, :] > pos[:, None, :, None]
+        start = (pos - (local_window - 1)).clamp(min=0)
+        local = (kpos[None, None, None, :] >= start[:, None, :, None]) & (kpos[None, None, None, :] <= pos[:, None, :, None])
+        sc = sc.masked_fill(future | local, float("-inf"))
+        pad = nblk * block_size - Sk
+        if pad:
+            sc = torch.nn.functional.pad(sc, (0, pad), value=float("-inf"))
+        out.append(sc.view(B, HI, c1 - c0, nblk, block_size).amax(-1))
+    bsc = torch.cat(out, dim=2)
+    if img_blk is not None:
+        bsc = bsc.masked_fill(~img_blk[:, None, None, :], float("-inf"))
+    if topk == 0:
+        return torch.empty(B, HI, T, 0, dtype=torch.long)
+    return topk_blocks(bsc, topk, invalid_at=float("-inf")), bsc
+
+
+def indexer_infer_block_scores(idx_q, idx_k, q_pos, nblk, block_size, local_window, q_chunk=2048):
+    """The stage0 == "indexer" branch of ``_block_scores_infer``
+    (HF/modeling_deepseekv2.py:419-430): idx_q [B, Lq, d], idx_k [B, S, d],
+    q_pos [B, Lq]; q . k clamped to +-ACT_CLAMP, future keys and keys
+    j > pos - local_window at SCORE_NEG, padded with SCORE_NEG to nblk blocks,
+    block amax.  [B, Lq, nblk]."""
+    B, S, _ = idx_k.shape
+    kpos = torch.arange(S)
+    out = []
+    for c0 in range(0, idx_q.shape[1], q_chunk):
+        c1 = min(c0 + q_chunk, idx_q.shape[1])
+        sc = torch.matmul(idx_q[:, c0:c1], idx_k.transpose(-1, -2)).clamp(-ACT_CLAMP, ACT_CLAMP)
+        pos = q_pos[:, c0:c1].long()
+        future = kpos[None, None, :] > pos[:, :, None]
+        local = (kpos[None, None, :] > (pos[:, :, None] - local_window)) & ~future
+        sc = sc.masked_fill(future | local, SCORE_NEG)
+        if nblk * block_size > S:
+            sc = torch.nn.functional.pad(sc, (0, nblk * block_size - S), value=SCORE_NEG)
+        out.append(sc.view(B, c1 - c0, nblk, block_size).amax(-1))
+    return torch.cat(out, dim=1)
+
+
 def topk_blocks(scores, k, invalid_at=SCORE_NEG * 0.5):
     """k best blocks per row: descending score, ties -> lower block id.
 
@@ -508,7 +563,8 @@ def topk_blocks(scores, k, invalid_at=SCORE_NEG * 0.5):
     """
     n = scores.shape[-1]
     kk = min(int(k), n)
-    s = torch.nan_to_num(scores.double(), nan=float("-inf"))
+    s = scores.double()
+    s = torch.where(torch.isnan(s), torch.full((), float("-inf"), dtype=s.dtype), s)   # +-inf kept as they are
     order = torch.sort(-s, dim=-1, stable=True).indices[..., :kk]
     top = s.gather(-1, order)
     out = order.masked_fill(~(top > invalid_at), -1)
@@ -524,7 +580,8 @@ def near_tie_rows(scores, k, rel=1e-4, invalid_at=SCORE_NEG * 0.5, floor=1.0):
     fp32 summation order and bit-exact comparison is reported separately.
     ``floor`` = 1 for scores of order one and above; 0 makes the gap purely
     relative (scores far below one, e.g. config 1's 1/sqrt(D)-scaled inputs)."""
-    s = torch.nan_to_num(scores.double(), nan=float("-inf"))
+    s = scores.double()
+    s = torch.where(torch.isnan(s), torch.full((), float("-inf"), dtype=s.dtype), s)   # +-inf kept as they are
     s = torch.where(s > invalid_at, s, torch.full((), float("-inf"), dtype=s.dtype))
     n = s.shape[-1]
     if k >= n:

@@ -652,3 +652,52 @@ def test_paged_prefill_no_window_is_causal_selected_keys():
     kv = torch.stack([kc[bt[0, 0], j, 0] for j in range(16)])
     vv = torch.stack([vc[bt[0, 0], j, 0] for j in range(16)])
     assert (got[1, 0] - torch.softmax(kv @ q[1, 0], 0) @ vv).abs().max() < 1e-12
+
+
+def test_indexer_forward_ids_equal_block_max_topk():
+    """DeepseekV2Indexer.forward's dense chunked form equals the block-max
+    restatement (itself pinned by brute force) followed by the tie-ordered
+    top-k, for any chunking, with and without the image-block mask."""
+    g = torch.Generator().manual_seed(31)
+    B, HI, T, Sk, d, bs, lw, K = 2, 2, 40, 150, 8, 16, 20, 4
+    q = _rand(B, HI, T, d, g=g)
+    k = _rand(B, 1, Sk, d, g=g)
+    pos = torch.stack([torch.randperm(Sk, generator=g)[:T] for _ in range(B)])
+    nblk = -(-Sk // bs)
+    img = torch.rand(B, nblk, generator=g) < 0.5
+    for chunk, ib in ((0, None), (7, None), (13, img)):
+        ids, bsc = O.indexer_forward_ids(q, k, pos, bs, lw, K, chunk=chunk, img_blk=ib)
+        ref = O.block_max_scores(q.reshape(B * HI, T, d), k.expand(B, HI, Sk, d).reshape(B * HI, Sk, d),
+                                 pos.repeat_interleave(HI, 0), torch.zeros(B * HI, T, dtype=torch.long), bs, nblk,
+                                 lw).view(B, HI, T, nblk)
+        if ib is not None:
+            ref = ref.masked_fill(~ib[:, None, None, :], float("-inf"))
+        assert torch.equal(bsc, ref)
+        assert torch.equal(ids, O.topk_blocks(ref, K, invalid_at=float("-inf")))
+    assert (ids == -1).any() and (ids >= 0).any()
+
+
+def test_indexer_infer_scores_equal_clamped_block_max():
+    """The stage0 "indexer" scores: block-max over keys j <= pos - LW (the
+    block-max restatement with seg 0), clamped to +-1e4, SCORE_NEG for blocks
+    without a key; the clamp is exercised with scaled-up inputs."""
+    g = torch.Generator().manual_seed(32)
+    B, Lq, S, d, bs, lw = 2, 30, 120, 8, 16, 24
+    for scale in (1.0, 200.0):
+        q = _rand(B, Lq, d, g=g) * scale
+        k = _rand(B, S, d, g=g) * scale
+        pos = torch.randint(0, S, (B, Lq), generator=g)
+        nblk = -(-S // bs) + 1
+        got = O.indexer_infer_block_scores(q, k, pos, nblk, bs, lw, q_chunk=11)
+        bm = O.block_max_scores(q, k, pos, torch.zeros_like(pos), bs, nblk, lw)
+        want = torch.where(torch.isinf(bm), torch.full_like(bm, O.SCORE_NEG), bm.clamp(-O.ACT_CLAMP, O.ACT_CLAMP))
+        assert torch.equal(got, want)
+    assert (got == O.ACT_CLAMP).any() and (got == O.SCORE_NEG).any()
+
+
+def test_topk_blocks_invalid_at_minus_inf():
+    """With invalid_at = -inf only -inf and NaN entries are invalid; -1e30 is
+    a valid score (so -inf must not be mapped to the most negative float)."""
+    s = torch.tensor([[-1e30, float("-inf"), float("nan"), -2e30, float("-inf")]], dtype=torch.float64)
+    assert O.topk_blocks(s, 4, invalid_at=float("-inf")).tolist() == [[0, 3, -1, -1]]
+    assert not O.near_tie_rows(s, 2, invalid_at=float("-inf")).any()

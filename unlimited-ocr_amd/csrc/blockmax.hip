@@ -15,8 +15,12 @@
 // K Q^T on v_mfma_f32_32x32x16; a chunk every row of the wave scores whole
 // skips the per-key masking; chunks past the tile's last remote key are
 // skipped and their blocks written as -inf.  No dense [B, C, Sk] score tensor
-// exists.
+// exists.  fp32 operands (the inference router's fp32 index q / k,
+// HF/modeling_deepseekv2.py:419-430) run the same tiling on
+// v_mfma_f32_32x32x2_f32: lane half h supplies head-dim elements 8m + 4h .. +3
+// of step group m to both operands, from one 16-byte read each.
 #include <algorithm>
+#include <type_traits>
 
 #include "mfma_common.h"
 
@@ -32,11 +36,53 @@ struct BmaxK {
   int nslab, slab_chunks;   // key slabs per (sequence, tile); chunks per slab (whole blocks)
 };
 
+// S^T tile (keys x 32 rows) of one 32-key half from the staged chunk
+template <typename T, int D> struct BmaxMac {
+  static constexpr int EPP = 8;                       // elements per 16-byte piece
+  static constexpr int KP = D + 8;
+  static constexpr int NQ = D / 16;                   // query fragments (uint4) per lane
+  __device__ __forceinline__ static void load_q(uint4* qf, const T* qrow, int h, bool ok) {
+#pragma unroll
+    for (int ks = 0; ks < NQ; ++ks)
+      qf[ks] = ok ? *reinterpret_cast<const uint4*>(qrow + 16 * ks + 8 * h) : make_uint4(0, 0, 0, 0);
+  }
+  __device__ __forceinline__ static f32x16_t tile(const T* sK, int key, const uint4* qf, int h) {
+    f32x16_t s = zero16();
+#pragma unroll
+    for (int ks = 0; ks < NQ; ++ks)
+      s = Mfma<T>::mac(*reinterpret_cast<const uint4*>(sK + key * KP + 16 * ks + 8 * h), qf[ks], s);
+    return s;
+  }
+};
+template <int D> struct BmaxMac<float, D> {
+  static constexpr int EPP = 4;
+  static constexpr int KP = D + 4;
+  static constexpr int NQ = D / 8;
+  __device__ __forceinline__ static void load_q(uint4* qf, const float* qrow, int h, bool ok) {
+#pragma unroll
+    for (int m = 0; m < NQ; ++m)
+      qf[m] = ok ? *reinterpret_cast<const uint4*>(qrow + 8 * m + 4 * h) : make_uint4(0, 0, 0, 0);
+  }
+  __device__ __forceinline__ static f32x16_t tile(const float* sK, int key, const uint4* qf, int h) {
+    f32x16_t s = zero16();
+#pragma unroll
+    for (int m = 0; m < NQ; ++m) {
+      const float4 kv = *reinterpret_cast<const float4*>(sK + key * KP + 8 * m + 4 * h);
+      const float4 qv = __builtin_bit_cast(float4, qf[m]);
+      s = __builtin_amdgcn_mfma_f32_32x32x2f32(kv.x, qv.x, s, 0, 0, 0);
+      s = __builtin_amdgcn_mfma_f32_32x32x2f32(kv.y, qv.y, s, 0, 0, 0);
+      s = __builtin_amdgcn_mfma_f32_32x32x2f32(kv.z, qv.z, s, 0, 0, 0);
+      s = __builtin_amdgcn_mfma_f32_32x32x2f32(kv.w, qv.w, s, 0, 0, 0);
+    }
+    return s;
+  }
+};
+
 template <typename T, int D>
 __global__ __launch_bounds__(kBmaxThreads) void block_max_kernel(BmaxK p) {
-  using M = Mfma<T>;
-  constexpr int KP = D + 8;
-  constexpr int KS = D / 16;
+  using MC = BmaxMac<T, D>;
+  constexpr int KP = MC::KP;
+  constexpr int EPP = MC::EPP;
   __shared__ __align__(16) T sK[kChunk * KP];
   __shared__ int s_maxls;
   const srswa_blockmax_args& a = p.a;
@@ -69,25 +115,21 @@ __global__ __launch_bounds__(kBmaxThreads) void block_max_kernel(BmaxK p) {
   const int blk_lo = c_lo * kChunk / BS;
   const int blk_hi = slab == p.nslab - 1 ? a.nblk : min(a.nblk, (c_lo + p.slab_chunks) * kChunk / BS);
 
-  uint4 qf[KS];
-  {
-    const T* qrow = reinterpret_cast<const T*>(a.q) + (int64_t)b * a.q_sb + (int64_t)(row_ok ? row : 0) * a.q_sc;
-#pragma unroll
-    for (int ks = 0; ks < KS; ++ks)
-      qf[ks] = row_ok ? *reinterpret_cast<const uint4*>(qrow + 16 * ks + 8 * h) : make_uint4(0, 0, 0, 0);
-  }
+  uint4 qf[MC::NQ];
+  MC::load_q(qf, reinterpret_cast<const T*>(a.q) + (int64_t)b * a.q_sb + (int64_t)(row_ok ? row : 0) * a.q_sc, h,
+             row_ok);
   float* orow = a.out + (int64_t)b * a.o_sb + (int64_t)(row_ok ? row : 0) * a.o_sc;
   const T* kg = reinterpret_cast<const T*>(a.k) + (int64_t)b * a.k_sb;
-  constexpr int PIECES = kChunk * D / 8;          // 16-byte pieces of a chunk
-  constexpr int PPT = PIECES / kBmaxThreads;      // per thread
+  constexpr int PR = D / EPP;                     // 16-byte pieces per key row
+  constexpr int PPT = kChunk * PR / kBmaxThreads; // per thread
   float run = -INFINITY;                          // running max of the open block (BS >= 64)
   uint4 pre[PPT];
   auto fetch = [&](int c) {
 #pragma unroll
     for (int i = 0; i < PPT; ++i) {
       const int pc = tid + kBmaxThreads * i;
-      const int j = c * kChunk + pc / (D / 8), col = pc % (D / 8);
-      pre[i] = j < a.Sk ? *reinterpret_cast<const uint4*>(kg + (int64_t)j * a.k_sk + col * 8)
+      const int j = c * kChunk + pc / PR, col = pc % PR;
+      pre[i] = j < a.Sk ? *reinterpret_cast<const uint4*>(kg + (int64_t)j * a.k_sk + col * EPP)
                         : make_uint4(0, 0, 0, 0);
     }
   };
@@ -99,16 +141,12 @@ __global__ __launch_bounds__(kBmaxThreads) void block_max_kernel(BmaxK p) {
 #pragma unroll
     for (int i = 0; i < PPT; ++i) {
       const int pc = tid + kBmaxThreads * i;
-      *reinterpret_cast<uint4*>(sK + (pc / (D / 8)) * KP + (pc % (D / 8)) * 8) = pre[i];
+      *reinterpret_cast<uint4*>(sK + (pc / PR) * KP + (pc % PR) * EPP) = pre[i];
     }
     __syncthreads();
     if (c + 1 < c_hi) fetch(c + 1);
-    f32x16_t s0 = zero16(), s1 = zero16();
-#pragma unroll
-    for (int ks = 0; ks < KS; ++ks) {
-      s0 = M::mac(*reinterpret_cast<const uint4*>(sK + rl * KP + 16 * ks + 8 * h), qf[ks], s0);
-      s1 = M::mac(*reinterpret_cast<const uint4*>(sK + (32 + rl) * KP + 16 * ks + 8 * h), qf[ks], s1);
-    }
+    const f32x16_t s0 = MC::tile(sK, rl, qf, h);
+    const f32x16_t s1 = MC::tile(sK, 32 + rl, qf, h);
     // every row of the wave scores the whole chunk: no per-key masks
     const bool whole = __all(!row_ok || (j0 >= seg && j0 + kChunk <= ls));
     if (BS >= kChunk) {
@@ -186,10 +224,11 @@ extern "C" int srswa_block_max_score(const srswa_blockmax_args* a, void* stream)
     return SRSWA_INVALID;
   }
   if (a->B == 0 || a->C == 0 || a->nblk == 0) return SRSWA_OK;
-  if (a->dtype != SRSWA_BF16 && a->dtype != SRSWA_F16) {
-    set_error("block max: matrix-core path takes bf16 / fp16");
+  if (a->dtype != SRSWA_BF16 && a->dtype != SRSWA_F16 && a->dtype != SRSWA_F32) {
+    set_error("block max: dtype %d not supported (bf16, fp16, fp32)", a->dtype);
     return SRSWA_UNSUPPORTED;
   }
+  const int64_t eb = a->dtype == SRSWA_F32 ? 4 : 2;
   if (!(a->D == 64 || a->D == 128)) {
     set_error("block max: head dim %d not supported", a->D);
     return SRSWA_UNSUPPORTED;
@@ -199,8 +238,8 @@ extern "C" int srswa_block_max_score(const srswa_blockmax_args* a, void* stream)
     set_error("block max: block size must be 16, 32 or a multiple of 64");
     return SRSWA_UNSUPPORTED;
   }
-  if (((uintptr_t)a->q & 15) || ((uintptr_t)a->k & 15) || (a->q_sb * 2) % 16 || (a->q_sc * 2) % 16 ||
-      (a->k_sb * 2) % 16 || (a->k_sk * 2) % 16) {
+  if (((uintptr_t)a->q & 15) || ((uintptr_t)a->k & 15) || (a->q_sb * eb) % 16 || (a->q_sc * eb) % 16 ||
+      (a->k_sb * eb) % 16 || (a->k_sk * eb) % 16) {
     set_error("block max: rows must be 16-byte aligned");
     return SRSWA_UNSUPPORTED;
   }
@@ -217,5 +256,6 @@ extern "C" int srswa_block_max_score(const srswa_blockmax_args* a, void* stream)
   }
   hipStream_t s = reinterpret_cast<hipStream_t>(stream);
   if (a->dtype == SRSWA_BF16) return a->D == 128 ? launch_bmax<bf16_t, 128>(k, s) : launch_bmax<bf16_t, 64>(k, s);
+  if (a->dtype == SRSWA_F32) return a->D == 128 ? launch_bmax<float, 128>(k, s) : launch_bmax<float, 64>(k, s);
   return a->D == 128 ? launch_bmax<__half, 128>(k, s) : launch_bmax<__half, 64>(k, s);
 }

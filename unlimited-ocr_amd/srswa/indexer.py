@@ -1,8 +1,14 @@
-"""The indexer's training step on the MI355X kernels: block selection and the
-distillation KL of ``DeepseekV2Indexer.select_and_kl_loss``
-(HF/_sparse_base_impl.py:3240-3516).
+"""The indexer's block selection on the MI355X kernels.
 
-Per query chunk (``kl_chunk_size`` rows):
+* ``indexer_forward`` -- ``DeepseekV2Indexer.forward``
+  (HF/_sparse_base_impl.py:3065-3105): remote top-k block ids per query from
+  the block-max scores, with the image-bucket block mask.
+* ``block_scores_indexer`` -- the stage0 == "indexer" branch of the
+  inference router's ``_block_scores_infer`` (HF/modeling_deepseekv2.py:419-430).
+* ``select_and_kl_loss`` -- the training step's selection and distillation KL
+  (HF/_sparse_base_impl.py:3240-3516), below.
+
+``select_and_kl_loss``, per query chunk (``kl_chunk_size`` rows):
 
 1. block scores -- ``srswa_block_max_score``: max over each 64-key block of
    the index logits over causal, non-local, same-sample keys (:3319-3348; the
@@ -36,6 +42,66 @@ from . import ops
 from ._lib import UnsupportedShape
 
 _DTYPES = (torch.bfloat16, torch.float16)
+SCORE_NEG = -1.0e9
+ACT_CLAMP = 1.0e4
+
+
+def _fold_heads(idx_q, idx_k):
+    """(q [B*HI, T, d], keys [B*HI, Sk, d]) of idx_q [B, HI, T, d] and the
+    shared idx_k [B, 1, Sk, d]."""
+    B, HI, T, D = idx_q.shape
+    Sk = idx_k.shape[2]
+    keys = idx_k[:, 0] if HI == 1 else idx_k.expand(B, HI, Sk, D).reshape(B * HI, Sk, D)
+    return idx_q.reshape(B * HI, T, D), keys
+
+
+@torch.no_grad()
+def indexer_forward(self, hidden_states, position_embeddings, past_key_values, position_ids, image_token_mask=None):
+    """int64 [B, HI, q_len, topk] remote block ids of ``DeepseekV2Indexer.forward``
+    (``self`` the indexer): the block max of q . k over each block's keys below
+    the query's token window (j < max(pos - local_window + 1, 0)), image-bucket
+    blocks only when the indexer is so configured (a row may then select
+    nothing), then the top-k, -1 where the score is -inf.  The reference's
+    per-chunk loop is one launch here (the rows are independent).  Raises
+    UnsupportedShape for what the kernels do not take."""
+    del position_embeddings                 # the reference projects without them as well (:3070)
+    if not hidden_states.is_cuda:
+        raise UnsupportedShape("indexer forward: host tensors")
+    bs = int(self.block_size)
+    idx_q, idx_k = self._project_index_qk(hidden_states, position_ids, past_key_values)
+    if idx_q.dtype != idx_k.dtype or idx_q.dtype not in (torch.bfloat16, torch.float16, torch.float32):
+        raise UnsupportedShape("indexer forward: index q / k dtype")
+    B, HI, T, D = idx_q.shape
+    k_len = int(idx_k.shape[2])
+    nblk = -(-k_len // bs)
+    topk = self._remote_topk(nblk)
+    if topk == 0:
+        return torch.empty(B, HI, T, 0, dtype=torch.long, device=idx_q.device)
+    q, keys = _fold_heads(idx_q, idx_k)
+    pos = position_ids.to(idx_q.device)
+    posh = pos.unsqueeze(1).expand(B, HI, T).reshape(B * HI, T)
+    sc = ops.block_max_score(q, keys, posh, None, block_size=bs, num_key_blocks=nblk,
+                             local_window=self.local_window).view(B, HI, T, nblk)
+    if self.image_bucket_constraint and image_token_mask is not None:
+        img_blk = self._build_image_block_allow_mask(image_token_mask, nblk)
+        sc = sc.masked_fill(~img_blk[:, None, None, :], float("-inf"))
+    return ops.topk_rows(sc, topk, invalid_at=float("-inf")).long()
+
+
+@torch.no_grad()
+def block_scores_indexer(router, idx_q, idx_k, q_pos, nblk):
+    """[B, Lq, nblk] fp32 scores of the stage0 == "indexer" router: per block
+    the max of q . k (clamped to +-1e4) over its keys j <= pos - local_window,
+    SCORE_NEG for a block without one.  idx_q [B, Lq, d], idx_k [B, S, d]
+    (the router's fp32 q / k; bf16 / fp16 also taken), q_pos [B, Lq]."""
+    if not idx_q.is_cuda:
+        raise UnsupportedShape("block scores: host tensors")
+    S = int(idx_k.shape[1])
+    if int(nblk) * int(router.block_size) < S:
+        raise UnsupportedShape("block scores: nblk blocks do not cover the keys")
+    sc = ops.block_max_score(idx_q, idx_k, q_pos, None, block_size=int(router.block_size), num_key_blocks=int(nblk),
+                             local_window=int(router.local_window))
+    return torch.where(sc == float("-inf"), torch.full_like(sc, SCORE_NEG), sc.clamp(-ACT_CLAMP, ACT_CLAMP))
 
 
 def _is_packed(position_ids) -> bool:

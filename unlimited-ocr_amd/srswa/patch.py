@@ -7,8 +7,10 @@ two kernel files (those are replaced file-for-file by
 ``srswa.sparse_gather_triton`` / ``srswa.sparse_gather_e2e_triton``):
 
 * ``_decode_attend``       (HF/modeling_deepseekv2.py:454-481) -> ``srswa.ops.decode_attend``
-* ``_block_scores_infer``  (HF/modeling_deepseekv2.py:380-430), stage0 "head_cls"
-                           -> the head_cls / mean-pool indexer kernel
+* ``_block_scores_infer``  (HF/modeling_deepseekv2.py:380-430): stage0 "head_cls"
+                           -> the head_cls / mean-pool indexer kernel; stage0
+                           "indexer" -> the block-max kernel
+                           (``srswa.indexer.block_scores_indexer``)
 * ``_infer_route_select``  (HF/modeling_deepseekv2.py:338-362) -> ``srswa.ops.dash_route``
 * page isolation and the Page2D indexer RoPE of ``_sparse_base_impl`` (reached as
   ``modeling_deepseekv2._base``): ``DeepseekV2Indexer._build_kl_candidate_mask``
@@ -19,7 +21,9 @@ two kernel files (those are replaced file-for-file by
 * ``_KLChunkFn`` (HF/_sparse_base_impl.py:2158-2190), the KL of the indexer
   distillation loss -> ``srswa.kl.KLChunkFn``
 * ``DeepseekV2Indexer.select_and_kl_loss`` (HF/_sparse_base_impl.py:3240-3516),
-  the indexer's training selection and KL -> ``srswa.indexer.select_and_kl_loss``
+  the indexer's training selection and KL -> ``srswa.indexer.select_and_kl_loss``,
+  and ``DeepseekV2Indexer.forward`` (:3065-3105), its block selection
+  -> ``srswa.indexer.indexer_forward``
 
 Every replacement keeps the reference signature and return convention, runs
 the HIP kernels for device tensors, and hands host tensors (or a case the
@@ -151,6 +155,18 @@ def _select_and_kl(base, done: list) -> None:
         return select_and_kl_loss
     _rebind(indexer_cls, "select_and_kl_loss", make, done, "DeepseekV2Indexer.select_and_kl_loss")
 
+    def make_fwd(orig):
+        def forward(self, hidden_states, position_embeddings, past_key_values, position_ids, image_token_mask=None):
+            try:
+                return indexer.indexer_forward(self, hidden_states, position_embeddings, past_key_values,
+                                               position_ids, image_token_mask)
+            except UnsupportedShape:
+                pass
+            return orig(self, hidden_states, position_embeddings, past_key_values, position_ids,
+                        image_token_mask=image_token_mask)
+        return forward
+    _rebind(indexer_cls, "forward", make_fwd, done, "DeepseekV2Indexer.forward")
+
 
 def apply(modeling_deepseekv2, modeling_unlimitedocr=None) -> list:
     """Rebind the hot-path functions of a loaded ``modeling_deepseekv2`` module
@@ -194,12 +210,18 @@ def apply(modeling_deepseekv2, modeling_unlimitedocr=None) -> list:
         mod._srswa_orig_block_scores_infer = orig_scores
 
         def _block_scores_infer(router, idx_q, idx_k, q_pos, nblk):
-            if idx_q.is_cuda and getattr(router, "stage0", None) == "head_cls":
+            stage0 = getattr(router, "stage0", None)
+            if idx_q.is_cuda and stage0 == "head_cls":
                 try:
                     hc = router.head_cls.detach().float()
                     hc = None if not bool(hc.any()) else hc      # zero head_cls == mean pooling
                     return head_cls_block_scores(idx_q, idx_k, q_pos, nblk, router.block_size,
                                                  router.local_blocks, hc)
+                except UnsupportedShape:
+                    pass
+            elif idx_q.is_cuda and stage0 == "indexer":
+                try:
+                    return indexer.block_scores_indexer(router, idx_q, idx_k, q_pos, nblk)
                 except UnsupportedShape:
                     pass
             return orig_scores(router, idx_q, idx_k, q_pos, nblk)
@@ -230,6 +252,7 @@ def restore(modeling_deepseekv2, modeling_unlimitedocr=None) -> None:
     base = getattr(mod, "_base", None)
     for owner, name in ((getattr(base, "DeepseekV2Indexer", None), "_build_kl_candidate_mask"),
                         (getattr(base, "DeepseekV2Indexer", None), "select_and_kl_loss"),
+                        (getattr(base, "DeepseekV2Indexer", None), "forward"),
                         (getattr(base, "DeepseekV2IndexerRotary2D", None), "forward"),
                         (base, "_llama_apply_rotary_pos_emb"), (mod, "_llama_apply_rotary_pos_emb"),
                         (base, "_KLChunkFn"),
