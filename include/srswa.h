@@ -436,6 +436,71 @@ typedef struct {
 int srswa_win_bounds(const srswa_win_bounds_args* a, void* stream);
 
 /* ------------------------------------------------------------------------
+ * Training DASH router (DashAttention._route / _select_and_bias,
+ * HF/dash_attention.py:1145-1204, with entmax15 :764-810), forward and
+ * backward, one query row per wavefront.  Values are computed in fp32 from
+ * the storage dtype (fp32 / bf16 / fp16), rounded to it where the reference's
+ * tensors are; the 1.5-entmax threshold in fp64.
+ *
+ * route (forward): remote = score > -5e8; cand = remote & block_cand[row]
+ *   (given) or remote & img[row / rows_per_seq] (given), a row without one
+ *   falls back to remote; x = cand ? rnd(score * scale) : rnd(neg);
+ *   z = rnd(x - max x) / 2; prior = rnd(max(z - tau, 0)^2) with tau the exact
+ *   1.5-entmax threshold (sum over z > tau of (z - tau)^2 = 1: the sorted
+ *   candidates' closed form, support = the ranks where it holds).
+ * route (backward): g = rnd(sqrt(prior)); dx = rnd(dprior * g);
+ *   q = rnd(sum dx) / max(rnd(sum g), 1e-12); dscore = cand ?
+ *   rnd(rnd(dx - rnd(q g)) * scale) : 0.
+ * select (forward): the K largest of sel = cand ? prior : -1 (ties -> lower
+ *   block id); valid = topv >= 0; logp = rnd(log(rnd(max(topv, floor))));
+ *   mu = rnd(rnd(sum_valid logp) / max(n_valid, 1));
+ *   bias = valid ? clamp(rnd(rnd(logp - mu) * inv_sigma), +-1e4) : 0.
+ * select (backward): u = valid & |bias| <= 1e4 ? dbias * inv_sigma : 0;
+ *   dlogp = u - valid * sum(u) / n; dprior[topi] = topv >= floor ?
+ *   dlogp / rnd(max(topv, floor)) : 0, every other block 0 (a dense row).
+ * ---------------------------------------------------------------------- */
+typedef struct {
+  const void* scores;        int64_t sc_sr;           /* [rows, nblk] fp32 / bf16 / fp16     */
+  const uint8_t* block_cand; int64_t bc_sr;           /* [rows, nblk] bool or NULL           */
+  const uint8_t* img;        int64_t img_sb;          /* [rows / rows_per_seq, nblk] or NULL */
+  void* prior;               int64_t p_sr;            /* [rows, nblk] scores' dtype          */
+  uint8_t* cand;             int64_t c_sr;            /* [rows, nblk] bool                   */
+  int32_t rows, nblk, rows_per_seq;
+  float scale, neg;
+  int32_t dtype;
+} srswa_dash_route_train_args;
+
+typedef struct {
+  const void* d_prior;   int64_t dp_sr;               /* [rows, nblk]                        */
+  const void* prior;     int64_t p_sr;                /* [rows, nblk] the forward's prior    */
+  const uint8_t* cand;   int64_t c_sr;                /* [rows, nblk]                        */
+  void* d_scores;        int64_t ds_sr;               /* [rows, nblk]                        */
+  int32_t rows, nblk;
+  float scale;
+  int32_t dtype;
+} srswa_dash_route_train_bwd_args;
+
+typedef struct {
+  const void* prior;     int64_t p_sr;                /* [rows, nblk]                        */
+  const uint8_t* cand;   int64_t c_sr;                /* [rows, nblk]                        */
+  int64_t* topi;         int64_t ti_sr;               /* [rows, K]                           */
+  void* bias;            int64_t b_sr;                /* [rows, K] prior's dtype (NULL: skip) */
+  uint8_t* valid;        int64_t v_sr;                /* [rows, K]                           */
+  const void* d_bias;    int64_t db_sr;               /* backward: [rows, K]                 */
+  void* d_prior;         int64_t dp_sr;               /* backward: [rows, nblk]              */
+  int32_t rows, nblk, K;
+  float floor, inv_sigma;
+  int32_t dtype;
+} srswa_dash_select_train_args;
+
+int srswa_dash_route_train(const srswa_dash_route_train_args* a, void* stream);
+int srswa_dash_route_train_bwd(const srswa_dash_route_train_bwd_args* a, void* stream);
+/* forward: reads prior / cand, writes topi / bias / valid; backward: reads
+ * prior / cand / topi / d_bias, writes d_prior */
+int srswa_dash_select_train(const srswa_dash_select_train_args* a, void* stream);
+int srswa_dash_select_train_bwd(const srswa_dash_select_train_args* a, void* stream);
+
+/* ------------------------------------------------------------------------
  * Page isolation and Page2D RoPE: the metadata step before scoring.
  * Index arrays marked "i32/i64" take int32 or int64 elements, chosen by the
  * matching *_i64 flag (0 = int32, 1 = int64).

@@ -615,6 +615,68 @@ def entmax15(x, dim=-1):
     return y.transpose(dim, -1)
 
 
+class Entmax15Ref(torch.autograd.Function):
+    """``entmax15`` with the reference's own backward (``_Entmax15.backward``,
+    HF/dash_attention.py:797-806): g = sqrt(y), dx = dy g - g sum(dy g) / sum(g)."""
+
+    @staticmethod
+    def forward(ctx, x, dim):
+        y = entmax15(x, dim)
+        ctx.dim = dim
+        ctx.save_for_backward(y)
+        return y
+
+    @staticmethod
+    def backward(ctx, dy):
+        (y,) = ctx.saved_tensors
+        g = y.sqrt()
+        dx = dy * g
+        q = (dx.sum(ctx.dim) / g.sum(ctx.dim).clamp_min(1e-12)).unsqueeze(ctx.dim)
+        return dx - q * g, None
+
+
+def dash_route_train(block_scores, image_block_mask, block_cand, idx_scale, neg=ENTMAX_NEG, image_only=True):
+    """``DashAttention._route`` (HF/dash_attention.py:1145-1174) without its
+    calibration hook: (prior [B, S, nblk], cand bool); differentiable in
+    block_scores."""
+    remote = block_scores > (SCORE_NEG * 0.5)
+    cand = remote
+    if block_cand is not None:
+        cand = remote & block_cand
+    elif image_only and image_block_mask is not None:
+        cand = remote & image_block_mask[:, None, :]
+    cand = torch.where(~cand.any(dim=-1, keepdim=True), remote, cand)
+    x = torch.where(cand, block_scores * idx_scale, block_scores.new_full((), neg))
+    x = torch.nan_to_num(x, nan=neg, posinf=neg, neginf=neg)
+    return Entmax15Ref.apply(x, -1), cand
+
+
+def dash_select_and_bias(prior, cand, K, floor, sigma):
+    """``DashAttention._select_and_bias`` (HF/dash_attention.py:1176-1204):
+    the K largest of the masked prior (non-candidates -1; ties -> lower block
+    id), valid = a candidate slot, bias = (log(max(p, floor)) - mean over the
+    valid slots) / sigma, 0 elsewhere, clamped to +-1e4.  (topi, bias, valid);
+    bias differentiable in prior."""
+    sel = prior.masked_fill(~cand, -1.0)
+    topi = torch.sort(-sel.detach(), dim=-1, stable=True).indices[..., :K]
+    bias, valid = dash_bias_given(prior, cand, topi, floor, sigma)
+    return topi, bias, valid
+
+
+def dash_bias_given(prior, cand, topi, floor, sigma):
+    """The bias / valid of ``_select_and_bias`` (HF/dash_attention.py:1196-1203)
+    for given slot ids: topv = the masked prior at topi.  (bias, valid)."""
+    sel = prior.masked_fill(~cand, -1.0)
+    topv = sel.gather(-1, topi)
+    valid = topv >= 0.0
+    logp = torch.log(topv.clamp_min(floor))
+    cnt = valid.sum(dim=-1, keepdim=True).clamp(min=1)
+    mu = torch.where(valid, logp, torch.zeros_like(logp)).sum(dim=-1, keepdim=True) / cnt
+    bias = (logp - mu) * (1.0 / sigma)
+    bias = torch.where(valid, bias, torch.zeros_like(bias)).clamp(-ACT_CLAMP, ACT_CLAMP)
+    return bias, valid
+
+
 def infer_route_select(block_scores, block_cand, idx_scale, floor, sigma, K, topm):
     """``_infer_route_select`` (HF/modeling_deepseekv2.py:338-362): top-M window,
     entmax-1.5 prior, first K slots, centred log-prior bias.  Top-M ties -> lower id."""

@@ -701,3 +701,79 @@ def test_topk_blocks_invalid_at_minus_inf():
     s = torch.tensor([[-1e30, float("-inf"), float("nan"), -2e30, float("-inf")]], dtype=torch.float64)
     assert O.topk_blocks(s, 4, invalid_at=float("-inf")).tolist() == [[0, 3, -1, -1]]
     assert not O.near_tie_rows(s, 2, invalid_at=float("-inf")).any()
+
+
+def _dash_train_case(g, B=2, S=5, nblk=9, scale=1.0):
+    sc = _rand(B, S, nblk, g=g) * scale
+    sc[0, 0, :] = O.SCORE_NEG                          # a row without a remote block
+    sc[0, 1, 3:] = O.SCORE_NEG                         # a row with three remote blocks
+    sc[1, :, -1] = O.SCORE_NEG
+    return sc
+
+
+def test_dash_route_train_rows_by_python_loop():
+    """Candidates (block mask / image mask / fallback) and the prior row by row
+    against a pure-Python restatement with the bisection entmax."""
+    g = torch.Generator().manual_seed(41)
+    sc = _dash_train_case(g)
+    B, S, n = sc.shape
+    bcand = torch.rand(B, S, n, generator=g) < 0.4
+    bcand[1, 2] = False                                # masked to nothing -> fallback
+    img = torch.rand(B, n, generator=g) < 0.5
+    for blk, im, only in ((None, None, True), (bcand, None, True), (None, img, True), (None, img, False)):
+        prior, cand = O.dash_route_train(sc, im, blk, 0.7, image_only=only)
+        for b in range(B):
+            for s in range(S):
+                remote = [float(v) > -5e8 for v in sc[b, s]]
+                m = [True] * n
+                if blk is not None:
+                    m = [bool(v) for v in blk[b, s]]
+                elif only and im is not None:
+                    m = [bool(v) for v in im[b]]
+                c = [r and mm for r, mm in zip(remote, m)]
+                if not any(c):
+                    c = remote
+                assert cand[b, s].tolist() == c
+                x = [float(sc[b, s, j]) * 0.7 if c[j] else -1e4 for j in range(n)]
+                want = _entmax_bisect(x)
+                assert max(abs(a - w) for a, w in zip(prior[b, s].tolist(), want)) < 1e-9
+
+
+def test_dash_select_and_bias_by_python_loop():
+    g = torch.Generator().manual_seed(42)
+    sc = _dash_train_case(g, scale=3.0)
+    prior, cand = O.dash_route_train(sc, None, None, 1.0)
+    for K, floor, sigma in ((4, 1e-4, 1.0), (6, 0.05, 0.5), (9, 1e-2, 2.0)):
+        topi, bias, valid = O.dash_select_and_bias(prior, cand, K, floor, sigma)
+        for b in range(sc.shape[0]):
+            for s in range(sc.shape[1]):
+                sel = [float(p) if bool(c) else -1.0 for p, c in zip(prior[b, s], cand[b, s])]
+                order = sorted(range(len(sel)), key=lambda j: (-sel[j], j))[:K]
+                assert topi[b, s].tolist() == order
+                v = [sel[j] >= 0 for j in order]
+                lp = [math.log(max(sel[j], floor)) for j in order]
+                mu = sum(l for l, vv in zip(lp, v) if vv) / max(sum(v), 1)
+                want = [(l - mu) / sigma if vv else 0.0 for l, vv in zip(lp, v)]
+                assert valid[b, s].tolist() == v
+                assert max(abs(a - w) for a, w in zip(bias[b, s].tolist(), want)) < 1e-9
+    # entmax zeros tie when its support is narrower than K: the lower ids fill the slots
+    p = torch.tensor([[[0.0, 0.7, 0.0, 0.3, 0.0, 0.0]]], dtype=torch.float64)
+    topi, _, valid = O.dash_select_and_bias(p, torch.ones_like(p, dtype=torch.bool), 4, 1e-4, 1.0)
+    assert topi.tolist() == [[[1, 3, 0, 2]]] and valid.all()
+
+
+def test_dash_train_router_gradcheck():
+    """The reference's entmax backward and the select / bias chain against
+    finite differences (fp64), with block / image masks and a short row."""
+    g = torch.Generator().manual_seed(43)
+    sc = _dash_train_case(g, B=2, S=3, nblk=7, scale=0.8)
+    img = torch.tensor([[1, 0, 1, 1, 0, 1, 1], [0, 1, 1, 1, 1, 0, 1]], dtype=torch.bool)
+    w = torch.randn(2, 3, 4, generator=g, dtype=torch.float64)
+
+    def f(x):
+        prior, cand = O.dash_route_train(x, img, None, 1.3)
+        _, bias, _ = O.dash_select_and_bias(prior, cand, 4, 1e-3, 0.7)
+        return (bias * w).sum() + (prior * prior).sum()
+
+    x = sc.clone().requires_grad_()
+    assert torch.autograd.gradcheck(f, (x,), eps=1e-7, atol=1e-6)

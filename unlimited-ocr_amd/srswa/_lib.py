@@ -230,6 +230,52 @@ class RouteServeArgs(ctypes.Structure):
     ]
 
 
+class DashRouteTrainArgs(ctypes.Structure):
+    """Mirror of ``srswa_dash_route_train_args``."""
+
+    _fields_ = [
+        ("scores", _vp), ("sc_sr", _i64),
+        ("block_cand", _vp), ("bc_sr", _i64),
+        ("img", _vp), ("img_sb", _i64),
+        ("prior", _vp), ("p_sr", _i64),
+        ("cand", _vp), ("c_sr", _i64),
+        ("rows", _i32), ("nblk", _i32), ("rows_per_seq", _i32),
+        ("scale", ctypes.c_float), ("neg", ctypes.c_float),
+        ("dtype", _i32),
+    ]
+
+
+class DashRouteTrainBwdArgs(ctypes.Structure):
+    """Mirror of ``srswa_dash_route_train_bwd_args``."""
+
+    _fields_ = [
+        ("d_prior", _vp), ("dp_sr", _i64),
+        ("prior", _vp), ("p_sr", _i64),
+        ("cand", _vp), ("c_sr", _i64),
+        ("d_scores", _vp), ("ds_sr", _i64),
+        ("rows", _i32), ("nblk", _i32),
+        ("scale", ctypes.c_float),
+        ("dtype", _i32),
+    ]
+
+
+class DashSelectTrainArgs(ctypes.Structure):
+    """Mirror of ``srswa_dash_select_train_args``."""
+
+    _fields_ = [
+        ("prior", _vp), ("p_sr", _i64),
+        ("cand", _vp), ("c_sr", _i64),
+        ("topi", _vp), ("ti_sr", _i64),
+        ("bias", _vp), ("b_sr", _i64),
+        ("valid", _vp), ("v_sr", _i64),
+        ("d_bias", _vp), ("db_sr", _i64),
+        ("d_prior", _vp), ("dp_sr", _i64),
+        ("rows", _i32), ("nblk", _i32), ("K", _i32),
+        ("floor", ctypes.c_float), ("inv_sigma", ctypes.c_float),
+        ("dtype", _i32),
+    ]
+
+
 class WinBoundsArgs(ctypes.Structure):
     """Mirror of ``srswa_win_bounds_args``."""
 
@@ -412,6 +458,10 @@ SIGNATURES = {
     "srswa_kbar_plan": (ctypes.c_int, [ctypes.POINTER(KbarPlanArgs), _vp]),
     "srswa_route_serve": (ctypes.c_int, [ctypes.POINTER(RouteServeArgs), _vp]),
     "srswa_win_bounds": (ctypes.c_int, [ctypes.POINTER(WinBoundsArgs), _vp]),
+    "srswa_dash_route_train": (ctypes.c_int, [ctypes.POINTER(DashRouteTrainArgs), _vp]),
+    "srswa_dash_route_train_bwd": (ctypes.c_int, [ctypes.POINTER(DashRouteTrainBwdArgs), _vp]),
+    "srswa_dash_select_train": (ctypes.c_int, [ctypes.POINTER(DashSelectTrainArgs), _vp]),
+    "srswa_dash_select_train_bwd": (ctypes.c_int, [ctypes.POINTER(DashSelectTrainArgs), _vp]),
     "srswa_gather_decode_paged_workspace": (ctypes.c_size_t, [ctypes.POINTER(PagedDecodeArgs)]),
     "srswa_gather_decode_paged": (ctypes.c_int, [ctypes.POINTER(PagedDecodeArgs), _vp, ctypes.c_size_t, _vp]),
     "srswa_page_decode_meta": (ctypes.c_int, [ctypes.POINTER(PageMetaArgs), _vp]),
@@ -433,6 +483,9 @@ STRUCTS = {"srswa_decode_args": DecodeArgs, "srswa_index_args": IndexArgs,
            "srswa_paged_decode_args": PagedDecodeArgs, "srswa_kbar_pages_args": KbarPagesArgs,
            "srswa_kbar_scores_args": KbarScoresArgs, "srswa_kbar_plan_args": KbarPlanArgs,
            "srswa_route_serve_args": RouteServeArgs, "srswa_win_bounds_args": WinBoundsArgs,
+           "srswa_dash_route_train_args": DashRouteTrainArgs,
+           "srswa_dash_route_train_bwd_args": DashRouteTrainBwdArgs,
+           "srswa_dash_select_train_args": DashSelectTrainArgs,
            "srswa_page_meta_args": PageMetaArgs,
            "srswa_page_allow_args": PageAllowArgs, "srswa_local_union_args": LocalUnionArgs,
            "srswa_cos_sin_args": CosSinArgs, "srswa_rope_args": RopeArgs,

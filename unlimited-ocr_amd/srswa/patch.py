@@ -18,6 +18,8 @@ two kernel files (those are replaced file-for-file by
   (:2046-2061) and the module's ``_llama_apply_rotary_pos_emb`` (:39-41)
   -> ``srswa.page_isolation``; with ``modeling_unlimitedocr`` given, also its
   ``_uocr_dash_decode_allow`` (HF/modeling_unlimitedocr.py:481-528)
+* ``DashAttention._route`` / ``_select_and_bias`` (HF/dash_attention.py:1145-1204),
+  the training router -> ``srswa.dash_train``
 * ``_KLChunkFn`` (HF/_sparse_base_impl.py:2158-2190), the KL of the indexer
   distillation loss -> ``srswa.kl.KLChunkFn``
 * ``DeepseekV2Indexer.select_and_kl_loss`` (HF/_sparse_base_impl.py:3240-3516),
@@ -33,9 +35,11 @@ eager path, exactly as the reference's wrappers fall back.
 
 from __future__ import annotations
 
+import sys
+
 import torch
 
-from . import indexer, kl, ops, page_isolation
+from . import dash_train, indexer, kl, ops, page_isolation
 from ._lib import UnsupportedShape
 
 SCORE_NEG = -1.0e9
@@ -168,6 +172,36 @@ def _select_and_kl(base, done: list) -> None:
     _rebind(indexer_cls, "forward", make_fwd, done, "DeepseekV2Indexer.forward")
 
 
+def _dash_router(mod, done: list) -> None:
+    dash_cls = getattr(mod, "DashAttention", None)
+    if dash_cls is None:
+        return
+    dash_mod = sys.modules.get(getattr(dash_cls, "__module__", ""), None)
+
+    def make_route(orig):
+        def _route(self, block_scores, image_block_mask, block_cand=None):
+            try:
+                return dash_train.route(self, block_scores, image_block_mask, block_cand,
+                                        sched=getattr(dash_mod, "_SCHED", None))
+            except UnsupportedShape:
+                pass
+            return orig(self, block_scores, image_block_mask, block_cand)
+        return _route
+
+    def make_select(orig):
+        def _select_and_bias(self, prior, cand, nblk):
+            ks = getattr(dash_mod, "_KS", None)
+            if ks is not None:
+                try:
+                    return dash_train.select_and_bias(self, prior, cand, nblk, k_budget=ks.k)
+                except UnsupportedShape:
+                    pass
+            return orig(self, prior, cand, nblk)
+        return _select_and_bias
+    _rebind(dash_cls, "_route", make_route, done, "DashAttention._route")
+    _rebind(dash_cls, "_select_and_bias", make_select, done, "DashAttention._select_and_bias")
+
+
 def apply(modeling_deepseekv2, modeling_unlimitedocr=None) -> list:
     """Rebind the hot-path functions of a loaded ``modeling_deepseekv2`` module
     (the reference's DASH overlay), of its ``_sparse_base_impl`` (``_base``)
@@ -178,6 +212,7 @@ def apply(modeling_deepseekv2, modeling_unlimitedocr=None) -> list:
     _page_isolation(mod, getattr(mod, "_base", None), done)
     _kl_chunk(getattr(mod, "_base", None), done)
     _select_and_kl(getattr(mod, "_base", None), done)
+    _dash_router(mod, done)
     if modeling_unlimitedocr is not None:
         def make_allow(orig):
             def _uocr_dash_decode_allow(indexer, input_ids, cache):
@@ -253,6 +288,8 @@ def restore(modeling_deepseekv2, modeling_unlimitedocr=None) -> None:
     for owner, name in ((getattr(base, "DeepseekV2Indexer", None), "_build_kl_candidate_mask"),
                         (getattr(base, "DeepseekV2Indexer", None), "select_and_kl_loss"),
                         (getattr(base, "DeepseekV2Indexer", None), "forward"),
+                        (getattr(mod, "DashAttention", None), "_route"),
+                        (getattr(mod, "DashAttention", None), "_select_and_bias"),
                         (getattr(base, "DeepseekV2IndexerRotary2D", None), "forward"),
                         (base, "_llama_apply_rotary_pos_emb"), (mod, "_llama_apply_rotary_pos_emb"),
                         (base, "_KLChunkFn"),
