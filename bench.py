@@ -728,6 +728,155 @@ def bench_kl(args):
                                                      "the kernel runs two)"}}
 
 
+def bench_route(args):
+    """Serving DASH router (srswa.unlimited_dash_ops.route_triton) on config 3's
+    paged cache: one decode step's routing for 64 requests (summary-cache
+    scores over every page, 1.5-entmax, top-8 budget, 16 packed slots), and a
+    2048-row prefill chunk against the same cache.  HBM-light, launch-bound:
+    the figure is the routed rows per second."""
+    import torch
+    from srswa import ops, unlimited_dash_ops as U, workloads as W
+    dev = torch.device("cuda:0")
+    B, BS, LW, K, M = 64, 64, 512, 8, 16
+    c = W.paged_decode_config(B=B, device=dev)
+    bt, sl = c["block_table"].to(dev), c["seq_lens"].to(dev)
+    Wd = int(bt.shape[1])
+    kbar = torch.zeros(c["num_pages"], 128, dtype=torch.float32, device=dev)
+    hc = torch.randn(128, device=dev)
+    ops.kbar_pages(c["idx_k_cache"], hc, bt, sl, kbar)
+    iq = c["idx_q"].to(dev)
+    out_idx = torch.empty(B, M, dtype=torch.int32, device=dev)
+    out_bias = torch.empty(B, M, dtype=torch.float32, device=dev)
+    score_buf = torch.empty(B, Wd, dtype=torch.float32, device=dev)
+    p = dict(idx_scale=128.0 / math.sqrt(128), prior_floor=1e-4, sigma=1.0)
+
+    def dec():
+        U.route_decode_triton(idx_q=iq, k_bar=kbar, block_table=bt, seq_lens=sl, image_allow=None, out_idx=out_idx,
+                              out_bias=out_bias, max_block=Wd, block_size=BS, local_blocks=LW // BS,
+                              decode_query_len=1, topm=M, score_buf=score_buf, budget=K, out_slots=M, **p)
+
+    ms_d = _time_launches(dec, args.steps, args.warmup, dev)
+    R, QL = 1, 2048                                      # one request's 2048-row chunk at the end of the longest
+    r = int(torch.argmax(sl))
+    L = int(sl[r])
+    btp, slp = bt[r:r + 1], sl[r:r + 1]
+    cu = torch.tensor([0, QL], dtype=torch.int32, device=dev)
+    ctx = slp - QL
+    row2req = torch.zeros(QL, dtype=torch.int32, device=dev)
+    iqp = torch.randn(QL, 128, device=dev)
+    pi = torch.empty(QL, M, dtype=torch.int32, device=dev)
+    pb = torch.empty(QL, M, dtype=torch.float32, device=dev)
+    sbp = torch.empty(QL, Wd, dtype=torch.float32, device=dev)
+
+    def pre():
+        U.route_prefill_triton(idx_q=iqp, k_bar=kbar, block_table=btp, seq_lens=slp, cu_seqlens_q=cu,
+                               context_lens=ctx, row2req=row2req, image_allow=None, out_idx=pi, out_bias=pb,
+                               max_block=Wd, block_size=BS, local_blocks=LW // BS, topm=M, budget=K,
+                               q_chunk=QL, score_buf=sbp, **p)
+
+    ms_p = _time_launches(pre, args.steps, args.warmup, dev)
+    return {"metric": "serving DASH router rows/s (decode step, config 3 cache)", "value": B / (ms_d * 1e-3),
+            "unit": "rows/s", "n_gpus": 1, "steps": args.steps, "warmup": args.warmup, "ms_per_step": ms_d,
+            "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "fp32",
+            "data": "synthetic (seeded)",
+            "config": {"workload": "route_decode_triton: 64 requests x up to 2048 pages, top-8 budget, 16 slots; "
+                                   "route_prefill_triton: 2048 rows of one request", "max_blocks": Wd,
+                       "prefill_rows": QL, "prefill_seq": L, "prefill_ms": ms_p,
+                       "prefill_rows_per_s": QL / (ms_p * 1e-3)}}
+
+
+def bench_dash_train(args):
+    """Training DASH router (srswa.dash_train) on config 5's shape: B=2 x 16384
+    query rows over 256 64-key blocks, bf16 block scores with the causal remote
+    pattern (8 local blocks) and an image-block mask, top-12 budget: forward
+    (candidates, 1.5-entmax prior, top-K, bias) + backward (bias -> prior ->
+    scores).  HBM-bound row passes."""
+    import torch
+    from srswa import dash_train as DT
+    dev = torch.device("cuda:0")
+    B, S, nblk, BS, LB, K = 2, 16384, 256, 64, 8, 12
+    g = torch.Generator(device=dev).manual_seed(5)
+    sc = torch.randn(B, S, nblk, device=dev, generator=g).to(torch.bfloat16)
+    lim = (torch.arange(S, device=dev) // BS - LB)[None, :, None]
+    sc = torch.where(torch.arange(nblk, device=dev)[None, None, :] <= lim, sc,
+                     torch.full((), -1.0e9, dtype=torch.bfloat16, device=dev)).requires_grad_()
+    img = torch.rand(B, nblk, device=dev, generator=g) < 0.4
+    gb = torch.randn(B, S, K, device=dev, generator=g).to(torch.bfloat16)
+    scale = 128.0 / math.sqrt(128)
+
+    def fwd():
+        prior, cand = DT.RouteTrainFn.apply(sc, None, img, scale, -1.0e4)
+        return DT.SelectTrainFn.apply(prior, cand, K, 1e-4, 1.0)
+
+    def step():
+        _, bias, _ = fwd()
+        torch.autograd.backward([bias], [gb])
+
+    ms = _time_launches(step, args.steps, args.warmup, dev)
+    with torch.no_grad():
+        ms_f = _time_launches(fwd, args.steps, args.warmup, dev)
+    E = B * S * nblk
+    traffic = 17 * E             # algorithmic bytes per step (config.bytes_per_element)
+    gbs = traffic / (ms * 1e-3) / 1e9
+    return {"metric": "training DASH router fwd+bwd rows/s (config 5 shape)", "value": B * S / (ms * 1e-3),
+            "unit": "rows/s", "n_gpus": 1, "steps": args.steps, "warmup": args.warmup, "ms_per_step": ms,
+            "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "bf16",
+            "data": "synthetic (seeded)",
+            "config": {"workload": "DashAttention._route + _select_and_bias fwd+bwd, B=2, S=16384, 256 blocks, "
+                                   "top-12, image-block mask", "fwd_ms": ms_f, "elements": E,
+                       "bytes_per_element": "scores 2 + prior 2 + cand 1 (route) + prior 2 + cand 1 (select) + "
+                                            "d prior 2 (select bwd) + d prior 2 + prior 2 + cand 1 + d scores 2 "
+                                            "(route bwd) = 17"},
+            "roofline": {"bound": "hbm", "achieved": gbs, "peak": 8000.0, "unit": "GB/s", "frac": gbs / 8000.0,
+                         "traffic": None, "kernel": "the four router kernels together (step time)"}}
+
+
+def bench_select_kl(args):
+    """The indexer's training step (srswa.indexer.select_and_kl_loss) on
+    config 5's shape: B=2 x 16384 rows, one index head, chunks of 1024 rows:
+    block-max scores -> top-8 -> gather-KL vs 10 main heads, + backward into
+    the index q / k."""
+    import torch
+    from srswa import indexer as IX
+    dev = torch.device("cuda:0")
+    B, T, H, D, BS, LB, TK = 2, 16384, 10, 128, 64, 8, 16
+    g = torch.Generator(device=dev).manual_seed(13)
+    iq = (torch.randn(B, 1, T, D, device=dev, generator=g) * D ** -0.5).to(torch.bfloat16).requires_grad_()
+    ik = torch.randn(B, 1, T, D, device=dev, generator=g).to(torch.bfloat16).requires_grad_()
+    qm = torch.randn(B, H, T, D, device=dev, generator=g).to(torch.bfloat16)
+    km = torch.randn(B, H, T, D, device=dev, generator=g).to(torch.bfloat16)
+    pos = torch.arange(T, device=dev).expand(B, T).contiguous()
+    hidden = torch.empty(B, T, 8, dtype=torch.bfloat16, device=dev)
+
+    class _Indexer:
+        num_heads, head_dim, block_size, local_blocks, local_window = 1, D, BS, LB, LB * BS
+        topk_blocks, kl_chunk_size, image_bucket_constraint, layer_idx, kl_log_interval = TK, 1024, False, 0, 1
+
+        def _project_index_qk(self, h, p, kv):
+            return iq * 1.0, ik * 1.0
+
+        def _remote_topk(self, nblk):
+            return min(max(self.topk_blocks - self.local_blocks, 0), nblk)
+
+        def _build_kl_candidate_mask(self, pos_chunk, nblk, img, batch, cq, image_token_page_ids=None,
+                                     query_token_page_ids=None):
+            return torch.ones(batch, 1, cq, nblk, dtype=torch.bool, device=pos_chunk.device)
+
+    idx = _Indexer()
+
+    def step():
+        _, loss = IX.select_and_kl_loss(idx, hidden, qm, km, None, pos, D ** -0.5)
+        loss.backward()
+
+    ms = _time_launches(step, args.steps, args.warmup, dev)
+    return {"metric": "indexer training step (select_and_kl_loss fwd+bwd) tokens/s (config 5 shape)",
+            "value": B * T / (ms * 1e-3), "unit": "tokens/s", "n_gpus": 1, "steps": args.steps,
+            "warmup": args.warmup, "ms_per_step": ms, "higher_is_better": True, "scaling": "weak",
+            "vs_baseline": None, "dtype": "bf16", "data": "synthetic (seeded)",
+            "config": {"workload": "block-max scores + top-8 + gather-KL (1 index head vs 10 main heads) + "
+                                   "backward, B=2, T=16384, D=128, chunks of 1024 rows"}}
+
+
 def bench_copycal(args):
     """Calibration for the HBM traffic counters: a plain device copy of a known
     size (4 GiB read + 4 GiB written per launch, far beyond the 256 MB
@@ -751,7 +900,7 @@ def main():
     ap.add_argument("--warmup", type=int, default=20)
     ap.add_argument("--config", default="decode",
                     choices=["decode", "indexer", "prefill", "fwdbwd", "paged", "paged_prefill", "dash", "page", "kl",
-                             "blockmax", "copycal"])
+                             "blockmax", "route", "dash_train", "select_kl", "copycal"])
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--no-check", action="store_true", help="skip the oracle spot check")
     ap.add_argument("--cpu-budget", type=float, default=12.0)
@@ -763,7 +912,8 @@ def main():
     fn = {"decode": bench_decode, "indexer": bench_indexer, "prefill": bench_prefill,
           "fwdbwd": bench_fwdbwd, "paged": bench_paged, "paged_prefill": bench_paged_prefill, "dash": bench_dash,
           "page": bench_page, "kl": bench_kl,
-          "blockmax": bench_blockmax,
+          "blockmax": bench_blockmax, "route": bench_route, "dash_train": bench_dash_train,
+          "select_kl": bench_select_kl,
           "copycal": bench_copycal}[args.config]
     res = fn(args)
     print(json.dumps(res), flush=True)

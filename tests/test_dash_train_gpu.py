@@ -51,6 +51,7 @@ CASES = {
     "bf16_flat_600_blocks": (1, 128, 600, 1.0, 0.1, torch.bfloat16, None, 16, 1e-4, 1.0),
     "bf16_shipped_scale": (2, 128, 64, 1.0, 11.3, torch.bfloat16, "image", 12, 1e-4, 1.0),
     "fp16_block": (1, 100, 40, 1.0, 3.0, torch.float16, "block", 10, 1e-2, 2.0),
+    "fp32_1500_blocks_k64": (1, 96, 1500, 1.0, 0.5, torch.float32, "image", 64, 1e-4, 1.0),
 }
 
 

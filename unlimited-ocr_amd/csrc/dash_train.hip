@@ -9,13 +9,14 @@
 // bf16); reductions accumulate in fp32, the entmax threshold in fp64:
 //   route:  candidates (score > -5e8, under the row's block / image mask,
 //           falling back to every remote block), x, z = (x - max) / 2; the z
-//           above -1 (every support member: tau >= max z - 1) are compacted to
-//           LDS and sorted descending (bitonic), their prefix sums give each
+//           above -1 (every support member: tau >= max z - 1) are compacted and
+//           sorted descending (bitonic: across the wave when at most 64, else
+//           in LDS), their fp64 prefix sums give each
 //           rank's closed-form threshold tau_r = mean - sqrt(max((1 - ss) / r,
 //           0)), support = #{r : tau_r <= z_(r)}, prior = max(z - tau_support, 0)^2;
-//   select: K rounds of "largest 64-bit key below the previous one" over
-//           (order key of the masked prior, ~block id), then the bias of the
-//           K slots by wave reductions;
+//   select: the top K of the 64-bit keys (order key of the masked prior,
+//           ~block id) by a lane-maximum threshold and a wave sort, then the
+//           bias of the K slots by wave reductions;
 //   backward: select scatters d topv into a dense LDS row (one wave per
 //           workgroup), route applies the entmax Jacobian-vector product.
 #include <algorithm>
@@ -79,68 +80,22 @@ __device__ __forceinline__ double entmax_tau(double s1, double s2, int r) {
 }
 
 // ------------------------------------------------------------ route forward
-// cand / x of block i of the row (x before the max shift)
+// x of one block (before the max shift) from its score and mask bit
 template <typename T>
-__device__ __forceinline__ float route_x(const srswa_dash_route_train_args& a, const void* sr, const uint8_t* bc,
-                                         const uint8_t* im, bool use_mask, int i, bool& cand) {
-  const float s = ldv<T>(sr, i);
-  const bool remote = s > kRemoteCut;
-  const bool m = !use_mask || (bc ? bc[i] != 0 : im[i] != 0);
-  cand = remote && m;
+__device__ __forceinline__ float route_x(const srswa_dash_route_train_args& a, float s, bool m, bool& cand) {
+  cand = s > kRemoteCut && m;
   float x = cand ? rnd<T>(s * a.scale) : rnd<T>(a.neg);
   if (!__builtin_isfinite(x)) x = rnd<T>(a.neg);
   return x;
 }
 
-template <typename T>
-__global__ __launch_bounds__(kWave) void route_train_kernel(srswa_dash_route_train_args a, int pcap) {
-  extern __shared__ float s_z[];                    // [pcap] compacted z, sorted in place
-  const int lane = threadIdx.x;
-  const int64_t row = blockIdx.x;
-  const int n = a.nblk;
-  const void* sr = reinterpret_cast<const char*>(a.scores) + row * a.sc_sr * (int64_t)sizeof(T);
-  const uint8_t* bc = a.block_cand ? a.block_cand + row * a.bc_sr : nullptr;
-  const uint8_t* im = (!bc && a.img) ? a.img + (row / a.rows_per_seq) * a.img_sb : nullptr;
-
-  // the row's mask applies when it leaves a candidate (HF/dash_attention.py:1159-1165)
-  bool any_masked = false;
-  if (bc || im) {
-    for (int i = lane; i < n; i += kWave) {
-      const bool remote = ldv<T>(sr, i) > kRemoteCut;
-      any_masked |= remote && (bc ? bc[i] != 0 : im[i] != 0);
-    }
-  }
-  const bool use_mask = (bc || im) && __any(any_masked);
-
-  float xm = -INFINITY;
-  for (int i = lane; i < n; i += kWave) {
-    bool c;
-    xm = fmaxf(xm, route_x<T>(a, sr, bc, im, use_mask, i, c));
-  }
-  xm = wave_max(xm);
-
-  // z = (x - max) / 2; z > -1 compacted to LDS (ascending block order), cand written
-  uint8_t* cr = a.cand + row * a.c_sr;
-  int c = 0;
-  for (int i0 = 0; i0 < n; i0 += kWave) {
-    const int i = i0 + lane;
-    float z = -INFINITY;
-    if (i < n) {
-      bool cd;
-      const float x = route_x<T>(a, sr, bc, im, use_mask, i, cd);
-      z = rnd<T>(x - xm) * 0.5f;
-      cr[i] = cd ? 1 : 0;
-    }
-    const bool keep = z > -1.f;
-    const uint64_t bal = __ballot(keep);
-    if (keep) s_z[c + __popcll(bal & ((1ull << lane) - 1ull))] = z;
-    c += __popcll(bal);
-  }
+// Sort the c (<= pcap) floats of s_z descending in LDS (bitonic over the
+// next power of two >= max(c, 64), padded with -inf); one wave per workgroup.
+__device__ __forceinline__ int lds_sort_desc(float* s_z, int c, int lane) {
   int P = kWave;
   while (P < c) P <<= 1;
   for (int i = c + lane; i < P; i += kWave) s_z[i] = -INFINITY;
   __syncthreads();
-  // bitonic sort, descending
   for (int k = 2; k <= P; k <<= 1) {
     for (int j = k >> 1; j > 0; j >>= 1) {
       for (int t = lane; t < P / 2; t += kWave) {
@@ -155,17 +110,21 @@ __global__ __launch_bounds__(kWave) void route_train_kernel(srswa_dash_route_tra
       __syncthreads();
     }
   }
-  // lane-segment prefix sums (ranks lane E + 1 .. lane E + E), then the support
-  const int E = P / kWave;
+  return P;
+}
+
+// tau of the c largest z, sorted descending: E per lane in s_z (lane-major),
+// or one per lane in `mine` (E == 0)
+__device__ __forceinline__ double entmax_threshold(const float* s_z, float mine, int c, int E, int lane) {
+  const int per = E > 0 ? E : 1;
+  auto val = [&](int e) __attribute__((always_inline)) { return E > 0 ? (double)s_z[lane * E + e] : (double)mine; };
   double l1 = 0.0, l2 = 0.0;
-  for (int e = 0; e < E; ++e) {
-    const int r = lane * E + e;
-    if (r < c) {
-      const double v = s_z[r];
+  for (int e = 0; e < per; ++e)
+    if (lane * per + e < c) {
+      const double v = val(e);
       l1 += v;
       l2 += v * v;
     }
-  }
   double i1 = l1, i2 = l2;                          // inclusive scan over lanes
 #pragma unroll
   for (int o = 1; o < kWave; o <<= 1) {
@@ -177,40 +136,138 @@ __global__ __launch_bounds__(kWave) void route_train_kernel(srswa_dash_route_tra
   }
   double b1 = __shfl_up(i1, 1, kWave), b2 = __shfl_up(i2, 1, kWave);
   if (lane == 0) b1 = b2 = 0.0;
+  // support = #{ranks r with tau_r <= z_(r)}; tau_r of every rank this lane holds
   int cnt = 0;
-  {
-    double s1 = b1, s2 = b2;
-    for (int e = 0; e < E; ++e) {
-      const int r = lane * E + e;
-      if (r < c) {
-        const double v = s_z[r];
-        s1 += v;
-        s2 += v * v;
-        cnt += entmax_tau(s1, s2, r + 1) <= v ? 1 : 0;
-      }
+  double s1 = b1, s2 = b2;
+  for (int e = 0; e < per; ++e)
+    if (lane * per + e < c) {
+      const double v = val(e);
+      s1 += v;
+      s2 += v * v;
+      cnt += entmax_tau(s1, s2, lane * per + e + 1) <= v ? 1 : 0;
     }
-  }
   const int support = max(wave_sum_i(cnt), 1);
-  const int owner = (support - 1) / E;
+  const int owner = (support - 1) / per;
   double tau = 0.0;
   if (lane == owner) {
-    double s1 = b1, s2 = b2;
-    for (int e = 0; lane * E + e < support; ++e) {
-      const double v = s_z[lane * E + e];
+    s1 = b1;
+    s2 = b2;
+    for (int e = 0; lane * per + e < support; ++e) {
+      const double v = val(e);
       s1 += v;
       s2 += v * v;
     }
     tau = entmax_tau(s1, s2, support);
   }
-  tau = __shfl(tau, owner, kWave);
+  return __shfl(tau, owner, kWave);
+}
+
+// NPL > 0: the row's scores and mask bits stay in registers (block i = lane +
+// 64 t); NPL == 0 re-reads the row for every pass (rows above 1024 blocks).
+// The z above -1 (usually few) are sorted across the wave when at most 64,
+// else in LDS.
+template <typename T, int NPL>
+__global__ __launch_bounds__(kWave) void route_train_kernel(srswa_dash_route_train_args a, int pcap) {
+  extern __shared__ float s_z[];                    // [pcap]
+  const int lane = threadIdx.x;
+  const int64_t row = blockIdx.x;
+  const int n = a.nblk;
+  const void* sr = reinterpret_cast<const char*>(a.scores) + row * a.sc_sr * (int64_t)sizeof(T);
+  const uint8_t* bc = a.block_cand ? a.block_cand + row * a.bc_sr : nullptr;
+  const uint8_t* im = (!bc && a.img) ? a.img + (row / a.rows_per_seq) * a.img_sb : nullptr;
+  constexpr int NR = NPL > 0 ? NPL : 1;
+  float sv[NR];
+  bool mv[NR];
+  auto score = [&](int t, int i) __attribute__((always_inline)) { return NPL > 0 ? sv[t] : ldv<T>(sr, i); };
+  auto maskb = [&](int t, int i) __attribute__((always_inline)) {
+    return NPL > 0 ? mv[t] : (bc ? bc[i] != 0 : (im ? im[i] != 0 : true));
+  };
+  if constexpr (NPL > 0) {
+#pragma unroll
+    for (int t = 0; t < NPL; ++t) {
+      const int i = lane + kWave * t;
+      sv[t] = i < n ? ldv<T>(sr, i) : -INFINITY;
+      mv[t] = i < n && (bc ? bc[i] != 0 : (im ? im[i] != 0 : true));
+    }
+  }
+  const int nt = NPL > 0 ? NPL : ceil_div(n, kWave);
+
+  // the row's mask applies when it leaves a candidate (HF/dash_attention.py:1159-1165)
+  bool any_masked = false;
+  if (bc || im) {
+    for (int t = 0; t < nt; ++t) {
+      const int i = lane + kWave * t;
+      if (i < n) any_masked |= score(t, i) > kRemoteCut && maskb(t, i);
+    }
+  }
+  const bool use_mask = (bc || im) && __any(any_masked);
+
+  float xm = -INFINITY;
+  for (int t = 0; t < nt; ++t) {
+    const int i = lane + kWave * t;
+    bool cd;
+    if (i < n) xm = fmaxf(xm, route_x<T>(a, score(t, i), !use_mask || maskb(t, i), cd));
+  }
+  xm = wave_max(xm);
+
+  // z = (x - max) / 2 (kept in sv for NPL > 0), cand written, the z > -1 counted
+  uint8_t* cr = a.cand + row * a.c_sr;
+  int cnt_hi = 0;
+  for (int t = 0; t < nt; ++t) {
+    const int i = lane + kWave * t;
+    if (i < n) {
+      bool cd;
+      const float z = rnd<T>(route_x<T>(a, score(t, i), !use_mask || maskb(t, i), cd) - xm) * 0.5f;
+      cr[i] = cd ? 1 : 0;
+      cnt_hi += z > -1.f ? 1 : 0;
+      if constexpr (NPL > 0) sv[t] = z;
+    }
+  }
+  const int c = wave_sum_i(cnt_hi);
+  // compaction of the z > -1 into s_z (ascending block order)
+  {
+    int base = 0;
+    for (int t = 0; t < nt; ++t) {
+      const int i = lane + kWave * t;
+      float z = -INFINITY;
+      if (i < n) {
+        if constexpr (NPL > 0) {
+          z = sv[t];
+        } else {
+          bool cd;
+          z = rnd<T>(route_x<T>(a, score(t, i), !use_mask || maskb(t, i), cd) - xm) * 0.5f;
+        }
+      }
+      const bool keep = z > -1.f;
+      const uint64_t bal = __ballot(keep);
+      if (keep) s_z[base + __popcll(bal & ((1ull << lane) - 1ull))] = z;
+      base += __popcll(bal);
+    }
+  }
+  double tau;
+  if (c <= kWave) {
+    __syncthreads();
+    const float mine = wave_sort_desc<float>(lane < c ? s_z[lane] : -INFINITY, lane);
+    tau = entmax_threshold(nullptr, mine, c, 0, lane);
+  } else {
+    const int P = lds_sort_desc(s_z, c, lane);
+    tau = entmax_threshold(s_z, 0.f, c, P / kWave, lane);
+  }
 
   void* pr = reinterpret_cast<char*>(a.prior) + row * a.p_sr * (int64_t)sizeof(T);
-  for (int i = lane; i < n; i += kWave) {
-    bool cd;
-    const float x = route_x<T>(a, sr, bc, im, use_mask, i, cd);
-    const float z = rnd<T>(x - xm) * 0.5f;
-    const float d = rnd<T>(fmaxf((float)((double)z - tau), 0.f));
-    stv<T>(pr, i, d * d);
+  for (int t = 0; t < nt; ++t) {
+    const int i = lane + kWave * t;
+    if (i < n) {
+      float z;
+      if constexpr (NPL > 0) {
+        z = sv[t];
+      } else {
+        bool cd;
+        z = rnd<T>(route_x<T>(a, score(t, i), !use_mask || maskb(t, i), cd) - xm) * 0.5f;
+      }
+      const float d = rnd<T>(fmaxf((float)((double)z - tau), 0.f));
+      stv<T>(pr, i, d * d);
+    }
   }
 }
 
@@ -243,10 +300,16 @@ __global__ __launch_bounds__(256) void route_train_bwd_kernel(srswa_dash_route_t
 }
 
 // ----------------------------------------------------------------- select
-// the K slots of the row: lane j < K ends with slot j's key (order key of
-// sel << 32 | ~block id); NPL > 0 keeps the row's keys in registers
+// The K slots of the row: lane j < K ends with slot j's key (order key of sel
+// << 32 | ~block id, unique per block).  NPL > 0 keeps the row's keys in
+// registers and finds them without K rounds over every key: the K-th largest
+// of the 64 lane maxima is a threshold with at least K keys at or above it;
+// those keys (at most 64 in an ordinary row) are compacted through LDS and
+// sorted across the wave.  More than 64, or NPL == 0 (rows above 1024
+// blocks): K rounds of "largest key below the previous one".
 template <typename T, int NPL>
-__device__ __forceinline__ uint64_t select_keys(const srswa_dash_select_train_args& a, int64_t row, int lane) {
+__device__ __forceinline__ uint64_t select_keys(const srswa_dash_select_train_args& a, int64_t row, int lane,
+                                                uint64_t* s_sel) {
   const int n = a.nblk;
   const int64_t es = sizeof(T);
   const void* pr = reinterpret_cast<const char*>(a.prior) + row * a.p_sr * es;
@@ -255,12 +318,37 @@ __device__ __forceinline__ uint64_t select_keys(const srswa_dash_select_train_ar
     const float sel = cr[i] ? ldv<T>(pr, i) : -1.f;
     return ((uint64_t)f32_order_key(sel) << 32) | (uint64_t)(0xffffffffu - (uint32_t)i);
   };
-  uint64_t keys[NPL > 0 ? NPL : 1];
+  constexpr int NR = NPL > 0 ? NPL : 1;
+  uint64_t keys[NR];
   if constexpr (NPL > 0) {
+    uint64_t lmax = 0ull;
 #pragma unroll
     for (int t = 0; t < NPL; ++t) {
       const int i = lane + kWave * t;
       keys[t] = i < n ? key_of(i) : 0ull;
+      lmax = keys[t] > lmax ? keys[t] : lmax;
+    }
+    // K <= min(n, 64) lanes hold a real key, so the threshold is a real key
+    const uint64_t T_ = __shfl(wave_sort_desc<uint64_t>(lmax, lane), a.K - 1, kWave);
+    int cnt = 0;
+#pragma unroll
+    for (int t = 0; t < NPL; ++t) cnt += keys[t] >= T_ ? 1 : 0;
+    int incl = cnt;
+#pragma unroll
+    for (int o = 1; o < kWave; o <<= 1) {
+      const int v = __shfl_up(incl, o, kWave);
+      incl += lane >= o ? v : 0;
+    }
+    const int total = __shfl(incl, kWave - 1, kWave);
+    if (total <= kWave) {
+      int off = incl - cnt;
+#pragma unroll
+      for (int t = 0; t < NPL; ++t)
+        if (keys[t] >= T_) s_sel[off++] = keys[t];
+      __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+      __builtin_amdgcn_wave_barrier();
+      __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+      return wave_sort_desc<uint64_t>(lane < total ? s_sel[lane] : 0ull, lane);
     }
   }
   uint64_t prev = ~0ull, mine = 0ull;
@@ -306,10 +394,11 @@ __device__ __forceinline__ SlotBias<T> slot_bias(const srswa_dash_select_train_a
 
 template <typename T, int NPL>
 __global__ __launch_bounds__(256) void select_train_kernel(srswa_dash_select_train_args a) {
-  const int lane = threadIdx.x % kWave;
-  const int64_t row = (int64_t)blockIdx.x * 4 + threadIdx.x / kWave;
+  __shared__ uint64_t s_sel[4][kWave];
+  const int lane = threadIdx.x % kWave, wave = threadIdx.x / kWave;
+  const int64_t row = (int64_t)blockIdx.x * 4 + wave;
   if (row >= a.rows) return;
-  const uint64_t key = select_keys<T, NPL>(a, row, lane);
+  const uint64_t key = select_keys<T, NPL>(a, row, lane, s_sel[wave]);
   const bool live = lane < a.K;
   const int id = (int)(0xffffffffu - (uint32_t)key);
   const float topv = f32_from_order_key((uint32_t)(key >> 32));
@@ -368,6 +457,17 @@ int check_dtype(int dtype, const char* what) {
 
 constexpr int kMaxBlocks = 8192;    // LDS row of one wavefront: 32 KB
 
+template <typename T>
+void launch_route(const srswa_dash_route_train_args& a, int pcap, hipStream_t s) {
+  const size_t lds = (size_t)pcap * sizeof(float);
+  if (a.nblk <= 4 * kWave)
+    hipLaunchKernelGGL((route_train_kernel<T, 4>), dim3(a.rows), dim3(kWave), lds, s, a, pcap);
+  else if (a.nblk <= 16 * kWave)
+    hipLaunchKernelGGL((route_train_kernel<T, 16>), dim3(a.rows), dim3(kWave), lds, s, a, pcap);
+  else
+    hipLaunchKernelGGL((route_train_kernel<T, 0>), dim3(a.rows), dim3(kWave), lds, s, a, pcap);
+}
+
 int launch_status(const char* what) {
   const hipError_t e = hipGetLastError();
   if (e != hipSuccess) {
@@ -401,13 +501,9 @@ extern "C" int srswa_dash_route_train(const srswa_dash_route_train_args* a, void
   int pcap = kWave;
   while (pcap < a->nblk) pcap <<= 1;
   hipStream_t s = reinterpret_cast<hipStream_t>(stream);
-  const size_t lds = (size_t)pcap * sizeof(float);
-  if (a->dtype == SRSWA_F32)
-    hipLaunchKernelGGL(route_train_kernel<float>, dim3(a->rows), dim3(kWave), lds, s, *a, pcap);
-  else if (a->dtype == SRSWA_BF16)
-    hipLaunchKernelGGL(route_train_kernel<bf16_t>, dim3(a->rows), dim3(kWave), lds, s, *a, pcap);
-  else
-    hipLaunchKernelGGL(route_train_kernel<__half>, dim3(a->rows), dim3(kWave), lds, s, *a, pcap);
+  if (a->dtype == SRSWA_F32) launch_route<float>(*a, pcap, s);
+  else if (a->dtype == SRSWA_BF16) launch_route<bf16_t>(*a, pcap, s);
+  else launch_route<__half>(*a, pcap, s);
   return launch_status("dash route train");
 }
 
@@ -453,7 +549,9 @@ int check_select(const srswa_dash_select_train_args* a, bool bwd) {
 template <typename T>
 void launch_select(const srswa_dash_select_train_args& a, hipStream_t s) {
   const dim3 grid((unsigned)ceil_div(a.rows, 4));
-  if (a.nblk <= 16 * kWave)
+  if (a.nblk <= 4 * kWave)
+    hipLaunchKernelGGL((select_train_kernel<T, 4>), grid, dim3(256), 0, s, a);
+  else if (a.nblk <= 16 * kWave)
     hipLaunchKernelGGL((select_train_kernel<T, 16>), grid, dim3(256), 0, s, a);
   else
     hipLaunchKernelGGL((select_train_kernel<T, 0>), grid, dim3(256), 0, s, a);

@@ -154,6 +154,7 @@ class RouteTrainFn(torch.autograd.Function):
     @staticmethod
     def forward(ctx, block_scores, block_cand, image_mask, scale, neg):
         prior, cand = route_forward(block_scores, block_cand, image_mask, scale, neg)
+        ctx.set_materialize_grads(False)     # no zero tensor for the bool output's gradient
         ctx.save_for_backward(prior, cand)
         ctx.scale = scale
         ctx.mark_non_differentiable(cand)
@@ -173,6 +174,7 @@ class SelectTrainFn(torch.autograd.Function):
     @staticmethod
     def forward(ctx, prior, cand, K, floor, sigma):
         topi, bias, valid = select_forward(prior, cand, K, floor, sigma)
+        ctx.set_materialize_grads(False)
         ctx.save_for_backward(prior, cand, topi)
         ctx.floor, ctx.sigma = floor, sigma
         ctx.mark_non_differentiable(topi, valid)

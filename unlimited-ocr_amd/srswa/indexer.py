@@ -8,7 +8,9 @@
 * ``select_and_kl_loss`` -- the training step's selection and distillation KL
   (HF/_sparse_base_impl.py:3240-3516), below.
 
-``select_and_kl_loss``, per query chunk (``kl_chunk_size`` rows):
+``select_and_kl_loss``, per pass of query rows (at least ``kl_chunk_size``;
+the reference's chunks bound its dense [B, H, C, Sk] tensors, which do not
+exist here):
 
 1. block scores -- ``srswa_block_max_score``: max over each 64-key block of
    the index logits over causal, non-local, same-sample keys (:3319-3348; the
@@ -168,8 +170,12 @@ def select_and_kl_loss(self, hidden_states, query_states, key_states, position_e
     keys = idx_k[:, 0] if n_idx_heads == 1 else \
         idx_k.expand(batch, n_idx_heads, k_len, D).reshape(batch * n_idx_heads, k_len, D)
 
-    for c0 in range(0, q_len, chunk):
-        c1 = min(c0 + chunk, q_len)
+    # passes of at least kl_chunk_size rows, as many as a 1 GiB fp32 score
+    # buffer holds: the rows are independent, so the pass size only sets the
+    # number of launches (small passes leave most of the GPU idle)
+    step = min(q_len, max(chunk, (1 << 30) // max(1, 4 * batch * n_idx_heads * nblk)))
+    for c0 in range(0, q_len, step):
+        c1 = min(c0 + step, q_len)
         cq = c1 - c0
         if packed:
             pos_chunk = torch.arange(c0, c1, device=position_ids.device).view(1, -1).expand(batch, -1)
