@@ -6,6 +6,8 @@
 #include <hip/hip_fp16.h>
 #include <stdint.h>
 
+#include <type_traits>
+
 #include "srswa.h"
 
 namespace srswa {
@@ -79,28 +81,82 @@ template <> struct Vec16<__half> {
   }
 };
 
-// Full-wavefront reductions (64 lanes).
+// Full-wavefront reductions (64 lanes, every lane active) on DPP: each level
+// is a VALU operand modifier instead of an LDS permute round trip.  Within each
+// 16-lane row: quad_perm [1,0,3,2], quad_perm [2,3,0,1], row_half_mirror,
+// row_mirror leave every lane with its row's total; row_bcast:15 then adds row
+// 0's total into row 1 and row 2's into row 3, row_bcast:31 adds lane 31's
+// (rows 0 + 1) into rows 2 and 3, so lane 63 holds the wave's total, which
+// readlane hands to every lane (the same bits everywhere).
+namespace dpp {
+constexpr int kXor1 = 0xb1;      // quad_perm [1, 0, 3, 2]
+constexpr int kXor2 = 0x4e;      // quad_perm [2, 3, 0, 1]
+constexpr int kHalfMirror = 0x141;
+constexpr int kMirror = 0x140;
+constexpr int kBcast15 = 0x142;
+constexpr int kBcast31 = 0x143;
+
+template <int CTRL, int ROWS = 0xf>
+__device__ __forceinline__ uint32_t mov(uint32_t identity, uint32_t v) {
+  return (uint32_t)__builtin_amdgcn_update_dpp((int)identity, (int)v, CTRL, ROWS, 0xf, false);
+}
+template <int CTRL, int ROWS = 0xf>
+__device__ __forceinline__ float movf(float identity, float v) {
+  return __uint_as_float(mov<CTRL, ROWS>(__float_as_uint(identity), __float_as_uint(v)));
+}
+template <int CTRL, int ROWS = 0xf>
+__device__ __forceinline__ uint64_t mov64(uint64_t identity, uint64_t v) {
+  const uint32_t lo = mov<CTRL, ROWS>((uint32_t)identity, (uint32_t)v);
+  const uint32_t hi = mov<CTRL, ROWS>((uint32_t)(identity >> 32), (uint32_t)(v >> 32));
+  return ((uint64_t)hi << 32) | lo;
+}
+
+// op over the wave; T is float, double (as its bits) or uint64_t
+template <typename T, typename Op>
+__device__ __forceinline__ T reduce(T v, T identity, Op op) {
+  auto m = [&](auto ctrl_tag, auto rows_tag, T x) __attribute__((always_inline)) {
+    constexpr int C = decltype(ctrl_tag)::value, R = decltype(rows_tag)::value;
+    if constexpr (sizeof(T) == 8) {
+      return __builtin_bit_cast(T, mov64<C, R>(__builtin_bit_cast(uint64_t, identity), __builtin_bit_cast(uint64_t, x)));
+    } else {
+      return __builtin_bit_cast(T, mov<C, R>(__builtin_bit_cast(uint32_t, identity), __builtin_bit_cast(uint32_t, x)));
+    }
+  };
+  using I = int;
+  v = op(v, m(std::integral_constant<I, kXor1>{}, std::integral_constant<I, 0xf>{}, v));
+  v = op(v, m(std::integral_constant<I, kXor2>{}, std::integral_constant<I, 0xf>{}, v));
+  v = op(v, m(std::integral_constant<I, kHalfMirror>{}, std::integral_constant<I, 0xf>{}, v));
+  v = op(v, m(std::integral_constant<I, kMirror>{}, std::integral_constant<I, 0xf>{}, v));
+  v = op(v, m(std::integral_constant<I, kBcast15>{}, std::integral_constant<I, 0xa>{}, v));
+  v = op(v, m(std::integral_constant<I, kBcast31>{}, std::integral_constant<I, 0xc>{}, v));
+  if constexpr (sizeof(T) == 8) {
+    const uint64_t b = __builtin_bit_cast(uint64_t, v);
+    const uint32_t lo = (uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)b, 63);
+    const uint32_t hi = (uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)(b >> 32), 63);
+    return __builtin_bit_cast(T, ((uint64_t)hi << 32) | lo);
+  } else {
+    return __builtin_bit_cast(T, (uint32_t)__builtin_amdgcn_readlane((int)__builtin_bit_cast(uint32_t, v), 63));
+  }
+}
+}  // namespace dpp
+
 __device__ __forceinline__ float wave_max(float v) {
-#pragma unroll
-  for (int o = 32; o >= 1; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, kWave));
-  return v;
+  return dpp::reduce<float>(v, -INFINITY, [](float a, float b) { return fmaxf(a, b); });
 }
 __device__ __forceinline__ float wave_sum(float v) {
-#pragma unroll
-  for (int o = 32; o >= 1; o >>= 1) v += __shfl_xor(v, o, kWave);
-  return v;
+  return dpp::reduce<float>(v, 0.f, [](float a, float b) { return a + b; });
 }
 __device__ __forceinline__ float wave_min(float v) {
-#pragma unroll
-  for (int o = 32; o >= 1; o >>= 1) v = fminf(v, __shfl_xor(v, o, kWave));
-  return v;
+  return dpp::reduce<float>(v, INFINITY, [](float a, float b) { return fminf(a, b); });
 }
-// fp64 butterfly sum: every lane ends with the same bits (each level adds the
-// same two values, in either order, on both partners)
 __device__ __forceinline__ double wave_sum_f64(double v) {
-#pragma unroll
-  for (int o = 32; o >= 1; o >>= 1) v += __shfl_xor(v, o, kWave);
-  return v;
+  return dpp::reduce<double>(v, 0.0, [](double a, double b) { return a + b; });
+}
+__device__ __forceinline__ int wave_sum_int(int v) {
+  return dpp::reduce<int>(v, 0, [](int a, int b) { return a + b; });
+}
+__device__ __forceinline__ uint64_t wave_max_u64(uint64_t v) {
+  return dpp::reduce<uint64_t>(v, 0ull, [](uint64_t a, uint64_t b) { return a > b ? a : b; });
 }
 
 // Bitonic sort of one unsigned value per lane, descending over the wave (lane 0

@@ -57,20 +57,6 @@ template <> __device__ __forceinline__ void stv<__half>(void* p, int64_t i, floa
   reinterpret_cast<__half*>(p)[i] = __float2half_rn(v);
 }
 
-__device__ __forceinline__ int wave_sum_i(int v) {
-#pragma unroll
-  for (int o = 32; o >= 1; o >>= 1) v += __shfl_xor(v, o, kWave);
-  return v;
-}
-__device__ __forceinline__ uint64_t wave_max_u64(uint64_t v) {
-#pragma unroll
-  for (int o = 32; o >= 1; o >>= 1) {
-    const uint64_t w = __shfl_xor(v, o, kWave);
-    v = w > v ? w : v;
-  }
-  return v;
-}
-
 // closed-form 1.5-entmax threshold of the r largest z (sums s1, s2 of z, z^2)
 __device__ __forceinline__ double entmax_tau(double s1, double s2, int r) {
   const double mean = s1 / r, msq = s2 / r;
@@ -146,7 +132,7 @@ __device__ __forceinline__ double entmax_threshold(const float* s_z, float mine,
       s2 += v * v;
       cnt += entmax_tau(s1, s2, lane * per + e + 1) <= v ? 1 : 0;
     }
-  const int support = max(wave_sum_i(cnt), 1);
+  const int support = max(wave_sum_int(cnt), 1);
   const int owner = (support - 1) / per;
   double tau = 0.0;
   if (lane == owner) {
@@ -223,7 +209,7 @@ __global__ __launch_bounds__(kWave) void route_train_kernel(srswa_dash_route_tra
       if constexpr (NPL > 0) sv[t] = z;
     }
   }
-  const int c = wave_sum_i(cnt_hi);
+  const int c = wave_sum_int(cnt_hi);
   // compaction of the z > -1 into s_z (ascending block order)
   {
     int base = 0;

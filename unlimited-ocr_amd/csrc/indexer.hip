@@ -116,15 +116,6 @@ __device__ __forceinline__ uint64_t order_key(float s, int idx) {
   return ((uint64_t)u << 32) | (uint64_t)(0xffffffffu - (uint32_t)idx);
 }
 
-__device__ __forceinline__ uint64_t wave_max_u64(uint64_t v) {
-#pragma unroll
-  for (int o = 32; o >= 1; o >>= 1) {
-    const uint64_t w = __shfl_xor(v, o, kWave);
-    v = w > v ? w : v;
-  }
-  return v;
-}
-
 struct TopkK {
   const float* scores;
   int64_t rows, row_stride;

@@ -7,8 +7,10 @@
 // :129-221 and _entmax_tiled_kernel :280-463 (the same selection over the
 // page-mask window), and _win_bounds_kernel :466-505.
 //
-// route_entmax_kernel: one wavefront per query row; the row's scores are read
-// in streaming passes (64 columns per step, L2-resident after the first):
+// route_entmax_regs_kernel (rows up to 2048 columns) holds the row in
+// registers and runs every step below as register loops; route_entmax_kernel
+// (wider rows): one wavefront per query row, the row's scores read in
+// streaming passes (64 columns per step, L2-resident after the first):
 //   1. candidate counts (remote, remote & page mask), max and min of x;
 //   2. the candidates with z > -1 -- the only ones a bisection midpoint in
 //      [-1, 0] can count -- are compacted into LDS; the 24 tau steps then sum
@@ -253,6 +255,158 @@ __global__ __launch_bounds__(kRsWaves * kWave) void route_entmax_kernel(srswa_ro
   }
 }
 
+// The same router with the row held in registers (column j = lane + 64 i,
+// i < NPL): one read of the scores and page mask, every later pass a register
+// loop.  Rows up to 64 NPL columns (2048 with NPL = 32).  The tau sums keep
+// four fp64 partial sums per lane (independent add chains); as in the
+// streaming kernel their order differs from the reference's reduction tree
+// only below fp64 resolution, and the sum is then rounded to fp32.
+template <int NPL>
+__global__ __launch_bounds__(kRsWaves * kWave) void route_entmax_regs_kernel(srswa_route_serve_args a) {
+  static_assert(NPL % 4 == 0 && NPL <= 32, "NPL: a multiple of 4, at most 32");
+  __shared__ uint32_t s_key[kRsWaves][kWave];
+  const int wave = threadIdx.x / kWave, lane = threadIdx.x % kWave;
+  const int64_t row = (int64_t)blockIdx.x * kRsWaves + wave;
+  if (row >= a.rows) return;
+  const unsigned long long lt = (1ull << lane) - 1ull;
+  const float* sc = a.scores + row * a.sc_sn;
+  const int8_t* im = a.img ? a.img + row * a.img_sn : nullptr;
+
+  float x[NPL];
+  uint32_t rem_bits = 0, img_bits = 0;
+#pragma unroll
+  for (int i = 0; i < NPL; ++i) {
+    const int j = lane + kWave * i;
+    const float s = j < a.W ? sc[j] : -INFINITY;
+    const bool remote = s > kScoreNeg * 0.5f;             // NaN / -inf: not remote
+    const bool ci = remote && im && im[j] != 0;
+    float xv = s * a.idx_scale;
+    x[i] = xv == xv ? xv : kEntmaxNeg;
+    rem_bits |= remote ? 1u << i : 0u;
+    img_bits |= ci ? 1u << i : 0u;
+  }
+  const int n_img = wave_sum_int(__popc(img_bits));
+  const bool use_img = n_img > 0;
+  const uint32_t cand = use_img ? img_bits : rem_bits;
+  const int n_cand = use_img ? n_img : wave_sum_int(__popc(rem_bits));
+  float mx = -INFINITY, mn = INFINITY;
+#pragma unroll
+  for (int i = 0; i < NPL; ++i)
+    if ((cand >> i) & 1u) {
+      mx = fmaxf(mx, x[i]);
+      mn = fminf(mn, x[i]);
+    }
+  const float xm = n_cand > 0 ? wave_max(mx) : 0.f;
+  const float zmin = (wave_min(mn) - xm) * 0.5f;
+  // x -> z in place; non-candidates -inf
+#pragma unroll
+  for (int i = 0; i < NPL; ++i) x[i] = ((cand >> i) & 1u) ? (x[i] - xm) * 0.5f : -INFINITY;
+  float* z = x;
+
+  // tau: the reference's 24 bisection steps; z <= -1 never counts
+  float lo = -1.f, hi = 0.f;
+  for (int it = 0; it < kTauIters; ++it) {
+    const float mid = (lo + hi) * 0.5f;
+    double acc[4] = {0.0, 0.0, 0.0, 0.0};
+#pragma unroll
+    for (int i = 0; i < NPL; ++i) {
+      const float p = fmaxf(z[i] - mid, 0.f);
+      acc[i & 3] += (double)(p * p);
+    }
+    const float ssum = (float)wave_sum_f64((acc[0] + acc[1]) + (acc[2] + acc[3]));
+    if (ssum > 1.f) lo = mid;
+    else hi = mid;
+  }
+  const float tau = (lo + hi) * 0.5f;
+
+  // budget: the (K+1)-th largest candidate z, then the reference's 40 steps
+  float zthr = -INFINITY;
+  if (n_cand > a.K) {
+    uint32_t keys[NPL];
+    uint32_t lmax = 0;
+#pragma unroll
+    for (int i = 0; i < NPL; ++i) {
+      keys[i] = ((cand >> i) & 1u) ? f32_order_key(z[i]) : 0u;
+      lmax = max(lmax, keys[i]);
+    }
+    uint32_t kth = 0;
+    bool found = false;
+    if (a.K + 1 <= kWave) {
+      const uint32_t T = __shfl(wave_sort_desc<uint32_t>(lmax, lane), a.K, kWave);
+      int cnt = 0;
+#pragma unroll
+      for (int i = 0; i < NPL; ++i) cnt += keys[i] >= T ? 1 : 0;
+      int incl = cnt;
+#pragma unroll
+      for (int o = 1; o < kWave; o <<= 1) {
+        const int v = __shfl_up(incl, o, kWave);
+        incl += lane >= o ? v : 0;
+      }
+      const int C = __shfl(incl, kWave - 1, kWave);
+      if (C <= kWave) {
+        int off = incl - cnt;
+#pragma unroll
+        for (int i = 0; i < NPL; ++i)
+          if (keys[i] >= T) s_key[wave][off++] = keys[i];
+        wave_sync_lds();
+        kth = __shfl(wave_sort_desc<uint32_t>(lane < C ? s_key[wave][lane] : 0u, lane), a.K, kWave);
+        found = true;
+      }
+    }
+    if (!found) {   // largest t with at least K + 1 keys >= t, bit by bit from the top
+      for (int bit = 31; bit >= 0; --bit) {
+        const uint32_t t = kth | (1u << bit);
+        int cnt = 0;
+#pragma unroll
+        for (int i = 0; i < NPL; ++i) cnt += keys[i] >= t ? 1 : 0;
+        if (wave_sum_int(cnt) >= a.K + 1) kth = t;
+      }
+    }
+    const float zk1 = f32_from_order_key(kth);
+    float lo2 = zmin - 1.f, hi2 = 0.f;
+    for (int it = 0; it < kCapIters; ++it) {
+      const float mid = (lo2 + hi2) * 0.5f;
+      if (zk1 > mid) lo2 = mid;
+      else hi2 = mid;
+    }
+    zthr = hi2;
+  }
+
+  // mu over the active blocks, then the packed write
+  float lp[NPL];
+  uint32_t act = 0;
+  double lsum = 0.0;
+#pragma unroll
+  for (int i = 0; i < NPL; ++i) {
+    float pr = fmaxf(z[i] - tau, 0.f);
+    pr = pr * pr;
+    lp[i] = logf(fmaxf(pr, a.prior_floor));
+    const bool ac = ((cand >> i) & 1u) && z[i] > zthr;
+    act |= ac ? 1u << i : 0u;
+    if (ac) lsum += (double)lp[i];
+  }
+  const int n_sel = wave_sum_int(__popc(act));
+  const float mu = (float)wave_sum_f64(lsum) / (float)max(n_sel, 1);
+  int32_t* oi = a.out_idx + row * a.oi_sn;
+  float* ob = a.out_bias + row * a.ob_sn;
+  int base = 0;
+#pragma unroll
+  for (int i = 0; i < NPL; ++i) {
+    const bool ac = (act >> i) & 1u;
+    const unsigned long long bal = __ballot(ac);
+    const int pos = base + __popcll(bal & lt);
+    if (ac && pos < a.M) {
+      oi[pos] = lane + kWave * i;
+      ob[pos] = (lp[i] - mu) * a.inv_sigma;
+    }
+    base += __popcll(bal);
+  }
+  for (int s2 = min(base, a.M) + lane; s2 < a.M; s2 += kWave) {
+    oi[s2] = -1;
+    ob[s2] = 0.f;
+  }
+}
+
 // One wavefront per decode query row.
 __global__ __launch_bounds__(kRsWaves * kWave) void win_bounds_kernel(srswa_win_bounds_args a) {
   const int wave = threadIdx.x / kWave, lane = threadIdx.x % kWave;
@@ -312,8 +466,13 @@ extern "C" int srswa_route_serve(const srswa_route_serve_args* a, void* stream) 
   }
   if (a->rows == 0) return SRSWA_OK;
   const dim3 grid((unsigned)((a->rows + kRsWaves - 1) / kRsWaves));
-  hipLaunchKernelGGL(route_entmax_kernel, grid, dim3(kRsWaves * kWave), 0, reinterpret_cast<hipStream_t>(stream),
-                     *a);
+  hipStream_t st = reinterpret_cast<hipStream_t>(stream);
+  if (a->W <= 8 * kWave)
+    hipLaunchKernelGGL(route_entmax_regs_kernel<8>, grid, dim3(kRsWaves * kWave), 0, st, *a);
+  else if (a->W <= 32 * kWave)
+    hipLaunchKernelGGL(route_entmax_regs_kernel<32>, grid, dim3(kRsWaves * kWave), 0, st, *a);
+  else
+    hipLaunchKernelGGL(route_entmax_kernel, grid, dim3(kRsWaves * kWave), 0, st, *a);
   return launch_status("route serve");
 }
 

@@ -46,11 +46,7 @@ __device__ __forceinline__ int key_id(uint64_t k) { return (int)(0x7fffffffu - (
 __device__ __forceinline__ bool key_cand(uint64_t k) { return (k & 1u) != 0; }
 __device__ __forceinline__ uint64_t kmax(uint64_t a, uint64_t b) { return a > b ? a : b; }
 
-__device__ __forceinline__ uint64_t wave_max_key(uint64_t v) {
-#pragma unroll
-  for (int o = 32; o >= 1; o >>= 1) v = kmax(v, __shfl_xor(v, o, kWave));
-  return v;
-}
+__device__ __forceinline__ uint64_t wave_max_key(uint64_t v) { return wave_max_u64(v); }
 
 __device__ __forceinline__ float readlane_f(float v, int l) {
   return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), l));
