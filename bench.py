@@ -422,11 +422,12 @@ def bench_paged_prefill(args):
     g = torch.Generator().manual_seed(W.SEED0 + 44)
     perm = torch.randperm(B * nb, generator=g)
     bt = perm.view(B, nb).to(torch.int32).to(dev)
-    kc = torch.empty(B * nb, BS, H, D, dtype=torch.bfloat16, device=dev)
+    kvd = _kv_dtype(args)
+    kc = torch.empty(B * nb, BS, H, D, dtype=kvd or torch.bfloat16, device=dev)
     vc = torch.empty_like(kc)
     for b in range(B):                       # scatter each sequence's blocks into its pages
-        kc[bt[b].long()] = c["k"][b].view(nb, BS, H, D)
-        vc[bt[b].long()] = c["v"][b].view(nb, BS, H, D)
+        kc[bt[b].long()] = c["k"][b].view(nb, BS, H, D).to(kc.dtype)
+        vc[bt[b].long()] = c["v"][b].view(nb, BS, H, D).to(kc.dtype)
     q = c["q"].reshape(B * T, H, D)
     ids = c["block_idx"][:, 0].reshape(B * T, K).to(torch.int32).to(dev)       # [total_q, K]
     di = ids.unsqueeze(0).expand(H, -1, -1)
@@ -445,8 +446,8 @@ def bench_paged_prefill(args):
             "warmup": args.warmup, "ms_per_step": ms, "higher_is_better": True, "scaling": "weak",
             "vs_baseline": None, "dtype": "bf16", "data": "synthetic (seeded), pages in seeded random order",
             "config": {"workload": "config 4 (B=4, 2048 of 65536 keys, 10 heads, block 64, top-8 + 512 window) "
-                                   "through dash_sparse_attn over a [16384, 64, 10, 128] paged cache",
-                       "flops_per_step": flops},
+                                   f"through dash_sparse_attn over a [16384, 64, 10, 128] paged {args.kv} cache",
+                       "flops_per_step": flops, "kv_cache": args.kv},
             "roofline": {"bound": "mfma", "achieved": tfs, "peak": 2500.0, "unit": "TFLOP/s",
                          "frac": tfs / 2500.0, "traffic": None,
                          "kernel": "srswa::fwd_kernel<bf16,128,paged>"}}
@@ -523,28 +524,42 @@ def bench_fwdbwd(args):
                          "kernel": "fwd_kernel + delta/touch/dq/dkv kernels"}}
 
 
+def _kv_dtype(args):
+    """The --kv cache dtype of the paged legs: None (bf16) or a torch fp8 dtype."""
+    import torch
+    return None if args.kv == "bf16" else getattr(torch, "float8_" + args.kv)
+
+
 def bench_paged(args):
     """Config 3 over the serving (paged) cache: the same selections and bytes as
-    the default leg, each sequence's blocks in randomly ordered pages."""
+    the default leg, each sequence's blocks in randomly ordered pages.  With
+    ``--kv e4m3fn`` (or another fp8 format) the K / V pages hold fp8 values
+    (half the bytes), converted to bf16 as they are read."""
     import torch
     from srswa import ops, workloads as W
     dev = torch.device("cuda:0")
     B, H, D, K, BS, LW = 64, 10, 128, 8, 64, 512
     c = W.paged_decode_config(B=B, H=H, D=D, k=K, block_size=BS, local_window=LW, device=dev)
     q = c["q"].view(B, H, D)
+    kvd = _kv_dtype(args)
+    if kvd is not None:
+        c["k_cache"], c["v_cache"] = c["k_cache"].to(kvd), c["v_cache"].to(kvd)
     launch, out = ops.prepare_gather_decode_paged(q, c["k_cache"], c["v_cache"], c["topk"].to(dev), None,
                                                   c["block_table"].to(dev), c["seq_lens"].to(dev),
                                                   decode_query_len=1, local_blocks=c["local_blocks"],
                                                   scale=c["scale"])
     ms = _time_launches(launch, args.steps, args.warmup, dev)
     nbytes = W.decode_bytes(B, H, D, K, BS, LW)
+    if kvd is not None:          # K / V bytes halve; q, o and the indices do not
+        kv_bytes = 2 * B * H * (LW + K * BS) * D * 2
+        nbytes -= kv_bytes // 2
     achieved = nbytes / (ms * 1e-3) / 1e9
     return {"metric": "paged decode sparse-attn tokens/s (config 3 over randomly ordered KV pages)",
             "value": B / (ms * 1e-3), "unit": "tokens/s", "n_gpus": 1, "steps": args.steps,
             "warmup": args.warmup, "ms_per_step": ms, "higher_is_better": True, "scaling": "weak",
             "vs_baseline": None, "dtype": "bf16", "data": "synthetic (seeded), pages in seeded random order",
-            "config": {"workload": "config 3, paged [num_pages, 64, 10, 128] bf16 cache", "B": B,
-                       "num_pages": c["num_pages"]},
+            "config": {"workload": f"config 3, paged [num_pages, 64, 10, 128] {args.kv} cache", "B": B,
+                       "num_pages": c["num_pages"], "kv_cache": args.kv},
             "roofline": {"bound": "hbm", "achieved": achieved, "peak": HBM_PEAK_GBS, "unit": "GB/s",
                          "frac": achieved / HBM_PEAK_GBS, "traffic": None, "algorithmic_bytes_per_launch": nbytes,
                          "kernel": "srswa::decode_kernel<bf16,bf16,128,8,paged> + decode_merge_kernel"}}
@@ -904,6 +919,8 @@ def main():
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--no-check", action="store_true", help="skip the oracle spot check")
     ap.add_argument("--cpu-budget", type=float, default=12.0)
+    ap.add_argument("--kv", default="bf16", choices=["bf16", "e4m3fn", "e4m3fnuz", "e5m2", "e5m2fnuz"],
+                    help="K / V cache dtype of the paged legs (fp8 formats: half the bytes)")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
         print("bench.py measures one GPU only: this build runs on a single MI355X "

@@ -37,7 +37,11 @@ typedef enum {
   SRSWA_LAUNCH = 4         /* HIP launch error */
 } srswa_status;
 
-typedef enum { SRSWA_F32 = 0, SRSWA_BF16 = 1, SRSWA_F16 = 2 } srswa_dtype;
+typedef enum {
+  SRSWA_F32 = 0, SRSWA_BF16 = 1, SRSWA_F16 = 2,
+  /* fp8 K/V caches of the paged serving kernels (kv_fp8 fields) */
+  SRSWA_FP8_E4M3FN = 3, SRSWA_FP8_E4M3FNUZ = 4, SRSWA_FP8_E5M2 = 5, SRSWA_FP8_E5M2FNUZ = 6
+} srswa_dtype;
 
 /* Library version, e.g. 100 for 0.1.0. */
 int srswa_version(void);
@@ -179,6 +183,8 @@ int srswa_gather_fwd(const srswa_fwd_args* a, void* stream);
  * fp32 product, as K10 does.  The reference runs the first count(id >= 0)
  * slots, which the router packs at the front; here every slot with id >= 0
  * counts, and a repeated id counts once (the router emits no repeats).
+ * kv_fp8 != 0: fp8 caches (USE_FP8, attend_triton.py:193, 225, 250, 277),
+ * converted exactly to dtype as the keys are staged.
  * ---------------------------------------------------------------------- */
 typedef struct {
   const void* q;        int64_t q_sn, q_sh;            /* [total_q, HQ, D]                  */
@@ -194,6 +200,7 @@ typedef struct {
   int32_t R, max_query_len, HQ, HKV, D, S, max_blocks, page_size, local_blocks;
   float scale;
   int32_t dtype;                                       /* SRSWA_BF16 or SRSWA_F16           */
+  int32_t kv_fp8;                                      /* 0, or the caches' fp8 srswa_dtype  */
 } srswa_paged_fwd_args;
 
 int srswa_gather_fwd_paged(const srswa_paged_fwd_args* a, void* stream);
@@ -266,6 +273,9 @@ int srswa_block_max_score(const srswa_blockmax_args* a, void* stream);
  *   remote  keys of the listed blocks below the window start, + bias
  * topk holds logical block ids per kv head (-1 = empty; a repeated id counts
  * once); block_table maps a request's logical block to its page.
+ * kv_fp8 != 0: the caches hold fp8 values of that srswa_dtype (USE_FP8,
+ * attend_triton.py:419, 442, 626), converted exactly to in_dtype (bf16 or
+ * fp16, out_dtype the same) as they are loaded; strides are in cache elements.
  * ---------------------------------------------------------------------- */
 typedef struct {
   const void* q;        int64_t q_sn, q_sh;            /* [total_q, HQ, D]                  */
@@ -279,6 +289,7 @@ typedef struct {
   int32_t R, dql, HQ, HKV, D, topk_n, max_blocks, page_size, local_blocks;
   float scale;
   int32_t in_dtype, out_dtype;
+  int32_t kv_fp8;                                      /* 0, or the caches' fp8 srswa_dtype  */
 } srswa_paged_decode_args;
 
 /* scratch bytes for the split-K records, as srswa_gather_decode_workspace */

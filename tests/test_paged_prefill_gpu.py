@@ -5,7 +5,8 @@ drop-in for the SGLang backend's K10 dash_sparse_attn) vs the CPU oracle
 Bar: bf16 / fp16 outputs max-abs <= 2e-2 beyond the output format's half-ulp
 (tests/tolerance.py) against fp64 on the same rounded inputs.  Inputs follow
 the router's contract: per-kv-head ids packed at the front (ascending,
-unique, -1 after), optional fp32 slot biases."""
+unique, -1 after), optional fp32 slot biases.  fp8 caches of the four torch
+fp8 formats are compared against the oracle on their exact values."""
 
 import math
 
@@ -19,14 +20,14 @@ from tolerance import assert_close_lowp
 pytestmark = pytest.mark.gpu
 
 
-def _case(seed, q_lens, ctx, page, Hkv, G, D, S, dtype, nb_extra=3, bias=True):
+def _case(seed, q_lens, ctx, page, Hkv, G, D, S, dtype, nb_extra=3, bias=True, kv=None):
     g = torch.Generator().manual_seed(seed)
     R = len(q_lens)
     seq = [c + q for c, q in zip(ctx, q_lens)]
     nb = max(-(-s // page) for s in seq) + nb_extra
     npages = R * nb + 4
-    kc = torch.randn(npages, page, Hkv, D, generator=g).to(dtype)
-    vc = torch.randn(npages, page, Hkv, D, generator=g).to(dtype)
+    kc = torch.randn(npages, page, Hkv, D, generator=g).to(kv or dtype)
+    vc = torch.randn(npages, page, Hkv, D, generator=g).to(kv or dtype)
     bt = torch.randperm(npages, generator=g)[:R * nb].view(R, nb).to(torch.int32)
     cu = [0]
     for ql in q_lens:
@@ -59,6 +60,14 @@ CASES = {
                          dtype=torch.float16, lb=6),
     "bf16_p128_no_window": dict(q_lens=[40, 65], ctx=[600, 200], page=128, Hkv=2, G=2, D=128, S=4,
                                 dtype=torch.bfloat16, lb=0),
+    "fp8_e4m3fn_p64": dict(q_lens=[70, 1, 130], ctx=[900, 40, 0], page=64, Hkv=2, G=2, D=128, S=8,
+                           dtype=torch.bfloat16, lb=8, kv=torch.float8_e4m3fn),
+    "fp8_e5m2_p32_nobias": dict(q_lens=[64, 33], ctx=[500, 1200], page=32, Hkv=1, G=3, D=128, S=6,
+                                dtype=torch.bfloat16, lb=4, bias=False, kv=torch.float8_e5m2),
+    "fp8_e4m3fnuz_fp16_d64": dict(q_lens=[90, 17, 5], ctx=[300, 0, 77], page=16, Hkv=2, G=1, D=64, S=5,
+                                  dtype=torch.float16, lb=6, kv=torch.float8_e4m3fnuz),
+    "fp8_e5m2fnuz_p128": dict(q_lens=[40, 65], ctx=[600, 200], page=128, Hkv=2, G=2, D=128, S=4,
+                              dtype=torch.bfloat16, lb=2, kv=torch.float8_e5m2fnuz),
 }
 
 
@@ -69,6 +78,7 @@ def test_dash_sparse_attn_matches_oracle(dev, name):
     c = _case(list(CASES).index(name) + 40, **kw)
     scale = 1 / math.sqrt(kw["D"])
     out = torch.full(c["q"].shape, float("nan"), dtype=c["q"].dtype, device=dev)
+    print(f"dash_sparse_attn {name}", flush=True)
     U.dash_sparse_attn(c["q"].to(dev), c["kc"].to(dev), c["vc"].to(dev), c["topk"].to(dev),
                        None if c["bias"] is None else c["bias"].to(dev), c["bt"].to(dev), c["cu"].to(dev),
                        c["seq"].to(dev), c["ctx"].to(dev), c["max_q"], c["Hkv"], scale, out, local_blocks=lb,

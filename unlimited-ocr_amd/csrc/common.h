@@ -81,6 +81,80 @@ template <> struct Vec16<__half> {
   }
 };
 
+// fp8 K/V cache formats (srswa_dtype codes of the k_cache / v_cache of the
+// paged serving kernels).  Every fp8 value is exact in bf16 and fp16, so the
+// kernels convert at load time and run their 16-bit paths unchanged, as the
+// reference's `k.to(q.dtype)` does, on gfx950's conversion instructions
+// (v_cvt_pk_f32_fp8 / _bf8 interpret the OCP e4m3fn / e5m2 formats).
+constexpr int kFp8E4M3FN = 3, kFp8E4M3FNUZ = 4, kFp8E5M2 = 5, kFp8E5M2FNUZ = 6;
+
+typedef float f32x2_t __attribute__((ext_vector_type(2)));
+
+// four fp8 bytes of w (byte 0 first) -> fp32.  An FNUZ byte is the same OCP
+// byte's value halved (its bias is one higher), except 0x80 (FNUZ NaN, OCP -0)
+// and the codes OCP keeps for NaN / infinity, which FNUZ uses for ordinary
+// values: |b| = 0x7f in e4m3 (240), exponent 31 in e5m2 ((1 + m/4) 2^15).
+template <int F>
+__device__ __forceinline__ void fp8x4_to_f32(uint32_t w, float* f) {
+  constexpr bool E4 = F == kFp8E4M3FN || F == kFp8E4M3FNUZ;
+  constexpr bool FNUZ = F == kFp8E4M3FNUZ || F == kFp8E5M2FNUZ;
+  f32x2_t lo, hi;
+  if constexpr (E4) {
+    lo = __builtin_amdgcn_cvt_pk_f32_fp8((int)w, false);
+    hi = __builtin_amdgcn_cvt_pk_f32_fp8((int)w, true);
+  } else {
+    lo = __builtin_amdgcn_cvt_pk_f32_bf8((int)w, false);
+    hi = __builtin_amdgcn_cvt_pk_f32_bf8((int)w, true);
+  }
+  f[0] = lo.x;
+  f[1] = lo.y;
+  f[2] = hi.x;
+  f[3] = hi.y;
+  if constexpr (FNUZ) {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) f[i] *= 0.5f;
+    // the bytes OCP reads differently (rare): a zero byte of t flags them
+    constexpr uint32_t kMask = E4 ? 0x7f7f7f7fu : 0x7c7c7c7cu;
+    const uint32_t t1 = (w & kMask) ^ kMask, t2 = w ^ 0x80808080u;
+    const uint32_t zero_byte = ((t1 - 0x01010101u) & ~t1 & 0x80808080u) | ((t2 - 0x01010101u) & ~t2 & 0x80808080u);
+    if (__builtin_expect(zero_byte != 0u, 0)) {
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const uint32_t b = (w >> (8 * i)) & 0xffu;
+        float v = f[i];
+        if constexpr (E4) {
+          v = (b & 0x7fu) == 0x7fu ? ((b & 0x80u) ? -240.f : 240.f) : v;
+        } else {
+          const float big = (float)(4u + (b & 3u)) * 8192.f;   // (1 + m/4) 2^15
+          v = (b & 0x7cu) == 0x7cu ? ((b & 0x80u) ? -big : big) : v;
+        }
+        f[i] = b == 0x80u ? __uint_as_float(0x7fc00000u) : v;
+      }
+    }
+  }
+}
+
+// eight fp8 bytes -> eight values of T (bf16 / fp16) as one 16-byte vector
+template <int F, typename T>
+__device__ __forceinline__ uint4 fp8x8_to(const uint2& w) {
+  float f[8];
+  fp8x4_to_f32<F>(w.x, f);
+  fp8x4_to_f32<F>(w.y, f + 4);
+  return Vec16<T>::pack(f);
+}
+
+// Runs fn(std::integral_constant<int, F>) for the fp8 format fmt: one uniform
+// branch around a whole loop instead of one per converted vector.
+template <typename Fn>
+__device__ __forceinline__ void fp8_dispatch(int fmt, Fn&& fn) {
+  switch (fmt) {
+    case kFp8E4M3FN: fn(std::integral_constant<int, kFp8E4M3FN>{}); break;
+    case kFp8E5M2: fn(std::integral_constant<int, kFp8E5M2>{}); break;
+    case kFp8E4M3FNUZ: fn(std::integral_constant<int, kFp8E4M3FNUZ>{}); break;
+    default: fn(std::integral_constant<int, kFp8E5M2FNUZ>{}); break;
+  }
+}
+
 // Full-wavefront reductions (64 lanes, every lane active) on DPP: each level
 // is a VALU operand modifier instead of an LDS permute round trip.  Within each
 // 16-lane row: quad_perm [1,0,3,2], quad_perm [2,3,0,1], row_half_mirror,

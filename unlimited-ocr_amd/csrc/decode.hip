@@ -70,6 +70,7 @@ struct DecodeK {
   const int32_t* bt;
   int64_t bt_sb, k_pst, v_pst;   // block-table row stride, page strides (elements)
   int bs_shift, max_blocks;
+  int kv8;                       // FP8 kernels: the caches' fp8 format (srswa_dtype)
 };
 
 template <typename TO>
@@ -150,10 +151,31 @@ __device__ __forceinline__ uint4 load_stream(const void* p) {
   const u32x4_t v = __builtin_nontemporal_load(reinterpret_cast<const u32x4_t*>(p));
   return make_uint4(v.x, v.y, v.z, v.w);
 }
+typedef unsigned int u32x2_t __attribute__((ext_vector_type(2)));
+__device__ __forceinline__ uint2 load_stream8(const void* p) {
+  const u32x2_t v = __builtin_nontemporal_load(reinterpret_cast<const u32x2_t*>(p));
+  return make_uint2(v.x, v.y);
+}
 
-template <typename T, typename TO, int D, int NI, bool PAGED>
+// A lane's 8 (16-bit) or 4 (fp32) elements of a K / V row: one 16-byte load,
+// or with an fp8 cache (FP8) one 8-byte load, converted after the loads are
+// issued (the raw words wait here).
+template <typename T, bool FP8> struct KVRaw {
+  uint4 w;
+  __device__ __forceinline__ void load(const void* p) { w = load_stream(p); }
+  __device__ __forceinline__ void zero() { w = make_uint4(0, 0, 0, 0); }
+};
+template <typename T> struct KVRaw<T, true> {
+  uint2 w;
+  __device__ __forceinline__ void load(const void* p) { w = load_stream8(p); }
+  __device__ __forceinline__ void zero() { w = make_uint2(0, 0); }
+};
+
+template <typename T, typename TO, int D, int NI, bool PAGED, bool FP8 = false>
 __global__ __launch_bounds__(kDecodeWaves * kWave) void decode_kernel(DecodeK p) {
   using V = Vec16<T>;
+  using KE = std::conditional_t<FP8, uint8_t, T>;   // cache element
+  static_assert(!FP8 || (PAGED && sizeof(T) == 2), "fp8 caches: paged, 16-bit queries");
   constexpr int EPV = V::N;           // elements per 16-byte vector
   constexpr int LPR = D / EPV;        // lanes per key row
   constexpr int RPI = kWave / LPR;    // key rows per load instruction
@@ -196,10 +218,10 @@ __global__ __launch_bounds__(kDecodeWaves * kWave) void decode_kernel(DecodeK p)
   const int64_t aux_off = (int64_t)b * a.idx_sb + (int64_t)ih * a.idx_sh +
                           (int64_t)lq * a.idx_sq;
 
-  const T* kbase = reinterpret_cast<const T*>(a.k) + (PAGED ? 0 : (int64_t)b * a.k_sb) +
-                   (int64_t)kvh * a.k_sh + c * EPV;
-  const T* vbase = reinterpret_cast<const T*>(a.v) + (PAGED ? 0 : (int64_t)b * a.v_sb) +
-                   (int64_t)kvh * a.v_sh + c * EPV;
+  const KE* kbase = reinterpret_cast<const KE*>(a.k) + (PAGED ? 0 : (int64_t)b * a.k_sb) +
+                    (int64_t)kvh * a.k_sh + c * EPV;
+  const KE* vbase = reinterpret_cast<const KE*>(a.v) + (PAGED ? 0 : (int64_t)b * a.v_sb) +
+                    (int64_t)kvh * a.v_sh + c * EPV;
   int max_blk = kvl > 0 ? (kvl - 1) / a.block_size : -1;
   if (PAGED) max_blk = min(max_blk, p.max_blocks - 1);
   const int32_t* bt_row = PAGED ? p.bt + (int64_t)b * p.bt_sb : nullptr;
@@ -304,15 +326,15 @@ __global__ __launch_bounds__(kDecodeWaves * kWave) void decode_kernel(DecodeK p)
     if (k1 <= klo) continue;   // uniform across the wave
 
     // unit base: the sequence's K / V rows (contiguous) or the unit's page
-    const T* kb = kbase;
-    const T* vb = vbase;
+    const KE* kb = kbase;
+    const KE* vb = vbase;
     int kr0 = k0;              // row of key k0 in kb / vb
     if (PAGED) {
       kb += (int64_t)page * p.k_pst;
       vb += (int64_t)page * p.v_pst;
       kr0 = k0 & (a.block_size - 1);
     }
-    uint4 kr[NI], vr[NI];
+    KVRaw<T, FP8> kw[NI], vw[NI];
     // key of unit slot kk (wrapped slots: LW further on, in page2)
     auto key_of = [&](int kk) { return k0 + kk + (PAGED && kk < wrap ? a.local_window : 0); };
     if (PAGED && wrap > 0) {
@@ -323,33 +345,42 @@ __global__ __launch_bounds__(kDecodeWaves * kWave) void decode_kernel(DecodeK p)
         const int kk = i * RPI + r;
         const int key = key_of(kk);
         const int64_t ro = kk < wrap ? dk + (int64_t)(w0 + kk) * a.k_st : (int64_t)(kr0 + kk) * a.k_st;
-        kr[i] = (key >= klo && key < k1) ? load_stream(kb + ro) : make_uint4(0, 0, 0, 0);
+        if (key >= klo && key < k1) kw[i].load(kb + ro);
+        else kw[i].zero();
       }
 #pragma unroll
       for (int i = 0; i < NI; ++i) {
         const int kk = i * RPI + r;
         const int key = key_of(kk);
         const int64_t ro = kk < wrap ? dv + (int64_t)(w0 + kk) * a.v_st : (int64_t)(kr0 + kk) * a.v_st;
-        vr[i] = (key >= klo && key < k1) ? load_stream(vb + ro) : make_uint4(0, 0, 0, 0);
+        if (key >= klo && key < k1) vw[i].load(vb + ro);
+        else vw[i].zero();
       }
     } else {
 #pragma unroll
       for (int i = 0; i < NI; ++i) {
         const int key = k0 + i * RPI + r;
-        kr[i] = ((!PAGED || key >= klo) && key < k1) ? load_stream(kb + (int64_t)(kr0 + i * RPI + r) * a.k_st)
-                                                     : make_uint4(0, 0, 0, 0);
+        if ((!PAGED || key >= klo) && key < k1) kw[i].load(kb + (int64_t)(kr0 + i * RPI + r) * a.k_st);
+        else kw[i].zero();
       }
 #pragma unroll
       for (int i = 0; i < NI; ++i) {
         const int key = k0 + i * RPI + r;
-        vr[i] = ((!PAGED || key >= klo) && key < k1) ? load_stream(vb + (int64_t)(kr0 + i * RPI + r) * a.v_st)
-                                                     : make_uint4(0, 0, 0, 0);
+        if ((!PAGED || key >= klo) && key < k1) vw[i].load(vb + (int64_t)(kr0 + i * RPI + r) * a.v_st);
+        else vw[i].zero();
       }
     }
 
     float part[NI];
+    if constexpr (FP8) {
+      fp8_dispatch(p.kv8, [&](auto F) {
 #pragma unroll
-    for (int i = 0; i < NI; ++i) part[i] = qf.dot(kr[i]);
+        for (int i = 0; i < NI; ++i) part[i] = qf.dot(fp8x8_to<decltype(F)::value, T>(kw[i].w));
+      });
+    } else {
+#pragma unroll
+      for (int i = 0; i < NI; ++i) part[i] = qf.dot(kw[i].w);
+    }
     // reduce-scatter across the LPR lanes of a row: NI partials -> 1 score
     reduce_scatter<NI, LPR / 2>(part, c);
 #pragma unroll
@@ -372,12 +403,25 @@ __global__ __launch_bounds__(kDecodeWaves * kWave) void decode_kernel(DecodeK p)
     float pv[NI];
 #pragma unroll
     for (int i = 0; i < NI; ++i) pv[i] = s_p[wave][r * NI + i];
+    if constexpr (FP8) {
+      fp8_dispatch(p.kv8, [&](auto F) {
 #pragma unroll
-    for (int i = 0; i < NI; ++i) {
-      float f[EPV];
-      V::unpack(vr[i], f);
+        for (int i = 0; i < NI; ++i) {
+          float f[8];
+          fp8x4_to_f32<decltype(F)::value>(vw[i].w.x, f);
+          fp8x4_to_f32<decltype(F)::value>(vw[i].w.y, f + 4);
 #pragma unroll
-      for (int e = 0; e < EPV; ++e) acc[e] = fmaf(pv[i], f[e], acc[e]);
+          for (int e = 0; e < EPV; ++e) acc[e] = fmaf(pv[i], f[e], acc[e]);
+        }
+      });
+    } else {
+#pragma unroll
+      for (int i = 0; i < NI; ++i) {
+        float f[EPV];
+        V::unpack(vw[i].w, f);
+#pragma unroll
+        for (int e = 0; e < EPV; ++e) acc[e] = fmaf(pv[i], f[e], acc[e]);
+      }
     }
     __builtin_amdgcn_wave_barrier();
   }
@@ -536,7 +580,14 @@ size_t scratch_bytes(const DecodePlan& pl) {
 
 template <typename T, typename TO, int D, int NI>
 int launch_decode_ni(const DecodeK& k, int64_t grid, hipStream_t st) {
-  if (k.bt)
+  if constexpr (sizeof(T) == 2 && std::is_same_v<T, TO>) {
+    if (k.kv8 && k.bt)
+      hipLaunchKernelGGL((decode_kernel<T, TO, D, NI, true, true>), dim3((unsigned)grid),
+                         dim3(kDecodeWaves * kWave), 0, st, k);
+  }
+  if (k.kv8) {
+    // fp8 caches take the 16-bit paged kernels only (checked by the caller)
+  } else if (k.bt)
     hipLaunchKernelGGL((decode_kernel<T, TO, D, NI, true>), dim3((unsigned)grid),
                        dim3(kDecodeWaves * kWave), 0, st, k);
   else
@@ -730,6 +781,14 @@ extern "C" int srswa_gather_decode_paged(const srswa_paged_decode_args* a, void*
     return SRSWA_UNSUPPORTED;
   }
   const int ib = elem_bytes(a->in_dtype), ob = elem_bytes(a->out_dtype);
+  const bool fp8 = a->kv_fp8 != 0;
+  if (fp8 && (a->kv_fp8 < SRSWA_FP8_E4M3FN || a->kv_fp8 > SRSWA_FP8_E5M2FNUZ || a->in_dtype == SRSWA_F32 ||
+              a->out_dtype != a->in_dtype)) {
+    set_error("paged decode: fp8 caches (kv_fp8 %d) take bf16 / fp16 queries and outputs of the same dtype",
+              a->kv_fp8);
+    return SRSWA_UNSUPPORTED;
+  }
+  const int kvb = fp8 ? 1 : ib;            // cache element bytes
   const int rpi = kWave / (a->D * ib / 16);
   if ((a->page_size & (a->page_size - 1)) || a->page_size < rpi) {
     set_error("paged decode: page size %d must be a power of two >= %d", a->page_size, rpi);
@@ -739,10 +798,17 @@ extern "C" int srswa_gather_decode_paged(const srswa_paged_decode_args* a, void*
     set_error("paged decode: at most 63 local blocks and 1024 slots");
     return SRSWA_UNSUPPORTED;
   }
-  const int64_t strides[] = {a->q_sn, a->q_sh, a->k_sp, a->k_st, a->k_sh, a->v_sp, a->v_st, a->v_sh};
-  for (int64_t st : strides)
+  const int64_t qstrides[] = {a->q_sn, a->q_sh};
+  for (int64_t st : qstrides)
     if ((st * ib) % 16 != 0) {
       set_error("paged decode: strides must keep rows 16-byte aligned");
+      return SRSWA_UNSUPPORTED;
+    }
+  // a lane reads 8 (16-bit) elements of a cache row: 16 bytes, 8 with fp8
+  const int64_t kvstrides[] = {a->k_sp, a->k_st, a->k_sh, a->v_sp, a->v_st, a->v_sh};
+  for (int64_t st : kvstrides)
+    if ((st * kvb) % (fp8 ? 8 : 16) != 0) {
+      set_error("paged decode: cache strides must keep rows %d-byte aligned", fp8 ? 8 : 16);
       return SRSWA_UNSUPPORTED;
     }
   if (((a->o_sn * ob) % 16) || ((a->o_sh * ob) % 16) || !aligned16(a->q) || !aligned16(a->k_cache) ||
@@ -777,6 +843,7 @@ extern "C" int srswa_gather_decode_paged(const srswa_paged_decode_args* a, void*
   k.v_pst = a->v_sp;
   k.bs_shift = __builtin_ctz((unsigned)a->page_size);
   k.max_blocks = a->max_blocks;
+  k.kv8 = a->kv_fp8;
   const int64_t grid = pl.rowheads * pl.nsplit;
   if (grid > 0x7fffffff) {
     set_error("paged decode: grid too large");

@@ -61,6 +61,7 @@ struct FwdK {
   const int32_t* seqlen;
   const int32_t* bt;
   int64_t bt_sr, k_pst, v_pst;
+  int kv8;                     // FP8: the caches' fp8 format (srswa_dtype)
 };
 
 template <int D> struct FwdLds {
@@ -71,8 +72,11 @@ template <int D> struct FwdLds {
   static constexpr int tileBytes = vOff + kChunk * VP * 2;
 };
 
-template <typename T, int D, bool PAGED>
+template <typename T, int D, bool PAGED, bool FP8 = false>
 __global__ __launch_bounds__(128, 2) void fwd_kernel(FwdK p) {
+  static_assert(!FP8 || PAGED, "fp8 caches: the paged form");
+  using KE = std::conditional_t<FP8, uint8_t, T>;   // cache element
+  using Pre = std::conditional_t<FP8, uint2, uint4>;  // a staged piece: 8 cache elements
   using M = Mfma<T>;
   using L = FwdLds<D>;
   constexpr int KP = L::KP, VP = L::VP;
@@ -209,15 +213,15 @@ __global__ __launch_bounds__(128, 2) void fwd_kernel(FwdK p) {
   // this thread's 16-byte piece of the first staged row; later pieces are RPP rows apart
   T* sKw = sK + (tid / (D / 8)) * KP + (tid % (D / 8)) * 8;
   T* sVw = sV + (tid / (D / 8)) * VP + (tid % (D / 8)) * 8;
-  uint4 kpre[PPT], vpre[PPT];
+  Pre kpre[PPT], vpre[PPT];
   // paged: the kv head's base (uniform) and this thread's column byte offset.
   // Piece i of a thread covers chunk row tid / (D/8) + i * RPP, whose 16-key
   // quarter is (i * RPP) / 16 for every thread (tid / (D/8) < RPP <= 16), so
   // the page of each piece is uniform: its base goes to scalar registers
   // (readfirstlane) and only a 32-bit in-page offset stays per lane.
-  const char* kpg = reinterpret_cast<const char*>(reinterpret_cast<const T*>(a.k) + (int64_t)kvh * a.k_sh);
-  const char* vpg = reinterpret_cast<const char*>(reinterpret_cast<const T*>(a.v) + (int64_t)kvh * a.v_sh);
-  const uint32_t col_b = (uint32_t)(tid % (D / 8)) * 16u;
+  const char* kpg = reinterpret_cast<const char*>(reinterpret_cast<const KE*>(a.k) + (int64_t)kvh * a.k_sh);
+  const char* vpg = reinterpret_cast<const char*>(reinterpret_cast<const KE*>(a.v) + (int64_t)kvh * a.v_sh);
+  const uint32_t col_b = (uint32_t)(tid % (D / 8)) * 8u * (uint32_t)sizeof(KE);
   auto fetch = [&](int u) {
     const int c = s_chunks[u];
     if constexpr (PAGED) {
@@ -242,17 +246,17 @@ __global__ __launch_bounds__(128, 2) void fwd_kernel(FwdK p) {
         const int j = c * kChunk + row;
         const int pg = qpg[(i * RPP) >> 4];
         const uint32_t jr = (uint32_t)(j & (BS - 1));
-        const char* kb = kpg + (int64_t)pg * p.k_pst * (int64_t)sizeof(T);
-        const char* vb = vpg + (int64_t)pg * p.v_pst * (int64_t)sizeof(T);
+        const char* kb = kpg + (int64_t)pg * p.k_pst * (int64_t)sizeof(KE);
+        const char* vb = vpg + (int64_t)pg * p.v_pst * (int64_t)sizeof(KE);
         if (j < Skb) {
-          kpre[i] = *reinterpret_cast<const uint4*>(kb + (jr * (uint32_t)a.k_st * (uint32_t)sizeof(T) + col_b));
-          vpre[i] = *reinterpret_cast<const uint4*>(vb + (jr * (uint32_t)a.v_st * (uint32_t)sizeof(T) + col_b));
+          kpre[i] = *reinterpret_cast<const Pre*>(kb + (jr * (uint32_t)a.k_st * (uint32_t)sizeof(KE) + col_b));
+          vpre[i] = *reinterpret_cast<const Pre*>(vb + (jr * (uint32_t)a.v_st * (uint32_t)sizeof(KE) + col_b));
         } else {
-          kpre[i] = make_uint4(0, 0, 0, 0);
-          vpre[i] = make_uint4(0, 0, 0, 0);
+          kpre[i] = Pre{};
+          vpre[i] = Pre{};
         }
       }
-    } else {
+    } else if constexpr (!FP8) {
       const uint32_t kso = (uint32_t)c * kChunk * (uint32_t)a.k_st * 2u;
       const uint32_t vso = (uint32_t)c * kChunk * (uint32_t)a.v_st * 2u;
 #pragma unroll
@@ -268,10 +272,20 @@ __global__ __launch_bounds__(128, 2) void fwd_kernel(FwdK p) {
   for (int u = 0; u < U; ++u) {
     const int j0 = (int)s_chunks[u] * kChunk;
     __syncthreads();   // previous chunk fully consumed
+    if constexpr (FP8) {
+      fp8_dispatch(p.kv8, [&](auto F) {
 #pragma unroll
-    for (int i = 0; i < PPT; ++i) {
-      *reinterpret_cast<uint4*>(sKw + i * RPP * KP) = kpre[i];
-      *reinterpret_cast<uint4*>(sVw + i * RPP * VP) = vpre[i];
+        for (int i = 0; i < PPT; ++i) {
+          *reinterpret_cast<uint4*>(sKw + i * RPP * KP) = fp8x8_to<decltype(F)::value, T>(kpre[i]);
+          *reinterpret_cast<uint4*>(sVw + i * RPP * VP) = fp8x8_to<decltype(F)::value, T>(vpre[i]);
+        }
+      });
+    } else {
+#pragma unroll
+      for (int i = 0; i < PPT; ++i) {
+        *reinterpret_cast<uint4*>(sKw + i * RPP * KP) = kpre[i];
+        *reinterpret_cast<uint4*>(sVw + i * RPP * VP) = vpre[i];
+      }
     }
     __syncthreads();
     if (u + 1 < U) fetch(u + 1);
@@ -483,11 +497,11 @@ int check_fwd(const srswa_fwd_args* a) {
   return SRSWA_OK;
 }
 
-template <typename T, int D, bool PAGED>
+template <typename T, int D, bool PAGED, bool FP8 = false>
 int launch_fwd(const FwdK& k, size_t smem, hipStream_t st) {
   static LdsGrant granted;
-  if (!ensure_dynamic_lds(&fwd_kernel<T, D, PAGED>, smem, &granted)) return SRSWA_UNSUPPORTED;
-  hipLaunchKernelGGL((fwd_kernel<T, D, PAGED>), dim3((unsigned)(8 * k.per_xcd)), dim3(128), smem, st, k);
+  if (!ensure_dynamic_lds(&fwd_kernel<T, D, PAGED, FP8>, smem, &granted)) return SRSWA_UNSUPPORTED;
+  hipLaunchKernelGGL((fwd_kernel<T, D, PAGED, FP8>), dim3((unsigned)(8 * k.per_xcd)), dim3(128), smem, st, k);
   const hipError_t e = hipGetLastError();
   if (e != hipSuccess) {
     set_error("fwd launch failed: %s", hipGetErrorString(e));
@@ -577,10 +591,22 @@ extern "C" int srswa_gather_fwd_paged(const srswa_paged_fwd_args* a, void* strea
     set_error("paged fwd: block table spans more than 4M keys");
     return SRSWA_UNSUPPORTED;
   }
-  const int64_t st[] = {a->q_sn, a->q_sh, a->k_sp, a->k_st, a->k_sh, a->v_sp, a->v_st, a->v_sh, a->o_sn, a->o_sh};
+  const bool fp8 = a->kv_fp8 != 0;
+  if (fp8 && (a->kv_fp8 < SRSWA_FP8_E4M3FN || a->kv_fp8 > SRSWA_FP8_E5M2FNUZ)) {
+    set_error("paged fwd: kv_fp8 %d is not an fp8 format", a->kv_fp8);
+    return SRSWA_UNSUPPORTED;
+  }
+  const int64_t st[] = {a->q_sn, a->q_sh, a->o_sn, a->o_sh};
   for (int64_t v : st)
     if ((v * 2) % 16) {
       set_error("paged fwd: rows must be 16-byte aligned");
+      return SRSWA_UNSUPPORTED;
+    }
+  // a staged piece is 8 cache elements: 16 bytes, 8 with fp8
+  const int64_t kvst[] = {a->k_sp, a->k_st, a->k_sh, a->v_sp, a->v_st, a->v_sh};
+  for (int64_t v : kvst)
+    if ((v * (fp8 ? 1 : 2)) % (fp8 ? 8 : 16)) {
+      set_error("paged fwd: cache rows must be %d-byte aligned", fp8 ? 8 : 16);
       return SRSWA_UNSUPPORTED;
     }
   if (!al16(a->q) || !al16(a->k_cache) || !al16(a->v_cache) || !al16(a->out)) {
@@ -607,6 +633,7 @@ extern "C" int srswa_gather_fwd_paged(const srswa_paged_fwd_args* a, void* strea
   k.bt_sr = a->bt_sr;
   k.k_pst = a->k_sp;
   k.v_pst = a->v_sp;
+  k.kv8 = a->kv_fp8;
   k.ntiles = ceil_div(a->max_query_len, kTileRows);
   const int nchunk = ceil_div((int)keys, kChunk);
   k.nwords = ceil_div(nchunk, 32);
@@ -644,6 +671,12 @@ extern "C" int srswa_gather_fwd_paged(const srswa_paged_fwd_args* a, void* strea
     return SRSWA_UNSUPPORTED;
   }
   hipStream_t s = reinterpret_cast<hipStream_t>(stream);
+  if (fp8) {
+    if (a->dtype == SRSWA_BF16)
+      return a->D == 128 ? launch_fwd<bf16_t, 128, true, true>(k, smem, s)
+                         : launch_fwd<bf16_t, 64, true, true>(k, smem, s);
+    return a->D == 128 ? launch_fwd<__half, 128, true, true>(k, smem, s) : launch_fwd<__half, 64, true, true>(k, smem, s);
+  }
   if (a->dtype == SRSWA_BF16)
     return a->D == 128 ? launch_fwd<bf16_t, 128, true>(k, smem, s) : launch_fwd<bf16_t, 64, true>(k, smem, s);
   return a->D == 128 ? launch_fwd<__half, 128, true>(k, smem, s) : launch_fwd<__half, 64, true>(k, smem, s);

@@ -110,6 +110,7 @@ class PagedFwdArgs(ctypes.Structure):
         ("max_blocks", _i32), ("page_size", _i32), ("local_blocks", _i32),
         ("scale", ctypes.c_float),
         ("dtype", _i32),
+        ("kv_fp8", _i32),
     ]
 
 
@@ -168,6 +169,7 @@ class PagedDecodeArgs(ctypes.Structure):
         ("max_blocks", _i32), ("page_size", _i32), ("local_blocks", _i32),
         ("scale", ctypes.c_float),
         ("in_dtype", _i32), ("out_dtype", _i32),
+        ("kv_fp8", _i32),
     ]
 
 
@@ -526,6 +528,17 @@ def check(status: int, what: str) -> None:
     if status == SRSWA_UNSUPPORTED:
         raise UnsupportedShape(f"{what}: {msg}")
     raise RuntimeError(f"{what} failed (status {status}): {msg}")
+
+
+FP8_CODES = {}
+for _name, _code in (("float8_e4m3fn", 3), ("float8_e4m3fnuz", 4), ("float8_e5m2", 5), ("float8_e5m2fnuz", 6)):
+    if hasattr(torch, _name):
+        FP8_CODES[getattr(torch, _name)] = _code
+
+
+def fp8_code(dt: torch.dtype) -> int:
+    """srswa_dtype of an fp8 K/V cache dtype, 0 for any other dtype."""
+    return FP8_CODES.get(dt, 0)
 
 
 def dtype_code(dt: torch.dtype) -> int:

@@ -266,6 +266,23 @@ def topk_rows(scores, k, *, invalid_at=SCORE_NEG * 0.5, ascending=False, return_
     return (idx, val) if return_values else idx
 
 
+def _kv_fp8(q, k_cache, v_cache) -> int:
+    """The fp8 format code of the paged caches (0 when they share q's dtype).
+    fp8 caches (float8_e4m3fn / e4m3fnuz / e5m2 / e5m2fnuz) are converted
+    exactly to q's dtype as the kernels load them, as the reference's
+    ``k.to(q.dtype)`` (WHL!layers/attention/unlimited_dash_ops/attend_triton.py:193)."""
+    if k_cache.dtype != v_cache.dtype:
+        raise ValueError("k_cache and v_cache must share a dtype")
+    code = _lib.fp8_code(k_cache.dtype)
+    if code:
+        if q.dtype not in (torch.bfloat16, torch.float16):
+            raise UnsupportedShape("fp8 caches take bf16 / fp16 queries")
+        return code
+    if q.dtype != k_cache.dtype:
+        raise ValueError("q, k_cache, v_cache must share a dtype")
+    return 0
+
+
 def prepare_gather_decode_paged(q, k_cache, v_cache, topk_idx, blk_bias, block_table, seq_lens, *,
                                 decode_query_len, local_blocks, scale, out=None):
     """Validate, allocate and build the launch of the paged decode
@@ -286,8 +303,7 @@ def prepare_gather_decode_paged(q, k_cache, v_cache, topk_idx, blk_bias, block_t
         raise ValueError(f"cache shape {tuple(k_cache.shape)} / {tuple(v_cache.shape)} vs q {tuple(q.shape)}")
     if topk_idx.dim() != 3 or topk_idx.shape[0] != HKV or topk_idx.shape[1] != total_q:
         raise ValueError(f"topk_idx shape {tuple(topk_idx.shape)} != ({HKV}, {total_q}, K)")
-    if q.dtype != k_cache.dtype or q.dtype != v_cache.dtype:
-        raise ValueError("q, k_cache, v_cache must share a dtype")
+    kv8 = _kv_fp8(q, k_cache, v_cache)
     for t in (q, k_cache, v_cache):
         if t.stride(-1) != 1:
             raise UnsupportedShape("head dim must be contiguous")
@@ -321,6 +337,7 @@ def prepare_gather_decode_paged(q, k_cache, v_cache, topk_idx, blk_bias, block_t
     a.scale = float(scale)
     a.in_dtype = _lib.dtype_code(q.dtype)
     a.out_dtype = _lib.dtype_code(out.dtype)
+    a.kv_fp8 = kv8
     L_ = _lib.lib()
     nscr = L_.srswa_gather_decode_paged_workspace(ctypes.byref(a))
     scr = _lib.scratch(q.device, nscr)
@@ -355,8 +372,7 @@ def gather_fwd_paged(q, k_cache, v_cache, topk_idx, blk_bias, block_table, cu_se
         raise ValueError(f"cache shape {tuple(k_cache.shape)} / {tuple(v_cache.shape)} vs q {tuple(q.shape)}")
     if topk_idx.dim() != 3 or topk_idx.shape[0] != HKV or topk_idx.shape[1] != total_q:
         raise ValueError(f"topk_idx shape {tuple(topk_idx.shape)} != ({HKV}, {total_q}, K)")
-    if q.dtype != k_cache.dtype or q.dtype != v_cache.dtype:
-        raise ValueError("q, k_cache, v_cache must share a dtype")
+    kv8 = _kv_fp8(q, k_cache, v_cache)
     for t in (q, k_cache, v_cache):
         if t.stride(-1) != 1:
             raise UnsupportedShape("head dim must be contiguous")
@@ -396,6 +412,7 @@ def gather_fwd_paged(q, k_cache, v_cache, topk_idx, blk_bias, block_table, cu_se
     a.max_blocks, a.page_size, a.local_blocks = bt.shape[1], page, int(local_blocks)
     a.scale = float(scale)
     a.dtype = _lib.dtype_code(q.dtype)
+    a.kv_fp8 = kv8
     _lib.check(_lib.lib().srswa_gather_fwd_paged(ctypes.byref(a), _lib.stream_ptr(q.device)),
                "srswa_gather_fwd_paged")
     return out
