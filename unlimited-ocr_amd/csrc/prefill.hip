@@ -251,9 +251,12 @@ __global__ __launch_bounds__(128, 2) void fwd_kernel(FwdK p) {
         if (j < Skb) {
           kpre[i] = *reinterpret_cast<const Pre*>(kb + (jr * (uint32_t)a.k_st * (uint32_t)sizeof(KE) + col_b));
           vpre[i] = *reinterpret_cast<const Pre*>(vb + (jr * (uint32_t)a.v_st * (uint32_t)sizeof(KE) + col_b));
+        } else if constexpr (FP8) {
+          kpre[i] = make_uint2(0, 0);
+          vpre[i] = make_uint2(0, 0);
         } else {
-          kpre[i] = Pre{};
-          vpre[i] = Pre{};
+          kpre[i] = make_uint4(0, 0, 0, 0);
+          vpre[i] = make_uint4(0, 0, 0, 0);
         }
       }
     } else if constexpr (!FP8) {
