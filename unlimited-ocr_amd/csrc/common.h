@@ -4,6 +4,7 @@
 
 #include <hip/hip_runtime.h>
 #include <hip/hip_fp16.h>
+#include <limits.h>
 #include <stdint.h>
 
 #include <type_traits>
@@ -213,6 +214,27 @@ __device__ __forceinline__ T reduce(T v, T identity, Op op) {
   }
 }
 }  // namespace dpp
+
+// max / sum of this lane's value and lane (l ^ 32)'s, on the VALU:
+// v_permlane32_swap exchanges the upper half of its first operand with the
+// lower half of its second, so with both operands v every lane ends holding
+// {v[l], v[l ^ 32]} (the two orders give the same bits: fmaxf and a two-term
+// sum are commutative)
+__device__ __forceinline__ float xor32_max(float v) {
+  const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+  return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
+}
+__device__ __forceinline__ float xor32_sum(float v) {
+  const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+  return __uint_as_float(r[0]) + __uint_as_float(r[1]);
+}
+
+__device__ __forceinline__ int wave_max_int(int v) {
+  return dpp::reduce<int>(v, INT_MIN, [](int a, int b) { return a > b ? a : b; });
+}
+__device__ __forceinline__ int wave_min_int(int v) {
+  return dpp::reduce<int>(v, INT_MAX, [](int a, int b) { return a < b ? a : b; });
+}
 
 __device__ __forceinline__ float wave_max(float v) {
   return dpp::reduce<float>(v, -INFINITY, [](float a, float b) { return fmaxf(a, b); });

@@ -108,6 +108,59 @@ constexpr int kIdEnd = 0x7fffffff;   // sentinel closing a row's sorted id list
 __device__ inline void sort_row_ids(const int32_t* ids, const float* bias, int S, int SP, int BS,
                                     int maxblk, int qi, int seg, int ls, int* sid, float* sb,
                                     int* sslot = nullptr) {
+  if (S <= 8) {
+    // up to 8 slots: every id (and bias) is loaded at once, so the row pays
+    // one memory latency, and the (id, slot) keys are sorted in registers by
+    // Batcher's odd-even merge network (19 compare-exchanges); a repeated id
+    // then follows its first slot, which is the one kept
+    int id8[8];
+    float b8[8];
+#pragma unroll
+    for (int s = 0; s < 8; ++s) id8[s] = s < S ? ids[s] : -1;
+#pragma unroll
+    for (int s = 0; s < 8; ++s) b8[s] = bias && s < S ? bias[s] : 0.f;
+    uint32_t key[8];
+#pragma unroll
+    for (int s = 0; s < 8; ++s) {
+      const int id = id8[s];
+      bool ok = id >= 0 && id <= maxblk;
+      const int base = ok ? id * BS : 0;
+      ok = ok && max(base, seg) < min(min(base + BS, ls), qi + 1);
+      key[s] = ok ? ((uint32_t)id << 3) | (uint32_t)s : 0xffffffffu;
+    }
+    auto cas = [&](int i, int j) __attribute__((always_inline)) {
+      const uint32_t lo = min(key[i], key[j]), hi = max(key[i], key[j]);
+      key[i] = lo;
+      key[j] = hi;
+    };
+    cas(0, 1); cas(2, 3); cas(4, 5); cas(6, 7);
+    cas(0, 2); cas(1, 3); cas(4, 6); cas(5, 7);
+    cas(1, 2); cas(5, 6);
+    cas(0, 4); cas(1, 5); cas(2, 6); cas(3, 7);
+    cas(2, 4); cas(3, 5);
+    cas(1, 2); cas(3, 4); cas(5, 6);
+    int n = 0;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      const uint32_t k = key[i];
+      if (k == 0xffffffffu || (i > 0 && (key[i - 1] >> 3) == (k >> 3))) continue;
+      const int slot = (int)(k & 7u);
+      sid[n] = (int)(k >> 3);
+      if (sb) {
+        float bv = b8[0];
+#pragma unroll
+        for (int t = 1; t < 8; ++t) bv = slot == t ? b8[t] : bv;
+        sb[n] = bv;
+      }
+      if (sslot) sslot[n] = slot;
+      ++n;
+    }
+    for (int i = n; i < SP; ++i) {
+      sid[i] = kIdEnd;
+      if (sslot) sslot[i] = -1;
+    }
+    return;
+  }
   int n = 0;
   for (int s = 0; s < S; ++s) {
     const int id = ids[s];

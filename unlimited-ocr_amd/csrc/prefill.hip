@@ -40,6 +40,7 @@
 // q*scale and P are rounded to the input dtype before their products, the
 // same rounding points as the reference kernels (HF/sparse_gather_triton.py:68,94).
 #include <algorithm>
+#include <cmath>
 
 #include "mfma_common.h"
 
@@ -130,6 +131,18 @@ __global__ __launch_bounds__(128, 2) void fwd_kernel(FwdK p) {
   // scales the fp32 product (attend_triton.py:204)
   const float l2s = PAGED ? a.scale * kLog2e : kLog2e;
 
+  // this lane's query row, loaded first so its latency overlaps the set-up
+  const int row = wave * 32 + rl;
+  const bool row_ok = row < nrows;
+  uint4 qf[KS];
+  {
+    const T* qrow = reinterpret_cast<const T*>(a.q) + (int64_t)b * a.q_sb +
+                    (int64_t)(q0 + t0 + (row_ok ? row : 0)) * a.q_st + (int64_t)hq * a.q_sh;
+#pragma unroll
+    for (int ks = 0; ks < KS; ++ks)
+      qf[ks] = row_ok ? *reinterpret_cast<const uint4*>(qrow + 16 * ks + 8 * h) : make_uint4(0, 0, 0, 0);
+  }
+
   if (tid < 64) {
     const int r = tid;
     int qi = -1, seg = 0, ls = 0;
@@ -169,27 +182,25 @@ __global__ __launch_bounds__(128, 2) void fwd_kernel(FwdK p) {
   }
 
   // this lane's row: window [ls, qi], remote candidates [seg, min(ls, qi + 1))
-  const int row = wave * 32 + rl;
-  const bool row_ok = row < nrows;
   const int my_ls = s_ls[row], my_seg = s_seg[row];
   const int my_hi = s_qi[row] + 1;
   const int rem_hi = min(my_ls, my_hi);
   const int* my_sid = s_sid + row * SP;
   const float* my_sb = s_sb ? s_sb + row * SP : nullptr;
+  // a chunk inside the window of every row of the wave, [w_ls_max, w_hi_min),
+  // takes no per-key mask, no bias and no walk of the selected ids (the
+  // bounds are wave-uniform)
+  const int w_ls_max = wave_max_int(row_ok ? my_ls : INT_MIN);
+  const int w_hi_min = wave_min_int(row_ok ? my_hi : INT_MAX);
+  const float inv_l2s = PAGED ? 1.f / a.scale * kLn2 : kLn2;
 
-  uint4 qf[KS];
-  {
-    const T* qrow = reinterpret_cast<const T*>(a.q) + (int64_t)b * a.q_sb +
-                    (int64_t)(q0 + t0 + (row_ok ? row : 0)) * a.q_st + (int64_t)hq * a.q_sh;
+
+  if constexpr (!PAGED) {
 #pragma unroll
     for (int ks = 0; ks < KS; ++ks) {
-      uint4 w = row_ok ? *reinterpret_cast<const uint4*>(qrow + 16 * ks + 8 * h) : make_uint4(0, 0, 0, 0);
-      if constexpr (!PAGED) {
-        uint32_t* ww = reinterpret_cast<uint32_t*>(&w);
+      uint32_t* ww = reinterpret_cast<uint32_t*>(&qf[ks]);
 #pragma unroll
-        for (int e = 0; e < 4; ++e) ww[e] = M::pack2(M::lo(ww[e]) * a.scale, M::hi(ww[e]) * a.scale);
-      }
-      qf[ks] = w;
+      for (int e = 0; e < 4; ++e) ww[e] = M::pack2(M::lo(ww[e]) * a.scale, M::hi(ww[e]) * a.scale);
     }
   }
 
@@ -293,37 +304,6 @@ __global__ __launch_bounds__(128, 2) void fwd_kernel(FwdK p) {
     __syncthreads();
     if (u + 1 < U) fetch(u + 1);
 
-    // the row's selected 16-key quarters of the chunk and their bias
-    uint32_t qmem = 0;
-    float bq[4] = {0.f, 0.f, 0.f, 0.f};
-    if (BS >= kChunk) {
-      const int blk = j0 >> p.bs_shift;
-      while (nid < blk) nid = my_sid[++cur];
-      if (nid == blk) {
-        qmem = 15u;
-        if (my_sb) bq[0] = bq[1] = bq[2] = bq[3] = my_sb[cur] * kLog2e;
-      }
-    } else {
-#pragma unroll
-      for (int qq = 0; qq < 4; ++qq) {
-        const int blk = (j0 + 16 * qq) >> p.bs_shift;
-        while (nid < blk) nid = my_sid[++cur];
-        if (nid == blk) {
-          qmem |= 1u << qq;
-          if (my_sb) bq[qq] = my_sb[cur] * kLog2e;
-        }
-      }
-    }
-    uint64_t qm = 0;
-#pragma unroll
-    for (int qq = 0; qq < 4; ++qq)
-      if (qmem & (1u << qq)) qm |= 0xffffull << (16 * qq);
-    const uint64_t wm = range64(min(max(my_ls - j0, 0), 64), min(max(my_hi - j0, 0), 64));
-    const uint64_t rm = range64(min(max(my_seg - j0, 0), 64), min(max(rem_hi - j0, 0), 64)) & qm;
-    const uint64_t keep = wm | rm;
-    const bool whole = !row_ok || (keep == ~0ull && (!my_sb || rm == 0ull || (rm == ~0ull && BS >= kChunk)));
-    const bool fast = __all(whole);
-
     // S^T (keys x rows) for the two 32-key halves of the chunk
     f32x16_t st[2] = {zero16(), zero16()};
     // the wave's issue priority is raised over its MFMA blocks: of the two waves
@@ -339,33 +319,75 @@ __global__ __launch_bounds__(128, 2) void fwd_kernel(FwdK p) {
     }
     __builtin_amdgcn_s_setprio(0);
 
-    // row max of the chunk's logits (log2 units); lane (l, h) holds keys
-    // 32 half + 8 (r / 4) + 4h + r % 4
-    float mloc = -INFINITY, addb = 0.f;
-    if (fast) {
-      if (my_sb && rm != 0ull) addb = bq[0];
+    // the row's keep mask: window keys | remote keys of its selected 16-key
+    // quarters (with their bias).  A chunk that every row of the wave keeps
+    // whole with one bias (always one inside every row's window) leaves the
+    // raw logits as they are; otherwise the masks and the bias are folded into
+    // them: a dropped key becomes -inf, a kept remote key's bias is added as
+    // bias / l2s (l2s > 0), so one softmax form below serves both.
+    float addb = 0.f;
+    if (!(j0 >= w_ls_max && j0 + kChunk <= w_hi_min)) {
+      uint32_t qmem = 0;
+      float bq[4] = {0.f, 0.f, 0.f, 0.f};
+      if (BS >= kChunk) {
+        const int blk = j0 >> p.bs_shift;
+        while (nid < blk) nid = my_sid[++cur];
+        if (nid == blk) {
+          qmem = 15u;
+          if (my_sb) bq[0] = bq[1] = bq[2] = bq[3] = my_sb[cur] * kLog2e;
+        }
+      } else {
 #pragma unroll
-      for (int half = 0; half < 2; ++half)
+        for (int qq = 0; qq < 4; ++qq) {
+          const int blk = (j0 + 16 * qq) >> p.bs_shift;
+          while (nid < blk) nid = my_sid[++cur];
+          if (nid == blk) {
+            qmem |= 1u << qq;
+            if (my_sb) bq[qq] = my_sb[cur] * kLog2e;
+          }
+        }
+      }
+      uint64_t qm = 0;
 #pragma unroll
-        for (int r = 0; r < 16; ++r) mloc = fmaxf(mloc, st[half][r]);
-      mloc = fmaf(mloc, l2s, addb);
-    } else {
-      const uint64_t kh = keep >> (4 * h), rh = rm >> (4 * h);
+      for (int qq = 0; qq < 4; ++qq)
+        if (qmem & (1u << qq)) qm |= 0xffffull << (16 * qq);
+      const uint64_t wm = range64(min(max(my_ls - j0, 0), 64), min(max(my_hi - j0, 0), 64));
+      const uint64_t rm = range64(min(max(my_seg - j0, 0), 64), min(max(rem_hi - j0, 0), 64)) & qm;
+      const uint64_t keep = wm | rm;
+      const bool whole = !row_ok || (keep == ~0ull && (!my_sb || rm == 0ull || (rm == ~0ull && BS >= kChunk)));
+      if (__all(whole)) {
+        if (my_sb && rm != 0ull) addb = bq[0];
+      } else {
+        const uint64_t kh = keep >> (4 * h), rh = rm >> (4 * h);
+        float bs[4];
 #pragma unroll
-      for (int half = 0; half < 2; ++half) {
-        const uint32_t k32 = (uint32_t)(kh >> (32 * half)), r32 = (uint32_t)(rh >> (32 * half));
+        for (int qq = 0; qq < 4; ++qq) bs[qq] = bq[qq] * inv_l2s;
 #pragma unroll
-        for (int r = 0; r < 16; ++r) {
-          const int bit = 8 * (r >> 2) + (r & 3);
-          float x = st[half][r] * l2s;
-          if (my_sb) x += ((r32 >> bit) & 1u) ? bq[2 * half + (r >> 3)] : 0.f;
-          x = ((k32 >> bit) & 1u) ? x : -INFINITY;
-          st[half][r] = x;
-          mloc = fmaxf(mloc, x);
+        for (int half = 0; half < 2; ++half) {
+          const uint32_t k32 = (uint32_t)(kh >> (32 * half)), r32 = (uint32_t)(rh >> (32 * half));
+#pragma unroll
+          for (int r = 0; r < 16; ++r) {
+            const int bit = 8 * (r >> 2) + (r & 3);
+            float x = st[half][r];
+            if (my_sb) x += ((r32 >> bit) & 1u) ? bs[2 * half + (r >> 3)] : 0.f;
+            st[half][r] = ((k32 >> bit) & 1u) ? x : -INFINITY;
+          }
         }
       }
     }
-    mloc = fmaxf(mloc, __shfl_xor(mloc, 32, kWave));
+
+    // row max of the chunk's logits (log2 units); lane (l, h) holds keys
+    // 32 half + 8 (r / 4) + 4h + r % 4
+    float mq[4];
+#pragma unroll
+    for (int g = 0; g < 4; ++g) {
+      const f32x16_t& s = st[g >> 1];
+      const int r0 = 8 * (g & 1);
+      mq[g] = fmaxf(fmaxf(fmaxf(s[r0], s[r0 + 1]), fmaxf(s[r0 + 2], s[r0 + 3])),
+                    fmaxf(fmaxf(s[r0 + 4], s[r0 + 5]), fmaxf(s[r0 + 6], s[r0 + 7])));
+    }
+    float mloc = fmaf(fmaxf(fmaxf(mq[0], mq[1]), fmaxf(mq[2], mq[3])), l2s, addb);
+    mloc = xor32_max(mloc);
     // lazy rescaling: the reference point m_b moves only when the chunk's max
     // exceeds it by more than 8 (p <= 2^8 stays exact in fp32 and in P's
     // rounding), so O is rescaled only on the rare chunks where a row's max jumps
@@ -382,29 +404,17 @@ __global__ __launch_bounds__(128, 2) void fwd_kernel(FwdK p) {
 #pragma unroll
         for (int r = 0; r < 16; ++r) o[mt][r] *= alpha;
     }
-    const float mb = m_b == -INFINITY ? 0.f : m_b;
-    float psum = 0.f;
-    if (fast) {
-      const float sub = addb - mb;
+    const float sub = addb - (m_b == -INFINITY ? 0.f : m_b);
+    float ps[4] = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-      for (int half = 0; half < 2; ++half)
+    for (int half = 0; half < 2; ++half)
 #pragma unroll
-        for (int r = 0; r < 16; ++r) {
-          const float pv = __builtin_amdgcn_exp2f(fmaf(st[half][r], l2s, sub));
-          st[half][r] = pv;
-          psum += pv;
-        }
-    } else {
-#pragma unroll
-      for (int half = 0; half < 2; ++half)
-#pragma unroll
-        for (int r = 0; r < 16; ++r) {
-          const float pv = __builtin_amdgcn_exp2f(st[half][r] - mb);
-          st[half][r] = pv;
-          psum += pv;
-        }
-    }
-    l_run += psum;
+      for (int r = 0; r < 16; ++r) {
+        const float pv = __builtin_amdgcn_exp2f(fmaf(st[half][r], l2s, sub));
+        st[half][r] = pv;
+        ps[2 * half + (r >> 3)] += pv;
+      }
+    l_run += (ps[0] + ps[1]) + (ps[2] + ps[3]);
 
     // P^T as B operands (4 steps of 16 keys), rounded to the input dtype
     uint4 pb[4];
@@ -428,7 +438,7 @@ __global__ __launch_bounds__(128, 2) void fwd_kernel(FwdK p) {
     __builtin_amdgcn_s_setprio(0);
   }
 
-  const float l_tot = l_run + __shfl_xor(l_run, 32, kWave);
+  const float l_tot = xor32_sum(l_run);
   if (!row_ok) return;
   const float inv = l_tot > 0.f ? 1.f / l_tot : 0.f;
   T* orow = reinterpret_cast<T*>(a.out) + (int64_t)b * a.o_sb + (int64_t)(q0 + t0 + row) * a.o_st +
@@ -592,6 +602,11 @@ extern "C" int srswa_gather_fwd_paged(const srswa_paged_fwd_args* a, void* strea
   const int64_t keys = (int64_t)a->max_blocks * a->page_size;
   if (ceil_div((int)std::min<int64_t>(keys, 1 << 30), kChunk) > 65536 || keys > (1 << 30)) {
     set_error("paged fwd: block table spans more than 4M keys");
+    return SRSWA_UNSUPPORTED;
+  }
+  // the kernel takes a chunk's row max before scaling (max(s) * scale = max(s * scale))
+  if (!(a->scale > 0.f) || !std::isfinite(a->scale)) {
+    set_error("paged fwd: scale must be positive and finite");
     return SRSWA_UNSUPPORTED;
   }
   const bool fp8 = a->kv_fp8 != 0;
