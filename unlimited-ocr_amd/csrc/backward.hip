@@ -9,18 +9,19 @@
 // [B, HI, T, M] block_mask scatter, HF/sparse_gather_triton.py:329,339-343).
 //
 // Kernels, in stream order:
-//   1. delta_kernel  -- delta[b,t,hq] = sum_d O*dO in fp32, and q*scale rounded
-//      to the input dtype as [B, HQ, T, D] (the dK operand, staged as is).
-//   2. zero + touch_kernel -- bit (chunk c, query tile tau) set when some row of
+//   1. zero + touch_kernel -- bit (chunk c, query tile tau) set when some row of
 //      tau reads a REMOTE key of chunk c.  The bitmap is tile-granular (64x
 //      smaller than the reference's per-token dense block mask) and its
 //      content does not depend on the order of the atomic ORs.
-//   3. dq_kernel  -- per 64-row query tile, the forward's chunk plan; per chunk
+//   2. dq_kernel  -- per 64-row query tile, the forward's chunk plan.  Its
+//      set-up computes each row's delta = sum_d O*dO in fp32 and q*scale
+//      rounded to the input dtype, and writes both for the dK / dV kernel
+//      (delta [B, T, HQ], q*scale [B, HQ, T, D]).  Per chunk
 //      S^T = K Q^T, dP^T = V dO^T, dS = P (dP - delta), dQ^T += K^T dS^T; the
 //      bias gradient (sum of fp32 dS over the remote keys of a selected block)
 //      is summed per (row, slot) in LDS and written once per query head --
 //      no atomics (the reference uses tl.atomic_add).
-//   4. dkv_kernel -- per 64-key chunk and kv head, every query tile whose
+//   3. dkv_kernel -- per 64-key chunk and kv head, every query tile whose
 //      window covers the chunk or whose touch bit is set, in ascending order:
 //      S = Q K^T, dP = dO V^T, dV^T += dO^T P, dK^T += Q^T dS, four waves split
 //      by key half and role (S / softmax / dV, dP / dS / dK).  Deterministic
@@ -47,48 +48,7 @@ struct BwdK {
   void* qs;           // [B, HQ, T, D] q * scale rounded to the input dtype (dK / dV operand)
 };
 
-// -------------------------------------------------------------- 1. delta
-template <typename T, int D>
-__global__ __launch_bounds__(256) void delta_kernel(BwdK p) {
-  constexpr int LPR = D / 8;                 // lanes per row (16-byte pieces)
-  constexpr int RPW = kWave / LPR;           // rows per wave
-  const srswa_bwd_args& a = p.a;
-  using M = Mfma<T>;
-  const int lane = threadIdx.x % kWave;
-  const int64_t row = ((int64_t)blockIdx.x * (blockDim.x / kWave) + threadIdx.x / kWave) * RPW + lane / LPR;
-  const int64_t rows = (int64_t)a.B * a.T * a.HQ;
-  const int c = lane % LPR;
-  float s = 0.f;
-  if (row < rows) {
-    const int hq = (int)(row % a.HQ);
-    const int64_t bt = row / a.HQ;
-    const int t = (int)(bt % a.T);
-    const int b = (int)(bt / a.T);
-    const uint4 ow = *reinterpret_cast<const uint4*>(reinterpret_cast<const T*>(a.o) + (int64_t)b * a.o_sb +
-                                                     (int64_t)t * a.o_st + (int64_t)hq * a.o_sh + c * 8);
-    const uint4 gw = *reinterpret_cast<const uint4*>(reinterpret_cast<const T*>(a.dout) + (int64_t)b * a.do_sb +
-                                                     (int64_t)t * a.do_st + (int64_t)hq * a.do_sh + c * 8);
-    const uint32_t* o4 = reinterpret_cast<const uint32_t*>(&ow);
-    const uint32_t* g4 = reinterpret_cast<const uint32_t*>(&gw);
-#pragma unroll
-    for (int e = 0; e < 4; ++e) s += M::lo(o4[e]) * M::lo(g4[e]) + M::hi(o4[e]) * M::hi(g4[e]);
-    if (p.qs) {
-      // q * scale rounded to the input dtype, [B, HQ, T, D]: the dK / dV kernel
-      // stages it as is (the reference's rounding point of the scaled query)
-      uint4 qw = *reinterpret_cast<const uint4*>(reinterpret_cast<const T*>(a.q) + (int64_t)b * a.q_sb +
-                                                 (int64_t)t * a.q_st + (int64_t)hq * a.q_sh + c * 8);
-      uint32_t* q4 = reinterpret_cast<uint32_t*>(&qw);
-#pragma unroll
-      for (int e = 0; e < 4; ++e) q4[e] = M::pack2(M::lo(q4[e]) * a.scale, M::hi(q4[e]) * a.scale);
-      *reinterpret_cast<uint4*>(reinterpret_cast<T*>(p.qs) + (((int64_t)b * a.HQ + hq) * a.T + t) * D + c * 8) = qw;
-    }
-  }
-#pragma unroll
-  for (int o = LPR / 2; o >= 1; o >>= 1) s += __shfl_xor(s, o, kWave);
-  if (row < rows && c == 0) p.delta[row] = s;
-}
-
-// -------------------------------------------------------------- 2. touch map
+// -------------------------------------------------------------- 1. touch map
 __global__ __launch_bounds__(256) void zero_words_kernel(uint32_t* w, int64_t n) {
   const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
   if (i < n) w[i] = 0u;
@@ -142,7 +102,7 @@ __global__ __launch_bounds__(256) void touch_kernel(BwdK p) {
   }
 }
 
-// -------------------------------------------------------------- 3. dQ
+// -------------------------------------------------------------- 2. dQ
 template <int D> struct DqLds {
   static constexpr int KP = D + 16;   // K: row reads (S^T) and transposing reads (dQ)
   static constexpr int VP = D + 8;    // V: row reads only
@@ -197,6 +157,27 @@ __global__ __launch_bounds__(128, D == 128 ? 1 : 2) void dq_kernel(BwdK p) {
   const int maxblk = (a.Sk - 1) >> p.bs_shift;
   const bool blk64 = BS >= kChunk;
 
+  // this lane's query row: q, dO, O and lse (log2 units; +inf for rows past
+  // T, so every P is 0), loaded first so their latency overlaps the set-up.
+  // Lanes l and l ^ 32 hold the two halves of a row's head dims.
+  const int row = wave * 32 + rl;
+  const bool row_ok = row < nrows;
+  const int trow = t0 + (row_ok ? row : 0);
+  uint4 qf[KS], gf[KS], of[KS];
+  {
+    const T* qrow = reinterpret_cast<const T*>(a.q) + (int64_t)b * a.q_sb + (int64_t)trow * a.q_st + (int64_t)hq * a.q_sh;
+    const T* grow = reinterpret_cast<const T*>(a.dout) + (int64_t)b * a.do_sb + (int64_t)trow * a.do_st + (int64_t)hq * a.do_sh;
+    const T* orow = reinterpret_cast<const T*>(a.o) + (int64_t)b * a.o_sb + (int64_t)trow * a.o_st + (int64_t)hq * a.o_sh;
+#pragma unroll
+    for (int ks = 0; ks < KS; ++ks) {
+      qf[ks] = row_ok ? *reinterpret_cast<const uint4*>(qrow + 16 * ks + 8 * h) : make_uint4(0, 0, 0, 0);
+      gf[ks] = row_ok ? *reinterpret_cast<const uint4*>(grow + 16 * ks + 8 * h) : make_uint4(0, 0, 0, 0);
+      of[ks] = row_ok ? *reinterpret_cast<const uint4*>(orow + 16 * ks + 8 * h) : make_uint4(0, 0, 0, 0);
+    }
+  }
+  const float lse_l2 = row_ok ? a.lse[(int64_t)b * a.lse_sb + (int64_t)trow * a.lse_st + (int64_t)hq * a.lse_sh] * kLog2e
+                              : INFINITY;
+
   if (tid < 64) {
     const int r = tid;
     int qi = -1, seg = 0, ls = 0;
@@ -220,9 +201,8 @@ __global__ __launch_bounds__(128, D == 128 ? 1 : 2) void dq_kernel(BwdK p) {
   __syncthreads();
   const int U = plan_chunks(s_qi, s_seg, s_ls, s_sid, SP, BS, LW, nrows, p.nwords, s_bits, s_chunks, s_count);
 
-  const int row = wave * 32 + rl;
   RowWalk w;
-  w.ok = row < nrows;
+  w.ok = row_ok;
   w.ls = s_ls[row];
   w.seg = s_seg[row];
   w.hi = s_qi[row] + 1;
@@ -231,25 +211,32 @@ __global__ __launch_bounds__(128, D == 128 ? 1 : 2) void dq_kernel(BwdK p) {
   w.sb = s_sb ? s_sb + row * SP : nullptr;
   w.cur = 0;
   w.nid = w.sid[0];
-  const int trow = t0 + (w.ok ? row : 0);
-  uint4 qf[KS], gf[KS];
-  {
-    const T* qrow = reinterpret_cast<const T*>(a.q) + (int64_t)b * a.q_sb + (int64_t)trow * a.q_st + (int64_t)hq * a.q_sh;
-    const T* grow = reinterpret_cast<const T*>(a.dout) + (int64_t)b * a.do_sb + (int64_t)trow * a.do_st + (int64_t)hq * a.do_sh;
+  // wave-uniform bounds of the rows' windows: [w_ls_max, w_hi_min) lies in every one
+  const int w_ls_max = wave_max_int(w.ok ? w.ls : INT_MIN);
+  const int w_hi_min = wave_min_int(w.ok ? w.hi : INT_MAX);
+  // delta = rowsum(O * dO) in fp32, published for the dK / dV kernel, and
+  // q * scale rounded to the input dtype (the reference's rounding point of
+  // the scaled query), kept here and written as [B, HQ, T, D] rows, which the
+  // dK / dV kernel stages as they are
+  float dpart = 0.f;
 #pragma unroll
-    for (int ks = 0; ks < KS; ++ks) {
-      uint4 x = w.ok ? *reinterpret_cast<const uint4*>(qrow + 16 * ks + 8 * h) : make_uint4(0, 0, 0, 0);
-      uint32_t* xx = reinterpret_cast<uint32_t*>(&x);
+  for (int ks = 0; ks < KS; ++ks) {
+    const uint32_t* o4 = reinterpret_cast<const uint32_t*>(&of[ks]);
+    const uint32_t* g4 = reinterpret_cast<const uint32_t*>(&gf[ks]);
 #pragma unroll
-      for (int e = 0; e < 4; ++e) xx[e] = M::pack2(M::lo(xx[e]) * a.scale, M::hi(xx[e]) * a.scale);
-      qf[ks] = x;
-      gf[ks] = w.ok ? *reinterpret_cast<const uint4*>(grow + 16 * ks + 8 * h) : make_uint4(0, 0, 0, 0);
-    }
+    for (int e = 0; e < 4; ++e) dpart += M::lo(o4[e]) * M::lo(g4[e]) + M::hi(o4[e]) * M::hi(g4[e]);
   }
-  // lse in log2 units (+inf for rows past T: every P is then 0) and delta
-  const float lse_l2 = w.ok ? a.lse[(int64_t)b * a.lse_sb + (int64_t)trow * a.lse_st + (int64_t)hq * a.lse_sh] * kLog2e
-                            : INFINITY;
-  const float dlt = w.ok ? p.delta[((int64_t)b * a.T + trow) * a.HQ + hq] : 0.f;
+  const float drow = xor32_sum(dpart);   // every lane of the pair is active
+  const float dlt = row_ok ? drow : 0.f;
+  T* qsrow = reinterpret_cast<T*>(p.qs) + (((int64_t)b * a.HQ + hq) * a.T + trow) * D;
+#pragma unroll
+  for (int ks = 0; ks < KS; ++ks) {
+    uint32_t* xx = reinterpret_cast<uint32_t*>(&qf[ks]);
+#pragma unroll
+    for (int e = 0; e < 4; ++e) xx[e] = M::pack2(M::lo(xx[e]) * a.scale, M::hi(xx[e]) * a.scale);
+    if (row_ok) *reinterpret_cast<uint4*>(qsrow + 16 * ks + 8 * h) = qf[ks];
+  }
+  if (row_ok && h == 0) p.delta[((int64_t)b * a.T + trow) * a.HQ + hq] = dlt;
 
   f32x16_t dq[MT];
 #pragma unroll
@@ -289,10 +276,13 @@ __global__ __launch_bounds__(128, D == 128 ? 1 : 2) void dq_kernel(BwdK p) {
     __syncthreads();
     if (u + 1 < U) fetch(s_chunks[u + 1]);
 
-    uint64_t keep, rm;
-    float bq[4];
-    int qix[4];
-    const bool fast = __all(chunk_mask(w, j0, p.bs_shift, blk64, keep, rm, bq, qix));
+    // a chunk inside every row's window needs no mask (and no walk of the ids)
+    uint64_t keep = ~0ull, rm = 0ull;
+    float bq[4] = {0.f, 0.f, 0.f, 0.f};
+    int qix[4] = {-1, -1, -1, -1};
+    bool fast = true;
+    if (!(j0 >= w_ls_max && j0 + kChunk <= w_hi_min))
+      fast = __all(chunk_mask(w, j0, p.bs_shift, blk64, keep, rm, bq, qix));
     const float addb = (fast && w.sb && rm != 0ull) ? bq[0] : 0.f;
     float dsum[4] = {0.f, 0.f, 0.f, 0.f};
     uint4 db[4];
@@ -306,14 +296,15 @@ __global__ __launch_bounds__(128, D == 128 ? 1 : 2) void dq_kernel(BwdK p) {
       }
       if (fast) {
         const float sub = addb - lse_l2;
+        float ds0 = 0.f;      // summed only for the bias gradient
 #pragma unroll
         for (int r = 0; r < 16; ++r) {
           const float pv = __builtin_amdgcn_exp2f(fmaf(st[r], kLog2e, sub));
           const float dsv = pv * (dp[r] - dlt);
           st[r] = dsv;
-          dsum[0] += dsv;
+          ds0 += dsv;
         }
-        if (rm == 0ull) dsum[0] = 0.f;
+        if (s_sdb && rm != 0ull) dsum[0] += ds0;
       } else {
         const uint32_t k32 = (uint32_t)((keep >> (4 * h)) >> (32 * half));
         const uint32_t r32 = (uint32_t)((rm >> (4 * h)) >> (32 * half));
@@ -347,7 +338,7 @@ __global__ __launch_bounds__(128, D == 128 ? 1 : 2) void dq_kernel(BwdK p) {
     if (s_sdb) {
 #pragma unroll
       for (int qq = 0; qq < 4; ++qq) {
-        const float tot = dsum[qq] + __shfl_xor(dsum[qq], 32, kWave);
+        const float tot = xor32_sum(dsum[qq]);
         if (h == 0 && w.ok && qix[qq] >= 0) s_sdb[row * SP + qix[qq]] += tot;
       }
     }
@@ -378,7 +369,7 @@ __global__ __launch_bounds__(128, D == 128 ? 1 : 2) void dq_kernel(BwdK p) {
   }
 }
 
-// -------------------------------------------------------------- 4. dK / dV
+// -------------------------------------------------------------- 3. dK / dV
 constexpr int kPreSlots = 8;          // selected ids per row fetched one visit ahead
 
 // One workgroup = (sequence, kv head, 64-key chunk), four waves.  For every
@@ -501,7 +492,7 @@ __global__ __launch_bounds__(256, 2) void dkv_kernel(BwdK p) {
     }
     __syncthreads();
     const int nt = s_ntiles;
-    // the scaled query from the delta pass ([T, D] rows of this head), dO as given
+    // the scaled query written by the dQ kernel ([T, D] rows of this head), dO as given
     const __amdgpu_buffer_rsrc_t qrs = make_rsrc(
         reinterpret_cast<const T*>(p.qs) + ((int64_t)b * a.HQ + hq) * a.T * D, (uint32_t)((int64_t)a.T * D * 2));
     const __amdgpu_buffer_rsrc_t grs = make_rsrc(
@@ -870,9 +861,6 @@ int launch_bwd(const BwdK& k, hipStream_t st) {
       !ensure_dynamic_lds(&dkv_kernel<T, D>, dkv_smem(k), &granted_dkv))
     return SRSWA_UNSUPPORTED;
   const srswa_bwd_args& a = k.a;
-  const int rpw = kWave / (D / 8);
-  const int64_t rows = (int64_t)a.B * a.T * a.HQ;
-  hipLaunchKernelGGL((delta_kernel<T, D>), dim3((unsigned)((rows + 4 * rpw - 1) / (4 * rpw))), dim3(256), 0, st, k);
   const int64_t nw = (int64_t)touch_words(k);
   if (nw > 0) hipLaunchKernelGGL(zero_words_kernel, dim3((unsigned)((nw + 255) / 256)), dim3(256), 0, st, k.touch, nw);
   const int64_t ne = (int64_t)a.B * a.HI * k.ntiles * a.S;     // one wavefront each
