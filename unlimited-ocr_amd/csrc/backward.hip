@@ -381,9 +381,10 @@ constexpr int kPreSlots = 8;          // selected ids per row fetched one visit 
 //     softmax -> P (fp32, published through LDS), dV^T += dO^T P;
 //   role B (waves 2, 3): V of its keys; dP = dO V^T, then dS = P (dP - delta)
 //     from the published P, dK^T += (q*scale)^T dS.
-// Per visit: stage Q / dO | S (A) and dP (B) | barrier | dV (A), dS and dK
-// (B) while wave 3 derives the NEXT visit's row data (keep masks, lse, delta,
-// bias) into the other of two buffers, off the S / softmax path.  A lane
+// Per visit: stage Q / dO | S (A) and dP (B) | the softmax (A) while wave 3
+// (B, which waits for P anyway) derives the NEXT visit's row data (keep masks,
+// lse, delta, bias) into the other of two buffers | barrier | dV (A), dS and
+// dK (B).  A lane
 // holds the same (row, key) elements in both roles (the same MFMA shape), so
 // role B reads role A's P lane for lane.
 template <int D> struct DkvLds {
@@ -700,7 +701,10 @@ __global__ __launch_bounds__(256, 2) void dkv_kernel(BwdK p) {
         else
           softmax(std::false_type{});
       }
-      __syncthreads();   // P published
+      // the next visit's row data (the other buffer), on a role-B wave while
+      // role A runs the softmax that role B waits for
+      if (wave == kMaskWave && it + 1 < nt) row_masks(it + 1);
+      __syncthreads();   // P published; the next visit's row data written
       if (role == 1) {
         // sg <- dS = P (dP - delta) in place
         const float* dlt = s_dlt(buf);
@@ -733,8 +737,6 @@ __global__ __launch_bounds__(256, 2) void dkv_kernel(BwdK p) {
 #pragma unroll
         for (int mt = 0; mt < MT; ++mt) acc[mt] = M::mac(xa[mt], pk[ks], acc[mt]);
       }
-      // the next visit's row data, while the matrix cores finish dK
-      if (wave == kMaskWave && it + 1 < nt) row_masks(it + 1);
     }
   }
 
