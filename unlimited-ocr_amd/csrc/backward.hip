@@ -117,8 +117,13 @@ template <int D> struct DqLds {
 // bias gradient (sum of fp32 dS over the remote keys of a selected block) is
 // summed per (row, sorted block) in LDS in a fixed order and written per slot
 // at the end (0 for repeated ids) -- no atomics.
+// Two waves per SIMD (four workgroups per CU, LDS permitting).  At D = 128
+// that fits the register file only without a staging prefetch: a chunk's K / V
+// are loaded at the top of its own iteration, and the co-resident workgroups'
+// waves cover the load latency (a one-chunk register prefetch needs 324
+// registers, one wave per SIMD, and is slower).  At D = 64 the prefetch fits.
 template <typename T, int D>
-__global__ __launch_bounds__(128, D == 128 ? 1 : 2) void dq_kernel(BwdK p) {
+__global__ __launch_bounds__(128, 2) void dq_kernel(BwdK p) {
   using M = Mfma<T>;
   using L = DqLds<D>;
   constexpr int KP = L::KP, VP = L::VP;
@@ -264,9 +269,11 @@ __global__ __launch_bounds__(128, D == 128 ? 1 : 2) void dq_kernel(BwdK p) {
   };
   const uint16_t* k16 = reinterpret_cast<const uint16_t*>(sK);
 
-  if (U > 0) fetch(s_chunks[0]);
+  constexpr bool kPrefetch = D < 128;
+  if (kPrefetch && U > 0) fetch(s_chunks[0]);
   for (int u = 0; u < U; ++u) {
     const int j0 = (int)s_chunks[u] * kChunk;
+    if (!kPrefetch) fetch(s_chunks[u]);   // in flight across the barrier
     __syncthreads();   // previous chunk fully consumed
 #pragma unroll
     for (int i = 0; i < PPT; ++i) {
@@ -274,7 +281,7 @@ __global__ __launch_bounds__(128, D == 128 ? 1 : 2) void dq_kernel(BwdK p) {
       *reinterpret_cast<uint4*>(sVw + i * RPP * VP) = vpre[i];
     }
     __syncthreads();
-    if (u + 1 < U) fetch(s_chunks[u + 1]);
+    if (kPrefetch && u + 1 < U) fetch(s_chunks[u + 1]);
 
     // a chunk inside every row's window needs no mask (and no walk of the ids)
     uint64_t keep = ~0ull, rm = 0ull;
