@@ -167,6 +167,17 @@ typedef struct {
 
 int srswa_gather_fwd(const srswa_fwd_args* a, void* stream);
 
+/* srswa_gather_fwd with a workspace for the tail split: when the launch's last
+ * round of 64-row tiles would fill at most a fifth of the GPU, those tiles
+ * run as four workgroups each over quarters of their key chunks, and a merge
+ * kernel combines the parts (same masks, rounding points and outputs).  Bytes needed
+ * from srswa_gather_fwd_workspace (0: no split for this shape); ws NULL or
+ * short runs every tile whole.  The same reference kernels as
+ * srswa_gather_fwd (HF/sparse_gather_triton.py:35-122,
+ * HF/sparse_gather_e2e_triton.py:36-121); the split has no counterpart there. */
+size_t srswa_gather_fwd_workspace(const srswa_fwd_args* a);
+int srswa_gather_fwd_ws(const srswa_fwd_args* a, void* ws, size_t ws_bytes, void* stream);
+
 /* ------------------------------------------------------------------------
  * Paged block-sparse prefill of the serving backend.  Replaces
  * _dash_sparse_fwd_kernel / dash_sparse_attn (K10,

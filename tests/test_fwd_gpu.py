@@ -74,3 +74,44 @@ def test_fwd_matches_oracle(dev, name):
     o, lse, ro, rl = _run(dev, q, k, v, bi, pos, bias, bs, lw, scale)
     assert_close_lowp(o, ro, c.get("dtype", torch.bfloat16), TOL, f"forward {name}: o")
     assert (lse - rl).abs().max().item() <= TOL
+
+
+@pytest.mark.parametrize("name", ["self_bs64", "bias", "gqa_hi"])
+def test_tail_split_matches_whole_tiles(dev, name):
+    """The tail split (a last round of tiles filling at most a fifth of the GPU
+    runs as four workgroups per tile over quarters of their key chunks, then a
+    merge) against every tile whole and the oracle: these small launches are
+    one such round, so the split takes every tile."""
+    import ctypes
+    from srswa import _lib
+    c = dict(CASES[name])
+    bs, lw = c["bs"], c["lw"]
+    q, k, v, bi, pos, bias = _case(40 + list(CASES).index(name), **c)
+    scale = 1 / math.sqrt(c["D"])
+    B, T, HQ, D = q.shape
+    Sk = k.shape[1]
+    seg = ops._seg_from_positions(pos.to(dev), T, Sk, dev)
+    args = dict(block_size=bs, local_window=lw, scale=scale, seg=seg, bias=None if bias is None else bias.to(dev))
+    qd, kd, vd, bd = q.to(dev), k.to(dev), v.to(dev), bi.to(dev)
+    o_s, l_s = ops.gather_fwd(qd, kd, vd, bd, **args)
+    o_w, l_w = ops.gather_fwd(qd, kd, vd, bd, tail_split=False, **args)
+    dense = None
+    if bias is not None:
+        dense = O.bias_slots_to_dense(bias.double(), bi[:, 0], -(-Sk // bs))
+    ro, rl = O.gather_attention(q.double().transpose(1, 2), k.double().transpose(1, 2),
+                                v.double().transpose(1, 2), bi, pos, bs, scale, lw, blk_bias_dense=dense)
+    ro, rl = ro.transpose(1, 2), rl.transpose(1, 2)
+    for o, l, what in ((o_s, l_s, "split"), (o_w, l_w, "whole")):
+        assert_close_lowp(o.cpu().double(), ro, c.get("dtype", torch.bfloat16), TOL, f"forward {name} {what}: o")
+        assert (l.cpu().double() - rl).abs().max().item() <= TOL
+    # the split must have happened: one partial round of tiles
+    a = _lib.FwdArgs()
+    a.B, a.T, a.Sk, a.HQ, a.HKV, a.HI, a.D, a.S = B, T, Sk, HQ, k.shape[2], bi.shape[1], D, bi.shape[-1]
+    a.q = a.k = a.v = a.out = qd.data_ptr()
+    a.idx = bd.data_ptr()
+    a.block_size, a.local_window, a.scale = bs, lw, scale
+    a.dtype = _lib.dtype_code(q.dtype)
+    ntiles = B * HQ * (-(-T // 64))
+    cus = torch.cuda.get_device_properties(dev).multi_processor_count
+    nws = _lib.lib().srswa_gather_fwd_workspace(ctypes.byref(a))
+    assert (nws > 0) == (ntiles * 5 <= 4 * cus), (nws, ntiles, cus)

@@ -339,4 +339,26 @@ inline bool ensure_dynamic_lds(F* kernel, size_t bytes, LdsGrant* g) {
   return true;
 }
 
+// Compute units of the current device (0 when the runtime cannot say),
+// remembered per device.
+inline int device_cu_count() {
+  static std::atomic<int> cached[kMaxDevices];   // zero-initialised in static storage
+  int dev = -1;
+  if (hipGetDevice(&dev) != hipSuccess) {
+    (void)hipGetLastError();
+    return 0;
+  }
+  if (dev >= 0 && dev < kMaxDevices) {
+    const int c = cached[dev].load(std::memory_order_relaxed);
+    if (c > 0) return c;
+  }
+  int n = 0;
+  if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess) {
+    (void)hipGetLastError();
+    return 0;
+  }
+  if (dev >= 0 && dev < kMaxDevices) cached[dev].store(n, std::memory_order_relaxed);
+  return n;
+}
+
 }  // namespace srswa

@@ -63,6 +63,12 @@ struct FwdK {
   const int32_t* bt;
   int64_t bt_sr, k_pst, v_pst;
   int kv8;                     // FP8: the caches' fp8 format (srswa_dtype)
+  // tail split: the last ntail logical tiles run as nsplit workgroups each, part
+  // p taking chunks [U p / nsplit, U (p + 1) / nsplit) of the tile's plan and
+  // writing an unnormalised record (O fp32 [64][D], then m, l per row) that
+  // fwd_merge_kernel combines.  The whole tiles come first in dispatch order.
+  int nsplit, ntail, per_xcd_p;
+  float* part;                 // [ntail * nsplit][64 * D + 128]
 };
 
 template <int D> struct FwdLds {
@@ -91,8 +97,18 @@ __global__ __launch_bounds__(128, 2) void fwd_kernel(FwdK p) {
   // The hardware deals workgroups to the 8 XCDs round-robin; logical tile
   // xcd * per_xcd + k keeps neighbouring tiles of one (sequence, head), which
   // share most of their window keys, on the same L2.
-  const int lid = (int)(blockIdx.x & 7) * p.per_xcd + (int)(blockIdx.x >> 3);
-  if (lid >= p.nlogical) return;
+  const int nwhole = p.nlogical - p.ntail;
+  int lid, part = 0, rec = -1;
+  if ((int)blockIdx.x < 8 * p.per_xcd) {
+    lid = (int)(blockIdx.x & 7) * p.per_xcd + (int)(blockIdx.x >> 3);
+    if (lid >= nwhole) return;
+  } else {
+    const int pid = (int)blockIdx.x - 8 * p.per_xcd;
+    rec = (pid & 7) * p.per_xcd_p + (pid >> 3);
+    if (rec >= p.ntail * p.nsplit) return;
+    lid = nwhole + rec / p.nsplit;
+    part = rec % p.nsplit;
+  }
 
   T* sK = reinterpret_cast<T*>(smem + L::kOff);
   T* sV = reinterpret_cast<T*>(smem + L::vOff);
@@ -282,8 +298,11 @@ __global__ __launch_bounds__(128, 2) void fwd_kernel(FwdK p) {
   };
   const uint16_t* v16 = reinterpret_cast<const uint16_t*>(sV);
 
-  if (U > 0) fetch(0);
-  for (int u = 0; u < U; ++u) {
+  // this workgroup's share of the plan (all of it unless the tile is split)
+  const int nsp = rec >= 0 ? p.nsplit : 1;
+  const int u_lo = (int)((int64_t)U * part / nsp), u_hi = (int)((int64_t)U * (part + 1) / nsp);
+  if (u_lo < u_hi) fetch(u_lo);
+  for (int u = u_lo; u < u_hi; ++u) {
     const int j0 = (int)s_chunks[u] * kChunk;
     __syncthreads();   // previous chunk fully consumed
     if constexpr (FP8) {
@@ -302,7 +321,7 @@ __global__ __launch_bounds__(128, 2) void fwd_kernel(FwdK p) {
       }
     }
     __syncthreads();
-    if (u + 1 < U) fetch(u + 1);
+    if (u + 1 < u_hi) fetch(u + 1);
 
     // S^T (keys x rows) for the two 32-key halves of the chunk
     f32x16_t st[2] = {zero16(), zero16()};
@@ -439,6 +458,18 @@ __global__ __launch_bounds__(128, 2) void fwd_kernel(FwdK p) {
   }
 
   const float l_tot = xor32_sum(l_run);
+  if (rec >= 0) {
+    // a part of a split tile: the unnormalised record, merged by fwd_merge_kernel
+    float* pr = p.part + (int64_t)rec * (64 * D + 128);
+#pragma unroll
+    for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+      for (int g = 0; g < 4; ++g)
+        *reinterpret_cast<float4*>(pr + row * D + 32 * mt + 8 * g + 4 * h) =
+            make_float4(o[mt][4 * g], o[mt][4 * g + 1], o[mt][4 * g + 2], o[mt][4 * g + 3]);
+    if (h == 0) *reinterpret_cast<float2*>(pr + 64 * D + 2 * row) = make_float2(m_b, l_tot);
+    return;
+  }
   if (!row_ok) return;
   const float inv = l_tot > 0.f ? 1.f / l_tot : 0.f;
   T* orow = reinterpret_cast<T*>(a.out) + (int64_t)b * a.o_sb + (int64_t)(q0 + t0 + row) * a.o_st +
@@ -456,6 +487,69 @@ __global__ __launch_bounds__(128, 2) void fwd_kernel(FwdK p) {
   if (!PAGED && a.lse && h == 0)
     a.lse[(int64_t)b * a.lse_sb + (int64_t)(t0 + row) * a.lse_st + (int64_t)hq * a.lse_sh] =
         l_tot > 0.f ? (m_b + log2f(l_tot)) * kLn2 : -INFINITY;
+}
+
+// Combines the nsplit (<= 4) part records of each split tile: m = max m_p,
+// O = sum 2^(m_p - m) O_p, l = sum 2^(m_p - m) l_p, out = O / l in the input
+// dtype, lse = (m + log2 l) ln 2.  A row with no keys in any part (l = 0)
+// writes zeros and lse = -inf, as the unsplit kernel does.  Four workgroups
+// per tile (16 rows each), 16 threads per row, every part's loads issued
+// before the combine.
+template <typename T, int D>
+__global__ __launch_bounds__(256) void fwd_merge_kernel(FwdK p) {
+  using M = Mfma<T>;
+  constexpr int TPR = 16, DPT = D / TPR;         // threads per row, dims per thread (8 or 4)
+  constexpr int REC = 64 * D + 128;              // floats per part record
+  const srswa_fwd_args& a = p.a;
+  const int ti = (int)blockIdx.x >> 2;
+  const int lid = p.nlogical - p.ntail + ti;
+  const int tile = lid % p.ntiles, bh = lid / p.ntiles;
+  const int hq = bh % a.HQ, b = bh / a.HQ;
+  const int t0 = tile * kTileRows;
+  const int nrows = min(kTileRows, a.T - t0);
+  const int r = 16 * ((int)blockIdx.x & 3) + (int)threadIdx.x / TPR, c = (int)threadIdx.x % TPR;
+  if (r >= nrows) return;
+  const float* rec = p.part + (int64_t)ti * p.nsplit * REC;
+  float2 ml[4];
+  float4 ov[4][DPT / 4];
+#pragma unroll
+  for (int q = 0; q < 4; ++q) {
+    const bool live = q < p.nsplit;
+    const float* pq = rec + (int64_t)(live ? q : 0) * REC;
+    ml[q] = live ? *reinterpret_cast<const float2*>(pq + 64 * D + 2 * r) : make_float2(-INFINITY, 0.f);
+#pragma unroll
+    for (int d = 0; d < DPT / 4; ++d)
+      ov[q][d] = live ? reinterpret_cast<const float4*>(pq + r * D + c * DPT)[d] : make_float4(0.f, 0.f, 0.f, 0.f);
+  }
+  const float mx = fmaxf(fmaxf(ml[0].x, ml[1].x), fmaxf(ml[2].x, ml[3].x));
+  float l = 0.f, acc[DPT];
+#pragma unroll
+  for (int d = 0; d < DPT; ++d) acc[d] = 0.f;
+#pragma unroll
+  for (int q = 0; q < 4; ++q) {
+    const float w = ml[q].x == -INFINITY ? 0.f : exp2f(ml[q].x - mx);
+    l += ml[q].y * w;
+#pragma unroll
+    for (int d = 0; d < DPT / 4; ++d) {
+      acc[4 * d] += w * ov[q][d].x;
+      acc[4 * d + 1] += w * ov[q][d].y;
+      acc[4 * d + 2] += w * ov[q][d].z;
+      acc[4 * d + 3] += w * ov[q][d].w;
+    }
+  }
+  const float inv = l > 0.f ? 1.f / l : 0.f;
+  T* orow = reinterpret_cast<T*>(a.out) + (int64_t)b * a.o_sb + (int64_t)(t0 + r) * a.o_st + (int64_t)hq * a.o_sh +
+            c * DPT;
+  if constexpr (DPT == 8) {
+    *reinterpret_cast<uint4*>(orow) =
+        make_uint4(M::pack2(acc[0] * inv, acc[1] * inv), M::pack2(acc[2] * inv, acc[3] * inv),
+                   M::pack2(acc[4] * inv, acc[5] * inv), M::pack2(acc[6] * inv, acc[7] * inv));
+  } else {
+    *reinterpret_cast<uint2*>(orow) = make_uint2(M::pack2(acc[0] * inv, acc[1] * inv), M::pack2(acc[2] * inv, acc[3] * inv));
+  }
+  if (c == 0 && a.lse)
+    a.lse[(int64_t)b * a.lse_sb + (int64_t)(t0 + r) * a.lse_st + (int64_t)hq * a.lse_sh] =
+        l > 0.f ? (mx + log2f(l)) * kLn2 : -INFINITY;
 }
 
 bool al16(const void* p) { return ((uintptr_t)p & 15u) == 0; }
@@ -514,7 +608,10 @@ template <typename T, int D, bool PAGED, bool FP8 = false>
 int launch_fwd(const FwdK& k, size_t smem, hipStream_t st) {
   static LdsGrant granted;
   if (!ensure_dynamic_lds(&fwd_kernel<T, D, PAGED, FP8>, smem, &granted)) return SRSWA_UNSUPPORTED;
-  hipLaunchKernelGGL((fwd_kernel<T, D, PAGED, FP8>), dim3((unsigned)(8 * k.per_xcd)), dim3(128), smem, st, k);
+  hipLaunchKernelGGL((fwd_kernel<T, D, PAGED, FP8>), dim3((unsigned)(8 * k.per_xcd + 8 * k.per_xcd_p)), dim3(128),
+                     smem, st, k);
+  if constexpr (!PAGED)
+    if (k.ntail > 0) hipLaunchKernelGGL((fwd_merge_kernel<T, D>), dim3((unsigned)(4 * k.ntail)), dim3(256), 0, st, k);
   const hipError_t e = hipGetLastError();
   if (e != hipSuccess) {
     set_error("fwd launch failed: %s", hipGetErrorString(e));
@@ -528,11 +625,13 @@ int launch_fwd(const FwdK& k, size_t smem, hipStream_t st) {
 
 using namespace srswa;
 
-extern "C" int srswa_gather_fwd(const srswa_fwd_args* a, void* stream) {
-  int st = check_fwd(a);
-  if (st != SRSWA_OK) return st;
-  if (a->B == 0 || a->T == 0) return SRSWA_OK;
-  FwdK k{};
+namespace srswa {
+namespace {
+
+// The forward's launch plan (no device work).  Returns SRSWA_OK with k, smem
+// and the split's workspace bytes filled in.
+int plan_fwd(const srswa_fwd_args* a, FwdK& k, size_t& smem, size_t& ws_bytes) {
+  k = FwdK{};
   k.a = *a;
   k.ntiles = ceil_div(a->T, kTileRows);
   const int nchunk = ceil_div(a->Sk, kChunk);
@@ -547,7 +646,6 @@ extern "C" int srswa_gather_fwd(const srswa_fwd_args* a, void* stream) {
     return SRSWA_UNSUPPORTED;
   }
   k.nlogical = (int)nlogical;
-  k.per_xcd = ceil_div(k.nlogical, 8);
   // distinct chunks one tile can visit: the selected blocks of 64 rows plus
   // the window span of 64 consecutive rows
   const int64_t per_tile = (int64_t)kTileRows * a->S * (ceil_div(a->block_size, kChunk) + 1) +
@@ -560,15 +658,76 @@ extern "C" int srswa_gather_fwd(const srswa_fwd_args* a, void* stream) {
   n += ((size_t)umax * 2 + 15) / 16 * 16;
   k.sid_off = (int)n;
   n += (size_t)64 * k.SP * 4 * (a->bias ? 2 : 1);
-  const size_t smem = (n + 15) / 16 * 16;
+  smem = (n + 15) / 16 * 16;
   if (smem > 156 * 1024) {
     set_error("fwd: %zu bytes of LDS needed (key length too large)", smem);
     return SRSWA_UNSUPPORTED;
   }
+  // Tail split.  The GPU holds `slots` workgroups at once (four per CU at two
+  // waves per SIMD, fewer when LDS runs out).  When the last round of tiles
+  // fills at most a fifth of them, its tiles run as four workgroups each over
+  // quarters of their chunk plans, so that round takes about a quarter of a
+  // tile's time.  A fuller last round is left whole: each part pays the
+  // tile's set-up and first-load latency again, and its fp32 record costs
+  // 8x the tile's output bytes, which outweighs the shorter round.  Measured
+  // (4 x 10 heads, 65536 keys, D 128): 80 tiles 39.5 -> 27.6 us, 200 tiles
+  // 40.9 -> 38.6 us, 1,040 tiles 110 -> 92 us split; 1,280 tiles on 1,024
+  // slots 129 us whole against 134 us split.
+  k.nsplit = 1;
+  k.ntail = 0;
+  ws_bytes = 0;
+  const int cus = device_cu_count();
+  const int per_cu = std::min<int>(4, (int)((160 * 1024) / smem));
+  if (cus > 0 && per_cu > 0) {
+    const int64_t slots = (int64_t)cus * per_cu;
+    const int64_t rounds = (nlogical + slots - 1) / slots;
+    const int64_t tail = nlogical - (rounds - 1) * slots;
+    const int64_t f = 4;
+    if (tail * 5 <= slots) {
+      k.nsplit = (int)f;
+      k.ntail = (int)tail;
+      ws_bytes = (size_t)tail * f * (64 * a->D + 128) * sizeof(float);
+    }
+  }
+  k.per_xcd = ceil_div(k.nlogical - k.ntail, 8);
+  k.per_xcd_p = ceil_div(k.ntail * k.nsplit, 8);
+  return SRSWA_OK;
+}
+
+}  // namespace
+}  // namespace srswa
+
+extern "C" size_t srswa_gather_fwd_workspace(const srswa_fwd_args* a) {
+  if (check_fwd(a) != SRSWA_OK || a->B == 0 || a->T == 0) return 0;
+  FwdK k;
+  size_t smem = 0, ws = 0;
+  return plan_fwd(a, k, smem, ws) == SRSWA_OK ? ws : 0;
+}
+
+extern "C" int srswa_gather_fwd_ws(const srswa_fwd_args* a, void* ws, size_t ws_bytes, void* stream) {
+  int st = check_fwd(a);
+  if (st != SRSWA_OK) return st;
+  if (a->B == 0 || a->T == 0) return SRSWA_OK;
+  FwdK k;
+  size_t smem = 0, need = 0;
+  st = plan_fwd(a, k, smem, need);
+  if (st != SRSWA_OK) return st;
+  if (k.ntail > 0 && (!ws || ws_bytes < need || ((uintptr_t)ws & 15u))) {
+    // no (usable) workspace: every tile runs whole
+    k.nsplit = 1;
+    k.ntail = 0;
+    k.per_xcd = ceil_div(k.nlogical, 8);
+    k.per_xcd_p = 0;
+  }
+  k.part = reinterpret_cast<float*>(ws);
   hipStream_t s = reinterpret_cast<hipStream_t>(stream);
   if (a->dtype == SRSWA_BF16)
     return a->D == 128 ? launch_fwd<bf16_t, 128, false>(k, smem, s) : launch_fwd<bf16_t, 64, false>(k, smem, s);
   return a->D == 128 ? launch_fwd<__half, 128, false>(k, smem, s) : launch_fwd<__half, 64, false>(k, smem, s);
+}
+
+extern "C" int srswa_gather_fwd(const srswa_fwd_args* a, void* stream) {
+  return srswa_gather_fwd_ws(a, nullptr, 0, stream);
 }
 
 extern "C" int srswa_gather_fwd_paged(const srswa_paged_fwd_args* a, void* stream) {
@@ -666,6 +825,7 @@ extern "C" int srswa_gather_fwd_paged(const srswa_paged_fwd_args* a, void* strea
   }
   k.nlogical = (int)nlogical;
   k.per_xcd = ceil_div(k.nlogical, 8);
+  k.nsplit = 1;                    // no tail split: the live tiles depend on device-side lengths
   const int64_t per_tile = (int64_t)kTileRows * a->S * (ceil_div(a->page_size, kChunk) + 1) +
                            ceil_div(f.local_window + kTileRows - 1, kChunk) + 1;
   const int umax = (int)std::min<int64_t>(nchunk, per_tile);

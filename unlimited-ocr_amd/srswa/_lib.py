@@ -450,6 +450,8 @@ SIGNATURES = {
     "srswa_topk_rows": (ctypes.c_int, [_vp, _i64, _i32, _i64, _i32, _i32, ctypes.c_float, _vp, _vp,
                                        _i64, _vp]),
     "srswa_gather_fwd": (ctypes.c_int, [ctypes.POINTER(FwdArgs), _vp]),
+    "srswa_gather_fwd_workspace": (ctypes.c_size_t, [ctypes.POINTER(FwdArgs)]),
+    "srswa_gather_fwd_ws": (ctypes.c_int, [ctypes.POINTER(FwdArgs), _vp, ctypes.c_size_t, _vp]),
     "srswa_gather_fwd_paged": (ctypes.c_int, [ctypes.POINTER(PagedFwdArgs), _vp]),
     "srswa_gather_bwd_workspace": (ctypes.c_size_t, [ctypes.POINTER(BwdArgs)]),
     "srswa_gather_bwd": (ctypes.c_int, [ctypes.POINTER(BwdArgs), _vp, ctypes.c_size_t, _vp]),

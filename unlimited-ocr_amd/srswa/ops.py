@@ -616,12 +616,13 @@ def _seg_from_positions(position_ids, T, Sk, device):
 
 
 def gather_fwd(q, k, v, block_indices, *, block_size, local_window, scale, seg=None, bias=None,
-               out=None, need_lse=True):
+               out=None, need_lse=True, tail_split=True):
     """Fused gather attention forward.
 
     q [B, T, HQ, D]; k, v [B, Sk, HKV, D] (Sk >= T, queries are the last T
     keys); block_indices [B, HI, T, S] (-1 pad); seg [B, T] int sample starts
     (None = 0); bias [B, T, S] or [B, HI, T, S] per-slot bias on remote keys.
+    tail_split=False runs every tile as one workgroup (no workspace).
     Returns (o [B, T, HQ, D], lse [B, T, HQ] fp32 or None)."""
     _require_cuda(q, k, v, block_indices, seg, bias)
     B, T, HQ, D = q.shape
@@ -662,7 +663,11 @@ def gather_fwd(q, k, v, block_indices, *, block_size, local_window, scale, seg=N
     a.block_size, a.local_window = int(block_size), max(1, int(local_window))
     a.scale = float(scale)
     a.dtype = _lib.dtype_code(q.dtype)
-    _lib.check(_lib.lib().srswa_gather_fwd(ctypes.byref(a), _lib.stream_ptr(q.device)), "srswa_gather_fwd")
+    # the tail split's workspace (0 bytes when the launch's last round is full)
+    nws = _lib.lib().srswa_gather_fwd_workspace(ctypes.byref(a)) if tail_split else 0
+    ws = _lib.scratch(q.device, nws)
+    _lib.check(_lib.lib().srswa_gather_fwd_ws(ctypes.byref(a), _lib.ptr(ws), nws, _lib.stream_ptr(q.device)),
+               "srswa_gather_fwd_ws")
     return out, lse
 
 
