@@ -265,6 +265,7 @@ template <int NPL>
 __global__ __launch_bounds__(kRsWaves * kWave) void route_entmax_regs_kernel(srswa_route_serve_args a) {
   static_assert(NPL % 4 == 0 && NPL <= 32, "NPL: a multiple of 4, at most 32");
   __shared__ uint32_t s_key[kRsWaves][kWave];
+  __shared__ float s_live[kRsWaves][4 * kWave];
   const int wave = threadIdx.x / kWave, lane = threadIdx.x % kWave;
   const int64_t row = (int64_t)blockIdx.x * kRsWaves + wave;
   if (row >= a.rows) return;
@@ -303,19 +304,60 @@ __global__ __launch_bounds__(kRsWaves * kWave) void route_entmax_regs_kernel(srs
   for (int i = 0; i < NPL; ++i) x[i] = ((cand >> i) & 1u) ? (x[i] - xm) * 0.5f : -INFINITY;
   float* z = x;
 
-  // tau: the reference's 24 bisection steps; z <= -1 never counts
+  // tau: the reference's 24 bisection steps.  Every midpoint lies in (-1, 0),
+  // so a z <= -1 adds exactly 0 to every step's sum: the live values (z > -1,
+  // usually the few near the row's max) are compacted through LDS into
+  // NC <= 4 per lane first, and the steps loop over those alone (the whole row
+  // when more than 256 are live).
+  uint32_t live = 0;
+#pragma unroll
+  for (int i = 0; i < NPL; ++i) live |= z[i] > -1.f ? 1u << i : 0u;
+  const int n_live = wave_sum_int(__popc(live));
   float lo = -1.f, hi = 0.f;
-  for (int it = 0; it < kTauIters; ++it) {
-    const float mid = (lo + hi) * 0.5f;
-    double acc[4] = {0.0, 0.0, 0.0, 0.0};
+  if (n_live <= 4 * kWave) {
+    int base = 0;
 #pragma unroll
     for (int i = 0; i < NPL; ++i) {
-      const float p = fmaxf(z[i] - mid, 0.f);
-      acc[i & 3] += (double)(p * p);
+      const bool lv = (live >> i) & 1u;
+      const unsigned long long bal = __ballot(lv);
+      if (lv) s_live[wave][base + __popcll(bal & lt)] = z[i];
+      base += __popcll(bal);
     }
-    const float ssum = (float)wave_sum_f64((acc[0] + acc[1]) + (acc[2] + acc[3]));
-    if (ssum > 1.f) lo = mid;
-    else hi = mid;
+    wave_sync_lds();
+    auto bisect = [&](auto nc_tag) __attribute__((always_inline)) {
+      constexpr int NC = decltype(nc_tag)::value;
+      float zc[NC];
+#pragma unroll
+      for (int k = 0; k < NC; ++k) zc[k] = lane + kWave * k < n_live ? s_live[wave][lane + kWave * k] : -INFINITY;
+      for (int it = 0; it < kTauIters; ++it) {
+        const float mid = (lo + hi) * 0.5f;
+        double acc = 0.0;
+#pragma unroll
+        for (int k = 0; k < NC; ++k) {
+          const float p = fmaxf(zc[k] - mid, 0.f);
+          acc += (double)(p * p);
+        }
+        const float ssum = (float)wave_sum_f64(acc);
+        if (ssum > 1.f) lo = mid;
+        else hi = mid;
+      }
+    };
+    if (n_live <= kWave) bisect(std::integral_constant<int, 1>{});
+    else if (n_live <= 2 * kWave) bisect(std::integral_constant<int, 2>{});
+    else bisect(std::integral_constant<int, 4>{});
+  } else {
+    for (int it = 0; it < kTauIters; ++it) {
+      const float mid = (lo + hi) * 0.5f;
+      double acc[4] = {0.0, 0.0, 0.0, 0.0};
+#pragma unroll
+      for (int i = 0; i < NPL; ++i) {
+        const float p = fmaxf(z[i] - mid, 0.f);
+        acc[i & 3] += (double)(p * p);
+      }
+      const float ssum = (float)wave_sum_f64((acc[0] + acc[1]) + (acc[2] + acc[3]));
+      if (ssum > 1.f) lo = mid;
+      else hi = mid;
+    }
   }
   const float tau = (lo + hi) * 0.5f;
 
