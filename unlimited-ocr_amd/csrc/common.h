@@ -258,9 +258,43 @@ __device__ __forceinline__ uint64_t wave_max_u64(uint64_t v) {
 // Bitonic sort of one unsigned value per lane, descending over the wave (lane 0
 // the largest): stage (K, J) compares lanes J apart; blocks with bit K of the
 // lane clear end descending, the others ascending, and K = 64 makes one run.
+// Lane (l ^ J)'s value for J in {1, 2, 4, 8, 16, 32}, on the VALU: DPP
+// quad_perm [1,0,3,2] / [2,3,0,1]; xor 4 as row_half_mirror of the quad
+// reversal [3,2,1,0] (lane i of an 8-lane half reads 7 - i after the quad
+// flip, which is i ^ 4); xor 8 as row_ror:8 (a 16-lane row rotated by half);
+// xor 16 / 32 by v_permlane16_swap / v_permlane32_swap, which exchange the odd
+// rows of the first operand with the even rows of the second (16 / 32-lane
+// rows): with both operands v, a lane whose row bit is clear finds the partner
+// in the second result, the others in the first.
+template <int J>
+__device__ __forceinline__ uint32_t xor_lane_u32(uint32_t v, int lane) {
+  if constexpr (J == 1) return dpp::mov<dpp::kXor1>(v, v);
+  else if constexpr (J == 2) return dpp::mov<dpp::kXor2>(v, v);
+  else if constexpr (J == 4) return dpp::mov<dpp::kHalfMirror>(v, dpp::mov<0x1b>(v, v));
+  else if constexpr (J == 8) return dpp::mov<0x128>(v, v);
+  else if constexpr (J == 16) {
+    const auto r = __builtin_amdgcn_permlane16_swap(v, v, false, false);
+    return (lane & 16) ? r[0] : r[1];
+  } else {
+    static_assert(J == 32, "J: a power of two below 64");
+    const auto r = __builtin_amdgcn_permlane32_swap(v, v, false, false);
+    return (lane & 32) ? r[0] : r[1];
+  }
+}
+template <int J, typename U>
+__device__ __forceinline__ U xor_lane(U v, int lane) {
+  if constexpr (sizeof(U) == 8) {
+    const uint64_t b = __builtin_bit_cast(uint64_t, v);
+    const uint32_t lo = xor_lane_u32<J>((uint32_t)b, lane), hi = xor_lane_u32<J>((uint32_t)(b >> 32), lane);
+    return __builtin_bit_cast(U, ((uint64_t)hi << 32) | lo);
+  } else {
+    return __builtin_bit_cast(U, xor_lane_u32<J>(__builtin_bit_cast(uint32_t, v), lane));
+  }
+}
+
 template <typename U, int K, int J>
 __device__ __forceinline__ U bitonic_merge(U v, int lane) {
-  const U w = __shfl_xor(v, J, kWave);
+  const U w = xor_lane<J>(v, lane);
   const bool take_max = ((lane & J) == 0) == ((lane & K) == 0);
   v = take_max ? (w > v ? w : v) : (w > v ? v : w);
   if constexpr (J > 1) return bitonic_merge<U, K, J / 2>(v, lane);
