@@ -345,9 +345,11 @@ __global__ __launch_bounds__(128, 2) void fwd_kernel(FwdK p) {
     // them: a dropped key becomes -inf, a kept remote key's bias is added as
     // bias / l2s (l2s > 0), so one softmax form below serves both.
     float addb = 0.f;
+    uint64_t keep = ~0ull, rm = 0ull;
+    float bq[4] = {0.f, 0.f, 0.f, 0.f};
+    int masked = 0;
     if (!(j0 >= w_ls_max && j0 + kChunk <= w_hi_min)) {
       uint32_t qmem = 0;
-      float bq[4] = {0.f, 0.f, 0.f, 0.f};
       if (BS >= kChunk) {
         const int blk = j0 >> p.bs_shift;
         while (nid < blk) nid = my_sid[++cur];
@@ -371,26 +373,34 @@ __global__ __launch_bounds__(128, 2) void fwd_kernel(FwdK p) {
       for (int qq = 0; qq < 4; ++qq)
         if (qmem & (1u << qq)) qm |= 0xffffull << (16 * qq);
       const uint64_t wm = range64(min(max(my_ls - j0, 0), 64), min(max(my_hi - j0, 0), 64));
-      const uint64_t rm = range64(min(max(my_seg - j0, 0), 64), min(max(rem_hi - j0, 0), 64)) & qm;
-      const uint64_t keep = wm | rm;
+      rm = range64(min(max(my_seg - j0, 0), 64), min(max(rem_hi - j0, 0), 64)) & qm;
+      keep = wm | rm;
       const bool whole = !row_ok || (keep == ~0ull && (!my_sb || rm == 0ull || (rm == ~0ull && BS >= kChunk)));
       if (__all(whole)) {
         if (my_sb && rm != 0ull) addb = bq[0];
       } else {
-        const uint64_t kh = keep >> (4 * h), rh = rm >> (4 * h);
-        float bs[4];
+        masked = 1;
+      }
+    }
+    // The mask is applied under an opaque per-lane flag, so the compiler
+    // predicates the update in place instead of branching around it (a
+    // uniform branch made it keep the raw logits in a second register set and
+    // copy all 32 back at the join, on every unmasked chunk).
+    asm volatile("" : "+v"(masked));
+    if (masked) {
+      const uint64_t kh = keep >> (4 * h), rh = rm >> (4 * h);
+      float bs[4];
 #pragma unroll
-        for (int qq = 0; qq < 4; ++qq) bs[qq] = bq[qq] * inv_l2s;
+      for (int qq = 0; qq < 4; ++qq) bs[qq] = bq[qq] * inv_l2s;
 #pragma unroll
-        for (int half = 0; half < 2; ++half) {
-          const uint32_t k32 = (uint32_t)(kh >> (32 * half)), r32 = (uint32_t)(rh >> (32 * half));
+      for (int half = 0; half < 2; ++half) {
+        const uint32_t k32 = (uint32_t)(kh >> (32 * half)), r32 = (uint32_t)(rh >> (32 * half));
 #pragma unroll
-          for (int r = 0; r < 16; ++r) {
-            const int bit = 8 * (r >> 2) + (r & 3);
-            float x = st[half][r];
-            if (my_sb) x += ((r32 >> bit) & 1u) ? bs[2 * half + (r >> 3)] : 0.f;
-            st[half][r] = ((k32 >> bit) & 1u) ? x : -INFINITY;
-          }
+        for (int r = 0; r < 16; ++r) {
+          const int bit = 8 * (r >> 2) + (r & 3);
+          float x = st[half][r];
+          if (my_sb) x += ((r32 >> bit) & 1u) ? bs[2 * half + (r >> 3)] : 0.f;
+          st[half][r] = ((k32 >> bit) & 1u) ? x : -INFINITY;
         }
       }
     }
