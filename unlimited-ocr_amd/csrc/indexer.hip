@@ -23,6 +23,8 @@
 // equal scores rank the LOWER id first); K rounds of "largest key below the
 // previous winner" (per-lane scan + 64-lane max) give the K best in
 // descending order, exactly and deterministically; invalid rows pad with -1.
+// Rows up to 2048 wide take topk_rows_regs_kernel: the same rounds over keys
+// held in registers.
 #include "summary.h"
 
 namespace srswa {
@@ -125,34 +127,9 @@ struct TopkK {
   float* out_val;
 };
 
-// one wavefront per row; 4 rows per workgroup
-__global__ __launch_bounds__(256) void topk_rows_kernel(TopkK p) {
-  const int wave = threadIdx.x / kWave, lane = threadIdx.x % kWave;
-  const int64_t row = (int64_t)blockIdx.x * 4 + wave;
-  if (row >= p.rows) return;
-  const float* s = p.scores + row * p.row_stride;
-  uint64_t prev = ~0ull;
-  int my_id = -1;             // lane k keeps the k-th winner
-  float my_val = 0.f;
-  int nsel = 0;
-  for (int k = 0; k < p.K; ++k) {
-    uint64_t best = 0;
-    for (int j = lane; j < p.n; j += kWave) {
-      const float v = s[j];
-      if (!(v > p.invalid_at)) continue;                 // invalid, -inf or NaN
-      const uint64_t key = order_key(v, j);
-      if (key < prev && key > best) best = key;
-    }
-    best = wave_max_u64(best);
-    if (best == 0) break;                                // no valid entry left
-    prev = best;
-    const int id = (int)(0xffffffffu - (uint32_t)(best & 0xffffffffu));
-    if (lane == k) {
-      my_id = id;
-      my_val = s[id];
-    }
-    ++nsel;
-  }
+// The K winners held one per lane (lane k the k-th largest): optionally
+// reordered by ascending id, then written with -1 / -inf padding.
+__device__ __forceinline__ void topk_write(const TopkK& p, int64_t row, int lane, int my_id, float my_val, int nsel) {
   if (p.ascending && nsel > 1) {
     // rank of this lane's id among the selected ids (ids are distinct)
     int rank = 0;
@@ -180,6 +157,75 @@ __global__ __launch_bounds__(256) void topk_rows_kernel(TopkK p) {
   }
 }
 
+// one wavefront per row; 4 rows per workgroup (rows of any width)
+__global__ __launch_bounds__(256) void topk_rows_kernel(TopkK p) {
+  const int wave = threadIdx.x / kWave, lane = threadIdx.x % kWave;
+  const int64_t row = (int64_t)blockIdx.x * 4 + wave;
+  if (row >= p.rows) return;
+  const float* s = p.scores + row * p.row_stride;
+  uint64_t prev = ~0ull;
+  int my_id = -1;             // lane k keeps the k-th winner
+  float my_val = 0.f;
+  int nsel = 0;
+  for (int k = 0; k < p.K; ++k) {
+    uint64_t best = 0;
+    for (int j = lane; j < p.n; j += kWave) {
+      const float v = s[j];
+      if (!(v > p.invalid_at)) continue;                 // invalid, -inf or NaN
+      const uint64_t key = order_key(v, j);
+      if (key < prev && key > best) best = key;
+    }
+    best = wave_max_u64(best);
+    if (best == 0) break;                                // no valid entry left
+    prev = best;
+    const int id = (int)(0xffffffffu - (uint32_t)(best & 0xffffffffu));
+    if (lane == k) {
+      my_id = id;
+      my_val = s[id];
+    }
+    ++nsel;
+  }
+  topk_write(p, row, lane, my_id, my_val, nsel);
+}
+
+// The same selection with the row held in registers (column j = lane + 64 i,
+// i < NPL; rows up to 64 NPL wide): one read of the scores, then each round a
+// register max, a DPP wave max and the winner's key cleared where it lives.
+// The winner's score comes back exactly from its key's upper half.
+template <int NPL>
+__global__ __launch_bounds__(256) void topk_rows_regs_kernel(TopkK p) {
+  const int wave = threadIdx.x / kWave, lane = threadIdx.x % kWave;
+  const int64_t row = (int64_t)blockIdx.x * 4 + wave;
+  if (row >= p.rows) return;
+  const float* s = p.scores + row * p.row_stride;
+  uint64_t key[NPL];
+#pragma unroll
+  for (int i = 0; i < NPL; ++i) {
+    const int j = lane + kWave * i;
+    const float v = j < p.n ? s[j] : -INFINITY;
+    key[i] = v > p.invalid_at ? order_key(v, j) : 0ull;  // invalid, -inf or NaN: never selected
+  }
+  int my_id = -1;
+  float my_val = 0.f;
+  int nsel = 0;
+  for (int k = 0; k < p.K; ++k) {
+    uint64_t best = 0;
+#pragma unroll
+    for (int i = 0; i < NPL; ++i) best = key[i] > best ? key[i] : best;
+    best = wave_max_u64(best);
+    if (best == 0) break;
+#pragma unroll
+    for (int i = 0; i < NPL; ++i) key[i] = key[i] == best ? 0ull : key[i];
+    if (lane == k) {
+      my_id = (int)(0xffffffffu - (uint32_t)(best & 0xffffffffu));
+      const uint32_t u = (uint32_t)(best >> 32);
+      my_val = __uint_as_float((u & 0x80000000u) ? (u & 0x7fffffffu) : ~u);
+    }
+    ++nsel;
+  }
+  topk_write(p, row, lane, my_id, my_val, nsel);
+}
+
 int elem_bytes_i(int dt) { return dt == SRSWA_F32 ? 4 : 2; }
 
 template <typename T, bool HC>
@@ -205,7 +251,16 @@ int dispatch_summary(const IndexK& k, hipStream_t st) {
 int run_topk(const TopkK& t, hipStream_t st) {
   if (t.rows == 0) return SRSWA_OK;
   const int64_t grid = (t.rows + 3) / 4;
-  hipLaunchKernelGGL(topk_rows_kernel, dim3((unsigned)grid), dim3(256), 0, st, t);
+  if (t.n <= 256)
+    hipLaunchKernelGGL(topk_rows_regs_kernel<4>, dim3((unsigned)grid), dim3(256), 0, st, t);
+  else if (t.n <= 512)
+    hipLaunchKernelGGL(topk_rows_regs_kernel<8>, dim3((unsigned)grid), dim3(256), 0, st, t);
+  else if (t.n <= 1024)
+    hipLaunchKernelGGL(topk_rows_regs_kernel<16>, dim3((unsigned)grid), dim3(256), 0, st, t);
+  else if (t.n <= 2048)
+    hipLaunchKernelGGL(topk_rows_regs_kernel<32>, dim3((unsigned)grid), dim3(256), 0, st, t);
+  else
+    hipLaunchKernelGGL(topk_rows_kernel, dim3((unsigned)grid), dim3(256), 0, st, t);
   const hipError_t e = hipGetLastError();
   if (e != hipSuccess) {
     set_error("topk launch failed: %s", hipGetErrorString(e));
