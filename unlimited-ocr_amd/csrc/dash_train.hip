@@ -169,11 +169,24 @@ __global__ __launch_bounds__(kWave) void route_train_kernel(srswa_dash_route_tra
     return NPL > 0 ? mv[t] : (bc ? bc[i] != 0 : (im ? im[i] != 0 : true));
   };
   if constexpr (NPL > 0) {
+    // two unconditional batches of loads (block clamped to the row, the tail
+    // masked after): under a per-block branch each load waits out its own
+    // round trip
+    const uint8_t* mrow = bc ? bc : im;
+    uint8_t mb[NR];
+    if (n > 0) {
+#pragma unroll
+      for (int t = 0; t < NPL; ++t) sv[t] = ldv<T>(sr, min(lane + kWave * t, n - 1));
+      if (mrow) {
+#pragma unroll
+        for (int t = 0; t < NPL; ++t) mb[t] = mrow[min(lane + kWave * t, n - 1)];
+      }
+    }
 #pragma unroll
     for (int t = 0; t < NPL; ++t) {
       const int i = lane + kWave * t;
-      sv[t] = i < n ? ldv<T>(sr, i) : -INFINITY;
-      mv[t] = i < n && (bc ? bc[i] != 0 : (im ? im[i] != 0 : true));
+      sv[t] = i < n ? sv[t] : -INFINITY;
+      mv[t] = i < n && (mrow ? mb[t] != 0 : true);
     }
   }
   const int nt = NPL > 0 ? NPL : ceil_div(n, kWave);
@@ -307,11 +320,22 @@ __device__ __forceinline__ uint64_t select_keys(const srswa_dash_select_train_ar
   constexpr int NR = NPL > 0 ? NPL : 1;
   uint64_t keys[NR];
   if constexpr (NPL > 0) {
+    // candidate bytes and priors as two unconditional batches of loads (block
+    // clamped to the row, the tail masked after), so they are in flight together
+    uint8_t cb[NPL];
+    float pv[NPL];
+    if (n > 0) {
+#pragma unroll
+      for (int t = 0; t < NPL; ++t) cb[t] = cr[min(lane + kWave * t, n - 1)];
+#pragma unroll
+      for (int t = 0; t < NPL; ++t) pv[t] = ldv<T>(pr, min(lane + kWave * t, n - 1));
+    }
     uint64_t lmax = 0ull;
 #pragma unroll
     for (int t = 0; t < NPL; ++t) {
       const int i = lane + kWave * t;
-      keys[t] = i < n ? key_of(i) : 0ull;
+      const float sel = cb[t] ? pv[t] : -1.f;
+      keys[t] = i < n ? ((uint64_t)f32_order_key(sel) << 32) | (uint64_t)(0xffffffffu - (uint32_t)i) : 0ull;
       lmax = keys[t] > lmax ? keys[t] : lmax;
     }
     // K <= min(n, 64) lanes hold a real key, so the threshold is a real key

@@ -198,11 +198,19 @@ __global__ __launch_bounds__(256) void topk_rows_regs_kernel(TopkK p) {
   const int64_t row = (int64_t)blockIdx.x * 4 + wave;
   if (row >= p.rows) return;
   const float* s = p.scores + row * p.row_stride;
+  // the row's scores as one unconditional batch of loads (column clamped to the
+  // row, the tail masked below): under a per-column branch each load would
+  // wait out its own round trip
+  float sv[NPL];
+  if (p.n > 0) {
+#pragma unroll
+    for (int i = 0; i < NPL; ++i) sv[i] = s[min(lane + kWave * i, p.n - 1)];
+  }
   uint64_t key[NPL];
 #pragma unroll
   for (int i = 0; i < NPL; ++i) {
     const int j = lane + kWave * i;
-    const float v = j < p.n ? s[j] : -INFINITY;
+    const float v = j < p.n ? sv[i] : -INFINITY;
     key[i] = v > p.invalid_at ? order_key(v, j) : 0ull;  // invalid, -inf or NaN: never selected
   }
   int my_id = -1;

@@ -273,14 +273,28 @@ __global__ __launch_bounds__(kRsWaves * kWave) void route_entmax_regs_kernel(srs
   const float* sc = a.scores + row * a.sc_sn;
   const int8_t* im = a.img ? a.img + row * a.img_sn : nullptr;
 
+  // The row's scores and page-mask bytes are loaded as two unconditional
+  // batches (column index clamped to the row, the tail masked afterwards), so
+  // all of a lane's loads are in flight together: loads under a per-column
+  // branch each wait out their own round trip.
   float x[NPL];
+  int8_t iv[NPL];
+  if (a.W > 0) {
+    const int wl = a.W - 1;
+#pragma unroll
+    for (int i = 0; i < NPL; ++i) x[i] = sc[min(lane + kWave * i, wl)];
+    if (im) {
+#pragma unroll
+      for (int i = 0; i < NPL; ++i) iv[i] = im[min(lane + kWave * i, wl)];
+    }
+  }
   uint32_t rem_bits = 0, img_bits = 0;
 #pragma unroll
   for (int i = 0; i < NPL; ++i) {
     const int j = lane + kWave * i;
-    const float s = j < a.W ? sc[j] : -INFINITY;
+    const float s = j < a.W ? x[i] : -INFINITY;
     const bool remote = s > kScoreNeg * 0.5f;             // NaN / -inf: not remote
-    const bool ci = remote && im && im[j] != 0;
+    const bool ci = remote && im && iv[i] != 0;
     float xv = s * a.idx_scale;
     x[i] = xv == xv ? xv : kEntmaxNeg;
     rem_bits |= remote ? 1u << i : 0u;
