@@ -56,6 +56,10 @@ CASES = {
     "all_tied": (4, 1000, "equal", 8, 8, 1.0, 1e-4, 1.0, False),
     "narrow_w5": (6, 5, "normal", 2, 4, 1.0, 1e-4, 1.0, True),
     "w65": (10, 65, "normal", 64, 64, 3.0, 1e-4, 1.0, False),
+    # rows whose waves fill more than the GPU's SIMDs (a prefill chunk) take one
+    # wave per row; the cases above, fewer rows, two (tau and budget side by side)
+    "many_rows_w2048": (1500, 2048, "normal", 8, 16, 128 / math.sqrt(128), 1e-4, 1.0, True),
+    "many_rows_w300": (1100, 300, "ties", 8, 8, 1.0, 1e-4, 1.0, False),
     # rows above 2048 columns take the streaming kernel (the others hold the row in registers)
     "stream_w4100": (8, 4100, "normal", 8, 16, 128 / math.sqrt(128), 1e-4, 1.0, True),
     "stream_flat_w3000": (4, 3000, "flat", 12, 16, 1.0, 1e-4, 1.0, False),

@@ -26,6 +26,7 @@
 // reference's fp32 Triton arithmetic rounds it.
 #include <algorithm>
 
+#include "mfma_common.h"   // device_cu_count
 #include "summary.h"
 
 namespace srswa {
@@ -261,14 +262,26 @@ __global__ __launch_bounds__(kRsWaves * kWave) void route_entmax_kernel(srswa_ro
 // four fp64 partial sums per lane (independent add chains); as in the
 // streaming kernel their order differs from the reference's reduction tree
 // only below fp64 resolution, and the sum is then rounded to fp32.
-template <int NPL>
+// SPLIT (few rows, a GPU mostly idle, as in a decode step): two waves per row.
+// The tau bisection (role 0) and the budget threshold (role 1) depend only on
+// the row's z, so they run side by side; role 1 hands its threshold to role 0
+// through LDS, and role 0 finishes the row.  Otherwise (a prefill chunk, the
+// GPU full) one wave per row runs both stages.
+template <int NPL, bool SPLIT>
 __global__ __launch_bounds__(kRsWaves * kWave) void route_entmax_regs_kernel(srswa_route_serve_args a) {
   static_assert(NPL % 4 == 0 && NPL <= 32, "NPL: a multiple of 4, at most 32");
-  __shared__ uint32_t s_key[kRsWaves][kWave];
-  __shared__ float s_live[kRsWaves][4 * kWave];
+  constexpr int kRows = SPLIT ? kRsWaves / 2 : kRsWaves;   // rows per workgroup
+  __shared__ uint32_t s_key[kRows][kWave];
+  __shared__ float s_live[kRows][4 * kWave];
+  __shared__ float s_thr[kRows];
   const int wave = threadIdx.x / kWave, lane = threadIdx.x % kWave;
-  const int64_t row = (int64_t)blockIdx.x * kRsWaves + wave;
-  if (row >= a.rows) return;
+  const int pr = SPLIT ? wave >> 1 : wave;
+  const int row_role = SPLIT ? wave & 1 : -1;      // -1: both stages
+  const int64_t row0 = (int64_t)blockIdx.x * kRows + pr;
+  // a pair past the last row works on the last row and writes nothing, so
+  // every wave reaches the barrier below
+  const bool live_row = row0 < a.rows;
+  const int64_t row = live_row ? row0 : a.rows - 1;
   const unsigned long long lt = (1ull << lane) - 1ull;
   const float* sc = a.scores + row * a.sc_sn;
   const int8_t* im = a.img ? a.img + row * a.img_sn : nullptr;
@@ -318,6 +331,8 @@ __global__ __launch_bounds__(kRsWaves * kWave) void route_entmax_regs_kernel(srs
   for (int i = 0; i < NPL; ++i) x[i] = ((cand >> i) & 1u) ? (x[i] - xm) * 0.5f : -INFINITY;
   float* z = x;
 
+  float tau = 0.f, zthr = -INFINITY;
+  if (row_role != 1) {
   // tau: the reference's 24 bisection steps.  Every midpoint lies in (-1, 0),
   // so a z <= -1 adds exactly 0 to every step's sum: the live values (z > -1,
   // usually the few near the row's max) are compacted through LDS into
@@ -334,7 +349,7 @@ __global__ __launch_bounds__(kRsWaves * kWave) void route_entmax_regs_kernel(srs
     for (int i = 0; i < NPL; ++i) {
       const bool lv = (live >> i) & 1u;
       const unsigned long long bal = __ballot(lv);
-      if (lv) s_live[wave][base + __popcll(bal & lt)] = z[i];
+      if (lv) s_live[pr][base + __popcll(bal & lt)] = z[i];
       base += __popcll(bal);
     }
     wave_sync_lds();
@@ -342,7 +357,7 @@ __global__ __launch_bounds__(kRsWaves * kWave) void route_entmax_regs_kernel(srs
       constexpr int NC = decltype(nc_tag)::value;
       float zc[NC];
 #pragma unroll
-      for (int k = 0; k < NC; ++k) zc[k] = lane + kWave * k < n_live ? s_live[wave][lane + kWave * k] : -INFINITY;
+      for (int k = 0; k < NC; ++k) zc[k] = lane + kWave * k < n_live ? s_live[pr][lane + kWave * k] : -INFINITY;
       for (int it = 0; it < kTauIters; ++it) {
         const float mid = (lo + hi) * 0.5f;
         double acc = 0.0;
@@ -373,10 +388,10 @@ __global__ __launch_bounds__(kRsWaves * kWave) void route_entmax_regs_kernel(srs
       else hi = mid;
     }
   }
-  const float tau = (lo + hi) * 0.5f;
-
+  tau = (lo + hi) * 0.5f;
+  }
+  if (row_role != 0) {
   // budget: the (K+1)-th largest candidate z, then the reference's 40 steps
-  float zthr = -INFINITY;
   if (n_cand > a.K) {
     uint32_t keys[NPL];
     uint32_t lmax = 0;
@@ -403,9 +418,9 @@ __global__ __launch_bounds__(kRsWaves * kWave) void route_entmax_regs_kernel(srs
         int off = incl - cnt;
 #pragma unroll
         for (int i = 0; i < NPL; ++i)
-          if (keys[i] >= T) s_key[wave][off++] = keys[i];
+          if (keys[i] >= T) s_key[pr][off++] = keys[i];
         wave_sync_lds();
-        kth = __shfl(wave_sort_desc<uint32_t>(lane < C ? s_key[wave][lane] : 0u, lane), a.K, kWave);
+        kth = __shfl(wave_sort_desc<uint32_t>(lane < C ? s_key[pr][lane] : 0u, lane), a.K, kWave);
         found = true;
       }
     }
@@ -427,19 +442,32 @@ __global__ __launch_bounds__(kRsWaves * kWave) void route_entmax_regs_kernel(srs
     }
     zthr = hi2;
   }
+  if (SPLIT && lane == 0) s_thr[pr] = zthr;
+  }
+  if constexpr (SPLIT) {
+    __syncthreads();
+    if (row_role == 1 || !live_row) return;
+    zthr = s_thr[pr];
+  } else if (!live_row) {
+    return;
+  }
 
-  // mu over the active blocks, then the packed write
+  // mu over the active blocks (the log prior of those alone), then the packed
+  // write
   float lp[NPL];
   uint32_t act = 0;
   double lsum = 0.0;
 #pragma unroll
   for (int i = 0; i < NPL; ++i) {
-    float pr = fmaxf(z[i] - tau, 0.f);
-    pr = pr * pr;
-    lp[i] = logf(fmaxf(pr, a.prior_floor));
     const bool ac = ((cand >> i) & 1u) && z[i] > zthr;
     act |= ac ? 1u << i : 0u;
-    if (ac) lsum += (double)lp[i];
+    lp[i] = 0.f;
+    if (ac) {
+      float pv = fmaxf(z[i] - tau, 0.f);
+      pv = pv * pv;
+      lp[i] = logf(fmaxf(pv, a.prior_floor));
+      lsum += (double)lp[i];
+    }
   }
   const int n_sel = wave_sum_int(__popc(act));
   const float mu = (float)wave_sum_f64(lsum) / (float)max(n_sel, 1);
@@ -522,12 +550,19 @@ extern "C" int srswa_route_serve(const srswa_route_serve_args* a, void* stream) 
   }
   if (a->rows == 0) return SRSWA_OK;
   const dim3 grid((unsigned)((a->rows + kRsWaves - 1) / kRsWaves));
+  const dim3 grid2((unsigned)((a->rows + kRsWaves / 2 - 1) / (kRsWaves / 2)));
   hipStream_t st = reinterpret_cast<hipStream_t>(stream);
-  if (a->W <= 8 * kWave)
-    hipLaunchKernelGGL(route_entmax_regs_kernel<8>, grid, dim3(kRsWaves * kWave), 0, st, *a);
-  else if (a->W <= 32 * kWave)
-    hipLaunchKernelGGL(route_entmax_regs_kernel<32>, grid, dim3(kRsWaves * kWave), 0, st, *a);
-  else
+  // two waves per row while those waves fit one per SIMD (a decode step); a
+  // prefill chunk, which fills the GPU, keeps one wave per row
+  const int cus = device_cu_count();
+  const bool split = cus > 0 && (int64_t)a->rows * 2 <= (int64_t)cus * 4;
+  if (a->W <= 8 * kWave) {
+    if (split) hipLaunchKernelGGL((route_entmax_regs_kernel<8, true>), grid2, dim3(kRsWaves * kWave), 0, st, *a);
+    else hipLaunchKernelGGL((route_entmax_regs_kernel<8, false>), grid, dim3(kRsWaves * kWave), 0, st, *a);
+  } else if (a->W <= 32 * kWave) {
+    if (split) hipLaunchKernelGGL((route_entmax_regs_kernel<32, true>), grid2, dim3(kRsWaves * kWave), 0, st, *a);
+    else hipLaunchKernelGGL((route_entmax_regs_kernel<32, false>), grid, dim3(kRsWaves * kWave), 0, st, *a);
+  } else
     hipLaunchKernelGGL(route_entmax_kernel, grid, dim3(kRsWaves * kWave), 0, st, *a);
   return launch_status("route serve");
 }
