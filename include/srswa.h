@@ -703,6 +703,17 @@ typedef struct {
 
 int srswa_gather_kl_fwd(const srswa_kl_args* a, void* stream);
 
+/* The same forward with a caller-owned workspace (bytes from
+ * srswa_gather_kl_fwd_workspace; 0 for an empty call).  With it, each 64-row
+ * tile whose rows' selected blocks form a union of more than 2 K blocks (rows
+ * that select unrelated blocks, as the reference's per-row top-k does,
+ * HF/_sparse_base_impl.py:3386-3403) is computed block-major: every key block
+ * visits only the rows that selected it.  Results are those of
+ * srswa_gather_kl_fwd up to fp32 rounding; no value depends on how rows are
+ * grouped.  Same reference interface as srswa_gather_kl_fwd. */
+size_t srswa_gather_kl_fwd_workspace(const srswa_kl_args* a);
+int srswa_gather_kl_fwd_ws(const srswa_kl_args* a, void* scratch, size_t scratch_bytes, void* stream);
+
 /* Backward of the student path (the teacher carries no gradient): with
  * g = grad[b, ih, t] and ds_j = rnd(g * dsel_j),
  *   dq_idx[b, ih, t] = rnd(sum_j ds_j idx_k[j]),  dk_idx[b, j] = rnd(sum_{rows} ds_j q_idx[row])

@@ -92,6 +92,33 @@ def test_forward_and_dsel(dev, case):
     del nblk
 
 
+def test_row_sparse_and_tile_paths_agree(dev):
+    """Tiles alternate between rows sharing one selection (the tile kernel
+    takes them) and rows selecting unrelated blocks (flagged, block-major);
+    T spans three 1024-row ranges.  The block-major path against the oracle,
+    and against the tile kernel run on every tile (fp32 rounding apart)."""
+    from srswa import kl as KL
+    B, HI, G, HKV, T, Sk, D, topk, dtype = 1, 1, 4, 2, 2200, 2600, 128, 8, torch.bfloat16
+    print(f"kl row-sparse vs tile B={B} T={T} Sk={Sk} K={topk}", flush=True)
+    q_idx, idx_k, q_main, k_main, sel, pos, seg, scaling = _case(11, B, HI, G, HKV, T, Sk, D, topk, dtype)
+    g = torch.Generator().manual_seed(12)
+    nblk = -(-Sk // 64)
+    for tau in range(0, -(-T // 64), 2):                  # even tiles: one selection for all their rows
+        sel[:, :, 64 * tau:64 * tau + 64] = torch.randperm(nblk, generator=g)[:topk].to(torch.int32)
+    lw = 256
+    args = (q_idx.to(dev), idx_k.to(dev), q_main.to(dev), k_main.to(dev), sel.to(dev), pos.to(dev))
+    kl, valid, dsel = KL.kl_forward(*args, block_size=64, local_window=lw, scaling=scaling)
+    kl_t, valid_t, dsel_t = KL.kl_forward(*args, block_size=64, local_window=lw, scaling=scaling, row_sparse=False)
+    assert torch.equal(valid, valid_t)
+    assert (kl - kl_t).abs().max().item() <= 1e-5 + 1e-5 * kl_t.abs().max().item()
+    assert (dsel - dsel_t).abs().max().item() <= 1e-5
+    rk, rv = K.gather_kl_dense(q_idx.double(), idx_k.double(), q_main.double(), k_main.double(), sel, pos,
+                               block_size=64, local_window=lw, scaling=scaling, seg=None, round_dtype=dtype)
+    assert torch.equal(valid.cpu(), rv)
+    err = (kl.cpu().double() - rk).abs() - 1e-3 * rk.abs()
+    assert err.max().item() <= 2e-3, err.max().item()
+
+
 @pytest.mark.parametrize("case", CASES[:3])
 def test_backward(dev, case):
     seed, B, HI, G, HKV, T, Sk, D, topk, dtype, packed, dup = case

@@ -42,6 +42,7 @@ struct KlK {
   int ntiles, nwords, G, KV;     // G = query heads per index head, KV = query heads per kv head
   int nlogical, per_xcd;
   int ids_off, bits_off, chunks_off, stats_off;   // LDS byte offsets
+  const uint32_t* rs_flag;       // [B, HI, ntiles]: tile taken by the row-sparse kernels, or NULL
 };
 
 template <int D> struct KlLds {
@@ -82,6 +83,7 @@ __global__ __launch_bounds__(256, 2) void kl_fwd_kernel(KlK p) {
   const int team = wave >> 1, rw = wave & 1;
   const int tile = lid % p.ntiles;
   const int bh = lid / p.ntiles;
+  if (p.rs_flag && p.rs_flag[(int64_t)bh * p.ntiles + tile]) return;   // the row-sparse kernels take it
   const int ih = bh % a.HI, b = bh / a.HI;
   const int t0 = tile * kTileRows;
   const int nrows = min(kTileRows, a.T - t0);
@@ -345,6 +347,371 @@ __global__ __launch_bounds__(256, 2) void kl_fwd_kernel(KlK p) {
   }
 }
 
+// -------------------------------------------------------------- row-sparse forward
+// Rows that select unrelated blocks (per-row top-k, as the indexer's own
+// selections are) give a 64-row tile a block union near the whole prefix, and
+// the tile kernel would spend most of its work on (row, block) pairs that no
+// row of the pair keeps.  Tiles whose union exceeds 2 K blocks are flagged on
+// the device and taken block-major: for every key block, the rows of flagged
+// tiles that selected it are gathered 64 at a time, so each (row, block) pair
+// is computed once.
+//   kl_rs_flag_kernel    per tile: the union size and the flag; for a flagged
+//                        tile, bit t of block c's row bitmap for every kept
+//                        (row t, block c) pair;
+//   kl_rs_pass_kernel    per (block, 1024-row range), over the same row groups
+//                        twice: STATS writes each pair's (max, sum) per head,
+//                        MIX (after the combine) mixes the teacher over the
+//                        heads, takes the student's log-softmax and writes the
+//                        pair's KL sum and its dsel row;
+//   kl_rs_combine_kernel per row: the pairs' statistics merged per head in slot
+//                        order, dsel zeroed for slots with nothing kept;
+//   kl_rs_final_kernel   per row: the KL as the sum of its pairs in slot order.
+// Every (row, slot) pair writes its own records, so no result depends on how
+// the rows are grouped.
+constexpr int kRsRange = 1024;   // rows per block-major workgroup (32 bitmap words)
+
+struct KlRsK {
+  srswa_kl_args a;
+  int ntiles, nblk, nwords, rwords, nrange, G, KV;
+  uint32_t* flag;     // [B, HI, ntiles]
+  uint32_t* rbm;      // [B, HI, nblk, rwords] rows of flagged tiles per block
+  float2* srec;       // [B, HI, T, K, G + 1] per pair and head: (max in log2 units, sum)
+  float2* rst;        // [B, HI, T, G + 1] per row and head: merged (max, sum)
+  float* klp;         // [B, HI, T, K] per pair: sum of the KL terms (log2 units)
+};
+
+// The row's kept key range [lo, hi): its sample start to the window start.
+__device__ __forceinline__ void kl_row_range(const srswa_kl_args& a, int b, int t, int& lo, int& hi) {
+  const int pos = a.pos[(int64_t)b * a.pos_sb + t];
+  lo = a.seg ? a.seg[(int64_t)b * a.seg_sb + t] : 0;
+  hi = min(max(pos - a.local_window + 1, 0), a.Sk);
+}
+
+// Block id of slot s of row t when it holds kept keys and is the id's first
+// slot (a repeated id counts once), else -1.
+__device__ __forceinline__ int kl_slot_block(const int32_t* ids, int s, int lo, int hi) {
+  int id = ids[s];
+  if (id < 0 || (int64_t)id * kChunk >= hi || (int64_t)id * kChunk + kChunk <= lo) return -1;
+  for (int s2 = 0; s2 < s; ++s2)
+    if (ids[s2] == id) return -1;
+  return id;
+}
+
+__device__ __forceinline__ const int32_t* kl_row_ids(const srswa_kl_args& a, int b, int ih, int t) {
+  return a.sel + (int64_t)b * a.sel_sb + (int64_t)ih * a.sel_sh + (int64_t)t * a.sel_st;
+}
+
+__global__ __launch_bounds__(256) void kl_rs_flag_kernel(KlRsK p) {
+  extern __shared__ uint32_t s_u[];                    // [nwords] union bits, [1] count, [64 K] ids
+  const srswa_kl_args& a = p.a;
+  const int tile = (int)(blockIdx.x % p.ntiles);
+  const int bh = (int)(blockIdx.x / p.ntiles);
+  const int ih = bh % a.HI, b = bh / a.HI;
+  const int t0 = tile * kTileRows, nrows = min(kTileRows, a.T - t0);
+  const int K = a.K, tid = threadIdx.x;
+  uint32_t* s_bits = s_u;
+  uint32_t* s_cnt = s_u + p.nwords;
+  int* s_ids = reinterpret_cast<int*>(s_u + p.nwords + 1);
+  for (int w = tid; w <= p.nwords; w += blockDim.x) s_u[w] = 0u;
+  __syncthreads();
+  for (int e = tid; e < kTileRows * K; e += blockDim.x) {
+    const int r = e / K, s = e % K;
+    int id = -1;
+    if (r < nrows) {
+      int lo, hi;
+      kl_row_range(a, b, t0 + r, lo, hi);
+      id = kl_slot_block(kl_row_ids(a, b, ih, t0 + r), s, lo, hi);
+      if (id >= 0) atomicOr(&s_bits[id >> 5], 1u << (id & 31));
+    }
+    s_ids[e] = id;
+  }
+  __syncthreads();
+  for (int w = tid; w < p.nwords; w += blockDim.x) atomicAdd(s_cnt, (uint32_t)__popc(s_bits[w]));
+  __syncthreads();
+  const bool rs = (int)*s_cnt > 2 * K;
+  if (tid == 0) p.flag[(int64_t)bh * p.ntiles + tile] = rs ? 1u : 0u;
+  if (!rs) return;
+  uint32_t* rb = p.rbm + (int64_t)bh * p.nblk * p.rwords;
+  for (int e = tid; e < nrows * K; e += blockDim.x) {
+    const int id = s_ids[e], t = t0 + e / K;
+    if (id >= 0) atomicOr(&rb[(int64_t)id * p.rwords + (t >> 5)], 1u << (t & 31));
+  }
+}
+
+// One workgroup per (sequence, index head, block c, 1024-row range), two waves
+// of 32 rows per group of 64 (lane = row, S^T = K Q^T over the block's 64
+// keys as in the tile kernel).  Stage (group, head): K of the head's block
+// staged in LDS, the rows' query fragments in registers, both fetched one
+// stage ahead.
+template <typename T, int D, bool MIX>
+__global__ __launch_bounds__(128, 2) void kl_rs_pass_kernel(KlRsK p) {
+  using M = Mfma<T>;
+  using L = KlLds<D>;
+  constexpr int KP = L::KP, KS = D / 16, NT = 128;
+  constexpr int PPT = kChunk * D / 8 / NT;
+  constexpr int RPP = NT / (D / 8);
+  __shared__ __align__(16) T sK[kChunk * KP];
+  __shared__ int s_rows[kRsRange];
+  __shared__ int s_n;
+  // MIX: the student's log q (log2 units) of the group's rows, [row][key] with
+  // a 68-float pitch (conflict-free 16-byte accesses)
+  constexpr int LQP = 68;
+  __shared__ __align__(16) float s_lq[MIX ? kTileRows * LQP : 4];
+  const srswa_kl_args& a = p.a;
+  const int range = (int)(blockIdx.x % p.nrange);
+  const int c = (int)((blockIdx.x / p.nrange) % p.nblk);
+  const int bh = (int)(blockIdx.x / ((int64_t)p.nrange * p.nblk));
+  const int ih = bh % a.HI, b = bh / a.HI;
+  const int tid = threadIdx.x, wave = tid / kWave, lane = tid % kWave;
+  const int h = lane >> 5, rl = lane & 31;
+  const int G = p.G, K = a.K;
+  const int j0 = c * kChunk;
+
+  // this range's rows of block c, ascending: one bitmap word per lane of wave 0
+  const uint32_t* rb = p.rbm + ((int64_t)bh * p.nblk + c) * p.rwords;
+  if (wave == 0) {
+    const int w = range * (kRsRange / 32) + lane;
+    const uint32_t bits = (lane < kRsRange / 32 && w < p.rwords) ? rb[w] : 0u;
+    const int cnt = __popc(bits);
+    int incl = cnt;
+#pragma unroll
+    for (int o = 1; o < kWave; o <<= 1) {
+      const int v = __shfl_up(incl, o, kWave);
+      if (lane >= o) incl += v;
+    }
+    int pos = incl - cnt;
+    uint32_t bb = bits;
+    while (bb) {
+      const int bit = __ffs(bb) - 1;
+      bb &= bb - 1;
+      s_rows[pos++] = w * 32 + bit;
+    }
+    if (lane == kWave - 1) s_n = incl;
+  }
+  __syncthreads();
+  const int n = s_n;
+  if (n == 0) return;
+  const int ngroups = (n + kTileRows - 1) / kTileRows;
+  const int nst = ngroups * (G + 1);
+  const int row = wave * 32 + rl;                    // row of the group this lane owns
+  // head of a stage's position j in its group: the student first (its log q
+  // is parked in LDS), then the teachers; the last teacher forms the terms
+  auto head_of = [&](int j) { return j == 0 ? G : j - 1; };
+
+  auto key_base = [&](int hh, int64_t& st) -> const T* {
+    if (hh == G) {
+      st = a.ik_st;
+      return reinterpret_cast<const T*>(a.idx_k) + (int64_t)b * a.ik_sb;
+    }
+    const int kvh = (ih * G + hh) / p.KV;
+    st = a.km_st;
+    return reinterpret_cast<const T*>(a.k_main) + (int64_t)b * a.km_sb + (int64_t)kvh * a.km_sh;
+  };
+  // the row of group g this lane owns, or -1 past the list (it then reads
+  // row s_rows[0]'s query and keeps nothing)
+  auto group_row = [&](int g) { const int i = g * kTileRows + row; return i < n ? s_rows[i] : -1; };
+  auto q_row = [&](int hh, int t) -> const T* {
+    const int tt = t >= 0 ? t : s_rows[0];
+    if (hh == G)
+      return reinterpret_cast<const T*>(a.q_idx) + (int64_t)b * a.qi_sb + (int64_t)ih * a.qi_sh + (int64_t)tt * a.qi_st;
+    return reinterpret_cast<const T*>(a.q_main) + (int64_t)b * a.qm_sb + (int64_t)(ih * G + hh) * a.qm_sh +
+           (int64_t)tt * a.qm_st;
+  };
+  T* sKw = sK + (tid / (D / 8)) * KP + (tid % (D / 8)) * 8;
+  uint4 kpre[PPT], qpre[KS], qf[KS];
+  auto fetch = [&](int i) {
+    const int g = i / (G + 1), hh = head_of(i % (G + 1));
+    int64_t st;
+    const T* base = key_base(hh, st);
+    const __amdgpu_buffer_rsrc_t rs = make_rsrc(base, (uint32_t)(((int64_t)(a.Sk - 1) * st + D) * 2));
+    const uint32_t vo = (uint32_t)((tid / (D / 8)) * st + (tid % (D / 8)) * 8) * 2;
+    const uint32_t so = (uint32_t)j0 * (uint32_t)st * 2u;
+#pragma unroll
+    for (int k = 0; k < PPT; ++k) kpre[k] = buffer_load16(rs, vo, so + (uint32_t)(k * RPP) * (uint32_t)st * 2u);
+    const T* qr = q_row(hh, group_row(g));
+#pragma unroll
+    for (int ks = 0; ks < KS; ++ks) qpre[ks] = *reinterpret_cast<const uint4*>(qr + 16 * ks + 8 * h);
+  };
+
+  const int64_t rowbase = (int64_t)bh * a.T;       // (b, ih) row offset of the per-row records
+  int t = -1, slot = -1;
+  uint64_t keep = 0ull;
+  float pacc[32];
+  fetch(0);
+  for (int i = 0; i < nst; ++i) {
+    const int g = i / (G + 1), j = i % (G + 1), hh = head_of(j);
+    __syncthreads();                                  // the previous stage's keys consumed
+#pragma unroll
+    for (int k = 0; k < PPT; ++k) *reinterpret_cast<uint4*>(sKw + k * RPP * KP) = kpre[k];
+#pragma unroll
+    for (int ks = 0; ks < KS; ++ks) qf[ks] = qpre[ks];
+    __syncthreads();
+    if (i + 1 < nst) fetch(i + 1);
+    if (j == 0) {                                     // a new group: the lane's row, slot and kept keys
+      t = group_row(g);
+      slot = -1;
+      keep = 0ull;
+      if (t >= 0) {
+        int lo, hi;
+        kl_row_range(a, b, t, lo, hi);
+        const int32_t* ids = kl_row_ids(a, b, ih, t);
+        for (int s = 0; s < K && slot < 0; ++s)
+          if (ids[s] == c) slot = s;                  // the first slot holding c (the bitmap holds kept pairs)
+        keep = range64(min(max(lo - j0, 0), 64), min(max(hi - j0, 0), 64));
+      }
+      if constexpr (MIX) {
+#pragma unroll
+        for (int r = 0; r < 32; ++r) pacc[r] = 0.f;
+      }
+    }
+    f32x16_t st[2] = {zero16(), zero16()};
+#pragma unroll
+    for (int ks = 0; ks < KS; ++ks) {
+#pragma unroll
+      for (int kh = 0; kh < 2; ++kh)
+        st[kh] = M::mac(*reinterpret_cast<const uint4*>(sK + (32 * kh + rl) * KP + 16 * ks + 8 * h), qf[ks], st[kh]);
+    }
+    // logits in the reference's rounding, in log2 units; register r of key
+    // half kh is key 32 kh + 8 (r / 4) + 4h + r % 4
+    const float mul2 = (hh == G ? 1.f : a.scaling) * kLog2e;
+    // logit of element r (0..31) of the lane: -inf where the key is not kept
+    auto xat = [&](int r) __attribute__((always_inline)) {
+      const int kh = r >> 4, rr = r & 15;
+      const int key = 32 * kh + 8 * (rr >> 2) + 4 * h + (rr & 3);
+      return ((keep >> key) & 1ull) ? round_to<T>(st[kh][rr]) * mul2 : -INFINITY;
+    };
+    if constexpr (!MIX) {
+      float x[32];
+#pragma unroll
+      for (int r = 0; r < 32; ++r) x[r] = xat(r);
+      float m = -INFINITY;
+#pragma unroll
+      for (int r = 0; r < 32; ++r) m = fmaxf(m, x[r]);
+      m = fmaxf(m, __shfl_xor(m, 32, kWave));
+      float l = 0.f;
+      if (m > -INFINITY) {
+#pragma unroll
+        for (int r = 0; r < 32; ++r) l += __builtin_amdgcn_exp2f(x[r] - m);   // a masked key adds 0
+      }
+      l += __shfl_xor(l, 32, kWave);
+      if (t >= 0 && h == 0) p.srec[((rowbase + t) * K + slot) * (G + 1) + hh] = make_float2(m, l);
+    } else {
+      const float2 ml = t >= 0 ? p.rst[(rowbase + t) * (G + 1) + hh] : make_float2(-INFINITY, 0.f);
+      float* lq = s_lq + row * LQP;
+      if (hh == G) {
+        // student: log q (log2 units) of the lane's keys into LDS, 4 keys per store
+        const float lse2 = ml.y > 0.f ? ml.x + __builtin_amdgcn_logf(ml.y) : 0.f;
+#pragma unroll
+        for (int kh = 0; kh < 2; ++kh)
+#pragma unroll
+          for (int r4 = 0; r4 < 4; ++r4) {
+            float v[4];
+#pragma unroll
+            for (int e = 0; e < 4; ++e) v[e] = xat(16 * kh + 4 * r4 + e) - lse2;
+            *reinterpret_cast<float4*>(lq + 32 * kh + 8 * r4 + 4 * h) = make_float4(v[0], v[1], v[2], v[3]);
+          }
+      } else if (ml.y > 0.f) {
+        const float cc = ml.x + __builtin_amdgcn_logf(ml.y);    // p = exp2(x - (m + log2 l))
+#pragma unroll
+        for (int r = 0; r < 32; ++r) pacc[r] += __builtin_amdgcn_exp2f(xat(r) - cc);
+      }
+      if (j == G) {
+        // the group's last teacher: the pair's KL terms and its dsel row
+        const float invg = 1.f / (float)G;
+        float kl_acc = 0.f;
+        float* drow = (a.dsel && t >= 0)
+                          ? a.dsel + (int64_t)b * a.ds_sb + (int64_t)ih * a.ds_sh + (int64_t)t * a.ds_st +
+                                (int64_t)slot * kChunk
+                          : nullptr;
+#pragma unroll
+        for (int kh = 0; kh < 2; ++kh)
+#pragma unroll
+          for (int r4 = 0; r4 < 4; ++r4) {
+            const float4 q4 = *reinterpret_cast<const float4*>(lq + 32 * kh + 8 * r4 + 4 * h);
+            const float lqv[4] = {q4.x, q4.y, q4.z, q4.w};
+            float dv[4];
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+              const int r = 16 * kh + 4 * r4 + e;
+              const int key = 32 * kh + 8 * r4 + 4 * h + e;
+              const bool kp = (keep >> key) & 1ull;
+              const float pv = pacc[r] * invg;
+              const float logq2 = lqv[e];
+              const float lp2 = __builtin_amdgcn_logf(fmaxf(pv, 1e-12f));
+              const float term = pv * (lp2 - logq2), d = __builtin_amdgcn_exp2f(logq2) - pv;
+              kl_acc += kp ? term : 0.f;
+              dv[e] = kp ? d : 0.f;
+            }
+            if (drow) *reinterpret_cast<float4*>(drow + 32 * kh + 8 * r4 + 4 * h) = make_float4(dv[0], dv[1], dv[2], dv[3]);
+          }
+        kl_acc += __shfl_xor(kl_acc, 32, kWave);
+        if (t >= 0 && h == 0) p.klp[(rowbase + t) * K + slot] = kl_acc;
+      }
+    }
+  }
+}
+
+// Per row of a flagged tile: every head's statistics merged over the row's
+// kept slots in slot order; dsel rows of slots with nothing kept zeroed.
+__global__ __launch_bounds__(256) void kl_rs_combine_kernel(KlRsK p) {
+  const srswa_kl_args& a = p.a;
+  const int64_t gid = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (gid >= (int64_t)a.B * a.HI * a.T) return;
+  const int t = (int)(gid % a.T);
+  const int bh = (int)(gid / a.T);
+  const int ih = bh % a.HI, b = bh / a.HI;
+  if (!p.flag[(int64_t)bh * p.ntiles + t / kTileRows]) return;
+  const int K = a.K, G = p.G;
+  int lo, hi;
+  kl_row_range(a, b, t, lo, hi);
+  const int32_t* ids = kl_row_ids(a, b, ih, t);
+  uint64_t live = 0ull;
+  for (int s = 0; s < K; ++s) {
+    if (kl_slot_block(ids, s, lo, hi) >= 0) {
+      live |= 1ull << s;
+    } else if (a.dsel) {
+      float4* z = reinterpret_cast<float4*>(a.dsel + (int64_t)b * a.ds_sb + (int64_t)ih * a.ds_sh +
+                                            (int64_t)t * a.ds_st + (int64_t)s * kChunk);
+#pragma unroll
+      for (int i = 0; i < kChunk / 4; ++i) z[i] = make_float4(0.f, 0.f, 0.f, 0.f);
+    }
+  }
+  const float2* rec = p.srec + gid * K * (G + 1);
+  for (int hh = 0; hh <= G; ++hh) {
+    float mm = -INFINITY;
+    for (int s = 0; s < K; ++s)
+      if ((live >> s) & 1ull) mm = fmaxf(mm, rec[s * (G + 1) + hh].x);
+    float ll = 0.f;
+    if (mm > -INFINITY)
+      for (int s = 0; s < K; ++s)
+        if ((live >> s) & 1ull) {
+          const float2 v = rec[s * (G + 1) + hh];
+          if (v.x > -INFINITY) ll += v.y * __builtin_amdgcn_exp2f(v.x - mm);
+        }
+    p.rst[gid * (G + 1) + hh] = make_float2(mm, ll);
+  }
+}
+
+// Per row of a flagged tile: kl = the sum of its pairs' KL sums in slot order.
+__global__ __launch_bounds__(256) void kl_rs_final_kernel(KlRsK p) {
+  const srswa_kl_args& a = p.a;
+  const int64_t gid = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (gid >= (int64_t)a.B * a.HI * a.T) return;
+  const int t = (int)(gid % a.T);
+  const int bh = (int)(gid / a.T);
+  const int ih = bh % a.HI, b = bh / a.HI;
+  if (!p.flag[(int64_t)bh * p.ntiles + t / kTileRows]) return;
+  int lo, hi;
+  kl_row_range(a, b, t, lo, hi);
+  const int32_t* ids = kl_row_ids(a, b, ih, t);
+  float kl = 0.f;
+  for (int s = 0; s < a.K; ++s)
+    if (kl_slot_block(ids, s, lo, hi) >= 0) kl += p.klp[gid * a.K + s];
+  const bool valid = p.rst[gid * (p.G + 1) + p.G].y > 0.f;
+  a.kl[(int64_t)b * a.kl_sb + (int64_t)ih * a.kl_sh + t] = valid ? kl * kLn2 : 0.f;
+  a.valid[(int64_t)b * a.va_sb + (int64_t)ih * a.va_sh + t] = valid ? 1 : 0;
+}
+
 // -------------------------------------------------------------- backward
 // Both kernels are tile products on the matrix cores with ds = rnd(g * dsel)
 // (the reference's bf16 gradient of the logits) staged in LDS:
@@ -603,7 +970,53 @@ int check_common(int dtype, int D, int block_size, int K, const char* what) {
 
 using namespace srswa;
 
+namespace srswa {
+namespace {
+
+// Workspace of the row-sparse kernels, in 256-byte aligned pieces.
+struct KlRsLayout {
+  size_t flag, rbm, srec, rst, klp, total;
+};
+KlRsLayout kl_rs_layout(const srswa_kl_args* a) {
+  auto al = [](size_t n) { return (n + 255) / 256 * 256; };
+  const int64_t bh = (int64_t)a->B * a->HI, rows = bh * a->T, G = a->HQ / std::max(a->HI, 1);
+  const int64_t ntiles = ceil_div(a->T, kTileRows), nblk = ceil_div(a->Sk, kChunk), rwords = ceil_div(a->T, 32);
+  KlRsLayout L{};
+  L.flag = 0;
+  L.rbm = L.flag + al((size_t)(bh * ntiles) * 4);
+  L.srec = L.rbm + al((size_t)(bh * nblk * rwords) * 4);
+  L.rst = L.srec + al((size_t)(rows * a->K * (G + 1)) * 8);
+  L.klp = L.rst + al((size_t)(rows * (G + 1)) * 8);
+  L.total = L.klp + al((size_t)(rows * a->K) * 4);
+  return L;
+}
+
+int kl_fwd_impl(const srswa_kl_args* a, void* scratch, size_t scratch_bytes, void* stream);
+
+}  // namespace
+}  // namespace srswa
+
+extern "C" size_t srswa_gather_kl_fwd_workspace(const srswa_kl_args* a) {
+  if (!a || a->B <= 0 || a->HI <= 0 || a->T <= 0 || a->Sk <= 0 || a->K <= 0) return 0;
+  return kl_rs_layout(a).total;
+}
+
 extern "C" int srswa_gather_kl_fwd(const srswa_kl_args* a, void* stream) {
+  return kl_fwd_impl(a, nullptr, 0, stream);
+}
+
+extern "C" int srswa_gather_kl_fwd_ws(const srswa_kl_args* a, void* scratch, size_t scratch_bytes, void* stream) {
+  if (!scratch) {
+    set_error("gather kl: null workspace (srswa_gather_kl_fwd runs without one)");
+    return SRSWA_INVALID;
+  }
+  return kl_fwd_impl(a, scratch, scratch_bytes, stream);
+}
+
+namespace srswa {
+namespace {
+
+int kl_fwd_impl(const srswa_kl_args* a, void* scratch, size_t scratch_bytes, void* stream) {
   if (!a || !a->q_idx || !a->idx_k || !a->q_main || !a->k_main || !a->sel || !a->pos || !a->kl || !a->valid) {
     set_error("gather kl: null argument");
     return SRSWA_INVALID;
@@ -631,6 +1044,14 @@ extern "C" int srswa_gather_kl_fwd(const srswa_kl_args* a, void* stream) {
     return SRSWA_UNSUPPORTED;
   }
   if (a->T == 0 || a->B == 0) return SRSWA_OK;
+  KlRsLayout rl{};
+  if (scratch) {
+    rl = kl_rs_layout(a);
+    if (scratch_bytes < rl.total) {
+      set_error("gather kl: workspace too small (%zu < %zu)", scratch_bytes, rl.total);
+      return SRSWA_WORKSPACE;
+    }
+  }
   KlK k;
   k.a = *a;
   k.ntiles = ceil_div(a->T, kTileRows);
@@ -640,6 +1061,32 @@ extern "C" int srswa_gather_kl_fwd(const srswa_kl_args* a, void* stream) {
   k.KV = a->HQ / a->HKV;
   k.nlogical = a->B * a->HI * k.ntiles;
   k.per_xcd = ceil_div(k.nlogical, 8);
+  k.rs_flag = nullptr;
+  hipStream_t st = reinterpret_cast<hipStream_t>(stream);
+  KlRsK rk{};
+  if (scratch) {
+    // the per-tile decision and the row bitmap first: the tile kernel skips
+    // the tiles the row-sparse kernels take
+    char* base = static_cast<char*>(scratch);
+    rk.a = *a;
+    rk.ntiles = k.ntiles;
+    rk.nblk = nblk;
+    rk.nwords = k.nwords;
+    rk.rwords = ceil_div(a->T, 32);
+    rk.nrange = ceil_div(a->T, kRsRange);
+    rk.G = k.G;
+    rk.KV = k.KV;
+    rk.flag = reinterpret_cast<uint32_t*>(base + rl.flag);
+    rk.rbm = reinterpret_cast<uint32_t*>(base + rl.rbm);
+    rk.srec = reinterpret_cast<float2*>(base + rl.srec);
+    rk.rst = reinterpret_cast<float2*>(base + rl.rst);
+    rk.klp = reinterpret_cast<float*>(base + rl.klp);
+    const int64_t rbm_words = (int64_t)a->B * a->HI * nblk * rk.rwords;
+    hipLaunchKernelGGL(kl_zero_kernel, dim3((unsigned)((rbm_words + 255) / 256)), dim3(256), 0, st, rk.rbm, rbm_words);
+    const size_t flds = ((size_t)k.nwords + 1 + (size_t)kTileRows * a->K) * 4;
+    hipLaunchKernelGGL(kl_rs_flag_kernel, dim3((unsigned)k.nlogical), dim3(256), flds, st, rk);
+    k.rs_flag = rk.flag;
+  }
 
   const int tile_bytes = a->D == 64 ? KlLds<64>::tileBytes : KlLds<128>::tileBytes;
   k.ids_off = tile_bytes;
@@ -652,7 +1099,6 @@ extern "C" int srswa_gather_kl_fwd(const srswa_kl_args* a, void* stream) {
     set_error("gather kl: %zu bytes of LDS needed", lds);
     return SRSWA_UNSUPPORTED;
   }
-  hipStream_t st = reinterpret_cast<hipStream_t>(stream);
   const dim3 grid((unsigned)(8 * k.per_xcd)), block(256);
   static LdsGrant granted[4];
   bool lds_ok = true;
@@ -666,6 +1112,21 @@ extern "C" int srswa_gather_kl_fwd(const srswa_kl_args* a, void* stream) {
   }
 #undef KL_LAUNCH
   if (!lds_ok) return SRSWA_LAUNCH;
+  if (scratch) {
+    const dim3 gp((unsigned)((int64_t)a->B * a->HI * nblk * rk.nrange));
+    const dim3 gr((unsigned)(((int64_t)a->B * a->HI * a->T + 255) / 256));
+#define KL_RS(T_, D_)                                                                   \
+  hipLaunchKernelGGL((kl_rs_pass_kernel<T_, D_, false>), gp, dim3(128), 0, st, rk);    \
+  hipLaunchKernelGGL(kl_rs_combine_kernel, gr, dim3(256), 0, st, rk);                   \
+  hipLaunchKernelGGL((kl_rs_pass_kernel<T_, D_, true>), gp, dim3(128), 0, st, rk);     \
+  hipLaunchKernelGGL(kl_rs_final_kernel, gr, dim3(256), 0, st, rk);
+    if (a->dtype == SRSWA_BF16) {
+      if (a->D == 128) { KL_RS(bf16_t, 128) } else { KL_RS(bf16_t, 64) }
+    } else {
+      if (a->D == 128) { KL_RS(__half, 128) } else { KL_RS(__half, 64) }
+    }
+#undef KL_RS
+  }
   const hipError_t e = hipGetLastError();
   if (e != hipSuccess) {
     set_error("gather kl launch failed: %s", hipGetErrorString(e));
@@ -673,6 +1134,9 @@ extern "C" int srswa_gather_kl_fwd(const srswa_kl_args* a, void* stream) {
   }
   return SRSWA_OK;
 }
+
+}  // namespace
+}  // namespace srswa
 
 extern "C" int srswa_gather_kl_bwd_workspace(const srswa_kl_bwd_args* a, size_t* scratch_bytes) {
   if (!a || !scratch_bytes) {

@@ -477,6 +477,8 @@ SIGNATURES = {
     "srswa_page_block_bounds": (ctypes.c_int, [ctypes.POINTER(BlockBoundsArgs), _vp]),
     "srswa_page_candidate_mask": (ctypes.c_int, [ctypes.POINTER(CandidateArgs), _vp]),
     "srswa_gather_kl_fwd": (ctypes.c_int, [ctypes.POINTER(KlArgs), _vp]),
+    "srswa_gather_kl_fwd_workspace": (ctypes.c_size_t, [ctypes.POINTER(KlArgs)]),
+    "srswa_gather_kl_fwd_ws": (ctypes.c_int, [ctypes.POINTER(KlArgs), _vp, ctypes.c_size_t, _vp]),
     "srswa_gather_kl_bwd_workspace": (ctypes.c_int, [ctypes.POINTER(KlBwdArgs), _szp]),
     "srswa_gather_kl_bwd": (ctypes.c_int, [ctypes.POINTER(KlBwdArgs), _vp, ctypes.c_size_t, _vp]),
 }

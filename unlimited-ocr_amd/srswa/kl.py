@@ -39,8 +39,11 @@ def _keys(idx_k: torch.Tensor) -> torch.Tensor:
 
 
 def kl_forward(q_idx, idx_k, q_main, k_main, sel, pos, *, block_size, local_window, scaling, seg=None,
-               with_dsel=True):
-    """(kl [B, HI, T] fp32, valid [B, HI, T] bool, dsel [B, HI, T, K, 64] fp32 or None)."""
+               with_dsel=True, row_sparse=True):
+    """(kl [B, HI, T] fp32, valid [B, HI, T] bool, dsel [B, HI, T, K, 64] fp32 or None).
+    ``row_sparse``: tiles whose rows select unrelated blocks are computed
+    block-major (srswa_gather_kl_fwd_ws); False runs every tile on the tile
+    kernel (srswa_gather_kl_fwd)."""
     _cuda(q_idx, idx_k, q_main, k_main, sel, pos, seg)
     q_idx, q_main, k_main = _inner(q_idx), _inner(q_main), _inner(k_main)
     ik = _inner(_keys(idx_k))
@@ -70,7 +73,16 @@ def kl_forward(q_idx, idx_k, q_main, k_main, sel, pos, *, block_size, local_wind
         ds_sh=0 if dsel is None else dsel.stride(1), ds_st=0 if dsel is None else dsel.stride(2),
         B=B, HI=HI, HQ=HQ, HKV=HKV, T=T, Sk=Sk, D=D, K=K, block_size=int(block_size),
         local_window=int(local_window), scaling=float(scaling), dtype=_lib.dtype_code(q_idx.dtype))
-    _lib.check(_lib.lib().srswa_gather_kl_fwd(ctypes.byref(a), _lib.stream_ptr(q_idx.device)), "srswa_gather_kl_fwd")
+    # with a workspace, tiles whose rows select unrelated blocks are taken by
+    # the block-major (row-sparse) kernels instead of the tile kernel
+    need = _lib.lib().srswa_gather_kl_fwd_workspace(ctypes.byref(a)) if row_sparse else 0
+    if need == 0:                                    # the tile kernel alone (or an empty batch)
+        _lib.check(_lib.lib().srswa_gather_kl_fwd(ctypes.byref(a), _lib.stream_ptr(q_idx.device)),
+                   "srswa_gather_kl_fwd")
+        return kl, valid, dsel
+    scr = _lib.scratch(q_idx.device, need)
+    _lib.check(_lib.lib().srswa_gather_kl_fwd_ws(ctypes.byref(a), _lib.ptr(scr), need, _lib.stream_ptr(q_idx.device)),
+               "srswa_gather_kl_fwd_ws")
     return kl, valid, dsel
 
 
