@@ -112,11 +112,22 @@ def test_row_sparse_and_tile_paths_agree(dev):
     assert torch.equal(valid, valid_t)
     assert (kl - kl_t).abs().max().item() <= 1e-5 + 1e-5 * kl_t.abs().max().item()
     assert (dsel - dsel_t).abs().max().item() <= 1e-5
-    rk, rv = K.gather_kl_dense(q_idx.double(), idx_k.double(), q_main.double(), k_main.double(), sel, pos,
+    qr = q_idx.double().requires_grad_()
+    kr = idx_k.double().requires_grad_()
+    rk, rv = K.gather_kl_dense(qr, kr, q_main.double(), k_main.double(), sel, pos,
                                block_size=64, local_window=lw, scaling=scaling, seg=None, round_dtype=dtype)
     assert torch.equal(valid.cpu(), rv)
-    err = (kl.cpu().double() - rk).abs() - 1e-3 * rk.abs()
+    err = (kl.cpu().double() - rk.detach()).abs() - 1e-3 * rk.detach().abs()
     assert err.max().item() <= 2e-3, err.max().item()
+    # backward: shared tiles on the tile dQ kernel, the others block-major
+    qd = q_idx.to(dev).requires_grad_()
+    kd = idx_k.to(dev).requires_grad_()
+    klg, vg = KL.gather_kl(qd, kd, q_main.to(dev), k_main.to(dev), sel.to(dev), pos.to(dev), block_size=64,
+                           local_window=lw, scaling=scaling)
+    K.kl_loss(klg, vg).backward()
+    K.kl_loss(rk, rv).backward()
+    assert_close_lowp(qd.grad.cpu(), qr.grad, dtype, what="d q_idx (mixed tiles)")
+    assert_close_lowp(kd.grad.cpu(), kr.grad, dtype, what="d idx_k (mixed tiles)")
 
 
 @pytest.mark.parametrize("case", CASES[:3])

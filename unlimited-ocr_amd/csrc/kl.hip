@@ -351,24 +351,24 @@ __global__ __launch_bounds__(256, 2) void kl_fwd_kernel(KlK p) {
 // Rows that select unrelated blocks (per-row top-k, as the indexer's own
 // selections are) give a 64-row tile a block union near the whole prefix, and
 // the tile kernel would spend most of its work on (row, block) pairs that no
-// row of the pair keeps.  Tiles whose union exceeds 2 K blocks are flagged on
-// the device and taken block-major: for every key block, the rows of flagged
+// row of the pair keeps.  Tiles whose union exceeds K blocks (rows that do not
+// all share one selection) are flagged on the device and taken block-major: for every key block, the rows of flagged
 // tiles that selected it are gathered 64 at a time, so each (row, block) pair
 // is computed once.
 //   kl_rs_flag_kernel    per tile: the union size and the flag; for a flagged
 //                        tile, bit t of block c's row bitmap for every kept
 //                        (row t, block c) pair;
-//   kl_rs_pass_kernel    per (block, 1024-row range), over the same row groups
+//   kl_rs_pass_kernel    per (block, 2048-row range), over the same row groups
 //                        twice: STATS writes each pair's (max, sum) per head,
 //                        MIX (after the combine) mixes the teacher over the
 //                        heads, takes the student's log-softmax and writes the
 //                        pair's KL sum and its dsel row;
-//   kl_rs_combine_kernel per row: the pairs' statistics merged per head in slot
-//                        order, dsel zeroed for slots with nothing kept;
+//   kl_rs_combine_kernel per (row, head): the pairs' statistics merged in slot
+//                        order; dsel zeroed for slots with nothing kept;
 //   kl_rs_final_kernel   per row: the KL as the sum of its pairs in slot order.
 // Every (row, slot) pair writes its own records, so no result depends on how
 // the rows are grouped.
-constexpr int kRsRange = 1024;   // rows per block-major workgroup (32 bitmap words)
+constexpr int kRsRange = 2048;   // rows per block-major workgroup (64 bitmap words, one per lane)
 
 struct KlRsK {
   srswa_kl_args a;
@@ -428,7 +428,7 @@ __global__ __launch_bounds__(256) void kl_rs_flag_kernel(KlRsK p) {
   __syncthreads();
   for (int w = tid; w < p.nwords; w += blockDim.x) atomicAdd(s_cnt, (uint32_t)__popc(s_bits[w]));
   __syncthreads();
-  const bool rs = (int)*s_cnt > 2 * K;
+  const bool rs = (int)*s_cnt > K;
   if (tid == 0) p.flag[(int64_t)bh * p.ntiles + tile] = rs ? 1u : 0u;
   if (!rs) return;
   uint32_t* rb = p.rbm + (int64_t)bh * p.nblk * p.rwords;
@@ -438,7 +438,7 @@ __global__ __launch_bounds__(256) void kl_rs_flag_kernel(KlRsK p) {
   }
 }
 
-// One workgroup per (sequence, index head, block c, 1024-row range), two waves
+// One workgroup per (sequence, index head, block c, 2048-row range), two waves
 // of 32 rows per group of 64 (lane = row, S^T = K Q^T over the block's 64
 // keys as in the tile kernel).  Stage (group, head): K of the head's block
 // staged in LDS, the rows' query fragments in registers, both fetched one
@@ -451,7 +451,7 @@ __global__ __launch_bounds__(128, 2) void kl_rs_pass_kernel(KlRsK p) {
   constexpr int PPT = kChunk * D / 8 / NT;
   constexpr int RPP = NT / (D / 8);
   __shared__ __align__(16) T sK[kChunk * KP];
-  __shared__ int s_rows[kRsRange];
+  __shared__ uint16_t s_rows[kRsRange];             // rows of the range, offsets from its first
   __shared__ int s_n;
   // MIX: the student's log q (log2 units) of the group's rows, [row][key] with
   // a 68-float pitch (conflict-free 16-byte accesses)
@@ -469,9 +469,11 @@ __global__ __launch_bounds__(128, 2) void kl_rs_pass_kernel(KlRsK p) {
 
   // this range's rows of block c, ascending: one bitmap word per lane of wave 0
   const uint32_t* rb = p.rbm + ((int64_t)bh * p.nblk + c) * p.rwords;
+  static_assert(kRsRange == 32 * kWave, "one bitmap word per lane of wave 0");
+  const int r0 = range * kRsRange;
   if (wave == 0) {
     const int w = range * (kRsRange / 32) + lane;
-    const uint32_t bits = (lane < kRsRange / 32 && w < p.rwords) ? rb[w] : 0u;
+    const uint32_t bits = w < p.rwords ? rb[w] : 0u;
     const int cnt = __popc(bits);
     int incl = cnt;
 #pragma unroll
@@ -484,7 +486,7 @@ __global__ __launch_bounds__(128, 2) void kl_rs_pass_kernel(KlRsK p) {
     while (bb) {
       const int bit = __ffs(bb) - 1;
       bb &= bb - 1;
-      s_rows[pos++] = w * 32 + bit;
+      s_rows[pos++] = (uint16_t)(lane * 32 + bit);
     }
     if (lane == kWave - 1) s_n = incl;
   }
@@ -509,9 +511,9 @@ __global__ __launch_bounds__(128, 2) void kl_rs_pass_kernel(KlRsK p) {
   };
   // the row of group g this lane owns, or -1 past the list (it then reads
   // row s_rows[0]'s query and keeps nothing)
-  auto group_row = [&](int g) { const int i = g * kTileRows + row; return i < n ? s_rows[i] : -1; };
+  auto group_row = [&](int g) { const int i = g * kTileRows + row; return i < n ? r0 + (int)s_rows[i] : -1; };
   auto q_row = [&](int hh, int t) -> const T* {
-    const int tt = t >= 0 ? t : s_rows[0];
+    const int tt = t >= 0 ? t : r0 + (int)s_rows[0];
     if (hh == G)
       return reinterpret_cast<const T*>(a.q_idx) + (int64_t)b * a.qi_sb + (int64_t)ih * a.qi_sh + (int64_t)tt * a.qi_st;
     return reinterpret_cast<const T*>(a.q_main) + (int64_t)b * a.qm_sb + (int64_t)(ih * G + hh) * a.qm_sh +
@@ -651,17 +653,21 @@ __global__ __launch_bounds__(128, 2) void kl_rs_pass_kernel(KlRsK p) {
   }
 }
 
-// Per row of a flagged tile: every head's statistics merged over the row's
-// kept slots in slot order; dsel rows of slots with nothing kept zeroed.
+// Per (row, head) of a flagged tile: the head's statistics merged over the
+// row's kept slots in slot order; the head-0 thread also zeroes the dsel rows
+// of slots with nothing kept.
 __global__ __launch_bounds__(256) void kl_rs_combine_kernel(KlRsK p) {
   const srswa_kl_args& a = p.a;
+  const int G1 = p.G + 1;
   const int64_t gid = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-  if (gid >= (int64_t)a.B * a.HI * a.T) return;
-  const int t = (int)(gid % a.T);
-  const int bh = (int)(gid / a.T);
+  if (gid >= (int64_t)a.B * a.HI * a.T * G1) return;
+  const int hh = (int)(gid % G1);
+  const int64_t rowi = gid / G1;                   // (b, ih, t) row index
+  const int t = (int)(rowi % a.T);
+  const int bh = (int)(rowi / a.T);
   const int ih = bh % a.HI, b = bh / a.HI;
   if (!p.flag[(int64_t)bh * p.ntiles + t / kTileRows]) return;
-  const int K = a.K, G = p.G;
+  const int K = a.K;
   int lo, hi;
   kl_row_range(a, b, t, lo, hi);
   const int32_t* ids = kl_row_ids(a, b, ih, t);
@@ -669,27 +675,25 @@ __global__ __launch_bounds__(256) void kl_rs_combine_kernel(KlRsK p) {
   for (int s = 0; s < K; ++s) {
     if (kl_slot_block(ids, s, lo, hi) >= 0) {
       live |= 1ull << s;
-    } else if (a.dsel) {
+    } else if (hh == 0 && a.dsel) {
       float4* z = reinterpret_cast<float4*>(a.dsel + (int64_t)b * a.ds_sb + (int64_t)ih * a.ds_sh +
                                             (int64_t)t * a.ds_st + (int64_t)s * kChunk);
 #pragma unroll
       for (int i = 0; i < kChunk / 4; ++i) z[i] = make_float4(0.f, 0.f, 0.f, 0.f);
     }
   }
-  const float2* rec = p.srec + gid * K * (G + 1);
-  for (int hh = 0; hh <= G; ++hh) {
-    float mm = -INFINITY;
+  const float2* rec = p.srec + rowi * K * G1 + hh;
+  float mm = -INFINITY;
+  for (int s = 0; s < K; ++s)
+    if ((live >> s) & 1ull) mm = fmaxf(mm, rec[s * G1].x);
+  float ll = 0.f;
+  if (mm > -INFINITY)
     for (int s = 0; s < K; ++s)
-      if ((live >> s) & 1ull) mm = fmaxf(mm, rec[s * (G + 1) + hh].x);
-    float ll = 0.f;
-    if (mm > -INFINITY)
-      for (int s = 0; s < K; ++s)
-        if ((live >> s) & 1ull) {
-          const float2 v = rec[s * (G + 1) + hh];
-          if (v.x > -INFINITY) ll += v.y * __builtin_amdgcn_exp2f(v.x - mm);
-        }
-    p.rst[gid * (G + 1) + hh] = make_float2(mm, ll);
-  }
+      if ((live >> s) & 1ull) {
+        const float2 v = rec[s * G1];                // a second read, from cache
+        if (v.x > -INFINITY) ll += v.y * __builtin_amdgcn_exp2f(v.x - mm);
+      }
+  p.rst[rowi * G1 + hh] = make_float2(mm, ll);
 }
 
 // Per row of a flagged tile: kl = the sum of its pairs' KL sums in slot order.
@@ -713,13 +717,20 @@ __global__ __launch_bounds__(256) void kl_rs_final_kernel(KlRsK p) {
 }
 
 // -------------------------------------------------------------- backward
-// Both kernels are tile products on the matrix cores with ds = rnd(g * dsel)
-// (the reference's bf16 gradient of the logits) staged in LDS:
-//   dq_kernel: per (sequence, index head, 64-row tile), over the tile's
-//              selected blocks: dQ[rows, d] += DS[rows, keys] K[keys, d];
-//   dk_kernel: per (sequence, block), over the 64-row tiles that selected it
-//              (a touch bitmap that dq_kernel sets; ascending: deterministic):
-//              dK[keys, d] += DS^T[keys, rows] Q[rows, d].
+// Tile products on the matrix cores with ds = rnd(g * dsel) (the reference's
+// bf16 gradient of the logits) staged in LDS.  kl_bwd_flag_kernel first
+// marks, per 64-row tile, whether its rows' selected blocks form a union of
+// more than K blocks (rows that do not share one selection) and fills two row
+// bitmaps per block: every row that selected it, and those of flagged tiles.
+//   dq_kernel:    per (sequence, index head, 64-row tile) not flagged, over
+//                 the tile's selected blocks: dQ[rows, d] += DS[rows, keys] K[keys, d];
+//   rs_dq_kernel: per (sequence, index head, block, 2048-row range), the
+//                 flagged rows that selected the block, 64 at a time: each
+//                 (row, slot) pair's product DS K written as an fp32 partial,
+//                 then summed per row in slot order (rs_dq_reduce_kernel);
+//   dk_kernel:    per (sequence, block), every row that selected it in
+//                 ascending order, 64 at a time (deterministic):
+//                 dK[keys, d] += DS^T[keys, rows] Q[rows, d].
 // Four waves; wave w owns output tiles (w / TPW halves of 32 rows / keys,
 // 32-wide head-dim slices); K and Q rows are read as B operands with
 // ds_read_b64_tr_b16 from their natural layout.
@@ -727,8 +738,11 @@ constexpr int kBwdThreads = 256;
 
 struct KlBwdK {
   srswa_kl_bwd_args a;
-  int ntiles, nblk, twords;
-  uint32_t* touch;          // [B, HI, nblk, twords]
+  int ntiles, nblk, nwords, rwords, nrange;
+  uint32_t* flag;           // [B, HI, ntiles]: rows of the tile taken by rs_dq_kernel
+  uint32_t* rbm;            // [B, HI, nblk, rwords] rows of flagged tiles per block
+  uint32_t* rbm_all;        // [B, HI, nblk, rwords] every row per block
+  float* dqp;               // [B, HI, T, K, D] per (row, slot): dQ partial of a flagged row
 };
 
 template <int D> struct KlBwdLds {
@@ -828,11 +842,12 @@ __global__ __launch_bounds__(kBwdThreads) void kl_dq_kernel(KlBwdK p) {
   const int tid = threadIdx.x, wave = tid / kWave, lane = tid % kWave;
   const int tile = blockIdx.x % p.ntiles;
   const int bh = blockIdx.x / p.ntiles;
+  if (p.flag[(int64_t)bh * p.ntiles + tile]) return;   // rs_dq_kernel takes the tile's rows
   const int ih = bh % a.HI, b = bh / a.HI;
   const int t0 = tile * kTileRows;
   const int nrows = min(kTileRows, a.T - t0);
   // the tile's selected blocks (rows with a nonzero gradient)
-  const int nwords = (p.nblk + 31) / 32;
+  const int nwords = p.nwords;
   for (int w = tid; w < nwords; w += kBwdThreads) s_bits[w] = 0u;
   __syncthreads();
   for (int e = tid; e < nrows * a.K; e += kBwdThreads) {
@@ -842,9 +857,6 @@ __global__ __launch_bounds__(kBwdThreads) void kl_dq_kernel(KlBwdK p) {
   }
   __syncthreads();
   const int U = compact_bitmap(s_bits, nwords, s_chunks, &s_count);
-  // this tile touches these blocks: one bit per (block, tile) for dk_kernel
-  for (int u = tid; u < U; u += kBwdThreads)
-    atomicOr(&p.touch[(((int64_t)b * a.HI + ih) * p.nblk + s_chunks[u]) * p.twords + (tile >> 5)], 1u << (tile & 31));
 
   f32x16_t acc[TPW];
 #pragma unroll
@@ -885,14 +897,199 @@ __global__ __launch_bounds__(kBwdThreads) void kl_dq_kernel(KlBwdK p) {
                     a.dq_st, nrows, acc, wave, lane);
 }
 
+// Rows of one 2048-row window of a block's row bitmap, ascending, as offsets
+// from the window's first row (wave 0: one word per lane); returns the count.
+__device__ __forceinline__ int window_rows(const uint32_t* words, int w0, int rwords, uint16_t* s_rows, int* s_n) {
+  const int tid = threadIdx.x, lane = tid % kWave;
+  if (tid < kWave) {
+    const int w = w0 + lane;
+    const uint32_t bits = w < rwords ? words[w] : 0u;
+    const int cnt = __popc(bits);
+    int incl = cnt;
+#pragma unroll
+    for (int o = 1; o < kWave; o <<= 1) {
+      const int v = __shfl_up(incl, o, kWave);
+      if (lane >= o) incl += v;
+    }
+    int pos = incl - cnt;
+    uint32_t bb = bits;
+    while (bb) {
+      const int bit = __ffs(bb) - 1;
+      bb &= bb - 1;
+      s_rows[pos++] = (uint16_t)(lane * 32 + bit);
+    }
+    if (lane == kWave - 1) *s_n = incl;
+  }
+  __syncthreads();
+  return *s_n;
+}
+
+// Per (sequence, index head, 64-row tile): the union of the rows' selected
+// blocks (0 <= id < nblk, an id's first slot) and the flag; a bit per (block,
+// row) pair in the all-rows bitmap, and in the flagged-rows bitmap for a
+// flagged tile.
+__global__ __launch_bounds__(256) void kl_bwd_flag_kernel(KlBwdK p) {
+  extern __shared__ uint32_t s_u[];                    // [nwords] union bits, [1] count, [64 K] ids
+  const srswa_kl_bwd_args& a = p.a;
+  const int tile = (int)(blockIdx.x % p.ntiles);
+  const int bh = (int)(blockIdx.x / p.ntiles);
+  const int ih = bh % a.HI, b = bh / a.HI;
+  const int t0 = tile * kTileRows, nrows = min(kTileRows, a.T - t0);
+  const int K = a.K, tid = threadIdx.x;
+  uint32_t* s_bits = s_u;
+  uint32_t* s_cnt = s_u + p.nwords;
+  int* s_ids = reinterpret_cast<int*>(s_u + p.nwords + 1);
+  for (int w = tid; w <= p.nwords; w += blockDim.x) s_u[w] = 0u;
+  __syncthreads();
+  for (int e = tid; e < kTileRows * K; e += blockDim.x) {
+    const int r = e / K, s = e % K;
+    int id = -1;
+    if (r < nrows) {
+      const int32_t* ids = a.sel + (int64_t)b * a.sel_sb + (int64_t)ih * a.sel_sh + (int64_t)(t0 + r) * a.sel_st;
+      id = ids[s];
+      if (id < 0 || id >= p.nblk) id = -1;
+      for (int s2 = 0; s2 < s && id >= 0; ++s2)
+        if (ids[s2] == id) id = -1;
+      if (id >= 0) atomicOr(&s_bits[id >> 5], 1u << (id & 31));
+    }
+    s_ids[e] = id;
+  }
+  __syncthreads();
+  for (int w = tid; w < p.nwords; w += blockDim.x) atomicAdd(s_cnt, (uint32_t)__popc(s_bits[w]));
+  __syncthreads();
+  const bool rs = (int)*s_cnt > K;
+  if (tid == 0) p.flag[(int64_t)bh * p.ntiles + tile] = rs ? 1u : 0u;
+  const int64_t base = (int64_t)bh * p.nblk * p.rwords;
+  for (int e = tid; e < nrows * K; e += blockDim.x) {
+    const int id = s_ids[e], t = t0 + e / K;
+    if (id < 0) continue;
+    const int64_t w = base + (int64_t)id * p.rwords + (t >> 5);
+    atomicOr(&p.rbm_all[w], 1u << (t & 31));
+    if (rs) atomicOr(&p.rbm[w], 1u << (t & 31));
+  }
+}
+
+// Per (sequence, index head, block c, 2048-row range): the flagged rows that
+// selected c, 64 at a time; each (row, slot) pair's dQ partial DS K, fp32.
+template <typename T, int D>
+__global__ __launch_bounds__(kBwdThreads) void kl_rs_dq_kernel(KlBwdK p) {
+  using M = Mfma<T>;
+  using L = KlBwdLds<D>;
+  constexpr int XP = L::XP, SP = L::SP, MT = D / 32, TPW = 2 * MT / 4;
+  extern __shared__ __align__(16) unsigned char smem[];
+  T* sK = reinterpret_cast<T*>(smem);
+  T* sDS = reinterpret_cast<T*>(smem + L::dsOff);
+  __shared__ uint16_t s_rows[kRsRange];
+  __shared__ int s_n, s_t[kTileRows], s_slot[kTileRows];
+  const srswa_kl_bwd_args& a = p.a;
+  const int tid = threadIdx.x, wave = tid / kWave, lane = tid % kWave;
+  const int range = (int)(blockIdx.x % p.nrange);
+  const int c = (int)((blockIdx.x / p.nrange) % p.nblk);
+  const int bh = (int)(blockIdx.x / ((int64_t)p.nrange * p.nblk));
+  const int ih = bh % a.HI, b = bh / a.HI;
+  const int r0 = range * kRsRange;
+  const int n = window_rows(p.rbm + ((int64_t)bh * p.nblk + c) * p.rwords, range * (kRsRange / 32), p.rwords,
+                            s_rows, &s_n);
+  if (n == 0) return;
+  stage_rows<T, D>(sK, reinterpret_cast<const T*>(a.idx_k) + (int64_t)b * a.ik_sb + (int64_t)c * kChunk * a.ik_st,
+                   a.ik_st, min(kChunk, a.Sk - c * kChunk));
+  const uint16_t* k16 = reinterpret_cast<const uint16_t*>(sK);
+  const int rr = tid / 4, kq = (tid % 4) * 16;    // DS staging: row, 16-key quarter
+  for (int g0 = 0; g0 < n; g0 += kTileRows) {
+    __syncthreads();                              // the previous group's DS consumed
+    {
+      const int i = g0 + rr;
+      const int t = i < n ? r0 + (int)s_rows[i] : -1;
+      const int slot = t >= 0 ? find_slot(a, b, ih, t, c) : -1;
+      if (kq == 0) {
+        s_t[rr] = t;
+        s_slot[rr] = slot;
+      }
+      float v[16];
+      ds16<T>(a, b, ih, t, slot, kq, v);
+      uint4 w0, w1;                               // keys in the transposing read's order (slot_of_key)
+      w0 = make_uint4(M::pack2(v[0], v[1]), M::pack2(v[2], v[3]), M::pack2(v[8], v[9]), M::pack2(v[10], v[11]));
+      w1 = make_uint4(M::pack2(v[4], v[5]), M::pack2(v[6], v[7]), M::pack2(v[12], v[13]), M::pack2(v[14], v[15]));
+      *reinterpret_cast<uint4*>(sDS + rr * SP + kq) = w0;
+      *reinterpret_cast<uint4*>(sDS + rr * SP + kq + 8) = w1;
+    }
+    __syncthreads();
+    f32x16_t acc[TPW];
+#pragma unroll
+    for (int i = 0; i < TPW; ++i) acc[i] = zero16();
+#pragma unroll
+    for (int ks = 0; ks < 4; ++ks) {
+#pragma unroll
+      for (int i = 0; i < TPW; ++i) {
+        const int tix = wave * TPW + i;
+        const int half = tix / MT, dt = tix % MT;
+        const uint4 av = *reinterpret_cast<const uint4*>(sDS + (32 * half + (lane & 31)) * SP + 16 * ks + 8 * (lane >> 5));
+        acc[i] = M::mac(av, a_operand_tr<XP>(k16, 16 * ks, 32 * dt, lane), acc[i]);
+      }
+    }
+    // row m of output tile (half, dt): 32 half + 8 (r / 4) + 4 (lane / 32) + r % 4
+#pragma unroll
+    for (int i = 0; i < TPW; ++i) {
+      const int tix = wave * TPW + i;
+      const int half = tix / MT, dt = tix % MT;
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        const int m = 32 * half + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3);
+        const int t = s_t[m];
+        if (t >= 0)
+          p.dqp[(((int64_t)bh * a.T + t) * a.K + s_slot[m]) * D + 32 * dt + (lane & 31)] = acc[i][r];
+      }
+    }
+  }
+}
+
+// dQ of a flagged row: its pairs' partials summed in slot order (an id's
+// first slot, 0 <= id < nblk), rounded once to the input dtype; four head
+// dims per thread.
+template <typename T, int D>
+__global__ __launch_bounds__(256) void kl_rs_dq_reduce_kernel(KlBwdK p) {
+  const srswa_kl_bwd_args& a = p.a;
+  const int64_t gid = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (gid >= (int64_t)a.B * a.HI * a.T * (D / 4)) return;
+  const int d = (int)(gid % (D / 4)) * 4;
+  const int64_t rowi = gid / (D / 4);
+  const int t = (int)(rowi % a.T);
+  const int bh = (int)(rowi / a.T);
+  const int ih = bh % a.HI, b = bh / a.HI;
+  if (!p.flag[(int64_t)bh * p.ntiles + t / kTileRows]) return;
+  const int32_t* ids = a.sel + (int64_t)b * a.sel_sb + (int64_t)ih * a.sel_sh + (int64_t)t * a.sel_st;
+  float4 acc = make_float4(0.f, 0.f, 0.f, 0.f);
+  for (int s = 0; s < a.K; ++s) {
+    int id = ids[s];
+    if (id < 0 || id >= p.nblk) continue;
+    bool first = true;
+    for (int s2 = 0; s2 < s; ++s2) first = first && ids[s2] != id;
+    if (first) {
+      const float4 v = *reinterpret_cast<const float4*>(p.dqp + (rowi * a.K + s) * D + d);
+      acc.x += v.x;
+      acc.y += v.y;
+      acc.z += v.z;
+      acc.w += v.w;
+    }
+  }
+  uint2 w;
+  w.x = Mfma<T>::pack2(acc.x, acc.y);
+  w.y = Mfma<T>::pack2(acc.z, acc.w);
+  *reinterpret_cast<uint2*>(reinterpret_cast<T*>(a.dq_idx) + (int64_t)b * a.dq_sb + (int64_t)ih * a.dq_sh +
+                            (int64_t)t * a.dq_st + d) = w;
+}
+
 template <typename T, int D>
 __global__ __launch_bounds__(kBwdThreads) void kl_dk_kernel(KlBwdK p) {
   using M = Mfma<T>;
   using L = KlBwdLds<D>;
   constexpr int XP = L::XP, SP = L::SP, MT = D / 32, TPW = 2 * MT / 4;
+  constexpr int PR = D / 8;                         // 16-byte pieces per Q row
   extern __shared__ __align__(16) unsigned char smem[];
   T* sQ = reinterpret_cast<T*>(smem);
   T* sDT = reinterpret_cast<T*>(smem + L::dsOff);   // DS^T [key][row]
+  __shared__ uint16_t s_rows[kRsRange];
+  __shared__ int s_n;
   const srswa_kl_bwd_args& a = p.a;
   const int tid = threadIdx.x, wave = tid / kWave, lane = tid % kWave;
   const int c = blockIdx.x % p.nblk, b = blockIdx.x / p.nblk;
@@ -902,26 +1099,32 @@ __global__ __launch_bounds__(kBwdThreads) void kl_dk_kernel(KlBwdK p) {
   const uint16_t* q16 = reinterpret_cast<const uint16_t*>(sQ);
   const int rr = tid / 4, kq = (tid % 4) * 16;
   for (int ih = 0; ih < a.HI; ++ih) {
-    const uint32_t* tb = p.touch + (((int64_t)b * a.HI + ih) * p.nblk + c) * p.twords;
-    for (int wd = 0; wd < p.twords; ++wd) {
-      uint32_t bits = tb[wd];
-      while (bits) {
-        const int tile = 32 * wd + __ffs(bits) - 1;
-        bits &= bits - 1;
-        const int t0 = tile * kTileRows;
-        const int nrows = min(kTileRows, a.T - t0);
+    const uint32_t* words = p.rbm_all + (((int64_t)b * a.HI + ih) * p.nblk + c) * p.rwords;
+    const T* qbase = reinterpret_cast<const T*>(a.q_idx) + (int64_t)b * a.qi_sb + (int64_t)ih * a.qi_sh;
+    for (int w0 = 0; w0 < p.rwords; w0 += kRsRange / 32) {
+      __syncthreads();                              // the previous window's list consumed
+      const int n = window_rows(words, w0, p.rwords, s_rows, &s_n);
+      const int r0 = w0 * 32;
+      for (int g0 = 0; g0 < n; g0 += kTileRows) {
         __syncthreads();
-        stage_rows<T, D>(sQ, reinterpret_cast<const T*>(a.q_idx) + (int64_t)b * a.qi_sb + (int64_t)ih * a.qi_sh +
-                                 (int64_t)t0 * a.qi_st,
-                         a.qi_st, nrows);
+        // the group's Q rows (gathered) and DS^T
+        for (int e = tid; e < kTileRows * PR; e += kBwdThreads) {
+          const int r = e / PR, cc = (e % PR) * 8;
+          const int i = g0 + r;
+          const uint4 v = i < n ? *reinterpret_cast<const uint4*>(qbase + (int64_t)(r0 + s_rows[i]) * a.qi_st + cc)
+                                : make_uint4(0, 0, 0, 0);
+          *reinterpret_cast<uint4*>(sQ + r * XP + cc) = v;
+        }
         {
+          const int i = g0 + rr;
+          const int t = i < n ? r0 + (int)s_rows[i] : -1;
+          const int slot = t >= 0 ? find_slot(a, b, ih, t, c) : -1;
           float v[16];
-          const int slot = rr < nrows ? find_slot(a, b, ih, t0 + rr, c) : -1;
-          ds16<T>(a, b, ih, t0 + rr, slot, kq, v);
+          ds16<T>(a, b, ih, t, slot, kq, v);
 #pragma unroll
-          for (int i = 0; i < 16; ++i)   // rows in the transposing read's order (slot_of_key)
-            reinterpret_cast<uint16_t*>(sDT)[(kq + i) * SP + slot_of_key(rr)] =
-                (uint16_t)(M::pack2(v[i], 0.f) & 0xffffu);
+          for (int k = 0; k < 16; ++k)   // rows in the transposing read's order (slot_of_key)
+            reinterpret_cast<uint16_t*>(sDT)[(kq + k) * SP + slot_of_key(rr)] =
+                (uint16_t)(M::pack2(v[k], 0.f) & 0xffffu);
         }
         __syncthreads();
         // dK[key, d] += DS^T[key, row] Q[row, d]
@@ -1115,9 +1318,10 @@ int kl_fwd_impl(const srswa_kl_args* a, void* scratch, size_t scratch_bytes, voi
   if (scratch) {
     const dim3 gp((unsigned)((int64_t)a->B * a->HI * nblk * rk.nrange));
     const dim3 gr((unsigned)(((int64_t)a->B * a->HI * a->T + 255) / 256));
+    const dim3 gc((unsigned)(((int64_t)a->B * a->HI * a->T * (k.G + 1) + 255) / 256));
 #define KL_RS(T_, D_)                                                                   \
   hipLaunchKernelGGL((kl_rs_pass_kernel<T_, D_, false>), gp, dim3(128), 0, st, rk);    \
-  hipLaunchKernelGGL(kl_rs_combine_kernel, gr, dim3(256), 0, st, rk);                   \
+  hipLaunchKernelGGL(kl_rs_combine_kernel, gc, dim3(256), 0, st, rk);                   \
   hipLaunchKernelGGL((kl_rs_pass_kernel<T_, D_, true>), gp, dim3(128), 0, st, rk);     \
   hipLaunchKernelGGL(kl_rs_final_kernel, gr, dim3(256), 0, st, rk);
     if (a->dtype == SRSWA_BF16) {
@@ -1138,13 +1342,33 @@ int kl_fwd_impl(const srswa_kl_args* a, void* scratch, size_t scratch_bytes, voi
 }  // namespace
 }  // namespace srswa
 
+namespace srswa {
+namespace {
+// Backward workspace, in 256-byte aligned pieces.
+struct KlBwdLayout {
+  size_t flag, rbm, rbm_all, dqp, total;
+};
+KlBwdLayout kl_bwd_layout(const srswa_kl_bwd_args* a) {
+  auto al = [](size_t n) { return (n + 255) / 256 * 256; };
+  const int64_t bh = (int64_t)std::max(a->B, 0) * std::max(a->HI, 0), T = std::max(a->T, 0);
+  const int64_t ntiles = ceil_div(T, kTileRows), nblk = ceil_div(std::max(a->Sk, 0), kChunk), rwords = ceil_div(T, 32);
+  KlBwdLayout L{};
+  L.flag = 0;
+  L.rbm = L.flag + al((size_t)(bh * ntiles) * 4);
+  L.rbm_all = L.rbm + al((size_t)(bh * nblk * rwords) * 4);
+  L.dqp = L.rbm_all + al((size_t)(bh * nblk * rwords) * 4);
+  L.total = L.dqp + al((size_t)(bh * T * std::max(a->K, 0) * std::max(a->D, 0)) * 4);
+  return L;
+}
+}  // namespace
+}  // namespace srswa
+
 extern "C" int srswa_gather_kl_bwd_workspace(const srswa_kl_bwd_args* a, size_t* scratch_bytes) {
   if (!a || !scratch_bytes) {
     set_error("gather kl backward workspace: null argument");
     return SRSWA_INVALID;
   }
-  const int64_t words = (int64_t)a->B * a->HI * ceil_div(a->Sk, kChunk) * ceil_div(ceil_div(a->T, kTileRows), 32);
-  *scratch_bytes = (size_t)std::max<int64_t>(words, 0) * 4;
+  *scratch_bytes = kl_bwd_layout(a).total;
   return SRSWA_OK;
 }
 
@@ -1159,8 +1383,9 @@ extern "C" int srswa_gather_kl_bwd(const srswa_kl_bwd_args* a, void* scratch, si
   }
   int rc = check_common(a->dtype, a->D, a->block_size, a->K, "gather kl backward");
   if (rc != SRSWA_OK) return rc;
-  bool ok = al16(a->q_idx) && al16(a->idx_k) && al16(a->dsel);
+  bool ok = al16(a->q_idx) && al16(a->idx_k) && al16(a->dsel) && ((uintptr_t)a->dq_idx & 7u) == 0;
   for (int64_t st : {a->qi_sb, a->qi_sh, a->qi_st, a->ik_sb, a->ik_st}) ok = ok && (st * 2) % 16 == 0;
+  for (int64_t st : {a->dq_sb, a->dq_sh, a->dq_st}) ok = ok && (st * 2) % 8 == 0;   // 4-element dQ stores
   ok = ok && (a->ds_sb * 4) % 16 == 0 && (a->ds_sh * 4) % 16 == 0 && (a->ds_st * 4) % 16 == 0;
   if (!ok) {
     set_error("gather kl backward: rows must be 16-byte aligned");
@@ -1177,19 +1402,33 @@ extern "C" int srswa_gather_kl_bwd(const srswa_kl_bwd_args* a, void* scratch, si
     set_error("gather kl backward: workspace too small (%zu < %zu)", scratch_bytes, need);
     return SRSWA_WORKSPACE;
   }
+  const KlBwdLayout bl = kl_bwd_layout(a);
+  char* base = static_cast<char*>(scratch);
   KlBwdK k;
   k.a = *a;
   k.ntiles = ceil_div(a->T, kTileRows);
   k.nblk = ceil_div(a->Sk, kChunk);
-  k.twords = ceil_div(k.ntiles, 32);
-  k.touch = static_cast<uint32_t*>(scratch);
+  k.nwords = ceil_div(k.nblk, 32);
+  k.rwords = ceil_div(a->T, 32);
+  k.nrange = ceil_div(a->T, kRsRange);
+  k.flag = reinterpret_cast<uint32_t*>(base + bl.flag);
+  k.rbm = reinterpret_cast<uint32_t*>(base + bl.rbm);
+  k.rbm_all = reinterpret_cast<uint32_t*>(base + bl.rbm_all);
+  k.dqp = reinterpret_cast<float*>(base + bl.dqp);
   hipStream_t st = reinterpret_cast<hipStream_t>(stream);
-  const int64_t words = (int64_t)need / 4;
-  hipLaunchKernelGGL(kl_zero_kernel, dim3((unsigned)((words + 255) / 256)), dim3(256), 0, st, k.touch, words);
-  const dim3 gdq((unsigned)((int64_t)a->B * a->HI * k.ntiles)), gdk((unsigned)((int64_t)a->B * k.nblk));
+  const int64_t words = (int64_t)(bl.dqp - bl.rbm) / 4;       // both row bitmaps
+  hipLaunchKernelGGL(kl_zero_kernel, dim3((unsigned)((words + 255) / 256)), dim3(256), 0, st, k.rbm, words);
+  const int64_t ntl = (int64_t)a->B * a->HI * k.ntiles;
+  const size_t flds = ((size_t)k.nwords + 1 + (size_t)kTileRows * a->K) * 4;
+  hipLaunchKernelGGL(kl_bwd_flag_kernel, dim3((unsigned)ntl), dim3(256), flds, st, k);
+  const dim3 gdq((unsigned)ntl), gdk((unsigned)((int64_t)a->B * k.nblk));
+  const dim3 grs((unsigned)((int64_t)a->B * a->HI * k.nblk * k.nrange));
+  const dim3 grd((unsigned)(((int64_t)a->B * a->HI * a->T * (a->D / 4) + 255) / 256));
   const size_t lds = a->D == 128 ? KlBwdLds<128>::bytes : KlBwdLds<64>::bytes;
 #define KL_BWD(T_, D_)                                                                      \
   hipLaunchKernelGGL((kl_dq_kernel<T_, D_>), gdq, dim3(kBwdThreads), lds, st, k);          \
+  hipLaunchKernelGGL((kl_rs_dq_kernel<T_, D_>), grs, dim3(kBwdThreads), lds, st, k);       \
+  hipLaunchKernelGGL((kl_rs_dq_reduce_kernel<T_, D_>), grd, dim3(256), 0, st, k);          \
   hipLaunchKernelGGL((kl_dk_kernel<T_, D_>), gdk, dim3(kBwdThreads), lds, st, k);
   if (a->dtype == SRSWA_BF16) {
     if (a->D == 128) { KL_BWD(bf16_t, 128) } else { KL_BWD(bf16_t, 64) }
