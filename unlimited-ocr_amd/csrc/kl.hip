@@ -358,7 +358,7 @@ __global__ __launch_bounds__(256, 2) void kl_fwd_kernel(KlK p) {
 //   kl_rs_flag_kernel    per tile: the union size and the flag; for a flagged
 //                        tile, bit t of block c's row bitmap for every kept
 //                        (row t, block c) pair;
-//   kl_rs_pass_kernel    per (block, 2048-row range), over the same row groups
+//   kl_rs_pass_kernel    per (block, 2048-row window), over the same row groups
 //                        twice: STATS writes each pair's (max, sum) per head,
 //                        MIX (after the combine) mixes the teacher over the
 //                        heads, takes the student's log-softmax and writes the
@@ -368,7 +368,8 @@ __global__ __launch_bounds__(256, 2) void kl_fwd_kernel(KlK p) {
 //   kl_rs_final_kernel   per row: the KL as the sum of its pairs in slot order.
 // Every (row, slot) pair writes its own records, so no result depends on how
 // the rows are grouped.
-constexpr int kRsRange = 2048;   // rows per block-major workgroup (64 bitmap words, one per lane)
+constexpr int kRsRange = 2048;   // row window of a block-major workgroup (64 bitmap words)
+constexpr int kRsWin = 2048;     // rows per window of the dK scan (64 bitmap words)
 
 struct KlRsK {
   srswa_kl_args a;
@@ -401,8 +402,63 @@ __device__ __forceinline__ const int32_t* kl_row_ids(const srswa_kl_args& a, int
   return a.sel + (int64_t)b * a.sel_sb + (int64_t)ih * a.sel_sh + (int64_t)t * a.sel_st;
 }
 
+// Rows of one window of NW bitmap words (32 NW rows) of a block's row bitmap,
+// ascending, as offsets from the window's first row (lanes < NW of wave 0 one
+// word each); returns the count.  Every thread of the workgroup calls it.
+template <int NW>
+__device__ __forceinline__ int window_rows(const uint32_t* words, int w0, int rwords, uint16_t* s_rows, int* s_n) {
+  static_assert(NW <= kWave, "one word per lane of wave 0");
+  const int tid = threadIdx.x, lane = tid % kWave;
+  if (tid < kWave) {
+    const int w = w0 + lane;
+    const uint32_t bits = (lane < NW && w < rwords) ? words[w] : 0u;
+    const int cnt = __popc(bits);
+    int incl = cnt;
+#pragma unroll
+    for (int o = 1; o < kWave; o <<= 1) {
+      const int v = __shfl_up(incl, o, kWave);
+      if (lane >= o) incl += v;
+    }
+    int pos = incl - cnt;
+    uint32_t bb = bits;
+    while (bb) {
+      const int bit = __ffs(bb) - 1;
+      bb &= bb - 1;
+      s_rows[pos++] = (uint16_t)(lane * 32 + bit);
+    }
+    if (lane == kWave - 1) *s_n = incl;
+  }
+  __syncthreads();
+  return *s_n;
+}
+
+// Bits of a 64-row tile's (block, row) pairs into row bitmaps: per block of the
+// tile's union (s_chunks, U entries), one wave ballots the rows whose kept ids
+// (s_ids, -1 = none) include it and ORs the two 32-row words once.
+__device__ __forceinline__ void tile_row_bits(const int* s_ids, int K, int nrows, const uint16_t* s_chunks, int U,
+                                              uint32_t* bm0, uint32_t* bm1, int rwords, int tile) {
+  const int wave = threadIdx.x / kWave, lane = threadIdx.x % kWave, nw = blockDim.x / kWave;
+  for (int u = wave; u < U; u += nw) {
+    const int c = s_chunks[u];
+    bool mine = false;
+    if (lane < nrows)
+      for (int s = 0; s < K; ++s) mine = mine || s_ids[lane * K + s] == c;
+    const uint64_t m = __ballot(mine);
+    if (lane < 2) {
+      const uint32_t w = (uint32_t)(m >> (32 * lane));
+      const int64_t at = (int64_t)c * rwords + 2 * tile + lane;
+      if (w && 2 * tile + lane < rwords) {
+        atomicOr(&bm0[at], w);
+        if (bm1) atomicOr(&bm1[at], w);
+      }
+    }
+  }
+}
+
 __global__ __launch_bounds__(256) void kl_rs_flag_kernel(KlRsK p) {
-  extern __shared__ uint32_t s_u[];                    // [nwords] union bits, [1] count, [64 K] ids
+  // LDS: [nwords] union bits, [1] count, [64 K] kept ids, [1] list length,
+  // then the union as a block list
+  extern __shared__ uint32_t s_u[];
   const srswa_kl_args& a = p.a;
   const int tile = (int)(blockIdx.x % p.ntiles);
   const int bh = (int)(blockIdx.x / p.ntiles);
@@ -412,6 +468,8 @@ __global__ __launch_bounds__(256) void kl_rs_flag_kernel(KlRsK p) {
   uint32_t* s_bits = s_u;
   uint32_t* s_cnt = s_u + p.nwords;
   int* s_ids = reinterpret_cast<int*>(s_u + p.nwords + 1);
+  int* s_len = s_ids + kTileRows * K;
+  uint16_t* s_chunks = reinterpret_cast<uint16_t*>(s_len + 1);
   for (int w = tid; w <= p.nwords; w += blockDim.x) s_u[w] = 0u;
   __syncthreads();
   for (int e = tid; e < kTileRows * K; e += blockDim.x) {
@@ -430,15 +488,13 @@ __global__ __launch_bounds__(256) void kl_rs_flag_kernel(KlRsK p) {
   __syncthreads();
   const bool rs = (int)*s_cnt > K;
   if (tid == 0) p.flag[(int64_t)bh * p.ntiles + tile] = rs ? 1u : 0u;
-  if (!rs) return;
-  uint32_t* rb = p.rbm + (int64_t)bh * p.nblk * p.rwords;
-  for (int e = tid; e < nrows * K; e += blockDim.x) {
-    const int id = s_ids[e], t = t0 + e / K;
-    if (id >= 0) atomicOr(&rb[(int64_t)id * p.rwords + (t >> 5)], 1u << (t & 31));
-  }
+  if (!rs) return;                                    // uniform: no barrier below is skipped by part of the group
+  const int U = compact_bitmap(s_bits, p.nwords, s_chunks, s_len);
+  tile_row_bits(s_ids, K, nrows, s_chunks, U, p.rbm + (int64_t)bh * p.nblk * p.rwords, nullptr, p.rwords, tile);
 }
 
-// One workgroup per (sequence, index head, block c, 2048-row range), two waves
+// One workgroup per (sequence, index head, block c, 2048-row window): the
+// window's rows that selected c, ascending, two waves
 // of 32 rows per group of 64 (lane = row, S^T = K Q^T over the block's 64
 // keys as in the tile kernel).  Stage (group, head): K of the head's block
 // staged in LDS, the rows' query fragments in registers, both fetched one
@@ -451,7 +507,7 @@ __global__ __launch_bounds__(128, 2) void kl_rs_pass_kernel(KlRsK p) {
   constexpr int PPT = kChunk * D / 8 / NT;
   constexpr int RPP = NT / (D / 8);
   __shared__ __align__(16) T sK[kChunk * KP];
-  __shared__ uint16_t s_rows[kRsRange];             // rows of the range, offsets from its first
+  __shared__ uint16_t s_rows[kRsRange];             // the window's rows of block c, offsets from its first
   __shared__ int s_n;
   // MIX: the student's log q (log2 units) of the group's rows, [row][key] with
   // a 68-float pitch (conflict-free 16-byte accesses)
@@ -467,31 +523,10 @@ __global__ __launch_bounds__(128, 2) void kl_rs_pass_kernel(KlRsK p) {
   const int G = p.G, K = a.K;
   const int j0 = c * kChunk;
 
-  // this range's rows of block c, ascending: one bitmap word per lane of wave 0
-  const uint32_t* rb = p.rbm + ((int64_t)bh * p.nblk + c) * p.rwords;
-  static_assert(kRsRange == 32 * kWave, "one bitmap word per lane of wave 0");
+  // the window's rows of block c, ascending
   const int r0 = range * kRsRange;
-  if (wave == 0) {
-    const int w = range * (kRsRange / 32) + lane;
-    const uint32_t bits = w < p.rwords ? rb[w] : 0u;
-    const int cnt = __popc(bits);
-    int incl = cnt;
-#pragma unroll
-    for (int o = 1; o < kWave; o <<= 1) {
-      const int v = __shfl_up(incl, o, kWave);
-      if (lane >= o) incl += v;
-    }
-    int pos = incl - cnt;
-    uint32_t bb = bits;
-    while (bb) {
-      const int bit = __ffs(bb) - 1;
-      bb &= bb - 1;
-      s_rows[pos++] = (uint16_t)(lane * 32 + bit);
-    }
-    if (lane == kWave - 1) s_n = incl;
-  }
-  __syncthreads();
-  const int n = s_n;
+  const int n = window_rows<kRsRange / 32>(p.rbm + ((int64_t)bh * p.nblk + c) * p.rwords, range * (kRsRange / 32),
+                                           p.rwords, s_rows, &s_n);
   if (n == 0) return;
   const int ngroups = (n + kTileRows - 1) / kTileRows;
   const int nst = ngroups * (G + 1);
@@ -897,39 +932,13 @@ __global__ __launch_bounds__(kBwdThreads) void kl_dq_kernel(KlBwdK p) {
                     a.dq_st, nrows, acc, wave, lane);
 }
 
-// Rows of one 2048-row window of a block's row bitmap, ascending, as offsets
-// from the window's first row (wave 0: one word per lane); returns the count.
-__device__ __forceinline__ int window_rows(const uint32_t* words, int w0, int rwords, uint16_t* s_rows, int* s_n) {
-  const int tid = threadIdx.x, lane = tid % kWave;
-  if (tid < kWave) {
-    const int w = w0 + lane;
-    const uint32_t bits = w < rwords ? words[w] : 0u;
-    const int cnt = __popc(bits);
-    int incl = cnt;
-#pragma unroll
-    for (int o = 1; o < kWave; o <<= 1) {
-      const int v = __shfl_up(incl, o, kWave);
-      if (lane >= o) incl += v;
-    }
-    int pos = incl - cnt;
-    uint32_t bb = bits;
-    while (bb) {
-      const int bit = __ffs(bb) - 1;
-      bb &= bb - 1;
-      s_rows[pos++] = (uint16_t)(lane * 32 + bit);
-    }
-    if (lane == kWave - 1) *s_n = incl;
-  }
-  __syncthreads();
-  return *s_n;
-}
-
 // Per (sequence, index head, 64-row tile): the union of the rows' selected
 // blocks (0 <= id < nblk, an id's first slot) and the flag; a bit per (block,
 // row) pair in the all-rows bitmap, and in the flagged-rows bitmap for a
 // flagged tile.
 __global__ __launch_bounds__(256) void kl_bwd_flag_kernel(KlBwdK p) {
-  extern __shared__ uint32_t s_u[];                    // [nwords] union bits, [1] count, [64 K] ids
+  // LDS as kl_rs_flag_kernel's
+  extern __shared__ uint32_t s_u[];
   const srswa_kl_bwd_args& a = p.a;
   const int tile = (int)(blockIdx.x % p.ntiles);
   const int bh = (int)(blockIdx.x / p.ntiles);
@@ -939,6 +948,8 @@ __global__ __launch_bounds__(256) void kl_bwd_flag_kernel(KlBwdK p) {
   uint32_t* s_bits = s_u;
   uint32_t* s_cnt = s_u + p.nwords;
   int* s_ids = reinterpret_cast<int*>(s_u + p.nwords + 1);
+  int* s_len = s_ids + kTileRows * K;
+  uint16_t* s_chunks = reinterpret_cast<uint16_t*>(s_len + 1);
   for (int w = tid; w <= p.nwords; w += blockDim.x) s_u[w] = 0u;
   __syncthreads();
   for (int e = tid; e < kTileRows * K; e += blockDim.x) {
@@ -959,18 +970,14 @@ __global__ __launch_bounds__(256) void kl_bwd_flag_kernel(KlBwdK p) {
   __syncthreads();
   const bool rs = (int)*s_cnt > K;
   if (tid == 0) p.flag[(int64_t)bh * p.ntiles + tile] = rs ? 1u : 0u;
+  const int U = compact_bitmap(s_bits, p.nwords, s_chunks, s_len);
   const int64_t base = (int64_t)bh * p.nblk * p.rwords;
-  for (int e = tid; e < nrows * K; e += blockDim.x) {
-    const int id = s_ids[e], t = t0 + e / K;
-    if (id < 0) continue;
-    const int64_t w = base + (int64_t)id * p.rwords + (t >> 5);
-    atomicOr(&p.rbm_all[w], 1u << (t & 31));
-    if (rs) atomicOr(&p.rbm[w], 1u << (t & 31));
-  }
+  tile_row_bits(s_ids, K, nrows, s_chunks, U, p.rbm_all + base, rs ? p.rbm + base : nullptr, p.rwords, tile);
 }
 
-// Per (sequence, index head, block c, 2048-row range): the flagged rows that
-// selected c, 64 at a time; each (row, slot) pair's dQ partial DS K, fp32.
+// Per (sequence, index head, block c, 2048-row window): the window's flagged
+// rows that selected c, 64 at a time; each (row, slot) pair's dQ partial
+// DS K, fp32.
 template <typename T, int D>
 __global__ __launch_bounds__(kBwdThreads) void kl_rs_dq_kernel(KlBwdK p) {
   using M = Mfma<T>;
@@ -988,8 +995,8 @@ __global__ __launch_bounds__(kBwdThreads) void kl_rs_dq_kernel(KlBwdK p) {
   const int bh = (int)(blockIdx.x / ((int64_t)p.nrange * p.nblk));
   const int ih = bh % a.HI, b = bh / a.HI;
   const int r0 = range * kRsRange;
-  const int n = window_rows(p.rbm + ((int64_t)bh * p.nblk + c) * p.rwords, range * (kRsRange / 32), p.rwords,
-                            s_rows, &s_n);
+  const int n = window_rows<kRsRange / 32>(p.rbm + ((int64_t)bh * p.nblk + c) * p.rwords, range * (kRsRange / 32),
+                                           p.rwords, s_rows, &s_n);
   if (n == 0) return;
   stage_rows<T, D>(sK, reinterpret_cast<const T*>(a.idx_k) + (int64_t)b * a.ik_sb + (int64_t)c * kChunk * a.ik_st,
                    a.ik_st, min(kChunk, a.Sk - c * kChunk));
@@ -1088,7 +1095,7 @@ __global__ __launch_bounds__(kBwdThreads) void kl_dk_kernel(KlBwdK p) {
   extern __shared__ __align__(16) unsigned char smem[];
   T* sQ = reinterpret_cast<T*>(smem);
   T* sDT = reinterpret_cast<T*>(smem + L::dsOff);   // DS^T [key][row]
-  __shared__ uint16_t s_rows[kRsRange];
+  __shared__ uint16_t s_rows[kRsWin];
   __shared__ int s_n;
   const srswa_kl_bwd_args& a = p.a;
   const int tid = threadIdx.x, wave = tid / kWave, lane = tid % kWave;
@@ -1101,9 +1108,9 @@ __global__ __launch_bounds__(kBwdThreads) void kl_dk_kernel(KlBwdK p) {
   for (int ih = 0; ih < a.HI; ++ih) {
     const uint32_t* words = p.rbm_all + (((int64_t)b * a.HI + ih) * p.nblk + c) * p.rwords;
     const T* qbase = reinterpret_cast<const T*>(a.q_idx) + (int64_t)b * a.qi_sb + (int64_t)ih * a.qi_sh;
-    for (int w0 = 0; w0 < p.rwords; w0 += kRsRange / 32) {
+    for (int w0 = 0; w0 < p.rwords; w0 += kRsWin / 32) {
       __syncthreads();                              // the previous window's list consumed
-      const int n = window_rows(words, w0, p.rwords, s_rows, &s_n);
+      const int n = window_rows<kRsWin / 32>(words, w0, p.rwords, s_rows, &s_n);
       const int r0 = w0 * 32;
       for (int g0 = 0; g0 < n; g0 += kTileRows) {
         __syncthreads();
@@ -1286,7 +1293,7 @@ int kl_fwd_impl(const srswa_kl_args* a, void* scratch, size_t scratch_bytes, voi
     rk.klp = reinterpret_cast<float*>(base + rl.klp);
     const int64_t rbm_words = (int64_t)a->B * a->HI * nblk * rk.rwords;
     hipLaunchKernelGGL(kl_zero_kernel, dim3((unsigned)((rbm_words + 255) / 256)), dim3(256), 0, st, rk.rbm, rbm_words);
-    const size_t flds = ((size_t)k.nwords + 1 + (size_t)kTileRows * a->K) * 4;
+    const size_t flds = ((size_t)k.nwords + 2 + (size_t)kTileRows * a->K) * 4 + (size_t)nblk * 2 + 16;
     hipLaunchKernelGGL(kl_rs_flag_kernel, dim3((unsigned)k.nlogical), dim3(256), flds, st, rk);
     k.rs_flag = rk.flag;
   }
@@ -1419,7 +1426,7 @@ extern "C" int srswa_gather_kl_bwd(const srswa_kl_bwd_args* a, void* scratch, si
   const int64_t words = (int64_t)(bl.dqp - bl.rbm) / 4;       // both row bitmaps
   hipLaunchKernelGGL(kl_zero_kernel, dim3((unsigned)((words + 255) / 256)), dim3(256), 0, st, k.rbm, words);
   const int64_t ntl = (int64_t)a->B * a->HI * k.ntiles;
-  const size_t flds = ((size_t)k.nwords + 1 + (size_t)kTileRows * a->K) * 4;
+  const size_t flds = ((size_t)k.nwords + 2 + (size_t)kTileRows * a->K) * 4 + (size_t)k.nblk * 2 + 16;
   hipLaunchKernelGGL(kl_bwd_flag_kernel, dim3((unsigned)ntl), dim3(256), flds, st, k);
   const dim3 gdq((unsigned)ntl), gdk((unsigned)((int64_t)a->B * k.nblk));
   const dim3 grs((unsigned)((int64_t)a->B * a->HI * k.nblk * k.nrange));
