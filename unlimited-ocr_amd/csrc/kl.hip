@@ -374,6 +374,7 @@ constexpr int kRsWin = 2048;     // rows per window of the dK scan (64 bitmap wo
 struct KlRsK {
   srswa_kl_args a;
   int ntiles, nblk, nwords, rwords, nrange, G, KV;
+  int per_xcd;        // block-major workgroups per XCD
   uint32_t* flag;     // [B, HI, ntiles]
   uint32_t* rbm;      // [B, HI, nblk, rwords] rows of flagged tiles per block
   float2* srec;       // [B, HI, T, K, G + 1] per pair and head: (max in log2 units, sum)
@@ -494,7 +495,9 @@ __global__ __launch_bounds__(256) void kl_rs_flag_kernel(KlRsK p) {
 }
 
 // One workgroup per (sequence, index head, block c, 2048-row window): the
-// window's rows that selected c, ascending, two waves
+// window's rows that selected c, ascending, two waves.  Logical order: window
+// major, block fastest, dealt to the XCDs in contiguous runs, so the workgroups
+// on one XCD gather query rows of the same windows from its L2.
 // of 32 rows per group of 64 (lane = row, S^T = K Q^T over the block's 64
 // keys as in the tile kernel).  Stage (group, head): K of the head's block
 // staged in LDS, the rows' query fragments in registers, both fetched one
@@ -514,9 +517,11 @@ __global__ __launch_bounds__(128, 2) void kl_rs_pass_kernel(KlRsK p) {
   constexpr int LQP = 68;
   __shared__ __align__(16) float s_lq[MIX ? kTileRows * LQP : 4];
   const srswa_kl_args& a = p.a;
-  const int range = (int)(blockIdx.x % p.nrange);
-  const int c = (int)((blockIdx.x / p.nrange) % p.nblk);
-  const int bh = (int)(blockIdx.x / ((int64_t)p.nrange * p.nblk));
+  const int64_t lid = (int64_t)(blockIdx.x & 7) * p.per_xcd + (blockIdx.x >> 3);
+  if (lid >= (int64_t)a.B * a.HI * p.nrange * p.nblk) return;
+  const int c = (int)(lid % p.nblk);
+  const int range = (int)((lid / p.nblk) % p.nrange);
+  const int bh = (int)(lid / ((int64_t)p.nblk * p.nrange));
   const int ih = bh % a.HI, b = bh / a.HI;
   const int tid = threadIdx.x, wave = tid / kWave, lane = tid % kWave;
   const int h = lane >> 5, rl = lane & 31;
@@ -774,6 +779,7 @@ constexpr int kBwdThreads = 256;
 struct KlBwdK {
   srswa_kl_bwd_args a;
   int ntiles, nblk, nwords, rwords, nrange;
+  int per_xcd;              // rs_dq workgroups per XCD (window major, block fastest)
   uint32_t* flag;           // [B, HI, ntiles]: rows of the tile taken by rs_dq_kernel
   uint32_t* rbm;            // [B, HI, nblk, rwords] rows of flagged tiles per block
   uint32_t* rbm_all;        // [B, HI, nblk, rwords] every row per block
@@ -990,9 +996,11 @@ __global__ __launch_bounds__(kBwdThreads) void kl_rs_dq_kernel(KlBwdK p) {
   __shared__ int s_n, s_t[kTileRows], s_slot[kTileRows];
   const srswa_kl_bwd_args& a = p.a;
   const int tid = threadIdx.x, wave = tid / kWave, lane = tid % kWave;
-  const int range = (int)(blockIdx.x % p.nrange);
-  const int c = (int)((blockIdx.x / p.nrange) % p.nblk);
-  const int bh = (int)(blockIdx.x / ((int64_t)p.nrange * p.nblk));
+  const int64_t lid = (int64_t)(blockIdx.x & 7) * p.per_xcd + (blockIdx.x >> 3);
+  if (lid >= (int64_t)a.B * a.HI * p.nrange * p.nblk) return;
+  const int c = (int)(lid % p.nblk);
+  const int range = (int)((lid / p.nblk) % p.nrange);
+  const int bh = (int)(lid / ((int64_t)p.nblk * p.nrange));
   const int ih = bh % a.HI, b = bh / a.HI;
   const int r0 = range * kRsRange;
   const int n = window_rows<kRsRange / 32>(p.rbm + ((int64_t)bh * p.nblk + c) * p.rwords, range * (kRsRange / 32),
@@ -1284,6 +1292,7 @@ int kl_fwd_impl(const srswa_kl_args* a, void* scratch, size_t scratch_bytes, voi
     rk.nwords = k.nwords;
     rk.rwords = ceil_div(a->T, 32);
     rk.nrange = ceil_div(a->T, kRsRange);
+    rk.per_xcd = (int)ceil_div((int64_t)a->B * a->HI * nblk * rk.nrange, (int64_t)8);
     rk.G = k.G;
     rk.KV = k.KV;
     rk.flag = reinterpret_cast<uint32_t*>(base + rl.flag);
@@ -1323,7 +1332,7 @@ int kl_fwd_impl(const srswa_kl_args* a, void* scratch, size_t scratch_bytes, voi
 #undef KL_LAUNCH
   if (!lds_ok) return SRSWA_LAUNCH;
   if (scratch) {
-    const dim3 gp((unsigned)((int64_t)a->B * a->HI * nblk * rk.nrange));
+    const dim3 gp((unsigned)(8 * (int64_t)rk.per_xcd));
     const dim3 gr((unsigned)(((int64_t)a->B * a->HI * a->T + 255) / 256));
     const dim3 gc((unsigned)(((int64_t)a->B * a->HI * a->T * (k.G + 1) + 255) / 256));
 #define KL_RS(T_, D_)                                                                   \
@@ -1418,6 +1427,7 @@ extern "C" int srswa_gather_kl_bwd(const srswa_kl_bwd_args* a, void* scratch, si
   k.nwords = ceil_div(k.nblk, 32);
   k.rwords = ceil_div(a->T, 32);
   k.nrange = ceil_div(a->T, kRsRange);
+  k.per_xcd = (int)ceil_div((int64_t)a->B * a->HI * k.nblk * k.nrange, (int64_t)8);
   k.flag = reinterpret_cast<uint32_t*>(base + bl.flag);
   k.rbm = reinterpret_cast<uint32_t*>(base + bl.rbm);
   k.rbm_all = reinterpret_cast<uint32_t*>(base + bl.rbm_all);
@@ -1429,7 +1439,7 @@ extern "C" int srswa_gather_kl_bwd(const srswa_kl_bwd_args* a, void* scratch, si
   const size_t flds = ((size_t)k.nwords + 2 + (size_t)kTileRows * a->K) * 4 + (size_t)k.nblk * 2 + 16;
   hipLaunchKernelGGL(kl_bwd_flag_kernel, dim3((unsigned)ntl), dim3(256), flds, st, k);
   const dim3 gdq((unsigned)ntl), gdk((unsigned)((int64_t)a->B * k.nblk));
-  const dim3 grs((unsigned)((int64_t)a->B * a->HI * k.nblk * k.nrange));
+  const dim3 grs((unsigned)(8 * (int64_t)k.per_xcd));
   const dim3 grd((unsigned)(((int64_t)a->B * a->HI * a->T * (a->D / 4) + 255) / 256));
   const size_t lds = a->D == 128 ? KlBwdLds<128>::bytes : KlBwdLds<64>::bytes;
 #define KL_BWD(T_, D_)                                                                      \
