@@ -731,7 +731,10 @@ typedef struct {
   int32_t dtype;
 } srswa_kl_bwd_args;
 
-/* Workspace: a (block, 64-row tile) touch bitmap, no initial content. */
+/* Workspace, no initial content: per (row tile) a flag, per (head, key block)
+ * two row bitmaps, fp32 dQ partials per (row, slot) of flagged tiles
+ * (B*HI*T*K*D*4 bytes) and fp32 dK partials per (key block, 2048-row window)
+ * (B*ceil(Sk/64)*ceil(T/2048)*64*D*4 bytes). */
 int srswa_gather_kl_bwd_workspace(const srswa_kl_bwd_args* a, size_t* scratch_bytes);
 int srswa_gather_kl_bwd(const srswa_kl_bwd_args* a, void* scratch, size_t scratch_bytes, void* stream);
 

@@ -768,9 +768,11 @@ __global__ __launch_bounds__(256) void kl_rs_final_kernel(KlRsK p) {
 //                 flagged rows that selected the block, 64 at a time: each
 //                 (row, slot) pair's product DS K written as an fp32 partial,
 //                 then summed per row in slot order (rs_dq_reduce_kernel);
-//   dk_kernel:    per (sequence, block), every row that selected it in
-//                 ascending order, 64 at a time (deterministic):
-//                 dK[keys, d] += DS^T[keys, rows] Q[rows, d].
+//   dk_kernel:    per (sequence, block, 2048-row window), the window's rows
+//                 that selected the block, ascending, 64 at a time:
+//                 dK[keys, d] += DS^T[keys, rows] Q[rows, d] as an fp32
+//                 partial; dk_reduce_kernel sums the windows in order
+//                 (deterministic).
 // Four waves; wave w owns output tiles (w / TPW halves of 32 rows / keys,
 // 32-wide head-dim slices); K and Q rows are read as B operands with
 // ds_read_b64_tr_b16 from their natural layout.
@@ -784,6 +786,9 @@ struct KlBwdK {
   uint32_t* rbm;            // [B, HI, nblk, rwords] rows of flagged tiles per block
   uint32_t* rbm_all;        // [B, HI, nblk, rwords] every row per block
   float* dqp;               // [B, HI, T, K, D] per (row, slot): dQ partial of a flagged row
+  float* dkp;               // [B, nblk, nwin, 64, D] per (block, 2048-row window): dK partial
+  uint32_t* dkw;            // [B, nblk, nwin]: the window wrote a partial
+  int nwin;
 };
 
 template <int D> struct KlBwdLds {
@@ -1107,58 +1112,99 @@ __global__ __launch_bounds__(kBwdThreads) void kl_dk_kernel(KlBwdK p) {
   __shared__ int s_n;
   const srswa_kl_bwd_args& a = p.a;
   const int tid = threadIdx.x, wave = tid / kWave, lane = tid % kWave;
-  const int c = blockIdx.x % p.nblk, b = blockIdx.x / p.nblk;
+  const int win = (int)(blockIdx.x % p.nwin);
+  const int c = (int)((blockIdx.x / p.nwin) % p.nblk), b = (int)(blockIdx.x / ((int64_t)p.nwin * p.nblk));
   f32x16_t acc[TPW];
 #pragma unroll
   for (int i = 0; i < TPW; ++i) acc[i] = zero16();
   const uint16_t* q16 = reinterpret_cast<const uint16_t*>(sQ);
   const int rr = tid / 4, kq = (tid % 4) * 16;
+  const int w0 = win * (kRsWin / 32), r0 = win * kRsWin;
+  int any = 0;
   for (int ih = 0; ih < a.HI; ++ih) {
     const uint32_t* words = p.rbm_all + (((int64_t)b * a.HI + ih) * p.nblk + c) * p.rwords;
     const T* qbase = reinterpret_cast<const T*>(a.q_idx) + (int64_t)b * a.qi_sb + (int64_t)ih * a.qi_sh;
-    for (int w0 = 0; w0 < p.rwords; w0 += kRsWin / 32) {
-      __syncthreads();                              // the previous window's list consumed
-      const int n = window_rows<kRsWin / 32>(words, w0, p.rwords, s_rows, &s_n);
-      const int r0 = w0 * 32;
-      for (int g0 = 0; g0 < n; g0 += kTileRows) {
-        __syncthreads();
-        // the group's Q rows (gathered) and DS^T
-        for (int e = tid; e < kTileRows * PR; e += kBwdThreads) {
-          const int r = e / PR, cc = (e % PR) * 8;
-          const int i = g0 + r;
-          const uint4 v = i < n ? *reinterpret_cast<const uint4*>(qbase + (int64_t)(r0 + s_rows[i]) * a.qi_st + cc)
-                                : make_uint4(0, 0, 0, 0);
-          *reinterpret_cast<uint4*>(sQ + r * XP + cc) = v;
-        }
-        {
-          const int i = g0 + rr;
-          const int t = i < n ? r0 + (int)s_rows[i] : -1;
-          const int slot = t >= 0 ? find_slot(a, b, ih, t, c) : -1;
-          float v[16];
-          ds16<T>(a, b, ih, t, slot, kq, v);
+    __syncthreads();                                // the previous head's list consumed
+    const int n = window_rows<kRsWin / 32>(words, w0, p.rwords, s_rows, &s_n);
+    any |= n;
+    for (int g0 = 0; g0 < n; g0 += kTileRows) {
+      __syncthreads();
+      // the group's Q rows (gathered) and DS^T
+      for (int e = tid; e < kTileRows * PR; e += kBwdThreads) {
+        const int r = e / PR, cc = (e % PR) * 8;
+        const int i = g0 + r;
+        const uint4 v = i < n ? *reinterpret_cast<const uint4*>(qbase + (int64_t)(r0 + s_rows[i]) * a.qi_st + cc)
+                              : make_uint4(0, 0, 0, 0);
+        *reinterpret_cast<uint4*>(sQ + r * XP + cc) = v;
+      }
+      {
+        const int i = g0 + rr;
+        const int t = i < n ? r0 + (int)s_rows[i] : -1;
+        const int slot = t >= 0 ? find_slot(a, b, ih, t, c) : -1;
+        float v[16];
+        ds16<T>(a, b, ih, t, slot, kq, v);
 #pragma unroll
-          for (int k = 0; k < 16; ++k)   // rows in the transposing read's order (slot_of_key)
-            reinterpret_cast<uint16_t*>(sDT)[(kq + k) * SP + slot_of_key(rr)] =
-                (uint16_t)(M::pack2(v[k], 0.f) & 0xffffu);
-        }
-        __syncthreads();
-        // dK[key, d] += DS^T[key, row] Q[row, d]
+        for (int k = 0; k < 16; ++k)   // rows in the transposing read's order (slot_of_key)
+          reinterpret_cast<uint16_t*>(sDT)[(kq + k) * SP + slot_of_key(rr)] = (uint16_t)(M::pack2(v[k], 0.f) & 0xffffu);
+      }
+      __syncthreads();
+      // dK[key, d] += DS^T[key, row] Q[row, d]
 #pragma unroll
-        for (int ks = 0; ks < 4; ++ks) {
+      for (int ks = 0; ks < 4; ++ks) {
 #pragma unroll
-          for (int i = 0; i < TPW; ++i) {
-            const int tix = wave * TPW + i;
-            const int half = tix / MT, dt = tix % MT;
-            const uint4 av =
-                *reinterpret_cast<const uint4*>(sDT + (32 * half + (lane & 31)) * SP + 16 * ks + 8 * (lane >> 5));
-            acc[i] = M::mac(av, a_operand_tr<XP>(q16, 16 * ks, 32 * dt, lane), acc[i]);
-          }
+        for (int i = 0; i < TPW; ++i) {
+          const int tix = wave * TPW + i;
+          const int half = tix / MT, dt = tix % MT;
+          const uint4 av = *reinterpret_cast<const uint4*>(sDT + (32 * half + (lane & 31)) * SP + 16 * ks + 8 * (lane >> 5));
+          acc[i] = M::mac(av, a_operand_tr<XP>(q16, 16 * ks, 32 * dt, lane), acc[i]);
         }
       }
     }
   }
-  store_tiles<T, D>(reinterpret_cast<T*>(a.dk_idx) + (int64_t)b * a.dk_sb + (int64_t)c * kChunk * a.dk_st, a.dk_st,
-                    min(kChunk, a.Sk - c * kChunk), acc, wave, lane);
+  const int64_t wi = ((int64_t)b * p.nblk + c) * p.nwin + win;
+  if (tid == 0) p.dkw[wi] = any ? 1u : 0u;
+  if (!any) return;
+  // the fp32 partial: key m of output tile (half, dt) is 32 half + 8 (r / 4) + 4 (lane / 32) + r % 4
+  float* out = p.dkp + wi * kChunk * D;
+#pragma unroll
+  for (int i = 0; i < TPW; ++i) {
+    const int tix = wave * TPW + i;
+    const int half = tix / MT, dt = tix % MT;
+#pragma unroll
+    for (int r = 0; r < 16; ++r) {
+      const int m = 32 * half + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3);
+      out[m * D + 32 * dt + (lane & 31)] = acc[i][r];
+    }
+  }
+}
+
+// dK of a block: its windows' partials summed in window order, rounded once to
+// the input dtype; four head dims per thread.
+template <typename T, int D>
+__global__ __launch_bounds__(256) void kl_dk_reduce_kernel(KlBwdK p) {
+  const srswa_kl_bwd_args& a = p.a;
+  const int64_t gid = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (gid >= (int64_t)a.B * p.nblk * kChunk * (D / 4)) return;
+  const int d = (int)(gid % (D / 4)) * 4;
+  const int key = (int)((gid / (D / 4)) % kChunk);
+  const int64_t bc = gid / ((int64_t)(D / 4) * kChunk);   // b * nblk + c
+  const int c = (int)(bc % p.nblk), b = (int)(bc / p.nblk);
+  if (c * kChunk + key >= a.Sk) return;
+  float4 acc = make_float4(0.f, 0.f, 0.f, 0.f);
+  for (int w = 0; w < p.nwin; ++w) {
+    const int64_t wi = bc * p.nwin + w;
+    if (!p.dkw[wi]) continue;
+    const float4 v = *reinterpret_cast<const float4*>(p.dkp + (wi * kChunk + key) * D + d);
+    acc.x += v.x;
+    acc.y += v.y;
+    acc.z += v.z;
+    acc.w += v.w;
+  }
+  uint2 w;
+  w.x = Mfma<T>::pack2(acc.x, acc.y);
+  w.y = Mfma<T>::pack2(acc.z, acc.w);
+  *reinterpret_cast<uint2*>(reinterpret_cast<T*>(a.dk_idx) + (int64_t)b * a.dk_sb +
+                            (int64_t)(c * kChunk + key) * a.dk_st + d) = w;
 }
 
 bool al16(const void* p) { return ((uintptr_t)p & 15u) == 0; }
@@ -1362,7 +1408,7 @@ namespace srswa {
 namespace {
 // Backward workspace, in 256-byte aligned pieces.
 struct KlBwdLayout {
-  size_t flag, rbm, rbm_all, dqp, total;
+  size_t flag, rbm, rbm_all, dqp, dkp, dkw, total;
 };
 KlBwdLayout kl_bwd_layout(const srswa_kl_bwd_args* a) {
   auto al = [](size_t n) { return (n + 255) / 256 * 256; };
@@ -1373,7 +1419,10 @@ KlBwdLayout kl_bwd_layout(const srswa_kl_bwd_args* a) {
   L.rbm = L.flag + al((size_t)(bh * ntiles) * 4);
   L.rbm_all = L.rbm + al((size_t)(bh * nblk * rwords) * 4);
   L.dqp = L.rbm_all + al((size_t)(bh * nblk * rwords) * 4);
-  L.total = L.dqp + al((size_t)(bh * T * std::max(a->K, 0) * std::max(a->D, 0)) * 4);
+  L.dkp = L.dqp + al((size_t)(bh * T * std::max(a->K, 0) * std::max(a->D, 0)) * 4);
+  const int64_t nwin = ceil_div(T, kRsWin), bb = std::max(a->B, 0);
+  L.dkw = L.dkp + al((size_t)(bb * nblk * nwin * kChunk * std::max(a->D, 0)) * 4);
+  L.total = L.dkw + al((size_t)(bb * nblk * nwin) * 4);
   return L;
 }
 }  // namespace
@@ -1401,7 +1450,8 @@ extern "C" int srswa_gather_kl_bwd(const srswa_kl_bwd_args* a, void* scratch, si
   if (rc != SRSWA_OK) return rc;
   bool ok = al16(a->q_idx) && al16(a->idx_k) && al16(a->dsel) && ((uintptr_t)a->dq_idx & 7u) == 0;
   for (int64_t st : {a->qi_sb, a->qi_sh, a->qi_st, a->ik_sb, a->ik_st}) ok = ok && (st * 2) % 16 == 0;
-  for (int64_t st : {a->dq_sb, a->dq_sh, a->dq_st}) ok = ok && (st * 2) % 8 == 0;   // 4-element dQ stores
+  for (int64_t st : {a->dq_sb, a->dq_sh, a->dq_st, a->dk_sb, a->dk_st}) ok = ok && (st * 2) % 8 == 0;   // 4-element stores
+  ok = ok && ((uintptr_t)a->dk_idx & 7u) == 0;
   ok = ok && (a->ds_sb * 4) % 16 == 0 && (a->ds_sh * 4) % 16 == 0 && (a->ds_st * 4) % 16 == 0;
   if (!ok) {
     set_error("gather kl backward: rows must be 16-byte aligned");
@@ -1432,13 +1482,17 @@ extern "C" int srswa_gather_kl_bwd(const srswa_kl_bwd_args* a, void* scratch, si
   k.rbm = reinterpret_cast<uint32_t*>(base + bl.rbm);
   k.rbm_all = reinterpret_cast<uint32_t*>(base + bl.rbm_all);
   k.dqp = reinterpret_cast<float*>(base + bl.dqp);
+  k.dkp = reinterpret_cast<float*>(base + bl.dkp);
+  k.dkw = reinterpret_cast<uint32_t*>(base + bl.dkw);
+  k.nwin = ceil_div(a->T, kRsWin);
   hipStream_t st = reinterpret_cast<hipStream_t>(stream);
   const int64_t words = (int64_t)(bl.dqp - bl.rbm) / 4;       // both row bitmaps
   hipLaunchKernelGGL(kl_zero_kernel, dim3((unsigned)((words + 255) / 256)), dim3(256), 0, st, k.rbm, words);
   const int64_t ntl = (int64_t)a->B * a->HI * k.ntiles;
   const size_t flds = ((size_t)k.nwords + 2 + (size_t)kTileRows * a->K) * 4 + (size_t)k.nblk * 2 + 16;
   hipLaunchKernelGGL(kl_bwd_flag_kernel, dim3((unsigned)ntl), dim3(256), flds, st, k);
-  const dim3 gdq((unsigned)ntl), gdk((unsigned)((int64_t)a->B * k.nblk));
+  const dim3 gdq((unsigned)ntl), gdk((unsigned)((int64_t)a->B * k.nblk * k.nwin));
+  const dim3 gdr((unsigned)(((int64_t)a->B * k.nblk * kChunk * (a->D / 4) + 255) / 256));
   const dim3 grs((unsigned)(8 * (int64_t)k.per_xcd));
   const dim3 grd((unsigned)(((int64_t)a->B * a->HI * a->T * (a->D / 4) + 255) / 256));
   const size_t lds = a->D == 128 ? KlBwdLds<128>::bytes : KlBwdLds<64>::bytes;
@@ -1446,7 +1500,8 @@ extern "C" int srswa_gather_kl_bwd(const srswa_kl_bwd_args* a, void* scratch, si
   hipLaunchKernelGGL((kl_dq_kernel<T_, D_>), gdq, dim3(kBwdThreads), lds, st, k);          \
   hipLaunchKernelGGL((kl_rs_dq_kernel<T_, D_>), grs, dim3(kBwdThreads), lds, st, k);       \
   hipLaunchKernelGGL((kl_rs_dq_reduce_kernel<T_, D_>), grd, dim3(256), 0, st, k);          \
-  hipLaunchKernelGGL((kl_dk_kernel<T_, D_>), gdk, dim3(kBwdThreads), lds, st, k);
+  hipLaunchKernelGGL((kl_dk_kernel<T_, D_>), gdk, dim3(kBwdThreads), lds, st, k);          \
+  hipLaunchKernelGGL((kl_dk_reduce_kernel<T_, D_>), gdr, dim3(256), 0, st, k);
   if (a->dtype == SRSWA_BF16) {
     if (a->D == 128) { KL_BWD(bf16_t, 128) } else { KL_BWD(bf16_t, 64) }
   } else {
