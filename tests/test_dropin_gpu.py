@@ -159,3 +159,19 @@ def test_block_max_score_key_slabs(dev, bs, d):
     nblk = -(-Sk // bs) + 2
     got = SG.triton_block_max_score(q.to(dev), k.to(dev), pos.to(dev), seg.to(dev), bs, nblk, lw).cpu()
     _check_block_max(got, q, k, pos, seg, bs, nblk, lw, f"block max key slabs bs={bs} d={d}")
+
+
+@pytest.mark.parametrize("bs,d", [(64, 64), (128, 128)])
+def test_block_max_score_fp16_row_tiles(dev, bs, d):
+    """fp16 operands over several 256-row query tiles (the last one partial),
+    rows at unrelated positions and segment starts, keys long enough for
+    several key slabs, and the last key block partial (Sk % 64 != 0)."""
+    g = torch.Generator().manual_seed(700 + bs + d)
+    B, C, Sk, lw = 2, 600, 3001, 128
+    q = torch.randn(B, C, d, generator=g).to(torch.float16)
+    k = torch.randn(B, Sk, d, generator=g).to(torch.float16)
+    pos = torch.randint(0, Sk + 300, (B, C), generator=g)
+    seg = torch.randint(0, 900, (B, C), generator=g)
+    nblk = -(-Sk // bs) + 1
+    got = SG.triton_block_max_score(q.to(dev), k.to(dev), pos.to(dev), seg.to(dev), bs, nblk, lw).cpu()
+    _check_block_max(got, q, k, pos, seg, bs, nblk, lw, f"block max fp16 row tiles bs={bs} d={d}")

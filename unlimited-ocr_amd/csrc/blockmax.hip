@@ -197,6 +197,220 @@ __global__ __launch_bounds__(kBmaxThreads) void block_max_kernel(BmaxK p) {
   }
 }
 
+// 16-bit operands, blocks of whole chunks (BS % 64 == 0): one workgroup =
+// (sequence, 256 rows, slab of kBm2Slab chunks), four waves of 64 rows.  A
+// wave holds two 32-row query tiles, so every K fragment it reads from LDS
+// feeds two MFMAs.  K chunks reach LDS by direct-to-LDS buffer loads
+// (buffer_load_dwordx4 ... lds) into a three-slot ring: two chunks in flight, no
+// staging registers, one barrier per chunk.  A key row is D * 2 bytes without
+// padding; its 16-byte pieces are XOR-swizzled so the A-operand reads (32
+// keys, one piece each) hit distinct banks.  Block maxima are staged in LDS
+// and written once per slab, so no global store sits between the ring's loads
+// and the vmcnt waits that count them.
+constexpr int kBm2Rows = 256;
+constexpr int kBm2Threads = 256;
+constexpr int kBm2Slab = 16;        // chunks per slab
+constexpr int kBm2Stages = 3;
+
+template <int D> struct Bm2Layout {
+  static constexpr int NP = D / 8;                    // 16-byte pieces per key row
+  static constexpr int RPL = 256 / (D * 2);           // key rows per 256 bytes (1 or 2)
+  static constexpr int kStage = kChunk * D;           // elements per ring slot
+  static constexpr int LPT = kChunk * NP / kBm2Threads;   // direct-to-LDS loads per thread per chunk
+  // element offset of piece p of key row r in a slot
+  __device__ __forceinline__ static int at(int r, int p) { return r * D + 8 * (p ^ ((r / RPL) % NP)); }
+};
+
+// max of three (IEEE maxNum: a quiet NaN operand is ignored, like fmaxf);
+// written out because fmaxf on MFMA results first canonicalises every input
+__device__ __forceinline__ float max3f(float a, float b, float c) {
+  float d;
+  asm("v_max3_f32 %0, %1, %2, %3" : "=v"(d) : "v"(a), "v"(b), "v"(c));
+  return d;
+}
+
+// s_waitcnt vmcnt(N), the other counters left alone (gfx9 encoding: vmcnt in
+// bits 3:0 and 15:14, expcnt 6:4, lgkmcnt 11:8)
+template <int N> __device__ __forceinline__ void wait_vm() {
+  static_assert(N >= 0 && N < 16, "vmcnt");
+  __builtin_amdgcn_s_waitcnt(N | (0x7 << 4) | (0xF << 8));
+}
+
+template <typename T, int D>
+__global__ __launch_bounds__(kBm2Threads, 2) void block_max16_kernel(BmaxK p) {
+  using L = Bm2Layout<D>;
+  using M = Mfma<T>;
+  constexpr int NQ = D / 16;
+  __shared__ __align__(16) T sK0[L::kStage];
+  __shared__ __align__(16) T sK1[L::kStage];
+  __shared__ __align__(16) T sK2[L::kStage];
+  __shared__ float s_out[kBm2Slab * kBm2Rows];
+  __shared__ int s_maxls;
+  const srswa_blockmax_args& a = p.a;
+  const int tid = threadIdx.x, wave = tid / kWave, lane = tid % kWave;
+  const int h = lane / 32, rl = lane % 32;
+  const int total = a.B * p.ntiles * p.nslab;
+  const int per_xcd = (int)(gridDim.x / 8);
+  const int lid = (int)(blockIdx.x & 7) * per_xcd + (int)(blockIdx.x >> 3);
+  if (lid >= total) return;
+  // tile fastest: one XCD's workgroups score consecutive tiles against the same key slab
+  const int tile = lid % p.ntiles;
+  const int slab = (lid / p.ntiles) % p.nslab;
+  const int b = lid / (p.ntiles * p.nslab);
+  const int BS = a.block_size, cpb = BS / kChunk;
+
+  int ls[2], seg[2];
+  bool ok[2];
+#pragma unroll
+  for (int rt = 0; rt < 2; ++rt) {
+    const int row = tile * kBm2Rows + wave * 64 + 32 * rt + rl;
+    ok[rt] = row < a.C;
+    ls[rt] = 0;
+    seg[rt] = 0;
+    if (ok[rt]) {
+      const int pos = a.pos[(int64_t)b * a.pos_sb + (int64_t)row * a.pos_sc];
+      seg[rt] = a.seg ? a.seg[(int64_t)b * a.seg_sb + (int64_t)row * a.seg_sc] : 0;
+      ls[rt] = min(max(pos - (a.local_window - 1), 0), a.Sk);
+    }
+  }
+  if (tid == 0) s_maxls = 0;
+#pragma unroll
+  for (int i = 0; i < kBm2Slab; ++i) s_out[i * kBm2Rows + tid] = -INFINITY;
+  __syncthreads();
+  if (ok[0] || ok[1]) atomicMax(&s_maxls, max(ls[0], ls[1]));
+  __syncthreads();
+  const int nchunks = ceil_div(s_maxls, kChunk);   // no row has a remote key at or past this chunk
+  const int c_lo = slab * p.slab_chunks;
+  const int c_hi = min(c_lo + p.slab_chunks, nchunks);
+  const int blk_lo = c_lo / cpb;
+  const int blk_hi = slab == p.nslab - 1 ? a.nblk : min(a.nblk, (c_lo + p.slab_chunks) / cpb);
+  const T* kg = reinterpret_cast<const T*>(a.k) + (int64_t)b * a.k_sb;
+  // the sequence's keys (the host checks that they span < 4 GiB)
+  const __amdgpu_buffer_rsrc_t krs =
+      make_rsrc(kg, a.Sk > 0 ? (uint32_t)(((int64_t)(a.Sk - 1) * a.k_sk + D) * (int64_t)sizeof(T)) : 0u);
+
+  uint4 qf[2][NQ];
+#pragma unroll
+  for (int rt = 0; rt < 2; ++rt) {
+    const int row = tile * kBm2Rows + wave * 64 + 32 * rt + rl;
+    const T* qrow = reinterpret_cast<const T*>(a.q) + (int64_t)b * a.q_sb + (int64_t)(ok[rt] ? row : 0) * a.q_sc;
+#pragma unroll
+    for (int ks = 0; ks < NQ; ++ks)
+      qf[rt][ks] = ok[rt] ? *reinterpret_cast<const uint4*>(qrow + 16 * ks + 8 * h) : make_uint4(0, 0, 0, 0);
+  }
+
+  // chunk c into a slot: load i of this thread fills the slot's 16-byte piece
+  // wave * 64 * LPT + 64 i + lane (a wave's load covers 1 KiB of the slot)
+  auto issue = [&](int c, T* slot) {
+#pragma unroll
+    for (int i = 0; i < L::LPT; ++i) {
+      const int piece = (wave * L::LPT + i) * kWave + lane;
+      const int r = piece / L::NP, q = piece % L::NP;
+      const int lp = q ^ ((r / L::RPL) % L::NP);
+      const int j = min(c * kChunk + r, a.Sk - 1);   // a tail chunk repeats the last key (masked below)
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(
+          krs, (__attribute__((address_space(3))) void*)(slot + (wave * L::LPT + i) * kWave * 8), 16,
+          (uint32_t)(((int64_t)j * a.k_sk + 8 * lp) * (int64_t)sizeof(T)), 0, 0, 0);
+    }
+  };
+  float run[2] = {-INFINITY, -INFINITY};
+  auto compute = [&](int c, const T* slot) {
+    const int j0 = c * kChunk;
+    f32x16_t acc[2][2];
+#pragma unroll
+    for (int rt = 0; rt < 2; ++rt) acc[rt][0] = acc[rt][1] = zero16();
+    // the fragments of step ks + 1 are read before the MFMAs of step ks
+    uint4 a0 = *reinterpret_cast<const uint4*>(slot + L::at(rl, h));
+    uint4 a1 = *reinterpret_cast<const uint4*>(slot + L::at(32 + rl, h));
+#pragma unroll
+    for (int ks = 0; ks < NQ; ++ks) {
+      uint4 n0 = a0, n1 = a1;
+      if (ks + 1 < NQ) {
+        n0 = *reinterpret_cast<const uint4*>(slot + L::at(rl, 2 * (ks + 1) + h));
+        n1 = *reinterpret_cast<const uint4*>(slot + L::at(32 + rl, 2 * (ks + 1) + h));
+      }
+#pragma unroll
+      for (int rt = 0; rt < 2; ++rt) {
+        acc[rt][0] = M::mac(a0, qf[rt][ks], acc[rt][0]);
+        acc[rt][1] = M::mac(a1, qf[rt][ks], acc[rt][1]);
+      }
+      a0 = n0;
+      a1 = n1;
+    }
+    __builtin_amdgcn_sched_group_barrier(0x100, 2, 0);     // DS reads of step 0
+#pragma unroll
+    for (int ks = 0; ks < NQ; ++ks) {
+      if (ks + 1 < NQ) __builtin_amdgcn_sched_group_barrier(0x100, 2, 0);   // step ks + 1's reads
+      __builtin_amdgcn_sched_group_barrier(0x008, 4, 0);                    // step ks's MFMAs
+    }
+    const bool whole = __all((!ok[0] || (j0 >= seg[0] && j0 + kChunk <= ls[0])) &&
+                             (!ok[1] || (j0 >= seg[1] && j0 + kChunk <= ls[1])));
+    if (whole) {
+#pragma unroll
+      for (int rt = 0; rt < 2; ++rt) {
+        float mx = max3f(run[rt], acc[rt][0][0], acc[rt][1][0]);
+#pragma unroll
+        for (int r = 1; r < 16; ++r) mx = max3f(mx, acc[rt][0][r], acc[rt][1][r]);
+        run[rt] = mx;
+      }
+    } else {
+#pragma unroll
+      for (int rt = 0; rt < 2; ++rt) {
+        // key offset 32 half + 8 (r / 4) + 4 h + r % 4 of the chunk is kept when
+        // seg <= j0 + offset < ls; the bounds pass an empty asm so the compiler
+        // keeps this rare path's arithmetic inside the branch
+        int lo = seg[rt] - j0 - 4 * h, hi = ls[rt] - j0 - 4 * h;
+        asm volatile("" : "+v"(lo), "+v"(hi));
+        float mx = run[rt];
+#pragma unroll
+        for (int r = 0; r < 16; ++r)
+#pragma unroll
+          for (int half = 0; half < 2; ++half) {
+            const int off = 32 * half + 8 * (r >> 2) + (r & 3);
+            if (off >= lo && off < hi) mx = fmaxf(mx, acc[rt][half][r]);
+          }
+        run[rt] = mx;
+      }
+    }
+    if (((c + 1) % cpb == 0) || (c == c_hi - 1)) {
+      // both lane halves end with both tiles' maxima; half h writes tile h
+      const float m0 = fmaxf(run[0], __shfl_xor(run[0], 32, kWave));
+      const float m1 = fmaxf(run[1], __shfl_xor(run[1], 32, kWave));
+      s_out[(c / cpb - blk_lo) * kBm2Rows + wave * 64 + 32 * h + rl] = h ? m1 : m0;
+      run[0] = run[1] = -INFINITY;
+    }
+  };
+  // one step: chunk c's loads landed for every thread, slot `nxt` (read two
+  // steps ago) refilled with chunk c + 2, chunk c scored from slot `cur`
+  auto step = [&](int c, const T* cur, T* nxt) {
+    if (c + 1 < c_hi) wait_vm<L::LPT>(); else wait_vm<0>();
+    __syncthreads();
+    if (c + 2 < c_hi) issue(c + 2, nxt);
+    compute(c, cur);
+  };
+  if (c_lo < c_hi) issue(c_lo, sK0);
+  if (c_lo + 1 < c_hi) issue(c_lo + 1, sK1);
+  for (int c = c_lo; c < c_hi; c += kBm2Stages) {
+    step(c, sK0, sK2);
+    if (c + 1 >= c_hi) break;
+    step(c + 1, sK1, sK0);
+    if (c + 2 >= c_hi) break;
+    step(c + 2, sK2, sK1);
+  }
+  __syncthreads();
+  // the slab's blocks, row-major; blocks past the staged ones (the last slab's
+  // tail when nblk exceeds the keys) hold no key
+  const int nb = blk_hi - blk_lo;
+  const int sb = p.slab_chunks / cpb;
+  for (int e = tid; e < kBm2Rows * nb; e += kBm2Threads) {
+    const int rw = e / nb, lb = e % nb;
+    const int row = tile * kBm2Rows + rw;
+    if (row < a.C)
+      a.out[(int64_t)b * a.o_sb + (int64_t)row * a.o_sc + (int64_t)(blk_lo + lb) * a.o_sn] =
+          lb < sb ? s_out[lb * kBm2Rows + rw] : -INFINITY;
+  }
+}
+
 template <typename T, int D>
 int launch_bmax(const BmaxK& k, hipStream_t st) {
   hipLaunchKernelGGL((block_max_kernel<T, D>), dim3((unsigned)((int64_t)k.a.B * k.ntiles * k.nslab)), dim3(kBmaxThreads), 0, st,
@@ -255,6 +469,33 @@ extern "C" int srswa_block_max_score(const srswa_blockmax_args* a, void* stream)
     return SRSWA_UNSUPPORTED;
   }
   hipStream_t s = reinterpret_cast<hipStream_t>(stream);
+  // the ring kernel addresses one sequence's keys with 32-bit byte offsets
+  const bool keys32 = ((int64_t)std::max(a->Sk - 1, 0) * a->k_sk + a->D) * eb < ((int64_t)1 << 32);
+  if (a->dtype != SRSWA_F32 && BS % kChunk == 0 && keys32) {
+    // 16-bit operands, whole-chunk blocks: the ring kernel (slabs of kBm2Slab chunks)
+    k.ntiles = ceil_div(a->C, kBm2Rows);
+    k.slab_chunks = cpb * ceil_div(kBm2Slab, cpb);
+    k.nslab = std::max(1, ceil_div(ceil_div(a->Sk, kChunk), k.slab_chunks));
+    const int64_t total = (int64_t)a->B * k.ntiles * k.nslab;
+    if (total > 0x7ffffff0) {
+      set_error("block max: grid too large");
+      return SRSWA_UNSUPPORTED;
+    }
+    const dim3 grid((unsigned)((total + 7) / 8 * 8));
+    if (a->dtype == SRSWA_BF16) {
+      if (a->D == 128) hipLaunchKernelGGL((block_max16_kernel<bf16_t, 128>), grid, dim3(kBm2Threads), 0, s, k);
+      else hipLaunchKernelGGL((block_max16_kernel<bf16_t, 64>), grid, dim3(kBm2Threads), 0, s, k);
+    } else {
+      if (a->D == 128) hipLaunchKernelGGL((block_max16_kernel<__half, 128>), grid, dim3(kBm2Threads), 0, s, k);
+      else hipLaunchKernelGGL((block_max16_kernel<__half, 64>), grid, dim3(kBm2Threads), 0, s, k);
+    }
+    const hipError_t e = hipGetLastError();
+    if (e != hipSuccess) {
+      set_error("block max launch failed: %s", hipGetErrorString(e));
+      return SRSWA_LAUNCH;
+    }
+    return SRSWA_OK;
+  }
   if (a->dtype == SRSWA_BF16) return a->D == 128 ? launch_bmax<bf16_t, 128>(k, s) : launch_bmax<bf16_t, 64>(k, s);
   if (a->dtype == SRSWA_F32) return a->D == 128 ? launch_bmax<float, 128>(k, s) : launch_bmax<float, 64>(k, s);
   return a->D == 128 ? launch_bmax<__half, 128>(k, s) : launch_bmax<__half, 64>(k, s);
