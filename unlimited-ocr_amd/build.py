@@ -77,7 +77,8 @@ def build(jobs: int | None = None, verbose: bool = False) -> str:
                 if warn and verbose:
                     print(warn, flush=True)
         tmp_out = OUT + ".tmp"
-        cmd = [hipcc(), f"--offload-arch={ARCH}", "-shared", "-fPIC", "-o", tmp_out, *objs]
+        # --no-undefined: a kernel whose host stub was not emitted fails here, not at load time
+        cmd = [hipcc(), f"--offload-arch={ARCH}", "-shared", "-fPIC", "-Wl,--no-undefined", "-o", tmp_out, *objs]
         if verbose:
             print(" ".join(cmd), flush=True)
         res = subprocess.run(cmd, capture_output=True, text=True)

@@ -209,8 +209,8 @@ __global__ __launch_bounds__(kBmaxThreads) void block_max_kernel(BmaxK p) {
 // and the vmcnt waits that count them.
 constexpr int kBm2Rows = 256;
 constexpr int kBm2Threads = 256;
-constexpr int kBm2Slab = 16;        // chunks per slab
-constexpr int kBm2Stages = 3;
+constexpr int kBm2Slab = 24;        // chunks per slab
+constexpr int kBm2Out = kBm2Slab + 1;   // staged maxima: row pitch (odd: no bank conflicts)
 
 template <int D> struct Bm2Layout {
   static constexpr int NP = D / 8;                    // 16-byte pieces per key row
@@ -222,12 +222,17 @@ template <int D> struct Bm2Layout {
 };
 
 // max of three (IEEE maxNum: a quiet NaN operand is ignored, like fmaxf);
-// written out because fmaxf on MFMA results first canonicalises every input
+// written out because fmaxf on MFMA results first canonicalises every input.
+// The compiler's hazard checks do not see into inline asm, so a caller that
+// feeds it MFMA results first waits them out with mfma_result_wait().
 __device__ __forceinline__ float max3f(float a, float b, float c) {
   float d;
-  asm("v_max3_f32 %0, %1, %2, %3" : "=v"(d) : "v"(a), "v"(b), "v"(c));
+  asm volatile("v_max3_f32 %0, %1, %2, %3" : "=v"(d) : "v"(a), "v"(b), "v"(c));
   return d;
 }
+// 20 wait states: a VALU read of an MFMA result needs the MFMA's passes + 2
+// (at most 18 for the 16-pass forms)
+__device__ __forceinline__ void mfma_result_wait() { asm volatile("s_nop 7\n\ts_nop 7\n\ts_nop 3"); }
 
 // s_waitcnt vmcnt(N), the other counters left alone (gfx9 encoding: vmcnt in
 // bits 3:0 and 15:14, expcnt 6:4, lgkmcnt 11:8)
@@ -244,7 +249,7 @@ __global__ __launch_bounds__(kBm2Threads, 2) void block_max16_kernel(BmaxK p) {
   __shared__ __align__(16) T sK0[L::kStage];
   __shared__ __align__(16) T sK1[L::kStage];
   __shared__ __align__(16) T sK2[L::kStage];
-  __shared__ float s_out[kBm2Slab * kBm2Rows];
+  __shared__ float s_out[kBm2Rows * kBm2Out];     // [row][block of the slab]
   __shared__ int s_maxls;
   const srswa_blockmax_args& a = p.a;
   const int tid = threadIdx.x, wave = tid / kWave, lane = tid % kWave;
@@ -257,7 +262,7 @@ __global__ __launch_bounds__(kBm2Threads, 2) void block_max16_kernel(BmaxK p) {
   const int tile = lid % p.ntiles;
   const int slab = (lid / p.ntiles) % p.nslab;
   const int b = lid / (p.ntiles * p.nslab);
-  const int BS = a.block_size, cpb = BS / kChunk;
+  const int cpb = a.block_size / kChunk;
 
   int ls[2], seg[2];
   bool ok[2];
@@ -265,29 +270,40 @@ __global__ __launch_bounds__(kBm2Threads, 2) void block_max16_kernel(BmaxK p) {
   for (int rt = 0; rt < 2; ++rt) {
     const int row = tile * kBm2Rows + wave * 64 + 32 * rt + rl;
     ok[rt] = row < a.C;
-    ls[rt] = 0;
-    seg[rt] = 0;
-    if (ok[rt]) {
-      const int pos = a.pos[(int64_t)b * a.pos_sb + (int64_t)row * a.pos_sc];
-      seg[rt] = a.seg ? a.seg[(int64_t)b * a.seg_sb + (int64_t)row * a.seg_sc] : 0;
-      ls[rt] = min(max(pos - (a.local_window - 1), 0), a.Sk);
-    }
+    const int pos = ok[rt] ? a.pos[(int64_t)b * a.pos_sb + (int64_t)row * a.pos_sc] : 0;
+    seg[rt] = ok[rt] && a.seg ? a.seg[(int64_t)b * a.seg_sb + (int64_t)row * a.seg_sc] : 0;
+    ls[rt] = ok[rt] ? min(max(pos - (a.local_window - 1), 0), a.Sk) : 0;
   }
-  if (tid == 0) s_maxls = 0;
-#pragma unroll
-  for (int i = 0; i < kBm2Slab; ++i) s_out[i * kBm2Rows + tid] = -INFINITY;
-  __syncthreads();
-  if (ok[0] || ok[1]) atomicMax(&s_maxls, max(ls[0], ls[1]));
-  __syncthreads();
-  const int nchunks = ceil_div(s_maxls, kChunk);   // no row has a remote key at or past this chunk
+
+  // the slab's first two chunks are requested before the rows' extent is known
+  // (a chunk past it is loaded for nothing; buffer loads past the keys read zeros)
   const int c_lo = slab * p.slab_chunks;
-  const int c_hi = min(c_lo + p.slab_chunks, nchunks);
-  const int blk_lo = c_lo / cpb;
-  const int blk_hi = slab == p.nslab - 1 ? a.nblk : min(a.nblk, (c_lo + p.slab_chunks) / cpb);
+  const int c_top = min(c_lo + p.slab_chunks, ceil_div(a.Sk, kChunk));
   const T* kg = reinterpret_cast<const T*>(a.k) + (int64_t)b * a.k_sb;
-  // the sequence's keys (the host checks that they span < 4 GiB)
+  // the sequence's keys (the host checks that a chunk past them stays < 4 GiB)
   const __amdgpu_buffer_rsrc_t krs =
       make_rsrc(kg, a.Sk > 0 ? (uint32_t)(((int64_t)(a.Sk - 1) * a.k_sk + D) * (int64_t)sizeof(T)) : 0u);
+  // load i of this thread fills the slot's 16-byte piece wave * 64 * LPT + 64 i + lane
+  // (a wave's load covers 1 KiB of the slot): key row r, swizzled piece
+  uint32_t voff[L::LPT];
+#pragma unroll
+  for (int i = 0; i < L::LPT; ++i) {
+    const int piece = (wave * L::LPT + i) * kWave + lane;
+    const int r = piece / L::NP, q = piece % L::NP;
+    voff[i] = (uint32_t)(((int64_t)r * a.k_sk + 8 * (q ^ ((r / L::RPL) % L::NP))) * (int64_t)sizeof(T));
+  }
+  const uint32_t chunk_bytes = (uint32_t)((int64_t)kChunk * a.k_sk * (int64_t)sizeof(T));
+  auto issue = [&](int c, T* slot) {
+    const uint32_t cb = (uint32_t)c * chunk_bytes;
+#pragma unroll
+    for (int i = 0; i < L::LPT; ++i) {
+      const uint32_t off = voff[i] + cb;
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(
+          krs, (__attribute__((address_space(3))) void*)(slot + (wave * L::LPT + i) * kWave * 8), 16, off, 0, 0, 0);
+    }
+  };
+  if (c_lo < c_top) issue(c_lo, sK0);
+  if (c_lo + 1 < c_top) issue(c_lo + 1, sK1);
 
   uint4 qf[2][NQ];
 #pragma unroll
@@ -299,21 +315,22 @@ __global__ __launch_bounds__(kBm2Threads, 2) void block_max16_kernel(BmaxK p) {
       qf[rt][ks] = ok[rt] ? *reinterpret_cast<const uint4*>(qrow + 16 * ks + 8 * h) : make_uint4(0, 0, 0, 0);
   }
 
-  // chunk c into a slot: load i of this thread fills the slot's 16-byte piece
-  // wave * 64 * LPT + 64 i + lane (a wave's load covers 1 KiB of the slot)
-  auto issue = [&](int c, T* slot) {
-#pragma unroll
-    for (int i = 0; i < L::LPT; ++i) {
-      const int piece = (wave * L::LPT + i) * kWave + lane;
-      const int r = piece / L::NP, q = piece % L::NP;
-      const int lp = q ^ ((r / L::RPL) % L::NP);
-      const int j = min(c * kChunk + r, a.Sk - 1);   // a tail chunk repeats the last key (masked below)
-      __builtin_amdgcn_raw_ptr_buffer_load_lds(
-          krs, (__attribute__((address_space(3))) void*)(slot + (wave * L::LPT + i) * kWave * 8), 16,
-          (uint32_t)(((int64_t)j * a.k_sk + 8 * lp) * (int64_t)sizeof(T)), 0, 0, 0);
-    }
-  };
+  // wave-uniform bounds: a chunk inside [wlo, whi) is scored whole by every row of the wave
+  const int wlo = wave_max_int(max(ok[0] ? seg[0] : INT_MIN, ok[1] ? seg[1] : INT_MIN));
+  const int whi = wave_min_int(min(ok[0] ? ls[0] : INT_MAX, ok[1] ? ls[1] : INT_MAX));
+  const int wls = wave_max_int(max(ls[0], ls[1]));
+  if (tid == 0) s_maxls = 0;
+  for (int i = tid; i < kBm2Rows * kBm2Out; i += kBm2Threads) s_out[i] = -INFINITY;
+  __syncthreads();
+  if (lane == 0) atomicMax(&s_maxls, wls);
+  __syncthreads();
+  const int c_hi = min(c_top, ceil_div(s_maxls, kChunk));   // no row has a remote key past this chunk
+  const int blk_lo = c_lo / cpb;
+  const int blk_hi = slab == p.nslab - 1 ? a.nblk : min(a.nblk, (c_lo + p.slab_chunks) / cpb);
+
   float run[2] = {-INFINITY, -INFINITY};
+  int cib = 0, lb = 0;                            // chunk inside the open block, its slab-local index
+  float* srow = s_out + (wave * 64 + 32 * h + rl) * kBm2Out;   // lane half h stages tile h's row
   auto compute = [&](int c, const T* slot) {
     const int j0 = c * kChunk;
     f32x16_t acc[2][2];
@@ -343,9 +360,8 @@ __global__ __launch_bounds__(kBm2Threads, 2) void block_max16_kernel(BmaxK p) {
       if (ks + 1 < NQ) __builtin_amdgcn_sched_group_barrier(0x100, 2, 0);   // step ks + 1's reads
       __builtin_amdgcn_sched_group_barrier(0x008, 4, 0);                    // step ks's MFMAs
     }
-    const bool whole = __all((!ok[0] || (j0 >= seg[0] && j0 + kChunk <= ls[0])) &&
-                             (!ok[1] || (j0 >= seg[1] && j0 + kChunk <= ls[1])));
-    if (whole) {
+    if (j0 >= wlo && j0 + kChunk <= whi) {
+      mfma_result_wait();
 #pragma unroll
       for (int rt = 0; rt < 2; ++rt) {
         float mx = max3f(run[rt], acc[rt][0][0], acc[rt][1][0]);
@@ -372,43 +388,51 @@ __global__ __launch_bounds__(kBm2Threads, 2) void block_max16_kernel(BmaxK p) {
         run[rt] = mx;
       }
     }
-    if (((c + 1) % cpb == 0) || (c == c_hi - 1)) {
-      // both lane halves end with both tiles' maxima; half h writes tile h
-      const float m0 = fmaxf(run[0], __shfl_xor(run[0], 32, kWave));
-      const float m1 = fmaxf(run[1], __shfl_xor(run[1], 32, kWave));
-      s_out[(c / cpb - blk_lo) * kBm2Rows + wave * 64 + 32 * h + rl] = h ? m1 : m0;
+    if (++cib == cpb || c == c_hi - 1) {
+      // both lane halves end with both tiles' maxima; half h stages tile h
+      const float m0 = xor32_max(run[0]), m1 = xor32_max(run[1]);
+      srow[lb] = h ? m1 : m0;
       run[0] = run[1] = -INFINITY;
+      cib = 0;
+      ++lb;
     }
   };
   // one step: chunk c's loads landed for every thread, slot `nxt` (read two
   // steps ago) refilled with chunk c + 2, chunk c scored from slot `cur`
   auto step = [&](int c, const T* cur, T* nxt) {
-    if (c + 1 < c_hi) wait_vm<L::LPT>(); else wait_vm<0>();
-    __syncthreads();
+    // chunk c + 1 is in flight (issued after chunk c) when the prologue asked for
+    // it or, later, when it lies before c_hi
+    if (c == c_lo ? c_lo + 1 < c_top : c + 1 < c_hi) wait_vm<L::LPT>(); else wait_vm<0>();
+    // an execution barrier only: the wait above already covers this thread's
+    // ring loads, and __syncthreads()'s fence would also wait for the chunk
+    // still in flight (LDS-DMA counts as an LDS store); the empty asm keeps
+    // the compiler from moving LDS accesses across it
+    asm volatile("" ::: "memory");
+    __builtin_amdgcn_s_barrier();
+    asm volatile("" ::: "memory");
     if (c + 2 < c_hi) issue(c + 2, nxt);
     compute(c, cur);
   };
-  if (c_lo < c_hi) issue(c_lo, sK0);
-  if (c_lo + 1 < c_hi) issue(c_lo + 1, sK1);
-  for (int c = c_lo; c < c_hi; c += kBm2Stages) {
+  for (int c = c_lo; c < c_hi; c += 3) {
     step(c, sK0, sK2);
     if (c + 1 >= c_hi) break;
     step(c + 1, sK1, sK0);
     if (c + 2 >= c_hi) break;
     step(c + 2, sK2, sK1);
   }
+  wait_vm<0>();      // a speculative chunk still in flight must land before the workgroup ends
   __syncthreads();
-  // the slab's blocks, row-major; blocks past the staged ones (the last slab's
-  // tail when nblk exceeds the keys) hold no key
+  // the slab's blocks: 16 lanes per row; blocks past the staged ones (the last
+  // slab's tail when nblk exceeds the keys) hold no key
   const int nb = blk_hi - blk_lo;
   const int sb = p.slab_chunks / cpb;
-  for (int e = tid; e < kBm2Rows * nb; e += kBm2Threads) {
-    const int rw = e / nb, lb = e % nb;
-    const int row = tile * kBm2Rows + rw;
-    if (row < a.C)
-      a.out[(int64_t)b * a.o_sb + (int64_t)row * a.o_sc + (int64_t)(blk_lo + lb) * a.o_sn] =
-          lb < sb ? s_out[lb * kBm2Rows + rw] : -INFINITY;
-  }
+  for (int k = tid & 15; k < nb; k += 16)
+    for (int rw = tid >> 4; rw < kBm2Rows; rw += kBm2Threads / 16) {
+      const int row = tile * kBm2Rows + rw;
+      if (row < a.C)
+        a.out[(int64_t)b * a.o_sb + (int64_t)row * a.o_sc + (int64_t)(blk_lo + k) * a.o_sn] =
+            k < sb ? s_out[rw * kBm2Out + k] : -INFINITY;
+    }
 }
 
 template <typename T, int D>
@@ -470,7 +494,7 @@ extern "C" int srswa_block_max_score(const srswa_blockmax_args* a, void* stream)
   }
   hipStream_t s = reinterpret_cast<hipStream_t>(stream);
   // the ring kernel addresses one sequence's keys with 32-bit byte offsets
-  const bool keys32 = ((int64_t)std::max(a->Sk - 1, 0) * a->k_sk + a->D) * eb < ((int64_t)1 << 32);
+  const bool keys32 = ((int64_t)(a->Sk + kChunk) * a->k_sk + a->D) * eb < ((int64_t)1 << 32);
   if (a->dtype != SRSWA_F32 && BS % kChunk == 0 && keys32) {
     // 16-bit operands, whole-chunk blocks: the ring kernel (slabs of kBm2Slab chunks)
     k.ntiles = ceil_div(a->C, kBm2Rows);
