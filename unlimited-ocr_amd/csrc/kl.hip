@@ -29,6 +29,7 @@
 // Backward (student path only, the teacher carries no gradient): tile
 // products on the matrix cores with ds = bf16(g dsel), see below.
 #include <algorithm>
+#include <mutex>
 
 #include <type_traits>
 
@@ -1280,6 +1281,55 @@ extern "C" int srswa_gather_kl_fwd_ws(const srswa_kl_args* a, void* scratch, siz
 namespace srswa {
 namespace {
 
+// The tile kernels (tiles whose rows share their selection) and the
+// block-major kernels (flagged tiles) write disjoint rows, and on per-row
+// selections the tile kernels occupy few CUs for a long time: they run on a
+// second default-priority stream per device, forked from the caller's stream
+// after the flag pass and joined back before the call returns.  One mutex
+// orders the event records of concurrent callers.
+struct KlSide {
+  hipStream_t s = nullptr;
+  hipEvent_t fork = nullptr, join = nullptr;
+};
+std::mutex g_side_mu;
+KlSide g_side[kMaxDevices];
+
+// the device's side stream and events (created on first use), or null
+KlSide* kl_side() {
+  int dev = -1;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDevices) return nullptr;
+  KlSide& sd = g_side[dev];
+  if (!sd.s) {
+    if (hipStreamCreateWithFlags(&sd.s, hipStreamNonBlocking) != hipSuccess) return nullptr;
+    if (hipEventCreateWithFlags(&sd.fork, hipEventDisableTiming) != hipSuccess ||
+        hipEventCreateWithFlags(&sd.join, hipEventDisableTiming) != hipSuccess)
+      return nullptr;
+  }
+  return &sd;
+}
+
+// launches `side_work` on the side stream beside `main_work` on st (both
+// after everything already queued on st); st then waits for both.  Without a
+// side stream both run on st in turn.
+template <typename SideF, typename MainF>
+hipError_t kl_fork(hipStream_t st, SideF side_work, MainF main_work) {
+  std::lock_guard<std::mutex> lock(g_side_mu);
+  KlSide* sd = kl_side();
+  if (!sd) {
+    side_work(st);
+    main_work(st);
+    return hipSuccess;   // launch errors are the caller's hipGetLastError()
+  }
+  hipError_t e = hipEventRecord(sd->fork, st);
+  if (e == hipSuccess) e = hipStreamWaitEvent(sd->s, sd->fork, 0);
+  if (e != hipSuccess) return e;
+  side_work(sd->s);
+  main_work(st);
+  e = hipEventRecord(sd->join, sd->s);
+  if (e == hipSuccess) e = hipStreamWaitEvent(st, sd->join, 0);
+  return e;
+}
+
 int kl_fwd_impl(const srswa_kl_args* a, void* scratch, size_t scratch_bytes, void* stream) {
   if (!a || !a->q_idx || !a->idx_k || !a->q_main || !a->k_main || !a->sel || !a->pos || !a->kl || !a->valid) {
     set_error("gather kl: null argument");
@@ -1367,31 +1417,47 @@ int kl_fwd_impl(const srswa_kl_args* a, void* scratch, size_t scratch_bytes, voi
   const dim3 grid((unsigned)(8 * k.per_xcd)), block(256);
   static LdsGrant granted[4];
   bool lds_ok = true;
-#define KL_LAUNCH(T_, D_, I_)                                                                    \
-  lds_ok = ensure_dynamic_lds(kl_fwd_kernel<T_, D_>, lds, &granted[I_]);                       \
-  if (lds_ok) hipLaunchKernelGGL((kl_fwd_kernel<T_, D_>), grid, block, lds, st, k);
+#define KL_GRANT(T_, D_, I_) lds_ok = ensure_dynamic_lds(kl_fwd_kernel<T_, D_>, lds, &granted[I_]);
   if (a->dtype == SRSWA_BF16) {
-    if (a->D == 128) { KL_LAUNCH(bf16_t, 128, 0) } else { KL_LAUNCH(bf16_t, 64, 1) }
+    if (a->D == 128) { KL_GRANT(bf16_t, 128, 0) } else { KL_GRANT(bf16_t, 64, 1) }
   } else {
-    if (a->D == 128) { KL_LAUNCH(__half, 128, 2) } else { KL_LAUNCH(__half, 64, 3) }
+    if (a->D == 128) { KL_GRANT(__half, 128, 2) } else { KL_GRANT(__half, 64, 3) }
   }
-#undef KL_LAUNCH
+#undef KL_GRANT
   if (!lds_ok) return SRSWA_LAUNCH;
-  if (scratch) {
+  auto tile_work = [&](hipStream_t s) {
+#define KL_LAUNCH(T_, D_) hipLaunchKernelGGL((kl_fwd_kernel<T_, D_>), grid, block, lds, s, k);
+    if (a->dtype == SRSWA_BF16) {
+      if (a->D == 128) { KL_LAUNCH(bf16_t, 128) } else { KL_LAUNCH(bf16_t, 64) }
+    } else {
+      if (a->D == 128) { KL_LAUNCH(__half, 128) } else { KL_LAUNCH(__half, 64) }
+    }
+#undef KL_LAUNCH
+  };
+  auto rs_work = [&](hipStream_t s) {
     const dim3 gp((unsigned)(8 * (int64_t)rk.per_xcd));
     const dim3 gr((unsigned)(((int64_t)a->B * a->HI * a->T + 255) / 256));
     const dim3 gc((unsigned)(((int64_t)a->B * a->HI * a->T * (k.G + 1) + 255) / 256));
-#define KL_RS(T_, D_)                                                                   \
-  hipLaunchKernelGGL((kl_rs_pass_kernel<T_, D_, false>), gp, dim3(128), 0, st, rk);    \
-  hipLaunchKernelGGL(kl_rs_combine_kernel, gc, dim3(256), 0, st, rk);                   \
-  hipLaunchKernelGGL((kl_rs_pass_kernel<T_, D_, true>), gp, dim3(128), 0, st, rk);     \
-  hipLaunchKernelGGL(kl_rs_final_kernel, gr, dim3(256), 0, st, rk);
+#define KL_RS(T_, D_)                                                                  \
+  hipLaunchKernelGGL((kl_rs_pass_kernel<T_, D_, false>), gp, dim3(128), 0, s, rk);    \
+  hipLaunchKernelGGL(kl_rs_combine_kernel, gc, dim3(256), 0, s, rk);                   \
+  hipLaunchKernelGGL((kl_rs_pass_kernel<T_, D_, true>), gp, dim3(128), 0, s, rk);     \
+  hipLaunchKernelGGL(kl_rs_final_kernel, gr, dim3(256), 0, s, rk);
     if (a->dtype == SRSWA_BF16) {
       if (a->D == 128) { KL_RS(bf16_t, 128) } else { KL_RS(bf16_t, 64) }
     } else {
       if (a->D == 128) { KL_RS(__half, 128) } else { KL_RS(__half, 64) }
     }
 #undef KL_RS
+  };
+  if (scratch) {
+    const hipError_t fe = kl_fork(st, tile_work, rs_work);
+    if (fe != hipSuccess) {
+      set_error("gather kl: side stream failed: %s", hipGetErrorString(fe));
+      return SRSWA_LAUNCH;
+    }
+  } else {
+    tile_work(st);
   }
   const hipError_t e = hipGetLastError();
   if (e != hipSuccess) {
@@ -1496,18 +1562,34 @@ extern "C" int srswa_gather_kl_bwd(const srswa_kl_bwd_args* a, void* scratch, si
   const dim3 grs((unsigned)(8 * (int64_t)k.per_xcd));
   const dim3 grd((unsigned)(((int64_t)a->B * a->HI * a->T * (a->D / 4) + 255) / 256));
   const size_t lds = a->D == 128 ? KlBwdLds<128>::bytes : KlBwdLds<64>::bytes;
+  // dQ of the unflagged tiles beside the block-major dQ and dK (disjoint outputs)
+  auto dq_work = [&](hipStream_t s) {
+#define KL_DQ(T_, D_) hipLaunchKernelGGL((kl_dq_kernel<T_, D_>), gdq, dim3(kBwdThreads), lds, s, k);
+    if (a->dtype == SRSWA_BF16) {
+      if (a->D == 128) { KL_DQ(bf16_t, 128) } else { KL_DQ(bf16_t, 64) }
+    } else {
+      if (a->D == 128) { KL_DQ(__half, 128) } else { KL_DQ(__half, 64) }
+    }
+#undef KL_DQ
+  };
+  auto rest_work = [&](hipStream_t s) {
 #define KL_BWD(T_, D_)                                                                      \
-  hipLaunchKernelGGL((kl_dq_kernel<T_, D_>), gdq, dim3(kBwdThreads), lds, st, k);          \
-  hipLaunchKernelGGL((kl_rs_dq_kernel<T_, D_>), grs, dim3(kBwdThreads), lds, st, k);       \
-  hipLaunchKernelGGL((kl_rs_dq_reduce_kernel<T_, D_>), grd, dim3(256), 0, st, k);          \
-  hipLaunchKernelGGL((kl_dk_kernel<T_, D_>), gdk, dim3(kBwdThreads), lds, st, k);          \
-  hipLaunchKernelGGL((kl_dk_reduce_kernel<T_, D_>), gdr, dim3(256), 0, st, k);
-  if (a->dtype == SRSWA_BF16) {
-    if (a->D == 128) { KL_BWD(bf16_t, 128) } else { KL_BWD(bf16_t, 64) }
-  } else {
-    if (a->D == 128) { KL_BWD(__half, 128) } else { KL_BWD(__half, 64) }
-  }
+  hipLaunchKernelGGL((kl_rs_dq_kernel<T_, D_>), grs, dim3(kBwdThreads), lds, s, k);        \
+  hipLaunchKernelGGL((kl_rs_dq_reduce_kernel<T_, D_>), grd, dim3(256), 0, s, k);           \
+  hipLaunchKernelGGL((kl_dk_kernel<T_, D_>), gdk, dim3(kBwdThreads), lds, s, k);           \
+  hipLaunchKernelGGL((kl_dk_reduce_kernel<T_, D_>), gdr, dim3(256), 0, s, k);
+    if (a->dtype == SRSWA_BF16) {
+      if (a->D == 128) { KL_BWD(bf16_t, 128) } else { KL_BWD(bf16_t, 64) }
+    } else {
+      if (a->D == 128) { KL_BWD(__half, 128) } else { KL_BWD(__half, 64) }
+    }
 #undef KL_BWD
+  };
+  const hipError_t fe = kl_fork(st, dq_work, rest_work);
+  if (fe != hipSuccess) {
+    set_error("gather kl backward: side stream failed: %s", hipGetErrorString(fe));
+    return SRSWA_LAUNCH;
+  }
   const hipError_t e = hipGetLastError();
   if (e != hipSuccess) {
     set_error("gather kl backward launch failed: %s", hipGetErrorString(e));
