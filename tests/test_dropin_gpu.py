@@ -161,6 +161,21 @@ def test_block_max_score_key_slabs(dev, bs, d):
     _check_block_max(got, q, k, pos, seg, bs, nblk, lw, f"block max key slabs bs={bs} d={d}")
 
 
+@pytest.mark.parametrize("sk", [50, 64, 129])
+def test_block_max_score_short_keys(dev, sk):
+    """Keys shorter than one or two 64-key chunks (a partial first chunk read
+    past the keys): rows at and past the end, window 1, two blocks past Sk."""
+    g = torch.Generator().manual_seed(900 + sk)
+    B, C, D, bs, lw = 2, 300, 128, 64, 1
+    q = torch.randn(B, C, D, generator=g).to(torch.bfloat16)
+    k = torch.randn(B, sk, D, generator=g).to(torch.bfloat16)
+    pos = torch.randint(0, sk + 40, (B, C), generator=g)
+    seg = torch.randint(0, max(1, sk // 2), (B, C), generator=g)
+    nblk = -(-sk // bs) + 2
+    got = SG.triton_block_max_score(q.to(dev), k.to(dev), pos.to(dev), seg.to(dev), bs, nblk, lw).cpu()
+    _check_block_max(got, q, k, pos, seg, bs, nblk, lw, f"block max short keys sk={sk}")
+
+
 @pytest.mark.parametrize("bs,d", [(64, 64), (128, 128)])
 def test_block_max_score_fp16_row_tiles(dev, bs, d):
     """fp16 operands over several 256-row query tiles (the last one partial),
