@@ -699,6 +699,16 @@ typedef struct {
   int32_t B, HI, HQ, HKV, T, Sk, D, K, block_size, local_window;
   float scaling;
   int32_t dtype;                                       /* srswa_dtype: bf16 or fp16       */
+  /* Optional second stream (hipStream_t) and two events (hipEvent_t) of the
+   * caller, all three or all NULL.  With them, srswa_gather_kl_fwd_ws runs the
+   * tile kernels on side_stream: fork_event is recorded on `stream` and waited
+   * on by side_stream, join_event is recorded on side_stream and waited on by
+   * `stream` before the call returns, so later work on `stream` sees every
+   * result.  Calls that share these handles must not overlap.  NULL: every
+   * kernel runs on `stream`. */
+  void* side_stream;
+  void* fork_event;
+  void* join_event;
 } srswa_kl_args;
 
 int srswa_gather_kl_fwd(const srswa_kl_args* a, void* stream);
@@ -729,6 +739,9 @@ typedef struct {
   void* dk_idx;       int64_t dk_sb, dk_st;            /* [B, Sk, D]                      */
   int32_t B, HI, T, Sk, D, K, block_size;
   int32_t dtype;
+  void* side_stream;   /* optional, as in srswa_kl_args: the unflagged tiles' dQ runs there */
+  void* fork_event;
+  void* join_event;
 } srswa_kl_bwd_args;
 
 /* Workspace, no initial content: per (row tile) a flag, per (head, key block)

@@ -133,3 +133,65 @@ def test_split_merge_is_deterministic(dev):
     for _ in range(2):
         out, lse = srswa.gather_decode(*args, **kw)
         assert torch.equal(out, first[0]) and torch.equal(lse, first[1])
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
+@pytest.mark.parametrize("K", [96, 200])
+def test_wide_slot_rows(dev, dtype, K):
+    """Rows of more than 64 slots take the kernel's wide-slot branch (slot
+    metadata re-read per unit, the duplicate scan over every earlier slot):
+    96 and 200 slots per row with repeated ids, invalid slots, ids of blocks
+    past q_pos and past the window start, random bias, GQA 2:1 and two decode
+    queries, against the oracle's _decode_attend restatement."""
+    g = torch.Generator().manual_seed(11 + K)
+    B, H, Hkv, Lq, D, BS, LW = 3, 4, 2, 2, 128, 16, 64
+    S = 6000
+    nblk = -(-S // BS)
+    q = torch.randn(B, H, Lq, D, generator=g).to(dtype)
+    k = torch.randn(B, Hkv, S, D, generator=g).to(dtype)
+    v = torch.randn(B, Hkv, S, D, generator=g).to(dtype)
+    q_pos = torch.tensor([[S - 2, S - 1], [3100, 3101], [700, 701]])
+    topi = torch.randint(0, nblk, (B, Lq, K), generator=g)
+    topi[:, :, 5] = topi[:, :, 2]                             # a repeat within the first 64 slots
+    topi[:, :, 70] = topi[:, :, 3]                            # a repeat beyond slot 64 of an early slot
+    topi[:, :, K - 1] = topi[:, :, 80]                        # a repeat between two wide slots
+    topi[1, :, 90] = q_pos[1, 0] // BS                        # overlaps the window
+    bias = torch.randn(B, Lq, K, generator=g)
+    valid = torch.rand(B, Lq, K, generator=g) > 0.25
+    valid[:, :, 3] = False                                    # the repeated id's first holder is invalid
+    ref = O.decode_attend(q.double(), k.double(), v.double(), topi, bias.double(), valid, q_pos,
+                          BS, LW, 1 / math.sqrt(D))
+    out = srswa.decode_attend(q.to(dev), k.to(dev), v.to(dev), topi.to(dev), bias.to(dev),
+                              valid.to(dev), q_pos.to(dev), BS, LW, 1 / math.sqrt(D)).cpu()
+    if dtype == torch.float32:
+        report(f"[err] decode wide slots K={K} fp32: max rel {_rel(out, ref):.3e} (bar {F32_REL})")
+        assert _rel(out, ref) <= F32_REL, _rel(out, ref)
+    else:
+        from tolerance import assert_close_lowp
+        assert_close_lowp(out, ref, dtype, BF16_TOL, f"decode wide slots K={K} bf16")
+
+
+@pytest.mark.parametrize("K", [96, 200])
+def test_wide_slot_gather_form(dev, K):
+    """Per-head block lists of 96 / 200 slots in the config-3 gather form
+    (contiguous [B,L,H,D] cache, ragged kv_len), -1 padding and repeats,
+    against the gather-form oracle."""
+    g = torch.Generator().manual_seed(21 + K)
+    B, H, D, L, BS, LW = 3, 4, 128, 16384, 64, 512
+    q = torch.randn(B, H, D, generator=g).to(torch.bfloat16)
+    kc = torch.randn(B, L, H, D, generator=g).to(torch.bfloat16)
+    vc = torch.randn(B, L, H, D, generator=g).to(torch.bfloat16)
+    q_pos = torch.tensor([L - 1, 14000, 13500])
+    idx = torch.empty(B, H, K, dtype=torch.int64)
+    for b in range(B):
+        top = (int(q_pos[b]) - LW + 1) // BS                   # blocks fully below the window
+        for h in range(H):
+            idx[b, h] = torch.randperm(top, generator=g)[:K]
+    idx[:, :, 77] = idx[:, :, 6]                              # repeat of an early slot
+    idx[:, :, K - 2:] = -1                                    # padding
+    idx[0, 1, 100 % K] = -1
+    ref = O.decode_attend_gather(q, kc, vc, idx, q_pos, BS, LW, 1 / math.sqrt(D))
+    out = srswa.gather_decode(q.to(dev), kc.to(dev), vc.to(dev), idx.to(dev), q_pos.to(dev),
+                              block_size=BS, local_window=LW, scale=1 / math.sqrt(D)).cpu()
+    from tolerance import assert_close_lowp
+    assert_close_lowp(out, ref.double(), torch.bfloat16, BF16_TOL, f"gather decode wide slots K={K}")

@@ -2,9 +2,9 @@
 CPU oracle cannot evaluate every row: sampled rows against the oracle, and
 size-independent identities of the backward over every key.
 
-* config 2 (indexer, B=32, L=32768): three whole sequences against the
-  oracle, block ids bit-exact outside near-ties, scores within 1e-5.
-* config 3 (decode, B=64, KV up to 128k): three sequences x 10 heads against
+* config 2 (indexer, B=32, L=32768): every sequence (all 320 id rows)
+  against the oracle, block ids bit-exact outside near-ties, scores within 1e-5.
+* config 3 (decode, B=64, KV up to 128k): every sequence x 10 heads against
   the gather-form oracle, bf16 within 2e-2.
 * config 4 (prefill, 2048 of 65536 keys) and config 5 (self-attention,
   T=16384): sampled rows (tile edges, the first / last rows, random ones) x all
@@ -77,13 +77,16 @@ def _check_fwd_rows(c, o, lse, T, Sk, rows, dev, label):
         assert (lse[b, r].cpu().double() - rl).abs().max().item() <= 2e-2
 
 
-def test_cfg2_full_indexer_sampled_sequences(dev):
+def test_cfg2_full_indexer_every_sequence(dev):
     c = W.indexer_config(B=32, H=10, D=128, L=32768, device=dev)
     LB, K = LW // BS, 8
     idx, sc = srswa.index_meanpool_topk(c["q"], c["k"], c["q_pos"].to(dev), block_size=BS, local_blocks=LB,
                                         topk=K, return_scores=True)
-    for b in (0, 17, 31):
-        print(f"config 2 full: sequence {b}", flush=True)
+    B = c["q"].shape[0]
+    got_all, ref_all = [], []
+    for b in range(B):
+        if b % 8 == 0:
+            print(f"config 2 full: sequence {b}", flush=True)
         q = c["q"][b:b + 1].cpu()
         k = c["k"][b:b + 1].cpu().float()
         ref = O.meanpool_block_scores(q[:, :, None, :], k.permute(0, 2, 1, 3), c["q_pos"][b:b + 1].cpu()[:, None],
@@ -93,21 +96,27 @@ def test_cfg2_full_indexer_sampled_sequences(dev):
         assert torch.equal(got > O.SCORE_NEG * 0.5, valid)
         scale = ref.abs().masked_fill(~valid, 0).amax(-1, keepdim=True).clamp(min=1.0)
         assert ((got - ref.double()).abs() / scale).masked_fill(~valid, 0).max().item() <= 1e-5
-        compare_selection(idx[b:b + 1].cpu()[:, :, None], ref, K, f"config 2 full size, sequence {b}")
+        got_all.append(idx[b:b + 1].cpu()[:, :, None])
+        ref_all.append(ref)
+    # one selection bar over all B x 10 rows
+    compare_selection(torch.cat(got_all), torch.cat(ref_all), K, f"config 2 full size, all {B} sequences")
 
 
-def test_cfg3_full_decode_sampled_sequences(dev):
+def test_cfg3_full_decode_every_sequence(dev):
     c = W.decode_config(device=dev)
     B = c["q"].shape[0]
     out = srswa.gather_decode(c["q"].to(dev), c["k_cache"], c["v_cache"], c["block_idx"].to(dev),
                               c["q_pos"].to(dev), block_size=BS, local_window=LW, scale=1.0 / math.sqrt(128))
-    for b in (0, B // 2, B - 1):
-        print(f"config 3 full: sequence {b}", flush=True)
+    refs = []
+    for b in range(B):
+        if b % 8 == 0:
+            print(f"config 3 full: sequence {b}", flush=True)
         Lb = int(c["seq_lens"][b])
-        ref = O.decode_attend_gather(c["q"][b:b + 1].cpu(), c["k_cache"][b:b + 1, :Lb].cpu(),
-                                     c["v_cache"][b:b + 1, :Lb].cpu(), c["block_idx"][b:b + 1],
-                                     c["q_pos"][b:b + 1], BS, LW, 1.0 / math.sqrt(128))
-        assert_close_lowp(out[b:b + 1].cpu(), ref.double(), torch.bfloat16, 2e-2, f"config 3 full decode, sequence {b}")
+        refs.append(O.decode_attend_gather(c["q"][b:b + 1].cpu(), c["k_cache"][b:b + 1, :Lb].cpu(),
+                                           c["v_cache"][b:b + 1, :Lb].cpu(), c["block_idx"][b:b + 1],
+                                           c["q_pos"][b:b + 1], BS, LW, 1.0 / math.sqrt(128)))
+    assert_close_lowp(out.cpu(), torch.cat(refs).double(), torch.bfloat16, 2e-2,
+                      f"config 3 full decode, all {B} sequences x 10 heads")
 
 
 def test_cfg4_full_prefill_sampled_rows(dev):

@@ -130,6 +130,44 @@ def test_row_sparse_and_tile_paths_agree(dev):
     assert_close_lowp(kd.grad.cpu(), kr.grad, dtype, what="d idx_k (mixed tiles)")
 
 
+def test_side_stream_is_the_callers_and_optional(dev):
+    """The row-sparse forward and the backward take the second stream and its
+    two events from the caller (srswa_kl_args / srswa_kl_bwd_args): with them
+    and without them (every kernel on the current stream) the results are the
+    same bits and match the oracle; handing over only some of the three is
+    rejected before anything is launched."""
+    import ctypes
+    from srswa import _lib, kl as KL
+    B, HI, G, HKV, T, Sk, D, topk, dtype = 1, 1, 2, 2, 1100, 1500, 128, 6, torch.bfloat16
+    q_idx, idx_k, q_main, k_main, sel, pos, seg, scaling = _case(31, B, HI, G, HKV, T, Sk, D, topk, dtype)
+    g = torch.Generator().manual_seed(32)
+    nblk = -(-Sk // 64)
+    for tau in range(0, -(-T // 64), 2):                  # mixed tiles: both kernel families run
+        sel[:, :, 64 * tau:64 * tau + 64] = torch.randperm(nblk, generator=g)[:topk].to(torch.int32)
+    lw = 128
+    args = (q_idx.to(dev), idx_k.to(dev), q_main.to(dev), k_main.to(dev), sel.to(dev), pos.to(dev))
+    two = KL.kl_forward(*args, block_size=64, local_window=lw, scaling=scaling, side_stream=True)
+    one = KL.kl_forward(*args, block_size=64, local_window=lw, scaling=scaling, side_stream=False)
+    for x, y in zip(two, one):
+        assert torch.equal(x, y)
+    grad = torch.randn(B, HI, T, generator=g).to(dev)
+    dq2, dk2 = KL.kl_backward(grad, args[0], args[1], args[4], two[2], block_size=64, side_stream=True)
+    dq1, dk1 = KL.kl_backward(grad, args[0], args[1], args[4], one[2], block_size=64, side_stream=False)
+    assert torch.equal(dq2, dq1) and torch.equal(dk2, dk1)
+    rk, rv = K.gather_kl_dense(q_idx.double(), idx_k.double(), q_main.double(), k_main.double(), sel, pos,
+                               block_size=64, local_window=lw, scaling=scaling, seg=None, round_dtype=dtype)
+    assert torch.equal(one[1].cpu(), rv)
+    assert ((one[0].cpu().double() - rk).abs() - 1e-3 * rk.abs()).max().item() <= 2e-3
+    # a stream without its events is refused (nothing launched)
+    s, _, _ = KL.side_channel(args[0].device)
+    a = _lib.KlBwdArgs(B=B, HI=HI, T=T, Sk=Sk, D=D, K=topk, block_size=64, dtype=_lib.dtype_code(dtype),
+                       q_idx=args[0].data_ptr(), idx_k=args[1].data_ptr(), sel=args[4].data_ptr(),
+                       dsel=one[2].data_ptr(), grad=grad.data_ptr(), dq_idx=dq1.data_ptr(), dk_idx=dk1.data_ptr(),
+                       side_stream=s.cuda_stream)
+    rc = _lib.lib().srswa_gather_kl_bwd(ctypes.byref(a), None, 0, _lib.stream_ptr(args[0].device))
+    assert rc == 2, rc                                    # SRSWA_INVALID
+
+
 @pytest.mark.parametrize("case", CASES[:3])
 def test_backward(dev, case):
     seed, B, HI, G, HKV, T, Sk, D, topk, dtype, packed, dup = case

@@ -29,6 +29,9 @@ def _case(seed, R, dql, H, Hkv, D, page, nb, K, lb, dtype, with_bias, kv=None):
     sl[0] = nb * page                                     # a full table
     topk = torch.randint(-1, nb, (Hkv, R * dql, K), generator=g).to(torch.int32)
     topk[:, 0, 1] = topk[:, 0, 0]                        # a repeated id
+    if K > 64:
+        topk[:, :, 70] = topk[:, :, 2]                   # a wide slot repeating an early one
+        topk[:, :, K - 1] = topk[:, :, 90]               # two wide slots holding one id
     bias = torch.randn(Hkv, R * dql, K, generator=g) if with_bias else None
     return q, kc, vc, topk, bias, bt, sl
 
@@ -56,6 +59,14 @@ CASES = {
                                   with_bias=False, kv=torch.float8_e4m3fnuz),
     "fp8_e5m2fnuz_d64_p128": dict(R=2, dql=1, H=4, Hkv=1, D=64, page=128, nb=10, K=4, lb=2, dtype=torch.bfloat16,
                                   with_bias=True, kv=torch.float8_e5m2fnuz),
+    # rows of more than 64 slots (the kernel's wide-slot branch): repeats, -1
+    # slots and ids of blocks past seq_len among 96 / 200 slots
+    "bf16_p16_wide96_dql2": dict(R=3, dql=2, H=8, Hkv=2, D=128, page=16, nb=300, K=96, lb=4,
+                                 dtype=torch.bfloat16, with_bias=True),
+    "bf16_p32_wide200": dict(R=2, dql=1, H=4, Hkv=4, D=128, page=32, nb=260, K=200, lb=8,
+                             dtype=torch.bfloat16, with_bias=True),
+    "fp32_p16_wide200_nobias": dict(R=2, dql=1, H=4, Hkv=2, D=128, page=16, nb=240, K=200, lb=2,
+                                    dtype=torch.float32, with_bias=False),
 }
 
 

@@ -230,9 +230,18 @@ __device__ __forceinline__ float max3f(float a, float b, float c) {
   asm volatile("v_max3_f32 %0, %1, %2, %3" : "=v"(d) : "v"(a), "v"(b), "v"(c));
   return d;
 }
-// 20 wait states: a VALU read of an MFMA result needs the MFMA's passes + 2
-// (at most 18 for the 16-pass forms)
-__device__ __forceinline__ void mfma_result_wait() { asm volatile("s_nop 7\n\ts_nop 7\n\ts_nop 3"); }
+// A VALU read of an MFMA result needs the MFMA's passes + 2 wait states; the
+// 32x32 16-bit MFMAs take at most 16 passes.  s_nop N waits N + 1 states.
+constexpr int kMfmaMaxPasses = 16;
+constexpr int kMfmaReadWait = kMfmaMaxPasses + 2;
+constexpr int kNopWaits = (7 + 1) + (7 + 1) + (3 + 1);
+static_assert(kNopWaits >= kMfmaReadWait, "s_nop sequence shorter than the MFMA read hazard");
+// The wait takes one result register of each of the four MFMAs as operands, so
+// it cannot be scheduled before any of them has issued; the max3f statements
+// are volatile asm too, so they stay after it in program order.
+__device__ __forceinline__ void mfma_result_wait(float r0, float r1, float r2, float r3) {
+  asm volatile("s_nop 7\n\ts_nop 7\n\ts_nop 3" ::"v"(r0), "v"(r1), "v"(r2), "v"(r3));
+}
 
 // s_waitcnt vmcnt(N), the other counters left alone (gfx9 encoding: vmcnt in
 // bits 3:0 and 15:14, expcnt 6:4, lgkmcnt 11:8)
@@ -361,7 +370,7 @@ __global__ __launch_bounds__(kBm2Threads, 2) void block_max16_kernel(BmaxK p) {
       __builtin_amdgcn_sched_group_barrier(0x008, 4, 0);                    // step ks's MFMAs
     }
     if (j0 >= wlo && j0 + kChunk <= whi) {
-      mfma_result_wait();
+      mfma_result_wait(acc[0][0][15], acc[0][1][15], acc[1][0][15], acc[1][1][15]);
 #pragma unroll
       for (int rt = 0; rt < 2; ++rt) {
         float mx = max3f(run[rt], acc[rt][0][0], acc[rt][1][0]);

@@ -29,7 +29,6 @@
 // Backward (student path only, the teacher carries no gradient): tile
 // products on the matrix cores with ds = bf16(g dsel), see below.
 #include <algorithm>
-#include <mutex>
 
 #include <type_traits>
 
@@ -1283,50 +1282,48 @@ namespace {
 
 // The tile kernels (tiles whose rows share their selection) and the
 // block-major kernels (flagged tiles) write disjoint rows, and on per-row
-// selections the tile kernels occupy few CUs for a long time: they run on a
-// second default-priority stream per device, forked from the caller's stream
-// after the flag pass and joined back before the call returns.  One mutex
-// orders the event records of concurrent callers.
+// selections the tile kernels occupy few CUs for a long time.  When the caller
+// passes a second stream and two events, the tile kernels run on that stream,
+// forked from the caller's stream after the flag pass and joined back before
+// the call returns; without them everything runs on the caller's stream in
+// turn.  The library owns no stream or event and keeps no state between calls.
 struct KlSide {
-  hipStream_t s = nullptr;
-  hipEvent_t fork = nullptr, join = nullptr;
+  hipStream_t s;
+  hipEvent_t fork, join;
 };
-std::mutex g_side_mu;
-KlSide g_side[kMaxDevices];
 
-// the device's side stream and events (created on first use), or null
-KlSide* kl_side() {
-  int dev = -1;
-  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDevices) return nullptr;
-  KlSide& sd = g_side[dev];
-  if (!sd.s) {
-    if (hipStreamCreateWithFlags(&sd.s, hipStreamNonBlocking) != hipSuccess) return nullptr;
-    if (hipEventCreateWithFlags(&sd.fork, hipEventDisableTiming) != hipSuccess ||
-        hipEventCreateWithFlags(&sd.join, hipEventDisableTiming) != hipSuccess)
-      return nullptr;
+// the caller's side stream and events: all three or none
+bool kl_side_of(void* s, void* fork, void* join, const char* what, KlSide* out) {
+  if (!s && !fork && !join) {
+    *out = KlSide{nullptr, nullptr, nullptr};
+    return true;
   }
-  return &sd;
+  if (!s || !fork || !join) {
+    set_error("%s: side_stream, fork_event and join_event are given together or not at all", what);
+    return false;
+  }
+  *out = KlSide{reinterpret_cast<hipStream_t>(s), reinterpret_cast<hipEvent_t>(fork),
+                reinterpret_cast<hipEvent_t>(join)};
+  return true;
 }
 
 // launches `side_work` on the side stream beside `main_work` on st (both
 // after everything already queued on st); st then waits for both.  Without a
 // side stream both run on st in turn.
 template <typename SideF, typename MainF>
-hipError_t kl_fork(hipStream_t st, SideF side_work, MainF main_work) {
-  std::lock_guard<std::mutex> lock(g_side_mu);
-  KlSide* sd = kl_side();
-  if (!sd) {
+hipError_t kl_fork(hipStream_t st, const KlSide& sd, SideF side_work, MainF main_work) {
+  if (!sd.s) {
     side_work(st);
     main_work(st);
     return hipSuccess;   // launch errors are the caller's hipGetLastError()
   }
-  hipError_t e = hipEventRecord(sd->fork, st);
-  if (e == hipSuccess) e = hipStreamWaitEvent(sd->s, sd->fork, 0);
+  hipError_t e = hipEventRecord(sd.fork, st);
+  if (e == hipSuccess) e = hipStreamWaitEvent(sd.s, sd.fork, 0);
   if (e != hipSuccess) return e;
-  side_work(sd->s);
+  side_work(sd.s);
   main_work(st);
-  e = hipEventRecord(sd->join, sd->s);
-  if (e == hipSuccess) e = hipStreamWaitEvent(st, sd->join, 0);
+  e = hipEventRecord(sd.join, sd.s);
+  if (e == hipSuccess) e = hipStreamWaitEvent(st, sd.join, 0);
   return e;
 }
 
@@ -1342,6 +1339,8 @@ int kl_fwd_impl(const srswa_kl_args* a, void* scratch, size_t scratch_bytes, voi
   }
   int rc = check_common(a->dtype, a->D, a->block_size, a->K, "gather kl");
   if (rc != SRSWA_OK) return rc;
+  KlSide side;
+  if (!kl_side_of(a->side_stream, a->fork_event, a->join_event, "gather kl", &side)) return SRSWA_INVALID;
   const int eb = 2;
   bool ok = al16(a->q_idx) && al16(a->idx_k) && al16(a->q_main) && al16(a->k_main) && (!a->dsel || al16(a->dsel));
   for (int64_t st : {a->qi_sb, a->qi_sh, a->qi_st, a->ik_sb, a->ik_st, a->qm_sb, a->qm_sh, a->qm_st, a->km_sb,
@@ -1451,7 +1450,7 @@ int kl_fwd_impl(const srswa_kl_args* a, void* scratch, size_t scratch_bytes, voi
 #undef KL_RS
   };
   if (scratch) {
-    const hipError_t fe = kl_fork(st, tile_work, rs_work);
+    const hipError_t fe = kl_fork(st, side, tile_work, rs_work);
     if (fe != hipSuccess) {
       set_error("gather kl: side stream failed: %s", hipGetErrorString(fe));
       return SRSWA_LAUNCH;
@@ -1514,6 +1513,8 @@ extern "C" int srswa_gather_kl_bwd(const srswa_kl_bwd_args* a, void* scratch, si
   }
   int rc = check_common(a->dtype, a->D, a->block_size, a->K, "gather kl backward");
   if (rc != SRSWA_OK) return rc;
+  KlSide side;
+  if (!kl_side_of(a->side_stream, a->fork_event, a->join_event, "gather kl backward", &side)) return SRSWA_INVALID;
   bool ok = al16(a->q_idx) && al16(a->idx_k) && al16(a->dsel) && ((uintptr_t)a->dq_idx & 7u) == 0;
   for (int64_t st : {a->qi_sb, a->qi_sh, a->qi_st, a->ik_sb, a->ik_st}) ok = ok && (st * 2) % 16 == 0;
   for (int64_t st : {a->dq_sb, a->dq_sh, a->dq_st, a->dk_sb, a->dk_st}) ok = ok && (st * 2) % 8 == 0;   // 4-element stores
@@ -1585,7 +1586,7 @@ extern "C" int srswa_gather_kl_bwd(const srswa_kl_bwd_args* a, void* scratch, si
     }
 #undef KL_BWD
   };
-  const hipError_t fe = kl_fork(st, dq_work, rest_work);
+  const hipError_t fe = kl_fork(st, side, dq_work, rest_work);
   if (fe != hipSuccess) {
     set_error("gather kl backward: side stream failed: %s", hipGetErrorString(fe));
     return SRSWA_LAUNCH;

@@ -38,12 +38,43 @@ def _keys(idx_k: torch.Tensor) -> torch.Tensor:
     return idx_k[:, 0] if idx_k.dim() == 4 else idx_k
 
 
+_SIDE: dict = {}
+
+
+def side_channel(device):
+    """(stream, fork event, join event) handles of ``device``, passed to the
+    KL entry points so that their tile kernels run beside the block-major
+    ones.  They belong to this module (the C library owns no stream or event):
+    created once per device with the default stream priority, on the first
+    call that asks for them -- make that call before any graph capture."""
+    idx = device.index if device.index is not None else torch.cuda.current_device()
+    sc = _SIDE.get(idx)
+    if sc is None:
+        with torch.cuda.device(idx):
+            s = torch.cuda.Stream(device=idx)
+            fork, join = torch.cuda.Event(), torch.cuda.Event()
+            fork.record(s)                           # torch creates an event on its first record
+            join.record(s)
+        sc = _SIDE[idx] = (s, fork, join)
+    return sc
+
+
+def _side_fields(device, use: bool) -> dict:
+    if not use:
+        return dict(side_stream=None, fork_event=None, join_event=None)
+    s, fork, join = side_channel(device)
+    return dict(side_stream=s.cuda_stream, fork_event=fork.cuda_event, join_event=join.cuda_event)
+
+
 def kl_forward(q_idx, idx_k, q_main, k_main, sel, pos, *, block_size, local_window, scaling, seg=None,
-               with_dsel=True, row_sparse=True):
+               with_dsel=True, row_sparse=True, side_stream=True):
     """(kl [B, HI, T] fp32, valid [B, HI, T] bool, dsel [B, HI, T, K, 64] fp32 or None).
     ``row_sparse``: tiles whose rows select unrelated blocks are computed
     block-major (srswa_gather_kl_fwd_ws); False runs every tile on the tile
-    kernel (srswa_gather_kl_fwd)."""
+    kernel (srswa_gather_kl_fwd).  ``side_stream``: the row-sparse call runs
+    its tile kernels on this module's second stream (``side_channel``), forked
+    from and joined back to the current stream; False keeps every kernel on
+    the current stream."""
     _cuda(q_idx, idx_k, q_main, k_main, sel, pos, seg)
     q_idx, q_main, k_main = _inner(q_idx), _inner(q_main), _inner(k_main)
     ik = _inner(_keys(idx_k))
@@ -72,7 +103,8 @@ def kl_forward(q_idx, idx_k, q_main, k_main, sel, pos, *, block_size, local_wind
         dsel=_lib.ptr(dsel), ds_sb=0 if dsel is None else dsel.stride(0),
         ds_sh=0 if dsel is None else dsel.stride(1), ds_st=0 if dsel is None else dsel.stride(2),
         B=B, HI=HI, HQ=HQ, HKV=HKV, T=T, Sk=Sk, D=D, K=K, block_size=int(block_size),
-        local_window=int(local_window), scaling=float(scaling), dtype=_lib.dtype_code(q_idx.dtype))
+        local_window=int(local_window), scaling=float(scaling), dtype=_lib.dtype_code(q_idx.dtype),
+        **_side_fields(q_idx.device, side_stream and row_sparse))
     # with a workspace, tiles whose rows select unrelated blocks are taken by
     # the block-major (row-sparse) kernels instead of the tile kernel
     need = _lib.lib().srswa_gather_kl_fwd_workspace(ctypes.byref(a)) if row_sparse else 0
@@ -86,8 +118,9 @@ def kl_forward(q_idx, idx_k, q_main, k_main, sel, pos, *, block_size, local_wind
     return kl, valid, dsel
 
 
-def kl_backward(grad, q_idx, idx_k, sel, dsel, *, block_size):
-    """(d q_idx like q_idx, d idx_k like idx_k) for d loss / d kl = grad [B, HI, T]."""
+def kl_backward(grad, q_idx, idx_k, sel, dsel, *, block_size, side_stream=True):
+    """(d q_idx like q_idx, d idx_k like idx_k) for d loss / d kl = grad [B, HI, T].
+    ``side_stream`` as in ``kl_forward``."""
     _cuda(grad, q_idx, idx_k, sel, dsel)
     qi = _inner(q_idx)
     ik = _inner(_keys(idx_k))
@@ -105,7 +138,8 @@ def kl_backward(grad, q_idx, idx_k, sel, dsel, *, block_size):
         grad=g.data_ptr(), g_sb=g.stride(0), g_sh=g.stride(1),
         dq_idx=dq.data_ptr(), dq_sb=dq.stride(0), dq_sh=dq.stride(1), dq_st=dq.stride(2),
         dk_idx=dk.data_ptr(), dk_sb=dk.stride(0), dk_st=dk.stride(1),
-        B=B, HI=HI, T=T, Sk=Sk, D=D, K=s.shape[-1], block_size=int(block_size), dtype=_lib.dtype_code(qi.dtype))
+        B=B, HI=HI, T=T, Sk=Sk, D=D, K=s.shape[-1], block_size=int(block_size), dtype=_lib.dtype_code(qi.dtype),
+        **_side_fields(qi.device, side_stream))
     need = ctypes.c_size_t()
     _lib.check(_lib.lib().srswa_gather_kl_bwd_workspace(ctypes.byref(a), ctypes.byref(need)),
                "srswa_gather_kl_bwd_workspace")
@@ -157,7 +191,10 @@ class KLChunkFn:
         del group, kv_group                    # implied by the head counts of the operands
         lw = block_size if local_window is None else local_window
         nblk = keep_block.shape[-1]
-        K = max(1, int(keep_block.sum(-1).max()))
+        # slots per row: every block when there are at most 64 (no read-back);
+        # beyond that the widest row's count is read back once per chunk (the
+        # kernels take at most 64 slots, wider rows go to the original)
+        K = nblk if nblk <= 64 else max(1, int(keep_block.sum(-1).max()))
         ar = torch.arange(nblk, device=keep_block.device, dtype=torch.int32)
         ids = torch.where(keep_block, ar, torch.full_like(ar, -1))
         sel = ids.topk(min(K, nblk), dim=-1).values

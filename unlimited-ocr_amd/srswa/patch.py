@@ -56,6 +56,23 @@ def head_cls_block_scores(idx_q, idx_k, q_pos, nblk, block_size, local_blocks, h
     return scores[:, 0]
 
 
+_HC_ZERO: dict = {}
+
+
+def _head_cls_or_none(param):
+    """head_cls as fp32, or None while it is all zero (zero head_cls weights
+    every valid key of a block equally: the mean-pool kernel path).  The zero
+    test reads the device once per parameter version (an optimizer step bumps
+    the version), not on every decode step."""
+    key = (id(param), param.data_ptr(), param._version)
+    zero = _HC_ZERO.get(key)
+    if zero is None:
+        if len(_HC_ZERO) > 256:
+            _HC_ZERO.clear()
+        zero = _HC_ZERO[key] = not bool(param.detach().any())
+    return None if zero else param.detach().float()
+
+
 def _rebind(owner, name: str, make, done: list, label: str) -> None:
     """owner.name = make(original); the original is kept once as
     owner._srswa_orig_<name> so ``restore`` can put it back."""
@@ -248,10 +265,8 @@ def apply(modeling_deepseekv2, modeling_unlimitedocr=None) -> list:
             stage0 = getattr(router, "stage0", None)
             if idx_q.is_cuda and stage0 == "head_cls":
                 try:
-                    hc = router.head_cls.detach().float()
-                    hc = None if not bool(hc.any()) else hc      # zero head_cls == mean pooling
                     return head_cls_block_scores(idx_q, idx_k, q_pos, nblk, router.block_size,
-                                                 router.local_blocks, hc)
+                                                 router.local_blocks, _head_cls_or_none(router.head_cls))
                 except UnsupportedShape:
                     pass
             elif idx_q.is_cuda and stage0 == "indexer":
