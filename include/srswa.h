@@ -751,6 +751,101 @@ typedef struct {
 int srswa_gather_kl_bwd_workspace(const srswa_kl_bwd_args* a, size_t* scratch_bytes);
 int srswa_gather_kl_bwd(const srswa_kl_bwd_args* a, void* scratch, size_t scratch_bytes, void* stream);
 
+/* ------------------------------------------------------------------------
+ * DASH training scorer, stage0 "head_cls": DashAttention._block_scores_headcls
+ * (HF/dash_attention.py:1053-1143) from its fp32 index queries / keys (the
+ * output of the projections, RMSNorms, RoPE and nan_to_num, :1063-1074, which
+ * stay the caller's) and head_cls.  Block c holds keys [c BS, min(c BS + BS, S));
+ *   pre_t = k_t . hc / sqrt(D), aw_t = clamp(pre_t, +-1e4), m = max valid aw (0 if none),
+ *   e_t = exp(aw_t - m), w_t = e_t / max(sum e, 1e-6), kbar_c = nan_to_num(sum_t w_t k_t)
+ *   z[b, i, c] = clamp(q_i . kbar_c / sqrt(D), +-1e4) when c <= pos[b, i] / BS - local_blocks
+ *                and c BS < S, else -1e9.
+ * The forward writes kbar (the backward's input) and z; every entry of both
+ * is written.
+ * ---------------------------------------------------------------------- */
+typedef struct {
+  const float* q;        int64_t q_sb, q_st;           /* [B, S, D] idx_q                   */
+  const float* k;        int64_t k_sb, k_st;           /* [B, S, D] idx_k                   */
+  const float* head_cls;                               /* [D]                               */
+  const int32_t* pos;    int64_t pos_sb, pos_st;       /* [B, S] position_ids               */
+  float* kbar;           int64_t kb_sb;                /* [B, nblk, D], rows D apart        */
+  float* z;              int64_t z_sb, z_st;           /* [B, S, nblk] block scores         */
+  int32_t B, S, D, nblk, block_size, local_blocks;
+} srswa_hc_score_args;
+
+int srswa_hc_score_fwd(const srswa_hc_score_args* a, void* stream);
+
+/* Backward for gz = d loss / d z (the block scores' hook has made it finite):
+ * with dz_raw = sanitize(gz / sqrt(D)) where -1e4 < z < 1e4, else 0 (the
+ * reference's hook on the score matmul output, :1131-1132; sanitize = nan/inf
+ * -> 0, clamp +-1e4),
+ *   dq_i = sum_c dz_raw[i, c] kbar_c,  dkbar_c = [kbar_c finite] sum_i dz_raw[i, c] q_i,
+ * then the softmax-summary backward into dk (every row < S written; rows past
+ * nblk * BS are the caller's) and dhc.  Deterministic (partials summed in a
+ * fixed order); the workspace holds fp32 partials of dkbar per 256-row chunk
+ * and of dhc per block.  Layout as srswa_hc_score_args; kbar and z are the
+ * forward's. */
+typedef struct {
+  const float* q;        int64_t q_sb, q_st;
+  const float* k;        int64_t k_sb, k_st;
+  const float* head_cls;
+  const int32_t* pos;    int64_t pos_sb, pos_st;
+  const float* kbar;     int64_t kb_sb;
+  const float* z;        int64_t z_sb, z_st;
+  const float* gz;       int64_t gz_sb, gz_st;         /* [B, S, nblk]                      */
+  float* dq;             int64_t dq_sb, dq_st;         /* [B, S, D]                         */
+  float* dk;             int64_t dk_sb, dk_st;         /* [B, S, D]                         */
+  float* dhc;                                          /* [D]                               */
+  int32_t B, S, D, nblk, block_size, local_blocks;
+} srswa_hc_score_bwd_args;
+
+int srswa_hc_score_bwd_workspace(const srswa_hc_score_bwd_args* a, size_t* scratch_bytes);
+int srswa_hc_score_bwd(const srswa_hc_score_bwd_args* a, void* scratch, size_t scratch_bytes, void* stream);
+
+/* ------------------------------------------------------------------------
+ * DASH training scorer, stage0 "indexer": DashAttention._block_scores
+ * (HF/dash_attention.py:1005-1050) from its fp32 index queries / keys (the
+ * projections, norms, RoPE and nan_to_num of :1011-1034 stay the caller's):
+ *   z[b, i, c] = max over keys j of block c with j <= pos[b, i] - local_window
+ *                of clamp(q_i . k_j, +-1e4); -1e9 when the block has none.
+ * The forward also writes, for the backward, code[b, c, i] (block-major: the
+ * first key offset taking the gradient in bits 0-7, the number of keys
+ * attaining the maximum in bits 8-15, bit 16 = several keys take it, bit 17 =
+ * none does) and, only where bit 16 is set, their 64-bit mask
+ * tiemask[b, i, c].  Block sizes 16, 32, 64.
+ * ---------------------------------------------------------------------- */
+typedef struct {
+  const float* q;        int64_t q_sb, q_st;           /* [B, S, D] idx_q                   */
+  const float* k;        int64_t k_sb, k_st;           /* [B, S, D] idx_k                   */
+  const int32_t* pos;    int64_t pos_sb, pos_st;       /* [B, S] position_ids               */
+  float* z;              int64_t z_sb, z_st;           /* [B, S, nblk] block scores         */
+  int32_t* code;                                       /* [B, nblk, S] dense                */
+  uint64_t* tiemask;                                   /* [B, S, nblk] dense, written sparsely */
+  int32_t B, S, D, nblk, block_size, local_window;
+} srswa_bm_score_args;
+
+int srswa_bm_score_fwd(const srswa_bm_score_args* a, void* stream);
+
+/* Backward (torch's amax rule) for gz = d loss / d z: the gradient of
+ * z[b, i, c] is divided evenly over the keys attaining the maximum and reaches
+ * those whose unclamped score lies in [-1e4, 1e4]:
+ *   dq_i += gz / n k_j,  dk_j += gz / n q_i.
+ * Every row of dq and every key row < min(S, nblk * BS) of dk is written;
+ * deterministic (each row's blocks and each key's rows summed in order). */
+typedef struct {
+  const float* q;        int64_t q_sb, q_st;
+  const float* k;        int64_t k_sb, k_st;
+  const int32_t* pos;    int64_t pos_sb, pos_st;
+  const int32_t* code;                                 /* from the forward                  */
+  const uint64_t* tiemask;
+  const float* gz;       int64_t gz_sb, gz_st;         /* [B, S, nblk]                      */
+  float* dq;             int64_t dq_sb, dq_st;         /* [B, S, D]                         */
+  float* dk;             int64_t dk_sb, dk_st;         /* [B, S, D]                         */
+  int32_t B, S, D, nblk, block_size, local_window;
+} srswa_bm_score_bwd_args;
+
+int srswa_bm_score_bwd(const srswa_bm_score_bwd_args* a, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

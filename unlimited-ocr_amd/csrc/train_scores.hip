@@ -1,0 +1,1077 @@
+// DASH training block scorers (gfx950), forward and backward.
+//
+// Replaces the stage-0 scoring of the DASH training router, from the index
+// queries / keys the layer's projections, RMSNorms, RoPE and nan_to_num
+// produced (those stay the caller's torch ops):
+//   DashAttention._block_scores_headcls  HF/dash_attention.py:1053-1143 (stage0 "head_cls", the shipped one)
+//   DashAttention._block_scores          HF/dash_attention.py:1005-1050 (stage0 "indexer")
+//
+// head_cls (fp32 throughout; q, k [B, S, D], position p[i] of query row i):
+//   block c holds keys [c BS, min(c BS + BS, S)) (the "valid" ones; none past S)
+//   pre_t = (k_t . hc) / sqrt(D), aw_t = clamp(pre_t, +-1e4)
+//   m = max over valid aw (0 for a block without keys), e_t = exp(aw_t - m) on valid keys
+//   w_t = e_t / max(sum e, 1e-6), kbar_c = nan_to_num(sum_t w_t k_t)
+//   z[i, c] = clamp(q_i . kbar_c / sqrt(D), +-1e4)  if c <= p[i] / BS - LB and block c holds a key
+//           = -1e9                                   otherwise
+// The reference pads the last block with zero keys; exp of a padding logit
+// (0 - m) overflows when m < -88.72, and inf * 0 makes that block's k_bar NaN
+// (zeroed by nan_to_num) and head_cls's gradient NaN: both kept here.
+//
+// Backward, for g = d loss / d z as the caller's hook leaves it:
+//   dz_raw[i, c] = sanitize(g[i, c] / sqrt(D)) where -1e4 < z[i, c] < 1e4 (kept and
+//                  inside the clamp), else 0  (sanitize: nan/inf -> 0, clamp +-1e4: the
+//                  reference's hook on the matmul output)
+//   dq_i   = sum_c dz_raw[i, c] kbar_c
+//   dkbar_c = [kbar_c finite] sum_i dz_raw[i, c] q_i
+//   dw_t = dkbar_c . k_t, dden = -[sum e >= 1e-6] sum_t dw_t e_t / max(sum e, 1e-6)^2
+//   de_t = dw_t / max(sum e, 1e-6) + dden, ds_t = [|pre_t| <= 1e4] de_t e_t / sqrt(D)
+//   dk_t = w_t dkbar_c + ds_t hc,  dhc = sum over every block and key of ds_t k_t
+// (the row max m carries sum_t de_t e_t = 0 exactly in real arithmetic; its
+// rounding residue is not propagated).
+//
+// block-max ("indexer" stage 0; fp32 q, k [B, S, D], no scaling):
+//   z[i, c] = max over keys j of block c with j <= p[i] - LW of clamp(q_i . k_j, +-1e4),
+//             -1e9 when the block holds no such key (and for blocks past the keys)
+// Backward (torch's amax rule): the gradient of z[i, c] is split evenly over
+// the keys attaining the maximum (count n), and reaches those whose
+// unclamped score lies in [-1e4, 1e4]: dq_i += g / n k_j, dk_j += g / n q_i.
+// The forward records per (row, block) an int32 code -- the first such key's
+// offset, n, and flags for "several keys take the gradient" (their 64-bit mask
+// is then written to a side array) and "none does" -- in block-major order.
+//
+// Kernels: hc_summary_fwd (one wave per block), hc_score_fwd (64 query rows
+// per workgroup, one lane per row, k_bar of 64 blocks staged in LDS and read
+// as broadcasts), hc_score_bwd_dq (16 rows per wave, four lanes per row over
+// interleaved head-dim slices), hc_score_bwd_dkbar (the same shape over blocks,
+// fp32 partials per 256-row chunk), hc_summary_bwd (one wave per block: the
+// partials summed in chunk order, stage 0 redone, then its backward), and
+// hc_dhc_reduce (block partials of d head_cls summed in block order);
+// bm_fwd (256 rows per workgroup, 64-key chunks through LDS, S^T = K Q^T on
+// v_mfma_f32_32x32x2_f32 as the inference block-max kernel, then per block the
+// clamped max, its tie and in-range masks), bm_bwd_dq (16 rows per wave, the
+// arg-max key rows of 64 blocks gathered with one load per row in flight
+// together) and bm_bwd_dk (four keys per wave, 16 lanes each, scanning the
+// block's codes in row order).  No atomics: every result is deterministic.
+#include <algorithm>
+#include <type_traits>
+
+#include "mfma_common.h"
+#include "summary.h"
+
+namespace srswa {
+namespace {
+
+constexpr int kTsRows = 64;      // query rows per score tile
+constexpr int kTsGroup = 64;     // blocks per staged group
+constexpr int kTsChunk = 256;    // query rows per d k_bar partial
+constexpr int kTsPad = kTsGroup + 1;
+
+__device__ __forceinline__ float clamp_act(float v) { return fminf(fmaxf(v, -kActClamp), kActClamp); }
+// nan_to_num(nan=0, posinf=0, neginf=0) then clamp to +-1e4: _sanitize_grad, HF/dash_attention.py:749-755
+__device__ __forceinline__ float sanitize(float g) { return isfinite(g) ? clamp_act(g) : 0.f; }
+
+// the last remote block of a query row at position p (none: -1)
+__device__ __forceinline__ int last_remote_block(int p, int BS, int LB) { return p >= 0 ? p / BS - LB : -1; }
+
+// ---------------------------------------------------------------- stage 0
+// One wave summarises block c of sequence b (nv valid keys, rows at kg, k_st
+// apart, read from global memory: a block is at most 64 KiB and stays in the
+// caches over the two passes).  s_w receives the weights w_t, s_e e_t and
+// s_pre the unclamped logits pre_t (one entry per key, BS of them).  Returns
+// sum e (den), the row max and the lane's slice of kbar_raw: head dims
+// EPL lane .. EPL lane + EPL - 1.
+template <int D> struct HcBlock {
+  static constexpr int EPL = D / kWave;      // head dims per lane
+  float den, rowmax;
+  bool pad_overflow;
+  float kb[EPL];
+};
+
+template <int D>
+__device__ void hc_block_forward(const float* kg, int64_t k_st, const float* s_hc, int nv, int BS, float isd,
+                                 float* s_w, float* s_e, float* s_pre, HcBlock<D>& out) {
+  constexpr int EPL = HcBlock<D>::EPL;
+  const int lane = threadIdx.x % kWave;
+  // logits, one key per lane (two rounds for BS = 128)
+  float mx = -INFINITY;
+  for (int t = lane; t < BS; t += kWave) {
+    float pre = 0.f;
+    if (t < nv) {
+      const float* row = kg + (int64_t)t * k_st;
+      float s = 0.f;
+#pragma unroll
+      for (int e = 0; e < D; e += 4) {
+        const float4 kv = *reinterpret_cast<const float4*>(row + e);
+        s = fmaf(kv.x, s_hc[e], s);
+        s = fmaf(kv.y, s_hc[e + 1], s);
+        s = fmaf(kv.z, s_hc[e + 2], s);
+        s = fmaf(kv.w, s_hc[e + 3], s);
+      }
+      pre = s * isd;
+      mx = fmaxf(mx, clamp_act(pre));
+    }
+    s_pre[t] = pre;
+  }
+  mx = wave_max(mx);
+  const float rowmax = nv > 0 ? mx : 0.f;
+  float part = 0.f;
+  for (int t = lane; t < BS; t += kWave) {
+    const float e = t < nv ? expf(clamp_act(s_pre[t]) - rowmax) : 0.f;
+    s_e[t] = e;
+    part += e;
+  }
+  const float den = wave_sum(part);
+  const float dn = fmaxf(den, 1e-6f);
+  for (int t = lane; t < BS; t += kWave) s_w[t] = s_e[t] / dn;
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+  __builtin_amdgcn_wave_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+  // kbar_raw over the lane's dims (coalesced rows)
+#pragma unroll
+  for (int j = 0; j < EPL; ++j) out.kb[j] = 0.f;
+#pragma unroll 4
+  for (int t = 0; t < nv; ++t) {
+    const float w = s_w[t];
+    const float* row = kg + (int64_t)t * k_st + EPL * lane;
+#pragma unroll
+    for (int j = 0; j < EPL; ++j) out.kb[j] = fmaf(w, row[j], out.kb[j]);
+  }
+  out.den = den;
+  out.rowmax = rowmax;
+  // a padding key's weight is exp(0 - m) * 0: NaN once exp(-m) overflows
+  out.pad_overflow = nv > 0 && nv < BS && isinf(expf(-rowmax));
+}
+
+struct HcK {
+  srswa_hc_score_args a;
+  float isd;
+  int ngroups;
+};
+
+template <int D>
+__global__ __launch_bounds__(256) void hc_summary_fwd_kernel(HcK p) {
+  constexpr int EPL = HcBlock<D>::EPL;
+  __shared__ float s_w[4][128], s_e[4][128], s_pre[4][128];
+  __shared__ float s_hc[D];
+  const srswa_hc_score_args& a = p.a;
+  const int wave = threadIdx.x / kWave, lane = threadIdx.x % kWave;
+  for (int e = threadIdx.x; e < D; e += blockDim.x) s_hc[e] = a.head_cls[e];
+  __syncthreads();
+  const int64_t gb = (int64_t)blockIdx.x * 4 + wave;
+  if (gb >= (int64_t)a.B * a.nblk) return;
+  const int b = (int)(gb / a.nblk), c = (int)(gb % a.nblk);
+  const int t0 = c * a.block_size;
+  const int nv = max(0, min(a.block_size, a.S - t0));
+  HcBlock<D> hb;
+  hc_block_forward<D>(a.k + (int64_t)b * a.k_sb + (int64_t)t0 * a.k_st, a.k_st, s_hc, nv, a.block_size, p.isd,
+                      s_w[wave], s_e[wave], s_pre[wave], hb);
+  float* dst = a.kbar + (int64_t)b * a.kb_sb + (int64_t)c * D + EPL * lane;
+#pragma unroll
+  for (int j = 0; j < EPL; ++j) dst[j] = (isfinite(hb.kb[j]) && !hb.pad_overflow) ? hb.kb[j] : 0.f;
+}
+
+// ---------------------------------------------------------------- scores
+// the row's last remote block and the tile's (block-wide max)
+__device__ __forceinline__ int tile_rmax(const srswa_hc_score_args& a, int b, int row, int* s_red) {
+  int rm = -1;
+  if (row < a.S) rm = last_remote_block(a.pos[(int64_t)b * a.pos_sb + (int64_t)row * a.pos_st], a.block_size,
+                                        a.local_blocks);
+  const int wm = wave_max_int(rm);
+  const int wave = threadIdx.x / kWave, lane = threadIdx.x % kWave;
+  if (lane == 0) s_red[wave] = wm;
+  __syncthreads();
+  int t = s_red[0];
+  for (int w = 1; w < (int)(blockDim.x / kWave); ++w) t = max(t, s_red[w]);
+  __syncthreads();
+  return t;
+}
+
+// the last block holding a key (chunk_valid) and the last one scored
+__device__ __forceinline__ int last_valid_block(const srswa_hc_score_args& a) {
+  return min(a.nblk - 1, (a.S - 1) / a.block_size);
+}
+
+template <int D>
+__global__ __launch_bounds__(256) void hc_score_fwd_kernel(HcK p) {
+  __shared__ __align__(16) float s_kb[kTsGroup * D];
+  __shared__ float s_out[kTsRows * kTsPad];
+  __shared__ int s_red[4];
+  const srswa_hc_score_args& a = p.a;
+  const int wave = threadIdx.x / kWave, lane = threadIdx.x % kWave;
+  const int ntiles = (a.S + kTsRows - 1) / kTsRows;
+  const int b = blockIdx.x / ntiles, tile = blockIdx.x % ntiles;
+  const int row = tile * kTsRows + lane;
+  const bool row_ok = row < a.S;
+  const int rm = row_ok ? last_remote_block(a.pos[(int64_t)b * a.pos_sb + (int64_t)row * a.pos_st], a.block_size,
+                                            a.local_blocks)
+                        : -1;
+  const int trm = min(tile_rmax(a, b, tile * kTsRows + (threadIdx.x % kTsRows), s_red), last_valid_block(a));
+  const int wrm = min(wave_max_int(rm), last_valid_block(a));
+  float qv[D];
+  const float* qrow = a.q + (int64_t)b * a.q_sb + (int64_t)(row_ok ? row : 0) * a.q_st;
+#pragma unroll
+  for (int e = 0; e < D; e += 4) {
+    const float4 v = row_ok ? *reinterpret_cast<const float4*>(qrow + e) : make_float4(0.f, 0.f, 0.f, 0.f);
+    qv[e] = v.x;
+    qv[e + 1] = v.y;
+    qv[e + 2] = v.z;
+    qv[e + 3] = v.w;
+  }
+  const int nrows = min(kTsRows, a.S - tile * kTsRows);
+  for (int g0 = 0; g0 < a.nblk; g0 += kTsGroup) {
+    const int gn = min(kTsGroup, a.nblk - g0);
+    const bool any = g0 <= trm;
+    if (any) {
+      for (int i = threadIdx.x; i < gn * (D / 4); i += blockDim.x) {
+        const int c = i / (D / 4), e = 4 * (i % (D / 4));
+        *reinterpret_cast<float4*>(s_kb + c * D + e) =
+            *reinterpret_cast<const float4*>(a.kbar + (int64_t)b * a.kb_sb + (int64_t)(g0 + c) * D + e);
+      }
+      __syncthreads();
+      // wave w scores blocks g0 + 16 w .. + 15, four at a time
+      for (int j0 = 16 * wave; j0 < min(16 * wave + 16, gn); j0 += 4) {
+        float acc[4] = {0.f, 0.f, 0.f, 0.f};
+        const int c0 = g0 + j0;
+        if (c0 <= wrm) {
+#pragma unroll
+          for (int e = 0; e < D; e += 4) {
+#pragma unroll
+            for (int u = 0; u < 4; ++u) {
+              const float4 kv = *reinterpret_cast<const float4*>(s_kb + min(j0 + u, gn - 1) * D + e);
+              acc[u] = fmaf(qv[e], kv.x, acc[u]);
+              acc[u] = fmaf(qv[e + 1], kv.y, acc[u]);
+              acc[u] = fmaf(qv[e + 2], kv.z, acc[u]);
+              acc[u] = fmaf(qv[e + 3], kv.w, acc[u]);
+            }
+          }
+        }
+#pragma unroll
+        for (int u = 0; u < 4; ++u) {
+          const int c = c0 + u;
+          if (j0 + u < gn)
+            s_out[lane * kTsPad + j0 + u] = (c <= rm && c <= last_valid_block(a)) ? clamp_act(acc[u] * p.isd)
+                                                                                   : kScoreNeg;
+        }
+      }
+      __syncthreads();
+    }
+    // the tile's rows of this group, coalesced along the blocks
+    for (int i = threadIdx.x; i < nrows * gn; i += blockDim.x) {
+      const int r = i / gn, c = i % gn;
+      a.z[(int64_t)b * a.z_sb + (int64_t)(tile * kTsRows + r) * a.z_st + g0 + c] = any ? s_out[r * kTsPad + c]
+                                                                                       : kScoreNeg;
+    }
+    if (any) __syncthreads();
+  }
+}
+
+// ---------------------------------------------------------------- backward
+struct HcBK {
+  srswa_hc_score_bwd_args a;
+  float isd;
+  int nchunks;
+  float* dkb_part;     // [nchunks, B, nblk, D]
+  float* dhc_part;     // [B, nblk, D]
+};
+
+// dz_raw of one (row, block) from g and the forward's z
+__device__ __forceinline__ float dz_raw(float g, float z, float isd) {
+  return (z > -kActClamp && z < kActClamp) ? sanitize(g * isd) : 0.f;
+}
+
+// four lanes per row / block: lane slice s owns head dims 16 m + 4 s .. + 3
+template <int D> struct Slice {
+  static constexpr int NM = D / 16;
+  __device__ __forceinline__ static int dim(int s, int m) { return 16 * m + 4 * s; }
+};
+
+// dz_raw of the tile (rows r0.., blocks g0..g0+gn) into s_dz[row][block]
+__device__ __forceinline__ void load_dz_tile(const srswa_hc_score_bwd_args& a, int b, int r0, int nr, int g0, int gn,
+                                             float isd, float* s_dz) {
+  for (int i = threadIdx.x; i < kTsRows * gn; i += blockDim.x) {
+    const int r = i / gn, c = i % gn;
+    float d = 0.f;
+    if (r < nr) {
+      const int64_t o = (int64_t)(r0 + r);
+      d = dz_raw(a.gz[(int64_t)b * a.gz_sb + o * a.gz_st + g0 + c], a.z[(int64_t)b * a.z_sb + o * a.z_st + g0 + c], isd);
+    }
+    s_dz[r * kTsPad + c] = d;
+  }
+}
+
+template <int D>
+__global__ __launch_bounds__(256) void hc_score_bwd_dq_kernel(HcBK p) {
+  using SL = Slice<D>;
+  __shared__ __align__(16) float s_kb[kTsGroup * D];
+  __shared__ float s_dz[kTsRows * kTsPad];
+  __shared__ int s_red[4];
+  const srswa_hc_score_bwd_args& a = p.a;
+  const int wave = threadIdx.x / kWave, lane = threadIdx.x % kWave;
+  const int ntiles = (a.S + kTsRows - 1) / kTsRows;
+  const int b = blockIdx.x / ntiles, tile = blockIdx.x % ntiles;
+  const int r0 = tile * kTsRows;
+  const int nr = min(kTsRows, a.S - r0);
+  const int rl = 16 * wave + lane / 4, s = lane % 4;
+  // tile_rmax over the workgroup's 64 rows (one per thread of the first 64... every
+  // thread maps to a row of the tile)
+  int rm = -1;
+  {
+    const int row = r0 + (int)(threadIdx.x % kTsRows);
+    if (row < a.S)
+      rm = last_remote_block(a.pos[(int64_t)b * a.pos_sb + (int64_t)row * a.pos_st], a.block_size, a.local_blocks);
+  }
+  const int wm = wave_max_int(rm);
+  if (lane == 0) s_red[wave] = wm;
+  __syncthreads();
+  const int trm = min(max(max(s_red[0], s_red[1]), max(s_red[2], s_red[3])),
+                      min(a.nblk - 1, (a.S - 1) / a.block_size));
+  float acc[4 * SL::NM];
+#pragma unroll
+  for (int i = 0; i < 4 * SL::NM; ++i) acc[i] = 0.f;
+  for (int g0 = 0; g0 <= trm; g0 += kTsGroup) {
+    const int gn = min(kTsGroup, a.nblk - g0);
+    __syncthreads();
+    for (int i = threadIdx.x; i < gn * (D / 4); i += blockDim.x) {
+      const int c = i / (D / 4), e = 4 * (i % (D / 4));
+      *reinterpret_cast<float4*>(s_kb + c * D + e) =
+          *reinterpret_cast<const float4*>(a.kbar + (int64_t)b * a.kb_sb + (int64_t)(g0 + c) * D + e);
+    }
+    load_dz_tile(a, b, r0, nr, g0, gn, p.isd, s_dz);
+    __syncthreads();
+    const int cn = min(gn, trm - g0 + 1);
+    for (int c = 0; c < cn; ++c) {
+      const float d = s_dz[rl * kTsPad + c];
+#pragma unroll
+      for (int m = 0; m < SL::NM; ++m) {
+        const float4 kv = *reinterpret_cast<const float4*>(s_kb + c * D + SL::dim(s, m));
+        acc[4 * m] = fmaf(d, kv.x, acc[4 * m]);
+        acc[4 * m + 1] = fmaf(d, kv.y, acc[4 * m + 1]);
+        acc[4 * m + 2] = fmaf(d, kv.z, acc[4 * m + 2]);
+        acc[4 * m + 3] = fmaf(d, kv.w, acc[4 * m + 3]);
+      }
+    }
+  }
+  if (rl < nr) {
+    float* dst = a.dq + (int64_t)b * a.dq_sb + (int64_t)(r0 + rl) * a.dq_st;
+#pragma unroll
+    for (int m = 0; m < SL::NM; ++m)
+      *reinterpret_cast<float4*>(dst + SL::dim(s, m)) =
+          make_float4(acc[4 * m], acc[4 * m + 1], acc[4 * m + 2], acc[4 * m + 3]);
+  }
+}
+
+// d k_bar partial of one 256-row chunk and 64 blocks: wave w owns blocks
+// 16 w .. 16 w + 15 of the group, four lanes per block
+template <int D>
+__global__ __launch_bounds__(256) void hc_score_bwd_dkbar_kernel(HcBK p) {
+  using SL = Slice<D>;
+  __shared__ __align__(16) float s_q[kTsRows * D];
+  __shared__ float s_dz[kTsRows * kTsPad];
+  __shared__ int s_red[4];
+  const srswa_hc_score_bwd_args& a = p.a;
+  const int wave = threadIdx.x / kWave, lane = threadIdx.x % kWave;
+  const int ngroups = (a.nblk + kTsGroup - 1) / kTsGroup;
+  const int chunk = blockIdx.x % p.nchunks;
+  const int g0 = ((blockIdx.x / p.nchunks) % ngroups) * kTsGroup;
+  const int b = blockIdx.x / (p.nchunks * ngroups);
+  const int gn = min(kTsGroup, a.nblk - g0);
+  const int cl = 16 * wave + lane / 4, s = lane % 4;
+  float acc[4 * SL::NM];
+#pragma unroll
+  for (int i = 0; i < 4 * SL::NM; ++i) acc[i] = 0.f;
+  const int lastv = min(a.nblk - 1, (a.S - 1) / a.block_size);
+  for (int sub = 0; sub < kTsChunk / kTsRows; ++sub) {
+    const int r0 = chunk * kTsChunk + sub * kTsRows;
+    if (r0 >= a.S) break;
+    const int nr = min(kTsRows, a.S - r0);
+    int rm = -1;
+    {
+      const int row = r0 + (int)(threadIdx.x % kTsRows);
+      if (row < a.S)
+        rm = last_remote_block(a.pos[(int64_t)b * a.pos_sb + (int64_t)row * a.pos_st], a.block_size, a.local_blocks);
+    }
+    const int wm = wave_max_int(rm);
+    __syncthreads();                      // the previous sub-chunk's tiles are consumed
+    if (lane == 0) s_red[wave] = wm;
+    __syncthreads();
+    const int srm = min(max(max(s_red[0], s_red[1]), max(s_red[2], s_red[3])), lastv);
+    if (srm < g0) continue;               // no row of the sub-chunk reaches the group (uniform)
+    for (int i = threadIdx.x; i < kTsRows * (D / 4); i += blockDim.x) {
+      const int r = i / (D / 4), e = 4 * (i % (D / 4));
+      *reinterpret_cast<float4*>(s_q + r * D + e) =
+          r < nr ? *reinterpret_cast<const float4*>(a.q + (int64_t)b * a.q_sb + (int64_t)(r0 + r) * a.q_st + e)
+                 : make_float4(0.f, 0.f, 0.f, 0.f);
+    }
+    load_dz_tile(a, b, r0, nr, g0, gn, p.isd, s_dz);
+    __syncthreads();
+    if (cl < gn) {
+      for (int r = 0; r < nr; ++r) {
+        const float d = s_dz[r * kTsPad + cl];
+#pragma unroll
+        for (int m = 0; m < SL::NM; ++m) {
+          const float4 qv = *reinterpret_cast<const float4*>(s_q + r * D + SL::dim(s, m));
+          acc[4 * m] = fmaf(d, qv.x, acc[4 * m]);
+          acc[4 * m + 1] = fmaf(d, qv.y, acc[4 * m + 1]);
+          acc[4 * m + 2] = fmaf(d, qv.z, acc[4 * m + 2]);
+          acc[4 * m + 3] = fmaf(d, qv.w, acc[4 * m + 3]);
+        }
+      }
+    }
+  }
+  if (cl < gn) {
+    float* dst = p.dkb_part + (((int64_t)chunk * a.B + b) * a.nblk + g0 + cl) * D;
+#pragma unroll
+    for (int m = 0; m < SL::NM; ++m)
+      *reinterpret_cast<float4*>(dst + SL::dim(s, m)) =
+          make_float4(acc[4 * m], acc[4 * m + 1], acc[4 * m + 2], acc[4 * m + 3]);
+  }
+}
+
+// stage-0 backward, one wave per block: d idx_k rows of the block and the
+// block's partial of d head_cls
+template <int D>
+__global__ __launch_bounds__(256) void hc_summary_bwd_kernel(HcBK p) {
+  constexpr int EPL = HcBlock<D>::EPL;
+  __shared__ float s_w[4][128], s_e[4][128], s_pre[4][128], s_ds[4][128];
+  __shared__ float s_dkb[4][D];
+  __shared__ float s_hc[D];
+  const srswa_hc_score_bwd_args& a = p.a;
+  const int wave = threadIdx.x / kWave, lane = threadIdx.x % kWave;
+  for (int e = threadIdx.x; e < D; e += blockDim.x) s_hc[e] = a.head_cls[e];
+  __syncthreads();
+  const int64_t gb = (int64_t)blockIdx.x * 4 + wave;
+  if (gb >= (int64_t)a.B * a.nblk) return;
+  const int b = (int)(gb / a.nblk), c = (int)(gb % a.nblk);
+  const int BS = a.block_size;
+  const int t0 = c * BS;
+  const int nv = max(0, min(BS, a.S - t0));
+  const float* kg = a.k + (int64_t)b * a.k_sb + (int64_t)t0 * a.k_st;
+  // d k_bar: the chunk partials in chunk order
+  float dkb[EPL];
+#pragma unroll
+  for (int j = 0; j < EPL; ++j) dkb[j] = 0.f;
+  for (int ch = 0; ch < p.nchunks; ++ch) {
+    const float* src = p.dkb_part + (((int64_t)ch * a.B + b) * a.nblk + c) * D + EPL * lane;
+#pragma unroll
+    for (int j = 0; j < EPL; ++j) dkb[j] += src[j];
+  }
+  HcBlock<D> hb;
+  hc_block_forward<D>(kg, a.k_st, s_hc, nv, BS, p.isd, s_w[wave], s_e[wave], s_pre[wave], hb);
+  // nan_to_num(k_bar) passes no gradient where k_bar_raw is not finite
+#pragma unroll
+  for (int j = 0; j < EPL; ++j) {
+    if (!isfinite(hb.kb[j]) || hb.pad_overflow) dkb[j] = 0.f;
+    s_dkb[wave][EPL * lane + j] = dkb[j];
+  }
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+  __builtin_amdgcn_wave_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+  const float dn = fmaxf(hb.den, 1e-6f);
+  // dw_t = dkbar . k_t, one key per lane
+  float dwv[2] = {0.f, 0.f};
+  float se = 0.f;
+  for (int r = 0; r < 2; ++r) {
+    const int t = lane + kWave * r;
+    if (t < nv) {
+      const float* row = kg + (int64_t)t * a.k_st;
+      float s = 0.f;
+#pragma unroll
+      for (int e = 0; e < D; e += 4) {
+        const float4 kv = *reinterpret_cast<const float4*>(row + e);
+        s = fmaf(kv.x, s_dkb[wave][e], s);
+        s = fmaf(kv.y, s_dkb[wave][e + 1], s);
+        s = fmaf(kv.z, s_dkb[wave][e + 2], s);
+        s = fmaf(kv.w, s_dkb[wave][e + 3], s);
+      }
+      dwv[r] = s;
+      se += s * s_e[wave][t];
+    }
+  }
+  const float dden = hb.den >= 1e-6f ? -wave_sum(se) / (dn * dn) : 0.f;
+  for (int r = 0; r < 2; ++r) {
+    const int t = lane + kWave * r;
+    if (t < BS) {
+      float ds = 0.f;
+      if (t < nv) {
+        const float de = dwv[r] / dn + dden;
+        const float pre = s_pre[wave][t];
+        ds = (pre >= -kActClamp && pre <= kActClamp) ? de * s_e[wave][t] * p.isd : 0.f;
+      }
+      s_ds[wave][t] = ds;
+    }
+  }
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+  __builtin_amdgcn_wave_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+  // d k_t over the lane's dims, and the block's d head_cls
+  float dh[EPL];
+#pragma unroll
+  for (int j = 0; j < EPL; ++j) dh[j] = 0.f;
+  float hcl[EPL];
+#pragma unroll
+  for (int j = 0; j < EPL; ++j) hcl[j] = s_hc[EPL * lane + j];
+#pragma unroll 4
+  for (int t = 0; t < nv; ++t) {
+    const float w = s_w[wave][t], ds = s_ds[wave][t];
+    const float* row = kg + (int64_t)t * a.k_st + EPL * lane;
+    float* dst = a.dk + (int64_t)b * a.dk_sb + (int64_t)(t0 + t) * a.dk_st + EPL * lane;
+#pragma unroll
+    for (int j = 0; j < EPL; ++j) {
+      dst[j] = hb.pad_overflow ? 0.f : fmaf(w, dkb[j], ds * hcl[j]);
+      dh[j] = fmaf(ds, row[j], dh[j]);
+    }
+  }
+  float* hp = p.dhc_part + ((int64_t)b * a.nblk + c) * D + EPL * lane;
+#pragma unroll
+  for (int j = 0; j < EPL; ++j) hp[j] = hb.pad_overflow ? __builtin_nanf("") : dh[j];
+}
+
+template <int D>
+__global__ __launch_bounds__(D) void hc_dhc_reduce_kernel(HcBK p) {
+  const int e = threadIdx.x;
+  const int64_t n = (int64_t)p.a.B * p.a.nblk;
+  float s = 0.f;
+  for (int64_t i = 0; i < n; ++i) s += p.dhc_part[i * D + e];
+  p.a.dhc[e] = s;
+}
+
+// ---------------------------------------------------------------- block max
+constexpr int kBmRows = 256;                 // query rows per workgroup (8 waves of 32)
+constexpr int kBmThreads = 2 * kBmRows;
+constexpr int kBmSlab = 16;                  // chunks of 64 keys per workgroup
+constexpr int kCodeMulti = 1 << 16;          // several keys take the gradient: mask in the side array
+constexpr int kCodeNone = 1 << 17;           // no key takes the gradient
+
+struct BmK {
+  srswa_bm_score_args a;
+  int ntiles, nslab;
+};
+
+// S^T tile (32 keys x 32 rows) from the staged chunk, fp32 operands: lane half
+// h supplies head dims 8 m + 4 h .. + 3 of step group m to both operands
+template <int D>
+__device__ __forceinline__ f32x16_t bm_tile(const float* sK, int key, const float4* qf, int h) {
+  constexpr int KP = D + 4;
+  f32x16_t s = zero16();
+#pragma unroll
+  for (int m = 0; m < D / 8; ++m) {
+    const float4 kv = *reinterpret_cast<const float4*>(sK + key * KP + 8 * m + 4 * h);
+    s = __builtin_amdgcn_mfma_f32_32x32x2f32(kv.x, qf[m].x, s, 0, 0, 0);
+    s = __builtin_amdgcn_mfma_f32_32x32x2f32(kv.y, qf[m].y, s, 0, 0, 0);
+    s = __builtin_amdgcn_mfma_f32_32x32x2f32(kv.z, qf[m].z, s, 0, 0, 0);
+    s = __builtin_amdgcn_mfma_f32_32x32x2f32(kv.w, qf[m].w, s, 0, 0, 0);
+  }
+  return s;
+}
+
+__device__ __forceinline__ uint64_t shfl_xor_u64(uint64_t v, int m) {
+  const uint32_t lo = __shfl_xor((uint32_t)v, m, kWave), hi = __shfl_xor((uint32_t)(v >> 32), m, kWave);
+  return ((uint64_t)hi << 32) | lo;
+}
+
+template <int D, int BS>
+__global__ __launch_bounds__(kBmThreads) void bm_fwd_kernel(BmK p) {
+  constexpr int KP = D + 4;
+  constexpr int NSUB = kChunk / BS;
+  __shared__ __align__(16) float sK[kChunk * KP];
+  __shared__ int s_maxls;
+  const srswa_bm_score_args& a = p.a;
+  const int tid = threadIdx.x, wave = tid / kWave, lane = tid % kWave;
+  const int h = lane / 32, rl = lane % 32;
+  const int slab = blockIdx.x % p.nslab;
+  const int bt = blockIdx.x / p.nslab;
+  const int tile = bt % p.ntiles;
+  const int b = bt / p.ntiles;
+  const int row = tile * kBmRows + wave * 32 + rl;
+  const bool row_ok = row < a.S;
+  int ls = 0;                                   // remote keys: j < ls
+  if (row_ok) {
+    const int pos = a.pos[(int64_t)b * a.pos_sb + (int64_t)row * a.pos_st];
+    ls = min(max(pos - a.local_window + 1, 0), a.S);
+  }
+  if (tid == 0) s_maxls = 0;
+  __syncthreads();
+  if (row_ok && h == 0) atomicMax(&s_maxls, ls);
+  __syncthreads();
+  const int nchunks = ceil_div(s_maxls, kChunk);
+  const int c_lo = slab * kBmSlab;
+  const int c_hi = min(c_lo + kBmSlab, nchunks);
+  const int blk_lo = c_lo * NSUB;
+  const int blk_hi = slab == p.nslab - 1 ? a.nblk : min(a.nblk, (c_lo + kBmSlab) * NSUB);
+
+  float4 qf[D / 8];
+  {
+    const float* qrow = a.q + (int64_t)b * a.q_sb + (int64_t)(row_ok ? row : 0) * a.q_st;
+#pragma unroll
+    for (int m = 0; m < D / 8; ++m)
+      qf[m] = row_ok ? *reinterpret_cast<const float4*>(qrow + 8 * m + 4 * h) : make_float4(0.f, 0.f, 0.f, 0.f);
+  }
+  float* zrow = a.z + (int64_t)b * a.z_sb + (int64_t)(row_ok ? row : 0) * a.z_st;
+  int32_t* code = a.code + (int64_t)b * a.nblk * a.S + (row_ok ? row : 0);      // [b][blk][row]
+  uint64_t* tm = a.tiemask + ((int64_t)b * a.S + (row_ok ? row : 0)) * a.nblk;   // [b][row][blk]
+  const float* kg = a.k + (int64_t)b * a.k_sb;
+  constexpr int PR = D / 4;                       // 16-byte pieces per key row
+  constexpr int PPT = kChunk * PR / kBmThreads;   // per thread
+  float4 pre[PPT];
+  auto fetch = [&](int c) {
+#pragma unroll
+    for (int i = 0; i < PPT; ++i) {
+      const int pc = tid + kBmThreads * i;
+      const int j = c * kChunk + pc / PR, col = pc % PR;
+      pre[i] = j < a.S ? *reinterpret_cast<const float4*>(kg + (int64_t)j * a.k_st + 4 * col)
+                       : make_float4(0.f, 0.f, 0.f, 0.f);
+    }
+  };
+  if (c_lo < c_hi) fetch(c_lo);
+  for (int c = c_lo; c < c_hi; ++c) {
+    const int j0 = c * kChunk;
+    __syncthreads();
+#pragma unroll
+    for (int i = 0; i < PPT; ++i) {
+      const int pc = tid + kBmThreads * i;
+      *reinterpret_cast<float4*>(sK + (pc / PR) * KP + (pc % PR) * 4) = pre[i];
+    }
+    __syncthreads();
+    if (c + 1 < c_hi) fetch(c + 1);
+    const f32x16_t s0 = bm_tile<D>(sK, rl, qf, h);
+    const f32x16_t s1 = bm_tile<D>(sK, 32 + rl, qf, h);
+#pragma unroll
+    for (int sb = 0; sb < NSUB; ++sb) {
+      float mx = -INFINITY;
+#pragma unroll
+      for (int r = 0; r < 16; ++r)
+#pragma unroll
+        for (int half = 0; half < 2; ++half) {
+          const int off = 32 * half + d_row(r, h);
+          if (off / BS == sb && j0 + off < ls) mx = fmaxf(mx, clamp_act(half ? s1[r] : s0[r]));
+        }
+      mx = fmaxf(mx, __shfl_xor(mx, 32, kWave));
+      uint64_t tie = 0, grad = 0;                 // block-relative key bits
+#pragma unroll
+      for (int r = 0; r < 16; ++r)
+#pragma unroll
+        for (int half = 0; half < 2; ++half) {
+          const int off = 32 * half + d_row(r, h);
+          if (off / BS == sb && j0 + off < ls) {
+            const float raw = half ? s1[r] : s0[r];
+            const float cv = clamp_act(raw);
+            const uint64_t bit = 1ull << (off - sb * BS);
+            if (cv == mx) {
+              tie |= bit;
+              if (raw == cv) grad |= bit;
+            }
+          }
+        }
+      tie |= shfl_xor_u64(tie, 32);
+      grad |= shfl_xor_u64(grad, 32);
+      const int blk = c * NSUB + sb;
+      if (row_ok && h == 0 && blk < a.nblk) {
+        const int ng = __popcll(grad);
+        int cd = kCodeNone;
+        if (ng > 0) cd = (int)__builtin_ctzll(grad) | (__popcll(tie) << 8) | (ng > 1 ? kCodeMulti : 0);
+        zrow[blk] = mx == -INFINITY ? kScoreNeg : mx;
+        code[(int64_t)blk * a.S] = cd;
+        if (ng > 1) tm[blk] = grad;
+      }
+    }
+  }
+  // the slab's blocks after the last visited chunk hold no remote key of any row
+  if (row_ok && h == 0) {
+    for (int blk = max(c_hi > c_lo ? c_hi * NSUB : blk_lo, blk_lo); blk < blk_hi; ++blk) {
+      zrow[blk] = kScoreNeg;
+      code[(int64_t)blk * a.S] = kCodeNone;
+    }
+  }
+}
+
+// dq: 16 rows per wave (64 per workgroup); per group of 64 blocks the codes
+// and weights g / n are staged in LDS, then for each block the 16 rows' key
+// rows are loaded together (lanes over the head dims) and accumulated in
+// block order
+template <int D, int BS>
+__global__ __launch_bounds__(256) void bm_bwd_dq_kernel(srswa_bm_score_bwd_args a) {
+  constexpr int EPL = D / kWave;
+  __shared__ int s_code[kTsGroup * kTsPad];     // [block][row]
+  __shared__ float s_w[kTsGroup * kTsPad];      // [block][row]
+  const int wave = threadIdx.x / kWave, lane = threadIdx.x % kWave;
+  const int ntiles = (a.S + kTsRows - 1) / kTsRows;
+  const int b = blockIdx.x / ntiles, tile = blockIdx.x % ntiles;
+  const int r0 = tile * kTsRows;
+  const int nr = min(kTsRows, a.S - r0);
+  const float* kg = a.k + (int64_t)b * a.k_sb + EPL * lane;
+  float acc[16][EPL];
+#pragma unroll
+  for (int r = 0; r < 16; ++r)
+#pragma unroll
+    for (int j = 0; j < EPL; ++j) acc[r][j] = 0.f;
+  const int nblk_keys = min(a.nblk, ceil_div(a.S, BS));   // blocks that can hold a key
+  for (int g0 = 0; g0 < nblk_keys; g0 += kTsGroup) {
+    const int gn = min(kTsGroup, nblk_keys - g0);
+    __syncthreads();
+    for (int i = threadIdx.x; i < gn * kTsRows; i += blockDim.x) {
+      const int c = i / kTsRows, r = i % kTsRows;           // codes: rows contiguous
+      s_code[c * kTsPad + r] = r < nr ? a.code[((int64_t)b * a.nblk + g0 + c) * a.S + r0 + r] : kCodeNone;
+    }
+    __syncthreads();
+    for (int i = threadIdx.x; i < gn * kTsRows; i += blockDim.x) {
+      const int r = i / gn, c = i % gn;                     // upstream gradient: blocks contiguous
+      const int cd = s_code[c * kTsPad + r];
+      float w = 0.f;
+      if (r < nr && !(cd & kCodeNone))
+        w = a.gz[(int64_t)b * a.gz_sb + (int64_t)(r0 + r) * a.gz_st + g0 + c] / (float)((cd >> 8) & 0xff);
+      s_w[c * kTsPad + r] = w;
+    }
+    __syncthreads();
+    for (int c = 0; c < gn; ++c) {
+      const int blk = g0 + c;
+      float kv[16][EPL];
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        const int rr = 16 * wave + r;
+        const int cd = s_code[c * kTsPad + rr];
+        const float w = s_w[c * kTsPad + rr];
+        const int j = blk * BS + (cd & 0xff);
+#pragma unroll
+        for (int e = 0; e < EPL; ++e) kv[r][e] = 0.f;
+        if (w != 0.f && !(cd & kCodeMulti)) {
+#pragma unroll
+          for (int e = 0; e < EPL; ++e) kv[r][e] = kg[(int64_t)j * a.k_st + e];
+        }
+      }
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        const int rr = 16 * wave + r;
+        const int cd = s_code[c * kTsPad + rr];
+        const float w = s_w[c * kTsPad + rr];
+        if (w == 0.f) continue;
+        if (!(cd & kCodeMulti)) {
+#pragma unroll
+          for (int e = 0; e < EPL; ++e) acc[r][e] = fmaf(w, kv[r][e], acc[r][e]);
+        } else {
+          // several keys share the gradient: each one in key order
+          uint64_t m = a.tiemask[((int64_t)b * a.S + r0 + rr) * a.nblk + blk];
+          while (m) {
+            const int off = __builtin_ctzll(m);
+            m &= m - 1;
+            const int j = blk * BS + off;
+#pragma unroll
+            for (int e = 0; e < EPL; ++e) acc[r][e] = fmaf(w, kg[(int64_t)j * a.k_st + e], acc[r][e]);
+          }
+        }
+      }
+    }
+  }
+#pragma unroll
+  for (int r = 0; r < 16; ++r) {
+    const int rr = 16 * wave + r;
+    if (rr < nr) {
+      float* dst = a.dq + (int64_t)b * a.dq_sb + (int64_t)(r0 + rr) * a.dq_st + EPL * lane;
+#pragma unroll
+      for (int e = 0; e < EPL; ++e) dst[e] = acc[r][e];
+    }
+  }
+}
+
+// dk: one wave per (sequence, block, four keys); lane group k (16 lanes)
+// owns key 4 w + k's D / 16 head dims per lane.  The block's codes are scanned
+// 64 rows at a time in row order; the rows whose gradient reaches a key are
+// taken one per lane group per step (four rows per load instruction).
+template <int D, int BS>
+__global__ __launch_bounds__(256) void bm_bwd_dk_kernel(srswa_bm_score_bwd_args a) {
+  constexpr int DPL = D / 16;                    // head dims per lane
+  constexpr int QPB = BS / 4;                    // key quads per block
+  const int wave = threadIdx.x / kWave, lane = threadIdx.x % kWave;
+  const int64_t gw = (int64_t)blockIdx.x * 4 + wave;
+  const int nblk_keys = min(a.nblk, ceil_div(a.S, BS));
+  if (gw >= (int64_t)a.B * nblk_keys * QPB) return;
+  const int quad = (int)(gw % QPB);
+  const int blk = (int)((gw / QPB) % nblk_keys);
+  const int b = (int)(gw / ((int64_t)QPB * nblk_keys));
+  const int kgrp = lane / 16, dl = lane % 16;
+  const int off0 = 4 * quad;                      // first key offset of the quad
+  const int my_key = off0 + kgrp;
+  const int32_t* col = a.code + ((int64_t)b * a.nblk + blk) * a.S;
+  const float* qb = a.q + (int64_t)b * a.q_sb + DPL * dl;
+  float acc[DPL];
+#pragma unroll
+  for (int e = 0; e < DPL; ++e) acc[e] = 0.f;
+  for (int i0 = 0; i0 < a.S; i0 += kWave) {
+    const int i = i0 + lane;
+    const int cd = i < a.S ? col[i] : kCodeNone;
+    // which keys of the quad this row's gradient reaches (bit k)
+    uint32_t hit = 0;
+    float w = 0.f;
+    if (!(cd & kCodeNone)) {
+      if (cd & kCodeMulti) {
+        const uint64_t m = a.tiemask[((int64_t)b * a.S + i) * a.nblk + blk];
+        hit = (uint32_t)((m >> off0) & 0xfu);
+      } else {
+        const int f = (cd & 0xff) - off0;
+        hit = (f >= 0 && f < 4) ? 1u << f : 0u;
+      }
+      if (hit) w = a.gz[(int64_t)b * a.gz_sb + (int64_t)i * a.gz_st + blk] / (float)((cd >> 8) & 0xff);
+    }
+    if (!__any(hit != 0)) continue;
+    uint64_t bal[4];
+#pragma unroll
+    for (int k = 0; k < 4; ++k) bal[k] = __ballot((hit >> k) & 1u);
+    uint64_t mine = bal[kgrp];
+    // step n: every lane group takes its n-th row (rows in ascending order)
+    while (__any(mine != 0)) {
+      const int rsel = mine ? (int)__builtin_ctzll(mine) : 0;
+      const float wr = __shfl(w, rsel, kWave);
+      if (mine) {
+        mine &= mine - 1;
+        const float* qrow = qb + (int64_t)(i0 + rsel) * a.q_st;
+#pragma unroll
+        for (int e = 0; e < DPL; e += 4) {
+          const float4 qv = *reinterpret_cast<const float4*>(qrow + e);
+          acc[e] = fmaf(wr, qv.x, acc[e]);
+          acc[e + 1] = fmaf(wr, qv.y, acc[e + 1]);
+          acc[e + 2] = fmaf(wr, qv.z, acc[e + 2]);
+          acc[e + 3] = fmaf(wr, qv.w, acc[e + 3]);
+        }
+      }
+    }
+  }
+  const int j = blk * BS + my_key;
+  if (j < a.S) {                                  // the last block may end past the keys
+    float* dst = a.dk + (int64_t)b * a.dk_sb + (int64_t)j * a.dk_st + DPL * dl;
+#pragma unroll
+    for (int e = 0; e < DPL; e += 4)
+      *reinterpret_cast<float4*>(dst + e) = make_float4(acc[e], acc[e + 1], acc[e + 2], acc[e + 3]);
+  }
+}
+
+int hc_check(int B, int S, int D, int nblk, int BS, int LB, const char* what) {
+  if (B < 0 || S < 0 || nblk < 0 || BS <= 0 || LB < 0) {
+    set_error("%s: bad sizes", what);
+    return SRSWA_INVALID;
+  }
+  if (!(D == 64 || D == 128)) {
+    set_error("%s: head dim %d not supported (64, 128)", what, D);
+    return SRSWA_UNSUPPORTED;
+  }
+  if (!(BS == 16 || BS == 32 || BS == 64 || BS == 128)) {
+    set_error("%s: block size %d not supported (16, 32, 64, 128)", what, BS);
+    return SRSWA_UNSUPPORTED;
+  }
+  return SRSWA_OK;
+}
+
+bool al16(const void* p) { return ((uintptr_t)p & 15u) == 0; }
+
+}  // namespace
+}  // namespace srswa
+
+using namespace srswa;
+
+extern "C" int srswa_hc_score_fwd(const srswa_hc_score_args* a, void* stream) {
+  if (!a || !a->q || !a->k || !a->head_cls || !a->pos || !a->kbar || !a->z) {
+    set_error("head_cls scores: null argument");
+    return SRSWA_INVALID;
+  }
+  int rc = hc_check(a->B, a->S, a->D, a->nblk, a->block_size, a->local_blocks, "head_cls scores");
+  if (rc != SRSWA_OK) return rc;
+  if (a->B == 0 || a->S == 0 || a->nblk == 0) return SRSWA_OK;
+  if (!al16(a->q) || !al16(a->k) || !al16(a->kbar) || (a->q_sb % 4) || (a->q_st % 4) || (a->k_sb % 4) ||
+      (a->k_st % 4) || (a->kb_sb % 4) || a->kb_sb < (int64_t)a->nblk * a->D) {
+    set_error("head_cls scores: rows must be 16-byte aligned and k_bar [B, nblk, D] dense per sequence");
+    return SRSWA_UNSUPPORTED;
+  }
+  HcK k{};
+  k.a = *a;
+  k.isd = 1.0f / sqrtf((float)a->D);
+  hipStream_t st = reinterpret_cast<hipStream_t>(stream);
+  const unsigned gs = (unsigned)(((int64_t)a->B * a->nblk + 3) / 4);
+  const unsigned gz = (unsigned)((int64_t)a->B * ((a->S + kTsRows - 1) / kTsRows));
+  if (a->D == 128) {
+    hipLaunchKernelGGL(hc_summary_fwd_kernel<128>, dim3(gs), dim3(256), 0, st, k);
+    hipLaunchKernelGGL(hc_score_fwd_kernel<128>, dim3(gz), dim3(256), 0, st, k);
+  } else {
+    hipLaunchKernelGGL(hc_summary_fwd_kernel<64>, dim3(gs), dim3(256), 0, st, k);
+    hipLaunchKernelGGL(hc_score_fwd_kernel<64>, dim3(gz), dim3(256), 0, st, k);
+  }
+  const hipError_t e = hipGetLastError();
+  if (e != hipSuccess) {
+    set_error("head_cls scores launch failed: %s", hipGetErrorString(e));
+    return SRSWA_LAUNCH;
+  }
+  return SRSWA_OK;
+}
+
+namespace srswa {
+namespace {
+int hc_bwd_chunks(const srswa_hc_score_bwd_args* a) { return (a->S + kTsChunk - 1) / kTsChunk; }
+}  // namespace
+}  // namespace srswa
+
+extern "C" int srswa_hc_score_bwd_workspace(const srswa_hc_score_bwd_args* a, size_t* scratch_bytes) {
+  if (!a || !scratch_bytes) {
+    set_error("head_cls scores backward: null argument");
+    return SRSWA_INVALID;
+  }
+  int rc = hc_check(a->B, a->S, a->D, a->nblk, a->block_size, a->local_blocks, "head_cls scores backward");
+  if (rc != SRSWA_OK) return rc;
+  const size_t blocks = (size_t)a->B * a->nblk * a->D;
+  *scratch_bytes = (size_t)(hc_bwd_chunks(a) + 1) * blocks * sizeof(float);
+  return SRSWA_OK;
+}
+
+extern "C" int srswa_hc_score_bwd(const srswa_hc_score_bwd_args* a, void* scratch, size_t scratch_bytes,
+                                  void* stream) {
+  if (!a || !a->q || !a->k || !a->head_cls || !a->pos || !a->kbar || !a->z || !a->gz || !a->dq || !a->dk ||
+      !a->dhc) {
+    set_error("head_cls scores backward: null argument");
+    return SRSWA_INVALID;
+  }
+  size_t need = 0;
+  int rc = srswa_hc_score_bwd_workspace(a, &need);
+  if (rc != SRSWA_OK) return rc;
+  if (a->B == 0 || a->S == 0 || a->nblk == 0) return SRSWA_OK;
+  if (!scratch || scratch_bytes < need || !al16(scratch)) {
+    set_error("head_cls scores backward: scratch of %zu bytes required (got %zu)", need, scratch_bytes);
+    return SRSWA_WORKSPACE;
+  }
+  if (!al16(a->q) || !al16(a->k) || !al16(a->kbar) || !al16(a->dq) || (a->q_sb % 4) || (a->q_st % 4) ||
+      (a->k_sb % 4) || (a->k_st % 4) || (a->kb_sb % 4) || (a->dq_sb % 4) || (a->dq_st % 4) ||
+      a->kb_sb < (int64_t)a->nblk * a->D) {
+    set_error("head_cls scores backward: rows must be 16-byte aligned and k_bar [B, nblk, D] dense per sequence");
+    return SRSWA_UNSUPPORTED;
+  }
+  HcBK k{};
+  k.a = *a;
+  k.isd = 1.0f / sqrtf((float)a->D);
+  k.nchunks = hc_bwd_chunks(a);
+  k.dkb_part = reinterpret_cast<float*>(scratch);
+  k.dhc_part = k.dkb_part + (size_t)k.nchunks * a->B * a->nblk * a->D;
+  hipStream_t st = reinterpret_cast<hipStream_t>(stream);
+  const int ntiles = (a->S + kTsRows - 1) / kTsRows;
+  const int ngroups = (a->nblk + kTsGroup - 1) / kTsGroup;
+  const dim3 gq((unsigned)((int64_t)a->B * ntiles));
+  const dim3 gk((unsigned)((int64_t)a->B * ngroups * k.nchunks));
+  const dim3 gs((unsigned)(((int64_t)a->B * a->nblk + 3) / 4));
+  if (a->D == 128) {
+    hipLaunchKernelGGL(hc_score_bwd_dq_kernel<128>, gq, dim3(256), 0, st, k);
+    hipLaunchKernelGGL(hc_score_bwd_dkbar_kernel<128>, gk, dim3(256), 0, st, k);
+    hipLaunchKernelGGL(hc_summary_bwd_kernel<128>, gs, dim3(256), 0, st, k);
+    hipLaunchKernelGGL(hc_dhc_reduce_kernel<128>, dim3(1), dim3(128), 0, st, k);
+  } else {
+    hipLaunchKernelGGL(hc_score_bwd_dq_kernel<64>, gq, dim3(256), 0, st, k);
+    hipLaunchKernelGGL(hc_score_bwd_dkbar_kernel<64>, gk, dim3(256), 0, st, k);
+    hipLaunchKernelGGL(hc_summary_bwd_kernel<64>, gs, dim3(256), 0, st, k);
+    hipLaunchKernelGGL(hc_dhc_reduce_kernel<64>, dim3(1), dim3(64), 0, st, k);
+  }
+  const hipError_t e = hipGetLastError();
+  if (e != hipSuccess) {
+    set_error("head_cls scores backward launch failed: %s", hipGetErrorString(e));
+    return SRSWA_LAUNCH;
+  }
+  return SRSWA_OK;
+}
+
+namespace srswa {
+namespace {
+
+int bm_check(const srswa_bm_score_args* a, const char* what) {
+  if (a->B < 0 || a->S < 0 || a->nblk < 0 || a->block_size <= 0 || a->local_window < 1) {
+    set_error("%s: bad sizes", what);
+    return SRSWA_INVALID;
+  }
+  if (!(a->D == 64 || a->D == 128)) {
+    set_error("%s: head dim %d not supported (64, 128)", what, a->D);
+    return SRSWA_UNSUPPORTED;
+  }
+  if (!(a->block_size == 16 || a->block_size == 32 || a->block_size == 64)) {
+    set_error("%s: block size %d not supported (16, 32, 64)", what, a->block_size);
+    return SRSWA_UNSUPPORTED;
+  }
+  return SRSWA_OK;
+}
+
+template <int D, int BS>
+void bm_launch_fwd(const BmK& k, hipStream_t st) {
+  const dim3 grid((unsigned)((int64_t)k.a.B * k.ntiles * k.nslab));
+  hipLaunchKernelGGL((bm_fwd_kernel<D, BS>), grid, dim3(kBmThreads), 0, st, k);
+}
+
+template <int D, int BS>
+void bm_launch_bwd(const srswa_bm_score_bwd_args& a, hipStream_t st) {
+  const int ntiles = (a.S + kTsRows - 1) / kTsRows;
+  hipLaunchKernelGGL((bm_bwd_dq_kernel<D, BS>), dim3((unsigned)((int64_t)a.B * ntiles)), dim3(256), 0, st, a);
+  const int64_t waves = (int64_t)a.B * std::min(a.nblk, (a.S + BS - 1) / BS) * (BS / 4);
+  if (waves > 0)
+    hipLaunchKernelGGL((bm_bwd_dk_kernel<D, BS>), dim3((unsigned)((waves + 3) / 4)), dim3(256), 0, st, a);
+}
+
+template <typename F>
+void bm_dispatch(int D, int BS, F&& f) {
+  if (D == 128) {
+    if (BS == 16) f(std::integral_constant<int, 128>{}, std::integral_constant<int, 16>{});
+    else if (BS == 32) f(std::integral_constant<int, 128>{}, std::integral_constant<int, 32>{});
+    else f(std::integral_constant<int, 128>{}, std::integral_constant<int, 64>{});
+  } else {
+    if (BS == 16) f(std::integral_constant<int, 64>{}, std::integral_constant<int, 16>{});
+    else if (BS == 32) f(std::integral_constant<int, 64>{}, std::integral_constant<int, 32>{});
+    else f(std::integral_constant<int, 64>{}, std::integral_constant<int, 64>{});
+  }
+}
+
+}  // namespace
+}  // namespace srswa
+
+extern "C" int srswa_bm_score_fwd(const srswa_bm_score_args* a, void* stream) {
+  if (!a || !a->q || !a->k || !a->pos || !a->z || !a->code || !a->tiemask) {
+    set_error("block-max scores: null argument");
+    return SRSWA_INVALID;
+  }
+  int rc = bm_check(a, "block-max scores");
+  if (rc != SRSWA_OK) return rc;
+  if (a->B == 0 || a->S == 0 || a->nblk == 0) return SRSWA_OK;
+  if (!al16(a->q) || !al16(a->k) || (a->q_sb % 4) || (a->q_st % 4) || (a->k_sb % 4) || (a->k_st % 4)) {
+    set_error("block-max scores: rows must be 16-byte aligned");
+    return SRSWA_UNSUPPORTED;
+  }
+  BmK k{};
+  k.a = *a;
+  k.ntiles = ceil_div(a->S, kBmRows);
+  k.nslab = std::max(1, ceil_div(ceil_div(a->S, kChunk), kBmSlab));
+  if ((int64_t)a->B * k.ntiles * k.nslab > 0x7fffffff) {
+    set_error("block-max scores: grid too large");
+    return SRSWA_UNSUPPORTED;
+  }
+  hipStream_t st = reinterpret_cast<hipStream_t>(stream);
+  bm_dispatch(a->D, a->block_size, [&](auto d, auto bs) { bm_launch_fwd<decltype(d)::value, decltype(bs)::value>(k, st); });
+  const hipError_t e = hipGetLastError();
+  if (e != hipSuccess) {
+    set_error("block-max scores launch failed: %s", hipGetErrorString(e));
+    return SRSWA_LAUNCH;
+  }
+  return SRSWA_OK;
+}
+
+extern "C" int srswa_bm_score_bwd(const srswa_bm_score_bwd_args* a, void* stream) {
+  if (!a || !a->q || !a->k || !a->pos || !a->code || !a->tiemask || !a->gz || !a->dq || !a->dk) {
+    set_error("block-max scores backward: null argument");
+    return SRSWA_INVALID;
+  }
+  srswa_bm_score_args f{};
+  f.B = a->B; f.S = a->S; f.D = a->D; f.nblk = a->nblk; f.block_size = a->block_size;
+  f.local_window = a->local_window;
+  int rc = bm_check(&f, "block-max scores backward");
+  if (rc != SRSWA_OK) return rc;
+  if (a->B == 0 || a->S == 0 || a->nblk == 0) return SRSWA_OK;
+  if (!al16(a->q) || !al16(a->k) || !al16(a->dk) || (a->q_sb % 4) || (a->q_st % 4) || (a->k_sb % 4) ||
+      (a->k_st % 4) || (a->dk_sb % 4) || (a->dk_st % 4)) {
+    set_error("block-max scores backward: rows must be 16-byte aligned");
+    return SRSWA_UNSUPPORTED;
+  }
+  hipStream_t st = reinterpret_cast<hipStream_t>(stream);
+  bm_dispatch(a->D, a->block_size, [&](auto d, auto bs) { bm_launch_bwd<decltype(d)::value, decltype(bs)::value>(*a, st); });
+  const hipError_t e = hipGetLastError();
+  if (e != hipSuccess) {
+    set_error("block-max scores backward launch failed: %s", hipGetErrorString(e));
+    return SRSWA_LAUNCH;
+  }
+  return SRSWA_OK;
+}

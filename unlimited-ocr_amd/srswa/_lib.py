@@ -440,6 +440,68 @@ class KlBwdArgs(ctypes.Structure):
     ]
 
 
+class HcScoreArgs(ctypes.Structure):
+    """Mirror of ``srswa_hc_score_args``."""
+
+    _fields_ = [
+        ("q", _vp), ("q_sb", _i64), ("q_st", _i64),
+        ("k", _vp), ("k_sb", _i64), ("k_st", _i64),
+        ("head_cls", _vp),
+        ("pos", _vp), ("pos_sb", _i64), ("pos_st", _i64),
+        ("kbar", _vp), ("kb_sb", _i64),
+        ("z", _vp), ("z_sb", _i64), ("z_st", _i64),
+        ("B", _i32), ("S", _i32), ("D", _i32), ("nblk", _i32), ("block_size", _i32), ("local_blocks", _i32),
+    ]
+
+
+class HcScoreBwdArgs(ctypes.Structure):
+    """Mirror of ``srswa_hc_score_bwd_args``."""
+
+    _fields_ = [
+        ("q", _vp), ("q_sb", _i64), ("q_st", _i64),
+        ("k", _vp), ("k_sb", _i64), ("k_st", _i64),
+        ("head_cls", _vp),
+        ("pos", _vp), ("pos_sb", _i64), ("pos_st", _i64),
+        ("kbar", _vp), ("kb_sb", _i64),
+        ("z", _vp), ("z_sb", _i64), ("z_st", _i64),
+        ("gz", _vp), ("gz_sb", _i64), ("gz_st", _i64),
+        ("dq", _vp), ("dq_sb", _i64), ("dq_st", _i64),
+        ("dk", _vp), ("dk_sb", _i64), ("dk_st", _i64),
+        ("dhc", _vp),
+        ("B", _i32), ("S", _i32), ("D", _i32), ("nblk", _i32), ("block_size", _i32), ("local_blocks", _i32),
+    ]
+
+
+class BmScoreArgs(ctypes.Structure):
+    """Mirror of ``srswa_bm_score_args``."""
+
+    _fields_ = [
+        ("q", _vp), ("q_sb", _i64), ("q_st", _i64),
+        ("k", _vp), ("k_sb", _i64), ("k_st", _i64),
+        ("pos", _vp), ("pos_sb", _i64), ("pos_st", _i64),
+        ("z", _vp), ("z_sb", _i64), ("z_st", _i64),
+        ("code", _vp),
+        ("tiemask", _vp),
+        ("B", _i32), ("S", _i32), ("D", _i32), ("nblk", _i32), ("block_size", _i32), ("local_window", _i32),
+    ]
+
+
+class BmScoreBwdArgs(ctypes.Structure):
+    """Mirror of ``srswa_bm_score_bwd_args``."""
+
+    _fields_ = [
+        ("q", _vp), ("q_sb", _i64), ("q_st", _i64),
+        ("k", _vp), ("k_sb", _i64), ("k_st", _i64),
+        ("pos", _vp), ("pos_sb", _i64), ("pos_st", _i64),
+        ("code", _vp),
+        ("tiemask", _vp),
+        ("gz", _vp), ("gz_sb", _i64), ("gz_st", _i64),
+        ("dq", _vp), ("dq_sb", _i64), ("dq_st", _i64),
+        ("dk", _vp), ("dk_sb", _i64), ("dk_st", _i64),
+        ("B", _i32), ("S", _i32), ("D", _i32), ("nblk", _i32), ("block_size", _i32), ("local_window", _i32),
+    ]
+
+
 # name -> (restype, argtypes) of every exported entry point
 SIGNATURES = {
     "srswa_version": (ctypes.c_int, []),
@@ -483,6 +545,11 @@ SIGNATURES = {
     "srswa_gather_kl_fwd_ws": (ctypes.c_int, [ctypes.POINTER(KlArgs), _vp, ctypes.c_size_t, _vp]),
     "srswa_gather_kl_bwd_workspace": (ctypes.c_int, [ctypes.POINTER(KlBwdArgs), _szp]),
     "srswa_gather_kl_bwd": (ctypes.c_int, [ctypes.POINTER(KlBwdArgs), _vp, ctypes.c_size_t, _vp]),
+    "srswa_hc_score_fwd": (ctypes.c_int, [ctypes.POINTER(HcScoreArgs), _vp]),
+    "srswa_hc_score_bwd_workspace": (ctypes.c_int, [ctypes.POINTER(HcScoreBwdArgs), _szp]),
+    "srswa_hc_score_bwd": (ctypes.c_int, [ctypes.POINTER(HcScoreBwdArgs), _vp, ctypes.c_size_t, _vp]),
+    "srswa_bm_score_fwd": (ctypes.c_int, [ctypes.POINTER(BmScoreArgs), _vp]),
+    "srswa_bm_score_bwd": (ctypes.c_int, [ctypes.POINTER(BmScoreBwdArgs), _vp]),
 }
 
 STRUCTS = {"srswa_decode_args": DecodeArgs, "srswa_index_args": IndexArgs,
@@ -498,7 +565,9 @@ STRUCTS = {"srswa_decode_args": DecodeArgs, "srswa_index_args": IndexArgs,
            "srswa_page_allow_args": PageAllowArgs, "srswa_local_union_args": LocalUnionArgs,
            "srswa_cos_sin_args": CosSinArgs, "srswa_rope_args": RopeArgs,
            "srswa_block_bounds_args": BlockBoundsArgs, "srswa_candidate_args": CandidateArgs,
-           "srswa_kl_args": KlArgs, "srswa_kl_bwd_args": KlBwdArgs}
+           "srswa_kl_args": KlArgs, "srswa_kl_bwd_args": KlBwdArgs,
+           "srswa_hc_score_args": HcScoreArgs, "srswa_hc_score_bwd_args": HcScoreBwdArgs,
+           "srswa_bm_score_args": BmScoreArgs, "srswa_bm_score_bwd_args": BmScoreBwdArgs}
 
 _lib = None
 _lock = threading.Lock()

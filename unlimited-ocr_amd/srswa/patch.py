@@ -20,6 +20,9 @@ two kernel files (those are replaced file-for-file by
   ``_uocr_dash_decode_allow`` (HF/modeling_unlimitedocr.py:481-528)
 * ``DashAttention._route`` / ``_select_and_bias`` (HF/dash_attention.py:1145-1204),
   the training router -> ``srswa.dash_train``
+* ``DashAttention._block_scores_headcls`` / ``_block_scores``
+  (HF/dash_attention.py:1053-1143 / 1005-1050), the training router's stage-0
+  scorers -> ``srswa.train_scores``
 * ``_KLChunkFn`` (HF/_sparse_base_impl.py:2158-2190), the KL of the indexer
   distillation loss -> ``srswa.kl.KLChunkFn``
 * ``DeepseekV2Indexer.select_and_kl_loss`` (HF/_sparse_base_impl.py:3240-3516),
@@ -39,7 +42,7 @@ import sys
 
 import torch
 
-from . import dash_train, indexer, kl, ops, page_isolation
+from . import dash_train, indexer, kl, ops, page_isolation, train_scores
 from ._lib import UnsupportedShape
 
 SCORE_NEG = -1.0e9
@@ -215,8 +218,36 @@ def _dash_router(mod, done: list) -> None:
                     pass
             return orig(self, prior, cand, nblk)
         return _select_and_bias
+    def make_headcls(orig):
+        def _block_scores_headcls(self, hidden_states, position_embeddings, position_ids, nblk):
+            if hidden_states.is_cuda:
+                try:
+                    return train_scores.block_scores_headcls(
+                        self, hidden_states, position_embeddings, position_ids, nblk,
+                        rope_fn=getattr(dash_mod, "_rope_fn", None),
+                        sanitize_grad=getattr(dash_mod, "_sanitize_grad", None))
+                except UnsupportedShape:
+                    pass
+            return orig(self, hidden_states, position_embeddings, position_ids, nblk)
+        return _block_scores_headcls
+
+    def make_blockmax(orig):
+        def _block_scores(self, hidden_states, position_embeddings, position_ids, nblk):
+            if hidden_states.is_cuda:
+                try:
+                    return train_scores.block_scores(
+                        self, hidden_states, position_embeddings, position_ids, nblk,
+                        rope_fn=getattr(dash_mod, "_rope_fn", None),
+                        sanitize_grad=getattr(dash_mod, "_sanitize_grad", None))
+                except UnsupportedShape:
+                    pass
+            return orig(self, hidden_states, position_embeddings, position_ids, nblk)
+        return _block_scores
+
     _rebind(dash_cls, "_route", make_route, done, "DashAttention._route")
     _rebind(dash_cls, "_select_and_bias", make_select, done, "DashAttention._select_and_bias")
+    _rebind(dash_cls, "_block_scores_headcls", make_headcls, done, "DashAttention._block_scores_headcls")
+    _rebind(dash_cls, "_block_scores", make_blockmax, done, "DashAttention._block_scores")
 
 
 def apply(modeling_deepseekv2, modeling_unlimitedocr=None) -> list:
@@ -305,6 +336,8 @@ def restore(modeling_deepseekv2, modeling_unlimitedocr=None) -> None:
                         (getattr(base, "DeepseekV2Indexer", None), "forward"),
                         (getattr(mod, "DashAttention", None), "_route"),
                         (getattr(mod, "DashAttention", None), "_select_and_bias"),
+                        (getattr(mod, "DashAttention", None), "_block_scores_headcls"),
+                        (getattr(mod, "DashAttention", None), "_block_scores"),
                         (getattr(base, "DeepseekV2IndexerRotary2D", None), "forward"),
                         (base, "_llama_apply_rotary_pos_emb"), (mod, "_llama_apply_rotary_pos_emb"),
                         (base, "_KLChunkFn"),
