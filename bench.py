@@ -892,6 +892,64 @@ def bench_select_kl(args):
                                    "backward, B=2, T=16384, D=128, chunks of 1024 rows"}}
 
 
+def bench_train_scores(args):
+    """The DASH training router's stage-0 scorers on config 5's shape (B=2,
+    S=16384, index dim 128, fp32 index q / k): head_cls (64-key blocks, 8
+    local blocks, the shipped stage) and block-max (512-token window), forward
+    and forward + backward.  head_cls is HBM-bound (the [B, S, nblk] fp32
+    scores dominate); block-max is an fp32 MFMA contraction over every remote
+    (query, key) pair."""
+    import torch
+    from srswa import train_scores as TS
+    dev = torch.device("cuda:0")
+    B, S, D, BS, LB = 2, 16384, 128, 64, 8
+    nblk = S // BS
+    g = torch.Generator(device=dev).manual_seed(17)
+    q = torch.randn(B, S, D, device=dev, generator=g).requires_grad_()
+    k = torch.randn(B, S, D, device=dev, generator=g).requires_grad_()
+    hc = (torch.randn(D, device=dev, generator=g) * 0.2).requires_grad_()
+    pos = torch.arange(S, device=dev)[None].expand(B, S)
+    gz = torch.randn(B, S, nblk, device=dev, generator=g)
+
+    def hc_fwd():
+        return TS.head_cls_scores(q, k, hc, pos, nblk, BS, LB)
+
+    def hc_step():
+        torch.autograd.backward([hc_fwd()], [gz])
+
+    def bm_fwd():
+        return TS.block_max_scores(q, k, pos, nblk, BS, LB * BS)
+
+    def bm_step():
+        torch.autograd.backward([bm_fwd()], [gz])
+
+    with torch.no_grad():
+        ms_hc_f = _time_launches(hc_fwd, args.steps, args.warmup, dev)
+        ms_bm_f = _time_launches(bm_fwd, max(2, args.steps // 4), 2, dev)
+    ms_hc = _time_launches(hc_step, args.steps, args.warmup, dev)
+    ms_bm = _time_launches(bm_step, max(2, args.steps // 4), 2, dev)
+    # algorithmic work: head_cls forward moves q, k (read) and the scores (written);
+    # block-max forward does 2 D flops per remote (query, key) pair
+    hc_bytes = 2 * B * S * D * 4 + B * S * nblk * 4 + B * nblk * D * 4
+    remote_pairs = B * sum(max(0, i - LB * BS + 1) for i in range(S))
+    bm_flops = 2 * D * remote_pairs
+    hc_gbs = hc_bytes / (ms_hc_f * 1e-3) / 1e9
+    bm_tfs = bm_flops / (ms_bm_f * 1e-3) / 1e12
+    return {"metric": "DASH training stage-0 scorer fwd+bwd rows/s (head_cls, config 5 shape)",
+            "value": B * S / (ms_hc * 1e-3), "unit": "rows/s", "n_gpus": 1, "steps": args.steps,
+            "warmup": args.warmup, "ms_per_step": ms_hc, "higher_is_better": True, "scaling": "weak",
+            "vs_baseline": None, "dtype": "f32", "data": "synthetic (seeded)",
+            "config": {"workload": "DashAttention._block_scores_headcls / _block_scores from fp32 index q/k, "
+                                   "B=2, S=16384, D=128, 64-key blocks", "head_cls_fwd_ms": ms_hc_f,
+                       "head_cls_fwd_bwd_ms": ms_hc, "block_max_fwd_ms": ms_bm_f, "block_max_fwd_bwd_ms": ms_bm,
+                       "head_cls_fwd_bytes": hc_bytes, "block_max_fwd_flops": bm_flops},
+            "roofline": {"bound": "hbm", "achieved": hc_gbs, "peak": 8000.0, "unit": "GB/s",
+                         "frac": hc_gbs / 8000.0, "traffic": None,
+                         "kernel": "head_cls forward (summary + score kernels)"},
+            "roofline_block_max": {"bound": "mfma", "achieved": bm_tfs, "peak": 157.3, "unit": "TFLOP/s",
+                                   "frac": bm_tfs / 157.3, "kernel": "bm_fwd_kernel (fp32 MFMA)"}}
+
+
 def bench_copycal(args):
     """Calibration for the HBM traffic counters: a plain device copy of a known
     size (4 GiB read + 4 GiB written per launch, far beyond the 256 MB
@@ -915,7 +973,7 @@ def main():
     ap.add_argument("--warmup", type=int, default=20)
     ap.add_argument("--config", default="decode",
                     choices=["decode", "indexer", "prefill", "fwdbwd", "paged", "paged_prefill", "dash", "page", "kl",
-                             "blockmax", "route", "dash_train", "select_kl", "copycal"])
+                             "blockmax", "route", "dash_train", "select_kl", "train_scores", "copycal"])
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--no-check", action="store_true", help="skip the oracle spot check")
     ap.add_argument("--cpu-budget", type=float, default=12.0)
@@ -930,7 +988,7 @@ def main():
           "fwdbwd": bench_fwdbwd, "paged": bench_paged, "paged_prefill": bench_paged_prefill, "dash": bench_dash,
           "page": bench_page, "kl": bench_kl,
           "blockmax": bench_blockmax, "route": bench_route, "dash_train": bench_dash_train,
-          "select_kl": bench_select_kl,
+          "select_kl": bench_select_kl, "train_scores": bench_train_scores,
           "copycal": bench_copycal}[args.config]
     res = fn(args)
     print(json.dumps(res), flush=True)

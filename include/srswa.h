@@ -844,7 +844,9 @@ typedef struct {
   int32_t B, S, D, nblk, block_size, local_window;
 } srswa_bm_score_bwd_args;
 
-int srswa_bm_score_bwd(const srswa_bm_score_bwd_args* a, void* stream);
+/* workspace: the per-(row, block) gradient weights, B * nblk * S fp32 */
+int srswa_bm_score_bwd_workspace(const srswa_bm_score_bwd_args* a, size_t* scratch_bytes);
+int srswa_bm_score_bwd(const srswa_bm_score_bwd_args* a, void* scratch, size_t scratch_bytes, void* stream);
 
 #ifdef __cplusplus
 }

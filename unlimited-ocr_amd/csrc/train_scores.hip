@@ -526,13 +526,25 @@ __global__ __launch_bounds__(256) void hc_summary_bwd_kernel(HcBK p) {
   for (int j = 0; j < EPL; ++j) hp[j] = hb.pad_overflow ? __builtin_nanf("") : dh[j];
 }
 
+// d head_cls: eight interleaved slices of the block partials, each summed in
+// block order, then the eight slice sums in slice order (fixed order)
+constexpr int kDhcParts = 8;
+
 template <int D>
-__global__ __launch_bounds__(D) void hc_dhc_reduce_kernel(HcBK p) {
-  const int e = threadIdx.x;
+__global__ __launch_bounds__(kDhcParts * D) void hc_dhc_reduce_kernel(HcBK p) {
+  __shared__ float s_part[kDhcParts][D];
+  const int e = threadIdx.x % D, part = threadIdx.x / D;
   const int64_t n = (int64_t)p.a.B * p.a.nblk;
   float s = 0.f;
-  for (int64_t i = 0; i < n; ++i) s += p.dhc_part[i * D + e];
-  p.a.dhc[e] = s;
+  for (int64_t i = part; i < n; i += kDhcParts) s += p.dhc_part[i * D + e];
+  s_part[part][e] = s;
+  __syncthreads();
+  if (part == 0) {
+    float t = s_part[0][e];
+#pragma unroll
+    for (int k = 1; k < kDhcParts; ++k) t += s_part[k][e];
+    p.a.dhc[e] = t;
+  }
 }
 
 // ---------------------------------------------------------------- block max
@@ -684,29 +696,62 @@ __global__ __launch_bounds__(kBmThreads) void bm_fwd_kernel(BmK p) {
   }
 }
 
+// The block-max backward's weights w[b, c, i] = gz[b, i, c] / n (0 where no key
+// of block c takes row i's gradient), block-major: written by bm_bwd_dq, read
+// by bm_bwd_dk.
+struct BmBK {
+  srswa_bm_score_bwd_args a;
+  float* wT;                 // [B, nblk, S]
+};
+
+// the last block holding a key at or below p - LW (-1: none)
+__device__ __forceinline__ int bm_last_remote(int p, int LW, int BS) { return p - LW >= 0 ? (p - LW) / BS : -1; }
+
 // dq: 16 rows per wave (64 per workgroup); per group of 64 blocks the codes
-// and weights g / n are staged in LDS, then for each block the 16 rows' key
-// rows are loaded together (lanes over the head dims) and accumulated in
-// block order
+// and weights g / n are staged in LDS (and the weights stored block-major for
+// bm_bwd_dk), then for each block up to the tile's last remote one the 16
+// rows' key rows are loaded together (lanes over the head dims) and
+// accumulated in block order.
 template <int D, int BS>
-__global__ __launch_bounds__(256) void bm_bwd_dq_kernel(srswa_bm_score_bwd_args a) {
+__global__ __launch_bounds__(256) void bm_bwd_dq_kernel(BmBK p) {
   constexpr int EPL = D / kWave;
   __shared__ int s_code[kTsGroup * kTsPad];     // [block][row]
   __shared__ float s_w[kTsGroup * kTsPad];      // [block][row]
+  __shared__ int s_red[4];
+  const srswa_bm_score_bwd_args& a = p.a;
   const int wave = threadIdx.x / kWave, lane = threadIdx.x % kWave;
   const int ntiles = (a.S + kTsRows - 1) / kTsRows;
   const int b = blockIdx.x / ntiles, tile = blockIdx.x % ntiles;
   const int r0 = tile * kTsRows;
   const int nr = min(kTsRows, a.S - r0);
   const float* kg = a.k + (int64_t)b * a.k_sb + EPL * lane;
+  const int nblk_keys = min(a.nblk, ceil_div(a.S, BS));   // blocks that can hold a key
+  int trm;                                                // the tile's last remote block
+  {
+    const int row = r0 + (int)(threadIdx.x % kTsRows);
+    const int rm = row < a.S ? bm_last_remote(a.pos[(int64_t)b * a.pos_sb + (int64_t)row * a.pos_st], a.local_window,
+                                              BS)
+                             : -1;
+    const int wm = wave_max_int(rm);
+    if (lane == 0) s_red[wave] = wm;
+    __syncthreads();
+    trm = min(max(max(s_red[0], s_red[1]), max(s_red[2], s_red[3])), nblk_keys - 1);
+  }
   float acc[16][EPL];
 #pragma unroll
   for (int r = 0; r < 16; ++r)
 #pragma unroll
     for (int j = 0; j < EPL; ++j) acc[r][j] = 0.f;
-  const int nblk_keys = min(a.nblk, ceil_div(a.S, BS));   // blocks that can hold a key
   for (int g0 = 0; g0 < nblk_keys; g0 += kTsGroup) {
     const int gn = min(kTsGroup, nblk_keys - g0);
+    float* wdst = p.wT + ((int64_t)b * a.nblk + g0) * a.S + r0;
+    if (g0 > trm) {                       // no row of the tile reaches these blocks
+      for (int i = threadIdx.x; i < gn * kTsRows; i += blockDim.x) {
+        const int c = i / kTsRows, r = i % kTsRows;
+        if (r < nr) wdst[(int64_t)c * a.S + r] = 0.f;
+      }
+      continue;
+    }
     __syncthreads();
     for (int i = threadIdx.x; i < gn * kTsRows; i += blockDim.x) {
       const int c = i / kTsRows, r = i % kTsRows;           // codes: rows contiguous
@@ -722,7 +767,12 @@ __global__ __launch_bounds__(256) void bm_bwd_dq_kernel(srswa_bm_score_bwd_args 
       s_w[c * kTsPad + r] = w;
     }
     __syncthreads();
-    for (int c = 0; c < gn; ++c) {
+    for (int i = threadIdx.x; i < gn * kTsRows; i += blockDim.x) {
+      const int c = i / kTsRows, r = i % kTsRows;           // weights, block-major
+      if (r < nr) wdst[(int64_t)c * a.S + r] = s_w[c * kTsPad + r];
+    }
+    const int cn = min(gn, trm - g0 + 1);
+    for (int c = 0; c < cn; ++c) {
       const int blk = g0 + c;
       float kv[16][EPL];
 #pragma unroll
@@ -730,10 +780,10 @@ __global__ __launch_bounds__(256) void bm_bwd_dq_kernel(srswa_bm_score_bwd_args 
         const int rr = 16 * wave + r;
         const int cd = s_code[c * kTsPad + rr];
         const float w = s_w[c * kTsPad + rr];
-        const int j = blk * BS + (cd & 0xff);
 #pragma unroll
         for (int e = 0; e < EPL; ++e) kv[r][e] = 0.f;
         if (w != 0.f && !(cd & kCodeMulti)) {
+          const int j = blk * BS + (cd & 0xff);
 #pragma unroll
           for (int e = 0; e < EPL; ++e) kv[r][e] = kg[(int64_t)j * a.k_st + e];
         }
@@ -773,15 +823,22 @@ __global__ __launch_bounds__(256) void bm_bwd_dq_kernel(srswa_bm_score_bwd_args 
 }
 
 // dk: one wave per (sequence, block, four keys); lane group k (16 lanes)
-// owns key 4 w + k's D / 16 head dims per lane.  The block's codes are scanned
-// 64 rows at a time in row order; the rows whose gradient reaches a key are
-// taken one per lane group per step (four rows per load instruction).
+// owns key 4 w + k's D / 16 head dims per lane.  The block's codes and
+// weights are scanned 64 rows at a time in row order (the next batch loaded
+// while this one is taken); the rows whose gradient reaches a key are taken
+// one per lane group per step (four rows per load instruction).
 template <int D, int BS>
-__global__ __launch_bounds__(256) void bm_bwd_dk_kernel(srswa_bm_score_bwd_args a) {
+__global__ __launch_bounds__(256) void bm_bwd_dk_kernel(BmBK p) {
   constexpr int DPL = D / 16;                    // head dims per lane
   constexpr int QPB = BS / 4;                    // key quads per block
+  const srswa_bm_score_bwd_args& a = p.a;
   const int wave = threadIdx.x / kWave, lane = threadIdx.x % kWave;
-  const int64_t gw = (int64_t)blockIdx.x * 4 + wave;
+  // workgroups are dealt to the eight XCDs round-robin: consecutive logical
+  // ids (the quads of one block) are kept on one XCD so its L2 serves the
+  // block's code column to all of them
+  const int per_xcd = (int)(gridDim.x / 8);
+  const int64_t lid = (int64_t)(blockIdx.x & 7) * per_xcd + (blockIdx.x >> 3);
+  const int64_t gw = lid * 4 + wave;
   const int nblk_keys = min(a.nblk, ceil_div(a.S, BS));
   if (gw >= (int64_t)a.B * nblk_keys * QPB) return;
   const int quad = (int)(gw % QPB);
@@ -791,17 +848,27 @@ __global__ __launch_bounds__(256) void bm_bwd_dk_kernel(srswa_bm_score_bwd_args 
   const int off0 = 4 * quad;                      // first key offset of the quad
   const int my_key = off0 + kgrp;
   const int32_t* col = a.code + ((int64_t)b * a.nblk + blk) * a.S;
+  const float* wcol = p.wT + ((int64_t)b * a.nblk + blk) * a.S;
   const float* qb = a.q + (int64_t)b * a.q_sb + DPL * dl;
   float acc[DPL];
 #pragma unroll
   for (int e = 0; e < DPL; ++e) acc[e] = 0.f;
+  int cd_n = lane < a.S ? col[lane] : kCodeNone;
+  float w_n = lane < a.S ? wcol[lane] : 0.f;
   for (int i0 = 0; i0 < a.S; i0 += kWave) {
     const int i = i0 + lane;
-    const int cd = i < a.S ? col[i] : kCodeNone;
+    const int cd = cd_n;
+    const float w = w_n;
+    if (i + kWave < a.S) {
+      cd_n = col[i + kWave];
+      w_n = wcol[i + kWave];
+    } else {
+      cd_n = kCodeNone;
+      w_n = 0.f;
+    }
     // which keys of the quad this row's gradient reaches (bit k)
     uint32_t hit = 0;
-    float w = 0.f;
-    if (!(cd & kCodeNone)) {
+    if (w != 0.f) {
       if (cd & kCodeMulti) {
         const uint64_t m = a.tiemask[((int64_t)b * a.S + i) * a.nblk + blk];
         hit = (uint32_t)((m >> off0) & 0xfu);
@@ -809,7 +876,6 @@ __global__ __launch_bounds__(256) void bm_bwd_dk_kernel(srswa_bm_score_bwd_args 
         const int f = (cd & 0xff) - off0;
         hit = (f >= 0 && f < 4) ? 1u << f : 0u;
       }
-      if (hit) w = a.gz[(int64_t)b * a.gz_sb + (int64_t)i * a.gz_st + blk] / (float)((cd >> 8) & 0xff);
     }
     if (!__any(hit != 0)) continue;
     uint64_t bal[4];
@@ -955,12 +1021,12 @@ extern "C" int srswa_hc_score_bwd(const srswa_hc_score_bwd_args* a, void* scratc
     hipLaunchKernelGGL(hc_score_bwd_dq_kernel<128>, gq, dim3(256), 0, st, k);
     hipLaunchKernelGGL(hc_score_bwd_dkbar_kernel<128>, gk, dim3(256), 0, st, k);
     hipLaunchKernelGGL(hc_summary_bwd_kernel<128>, gs, dim3(256), 0, st, k);
-    hipLaunchKernelGGL(hc_dhc_reduce_kernel<128>, dim3(1), dim3(128), 0, st, k);
+    hipLaunchKernelGGL(hc_dhc_reduce_kernel<128>, dim3(1), dim3(kDhcParts * 128), 0, st, k);
   } else {
     hipLaunchKernelGGL(hc_score_bwd_dq_kernel<64>, gq, dim3(256), 0, st, k);
     hipLaunchKernelGGL(hc_score_bwd_dkbar_kernel<64>, gk, dim3(256), 0, st, k);
     hipLaunchKernelGGL(hc_summary_bwd_kernel<64>, gs, dim3(256), 0, st, k);
-    hipLaunchKernelGGL(hc_dhc_reduce_kernel<64>, dim3(1), dim3(64), 0, st, k);
+    hipLaunchKernelGGL(hc_dhc_reduce_kernel<64>, dim3(1), dim3(kDhcParts * 64), 0, st, k);
   }
   const hipError_t e = hipGetLastError();
   if (e != hipSuccess) {
@@ -996,12 +1062,14 @@ void bm_launch_fwd(const BmK& k, hipStream_t st) {
 }
 
 template <int D, int BS>
-void bm_launch_bwd(const srswa_bm_score_bwd_args& a, hipStream_t st) {
+void bm_launch_bwd(const BmBK& k, hipStream_t st) {
+  const srswa_bm_score_bwd_args& a = k.a;
   const int ntiles = (a.S + kTsRows - 1) / kTsRows;
-  hipLaunchKernelGGL((bm_bwd_dq_kernel<D, BS>), dim3((unsigned)((int64_t)a.B * ntiles)), dim3(256), 0, st, a);
+  hipLaunchKernelGGL((bm_bwd_dq_kernel<D, BS>), dim3((unsigned)((int64_t)a.B * ntiles)), dim3(256), 0, st, k);
   const int64_t waves = (int64_t)a.B * std::min(a.nblk, (a.S + BS - 1) / BS) * (BS / 4);
-  if (waves > 0)
-    hipLaunchKernelGGL((bm_bwd_dk_kernel<D, BS>), dim3((unsigned)((waves + 3) / 4)), dim3(256), 0, st, a);
+  if (waves > 0)   // a multiple of 8 workgroups (the XCD deal), surplus ones exit at once
+    hipLaunchKernelGGL((bm_bwd_dk_kernel<D, BS>), dim3((unsigned)(((waves + 3) / 4 + 7) / 8 * 8)), dim3(256), 0,
+                       st, k);
 }
 
 template <typename F>
@@ -1050,8 +1118,8 @@ extern "C" int srswa_bm_score_fwd(const srswa_bm_score_args* a, void* stream) {
   return SRSWA_OK;
 }
 
-extern "C" int srswa_bm_score_bwd(const srswa_bm_score_bwd_args* a, void* stream) {
-  if (!a || !a->q || !a->k || !a->pos || !a->code || !a->tiemask || !a->gz || !a->dq || !a->dk) {
+extern "C" int srswa_bm_score_bwd_workspace(const srswa_bm_score_bwd_args* a, size_t* scratch_bytes) {
+  if (!a || !scratch_bytes) {
     set_error("block-max scores backward: null argument");
     return SRSWA_INVALID;
   }
@@ -1060,14 +1128,34 @@ extern "C" int srswa_bm_score_bwd(const srswa_bm_score_bwd_args* a, void* stream
   f.local_window = a->local_window;
   int rc = bm_check(&f, "block-max scores backward");
   if (rc != SRSWA_OK) return rc;
+  *scratch_bytes = (size_t)a->B * a->nblk * a->S * sizeof(float);
+  return SRSWA_OK;
+}
+
+extern "C" int srswa_bm_score_bwd(const srswa_bm_score_bwd_args* a, void* scratch, size_t scratch_bytes,
+                                  void* stream) {
+  if (!a || !a->q || !a->k || !a->pos || !a->code || !a->tiemask || !a->gz || !a->dq || !a->dk) {
+    set_error("block-max scores backward: null argument");
+    return SRSWA_INVALID;
+  }
+  size_t need = 0;
+  int rc = srswa_bm_score_bwd_workspace(a, &need);
+  if (rc != SRSWA_OK) return rc;
   if (a->B == 0 || a->S == 0 || a->nblk == 0) return SRSWA_OK;
+  if (!scratch || scratch_bytes < need || !al16(scratch)) {
+    set_error("block-max scores backward: scratch of %zu bytes required (got %zu)", need, scratch_bytes);
+    return SRSWA_WORKSPACE;
+  }
   if (!al16(a->q) || !al16(a->k) || !al16(a->dk) || (a->q_sb % 4) || (a->q_st % 4) || (a->k_sb % 4) ||
       (a->k_st % 4) || (a->dk_sb % 4) || (a->dk_st % 4)) {
     set_error("block-max scores backward: rows must be 16-byte aligned");
     return SRSWA_UNSUPPORTED;
   }
+  BmBK k{};
+  k.a = *a;
+  k.wT = reinterpret_cast<float*>(scratch);
   hipStream_t st = reinterpret_cast<hipStream_t>(stream);
-  bm_dispatch(a->D, a->block_size, [&](auto d, auto bs) { bm_launch_bwd<decltype(d)::value, decltype(bs)::value>(*a, st); });
+  bm_dispatch(a->D, a->block_size, [&](auto d, auto bs) { bm_launch_bwd<decltype(d)::value, decltype(bs)::value>(k, st); });
   const hipError_t e = hipGetLastError();
   if (e != hipSuccess) {
     set_error("block-max scores backward launch failed: %s", hipGetErrorString(e));

@@ -549,7 +549,8 @@ SIGNATURES = {
     "srswa_hc_score_bwd_workspace": (ctypes.c_int, [ctypes.POINTER(HcScoreBwdArgs), _szp]),
     "srswa_hc_score_bwd": (ctypes.c_int, [ctypes.POINTER(HcScoreBwdArgs), _vp, ctypes.c_size_t, _vp]),
     "srswa_bm_score_fwd": (ctypes.c_int, [ctypes.POINTER(BmScoreArgs), _vp]),
-    "srswa_bm_score_bwd": (ctypes.c_int, [ctypes.POINTER(BmScoreBwdArgs), _vp]),
+    "srswa_bm_score_bwd_workspace": (ctypes.c_int, [ctypes.POINTER(BmScoreBwdArgs), _szp]),
+    "srswa_bm_score_bwd": (ctypes.c_int, [ctypes.POINTER(BmScoreBwdArgs), _vp, ctypes.c_size_t, _vp]),
 }
 
 STRUCTS = {"srswa_decode_args": DecodeArgs, "srswa_index_args": IndexArgs,

@@ -195,7 +195,12 @@ class BlockMaxScoreFn(torch.autograd.Function):
             dq=dq.data_ptr(), dq_sb=dq.stride(0), dq_st=dq.stride(1),
             dk=dk.data_ptr(), dk_sb=dk.stride(0), dk_st=dk.stride(1),
             B=B, S=S, D=D, nblk=nblk, block_size=block_size, local_window=local_window)
-        _lib.check(_lib.lib().srswa_bm_score_bwd(ctypes.byref(a), _lib.stream_ptr(q.device)), "srswa_bm_score_bwd")
+        need = ctypes.c_size_t()
+        _lib.check(_lib.lib().srswa_bm_score_bwd_workspace(ctypes.byref(a), ctypes.byref(need)),
+                   "srswa_bm_score_bwd_workspace")
+        scr = _lib.scratch(q.device, need.value)
+        _lib.check(_lib.lib().srswa_bm_score_bwd(ctypes.byref(a), _lib.ptr(scr), need.value, _lib.stream_ptr(q.device)),
+                   "srswa_bm_score_bwd")
         return dq, dk, None, None, None, None
 
 
