@@ -10,6 +10,7 @@ import pytest
 import torch
 
 from oracle import srswa_oracle as O
+from parity_report import report_error
 from srswa import ops
 from tolerance import assert_close_lowp
 
@@ -104,6 +105,11 @@ def test_tail_split_matches_whole_tiles(dev, name):
     for o, l, what in ((o_s, l_s, "split"), (o_w, l_w, "whole")):
         assert_close_lowp(o.cpu().double(), ro, c.get("dtype", torch.bfloat16), TOL, f"forward {name} {what}: o")
         assert (l.cpu().double() - rl).abs().max().item() <= TOL
+    # the two forms of the same rows against each other: only their rounding differs
+    d_o = (o_s.double() - o_w.double()).abs().max().item()
+    d_l = (l_s.double() - l_w.double()).abs().max().item()
+    report_error(f"forward {name} split vs whole: o", o_s, o_w, TOL)
+    assert d_o <= TOL and d_l <= 1e-4, (d_o, d_l)
     # the split must have happened: one partial round of tiles
     a = _lib.FwdArgs()
     a.B, a.T, a.Sk, a.HQ, a.HKV, a.HI, a.D, a.S = B, T, Sk, HQ, k.shape[2], bi.shape[1], D, bi.shape[-1]
