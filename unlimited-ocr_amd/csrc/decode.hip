@@ -476,7 +476,7 @@ __global__ __launch_bounds__(kDecodeWaves * kWave) void decode_kernel(DecodeK p)
   }
   if (a.lse && lane == 0) {
     a.lse[(int64_t)b * a.lse_sb + (int64_t)lq * a.lse_sq + (int64_t)hq * a.lse_sh] =
-        L > 0.f ? M * kLn2 + logf(L) : -INFINITY;
+        L > 0.f ? fmaf(M, kLn2, logf(L)) : -INFINITY;   // one rounding wherever it is inlined
   }
 }
 
@@ -533,7 +533,7 @@ __global__ __launch_bounds__(256) void decode_merge_kernel(DecodeK p) {
   store_out<TO>(orow, O, DPL);
   if (a.lse && lane == 0)
     a.lse[(int64_t)b * a.lse_sb + (int64_t)lq * a.lse_sq + (int64_t)hq * a.lse_sh] =
-        L > 0.f ? M * kLn2 + logf(L) : -INFINITY;
+        L > 0.f ? fmaf(M, kLn2, logf(L)) : -INFINITY;   // one rounding wherever it is inlined
 }
 
 int elem_bytes(int dt) { return dt == SRSWA_F32 ? 4 : 2; }
