@@ -117,14 +117,15 @@ def test_paged_decode_head_expanded_ids(dev, with_bias):
     assert_close_lowp(outs[0].cpu(), ref, c["dtype"], 2e-2, "expanded ids")
 
 
+@pytest.mark.parametrize("qdt", [torch.bfloat16, torch.float16])
 @pytest.mark.parametrize("fmt", ["float8_e4m3fn", "float8_e4m3fnuz", "float8_e5m2", "float8_e5m2fnuz"])
-def test_fp8_cache_every_byte_exact(dev, fmt):
+def test_fp8_cache_every_byte_exact(dev, fmt, qdt):
     """Every byte value of the fp8 format, NaN and infinity codes included,
     through both paged kernels: each request holds one key, so its output is
-    its V row converted to bf16, which must equal torch's conversion exactly
-    (the decode and the K10 prefill)."""
+    its V row converted to q's dtype, which must equal torch's conversion
+    exactly (the decode and the K10 prefill, bf16 and fp16 queries)."""
     from srswa import unlimited_dash_ops as U
-    print(f"fp8 bytes {fmt}", flush=True)
+    print(f"fp8 bytes {fmt} {qdt}", flush=True)
     dt = getattr(torch, fmt)
     R, page, D = 2, 16, 128
     kc = torch.zeros(R, page, 1, D, dtype=torch.uint8)               # K = +0 (code 0 in every format)
@@ -132,10 +133,10 @@ def test_fp8_cache_every_byte_exact(dev, fmt):
     vc[0, 0, 0] = torch.arange(128, dtype=torch.uint8)
     vc[1, 0, 0] = torch.arange(128, 256, dtype=torch.uint8)
     kc, vc = kc.view(dt), vc.view(dt)
-    want = vc[:, 0, 0].to(torch.float32).to(torch.bfloat16)         # [R, D]
+    want = vc[:, 0, 0].to(torch.float32).to(qdt)                    # [R, D]
     bt = torch.arange(R, dtype=torch.int32).view(R, 1)
     sl = torch.ones(R, dtype=torch.int32)
-    q = torch.randn(R, 1, D).to(torch.bfloat16)
+    q = torch.randn(R, 1, D).to(qdt)
     topk = torch.full((1, R, 4), -1, dtype=torch.int32)
 
     def same(got, what):
@@ -145,11 +146,11 @@ def test_fp8_cache_every_byte_exact(dev, fmt):
         ok = (g == w) | (torch.isnan(g) & torch.isnan(w))
         assert ok.all(), (what, fmt, int((~ok).sum()))
 
-    out = torch.empty(R, 1, D, dtype=torch.bfloat16, device=dev)
+    out = torch.empty(R, 1, D, dtype=qdt, device=dev)
     U.dash_sparse_attn_decode(q.to(dev), kc.to(dev), vc.to(dev), topk.to(dev), None, bt.to(dev), sl.to(dev), 1,
                               0.1, out, 1, local_blocks=1, sparse_block_size=page)
     same(out, "decode")
-    out2 = torch.empty(R, 1, D, dtype=torch.bfloat16, device=dev)
+    out2 = torch.empty(R, 1, D, dtype=qdt, device=dev)
     cu = torch.arange(R + 1, dtype=torch.int32)
     U.dash_sparse_attn(q.to(dev), kc.to(dev), vc.to(dev), topk.to(dev), None, bt.to(dev), cu.to(dev), sl.to(dev),
                        torch.zeros(R, dtype=torch.int32).to(dev), 1, 1, 0.1, out2, local_blocks=1,

@@ -85,63 +85,131 @@ template <> struct Vec16<__half> {
 // fp8 K/V cache formats (srswa_dtype codes of the k_cache / v_cache of the
 // paged serving kernels).  Every fp8 value is exact in bf16 and fp16, so the
 // kernels convert at load time and run their 16-bit paths unchanged, as the
-// reference's `k.to(q.dtype)` does, on gfx950's conversion instructions
-// (v_cvt_pk_f32_fp8 / _bf8 interpret the OCP e4m3fn / e5m2 formats).
+// reference's `k.to(q.dtype)` does, on gfx950's scaled conversions
+// (v_cvt_scalef32_pk_{f32,bf16,f16}_{fp8,bf8}: two bytes of a word per
+// instruction, read as the OCP e4m3fn / e5m2 formats and multiplied by a power
+// of two).
 constexpr int kFp8E4M3FN = 3, kFp8E4M3FNUZ = 4, kFp8E5M2 = 5, kFp8E5M2FNUZ = 6;
 
 typedef float f32x2_t __attribute__((ext_vector_type(2)));
+typedef _Float16 f16x2_native_t __attribute__((ext_vector_type(2)));
 
-// four fp8 bytes of w (byte 0 first) -> fp32.  An FNUZ byte is the same OCP
-// byte's value halved (its bias is one higher), except 0x80 (FNUZ NaN, OCP -0)
-// and the codes OCP keeps for NaN / infinity, which FNUZ uses for ordinary
-// values: |b| = 0x7f in e4m3 (240), exponent 31 in e5m2 ((1 + m/4) 2^15).
+// An FNUZ byte is the same OCP byte's value halved (its exponent bias is one
+// higher), so the FNUZ formats convert with scale 1/2, except three kinds of
+// byte that OCP reads differently: 0x80 (FNUZ NaN, OCP -0) and the codes OCP
+// keeps for NaN / infinity, which FNUZ uses for ordinary values (|b| = 0x7f in
+// e4m3: 240; exponent 31 in e5m2: (1 + m/4) 2^15).
+template <int F>
+struct Fp8Fmt {
+  static constexpr bool E4 = F == kFp8E4M3FN || F == kFp8E4M3FNUZ;
+  static constexpr bool FNUZ = F == kFp8E4M3FNUZ || F == kFp8E5M2FNUZ;
+  static constexpr float kScale = FNUZ ? 0.5f : 1.f;
+};
+
+// Bit 7 of a byte of the result is set when that byte of w may be one of the
+// FNUZ bytes above (never missed; a borrow between bytes can flag a harmless
+// neighbour), so a word whose result is 0 takes the fast conversion as is.
+//   (~w & e) - 1: a byte with all exponent bits set (and, for e4m3, all
+//                 mantissa bits) is 0 before the subtraction and 0xff after;
+//                 any other byte stays below 0x80;
+//   ((w & 0x7f) - 1) & w: bit 7 of 0x80 (magnitude 0, sign set).
+template <bool E4>
+__device__ __forceinline__ uint32_t fnuz_special_bits(uint32_t w) {
+  constexpr uint32_t kE = E4 ? 0x7f7f7f7fu : 0x7c7c7c7cu;
+  const uint32_t t1 = (~w & kE) - 0x01010101u;
+  const uint32_t t2 = ((w & 0x7f7f7f7fu) - 0x01010101u) & w;
+  return t1 | t2;
+}
+
+// the FNUZ value of byte i of w when it is one of the bytes OCP reads
+// differently, else v (that byte's fast conversion)
+template <bool E4>
+__device__ __forceinline__ float fnuz_fix(uint32_t w, int i, float v) {
+  const uint32_t b = (w >> (8 * i)) & 0xffu;
+  if constexpr (E4) {
+    v = (b & 0x7fu) == 0x7fu ? ((b & 0x80u) ? -240.f : 240.f) : v;
+  } else {
+    const float big = (float)(4u + (b & 3u)) * 8192.f;   // (1 + m/4) 2^15
+    v = (b & 0x7cu) == 0x7cu ? ((b & 0x80u) ? -big : big) : v;
+  }
+  return b == 0x80u ? __uint_as_float(0x7fc00000u) : v;
+}
+
+// two bytes (the low half of w, or the high half when HI) -> fp32 pair
+template <int F, bool HI>
+__device__ __forceinline__ f32x2_t fp8x2_f32(uint32_t w) {
+  if constexpr (Fp8Fmt<F>::E4) return __builtin_amdgcn_cvt_scalef32_pk_f32_fp8(w, Fp8Fmt<F>::kScale, HI);
+  else return __builtin_amdgcn_cvt_scalef32_pk_f32_bf8(w, Fp8Fmt<F>::kScale, HI);
+}
+
+// four fp8 bytes of w (byte 0 first) -> fp32
 template <int F>
 __device__ __forceinline__ void fp8x4_to_f32(uint32_t w, float* f) {
-  constexpr bool E4 = F == kFp8E4M3FN || F == kFp8E4M3FNUZ;
-  constexpr bool FNUZ = F == kFp8E4M3FNUZ || F == kFp8E5M2FNUZ;
-  f32x2_t lo, hi;
-  if constexpr (E4) {
-    lo = __builtin_amdgcn_cvt_pk_f32_fp8((int)w, false);
-    hi = __builtin_amdgcn_cvt_pk_f32_fp8((int)w, true);
-  } else {
-    lo = __builtin_amdgcn_cvt_pk_f32_bf8((int)w, false);
-    hi = __builtin_amdgcn_cvt_pk_f32_bf8((int)w, true);
-  }
-  f[0] = lo.x;
-  f[1] = lo.y;
-  f[2] = hi.x;
-  f[3] = hi.y;
-  if constexpr (FNUZ) {
+  const f32x2_t lo = fp8x2_f32<F, false>(w), hi = fp8x2_f32<F, true>(w);
+  f[0] = lo[0];
+  f[1] = lo[1];
+  f[2] = hi[0];
+  f[3] = hi[1];
+  if constexpr (Fp8Fmt<F>::FNUZ) {
+    if (__builtin_expect((fnuz_special_bits<Fp8Fmt<F>::E4>(w) & 0x80808080u) != 0u, 0)) {
 #pragma unroll
-    for (int i = 0; i < 4; ++i) f[i] *= 0.5f;
-    // the bytes OCP reads differently (rare): a zero byte of t flags them
-    constexpr uint32_t kMask = E4 ? 0x7f7f7f7fu : 0x7c7c7c7cu;
-    const uint32_t t1 = (w & kMask) ^ kMask, t2 = w ^ 0x80808080u;
-    const uint32_t zero_byte = ((t1 - 0x01010101u) & ~t1 & 0x80808080u) | ((t2 - 0x01010101u) & ~t2 & 0x80808080u);
-    if (__builtin_expect(zero_byte != 0u, 0)) {
+      for (int i = 0; i < 4; ++i) f[i] = fnuz_fix<Fp8Fmt<F>::E4>(w, i, f[i]);
+    }
+  }
+}
+
+// eight fp8 bytes -> fp32, one word test for both words
+template <int F>
+__device__ __forceinline__ void fp8x8_to_f32(const uint2& w, float* f) {
+  const f32x2_t p0 = fp8x2_f32<F, false>(w.x), p1 = fp8x2_f32<F, true>(w.x);
+  const f32x2_t p2 = fp8x2_f32<F, false>(w.y), p3 = fp8x2_f32<F, true>(w.y);
+  f[0] = p0[0]; f[1] = p0[1]; f[2] = p1[0]; f[3] = p1[1];
+  f[4] = p2[0]; f[5] = p2[1]; f[6] = p3[0]; f[7] = p3[1];
+  if constexpr (Fp8Fmt<F>::FNUZ) {
+    constexpr bool E4 = Fp8Fmt<F>::E4;
+    if (__builtin_expect(((fnuz_special_bits<E4>(w.x) | fnuz_special_bits<E4>(w.y)) & 0x80808080u) != 0u, 0)) {
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
-        const uint32_t b = (w >> (8 * i)) & 0xffu;
-        float v = f[i];
-        if constexpr (E4) {
-          v = (b & 0x7fu) == 0x7fu ? ((b & 0x80u) ? -240.f : 240.f) : v;
-        } else {
-          const float big = (float)(4u + (b & 3u)) * 8192.f;   // (1 + m/4) 2^15
-          v = (b & 0x7cu) == 0x7cu ? ((b & 0x80u) ? -big : big) : v;
-        }
-        f[i] = b == 0x80u ? __uint_as_float(0x7fc00000u) : v;
+        f[i] = fnuz_fix<E4>(w.x, i, f[i]);
+        f[4 + i] = fnuz_fix<E4>(w.y, i, f[4 + i]);
       }
     }
   }
 }
 
-// eight fp8 bytes -> eight values of T (bf16 / fp16) as one 16-byte vector
+// two bytes (the low half of w, or the high half when HI) -> a packed pair of T
+// (bf16 / fp16)
+template <int F, typename T, bool HI>
+__device__ __forceinline__ uint32_t fp8x2_to(uint32_t w) {
+  constexpr bool E4 = Fp8Fmt<F>::E4;
+  constexpr float s = Fp8Fmt<F>::kScale;
+  if constexpr (std::is_same<T, bf16_t>::value) {
+    if constexpr (E4) return __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(w, s, HI));
+    else return __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_bf8(w, s, HI));
+  } else {
+    static_assert(std::is_same<T, __half>::value, "fp8 caches convert to bf16 or fp16");
+    if constexpr (E4) return __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_f16_fp8(w, s, HI));
+    else return __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_f16_bf8(w, s, HI));
+  }
+}
+
+// eight fp8 bytes -> eight values of T (bf16 / fp16) as one 16-byte vector:
+// one instruction per pair, and for FNUZ one word test for both words (the
+// rare flagged piece is converted again through fp32 and fixed up)
 template <int F, typename T>
 __device__ __forceinline__ uint4 fp8x8_to(const uint2& w) {
-  float f[8];
-  fp8x4_to_f32<F>(w.x, f);
-  fp8x4_to_f32<F>(w.y, f + 4);
-  return Vec16<T>::pack(f);
+  uint4 r = make_uint4(fp8x2_to<F, T, false>(w.x), fp8x2_to<F, T, true>(w.x), fp8x2_to<F, T, false>(w.y),
+                       fp8x2_to<F, T, true>(w.y));
+  if constexpr (Fp8Fmt<F>::FNUZ) {
+    constexpr bool E4 = Fp8Fmt<F>::E4;
+    if (__builtin_expect(((fnuz_special_bits<E4>(w.x) | fnuz_special_bits<E4>(w.y)) & 0x80808080u) != 0u, 0)) {
+      float f[8];
+      fp8x4_to_f32<F>(w.x, f);
+      fp8x4_to_f32<F>(w.y, f + 4);
+      r = Vec16<T>::pack(f);
+    }
+  }
+  return r;
 }
 
 // Runs fn(std::integral_constant<int, F>) for the fp8 format fmt: one uniform

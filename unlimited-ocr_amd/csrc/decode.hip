@@ -408,8 +408,7 @@ __global__ __launch_bounds__(kDecodeWaves * kWave) void decode_kernel(DecodeK p)
 #pragma unroll
         for (int i = 0; i < NI; ++i) {
           float f[8];
-          fp8x4_to_f32<decltype(F)::value>(vw[i].w.x, f);
-          fp8x4_to_f32<decltype(F)::value>(vw[i].w.y, f + 4);
+          fp8x8_to_f32<decltype(F)::value>(vw[i].w, f);
 #pragma unroll
           for (int e = 0; e < EPV; ++e) acc[e] = fmaf(pv[i], f[e], acc[e]);
         }
