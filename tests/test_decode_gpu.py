@@ -195,3 +195,27 @@ def test_wide_slot_gather_form(dev, K):
                               block_size=BS, local_window=LW, scale=1 / math.sqrt(D)).cpu()
     from tolerance import assert_close_lowp
     assert_close_lowp(out, ref.double(), torch.bfloat16, BF16_TOL, f"gather decode wide slots K={K}")
+
+
+def test_overlapping_cache_rows(dev):
+    """A cache view whose row stride is below the head dim (rows overlap) is
+    read through its strides as given (the ABI takes any strides with a unit
+    head-dim stride): gather form, bf16, two positions, against the
+    gather-form oracle on the materialised view."""
+    g = torch.Generator().manual_seed(31)
+    B, H, D, L, BS, LW, K = 2, 1, 128, 3000, 64, 256, 6
+    st = 64                                                   # row stride (elements) < D
+    kb = torch.randn(B, L * st + D, generator=g).to(torch.bfloat16)
+    vb = torch.randn(B, L * st + D, generator=g).to(torch.bfloat16)
+    kc = kb.as_strided((B, L, H, D), (L * st + D, st, D, 1))
+    vc = vb.as_strided((B, L, H, D), (L * st + D, st, D, 1))
+    q = torch.randn(B, H, D, generator=g).to(torch.bfloat16)
+    q_pos = torch.tensor([L - 1, 2100])
+    idx = torch.stack([torch.randperm((int(p) - LW + 1) // BS, generator=g)[:K] for p in q_pos]).view(B, H, K)
+    ref = O.decode_attend_gather(q, kc.contiguous(), vc.contiguous(), idx, q_pos, BS, LW, 1 / math.sqrt(D))
+    kd = kb.to(dev).as_strided((B, L, H, D), (L * st + D, st, D, 1))
+    vd = vb.to(dev).as_strided((B, L, H, D), (L * st + D, st, D, 1))
+    out = srswa.gather_decode(q.to(dev), kd, vd, idx.to(dev), q_pos.to(dev), block_size=BS, local_window=LW,
+                              scale=1 / math.sqrt(D)).cpu()
+    from tolerance import assert_close_lowp
+    assert_close_lowp(out, ref.double(), torch.bfloat16, BF16_TOL, "gather decode overlapping rows")

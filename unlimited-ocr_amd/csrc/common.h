@@ -142,37 +142,37 @@ __device__ __forceinline__ f32x2_t fp8x2_f32(uint32_t w) {
   else return __builtin_amdgcn_cvt_scalef32_pk_f32_bf8(w, Fp8Fmt<F>::kScale, HI);
 }
 
-// four fp8 bytes of w (byte 0 first) -> fp32
+// The FNUZ special-byte flags of an 8-byte piece (bit 7 of a byte, as
+// fnuz_special_bits; constant 0 for the OCP formats).  A loop ORs the flags of
+// all its pieces and takes one branch: the fast conversions below when no bit
+// 7 is set, the exact ones (per-byte fix-up) otherwise.
 template <int F>
-__device__ __forceinline__ void fp8x4_to_f32(uint32_t w, float* f) {
-  const f32x2_t lo = fp8x2_f32<F, false>(w), hi = fp8x2_f32<F, true>(w);
-  f[0] = lo[0];
-  f[1] = lo[1];
-  f[2] = hi[0];
-  f[3] = hi[1];
-  if constexpr (Fp8Fmt<F>::FNUZ) {
-    if (__builtin_expect((fnuz_special_bits<Fp8Fmt<F>::E4>(w) & 0x80808080u) != 0u, 0)) {
-#pragma unroll
-      for (int i = 0; i < 4; ++i) f[i] = fnuz_fix<Fp8Fmt<F>::E4>(w, i, f[i]);
-    }
-  }
+__device__ __forceinline__ uint32_t fp8_special_bits(const uint2& w) {
+  if constexpr (Fp8Fmt<F>::FNUZ)
+    return fnuz_special_bits<Fp8Fmt<F>::E4>(w.x) | fnuz_special_bits<Fp8Fmt<F>::E4>(w.y);
+  else
+    return 0u;
 }
+__device__ __forceinline__ bool fp8_any_special(uint32_t bits) { return (bits & 0x80808080u) != 0u; }
 
-// eight fp8 bytes -> fp32, one word test for both words
+// eight fp8 bytes (byte 0 of w.x first) -> fp32, without the FNUZ fix-up
 template <int F>
-__device__ __forceinline__ void fp8x8_to_f32(const uint2& w, float* f) {
+__device__ __forceinline__ void fp8x8_to_f32_fast(const uint2& w, float* f) {
   const f32x2_t p0 = fp8x2_f32<F, false>(w.x), p1 = fp8x2_f32<F, true>(w.x);
   const f32x2_t p2 = fp8x2_f32<F, false>(w.y), p3 = fp8x2_f32<F, true>(w.y);
   f[0] = p0[0]; f[1] = p0[1]; f[2] = p1[0]; f[3] = p1[1];
   f[4] = p2[0]; f[5] = p2[1]; f[6] = p3[0]; f[7] = p3[1];
+}
+
+// eight fp8 bytes -> fp32, exact for every byte
+template <int F>
+__device__ __forceinline__ void fp8x8_to_f32_exact(const uint2& w, float* f) {
+  fp8x8_to_f32_fast<F>(w, f);
   if constexpr (Fp8Fmt<F>::FNUZ) {
-    constexpr bool E4 = Fp8Fmt<F>::E4;
-    if (__builtin_expect(((fnuz_special_bits<E4>(w.x) | fnuz_special_bits<E4>(w.y)) & 0x80808080u) != 0u, 0)) {
 #pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        f[i] = fnuz_fix<E4>(w.x, i, f[i]);
-        f[4 + i] = fnuz_fix<E4>(w.y, i, f[4 + i]);
-      }
+    for (int i = 0; i < 4; ++i) {
+      f[i] = fnuz_fix<Fp8Fmt<F>::E4>(w.x, i, f[i]);
+      f[4 + i] = fnuz_fix<Fp8Fmt<F>::E4>(w.y, i, f[4 + i]);
     }
   }
 }
@@ -193,23 +193,24 @@ __device__ __forceinline__ uint32_t fp8x2_to(uint32_t w) {
   }
 }
 
-// eight fp8 bytes -> eight values of T (bf16 / fp16) as one 16-byte vector:
-// one instruction per pair, and for FNUZ one word test for both words (the
-// rare flagged piece is converted again through fp32 and fixed up)
+// eight fp8 bytes -> eight values of T as one 16-byte vector, one instruction
+// per pair, without the FNUZ fix-up
 template <int F, typename T>
-__device__ __forceinline__ uint4 fp8x8_to(const uint2& w) {
-  uint4 r = make_uint4(fp8x2_to<F, T, false>(w.x), fp8x2_to<F, T, true>(w.x), fp8x2_to<F, T, false>(w.y),
-                       fp8x2_to<F, T, true>(w.y));
+__device__ __forceinline__ uint4 fp8x8_to_fast(const uint2& w) {
+  return make_uint4(fp8x2_to<F, T, false>(w.x), fp8x2_to<F, T, true>(w.x), fp8x2_to<F, T, false>(w.y),
+                    fp8x2_to<F, T, true>(w.y));
+}
+
+// eight fp8 bytes -> eight values of T, exact for every byte (through fp32)
+template <int F, typename T>
+__device__ __forceinline__ uint4 fp8x8_to_exact(const uint2& w) {
   if constexpr (Fp8Fmt<F>::FNUZ) {
-    constexpr bool E4 = Fp8Fmt<F>::E4;
-    if (__builtin_expect(((fnuz_special_bits<E4>(w.x) | fnuz_special_bits<E4>(w.y)) & 0x80808080u) != 0u, 0)) {
-      float f[8];
-      fp8x4_to_f32<F>(w.x, f);
-      fp8x4_to_f32<F>(w.y, f + 4);
-      r = Vec16<T>::pack(f);
-    }
+    float f[8];
+    fp8x8_to_f32_exact<F>(w, f);
+    return Vec16<T>::pack(f);
+  } else {
+    return fp8x8_to_fast<F, T>(w);
   }
-  return r;
 }
 
 // Runs fn(std::integral_constant<int, F>) for the fp8 format fmt: one uniform

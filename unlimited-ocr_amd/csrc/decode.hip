@@ -374,8 +374,17 @@ __global__ __launch_bounds__(kDecodeWaves * kWave) void decode_kernel(DecodeK p)
     float part[NI];
     if constexpr (FP8) {
       fp8_dispatch(p.kv8, [&](auto F) {
+        constexpr int FF = decltype(F)::value;
+        uint32_t sp = 0u;
 #pragma unroll
-        for (int i = 0; i < NI; ++i) part[i] = qf.dot(fp8x8_to<decltype(F)::value, T>(kw[i].w));
+        for (int i = 0; i < NI; ++i) sp |= fp8_special_bits<FF>(kw[i].w);
+        if (__builtin_expect(!fp8_any_special(sp), 1)) {
+#pragma unroll
+          for (int i = 0; i < NI; ++i) part[i] = qf.dot(fp8x8_to_fast<FF, T>(kw[i].w));
+        } else {
+#pragma unroll
+          for (int i = 0; i < NI; ++i) part[i] = qf.dot(fp8x8_to_exact<FF, T>(kw[i].w));
+        }
       });
     } else {
 #pragma unroll
@@ -405,12 +414,26 @@ __global__ __launch_bounds__(kDecodeWaves * kWave) void decode_kernel(DecodeK p)
     for (int i = 0; i < NI; ++i) pv[i] = s_p[wave][r * NI + i];
     if constexpr (FP8) {
       fp8_dispatch(p.kv8, [&](auto F) {
+        constexpr int FF = decltype(F)::value;
+        uint32_t sp = 0u;
 #pragma unroll
-        for (int i = 0; i < NI; ++i) {
-          float f[8];
-          fp8x8_to_f32<decltype(F)::value>(vw[i].w, f);
+        for (int i = 0; i < NI; ++i) sp |= fp8_special_bits<FF>(vw[i].w);
+        if (__builtin_expect(!fp8_any_special(sp), 1)) {
 #pragma unroll
-          for (int e = 0; e < EPV; ++e) acc[e] = fmaf(pv[i], f[e], acc[e]);
+          for (int i = 0; i < NI; ++i) {
+            float f[8];
+            fp8x8_to_f32_fast<FF>(vw[i].w, f);
+#pragma unroll
+            for (int e = 0; e < EPV; ++e) acc[e] = fmaf(pv[i], f[e], acc[e]);
+          }
+        } else {
+#pragma unroll
+          for (int i = 0; i < NI; ++i) {
+            float f[8];
+            fp8x8_to_f32_exact<FF>(vw[i].w, f);
+#pragma unroll
+            for (int e = 0; e < EPV; ++e) acc[e] = fmaf(pv[i], f[e], acc[e]);
+          }
         }
       });
     } else {
@@ -539,7 +562,7 @@ int elem_bytes(int dt) { return dt == SRSWA_F32 ? 4 : 2; }
 
 // Tuning knobs (environment, read once): SRSWA_DECODE_NI = 8 (default) | 16
 // load instructions per unit (bf16 D=128: 32 | 64 keys); SRSWA_DECODE_UPW =
-// units per wave (default 2).
+// units per wave (default 2, 8 with fp8 caches).
 int env_int(const char* name, int dflt) {
   const char* v = getenv(name);
   return (v && *v) ? atoi(v) : dflt;
@@ -553,7 +576,7 @@ int decode_ni(int dt, int D) {
   return (want == 8 && ni == 16) ? 8 : ni;
 }
 
-DecodePlan make_plan(const srswa_decode_args* a, bool paged = false) {
+DecodePlan make_plan(const srswa_decode_args* a, bool paged = false, bool fp8 = false) {
   DecodePlan pl{};
   const int lpr = a->D * elem_bytes(a->in_dtype) / 16;
   int ni = decode_ni(a->in_dtype, a->D);
@@ -565,8 +588,10 @@ DecodePlan make_plan(const srswa_decode_args* a, bool paged = false) {
   // paged windows run on the UK grid, LW / UK units with the first one
   // wrapped (UK divides the page size, which divides LW)
   pl.n_units = pl.n_remote_units + ceil_div(a->local_window, pl.UK);
-  static const int upw = env_int("SRSWA_DECODE_UPW", 2);
-  pl.upw = upw > 1 ? upw : 1;
+  // an fp8 unit holds half the bytes: four times the units per wave (at
+  // config 3 one workgroup per row, so no split-K merge)
+  static const int upw = env_int("SRSWA_DECODE_UPW", 0);
+  pl.upw = upw > 0 ? upw : (fp8 ? 8 : 2);
   pl.nsplit = ceil_div(pl.n_units, kDecodeWaves * pl.upw);
   pl.pstride = ceil_div(a->D + 2, 32) * 32;
   pl.rowheads = (int64_t)a->B * a->Lq * a->HQ;
@@ -752,7 +777,7 @@ extern "C" size_t srswa_gather_decode_paged_workspace(const srswa_paged_decode_a
   if (a && a->R > 0 && a->dql > 0 && a->HQ > 0 && a->D > 0 && a->page_size > 0 && a->topk_n >= 0 &&
       a->local_blocks >= 0) {
     const srswa_decode_args d = paged_as_decode(a);
-    return scratch_bytes(make_plan(&d, true));
+    return scratch_bytes(make_plan(&d, true, a->kv_fp8 != 0));
   }
   return 0;
 }
@@ -816,7 +841,7 @@ extern "C" int srswa_gather_decode_paged(const srswa_paged_decode_args* a, void*
     return SRSWA_UNSUPPORTED;
   }
   const srswa_decode_args d = paged_as_decode(a);
-  const DecodePlan pl = make_plan(&d, true);
+  const DecodePlan pl = make_plan(&d, true, a->kv_fp8 != 0);
   const size_t need = scratch_bytes(pl);
   if (need > 0 && (!ws || ws_bytes < need)) {
     set_error("paged decode: scratch of %zu bytes required (got %zu)", need, ws_bytes);

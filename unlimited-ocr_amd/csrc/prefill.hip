@@ -307,10 +307,22 @@ __global__ __launch_bounds__(128, 2) void fwd_kernel(FwdK p) {
     __syncthreads();   // previous chunk fully consumed
     if constexpr (FP8) {
       fp8_dispatch(p.kv8, [&](auto F) {
+        constexpr int FF = decltype(F)::value;
+        uint32_t sp = 0u;
 #pragma unroll
-        for (int i = 0; i < PPT; ++i) {
-          *reinterpret_cast<uint4*>(sKw + i * RPP * KP) = fp8x8_to<decltype(F)::value, T>(kpre[i]);
-          *reinterpret_cast<uint4*>(sVw + i * RPP * VP) = fp8x8_to<decltype(F)::value, T>(vpre[i]);
+        for (int i = 0; i < PPT; ++i) sp |= fp8_special_bits<FF>(kpre[i]) | fp8_special_bits<FF>(vpre[i]);
+        if (__builtin_expect(!fp8_any_special(sp), 1)) {
+#pragma unroll
+          for (int i = 0; i < PPT; ++i) {
+            *reinterpret_cast<uint4*>(sKw + i * RPP * KP) = fp8x8_to_fast<FF, T>(kpre[i]);
+            *reinterpret_cast<uint4*>(sVw + i * RPP * VP) = fp8x8_to_fast<FF, T>(vpre[i]);
+          }
+        } else {
+#pragma unroll
+          for (int i = 0; i < PPT; ++i) {
+            *reinterpret_cast<uint4*>(sKw + i * RPP * KP) = fp8x8_to_exact<FF, T>(kpre[i]);
+            *reinterpret_cast<uint4*>(sVw + i * RPP * VP) = fp8x8_to_exact<FF, T>(vpre[i]);
+          }
         }
       });
     } else {
