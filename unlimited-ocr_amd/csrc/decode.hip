@@ -55,6 +55,7 @@ struct DecodePlan {
   int nsplit;          // workgroups per (row, head)
   int pstride;         // floats per partial record (128-byte multiple)
   int64_t rowheads;    // B * Lq * HQ
+  int gq;              // query heads per workgroup (gqa_heads)
 };
 
 struct DecodeK {
@@ -71,6 +72,7 @@ struct DecodeK {
   int64_t bt_sb, k_pst, v_pst;   // block-table row stride, page strides (elements)
   int bs_shift, max_blocks;
   int kv8;                       // FP8 kernels: the caches' fp8 format (srswa_dtype)
+  int gq;                        // query heads per workgroup (gqa_heads)
 };
 
 template <typename TO>
@@ -171,7 +173,9 @@ template <typename T> struct KVRaw<T, true> {
   __device__ __forceinline__ void zero() { w = make_uint2(0, 0); }
 };
 
-template <typename T, typename TO, int D, int NI, bool PAGED, bool FP8 = false>
+// GQ query heads per workgroup (GQA: heads of one kv head that read one id
+// row): each K / V row is loaded once and scored for all GQ heads.
+template <typename T, typename TO, int D, int NI, bool PAGED, bool FP8 = false, int GQ = 1>
 __global__ __launch_bounds__(kDecodeWaves * kWave) void decode_kernel(DecodeK p) {
   using V = Vec16<T>;
   using KE = std::conditional_t<FP8, uint8_t, T>;   // cache element
@@ -184,9 +188,9 @@ __global__ __launch_bounds__(kDecodeWaves * kWave) void decode_kernel(DecodeK p)
   static_assert(LPR <= kWave && kWave % LPR == 0, "row must fit a wavefront");
   static_assert(NI <= LPR && LPR % NI == 0, "NI must divide LPR");
 
-  __shared__ float s_p[kDecodeWaves][64];
-  __shared__ float s_o[kDecodeWaves][D];
-  __shared__ float s_m[kDecodeWaves], s_l[kDecodeWaves];
+  __shared__ float s_p[kDecodeWaves][GQ][64];
+  __shared__ float s_o[kDecodeWaves][GQ][D];
+  __shared__ float s_m[kDecodeWaves][GQ], s_l[kDecodeWaves][GQ];
 
   const srswa_decode_args& a = p.a;
   const int wave = threadIdx.x / kWave;
@@ -195,13 +199,14 @@ __global__ __launch_bounds__(kDecodeWaves * kWave) void decode_kernel(DecodeK p)
   const int c = lane % LPR;
 
   const int split = blockIdx.x % p.nsplit;
-  const int64_t rh = blockIdx.x / p.nsplit;     // ((b * Lq) + lq) * HQ + hq
-  const int hq = (int)(rh % a.HQ);
-  const int64_t bl = rh / a.HQ;
+  const int64_t rg = blockIdx.x / p.nsplit;     // ((b * Lq) + lq) * (HQ / GQ) + head group
+  const int hq0 = (int)(rg % (a.HQ / GQ)) * GQ; // the group's first query head
+  const int64_t bl = rg / (a.HQ / GQ);
+  const int64_t rh0 = bl * a.HQ + hq0;          // ((b * Lq) + lq) * HQ + hq0
   const int lq = (int)(bl % a.Lq);
   const int b = (int)(bl / a.Lq);
-  const int kvh = hq / p.G;
-  const int ih = hq / p.IG;
+  const int kvh = hq0 / p.G;
+  const int ih = hq0 / p.IG;
 
   const int kvl = a.kv_len ? min(a.kv_len[b], a.L) : a.L;
   const int qp = PAGED ? a.kv_len[b] - a.Lq + lq : a.q_pos[b * a.pos_sb + lq * a.pos_sq];
@@ -209,10 +214,12 @@ __global__ __launch_bounds__(kDecodeWaves * kWave) void decode_kernel(DecodeK p)
   const int ws = max(qp - a.local_window + 1, 0);      // first window key
   const int remote_end = min(ws, last + 1);            // remote keys are < this
 
-  // this lane's slice of q
-  QFrag<T> qf;
-  qf.load(reinterpret_cast<const T*>(a.q) + (int64_t)b * a.q_sb + (int64_t)lq * a.q_sq +
-          (int64_t)hq * a.q_sh + c * EPV);
+  // this lane's slice of each head's q
+  QFrag<T> qf[GQ];
+#pragma unroll
+  for (int g = 0; g < GQ; ++g)
+    qf[g].load(reinterpret_cast<const T*>(a.q) + (int64_t)b * a.q_sb + (int64_t)lq * a.q_sq +
+               (int64_t)(hq0 + g) * a.q_sh + c * EPV);
   const int32_t* idx_row = a.idx + (int64_t)b * a.idx_sb + (int64_t)ih * a.idx_sh +
                            (int64_t)lq * a.idx_sq;
   const int64_t aux_off = (int64_t)b * a.idx_sb + (int64_t)ih * a.idx_sh +
@@ -235,10 +242,15 @@ __global__ __launch_bounds__(kDecodeWaves * kWave) void decode_kernel(DecodeK p)
     if (wb <= max_blk) win_page = bt_row[wb];
   }
 
-  float m = -INFINITY, l = 0.f;
-  float acc[EPV];
+  float m[GQ], l[GQ];
+  float acc[GQ][EPV];
 #pragma unroll
-  for (int e = 0; e < EPV; ++e) acc[e] = 0.f;
+  for (int g = 0; g < GQ; ++g) {
+    m[g] = -INFINITY;
+    l[g] = 0.f;
+#pragma unroll
+    for (int e = 0; e < EPV; ++e) acc[g][e] = 0.f;
+  }
 
   // Slot metadata in one round trip: lane s holds slot s (S <= 64) -- its id,
   // whether it survives (valid, in range, first slot holding that id) and its
@@ -371,7 +383,7 @@ __global__ __launch_bounds__(kDecodeWaves * kWave) void decode_kernel(DecodeK p)
       }
     }
 
-    float part[NI];
+    float part[GQ][NI];
     if constexpr (FP8) {
       fp8_dispatch(p.kv8, [&](auto F) {
         constexpr int FF = decltype(F)::value;
@@ -380,38 +392,54 @@ __global__ __launch_bounds__(kDecodeWaves * kWave) void decode_kernel(DecodeK p)
         for (int i = 0; i < NI; ++i) sp |= fp8_special_bits<FF>(kw[i].w);
         if (__builtin_expect(!fp8_any_special(sp), 1)) {
 #pragma unroll
-          for (int i = 0; i < NI; ++i) part[i] = qf.dot(fp8x8_to_fast<FF, T>(kw[i].w));
+          for (int i = 0; i < NI; ++i) {
+            const uint4 kc = fp8x8_to_fast<FF, T>(kw[i].w);
+#pragma unroll
+            for (int g = 0; g < GQ; ++g) part[g][i] = qf[g].dot(kc);
+          }
         } else {
 #pragma unroll
-          for (int i = 0; i < NI; ++i) part[i] = qf.dot(fp8x8_to_exact<FF, T>(kw[i].w));
+          for (int i = 0; i < NI; ++i) {
+            const uint4 kc = fp8x8_to_exact<FF, T>(kw[i].w);
+#pragma unroll
+            for (int g = 0; g < GQ; ++g) part[g][i] = qf[g].dot(kc);
+          }
         }
       });
     } else {
 #pragma unroll
-      for (int i = 0; i < NI; ++i) part[i] = qf.dot(kw[i].w);
-    }
-    // reduce-scatter across the LPR lanes of a row: NI partials -> 1 score
-    reduce_scatter<NI, LPR / 2>(part, c);
+      for (int i = 0; i < NI; ++i)
 #pragma unroll
-    for (int o = DUP / 2; o >= 1; o >>= 1) part[0] += __shfl_xor(part[0], o, kWave);
+        for (int g = 0; g < GQ; ++g) part[g][i] = qf[g].dot(kw[i].w);
+    }
     const int i_own = c / DUP;                    // which instruction's key this lane holds
     const int key = key_of(i_own * RPI + r);
     const bool owner = (c % DUP) == 0;
-    const float t = ((!PAGED || key >= klo) && key < k1) ? part[0] * p.scale_l2 + bias_l2 : -INFINITY;
-    const float mnew = fmaxf(m, wave_max(t));     // finite: key klo is always kept
-    const float alpha = exp2f(m - mnew);
-    const float pj = exp2f(t - mnew);
-    l = l * alpha + (owner ? pj : 0.f);   // per-lane; summed over the wave once at the end
-    m = mnew;
+    const bool kept = (!PAGED || key >= klo) && key < k1;
 #pragma unroll
-    for (int e = 0; e < EPV; ++e) acc[e] *= alpha;
-    if (owner) s_p[wave][r * NI + i_own] = pj;
+    for (int g = 0; g < GQ; ++g) {
+      // reduce-scatter across the LPR lanes of a row: NI partials -> 1 score
+      reduce_scatter<NI, LPR / 2>(part[g], c);
+#pragma unroll
+      for (int o = DUP / 2; o >= 1; o >>= 1) part[g][0] += __shfl_xor(part[g][0], o, kWave);
+      const float t = kept ? part[g][0] * p.scale_l2 + bias_l2 : -INFINITY;
+      const float mnew = fmaxf(m[g], wave_max(t));     // finite: key klo is always kept
+      const float alpha = exp2f(m[g] - mnew);
+      const float pj = exp2f(t - mnew);
+      l[g] = l[g] * alpha + (owner ? pj : 0.f);   // per-lane; summed over the wave once at the end
+      m[g] = mnew;
+#pragma unroll
+      for (int e = 0; e < EPV; ++e) acc[g][e] *= alpha;
+      if (owner) s_p[wave][g][r * NI + i_own] = pj;
+    }
     __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
     __builtin_amdgcn_wave_barrier();
     __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-    float pv[NI];
+    float pv[GQ][NI];
 #pragma unroll
-    for (int i = 0; i < NI; ++i) pv[i] = s_p[wave][r * NI + i];
+    for (int g = 0; g < GQ; ++g)
+#pragma unroll
+      for (int i = 0; i < NI; ++i) pv[g][i] = s_p[wave][g][r * NI + i];
     if constexpr (FP8) {
       fp8_dispatch(p.kv8, [&](auto F) {
         constexpr int FF = decltype(F)::value;
@@ -424,7 +452,9 @@ __global__ __launch_bounds__(kDecodeWaves * kWave) void decode_kernel(DecodeK p)
             float f[8];
             fp8x8_to_f32_fast<FF>(vw[i].w, f);
 #pragma unroll
-            for (int e = 0; e < EPV; ++e) acc[e] = fmaf(pv[i], f[e], acc[e]);
+            for (int g = 0; g < GQ; ++g)
+#pragma unroll
+              for (int e = 0; e < EPV; ++e) acc[g][e] = fmaf(pv[g][i], f[e], acc[g][e]);
           }
         } else {
 #pragma unroll
@@ -432,7 +462,9 @@ __global__ __launch_bounds__(kDecodeWaves * kWave) void decode_kernel(DecodeK p)
             float f[8];
             fp8x8_to_f32_exact<FF>(vw[i].w, f);
 #pragma unroll
-            for (int e = 0; e < EPV; ++e) acc[e] = fmaf(pv[i], f[e], acc[e]);
+            for (int g = 0; g < GQ; ++g)
+#pragma unroll
+              for (int e = 0; e < EPV; ++e) acc[g][e] = fmaf(pv[g][i], f[e], acc[g][e]);
           }
         }
       });
@@ -442,7 +474,9 @@ __global__ __launch_bounds__(kDecodeWaves * kWave) void decode_kernel(DecodeK p)
         float f[EPV];
         V::unpack(vw[i].w, f);
 #pragma unroll
-        for (int e = 0; e < EPV; ++e) acc[e] = fmaf(pv[i], f[e], acc[e]);
+        for (int g = 0; g < GQ; ++g)
+#pragma unroll
+          for (int e = 0; e < EPV; ++e) acc[g][e] = fmaf(pv[g][i], f[e], acc[g][e]);
       }
     }
     __builtin_amdgcn_wave_barrier();
@@ -450,55 +484,68 @@ __global__ __launch_bounds__(kDecodeWaves * kWave) void decode_kernel(DecodeK p)
 
   // sum the RPI row groups of the wave
 #pragma unroll
-  for (int o = LPR; o < kWave; o <<= 1)
+  for (int g = 0; g < GQ; ++g)
 #pragma unroll
-    for (int e = 0; e < EPV; ++e) acc[e] += __shfl_xor(acc[e], o, kWave);
+    for (int o = LPR; o < kWave; o <<= 1)
+#pragma unroll
+      for (int e = 0; e < EPV; ++e) acc[g][e] += __shfl_xor(acc[g][e], o, kWave);
 
   if (r == 0) {
 #pragma unroll
-    for (int e = 0; e < EPV; ++e) s_o[wave][c * EPV + e] = acc[e];
+    for (int g = 0; g < GQ; ++g)
+#pragma unroll
+      for (int e = 0; e < EPV; ++e) s_o[wave][g][c * EPV + e] = acc[g][e];
   }
-  l = wave_sum(l);
-  if (lane == 0) { s_m[wave] = m; s_l[wave] = l; }
+#pragma unroll
+  for (int g = 0; g < GQ; ++g) l[g] = wave_sum(l[g]);
+  if (lane == 0) {
+#pragma unroll
+    for (int g = 0; g < GQ; ++g) { s_m[wave][g] = m[g]; s_l[wave][g] = l[g]; }
+  }
   __syncthreads();
   if (wave != 0) return;
 
-  // merge the workgroup's waves (wave 0)
-  float M = -INFINITY;
+  // merge the workgroup's waves (wave 0), head by head
 #pragma unroll
-  for (int w = 0; w < kDecodeWaves; ++w) M = fmaxf(M, s_m[w]);
-  float L = 0.f, O[EPV];
+  for (int g = 0; g < GQ; ++g) {
+    const int64_t rh = rh0 + g;
+    const int hq = hq0 + g;
+    float M = -INFINITY;
 #pragma unroll
-  for (int e = 0; e < EPV; ++e) O[e] = 0.f;
+    for (int w = 0; w < kDecodeWaves; ++w) M = fmaxf(M, s_m[w][g]);
+    float L = 0.f, O[EPV];
 #pragma unroll
-  for (int w = 0; w < kDecodeWaves; ++w) {
-    const float wt = s_m[w] == -INFINITY ? 0.f : exp2f(s_m[w] - M);
-    L += s_l[w] * wt;
+    for (int e = 0; e < EPV; ++e) O[e] = 0.f;
+#pragma unroll
+    for (int w = 0; w < kDecodeWaves; ++w) {
+      const float wt = s_m[w][g] == -INFINITY ? 0.f : exp2f(s_m[w][g] - M);
+      L += s_l[w][g] * wt;
+      if (r == 0) {
+#pragma unroll
+        for (int e = 0; e < EPV; ++e) O[e] = fmaf(s_o[w][g][c * EPV + e], wt, O[e]);
+      }
+    }
+
+    if (p.nsplit > 1) {
+      // record: O[0..D) then M, L; records are 128-byte aligned
+      float* rec = p.part + (rh * p.nsplit + split) * p.pstride;
+      if (r == 0) store_out<float>(rec + c * EPV, O, EPV);
+      if (lane == 0) { rec[D] = M; rec[D + 1] = L; }
+      continue;   // decode_merge_kernel combines the records
+    }
+
+    const float inv = L > 0.f ? 1.f / L : 0.f;
     if (r == 0) {
 #pragma unroll
-      for (int e = 0; e < EPV; ++e) O[e] = fmaf(s_o[w][c * EPV + e], wt, O[e]);
+      for (int e = 0; e < EPV; ++e) O[e] *= inv;
+      TO* orow = reinterpret_cast<TO*>(a.out) + (int64_t)b * a.o_sb + (int64_t)lq * a.o_sq +
+                 (int64_t)hq * a.o_sh + c * EPV;
+      store_out<TO>(orow, O, EPV);
     }
-  }
-
-  if (p.nsplit > 1) {
-    // record: O[0..D) then M, L; records are 128-byte aligned
-    float* rec = p.part + (rh * p.nsplit + split) * p.pstride;
-    if (r == 0) store_out<float>(rec + c * EPV, O, EPV);
-    if (lane == 0) { rec[D] = M; rec[D + 1] = L; }
-    return;   // decode_merge_kernel combines the records
-  }
-
-  const float inv = L > 0.f ? 1.f / L : 0.f;
-  if (r == 0) {
-#pragma unroll
-    for (int e = 0; e < EPV; ++e) O[e] *= inv;
-    TO* orow = reinterpret_cast<TO*>(a.out) + (int64_t)b * a.o_sb + (int64_t)lq * a.o_sq +
-               (int64_t)hq * a.o_sh + c * EPV;
-    store_out<TO>(orow, O, EPV);
-  }
-  if (a.lse && lane == 0) {
-    a.lse[(int64_t)b * a.lse_sb + (int64_t)lq * a.lse_sq + (int64_t)hq * a.lse_sh] =
-        L > 0.f ? fmaf(M, kLn2, logf(L)) : -INFINITY;   // one rounding wherever it is inlined
+    if (a.lse && lane == 0) {
+      a.lse[(int64_t)b * a.lse_sb + (int64_t)lq * a.lse_sq + (int64_t)hq * a.lse_sh] =
+          L > 0.f ? fmaf(M, kLn2, logf(L)) : -INFINITY;   // one rounding wherever it is inlined
+    }
   }
 }
 
@@ -576,6 +623,20 @@ int decode_ni(int dt, int D) {
   return (want == 8 && ni == 16) ? 8 : ni;
 }
 
+// Query heads served per workgroup: under GQA the heads of one kv head that
+// also share one id row (G and IG multiples of the group) are scored together,
+// so each K / V row is read once per group instead of once per head.  Groups
+// take 16-bit queries with outputs of the same dtype and units of at most 8
+// loads; SRSWA_DECODE_GQA=0 turns them off.
+int gqa_heads(const srswa_decode_args* a, int ni) {
+  static const int on = env_int("SRSWA_DECODE_GQA", 1);
+  if (!on || a->in_dtype == SRSWA_F32 || a->out_dtype != a->in_dtype || ni > 8) return 1;
+  const int G = a->HQ / a->HKV, IG = a->HQ / a->HI;
+  for (int gq : {4, 2})
+    if (G % gq == 0 && IG % gq == 0) return gq;
+  return 1;
+}
+
 DecodePlan make_plan(const srswa_decode_args* a, bool paged = false, bool fp8 = false) {
   DecodePlan pl{};
   const int lpr = a->D * elem_bytes(a->in_dtype) / 16;
@@ -595,6 +656,7 @@ DecodePlan make_plan(const srswa_decode_args* a, bool paged = false, bool fp8 = 
   pl.nsplit = ceil_div(pl.n_units, kDecodeWaves * pl.upw);
   pl.pstride = ceil_div(a->D + 2, 32) * 32;
   pl.rowheads = (int64_t)a->B * a->Lq * a->HQ;
+  pl.gq = gqa_heads(a, ni);
   return pl;
 }
 
@@ -602,21 +664,31 @@ size_t scratch_bytes(const DecodePlan& pl) {
   return pl.nsplit <= 1 ? 0 : (size_t)pl.rowheads * pl.nsplit * pl.pstride * 4;
 }
 
-template <typename T, typename TO, int D, int NI>
-int launch_decode_ni(const DecodeK& k, int64_t grid, hipStream_t st) {
+template <typename T, typename TO, int D, int NI, int GQ>
+void launch_decode_gq(const DecodeK& k, int64_t grid, hipStream_t st) {
   if constexpr (sizeof(T) == 2 && std::is_same_v<T, TO>) {
     if (k.kv8 && k.bt)
-      hipLaunchKernelGGL((decode_kernel<T, TO, D, NI, true, true>), dim3((unsigned)grid),
+      hipLaunchKernelGGL((decode_kernel<T, TO, D, NI, true, true, GQ>), dim3((unsigned)grid),
                          dim3(kDecodeWaves * kWave), 0, st, k);
   }
   if (k.kv8) {
     // fp8 caches take the 16-bit paged kernels only (checked by the caller)
   } else if (k.bt)
-    hipLaunchKernelGGL((decode_kernel<T, TO, D, NI, true>), dim3((unsigned)grid),
+    hipLaunchKernelGGL((decode_kernel<T, TO, D, NI, true, false, GQ>), dim3((unsigned)grid),
                        dim3(kDecodeWaves * kWave), 0, st, k);
   else
-    hipLaunchKernelGGL((decode_kernel<T, TO, D, NI, false>), dim3((unsigned)grid),
+    hipLaunchKernelGGL((decode_kernel<T, TO, D, NI, false, false, GQ>), dim3((unsigned)grid),
                        dim3(kDecodeWaves * kWave), 0, st, k);
+}
+
+template <typename T, typename TO, int D, int NI>
+int launch_decode_ni(const DecodeK& k, int64_t grid, hipStream_t st) {
+  // head groups: 16-bit queries with 16-bit outputs of their dtype, units of
+  // at most 8 load instructions (gqa_heads never picks a group otherwise)
+  constexpr bool kGroups = sizeof(T) == 2 && std::is_same_v<T, TO> && NI <= 8;
+  if (kGroups && k.gq == 4) launch_decode_gq<T, TO, D, NI, kGroups ? 4 : 1>(k, grid / 4, st);
+  else if (kGroups && k.gq == 2) launch_decode_gq<T, TO, D, NI, kGroups ? 2 : 1>(k, grid / 2, st);
+  else launch_decode_gq<T, TO, D, NI, 1>(k, grid, st);
   if (k.nsplit > 1)
     hipLaunchKernelGGL((decode_merge_kernel<TO, D>), dim3((unsigned)((k.rowheads + 3) / 4)),
                        dim3(256), 0, st, k);
@@ -734,6 +806,7 @@ extern "C" int srswa_gather_decode(const srswa_decode_args* a, void* ws, size_t 
   k.pstride = pl.pstride;
   k.scale_l2 = a->scale * kLog2e;
   k.rowheads = pl.rowheads;
+  k.gq = pl.gq;
   if (need > 0) k.part = reinterpret_cast<float*>(ws);
   const int64_t grid = pl.rowheads * pl.nsplit;
   if (grid > 0x7fffffff) {
@@ -860,6 +933,7 @@ extern "C" int srswa_gather_decode_paged(const srswa_paged_decode_args* a, void*
   k.pstride = pl.pstride;
   k.scale_l2 = d.scale * kLog2e;
   k.rowheads = pl.rowheads;
+  k.gq = pl.gq;
   if (need > 0) k.part = reinterpret_cast<float*>(ws);
   k.bt = a->block_table;
   k.bt_sb = a->bt_sr;
