@@ -684,6 +684,13 @@ int srswa_page_candidate_mask(const srswa_candidate_args* a, void* stream);
  *   kl[t] = sum_j p_j (log max(p_j, 1e-12) - log q_j), valid[t] = any key kept
  * dsel (optional, [.., K, 64] fp32 per row) = q_j - p_j on kept keys, else 0:
  * d kl / d logit, the input of srswa_gather_kl_bwd.  kv(h) = h / (HQ / HKV).
+ * K is 1..64 selected blocks per row, or, with slots_are_blocks = 1, the
+ * number of key blocks ceil(Sk / 64) (at most 2048): sel[t, s] is then s (block
+ * s listed) or -1, so a row may list every block, as the warmup stage's KL does
+ * (keep_block = every KL-eligible block, restrict_to_selected=False,
+ * HF/_sparse_base_impl.py:3186-3187).  In that form dsel rows of unlisted slots
+ * are left unwritten (srswa_gather_kl_bwd never reads them) and the forward
+ * needs no workspace (srswa_gather_kl_fwd_workspace returns 0).
  * ---------------------------------------------------------------------- */
 typedef struct {
   const void* q_idx;  int64_t qi_sb, qi_sh, qi_st;     /* [B, HI, T, D] index queries     */
@@ -699,6 +706,7 @@ typedef struct {
   int32_t B, HI, HQ, HKV, T, Sk, D, K, block_size, local_window;
   float scaling;
   int32_t dtype;                                       /* srswa_dtype: bf16 or fp16       */
+  int32_t slots_are_blocks;                            /* 1: slot s is block s (see above) */
   /* Optional second stream (hipStream_t) and two events (hipEvent_t) of the
    * caller, all three or all NULL.  With them, srswa_gather_kl_fwd_ws runs the
    * tile kernels on side_stream: fork_event is recorded on `stream` and waited
@@ -739,6 +747,7 @@ typedef struct {
   void* dk_idx;       int64_t dk_sb, dk_st;            /* [B, Sk, D]                      */
   int32_t B, HI, T, Sk, D, K, block_size;
   int32_t dtype;
+  int32_t slots_are_blocks;   /* as in srswa_kl_args (the forward's value) */
   void* side_stream;   /* optional, as in srswa_kl_args: the unflagged tiles' dQ runs there */
   void* fork_event;
   void* join_event;
@@ -746,8 +755,8 @@ typedef struct {
 
 /* Workspace, no initial content: per (row tile) a flag, per (head, key block)
  * two row bitmaps, fp32 dQ partials per (row, slot) of flagged tiles
- * (B*HI*T*K*D*4 bytes) and fp32 dK partials per (key block, 2048-row window)
- * (B*ceil(Sk/64)*ceil(T/2048)*64*D*4 bytes). */
+ * (B*HI*T*K*D*4 bytes; none with slots_are_blocks) and fp32 dK partials per
+ * (key block, 2048-row window) (B*ceil(Sk/64)*ceil(T/2048)*64*D*4 bytes). */
 int srswa_gather_kl_bwd_workspace(const srswa_kl_bwd_args* a, size_t* scratch_bytes);
 int srswa_gather_kl_bwd(const srswa_kl_bwd_args* a, void* scratch, size_t scratch_bytes, void* stream);
 

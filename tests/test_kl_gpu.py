@@ -222,6 +222,95 @@ def test_kl_chunk_fn_dropin(dev):
     assert qd.grad is not None and torch.isfinite(qd.grad.float()).all()
 
 
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+def test_slots_are_blocks_every_block(dev, dtype):
+    """The warmup stage's KL: a row lists every KL-eligible block (far more than
+    64), slot s = block s.  150 key blocks, two index heads of a GQA teacher,
+    packed rows, some blocks unlisted (an image constraint) and some listed past
+    the row's window start (no kept key: a zero dsel row); kl / valid / dsel
+    against the dense oracle, then the gradients of the loss."""
+    from srswa import kl as KL
+    print(f"kl slots_are_blocks {dtype}", flush=True)
+    g = torch.Generator().manual_seed(41)
+    B, HI, G, HKV, T, Sk, D, lw = 1, 2, 3, 2, 300, 64 * 150 - 10, 128, 256
+    HQ = HI * G
+    nblk = -(-Sk // 64)
+    q_idx = (torch.randn(B, HI, T, D, generator=g) * D ** -0.5).to(dtype)
+    idx_k = torch.randn(B, Sk, D, generator=g).to(dtype)
+    q_main = torch.randn(B, HQ, T, D, generator=g).to(dtype)
+    k_main = torch.randn(B, HKV, Sk, D, generator=g).to(dtype)
+    pos = (torch.arange(T) * 31 + 100).expand(B, T).clone().to(torch.int32)       # rows spread over the keys
+    seg = torch.where(torch.arange(T) >= 200, 64 * 100 + 17, 0).expand(B, T).to(torch.int32)
+    ar = torch.arange(nblk, dtype=torch.int32)
+    listed = torch.rand(B, HI, T, nblk, generator=g) > 0.15
+    sel = torch.where(listed, ar, torch.full_like(ar, -1))
+    qd = q_idx.to(dev).requires_grad_()
+    kd = idx_k.to(dev).requires_grad_()
+    kw = dict(block_size=64, local_window=lw, scaling=D ** -0.5)
+    kl, valid, dsel = KL.kl_forward(q_idx.to(dev), idx_k.to(dev), q_main.to(dev), k_main.to(dev), sel.to(dev),
+                                    pos.to(dev), seg=seg.to(dev), slots_are_blocks=True, **kw)
+    rk, rv = K.gather_kl_dense(q_idx.double(), idx_k.double(), q_main.double(), k_main.double(), sel, pos,
+                               seg=seg, round_dtype=dtype, **kw)
+    assert torch.equal(valid.cpu(), rv)
+    assert rv.any() and (~rv).any()
+    err = (kl.cpu().double() - rk).abs() - 1e-3 * rk.abs()
+    assert err.max().item() <= 2e-3, err.max().item()
+    # dsel on every listed slot: softmax(student) - p on kept keys, 0 elsewhere
+    keep = K.keep_mask(sel, pos, Sk, 64, lw, seg)
+    s = K._round(torch.einsum("bhtd,bsd->bhts", q_idx.double(), idx_k.double()), dtype).masked_fill(~keep, K.NEG)
+    sm = torch.softmax(s, -1)
+    p = torch.zeros_like(sm)
+    for h in range(HQ):
+        sh = K._round(torch.einsum("btd,bsd->bts", q_main[:, h].double(), k_main[:, h // (HQ // HKV)].double()),
+                      dtype) * kw["scaling"]
+        p[:, h // G] += torch.softmax(sh.masked_fill(~keep[:, h // G], K.NEG), -1)
+    p /= G
+    ref_ds = torch.where(keep, sm - p, torch.zeros_like(p))
+    ref_ds = torch.nn.functional.pad(ref_ds, (0, nblk * 64 - Sk)).view(B, HI, T, nblk, 64)
+    got = dsel.cpu().double()
+    lst = listed[..., None].expand_as(got)
+    assert (got[lst] - ref_ds[lst]).abs().max().item() <= 1e-4
+    # the gradients (the backward reads the listed slots only)
+    kl2, valid2 = KL.gather_kl(qd, kd, q_main.to(dev), k_main.to(dev), sel.to(dev), pos.to(dev), seg=seg.to(dev),
+                               slots_are_blocks=True, **kw)
+    K.kl_loss(kl2, valid2).backward()
+    qr = q_idx.double().requires_grad_()
+    kr = idx_k.double().requires_grad_()
+    rk2, rv2 = K.gather_kl_dense(qr, kr, q_main.double(), k_main.double(), sel, pos, seg=seg, round_dtype=dtype,
+                                 **kw)
+    K.kl_loss(rk2, rv2).backward()
+    assert_close_lowp(qd.grad.cpu(), qr.grad, dtype, what="d q_idx (every block)")
+    assert_close_lowp(kd.grad.cpu(), kr.grad, dtype, what="d idx_k (every block)")
+
+
+def test_kl_chunk_fn_warmup_keep_all(dev):
+    """KLChunkFn.apply as the warmup stage calls it: keep_block = every
+    KL-eligible block (restrict_to_selected=False), 130 blocks, against the
+    dense oracle, and its gradient."""
+    from srswa import kl as KL
+    g = torch.Generator().manual_seed(43)
+    B, HI, G, T, Sk, D, lw = 1, 1, 4, 128, 64 * 130, 128, 512
+    q_idx = (torch.randn(B, HI, T, D, generator=g) * D ** -0.5).to(torch.bfloat16)
+    idx_k = torch.randn(B, Sk, D, generator=g).to(torch.bfloat16)
+    q_main = torch.randn(B, HI * G, T, D, generator=g).to(torch.bfloat16)
+    k_main = torch.randn(B, 2, Sk, D, generator=g).to(torch.bfloat16)
+    pos = (Sk - 64 * T + torch.arange(T) * 64).expand(B, T).clone().to(torch.int32)
+    nblk = Sk // 64
+    keep_block = torch.ones(B, 1, T, nblk, dtype=torch.bool)
+    qd = q_idx.to(dev).requires_grad_()
+    kl = KL.KLChunkFn.apply(qd, idx_k[:, None].to(dev), q_main.to(dev), k_main.to(dev), keep_block.to(dev),
+                            pos.to(dev), 64, D ** -0.5, G, 2, lw, None)
+    sel = torch.arange(nblk, dtype=torch.int32).expand(B, HI, T, nblk)
+    qr = q_idx.double().requires_grad_()
+    rk, _ = K.gather_kl_dense(qr, idx_k.double(), q_main.double(), k_main.double(), sel, pos, block_size=64,
+                              local_window=lw, scaling=D ** -0.5, round_dtype=torch.bfloat16)
+    err = (kl.detach().cpu().double() - rk.detach()).abs() - 1e-3 * rk.detach().abs()
+    assert err.max().item() <= 2e-3
+    kl.sum().backward()
+    rk.sum().backward()
+    assert_close_lowp(qd.grad.cpu(), qr.grad, torch.bfloat16, what="KLChunkFn warmup d q_idx")
+
+
 def test_patch_rebinds_kl_chunk_fn(dev):
     import types
     from srswa import patch

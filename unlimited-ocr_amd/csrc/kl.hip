@@ -69,7 +69,9 @@ __global__ __launch_bounds__(256, 2) void kl_fwd_kernel(KlK p) {
   const int lid = (int)(blockIdx.x & 7) * p.per_xcd + (int)(blockIdx.x >> 3);
   if (lid >= p.nlogical) return;
   T* sK = reinterpret_cast<T*>(smem);
-  int* s_ids = reinterpret_cast<int*>(smem + p.ids_off);          // [64][K], -1 = no kept key
+  // [64][K] kept ids (-1 = none), or with slots_are_blocks [64][ceil(K / 32)]
+  // bitmaps of the kept blocks (slot = block)
+  int* s_ids = reinterpret_cast<int*>(smem + p.ids_off);
   uint32_t* s_bits = reinterpret_cast<uint32_t*>(smem + p.bits_off);
   uint16_t* s_chunks = reinterpret_cast<uint16_t*>(smem + p.chunks_off);
   int* s_count = reinterpret_cast<int*>(s_bits + p.nwords);
@@ -98,9 +100,37 @@ __global__ __launch_bounds__(256, 2) void kl_fwd_kernel(KlK p) {
   };
 
   // set-up: the rows' selected blocks that hold kept keys, and their union
+  const bool dense = a.slots_are_blocks != 0;
+  const int nwk = (K + 31) >> 5;                  // bitmap words per row (slots_are_blocks)
+  uint32_t* s_kb = reinterpret_cast<uint32_t*>(s_ids);
   for (int w = tid; w < p.nwords; w += NT) s_bits[w] = 0u;
   __syncthreads();
-  for (int e = tid; e < kTileRows * K; e += NT) {
+  // slot = block: a row lists block s as sel[s] == s (no repeats possible);
+  // a listed block with no kept key gets a zero dsel row (the backward reads
+  // every listed slot), unlisted slots are left alone
+  for (int e = tid; dense && e < kTileRows * nwk; e += NT) {
+    const int r = e / nwk, w = e % nwk;
+    uint32_t bits = 0u;
+    if (r < nrows) {
+      int lo, hi;
+      row_range(r, lo, hi);
+      const int32_t* ids = a.sel + (int64_t)b * a.sel_sb + (int64_t)ih * a.sel_sh + (int64_t)(t0 + r) * a.sel_st;
+      for (int j = 0; j < 32; ++j) {
+        const int s = 32 * w + j;
+        if (s >= K || ids[s] != s) continue;
+        if ((int64_t)s * kChunk < hi && (int64_t)s * kChunk + kChunk > lo) {
+          bits |= 1u << j;
+        } else if (a.dsel) {
+          float4* z = reinterpret_cast<float4*>(a.dsel + ds_tile + (int64_t)(t0 + r) * a.ds_st + (int64_t)s * kChunk);
+#pragma unroll
+          for (int i = 0; i < kChunk / 4; ++i) z[i] = make_float4(0.f, 0.f, 0.f, 0.f);
+        }
+      }
+    }
+    s_kb[e] = bits;
+    if (bits) atomicOr(&s_bits[w], bits);
+  }
+  for (int e = tid; !dense && e < kTileRows * K; e += NT) {
     const int r = e / K, s = e % K;
     int id = -1;
     if (r < nrows) {
@@ -139,14 +169,15 @@ __global__ __launch_bounds__(256, 2) void kl_fwd_kernel(KlK p) {
   };
   int lo = 0, hi = 0;
   if (row_ok) row_range(row, lo, hi);
-  const int* my_ids = s_ids + row * K;
+  const int* my_ids = s_ids + (dense ? 0 : row * K);
   // the row's first kKlIdRegs filtered ids in registers (the slot search of
   // every stage then has no LDS round trip); slots past them are read from LDS
   constexpr int kKlIdRegs = 8;
   int id_reg[kKlIdRegs];
 #pragma unroll
-  for (int s = 0; s < kKlIdRegs; ++s) id_reg[s] = s < K ? my_ids[s] : -1;
+  for (int s = 0; s < kKlIdRegs; ++s) id_reg[s] = (!dense && s < K) ? my_ids[s] : -1;
   auto find_slot_of = [&](int c) __attribute__((always_inline)) {
+    if (dense) return ((s_kb[row * nwk + (c >> 5)] >> (c & 31)) & 1u) ? c : -1;
     int found = -1;
 #pragma unroll
     for (int s = kKlIdRegs - 1; s >= 0; --s) found = id_reg[s] == c ? s : found;   // first slot wins
@@ -390,12 +421,15 @@ __device__ __forceinline__ void kl_row_range(const srswa_kl_args& a, int b, int 
 }
 
 // Block id of slot s of row t when it holds kept keys and is the id's first
-// slot (a repeated id counts once), else -1.
-__device__ __forceinline__ int kl_slot_block(const int32_t* ids, int s, int lo, int hi) {
+// slot (a repeated id counts once), else -1.  With slots_are_blocks (dense)
+// slot s holds block s exactly when ids[s] == s (no repeats to look for).
+__device__ __forceinline__ int kl_slot_block(const int32_t* ids, int s, int lo, int hi, bool dense = false) {
   int id = ids[s];
+  if (dense && id != s) return -1;
   if (id < 0 || (int64_t)id * kChunk >= hi || (int64_t)id * kChunk + kChunk <= lo) return -1;
-  for (int s2 = 0; s2 < s; ++s2)
-    if (ids[s2] == id) return -1;
+  if (!dense)
+    for (int s2 = 0; s2 < s; ++s2)
+      if (ids[s2] == id) return -1;
   return id;
 }
 
@@ -436,13 +470,16 @@ __device__ __forceinline__ int window_rows(const uint32_t* words, int w0, int rw
 // Bits of a 64-row tile's (block, row) pairs into row bitmaps: per block of the
 // tile's union (s_chunks, U entries), one wave ballots the rows whose kept ids
 // (s_ids, -1 = none) include it and ORs the two 32-row words once.
-__device__ __forceinline__ void tile_row_bits(const int* s_ids, int K, int nrows, const uint16_t* s_chunks, int U,
-                                              uint32_t* bm0, uint32_t* bm1, int rwords, int tile) {
+__device__ __forceinline__ void tile_row_bits(const int* s_ids, int K, bool dense, int nrows, const uint16_t* s_chunks,
+                                              int U, uint32_t* bm0, uint32_t* bm1, int rwords, int tile) {
   const int wave = threadIdx.x / kWave, lane = threadIdx.x % kWave, nw = blockDim.x / kWave;
+  const int nwk = (K + 31) >> 5;
   for (int u = wave; u < U; u += nw) {
     const int c = s_chunks[u];
     bool mine = false;
-    if (lane < nrows)
+    if (lane < nrows && dense)     // s_ids: per-row bitmaps of the listed blocks (slot = block)
+      mine = (reinterpret_cast<const uint32_t*>(s_ids)[lane * nwk + (c >> 5)] >> (c & 31)) & 1u;
+    else if (lane < nrows)
       for (int s = 0; s < K; ++s) mine = mine || s_ids[lane * K + s] == c;
     const uint64_t m = __ballot(mine);
     if (lane < 2) {
@@ -469,11 +506,38 @@ __global__ __launch_bounds__(256) void kl_rs_flag_kernel(KlRsK p) {
   uint32_t* s_bits = s_u;
   uint32_t* s_cnt = s_u + p.nwords;
   int* s_ids = reinterpret_cast<int*>(s_u + p.nwords + 1);
-  int* s_len = s_ids + kTileRows * K;
+  // with slots_are_blocks the ids region holds [64][ceil(K / 32)] bitmaps of
+  // the kept blocks
+  const bool dense = a.slots_are_blocks != 0;
+  const int nwk = (K + 31) >> 5;
+  int* s_len = s_ids + kTileRows * (dense ? nwk : K);
   uint16_t* s_chunks = reinterpret_cast<uint16_t*>(s_len + 1);
   for (int w = tid; w <= p.nwords; w += blockDim.x) s_u[w] = 0u;
   __syncthreads();
-  for (int e = tid; e < kTileRows * K; e += blockDim.x) {
+  for (int e = tid; dense && e < kTileRows * nwk; e += blockDim.x) {
+    const int r = e / nwk, w = e % nwk;
+    uint32_t bits = 0u;
+    if (r < nrows) {
+      int lo, hi;
+      kl_row_range(a, b, t0 + r, lo, hi);
+      const int32_t* ids = kl_row_ids(a, b, ih, t0 + r);
+      for (int j = 0; j < 32; ++j) {
+        const int s = 32 * w + j;
+        if (s >= K) break;
+        if (kl_slot_block(ids, s, lo, hi, true) >= 0) {
+          bits |= 1u << j;
+        } else if (ids[s] == s && a.dsel) {          // listed, nothing kept: a zero dsel row
+          float4* z = reinterpret_cast<float4*>(a.dsel + (int64_t)b * a.ds_sb + (int64_t)ih * a.ds_sh +
+                                                (int64_t)(t0 + r) * a.ds_st + (int64_t)s * kChunk);
+#pragma unroll
+          for (int i = 0; i < kChunk / 4; ++i) z[i] = make_float4(0.f, 0.f, 0.f, 0.f);
+        }
+      }
+    }
+    reinterpret_cast<uint32_t*>(s_ids)[e] = bits;
+    if (bits) atomicOr(&s_bits[w], bits);
+  }
+  for (int e = tid; !dense && e < kTileRows * K; e += blockDim.x) {
     const int r = e / K, s = e % K;
     int id = -1;
     if (r < nrows) {
@@ -487,11 +551,14 @@ __global__ __launch_bounds__(256) void kl_rs_flag_kernel(KlRsK p) {
   __syncthreads();
   for (int w = tid; w < p.nwords; w += blockDim.x) atomicAdd(s_cnt, (uint32_t)__popc(s_bits[w]));
   __syncthreads();
-  const bool rs = (int)*s_cnt > K;
+  // slot = block: the host runs these kernels only when every tile goes
+  // block-major (too few tiles to fill the chip)
+  const bool rs = dense || (int)*s_cnt > K;
   if (tid == 0) p.flag[(int64_t)bh * p.ntiles + tile] = rs ? 1u : 0u;
   if (!rs) return;                                    // uniform: no barrier below is skipped by part of the group
   const int U = compact_bitmap(s_bits, p.nwords, s_chunks, s_len);
-  tile_row_bits(s_ids, K, nrows, s_chunks, U, p.rbm + (int64_t)bh * p.nblk * p.rwords, nullptr, p.rwords, tile);
+  tile_row_bits(s_ids, K, dense, nrows, s_chunks, U, p.rbm + (int64_t)bh * p.nblk * p.rwords, nullptr, p.rwords,
+                tile);
 }
 
 // One workgroup per (sequence, index head, block c, 2048-row window): the
@@ -597,6 +664,7 @@ __global__ __launch_bounds__(128, 2) void kl_rs_pass_kernel(KlRsK p) {
         int lo, hi;
         kl_row_range(a, b, t, lo, hi);
         const int32_t* ids = kl_row_ids(a, b, ih, t);
+        if (a.slots_are_blocks) slot = c;           // the bitmap holds kept pairs
         for (int s = 0; s < K && slot < 0; ++s)
           if (ids[s] == c) slot = s;                  // the first slot holding c (the bitmap holds kept pairs)
         keep = range64(min(max(lo - j0, 0), 64), min(max(hi - j0, 0), 64));
@@ -695,7 +763,7 @@ __global__ __launch_bounds__(128, 2) void kl_rs_pass_kernel(KlRsK p) {
 
 // Per (row, head) of a flagged tile: the head's statistics merged over the
 // row's kept slots in slot order; the head-0 thread also zeroes the dsel rows
-// of slots with nothing kept.
+// of slots with nothing kept (with slots_are_blocks the flag kernel does).
 __global__ __launch_bounds__(256) void kl_rs_combine_kernel(KlRsK p) {
   const srswa_kl_args& a = p.a;
   const int G1 = p.G + 1;
@@ -708,11 +776,16 @@ __global__ __launch_bounds__(256) void kl_rs_combine_kernel(KlRsK p) {
   const int ih = bh % a.HI, b = bh / a.HI;
   if (!p.flag[(int64_t)bh * p.ntiles + t / kTileRows]) return;
   const int K = a.K;
+  const bool dense = a.slots_are_blocks != 0;
   int lo, hi;
   kl_row_range(a, b, t, lo, hi);
   const int32_t* ids = kl_row_ids(a, b, ih, t);
+  // the kept slots: a bitmap (at most 64 slots), or with slots_are_blocks the
+  // constant-time test of the slot itself
+  // (dense: kl_rs_flag_kernel zeroes the dsel rows of listed slots with
+  // nothing kept)
   uint64_t live = 0ull;
-  for (int s = 0; s < K; ++s) {
+  for (int s = 0; s < K && !dense; ++s) {
     if (kl_slot_block(ids, s, lo, hi) >= 0) {
       live |= 1ull << s;
     } else if (hh == 0 && a.dsel) {
@@ -722,14 +795,17 @@ __global__ __launch_bounds__(256) void kl_rs_combine_kernel(KlRsK p) {
       for (int i = 0; i < kChunk / 4; ++i) z[i] = make_float4(0.f, 0.f, 0.f, 0.f);
     }
   }
+  auto is_live = [&](int s) { return dense ? kl_slot_block(ids, s, lo, hi, true) >= 0 : ((live >> s) & 1ull) != 0; };
+  // dense: only the blocks of the row's kept key range can be live
+  const int s0 = dense ? lo / kChunk : 0, s1 = dense ? min(K, (hi + kChunk - 1) / kChunk) : K;
   const float2* rec = p.srec + rowi * K * G1 + hh;
   float mm = -INFINITY;
-  for (int s = 0; s < K; ++s)
-    if ((live >> s) & 1ull) mm = fmaxf(mm, rec[s * G1].x);
+  for (int s = s0; s < s1; ++s)
+    if (is_live(s)) mm = fmaxf(mm, rec[s * G1].x);
   float ll = 0.f;
   if (mm > -INFINITY)
-    for (int s = 0; s < K; ++s)
-      if ((live >> s) & 1ull) {
+    for (int s = s0; s < s1; ++s)
+      if (is_live(s)) {
         const float2 v = rec[s * G1];                // a second read, from cache
         if (v.x > -INFINITY) ll += v.y * __builtin_amdgcn_exp2f(v.x - mm);
       }
@@ -749,8 +825,10 @@ __global__ __launch_bounds__(256) void kl_rs_final_kernel(KlRsK p) {
   kl_row_range(a, b, t, lo, hi);
   const int32_t* ids = kl_row_ids(a, b, ih, t);
   float kl = 0.f;
-  for (int s = 0; s < a.K; ++s)
-    if (kl_slot_block(ids, s, lo, hi) >= 0) kl += p.klp[gid * a.K + s];
+  const bool dense = a.slots_are_blocks != 0;   // only the blocks of the kept key range can hold a pair
+  const int s0 = dense ? lo / kChunk : 0, s1 = dense ? min(a.K, (hi + kChunk - 1) / kChunk) : a.K;
+  for (int s = s0; s < s1; ++s)
+    if (kl_slot_block(ids, s, lo, hi, dense) >= 0) kl += p.klp[gid * a.K + s];
   const bool valid = p.rst[gid * (p.G + 1) + p.G].y > 0.f;
   a.kl[(int64_t)b * a.kl_sb + (int64_t)ih * a.kl_sh + t] = valid ? kl * kLn2 : 0.f;
   a.valid[(int64_t)b * a.va_sb + (int64_t)ih * a.va_sh + t] = valid ? 1 : 0;
@@ -798,9 +876,11 @@ template <int D> struct KlBwdLds {
   static constexpr int bytes = dsOff + 64 * SP * 2;
 };
 
-// the slot of block c among row (b, ih, t)'s ids (first occurrence), -1 if none
+// the slot of block c among row (b, ih, t)'s ids (first occurrence), -1 if
+// none; with slots_are_blocks slot c itself when the row lists block c
 __device__ __forceinline__ int find_slot(const srswa_kl_bwd_args& a, int b, int ih, int t, int c) {
   const int32_t* ids = a.sel + (int64_t)b * a.sel_sb + (int64_t)ih * a.sel_sh + (int64_t)t * a.sel_st;
+  if (a.slots_are_blocks) return (c < a.K && ids[c] == c) ? c : -1;
   for (int s = 0; s < a.K; ++s)
     if (ids[s] == c) return s;
   return -1;
@@ -899,7 +979,7 @@ __global__ __launch_bounds__(kBwdThreads) void kl_dq_kernel(KlBwdK p) {
   for (int e = tid; e < nrows * a.K; e += kBwdThreads) {
     const int r = e / a.K, s = e % a.K;
     const int id = a.sel[(int64_t)b * a.sel_sb + (int64_t)ih * a.sel_sh + (int64_t)(t0 + r) * a.sel_st + s];
-    if (id >= 0 && id < p.nblk) atomicOr(&s_bits[id >> 5], 1u << (id & 31));
+    if (id >= 0 && id < p.nblk && (!a.slots_are_blocks || id == s)) atomicOr(&s_bits[id >> 5], 1u << (id & 31));
   }
   __syncthreads();
   const int U = compact_bitmap(s_bits, nwords, s_chunks, &s_count);
@@ -959,11 +1039,28 @@ __global__ __launch_bounds__(256) void kl_bwd_flag_kernel(KlBwdK p) {
   uint32_t* s_bits = s_u;
   uint32_t* s_cnt = s_u + p.nwords;
   int* s_ids = reinterpret_cast<int*>(s_u + p.nwords + 1);
-  int* s_len = s_ids + kTileRows * K;
+  // with slots_are_blocks the ids region holds [64][ceil(K / 32)] bitmaps
+  int* s_len = s_ids + kTileRows * (a.slots_are_blocks ? (K + 31) >> 5 : K);
   uint16_t* s_chunks = reinterpret_cast<uint16_t*>(s_len + 1);
   for (int w = tid; w <= p.nwords; w += blockDim.x) s_u[w] = 0u;
   __syncthreads();
-  for (int e = tid; e < kTileRows * K; e += blockDim.x) {
+  const bool dense = a.slots_are_blocks != 0;
+  const int nwk = (K + 31) >> 5;
+  // slot = block: per-row bitmaps of the listed blocks in place of the ids
+  for (int e = tid; dense && e < kTileRows * nwk; e += blockDim.x) {
+    const int r = e / nwk, w = e % nwk;
+    uint32_t bits = 0u;
+    if (r < nrows) {
+      const int32_t* ids = a.sel + (int64_t)b * a.sel_sb + (int64_t)ih * a.sel_sh + (int64_t)(t0 + r) * a.sel_st;
+      for (int j = 0; j < 32; ++j) {
+        const int s = 32 * w + j;
+        if (s < K && s < p.nblk && ids[s] == s) bits |= 1u << j;
+      }
+    }
+    reinterpret_cast<uint32_t*>(s_ids)[e] = bits;
+    if (bits) atomicOr(&s_bits[w], bits);
+  }
+  for (int e = tid; !dense && e < kTileRows * K; e += blockDim.x) {
     const int r = e / K, s = e % K;
     int id = -1;
     if (r < nrows) {
@@ -979,11 +1076,11 @@ __global__ __launch_bounds__(256) void kl_bwd_flag_kernel(KlBwdK p) {
   __syncthreads();
   for (int w = tid; w < p.nwords; w += blockDim.x) atomicAdd(s_cnt, (uint32_t)__popc(s_bits[w]));
   __syncthreads();
-  const bool rs = (int)*s_cnt > K;
+  const bool rs = !dense && (int)*s_cnt > K;   // slot = block: a union never exceeds K
   if (tid == 0) p.flag[(int64_t)bh * p.ntiles + tile] = rs ? 1u : 0u;
   const int U = compact_bitmap(s_bits, p.nwords, s_chunks, s_len);
   const int64_t base = (int64_t)bh * p.nblk * p.rwords;
-  tile_row_bits(s_ids, K, nrows, s_chunks, U, p.rbm_all + base, rs ? p.rbm + base : nullptr, p.rwords, tile);
+  tile_row_bits(s_ids, K, dense, nrows, s_chunks, U, p.rbm_all + base, rs ? p.rbm + base : nullptr, p.rwords, tile);
 }
 
 // Per (sequence, index head, block c, 2048-row window): the window's flagged
@@ -1209,7 +1306,7 @@ __global__ __launch_bounds__(256) void kl_dk_reduce_kernel(KlBwdK p) {
 
 bool al16(const void* p) { return ((uintptr_t)p & 15u) == 0; }
 
-int check_common(int dtype, int D, int block_size, int K, const char* what) {
+int check_common(int dtype, int D, int block_size, int K, int Sk, int slots_are_blocks, const char* what) {
   if (dtype != SRSWA_BF16 && dtype != SRSWA_F16) {
     set_error("%s: dtype %d not supported (bf16, fp16)", what, dtype);
     return SRSWA_UNSUPPORTED;
@@ -1222,7 +1319,13 @@ int check_common(int dtype, int D, int block_size, int K, const char* what) {
     set_error("%s: block_size %d not supported (64)", what, block_size);
     return SRSWA_UNSUPPORTED;
   }
-  if (K <= 0 || K > 64) {
+  if (slots_are_blocks) {
+    const int nblk = (int)ceil_div(Sk, kChunk);
+    if (K != nblk || nblk > 64 * 32) {
+      set_error("%s: slots_are_blocks needs K = ceil(Sk / 64) = %d <= 2048 (got K = %d)", what, nblk, K);
+      return SRSWA_UNSUPPORTED;
+    }
+  } else if (K <= 0 || K > 64) {
     set_error("%s: %d selected blocks per row not supported (1..64)", what, K);
     return SRSWA_UNSUPPORTED;
   }
@@ -1257,11 +1360,19 @@ KlRsLayout kl_rs_layout(const srswa_kl_args* a) {
 
 int kl_fwd_impl(const srswa_kl_args* a, void* scratch, size_t scratch_bytes, void* stream);
 
+// slots_are_blocks: every tile goes block-major when the tiles alone cannot
+// fill the chip (a chunk of the warmup stage's rows), else the tile kernel
+// runs alone (a tile's union never exceeds K)
+bool kl_dense_block_major(const srswa_kl_args* a) {
+  return a->slots_are_blocks && (int64_t)a->B * a->HI * ceil_div(a->T, kTileRows) < 512;
+}
+
 }  // namespace
 }  // namespace srswa
 
 extern "C" size_t srswa_gather_kl_fwd_workspace(const srswa_kl_args* a) {
   if (!a || a->B <= 0 || a->HI <= 0 || a->T <= 0 || a->Sk <= 0 || a->K <= 0) return 0;
+  if (a->slots_are_blocks && !kl_dense_block_major(a)) return 0;
   return kl_rs_layout(a).total;
 }
 
@@ -1337,7 +1448,7 @@ int kl_fwd_impl(const srswa_kl_args* a, void* scratch, size_t scratch_bytes, voi
     set_error("gather kl: bad sizes (HQ must be a multiple of HI and HKV)");
     return SRSWA_INVALID;
   }
-  int rc = check_common(a->dtype, a->D, a->block_size, a->K, "gather kl");
+  int rc = check_common(a->dtype, a->D, a->block_size, a->K, a->Sk, a->slots_are_blocks, "gather kl");
   if (rc != SRSWA_OK) return rc;
   KlSide side;
   if (!kl_side_of(a->side_stream, a->fork_event, a->join_event, "gather kl", &side)) return SRSWA_INVALID;
@@ -1357,6 +1468,7 @@ int kl_fwd_impl(const srswa_kl_args* a, void* scratch, size_t scratch_bytes, voi
     return SRSWA_UNSUPPORTED;
   }
   if (a->T == 0 || a->B == 0) return SRSWA_OK;
+  if (a->slots_are_blocks && !kl_dense_block_major(a)) scratch = nullptr;   // the tile kernel alone
   KlRsLayout rl{};
   if (scratch) {
     rl = kl_rs_layout(a);
@@ -1397,14 +1509,16 @@ int kl_fwd_impl(const srswa_kl_args* a, void* scratch, size_t scratch_bytes, voi
     rk.klp = reinterpret_cast<float*>(base + rl.klp);
     const int64_t rbm_words = (int64_t)a->B * a->HI * nblk * rk.rwords;
     hipLaunchKernelGGL(kl_zero_kernel, dim3((unsigned)((rbm_words + 255) / 256)), dim3(256), 0, st, rk.rbm, rbm_words);
-    const size_t flds = ((size_t)k.nwords + 2 + (size_t)kTileRows * a->K) * 4 + (size_t)nblk * 2 + 16;
+    const size_t idw = a->slots_are_blocks ? (size_t)ceil_div(a->K, 32) : (size_t)a->K;
+    const size_t flds = ((size_t)k.nwords + 2 + (size_t)kTileRows * idw) * 4 + (size_t)nblk * 2 + 16;
     hipLaunchKernelGGL(kl_rs_flag_kernel, dim3((unsigned)k.nlogical), dim3(256), flds, st, rk);
     k.rs_flag = rk.flag;
   }
 
   const int tile_bytes = a->D == 64 ? KlLds<64>::tileBytes : KlLds<128>::tileBytes;
   k.ids_off = tile_bytes;
-  k.bits_off = k.ids_off + kTileRows * a->K * 4;
+  // per row: K ids, or with slots_are_blocks a bitmap of ceil(K / 32) words
+  k.bits_off = k.ids_off + kTileRows * (a->slots_are_blocks ? (int)ceil_div(a->K, 32) : a->K) * 4;
   k.chunks_off = k.bits_off + (k.nwords + 4) * 4;
   const int nchunk_max = std::min(kTileRows * a->K, nblk);
   k.stats_off = (k.chunks_off + nchunk_max * 2 + 15) & ~15;
@@ -1449,7 +1563,9 @@ int kl_fwd_impl(const srswa_kl_args* a, void* scratch, size_t scratch_bytes, voi
     }
 #undef KL_RS
   };
-  if (scratch) {
+  if (scratch && kl_dense_block_major(a)) {
+    rs_work(st);   // every tile is flagged: the tile kernel would have nothing to do
+  } else if (scratch) {
     const hipError_t fe = kl_fork(st, side, tile_work, rs_work);
     if (fe != hipSuccess) {
       set_error("gather kl: side stream failed: %s", hipGetErrorString(fe));
@@ -1484,7 +1600,8 @@ KlBwdLayout kl_bwd_layout(const srswa_kl_bwd_args* a) {
   L.rbm = L.flag + al((size_t)(bh * ntiles) * 4);
   L.rbm_all = L.rbm + al((size_t)(bh * nblk * rwords) * 4);
   L.dqp = L.rbm_all + al((size_t)(bh * nblk * rwords) * 4);
-  L.dkp = L.dqp + al((size_t)(bh * T * std::max(a->K, 0) * std::max(a->D, 0)) * 4);
+  const int64_t kp = a->slots_are_blocks ? 0 : std::max(a->K, 0);   // flagged rows' dQ partials
+  L.dkp = L.dqp + al((size_t)(bh * T * kp * std::max(a->D, 0)) * 4);
   const int64_t nwin = ceil_div(T, kRsWin), bb = std::max(a->B, 0);
   L.dkw = L.dkp + al((size_t)(bb * nblk * nwin * kChunk * std::max(a->D, 0)) * 4);
   L.total = L.dkw + al((size_t)(bb * nblk * nwin) * 4);
@@ -1511,7 +1628,7 @@ extern "C" int srswa_gather_kl_bwd(const srswa_kl_bwd_args* a, void* scratch, si
     set_error("gather kl backward: bad sizes");
     return SRSWA_INVALID;
   }
-  int rc = check_common(a->dtype, a->D, a->block_size, a->K, "gather kl backward");
+  int rc = check_common(a->dtype, a->D, a->block_size, a->K, a->Sk, a->slots_are_blocks, "gather kl backward");
   if (rc != SRSWA_OK) return rc;
   KlSide side;
   if (!kl_side_of(a->side_stream, a->fork_event, a->join_event, "gather kl backward", &side)) return SRSWA_INVALID;
@@ -1556,7 +1673,8 @@ extern "C" int srswa_gather_kl_bwd(const srswa_kl_bwd_args* a, void* scratch, si
   const int64_t words = (int64_t)(bl.dqp - bl.rbm) / 4;       // both row bitmaps
   hipLaunchKernelGGL(kl_zero_kernel, dim3((unsigned)((words + 255) / 256)), dim3(256), 0, st, k.rbm, words);
   const int64_t ntl = (int64_t)a->B * a->HI * k.ntiles;
-  const size_t flds = ((size_t)k.nwords + 2 + (size_t)kTileRows * a->K) * 4 + (size_t)k.nblk * 2 + 16;
+  const size_t idw = a->slots_are_blocks ? (size_t)ceil_div(a->K, 32) : (size_t)a->K;
+  const size_t flds = ((size_t)k.nwords + 2 + (size_t)kTileRows * idw) * 4 + (size_t)k.nblk * 2 + 16;
   hipLaunchKernelGGL(kl_bwd_flag_kernel, dim3((unsigned)ntl), dim3(256), flds, st, k);
   const dim3 gdq((unsigned)ntl), gdk((unsigned)((int64_t)a->B * k.nblk * k.nwin));
   const dim3 gdr((unsigned)(((int64_t)a->B * k.nblk * kChunk * (a->D / 4) + 255) / 256));
@@ -1574,10 +1692,12 @@ extern "C" int srswa_gather_kl_bwd(const srswa_kl_bwd_args* a, void* scratch, si
 #undef KL_DQ
   };
   auto rest_work = [&](hipStream_t s) {
-#define KL_BWD(T_, D_)                                                                      \
-  hipLaunchKernelGGL((kl_rs_dq_kernel<T_, D_>), grs, dim3(kBwdThreads), lds, s, k);        \
-  hipLaunchKernelGGL((kl_rs_dq_reduce_kernel<T_, D_>), grd, dim3(256), 0, s, k);           \
-  hipLaunchKernelGGL((kl_dk_kernel<T_, D_>), gdk, dim3(kBwdThreads), lds, s, k);           \
+    // slot = block: no tile is flagged, so the block-major dQ has no rows
+    const bool rs = !a->slots_are_blocks;
+#define KL_BWD(T_, D_)                                                                              \
+  if (rs) hipLaunchKernelGGL((kl_rs_dq_kernel<T_, D_>), grs, dim3(kBwdThreads), lds, s, k);        \
+  if (rs) hipLaunchKernelGGL((kl_rs_dq_reduce_kernel<T_, D_>), grd, dim3(256), 0, s, k);           \
+  hipLaunchKernelGGL((kl_dk_kernel<T_, D_>), gdk, dim3(kBwdThreads), lds, s, k);                   \
   hipLaunchKernelGGL((kl_dk_reduce_kernel<T_, D_>), gdr, dim3(256), 0, s, k);
     if (a->dtype == SRSWA_BF16) {
       if (a->D == 128) { KL_BWD(bf16_t, 128) } else { KL_BWD(bf16_t, 64) }

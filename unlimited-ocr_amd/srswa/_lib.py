@@ -419,6 +419,7 @@ class KlArgs(ctypes.Structure):
         ("K", _i32), ("block_size", _i32), ("local_window", _i32),
         ("scaling", ctypes.c_float),
         ("dtype", _i32),
+        ("slots_are_blocks", _i32),
         ("side_stream", _vp), ("fork_event", _vp), ("join_event", _vp),
     ]
 
@@ -436,6 +437,7 @@ class KlBwdArgs(ctypes.Structure):
         ("dk_idx", _vp), ("dk_sb", _i64), ("dk_st", _i64),
         ("B", _i32), ("HI", _i32), ("T", _i32), ("Sk", _i32), ("D", _i32), ("K", _i32), ("block_size", _i32),
         ("dtype", _i32),
+        ("slots_are_blocks", _i32),
         ("side_stream", _vp), ("fork_event", _vp), ("join_event", _vp),
     ]
 

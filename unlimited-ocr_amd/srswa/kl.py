@@ -67,8 +67,11 @@ def _side_fields(device, use: bool) -> dict:
 
 
 def kl_forward(q_idx, idx_k, q_main, k_main, sel, pos, *, block_size, local_window, scaling, seg=None,
-               with_dsel=True, row_sparse=True, side_stream=True):
+               with_dsel=True, row_sparse=True, side_stream=True, slots_are_blocks=False):
     """(kl [B, HI, T] fp32, valid [B, HI, T] bool, dsel [B, HI, T, K, 64] fp32 or None).
+    ``slots_are_blocks``: sel [B, HI, T, ceil(Sk / 64)] lists block s in slot s
+    (sel[..., s] == s, else -1), any number of blocks per row; dsel rows of
+    unlisted slots are left unwritten.
     ``row_sparse``: tiles whose rows select unrelated blocks are computed
     block-major (srswa_gather_kl_fwd_ws); False runs every tile on the tile
     kernel (srswa_gather_kl_fwd).  ``side_stream``: the row-sparse call runs
@@ -104,6 +107,7 @@ def kl_forward(q_idx, idx_k, q_main, k_main, sel, pos, *, block_size, local_wind
         ds_sh=0 if dsel is None else dsel.stride(1), ds_st=0 if dsel is None else dsel.stride(2),
         B=B, HI=HI, HQ=HQ, HKV=HKV, T=T, Sk=Sk, D=D, K=K, block_size=int(block_size),
         local_window=int(local_window), scaling=float(scaling), dtype=_lib.dtype_code(q_idx.dtype),
+        slots_are_blocks=1 if slots_are_blocks else 0,
         **_side_fields(q_idx.device, side_stream and row_sparse))
     # with a workspace, tiles whose rows select unrelated blocks are taken by
     # the block-major (row-sparse) kernels instead of the tile kernel
@@ -118,9 +122,9 @@ def kl_forward(q_idx, idx_k, q_main, k_main, sel, pos, *, block_size, local_wind
     return kl, valid, dsel
 
 
-def kl_backward(grad, q_idx, idx_k, sel, dsel, *, block_size, side_stream=True):
+def kl_backward(grad, q_idx, idx_k, sel, dsel, *, block_size, side_stream=True, slots_are_blocks=False):
     """(d q_idx like q_idx, d idx_k like idx_k) for d loss / d kl = grad [B, HI, T].
-    ``side_stream`` as in ``kl_forward``."""
+    ``side_stream`` and ``slots_are_blocks`` as in ``kl_forward``."""
     _cuda(grad, q_idx, idx_k, sel, dsel)
     qi = _inner(q_idx)
     ik = _inner(_keys(idx_k))
@@ -139,7 +143,7 @@ def kl_backward(grad, q_idx, idx_k, sel, dsel, *, block_size, side_stream=True):
         dq_idx=dq.data_ptr(), dq_sb=dq.stride(0), dq_sh=dq.stride(1), dq_st=dq.stride(2),
         dk_idx=dk.data_ptr(), dk_sb=dk.stride(0), dk_st=dk.stride(1),
         B=B, HI=HI, T=T, Sk=Sk, D=D, K=s.shape[-1], block_size=int(block_size), dtype=_lib.dtype_code(qi.dtype),
-        **_side_fields(qi.device, side_stream))
+        slots_are_blocks=1 if slots_are_blocks else 0, **_side_fields(qi.device, side_stream))
     need = ctypes.c_size_t()
     _lib.check(_lib.lib().srswa_gather_kl_bwd_workspace(ctypes.byref(a), ctypes.byref(need)),
                "srswa_gather_kl_bwd_workspace")
@@ -153,12 +157,15 @@ class GatherKLFn(torch.autograd.Function):
     """(kl, valid) with the student-path gradient (the teacher is detached)."""
 
     @staticmethod
-    def forward(ctx, q_idx, idx_k, q_main, k_main, sel, pos, seg, block_size, local_window, scaling):
+    def forward(ctx, q_idx, idx_k, q_main, k_main, sel, pos, seg, block_size, local_window, scaling,
+                slots_are_blocks=False):
         kl, valid, dsel = kl_forward(q_idx, idx_k, q_main.detach(), k_main.detach(), sel, pos,
                                      block_size=block_size, local_window=local_window, scaling=scaling, seg=seg,
-                                     with_dsel=q_idx.requires_grad or idx_k.requires_grad)
+                                     with_dsel=q_idx.requires_grad or idx_k.requires_grad,
+                                     slots_are_blocks=slots_are_blocks)
         ctx.save_for_backward(q_idx, idx_k, sel, dsel if dsel is not None else kl)
         ctx.block_size = block_size
+        ctx.slots_are_blocks = slots_are_blocks
         ctx.mark_non_differentiable(valid)
         return kl, valid
 
@@ -166,18 +173,23 @@ class GatherKLFn(torch.autograd.Function):
     def backward(ctx, gkl, gvalid):
         q_idx, idx_k, sel, dsel = ctx.saved_tensors
         if gkl is None:
-            return (None,) * 10
-        dq, dk = kl_backward(gkl, q_idx, idx_k, sel, dsel, block_size=ctx.block_size)
-        return dq, dk, None, None, None, None, None, None, None, None
+            return (None,) * 11
+        dq, dk = kl_backward(gkl, q_idx, idx_k, sel, dsel, block_size=ctx.block_size,
+                             slots_are_blocks=ctx.slots_are_blocks)
+        return dq, dk, None, None, None, None, None, None, None, None, None
 
 
-def gather_kl(q_idx, idx_k, q_main, k_main, sel, pos, *, block_size, local_window, scaling, seg=None):
+def gather_kl(q_idx, idx_k, q_main, k_main, sel, pos, *, block_size, local_window, scaling, seg=None,
+              slots_are_blocks=False):
     """Per-row KL [B, HI, T] (fp32, differentiable in q_idx / idx_k) and its
     validity [B, HI, T] (bool).  q_idx [B, HI, T, d]; idx_k [B, Sk, d] or
     [B, 1, Sk, d]; q_main [B, HQ, T, d]; k_main [B, HKV, Sk, d]; sel
-    [B, HI, T, K] block ids (-1 = empty); pos [B, T] key positions of the rows;
-    seg [B, T] first key of each row's sample (packed rows) or None."""
-    return GatherKLFn.apply(q_idx, idx_k, q_main, k_main, sel, pos, seg, block_size, local_window, scaling)
+    [B, HI, T, K] block ids (-1 = empty), K <= 64, or with ``slots_are_blocks``
+    [B, HI, T, ceil(Sk / 64)] with sel[..., s] in {s, -1}; pos [B, T] key
+    positions of the rows; seg [B, T] first key of each row's sample (packed
+    rows) or None."""
+    return GatherKLFn.apply(q_idx, idx_k, q_main, k_main, sel, pos, seg, block_size, local_window, scaling,
+                            slots_are_blocks)
 
 
 class KLChunkFn:
@@ -191,16 +203,20 @@ class KLChunkFn:
         del group, kv_group                    # implied by the head counts of the operands
         lw = block_size if local_window is None else local_window
         nblk = keep_block.shape[-1]
-        # slots per row: every block when there are at most 64 (no read-back);
-        # beyond that the widest row's count is read back once per chunk (the
-        # kernels take at most 64 slots, wider rows go to the original)
-        K = nblk if nblk <= 64 else max(1, int(keep_block.sum(-1).max()))
+        # slot s holds block s (-1 where not kept): every block of the row's
+        # keep mask, however many (the warmup stage keeps every KL-eligible
+        # block), with no read-back; listed blocks outside the row's kept key
+        # range are dropped here (the kernels would give them zero rows)
         ar = torch.arange(nblk, device=keep_block.device, dtype=torch.int32)
-        ids = torch.where(keep_block, ar, torch.full_like(ar, -1))
-        sel = ids.topk(min(K, nblk), dim=-1).values
         seg = None
         if same_seg is not None:               # [B, 1, C, Sk]: first key of the row's sample
             seg = same_seg[:, 0].to(torch.int8).argmax(dim=-1)
+        hi = (pos_chunk.to(torch.int64) - lw + 1).clamp(min=0)                       # [B, C]
+        lo = seg.to(torch.int64) if seg is not None else torch.zeros_like(hi)
+        in_range = (ar[None, None, :] * block_size < hi[..., None]) & (ar[None, None, :] * block_size + block_size >
+                                                                       lo[..., None])
+        keep = keep_block & in_range[:, None]
+        sel = torch.where(keep, ar, torch.full_like(ar, -1))
         kl, _ = gather_kl(q_chunk, idx_k, q_main_chunk, k_main, sel, pos_chunk, block_size=block_size,
-                          local_window=lw, scaling=scaling, seg=seg)
+                          local_window=lw, scaling=scaling, seg=seg, slots_are_blocks=True)
         return kl
