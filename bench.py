@@ -336,6 +336,17 @@ def cpu_baseline_indexer(budget_s):
                       f"_block_scores_infer head_cls + top-k (fp32)", "host": host_info()}
 
 
+def _attn_dtype(args, c, names):
+    """--dtype fp32: the legs' operands as fp32 (in place in ``c``); returns
+    (dtype label, MFMA peak TFLOP/s, kernel type label)."""
+    import torch
+    if getattr(args, "dtype", "bf16") != "fp32":
+        return "bf16", 2500.0, "bf16"
+    for n in names:
+        c[n] = c[n].to(torch.float32)
+    return "fp32", 157.3, "float"
+
+
 def bench_prefill(args):
     """Config 4: chunked prefill, B=4 x 2048 query rows at the tail of 65536 keys."""
     import torch
@@ -343,6 +354,7 @@ def bench_prefill(args):
     dev = torch.device("cuda:0")
     B, T, Sk, H, D, BS, LW, K = 4, 2048, 65536, 10, 128, 64, 512, 8
     c = W.prefill_config(B=B, T=T, Sk=Sk, H=H, D=D, device=dev)
+    dtl, peak, kt = _attn_dtype(args, c, ("q", "k", "v"))
     idx = c["block_idx"].to(dev)
     fn = lambda: ops.gather_fwd(c["q"], c["k"], c["v"], idx, block_size=BS, local_window=LW, scale=c["scale"])
     ms = _time_launches(fn, args.steps, args.warmup, dev)
@@ -353,13 +365,13 @@ def bench_prefill(args):
     return {"metric": "chunked-prefill tokens/s + MFMA TFLOP/s (config 4)", "value": B * T / (ms * 1e-3),
             "cpu_baseline": cpu,
             "unit": "tokens/s", "n_gpus": 1, "steps": args.steps, "warmup": args.warmup, "ms_per_step": ms,
-            "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "bf16",
+            "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": dtl,
             "data": "synthetic (seeded N(0,1); top-8 per 64-query tile from the prefix)",
             "config": {"workload": "config 4: chunked prefill B=4, 2048 of 65536, 10 heads, block 64, "
                                    "top-8 + 512 window", "flops_per_step": flops},
-            "roofline": {"bound": "mfma", "achieved": tfs, "peak": 2500.0, "unit": "TFLOP/s",
-                         "frac": tfs / 2500.0, "traffic": None,
-                         "kernel": "srswa::fwd_kernel<bf16,128>"}}
+            "roofline": {"bound": "mfma", "achieved": tfs, "peak": peak, "unit": "TFLOP/s",
+                         "frac": tfs / peak, "traffic": None,
+                         "kernel": f"srswa::fwd_kernel<{kt},128>"}}
 
 
 def cpu_baseline_rows(c, Sk, T, BS, LW, budget_s, backward):
@@ -491,6 +503,7 @@ def bench_fwdbwd(args):
     dev = torch.device("cuda:0")
     B, T, H, D, BS, LW, K = 2, 16384, 10, 128, 64, 512, 8
     c = W.fwdbwd_config(B=B, T=T, H=H, D=D, device=dev)
+    dtl, peak, kt = _attn_dtype(args, c, ("q", "k", "v", "do"))
     idx = c["block_idx"].to(dev)
     q, k, v, do = c["q"], c["k"], c["v"], c["do"]
 
@@ -513,15 +526,15 @@ def bench_fwdbwd(args):
     return {"metric": "fwd+bwd tokens/s + MFMA TFLOP/s (config 5)", "value": B * T / (ms * 1e-3),
             "cpu_baseline": cpu,
             "unit": "tokens/s", "n_gpus": 1, "steps": args.steps, "warmup": args.warmup, "ms_per_step": ms,
-            "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "bf16",
+            "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": dtl,
             "data": "synthetic (seeded N(0,1); tile m selects min(8, m-8) blocks below m-8)",
             "config": {"workload": "config 5: fwd+bwd B=2, T=16384, 10 heads, block 64, top-8 + 512 window",
                        "flops_per_step": flops, "fwd_ms": ms_f, "bwd_ms": ms_b,
                        "fwd_tflops": pairs * 4 * D / (ms_f * 1e-3) / 1e12,
                        "bwd_tflops": pairs * 10 * D / (ms_b * 1e-3) / 1e12},
-            "roofline": {"bound": "mfma", "achieved": tfs, "peak": 2500.0, "unit": "TFLOP/s",
-                         "frac": tfs / 2500.0, "traffic": None,
-                         "kernel": "fwd_kernel + delta/touch/dq/dkv kernels"}}
+            "roofline": {"bound": "mfma", "achieved": tfs, "peak": peak, "unit": "TFLOP/s",
+                         "frac": tfs / peak, "traffic": None,
+                         "kernel": f"fwd_kernel<{kt}> + delta/touch/dq/dkv kernels"}}
 
 
 def _kv_dtype(args):
@@ -977,6 +990,8 @@ def main():
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--no-check", action="store_true", help="skip the oracle spot check")
     ap.add_argument("--cpu-budget", type=float, default=12.0)
+    ap.add_argument("--dtype", default="bf16", choices=["bf16", "fp32"],
+                    help="operand dtype of the prefill / fwdbwd legs (fp32: the fp32 MFMA form, 157.3 TFLOP/s peak)")
     ap.add_argument("--kv", default="bf16", choices=["bf16", "e4m3fn", "e4m3fnuz", "e5m2", "e5m2fnuz"],
                     help="K / V cache dtype of the paged legs (fp8 formats: half the bytes)")
     args = ap.parse_args()

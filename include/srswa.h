@@ -148,8 +148,10 @@ int srswa_topk_rows(const float* scores, int64_t rows, int32_t n, int64_t row_st
  * sample starts at seg[b, t] (packing; NULL = 0), ls = max(qi - LW + 1, seg):
  *   window keys ls <= j <= qi                      logit = scale*q.k
  *   remote keys j of a selected block, seg <= j < ls  logit = scale*q.k + bias
- * Duplicate ids count once (first slot's bias).  bf16 / fp16 only; q*scale and
- * P are rounded to the input dtype before their products (as the reference).
+ * Duplicate ids count once (first slot's bias).  bf16 / fp16: q*scale and P
+ * are rounded to the input dtype before their products (as the reference);
+ * fp32 (SRSWA_F32, the reference kernels are dtype-generic): fp32 operands,
+ * products and sums throughout, on v_mfma_f32_32x32x2_f32.
  * ---------------------------------------------------------------------- */
 typedef struct {
   const void* q;       int64_t q_sb, q_st, q_sh;       /* [B, T, HQ, D]                 */
@@ -162,7 +164,7 @@ typedef struct {
   float* lse;          int64_t lse_sb, lse_st, lse_sh; /* [B, T, HQ]; NULL = skip       */
   int32_t B, T, Sk, HQ, HKV, HI, D, S, block_size, local_window;
   float scale;
-  int32_t dtype;                                       /* SRSWA_BF16 or SRSWA_F16        */
+  int32_t dtype;                                       /* SRSWA_BF16, SRSWA_F16 or SRSWA_F32 */
 } srswa_fwd_args;
 
 int srswa_gather_fwd(const srswa_fwd_args* a, void* stream);
@@ -246,7 +248,7 @@ typedef struct {
   float* dbias;        int64_t db_sb, db_sh, db_st;    /* [B, HQ, T, S], slot stride 1; NULL = skip */
   int32_t B, T, Sk, HQ, HKV, HI, D, S, block_size, local_window;
   float scale;
-  int32_t dtype;
+  int32_t dtype;                                       /* as srswa_fwd_args (bf16, fp16, fp32) */
 } srswa_bwd_args;
 
 /* scratch bytes: delta [B, T, HQ] fp32 + q*scale [B, HQ, T, D] in the input

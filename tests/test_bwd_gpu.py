@@ -89,6 +89,31 @@ def test_bwd_matches_oracle(dev, name):
         assert_close_lowp(gt, rf, dt if nm != "dbias" else torch.float32, TOL, f"backward {name}: {nm}")
 
 
+F32_CASES = {
+    "f32_self_bs64": dict(B=1, HQ=2, HKV=2, HI=1, T=300, Sk=300, D=128, bs=64, lw=128, S=4),
+    "f32_packed_gqa_d64": dict(B=1, HQ=4, HKV=2, HI=1, T=257, Sk=257, D=64, bs=16, lw=40, S=3, packed=True),
+    "f32_bias_prefix": dict(B=1, HQ=2, HKV=1, HI=1, T=130, Sk=700, D=128, bs=32, lw=128, S=4, bias=True),
+}
+
+
+@pytest.mark.parametrize("name", list(F32_CASES))
+def test_bwd_fp32_matches_oracle(dev, name):
+    """fp32 operands on the fp32 MFMA form: every gradient (and the bias
+    gradient) within 1e-5 relative (max-abs error / max-abs reference) of fp64
+    autograd, the fp32 bar."""
+    c = dict(F32_CASES[name])
+    bs, lw = c["bs"], c["lw"]
+    q, k, v, do, bi, pos, bsl = _inputs(60 + list(F32_CASES).index(name), dtype=torch.float32, **c)
+    scale = 1 / math.sqrt(c["D"])
+    got = _gpu(dev, q, k, v, do, bi, pos, bsl, bs, lw, scale)
+    ref = _ref(q, k, v, do, bi, pos, bsl, bs, lw, scale)
+    from parity_report import report
+    for nm, gt, rf in zip(("dq", "dk", "dv", "dbias"), got, ref):
+        rel = (gt - rf).abs().max().item() / max(rf.abs().max().item(), 1e-30)
+        report(f"[err] backward fp32 {name}: {nm} max rel {rel:.3e} (bar 1e-5)")
+        assert rel <= 1e-5, (nm, rel)
+
+
 def test_bwd_is_deterministic(dev):
     c = dict(CASES["bias"])
     bs, lw = c["bs"], c["lw"]

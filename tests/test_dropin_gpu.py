@@ -35,9 +35,13 @@ def test_gather_attention_reference_layout_and_gates(dev):
     assert SG.triton_gather_attention(q.to(dev), k.to(dev), v.to(dev), bi.to(dev), None, None, bs, 0.1) is None
     bad_hi = torch.zeros(B, 3, T, 4, dtype=torch.long, device=dev)
     assert SG.triton_gather_attention(q.to(dev), k.to(dev), v.to(dev), bad_hi, pos.to(dev), None, bs, 0.1) is None
-    # fp32 is not a matrix-core dtype: None (the caller's eager fallback), never a CPU path
-    assert SG.triton_gather_attention(q.float().to(dev), k.float().to(dev), v.float().to(dev), bi.to(dev),
-                                      pos.to(dev), None, bs, 0.1) is None
+    # fp32 operands run on the fp32 matrix-core form (the reference kernels are
+    # dtype-generic): fp32 products and sums, within 1e-5 relative
+    out32 = SG.triton_gather_attention(q.float().to(dev), k.float().to(dev), v.float().to(dev), bi.to(dev),
+                                       pos.to(dev), None, bs, 1 / math.sqrt(D), local_window=lw)
+    assert out32 is not None and out32.dtype == torch.float32
+    ref32, _ = O.gather_attention(q.double(), k.double(), v.double(), bi, pos, bs, 1 / math.sqrt(D), lw)
+    assert (out32.cpu().double() - ref32).abs().max().item() <= 1e-5 * ref32.abs().max().item()
     assert SG.SPARSE_BLOCK_SIZE_SENTINEL == 128
 
 

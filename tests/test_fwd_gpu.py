@@ -77,6 +77,31 @@ def test_fwd_matches_oracle(dev, name):
     assert (lse - rl).abs().max().item() <= TOL
 
 
+F32_CASES = {
+    "f32_self_bs64": dict(B=2, HQ=2, HKV=2, HI=1, T=300, Sk=300, D=128, bs=64, lw=128, S=4),
+    "f32_prefix_bias": dict(B=1, HQ=2, HKV=1, HI=1, T=130, Sk=1000, D=128, bs=32, lw=256, S=5, bias=True),
+    "f32_packed_d64": dict(B=1, HQ=4, HKV=2, HI=2, T=257, Sk=257, D=64, bs=16, lw=40, S=3, packed=True),
+}
+
+
+@pytest.mark.parametrize("name", list(F32_CASES))
+def test_fwd_fp32_matches_oracle(dev, name):
+    """fp32 operands on v_mfma_f32_32x32x2_f32 (fp32 products and sums): relative
+    error of o and lse within 1e-5 of the fp64 oracle (the fp32 bar)."""
+    c = dict(F32_CASES[name])
+    bs, lw = c["bs"], c["lw"]
+    q, k, v, bi, pos, bias = _case(40 + list(F32_CASES).index(name), dtype=torch.float32, **c)
+    scale = 1 / math.sqrt(c["D"])
+    o, lse, ro, rl = _run(dev, q, k, v, bi, pos, bias, bs, lw, scale)
+    rel_o = (o - ro).abs().max().item() / ro.abs().max().item()
+    fin = torch.isfinite(rl)
+    assert torch.equal(torch.isfinite(lse), fin)
+    rel_l = (lse[fin] - rl[fin]).abs().max().item() / rl[fin].abs().max().item()
+    from parity_report import report
+    report(f"[err] forward fp32 {name}: o max rel {rel_o:.3e}, lse max rel {rel_l:.3e} (bar 1e-5)")
+    assert rel_o <= 1e-5 and rel_l <= 1e-5, (rel_o, rel_l)
+
+
 @pytest.mark.parametrize("name", ["self_bs64", "bias", "gqa_hi"])
 def test_tail_split_matches_whole_tiles(dev, name):
     """The tail split (a last round of tiles filling at most a fifth of the GPU

@@ -103,11 +103,13 @@ __global__ __launch_bounds__(256) void touch_kernel(BwdK p) {
 }
 
 // -------------------------------------------------------------- 2. dQ
-template <int D> struct DqLds {
-  static constexpr int KP = D + 16;   // K: row reads (S^T) and transposing reads (dQ)
-  static constexpr int VP = D + 8;    // V: row reads only
-  static constexpr int vOff = kChunk * KP * 2;
-  static constexpr int tileBytes = vOff + kChunk * VP * 2;
+// ES: element bytes (2, or 4 for fp32, whose K^T operand is read as scalars:
+// a 4-float pad keeps the lane halves' rows, 4 apart, on different banks)
+template <int D, int ES = 2> struct DqLds {
+  static constexpr int KP = ES == 4 ? D + 4 : D + 16;   // K: row reads (S^T) and K^T reads (dQ)
+  static constexpr int VP = ES == 4 ? D + 4 : D + 8;    // V: row reads only
+  static constexpr int vOff = kChunk * KP * ES;
+  static constexpr int tileBytes = vOff + kChunk * VP * ES;
 };
 
 // One workgroup = (sequence, query head, 64-row tile), two waves of 32 rows,
@@ -122,10 +124,15 @@ template <int D> struct DqLds {
 // are loaded at the top of its own iteration, and the co-resident workgroups'
 // waves cover the load latency (a one-chunk register prefetch needs 324
 // registers, one wave per SIMD, and is slower).  At D = 64 the prefetch fits.
+// The fp32 form (8 MFMAs per k step, twice the operand registers) runs one
+// wave per SIMD at D = 128, with the accumulators in the second register file.
 template <typename T, int D>
-__global__ __launch_bounds__(128, 2) void dq_kernel(BwdK p) {
+__global__ __launch_bounds__(128) __attribute__((amdgpu_waves_per_eu(std::is_same<T, float>::value && D == 128 ? 1 : 2)))
+void dq_kernel(BwdK p) {
+  constexpr bool F32 = std::is_same<T, float>::value;
+  constexpr uint32_t ES = sizeof(T);
   using M = Mfma<T>;
-  using L = DqLds<D>;
+  using L = DqLds<D, (int)sizeof(T)>;
   constexpr int KP = L::KP, VP = L::VP;
   constexpr int KS = D / 16, MT = D / 32, NT = 128;
   constexpr int PPT = kChunk * D / 8 / NT;
@@ -168,16 +175,16 @@ __global__ __launch_bounds__(128, 2) void dq_kernel(BwdK p) {
   const int row = wave * 32 + rl;
   const bool row_ok = row < nrows;
   const int trow = t0 + (row_ok ? row : 0);
-  uint4 qf[KS], gf[KS], of[KS];
+  Frag<T> qf[KS], gf[KS], of[KS];
   {
     const T* qrow = reinterpret_cast<const T*>(a.q) + (int64_t)b * a.q_sb + (int64_t)trow * a.q_st + (int64_t)hq * a.q_sh;
     const T* grow = reinterpret_cast<const T*>(a.dout) + (int64_t)b * a.do_sb + (int64_t)trow * a.do_st + (int64_t)hq * a.do_sh;
     const T* orow = reinterpret_cast<const T*>(a.o) + (int64_t)b * a.o_sb + (int64_t)trow * a.o_st + (int64_t)hq * a.o_sh;
 #pragma unroll
     for (int ks = 0; ks < KS; ++ks) {
-      qf[ks] = row_ok ? *reinterpret_cast<const uint4*>(qrow + 16 * ks + 8 * h) : make_uint4(0, 0, 0, 0);
-      gf[ks] = row_ok ? *reinterpret_cast<const uint4*>(grow + 16 * ks + 8 * h) : make_uint4(0, 0, 0, 0);
-      of[ks] = row_ok ? *reinterpret_cast<const uint4*>(orow + 16 * ks + 8 * h) : make_uint4(0, 0, 0, 0);
+      qf[ks] = row_ok ? *reinterpret_cast<const Frag<T>*>(qrow + 16 * ks + 8 * h) : Frag<T>{};
+      gf[ks] = row_ok ? *reinterpret_cast<const Frag<T>*>(grow + 16 * ks + 8 * h) : Frag<T>{};
+      of[ks] = row_ok ? *reinterpret_cast<const Frag<T>*>(orow + 16 * ks + 8 * h) : Frag<T>{};
     }
   }
   const float lse_l2 = row_ok ? a.lse[(int64_t)b * a.lse_sb + (int64_t)trow * a.lse_st + (int64_t)hq * a.lse_sh] * kLog2e
@@ -228,8 +235,13 @@ __global__ __launch_bounds__(128, 2) void dq_kernel(BwdK p) {
   for (int ks = 0; ks < KS; ++ks) {
     const uint32_t* o4 = reinterpret_cast<const uint32_t*>(&of[ks]);
     const uint32_t* g4 = reinterpret_cast<const uint32_t*>(&gf[ks]);
+    if constexpr (F32) {
 #pragma unroll
-    for (int e = 0; e < 4; ++e) dpart += M::lo(o4[e]) * M::lo(g4[e]) + M::hi(o4[e]) * M::hi(g4[e]);
+      for (int e = 0; e < 8; ++e) dpart += __uint_as_float(o4[e]) * __uint_as_float(g4[e]);
+    } else {
+#pragma unroll
+      for (int e = 0; e < 4; ++e) dpart += M::lo(o4[e]) * M::lo(g4[e]) + M::hi(o4[e]) * M::hi(g4[e]);
+    }
   }
   const float drow = xor32_sum(dpart);   // every lane of the pair is active
   const float dlt = row_ok ? drow : 0.f;
@@ -237,9 +249,14 @@ __global__ __launch_bounds__(128, 2) void dq_kernel(BwdK p) {
 #pragma unroll
   for (int ks = 0; ks < KS; ++ks) {
     uint32_t* xx = reinterpret_cast<uint32_t*>(&qf[ks]);
+    if constexpr (F32) {
 #pragma unroll
-    for (int e = 0; e < 4; ++e) xx[e] = M::pack2(M::lo(xx[e]) * a.scale, M::hi(xx[e]) * a.scale);
-    if (row_ok) *reinterpret_cast<uint4*>(qsrow + 16 * ks + 8 * h) = qf[ks];
+      for (int e = 0; e < 8; ++e) xx[e] = __float_as_uint(__uint_as_float(xx[e]) * a.scale);
+    } else {
+#pragma unroll
+      for (int e = 0; e < 4; ++e) xx[e] = M::pack2(M::lo(xx[e]) * a.scale, M::hi(xx[e]) * a.scale);
+    }
+    if (row_ok) *reinterpret_cast<Frag<T>*>(qsrow + 16 * ks + 8 * h) = qf[ks];
   }
   if (row_ok && h == 0) p.delta[((int64_t)b * a.T + trow) * a.HQ + hq] = dlt;
 
@@ -249,27 +266,34 @@ __global__ __launch_bounds__(128, 2) void dq_kernel(BwdK p) {
 
   const __amdgpu_buffer_rsrc_t krs = make_rsrc(
       reinterpret_cast<const T*>(a.k) + (int64_t)b * a.k_sb + (int64_t)kvh * a.k_sh,
-      (uint32_t)(((int64_t)(a.Sk - 1) * a.k_st + D) * 2));
+      (uint32_t)(((int64_t)(a.Sk - 1) * a.k_st + D) * ES));
   const __amdgpu_buffer_rsrc_t vrs = make_rsrc(
       reinterpret_cast<const T*>(a.v) + (int64_t)b * a.v_sb + (int64_t)kvh * a.v_sh,
-      (uint32_t)(((int64_t)(a.Sk - 1) * a.v_st + D) * 2));
-  const uint32_t kvo = (uint32_t)((tid / (D / 8)) * a.k_st + (tid % (D / 8)) * 8) * 2;
-  const uint32_t vvo = (uint32_t)((tid / (D / 8)) * a.v_st + (tid % (D / 8)) * 8) * 2;
+      (uint32_t)(((int64_t)(a.Sk - 1) * a.v_st + D) * ES));
+  const uint32_t kvo = (uint32_t)((tid / (D / 8)) * a.k_st + (tid % (D / 8)) * 8) * ES;
+  const uint32_t vvo = (uint32_t)((tid / (D / 8)) * a.v_st + (tid % (D / 8)) * 8) * ES;
   T* sKw = sK + (tid / (D / 8)) * KP + (tid % (D / 8)) * 8;
   T* sVw = sV + (tid / (D / 8)) * VP + (tid % (D / 8)) * 8;
-  uint4 kpre[PPT], vpre[PPT];
+  Frag<T> kpre[PPT], vpre[PPT];
   auto fetch = [&](int c) {
-    const uint32_t kso = (uint32_t)c * kChunk * (uint32_t)a.k_st * 2u;
-    const uint32_t vso = (uint32_t)c * kChunk * (uint32_t)a.v_st * 2u;
+    const uint32_t kso = (uint32_t)c * kChunk * (uint32_t)a.k_st * ES;
+    const uint32_t vso = (uint32_t)c * kChunk * (uint32_t)a.v_st * ES;
 #pragma unroll
     for (int i = 0; i < PPT; ++i) {
-      kpre[i] = buffer_load16(krs, kvo, kso + (uint32_t)(i * RPP) * (uint32_t)a.k_st * 2u);
-      vpre[i] = buffer_load16(vrs, vvo, vso + (uint32_t)(i * RPP) * (uint32_t)a.v_st * 2u);
+      if constexpr (F32) {     // both offsets in the lane part: the range check reads keys past Sk as zero
+        const uint32_t ko = kvo + kso + (uint32_t)(i * RPP) * (uint32_t)a.k_st * ES;
+        const uint32_t vo = vvo + vso + (uint32_t)(i * RPP) * (uint32_t)a.v_st * ES;
+        kpre[i] = Frag<T>{buffer_load16(krs, ko, 0), buffer_load16(krs, ko + 16, 0)};
+        vpre[i] = Frag<T>{buffer_load16(vrs, vo, 0), buffer_load16(vrs, vo + 16, 0)};
+      } else {
+        kpre[i] = buffer_load16(krs, kvo, kso + (uint32_t)(i * RPP) * (uint32_t)a.k_st * 2u);
+        vpre[i] = buffer_load16(vrs, vvo, vso + (uint32_t)(i * RPP) * (uint32_t)a.v_st * 2u);
+      }
     }
   };
   const uint16_t* k16 = reinterpret_cast<const uint16_t*>(sK);
 
-  constexpr bool kPrefetch = D < 128;
+  constexpr bool kPrefetch = D < 128 && !F32;   // fp32 at D = 64: the prefetch would spill
   if (kPrefetch && U > 0) fetch(s_chunks[0]);
   for (int u = 0; u < U; ++u) {
     const int j0 = (int)s_chunks[u] * kChunk;
@@ -277,8 +301,8 @@ __global__ __launch_bounds__(128, 2) void dq_kernel(BwdK p) {
     __syncthreads();   // previous chunk fully consumed
 #pragma unroll
     for (int i = 0; i < PPT; ++i) {
-      *reinterpret_cast<uint4*>(sKw + i * RPP * KP) = kpre[i];
-      *reinterpret_cast<uint4*>(sVw + i * RPP * VP) = vpre[i];
+      *reinterpret_cast<Frag<T>*>(sKw + i * RPP * KP) = kpre[i];
+      *reinterpret_cast<Frag<T>*>(sVw + i * RPP * VP) = vpre[i];
     }
     __syncthreads();
     if (kPrefetch && u + 1 < U) fetch(s_chunks[u + 1]);
@@ -292,14 +316,14 @@ __global__ __launch_bounds__(128, 2) void dq_kernel(BwdK p) {
       fast = __all(chunk_mask(w, j0, p.bs_shift, blk64, keep, rm, bq, qix));
     const float addb = (fast && w.sb && rm != 0ull) ? bq[0] : 0.f;
     float dsum[4] = {0.f, 0.f, 0.f, 0.f};
-    uint4 db[4];
+    Frag<T> db[4];
 #pragma unroll
     for (int half = 0; half < 2; ++half) {
       f32x16_t st = zero16(), dp = zero16();
 #pragma unroll
       for (int ks = 0; ks < KS; ++ks) {
-        st = M::mac(*reinterpret_cast<const uint4*>(sK + (32 * half + rl) * KP + 16 * ks + 8 * h), qf[ks], st);
-        dp = M::mac(*reinterpret_cast<const uint4*>(sV + (32 * half + rl) * VP + 16 * ks + 8 * h), gf[ks], dp);
+        st = M::mac(*reinterpret_cast<const Frag<T>*>(sK + (32 * half + rl) * KP + 16 * ks + 8 * h), qf[ks], st);
+        dp = M::mac(*reinterpret_cast<const Frag<T>*>(sV + (32 * half + rl) * VP + 16 * ks + 8 * h), gf[ks], dp);
       }
       if (fast) {
         const float sub = addb - lse_l2;
@@ -327,17 +351,30 @@ __global__ __launch_bounds__(128, 2) void dq_kernel(BwdK p) {
           if (remb) dsum[qq] += dsv;
         }
       }
-      db[2 * half] = make_uint4(M::pack2(st[0], st[1]), M::pack2(st[2], st[3]), M::pack2(st[4], st[5]),
-                                M::pack2(st[6], st[7]));
-      db[2 * half + 1] = make_uint4(M::pack2(st[8], st[9]), M::pack2(st[10], st[11]), M::pack2(st[12], st[13]),
-                                    M::pack2(st[14], st[15]));
+      if constexpr (F32) {
+        float v[16];
+#pragma unroll
+        for (int r = 0; r < 16; ++r) v[r] = st[r];
+        db[2 * half] = f32x8(v);
+        db[2 * half + 1] = f32x8(v + 8);
+      } else {
+        db[2 * half] = make_uint4(M::pack2(st[0], st[1]), M::pack2(st[2], st[3]), M::pack2(st[4], st[5]),
+                                  M::pack2(st[6], st[7]));
+        db[2 * half + 1] = make_uint4(M::pack2(st[8], st[9]), M::pack2(st[10], st[11]), M::pack2(st[12], st[13]),
+                                      M::pack2(st[14], st[15]));
+      }
     }
     // dQ^T += K^T dS^T (k-step outer: MT interleaved accumulator chains)
 #pragma unroll
     for (int ks = 0; ks < 4; ++ks) {
-      uint4 ka[MT];
+      Frag<T> ka[MT];
 #pragma unroll
-      for (int mt = 0; mt < MT; ++mt) ka[mt] = a_operand_tr<KP>(k16, 16 * ks, 32 * mt, lane);
+      for (int mt = 0; mt < MT; ++mt) {
+        if constexpr (F32)
+          ka[mt] = a_operand_f32<KP>(reinterpret_cast<const float*>(sK), 16 * ks, 32 * mt, lane);
+        else
+          ka[mt] = a_operand_tr<KP>(k16, 16 * ks, 32 * mt, lane);
+      }
 #pragma unroll
       for (int mt = 0; mt < MT; ++mt) dq[mt] = M::mac(ka[mt], db[ks], dq[mt]);
     }
@@ -358,10 +395,15 @@ __global__ __launch_bounds__(128, 2) void dq_kernel(BwdK p) {
 #pragma unroll
       for (int g = 0; g < 4; ++g) {
         const int d0 = 32 * mt + 8 * g + 4 * h;
-        uint2 x;
-        x.x = M::pack2(dq[mt][4 * g] * a.scale, dq[mt][4 * g + 1] * a.scale);
-        x.y = M::pack2(dq[mt][4 * g + 2] * a.scale, dq[mt][4 * g + 3] * a.scale);
-        *reinterpret_cast<uint2*>(qrow + d0) = x;
+        if constexpr (F32) {
+          *reinterpret_cast<float4*>(qrow + d0) = make_float4(dq[mt][4 * g] * a.scale, dq[mt][4 * g + 1] * a.scale,
+                                                              dq[mt][4 * g + 2] * a.scale, dq[mt][4 * g + 3] * a.scale);
+        } else {
+          uint2 x;
+          x.x = M::pack2(dq[mt][4 * g] * a.scale, dq[mt][4 * g + 1] * a.scale);
+          x.y = M::pack2(dq[mt][4 * g + 2] * a.scale, dq[mt][4 * g + 3] * a.scale);
+          *reinterpret_cast<uint2*>(qrow + d0) = x;
+        }
       }
   }
   if (s_sdb) {
@@ -394,9 +436,10 @@ constexpr int kPreSlots = 8;          // selected ids per row fetched one visit 
 // dK (B).  A lane
 // holds the same (row, key) elements in both roles (the same MFMA shape), so
 // role B reads role A's P lane for lane.
-template <int D> struct DkvLds {
-  static constexpr int QP = D + 16;                 // Q / dO tiles: row reads and transposing reads
-  static constexpr int gOff = kTileRows * QP * 2;   // dO tile
+template <int D, int ES = 2> struct DkvLds {
+  // Q / dO tiles: row reads and transposed (fp32: scalar) reads
+  static constexpr int QP = ES == 4 ? D + 4 : D + 16;
+  static constexpr int gOff = kTileRows * QP * ES;  // dO tile
   static constexpr int pOff = 2 * gOff;             // P: [key half][8 x float4][64 lanes]
   static constexpr int rowOff = pOff + 2 * 8 * 64 * 16;
   // one row-data buffer: lse[64], delta[64], keep[2][64], remote[2][64] (32-bit
@@ -406,9 +449,12 @@ template <int D> struct DkvLds {
 };
 
 template <typename T, int D>
-__global__ __launch_bounds__(256, 2) void dkv_kernel(BwdK p) {
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(std::is_same<T, float>::value && D == 128 ? 1 : 2)))
+void dkv_kernel(BwdK p) {
+  constexpr bool F32 = std::is_same<T, float>::value;   // fp32: one wave per SIMD at D = 128
+  constexpr uint32_t ES = sizeof(T);
   using M = Mfma<T>;
-  using L = DkvLds<D>;
+  using L = DkvLds<D, (int)sizeof(T)>;
   constexpr int QP = L::QP;
   constexpr int KS = D / 16, MT = D / 32, NT = 256;
   constexpr int PPT = kTileRows * D / 8 / NT;
@@ -450,7 +496,7 @@ __global__ __launch_bounds__(256, 2) void dkv_kernel(BwdK p) {
   const bool one_blk = ((j0 + kChunk - 1) >> p.bs_shift) == qb0;   // block size >= 64
 
   // role A: K of this lane's key; role B: V
-  uint4 kv[KS];
+  Frag<T> kv[KS];
   {
     const T* base = role == 0 ? reinterpret_cast<const T*>(a.k) + (int64_t)b * a.k_sb + (int64_t)kvh * a.k_sh
                               : reinterpret_cast<const T*>(a.v) + (int64_t)b * a.v_sb + (int64_t)kvh * a.v_sh;
@@ -458,7 +504,7 @@ __global__ __launch_bounds__(256, 2) void dkv_kernel(BwdK p) {
     const T* row = base + (int64_t)(key_ok ? jmine : 0) * st;
 #pragma unroll
     for (int ks = 0; ks < KS; ++ks)
-      kv[ks] = key_ok ? *reinterpret_cast<const uint4*>(row + 16 * ks + 8 * h) : make_uint4(0, 0, 0, 0);
+      kv[ks] = key_ok ? *reinterpret_cast<const Frag<T>*>(row + 16 * ks + 8 * h) : Frag<T>{};
   }
   f32x16_t acc[MT];                            // role A: dV^T, role B: dK^T
 #pragma unroll
@@ -475,9 +521,10 @@ __global__ __launch_bounds__(256, 2) void dkv_kernel(BwdK p) {
   const uint16_t* g16 = reinterpret_cast<const uint16_t*>(sG);
   const T* sX = role == 0 ? sQ : sG;           // the row operand of S (A) / dP (B)
   const uint16_t* x16 = role == 0 ? g16 : q16; // the transposed operand of dV (A) / dK (B)
+  const float* x32 = reinterpret_cast<const float*>(role == 0 ? sG : sQ);   // the same, fp32
   float4* sPl = sP + kh * 8 * 64 + lane;       // this lane's P records
   __shared__ int s_ntiles;
-  uint4 qpre[PPT], gpre[PPT];
+  Frag<T> qpre[PPT], gpre[PPT];
 
   for (int gq = 0; gq < p.G; ++gq) {
     const int hq = kvh * p.G + gq;
@@ -502,19 +549,26 @@ __global__ __launch_bounds__(256, 2) void dkv_kernel(BwdK p) {
     const int nt = s_ntiles;
     // the scaled query written by the dQ kernel ([T, D] rows of this head), dO as given
     const __amdgpu_buffer_rsrc_t qrs = make_rsrc(
-        reinterpret_cast<const T*>(p.qs) + ((int64_t)b * a.HQ + hq) * a.T * D, (uint32_t)((int64_t)a.T * D * 2));
+        reinterpret_cast<const T*>(p.qs) + ((int64_t)b * a.HQ + hq) * a.T * D, (uint32_t)((int64_t)a.T * D * ES));
     const __amdgpu_buffer_rsrc_t grs = make_rsrc(
         reinterpret_cast<const T*>(a.dout) + (int64_t)b * a.do_sb + (int64_t)hq * a.do_sh,
-        (uint32_t)(((int64_t)(a.T - 1) * a.do_st + D) * 2));
-    const uint32_t qvo = (uint32_t)((tid / (D / 8)) * D + (tid % (D / 8)) * 8) * 2;
-    const uint32_t gvo = (uint32_t)((tid / (D / 8)) * a.do_st + (tid % (D / 8)) * 8) * 2;
+        (uint32_t)(((int64_t)(a.T - 1) * a.do_st + D) * ES));
+    const uint32_t qvo = (uint32_t)((tid / (D / 8)) * D + (tid % (D / 8)) * 8) * ES;
+    const uint32_t gvo = (uint32_t)((tid / (D / 8)) * a.do_st + (tid % (D / 8)) * 8) * ES;
     auto fetch = [&](int tau) {
-      const uint32_t qso = (uint32_t)tau * kTileRows * (uint32_t)D * 2u;
-      const uint32_t gso = (uint32_t)tau * kTileRows * (uint32_t)a.do_st * 2u;
+      const uint32_t qso = (uint32_t)tau * kTileRows * (uint32_t)D * ES;
+      const uint32_t gso = (uint32_t)tau * kTileRows * (uint32_t)a.do_st * ES;
 #pragma unroll
       for (int i = 0; i < PPT; ++i) {
-        qpre[i] = buffer_load16(qrs, qvo, qso + (uint32_t)(i * RPP) * (uint32_t)D * 2u);
-        gpre[i] = buffer_load16(grs, gvo, gso + (uint32_t)(i * RPP) * (uint32_t)a.do_st * 2u);
+        if constexpr (F32) {   // both offsets in the lane part: rows past T read as zero
+          const uint32_t qo = qvo + qso + (uint32_t)(i * RPP) * (uint32_t)D * ES;
+          const uint32_t go = gvo + gso + (uint32_t)(i * RPP) * (uint32_t)a.do_st * ES;
+          qpre[i] = Frag<T>{buffer_load16(qrs, qo, 0), buffer_load16(qrs, qo + 16, 0)};
+          gpre[i] = Frag<T>{buffer_load16(grs, go, 0), buffer_load16(grs, go + 16, 0)};
+        } else {
+          qpre[i] = buffer_load16(qrs, qvo, qso + (uint32_t)(i * RPP) * (uint32_t)D * 2u);
+          gpre[i] = buffer_load16(grs, gvo, gso + (uint32_t)(i * RPP) * (uint32_t)a.do_st * 2u);
+        }
       }
     };
     // row data of a tile for the mask wave (lane = row): sample start, lse
@@ -626,8 +680,8 @@ __global__ __launch_bounds__(256, 2) void dkv_kernel(BwdK p) {
       __syncthreads();   // previous tile consumed (Q, dO, P); this visit's row data written
 #pragma unroll
       for (int i = 0; i < PPT; ++i) {
-        *reinterpret_cast<uint4*>(sQw + i * RPP * QP) = qpre[i];
-        *reinterpret_cast<uint4*>(sGw + i * RPP * QP) = gpre[i];
+        *reinterpret_cast<Frag<T>*>(sQw + i * RPP * QP) = qpre[i];
+        *reinterpret_cast<Frag<T>*>(sGw + i * RPP * QP) = gpre[i];
       }
       if (it + 1 < nt) fetch(s_tiles[it + 1]);
       __syncthreads();
@@ -639,7 +693,7 @@ __global__ __launch_bounds__(256, 2) void dkv_kernel(BwdK p) {
       for (int ks = 0; ks < KS; ++ks) {
 #pragma unroll
         for (int half = 0; half < 2; ++half)
-          sg[half] = M::mac(*reinterpret_cast<const uint4*>(sX + (32 * half + rl) * QP + 16 * ks + 8 * h), kv[ks], sg[half]);
+          sg[half] = M::mac(*reinterpret_cast<const Frag<T>*>(sX + (32 * half + rl) * QP + 16 * ks + 8 * h), kv[ks], sg[half]);
       }
       if (role == 0) {
         const bool fast = s_flag(buf)[0] != 0;
@@ -727,20 +781,32 @@ __global__ __launch_bounds__(256, 2) void dkv_kernel(BwdK p) {
             for (int e = 0; e < 4; ++e) sg[half][4 * r4 + e] = pv[e] * (sg[half][4 * r4 + e] - dv4[e]);
           }
       }
-      uint4 pk[4];
+      Frag<T> pk[4];
 #pragma unroll
       for (int ks = 0; ks < 4; ++ks) {
         const int hf = ks >> 1, r0 = 8 * (ks & 1);
-        pk[ks] = make_uint4(M::pack2(sg[hf][r0], sg[hf][r0 + 1]), M::pack2(sg[hf][r0 + 2], sg[hf][r0 + 3]),
-                            M::pack2(sg[hf][r0 + 4], sg[hf][r0 + 5]), M::pack2(sg[hf][r0 + 6], sg[hf][r0 + 7]));
+        if constexpr (F32) {
+          float v[8];
+#pragma unroll
+          for (int j = 0; j < 8; ++j) v[j] = sg[hf][r0 + j];
+          pk[ks] = f32x8(v);
+        } else {
+          pk[ks] = make_uint4(M::pack2(sg[hf][r0], sg[hf][r0 + 1]), M::pack2(sg[hf][r0 + 2], sg[hf][r0 + 3]),
+                              M::pack2(sg[hf][r0 + 4], sg[hf][r0 + 5]), M::pack2(sg[hf][r0 + 6], sg[hf][r0 + 7]));
+        }
       }
       // A: dV^T += dO^T P; B: dK^T += (q*scale)^T dS (k-step outer, a step's
       // operands read before its MFMAs)
 #pragma unroll
       for (int ks = 0; ks < 4; ++ks) {
-        uint4 xa[MT];
+        Frag<T> xa[MT];
 #pragma unroll
-        for (int mt = 0; mt < MT; ++mt) xa[mt] = a_operand_tr<QP>(x16, 16 * ks, 32 * mt, lane);
+        for (int mt = 0; mt < MT; ++mt) {
+          if constexpr (F32)
+            xa[mt] = a_operand_f32<QP>(x32, 16 * ks, 32 * mt, lane);
+          else
+            xa[mt] = a_operand_tr<QP>(x16, 16 * ks, 32 * mt, lane);
+        }
 #pragma unroll
         for (int mt = 0; mt < MT; ++mt) acc[mt] = M::mac(xa[mt], pk[ks], acc[mt]);
       }
@@ -756,10 +822,15 @@ __global__ __launch_bounds__(256, 2) void dkv_kernel(BwdK p) {
 #pragma unroll
     for (int g = 0; g < 4; ++g) {
       const int d0 = 32 * mt + 8 * g + 4 * h;
-      uint2 w;
-      w.x = M::pack2(acc[mt][4 * g], acc[mt][4 * g + 1]);
-      w.y = M::pack2(acc[mt][4 * g + 2], acc[mt][4 * g + 3]);
-      *reinterpret_cast<uint2*>(out + d0) = w;
+      if constexpr (F32) {
+        *reinterpret_cast<float4*>(out + d0) =
+            make_float4(acc[mt][4 * g], acc[mt][4 * g + 1], acc[mt][4 * g + 2], acc[mt][4 * g + 3]);
+      } else {
+        uint2 w;
+        w.x = M::pack2(acc[mt][4 * g], acc[mt][4 * g + 1]);
+        w.y = M::pack2(acc[mt][4 * g + 2], acc[mt][4 * g + 3]);
+        *reinterpret_cast<uint2*>(out + d0) = w;
+      }
     }
 }
 
@@ -781,10 +852,11 @@ int check_bwd(const srswa_bwd_args* a) {
     set_error("bwd: HQ must be a multiple of HKV and HI");
     return SRSWA_UNSUPPORTED;
   }
-  if (a->dtype != SRSWA_BF16 && a->dtype != SRSWA_F16) {
-    set_error("bwd: matrix-core path takes bf16 / fp16");
+  if (a->dtype != SRSWA_BF16 && a->dtype != SRSWA_F16 && a->dtype != SRSWA_F32) {
+    set_error("bwd: dtype %d not supported (bf16, fp16, fp32)", a->dtype);
     return SRSWA_UNSUPPORTED;
   }
+  const int es = a->dtype == SRSWA_F32 ? 4 : 2;   // element bytes
   if (!(a->D == 64 || a->D == 128) || a->block_size < 16 || (a->block_size & (a->block_size - 1)) || a->S > 64) {
     set_error("bwd: D in {64,128}, block size a power of two >= 16, <= 64 slots");
     return SRSWA_UNSUPPORTED;
@@ -797,8 +869,8 @@ int check_bwd(const srswa_bwd_args* a) {
     set_error("bwd: key length above 4M");
     return SRSWA_UNSUPPORTED;
   }
-  const int64_t span = ((int64_t)ceil_div(a->Sk, kChunk) * kChunk * std::max(a->k_st, a->v_st) + a->D) * 2;
-  const int64_t qspan = ((int64_t)ceil_div(a->T, kTileRows) * kTileRows * std::max(a->q_st, a->do_st) + a->D) * 2;
+  const int64_t span = ((int64_t)ceil_div(a->Sk, kChunk) * kChunk * std::max(a->k_st, a->v_st) + a->D) * es;
+  const int64_t qspan = ((int64_t)ceil_div(a->T, kTileRows) * kTileRows * std::max(a->q_st, a->do_st) + a->D) * es;
   if (span >= ((int64_t)1 << 32) || qspan >= ((int64_t)1 << 32)) {
     set_error("bwd: one sequence's tensors span 4 GiB or more");
     return SRSWA_UNSUPPORTED;
@@ -807,7 +879,7 @@ int check_bwd(const srswa_bwd_args* a) {
                         a->o_sb, a->o_st, a->o_sh, a->do_sb, a->do_st, a->do_sh, a->dq_sb, a->dq_st,
                         a->dq_sh, a->dk_sb, a->dk_st, a->dk_sh, a->dv_sb, a->dv_st, a->dv_sh};
   for (int64_t s : st)
-    if ((s * 2) % 16) {
+    if ((s * es) % 16) {
       set_error("bwd: rows must be 16-byte aligned");
       return SRSWA_UNSUPPORTED;
     }
@@ -839,7 +911,9 @@ void plan_bwd(const srswa_bwd_args* a, BwdK& k) {
   k.per_xcd_kv = ceil_div(k.nlogical_kv, 8);
   // dQ LDS: K / V tiles (the set-up arrays alias them), chunk list, sorted ids
   // (+ bias, + slot map and bias-gradient sums)
-  const size_t tile = a->D == 128 ? DqLds<128>::tileBytes : DqLds<64>::tileBytes;
+  const bool f32 = a->dtype == SRSWA_F32;
+  const size_t tile = a->D == 128 ? (f32 ? DqLds<128, 4>::tileBytes : DqLds<128>::tileBytes)
+                                  : (f32 ? DqLds<64, 4>::tileBytes : DqLds<64>::tileBytes);
   const size_t setup = (3 * 64 + 4) * 4 + (size_t)k.nwords * 4;
   size_t n = std::max(tile, setup);
   k.chunks_off = (int)n;
@@ -851,7 +925,10 @@ size_t delta_bytes(const BwdK& k) {
   return ((size_t)k.a.B * k.a.T * k.a.HQ * 4 + 255) / 256 * 256;
 }
 size_t touch_words(const BwdK& k) { return (size_t)k.a.B * k.a.HI * k.nchunk * k.twords; }
-size_t qs_bytes(const BwdK& k) { return ((size_t)k.a.B * k.a.HQ * k.a.T * k.a.D * 2 + 255) / 256 * 256; }
+size_t qs_bytes(const BwdK& k) {
+  const size_t es = k.a.dtype == SRSWA_F32 ? 4 : 2;
+  return ((size_t)k.a.B * k.a.HQ * k.a.T * k.a.D * es + 255) / 256 * 256;
+}
 
 size_t dq_smem(const BwdK& k) {
   const size_t n = (size_t)k.sid_off + (size_t)64 * k.SP * 4 * (1 + (k.a.bias ? 1 : 0) + (k.a.dbias ? 2 : 0));
@@ -859,7 +936,9 @@ size_t dq_smem(const BwdK& k) {
 }
 
 size_t dkv_smem(const BwdK& k) {
-  const size_t fixed = k.a.D == 128 ? DkvLds<128>::fixedBytes : DkvLds<64>::fixedBytes;  // + visit list
+  const bool f32 = k.a.dtype == SRSWA_F32;
+  const size_t fixed = k.a.D == 128 ? (f32 ? DkvLds<128, 4>::fixedBytes : DkvLds<128>::fixedBytes)
+                                    : (f32 ? DkvLds<64, 4>::fixedBytes : DkvLds<64>::fixedBytes);  // + visit list
   return (fixed + (size_t)k.ntiles * 4 + 15) / 16 * 16;
 }
 
@@ -916,6 +995,8 @@ extern "C" int srswa_gather_bwd(const srswa_bwd_args* a, void* scratch, size_t s
   k.qs = reinterpret_cast<char*>(scratch) + delta_bytes(k);
   k.touch = reinterpret_cast<uint32_t*>(reinterpret_cast<char*>(scratch) + delta_bytes(k) + qs_bytes(k));
   hipStream_t s = reinterpret_cast<hipStream_t>(stream);
+  if (a->dtype == SRSWA_F32)
+    return a->D == 128 ? launch_bwd<float, 128>(k, s) : launch_bwd<float, 64>(k, s);
   if (a->dtype == SRSWA_BF16)
     return a->D == 128 ? launch_bwd<bf16_t, 128>(k, s) : launch_bwd<bf16_t, 64>(k, s);
   return a->D == 128 ? launch_bwd<__half, 128>(k, s) : launch_bwd<__half, 64>(k, s);

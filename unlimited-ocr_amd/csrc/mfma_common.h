@@ -48,6 +48,49 @@ template <> struct Mfma<__half> {
   __device__ __forceinline__ static float hi(uint32_t w) { return h16_hi(w); }
 };
 
+// fp32 operands: a lane's 8 values (two 16-byte words) feed eight
+// v_mfma_f32_32x32x2_f32, value j of lane half h being that product's k index
+// h.  Both operands list their 8 values in one key order, so the eight
+// products together sum the 16 k of a bf16 / fp16 step, in fp32 throughout.
+struct F32x8 {
+  uint4 lo, hi;
+};
+template <> struct Mfma<float> {
+  __device__ __forceinline__ static f32x16_t mac(const F32x8& a, const F32x8& b, f32x16_t c) {
+    c = __builtin_amdgcn_mfma_f32_32x32x2f32(__uint_as_float(a.lo.x), __uint_as_float(b.lo.x), c, 0, 0, 0);
+    c = __builtin_amdgcn_mfma_f32_32x32x2f32(__uint_as_float(a.lo.y), __uint_as_float(b.lo.y), c, 0, 0, 0);
+    c = __builtin_amdgcn_mfma_f32_32x32x2f32(__uint_as_float(a.lo.z), __uint_as_float(b.lo.z), c, 0, 0, 0);
+    c = __builtin_amdgcn_mfma_f32_32x32x2f32(__uint_as_float(a.lo.w), __uint_as_float(b.lo.w), c, 0, 0, 0);
+    c = __builtin_amdgcn_mfma_f32_32x32x2f32(__uint_as_float(a.hi.x), __uint_as_float(b.hi.x), c, 0, 0, 0);
+    c = __builtin_amdgcn_mfma_f32_32x32x2f32(__uint_as_float(a.hi.y), __uint_as_float(b.hi.y), c, 0, 0, 0);
+    c = __builtin_amdgcn_mfma_f32_32x32x2f32(__uint_as_float(a.hi.z), __uint_as_float(b.hi.z), c, 0, 0, 0);
+    return __builtin_amdgcn_mfma_f32_32x32x2f32(__uint_as_float(a.hi.w), __uint_as_float(b.hi.w), c, 0, 0, 0);
+  }
+};
+// a lane's operand fragment of one 16-wide k step: 8 values of T
+template <typename T> using Frag = std::conditional_t<std::is_same<T, float>::value, F32x8, uint4>;
+__device__ __forceinline__ F32x8 f32x8(const float* v) {
+  return F32x8{make_uint4(__float_as_uint(v[0]), __float_as_uint(v[1]), __float_as_uint(v[2]), __float_as_uint(v[3])),
+               make_uint4(__float_as_uint(v[4]), __float_as_uint(v[5]), __float_as_uint(v[6]), __float_as_uint(v[7]))};
+}
+
+// The fp32 A operand X^T (M = feature d, K = 16 rows of X) in the key order of
+// the MFMA output rows that form the B operand: lane (d = l % 32, h) value j
+// is X[r0 + 4h + j][c0 + d] for j < 4 and X[r0 + 8 + 4h + (j - 4)][c0 + d]
+// after (the order a_operand_tr gives the 16-bit forms), read as scalars.
+template <int PITCH>
+__device__ __forceinline__ F32x8 a_operand_f32(const float* x, int r0, int c0, int lane) {
+  const int d = lane & 31, h = lane >> 5;
+  const float* p = x + (r0 + 4 * h) * PITCH + c0 + d;
+  float v[8];
+#pragma unroll
+  for (int e = 0; e < 4; ++e) {
+    v[e] = p[e * PITCH];
+    v[4 + e] = p[(8 + e) * PITCH];
+  }
+  return f32x8(v);
+}
+
 // Raw buffer loads (gfx9 buffer resource, byte offsets): one 32-bit lane
 // offset plus a scalar offset per load instead of a 64-bit address per load,
 // and a hardware range check -- bytes at or beyond `bytes` read as zero.

@@ -71,21 +71,29 @@ struct FwdK {
   float* part;                 // [ntail * nsplit][64 * D + 128]
 };
 
-template <int D> struct FwdLds {
-  static constexpr int KP = D + 8;    // K row pitch (elements): conflict-free 16-byte row reads
-  static constexpr int VP = D + 16;   // V row pitch: conflict-free transposing reads
+// ES: element bytes (2, or 4 for fp32, whose V^T operand is read as scalars:
+// a 4-float pad keeps the two lane halves' rows, 4 apart, on different banks)
+template <int D, int ES = 2> struct FwdLds {
+  static constexpr int KP = D + 8;                  // K row pitch (elements): conflict-free row reads
+  static constexpr int VP = ES == 4 ? D + 4 : D + 16;   // V row pitch: conflict-free V^T reads
   static constexpr int kOff = 0;
-  static constexpr int vOff = kChunk * KP * 2;
-  static constexpr int tileBytes = vOff + kChunk * VP * 2;
+  static constexpr int vOff = kChunk * KP * ES;
+  static constexpr int tileBytes = vOff + kChunk * VP * ES;
 };
 
+// Two waves per SIMD; the fp32 form at D = 128 (twice the operand registers)
+// one, with the accumulators in the second register file.
 template <typename T, int D, bool PAGED, bool FP8 = false>
-__global__ __launch_bounds__(128, 2) void fwd_kernel(FwdK p) {
+__global__ __launch_bounds__(128) __attribute__((amdgpu_waves_per_eu(std::is_same<T, float>::value && D == 128 ? 1 : 2)))
+void fwd_kernel(FwdK p) {
   static_assert(!FP8 || PAGED, "fp8 caches: the paged form");
+  constexpr bool F32 = std::is_same<T, float>::value;   // fp32: the unpaged form, 8 MFMAs per k step
+  static_assert(!F32 || !PAGED, "fp32: the unpaged form");
   using KE = std::conditional_t<FP8, uint8_t, T>;   // cache element
-  using Pre = std::conditional_t<FP8, uint2, uint4>;  // a staged piece: 8 cache elements
+  // a staged piece: 8 cache elements
+  using Pre = std::conditional_t<FP8, uint2, Frag<T>>;
   using M = Mfma<T>;
-  using L = FwdLds<D>;
+  using L = FwdLds<D, (int)sizeof(T)>;
   constexpr int KP = L::KP, VP = L::VP;
   constexpr int KS = D / 16;         // k-steps over the head dim
   constexpr int MT = D / 32;         // 32-row tiles of O^T
@@ -150,13 +158,13 @@ __global__ __launch_bounds__(128, 2) void fwd_kernel(FwdK p) {
   // this lane's query row, loaded first so its latency overlaps the set-up
   const int row = wave * 32 + rl;
   const bool row_ok = row < nrows;
-  uint4 qf[KS];
+  Frag<T> qf[KS];
   {
     const T* qrow = reinterpret_cast<const T*>(a.q) + (int64_t)b * a.q_sb +
                     (int64_t)(q0 + t0 + (row_ok ? row : 0)) * a.q_st + (int64_t)hq * a.q_sh;
 #pragma unroll
     for (int ks = 0; ks < KS; ++ks)
-      qf[ks] = row_ok ? *reinterpret_cast<const uint4*>(qrow + 16 * ks + 8 * h) : make_uint4(0, 0, 0, 0);
+      qf[ks] = row_ok ? *reinterpret_cast<const Frag<T>*>(qrow + 16 * ks + 8 * h) : Frag<T>{};
   }
 
   if (tid < 64) {
@@ -211,7 +219,15 @@ __global__ __launch_bounds__(128, 2) void fwd_kernel(FwdK p) {
   const float inv_l2s = PAGED ? 1.f / a.scale * kLn2 : kLn2;
 
 
-  if constexpr (!PAGED) {
+  if constexpr (F32) {
+    // fp32: q * scale, each product rounded once (as the reference's fp32 q * scale)
+#pragma unroll
+    for (int ks = 0; ks < KS; ++ks) {
+      uint32_t* ww = reinterpret_cast<uint32_t*>(&qf[ks]);
+#pragma unroll
+      for (int e = 0; e < 8; ++e) ww[e] = __float_as_uint(__uint_as_float(ww[e]) * a.scale);
+    }
+  } else if constexpr (!PAGED) {
 #pragma unroll
     for (int ks = 0; ks < KS; ++ks) {
       uint32_t* ww = reinterpret_cast<uint32_t*>(&qf[ks]);
@@ -228,15 +244,16 @@ __global__ __launch_bounds__(128, 2) void fwd_kernel(FwdK p) {
 
   // K / V of this (sequence, kv head) as buffer resources ending at key Sk - 1
   // (keys of a chunk beyond Sk read as zero)
+  constexpr uint32_t ES = sizeof(T);
   const __amdgpu_buffer_rsrc_t krs = make_rsrc(
       reinterpret_cast<const T*>(a.k) + (int64_t)b * a.k_sb + (int64_t)kvh * a.k_sh,
-      (uint32_t)(((int64_t)(a.Sk - 1) * a.k_st + D) * 2));
+      (uint32_t)(((int64_t)(a.Sk - 1) * a.k_st + D) * ES));
   const __amdgpu_buffer_rsrc_t vrs = make_rsrc(
       reinterpret_cast<const T*>(a.v) + (int64_t)b * a.v_sb + (int64_t)kvh * a.v_sh,
-      (uint32_t)(((int64_t)(a.Sk - 1) * a.v_st + D) * 2));
+      (uint32_t)(((int64_t)(a.Sk - 1) * a.v_st + D) * ES));
   constexpr int RPP = NT / (D / 8);            // rows per pass of the 128 threads
-  const uint32_t kvo = (uint32_t)((tid / (D / 8)) * a.k_st + (tid % (D / 8)) * 8) * 2;
-  const uint32_t vvo = (uint32_t)((tid / (D / 8)) * a.v_st + (tid % (D / 8)) * 8) * 2;
+  const uint32_t kvo = (uint32_t)((tid / (D / 8)) * a.k_st + (tid % (D / 8)) * 8) * ES;
+  const uint32_t vvo = (uint32_t)((tid / (D / 8)) * a.v_st + (tid % (D / 8)) * 8) * ES;
   // this thread's 16-byte piece of the first staged row; later pieces are RPP rows apart
   T* sKw = sK + (tid / (D / 8)) * KP + (tid % (D / 8)) * 8;
   T* sVw = sV + (tid / (D / 8)) * VP + (tid % (D / 8)) * 8;
@@ -278,13 +295,22 @@ __global__ __launch_bounds__(128, 2) void fwd_kernel(FwdK p) {
         if (j < Skb) {
           kpre[i] = *reinterpret_cast<const Pre*>(kb + (jr * (uint32_t)a.k_st * (uint32_t)sizeof(KE) + col_b));
           vpre[i] = *reinterpret_cast<const Pre*>(vb + (jr * (uint32_t)a.v_st * (uint32_t)sizeof(KE) + col_b));
-        } else if constexpr (FP8) {
-          kpre[i] = make_uint2(0, 0);
-          vpre[i] = make_uint2(0, 0);
         } else {
-          kpre[i] = make_uint4(0, 0, 0, 0);
-          vpre[i] = make_uint4(0, 0, 0, 0);
+          kpre[i] = Pre{};
+          vpre[i] = Pre{};
         }
+      }
+    } else if constexpr (F32) {
+      // two 16-byte words per 8-float piece, both offsets in the lane part
+      // (the buffer range check reads keys past Sk as zero)
+      const uint32_t kso = (uint32_t)c * kChunk * (uint32_t)a.k_st * ES;
+      const uint32_t vso = (uint32_t)c * kChunk * (uint32_t)a.v_st * ES;
+#pragma unroll
+      for (int i = 0; i < PPT; ++i) {
+        const uint32_t ko = kvo + kso + (uint32_t)(i * RPP) * (uint32_t)a.k_st * ES;
+        const uint32_t vo = vvo + vso + (uint32_t)(i * RPP) * (uint32_t)a.v_st * ES;
+        kpre[i] = Pre{buffer_load16(krs, ko, 0), buffer_load16(krs, ko + 16, 0)};
+        vpre[i] = Pre{buffer_load16(vrs, vo, 0), buffer_load16(vrs, vo + 16, 0)};
       }
     } else if constexpr (!FP8) {
       const uint32_t kso = (uint32_t)c * kChunk * (uint32_t)a.k_st * 2u;
@@ -328,8 +354,8 @@ __global__ __launch_bounds__(128, 2) void fwd_kernel(FwdK p) {
     } else {
 #pragma unroll
       for (int i = 0; i < PPT; ++i) {
-        *reinterpret_cast<uint4*>(sKw + i * RPP * KP) = kpre[i];
-        *reinterpret_cast<uint4*>(sVw + i * RPP * VP) = vpre[i];
+        *reinterpret_cast<Pre*>(sKw + i * RPP * KP) = kpre[i];
+        *reinterpret_cast<Pre*>(sVw + i * RPP * VP) = vpre[i];
       }
     }
     __syncthreads();
@@ -343,8 +369,8 @@ __global__ __launch_bounds__(128, 2) void fwd_kernel(FwdK p) {
     __builtin_amdgcn_s_setprio(1);
 #pragma unroll
     for (int ks = 0; ks < KS; ++ks) {
-      const uint4 a0 = *reinterpret_cast<const uint4*>(sK + rl * KP + 16 * ks + 8 * h);
-      const uint4 a1 = *reinterpret_cast<const uint4*>(sK + (32 + rl) * KP + 16 * ks + 8 * h);
+      const Frag<T> a0 = *reinterpret_cast<const Frag<T>*>(sK + rl * KP + 16 * ks + 8 * h);
+      const Frag<T> a1 = *reinterpret_cast<const Frag<T>*>(sK + (32 + rl) * KP + 16 * ks + 8 * h);
       st[0] = M::mac(a0, qf[ks], st[0]);
       st[1] = M::mac(a1, qf[ks], st[1]);
     }
@@ -458,21 +484,33 @@ __global__ __launch_bounds__(128, 2) void fwd_kernel(FwdK p) {
     l_run += (ps[0] + ps[1]) + (ps[2] + ps[3]);
 
     // P^T as B operands (4 steps of 16 keys), rounded to the input dtype
-    uint4 pb[4];
+    Frag<T> pb[4];
 #pragma unroll
     for (int ks = 0; ks < 4; ++ks) {
       const int hf = ks >> 1, r0 = 8 * (ks & 1);
-      pb[ks] = make_uint4(M::pack2(st[hf][r0], st[hf][r0 + 1]), M::pack2(st[hf][r0 + 2], st[hf][r0 + 3]),
-                          M::pack2(st[hf][r0 + 4], st[hf][r0 + 5]), M::pack2(st[hf][r0 + 6], st[hf][r0 + 7]));
+      if constexpr (F32) {
+        float v[8];
+#pragma unroll
+        for (int j = 0; j < 8; ++j) v[j] = st[hf][r0 + j];
+        pb[ks] = f32x8(v);
+      } else {
+        pb[ks] = make_uint4(M::pack2(st[hf][r0], st[hf][r0 + 1]), M::pack2(st[hf][r0 + 2], st[hf][r0 + 3]),
+                            M::pack2(st[hf][r0 + 4], st[hf][r0 + 5]), M::pack2(st[hf][r0 + 6], st[hf][r0 + 7]));
+      }
     }
     // O^T += V^T P^T, k-step outer: the MT accumulators form independent
     // chains that interleave, and a step's operands are read before its MFMAs
     __builtin_amdgcn_s_setprio(1);
 #pragma unroll
     for (int ks = 0; ks < 4; ++ks) {
-      uint4 va[MT];
+      Frag<T> va[MT];
 #pragma unroll
-      for (int mt = 0; mt < MT; ++mt) va[mt] = a_operand_tr<VP>(v16, 16 * ks, 32 * mt, lane);
+      for (int mt = 0; mt < MT; ++mt) {
+        if constexpr (F32)
+          va[mt] = a_operand_f32<VP>(reinterpret_cast<const float*>(sV), 16 * ks, 32 * mt, lane);
+        else
+          va[mt] = a_operand_tr<VP>(v16, 16 * ks, 32 * mt, lane);
+      }
 #pragma unroll
       for (int mt = 0; mt < MT; ++mt) o[mt] = M::mac(va[mt], pb[ks], o[mt]);
     }
@@ -501,10 +539,15 @@ __global__ __launch_bounds__(128, 2) void fwd_kernel(FwdK p) {
 #pragma unroll
     for (int g = 0; g < 4; ++g) {
       const int d0 = 32 * mt + 8 * g + 4 * h;
-      uint2 w;
-      w.x = M::pack2(o[mt][4 * g] * inv, o[mt][4 * g + 1] * inv);
-      w.y = M::pack2(o[mt][4 * g + 2] * inv, o[mt][4 * g + 3] * inv);
-      *reinterpret_cast<uint2*>(orow + d0) = w;
+      if constexpr (F32) {
+        *reinterpret_cast<float4*>(orow + d0) =
+            make_float4(o[mt][4 * g] * inv, o[mt][4 * g + 1] * inv, o[mt][4 * g + 2] * inv, o[mt][4 * g + 3] * inv);
+      } else {
+        uint2 w;
+        w.x = M::pack2(o[mt][4 * g] * inv, o[mt][4 * g + 1] * inv);
+        w.y = M::pack2(o[mt][4 * g + 2] * inv, o[mt][4 * g + 3] * inv);
+        *reinterpret_cast<uint2*>(orow + d0) = w;
+      }
     }
   if (!PAGED && a.lse && h == 0)
     a.lse[(int64_t)b * a.lse_sb + (int64_t)(t0 + row) * a.lse_st + (int64_t)hq * a.lse_sh] =
@@ -562,7 +605,12 @@ __global__ __launch_bounds__(256) void fwd_merge_kernel(FwdK p) {
   const float inv = l > 0.f ? 1.f / l : 0.f;
   T* orow = reinterpret_cast<T*>(a.out) + (int64_t)b * a.o_sb + (int64_t)(t0 + r) * a.o_st + (int64_t)hq * a.o_sh +
             c * DPT;
-  if constexpr (DPT == 8) {
+  if constexpr (std::is_same<T, float>::value) {
+#pragma unroll
+    for (int d = 0; d < DPT / 4; ++d)
+      reinterpret_cast<float4*>(orow)[d] =
+          make_float4(acc[4 * d] * inv, acc[4 * d + 1] * inv, acc[4 * d + 2] * inv, acc[4 * d + 3] * inv);
+  } else if constexpr (DPT == 8) {
     *reinterpret_cast<uint4*>(orow) =
         make_uint4(M::pack2(acc[0] * inv, acc[1] * inv), M::pack2(acc[2] * inv, acc[3] * inv),
                    M::pack2(acc[4] * inv, acc[5] * inv), M::pack2(acc[6] * inv, acc[7] * inv));
@@ -590,14 +638,15 @@ int check_fwd(const srswa_fwd_args* a) {
     set_error("fwd: HQ must be a multiple of HKV and HI");
     return SRSWA_UNSUPPORTED;
   }
-  if (a->dtype != SRSWA_BF16 && a->dtype != SRSWA_F16) {
-    set_error("fwd: matrix-core path takes bf16 / fp16");
+  if (a->dtype != SRSWA_BF16 && a->dtype != SRSWA_F16 && a->dtype != SRSWA_F32) {
+    set_error("fwd: dtype %d not supported (bf16, fp16, fp32)", a->dtype);
     return SRSWA_UNSUPPORTED;
   }
   if (!(a->D == 64 || a->D == 128)) {
     set_error("fwd: head dim %d not supported (64, 128)", a->D);
     return SRSWA_UNSUPPORTED;
   }
+  const int es = a->dtype == SRSWA_F32 ? 4 : 2;   // element bytes
   if (a->block_size < 16 || (a->block_size & (a->block_size - 1)) || a->S > 64) {
     set_error("fwd: block size must be a power of two >= 16, at most 64 slots");
     return SRSWA_UNSUPPORTED;
@@ -607,7 +656,7 @@ int check_fwd(const srswa_fwd_args* a) {
     return SRSWA_UNSUPPORTED;
   }
   // K / V of one (sequence, kv head) are addressed with 32-bit byte offsets
-  const int64_t span = ((int64_t)ceil_div(a->Sk, kChunk) * kChunk * std::max(a->k_st, a->v_st) + a->D) * 2;
+  const int64_t span = ((int64_t)ceil_div(a->Sk, kChunk) * kChunk * std::max(a->k_st, a->v_st) + a->D) * es;
   if (span >= ((int64_t)1 << 32)) {
     set_error("fwd: one sequence's K / V span 4 GiB or more");
     return SRSWA_UNSUPPORTED;
@@ -615,7 +664,7 @@ int check_fwd(const srswa_fwd_args* a) {
   const int64_t st[] = {a->q_sb, a->q_st, a->q_sh, a->k_sb, a->k_st, a->k_sh, a->v_sb, a->v_st,
                         a->v_sh, a->o_sb, a->o_st, a->o_sh};
   for (int64_t s : st)
-    if ((s * 2) % 16) {
+    if ((s * es) % 16) {
       set_error("fwd: rows must be 16-byte aligned");
       return SRSWA_UNSUPPORTED;
     }
@@ -673,7 +722,9 @@ int plan_fwd(const srswa_fwd_args* a, FwdK& k, size_t& smem, size_t& ws_bytes) {
   const int64_t per_tile = (int64_t)kTileRows * a->S * (ceil_div(a->block_size, kChunk) + 1) +
                            ceil_div(a->local_window + kTileRows - 1, kChunk) + 1;
   const int umax = (int)std::min<int64_t>(nchunk, per_tile);
-  const size_t tile = a->D == 128 ? FwdLds<128>::tileBytes : FwdLds<64>::tileBytes;
+  const bool f32 = a->dtype == SRSWA_F32;
+  const size_t tile = a->D == 128 ? (f32 ? FwdLds<128, 4>::tileBytes : FwdLds<128>::tileBytes)
+                                  : (f32 ? FwdLds<64, 4>::tileBytes : FwdLds<64>::tileBytes);
   const size_t setup = (3 * 64 + 4) * 4 + (size_t)k.nwords * 4;
   size_t n = std::max(tile, setup);
   k.chunks_off = (int)n;
@@ -743,6 +794,8 @@ extern "C" int srswa_gather_fwd_ws(const srswa_fwd_args* a, void* ws, size_t ws_
   }
   k.part = reinterpret_cast<float*>(ws);
   hipStream_t s = reinterpret_cast<hipStream_t>(stream);
+  if (a->dtype == SRSWA_F32)
+    return a->D == 128 ? launch_fwd<float, 128, false>(k, smem, s) : launch_fwd<float, 64, false>(k, smem, s);
   if (a->dtype == SRSWA_BF16)
     return a->D == 128 ? launch_fwd<bf16_t, 128, false>(k, smem, s) : launch_fwd<bf16_t, 64, false>(k, smem, s);
   return a->D == 128 ? launch_fwd<__half, 128, false>(k, smem, s) : launch_fwd<__half, 64, false>(k, smem, s);
