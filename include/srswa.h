@@ -561,6 +561,110 @@ typedef struct {
 
 int srswa_page_decode_meta(const srswa_page_meta_args* a, void* stream);
 
+/* Multi-token step of the per-slot page state (prefill chunks and decode
+ * tokens of one serving step): replaces PageIsolationState.step
+ * (WHL!layers/attention/unlimited_dash_ops/page_state.py:218-313).  Request r
+ * owns tokens [q_start[r], q_start[r + 1]) (tokens past q_start[R] continue
+ * request R - 1); carry-in (marker count, image run, prompt pages) from the
+ * slot of position start_pos[r] - 1 (zeros when < 0); per token, in order,
+ *   marker = carry + markers so far, run = carry + image tokens so far,
+ *   pp = max(carry pp, max over the request's image tokens so far of marker),
+ *   img_page = is_img ? (marker > 0 ? marker - 1 : (run - 1) / per_page) : -1,
+ *   generated = t < num_decode_tokens || start_pos + (t - q_start) >= gen_start[r],
+ *   q_page = is_img ? img_page : generated ? (marker - 1 - pp >= 0 ? marker - 1 - pp : -1)
+ *                                          : (marker > pp ? marker - 1 : -1);
+ * the four states are written at slot_mapping[t] (clamped to [0, n_slots)),
+ * then the image page of every slot past the request's new end in its last
+ * block is reset to -1.  is_img = id >= 1000000 || id == image_token_id,
+ * is_mark = has_marker && id == page_token_id.  Tokens that share a slot race
+ * (as the reference's scatter). */
+typedef struct {
+  const void* input_ids;     int32_t ids_i64;          /* [T] i32/i64                         */
+  const int64_t* q_start;                              /* [R + 1]                              */
+  const int64_t* start_pos;                            /* [R] KV position of the first token  */
+  const int64_t* gen_start;                            /* [R] first generated position, or NULL */
+  const void* block_table;   int32_t bt_i64; int64_t bt_sr;  /* [R, bt_w] page ids            */
+  const void* slot_mapping;  int32_t slot_i64;         /* [T] KV slot of each token           */
+  int32_t* s_page; int32_t* s_mark; int32_t* s_run; int32_t* s_pp;   /* [n_slots] state   */
+  int32_t* q_page;                                     /* [T] out                             */
+  int64_t image_token_id, page_token_id;
+  int64_t num_decode_tokens;
+  int32_t R, T, bt_w, n_slots, block_size, per_page, has_marker;
+} srswa_page_step_args;
+
+int srswa_page_step(const srswa_page_step_args* a, void* stream);
+
+/* The scans, ranks and carry of PageCoordState.step
+ * (WHL!layers/attention/unlimited_dash_ops/page2d_rope.py:534-620) for rows
+ * already chosen by the caller (the row allocation, the speculative rewind
+ * and the snapshot stay the caller's): request r uses state row row[r];
+ *   marker = st_marker + markers so far, pp = max(st_pp, max over image tokens
+ *   so far of marker), generated as srswa_page_step,
+ *   in_prefill = !generated && (is_img || marker > pp),
+ *   page = clamp(in_prefill ? marker : min(max(marker - pp, 0), pp), 0, pages - 1),
+ *   tok = cnt[row, page] + (earlier tokens of the request in that page);
+ * then cnt[row] += this step's tokens per page, st_marker / st_pp = the values
+ * at the request's last token (a request with no tokens keeps its row).
+ * marker_out / pp_out (optional, [T] int32) return marker and pp (the
+ * snapshot's inputs).  pages <= 16384. */
+typedef struct {
+  const void* input_ids;     int32_t ids_i64;          /* [T] i32/i64                         */
+  const int64_t* q_start;                              /* [R + 1]                              */
+  const int64_t* start_pos;                            /* [R]                                  */
+  const int64_t* gen_start;                            /* [R] or NULL                          */
+  const int64_t* row;                                  /* [R] state row of each request       */
+  int32_t* st_marker; int32_t* st_pp;                  /* [n_rows]                             */
+  int32_t* cnt;              int64_t cnt_sr;           /* [n_rows, pages]                      */
+  int64_t* tok; int64_t* page;                         /* [T] out                              */
+  int32_t* marker_out; int32_t* pp_out;                /* [T] out or NULL                      */
+  int64_t image_token_id, page_token_id;
+  int64_t num_decode_tokens;
+  int32_t R, T, n_rows, pages, has_marker;
+} srswa_coord_step_args;
+
+int srswa_coord_step(const srswa_coord_step_args* a, void* stream);
+
+/* Page ids of whole prompts: replaces DeepseekV2Indexer._build_page_aware_ids
+ * (HF/_sparse_base_impl.py:2404-2502) without its diagnostics.  Row b reads
+ * ids[b, 0 .. n_ids) and pads to L with -1; last = the last image token (-1:
+ * none), prompt_pages = markers at or before it (0 without an image),
+ * marker_mode = prompt_pages > 0; per token i (cum = markers so far, run =
+ * image tokens so far - 1):
+ *   img_mask = is_img, img_page = is_img ? (marker_mode ? cum - 1 : run / per_page) : -1,
+ *   q_page = i <= last ? (page_scope_prefill ? cum - 1 : -1)
+ *                      : cum - 1 - (marker_mode ? prompt_pages : 0), then -1 where < 0;
+ * row_counts (optional, [B, 2] int32): tokens with q_page >= 0, image tokens. */
+typedef struct {
+  const void* ids;           int32_t ids_i64; int64_t id_sb;   /* [B, n_ids]              */
+  uint8_t* img_mask;  int64_t* img_page;  int64_t* q_page;  int64_t o_sb;   /* [B, L] out */
+  int32_t* row_counts;
+  int64_t image_token_id, page_token_id;
+  int32_t B, L, n_ids, per_page, page_scope_prefill;
+} srswa_page_ids_args;
+
+int srswa_page_ids(const srswa_page_ids_args* a, void* stream);
+
+/* Page2D positions of whole prompts: replaces _build_page_rope_pos and the
+ * running counts of _page_rope_offsets (HF/_sparse_base_impl.py:2511-2570).
+ * srswa_page_rope_pos: last image token, n_pages = markers at or before it,
+ *   page[b, i] = max(i <= last ? cum : cum - n_pages, 0), prefill[b, i] = i <= last,
+ *   row_info[b] = {n_pages, max page, any image token, any marker};
+ * srswa_page_rope_tok (after the caller reads n_pg = 1 + the largest page):
+ *   tok[b, i] = earlier tokens of row b in page[b, i], pf_cnt[b, p] = prefill
+ *   tokens of page p (n_pg <= 8192). */
+typedef struct {
+  const void* ids;           int32_t ids_i64; int64_t id_sb;   /* [B, n_ids]              */
+  int32_t* page;  uint8_t* prefill;  int64_t o_sb;              /* [B, L] out / in        */
+  int32_t* row_info;                                            /* [B, 4] out             */
+  int64_t* tok;                                                 /* [B, L] out (pass 2)    */
+  int32_t* pf_cnt;           int64_t pf_sb;                     /* [B, n_pg] out (pass 2) */
+  int64_t image_token_id, page_token_id;
+  int32_t B, L, n_ids, n_pg;
+} srswa_page_pos_args;
+
+int srswa_page_rope_pos(const srswa_page_pos_args* a, void* stream);
+int srswa_page_rope_tok(const srswa_page_pos_args* a, void* stream);
+
 /* Page-isolation candidate mask of the decode rows (replaces
  * _decode_allow_kernel / decode_allow_fused, decode_meta_triton.py:107-163,318-351):
  * per request r and column w < max_block, with W = min(max_block, bt_w),

@@ -286,3 +286,189 @@ def angle_close(a, b):
     """|a - b| as angles (helper for the identity checks)."""
     d = np.remainder(np.asarray(a) - np.asarray(b) + math.pi, 2 * math.pi) - math.pi
     return np.abs(d)
+
+
+# ----------------------------------------------------------------- multi-token steps
+def _seg_scan(vals, q_start, T, op, init):
+    """Per-request inclusive scan (request r owns [q_start[r], q_start[r+1]),
+    the tokens past q_start[R] continue request R - 1) seeded with init[r]."""
+    out = np.zeros(T, np.int64)
+    R = len(q_start) - 1
+    for r in range(R):
+        lo = int(q_start[r])
+        hi = T if r == R - 1 else int(q_start[r + 1])
+        acc = int(init[r])
+        for t in range(lo, hi):
+            acc = op(acc, int(vals[t]))
+            out[t] = acc
+    return out
+
+
+def _req_of(q_start, T):
+    R = len(q_start) - 1
+    req = np.zeros(T, np.int64)
+    for r in range(R):
+        hi = T if r == R - 1 else int(q_start[r + 1])
+        req[int(q_start[r]):hi] = r
+    return req
+
+
+def _generated(T, q_start, start_pos, gen_start, num_decode_tokens):
+    """``generated_mask`` WHL!…/page_state.py:56-62."""
+    req = _req_of(q_start, T)
+    t = np.arange(T)
+    gen = t < int(num_decode_tokens)
+    if gen_start is not None:
+        abs_pos = np.asarray(start_pos)[req] + (t - np.asarray(q_start)[req])
+        gen = gen | (abs_pos >= np.asarray(gen_start)[req])
+    return gen
+
+
+def page_step(ids, q_start, start_pos, block_table, slot_mapping, st: SlotState, image_token_id: int,
+              page_token_id, per_page: int, block_size: int, num_decode_tokens: int = 0, gen_start=None):
+    """Multi-token ``PageIsolationState.step`` (WHL!…/page_state.py:218-313):
+    the carry-in of ``_carry`` (:200-216), the per-request scans, the page
+    rules and the per-slot scatter, then the stale-tail reset.  Mutates
+    ``st``; returns q_page int32 [T]."""
+    ids = np.asarray(ids, np.int64)
+    T = len(ids)
+    R = len(q_start) - 1
+    n = len(st.img_page)
+    bs = block_size
+    bt_w = block_table.shape[1]
+    is_img = (ids >= MM_PAD_SHIFT) | (ids == image_token_id)
+    is_mark = np.zeros(T, bool) if page_token_id is None else ids == page_token_id
+    pm, pi, ppp = np.zeros(R, np.int64), np.zeros(R, np.int64), np.zeros(R, np.int64)
+    for r in range(R):
+        p = int(start_pos[r]) - 1
+        if p >= 0:
+            blk = min(p // bs, bt_w - 1)
+            slot = min(max(int(block_table[r, blk]) * bs + p % bs, 0), n - 1)
+            pm[r], pi[r], ppp[r] = st.marker_cum[slot], st.img_run[slot], st.prompt_pages[slot]
+    marker = _seg_scan(is_mark.astype(np.int64), q_start, T, lambda a, b: a + b, pm)
+    run = _seg_scan(is_img.astype(np.int64), q_start, T, lambda a, b: a + b, pi)
+    pp = _seg_scan(np.where(is_img, marker, 0), q_start, T, max, ppp)
+    img_page = np.where(marker > 0, marker - 1, (run - 1) // per_page)
+    img_page = np.where(is_img, img_page, -1)
+    gen = _generated(T, q_start, start_pos, gen_start, num_decode_tokens)
+    prefill_page = np.where(marker > pp, marker - 1, -1)
+    resp = marker - 1 - pp
+    resp = np.where(resp >= 0, resp, -1)
+    q_page = np.where(is_img, img_page, np.where(gen, resp, prefill_page)).astype(np.int32)
+    for t in range(T):
+        sl = min(max(int(slot_mapping[t]), 0), n - 1)
+        st.img_page[sl] = img_page[t]
+        st.marker_cum[sl] = marker[t]
+        st.img_run[sl] = run[t]
+        st.prompt_pages[sl] = pp[t]
+    for r in range(R):
+        end = int(start_pos[r]) + int(q_start[r + 1]) - int(q_start[r])
+        rem = end % bs
+        if rem > 0:
+            blk = min(max((end - 1) // bs, 0), bt_w - 1)
+            phys = int(block_table[r, blk])
+            for off in range(rem, bs):
+                st.img_page[min(max(phys * bs + off, 0), n - 1)] = -1
+    return q_page
+
+
+def coord_step(ids, q_start, start_pos, rows, cs: CoordState, image_token_id: int, page_token_id,
+               num_decode_tokens: int = 0, gen_start=None):
+    """The scans, ranks and carry of ``PageCoordState.step``
+    (WHL!…/page2d_rope.py:534-620) for given state rows: marker / pp scans
+    seeded by the row's carry, the page rule, tok = the row's count plus the
+    rank among the request's earlier tokens of that page (stable sort),
+    then the carry written back.  Mutates ``cs``; returns (tok, page, marker, pp)."""
+    ids = np.asarray(ids, np.int64)
+    T = len(ids)
+    R = len(q_start) - 1
+    pages = cs.max_pages
+    is_img = (ids >= MM_PAD_SHIFT) | (ids == image_token_id)
+    is_mark = np.zeros(T, bool) if page_token_id is None else ids == page_token_id
+    rows = np.asarray(rows, np.int64)
+    marker = _seg_scan(is_mark.astype(np.int64), q_start, T, lambda a, b: a + b, cs.st_marker[rows])
+    pp = _seg_scan(np.where(is_img, marker, 0), q_start, T, max, cs.st_pp[rows])
+    gen = _generated(T, q_start, start_pos, gen_start, num_decode_tokens)
+    in_prefill = (~gen) & (is_img | (marker > pp))
+    resp = np.minimum(np.maximum(marker - pp, 0), pp)
+    page = np.clip(np.where(in_prefill, marker, resp), 0, pages - 1)
+    req = _req_of(q_start, T)
+    flat = req * pages + page
+    order = np.argsort(flat, kind="stable")
+    rank = np.zeros(T, np.int64)
+    prev, start = None, 0
+    for i, t in enumerate(order):
+        if flat[t] != prev:
+            prev, start = flat[t], i
+        rank[t] = i - start
+    cnt_in = cs.cnt[rows]
+    tok = cnt_in[req, page] + rank
+    for r in range(R):
+        lo, hi = int(q_start[r]), int(q_start[r + 1])
+        if hi <= lo:
+            continue
+        row = int(rows[r])
+        for t in range(lo, hi):
+            cs.cnt[row, page[t]] += 1
+        cs.st_marker[row] = marker[hi - 1]
+        cs.st_pp[row] = pp[hi - 1]
+    return tok.astype(np.int64), page.astype(np.int64), marker.astype(np.int32), pp.astype(np.int32)
+
+
+def page_aware_ids(source_ids, image_token_id: int, page_token_id: int, key_length: int, per_page: int,
+                   page_scope_prefill: bool = True):
+    """``DeepseekV2Indexer._build_page_aware_ids`` (HF/_sparse_base_impl.py:2404-2502)
+    without its one-shot diagnostic print: (image_token_mask, image_token_page_ids,
+    query_token_page_ids) [B, key_length], or (None, None, None)."""
+    ids = np.asarray(source_ids, np.int64)[:, :key_length]
+    if ids.shape[1] < key_length:
+        ids = np.pad(ids, ((0, 0), (0, key_length - ids.shape[1])), constant_values=-1)
+    B, S = ids.shape
+    img = ids == image_token_id
+    mk = ids == page_token_id
+    cum = np.cumsum(mk, axis=1)
+    ar = np.arange(S)
+    last = (img * (ar + 1)).max(axis=1) - 1
+    prompt_pages = cum[np.arange(B), np.maximum(last, 0)] * (last >= 0)
+    marker_mode = prompt_pages > 0
+    run = np.cumsum(img, axis=1) - 1
+    ipage = np.where(marker_mode[:, None], cum - 1, run // per_page)
+    ipage = np.where(img, ipage, -1)
+    raw = cum - 1
+    resp = raw - np.where(marker_mode, prompt_pages, 0)[:, None]
+    in_prefill = ar[None, :] <= last[:, None]
+    q = np.where(in_prefill, raw, resp)
+    if not page_scope_prefill:
+        q = np.where(in_prefill, -1, q)
+    q = np.where(q < 0, -1, q)
+    if img.sum() == 0 or (q >= 0).sum() == 0:
+        return None, None, None
+    return img, ipage.astype(np.int64), q.astype(np.int64)
+
+
+def page_rope_pos(source_ids, image_token_id: int, page_token_id: int, key_length: int):
+    """``_build_page_rope_pos`` + the running counts of ``_page_rope_offsets``
+    (HF/_sparse_base_impl.py:2511-2570, no span ablation): (tok_pos, page_pos,
+    pf_cnt) or None where the reference bails to the 1D RoPE."""
+    ids = np.asarray(source_ids, np.int64)[:, :key_length]
+    if ids.shape[1] < key_length:
+        ids = np.pad(ids, ((0, 0), (0, key_length - ids.shape[1])), constant_values=-1)
+    B, S = ids.shape
+    ar = np.arange(S)
+    img = ids == image_token_id
+    mk = ids == page_token_id
+    if not img.any() or not mk.any():
+        return None
+    cum = np.cumsum(mk, axis=1)
+    last = (img * (ar + 1)).max(axis=1) - 1
+    n_pages = cum[np.arange(B), np.maximum(last, 0)] * (last >= 0)
+    if not (n_pages > 0).all():
+        return None
+    in_prefill = ar[None, :] <= last[:, None]
+    page = np.maximum(np.where(in_prefill, cum, cum - n_pages[:, None]), 0)
+    n_pg = int(page.max()) + 1
+    onehot = np.eye(n_pg, dtype=np.int64)[page]                   # [B, S, n_pg]
+    run = np.cumsum(onehot, axis=1)
+    tok = np.take_along_axis(run, page[:, :, None], axis=2)[:, :, 0] - 1
+    pf_cnt = (onehot * in_prefill[:, :, None]).sum(axis=1)
+    return tok.astype(np.int64), page.astype(np.int64), pf_cnt.astype(np.int64)

@@ -262,3 +262,187 @@ def test_rope_identities():
     back = P.rope_apply(y, c, -s, "f32")
     assert np.abs(back - x).max() < 1e-5
     assert np.allclose(np.linalg.norm(y, axis=-1), np.linalg.norm(x, axis=-1), rtol=1e-5)
+
+
+# ------------------------------------------------------------ multi-token steps
+def _layout(rng, docs, chunks, bs, n_extra_pages=5):
+    """Per-request block tables and the slots of every position."""
+    R = len(docs)
+    L = max(len(d) for d in docs)
+    nblk = -(-L // bs) + 1
+    perm = rng.permutation(R * nblk + n_extra_pages)
+    bt = perm[:R * nblk].reshape(R, nblk).astype(np.int64)
+    n_slots = (R * nblk + n_extra_pages) * bs
+    return bt, n_slots
+
+
+def _step_inputs(docs, pos, lens, bt, bs):
+    """One serving step: request r contributes docs[r][pos[r]:pos[r]+lens[r]]."""
+    ids, slots, q_start = [], [], [0]
+    for r, d in enumerate(docs):
+        for t in range(pos[r], pos[r] + lens[r]):
+            ids.append(d[t])
+            slots.append(bt[r, t // bs] * bs + t % bs)
+        q_start.append(q_start[-1] + lens[r])
+    return np.array(ids, np.int64), np.array(slots, np.int64), np.array(q_start, np.int64)
+
+
+@pytest.mark.parametrize("seed", [11, 12])
+def test_page_step_chunked_equals_token_by_token(seed):
+    """PageIsolationState.step's whole-step scans (oracle.page_step), run over
+    whole prompts in random chunk sizes, give the q_page / per-slot state of the
+    token-by-token state machine (the same step one token at a time, a
+    different formulation: no scans), and on generated tokens the pinned
+    one-token decode restatement."""
+    rng = np.random.default_rng(seed)
+    bs, per_page = 16, 24
+    docs = [_document(rng, int(rng.integers(1, 4)), with_markers=bool(r % 2 == 0)) for r in range(3)]
+    bt, n_slots = _layout(rng, docs, None, bs)
+    R = len(docs)
+    st_a, st_b = P.SlotState(n_slots), P.SlotState(n_slots)
+    L = [len(d) for d in docs]
+    q_a = [np.zeros(n, np.int32) for n in L]
+    q_b = [np.zeros(n, np.int32) for n in L]
+    # (a) random chunks, all requests in one step each time
+    pos = [0] * R
+    while any(pos[r] < L[r] for r in range(R)):
+        lens = [min(int(rng.integers(0, 40)), L[r] - pos[r]) for r in range(R)]
+        ids, slots, q_start = _step_inputs(docs, pos, lens, bt, bs)
+        if len(ids) == 0:
+            continue
+        q = P.page_step(ids, q_start, np.array(pos), bt, slots, st_a, IMG, PG, per_page, bs)
+        for r in range(R):
+            q_a[r][pos[r]:pos[r] + lens[r]] = q[q_start[r]:q_start[r + 1]]
+            pos[r] += lens[r]
+    # (b) token by token as a plain state machine
+    n = n_slots
+    for r in range(R):
+        m = run = pp = 0
+        for t in range(L[r]):
+            tid = int(docs[r][t])
+            img = tid >= P.MM_PAD_SHIFT or tid == IMG
+            m += int(tid == PG)
+            run += int(img)
+            if img:
+                pp = max(pp, m)
+            ip = (m - 1 if m > 0 else (run - 1) // per_page) if img else -1
+            q_b[r][t] = ip if img else (m - 1 if m > pp else -1)
+            sl = bt[r, t // bs] * bs + t % bs
+            st_b.img_page[sl], st_b.marker_cum[sl], st_b.img_run[sl], st_b.prompt_pages[sl] = ip, m, run, pp
+        end = L[r]
+        if end % bs:
+            last = bt[r, (end - 1) // bs] * bs
+            st_b.img_page[last + end % bs:last + bs] = -1
+    for r in range(R):
+        np.testing.assert_array_equal(q_a[r], q_b[r])
+        slots = bt[r, np.arange(L[r]) // bs] * bs + np.arange(L[r]) % bs
+        for f in ("img_page", "marker_cum", "img_run", "prompt_pages"):
+            np.testing.assert_array_equal(getattr(st_a, f)[slots], getattr(st_b, f)[slots], err_msg=f)
+    # (c) generated tokens: page_step with every token generated equals the
+    # pinned one-token decode restatement
+    st_c, st_d = P.SlotState(n_slots), P.SlotState(n_slots)
+    cs = P.CoordState(R, 64)
+    T = min(L)
+    for t in range(T):
+        ids = np.array([d[t] for d in docs], np.int64)
+        slots = bt[np.arange(R), t // bs] * bs + t % bs
+        qs = np.arange(R + 1, dtype=np.int64)
+        qc = P.page_step(ids, qs, np.full(R, t), bt, slots, st_c, IMG, PG, per_page, bs, num_decode_tokens=R)
+        qd, _, _ = P.decode_meta_step(ids, bt, np.full(R, t + 1), slots, np.arange(R), st_d, cs, IMG, PG,
+                                      per_page, bs)
+        np.testing.assert_array_equal(qc, qd)
+
+
+def test_coord_step_chunked_equals_token_by_token():
+    """PageCoordState.step's scans + stable-sort ranks (oracle.coord_step) over
+    random chunks equal a per-token state machine with per-page counters, and
+    on generated tokens the pinned one-token decode coordinates."""
+    rng = np.random.default_rng(13)
+    docs = [_document(rng, int(rng.integers(1, 4))) for _ in range(3)]
+    R, pages = len(docs), 32
+    L = [len(d) for d in docs]
+    cs = P.CoordState(R + 2, pages)
+    rows = np.array([2, 0, 3])
+    tok_a = [np.zeros(n, np.int64) for n in L]
+    page_a = [np.zeros(n, np.int64) for n in L]
+    pos = [0] * R
+    gen_start = np.array([L[r] - 6 for r in range(R)])   # the last 6 tokens are generated
+    while any(pos[r] < L[r] for r in range(R)):
+        lens = [min(int(rng.integers(0, 30)), L[r] - pos[r]) for r in range(R)]
+        ids, _, q_start = _step_inputs(docs, pos, lens, np.zeros((R, 64), np.int64), 16)
+        if len(ids) == 0:
+            continue
+        tok, page, _, _ = P.coord_step(ids, q_start, np.array(pos), rows, cs, IMG, PG, gen_start=gen_start)
+        for r in range(R):
+            tok_a[r][pos[r]:pos[r] + lens[r]] = tok[q_start[r]:q_start[r + 1]]
+            page_a[r][pos[r]:pos[r] + lens[r]] = page[q_start[r]:q_start[r + 1]]
+            pos[r] += lens[r]
+    for r in range(R):
+        m = pp = 0
+        cnt = np.zeros(pages, np.int64)
+        for t in range(L[r]):
+            tid = int(docs[r][t])
+            img = tid >= P.MM_PAD_SHIFT or tid == IMG
+            m += int(tid == PG)
+            if img:
+                pp = max(pp, m)
+            gen = t >= gen_start[r]
+            pre = (not gen) and (img or m > pp)
+            pg = min(max(m if pre else min(max(m - pp, 0), pp), 0), pages - 1)
+            assert page_a[r][t] == pg and tok_a[r][t] == cnt[pg], (r, t)
+            cnt[pg] += 1
+        np.testing.assert_array_equal(cs.cnt[rows[r]], cnt)
+
+
+def _ids_batch(rng, B, marker_rows=True):
+    docs = [_document(rng, int(rng.integers(1, 4)), with_markers=marker_rows or b % 2 == 1) for b in range(B)]
+    L = max(len(d) for d in docs)
+    return np.stack([np.concatenate([d, np.full(L - len(d), 5)]) for d in docs]), L
+
+
+@pytest.mark.parametrize("scope", [True, False])
+def test_page_aware_ids_per_token_state_machine(scope):
+    """_build_page_aware_ids (oracle.page_aware_ids) against a per-row walk
+    that counts markers / image tokens as it goes (two passes: find the last
+    image token, then assign)."""
+    rng = np.random.default_rng(14)
+    ids, L = _ids_batch(rng, 4, marker_rows=False)
+    klen = L + 7                                            # padded with -1 past the ids
+    img, ipage, q = P.page_aware_ids(ids, IMG, PG, klen, 24, page_scope_prefill=scope)
+    for b in range(len(ids)):
+        row = list(ids[b]) + [-1] * 7
+        last = max([i for i, v in enumerate(row) if v == IMG], default=-1)
+        npp = sum(1 for v in row[:last + 1] if v == PG) if last >= 0 else 0
+        cum = run = 0
+        for i, v in enumerate(row):
+            cum += int(v == PG)
+            run += int(v == IMG)
+            assert img[b, i] == (v == IMG)
+            exp_ip = ((cum - 1) if npp > 0 else (run - 1) // 24) if v == IMG else -1
+            assert ipage[b, i] == exp_ip
+            if i <= last:
+                eq = cum - 1 if scope else -1
+            else:
+                eq = cum - 1 - (npp if npp > 0 else 0)
+            assert q[b, i] == (eq if eq >= 0 else -1), (b, i)
+    none = P.page_aware_ids(np.full((2, 30), 7), IMG, PG, 30, 24)
+    assert none == (None, None, None)
+
+
+def test_page_rope_pos_brute_force():
+    """_build_page_rope_pos + the running counts (oracle.page_rope_pos):
+    tok = earlier tokens of the row in the same page, pf_cnt = prefill tokens
+    per page, both by brute force; bails where the reference bails."""
+    rng = np.random.default_rng(15)
+    ids, L = _ids_batch(rng, 3)
+    tok, page, pf = P.page_rope_pos(ids, IMG, PG, L)
+    for b in range(len(ids)):
+        row = list(ids[b])
+        last = max(i for i, v in enumerate(row) if v == IMG)
+        for i in range(L):
+            assert tok[b, i] == sum(1 for j in range(i) if page[b, j] == page[b, i])
+        for p in range(pf.shape[1]):
+            assert pf[b, p] == sum(1 for j in range(last + 1) if page[b, j] == p)
+    assert P.page_rope_pos(np.full((1, 20), 3), IMG, PG, 20) is None
+    no_mark = np.array([[0] + [IMG] * 10 + [5] * 4])
+    assert P.page_rope_pos(no_mark, IMG, PG, 15) is None

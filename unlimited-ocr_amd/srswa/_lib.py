@@ -306,6 +306,61 @@ class RouteArgs(ctypes.Structure):
     ]
 
 
+class PageStepArgs(ctypes.Structure):
+    """Mirror of ``srswa_page_step_args``."""
+
+    _fields_ = [
+        ("input_ids", _vp), ("ids_i64", _i32),
+        ("q_start", _vp), ("start_pos", _vp), ("gen_start", _vp),
+        ("block_table", _vp), ("bt_i64", _i32), ("bt_sr", _i64),
+        ("slot_mapping", _vp), ("slot_i64", _i32),
+        ("s_page", _vp), ("s_mark", _vp), ("s_run", _vp), ("s_pp", _vp),
+        ("q_page", _vp),
+        ("image_token_id", _i64), ("page_token_id", _i64), ("num_decode_tokens", _i64),
+        ("R", _i32), ("T", _i32), ("bt_w", _i32), ("n_slots", _i32), ("block_size", _i32), ("per_page", _i32),
+        ("has_marker", _i32),
+    ]
+
+
+class CoordStepArgs(ctypes.Structure):
+    """Mirror of ``srswa_coord_step_args``."""
+
+    _fields_ = [
+        ("input_ids", _vp), ("ids_i64", _i32),
+        ("q_start", _vp), ("start_pos", _vp), ("gen_start", _vp), ("row", _vp),
+        ("st_marker", _vp), ("st_pp", _vp), ("cnt", _vp), ("cnt_sr", _i64),
+        ("tok", _vp), ("page", _vp), ("marker_out", _vp), ("pp_out", _vp),
+        ("image_token_id", _i64), ("page_token_id", _i64), ("num_decode_tokens", _i64),
+        ("R", _i32), ("T", _i32), ("n_rows", _i32), ("pages", _i32), ("has_marker", _i32),
+    ]
+
+
+class PageIdsArgs(ctypes.Structure):
+    """Mirror of ``srswa_page_ids_args``."""
+
+    _fields_ = [
+        ("ids", _vp), ("ids_i64", _i32), ("id_sb", _i64),
+        ("img_mask", _vp), ("img_page", _vp), ("q_page", _vp), ("o_sb", _i64),
+        ("row_counts", _vp),
+        ("image_token_id", _i64), ("page_token_id", _i64),
+        ("B", _i32), ("L", _i32), ("n_ids", _i32), ("per_page", _i32), ("page_scope_prefill", _i32),
+    ]
+
+
+class PagePosArgs(ctypes.Structure):
+    """Mirror of ``srswa_page_pos_args``."""
+
+    _fields_ = [
+        ("ids", _vp), ("ids_i64", _i32), ("id_sb", _i64),
+        ("page", _vp), ("prefill", _vp), ("o_sb", _i64),
+        ("row_info", _vp),
+        ("tok", _vp),
+        ("pf_cnt", _vp), ("pf_sb", _i64),
+        ("image_token_id", _i64), ("page_token_id", _i64),
+        ("B", _i32), ("L", _i32), ("n_ids", _i32), ("n_pg", _i32),
+    ]
+
+
 class PageMetaArgs(ctypes.Structure):
     """Mirror of ``srswa_page_meta_args``."""
 
@@ -535,6 +590,11 @@ SIGNATURES = {
     "srswa_gather_decode_paged_workspace": (ctypes.c_size_t, [ctypes.POINTER(PagedDecodeArgs)]),
     "srswa_gather_decode_paged": (ctypes.c_int, [ctypes.POINTER(PagedDecodeArgs), _vp, ctypes.c_size_t, _vp]),
     "srswa_page_decode_meta": (ctypes.c_int, [ctypes.POINTER(PageMetaArgs), _vp]),
+    "srswa_page_step": (ctypes.c_int, [ctypes.POINTER(PageStepArgs), _vp]),
+    "srswa_coord_step": (ctypes.c_int, [ctypes.POINTER(CoordStepArgs), _vp]),
+    "srswa_page_ids": (ctypes.c_int, [ctypes.POINTER(PageIdsArgs), _vp]),
+    "srswa_page_rope_pos": (ctypes.c_int, [ctypes.POINTER(PagePosArgs), _vp]),
+    "srswa_page_rope_tok": (ctypes.c_int, [ctypes.POINTER(PagePosArgs), _vp]),
     "srswa_page_decode_allow_workspace": (ctypes.c_int, [ctypes.POINTER(PageAllowArgs), _szp]),
     "srswa_page_decode_allow": (ctypes.c_int, [ctypes.POINTER(PageAllowArgs), _vp, ctypes.c_size_t, _vp]),
     "srswa_page_local_union": (ctypes.c_int, [ctypes.POINTER(LocalUnionArgs), _vp]),
@@ -564,7 +624,9 @@ STRUCTS = {"srswa_decode_args": DecodeArgs, "srswa_index_args": IndexArgs,
            "srswa_dash_route_train_args": DashRouteTrainArgs,
            "srswa_dash_route_train_bwd_args": DashRouteTrainBwdArgs,
            "srswa_dash_select_train_args": DashSelectTrainArgs,
-           "srswa_page_meta_args": PageMetaArgs,
+           "srswa_page_meta_args": PageMetaArgs, "srswa_page_step_args": PageStepArgs,
+           "srswa_coord_step_args": CoordStepArgs, "srswa_page_ids_args": PageIdsArgs,
+           "srswa_page_pos_args": PagePosArgs,
            "srswa_page_allow_args": PageAllowArgs, "srswa_local_union_args": LocalUnionArgs,
            "srswa_cos_sin_args": CosSinArgs, "srswa_rope_args": RopeArgs,
            "srswa_block_bounds_args": BlockBoundsArgs, "srswa_candidate_args": CandidateArgs,

@@ -12,6 +12,13 @@ which ``srswa.patch`` passes in as ``orig``:
 * ``apply_rotary_pos_emb``     -- transformers' llama ``apply_rotary_pos_emb`` as the
   indexer imports it (HF/_sparse_base_impl.py:39-41, applied at :3049)
 * ``uocr_dash_decode_allow``   -- ``_uocr_dash_decode_allow`` (HF/modeling_unlimitedocr.py:481-528)
+* ``build_page_aware_ids``     -- ``DeepseekV2Indexer._build_page_aware_ids`` (HF/_sparse_base_impl.py:2404-2502)
+* ``build_page_rope_pos``      -- ``DeepseekV2Indexer._build_page_rope_pos`` with ``_page_rope_offsets``
+  (HF/_sparse_base_impl.py:2511-2570)
+
+The two prompt-wide builders print a one-shot diagnostic in the reference;
+their first call on a model goes to the original (which prints it and sets
+the model's flag), every later call runs the kernels.
 """
 
 from __future__ import annotations
@@ -113,3 +120,63 @@ def uocr_dash_decode_allow(indexer, input_ids, cache):
     nblk = -(-total // bs)
     out = page_ops.page_candidate_mask(st["bounds"], None, qp, None, nblk=nblk, block_size=bs, range_test=True)
     return out[:, 0]
+
+
+@torch.no_grad()
+def build_page_aware_ids(self, source_input_ids, img_context_token_id, page_token_id, key_length, *,
+                         page_scope_prefill=True):
+    """(image_token_mask, image_token_page_ids, query_token_page_ids) [B,
+    key_length], or (None, None, None) as the reference (nothing to
+    constrain); one read-back of the per-row counts for that test, as the
+    reference's own ``.sum() == 0`` checks."""
+    if source_input_ids is None or img_context_token_id is None or page_token_id is None:
+        return None, None, None
+    if source_input_ids.ndim != 2:
+        return None, None, None
+    device = self.q_proj.weight.device
+    if device.type != "cuda":
+        raise UnsupportedShape("host model")
+    img, ipage, qpage, counts = page_ops.page_aware_ids(
+        source_input_ids, image_token_id=int(img_context_token_id), page_token_id=int(page_token_id),
+        key_length=int(key_length), per_page=max(1, int(self.per_page_image_tokens)),
+        page_scope_prefill=page_scope_prefill, device=device)
+    nq, ni = (int(x) for x in counts.sum(0).tolist())
+    if ni == 0 or nq == 0:
+        return None, None, None
+    return img, ipage, qpage
+
+
+@torch.no_grad()
+def build_page_rope_pos(self, source_input_ids, key_length):
+    """(tok_pos, page_pos) [B, key_length] int64 for the 2-axis indexer RoPE,
+    or the reference's bail (``self._page_rope_bail``) where it bails; sets
+    ``self._page_rope_meta`` as ``_page_rope_offsets`` does."""
+    if source_input_ids is None or getattr(source_input_ids, "ndim", 0) != 2:
+        return self._page_rope_bail("no source_input_ids")
+    if self.image_token_id is None or self.page_token_id is None:
+        return self._page_rope_bail("image_token_id / page_token_id unavailable")
+    device = self.q_proj.weight.device
+    if device.type != "cuda":
+        raise UnsupportedShape("host model")
+    page, pre, info = page_ops.page_rope_pos(source_input_ids, image_token_id=int(self.image_token_id),
+                                             page_token_id=int(self.page_token_id), key_length=int(key_length),
+                                             device=device)
+    inf = info.cpu()                                   # the reference's data-dependent checks
+    if not bool(inf[:, 2].any()) or not bool(inf[:, 3].any()):
+        return self._page_rope_bail("row has no image token / no <PAGE> marker")
+    if not bool((inf[:, 0] > 0).all()):
+        return self._page_rope_bail("non-marker mode (prompt carries no <PAGE>)")
+    n_pg = int(inf[:, 1].max()) + 1
+    tok, pf_cnt = page_ops.page_rope_tok(page, pre, n_pg)
+    page = page.to(torch.int64)
+    self._page_rope_meta = {"pf_cnt": pf_cnt, "n_pg": n_pg}
+    if getattr(self, "rope_page_span", 0) > 0:
+        # the span-normalisation ablation of _page_rope_offsets, on the kernel's counts
+        in_prefill = pre.bool()
+        pf_k = pf_cnt.gather(1, page)
+        s_span = float(self.rope_page_span)
+        scaled_pre = torch.round(tok.float() * s_span / pf_k.clamp(min=1).float())
+        post = s_span + (tok - pf_k).float()
+        scaled = torch.where(in_prefill, scaled_pre, post).to(torch.int64)
+        tok = torch.where(page > 0, scaled, tok)
+    return tok, page

@@ -294,3 +294,140 @@ def page_candidate_mask(bounds, ids, qpage, pos=None, *, nblk, block_size, range
                            block_size=int(block_size), range_test=int(bool(range_test)))
     _run("srswa_page_candidate_mask", a, device=bounds.device)
     return out
+
+
+# ---------------------------------------------------------------------------
+# multi-token steps: serving page state / coordinates, HF prompt-wide ids
+# ---------------------------------------------------------------------------
+def _i64vec(t: torch.Tensor) -> torch.Tensor:
+    t = t.to(torch.int64)
+    return t if t.is_contiguous() else t.contiguous()
+
+
+def page_step(input_ids, q_start, start_pos, block_table, slot_mapping, *, s_page, s_mark, s_run, s_pp,
+              image_token_id, page_token_id, per_page, block_size, num_decode_tokens=0, gen_start=None,
+              n_slots=None, out_q_page=None):
+    """Multi-token page-state step (``srswa_page_step``): q_page int32 [T]
+    for the T tokens of ``input_ids`` laid out by ``q_start`` [R + 1] /
+    ``start_pos`` [R]; the per-slot state ``s_*`` is updated in place."""
+    _cuda(input_ids, q_start, start_pos, block_table, slot_mapping, s_page, gen_start)
+    T = int(input_ids.shape[0])
+    R = int(start_pos.shape[0])
+    dev = input_ids.device
+    ids, ids64 = _vec(input_ids)
+    qs, sp = _i64vec(q_start), _i64vec(start_pos)
+    gs = None if gen_start is None else _i64vec(gen_start)
+    bt, bt64 = _ix(block_table)
+    sm, sm64 = _vec(slot_mapping[:T])
+    for t, n in ((s_page, "s_page"), (s_mark, "s_mark"), (s_run, "s_run"), (s_pp, "s_pp")):
+        _state(t, n)
+    q_page = out_q_page[:T] if out_q_page is not None and out_q_page.shape[0] >= T else \
+        torch.empty(T, dtype=torch.int32, device=dev)
+    a = _lib.PageStepArgs(
+        input_ids=ids.data_ptr(), ids_i64=ids64, q_start=qs.data_ptr(), start_pos=sp.data_ptr(),
+        gen_start=_lib.ptr(gs), block_table=bt.data_ptr(), bt_i64=bt64, bt_sr=bt.stride(0),
+        slot_mapping=sm.data_ptr(), slot_i64=sm64, s_page=s_page.data_ptr(), s_mark=s_mark.data_ptr(),
+        s_run=s_run.data_ptr(), s_pp=s_pp.data_ptr(), q_page=q_page.data_ptr(),
+        image_token_id=int(image_token_id), page_token_id=int(page_token_id or 0),
+        num_decode_tokens=int(num_decode_tokens), R=R, T=T, bt_w=int(bt.shape[1]),
+        n_slots=min(int(n_slots or s_page.numel()), s_page.numel()), block_size=int(block_size),
+        per_page=max(1, int(per_page)), has_marker=int(page_token_id is not None))
+    _run("srswa_page_step", a, device=dev)
+    return q_page
+
+
+def coord_step(input_ids, q_start, start_pos, rows, *, st_marker, st_pp, cnt, image_token_id, page_token_id,
+               num_decode_tokens=0, gen_start=None, with_carry=False):
+    """The scans, ranks and carry of a Page2D coordinate step
+    (``srswa_coord_step``) for state rows ``rows`` [R]: (tok int64 [T],
+    page int64 [T]) and, with ``with_carry``, marker / pp int32 [T]; the row
+    state is updated in place."""
+    _cuda(input_ids, q_start, start_pos, rows, st_marker, cnt, gen_start)
+    T = int(input_ids.shape[0])
+    R = int(start_pos.shape[0])
+    dev = input_ids.device
+    ids, ids64 = _vec(input_ids)
+    qs, sp, rw = _i64vec(q_start), _i64vec(start_pos), _i64vec(rows)
+    gs = None if gen_start is None else _i64vec(gen_start)
+    _state(st_marker, "st_marker")
+    _state(st_pp, "st_pp")
+    if cnt.dtype != torch.int32 or cnt.dim() != 2 or cnt.stride(1) != 1:
+        raise ValueError("cnt must be an int32 [rows, pages] tensor with unit inner stride")
+    tok = torch.empty(T, dtype=torch.int64, device=dev)
+    page = torch.empty(T, dtype=torch.int64, device=dev)
+    mk = torch.empty(T, dtype=torch.int32, device=dev) if with_carry else None
+    pp = torch.empty(T, dtype=torch.int32, device=dev) if with_carry else None
+    a = _lib.CoordStepArgs(
+        input_ids=ids.data_ptr(), ids_i64=ids64, q_start=qs.data_ptr(), start_pos=sp.data_ptr(),
+        gen_start=_lib.ptr(gs), row=rw.data_ptr(), st_marker=st_marker.data_ptr(), st_pp=st_pp.data_ptr(),
+        cnt=cnt.data_ptr(), cnt_sr=cnt.stride(0), tok=tok.data_ptr(), page=page.data_ptr(),
+        marker_out=_lib.ptr(mk), pp_out=_lib.ptr(pp), image_token_id=int(image_token_id),
+        page_token_id=int(page_token_id or 0), num_decode_tokens=int(num_decode_tokens), R=R, T=T,
+        n_rows=min(st_marker.numel(), st_pp.numel(), int(cnt.shape[0])), pages=int(cnt.shape[1]),
+        has_marker=int(page_token_id is not None))
+    _run("srswa_coord_step", a, device=dev)
+    return (tok, page, mk, pp) if with_carry else (tok, page)
+
+
+def _ids2d(ids, key_length, device):
+    t = ids.to(device)
+    if t.dtype not in (torch.int32, torch.int64):
+        t = t.to(torch.int64)
+    if t.stride(-1) != 1:
+        t = t.contiguous()
+    return t, int(t.dtype == torch.int64), min(int(t.shape[-1]), int(key_length))
+
+
+def page_aware_ids(source_ids, *, image_token_id, page_token_id, key_length, per_page, page_scope_prefill=True,
+                   device=None):
+    """Prompt-wide page ids (``srswa_page_ids``): (image_token_mask bool,
+    image_token_page_ids int64, query_token_page_ids int64) [B, key_length]
+    and the per-row counts [B, 2] int32 (query tokens with a page, image tokens)."""
+    dev = device or source_ids.device
+    ids, ids64, n_ids = _ids2d(source_ids, key_length, dev)
+    _cuda(ids)
+    B, L = int(ids.shape[0]), int(key_length)
+    img = torch.empty(B, L, dtype=torch.bool, device=dev)
+    ipage = torch.empty(B, L, dtype=torch.int64, device=dev)
+    qpage = torch.empty(B, L, dtype=torch.int64, device=dev)
+    counts = torch.empty(B, 2, dtype=torch.int32, device=dev)
+    a = _lib.PageIdsArgs(ids=ids.data_ptr(), ids_i64=ids64, id_sb=ids.stride(0), img_mask=img.data_ptr(),
+                         img_page=ipage.data_ptr(), q_page=qpage.data_ptr(), o_sb=L, row_counts=counts.data_ptr(),
+                         image_token_id=int(image_token_id), page_token_id=int(page_token_id), B=B, L=L,
+                         n_ids=n_ids, per_page=max(1, int(per_page)), page_scope_prefill=int(bool(page_scope_prefill)))
+    _run("srswa_page_ids", a, device=dev)
+    return img, ipage, qpage, counts
+
+
+def page_rope_pos(source_ids, *, image_token_id, page_token_id, key_length, device=None):
+    """Prompt-wide Page2D positions: pass 1 (``srswa_page_rope_pos``) gives
+    page / in_prefill [B, L] and the per-row info [B, 4] (n_pages, max page,
+    any image, any marker); the caller reads it back (the reference's own
+    data-dependent checks) and, unless it bails, calls ``page_rope_tok``."""
+    dev = device or source_ids.device
+    ids, ids64, n_ids = _ids2d(source_ids, key_length, dev)
+    _cuda(ids)
+    B, L = int(ids.shape[0]), int(key_length)
+    page = torch.empty(B, L, dtype=torch.int32, device=dev)
+    pre = torch.empty(B, L, dtype=torch.uint8, device=dev)
+    info = torch.empty(B, 4, dtype=torch.int32, device=dev)
+    a = _lib.PagePosArgs(ids=ids.data_ptr(), ids_i64=ids64, id_sb=ids.stride(0), page=page.data_ptr(),
+                         prefill=pre.data_ptr(), o_sb=L, row_info=info.data_ptr(),
+                         image_token_id=int(image_token_id), page_token_id=int(page_token_id), B=B, L=L,
+                         n_ids=n_ids, n_pg=0)
+    _run("srswa_page_rope_pos", a, device=dev)
+    return page, pre, info
+
+
+def page_rope_tok(page, prefill, n_pg):
+    """Pass 2: (tok int64 [B, L] running count inside each page bucket,
+    pf_cnt int64 [B, n_pg] prefill tokens per page)."""
+    _cuda(page, prefill)
+    B, L = int(page.shape[0]), int(page.shape[1])
+    dev = page.device
+    tok = torch.empty(B, L, dtype=torch.int64, device=dev)
+    pf = torch.empty(B, int(n_pg), dtype=torch.int32, device=dev)
+    a = _lib.PagePosArgs(page=page.data_ptr(), prefill=prefill.data_ptr(), o_sb=L, tok=tok.data_ptr(),
+                         pf_cnt=pf.data_ptr(), pf_sb=int(n_pg), B=B, L=L, n_pg=int(n_pg))
+    _run("srswa_page_rope_tok", a, device=dev)
+    return tok, pf.to(torch.int64)

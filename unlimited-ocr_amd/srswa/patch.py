@@ -14,7 +14,8 @@ two kernel files (those are replaced file-for-file by
 * ``_infer_route_select``  (HF/modeling_deepseekv2.py:338-362) -> ``srswa.ops.dash_route``
 * page isolation and the Page2D indexer RoPE of ``_sparse_base_impl`` (reached as
   ``modeling_deepseekv2._base``): ``DeepseekV2Indexer._build_kl_candidate_mask``
-  (HF/_sparse_base_impl.py:2706-2737), ``DeepseekV2IndexerRotary2D.forward``
+  (HF/_sparse_base_impl.py:2706-2737), ``_build_page_aware_ids`` (:2404-2502),
+  ``_build_page_rope_pos`` (:2511-2570), ``DeepseekV2IndexerRotary2D.forward``
   (:2046-2061) and the module's ``_llama_apply_rotary_pos_emb`` (:39-41)
   -> ``srswa.page_isolation``; with ``modeling_unlimitedocr`` given, also its
   ``_uocr_dash_decode_allow`` (HF/modeling_unlimitedocr.py:481-528)
@@ -112,6 +113,31 @@ def _page_isolation(mod, base, done: list) -> None:
                             image_token_page_ids, query_token_page_ids)
             return _build_kl_candidate_mask
         _rebind(indexer_cls, "_build_kl_candidate_mask", make_mask, done, "DeepseekV2Indexer._build_kl_candidate_mask")
+    if indexer_cls is not None:
+        def make_ids(orig):
+            def _build_page_aware_ids(self, source_input_ids, img_context_token_id, page_token_id, key_length):
+                # the first call prints the reference's one-shot diagnostic
+                if getattr(self, "_page_aware_diag_logged", False) and source_input_ids is not None:
+                    try:
+                        return page_isolation.build_page_aware_ids(
+                            self, source_input_ids, img_context_token_id, page_token_id, key_length,
+                            page_scope_prefill=bool(getattr(base, "_PAGE_SCOPE_PREFILL", True)))
+                    except UnsupportedShape:
+                        pass
+                return orig(self, source_input_ids, img_context_token_id, page_token_id, key_length)
+            return _build_page_aware_ids
+        _rebind(indexer_cls, "_build_page_aware_ids", make_ids, done, "DeepseekV2Indexer._build_page_aware_ids")
+
+        def make_pos(orig):
+            def _build_page_rope_pos(self, source_input_ids, key_length):
+                if getattr(self, "_page_rope_diag_logged", False) and source_input_ids is not None:
+                    try:
+                        return page_isolation.build_page_rope_pos(self, source_input_ids, key_length)
+                    except UnsupportedShape:
+                        pass
+                return orig(self, source_input_ids, key_length)
+            return _build_page_rope_pos
+        _rebind(indexer_cls, "_build_page_rope_pos", make_pos, done, "DeepseekV2Indexer._build_page_rope_pos")
     rot_cls = getattr(base, "DeepseekV2IndexerRotary2D", None)
     if rot_cls is not None:
         def make_rot(orig):
@@ -332,6 +358,8 @@ def restore(modeling_deepseekv2, modeling_unlimitedocr=None) -> None:
     mod = modeling_deepseekv2
     base = getattr(mod, "_base", None)
     for owner, name in ((getattr(base, "DeepseekV2Indexer", None), "_build_kl_candidate_mask"),
+                        (getattr(base, "DeepseekV2Indexer", None), "_build_page_aware_ids"),
+                        (getattr(base, "DeepseekV2Indexer", None), "_build_page_rope_pos"),
                         (getattr(base, "DeepseekV2Indexer", None), "select_and_kl_loss"),
                         (getattr(base, "DeepseekV2Indexer", None), "forward"),
                         (getattr(mod, "DashAttention", None), "_route"),
