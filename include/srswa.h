@@ -251,7 +251,9 @@ typedef struct {
   int32_t dtype;                                       /* as srswa_fwd_args (bf16, fp16, fp32) */
 } srswa_bwd_args;
 
-/* scratch bytes: delta [B, T, HQ] fp32 + q*scale [B, HQ, T, D] in the input
+/* scratch bytes: per-row records for the dK / dV kernel (lse, delta and
+ * sample start per (sequence, query head, row); the first 8 slot ids and
+ * biases per (sequence, index head, row)) + q*scale [B, HQ, T, D] in the input
  * dtype (the dK / dV operand) + the query-tile touch bitmap */
 size_t srswa_gather_bwd_workspace(const srswa_bwd_args* a);
 int srswa_gather_bwd(const srswa_bwd_args* a, void* scratch, size_t scratch_bytes, void* stream);

@@ -15,8 +15,9 @@
 //      content does not depend on the order of the atomic ORs.
 //   2. dq_kernel  -- per 64-row query tile, the forward's chunk plan.  Its
 //      set-up computes each row's delta = sum_d O*dO in fp32 and q*scale
-//      rounded to the input dtype, and writes both for the dK / dV kernel
-//      (delta [B, T, HQ], q*scale [B, HQ, T, D]).  Per chunk
+//      rounded to the input dtype, and writes for the dK / dV kernel
+//      q*scale [B, HQ, T, D], a 16-byte record per row (lse, delta, sample
+//      start) and, per index head, the rows' first slot ids and biases.  Per chunk
 //      S^T = K Q^T, dP^T = V dO^T, dS = P (dP - delta), dQ^T += K^T dS^T; the
 //      bias gradient (sum of fp32 dS over the remote keys of a selected block)
 //      is summed per (row, slot) in LDS and written once per query head --
@@ -41,12 +42,19 @@ struct BwdK {
   int ntiles, nchunk, nwords, umax, twords, SP, bs_shift;
   int G, IG;
   int nlogical, per_xcd;          // dQ workgroups (sequence, query head, tile), XCD-aware order
-  int nlogical_kv, per_xcd_kv;    // dK/dV workgroups (sequence, kv head, chunk)
+  int nlogical_kv;                // dK/dV workgroups (sequence, kv head, chunk)
   int chunks_off, sid_off;        // dQ LDS byte offsets of the chunk list and sorted ids
-  float* delta;       // [B, T, HQ]
+  int Tp;                         // T rounded up to whole tiles (rows of the row records)
+  // row records, written by dQ, read by dK / dV (one buffer resource over all three):
+  float4* rows;       // [B, HQ, Tp] {lse in log2 units (+inf past T), delta (0 past T), sample start, 0}
+  uint32_t ids_off;   // byte offset from `rows` of the slot records [B, HI, Tp, kPreSlots] int32 (-1 padded)
+  uint32_t bias_off;  // ... and of the bias records [B, HI, Tp, kPreSlots] fp32 (0 padded; with a bias)
+  uint32_t rec_bytes; // bytes of the three
   uint32_t* touch;    // [B, HI, nchunk, twords]
   void* qs;           // [B, HQ, T, D] q * scale rounded to the input dtype (dK / dV operand)
 };
+
+constexpr int kPreSlots = 8;   // slots per row in the slot records (the dK / dV kernel's first look)
 
 // -------------------------------------------------------------- 1. touch map
 __global__ __launch_bounds__(256) void zero_words_kernel(uint32_t* w, int64_t n) {
@@ -207,6 +215,27 @@ void dq_kernel(BwdK p) {
         a.bias ? a.bias + (int64_t)b * a.bias_sb + (int64_t)ih * a.bias_sh + (int64_t)(t0 + rr) * a.bias_st : nullptr;
     sort_row_ids(ids, bias, r < nrows ? a.S : 0, SP, BS, maxblk, qi, seg, ls, s_sid + r * SP,
                  s_sb ? s_sb + r * SP : nullptr, s_sslot ? s_sslot + r * SP : nullptr);
+    if (hq % p.IG == 0) {
+      // the slot records of this index head's rows (one query head writes them):
+      // the first kPreSlots ids and biases, -1 / 0 past S and past T
+      int id8[kPreSlots];
+      float b8[kPreSlots];
+#pragma unroll
+      for (int s = 0; s < kPreSlots; ++s) {
+        const bool in = r < nrows && s < a.S;
+        id8[s] = in ? ids[s] : -1;
+        b8[s] = in && bias ? bias[s] : 0.f;
+      }
+      const int64_t rec = ((int64_t)b * a.HI + ih) * p.Tp + t0 + r;
+      int4* ir = reinterpret_cast<int4*>(reinterpret_cast<char*>(p.rows) + p.ids_off) + rec * 2;
+      ir[0] = make_int4(id8[0], id8[1], id8[2], id8[3]);
+      ir[1] = make_int4(id8[4], id8[5], id8[6], id8[7]);
+      if (bias) {
+        float4* br = reinterpret_cast<float4*>(reinterpret_cast<char*>(p.rows) + p.bias_off) + rec * 2;
+        br[0] = make_float4(b8[0], b8[1], b8[2], b8[3]);
+        br[1] = make_float4(b8[4], b8[5], b8[6], b8[7]);
+      }
+    }
     if (s_sdb)
       for (int i = 0; i < SP; ++i) s_sdb[r * SP + i] = 0.f;
   }
@@ -258,7 +287,8 @@ void dq_kernel(BwdK p) {
     }
     if (row_ok) *reinterpret_cast<Frag<T>*>(qsrow + 16 * ks + 8 * h) = qf[ks];
   }
-  if (row_ok && h == 0) p.delta[((int64_t)b * a.T + trow) * a.HQ + hq] = dlt;
+  // this row's record for the dK / dV kernel (rows past T too: +inf, 0, 0)
+  if (h == 0) p.rows[((int64_t)b * a.HQ + hq) * p.Tp + t0 + row] = make_float4(lse_l2, dlt, __int_as_float(w.seg), 0.f);
 
   f32x16_t dq[MT];
 #pragma unroll
@@ -419,7 +449,15 @@ void dq_kernel(BwdK p) {
 }
 
 // -------------------------------------------------------------- 3. dK / dV
-constexpr int kPreSlots = 8;          // selected ids per row fetched one visit ahead
+
+// bits [lo, hi) of a 32-bit word, the bounds clamped to [0, 32]
+__device__ __forceinline__ uint32_t span32(int lo, int hi) {
+  lo = min(max(lo, 0), 32);
+  hi = min(max(hi, 0), 32);
+  const uint32_t above = lo >= 32 ? 0u : (~0u << lo);
+  const uint32_t below = hi >= 32 ? ~0u : ~(~0u << hi);
+  return above & below;
+}
 
 // One workgroup = (sequence, kv head, 64-key chunk), four waves.  For every
 // query head of the group, the query tiles whose windows cover the chunk or
@@ -430,10 +468,10 @@ constexpr int kPreSlots = 8;          // selected ids per row fetched one visit 
 //     softmax -> P (fp32, published through LDS), dV^T += dO^T P;
 //   role B (waves 2, 3): V of its keys; dP = dO V^T, then dS = P (dP - delta)
 //     from the published P, dK^T += (q*scale)^T dS.
-// Per visit: stage Q / dO | S (A) and dP (B) | the softmax (A) while wave 3
-// (B, which waits for P anyway) derives the NEXT visit's row data (keep masks,
-// lse, delta, bias) into the other of two buffers | barrier | dV (A), dS and
-// dK (B).  A lane
+// Per visit: stage Q / dO | S (A) and dP (B) | the softmax (A) while the
+// role-B waves (which wait for P anyway) derive the NEXT visit's row data
+// (keep masks and biases of their key half, lse, delta) into the other of two
+// buffers | barrier | dV (A), dS and dK (B).  A lane
 // holds the same (row, key) elements in both roles (the same MFMA shape), so
 // role B reads role A's P lane for lane.
 template <int D, int ES = 2> struct DkvLds {
@@ -459,12 +497,16 @@ void dkv_kernel(BwdK p) {
   constexpr int KS = D / 16, MT = D / 32, NT = 256;
   constexpr int PPT = kTileRows * D / 8 / NT;
   constexpr int RPP = NT / (D / 8);
-  constexpr int kMaskWave = 3;
   extern __shared__ __align__(16) unsigned char smem[];
   const srswa_bwd_args& a = p.a;
 
-  const int lid = (int)(blockIdx.x & 7) * p.per_xcd_kv + (int)(blockIdx.x >> 3);
-  if (lid >= p.nlogical_kv) return;
+  // chunk-ascending dispatch (every (sequence, kv head) of chunk 0 first, ...,
+  // consecutive workgroups on different XCDs): the early chunks, which every
+  // later tile can select, have the longest visit lists and start first, so
+  // the last workgroups to start are short ones
+  const int g = (int)blockIdx.x, BK = p.nlogical_kv / p.nchunk;
+  if (g >= p.nlogical_kv) return;
+  const int lid = (g % BK) * p.nchunk + g / BK;
 
   T* sQ = reinterpret_cast<T*>(smem);
   T* sG = reinterpret_cast<T*>(smem + L::gOff);
@@ -490,10 +532,11 @@ void dkv_kernel(BwdK p) {
   const bool key_ok = jmine < a.Sk;
   const int off = a.Sk - a.T;
   const int LW = a.local_window, S = a.S;
-  const int maxblk = (a.Sk - 1) >> p.bs_shift;
   const int myq = kk >> 4;                     // this key's 16-key quarter
-  const int qb0 = j0 >> p.bs_shift;            // block of the chunk's first quarter
-  const bool one_blk = ((j0 + kChunk - 1) >> p.bs_shift) == qb0;   // block size >= 64
+  // role B: this key half's first key and the blocks of its two 16-key
+  // quarters (a quarter past the keys has no remote bits, whatever matches it)
+  const int hj0 = j0 + 32 * kh;
+  const int qa = hj0 >> p.bs_shift, qb = (hj0 + 16) >> p.bs_shift;
 
   // role A: K of this lane's key; role B: V
   Frag<T> kv[KS];
@@ -525,25 +568,42 @@ void dkv_kernel(BwdK p) {
   float4* sPl = sP + kh * 8 * 64 + lane;       // this lane's P records
   __shared__ int s_ntiles;
   Frag<T> qpre[PPT], gpre[PPT];
+  const __amdgpu_buffer_rsrc_t rrs = make_rsrc(p.rows, p.rec_bytes);   // row and slot records
 
   for (int gq = 0; gq < p.G; ++gq) {
     const int hq = kvh * p.G + gq;
     const int ih = hq / p.IG;
     const uint32_t* tb = p.touch + (((int64_t)b * a.HI + ih) * p.nchunk + c) * p.twords;
     __syncthreads();
-    if (tid == 0) {
+    if (wave == 0) {
+      // the visit list: window tiles | touched tiles, ascending; lane = 32-tile
+      // word (all words loaded at once), positions from a prefix sum of counts
       int n = 0;
-      for (int wd = 0; wd < p.twords; ++wd) {
-        uint32_t bits = tb[wd];
-        const int lo = max(tau_a - 32 * wd, 0), hi = min(tau_b - 32 * wd, 31);
-        if (lo <= hi) bits |= (hi - lo == 31) ? 0xffffffffu : (((1u << (hi - lo + 1)) - 1u) << lo);
-        while (bits) {
-          const int tau = 32 * wd + __ffs(bits) - 1;
-          bits &= bits - 1;
-          if (tau < p.ntiles) s_tiles[n++] = tau;
+      for (int w0 = 0; w0 < p.twords; w0 += kWave) {
+        const int wd = w0 + lane;
+        uint32_t bits = 0u;
+        if (wd < p.twords) {
+          bits = tb[wd];
+          const int lo = max(tau_a - 32 * wd, 0), hi = min(tau_b - 32 * wd, 31);
+          if (lo <= hi) bits |= (hi - lo == 31) ? 0xffffffffu : (((1u << (hi - lo + 1)) - 1u) << lo);
+          const int nvalid = p.ntiles - 32 * wd;
+          if (nvalid < 32) bits &= (1u << nvalid) - 1u;
         }
+        const int cnt = __popc(bits);
+        int incl = cnt;
+#pragma unroll
+        for (int o = 1; o < kWave; o <<= 1) {
+          const int y = __shfl_up(incl, o, kWave);
+          if (lane >= o) incl += y;
+        }
+        int pos = n + incl - cnt;
+        while (bits) {
+          s_tiles[pos++] = 32 * wd + __ffs(bits) - 1;
+          bits &= bits - 1;
+        }
+        n += __shfl(incl, kWave - 1, kWave);
       }
-      s_ntiles = n;
+      if (lane == 0) s_ntiles = n;
     }
     __syncthreads();
     const int nt = s_ntiles;
@@ -571,106 +631,96 @@ void dkv_kernel(BwdK p) {
         }
       }
     };
-    // row data of a tile for the mask wave (lane = row): sample start, lse
-    // (log2 units, +inf past T), delta and the first kPreSlots ids / biases
-    int pf_seg = 0, pf_id[kPreSlots];
-    float pf_lse = INFINITY, pf_dlt = 0.f, pf_b[kPreSlots];
+    // row data of a tile for the role-B waves (lane = row): its row record
+    // (lse, delta, sample start) and slot record (the first kPreSlots ids and
+    // biases), five 16-byte buffer loads with scalar tile offsets.  Nothing is
+    // computed from a loaded value here: that would wait for the load at once,
+    // and with it for the Q / dO prefetch issued just before.  Without a bias
+    // the bias loads read the slot record again (row_masks then ignores them).
+    const uint32_t row_so = (uint32_t)(((int64_t)b * a.HQ + hq) * p.Tp) * 16u;
+    const uint32_t ids_so = p.ids_off + (uint32_t)(((int64_t)b * a.HI + ih) * p.Tp) * 32u;
+    const uint32_t bias_so = (a.bias ? p.bias_off - p.ids_off : 0u) + ids_so;
+    uint4 pf_rec, pf_i0, pf_i1, pf_b0, pf_b1;
     auto rfetch = [&](int tau) {
-      const int t = tau * kTileRows + lane;
-      const bool valid = t < a.T;
-      const int tt = valid ? t : 0;
-      pf_seg = (valid && a.seg) ? a.seg[(int64_t)b * a.seg_sb + tt] : 0;
-      pf_lse = valid ? a.lse[(int64_t)b * a.lse_sb + (int64_t)tt * a.lse_st + (int64_t)hq * a.lse_sh] * kLog2e : INFINITY;
-      pf_dlt = valid ? p.delta[((int64_t)b * a.T + tt) * a.HQ + hq] : 0.f;
-      const int32_t* ids = a.idx + (int64_t)b * a.idx_sb + (int64_t)ih * a.idx_sh + (int64_t)tt * a.idx_st;
-      const float* bias = a.bias ? a.bias + (int64_t)b * a.bias_sb + (int64_t)ih * a.bias_sh + (int64_t)tt * a.bias_st : nullptr;
-#pragma unroll
-      for (int s = 0; s < kPreSlots; ++s) {
-        pf_id[s] = (valid && s < S) ? ids[s] : -1;
-        pf_b[s] = (valid && s < S && bias) ? bias[s] : 0.f;
-      }
+      const uint32_t t16 = (uint32_t)tau * kTileRows * 16u, t32 = 2u * t16;
+      pf_rec = buffer_load16(rrs, lane * 16u, row_so + t16);
+      pf_i0 = buffer_load16(rrs, lane * 32u, ids_so + t32);
+      pf_i1 = buffer_load16(rrs, lane * 32u + 16u, ids_so + t32);
+      pf_b0 = buffer_load16(rrs, lane * 32u, bias_so + t32);
+      pf_b1 = buffer_load16(rrs, lane * 32u + 16u, bias_so + t32);
     };
-    // the mask wave: row data of visit `v` (fetched by rfetch) into buffer v & 1,
-    // then the fetch of visit v + 1
+    // the role-B wave of key half kh: row data of visit v for the half's 32
+    // keys into buffer v & 1 -- keep / remote bits, the biases of its two
+    // 16-key quarters, the lse (kh 0) or delta (kh 1), whether every row keeps
+    // the half whole -- then the loads of visit v + 1's row data.  Both role-B
+    // waves wait for P in this phase anyway.
     auto row_masks = [&](int v) {
       const int buf = v & 1;
       const int t0 = s_tiles[v] * kTileRows;
       const int nrows = min(kTileRows, a.T - t0);
       const int r = lane;
-      uint64_t keep = 0ull, rm = 0ull;
-      float bqv[4] = {0.f, 0.f, 0.f, 0.f};
+      uint32_t keep = 0u, rm = 0u;
+      float b0 = 0.f, b1 = 0.f;
       if (r < nrows) {
-        const int t = t0 + r;
-        const int qi = off + t;
-        const int seg = pf_seg;
+        const int qi = off + t0 + r;
+        const int seg = (int)pf_rec.z;
         const int ls = max(qi - LW + 1, seg);
-        uint32_t qmem = 0;
-        auto take = [&](int id, float bv) {
-          if (id < 0 || id > maxblk) return;
+        const int pf_id[kPreSlots] = {(int)pf_i0.x, (int)pf_i0.y, (int)pf_i0.z, (int)pf_i0.w,
+                                      (int)pf_i1.x, (int)pf_i1.y, (int)pf_i1.z, (int)pf_i1.w};
+        const uint32_t pf_b[kPreSlots] = {pf_b0.x, pf_b0.y, pf_b0.z, pf_b0.w, pf_b1.x, pf_b1.y, pf_b1.z, pf_b1.w};
+        // the first slot holding each quarter's block (the scan runs down, so
+        // the lowest matching slot's bias stays)
+        bool m0 = false, m1 = false;
 #pragma unroll
-          for (int qq = 0; qq < 4; ++qq)
-            if (id == ((j0 + 16 * qq) >> p.bs_shift) && !(qmem & (1u << qq))) {   // first slot wins
-              qmem |= 1u << qq;
-              bqv[qq] = bv * kLog2e;
-            }
-        };
-        if (one_blk) {
-          // the chunk lies in one block: one compare per slot, first slot's bias
-          bool found = false;
-          float bv = 0.f;
-#pragma unroll
-          for (int s = 0; s < kPreSlots; ++s) {
-            const bool hit = pf_id[s] == qb0;
-            bv = (hit && !found) ? pf_b[s] : bv;
-            found = found || hit;
-          }
-          if (S > kPreSlots) {
-            const int32_t* ids = a.idx + (int64_t)b * a.idx_sb + (int64_t)ih * a.idx_sh + (int64_t)t * a.idx_st;
-            const float* bias = a.bias ? a.bias + (int64_t)b * a.bias_sb + (int64_t)ih * a.bias_sh + (int64_t)t * a.bias_st : nullptr;
-            for (int s = kPreSlots; s < S && !found; ++s)
-              if (ids[s] == qb0) {
-                found = true;
-                bv = bias ? bias[s] : 0.f;
-              }
-          }
-          if (found) {
-            qmem = 0xfu;
-#pragma unroll
-            for (int qq = 0; qq < 4; ++qq) bqv[qq] = bv * kLog2e;
-          }
-        } else {
-#pragma unroll
-          for (int s = 0; s < kPreSlots; ++s) take(pf_id[s], pf_b[s]);
-          if (S > kPreSlots) {
-            const int32_t* ids = a.idx + (int64_t)b * a.idx_sb + (int64_t)ih * a.idx_sh + (int64_t)t * a.idx_st;
-            const float* bias = a.bias ? a.bias + (int64_t)b * a.bias_sb + (int64_t)ih * a.bias_sh + (int64_t)t * a.bias_st : nullptr;
-            for (int s = kPreSlots; s < S; ++s) take(ids[s], bias ? bias[s] : 0.f);
-          }
+        for (int s = kPreSlots - 1; s >= 0; --s) {
+          const bool h0 = pf_id[s] == qa, h1 = pf_id[s] == qb;
+          b0 = h0 ? __uint_as_float(pf_b[s]) : b0;
+          b1 = h1 ? __uint_as_float(pf_b[s]) : b1;
+          m0 = m0 || h0;
+          m1 = m1 || h1;
         }
-        uint64_t qm = 0;
-#pragma unroll
-        for (int qq = 0; qq < 4; ++qq)
-          if (qmem & (1u << qq)) qm |= 0xffffull << (16 * qq);
-        const uint64_t wm = range64(min(max(ls - j0, 0), 64), min(max(qi + 1 - j0, 0), 64));
-        rm = range64(min(max(seg - j0, 0), 64), min(max(min(ls, qi + 1) - j0, 0), 64)) & qm;
-        keep = wm | rm;
+        b0 *= kLog2e;
+        b1 *= kLog2e;
+        if (S > kPreSlots && !(m0 && m1)) {
+          // the remaining slots (read here; each value is used, and waited
+          // for, inside this branch, so the common path keeps its short wait)
+          const int32_t* ids = a.idx + (int64_t)b * a.idx_sb + (int64_t)ih * a.idx_sh + (int64_t)(t0 + r) * a.idx_st;
+          const float* bias = a.bias ? a.bias + (int64_t)b * a.bias_sb + (int64_t)ih * a.bias_sh + (int64_t)(t0 + r) * a.bias_st : nullptr;
+          for (int s = kPreSlots; s < S && !(m0 && m1); ++s) {
+            const int id = ids[s];
+            if (!m0 && id == qa) {
+              m0 = true;
+              b0 = bias ? bias[s] * kLog2e : 0.f;
+            }
+            if (!m1 && id == qb) {
+              m1 = true;
+              b1 = bias ? bias[s] * kLog2e : 0.f;
+            }
+          }
+          __builtin_amdgcn_s_waitcnt(0x0f70);   // vmcnt(0): nothing of this branch left in flight
+        }
+        b0 = (m0 && a.bias) ? b0 : 0.f;
+        b1 = (m1 && a.bias) ? b1 : 0.f;
+        const uint32_t qm = (m0 ? 0x0000ffffu : 0u) | (m1 ? 0xffff0000u : 0u);
+        rm = span32(seg - hj0, min(ls, qi + 1) - hj0) & qm;
+        keep = span32(ls - hj0, qi + 1 - hj0) | rm;
       }
-      s_keep(buf)[r] = (uint32_t)keep;
-      s_keep(buf)[64 + r] = (uint32_t)(keep >> 32);
-      s_rem(buf)[r] = (uint32_t)rm;
-      s_rem(buf)[64 + r] = (uint32_t)(rm >> 32);
-      s_lse(buf)[r] = pf_lse;
-      s_dlt(buf)[r] = pf_dlt;
-#pragma unroll
-      for (int qq = 0; qq < 4; ++qq) s_bq(buf)[qq * 64 + r] = bqv[qq];
-      const bool whole = r >= nrows || (keep == ~0ull && (!a.bias || rm == 0ull));
+      s_keep(buf)[64 * kh + r] = keep;
+      s_rem(buf)[64 * kh + r] = rm;
+      s_bq(buf)[(2 * kh) * 64 + r] = b0;
+      s_bq(buf)[(2 * kh + 1) * 64 + r] = b1;
+      if (kh == 0)
+        s_lse(buf)[r] = __uint_as_float(pf_rec.x);   // log2 units, +inf past T
+      else
+        s_dlt(buf)[r] = __uint_as_float(pf_rec.y);
+      const bool whole = r >= nrows || (keep == ~0u && (!a.bias || rm == 0u));
       const bool all = __all(whole);
-      if (r == 0) s_flag(buf)[0] = all ? 1 : 0;
+      if (r == 0) s_flag(buf)[kh] = all ? 1 : 0;
       if (v + 1 < nt) rfetch(s_tiles[v + 1]);
     };
     if (nt > 0) {
       fetch(s_tiles[0]);
-      if (wave == kMaskWave) {
+      if (role == 1) {
         rfetch(s_tiles[0]);
         row_masks(0);
       }
@@ -683,7 +733,10 @@ void dkv_kernel(BwdK p) {
         *reinterpret_cast<Frag<T>*>(sQw + i * RPP * QP) = qpre[i];
         *reinterpret_cast<Frag<T>*>(sGw + i * RPP * QP) = gpre[i];
       }
-      if (it + 1 < nt) fetch(s_tiles[it + 1]);
+      // issued on every visit (the last one fetches its own tile again, unused):
+      // with a fetch on some paths only, the row-data reads of phase 2 would
+      // wait for every load in flight, this prefetch included
+      fetch(s_tiles[min(it + 1, nt - 1)]);
       __syncthreads();
 
       // S = Q K^T (A) or dP = dO V^T (B): 64 rows x this lane's key; register r
@@ -696,7 +749,7 @@ void dkv_kernel(BwdK p) {
           sg[half] = M::mac(*reinterpret_cast<const Frag<T>*>(sX + (32 * half + rl) * QP + 16 * ks + 8 * h), kv[ks], sg[half]);
       }
       if (role == 0) {
-        const bool fast = s_flag(buf)[0] != 0;
+        const bool fast = s_flag(buf)[kh] != 0;   // every row keeps this key half whole
         const float* lse = s_lse(buf);
         // keep / remote bits of this lane's key for the 32 rows it holds in the
         // MFMA layout (bit 16 half + 4 r4 + e <-> row 32 half + 8 r4 + 4 h + e),
@@ -762,9 +815,9 @@ void dkv_kernel(BwdK p) {
         else
           softmax(std::false_type{});
       }
-      // the next visit's row data (the other buffer), on a role-B wave while
+      // the next visit's row data (the other buffer), on the role-B waves while
       // role A runs the softmax that role B waits for
-      if (wave == kMaskWave && it + 1 < nt) row_masks(it + 1);
+      if (role == 1 && it + 1 < nt) row_masks(it + 1);
       __syncthreads();   // P published; the next visit's row data written
       if (role == 1) {
         // sg <- dS = P (dP - delta) in place
@@ -897,6 +950,7 @@ void plan_bwd(const srswa_bwd_args* a, BwdK& k) {
   k.ntiles = ceil_div(a->T, kTileRows);
   k.nchunk = ceil_div(a->Sk, kChunk);
   k.nwords = ceil_div(k.nchunk, 32);
+  k.Tp = k.ntiles * kTileRows;
   const int64_t per_tile = (int64_t)kTileRows * a->S * (ceil_div(a->block_size, kChunk) + 1) +
                            ceil_div(a->local_window + kTileRows - 1, kChunk) + 1;
   k.umax = (int)std::min<int64_t>((int64_t)k.nchunk, per_tile);
@@ -908,7 +962,6 @@ void plan_bwd(const srswa_bwd_args* a, BwdK& k) {
   k.nlogical = (int)std::min<int64_t>((int64_t)a->B * a->HQ * k.ntiles, INT32_MAX);
   k.per_xcd = ceil_div(k.nlogical, 8);
   k.nlogical_kv = (int)std::min<int64_t>((int64_t)a->B * a->HKV * k.nchunk, INT32_MAX);
-  k.per_xcd_kv = ceil_div(k.nlogical_kv, 8);
   // dQ LDS: K / V tiles (the set-up arrays alias them), chunk list, sorted ids
   // (+ bias, + slot map and bias-gradient sums)
   const bool f32 = a->dtype == SRSWA_F32;
@@ -921,8 +974,10 @@ void plan_bwd(const srswa_bwd_args* a, BwdK& k) {
   k.sid_off = (int)n;
 }
 
-size_t delta_bytes(const BwdK& k) {
-  return ((size_t)k.a.B * k.a.T * k.a.HQ * 4 + 255) / 256 * 256;
+// the row records [B, HQ, Tp] x 16 B, then the slot and bias records [B, HI, Tp] x 32 B each
+size_t rec_bytes(const BwdK& k) {
+  const size_t rows = (size_t)k.a.B * k.a.HQ * k.Tp * 16, slots = (size_t)k.a.B * k.a.HI * k.Tp * 32;
+  return (rows + 2 * slots + 255) / 256 * 256;
 }
 size_t touch_words(const BwdK& k) { return (size_t)k.a.B * k.a.HI * k.nchunk * k.twords; }
 size_t qs_bytes(const BwdK& k) {
@@ -954,7 +1009,7 @@ int launch_bwd(const BwdK& k, hipStream_t st) {
   const int64_t ne = (int64_t)a.B * a.HI * k.ntiles * a.S;     // one wavefront each
   if (ne > 0) hipLaunchKernelGGL(touch_kernel, dim3((unsigned)((ne + 3) / 4)), dim3(256), 0, st, k);
   hipLaunchKernelGGL((dq_kernel<T, D>), dim3((unsigned)(8 * k.per_xcd)), dim3(128), dq_smem(k), st, k);
-  hipLaunchKernelGGL((dkv_kernel<T, D>), dim3((unsigned)(8 * k.per_xcd_kv)), dim3(256), dkv_smem(k), st, k);
+  hipLaunchKernelGGL((dkv_kernel<T, D>), dim3((unsigned)k.nlogical_kv), dim3(256), dkv_smem(k), st, k);
   const hipError_t e = hipGetLastError();
   if (e != hipSuccess) {
     set_error("bwd launch failed: %s", hipGetErrorString(e));
@@ -972,7 +1027,7 @@ extern "C" size_t srswa_gather_bwd_workspace(const srswa_bwd_args* a) {
   if (!a || a->B <= 0 || a->T <= 0 || a->HQ <= 0 || a->HI <= 0 || a->Sk <= 0) return 0;
   BwdK k{};
   plan_bwd(a, k);
-  return delta_bytes(k) + qs_bytes(k) + touch_words(k) * 4;
+  return rec_bytes(k) + qs_bytes(k) + touch_words(k) * 4;
 }
 
 extern "C" int srswa_gather_bwd(const srswa_bwd_args* a, void* scratch, size_t scratch_bytes,
@@ -982,7 +1037,7 @@ extern "C" int srswa_gather_bwd(const srswa_bwd_args* a, void* scratch, size_t s
   if (a->B == 0 || a->T == 0) return SRSWA_OK;
   BwdK k{};
   plan_bwd(a, k);
-  const size_t need = delta_bytes(k) + qs_bytes(k) + touch_words(k) * 4;
+  const size_t need = rec_bytes(k) + qs_bytes(k) + touch_words(k) * 4;
   if (!scratch || scratch_bytes < need) {
     set_error("bwd: scratch of %zu bytes required (got %zu)", need, scratch_bytes);
     return SRSWA_WORKSPACE;
@@ -991,9 +1046,16 @@ extern "C" int srswa_gather_bwd(const srswa_bwd_args* a, void* scratch, size_t s
     set_error("bwd: LDS budget exceeded (key length too large)");
     return SRSWA_UNSUPPORTED;
   }
-  k.delta = reinterpret_cast<float*>(scratch);
-  k.qs = reinterpret_cast<char*>(scratch) + delta_bytes(k);
-  k.touch = reinterpret_cast<uint32_t*>(reinterpret_cast<char*>(scratch) + delta_bytes(k) + qs_bytes(k));
+  if (rec_bytes(k) >= ((size_t)1 << 31)) {
+    set_error("bwd: row records of 2 GiB or more");
+    return SRSWA_UNSUPPORTED;
+  }
+  k.rows = reinterpret_cast<float4*>(scratch);
+  k.ids_off = (uint32_t)((size_t)k.a.B * k.a.HQ * k.Tp * 16);
+  k.bias_off = k.ids_off + (uint32_t)((size_t)k.a.B * k.a.HI * k.Tp * 32);
+  k.rec_bytes = (uint32_t)rec_bytes(k);
+  k.qs = reinterpret_cast<char*>(scratch) + rec_bytes(k);
+  k.touch = reinterpret_cast<uint32_t*>(reinterpret_cast<char*>(scratch) + rec_bytes(k) + qs_bytes(k));
   hipStream_t s = reinterpret_cast<hipStream_t>(stream);
   if (a->dtype == SRSWA_F32)
     return a->D == 128 ? launch_bwd<float, 128>(k, s) : launch_bwd<float, 64>(k, s);
