@@ -177,12 +177,34 @@ void dq_kernel(BwdK p) {
   const int maxblk = (a.Sk - 1) >> p.bs_shift;
   const bool blk64 = BS >= kChunk;
 
-  // this lane's query row: q, dO, O and lse (log2 units; +inf for rows past
-  // T, so every P is 0), loaded first so their latency overlaps the set-up.
-  // Lanes l and l ^ 32 hold the two halves of a row's head dims.
+  // Loads first, in the order their values are needed, and nothing computed
+  // from a loaded value until all are issued (a use waits for its own load
+  // and for every load issued before it): the set-up row's sample start and
+  // first slots (tid < 64, row r = tid), then this lane's lse, q, dO and O
+  // rows, which stay in flight across the sort and the chunk plan.  Rows past
+  // T read row t0 (valid memory); their values are masked where used.
   const int row = wave * 32 + rl;
   const bool row_ok = row < nrows;
   const int trow = t0 + (row_ok ? row : 0);
+  const int r = tid, rr = min(r, nrows - 1);
+  const int smax = max(a.S - 1, 0);
+  const int32_t* ids = a.S > 0 ? a.idx + (int64_t)b * a.idx_sb + (int64_t)ih * a.idx_sh + (int64_t)(t0 + rr) * a.idx_st
+                               : reinterpret_cast<const int32_t*>(a.lse);   // a valid stand-in, never used
+  const float* bias = a.bias ? a.bias + (int64_t)b * a.bias_sb + (int64_t)ih * a.bias_sh + (int64_t)(t0 + rr) * a.bias_st
+                             : reinterpret_cast<const float*>(ids);
+  const int* segp = a.seg ? a.seg + (int64_t)b * a.seg_sb + t0 + rr : ids;
+  int seg_ld = 0, id8[kPreSlots];
+  float b8[kPreSlots];
+  if (tid < 64) {
+    seg_ld = *segp;
+#pragma unroll
+    for (int s = 0; s < kPreSlots; ++s) {
+      id8[s] = ids[min(s, smax)];
+      b8[s] = bias[min(s, smax)];
+    }
+  }
+  const float lse_ld = a.lse[(int64_t)b * a.lse_sb + (int64_t)trow * a.lse_st + (int64_t)hq * a.lse_sh];
+  // lanes l and l ^ 32 hold the two halves of a row's head dims
   Frag<T> qf[KS], gf[KS], of[KS];
   {
     const T* qrow = reinterpret_cast<const T*>(a.q) + (int64_t)b * a.q_sb + (int64_t)trow * a.q_st + (int64_t)hq * a.q_sh;
@@ -190,47 +212,42 @@ void dq_kernel(BwdK p) {
     const T* orow = reinterpret_cast<const T*>(a.o) + (int64_t)b * a.o_sb + (int64_t)trow * a.o_st + (int64_t)hq * a.o_sh;
 #pragma unroll
     for (int ks = 0; ks < KS; ++ks) {
-      qf[ks] = row_ok ? *reinterpret_cast<const Frag<T>*>(qrow + 16 * ks + 8 * h) : Frag<T>{};
-      gf[ks] = row_ok ? *reinterpret_cast<const Frag<T>*>(grow + 16 * ks + 8 * h) : Frag<T>{};
-      of[ks] = row_ok ? *reinterpret_cast<const Frag<T>*>(orow + 16 * ks + 8 * h) : Frag<T>{};
+      qf[ks] = *reinterpret_cast<const Frag<T>*>(qrow + 16 * ks + 8 * h);
+      gf[ks] = *reinterpret_cast<const Frag<T>*>(grow + 16 * ks + 8 * h);
+      of[ks] = *reinterpret_cast<const Frag<T>*>(orow + 16 * ks + 8 * h);
     }
   }
-  const float lse_l2 = row_ok ? a.lse[(int64_t)b * a.lse_sb + (int64_t)trow * a.lse_st + (int64_t)hq * a.lse_sh] * kLog2e
-                              : INFINITY;
-
   if (tid < 64) {
-    const int r = tid;
     int qi = -1, seg = 0, ls = 0;
     if (r < nrows) {
       qi = off + t0 + r;
-      seg = a.seg ? a.seg[(int64_t)b * a.seg_sb + t0 + r] : 0;
+      seg = a.seg ? seg_ld : 0;
       ls = max(qi - LW + 1, seg);
     }
     s_qi[r] = qi;
     s_seg[r] = seg;
     s_ls[r] = ls;
-    const int rr = min(r, nrows - 1);
-    const int32_t* ids = a.idx + (int64_t)b * a.idx_sb + (int64_t)ih * a.idx_sh + (int64_t)(t0 + rr) * a.idx_st;
-    const float* bias =
-        a.bias ? a.bias + (int64_t)b * a.bias_sb + (int64_t)ih * a.bias_sh + (int64_t)(t0 + rr) * a.bias_st : nullptr;
-    sort_row_ids(ids, bias, r < nrows ? a.S : 0, SP, BS, maxblk, qi, seg, ls, s_sid + r * SP,
-                 s_sb ? s_sb + r * SP : nullptr, s_sslot ? s_sslot + r * SP : nullptr);
-    if (hq % p.IG == 0) {
-      // the slot records of this index head's rows (one query head writes them):
-      // the first kPreSlots ids and biases, -1 / 0 past S and past T
-      int id8[kPreSlots];
-      float b8[kPreSlots];
+    // the row's first slots, -1 / 0 past S and past T
 #pragma unroll
-      for (int s = 0; s < kPreSlots; ++s) {
-        const bool in = r < nrows && s < a.S;
-        id8[s] = in ? ids[s] : -1;
-        b8[s] = in && bias ? bias[s] : 0.f;
-      }
+    for (int s = 0; s < kPreSlots; ++s) {
+      const bool in = r < nrows && s < a.S;
+      id8[s] = in ? id8[s] : -1;
+      b8[s] = in && a.bias ? b8[s] : 0.f;
+    }
+    if (a.S <= kPreSlots)
+      sort_row_ids8(id8, b8, SP, BS, maxblk, qi, seg, ls, s_sid + r * SP, s_sb ? s_sb + r * SP : nullptr,
+                    s_sslot ? s_sslot + r * SP : nullptr);
+    else
+      sort_row_ids(ids, a.bias ? bias : nullptr, r < nrows ? a.S : 0, SP, BS, maxblk, qi, seg, ls, s_sid + r * SP,
+                   s_sb ? s_sb + r * SP : nullptr, s_sslot ? s_sslot + r * SP : nullptr);
+    if (hq % p.IG == 0) {
+      // the slot records of this index head's rows, for the dK / dV kernel
+      // (one query head of the index head writes them)
       const int64_t rec = ((int64_t)b * a.HI + ih) * p.Tp + t0 + r;
       int4* ir = reinterpret_cast<int4*>(reinterpret_cast<char*>(p.rows) + p.ids_off) + rec * 2;
       ir[0] = make_int4(id8[0], id8[1], id8[2], id8[3]);
       ir[1] = make_int4(id8[4], id8[5], id8[6], id8[7]);
-      if (bias) {
+      if (a.bias) {
         float4* br = reinterpret_cast<float4*>(reinterpret_cast<char*>(p.rows) + p.bias_off) + rec * 2;
         br[0] = make_float4(b8[0], b8[1], b8[2], b8[3]);
         br[1] = make_float4(b8[4], b8[5], b8[6], b8[7]);
@@ -239,8 +256,9 @@ void dq_kernel(BwdK p) {
     if (s_sdb)
       for (int i = 0; i < SP; ++i) s_sdb[r * SP + i] = 0.f;
   }
-  __syncthreads();
+  lds_barrier();   // the row loads above stay in flight across the plan
   const int U = plan_chunks(s_qi, s_seg, s_ls, s_sid, SP, BS, LW, nrows, p.nwords, s_bits, s_chunks, s_count);
+  const float lse_l2 = row_ok ? lse_ld * kLog2e : INFINITY;   // log2 units; +inf past T, so every P is 0
 
   RowWalk w;
   w.ok = row_ok;

@@ -298,6 +298,14 @@ __device__ __forceinline__ float xor32_sum(float v) {
   return __uint_as_float(r[0]) + __uint_as_float(r[1]);
 }
 
+// A workgroup barrier for LDS traffic only: this wave's LDS operations are
+// complete (lgkmcnt(0)) and every wave has arrived, while its global loads stay
+// in flight (__syncthreads()'s fence also waits for those).  One volatile asm
+// with a memory clobber, so no memory access is moved across it.
+__device__ __forceinline__ void lds_barrier() {
+  asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+}
+
 __device__ __forceinline__ int wave_max_int(int v) {
   return dpp::reduce<int>(v, INT_MIN, [](int a, int b) { return a > b ? a : b; });
 }

@@ -148,60 +148,68 @@ constexpr int kIdEnd = 0x7fffffff;   // sentinel closing a row's sorted id list
 // repeated id kept once with its first slot's bias (and, when sslot is given,
 // that slot's index), then kIdEnd padding up to SP = S + 1 entries (so a
 // cursor never runs past the list).
+//
+// Up to 8 slots, from registers (id8 / b8: -1 / 0 past the row's slots): the
+// (id, slot) keys are sorted by Batcher's odd-even merge network (19
+// compare-exchanges); a repeated id then follows its first slot, which is the
+// one kept.
+__device__ inline void sort_row_ids8(const int* id8, const float* b8, int SP, int BS, int maxblk, int qi, int seg,
+                                     int ls, int* sid, float* sb, int* sslot = nullptr) {
+  uint32_t key[8];
+  float bk[8];   // each key's bias, carried through the network with it
+#pragma unroll
+  for (int s = 0; s < 8; ++s) {
+    const int id = id8[s];
+    bool ok = id >= 0 && id <= maxblk;
+    const int base = ok ? id * BS : 0;
+    ok = ok && max(base, seg) < min(min(base + BS, ls), qi + 1);
+    key[s] = ok ? ((uint32_t)id << 3) | (uint32_t)s : 0xffffffffu;
+    bk[s] = b8[s];
+  }
+  auto cas = [&](int i, int j) __attribute__((always_inline)) {
+    const bool sw = key[j] < key[i];
+    const uint32_t ki = key[i];
+    const float bi = bk[i];
+    key[i] = sw ? key[j] : ki;
+    key[j] = sw ? ki : key[j];
+    bk[i] = sw ? bk[j] : bi;
+    bk[j] = sw ? bi : bk[j];
+  };
+  cas(0, 1); cas(2, 3); cas(4, 5); cas(6, 7);
+  cas(0, 2); cas(1, 3); cas(4, 6); cas(5, 7);
+  cas(1, 2); cas(5, 6);
+  cas(0, 4); cas(1, 5); cas(2, 6); cas(3, 7);
+  cas(2, 4); cas(3, 5);
+  cas(1, 2); cas(3, 4); cas(5, 6);
+  int n = 0;
+#pragma unroll
+  for (int i = 0; i < 8; ++i) {
+    const uint32_t k = key[i];
+    if (k == 0xffffffffu || (i > 0 && (key[i - 1] >> 3) == (k >> 3))) continue;
+    sid[n] = (int)(k >> 3);
+    if (sb) sb[n] = bk[i];
+    if (sslot) sslot[n] = (int)(k & 7u);
+    ++n;
+  }
+  for (int i = n; i < SP; ++i) {
+    sid[i] = kIdEnd;
+    if (sslot) sslot[i] = -1;
+  }
+}
+
+// The same from the row's slots in memory (S of them, any number).
 __device__ inline void sort_row_ids(const int32_t* ids, const float* bias, int S, int SP, int BS,
                                     int maxblk, int qi, int seg, int ls, int* sid, float* sb,
                                     int* sslot = nullptr) {
   if (S <= 8) {
-    // up to 8 slots: every id (and bias) is loaded at once, so the row pays
-    // one memory latency, and the (id, slot) keys are sorted in registers by
-    // Batcher's odd-even merge network (19 compare-exchanges); a repeated id
-    // then follows its first slot, which is the one kept
+    // every id (and bias) is loaded at once, so the row pays one memory latency
     int id8[8];
     float b8[8];
 #pragma unroll
     for (int s = 0; s < 8; ++s) id8[s] = s < S ? ids[s] : -1;
 #pragma unroll
     for (int s = 0; s < 8; ++s) b8[s] = bias && s < S ? bias[s] : 0.f;
-    uint32_t key[8];
-#pragma unroll
-    for (int s = 0; s < 8; ++s) {
-      const int id = id8[s];
-      bool ok = id >= 0 && id <= maxblk;
-      const int base = ok ? id * BS : 0;
-      ok = ok && max(base, seg) < min(min(base + BS, ls), qi + 1);
-      key[s] = ok ? ((uint32_t)id << 3) | (uint32_t)s : 0xffffffffu;
-    }
-    auto cas = [&](int i, int j) __attribute__((always_inline)) {
-      const uint32_t lo = min(key[i], key[j]), hi = max(key[i], key[j]);
-      key[i] = lo;
-      key[j] = hi;
-    };
-    cas(0, 1); cas(2, 3); cas(4, 5); cas(6, 7);
-    cas(0, 2); cas(1, 3); cas(4, 6); cas(5, 7);
-    cas(1, 2); cas(5, 6);
-    cas(0, 4); cas(1, 5); cas(2, 6); cas(3, 7);
-    cas(2, 4); cas(3, 5);
-    cas(1, 2); cas(3, 4); cas(5, 6);
-    int n = 0;
-#pragma unroll
-    for (int i = 0; i < 8; ++i) {
-      const uint32_t k = key[i];
-      if (k == 0xffffffffu || (i > 0 && (key[i - 1] >> 3) == (k >> 3))) continue;
-      const int slot = (int)(k & 7u);
-      sid[n] = (int)(k >> 3);
-      if (sb) {
-        float bv = b8[0];
-#pragma unroll
-        for (int t = 1; t < 8; ++t) bv = slot == t ? b8[t] : bv;
-        sb[n] = bv;
-      }
-      if (sslot) sslot[n] = slot;
-      ++n;
-    }
-    for (int i = n; i < SP; ++i) {
-      sid[i] = kIdEnd;
-      if (sslot) sslot[i] = -1;
-    }
+    sort_row_ids8(id8, b8, SP, BS, maxblk, qi, seg, ls, sid, sb, sslot);
     return;
   }
   int n = 0;
@@ -316,7 +324,7 @@ __device__ inline int compact_bitmap(const uint32_t* s_bits, int nwords, uint16_
     }
     if (tid == 0) *s_count = base;
   }
-  __syncthreads();
+  lds_barrier();
   return *s_count;
 }
 
@@ -330,22 +338,48 @@ __device__ inline int plan_chunks(const int* s_qi, const int* s_seg, const int* 
                                   uint16_t* s_chunks, int* s_count) {
   const int tid = threadIdx.x, nthr = blockDim.x;
   for (int w = tid; w < nwords; w += nthr) s_bits[w] = 0u;
-  __syncthreads();
-  const int wspan = (LW + kChunk - 1) / kChunk + 1;
-  for (int e = tid; e < nrows * wspan; e += nthr) {
-    const int r = e / wspan, k = e % wspan;
-    const int c = max(s_ls[r], 0) / kChunk + k;
-    if (c <= s_qi[r] / kChunk) atomicOr(&s_bits[c >> 5], 1u << (c & 31));
+  lds_barrier();
+  if (tid < kWave) {
+    // the first wavefront, lane = row
+    const int r = tid;
+    const bool live = r < nrows;
+    // windows: each row's chunks [ls / 64, qi / 64]; a row's range starts at
+    // most one chunk past the previous row's end (ls <= qi = previous qi + 1),
+    // so the union over the rows is the single range [min start, max end]
+    const int c_lo = wave_min_int(live ? max(s_ls[r], 0) / kChunk : INT_MAX);
+    const int c_hi = wave_max_int(live ? s_qi[r] / kChunk : INT_MIN);
+    if (c_lo <= c_hi) {
+      for (int w = (c_lo >> 5) + r; w <= (c_hi >> 5); w += kWave) {
+        const int lo = max(c_lo - 32 * w, 0), hi = min(c_hi - 32 * w, 31);
+        s_bits[w] |= (hi - lo == 31) ? 0xffffffffu : (((1u << (hi - lo + 1)) - 1u) << lo);
+      }
+    }
+    // remote keys: the i-th listed block of every row; rows sharing a selection
+    // list the same blocks, and then one lane sets the bits for the wave
+    for (int i = 0; i < SP; ++i) {
+      const int id = live ? sid[r * SP + i] : kIdEnd;
+      const bool has = id != kIdEnd;
+      const uint64_t m = __ballot(has);
+      if (m == 0ull) break;   // every row's list has ended (kIdEnd pads each list)
+      int c0 = 0, c1 = -1;
+      if (has) {
+        const int lo = max(id * BS, s_seg[r]);
+        const int hi = min(min(id * BS + BS, s_ls[r]), s_qi[r] + 1);
+        c0 = lo / kChunk;
+        c1 = (hi - 1) / kChunk;
+      }
+      const int first = __ffsll((long long)m) - 1;
+      const int f0 = __shfl(c0, first, kWave), f1 = __shfl(c1, first, kWave);
+      const bool same = __all(!has || (c0 == f0 && c1 == f1));
+      if (same) {
+        if (r == first)
+          for (int c = f0; c <= f1; ++c) atomicOr(&s_bits[c >> 5], 1u << (c & 31));
+      } else if (has) {
+        for (int c = c0; c <= c1; ++c) atomicOr(&s_bits[c >> 5], 1u << (c & 31));
+      }
+    }
   }
-  for (int e = tid; e < nrows * SP; e += nthr) {
-    const int r = e / SP;
-    const int id = sid[e];
-    if (id == kIdEnd) continue;
-    const int lo = max(id * BS, s_seg[r]);
-    const int hi = min(min(id * BS + BS, s_ls[r]), s_qi[r] + 1);
-    for (int c = lo / kChunk; c <= (hi - 1) / kChunk; ++c) atomicOr(&s_bits[c >> 5], 1u << (c & 31));
-  }
-  __syncthreads();
+  lds_barrier();
   return compact_bitmap(s_bits, nwords, s_chunks, s_count);
 }
 

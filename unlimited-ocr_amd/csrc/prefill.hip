@@ -155,39 +155,62 @@ void fwd_kernel(FwdK p) {
   // scales the fp32 product (attend_triton.py:204)
   const float l2s = PAGED ? a.scale * kLog2e : kLog2e;
 
-  // this lane's query row, loaded first so its latency overlaps the set-up
+  // Loads first, and nothing computed from a loaded value until all are
+  // issued (a use waits for its own load and every load issued before it):
+  // the set-up row's sample start and first 8 slots (tid < 64, row r = tid),
+  // then this lane's query row, in flight across the sort and the chunk plan.
+  // Rows past T read row t0 (valid memory) and are masked where used (their
+  // output and lse are never written).
   const int row = wave * 32 + rl;
   const bool row_ok = row < nrows;
+  const int r = tid, rr = min(r, nrows - 1);
+  const int smax = max(a.S - 1, 0);
+  const int32_t* ids = a.S > 0 ? a.idx + (int64_t)b * a.idx_sb + (int64_t)ih * a.idx_sh + (int64_t)(q0 + t0 + rr) * a.idx_st
+                               : reinterpret_cast<const int32_t*>(a.q);   // a valid stand-in, never used
+  const float* bias = a.bias ? a.bias + (int64_t)b * a.bias_sb + (int64_t)ih * a.bias_sh + (int64_t)(q0 + t0 + rr) * a.bias_st
+                             : reinterpret_cast<const float*>(ids);
+  const int* segp = a.seg ? a.seg + (int64_t)b * a.seg_sb + t0 + rr : ids;
+  int seg_ld = 0, id8[8];
+  float b8[8];
+  if (tid < 64) {
+    seg_ld = *segp;
+#pragma unroll
+    for (int s = 0; s < 8; ++s) {
+      id8[s] = ids[min(s, smax)];
+      b8[s] = bias[min(s, smax)];
+    }
+  }
   Frag<T> qf[KS];
   {
     const T* qrow = reinterpret_cast<const T*>(a.q) + (int64_t)b * a.q_sb +
                     (int64_t)(q0 + t0 + (row_ok ? row : 0)) * a.q_st + (int64_t)hq * a.q_sh;
 #pragma unroll
-    for (int ks = 0; ks < KS; ++ks)
-      qf[ks] = row_ok ? *reinterpret_cast<const Frag<T>*>(qrow + 16 * ks + 8 * h) : Frag<T>{};
+    for (int ks = 0; ks < KS; ++ks) qf[ks] = *reinterpret_cast<const Frag<T>*>(qrow + 16 * ks + 8 * h);
   }
-
   if (tid < 64) {
-    const int r = tid;
     int qi = -1, seg = 0, ls = 0;
     if (r < nrows) {
       qi = off + t0 + r;
-      seg = a.seg ? a.seg[(int64_t)b * a.seg_sb + t0 + r] : 0;
+      seg = a.seg ? seg_ld : 0;
       ls = max(qi - LW + 1, seg);
     }
     s_qi[r] = qi;
     s_seg[r] = seg;
     s_ls[r] = ls;
-    const int rr = min(r, nrows - 1);
-    const int32_t* ids =
-        a.idx + (int64_t)b * a.idx_sb + (int64_t)ih * a.idx_sh + (int64_t)(q0 + t0 + rr) * a.idx_st;
-    const float* bias = a.bias ? a.bias + (int64_t)b * a.bias_sb + (int64_t)ih * a.bias_sh +
-                                     (int64_t)(q0 + t0 + rr) * a.bias_st
-                               : nullptr;
-    sort_row_ids(ids, bias, r < nrows ? a.S : 0, SP, BS, maxblk, qi, seg, ls, s_sid + r * SP,
-                 s_sb ? s_sb + r * SP : nullptr);
+    if (a.S <= 8) {
+#pragma unroll
+      for (int s = 0; s < 8; ++s) {   // -1 / 0 past S and past T
+        const bool in = r < nrows && s < a.S;
+        id8[s] = in ? id8[s] : -1;
+        b8[s] = in && a.bias ? b8[s] : 0.f;
+      }
+      sort_row_ids8(id8, b8, SP, BS, maxblk, qi, seg, ls, s_sid + r * SP, s_sb ? s_sb + r * SP : nullptr);
+    } else {
+      sort_row_ids(ids, a.bias ? bias : nullptr, r < nrows ? a.S : 0, SP, BS, maxblk, qi, seg, ls, s_sid + r * SP,
+                   s_sb ? s_sb + r * SP : nullptr);
+    }
   }
-  __syncthreads();
+  lds_barrier();
   const int U = plan_chunks(s_qi, s_seg, s_ls, s_sid, SP, BS, LW, nrows, p.nwords, s_bits, s_chunks, s_count);
   // paged: the page of each 16-key quarter of every visited chunk, looked up
   // once here, so a prefetch issues its K / V loads without a dependent read
