@@ -822,7 +822,11 @@ void dkv_kernel(BwdK p) {
                   x = fmaf(sg[half][r], kLog2e, (remb ? bv[e] : 0.f) - lv[e]);
                   x = ((km32 >> bit) & 1u) ? x : -INFINITY;      // exp2(-inf) = 0
                 }
-                pv[e] = key_ok ? __builtin_amdgcn_exp2f(x) : 0.f;
+                // a key past Sk needs no test: no row keeps it (windows and
+                // remote ranges end at qi + 1 <= Sk), so it is -inf above and
+                // never in a half every row keeps whole (the fast form); and
+                // its P only reaches its own dK / dV, which are not written
+                pv[e] = __builtin_amdgcn_exp2f(x);
                 sg[half][r] = pv[e];
               }
               sPl[(4 * half + r4) * 64] = make_float4(pv[0], pv[1], pv[2], pv[3]);
