@@ -19,7 +19,7 @@
 //     LPR lanes of a row (each lane ends holding one key's score);
 //   * online softmax in the log2 domain (wave max/sum via shuffles), p is
 //     broadcast back through 256 bytes of LDS per wave, then o += p v;
-// Four waves (one workgroup) merge their (m, l, o) in LDS; the workgroups of
+// Four waves (one workgroup; eight with fp8 caches) merge their (m, l, o) in LDS; the workgroups of
 // one (row, head) write (O, M, L) records to a scratch buffer, and a second
 // small kernel combines them (decode_merge_kernel).
 #include <stdarg.h>
@@ -56,6 +56,7 @@ struct DecodePlan {
   int pstride;         // floats per partial record (128-byte multiple)
   int64_t rowheads;    // B * Lq * HQ
   int gq;              // query heads per workgroup (gqa_heads)
+  int nw;              // waves per workgroup
 };
 
 struct DecodeK {
@@ -73,6 +74,7 @@ struct DecodeK {
   int bs_shift, max_blocks;
   int kv8;                       // FP8 kernels: the caches' fp8 format (srswa_dtype)
   int gq;                        // query heads per workgroup (gqa_heads)
+  int nw;                        // waves per workgroup (4; the fp8 paged form 8)
 };
 
 template <typename TO>
@@ -175,8 +177,8 @@ template <typename T> struct KVRaw<T, true> {
 
 // GQ query heads per workgroup (GQA: heads of one kv head that read one id
 // row): each K / V row is loaded once and scored for all GQ heads.
-template <typename T, typename TO, int D, int NI, bool PAGED, bool FP8 = false, int GQ = 1>
-__global__ __launch_bounds__(kDecodeWaves * kWave) void decode_kernel(DecodeK p) {
+template <typename T, typename TO, int D, int NI, bool PAGED, bool FP8 = false, int GQ = 1, int NW = kDecodeWaves>
+__global__ __launch_bounds__(NW * kWave) void decode_kernel(DecodeK p) {
   using V = Vec16<T>;
   using KE = std::conditional_t<FP8, uint8_t, T>;   // cache element
   static_assert(!FP8 || (PAGED && sizeof(T) == 2), "fp8 caches: paged, 16-bit queries");
@@ -188,9 +190,9 @@ __global__ __launch_bounds__(kDecodeWaves * kWave) void decode_kernel(DecodeK p)
   static_assert(LPR <= kWave && kWave % LPR == 0, "row must fit a wavefront");
   static_assert(NI <= LPR && LPR % NI == 0, "NI must divide LPR");
 
-  __shared__ float s_p[kDecodeWaves][GQ][64];
-  __shared__ float s_o[kDecodeWaves][GQ][D];
-  __shared__ float s_m[kDecodeWaves][GQ], s_l[kDecodeWaves][GQ];
+  __shared__ float s_p[NW][GQ][64];
+  __shared__ float s_o[NW][GQ][D];
+  __shared__ float s_m[NW][GQ], s_l[NW][GQ];
 
   const srswa_decode_args& a = p.a;
   const int wave = threadIdx.x / kWave;
@@ -278,9 +280,9 @@ __global__ __launch_bounds__(kDecodeWaves * kWave) void decode_kernel(DecodeK p)
 
   // the workgroup's units, dealt round-robin to its waves so that every wave
   // mixes remote (scattered) and window (contiguous) units
-  const int u_base = split * kDecodeWaves * p.upw;
+  const int u_base = split * NW * p.upw;
   for (int i = 0; i < p.upw; ++i) {
-    const int u = u_base + wave + i * kDecodeWaves;
+    const int u = u_base + wave + i * NW;
     if (u >= p.n_units) break;
     int k0, k1, klo;
     int page = 0, page2 = 0;
@@ -512,12 +514,12 @@ __global__ __launch_bounds__(kDecodeWaves * kWave) void decode_kernel(DecodeK p)
     const int hq = hq0 + g;
     float M = -INFINITY;
 #pragma unroll
-    for (int w = 0; w < kDecodeWaves; ++w) M = fmaxf(M, s_m[w][g]);
+    for (int w = 0; w < NW; ++w) M = fmaxf(M, s_m[w][g]);
     float L = 0.f, O[EPV];
 #pragma unroll
     for (int e = 0; e < EPV; ++e) O[e] = 0.f;
 #pragma unroll
-    for (int w = 0; w < kDecodeWaves; ++w) {
+    for (int w = 0; w < NW; ++w) {
       const float wt = s_m[w][g] == -INFINITY ? 0.f : exp2f(s_m[w][g] - M);
       L += s_l[w][g] * wt;
       if (r == 0) {
@@ -609,7 +611,7 @@ int elem_bytes(int dt) { return dt == SRSWA_F32 ? 4 : 2; }
 
 // Tuning knobs (environment, read once): SRSWA_DECODE_NI = 8 (default) | 16
 // load instructions per unit (bf16 D=128: 32 | 64 keys); SRSWA_DECODE_UPW =
-// units per wave (default 2, 8 with fp8 caches).
+// units per wave (default 2, 4 with fp8 caches).
 int env_int(const char* name, int dflt) {
   const char* v = getenv(name);
   return (v && *v) ? atoi(v) : dflt;
@@ -649,11 +651,14 @@ DecodePlan make_plan(const srswa_decode_args* a, bool paged = false, bool fp8 = 
   // paged windows run on the UK grid, LW / UK units with the first one
   // wrapped (UK divides the page size, which divides LW)
   pl.n_units = pl.n_remote_units + ceil_div(a->local_window, pl.UK);
-  // an fp8 unit holds half the bytes: four times the units per wave (at
-  // config 3 one workgroup per row, so no split-K merge)
+  // an fp8 unit holds half the bytes: a workgroup takes four times the
+  // units, as eight waves of four (at config 3 one workgroup per row, so no
+  // split-K merge; eight waves of four beat four of eight by about 1%, and
+  // sixteen of two lose a quarter)
+  pl.nw = fp8 && paged ? 8 : kDecodeWaves;
   static const int upw = env_int("SRSWA_DECODE_UPW", 0);
-  pl.upw = upw > 0 ? upw : (fp8 ? 8 : 2);
-  pl.nsplit = ceil_div(pl.n_units, kDecodeWaves * pl.upw);
+  pl.upw = upw > 0 ? upw : (fp8 ? 4 : 2);
+  pl.nsplit = ceil_div(pl.n_units, pl.nw * pl.upw);
   pl.pstride = ceil_div(a->D + 2, 32) * 32;
   pl.rowheads = (int64_t)a->B * a->Lq * a->HQ;
   pl.gq = gqa_heads(a, ni);
@@ -667,9 +672,14 @@ size_t scratch_bytes(const DecodePlan& pl) {
 template <typename T, typename TO, int D, int NI, int GQ>
 void launch_decode_gq(const DecodeK& k, int64_t grid, hipStream_t st) {
   if constexpr (sizeof(T) == 2 && std::is_same_v<T, TO>) {
-    if (k.kv8 && k.bt)
-      hipLaunchKernelGGL((decode_kernel<T, TO, D, NI, true, true, GQ>), dim3((unsigned)grid),
-                         dim3(kDecodeWaves * kWave), 0, st, k);
+    if (k.kv8 && k.bt) {
+      if (k.nw == 8)
+        hipLaunchKernelGGL((decode_kernel<T, TO, D, NI, true, true, GQ, 8>), dim3((unsigned)grid),
+                           dim3(8 * kWave), 0, st, k);
+      else
+        hipLaunchKernelGGL((decode_kernel<T, TO, D, NI, true, true, GQ>), dim3((unsigned)grid),
+                           dim3(kDecodeWaves * kWave), 0, st, k);
+    }
   }
   if (k.kv8) {
     // fp8 caches take the 16-bit paged kernels only (checked by the caller)
@@ -802,6 +812,7 @@ extern "C" int srswa_gather_decode(const srswa_decode_args* a, void* ws, size_t 
   k.n_remote_units = pl.n_remote_units;
   k.n_units = pl.n_units;
   k.upw = pl.upw;
+  k.nw = pl.nw;
   k.nsplit = pl.nsplit;
   k.pstride = pl.pstride;
   k.scale_l2 = a->scale * kLog2e;
@@ -929,6 +940,7 @@ extern "C" int srswa_gather_decode_paged(const srswa_paged_decode_args* a, void*
   k.n_remote_units = pl.n_remote_units;
   k.n_units = pl.n_units;
   k.upw = pl.upw;
+  k.nw = pl.nw;
   k.nsplit = pl.nsplit;
   k.pstride = pl.pstride;
   k.scale_l2 = d.scale * kLog2e;
