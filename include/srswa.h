@@ -878,7 +878,8 @@ int srswa_gather_kl_bwd(const srswa_kl_bwd_args* a, void* scratch, size_t scratc
  *   z[b, i, c] = clamp(q_i . kbar_c / sqrt(D), +-1e4) when c <= pos[b, i] / BS - local_blocks
  *                and c BS < S, else -1e9.
  * The forward writes kbar (the backward's input) and z; every entry of both
- * is written.
+ * is written.  Rows of z must not overlap (z_st >= nblk); z_st and nblk * D
+ * stay below 2^23 elements (SRSWA_UNSUPPORTED otherwise).
  * ---------------------------------------------------------------------- */
 typedef struct {
   const float* q;        int64_t q_sb, q_st;           /* [B, S, D] idx_q                   */
@@ -901,7 +902,9 @@ int srswa_hc_score_fwd(const srswa_hc_score_args* a, void* stream);
  * nblk * BS are the caller's) and dhc.  Deterministic (partials summed in a
  * fixed order); the workspace holds fp32 partials of dkbar per 256-row chunk
  * and of dhc per block.  Layout as srswa_hc_score_args; kbar and z are the
- * forward's. */
+ * forward's.  Rows must not overlap (z_st, gz_st >= nblk, q_st >= D), and the
+ * row strides q_st, z_st, gz_st and nblk * D stay below 2^23 elements
+ * (SRSWA_UNSUPPORTED otherwise). */
 typedef struct {
   const float* q;        int64_t q_sb, q_st;
   const float* k;        int64_t k_sb, k_st;

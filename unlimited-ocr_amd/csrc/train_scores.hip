@@ -80,6 +80,8 @@ __device__ __forceinline__ int last_remote_block(int p, int BS, int LB) { return
 // s_pre the unclamped logits pre_t (one entry per key, BS of them).  Returns
 // sum e (den), the row max and the lane's slice of kbar_raw: head dims
 // EPL lane .. EPL lane + EPL - 1.
+constexpr int kRowsAhead = 16;   // key rows loaded together by the block passes
+
 template <int D> struct HcBlock {
   static constexpr int EPL = D / kWave;      // head dims per lane
   float den, rowmax;
@@ -126,15 +128,25 @@ __device__ void hc_block_forward(const float* kg, int64_t k_st, const float* s_h
   __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
   __builtin_amdgcn_wave_barrier();
   __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-  // kbar_raw over the lane's dims (coalesced rows)
+  // kbar_raw over the lane's dims (coalesced rows), in key order: rows loaded
+  // kRowsAhead at a time so their latencies overlap
 #pragma unroll
   for (int j = 0; j < EPL; ++j) out.kb[j] = 0.f;
-#pragma unroll 4
-  for (int t = 0; t < nv; ++t) {
-    const float w = s_w[t];
-    const float* row = kg + (int64_t)t * k_st + EPL * lane;
+  for (int t0 = 0; t0 < nv; t0 += kRowsAhead) {
+    float rv[kRowsAhead][EPL];
 #pragma unroll
-    for (int j = 0; j < EPL; ++j) out.kb[j] = fmaf(w, row[j], out.kb[j]);
+    for (int u = 0; u < kRowsAhead; ++u) {
+      const float* row = kg + (int64_t)min(t0 + u, nv - 1) * k_st + EPL * lane;
+#pragma unroll
+      for (int j = 0; j < EPL; ++j) rv[u][j] = row[j];
+    }
+#pragma unroll
+    for (int u = 0; u < kRowsAhead; ++u)
+      if (t0 + u < nv) {
+        const float w = s_w[t0 + u];
+#pragma unroll
+        for (int j = 0; j < EPL; ++j) out.kb[j] = fmaf(w, rv[u][j], out.kb[j]);
+      }
   }
   out.den = den;
   out.rowmax = rowmax;
@@ -171,97 +183,120 @@ __global__ __launch_bounds__(256) void hc_summary_fwd_kernel(HcK p) {
 }
 
 // ---------------------------------------------------------------- scores
-// the row's last remote block and the tile's (block-wide max)
-__device__ __forceinline__ int tile_rmax(const srswa_hc_score_args& a, int b, int row, int* s_red) {
-  int rm = -1;
-  if (row < a.S) rm = last_remote_block(a.pos[(int64_t)b * a.pos_sb + (int64_t)row * a.pos_st], a.block_size,
-                                        a.local_blocks);
-  const int wm = wave_max_int(rm);
-  const int wave = threadIdx.x / kWave, lane = threadIdx.x % kWave;
-  if (lane == 0) s_red[wave] = wm;
-  __syncthreads();
-  int t = s_red[0];
-  for (int w = 1; w < (int)(blockDim.x / kWave); ++w) t = max(t, s_red[w]);
-  __syncthreads();
-  return t;
-}
-
 // the last block holding a key (chunk_valid) and the last one scored
 __device__ __forceinline__ int last_valid_block(const srswa_hc_score_args& a) {
   return min(a.nblk - 1, (a.S - 1) / a.block_size);
 }
 
+// Workgroup blockIdx.x's work item and part: items are dealt to the 8 XCDs
+// round-robin by workgroup index, and the `parts` workgroups of one item go to
+// one XCD one after another, so what they share stays in that XCD's L2.
+// Launched over ceil(nitems / 8) * 8 * parts workgroups; false past the last item.
+__device__ __forceinline__ bool xcd_item(int nitems, int parts, int& item, int& part) {
+  const int j = (int)blockIdx.x, x = j % 8, k = j / 8;
+  part = k % parts;
+  item = (k / parts) * 8 + x;
+  return item < nitems;
+}
+
+// Scores of 64 query rows per workgroup on fp32 MFMA.  Per group of 64 blocks
+// the k_bar rows are staged in LDS (the next group's loaded ahead), and wave w
+// computes the 32 x 32 tile of rows 32 (w & 1) .. + 31 against blocks
+// 32 (w >> 1) .. + 31 as Q K_bar^T (v_mfma_f32_32x32x2f32; in step group m
+// lane half h supplies head dims 8 m + 4 h .. + 3 to both operands), its query
+// rows held in registers for the whole tile.  A lane's accumulators are one
+// block's scores for 16 rows, so a store instruction writes 32 consecutive
+// blocks of two rows.  Waves whose rows reach none of their blocks, and groups
+// past the tile's last remote block, store -1e9 without scoring.  Tiles go
+// heaviest (last rows) first.
 template <int D>
 __global__ __launch_bounds__(256) void hc_score_fwd_kernel(HcK p) {
-  __shared__ __align__(16) float s_kb[kTsGroup * D];
-  __shared__ float s_out[kTsRows * kTsPad];
-  __shared__ int s_red[4];
+  constexpr int KP = D + 4;                         // k_bar row pitch in LDS
+  constexpr int PR = D / 4;                         // 16-byte pieces per k_bar row
+  constexpr int PPT = kTsGroup * PR / 256;          // pieces per thread
+  __shared__ __align__(16) float s_kb[kTsGroup * KP];
+  __shared__ int s_rm[kTsRows];
+  __shared__ int s_trm;
   const srswa_hc_score_args& a = p.a;
-  const int wave = threadIdx.x / kWave, lane = threadIdx.x % kWave;
-  const int ntiles = (a.S + kTsRows - 1) / kTsRows;
-  const int b = blockIdx.x / ntiles, tile = blockIdx.x % ntiles;
-  const int row = tile * kTsRows + lane;
-  const bool row_ok = row < a.S;
-  const int rm = row_ok ? last_remote_block(a.pos[(int64_t)b * a.pos_sb + (int64_t)row * a.pos_st], a.block_size,
-                                            a.local_blocks)
-                        : -1;
-  const int trm = min(tile_rmax(a, b, tile * kTsRows + (threadIdx.x % kTsRows), s_red), last_valid_block(a));
-  const int wrm = min(wave_max_int(rm), last_valid_block(a));
-  float qv[D];
-  const float* qrow = a.q + (int64_t)b * a.q_sb + (int64_t)(row_ok ? row : 0) * a.q_st;
-#pragma unroll
-  for (int e = 0; e < D; e += 4) {
-    const float4 v = row_ok ? *reinterpret_cast<const float4*>(qrow + e) : make_float4(0.f, 0.f, 0.f, 0.f);
-    qv[e] = v.x;
-    qv[e + 1] = v.y;
-    qv[e + 2] = v.z;
-    qv[e + 3] = v.w;
+  const int tid = threadIdx.x, wave = __builtin_amdgcn_readfirstlane(tid / kWave), lane = tid % kWave;
+  const int h = lane / 32, rl = lane % 32;
+  const int ntiles = ceil_div(a.S, kTsRows);
+  const int b = (int)(blockIdx.x % (unsigned)a.B), tile = ntiles - 1 - (int)(blockIdx.x / (unsigned)a.B);
+  const int row0 = tile * kTsRows;
+  const int lastv = last_valid_block(a);
+  if (tid < kTsRows) {                              // wave 0: the rows' last scored blocks
+    const int row = row0 + tid;
+    const int rm = row < a.S ? min(last_remote_block(a.pos[(int64_t)b * a.pos_sb + (int64_t)row * a.pos_st],
+                                                     a.block_size, a.local_blocks), lastv)
+                             : -1;
+    s_rm[tid] = rm;
+    const int wm = wave_max_int(rm);
+    if (tid == 0) s_trm = wm;
   }
-  const int nrows = min(kTsRows, a.S - tile * kTsRows);
-  for (int g0 = 0; g0 < a.nblk; g0 += kTsGroup) {
-    const int gn = min(kTsGroup, a.nblk - g0);
-    const bool any = g0 <= trm;
-    if (any) {
-      for (int i = threadIdx.x; i < gn * (D / 4); i += blockDim.x) {
-        const int c = i / (D / 4), e = 4 * (i % (D / 4));
-        *reinterpret_cast<float4*>(s_kb + c * D + e) =
-            *reinterpret_cast<const float4*>(a.kbar + (int64_t)b * a.kb_sb + (int64_t)(g0 + c) * D + e);
+  const int wr = 32 * (wave & 1), wc = 32 * (wave >> 1);
+  float4 qf[D / 8];
+  {                                                 // rows past S: loaded from row S - 1, never stored
+    const float* qrow = a.q + (int64_t)b * a.q_sb + (int64_t)min(row0 + wr + rl, a.S - 1) * a.q_st + 4 * h;
+#pragma unroll
+    for (int m = 0; m < D / 8; ++m) qf[m] = *reinterpret_cast<const float4*>(qrow + 8 * m);
+  }
+  // k_bar rows of a group: blocks past nblk read as zero
+  const auto rkb = make_rsrc(a.kbar + (int64_t)b * a.kb_sb, (uint32_t)a.nblk * D * 4);
+  uint4 pre[PPT];
+  auto fetch = [&](int g0) {
+#pragma unroll
+    for (int i = 0; i < PPT; ++i) pre[i] = buffer_load16(rkb, 4 * ((uint32_t)g0 * D + tid * 4 + 1024 * i), 0);
+  };
+  lds_barrier();
+  const int trm = __builtin_amdgcn_readfirstlane(s_trm);
+  int rmv[16];
+  int wrm = -1;
+#pragma unroll
+  for (int r = 0; r < 16; ++r) {
+    rmv[r] = s_rm[wr + d_row(r, h)];
+    wrm = max(wrm, rmv[r]);
+  }
+  wrm = __builtin_amdgcn_readfirstlane(max(wrm, __shfl_xor(wrm, 32, kWave)));
+  const int ngs = trm >= 0 ? trm / kTsGroup + 1 : 0;      // groups holding a scored block
+  if (ngs > 0) fetch(0);
+  // z through unconditional buffer stores (a conditional store would make each
+  // wait for the prefetch wait for every store): the range ends at the tile's
+  // last row's last block, so rows past S fall outside it; blocks past nblk
+  // are sent past it
+  const int nr = min(kTsRows, a.S - row0);
+  const auto rzs = make_rsrc(a.z + (int64_t)b * a.z_sb + (int64_t)row0 * a.z_st,
+                             (uint32_t)(((int64_t)(nr - 1) * a.z_st + a.nblk) * 4));
+  const uint32_t zst4 = 4 * (uint32_t)a.z_st;
+  const uint32_t zoff = (uint32_t)(wr + 4 * h) * zst4 + 4 * (uint32_t)(wc + rl);
+  for (int gi = 0; gi < p.ngroups; ++gi) {
+    const int g0 = gi * kTsGroup, c = g0 + wc + rl;
+    f32x16_t s = zero16();
+    if (gi < ngs) {
+      lds_barrier();                                // the previous group's k_bar is consumed
+#pragma unroll
+      for (int i = 0; i < PPT; ++i) {
+        const int pc = tid + 256 * i;
+        *reinterpret_cast<uint4*>(s_kb + (pc / PR) * KP + 4 * (pc % PR)) = pre[i];
       }
-      __syncthreads();
-      // wave w scores blocks g0 + 16 w .. + 15, four at a time
-      for (int j0 = 16 * wave; j0 < min(16 * wave + 16, gn); j0 += 4) {
-        float acc[4] = {0.f, 0.f, 0.f, 0.f};
-        const int c0 = g0 + j0;
-        if (c0 <= wrm) {
+      lds_barrier();
+      if (gi + 1 < ngs) fetch(g0 + kTsGroup);
+      if (g0 + wc <= wrm) {
+        const float* kr = s_kb + (wc + rl) * KP + 4 * h;
 #pragma unroll
-          for (int e = 0; e < D; e += 4) {
-#pragma unroll
-            for (int u = 0; u < 4; ++u) {
-              const float4 kv = *reinterpret_cast<const float4*>(s_kb + min(j0 + u, gn - 1) * D + e);
-              acc[u] = fmaf(qv[e], kv.x, acc[u]);
-              acc[u] = fmaf(qv[e + 1], kv.y, acc[u]);
-              acc[u] = fmaf(qv[e + 2], kv.z, acc[u]);
-              acc[u] = fmaf(qv[e + 3], kv.w, acc[u]);
-            }
-          }
-        }
-#pragma unroll
-        for (int u = 0; u < 4; ++u) {
-          const int c = c0 + u;
-          if (j0 + u < gn)
-            s_out[lane * kTsPad + j0 + u] = (c <= rm && c <= last_valid_block(a)) ? clamp_act(acc[u] * p.isd)
-                                                                                   : kScoreNeg;
+        for (int m = 0; m < D / 8; ++m) {
+          const float4 kv = *reinterpret_cast<const float4*>(kr + 8 * m);
+          s = __builtin_amdgcn_mfma_f32_32x32x2f32(qf[m].x, kv.x, s, 0, 0, 0);
+          s = __builtin_amdgcn_mfma_f32_32x32x2f32(qf[m].y, kv.y, s, 0, 0, 0);
+          s = __builtin_amdgcn_mfma_f32_32x32x2f32(qf[m].z, kv.z, s, 0, 0, 0);
+          s = __builtin_amdgcn_mfma_f32_32x32x2f32(qf[m].w, kv.w, s, 0, 0, 0);
         }
       }
-      __syncthreads();
     }
-    // the tile's rows of this group, coalesced along the blocks
-    for (int i = threadIdx.x; i < nrows * gn; i += blockDim.x) {
-      const int r = i / gn, c = i % gn;
-      a.z[(int64_t)b * a.z_sb + (int64_t)(tile * kTsRows + r) * a.z_st + g0 + c] = any ? s_out[r * kTsPad + c]
-                                                                                       : kScoreNeg;
-    }
-    if (any) __syncthreads();
+    const uint32_t off = c < a.nblk ? zoff + 4 * (uint32_t)g0 : 0x80000000u;
+#pragma unroll
+    for (int r = 0; r < 16; ++r)
+      __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint(c <= rmv[r] ? clamp_act(s[r] * p.isd) : kScoreNeg), rzs,
+                                            off + (uint32_t)d_row(r, 0) * zst4, 0, 0);
   }
 }
 
@@ -279,151 +314,209 @@ __device__ __forceinline__ float dz_raw(float g, float z, float isd) {
   return (z > -kActClamp && z < kActClamp) ? sanitize(g * isd) : 0.f;
 }
 
-// four lanes per row / block: lane slice s owns head dims 16 m + 4 s .. + 3
-template <int D> struct Slice {
-  static constexpr int NM = D / 16;
-  __device__ __forceinline__ static int dim(int s, int m) { return 16 * m + 4 * s; }
+// the rows' last scored blocks (min'd with the last valid block) for rows
+// r0 .. r0 + 63, by wave 0: each lane its row, the wave's maximum returned
+__device__ __forceinline__ int rows_reach(const srswa_hc_score_bwd_args& a, int b, int row, int lastv) {
+  return row < a.S ? min(last_remote_block(a.pos[(int64_t)b * a.pos_sb + (int64_t)row * a.pos_st], a.block_size,
+                                           a.local_blocks),
+                         lastv)
+                   : -1;
+}
+
+// dZ of a 64 x 64 (rows x blocks) tile, loaded ahead: a thread's entries are
+// rows tid / 64 + 4 i and block tid % 64.  Buffer loads from the tile's first
+// row: the range ends at the last row's last block, so rows past S read as
+// zero (and give dZ = 0); blocks past nblk are dropped when stored.
+constexpr int kZpt = kTsRows * kTsGroup / 256;
+
+struct DzAhead {
+  float g[kZpt], z[kZpt];
+  __device__ __forceinline__ void fetch(const srswa_hc_score_bwd_args& a, int b, int r0, int g0) {
+    const int nr = min(kTsRows, a.S - r0);
+    const auto rg = make_rsrc(a.gz + (int64_t)b * a.gz_sb + (int64_t)r0 * a.gz_st + g0,
+                              (uint32_t)(((int64_t)(nr - 1) * a.gz_st + a.nblk - g0) * 4));
+    const auto rz = make_rsrc(a.z + (int64_t)b * a.z_sb + (int64_t)r0 * a.z_st + g0,
+                              (uint32_t)(((int64_t)(nr - 1) * a.z_st + a.nblk - g0) * 4));
+    const uint32_t r = threadIdx.x / kTsGroup, c = threadIdx.x % kTsGroup;
+#pragma unroll
+    for (int i = 0; i < kZpt; ++i) {
+      g[i] = __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(rg, 4 * ((r + 4 * i) * (uint32_t)a.gz_st + c), 0, 0));
+      z[i] = __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(rz, 4 * ((r + 4 * i) * (uint32_t)a.z_st + c), 0, 0));
+    }
+  }
+  // dZ into s_dz[row * pitch + block]
+  __device__ __forceinline__ void store(const srswa_hc_score_bwd_args& a, int g0, float isd, float* s_dz,
+                                        int pitch) const {
+    const int r = threadIdx.x / kTsGroup, c = threadIdx.x % kTsGroup;
+    const uint32_t keep = g0 + c < a.nblk ? ~0u : 0u;      // a mask, not a branch
+#pragma unroll
+    for (int i = 0; i < kZpt; ++i)
+      s_dz[(r + 4 * i) * pitch + c] = __uint_as_float(__float_as_uint(dz_raw(g[i], z[i], isd)) & keep);
+  }
 };
 
-// dz_raw of the tile (rows r0.., blocks g0..g0+gn) into s_dz[row][block]
-__device__ __forceinline__ void load_dz_tile(const srswa_hc_score_bwd_args& a, int b, int r0, int nr, int g0, int gn,
-                                             float isd, float* s_dz) {
-  for (int i = threadIdx.x; i < kTsRows * gn; i += blockDim.x) {
-    const int r = i / gn, c = i % gn;
-    float d = 0.f;
-    if (r < nr) {
-      const int64_t o = (int64_t)(r0 + r);
-      d = dz_raw(a.gz[(int64_t)b * a.gz_sb + o * a.gz_st + g0 + c], a.z[(int64_t)b * a.z_sb + o * a.z_st + g0 + c], isd);
-    }
-    s_dz[r * kTsPad + c] = d;
-  }
-}
-
+// dQ = dZ K_bar over the remote blocks on fp32 MFMA, one 64-row tile and a
+// 64-dim slice of the head dims per workgroup: per group of 64 blocks up to
+// the tile's last remote one, dZ (from the upstream gradient and the
+// forward's scores) and the slice of the blocks' k_bar rows are staged in
+// LDS, the next group's loaded ahead.  Wave w accumulates the 32 x 32 tile of
+// rows 32 (w & 1) .. + 31 and slice dims 32 (w >> 1) .. + 31; in step group m
+// lane half h supplies blocks 8 m + 4 h .. + 3 (dZ one 16-byte read, k_bar
+// single reads whose lane halves fall 32 banks apart).  The D / 64 slices of a
+// tile run on one XCD one after another (dZ stays in that L2); tiles go
+// heaviest (last rows) first.
 template <int D>
 __global__ __launch_bounds__(256) void hc_score_bwd_dq_kernel(HcBK p) {
-  using SL = Slice<D>;
-  __shared__ __align__(16) float s_kb[kTsGroup * D];
-  __shared__ float s_dz[kTsRows * kTsPad];
-  __shared__ int s_red[4];
+  constexpr int NS = D / 64;                       // dim slices
+  constexpr int KBP = 64 + 8;                      // k_bar slice pitch
+  constexpr int DZP = kTsGroup + 4;                // dZ row pitch
+  constexpr int KPT = kTsGroup * 16 / 256;         // 16-byte k_bar pieces per thread
+  __shared__ __align__(16) float s_kb[kTsGroup * KBP];
+  __shared__ __align__(16) float s_dz[kTsRows * DZP];
+  __shared__ int s_trm;
   const srswa_hc_score_bwd_args& a = p.a;
-  const int wave = threadIdx.x / kWave, lane = threadIdx.x % kWave;
-  const int ntiles = (a.S + kTsRows - 1) / kTsRows;
-  const int b = blockIdx.x / ntiles, tile = blockIdx.x % ntiles;
-  const int r0 = tile * kTsRows;
-  const int nr = min(kTsRows, a.S - r0);
-  const int rl = 16 * wave + lane / 4, s = lane % 4;
-  // tile_rmax over the workgroup's 64 rows (one per thread of the first 64... every
-  // thread maps to a row of the tile)
-  int rm = -1;
-  {
-    const int row = r0 + (int)(threadIdx.x % kTsRows);
-    if (row < a.S)
-      rm = last_remote_block(a.pos[(int64_t)b * a.pos_sb + (int64_t)row * a.pos_st], a.block_size, a.local_blocks);
+  const int tid = threadIdx.x, wave = __builtin_amdgcn_readfirstlane(tid / kWave), lane = tid % kWave;
+  const int h = lane / 32, rl = lane % 32;
+  const int ntiles = ceil_div(a.S, kTsRows);
+  int item, ds;
+  if (!xcd_item(a.B * ntiles, NS, item, ds)) return;
+  const int b = item % a.B, tile = ntiles - 1 - item / a.B;
+  const int r0 = tile * kTsRows, d0 = 64 * ds;
+  const int lastv = min(a.nblk - 1, (a.S - 1) / a.block_size);
+  if (tid < kTsRows) {
+    const int wm = wave_max_int(rows_reach(a, b, r0 + tid, lastv));
+    if (tid == 0) s_trm = wm;
   }
-  const int wm = wave_max_int(rm);
-  if (lane == 0) s_red[wave] = wm;
-  __syncthreads();
-  const int trm = min(max(max(s_red[0], s_red[1]), max(s_red[2], s_red[3])),
-                      min(a.nblk - 1, (a.S - 1) / a.block_size));
-  float acc[4 * SL::NM];
+  const int wr = 32 * (wave & 1), wd = 32 * (wave >> 1);
+  // the slice of the k_bar rows: blocks past nblk read as zero
+  const auto rkb = make_rsrc(a.kbar + (int64_t)b * a.kb_sb + d0, (uint32_t)(a.nblk * D - d0) * 4);
+  uint4 kpre[KPT];
+  DzAhead dza;
+  auto fetch = [&](int g0) {
 #pragma unroll
-  for (int i = 0; i < 4 * SL::NM; ++i) acc[i] = 0.f;
-  for (int g0 = 0; g0 <= trm; g0 += kTsGroup) {
-    const int gn = min(kTsGroup, a.nblk - g0);
-    __syncthreads();
-    for (int i = threadIdx.x; i < gn * (D / 4); i += blockDim.x) {
-      const int c = i / (D / 4), e = 4 * (i % (D / 4));
-      *reinterpret_cast<float4*>(s_kb + c * D + e) =
-          *reinterpret_cast<const float4*>(a.kbar + (int64_t)b * a.kb_sb + (int64_t)(g0 + c) * D + e);
+    for (int i = 0; i < KPT; ++i) {
+      const uint32_t pc = tid + 256 * i;
+      kpre[i] = buffer_load16(rkb, 4 * (((uint32_t)g0 + pc / 16) * D + 4 * (pc % 16)), 0);
     }
-    load_dz_tile(a, b, r0, nr, g0, gn, p.isd, s_dz);
-    __syncthreads();
-    const int cn = min(gn, trm - g0 + 1);
-    for (int c = 0; c < cn; ++c) {
-      const float d = s_dz[rl * kTsPad + c];
+    dza.fetch(a, b, r0, g0);
+  };
+  lds_barrier();
+  const int trm = __builtin_amdgcn_readfirstlane(s_trm);
+  const int ngs = trm >= 0 ? trm / kTsGroup + 1 : 0;
+  f32x16_t acc = zero16();
+  if (ngs > 0) fetch(0);
+  for (int gi = 0; gi < ngs; ++gi) {
+    const int g0 = gi * kTsGroup;
+    lds_barrier();                                 // the previous group is consumed
 #pragma unroll
-      for (int m = 0; m < SL::NM; ++m) {
-        const float4 kv = *reinterpret_cast<const float4*>(s_kb + c * D + SL::dim(s, m));
-        acc[4 * m] = fmaf(d, kv.x, acc[4 * m]);
-        acc[4 * m + 1] = fmaf(d, kv.y, acc[4 * m + 1]);
-        acc[4 * m + 2] = fmaf(d, kv.z, acc[4 * m + 2]);
-        acc[4 * m + 3] = fmaf(d, kv.w, acc[4 * m + 3]);
-      }
+    for (int i = 0; i < KPT; ++i) {
+      const int pc = tid + 256 * i;
+      *reinterpret_cast<uint4*>(s_kb + (pc / 16) * KBP + 4 * (pc % 16)) = kpre[i];
+    }
+    dza.store(a, g0, p.isd, s_dz, DZP);
+    lds_barrier();
+    if (gi + 1 < ngs) fetch(g0 + kTsGroup);
+    // every block of the group (dZ is zero past the rows' reach): a skip per
+    // step would split the accumulator chain
+    const float* dzr = s_dz + (wr + rl) * DZP + 4 * h;
+    const float* kbr = s_kb + 4 * h * KBP + wd + rl;
+#pragma unroll
+    for (int m = 0; m < kTsGroup / 8; ++m) {
+      const float4 d4 = *reinterpret_cast<const float4*>(dzr + 8 * m);
+      acc = __builtin_amdgcn_mfma_f32_32x32x2f32(d4.x, kbr[(8 * m) * KBP], acc, 0, 0, 0);
+      acc = __builtin_amdgcn_mfma_f32_32x32x2f32(d4.y, kbr[(8 * m + 1) * KBP], acc, 0, 0, 0);
+      acc = __builtin_amdgcn_mfma_f32_32x32x2f32(d4.z, kbr[(8 * m + 2) * KBP], acc, 0, 0, 0);
+      acc = __builtin_amdgcn_mfma_f32_32x32x2f32(d4.w, kbr[(8 * m + 3) * KBP], acc, 0, 0, 0);
     }
   }
-  if (rl < nr) {
-    float* dst = a.dq + (int64_t)b * a.dq_sb + (int64_t)(r0 + rl) * a.dq_st;
+  float* dq = a.dq + (int64_t)b * a.dq_sb + d0 + wd + rl;
 #pragma unroll
-    for (int m = 0; m < SL::NM; ++m)
-      *reinterpret_cast<float4*>(dst + SL::dim(s, m)) =
-          make_float4(acc[4 * m], acc[4 * m + 1], acc[4 * m + 2], acc[4 * m + 3]);
+  for (int r = 0; r < 16; ++r) {
+    const int row = r0 + wr + d_row(r, h);
+    if (row < a.S) dq[(int64_t)row * a.dq_st] = acc[r];
   }
 }
 
-// d k_bar partial of one 256-row chunk and 64 blocks: wave w owns blocks
-// 16 w .. 16 w + 15 of the group, four lanes per block
+// d k_bar partial of one 256-row chunk, 64 blocks and a 64-dim slice of the
+// head dims per workgroup on fp32 MFMA: per 64-row sub-chunk whose rows reach
+// the group, dZ and the slice of the query rows are staged in LDS (the next
+// such sub-chunk loaded ahead).  Wave w accumulates the 32 x 32 tile of
+// blocks 32 (w & 1) .. + 31 and slice dims 32 (w >> 1) .. + 31 (dZ^T Q); in
+// step group m lane half h supplies rows 8 m + 4 h .. + 3, both operands as
+// single reads whose lane halves fall 32 banks apart.  The partial is summed
+// over the sub-chunks in row order.  The D / 64 slices of a (chunk, group)
+// run on one XCD one after another.
 template <int D>
 __global__ __launch_bounds__(256) void hc_score_bwd_dkbar_kernel(HcBK p) {
-  using SL = Slice<D>;
-  __shared__ __align__(16) float s_q[kTsRows * D];
-  __shared__ float s_dz[kTsRows * kTsPad];
-  __shared__ int s_red[4];
+  constexpr int NS = D / 64;
+  constexpr int DZP = kTsGroup + 8;                // dZ row pitch
+  constexpr int QP = 64 + 8;                       // query slice pitch
+  constexpr int QPT = kTsRows * 16 / 256;          // 16-byte query pieces per thread
+  constexpr int NSUB = kTsChunk / kTsRows;
+  __shared__ __align__(16) float s_q[kTsRows * QP];
+  __shared__ __align__(16) float s_dz[kTsRows * DZP];
+  __shared__ int s_srm[NSUB];
   const srswa_hc_score_bwd_args& a = p.a;
-  const int wave = threadIdx.x / kWave, lane = threadIdx.x % kWave;
-  const int ngroups = (a.nblk + kTsGroup - 1) / kTsGroup;
-  const int chunk = blockIdx.x % p.nchunks;
-  const int g0 = ((blockIdx.x / p.nchunks) % ngroups) * kTsGroup;
-  const int b = blockIdx.x / (p.nchunks * ngroups);
-  const int gn = min(kTsGroup, a.nblk - g0);
-  const int cl = 16 * wave + lane / 4, s = lane % 4;
-  float acc[4 * SL::NM];
-#pragma unroll
-  for (int i = 0; i < 4 * SL::NM; ++i) acc[i] = 0.f;
+  const int tid = threadIdx.x, wave = __builtin_amdgcn_readfirstlane(tid / kWave), lane = tid % kWave;
+  const int h = lane / 32, rl = lane % 32;
+  const int ngroups = ceil_div(a.nblk, kTsGroup);
+  int item, ds;
+  if (!xcd_item(a.B * ngroups * p.nchunks, NS, item, ds)) return;
+  const int chunk = item % p.nchunks;
+  const int g0 = ((item / p.nchunks) % ngroups) * kTsGroup;
+  const int b = item / (p.nchunks * ngroups);
+  const int d0 = 64 * ds;
   const int lastv = min(a.nblk - 1, (a.S - 1) / a.block_size);
-  for (int sub = 0; sub < kTsChunk / kTsRows; ++sub) {
-    const int r0 = chunk * kTsChunk + sub * kTsRows;
-    if (r0 >= a.S) break;
-    const int nr = min(kTsRows, a.S - r0);
-    int rm = -1;
-    {
-      const int row = r0 + (int)(threadIdx.x % kTsRows);
-      if (row < a.S)
-        rm = last_remote_block(a.pos[(int64_t)b * a.pos_sb + (int64_t)row * a.pos_st], a.block_size, a.local_blocks);
-    }
-    const int wm = wave_max_int(rm);
-    __syncthreads();                      // the previous sub-chunk's tiles are consumed
-    if (lane == 0) s_red[wave] = wm;
-    __syncthreads();
-    const int srm = min(max(max(s_red[0], s_red[1]), max(s_red[2], s_red[3])), lastv);
-    if (srm < g0) continue;               // no row of the sub-chunk reaches the group (uniform)
-    for (int i = threadIdx.x; i < kTsRows * (D / 4); i += blockDim.x) {
-      const int r = i / (D / 4), e = 4 * (i % (D / 4));
-      *reinterpret_cast<float4*>(s_q + r * D + e) =
-          r < nr ? *reinterpret_cast<const float4*>(a.q + (int64_t)b * a.q_sb + (int64_t)(r0 + r) * a.q_st + e)
-                 : make_float4(0.f, 0.f, 0.f, 0.f);
-    }
-    load_dz_tile(a, b, r0, nr, g0, gn, p.isd, s_dz);
-    __syncthreads();
-    if (cl < gn) {
-      for (int r = 0; r < nr; ++r) {
-        const float d = s_dz[r * kTsPad + cl];
-#pragma unroll
-        for (int m = 0; m < SL::NM; ++m) {
-          const float4 qv = *reinterpret_cast<const float4*>(s_q + r * D + SL::dim(s, m));
-          acc[4 * m] = fmaf(d, qv.x, acc[4 * m]);
-          acc[4 * m + 1] = fmaf(d, qv.y, acc[4 * m + 1]);
-          acc[4 * m + 2] = fmaf(d, qv.z, acc[4 * m + 2]);
-          acc[4 * m + 3] = fmaf(d, qv.w, acc[4 * m + 3]);
-        }
-      }
-    }
+  {                                                // wave s: sub-chunk s's rows
+    const int wm = wave_max_int(rows_reach(a, b, chunk * kTsChunk + tid, lastv));
+    if (lane == 0) s_srm[wave] = wm;
   }
-  if (cl < gn) {
-    float* dst = p.dkb_part + (((int64_t)chunk * a.B + b) * a.nblk + g0 + cl) * D;
+  const int wc = 32 * (wave & 1), wd = 32 * (wave >> 1);
+  uint4 qpre[QPT];
+  DzAhead dza;
+  auto fetch = [&](int r0) {          // the sub-chunk's query slice: rows past S read as zero
+    const int nr = min(kTsRows, a.S - r0);
+    const auto rq = make_rsrc(a.q + (int64_t)b * a.q_sb + (int64_t)r0 * a.q_st + d0,
+                              (uint32_t)(((int64_t)(nr - 1) * a.q_st + 64) * 4));
 #pragma unroll
-    for (int m = 0; m < SL::NM; ++m)
-      *reinterpret_cast<float4*>(dst + SL::dim(s, m)) =
-          make_float4(acc[4 * m], acc[4 * m + 1], acc[4 * m + 2], acc[4 * m + 3]);
+    for (int i = 0; i < QPT; ++i) {
+      const uint32_t pc = tid + 256 * i;
+      qpre[i] = buffer_load16(rq, 4 * ((pc / 16) * (uint32_t)a.q_st + 4 * (pc % 16)), 0);
+    }
+    dza.fetch(a, b, r0, g0);
+  };
+  lds_barrier();
+  unsigned live = 0;                               // sub-chunks whose rows reach the group
+#pragma unroll
+  for (int s = 0; s < NSUB; ++s)
+    if (chunk * kTsChunk + s * kTsRows < a.S && s_srm[s] >= g0) live |= 1u << s;
+  live = __builtin_amdgcn_readfirstlane(live);
+  f32x16_t acc = zero16();
+  if (live) fetch(chunk * kTsChunk + kTsRows * __builtin_ctz(live));
+  while (live) {
+    live &= live - 1;                              // this sub-chunk's rows are the ones loaded ahead
+    lds_barrier();                                 // the previous sub-chunk is consumed
+#pragma unroll
+    for (int i = 0; i < QPT; ++i) {
+      const int pc = tid + 256 * i;
+      *reinterpret_cast<uint4*>(s_q + (pc / 16) * QP + 4 * (pc % 16)) = qpre[i];
+    }
+    dza.store(a, g0, p.isd, s_dz, DZP);
+    lds_barrier();
+    if (live) fetch(chunk * kTsChunk + kTsRows * __builtin_ctz(live));
+    const float* dzc = s_dz + 4 * h * DZP + wc + rl;
+    const float* qc = s_q + 4 * h * QP + wd + rl;
+#pragma unroll
+    for (int m = 0; m < kTsRows / 8; ++m)
+#pragma unroll
+      for (int x = 0; x < 4; ++x)
+        acc = __builtin_amdgcn_mfma_f32_32x32x2f32(dzc[(8 * m + x) * DZP], qc[(8 * m + x) * QP], acc, 0, 0, 0);
+  }
+  float* dst = p.dkb_part + ((int64_t)chunk * a.B + b) * a.nblk * D + d0 + wd + rl;
+#pragma unroll
+  for (int r = 0; r < 16; ++r) {
+    const int c = g0 + wc + d_row(r, h);
+    if (c < a.nblk) dst[(int64_t)c * D] = acc[r];
   }
 }
 
@@ -450,10 +543,21 @@ __global__ __launch_bounds__(256) void hc_summary_bwd_kernel(HcBK p) {
   float dkb[EPL];
 #pragma unroll
   for (int j = 0; j < EPL; ++j) dkb[j] = 0.f;
-  for (int ch = 0; ch < p.nchunks; ++ch) {
-    const float* src = p.dkb_part + (((int64_t)ch * a.B + b) * a.nblk + c) * D + EPL * lane;
+  constexpr int kAhead = 16;                       // partials loaded together, then added in chunk order
+  for (int ch0 = 0; ch0 < p.nchunks; ch0 += kAhead) {
+    float v[kAhead][EPL];
 #pragma unroll
-    for (int j = 0; j < EPL; ++j) dkb[j] += src[j];
+    for (int u = 0; u < kAhead; ++u) {
+      const int ch = min(ch0 + u, p.nchunks - 1);
+      const float* src = p.dkb_part + (((int64_t)ch * a.B + b) * a.nblk + c) * D + EPL * lane;
+#pragma unroll
+      for (int j = 0; j < EPL; ++j) v[u][j] = src[j];
+    }
+#pragma unroll
+    for (int u = 0; u < kAhead; ++u)
+      if (ch0 + u < p.nchunks)
+#pragma unroll
+        for (int j = 0; j < EPL; ++j) dkb[j] += v[u][j];
   }
   HcBlock<D> hb;
   hc_block_forward<D>(kg, a.k_st, s_hc, nv, BS, p.isd, s_w[wave], s_e[wave], s_pre[wave], hb);
@@ -510,16 +614,27 @@ __global__ __launch_bounds__(256) void hc_summary_bwd_kernel(HcBK p) {
   float hcl[EPL];
 #pragma unroll
   for (int j = 0; j < EPL; ++j) hcl[j] = s_hc[EPL * lane + j];
-#pragma unroll 4
-  for (int t = 0; t < nv; ++t) {
+  for (int u0 = 0; u0 < nv; u0 += kRowsAhead) {    // d head_cls, in key order
+    float rv[kRowsAhead][EPL];
+#pragma unroll
+    for (int u = 0; u < kRowsAhead; ++u) {
+      const float* row = kg + (int64_t)min(u0 + u, nv - 1) * a.k_st + EPL * lane;
+#pragma unroll
+      for (int j = 0; j < EPL; ++j) rv[u][j] = row[j];
+    }
+#pragma unroll
+    for (int u = 0; u < kRowsAhead; ++u)
+      if (u0 + u < nv) {
+        const float ds = s_ds[wave][u0 + u];
+#pragma unroll
+        for (int j = 0; j < EPL; ++j) dh[j] = fmaf(ds, rv[u][j], dh[j]);
+      }
+  }
+  for (int t = 0; t < nv; ++t) {                     // d k rows
     const float w = s_w[wave][t], ds = s_ds[wave][t];
-    const float* row = kg + (int64_t)t * a.k_st + EPL * lane;
     float* dst = a.dk + (int64_t)b * a.dk_sb + (int64_t)(t0 + t) * a.dk_st + EPL * lane;
 #pragma unroll
-    for (int j = 0; j < EPL; ++j) {
-      dst[j] = hb.pad_overflow ? 0.f : fmaf(w, dkb[j], ds * hcl[j]);
-      dh[j] = fmaf(ds, row[j], dh[j]);
-    }
+    for (int j = 0; j < EPL; ++j) dst[j] = hb.pad_overflow ? 0.f : fmaf(w, dkb[j], ds * hcl[j]);
   }
   float* hp = p.dhc_part + ((int64_t)b * a.nblk + c) * D + EPL * lane;
 #pragma unroll
@@ -536,7 +651,15 @@ __global__ __launch_bounds__(kDhcParts * D) void hc_dhc_reduce_kernel(HcBK p) {
   const int e = threadIdx.x % D, part = threadIdx.x / D;
   const int64_t n = (int64_t)p.a.B * p.a.nblk;
   float s = 0.f;
-  for (int64_t i = part; i < n; i += kDhcParts) s += p.dhc_part[i * D + e];
+  constexpr int kAhead = 16;                       // partials loaded together, then added in order
+  for (int64_t i0 = part; i0 < n; i0 += (int64_t)kAhead * kDhcParts) {
+    float v[kAhead];
+#pragma unroll
+    for (int u = 0; u < kAhead; ++u) v[u] = p.dhc_part[min(i0 + (int64_t)u * kDhcParts, n - 1) * D + e];
+#pragma unroll
+    for (int u = 0; u < kAhead; ++u)
+      if (i0 + (int64_t)u * kDhcParts < n) s += v[u];
+  }
   s_part[part][e] = s;
   __syncthreads();
   if (part == 0) {
@@ -588,7 +711,7 @@ __global__ __launch_bounds__(kBmThreads) void bm_fwd_kernel(BmK p) {
   __shared__ __align__(16) float sK[kChunk * KP];
   __shared__ int s_maxls;
   const srswa_bm_score_args& a = p.a;
-  const int tid = threadIdx.x, wave = tid / kWave, lane = tid % kWave;
+  const int tid = threadIdx.x, wave = __builtin_amdgcn_readfirstlane(tid / kWave), lane = tid % kWave;
   const int h = lane / 32, rl = lane % 32;
   const int slab = blockIdx.x % p.nslab;
   const int bt = blockIdx.x / p.nslab;
@@ -945,12 +1068,23 @@ extern "C" int srswa_hc_score_fwd(const srswa_hc_score_args* a, void* stream) {
     set_error("head_cls scores: rows must be 16-byte aligned and k_bar [B, nblk, D] dense per sequence");
     return SRSWA_UNSUPPORTED;
   }
+  // 32-bit buffer offsets into k_bar and a 64-row tile of z
+  if ((int64_t)a->nblk * a->D >= (int64_t(1) << 23) || a->z_st < a->nblk || a->z_st >= (int64_t(1) << 23)) {
+    set_error("head_cls scores: score rows must not overlap (z_st >= nblk) and z_st, nblk * D must stay below 2^23");
+    return SRSWA_UNSUPPORTED;
+  }
   HcK k{};
   k.a = *a;
   k.isd = 1.0f / sqrtf((float)a->D);
   hipStream_t st = reinterpret_cast<hipStream_t>(stream);
+  k.ngroups = ceil_div(a->nblk, kTsGroup);
   const unsigned gs = (unsigned)(((int64_t)a->B * a->nblk + 3) / 4);
-  const unsigned gz = (unsigned)((int64_t)a->B * ((a->S + kTsRows - 1) / kTsRows));
+  const int64_t gz64 = (int64_t)a->B * ceil_div(a->S, kTsRows);
+  if (gz64 > 0x7fffffff) {
+    set_error("head_cls scores: too many row tiles");
+    return SRSWA_UNSUPPORTED;
+  }
+  const unsigned gz = (unsigned)gz64;
   if (a->D == 128) {
     hipLaunchKernelGGL(hc_summary_fwd_kernel<128>, dim3(gs), dim3(256), 0, st, k);
     hipLaunchKernelGGL(hc_score_fwd_kernel<128>, dim3(gz), dim3(256), 0, st, k);
@@ -1005,6 +1139,14 @@ extern "C" int srswa_hc_score_bwd(const srswa_hc_score_bwd_args* a, void* scratc
     set_error("head_cls scores backward: rows must be 16-byte aligned and k_bar [B, nblk, D] dense per sequence");
     return SRSWA_UNSUPPORTED;
   }
+  // 32-bit buffer offsets within a 64-row tile
+  constexpr int64_t kMaxStride = int64_t(1) << 23;
+  if (a->z_st < a->nblk || a->gz_st < a->nblk || a->q_st < a->D || a->z_st >= kMaxStride ||
+      a->gz_st >= kMaxStride || a->q_st >= kMaxStride || (int64_t)a->nblk * a->D >= kMaxStride) {
+    set_error("head_cls scores backward: rows must not overlap (z_st, gz_st >= nblk, q_st >= D) and q_st, z_st, "
+              "gz_st, nblk * D must stay below 2^23");
+    return SRSWA_UNSUPPORTED;
+  }
   HcBK k{};
   k.a = *a;
   k.isd = 1.0f / sqrtf((float)a->D);
@@ -1012,10 +1154,16 @@ extern "C" int srswa_hc_score_bwd(const srswa_hc_score_bwd_args* a, void* scratc
   k.dkb_part = reinterpret_cast<float*>(scratch);
   k.dhc_part = k.dkb_part + (size_t)k.nchunks * a->B * a->nblk * a->D;
   hipStream_t st = reinterpret_cast<hipStream_t>(stream);
-  const int ntiles = (a->S + kTsRows - 1) / kTsRows;
-  const int ngroups = (a->nblk + kTsGroup - 1) / kTsGroup;
-  const dim3 gq((unsigned)((int64_t)a->B * ntiles));
-  const dim3 gk((unsigned)((int64_t)a->B * ngroups * k.nchunks));
+  // work items dealt to the XCDs with their D / 64 dim slices: (row tile) for
+  // dQ, (256-row chunk, block group) for d k_bar
+  const int64_t nq = (int64_t)a->B * ceil_div(a->S, kTsRows);
+  const int64_t nk = (int64_t)a->B * ceil_div(a->nblk, kTsGroup) * k.nchunks;
+  const int64_t gq64 = (nq + 7) / 8 * 8 * (a->D / 64), gk64 = (nk + 7) / 8 * 8 * (a->D / 64);
+  if (gq64 > 0x7fffffff || gk64 > 0x7fffffff) {
+    set_error("head_cls scores backward: too many work items");
+    return SRSWA_UNSUPPORTED;
+  }
+  const dim3 gq((unsigned)gq64), gk((unsigned)gk64);
   const dim3 gs((unsigned)(((int64_t)a->B * a->nblk + 3) / 4));
   if (a->D == 128) {
     hipLaunchKernelGGL(hc_score_bwd_dq_kernel<128>, gq, dim3(256), 0, st, k);
