@@ -39,13 +39,14 @@
 // offset, n, and flags for "several keys take the gradient" (their 64-bit mask
 // is then written to a side array) and "none does" -- in block-major order.
 //
-// Kernels: hc_summary_fwd (one wave per block), hc_score_fwd (64 query rows
-// per workgroup, one lane per row, k_bar of 64 blocks staged in LDS and read
-// as broadcasts), hc_score_bwd_dq (16 rows per wave, four lanes per row over
-// interleaved head-dim slices), hc_score_bwd_dkbar (the same shape over blocks,
-// fp32 partials per 256-row chunk), hc_summary_bwd (one wave per block: the
-// partials summed in chunk order, stage 0 redone, then its backward), and
-// hc_dhc_reduce (block partials of d head_cls summed in block order);
+// Kernels: hc_summary_fwd (one workgroup per block), hc_score_fwd (64 query
+// rows per workgroup, Z = Q K_bar^T as 32 x 32 fp32 MFMA tiles against groups
+// of 64 blocks staged in LDS), hc_score_bwd_dq (dQ = dZ K_bar, one row tile and
+// 64 head dims per workgroup), hc_score_bwd_dkbar (dK_bar = dZ^T Q as fp32
+// partials per 256-row chunk, one block group and 64 head dims per
+// workgroup), hc_summary_bwd (one workgroup per block: the partials summed in
+// a fixed chunk order, stage 0 redone, then its backward), and hc_dhc_reduce
+// (block partials of d head_cls summed in a fixed order);
 // bm_fwd (256 rows per workgroup, 64-key chunks through LDS, S^T = K Q^T on
 // v_mfma_f32_32x32x2_f32 as the inference block-max kernel, then per block the
 // clamped max, its tie and in-range masks), bm_bwd_dq (16 rows per wave, the
@@ -74,80 +75,111 @@ __device__ __forceinline__ float sanitize(float g) { return isfinite(g) ? clamp_
 __device__ __forceinline__ int last_remote_block(int p, int BS, int LB) { return p >= 0 ? p / BS - LB : -1; }
 
 // ---------------------------------------------------------------- stage 0
-// One wave summarises block c of sequence b (nv valid keys, rows at kg, k_st
-// apart, read from global memory: a block is at most 64 KiB and stays in the
-// caches over the two passes).  s_w receives the weights w_t, s_e e_t and
-// s_pre the unclamped logits pre_t (one entry per key, BS of them).  Returns
-// sum e (den), the row max and the lane's slice of kbar_raw: head dims
-// EPL lane .. EPL lane + EPL - 1.
+// One workgroup (256 threads) per block c of sequence b: nv valid keys, rows
+// at kg, k_st apart, read from global memory (a block is at most 64 KiB and
+// stays in the caches over the passes).  The logits go one key per thread;
+// passes over the key rows go one head dim per thread, in NQ = 256 / D key
+// slices (slice q takes keys q, q + NQ, ... in key order, rows loaded
+// kRowsAhead at a time), whose partials are then added in slice order.
 constexpr int kRowsAhead = 16;   // key rows loaded together by the block passes
 
-template <int D> struct HcBlock {
-  static constexpr int EPL = D / kWave;      // head dims per lane
-  float den, rowmax;
-  bool pad_overflow;
-  float kb[EPL];
+struct HcWgLds {
+  float pre[128], e[128], w[128], ds[128];   // per key: unclamped logit, exp, weight, d logit
+  float part[256];                           // slice partials [NQ][D]
+  float hc[128], dkb[128];
+  float red[4];
 };
 
+// the workgroup's max / sum of v (waves combined in wave order; every thread
+// gets the result)
+__device__ __forceinline__ float wg_max(float v, float* red) {
+  v = wave_max(v);
+  if (threadIdx.x % kWave == 0) red[threadIdx.x / kWave] = v;
+  __syncthreads();
+  const float r = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
+  __syncthreads();
+  return r;
+}
+__device__ __forceinline__ float wg_sum(float v, float* red) {
+  v = wave_sum(v);
+  if (threadIdx.x % kWave == 0) red[threadIdx.x / kWave] = v;
+  __syncthreads();
+  const float r = ((red[0] + red[1]) + red[2]) + red[3];
+  __syncthreads();
+  return r;
+}
+
+// sum over keys t < nv of coef[t] * k_t[e] for this thread's dim e, summed
+// over the key slices in order (valid for threads tid < D after the call)
 template <int D>
-__device__ void hc_block_forward(const float* kg, int64_t k_st, const float* s_hc, int nv, int BS, float isd,
-                                 float* s_w, float* s_e, float* s_pre, HcBlock<D>& out) {
-  constexpr int EPL = HcBlock<D>::EPL;
-  const int lane = threadIdx.x % kWave;
-  // logits, one key per lane (two rounds for BS = 128)
-  float mx = -INFINITY;
-  for (int t = lane; t < BS; t += kWave) {
-    float pre = 0.f;
-    if (t < nv) {
-      const float* row = kg + (int64_t)t * k_st;
-      float s = 0.f;
+__device__ __forceinline__ float keys_weighted(const float* kg, int64_t k_st, int nv, const float* coef, float* part) {
+  constexpr int NQ = 256 / D;
+  const int e = threadIdx.x % D, q = threadIdx.x / D;
+  float acc = 0.f;
+  for (int t0 = q; t0 < nv; t0 += NQ * kRowsAhead) {
+    float rv[kRowsAhead];
 #pragma unroll
-      for (int e = 0; e < D; e += 4) {
-        const float4 kv = *reinterpret_cast<const float4*>(row + e);
-        s = fmaf(kv.x, s_hc[e], s);
-        s = fmaf(kv.y, s_hc[e + 1], s);
-        s = fmaf(kv.z, s_hc[e + 2], s);
-        s = fmaf(kv.w, s_hc[e + 3], s);
-      }
-      pre = s * isd;
-      mx = fmaxf(mx, clamp_act(pre));
-    }
-    s_pre[t] = pre;
-  }
-  mx = wave_max(mx);
-  const float rowmax = nv > 0 ? mx : 0.f;
-  float part = 0.f;
-  for (int t = lane; t < BS; t += kWave) {
-    const float e = t < nv ? expf(clamp_act(s_pre[t]) - rowmax) : 0.f;
-    s_e[t] = e;
-    part += e;
-  }
-  const float den = wave_sum(part);
-  const float dn = fmaxf(den, 1e-6f);
-  for (int t = lane; t < BS; t += kWave) s_w[t] = s_e[t] / dn;
-  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-  __builtin_amdgcn_wave_barrier();
-  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-  // kbar_raw over the lane's dims (coalesced rows), in key order: rows loaded
-  // kRowsAhead at a time so their latencies overlap
-#pragma unroll
-  for (int j = 0; j < EPL; ++j) out.kb[j] = 0.f;
-  for (int t0 = 0; t0 < nv; t0 += kRowsAhead) {
-    float rv[kRowsAhead][EPL];
-#pragma unroll
-    for (int u = 0; u < kRowsAhead; ++u) {
-      const float* row = kg + (int64_t)min(t0 + u, nv - 1) * k_st + EPL * lane;
-#pragma unroll
-      for (int j = 0; j < EPL; ++j) rv[u][j] = row[j];
-    }
+    for (int u = 0; u < kRowsAhead; ++u) rv[u] = kg[(int64_t)min(t0 + u * NQ, nv - 1) * k_st + e];
 #pragma unroll
     for (int u = 0; u < kRowsAhead; ++u)
-      if (t0 + u < nv) {
-        const float w = s_w[t0 + u];
-#pragma unroll
-        for (int j = 0; j < EPL; ++j) out.kb[j] = fmaf(w, rv[u][j], out.kb[j]);
-      }
+      if (t0 + u * NQ < nv) acc = fmaf(coef[t0 + u * NQ], rv[u], acc);
   }
+  part[q * D + e] = acc;
+  __syncthreads();
+  float s = 0.f;
+  if (threadIdx.x < D) {
+    s = part[threadIdx.x];
+#pragma unroll
+    for (int r = 1; r < NQ; ++r) s += part[r * D + threadIdx.x];
+  }
+  __syncthreads();
+  return s;
+}
+
+// k_t . v over the D dims for key t (v in LDS), fmaf chain in dim order
+template <int D>
+__device__ __forceinline__ float key_dot(const float* row, const float* v) {
+  float s = 0.f;
+#pragma unroll
+  for (int e = 0; e < D; e += 4) {
+    const float4 kv = *reinterpret_cast<const float4*>(row + e);
+    s = fmaf(kv.x, v[e], s);
+    s = fmaf(kv.y, v[e + 1], s);
+    s = fmaf(kv.z, v[e + 2], s);
+    s = fmaf(kv.w, v[e + 3], s);
+  }
+  return s;
+}
+
+struct HcBlockOut {
+  float den, rowmax;
+  bool pad_overflow;
+  float kb;          // kbar_raw of head dim tid (threads tid < D)
+};
+
+// The block's stage-0 forward: L.pre, L.e, L.w per key (BS entries), the
+// weighted summary kbar_raw and the softmax statistics.  L.hc holds head_cls.
+template <int D>
+__device__ void hc_block_forward(const float* kg, int64_t k_st, int nv, int BS, float isd, HcWgLds& L,
+                                 HcBlockOut& out) {
+  const int tid = threadIdx.x;
+  float pre = 0.f, cl = -INFINITY;
+  if (tid < nv) {
+    pre = key_dot<D>(kg + (int64_t)tid * k_st, L.hc) * isd;
+    cl = clamp_act(pre);
+  }
+  if (tid < BS) L.pre[tid] = pre;
+  const float mx = wg_max(cl, L.red);
+  const float rowmax = nv > 0 ? mx : 0.f;
+  const float e = tid < nv ? expf(cl - rowmax) : 0.f;
+  const float den = wg_sum(e, L.red);
+  const float dn = fmaxf(den, 1e-6f);
+  if (tid < BS) {
+    L.e[tid] = e;
+    L.w[tid] = e / dn;
+  }
+  __syncthreads();
+  out.kb = keys_weighted<D>(kg, k_st, nv, L.w, L.part);
   out.den = den;
   out.rowmax = rowmax;
   // a padding key's weight is exp(0 - m) * 0: NaN once exp(-m) overflows
@@ -162,24 +194,17 @@ struct HcK {
 
 template <int D>
 __global__ __launch_bounds__(256) void hc_summary_fwd_kernel(HcK p) {
-  constexpr int EPL = HcBlock<D>::EPL;
-  __shared__ float s_w[4][128], s_e[4][128], s_pre[4][128];
-  __shared__ float s_hc[D];
+  __shared__ HcWgLds L;
   const srswa_hc_score_args& a = p.a;
-  const int wave = threadIdx.x / kWave, lane = threadIdx.x % kWave;
-  for (int e = threadIdx.x; e < D; e += blockDim.x) s_hc[e] = a.head_cls[e];
+  const int b = (int)(blockIdx.x / (unsigned)a.nblk), c = (int)(blockIdx.x % (unsigned)a.nblk);
+  if (threadIdx.x < D) L.hc[threadIdx.x] = a.head_cls[threadIdx.x];
   __syncthreads();
-  const int64_t gb = (int64_t)blockIdx.x * 4 + wave;
-  if (gb >= (int64_t)a.B * a.nblk) return;
-  const int b = (int)(gb / a.nblk), c = (int)(gb % a.nblk);
   const int t0 = c * a.block_size;
   const int nv = max(0, min(a.block_size, a.S - t0));
-  HcBlock<D> hb;
-  hc_block_forward<D>(a.k + (int64_t)b * a.k_sb + (int64_t)t0 * a.k_st, a.k_st, s_hc, nv, a.block_size, p.isd,
-                      s_w[wave], s_e[wave], s_pre[wave], hb);
-  float* dst = a.kbar + (int64_t)b * a.kb_sb + (int64_t)c * D + EPL * lane;
-#pragma unroll
-  for (int j = 0; j < EPL; ++j) dst[j] = (isfinite(hb.kb[j]) && !hb.pad_overflow) ? hb.kb[j] : 0.f;
+  HcBlockOut hb;
+  hc_block_forward<D>(a.k + (int64_t)b * a.k_sb + (int64_t)t0 * a.k_st, a.k_st, nv, a.block_size, p.isd, L, hb);
+  if (threadIdx.x < D)
+    a.kbar[(int64_t)b * a.kb_sb + (int64_t)c * D + threadIdx.x] = (isfinite(hb.kb) && !hb.pad_overflow) ? hb.kb : 0.f;
 }
 
 // ---------------------------------------------------------------- scores
@@ -520,125 +545,75 @@ __global__ __launch_bounds__(256) void hc_score_bwd_dkbar_kernel(HcBK p) {
   }
 }
 
-// stage-0 backward, one wave per block: d idx_k rows of the block and the
-// block's partial of d head_cls
+// stage-0 backward, one workgroup per block: d idx_k rows of the block and
+// the block's partial of d head_cls
 template <int D>
 __global__ __launch_bounds__(256) void hc_summary_bwd_kernel(HcBK p) {
-  constexpr int EPL = HcBlock<D>::EPL;
-  __shared__ float s_w[4][128], s_e[4][128], s_pre[4][128], s_ds[4][128];
-  __shared__ float s_dkb[4][D];
-  __shared__ float s_hc[D];
+  constexpr int NQ = 256 / D;
+  __shared__ HcWgLds L;
   const srswa_hc_score_bwd_args& a = p.a;
-  const int wave = threadIdx.x / kWave, lane = threadIdx.x % kWave;
-  for (int e = threadIdx.x; e < D; e += blockDim.x) s_hc[e] = a.head_cls[e];
-  __syncthreads();
-  const int64_t gb = (int64_t)blockIdx.x * 4 + wave;
-  if (gb >= (int64_t)a.B * a.nblk) return;
-  const int b = (int)(gb / a.nblk), c = (int)(gb % a.nblk);
+  const int tid = threadIdx.x;
+  const int b = (int)(blockIdx.x / (unsigned)a.nblk), c = (int)(blockIdx.x % (unsigned)a.nblk);
+  if (tid < D) L.hc[tid] = a.head_cls[tid];
   const int BS = a.block_size;
   const int t0 = c * BS;
   const int nv = max(0, min(BS, a.S - t0));
   const float* kg = a.k + (int64_t)b * a.k_sb + (int64_t)t0 * a.k_st;
-  // d k_bar: the chunk partials in chunk order
-  float dkb[EPL];
+  {
+    // d k_bar: the chunk partials, slice q taking chunks q, q + NQ, ... in
+    // order, the slices then added in order
+    const int e = tid % D, q = tid / D;
+    constexpr int kAhead = 16;
+    float acc = 0.f;
+    for (int ch0 = q; ch0 < p.nchunks; ch0 += NQ * kAhead) {
+      float v[kAhead];
 #pragma unroll
-  for (int j = 0; j < EPL; ++j) dkb[j] = 0.f;
-  constexpr int kAhead = 16;                       // partials loaded together, then added in chunk order
-  for (int ch0 = 0; ch0 < p.nchunks; ch0 += kAhead) {
-    float v[kAhead][EPL];
+      for (int u = 0; u < kAhead; ++u)
+        v[u] = p.dkb_part[(((int64_t)min(ch0 + u * NQ, p.nchunks - 1) * a.B + b) * a.nblk + c) * D + e];
 #pragma unroll
-    for (int u = 0; u < kAhead; ++u) {
-      const int ch = min(ch0 + u, p.nchunks - 1);
-      const float* src = p.dkb_part + (((int64_t)ch * a.B + b) * a.nblk + c) * D + EPL * lane;
-#pragma unroll
-      for (int j = 0; j < EPL; ++j) v[u][j] = src[j];
+      for (int u = 0; u < kAhead; ++u)
+        if (ch0 + u * NQ < p.nchunks) acc += v[u];
     }
-#pragma unroll
-    for (int u = 0; u < kAhead; ++u)
-      if (ch0 + u < p.nchunks)
-#pragma unroll
-        for (int j = 0; j < EPL; ++j) dkb[j] += v[u][j];
+    L.part[q * D + e] = acc;
   }
-  HcBlock<D> hb;
-  hc_block_forward<D>(kg, a.k_st, s_hc, nv, BS, p.isd, s_w[wave], s_e[wave], s_pre[wave], hb);
+  __syncthreads();
+  float dkb = 0.f;
+  if (tid < D) {
+    dkb = L.part[tid];
+#pragma unroll
+    for (int r = 1; r < NQ; ++r) dkb += L.part[r * D + tid];
+  }
+  __syncthreads();
+  HcBlockOut hb;
+  hc_block_forward<D>(kg, a.k_st, nv, BS, p.isd, L, hb);
   // nan_to_num(k_bar) passes no gradient where k_bar_raw is not finite
-#pragma unroll
-  for (int j = 0; j < EPL; ++j) {
-    if (!isfinite(hb.kb[j]) || hb.pad_overflow) dkb[j] = 0.f;
-    s_dkb[wave][EPL * lane + j] = dkb[j];
-  }
-  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-  __builtin_amdgcn_wave_barrier();
-  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+  if (tid < D) L.dkb[tid] = (!isfinite(hb.kb) || hb.pad_overflow) ? 0.f : dkb;
+  __syncthreads();
   const float dn = fmaxf(hb.den, 1e-6f);
-  // dw_t = dkbar . k_t, one key per lane
-  float dwv[2] = {0.f, 0.f};
-  float se = 0.f;
-  for (int r = 0; r < 2; ++r) {
-    const int t = lane + kWave * r;
-    if (t < nv) {
-      const float* row = kg + (int64_t)t * a.k_st;
-      float s = 0.f;
-#pragma unroll
-      for (int e = 0; e < D; e += 4) {
-        const float4 kv = *reinterpret_cast<const float4*>(row + e);
-        s = fmaf(kv.x, s_dkb[wave][e], s);
-        s = fmaf(kv.y, s_dkb[wave][e + 1], s);
-        s = fmaf(kv.z, s_dkb[wave][e + 2], s);
-        s = fmaf(kv.w, s_dkb[wave][e + 3], s);
-      }
-      dwv[r] = s;
-      se += s * s_e[wave][t];
+  // dw_t = dkbar . k_t, one key per thread
+  float dw = 0.f;
+  if (tid < nv) dw = key_dot<D>(kg + (int64_t)tid * a.k_st, L.dkb);
+  const float se = wg_sum(tid < nv ? dw * L.e[tid] : 0.f, L.red);
+  const float dden = hb.den >= 1e-6f ? -se / (dn * dn) : 0.f;
+  if (tid < BS) {
+    float ds = 0.f;
+    if (tid < nv) {
+      const float de = dw / dn + dden;
+      const float pre = L.pre[tid];
+      ds = (pre >= -kActClamp && pre <= kActClamp) ? de * L.e[tid] * p.isd : 0.f;
     }
+    L.ds[tid] = ds;
   }
-  const float dden = hb.den >= 1e-6f ? -wave_sum(se) / (dn * dn) : 0.f;
-  for (int r = 0; r < 2; ++r) {
-    const int t = lane + kWave * r;
-    if (t < BS) {
-      float ds = 0.f;
-      if (t < nv) {
-        const float de = dwv[r] / dn + dden;
-        const float pre = s_pre[wave][t];
-        ds = (pre >= -kActClamp && pre <= kActClamp) ? de * s_e[wave][t] * p.isd : 0.f;
-      }
-      s_ds[wave][t] = ds;
-    }
-  }
-  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-  __builtin_amdgcn_wave_barrier();
-  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-  // d k_t over the lane's dims, and the block's d head_cls
-  float dh[EPL];
-#pragma unroll
-  for (int j = 0; j < EPL; ++j) dh[j] = 0.f;
-  float hcl[EPL];
-#pragma unroll
-  for (int j = 0; j < EPL; ++j) hcl[j] = s_hc[EPL * lane + j];
-  for (int u0 = 0; u0 < nv; u0 += kRowsAhead) {    // d head_cls, in key order
-    float rv[kRowsAhead][EPL];
-#pragma unroll
-    for (int u = 0; u < kRowsAhead; ++u) {
-      const float* row = kg + (int64_t)min(u0 + u, nv - 1) * a.k_st + EPL * lane;
-#pragma unroll
-      for (int j = 0; j < EPL; ++j) rv[u][j] = row[j];
-    }
-#pragma unroll
-    for (int u = 0; u < kRowsAhead; ++u)
-      if (u0 + u < nv) {
-        const float ds = s_ds[wave][u0 + u];
-#pragma unroll
-        for (int j = 0; j < EPL; ++j) dh[j] = fmaf(ds, rv[u][j], dh[j]);
-      }
-  }
-  for (int t = 0; t < nv; ++t) {                     // d k rows
-    const float w = s_w[wave][t], ds = s_ds[wave][t];
-    float* dst = a.dk + (int64_t)b * a.dk_sb + (int64_t)(t0 + t) * a.dk_st + EPL * lane;
-#pragma unroll
-    for (int j = 0; j < EPL; ++j) dst[j] = hb.pad_overflow ? 0.f : fmaf(w, dkb[j], ds * hcl[j]);
-  }
-  float* hp = p.dhc_part + ((int64_t)b * a.nblk + c) * D + EPL * lane;
-#pragma unroll
-  for (int j = 0; j < EPL; ++j) hp[j] = hb.pad_overflow ? __builtin_nanf("") : dh[j];
+  __syncthreads();
+  // the block's d head_cls, then the d k rows (a dim per thread, slice q
+  // writing keys q, q + NQ, ...)
+  const float dh = keys_weighted<D>(kg, a.k_st, nv, L.ds, L.part);
+  if (tid < D) p.dhc_part[((int64_t)b * a.nblk + c) * D + tid] = hb.pad_overflow ? __builtin_nanf("") : dh;
+  const int e = tid % D;
+  const float dke = L.dkb[e], hce = L.hc[e];
+  float* dk = a.dk + (int64_t)b * a.dk_sb + (int64_t)t0 * a.dk_st + e;
+  for (int t = tid / D; t < nv; t += NQ)
+    dk[(int64_t)t * a.dk_st] = hb.pad_overflow ? 0.f : fmaf(L.w[t], dke, L.ds[t] * hce);
 }
 
 // d head_cls: eight interleaved slices of the block partials, each summed in
@@ -1078,7 +1053,7 @@ extern "C" int srswa_hc_score_fwd(const srswa_hc_score_args* a, void* stream) {
   k.isd = 1.0f / sqrtf((float)a->D);
   hipStream_t st = reinterpret_cast<hipStream_t>(stream);
   k.ngroups = ceil_div(a->nblk, kTsGroup);
-  const unsigned gs = (unsigned)(((int64_t)a->B * a->nblk + 3) / 4);
+  const unsigned gs = (unsigned)((int64_t)a->B * a->nblk);     // a workgroup per block
   const int64_t gz64 = (int64_t)a->B * ceil_div(a->S, kTsRows);
   if (gz64 > 0x7fffffff) {
     set_error("head_cls scores: too many row tiles");
@@ -1164,7 +1139,7 @@ extern "C" int srswa_hc_score_bwd(const srswa_hc_score_bwd_args* a, void* scratc
     return SRSWA_UNSUPPORTED;
   }
   const dim3 gq((unsigned)gq64), gk((unsigned)gk64);
-  const dim3 gs((unsigned)(((int64_t)a->B * a->nblk + 3) / 4));
+  const dim3 gs((unsigned)((int64_t)a->B * a->nblk));          // a workgroup per block
   if (a->D == 128) {
     hipLaunchKernelGGL(hc_score_bwd_dq_kernel<128>, gq, dim3(256), 0, st, k);
     hipLaunchKernelGGL(hc_score_bwd_dkbar_kernel<128>, gk, dim3(256), 0, st, k);
