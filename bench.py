@@ -936,7 +936,38 @@ def bench_train_scores(args):
     def bm_step():
         torch.autograd.backward([bm_fwd()], [gz])
 
+    # the head_cls kernels alone: the C ABI's forward and backward entry points
+    # on prebuilt arguments (no autograd, allocation or gradient accumulation,
+    # whose host time bounds the step at this size)
+    import ctypes
+    from srswa import _lib
+    lib, sp = _lib.lib(), _lib.stream_ptr(dev)
+    p32 = pos.to(torch.int32)
+    kbar = torch.empty(B, nblk, D, device=dev)
+    zk = torch.empty(B, S, nblk, device=dev)
+    dqk, dkk, dhk = torch.empty_like(q), torch.empty_like(k), torch.empty(D, device=dev)
+    common = dict(q=q.data_ptr(), q_sb=q.stride(0), q_st=q.stride(1), k=k.data_ptr(), k_sb=k.stride(0),
+                  k_st=k.stride(1), head_cls=hc.data_ptr(), pos=p32.data_ptr(), pos_sb=p32.stride(0),
+                  pos_st=p32.stride(1), kbar=kbar.data_ptr(), kb_sb=kbar.stride(0), z=zk.data_ptr(),
+                  z_sb=zk.stride(0), z_st=zk.stride(1), B=B, S=S, D=D, nblk=nblk, block_size=BS, local_blocks=LB)
+    fa = _lib.HcScoreArgs(**common)
+    ba = _lib.HcScoreBwdArgs(**common, gz=gz.data_ptr(), gz_sb=gz.stride(0), gz_st=gz.stride(1),
+                             dq=dqk.data_ptr(), dq_sb=dqk.stride(0), dq_st=dqk.stride(1), dk=dkk.data_ptr(),
+                             dk_sb=dkk.stride(0), dk_st=dkk.stride(1), dhc=dhk.data_ptr())
+    need = ctypes.c_size_t()
+    _lib.check(lib.srswa_hc_score_bwd_workspace(ctypes.byref(ba), ctypes.byref(need)), "hc bwd workspace")
+    scr = torch.empty(need.value, dtype=torch.uint8, device=dev)
+
+    def hc_fwd_kernels():
+        _lib.check(lib.srswa_hc_score_fwd(ctypes.byref(fa), sp), "srswa_hc_score_fwd")
+
+    def hc_bwd_kernels():
+        _lib.check(lib.srswa_hc_score_bwd(ctypes.byref(ba), ctypes.c_void_p(scr.data_ptr()), need.value, sp),
+                   "srswa_hc_score_bwd")
+
     with torch.no_grad():
+        ms_hc_fk = _time_launches(hc_fwd_kernels, args.steps, args.warmup, dev)
+        ms_hc_bk = _time_launches(hc_bwd_kernels, args.steps, args.warmup, dev)
         ms_hc_f = _time_launches(hc_fwd, args.steps, args.warmup, dev)
         ms_bm_f = _time_launches(bm_fwd, max(2, args.steps // 4), 2, dev)
     ms_hc = _time_launches(hc_step, args.steps, args.warmup, dev)
@@ -946,7 +977,7 @@ def bench_train_scores(args):
     hc_bytes = 2 * B * S * D * 4 + B * S * nblk * 4 + B * nblk * D * 4
     remote_pairs = B * sum(max(0, i - LB * BS + 1) for i in range(S))
     bm_flops = 2 * D * remote_pairs
-    hc_gbs = hc_bytes / (ms_hc_f * 1e-3) / 1e9
+    hc_gbs = hc_bytes / (ms_hc_fk * 1e-3) / 1e9
     bm_tfs = bm_flops / (ms_bm_f * 1e-3) / 1e12
     return {"metric": "DASH training stage-0 scorer fwd+bwd rows/s (head_cls, config 5 shape)",
             "value": B * S / (ms_hc * 1e-3), "unit": "rows/s", "n_gpus": 1, "steps": args.steps,
@@ -954,11 +985,12 @@ def bench_train_scores(args):
             "vs_baseline": None, "dtype": "f32", "data": "synthetic (seeded)",
             "config": {"workload": "DashAttention._block_scores_headcls / _block_scores from fp32 index q/k, "
                                    "B=2, S=16384, D=128, 64-key blocks", "head_cls_fwd_ms": ms_hc_f,
-                       "head_cls_fwd_bwd_ms": ms_hc, "block_max_fwd_ms": ms_bm_f, "block_max_fwd_bwd_ms": ms_bm,
+                       "head_cls_fwd_bwd_ms": ms_hc, "head_cls_fwd_kernels_ms": ms_hc_fk,
+                       "head_cls_bwd_kernels_ms": ms_hc_bk, "block_max_fwd_ms": ms_bm_f, "block_max_fwd_bwd_ms": ms_bm,
                        "head_cls_fwd_bytes": hc_bytes, "block_max_fwd_flops": bm_flops},
             "roofline": {"bound": "hbm", "achieved": hc_gbs, "peak": 8000.0, "unit": "GB/s",
                          "frac": hc_gbs / 8000.0, "traffic": None,
-                         "kernel": "head_cls forward (summary + score kernels)"},
+                         "kernel": "head_cls forward kernels (summary + score), launched on prebuilt arguments"},
             "roofline_block_max": {"bound": "mfma", "achieved": bm_tfs, "peak": 157.3, "unit": "TFLOP/s",
                                    "frac": bm_tfs / 157.3, "kernel": "bm_fwd_kernel (fp32 MFMA)"}}
 
