@@ -47,10 +47,10 @@
 // workgroup), hc_summary_bwd (one workgroup per block: the partials summed in
 // a fixed chunk order, stage 0 redone, then its backward), and hc_dhc_reduce
 // (block partials of d head_cls summed in a fixed order);
-// bm_fwd (256 rows per workgroup, 64-key chunks through LDS, S^T = K Q^T on
+// bm_fwd (128 rows per workgroup, 64-key chunks through LDS, S^T = K Q^T on
 // v_mfma_f32_32x32x2_f32 as the inference block-max kernel, then per block the
-// clamped max, its tie and in-range masks), bm_bwd_dq (16 rows per wave, the
-// arg-max key rows of 64 blocks gathered with one load per row in flight
+// clamped max, its tie and in-range masks), bm_bwd_dq (4 rows per wave, 16
+// waves per 64-row tile, the arg-max key rows of two blocks gathered
 // together) and bm_bwd_dk (four keys per wave, 16 lanes each, scanning the
 // block's codes in row order).  No atomics: every result is deterministic.
 #include <algorithm>
@@ -646,7 +646,7 @@ __global__ __launch_bounds__(kDhcParts * D) void hc_dhc_reduce_kernel(HcBK p) {
 }
 
 // ---------------------------------------------------------------- block max
-constexpr int kBmRows = 256;                 // query rows per workgroup (8 waves of 32)
+constexpr int kBmRows = 128;                 // query rows per workgroup (4 waves of 32)
 constexpr int kBmThreads = 2 * kBmRows;
 constexpr int kBmSlab = 16;                  // chunks of 64 keys per workgroup
 constexpr int kCodeMulti = 1 << 16;          // several keys take the gradient: mask in the side array
@@ -680,7 +680,7 @@ __device__ __forceinline__ uint64_t shfl_xor_u64(uint64_t v, int m) {
 }
 
 template <int D, int BS>
-__global__ __launch_bounds__(kBmThreads) void bm_fwd_kernel(BmK p) {
+__global__ __launch_bounds__(kBmThreads, 2) void bm_fwd_kernel(BmK p) {
   constexpr int KP = D + 4;
   constexpr int NSUB = kChunk / BS;
   __shared__ __align__(16) float sK[kChunk * KP];
@@ -805,17 +805,21 @@ struct BmBK {
 // the last block holding a key at or below p - LW (-1: none)
 __device__ __forceinline__ int bm_last_remote(int p, int LW, int BS) { return p - LW >= 0 ? (p - LW) / BS : -1; }
 
-// dq: 16 rows per wave (64 per workgroup); per group of 64 blocks the codes
-// and weights g / n are staged in LDS (and the weights stored block-major for
-// bm_bwd_dk), then for each block up to the tile's last remote one the 16
-// rows' key rows are loaded together (lanes over the head dims) and
-// accumulated in block order.
+// dq: 4 rows per wave, 16 waves per workgroup (64 rows); per group of 64
+// blocks the codes and weights g / n are staged in LDS (and the weights
+// stored block-major for bm_bwd_dk), then for each kBmBpi blocks up to the
+// tile's last remote one the wave's key rows of all of them are loaded
+// together (lanes over the head dims) and accumulated in block order.
+constexpr int kBmRpw = 4;                               // rows per wave
+constexpr int kBmDqWaves = kTsRows / kBmRpw;
+constexpr int kBmBpi = 2;                               // blocks gathered together (divides kTsGroup)
+
 template <int D, int BS>
-__global__ __launch_bounds__(256) void bm_bwd_dq_kernel(BmBK p) {
+__global__ __launch_bounds__(kBmDqWaves * kWave) void bm_bwd_dq_kernel(BmBK p) {
   constexpr int EPL = D / kWave;
   __shared__ int s_code[kTsGroup * kTsPad];     // [block][row]
   __shared__ float s_w[kTsGroup * kTsPad];      // [block][row]
-  __shared__ int s_red[4];
+  __shared__ int s_red[kBmDqWaves];
   const srswa_bm_score_bwd_args& a = p.a;
   const int wave = threadIdx.x / kWave, lane = threadIdx.x % kWave;
   const int ntiles = (a.S + kTsRows - 1) / kTsRows;
@@ -833,11 +837,14 @@ __global__ __launch_bounds__(256) void bm_bwd_dq_kernel(BmBK p) {
     const int wm = wave_max_int(rm);
     if (lane == 0) s_red[wave] = wm;
     __syncthreads();
-    trm = min(max(max(s_red[0], s_red[1]), max(s_red[2], s_red[3])), nblk_keys - 1);
-  }
-  float acc[16][EPL];
+    trm = s_red[0];
 #pragma unroll
-  for (int r = 0; r < 16; ++r)
+    for (int w = 1; w < kBmDqWaves; ++w) trm = max(trm, s_red[w]);
+    trm = min(trm, nblk_keys - 1);
+  }
+  float acc[kBmRpw][EPL];
+#pragma unroll
+  for (int r = 0; r < kBmRpw; ++r)
 #pragma unroll
     for (int j = 0; j < EPL; ++j) acc[r][j] = 0.f;
   for (int g0 = 0; g0 < nblk_keys; g0 += kTsGroup) {
@@ -870,48 +877,55 @@ __global__ __launch_bounds__(256) void bm_bwd_dq_kernel(BmBK p) {
       if (r < nr) wdst[(int64_t)c * a.S + r] = s_w[c * kTsPad + r];
     }
     const int cn = min(gn, trm - g0 + 1);
-    for (int c = 0; c < cn; ++c) {
-      const int blk = g0 + c;
-      float kv[16][EPL];
+    for (int c0 = 0; c0 < cn; c0 += kBmBpi) {               // c0 + kBmBpi <= 64: in the staged arrays
+      float kv[kBmBpi][kBmRpw][EPL];
 #pragma unroll
-      for (int r = 0; r < 16; ++r) {
-        const int rr = 16 * wave + r;
-        const int cd = s_code[c * kTsPad + rr];
-        const float w = s_w[c * kTsPad + rr];
+      for (int u = 0; u < kBmBpi; ++u)
 #pragma unroll
-        for (int e = 0; e < EPL; ++e) kv[r][e] = 0.f;
-        if (w != 0.f && !(cd & kCodeMulti)) {
-          const int j = blk * BS + (cd & 0xff);
+        for (int r = 0; r < kBmRpw; ++r) {
+          const int c = c0 + u, rr = kBmRpw * wave + r;
+          const int cd = s_code[c * kTsPad + rr];
+          const float w = s_w[c * kTsPad + rr];
 #pragma unroll
-          for (int e = 0; e < EPL; ++e) kv[r][e] = kg[(int64_t)j * a.k_st + e];
+          for (int e = 0; e < EPL; ++e) kv[u][r][e] = 0.f;
+          if (c < cn && w != 0.f && !(cd & kCodeMulti)) {
+            const int j = (g0 + c) * BS + (cd & 0xff);
+#pragma unroll
+            for (int e = 0; e < EPL; ++e) kv[u][r][e] = kg[(int64_t)j * a.k_st + e];
+          }
         }
-      }
 #pragma unroll
-      for (int r = 0; r < 16; ++r) {
-        const int rr = 16 * wave + r;
-        const int cd = s_code[c * kTsPad + rr];
-        const float w = s_w[c * kTsPad + rr];
-        if (w == 0.f) continue;
-        if (!(cd & kCodeMulti)) {
+      for (int u = 0; u < kBmBpi; ++u) {
+        const int c = c0 + u;
+        if (c >= cn) break;
+        const int blk = g0 + c;
 #pragma unroll
-          for (int e = 0; e < EPL; ++e) acc[r][e] = fmaf(w, kv[r][e], acc[r][e]);
-        } else {
-          // several keys share the gradient: each one in key order
-          uint64_t m = a.tiemask[((int64_t)b * a.S + r0 + rr) * a.nblk + blk];
-          while (m) {
-            const int off = __builtin_ctzll(m);
-            m &= m - 1;
-            const int j = blk * BS + off;
+        for (int r = 0; r < kBmRpw; ++r) {
+          const int rr = kBmRpw * wave + r;
+          const int cd = s_code[c * kTsPad + rr];
+          const float w = s_w[c * kTsPad + rr];
+          if (w == 0.f) continue;
+          if (!(cd & kCodeMulti)) {
 #pragma unroll
-            for (int e = 0; e < EPL; ++e) acc[r][e] = fmaf(w, kg[(int64_t)j * a.k_st + e], acc[r][e]);
+            for (int e = 0; e < EPL; ++e) acc[r][e] = fmaf(w, kv[u][r][e], acc[r][e]);
+          } else {
+            // several keys share the gradient: each one in key order
+            uint64_t m = a.tiemask[((int64_t)b * a.S + r0 + rr) * a.nblk + blk];
+            while (m) {
+              const int off = __builtin_ctzll(m);
+              m &= m - 1;
+              const int j = blk * BS + off;
+#pragma unroll
+              for (int e = 0; e < EPL; ++e) acc[r][e] = fmaf(w, kg[(int64_t)j * a.k_st + e], acc[r][e]);
+            }
           }
         }
       }
     }
   }
 #pragma unroll
-  for (int r = 0; r < 16; ++r) {
-    const int rr = 16 * wave + r;
+  for (int r = 0; r < kBmRpw; ++r) {
+    const int rr = kBmRpw * wave + r;
     if (rr < nr) {
       float* dst = a.dq + (int64_t)b * a.dq_sb + (int64_t)(r0 + rr) * a.dq_st + EPL * lane;
 #pragma unroll
@@ -1188,7 +1202,8 @@ template <int D, int BS>
 void bm_launch_bwd(const BmBK& k, hipStream_t st) {
   const srswa_bm_score_bwd_args& a = k.a;
   const int ntiles = (a.S + kTsRows - 1) / kTsRows;
-  hipLaunchKernelGGL((bm_bwd_dq_kernel<D, BS>), dim3((unsigned)((int64_t)a.B * ntiles)), dim3(256), 0, st, k);
+  hipLaunchKernelGGL((bm_bwd_dq_kernel<D, BS>), dim3((unsigned)((int64_t)a.B * ntiles)), dim3(kBmDqWaves * kWave), 0,
+                     st, k);
   const int64_t waves = (int64_t)a.B * std::min(a.nblk, (a.S + BS - 1) / BS) * (BS / 4);
   if (waves > 0)   // a multiple of 8 workgroups (the XCD deal), surplus ones exit at once
     hipLaunchKernelGGL((bm_bwd_dk_kernel<D, BS>), dim3((unsigned)(((waves + 3) / 4 + 7) / 8 * 8)), dim3(256), 0,
