@@ -690,7 +690,7 @@ __global__ __launch_bounds__(kBmThreads, 2) void bm_fwd_kernel(BmK p) {
   const int h = lane / 32, rl = lane % 32;
   const int slab = blockIdx.x % p.nslab;
   const int bt = blockIdx.x / p.nslab;
-  const int tile = bt % p.ntiles;
+  const int tile = p.ntiles - 1 - bt % p.ntiles;   // heaviest (last rows) first
   const int b = bt / p.ntiles;
   const int row = tile * kBmRows + wave * 32 + rl;
   const bool row_ok = row < a.S;
