@@ -565,17 +565,21 @@ __global__ __launch_bounds__(256) void decode_merge_kernel(DecodeK p) {
 #pragma unroll
   for (int e = 0; e < DPL; ++e) O[e] = 0.f;
   for (int s0 = 0; s0 < p.nsplit; s0 += 8) {
-    // issue all loads of up to 8 records before combining them
+    // all loads of up to 8 records issued before any is used: unconditional,
+    // from clamped record indices (a load behind a branch per record would be
+    // waited for on its own); the records past nsplit are masked afterwards
     float ms[8], ls[8], os[8][DPL];
 #pragma unroll
     for (int j = 0; j < 8; ++j) {
-      const bool in = s0 + j < p.nsplit;
-      const float* rec = recs + (int64_t)(in ? s0 + j : s0) * p.pstride;
-      ms[j] = in ? rec[D] : -INFINITY;
-      ls[j] = in ? rec[D + 1] : 0.f;
+      const float* rec = recs + (int64_t)min(s0 + j, p.nsplit - 1) * p.pstride;
+      ms[j] = rec[D];
+      ls[j] = rec[D + 1];
 #pragma unroll
-      for (int e = 0; e < DPL; ++e) os[j][e] = in ? rec[lane * DPL + e] : 0.f;
+      for (int e = 0; e < DPL; ++e) os[j][e] = rec[lane * DPL + e];
     }
+#pragma unroll
+    for (int j = 0; j < 8; ++j)
+      if (s0 + j >= p.nsplit) ms[j] = -INFINITY;    // wave-uniform
     float Mn = M;
 #pragma unroll
     for (int j = 0; j < 8; ++j) Mn = fmaxf(Mn, ms[j]);
@@ -585,7 +589,8 @@ __global__ __launch_bounds__(256) void decode_merge_kernel(DecodeK p) {
     for (int e = 0; e < DPL; ++e) O[e] *= r0;
 #pragma unroll
     for (int j = 0; j < 8; ++j) {
-      const float wt = ms[j] == -INFINITY ? 0.f : exp2f(ms[j] - Mn);
+      if (ms[j] == -INFINITY) continue;            // an empty or masked record adds nothing
+      const float wt = exp2f(ms[j] - Mn);
       L = fmaf(ls[j], wt, L);
 #pragma unroll
       for (int e = 0; e < DPL; ++e) O[e] = fmaf(os[j][e], wt, O[e]);
