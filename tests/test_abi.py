@@ -72,3 +72,37 @@ def test_workspace_query_needs_no_gpu():
     # 640 (row, head) pairs x 4 workgroups x 160-float records
     assert scr == 640 * 4 * 160 * 4
     assert srswa.__version__
+
+
+def _hc_args(cls, **over):
+    """head_cls scorer arguments with dummy 16-byte-aligned device addresses
+    (never dereferenced: every case below is refused before any launch)."""
+    a = cls()
+    B, S, D, nblk = 2, 1024, 128, 16
+    for i, name in enumerate(n for n, _ in cls._fields_ if n in ("q", "k", "head_cls", "pos", "kbar", "z", "gz",
+                                                                     "dq", "dk", "dhc")):
+        setattr(a, name, 0x100000 * (i + 1))
+    a.B, a.S, a.D, a.nblk, a.block_size, a.local_blocks = B, S, D, nblk, 64, 8
+    a.q_sb, a.q_st, a.k_sb, a.k_st = S * D, D, S * D, D
+    a.pos_sb, a.pos_st, a.kb_sb, a.z_sb, a.z_st = S, 1, nblk * D, S * nblk, nblk
+    if cls is _lib.HcScoreBwdArgs:
+        a.gz_sb, a.gz_st, a.dq_sb, a.dq_st, a.dk_sb, a.dk_st = S * nblk, nblk, S * D, D, S * D, D
+    for k, v in over.items():
+        setattr(a, k, v)
+    return a
+
+
+def test_hc_scores_refuse_overlapping_or_huge_rows():
+    """The head_cls scorers address z / gz / q tiles through buffer resources
+    with 32-bit offsets: overlapping rows and strides of 2^23 or more are
+    refused with SRSWA_UNSUPPORTED on the host (no GPU needed)."""
+    lib = _lib.lib()
+    assert lib.srswa_hc_score_fwd(ctypes.byref(_hc_args(_lib.HcScoreArgs, z_st=8)), None) == _lib.SRSWA_UNSUPPORTED
+    assert lib.srswa_hc_score_fwd(ctypes.byref(_hc_args(_lib.HcScoreArgs, z_st=1 << 23, z_sb=1 << 34)),
+                                  None) == _lib.SRSWA_UNSUPPORTED
+    for over in (dict(z_st=8), dict(gz_st=8), dict(q_st=64, k_st=128), dict(gz_st=1 << 23, gz_sb=1 << 34)):
+        a = _hc_args(_lib.HcScoreBwdArgs, **over)
+        need = ctypes.c_size_t()
+        assert lib.srswa_hc_score_bwd_workspace(ctypes.byref(a), ctypes.byref(need)) == _lib.SRSWA_OK
+        rc = lib.srswa_hc_score_bwd(ctypes.byref(a), ctypes.c_void_p(0x4000000), need.value, None)
+        assert rc == _lib.SRSWA_UNSUPPORTED, over
