@@ -74,6 +74,45 @@ def test_head_cls_scores_fwd_bwd(dev, name):
         assert e <= F32_REL, (ez, eq, ek, eh)
 
 
+@pytest.mark.parametrize("name", ["random_positions", "fewer_blocks_than_keys"])
+def test_head_cls_scores_general_layouts(dev, name):
+    """Arbitrary (non-monotonic) positions, so the rows of one 64-row tile reach
+    different blocks and some reach past the keys; and a block grid shorter
+    than the keys (nblk * bs < S: the later keys take no part and their dk rows
+    stay zero)."""
+    from srswa import train_scores as TS
+    g = torch.Generator().manual_seed(71 if name == "random_positions" else 72)
+    if name == "random_positions":
+        B, S, d, bs, lb = 2, 1300, 128, 32, 2
+        nblk = -(-S // bs)
+        pos = torch.randint(0, 1600, (B, S), generator=g)
+    else:
+        B, S, d, bs, lb = 1, 1000, 64, 16, 3
+        nblk = S // bs - 5
+        pos = torch.arange(S)[None] + 100
+    q = torch.randn(B, S, d, generator=g)
+    k = torch.randn(B, S, d, generator=g)
+    hc = torch.randn(d, generator=g) * 0.5
+    print(f"head_cls scores {name}: B={B} S={S} d={d} bs={bs} nblk={nblk}", flush=True)
+    qr, kr, hr = (x.double().requires_grad_() for x in (q, k, hc))
+    zr = T.headcls_scores(qr, kr, hr, pos, nblk, bs, lb)
+    gz = _upstream(zr.detach(), 8)
+    zr.backward(gz)
+    qd, kd, hd = (x.to(dev).requires_grad_() for x in (q, k, hc))
+    z = TS.head_cls_scores(qd, kd, hd, pos.to(dev), nblk, bs, lb)
+    masked = zr.detach() <= -1e8
+    assert torch.equal((z.detach().cpu() <= -1e8), masked)
+    ez = _rel(z.detach().masked_fill(masked.to(dev), 0), zr.detach().masked_fill(masked, 0))
+    z.backward(gz.float().to(dev))
+    eq, ek, eh = _rel(qd.grad, qr.grad), _rel(kd.grad, kr.grad), _rel(hd.grad, hr.grad)
+    report(f"[err] head_cls scores {name}: z max rel {ez:.3e}, dq {eq:.3e}, dk {ek:.3e}, "
+           f"d head_cls {eh:.3e} (bar {F32_REL})")
+    for e in (ez, eq, ek, eh):
+        assert e <= F32_REL, (ez, eq, ek, eh)
+    if name == "fewer_blocks_than_keys":
+        assert (kd.grad[:, nblk * bs:] == 0).all()
+
+
 def test_head_cls_scores_deterministic(dev):
     from srswa import train_scores as TS
     q, k, hc, pos, nblk, bs, lb = _hc_case("shipped_bs32_lb4", dev)
