@@ -616,14 +616,16 @@ __global__ __launch_bounds__(256) void hc_summary_bwd_kernel(HcBK p) {
     dk[(int64_t)t * a.dk_st] = hb.pad_overflow ? 0.f : fmaf(L.w[t], dke, L.ds[t] * hce);
 }
 
-// d head_cls: eight interleaved slices of the block partials, each summed in
-// block order, then the eight slice sums in slice order (fixed order)
-constexpr int kDhcParts = 8;
+// d head_cls: a workgroup per 16 head dims; sixteen interleaved slices of the
+// block partials, each summed in block order, then the slice sums in slice
+// order (fixed order)
+constexpr int kDhcDims = 16, kDhcParts = 16;
 
 template <int D>
-__global__ __launch_bounds__(kDhcParts * D) void hc_dhc_reduce_kernel(HcBK p) {
-  __shared__ float s_part[kDhcParts][D];
-  const int e = threadIdx.x % D, part = threadIdx.x / D;
+__global__ __launch_bounds__(kDhcDims * kDhcParts) void hc_dhc_reduce_kernel(HcBK p) {
+  __shared__ float s_part[kDhcParts][kDhcDims];
+  const int el = threadIdx.x % kDhcDims, part = threadIdx.x / kDhcDims;
+  const int e = blockIdx.x * kDhcDims + el;
   const int64_t n = (int64_t)p.a.B * p.a.nblk;
   float s = 0.f;
   constexpr int kAhead = 16;                       // partials loaded together, then added in order
@@ -635,12 +637,12 @@ __global__ __launch_bounds__(kDhcParts * D) void hc_dhc_reduce_kernel(HcBK p) {
     for (int u = 0; u < kAhead; ++u)
       if (i0 + (int64_t)u * kDhcParts < n) s += v[u];
   }
-  s_part[part][e] = s;
+  s_part[part][el] = s;
   __syncthreads();
   if (part == 0) {
-    float t = s_part[0][e];
+    float t = s_part[0][el];
 #pragma unroll
-    for (int k = 1; k < kDhcParts; ++k) t += s_part[k][e];
+    for (int k = 1; k < kDhcParts; ++k) t += s_part[k][el];
     p.a.dhc[e] = t;
   }
 }
@@ -1158,12 +1160,12 @@ extern "C" int srswa_hc_score_bwd(const srswa_hc_score_bwd_args* a, void* scratc
     hipLaunchKernelGGL(hc_score_bwd_dq_kernel<128>, gq, dim3(256), 0, st, k);
     hipLaunchKernelGGL(hc_score_bwd_dkbar_kernel<128>, gk, dim3(256), 0, st, k);
     hipLaunchKernelGGL(hc_summary_bwd_kernel<128>, gs, dim3(256), 0, st, k);
-    hipLaunchKernelGGL(hc_dhc_reduce_kernel<128>, dim3(1), dim3(kDhcParts * 128), 0, st, k);
+    hipLaunchKernelGGL(hc_dhc_reduce_kernel<128>, dim3(128 / kDhcDims), dim3(kDhcDims * kDhcParts), 0, st, k);
   } else {
     hipLaunchKernelGGL(hc_score_bwd_dq_kernel<64>, gq, dim3(256), 0, st, k);
     hipLaunchKernelGGL(hc_score_bwd_dkbar_kernel<64>, gk, dim3(256), 0, st, k);
     hipLaunchKernelGGL(hc_summary_bwd_kernel<64>, gs, dim3(256), 0, st, k);
-    hipLaunchKernelGGL(hc_dhc_reduce_kernel<64>, dim3(1), dim3(kDhcParts * 64), 0, st, k);
+    hipLaunchKernelGGL(hc_dhc_reduce_kernel<64>, dim3(64 / kDhcDims), dim3(kDhcDims * kDhcParts), 0, st, k);
   }
   const hipError_t e = hipGetLastError();
   if (e != hipSuccess) {
