@@ -902,7 +902,8 @@ int srswa_hc_score_fwd(const srswa_hc_score_args* a, void* stream);
  * nblk * BS are the caller's) and dhc.  Deterministic (partials summed in a
  * fixed order); the workspace holds fp32 partials of dkbar per 256-row chunk
  * and of dhc per block.  Layout as srswa_hc_score_args; kbar and z are the
- * forward's.  Rows must not overlap (z_st, gz_st >= nblk, q_st >= D), and the
+ * forward's; the q, k, dq and dk rows are 16-byte aligned (base and strides).
+ * Rows must not overlap (z_st, gz_st >= nblk, q_st >= D), and the
  * row strides q_st, z_st, gz_st and nblk * D stay below 2^23 elements
  * (SRSWA_UNSUPPORTED otherwise). */
 typedef struct {

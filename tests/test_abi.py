@@ -95,12 +95,15 @@ def _hc_args(cls, **over):
 def test_hc_scores_refuse_overlapping_or_huge_rows():
     """The head_cls scorers address z / gz / q tiles through buffer resources
     with 32-bit offsets: overlapping rows and strides of 2^23 or more are
-    refused with SRSWA_UNSUPPORTED on the host (no GPU needed)."""
+    refused with SRSWA_UNSUPPORTED on the host (no GPU needed), and so are
+    q / k / dq / dk rows that are not 16-byte aligned (read and written as
+    float4)."""
     lib = _lib.lib()
     assert lib.srswa_hc_score_fwd(ctypes.byref(_hc_args(_lib.HcScoreArgs, z_st=8)), None) == _lib.SRSWA_UNSUPPORTED
     assert lib.srswa_hc_score_fwd(ctypes.byref(_hc_args(_lib.HcScoreArgs, z_st=1 << 23, z_sb=1 << 34)),
                                   None) == _lib.SRSWA_UNSUPPORTED
-    for over in (dict(z_st=8), dict(gz_st=8), dict(q_st=64, k_st=128), dict(gz_st=1 << 23, gz_sb=1 << 34)):
+    for over in (dict(z_st=8), dict(gz_st=8), dict(q_st=64, k_st=128), dict(gz_st=1 << 23, gz_sb=1 << 34),
+                 dict(dk=0x100004), dict(dk_st=130), dict(dk_sb=1024 * 128 + 2), dict(k_st=129)):
         a = _hc_args(_lib.HcScoreBwdArgs, **over)
         need = ctypes.c_size_t()
         assert lib.srswa_hc_score_bwd_workspace(ctypes.byref(a), ctypes.byref(need)) == _lib.SRSWA_OK

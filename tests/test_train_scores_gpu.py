@@ -37,6 +37,11 @@ HC_CASES = {
     "cfg5_shape_bs64_lb8": (1, 4096, 128, 64, 8, 0.3, (0,)),
     "ragged_last_block_d64": (3, 1001, 64, 16, 2, 1.0, (0, 40, 7)),
     "bs128_zero_head_cls": (1, 777, 128, 128, 1, 0.0, (300,)),
+    # the remaining (head dim, block size) pairs, each with a ragged last block
+    "d128_bs16_lb3": (1, 509, 128, 16, 3, 0.7, (0,)),
+    "d64_bs32_lb2": (2, 611, 64, 32, 2, 0.9, (0, 13)),
+    "d64_bs64_lb1": (1, 700, 64, 64, 1, 1.2, (0,)),
+    "d64_bs128_lb1": (1, 900, 64, 128, 1, 0.6, (50,)),
 }
 
 

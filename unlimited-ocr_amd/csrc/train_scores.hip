@@ -75,20 +75,63 @@ __device__ __forceinline__ float sanitize(float g) { return isfinite(g) ? clamp_
 __device__ __forceinline__ int last_remote_block(int p, int BS, int LB) { return p >= 0 ? p / BS - LB : -1; }
 
 // ---------------------------------------------------------------- stage 0
-// One workgroup (256 threads) per block c of sequence b: nv valid keys, rows
-// at kg, k_st apart, read from global memory (a block is at most 64 KiB and
-// stays in the caches over the passes).  The logits go one key per thread;
-// passes over the key rows go one head dim per thread, in NQ = 256 / D key
-// slices (slice q takes keys q, q + NQ, ... in key order, rows loaded
-// kRowsAhead at a time), whose partials are then added in slice order.
-constexpr int kRowsAhead = 16;   // key rows loaded together by the block passes
+// One workgroup (256 threads) per block c of sequence b: nv valid keys
+// (nv <= BS), rows at kg, k_st apart.  Each key row is read once, into
+// registers: key t belongs to threads TPK t .. TPK t + TPK - 1 (TPK = 256 / BS),
+// thread j of them holding the float4 chunks j, j + TPK, j + 2 TPK, ... of the
+// row (D / TPK dims; a key's threads read consecutive chunks).  A
+// per-key dot product is summed over the key's threads by a butterfly (every
+// lane of the key ends with the same bits: each step adds a pair in both
+// orders, and fp32 addition commutes); per-dim sums over the keys go through
+// an LDS tile of the weighted rows, summed column-wise in key order.
+template <int D, int BS> struct HcKeys {
+  static constexpr int TPK = 256 / BS, NV4 = D / (4 * TPK);
+  // first head dim of this thread's chunk i
+  static __device__ __forceinline__ int dim(int i) { return 4 * ((int)threadIdx.x % TPK + TPK * i); }
+  float4 v[NV4];
+};
 
-struct HcWgLds {
-  float pre[128], e[128], w[128], ds[128];   // per key: unclamped logit, exp, weight, d logit
-  float part[256];                           // slice partials [NQ][D]
+template <int D, int BS> struct HcWgLds {
+  static constexpr int WP = D + 4;           // row pitch of wk (rows start 4 banks apart)
+  float wk[BS * WP];                         // weighted key rows [t][e]
   float hc[128], dkb[128];
+  float part[256];                           // slice partials of the chunk sums [NQ][D]
   float red[4];
 };
+
+// the block's key rows into registers (rows past nv repeat row nv - 1; they are
+// masked wherever they could count)
+template <int D, int BS>
+__device__ __forceinline__ void load_keys(const float* kg, int64_t k_st, int nv, HcKeys<D, BS>& K) {
+  using KS = HcKeys<D, BS>;
+  const int t = threadIdx.x / KS::TPK;
+  if (nv > 0) {
+    const float* row = kg + (int64_t)min(t, nv - 1) * k_st;
+#pragma unroll
+    for (int i = 0; i < KS::NV4; ++i) K.v[i] = *reinterpret_cast<const float4*>(row + KS::dim(i));
+  } else {
+#pragma unroll
+    for (int i = 0; i < KS::NV4; ++i) K.v[i] = make_float4(0.f, 0.f, 0.f, 0.f);
+  }
+}
+
+// k_t . v (v in LDS, D entries) for this thread's key t, on every lane of the key
+template <int D, int BS>
+__device__ __forceinline__ float key_dot(const HcKeys<D, BS>& K, const float* v) {
+  using KS = HcKeys<D, BS>;
+  float s = 0.f;
+#pragma unroll
+  for (int i = 0; i < KS::NV4; ++i) {
+    const float4 w = *reinterpret_cast<const float4*>(v + KS::dim(i));
+    s = fmaf(K.v[i].x, w.x, s);
+    s = fmaf(K.v[i].y, w.y, s);
+    s = fmaf(K.v[i].z, w.z, s);
+    s = fmaf(K.v[i].w, w.w, s);
+  }
+#pragma unroll
+  for (int o = 1; o < KS::TPK; o <<= 1) s += __shfl_xor(s, o, kWave);
+  return s;
+}
 
 // the workgroup's max / sum of v (waves combined in wave order; every thread
 // gets the result)
@@ -109,45 +152,22 @@ __device__ __forceinline__ float wg_sum(float v, float* red) {
   return r;
 }
 
-// sum over keys t < nv of coef[t] * k_t[e] for this thread's dim e, summed
-// over the key slices in order (valid for threads tid < D after the call)
-template <int D>
-__device__ __forceinline__ float keys_weighted(const float* kg, int64_t k_st, int nv, const float* coef, float* part) {
-  constexpr int NQ = 256 / D;
-  const int e = threadIdx.x % D, q = threadIdx.x / D;
-  float acc = 0.f;
-  for (int t0 = q; t0 < nv; t0 += NQ * kRowsAhead) {
-    float rv[kRowsAhead];
+// sum over keys t < nv of coef_t k_t[e] for head dim e = tid (threads tid < D),
+// coef_t this thread's key's coefficient, summed in key order
+template <int D, int BS>
+__device__ __forceinline__ float keys_weighted(const HcKeys<D, BS>& K, int nv, float coef, HcWgLds<D, BS>& L) {
+  using KS = HcKeys<D, BS>;
+  using LS = HcWgLds<D, BS>;
+  float* dst = L.wk + (threadIdx.x / KS::TPK) * LS::WP;
 #pragma unroll
-    for (int u = 0; u < kRowsAhead; ++u) rv[u] = kg[(int64_t)min(t0 + u * NQ, nv - 1) * k_st + e];
-#pragma unroll
-    for (int u = 0; u < kRowsAhead; ++u)
-      if (t0 + u * NQ < nv) acc = fmaf(coef[t0 + u * NQ], rv[u], acc);
-  }
-  part[q * D + e] = acc;
+  for (int i = 0; i < KS::NV4; ++i)
+    *reinterpret_cast<float4*>(dst + KS::dim(i)) =
+        make_float4(coef * K.v[i].x, coef * K.v[i].y, coef * K.v[i].z, coef * K.v[i].w);
   __syncthreads();
   float s = 0.f;
-  if (threadIdx.x < D) {
-    s = part[threadIdx.x];
-#pragma unroll
-    for (int r = 1; r < NQ; ++r) s += part[r * D + threadIdx.x];
-  }
+  if (threadIdx.x < D)
+    for (int u = 0; u < nv; ++u) s += L.wk[u * LS::WP + threadIdx.x];
   __syncthreads();
-  return s;
-}
-
-// k_t . v over the D dims for key t (v in LDS), fmaf chain in dim order
-template <int D>
-__device__ __forceinline__ float key_dot(const float* row, const float* v) {
-  float s = 0.f;
-#pragma unroll
-  for (int e = 0; e < D; e += 4) {
-    const float4 kv = *reinterpret_cast<const float4*>(row + e);
-    s = fmaf(kv.x, v[e], s);
-    s = fmaf(kv.y, v[e + 1], s);
-    s = fmaf(kv.z, v[e + 2], s);
-    s = fmaf(kv.w, v[e + 3], s);
-  }
   return s;
 }
 
@@ -155,33 +175,32 @@ struct HcBlockOut {
   float den, rowmax;
   bool pad_overflow;
   float kb;          // kbar_raw of head dim tid (threads tid < D)
+  float pre, e, w;   // this thread's key: unclamped logit, exp, weight (0 past nv)
 };
 
-// The block's stage-0 forward: L.pre, L.e, L.w per key (BS entries), the
-// weighted summary kbar_raw and the softmax statistics.  L.hc holds head_cls.
-template <int D>
-__device__ void hc_block_forward(const float* kg, int64_t k_st, int nv, int BS, float isd, HcWgLds& L,
-                                 HcBlockOut& out) {
-  const int tid = threadIdx.x;
-  float pre = 0.f, cl = -INFINITY;
-  if (tid < nv) {
-    pre = key_dot<D>(kg + (int64_t)tid * k_st, L.hc) * isd;
-    cl = clamp_act(pre);
-  }
-  if (tid < BS) L.pre[tid] = pre;
+// The block's stage-0 forward from the keys in registers: the weighted summary
+// kbar_raw, the softmax statistics and the thread's key's logit, exp and weight.
+// L.hc holds head_cls.
+template <int D, int BS>
+__device__ void hc_block_forward(const HcKeys<D, BS>& K, int nv, float isd, HcWgLds<D, BS>& L, HcBlockOut& out) {
+  using KS = HcKeys<D, BS>;
+  const int t = threadIdx.x / KS::TPK, j = threadIdx.x % KS::TPK;
+  const bool valid = t < nv;
+  const float dot = key_dot<D, BS>(K, L.hc);
+  const float pre = valid ? dot * isd : 0.f;
+  const float cl = valid ? clamp_act(pre) : -INFINITY;
   const float mx = wg_max(cl, L.red);
   const float rowmax = nv > 0 ? mx : 0.f;
-  const float e = tid < nv ? expf(cl - rowmax) : 0.f;
-  const float den = wg_sum(e, L.red);
+  const float e = valid ? expf(cl - rowmax) : 0.f;
+  const float den = wg_sum(j == 0 ? e : 0.f, L.red);
   const float dn = fmaxf(den, 1e-6f);
-  if (tid < BS) {
-    L.e[tid] = e;
-    L.w[tid] = e / dn;
-  }
-  __syncthreads();
-  out.kb = keys_weighted<D>(kg, k_st, nv, L.w, L.part);
+  const float w = e / dn;
+  out.kb = keys_weighted<D, BS>(K, nv, w, L);
   out.den = den;
   out.rowmax = rowmax;
+  out.pre = pre;
+  out.e = e;
+  out.w = w;
   // a padding key's weight is exp(0 - m) * 0: NaN once exp(-m) overflows
   out.pad_overflow = nv > 0 && nv < BS && isinf(expf(-rowmax));
 }
@@ -192,17 +211,19 @@ struct HcK {
   int ngroups;
 };
 
-template <int D>
+template <int D, int BS>
 __global__ __launch_bounds__(256) void hc_summary_fwd_kernel(HcK p) {
-  __shared__ HcWgLds L;
+  __shared__ __align__(16) HcWgLds<D, BS> L;
   const srswa_hc_score_args& a = p.a;
   const int b = (int)(blockIdx.x / (unsigned)a.nblk), c = (int)(blockIdx.x % (unsigned)a.nblk);
+  const int t0 = c * BS;
+  const int nv = max(0, min(BS, a.S - t0));
+  HcKeys<D, BS> K;
+  load_keys<D, BS>(a.k + (int64_t)b * a.k_sb + (int64_t)t0 * a.k_st, a.k_st, nv, K);
   if (threadIdx.x < D) L.hc[threadIdx.x] = a.head_cls[threadIdx.x];
   __syncthreads();
-  const int t0 = c * a.block_size;
-  const int nv = max(0, min(a.block_size, a.S - t0));
   HcBlockOut hb;
-  hc_block_forward<D>(a.k + (int64_t)b * a.k_sb + (int64_t)t0 * a.k_st, a.k_st, nv, a.block_size, p.isd, L, hb);
+  hc_block_forward<D, BS>(K, nv, p.isd, L, hb);
   if (threadIdx.x < D)
     a.kbar[(int64_t)b * a.kb_sb + (int64_t)c * D + threadIdx.x] = (isfinite(hb.kb) && !hb.pad_overflow) ? hb.kb : 0.f;
 }
@@ -546,19 +567,20 @@ __global__ __launch_bounds__(256) void hc_score_bwd_dkbar_kernel(HcBK p) {
 }
 
 // stage-0 backward, one workgroup per block: d idx_k rows of the block and
-// the block's partial of d head_cls
-template <int D>
+// the block's partial of d head_cls (the key rows read once, into registers)
+template <int D, int BS>
 __global__ __launch_bounds__(256) void hc_summary_bwd_kernel(HcBK p) {
   constexpr int NQ = 256 / D;
-  __shared__ HcWgLds L;
+  using KS = HcKeys<D, BS>;
+  __shared__ __align__(16) HcWgLds<D, BS> L;
   const srswa_hc_score_bwd_args& a = p.a;
   const int tid = threadIdx.x;
   const int b = (int)(blockIdx.x / (unsigned)a.nblk), c = (int)(blockIdx.x % (unsigned)a.nblk);
-  if (tid < D) L.hc[tid] = a.head_cls[tid];
-  const int BS = a.block_size;
   const int t0 = c * BS;
   const int nv = max(0, min(BS, a.S - t0));
-  const float* kg = a.k + (int64_t)b * a.k_sb + (int64_t)t0 * a.k_st;
+  HcKeys<D, BS> K;
+  load_keys<D, BS>(a.k + (int64_t)b * a.k_sb + (int64_t)t0 * a.k_st, a.k_st, nv, K);
+  if (tid < D) L.hc[tid] = a.head_cls[tid];
   {
     // d k_bar: the chunk partials, slice q taking chunks q, q + NQ, ... in
     // order, the slices then added in order
@@ -585,35 +607,34 @@ __global__ __launch_bounds__(256) void hc_summary_bwd_kernel(HcBK p) {
   }
   __syncthreads();
   HcBlockOut hb;
-  hc_block_forward<D>(kg, a.k_st, nv, BS, p.isd, L, hb);
+  hc_block_forward<D, BS>(K, nv, p.isd, L, hb);
   // nan_to_num(k_bar) passes no gradient where k_bar_raw is not finite
   if (tid < D) L.dkb[tid] = (!isfinite(hb.kb) || hb.pad_overflow) ? 0.f : dkb;
   __syncthreads();
+  const int t = tid / KS::TPK, j = tid % KS::TPK;
+  const bool valid = t < nv;
   const float dn = fmaxf(hb.den, 1e-6f);
-  // dw_t = dkbar . k_t, one key per thread
-  float dw = 0.f;
-  if (tid < nv) dw = key_dot<D>(kg + (int64_t)tid * a.k_st, L.dkb);
-  const float se = wg_sum(tid < nv ? dw * L.e[tid] : 0.f, L.red);
+  const float dw = key_dot<D, BS>(K, L.dkb);                 // dw_t = dkbar . k_t
+  const float se = wg_sum((valid && j == 0) ? dw * hb.e : 0.f, L.red);
   const float dden = hb.den >= 1e-6f ? -se / (dn * dn) : 0.f;
-  if (tid < BS) {
-    float ds = 0.f;
-    if (tid < nv) {
-      const float de = dw / dn + dden;
-      const float pre = L.pre[tid];
-      ds = (pre >= -kActClamp && pre <= kActClamp) ? de * L.e[tid] * p.isd : 0.f;
-    }
-    L.ds[tid] = ds;
+  float ds = 0.f;
+  if (valid) {
+    const float de = dw / dn + dden;
+    ds = (hb.pre >= -kActClamp && hb.pre <= kActClamp) ? de * hb.e * p.isd : 0.f;
   }
-  __syncthreads();
-  // the block's d head_cls, then the d k rows (a dim per thread, slice q
-  // writing keys q, q + NQ, ...)
-  const float dh = keys_weighted<D>(kg, a.k_st, nv, L.ds, L.part);
+  const float dh = keys_weighted<D, BS>(K, nv, ds, L);       // the block's d head_cls
   if (tid < D) p.dhc_part[((int64_t)b * a.nblk + c) * D + tid] = hb.pad_overflow ? __builtin_nanf("") : dh;
-  const int e = tid % D;
-  const float dke = L.dkb[e], hce = L.hc[e];
-  float* dk = a.dk + (int64_t)b * a.dk_sb + (int64_t)t0 * a.dk_st + e;
-  for (int t = tid / D; t < nv; t += NQ)
-    dk[(int64_t)t * a.dk_st] = hb.pad_overflow ? 0.f : fmaf(L.w[t], dke, L.ds[t] * hce);
+  if (valid) {                                               // this thread's dims of d k_t
+    float* dst = a.dk + (int64_t)b * a.dk_sb + (int64_t)(t0 + t) * a.dk_st;
+#pragma unroll
+    for (int i = 0; i < KS::NV4; ++i) {
+      const int e0 = KS::dim(i);
+      float o[4];
+#pragma unroll
+      for (int x = 0; x < 4; ++x) o[x] = hb.pad_overflow ? 0.f : fmaf(hb.w, L.dkb[e0 + x], ds * L.hc[e0 + x]);
+      *reinterpret_cast<float4*>(dst + e0) = make_float4(o[0], o[1], o[2], o[3]);
+    }
+  }
 }
 
 // d head_cls: a workgroup per 16 head dims; sixteen interleaved slices of the
@@ -1023,6 +1044,15 @@ __global__ __launch_bounds__(256) void bm_bwd_dk_kernel(BmBK p) {
   }
 }
 
+// the head_cls block size as a template argument (16, 32, 64 or 128; checked by hc_check)
+template <int D, typename F>
+void hc_dispatch_bs(int BS, F&& f) {
+  if (BS == 16) f(std::integral_constant<int, 16>{});
+  else if (BS == 32) f(std::integral_constant<int, 32>{});
+  else if (BS == 64) f(std::integral_constant<int, 64>{});
+  else f(std::integral_constant<int, 128>{});
+}
+
 int hc_check(int B, int S, int D, int nblk, int BS, int LB, const char* what) {
   if (B < 0 || S < 0 || nblk < 0 || BS <= 0 || LB < 0) {
     set_error("%s: bad sizes", what);
@@ -1077,10 +1107,14 @@ extern "C" int srswa_hc_score_fwd(const srswa_hc_score_args* a, void* stream) {
   }
   const unsigned gz = (unsigned)gz64;
   if (a->D == 128) {
-    hipLaunchKernelGGL(hc_summary_fwd_kernel<128>, dim3(gs), dim3(256), 0, st, k);
+    hc_dispatch_bs<128>(a->block_size, [&](auto bs) {
+      hipLaunchKernelGGL((hc_summary_fwd_kernel<128, decltype(bs)::value>), dim3(gs), dim3(256), 0, st, k);
+    });
     hipLaunchKernelGGL(hc_score_fwd_kernel<128>, dim3(gz), dim3(256), 0, st, k);
   } else {
-    hipLaunchKernelGGL(hc_summary_fwd_kernel<64>, dim3(gs), dim3(256), 0, st, k);
+    hc_dispatch_bs<64>(a->block_size, [&](auto bs) {
+      hipLaunchKernelGGL((hc_summary_fwd_kernel<64, decltype(bs)::value>), dim3(gs), dim3(256), 0, st, k);
+    });
     hipLaunchKernelGGL(hc_score_fwd_kernel<64>, dim3(gz), dim3(256), 0, st, k);
   }
   const hipError_t e = hipGetLastError();
@@ -1124,9 +1158,9 @@ extern "C" int srswa_hc_score_bwd(const srswa_hc_score_bwd_args* a, void* scratc
     set_error("head_cls scores backward: scratch of %zu bytes required (got %zu)", need, scratch_bytes);
     return SRSWA_WORKSPACE;
   }
-  if (!al16(a->q) || !al16(a->k) || !al16(a->kbar) || !al16(a->dq) || (a->q_sb % 4) || (a->q_st % 4) ||
-      (a->k_sb % 4) || (a->k_st % 4) || (a->kb_sb % 4) || (a->dq_sb % 4) || (a->dq_st % 4) ||
-      a->kb_sb < (int64_t)a->nblk * a->D) {
+  if (!al16(a->q) || !al16(a->k) || !al16(a->kbar) || !al16(a->dq) || !al16(a->dk) || (a->q_sb % 4) ||
+      (a->q_st % 4) || (a->k_sb % 4) || (a->k_st % 4) || (a->kb_sb % 4) || (a->dq_sb % 4) || (a->dq_st % 4) ||
+      (a->dk_sb % 4) || (a->dk_st % 4) || a->kb_sb < (int64_t)a->nblk * a->D) {
     set_error("head_cls scores backward: rows must be 16-byte aligned and k_bar [B, nblk, D] dense per sequence");
     return SRSWA_UNSUPPORTED;
   }
@@ -1159,12 +1193,16 @@ extern "C" int srswa_hc_score_bwd(const srswa_hc_score_bwd_args* a, void* scratc
   if (a->D == 128) {
     hipLaunchKernelGGL(hc_score_bwd_dq_kernel<128>, gq, dim3(256), 0, st, k);
     hipLaunchKernelGGL(hc_score_bwd_dkbar_kernel<128>, gk, dim3(256), 0, st, k);
-    hipLaunchKernelGGL(hc_summary_bwd_kernel<128>, gs, dim3(256), 0, st, k);
+    hc_dispatch_bs<128>(a->block_size, [&](auto bs) {
+      hipLaunchKernelGGL((hc_summary_bwd_kernel<128, decltype(bs)::value>), gs, dim3(256), 0, st, k);
+    });
     hipLaunchKernelGGL(hc_dhc_reduce_kernel<128>, dim3(128 / kDhcDims), dim3(kDhcDims * kDhcParts), 0, st, k);
   } else {
     hipLaunchKernelGGL(hc_score_bwd_dq_kernel<64>, gq, dim3(256), 0, st, k);
     hipLaunchKernelGGL(hc_score_bwd_dkbar_kernel<64>, gk, dim3(256), 0, st, k);
-    hipLaunchKernelGGL(hc_summary_bwd_kernel<64>, gs, dim3(256), 0, st, k);
+    hc_dispatch_bs<64>(a->block_size, [&](auto bs) {
+      hipLaunchKernelGGL((hc_summary_bwd_kernel<64, decltype(bs)::value>), gs, dim3(256), 0, st, k);
+    });
     hipLaunchKernelGGL(hc_dhc_reduce_kernel<64>, dim3(64 / kDhcDims), dim3(kDhcDims * kDhcParts), 0, st, k);
   }
   const hipError_t e = hipGetLastError();
