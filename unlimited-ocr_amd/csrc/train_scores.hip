@@ -39,7 +39,8 @@
 // offset, n, and flags for "several keys take the gradient" (their 64-bit mask
 // is then written to a side array) and "none does" -- in block-major order.
 //
-// Kernels: hc_summary_fwd (one workgroup per block), hc_score_fwd (64 query
+// Kernels: hc_summary_fwd (one workgroup per block, its key rows read once
+// into registers), hc_score_fwd (64 query
 // rows per workgroup, Z = Q K_bar^T as 32 x 32 fp32 MFMA tiles against groups
 // of 64 blocks staged in LDS), hc_score_bwd_dq (dQ = dZ K_bar, one row tile and
 // 64 head dims per workgroup), hc_score_bwd_dkbar (dK_bar = dZ^T Q as fp32
