@@ -989,7 +989,7 @@ def bench_train_scores(args):
                        "head_cls_bwd_kernels_ms": ms_hc_bk, "block_max_fwd_ms": ms_bm_f, "block_max_fwd_bwd_ms": ms_bm,
                        "head_cls_fwd_bytes": hc_bytes, "block_max_fwd_flops": bm_flops},
             "roofline": {"bound": "hbm", "achieved": hc_gbs, "peak": 8000.0, "unit": "GB/s",
-                         "frac": hc_gbs / 8000.0, "traffic": None,
+                         "frac": hc_gbs / 8000.0, "traffic": _pmc_traffic("train_scores_cfg5_traffic"),
                          "kernel": "head_cls forward kernels (summary + score), launched on prebuilt arguments"},
             "roofline_block_max": {"bound": "mfma", "achieved": bm_tfs, "peak": 157.3, "unit": "TFLOP/s",
                                    "frac": bm_tfs / 157.3, "kernel": "bm_fwd_kernel (fp32 MFMA)"}}
