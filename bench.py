@@ -574,8 +574,10 @@ def bench_paged(args):
             "config": {"workload": f"config 3, paged [num_pages, 64, 10, 128] {args.kv} cache", "B": B,
                        "num_pages": c["num_pages"], "kv_cache": args.kv},
             "roofline": {"bound": "hbm", "achieved": achieved, "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                         "frac": achieved / HBM_PEAK_GBS, "traffic": None, "algorithmic_bytes_per_launch": nbytes,
-                         "kernel": "srswa::decode_kernel<bf16,bf16,128,8,paged> + decode_merge_kernel"}}
+                         "frac": achieved / HBM_PEAK_GBS, "traffic": _pmc_traffic(f"paged_cfg3_{args.kv}_traffic"),
+                         "algorithmic_bytes_per_launch": nbytes,
+                         "kernel": "srswa::decode_kernel<bf16,bf16,128,8,paged>"
+                                   + (" (fp8 cache, no merge)" if kvd is not None else " + decode_merge_kernel")}}
 
 
 def bench_dash(args):
