@@ -703,7 +703,8 @@ def bench_page(args):
             "config": {"workload": "apply_page2d_rope_pair, q and k [16384, 10*128] bf16, cos/sin [16384, 128]",
                        "T": T, "heads": H, "head_dim": hd},
             "roofline": {"bound": "hbm", "achieved": rope_gbs, "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                         "frac": rope_gbs / HBM_PEAK_GBS, "traffic": None, "algorithmic_bytes_per_launch": rope_bytes,
+                         "frac": rope_gbs / HBM_PEAK_GBS, "traffic": _pmc_traffic("rope_page2d_16k_traffic"),
+                         "algorithmic_bytes_per_launch": rope_bytes,
                          "kernel": "srswa::rope_kernel<bf16>"},
             "cos_sin_table_us": ms_cs * 1e3,
             "decode_allow": {"workload": "config 3 paged cache, 64 requests, per-slot image pages of every live page",
